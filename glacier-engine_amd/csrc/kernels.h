@@ -1,0 +1,107 @@
+// kernels.h — launch interface of the gfx950 kernels (host-callable C++).
+//
+// Device data layouts shared by the kernels and the host runtime:
+//
+// INT4 weight tiles (replaces the reference's row-major packed layout,
+// int4_weights.zig:79-107; arithmetic unchanged):
+//   codes  uint4  [NB = N/16][KQ = K/128][64 lanes]
+//          lane l -> output row n = 16*nb + (l & 15), k-chunk c = l >> 4;
+//          u32 word j (0..3) covers group g = 4*kq + j, columns
+//          k = 32*g + 8*c + b (low nibble of byte b) and k + 4 (high nibble).
+//          Code u decodes to (u - 7) (int4_matmul.zig:22-25).
+//   scales uint2  [NB][KQ][16] = fp16 w_scale[n][4*kq + j], j = 0..3.
+//
+// Activation digit planes (A operand of v_mfma_i32_16x16x32_i8):
+//   q      int8   [G][D][M][32]   (D = digit planes: 1 for Q8, 3 for F32)
+//   meta   {f32 scale, i32 corr} [G][M]
+//   The group dot is  (f32(T - corr) * w_scale) * scale  with
+//   T = sum_d 128^(D-1-d) * sum_k u_k * q_d[k]   (u = stored code).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gk {
+
+struct ActMeta {
+  float scale;
+  int32_t corr;
+};
+
+enum Epilogue : int {
+  EPI_PLAIN = 0,   // y = sum (+ bias)
+  EPI_RESID = 1,   // y = resid + sum
+  EPI_SWIGLU = 2,  // rows paired gate/up in 8-row halves; y = silu(g) * u
+  EPI_QKV = 3,     // q/k RoPE pairs + KV page write
+};
+
+// Arguments of the fused QKV epilogue.
+struct QkvArgs {
+  float *q_out;            // [M][Hq*hd]
+  void *kv_pool;           // pages [page][L][2][16][kv_dim]
+  int kv_f16;
+  const int32_t *page_table;  // [lanes][max_pages]
+  int max_pages;
+  const int32_t *lane_of_row; // [M] lane id of activation row m
+  const int32_t *pos_of_row;  // [M] position of activation row m
+  const float *rope_cos, *rope_sin;  // [positions][hd/2]
+  int layer, num_layers;
+  int num_heads, num_kv_heads, head_dim;
+};
+
+struct GemvArgs {
+  const uint4 *codes;
+  const uint2 *scales;
+  int N, K;                 // device rows / columns
+  const int8_t *act_q;
+  const ActMeta *act_meta;
+  int M, D;
+  const float *bias;        // [N] logical order (EPI_PLAIN/QKV), may be null
+  float *y;                 // EPI_PLAIN/RESID: [M][N]; SWIGLU: [M][N/2]
+  const float *resid;       // EPI_RESID
+  int S;                    // K splits
+  float *partial;           // [S][M][N] (S > 1)
+  uint32_t *counters;       // [NB] zero-initialised, self-resetting
+  int epi;
+  QkvArgs qkv;
+};
+
+// Prepare activation planes from x [M][K] (f32 or bf16), optionally
+// RMS-normalised with weight `norm_w` first (kernels.zig:141-220).
+hipError_t launch_prep_act(const void *x, int x_bf16, const float *norm_w, float eps,
+                           int M, int K, int D, int8_t *act_q, ActMeta *meta,
+                           float *normed_out, hipStream_t st);
+
+hipError_t launch_gemv(const GemvArgs &a, hipStream_t st);
+
+// Choose the split count for a GEMV of NB row blocks and KQ quads.
+int choose_splits(int NB, int KQ, int M);
+
+hipError_t launch_rmsnorm(const float *x, const float *w, int rows, int dim, float eps,
+                          float *out, hipStream_t st);
+
+hipError_t launch_gather_rows(const float *table, const int32_t *ids, int M, int dim,
+                              float *out, hipStream_t st);
+
+// Paged GQA decode attention. Writes out [M][Hq*hd]. Scratch must hold
+// attention_scratch_floats(...) floats.
+size_t attention_scratch_floats(int M, int num_heads, int head_dim, int max_ctx);
+hipError_t launch_attention(const float *q, const void *kv_pool, int kv_f16,
+                            const int32_t *page_table, int max_pages, const int32_t *lane_of_row,
+                            const int32_t *ctx_len, int M, int layer, int num_layers,
+                            int num_heads, int num_kv_heads, int head_dim, int max_ctx,
+                            float *scratch, float *out, hipStream_t st);
+
+// Argmax over rows x n. Eligible variant when words != null. Results to
+// `result` [rows] = {index (u64), eligible_rows (u64), status (i32), pad}.
+struct ArgmaxResult {
+  uint64_t index;
+  uint64_t eligible_rows;
+  int32_t status;
+  int32_t pad;
+};
+size_t argmax_scratch_bytes(int rows, long n);
+hipError_t launch_argmax(const float *logits, long n, int rows, const uint64_t *words,
+                         long word_count, void *scratch, uint32_t *counters,
+                         ArgmaxResult *result, hipStream_t st);
+
+}  // namespace gk

@@ -1,0 +1,82 @@
+// runtime.h — internal structures shared by the C-ABI implementation files.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/glacier_hip.h"
+#include "kernels.h"
+
+struct glacier_hip_context {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  hipDeviceProp_t props{};
+  uint64_t epoch = 0;  // binds allocation quotes to this context
+  std::mutex mu;       // one submission at a time (int4_executor.zig:2267)
+  std::string last_error;
+  struct Buf {
+    void *ptr;
+    uint64_t requested, charged;
+  };
+  std::map<uint64_t, Buf> buffers;
+  uint64_t next_buffer_id = 1;
+  uint64_t live_weights = 0;
+  // scratch for the stand-alone kernel entry points
+  void *scratch = nullptr;
+  size_t scratch_bytes = 0;
+  uint32_t *counters = nullptr;  // zeroed once, self-resetting
+  size_t counter_count = 0;
+  gk::ArgmaxResult *results_host = nullptr;  // pinned
+};
+
+struct glacier_hip_int4_weight {
+  glacier_hip_context *ctx = nullptr;
+  uint32_t out_f = 0, in_f = 0, group = 32;
+  uint4 *codes = nullptr;
+  uint2 *scales = nullptr;
+  uint64_t device_bytes = 0;
+};
+
+namespace gh {
+
+// Record a HIP failure on the context and map it to a status code.
+int hip_fail(glacier_hip_context *ctx, hipError_t e, const char *what);
+#define GH_CHECK(ctx, expr)                                   \
+  do {                                                        \
+    hipError_t _e = (expr);                                   \
+    if (_e != hipSuccess) return gh::hip_fail((ctx), _e, #expr); \
+  } while (0)
+
+// Device row source for the tile repack: row `row` of a reference-layout
+// matrix (packed codes + f32 scales), or an all-zero row when packed == null.
+struct RowSrc {
+  const uint8_t *packed;
+  const float *scales_f32;
+  const uint16_t *scales_f16;
+  uint64_t row;
+};
+
+// Build the device tile layout (kernels.h) for rows[0..N) of width K.
+void repack_tiles(const std::vector<RowSrc> &rows, uint32_t K, std::vector<uint32_t> &codes,
+                  std::vector<uint16_t> &scales);
+
+glacier_hip_int4_weight *upload_weight(glacier_hip_context *ctx, uint32_t out_f, uint32_t in_f,
+                                       const std::vector<uint32_t> &codes,
+                                       const std::vector<uint16_t> &scales);
+
+// Ensure ctx->scratch holds at least `bytes` and ctx->counters `count`.
+int ensure_scratch(glacier_hip_context *ctx, size_t bytes, size_t counters);
+
+// Run one projection on the device: prep (+ optional norm) then GEMV.
+struct ProjBuffers {
+  int8_t *act_q;
+  gk::ActMeta *meta;
+  float *partial;
+  uint32_t *counters;
+};
+int resolve_activation(int activation, uint32_t out_f, uint32_t in_f);
+
+}  // namespace gh

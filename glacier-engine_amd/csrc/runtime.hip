@@ -1,0 +1,666 @@
+// runtime.hip — C ABI: context, buffers and allocation lease, device
+// capability, persistent INT4 weights, and the stand-alone kernel entry
+// points (GEMV, RMSNorm, paged attention, argmax). The model/session token
+// loop lives in session.hip.
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <cstdio>
+
+#include "host_util.h"
+#include "runtime.h"
+
+using gh::hip_fail;
+
+namespace gh {
+
+int hip_fail(glacier_hip_context *ctx, hipError_t e, const char *what) {
+  if (ctx) {
+    ctx->last_error = std::string(what) + ": " + hipGetErrorString(e);
+  }
+  if (e == hipErrorOutOfMemory) return GLACIER_HIP_OUT_OF_MEMORY;
+  return GLACIER_HIP_DEVICE_ERROR;
+}
+
+int resolve_activation(int activation, uint32_t out_f, uint32_t in_f) {
+  if (activation == GLACIER_HIP_ACT_AUTO)
+    // int4_matmul.zig:461-463 (vocabulary head) and :372-374 (wide input)
+    return (out_f > 65536 || in_f > 16384) ? GLACIER_HIP_ACT_F32 : GLACIER_HIP_ACT_Q8;
+  return activation;
+}
+
+void repack_tiles(const std::vector<RowSrc> &rows, uint32_t K, std::vector<uint32_t> &codes,
+                  std::vector<uint16_t> &scales) {
+  const size_t N = rows.size();
+  const size_t NB = N / 16, KQ = K / 128, G = K / 32;
+  codes.assign(NB * KQ * 64 * 4, 0u);
+  scales.assign(NB * KQ * 16 * 4, 0u);
+  parallel_for(NB, [&](size_t b0, size_t b1) {
+    for (size_t nb = b0; nb < b1; ++nb)
+      for (int nl = 0; nl < 16; ++nl) {
+        const RowSrc &src = rows[nb * 16 + nl];
+        const uint8_t *rp = src.packed ? src.packed + src.row * (K / 2) : nullptr;
+        for (size_t g = 0; g < G; ++g) {
+          const size_t kq = g / 4, j = g % 4;
+          uint16_t sh = 0;
+          if (src.scales_f16) sh = src.scales_f16[src.row * G + g];
+          else if (src.scales_f32) sh = f32_to_f16(src.scales_f32[src.row * G + g]);
+          scales[((nb * KQ + kq) * 16 + nl) * 4 + j] = sh;
+          for (int c = 0; c < 4; ++c) {
+            uint32_t word = 0x77777777u;  // code 7 decodes to 0 for absent rows
+            if (rp) {
+              const uint8_t *b = rp + g * 16 + c * 4;  // columns 32g + 8c .. +8
+              uint8_t code[8];
+              for (int t = 0; t < 8; ++t) code[t] = (b[t / 2] >> (4 * (t & 1))) & 0xF;
+              word = 0;
+              for (int bb = 0; bb < 4; ++bb)
+                word |= (uint32_t)(code[bb] | (code[bb + 4] << 4)) << (8 * bb);
+            }
+            const size_t lane = (size_t)c * 16 + nl;
+            codes[((nb * KQ + kq) * 64 + lane) * 4 + j] = word;
+          }
+        }
+      }
+  }, 4);
+}
+
+glacier_hip_int4_weight *upload_weight(glacier_hip_context *ctx, uint32_t out_f, uint32_t in_f,
+                                       const std::vector<uint32_t> &codes,
+                                       const std::vector<uint16_t> &scales) {
+  auto *w = new glacier_hip_int4_weight();
+  w->ctx = ctx;
+  w->out_f = out_f;
+  w->in_f = in_f;
+  const size_t cb = codes.size() * 4, sb = scales.size() * 2;
+  if (hipMalloc(&w->codes, cb) != hipSuccess || hipMalloc(&w->scales, sb) != hipSuccess ||
+      hipMemcpy(w->codes, codes.data(), cb, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(w->scales, scales.data(), sb, hipMemcpyHostToDevice) != hipSuccess) {
+    ctx->last_error = "int4 weight upload failed";
+    if (w->codes) (void)hipFree(w->codes);
+    if (w->scales) (void)hipFree(w->scales);
+    delete w;
+    return nullptr;
+  }
+  w->device_bytes = cb + sb;
+  ctx->live_weights++;
+  return w;
+}
+
+int ensure_scratch(glacier_hip_context *ctx, size_t bytes, size_t counters) {
+  if (bytes > ctx->scratch_bytes) {
+    if (ctx->scratch) GH_CHECK(ctx, hipFree(ctx->scratch));
+    ctx->scratch = nullptr;
+    ctx->scratch_bytes = 0;
+    GH_CHECK(ctx, hipMalloc(&ctx->scratch, bytes));
+    ctx->scratch_bytes = bytes;
+  }
+  if (counters > ctx->counter_count) {
+    if (ctx->counters) GH_CHECK(ctx, hipFree(ctx->counters));
+    ctx->counters = nullptr;
+    ctx->counter_count = 0;
+    GH_CHECK(ctx, hipMalloc(&ctx->counters, counters * sizeof(uint32_t)));
+    GH_CHECK(ctx, hipMemset(ctx->counters, 0, counters * sizeof(uint32_t)));
+    ctx->counter_count = counters;
+  }
+  return GLACIER_HIP_OK;
+}
+
+}  // namespace gh
+
+extern "C" {
+
+uint64_t glacier_hip_abi_version(void) { return 0x4748495000000001ull; }
+
+static std::string g_init_error;
+
+glacier_hip_context *glacier_hip_init(int device_ordinal) {
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || device_ordinal < 0 || device_ordinal >= count) {
+    g_init_error = std::string("hipGetDeviceCount: ") + hipGetErrorString(e) +
+                   " count=" + std::to_string(count);
+    return nullptr;
+  }
+  if ((e = hipSetDevice(device_ordinal)) != hipSuccess) {
+    g_init_error = std::string("hipSetDevice: ") + hipGetErrorString(e);
+    return nullptr;
+  }
+  auto *ctx = new glacier_hip_context();
+  ctx->device = device_ordinal;
+  const char *what = "hipGetDeviceProperties";
+  e = hipGetDeviceProperties(&ctx->props, device_ordinal);
+  if (e == hipSuccess) {
+    what = "hipStreamCreateWithFlags";
+    e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+  }
+  if (e == hipSuccess) {
+    what = "hipHostMalloc";
+    e = hipHostMalloc((void **)&ctx->results_host, sizeof(gk::ArgmaxResult) * 64);
+  }
+  if (e != hipSuccess) {
+    g_init_error = std::string(what) + ": " + hipGetErrorString(e);
+    delete ctx;
+    return nullptr;
+  }
+  static uint64_t epoch_counter = 0x6c61636965720000ull;
+  ctx->epoch = ++epoch_counter;
+  return ctx;
+}
+
+int glacier_hip_deinit(glacier_hip_context *ctx) {
+  if (!ctx) return GLACIER_HIP_INVALID_HANDLE;
+  if (!ctx->buffers.empty() || ctx->live_weights != 0) return GLACIER_HIP_BUSY;
+  (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->scratch) (void)hipFree(ctx->scratch);
+  if (ctx->counters) (void)hipFree(ctx->counters);
+  if (ctx->results_host) (void)hipHostFree(ctx->results_host);
+  (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return GLACIER_HIP_OK;
+}
+
+const char *glacier_hip_last_error(glacier_hip_context *ctx) {
+  return ctx ? ctx->last_error.c_str() : g_init_error.c_str();
+}
+
+int glacier_hip_synchronize(glacier_hip_context *ctx) {
+  if (!ctx) return GLACIER_HIP_INVALID_HANDLE;
+  GH_CHECK(ctx, hipStreamSynchronize(ctx->stream));
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_device_info(glacier_hip_context *ctx, glacier_hip_device_info_t *out) {
+  if (!ctx || !out) return GLACIER_HIP_INVALID_ARGUMENT;
+  memset(out, 0, sizeof *out);
+  const hipDeviceProp_t &p = ctx->props;
+  snprintf(out->name, sizeof out->name, "%s", p.name);
+  snprintf(out->arch, sizeof out->arch, "%s", p.gcnArchName);
+  out->compute_units = (uint32_t)p.multiProcessorCount;
+  out->wavefront_size = (uint32_t)p.warpSize;
+  out->total_global_bytes = p.totalGlobalMem;
+  out->max_single_allocation_bytes = p.totalGlobalMem;
+  out->lds_bytes_per_block = (uint32_t)p.sharedMemPerBlock;
+  out->l2_bytes = (uint32_t)p.l2CacheSize;
+  out->clock_khz = (uint32_t)p.clockRate;
+  out->memory_clock_khz = (uint32_t)p.memoryClockRate;
+  out->memory_bus_width_bits = (uint32_t)p.memoryBusWidth;
+  out->device_ordinal = (uint32_t)ctx->device;
+  return GLACIER_HIP_OK;
+}
+
+static const uint64_t kGranularity = 2ull << 20;  // hipMalloc rounds large buffers to 2 MiB
+
+static uint64_t charged_size(uint64_t requested) {
+  if (requested == 0) return 0;
+  return (requested + kGranularity - 1) / kGranularity * kGranularity;
+}
+
+int glacier_hip_allocation_limits(glacier_hip_context *ctx, glacier_hip_allocation_limits_t *out) {
+  if (!ctx || !out) return GLACIER_HIP_INVALID_ARGUMENT;
+  out->max_single_allocation_bytes = ctx->props.totalGlobalMem;
+  out->max_total_device_bytes = ctx->props.totalGlobalMem;
+  out->allocation_granularity_bytes = kGranularity;
+  out->max_queue_slots = 1;
+  return GLACIER_HIP_OK;
+}
+
+// device_capability_contract.zig:331-350 capabilityRootV1
+static void capability_root(const glacier_hip_device_capability_v1_t &c, uint8_t out[32]) {
+  gh::Sha256 h;
+  h.update("glacier-device-capability-v1\0", 29);
+  h.u64(c.abi_version);
+  h.u64(c.backend_kind);
+  h.u64(c.device_class);
+  h.u64(c.operation_profile_bits);
+  h.u64(c.operator_bits);
+  h.u64(c.element_type_bits);
+  h.u64(c.numerical_policy_bits);
+  h.u64(c.feature_bits);
+  h.u64(c.max_single_allocation_bytes);
+  h.u64(c.max_total_device_bytes);
+  h.u64(c.max_queue_slots);
+  h.update(c.backend_sha256, 32);
+  h.update(c.device_sha256, 32);
+  h.update(c.driver_sha256, 32);
+  h.update(c.placement_sha256, 32);
+  h.final(out);
+}
+
+int glacier_hip_device_capability_v1(glacier_hip_context *ctx,
+                                     glacier_hip_device_capability_v1_t *out) {
+  if (!ctx || !out) return GLACIER_HIP_INVALID_ARGUMENT;
+  memset(out, 0, sizeof *out);
+  out->abi_version = 0x4744434100000001ull;
+  out->backend_kind = 3;  // portable_compute
+  out->device_class = 2;  // accelerator
+  // matvec_int4_f32_bounded profile: operator matvec_int4_f32, element
+  // types packed_int4 + float32, numerical policy bounded_float32.
+  out->operation_profile_bits = 1ull << 2;
+  out->operator_bits = 1ull << 2;
+  out->element_type_bits = (1ull << 0) | (1ull << 2);
+  out->numerical_policy_bits = 1ull << 1;
+  // allocation | dispatch | completion_fence | persistent_weights
+  out->feature_bits = (1ull << 0) | (1ull << 1) | (1ull << 2) | (1ull << 3);
+  out->max_single_allocation_bytes = ctx->props.totalGlobalMem;
+  out->max_total_device_bytes = ctx->props.totalGlobalMem;
+  out->max_queue_slots = 1;
+  {
+    gh::Sha256 h;
+    h.update("glacier-hip-backend-gfx950-v1", 29);
+    h.final(out->backend_sha256);
+  }
+  {
+    gh::Sha256 h;
+    h.update(ctx->props.name, strnlen(ctx->props.name, sizeof ctx->props.name));
+    h.update(ctx->props.gcnArchName, strnlen(ctx->props.gcnArchName, sizeof ctx->props.gcnArchName));
+    h.u64((uint64_t)ctx->props.multiProcessorCount);
+    h.u64((uint64_t)ctx->props.totalGlobalMem);
+    h.final(out->device_sha256);
+  }
+  {
+    int rt = 0, drv = 0;
+    (void)hipRuntimeGetVersion(&rt);
+    (void)hipDriverGetVersion(&drv);
+    gh::Sha256 h;
+    h.u64((uint64_t)rt);
+    h.u64((uint64_t)drv);
+    h.final(out->driver_sha256);
+  }
+  {
+    gh::Sha256 h;
+    h.update("hip-device-ordinal", 18);
+    h.u64((uint64_t)ctx->device);
+    h.u64((uint64_t)ctx->props.pciBusID);
+    h.final(out->placement_sha256);
+  }
+  capability_root(*out, out->capability_sha256);
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_buffer_create(glacier_hip_context *ctx, uint64_t requested_length,
+                              glacier_hip_buffer_token_t *out) {
+  glacier_hip_allocation_quote_t q;
+  int rc = glacier_hip_allocation_quote(ctx, requested_length, &q);
+  if (rc) return rc;
+  return glacier_hip_allocation_allocate(ctx, &q, out);
+}
+
+int glacier_hip_allocation_quote(glacier_hip_context *ctx, uint64_t requested_bytes,
+                                 glacier_hip_allocation_quote_t *out) {
+  if (!ctx || !out || requested_bytes == 0) return GLACIER_HIP_INVALID_ARGUMENT;
+  if (requested_bytes > ctx->props.totalGlobalMem) return GLACIER_HIP_OUT_OF_MEMORY;
+  out->requested_bytes = requested_bytes;
+  out->charged_bytes = charged_size(requested_bytes);
+  out->context_epoch = ctx->epoch;
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_allocation_allocate(glacier_hip_context *ctx,
+                                    const glacier_hip_allocation_quote_t *quote,
+                                    glacier_hip_buffer_token_t *out) {
+  if (!ctx || !quote || !out) return GLACIER_HIP_INVALID_ARGUMENT;
+  if (quote->context_epoch != ctx->epoch || quote->requested_bytes == 0 ||
+      quote->charged_bytes != charged_size(quote->requested_bytes))
+    return GLACIER_HIP_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  void *p = nullptr;
+  hipError_t e = hipMalloc(&p, quote->requested_bytes);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipMalloc");  // nothing was created
+  const uint64_t id = ctx->next_buffer_id++;
+  ctx->buffers[id] = {p, quote->requested_bytes, quote->charged_bytes};
+  out->id = id;
+  out->requested_bytes = quote->requested_bytes;
+  out->charged_bytes = quote->charged_bytes;
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_allocation_free(glacier_hip_context *ctx, const glacier_hip_buffer_token_t *token) {
+  return glacier_hip_buffer_release(ctx, token);
+}
+
+int glacier_hip_buffer_info(glacier_hip_context *ctx, const glacier_hip_buffer_token_t *token,
+                            glacier_hip_buffer_info_t *out) {
+  if (!ctx || !token || !out) return GLACIER_HIP_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  auto it = ctx->buffers.find(token->id);
+  if (it == ctx->buffers.end() || it->second.requested != token->requested_bytes)
+    return GLACIER_HIP_INVALID_HANDLE;
+  out->id = token->id;
+  out->requested_bytes = it->second.requested;
+  out->charged_bytes = it->second.charged;
+  out->device_address = (uint64_t)(uintptr_t)it->second.ptr;
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_buffer_release(glacier_hip_context *ctx, const glacier_hip_buffer_token_t *token) {
+  if (!ctx || !token) return GLACIER_HIP_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  auto it = ctx->buffers.find(token->id);
+  if (it == ctx->buffers.end() || it->second.requested != token->requested_bytes)
+    return GLACIER_HIP_INVALID_HANDLE;
+  hipError_t e = hipFree(it->second.ptr);
+  if (e != hipSuccess) return hip_fail(ctx, e, "hipFree");  // the buffer stays live
+  ctx->buffers.erase(it);
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_live_buffer_count(glacier_hip_context *ctx, uint64_t *out) {
+  if (!ctx || !out) return GLACIER_HIP_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  *out = ctx->buffers.size();
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_live_weight_count(glacier_hip_context *ctx, uint64_t *out) {
+  if (!ctx || !out) return GLACIER_HIP_INVALID_ARGUMENT;
+  *out = ctx->live_weights;
+  return GLACIER_HIP_OK;
+}
+
+// ---- INT4 weights ---------------------------------------------------------
+static glacier_hip_int4_weight *weight_create(glacier_hip_context *ctx, const uint8_t *packed,
+                                              uint64_t packed_bytes, const float *s32,
+                                              const uint16_t *s16, uint64_t scale_count,
+                                              uint32_t group, uint32_t in_f, uint32_t out_f) {
+  if (!ctx || !packed || (!s32 && !s16)) return nullptr;
+  if (group != 32 || out_f == 0 || in_f == 0 || out_f % 16 != 0 || in_f % 128 != 0) {
+    ctx->last_error = "int4 weight: need group 32, out_f % 16 == 0, in_f % 128 == 0";
+    return nullptr;
+  }
+  const uint64_t n = (uint64_t)out_f * in_f;
+  if (packed_bytes < n / 2 || scale_count < n / group) {
+    ctx->last_error = "int4 weight: truncated packed bytes or scales";
+    return nullptr;
+  }
+  std::vector<gh::RowSrc> rows(out_f);
+  for (uint32_t r = 0; r < out_f; ++r) rows[r] = {packed, s32, s16, r};
+  std::vector<uint32_t> codes;
+  std::vector<uint16_t> scales;
+  gh::repack_tiles(rows, in_f, codes, scales);
+  auto *w = gh::upload_weight(ctx, out_f, in_f, codes, scales);
+  if (w) w->group = group;
+  return w;
+}
+
+glacier_hip_int4_weight *glacier_hip_int4_weight_create(glacier_hip_context *ctx,
+                                                        const uint8_t *packed,
+                                                        uint64_t packed_bytes,
+                                                        const float *scales, uint64_t scale_count,
+                                                        uint32_t group_size, uint32_t in_features,
+                                                        uint32_t out_features) {
+  return weight_create(ctx, packed, packed_bytes, scales, nullptr, scale_count, group_size,
+                       in_features, out_features);
+}
+
+glacier_hip_int4_weight *glacier_hip_int4_weight_create_f16scales(
+    glacier_hip_context *ctx, const uint8_t *packed, uint64_t packed_bytes,
+    const uint16_t *scales_f16, uint64_t scale_count, uint32_t group_size, uint32_t in_features,
+    uint32_t out_features) {
+  return weight_create(ctx, packed, packed_bytes, nullptr, scales_f16, scale_count, group_size,
+                       in_features, out_features);
+}
+
+void glacier_hip_int4_weight_destroy(glacier_hip_int4_weight *w) {
+  if (!w) return;
+  if (w->codes) (void)hipFree(w->codes);
+  if (w->scales) (void)hipFree(w->scales);
+  if (w->ctx && w->ctx->live_weights) w->ctx->live_weights--;
+  delete w;
+}
+
+uint64_t glacier_hip_int4_weight_device_bytes(const glacier_hip_int4_weight *w) {
+  return w ? w->device_bytes : 0;
+}
+
+static int gemv_common(glacier_hip_context *ctx, glacier_hip_int4_weight *w, const void *x_dev,
+                       int x_dtype, uint32_t m, const float *bias_dev, float *y_dev,
+                       int activation, hipStream_t st) {
+  if (!ctx || !w || !x_dev || !y_dev) return GLACIER_HIP_INVALID_ARGUMENT;
+  if (w->ctx != ctx) return GLACIER_HIP_INVALID_HANDLE;
+  if (m == 0 || m > 32) return GLACIER_HIP_SHAPE_MISMATCH;
+  if (x_dtype != GLACIER_HIP_F32 && x_dtype != GLACIER_HIP_BF16) return GLACIER_HIP_DTYPE_UNSUPPORTED;
+  const int act = gh::resolve_activation(activation, w->out_f, w->in_f);
+  if (act != GLACIER_HIP_ACT_Q8 && act != GLACIER_HIP_ACT_F32) return GLACIER_HIP_INVALID_ARGUMENT;
+  const int D = act == GLACIER_HIP_ACT_Q8 ? 1 : 3;
+  const int N = (int)w->out_f, K = (int)w->in_f;
+  const int NB = N / 16, KQ = K / 128, G = K / 32;
+  const int S = gk::choose_splits(NB, KQ, (int)m);
+  const size_t q_bytes = (size_t)G * D * m * 32;
+  const size_t meta_bytes = (size_t)G * m * sizeof(gk::ActMeta);
+  const size_t part_bytes = S > 1 ? (size_t)S * m * N * sizeof(float) : 0;
+  auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+  int rc = gh::ensure_scratch(ctx, al(q_bytes) + al(meta_bytes) + al(part_bytes), (size_t)NB);
+  if (rc) return rc;
+  char *base = (char *)ctx->scratch;
+  gk::GemvArgs a{};
+  a.codes = w->codes;
+  a.scales = w->scales;
+  a.N = N;
+  a.K = K;
+  a.act_q = (int8_t *)base;
+  a.act_meta = (gk::ActMeta *)(base + al(q_bytes));
+  a.M = (int)m;
+  a.D = D;
+  a.bias = bias_dev;
+  a.y = y_dev;
+  a.S = S;
+  a.partial = (float *)(base + al(q_bytes) + al(meta_bytes));
+  a.counters = ctx->counters;
+  a.epi = gk::EPI_PLAIN;
+  GH_CHECK(ctx, gk::launch_prep_act(x_dev, x_dtype == GLACIER_HIP_BF16, nullptr, 0.0f, (int)m, K,
+                                    D, (int8_t *)a.act_q, (gk::ActMeta *)a.act_meta, nullptr, st));
+  GH_CHECK(ctx, gk::launch_gemv(a, st));
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_int4_gemv(glacier_hip_context *ctx, glacier_hip_int4_weight *w, const void *x_dev,
+                          int x_dtype, uint32_t m, const float *bias_dev, float *y_dev,
+                          int activation, void *stream) {
+  if (!ctx) return GLACIER_HIP_INVALID_HANDLE;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  return gemv_common(ctx, w, x_dev, x_dtype, m, bias_dev, y_dev, activation,
+                     stream ? (hipStream_t)stream : ctx->stream);
+}
+
+int glacier_hip_int4_matvec_dispatch(glacier_hip_context *ctx, glacier_hip_int4_weight *w,
+                                     const float *input, uint64_t input_count, float *output,
+                                     uint64_t output_count) {
+  if (!ctx || !w || !input || !output) return GLACIER_HIP_INVALID_ARGUMENT;
+  if (input_count != w->in_f || output_count != w->out_f) return GLACIER_HIP_SHAPE_MISMATCH;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  float *xd = nullptr, *yd = nullptr;
+  GH_CHECK(ctx, hipMalloc(&xd, input_count * 4));
+  hipError_t e = hipMalloc(&yd, output_count * 4);
+  if (e != hipSuccess) {
+    (void)hipFree(xd);
+    return hip_fail(ctx, e, "hipMalloc");
+  }
+  int rc = GLACIER_HIP_OK;
+  e = hipMemcpyAsync(xd, input, input_count * 4, hipMemcpyHostToDevice, ctx->stream);
+  if (e != hipSuccess) rc = hip_fail(ctx, e, "copy in");
+  if (!rc) rc = gemv_common(ctx, w, xd, GLACIER_HIP_F32, 1, nullptr, yd, GLACIER_HIP_ACT_F32, ctx->stream);
+  if (!rc) {
+    e = hipMemcpyAsync(output, yd, output_count * 4, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) rc = hip_fail(ctx, e, "copy out");
+  }
+  (void)hipFree(xd);
+  (void)hipFree(yd);
+  return rc;
+}
+
+int glacier_hip_rmsnorm(glacier_hip_context *ctx, const float *x_dev, const float *w_dev,
+                        uint32_t rows, uint32_t dim, float eps, float *out_dev, void *stream) {
+  if (!ctx || !x_dev || !w_dev || !out_dev) return GLACIER_HIP_INVALID_ARGUMENT;
+  if (rows == 0 || dim == 0) return GLACIER_HIP_SHAPE_MISMATCH;
+  GH_CHECK(ctx, gk::launch_rmsnorm(x_dev, w_dev, (int)rows, (int)dim, eps, out_dev,
+                                   stream ? (hipStream_t)stream : ctx->stream));
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_paged_attention(glacier_hip_context *ctx, const float *q_dev,
+                                const void *kv_pool_dev, int kv_dtype,
+                                const int32_t *page_table_dev, uint32_t max_pages_per_lane,
+                                const int32_t *ctx_lens_dev, uint32_t lanes, uint32_t layer,
+                                uint32_t num_layers, uint32_t num_heads, uint32_t num_kv_heads,
+                                uint32_t head_dim, uint32_t max_ctx, float *out_dev,
+                                void *stream) {
+  if (!ctx || !q_dev || !kv_pool_dev || !page_table_dev || !ctx_lens_dev || !out_dev)
+    return GLACIER_HIP_INVALID_ARGUMENT;
+  if (kv_dtype != GLACIER_HIP_F32 && kv_dtype != GLACIER_HIP_F16) return GLACIER_HIP_DTYPE_UNSUPPORTED;
+  if (lanes == 0 || lanes > 64 || num_kv_heads == 0 || num_heads % num_kv_heads != 0 ||
+      num_heads / num_kv_heads > 8 || (head_dim != 64 && head_dim != 128) ||
+      layer >= num_layers || max_ctx == 0 || (max_ctx + 15) / 16 > max_pages_per_lane)
+    return GLACIER_HIP_SHAPE_MISMATCH;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
+  // lane_of_row = identity: row i attends with page-table row i
+  const size_t sc = gk::attention_scratch_floats((int)lanes, (int)num_heads, (int)head_dim, (int)max_ctx);
+  int rc = gh::ensure_scratch(ctx, sc * 4 + 256 + lanes * 4, 1);
+  if (rc) return rc;
+  int32_t *ident = (int32_t *)((char *)ctx->scratch + ((sc * 4 + 255) & ~(size_t)255));
+  std::vector<int32_t> h(lanes);
+  for (uint32_t i = 0; i < lanes; ++i) h[i] = (int32_t)i;
+  GH_CHECK(ctx, hipMemcpyAsync(ident, h.data(), lanes * 4, hipMemcpyHostToDevice, st));
+  GH_CHECK(ctx, gk::launch_attention(q_dev, kv_pool_dev, kv_dtype == GLACIER_HIP_F16, page_table_dev,
+                                     (int)max_pages_per_lane, ident, ctx_lens_dev, (int)lanes,
+                                     (int)layer, (int)num_layers, (int)num_heads,
+                                     (int)num_kv_heads, (int)head_dim, (int)max_ctx,
+                                     (float *)ctx->scratch, out_dev, st));
+  // `h` must outlive the async copy
+  GH_CHECK(ctx, hipStreamSynchronize(st));
+  return GLACIER_HIP_OK;
+}
+
+static int argmax_common(glacier_hip_context *ctx, const float *logits_dev, uint64_t n,
+                         const uint64_t *words_dev, uint64_t word_count, uint32_t rows,
+                         glacier_hip_argmax_result_t *out, hipStream_t st) {
+  if (!ctx || !logits_dev || !out) return GLACIER_HIP_INVALID_ARGUMENT;
+  if (rows == 0 || rows > 64) return GLACIER_HIP_SHAPE_MISMATCH;
+  if (words_dev) {
+    const uint64_t wc = n / 64 + (n % 64 != 0);
+    if (wc == 0 || word_count != wc) {
+      for (uint32_t r = 0; r < rows; ++r) out[r] = {0, 0, GLACIER_HIP_INVALID_MASK, 0};
+      return GLACIER_HIP_INVALID_MASK;
+    }
+  } else if (n == 0) {
+    return GLACIER_HIP_SHAPE_MISMATCH;
+  }
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  const size_t sb = gk::argmax_scratch_bytes((int)rows, (long)n);
+  int rc = gh::ensure_scratch(ctx, sb + 256 + rows * sizeof(gk::ArgmaxResult), rows);
+  if (rc) return rc;
+  auto *res_dev = (gk::ArgmaxResult *)((char *)ctx->scratch + ((sb + 255) & ~(size_t)255));
+  GH_CHECK(ctx, gk::launch_argmax(logits_dev, (long)n, (int)rows, words_dev, (long)word_count,
+                                  ctx->scratch, ctx->counters, res_dev, st));
+  GH_CHECK(ctx, hipMemcpyAsync(ctx->results_host, res_dev, rows * sizeof(gk::ArgmaxResult),
+                               hipMemcpyDeviceToHost, st));
+  GH_CHECK(ctx, hipStreamSynchronize(st));
+  int status = GLACIER_HIP_OK;
+  for (uint32_t r = 0; r < rows; ++r) {
+    const gk::ArgmaxResult &g = ctx->results_host[r];
+    out[r].token_index = g.index;
+    out[r].eligible_rows = g.eligible_rows;
+    out[r].status = g.status;
+    out[r].reserved = 0;
+    if (g.status && !status) status = g.status;
+  }
+  return status;
+}
+
+int glacier_hip_argmax(glacier_hip_context *ctx, const float *logits_dev, uint64_t n,
+                       uint32_t rows, uint64_t *index_host, void *stream) {
+  if (!index_host) return GLACIER_HIP_INVALID_ARGUMENT;
+  std::vector<glacier_hip_argmax_result_t> r(rows ? rows : 1);
+  int rc = argmax_common(ctx, logits_dev, n, nullptr, 0, rows, r.data(),
+                         stream ? (hipStream_t)stream : (ctx ? ctx->stream : nullptr));
+  if (rc) return rc;
+  for (uint32_t i = 0; i < rows; ++i) index_host[i] = r[i].token_index;
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_eligible_argmax(glacier_hip_context *ctx, const float *logits_dev, uint64_t n,
+                                const uint64_t *words_dev, uint64_t word_count, uint32_t rows,
+                                glacier_hip_argmax_result_t *results_host, void *stream) {
+  if (!words_dev) return GLACIER_HIP_INVALID_ARGUMENT;
+  return argmax_common(ctx, logits_dev, n, words_dev, word_count, rows, results_host,
+                       stream ? (hipStream_t)stream : (ctx ? ctx->stream : nullptr));
+}
+
+// ---- synthetic generator ----------------------------------------------------
+static inline uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+static inline uint64_t stream_key(uint64_t seed, uint64_t tensor_id) {
+  return mix64(seed ^ mix64(tensor_id + 0x632be59bd9b4e019ull));
+}
+static inline uint64_t stream_at(uint64_t key, uint64_t i) {
+  return mix64(key + (i + 1) * 0x9e3779b97f4a7c15ull);
+}
+// Box-Muller pair from stream values 2i and 2i+1, in double precision.
+static inline void normal_pair(uint64_t key, uint64_t i, double *z0, double *z1) {
+  const double u1 = (double)((stream_at(key, 2 * i) >> 11) + 1) * 0x1.0p-53;
+  const double u2 = (double)(stream_at(key, 2 * i + 1) >> 11) * 0x1.0p-53;
+  const double r = sqrt(-2.0 * log(u1));
+  const double a = 6.283185307179586 * u2;
+  *z0 = r * cos(a);
+  *z1 = r * sin(a);
+}
+
+void glacier_hip_synth_int4(uint64_t seed, uint64_t tensor_id, uint8_t *packed, uint64_t bytes) {
+  const uint64_t key = stream_key(seed, tensor_id);
+  const uint64_t words = bytes / 8;
+  gh::parallel_for(words, [&](size_t b, size_t e) {
+    for (size_t i = b; i < e; ++i) {
+      const uint64_t v = stream_at(key, i);
+      memcpy(packed + 8 * i, &v, 8);
+    }
+  }, 1 << 16);
+  if (bytes % 8) {
+    const uint64_t v = stream_at(key, words);
+    memcpy(packed + 8 * words, &v, bytes % 8);
+  }
+}
+
+void glacier_hip_synth_scales_f16(uint64_t seed, uint64_t tensor_id, float sigma, uint16_t *out,
+                                  uint64_t count) {
+  const uint64_t key = stream_key(seed, tensor_id);
+  gh::parallel_for((count + 1) / 2, [&](size_t b, size_t e) {
+    for (size_t i = b; i < e; ++i) {
+      double z0, z1;
+      normal_pair(key, i, &z0, &z1);
+      out[2 * i] = gh::f32_to_f16(fabsf((float)(sigma * z0)));
+      if (2 * i + 1 < count) out[2 * i + 1] = gh::f32_to_f16(fabsf((float)(sigma * z1)));
+    }
+  }, 1 << 14);
+}
+
+void glacier_hip_synth_normal_f32(uint64_t seed, uint64_t tensor_id, float sigma, float *out,
+                                  uint64_t count) {
+  const uint64_t key = stream_key(seed, tensor_id);
+  gh::parallel_for((count + 1) / 2, [&](size_t b, size_t e) {
+    for (size_t i = b; i < e; ++i) {
+      double z0, z1;
+      normal_pair(key, i, &z0, &z1);
+      out[2 * i] = (float)(sigma * z0);
+      if (2 * i + 1 < count) out[2 * i + 1] = (float)(sigma * z1);
+    }
+  }, 1 << 14);
+}
+
+void glacier_hip_synth_tokens(uint64_t seed, uint64_t tensor_id, uint32_t vocab, uint32_t *out,
+                              uint64_t count) {
+  const uint64_t key = stream_key(seed, tensor_id);
+  for (uint64_t i = 0; i < count; ++i) out[i] = (uint32_t)(stream_at(key, i) % vocab);
+}
+
+uint64_t glacier_hip_synth_tensor_id(uint32_t layer, uint32_t which) {
+  return ((uint64_t)layer + 1) << 8 | which;
+}
+
+float glacier_hip_f16_to_f32(uint16_t h) { return gh::f16_to_f32(h); }
+
+}  // extern "C"

@@ -1,0 +1,942 @@
+// session.hip — model + session: the per-token decode step over paged KV.
+//
+// Host-side semantics restated from the reference:
+//  * layer composition  generate.zig:1511-1967 (forwardLayerCached)
+//  * token loop         generate.zig:4665-5613 (prefill one token at a time,
+//                       then greedy decode; first token from the prompt logits)
+//  * paged KV pages     paged_kv_cache.zig:1006-1160 (beginRow installs a page
+//                       at row 0 with ownership_generation = next++, the root
+//                       digest chain appendOwnershipDigest :341-353, commit /
+//                       abort of the row transaction)
+//  * digests            generate.zig:3150-3203
+//  * RNG                std.Random.DefaultPrng.init(seed) (generate.zig:5221)
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+
+#include "host_util.h"
+#include "runtime.h"
+
+using gh::hip_fail;
+
+namespace {
+
+constexpr uint64_t kPageRefAbi = 0x4750524600000001ull;
+
+struct LayerDev {
+  float *in_norm = nullptr, *post_norm = nullptr, *qkv_bias = nullptr;
+  glacier_hip_int4_weight *qkv = nullptr, *o = nullptr, *gu = nullptr, *down = nullptr;
+};
+
+void emptyOwnershipDigest(uint64_t inst, uint64_t L, uint64_t dim, uint64_t max_seq,
+                          uint8_t out[32]) {
+  // paged_kv_cache.zig:323-338
+  gh::Sha256 h;
+  h.update("glacier-paged-kv-ownership-v1\0", 30);
+  h.u64(inst);
+  h.u64(L);
+  h.u64(dim);
+  h.u64(max_seq);
+  h.u64(16);
+  h.final(out);
+}
+
+void appendOwnershipDigest(const uint8_t before[32], uint64_t inst, uint64_t page, uint64_t gen,
+                           uint8_t out[32]) {
+  // paged_kv_cache.zig:341-353
+  gh::Sha256 h;
+  h.update("glacier-paged-kv-root-append-v1\0", 32);
+  h.update(before, 32);
+  h.u64(kPageRefAbi);
+  h.u64(inst);
+  h.u64(page);
+  h.u64(gen);
+  h.final(out);
+}
+
+uint64_t g_next_cache_instance = 1;  // reserveCacheInstance (process-local, nonzero)
+
+}  // namespace
+
+struct glacier_hip_model {
+  glacier_hip_context *ctx = nullptr;
+  glacier_hip_model_config_t cfg{};
+  std::vector<LayerDev> layers;
+  std::vector<bool> layer_set;
+  bool globals_set = false;
+  float *embed = nullptr, *final_norm = nullptr;
+  glacier_hip_int4_weight *head = nullptr;
+  uint64_t bytes = 0;
+};
+
+struct Lane {
+  bool active = false;
+  uint64_t instance = 0;
+  uint64_t len = 0;
+  std::vector<int32_t> page_of;   // logical page -> physical page, -1 = none
+  std::vector<uint64_t> page_gen; // ownership generation
+  uint64_t next_page_generation = 1;
+  uint64_t next_root_generation = 2;
+  glacier_hip_page_map_root_t root{};
+  uint64_t sampling_calls = 0;
+  uint64_t rng[4] = {0, 0, 0, 0};
+  std::vector<uint32_t> output;
+};
+
+struct StepInputs {  // uploaded once per step, in one copy
+  int32_t tokens[64];
+  int32_t lane_of_row[64];
+  int32_t pos_of_row[64];
+  int32_t ctx_len[64];
+};
+
+struct glacier_hip_session {
+  glacier_hip_model *model = nullptr;
+  glacier_hip_session_options_t opt{};
+  uint32_t max_pages = 0;  // per lane
+  uint32_t total_pages = 0;
+  std::vector<int32_t> free_pages;
+  std::vector<Lane> lanes;
+  // device
+  void *kv_pool = nullptr;
+  int32_t *page_table = nullptr;
+  float *rope_cos = nullptr, *rope_sin = nullptr;
+  float *x_res = nullptr, *h = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr,
+        *logits = nullptr;
+  int8_t *act_q = nullptr;
+  gk::ActMeta *act_meta = nullptr;
+  float *partial = nullptr;
+  uint32_t *counters = nullptr;
+  float *att_scratch = nullptr;
+  void *arg_scratch = nullptr;
+  uint32_t *arg_counters = nullptr;
+  gk::ArgmaxResult *arg_result = nullptr;
+  uint64_t *elig_words = nullptr;
+  StepInputs *step_dev = nullptr;
+  // host pinned
+  StepInputs *step_host = nullptr;
+  gk::ArgmaxResult *res_host = nullptr;
+  bool inject_failure = false;
+  // graph cache: key = (rows, with_head, eligible)
+  struct GraphEntry {
+    uint32_t rows;
+    bool head, elig;
+    hipGraphExec_t exec;
+  };
+  std::vector<GraphEntry> graphs;
+};
+
+// ---------------------------------------------------------------------------
+// model
+// ---------------------------------------------------------------------------
+static int upload_f32(glacier_hip_context *ctx, float **dst, const float *src, size_t n) {
+  if (!*dst) GH_CHECK(ctx, hipMalloc(dst, n * 4));
+  if (src) GH_CHECK(ctx, hipMemcpy(*dst, src, n * 4, hipMemcpyHostToDevice));
+  else GH_CHECK(ctx, hipMemset(*dst, 0, n * 4));
+  return GLACIER_HIP_OK;
+}
+
+extern "C" {
+
+glacier_hip_model *glacier_hip_model_create(glacier_hip_context *ctx,
+                                            const glacier_hip_model_config_t *cfg) {
+  if (!ctx || !cfg) return nullptr;
+  const auto &c = *cfg;
+  if (c.num_layers == 0 || c.dim == 0 || c.hidden_dim == 0 || c.num_heads == 0 ||
+      c.num_kv_heads == 0 || c.num_heads % c.num_kv_heads != 0 ||
+      c.num_heads / c.num_kv_heads > 8 || (c.head_dim != 64 && c.head_dim != 128) ||
+      c.dim % 128 != 0 || c.hidden_dim % 128 != 0 || c.vocab_size % 16 != 0 ||
+      c.group_size != 32 || c.num_heads * c.head_dim != c.dim) {
+    ctx->last_error = "model config unsupported";
+    return nullptr;
+  }
+  auto *m = new glacier_hip_model();
+  m->ctx = ctx;
+  m->cfg = c;
+  m->layers.resize(c.num_layers);
+  m->layer_set.assign(c.num_layers, false);
+  return m;
+}
+
+static int set_layer_impl(glacier_hip_model *m, uint32_t li, const glacier_hip_layer_host_t &w,
+                          const uint16_t *s16[7]) {
+  glacier_hip_context *ctx = m->ctx;
+  const auto &c = m->cfg;
+  const uint32_t D = c.dim, F = c.hidden_dim, hd = c.head_dim;
+  const uint32_t kvd = c.num_kv_heads * hd;
+  LayerDev &L = m->layers[li];
+  int rc;
+  if ((rc = upload_f32(ctx, &L.in_norm, w.input_norm, D))) return rc;
+  if ((rc = upload_f32(ctx, &L.post_norm, w.post_attn_norm, D))) return rc;
+  auto src = [&](const uint8_t *p, const float *s32, int idx, uint64_t row) {
+    return gh::RowSrc{p, s32, s16 ? s16[idx] : nullptr, row};
+  };
+  // fused QKV: q and k rows grouped as RoPE pairs (p, p + hd/2), 8 pairs per block
+  std::vector<gh::RowSrc> rows;
+  rows.reserve(D + 2 * kvd);
+  auto add_rope_rows = [&](const uint8_t *p, const float *s32, int idx, uint32_t heads) {
+    for (uint32_t h = 0; h < heads; ++h)
+      for (uint32_t b = 0; b < hd / 16; ++b) {
+        for (uint32_t i = 0; i < 8; ++i) rows.push_back(src(p, s32, idx, h * hd + 8 * b + i));
+        for (uint32_t i = 0; i < 8; ++i)
+          rows.push_back(src(p, s32, idx, h * hd + 8 * b + i + hd / 2));
+      }
+  };
+  add_rope_rows(w.wq, w.sq, 0, c.num_heads);
+  add_rope_rows(w.wk, w.sk, 1, c.num_kv_heads);
+  for (uint32_t r = 0; r < kvd; ++r) rows.push_back(src(w.wv, w.sv, 2, r));
+  std::vector<uint32_t> codes;
+  std::vector<uint16_t> scales;
+  auto build = [&](glacier_hip_int4_weight **dst, uint32_t K) -> int {
+    gh::repack_tiles(rows, K, codes, scales);
+    if (*dst) glacier_hip_int4_weight_destroy(*dst);
+    *dst = gh::upload_weight(ctx, (uint32_t)rows.size(), K, codes, scales);
+    return *dst ? GLACIER_HIP_OK : GLACIER_HIP_OUT_OF_MEMORY;
+  };
+  if ((rc = build(&L.qkv, D))) return rc;
+  if (w.bq || w.bk || w.bv) {
+    std::vector<float> b(D + 2 * kvd, 0.0f);
+    if (w.bq) memcpy(b.data(), w.bq, D * 4);
+    if (w.bk) memcpy(b.data() + D, w.bk, kvd * 4);
+    if (w.bv) memcpy(b.data() + D + kvd, w.bv, kvd * 4);
+    if ((rc = upload_f32(ctx, &L.qkv_bias, b.data(), b.size()))) return rc;
+  }
+  rows.clear();
+  for (uint32_t r = 0; r < D; ++r) rows.push_back(src(w.wo, w.so, 3, r));
+  if ((rc = build(&L.o, D))) return rc;
+  // fused gate/up: rows 0..7 gate 8b..8b+7, rows 8..15 up 8b..8b+7
+  rows.clear();
+  for (uint32_t b = 0; b < F / 8; ++b) {
+    for (uint32_t i = 0; i < 8; ++i) rows.push_back(src(w.w_gate, w.s_gate, 4, 8 * b + i));
+    for (uint32_t i = 0; i < 8; ++i) rows.push_back(src(w.w_up, w.s_up, 5, 8 * b + i));
+  }
+  if ((rc = build(&L.gu, D))) return rc;
+  rows.clear();
+  for (uint32_t r = 0; r < D; ++r) rows.push_back(src(w.w_down, w.s_down, 6, r));
+  if ((rc = build(&L.down, F))) return rc;
+  m->layer_set[li] = true;
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_model_set_layer(glacier_hip_model *m, uint32_t layer,
+                                const glacier_hip_layer_host_t *w) {
+  if (!m || !w) return GLACIER_HIP_INVALID_ARGUMENT;
+  if (layer >= m->cfg.num_layers) return GLACIER_HIP_SHAPE_MISMATCH;
+  if (!w->wq || !w->wk || !w->wv || !w->wo || !w->w_gate || !w->w_up || !w->w_down || !w->sq ||
+      !w->sk || !w->sv || !w->so || !w->s_gate || !w->s_up || !w->s_down || !w->input_norm ||
+      !w->post_attn_norm)
+    return GLACIER_HIP_INVALID_ARGUMENT;
+  return set_layer_impl(m, layer, *w, nullptr);
+}
+
+int glacier_hip_model_set_globals(glacier_hip_model *m, const float *token_embedding,
+                                  const float *final_norm, const uint8_t *lm_head_packed,
+                                  const float *lm_head_scales) {
+  if (!m || !token_embedding || !final_norm || !lm_head_packed || !lm_head_scales)
+    return GLACIER_HIP_INVALID_ARGUMENT;
+  const auto &c = m->cfg;
+  int rc;
+  if ((rc = upload_f32(m->ctx, &m->embed, token_embedding, (size_t)c.vocab_size * c.dim))) return rc;
+  if ((rc = upload_f32(m->ctx, &m->final_norm, final_norm, c.dim))) return rc;
+  if (m->head) glacier_hip_int4_weight_destroy(m->head);
+  m->head = glacier_hip_int4_weight_create(m->ctx, lm_head_packed, (uint64_t)c.vocab_size * c.dim / 2,
+                                           lm_head_scales, (uint64_t)c.vocab_size * c.dim / 32, 32,
+                                           c.dim, c.vocab_size);
+  if (!m->head) return GLACIER_HIP_OUT_OF_MEMORY;
+  m->globals_set = true;
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_model_init_random(glacier_hip_model *m, uint64_t seed) {
+  if (!m) return GLACIER_HIP_INVALID_ARGUMENT;
+  const auto &c = m->cfg;
+  const uint32_t D = c.dim, F = c.hidden_dim, kvd = c.num_kv_heads * c.head_dim, V = c.vocab_size;
+  const float sigma = 0.02f;
+  std::vector<float> n1(D), n2(D);
+  std::vector<uint8_t> wq((size_t)D * D / 2), wk((size_t)kvd * D / 2), wv((size_t)kvd * D / 2),
+      wo((size_t)D * D / 2), wg((size_t)F * D / 2), wu((size_t)F * D / 2), wd((size_t)D * F / 2);
+  std::vector<uint16_t> sq((size_t)D * D / 32), sk((size_t)kvd * D / 32), sv((size_t)kvd * D / 32),
+      so((size_t)D * D / 32), sg((size_t)F * D / 32), su((size_t)F * D / 32), sd((size_t)D * F / 32);
+  for (uint32_t l = 0; l < c.num_layers; ++l) {
+    auto id = [&](uint32_t which) { return glacier_hip_synth_tensor_id(l, which); };
+    glacier_hip_synth_normal_f32(seed, id(0), sigma, n1.data(), D);
+    glacier_hip_synth_normal_f32(seed, id(1), sigma, n2.data(), D);
+    uint8_t *ws[7] = {wq.data(), wk.data(), wv.data(), wo.data(), wg.data(), wu.data(), wd.data()};
+    size_t wb[7] = {wq.size(), wk.size(), wv.size(), wo.size(), wg.size(), wu.size(), wd.size()};
+    uint16_t *ss[7] = {sq.data(), sk.data(), sv.data(), so.data(), sg.data(), su.data(), sd.data()};
+    size_t sn[7] = {sq.size(), sk.size(), sv.size(), so.size(), sg.size(), su.size(), sd.size()};
+    for (int i = 0; i < 7; ++i) {
+      glacier_hip_synth_int4(seed, id(2 + 2 * i), ws[i], wb[i]);
+      glacier_hip_synth_scales_f16(seed, id(3 + 2 * i), sigma, ss[i], sn[i]);
+    }
+    glacier_hip_layer_host_t w{};
+    w.input_norm = n1.data();
+    w.post_attn_norm = n2.data();
+    w.wq = wq.data(); w.wk = wk.data(); w.wv = wv.data(); w.wo = wo.data();
+    w.w_gate = wg.data(); w.w_up = wu.data(); w.w_down = wd.data();
+    const uint16_t *s16[7] = {sq.data(), sk.data(), sv.data(), so.data(), sg.data(), su.data(), sd.data()};
+    int rc = set_layer_impl(m, l, w, s16);
+    if (rc) return rc;
+  }
+  const uint32_t G = 0xFFFFFF;
+  std::vector<float> emb((size_t)V * D), fn(D);
+  glacier_hip_synth_normal_f32(seed, glacier_hip_synth_tensor_id(G, 20), sigma, emb.data(), emb.size());
+  glacier_hip_synth_normal_f32(seed, glacier_hip_synth_tensor_id(G, 21), sigma, fn.data(), D);
+  std::vector<uint8_t> hp((size_t)V * D / 2);
+  std::vector<uint16_t> hs((size_t)V * D / 32);
+  glacier_hip_synth_int4(seed, glacier_hip_synth_tensor_id(G, 22), hp.data(), hp.size());
+  glacier_hip_synth_scales_f16(seed, glacier_hip_synth_tensor_id(G, 23), sigma, hs.data(), hs.size());
+  int rc;
+  if ((rc = upload_f32(m->ctx, &m->embed, emb.data(), emb.size()))) return rc;
+  if ((rc = upload_f32(m->ctx, &m->final_norm, fn.data(), D))) return rc;
+  if (m->head) glacier_hip_int4_weight_destroy(m->head);
+  m->head = glacier_hip_int4_weight_create_f16scales(m->ctx, hp.data(), hp.size(), hs.data(),
+                                                     hs.size(), 32, D, V);
+  if (!m->head) return GLACIER_HIP_OUT_OF_MEMORY;
+  m->globals_set = true;
+  return GLACIER_HIP_OK;
+}
+
+void glacier_hip_model_destroy(glacier_hip_model *m) {
+  if (!m) return;
+  for (auto &L : m->layers) {
+    if (L.in_norm) (void)hipFree(L.in_norm);
+    if (L.post_norm) (void)hipFree(L.post_norm);
+    if (L.qkv_bias) (void)hipFree(L.qkv_bias);
+    glacier_hip_int4_weight_destroy(L.qkv);
+    glacier_hip_int4_weight_destroy(L.o);
+    glacier_hip_int4_weight_destroy(L.gu);
+    glacier_hip_int4_weight_destroy(L.down);
+  }
+  if (m->embed) (void)hipFree(m->embed);
+  if (m->final_norm) (void)hipFree(m->final_norm);
+  glacier_hip_int4_weight_destroy(m->head);
+  delete m;
+}
+
+uint64_t glacier_hip_model_weight_bytes(const glacier_hip_model *m) {
+  if (!m) return 0;
+  uint64_t b = 0;
+  for (const auto &L : m->layers)
+    b += glacier_hip_int4_weight_device_bytes(L.qkv) + glacier_hip_int4_weight_device_bytes(L.o) +
+         glacier_hip_int4_weight_device_bytes(L.gu) + glacier_hip_int4_weight_device_bytes(L.down);
+  return b + glacier_hip_int4_weight_device_bytes(m->head);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// session
+// ---------------------------------------------------------------------------
+namespace {
+
+struct GemvPlan {
+  int S;
+};
+
+int layer_D(const glacier_hip_session *s, uint32_t out_f, uint32_t in_f) {
+  return gh::resolve_activation(s->opt.layer_activation, out_f, in_f) == GLACIER_HIP_ACT_Q8 ? 1 : 3;
+}
+
+int head_D(const glacier_hip_session *s) {
+  const auto &c = s->model->cfg;
+  return gh::resolve_activation(s->opt.head_activation, c.vocab_size, c.dim) == GLACIER_HIP_ACT_Q8 ? 1 : 3;
+}
+
+hipError_t run_proj(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, int rows,
+                    const float *x, const float *norm_w, int epi, const float *bias, float *y,
+                    const float *resid, hipStream_t st) {
+  const auto &c = s->model->cfg;
+  hipError_t e = gk::launch_prep_act(x, 0, norm_w, c.rms_eps, rows, (int)w->in_f, D, s->act_q,
+                                     s->act_meta, nullptr, st);
+  if (e != hipSuccess) return e;
+  gk::GemvArgs a{};
+  a.codes = w->codes;
+  a.scales = w->scales;
+  a.N = (int)w->out_f;
+  a.K = (int)w->in_f;
+  a.act_q = s->act_q;
+  a.act_meta = s->act_meta;
+  a.M = rows;
+  a.D = D;
+  a.bias = bias;
+  a.y = y;
+  a.resid = resid;
+  a.S = gk::choose_splits(a.N / 16, a.K / 128, rows);
+  a.partial = s->partial;
+  a.counters = s->counters;
+  a.epi = epi;
+  if (epi == gk::EPI_QKV) {
+    gk::QkvArgs &q = a.qkv;
+    q.q_out = s->q;
+    q.kv_pool = s->kv_pool;
+    q.kv_f16 = s->opt.kv_dtype == GLACIER_HIP_F16;
+    q.page_table = s->page_table;
+    q.max_pages = (int)s->max_pages;
+    q.lane_of_row = s->step_dev->lane_of_row;
+    q.pos_of_row = s->step_dev->pos_of_row;
+    q.rope_cos = s->rope_cos;
+    q.rope_sin = s->rope_sin;
+    q.num_layers = (int)c.num_layers;
+    q.num_heads = (int)c.num_heads;
+    q.num_kv_heads = (int)c.num_kv_heads;
+    q.head_dim = (int)c.head_dim;
+  }
+  return gk::launch_gemv(a, st);
+}
+
+// The full launch sequence of one token step for `rows` activation rows.
+hipError_t enqueue_step(glacier_hip_session *s, int rows, bool head, bool elig, hipStream_t st) {
+  glacier_hip_model *m = s->model;
+  const auto &c = m->cfg;
+  const int D = (int)c.dim, F = (int)c.hidden_dim;
+  hipError_t e = gk::launch_gather_rows(m->embed, s->step_dev->tokens, rows, D, s->x_res, st);
+  if (e != hipSuccess) return e;
+  for (uint32_t l = 0; l < c.num_layers; ++l) {
+    const LayerDev &L = m->layers[l];
+    gk::GemvArgs dummy{};
+    (void)dummy;
+    // QKV (+RoPE, KV row write)
+    {
+      const int Dq = layer_D(s, L.qkv->out_f, L.qkv->in_f);
+      e = gk::launch_prep_act(s->x_res, 0, L.in_norm, c.rms_eps, rows, D, Dq, s->act_q,
+                              s->act_meta, nullptr, st);
+      if (e != hipSuccess) return e;
+      gk::GemvArgs a{};
+      a.codes = L.qkv->codes;
+      a.scales = L.qkv->scales;
+      a.N = (int)L.qkv->out_f;
+      a.K = D;
+      a.act_q = s->act_q;
+      a.act_meta = s->act_meta;
+      a.M = rows;
+      a.D = Dq;
+      a.bias = L.qkv_bias;
+      a.S = gk::choose_splits(a.N / 16, a.K / 128, rows);
+      a.partial = s->partial;
+      a.counters = s->counters;
+      a.epi = gk::EPI_QKV;
+      gk::QkvArgs &q = a.qkv;
+      q.q_out = s->q;
+      q.kv_pool = s->kv_pool;
+      q.kv_f16 = s->opt.kv_dtype == GLACIER_HIP_F16;
+      q.page_table = s->page_table;
+      q.max_pages = (int)s->max_pages;
+      q.lane_of_row = s->step_dev->lane_of_row;
+      q.pos_of_row = s->step_dev->pos_of_row;
+      q.rope_cos = s->rope_cos;
+      q.rope_sin = s->rope_sin;
+      q.layer = (int)l;
+      q.num_layers = (int)c.num_layers;
+      q.num_heads = (int)c.num_heads;
+      q.num_kv_heads = (int)c.num_kv_heads;
+      q.head_dim = (int)c.head_dim;
+      e = gk::launch_gemv(a, st);
+      if (e != hipSuccess) return e;
+    }
+    e = gk::launch_attention(s->q, s->kv_pool, s->opt.kv_dtype == GLACIER_HIP_F16, s->page_table,
+                             (int)s->max_pages, s->step_dev->lane_of_row, s->step_dev->ctx_len,
+                             rows, (int)l, (int)c.num_layers, (int)c.num_heads,
+                             (int)c.num_kv_heads, (int)c.head_dim, (int)s->opt.max_positions,
+                             s->att_scratch, s->attn, st);
+    if (e != hipSuccess) return e;
+    e = run_proj(s, L.o, layer_D(s, L.o->out_f, L.o->in_f), rows, s->attn, nullptr,
+                 gk::EPI_RESID, nullptr, s->h, s->x_res, st);
+    if (e != hipSuccess) return e;
+    e = run_proj(s, L.gu, layer_D(s, L.gu->out_f / 2, L.gu->in_f), rows, s->h, L.post_norm,
+                 gk::EPI_SWIGLU, nullptr, s->act, nullptr, st);
+    if (e != hipSuccess) return e;
+    e = run_proj(s, L.down, layer_D(s, L.down->out_f, L.down->in_f), rows, s->act, nullptr,
+                 gk::EPI_RESID, nullptr, s->x_res, s->h, st);
+    if (e != hipSuccess) return e;
+    (void)F;
+  }
+  if (!head) return hipSuccess;
+  e = run_proj(s, m->head, head_D(s), rows, s->x_res, m->final_norm, gk::EPI_PLAIN, nullptr,
+               s->logits, nullptr, st);
+  if (e != hipSuccess) return e;
+  const long V = (long)c.vocab_size;
+  const long W = (V + 63) / 64;
+  return gk::launch_argmax(s->logits, V, rows, elig ? s->elig_words : nullptr, W, s->arg_scratch,
+                           s->arg_counters, s->arg_result, st);
+}
+
+void destroy_session(glacier_hip_session *s) {
+  void *ptrs[] = {s->kv_pool, s->page_table, s->rope_cos, s->rope_sin, s->x_res, s->h, s->q,
+                  s->attn, s->act, s->logits, s->act_q, s->act_meta, s->partial, s->counters,
+                  s->att_scratch, s->arg_scratch, s->arg_counters, s->arg_result, s->elig_words,
+                  s->step_dev};
+  for (void *p : ptrs)
+    if (p) (void)hipFree(p);
+  if (s->step_host) (void)hipHostFree(s->step_host);
+  if (s->res_host) (void)hipHostFree(s->res_host);
+  for (auto &g : s->graphs) (void)hipGraphExecDestroy(g.exec);
+  delete s;
+}
+
+void reset_lane(glacier_hip_session *s, Lane &ln, uint64_t seed) {
+  // return pages to the pool
+  for (auto &p : ln.page_of)
+    if (p >= 0) {
+      s->free_pages.push_back(p);
+      p = -1;
+    }
+  ln.page_of.assign(s->max_pages, -1);
+  ln.page_gen.assign(s->max_pages, 0);
+  ln.active = true;
+  ln.instance = g_next_cache_instance++;
+  ln.len = 0;
+  ln.next_page_generation = 1;
+  ln.next_root_generation = 2;
+  const auto &c = s->model->cfg;
+  ln.root.cache_instance = ln.instance;
+  ln.root.generation = 1;
+  ln.root.committed_len = 0;
+  ln.root.committed_pages = 0;
+  emptyOwnershipDigest(ln.instance, c.num_layers, (uint64_t)c.num_kv_heads * c.head_dim,
+                       s->opt.max_positions, ln.root.ownership_sha256);
+  ln.sampling_calls = 0;
+  // SplitMix64-seeded Xoshiro256 state (std.Random.DefaultPrng.init)
+  uint64_t st = seed;
+  for (int i = 0; i < 4; ++i) {
+    st += 0x9e3779b97f4a7c15ull;
+    uint64_t z = st;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    ln.rng[i] = z ^ (z >> 31);
+  }
+  ln.output.clear();
+}
+
+struct RowTxn {
+  uint32_t lane;
+  uint64_t pos;
+  bool installs;
+  int32_t page;
+  uint64_t gen;
+  glacier_hip_page_map_root_t after;
+};
+
+// beginRow (paged_kv_cache.zig:1006-1072) for every participating lane.
+int begin_rows(glacier_hip_session *s, const uint32_t *lanes, uint32_t count,
+               std::vector<RowTxn> &txns) {
+  txns.clear();
+  for (uint32_t i = 0; i < count; ++i) {
+    Lane &ln = s->lanes[lanes[i]];
+    RowTxn t{};
+    t.lane = lanes[i];
+    t.pos = ln.len;
+    const uint64_t page = ln.len / 16, row = ln.len % 16;
+    t.installs = row == 0;
+    if (t.installs) {
+      if (s->free_pages.empty()) {
+        // roll back the installs made so far in this step
+        for (auto &u : txns)
+          if (u.installs) {
+            s->free_pages.push_back(u.page);
+            s->lanes[u.lane].page_of[u.pos / 16] = -1;
+            s->lanes[u.lane].page_gen[u.pos / 16] = 0;
+          }
+        txns.clear();
+        return GLACIER_HIP_CACHE_FULL;
+      }
+      t.page = s->free_pages.back();
+      s->free_pages.pop_back();
+      t.gen = ln.next_page_generation;
+      ln.page_of[page] = t.page;
+      ln.page_gen[page] = t.gen;
+    } else {
+      t.page = ln.page_of[page];
+      t.gen = ln.page_gen[page];
+    }
+    t.after.cache_instance = ln.instance;
+    t.after.generation = ln.next_root_generation;
+    t.after.committed_len = ln.len + 1;
+    t.after.committed_pages = ln.root.committed_pages + (t.installs ? 1 : 0);
+    if (t.installs)
+      appendOwnershipDigest(ln.root.ownership_sha256, ln.instance, page, t.gen,
+                            t.after.ownership_sha256);
+    else
+      memcpy(t.after.ownership_sha256, ln.root.ownership_sha256, 32);
+    txns.push_back(t);
+  }
+  return GLACIER_HIP_OK;
+}
+
+void abort_rows(glacier_hip_session *s, std::vector<RowTxn> &txns) {
+  // abortRow (paged_kv_cache.zig:1146-1160): a newly installed page loses
+  // its ownership generation; nothing else changes.
+  for (auto &t : txns) {
+    Lane &ln = s->lanes[t.lane];
+    if (t.installs) {
+      ln.page_of[t.pos / 16] = -1;
+      ln.page_gen[t.pos / 16] = 0;
+      s->free_pages.push_back(t.page);
+    }
+  }
+  txns.clear();
+}
+
+void commit_rows(glacier_hip_session *s, std::vector<RowTxn> &txns) {
+  for (auto &t : txns) {
+    Lane &ln = s->lanes[t.lane];
+    if (t.installs) ln.next_page_generation++;
+    ln.next_root_generation++;
+    ln.root = t.after;
+    ln.len = t.pos + 1;
+  }
+  txns.clear();
+}
+
+// Execute one step for `count` rows; on success results are in res_host.
+int run_step(glacier_hip_session *s, const uint32_t *lanes, const uint32_t *tokens,
+             uint32_t count, bool head, const uint64_t *elig_host, float *logits_host,
+             std::vector<RowTxn> &txns) {
+  glacier_hip_context *ctx = s->model->ctx;
+  const auto &c = s->model->cfg;
+  hipStream_t st = ctx->stream;
+  int rc = begin_rows(s, lanes, count, txns);
+  if (rc) return rc;
+  for (uint32_t i = 0; i < count; ++i) {
+    s->step_host->tokens[i] = (int32_t)tokens[i];
+    s->step_host->lane_of_row[i] = (int32_t)lanes[i];
+    s->step_host->pos_of_row[i] = (int32_t)txns[i].pos;
+    s->step_host->ctx_len[i] = (int32_t)txns[i].pos + 1;
+  }
+  auto fail = [&](hipError_t e, const char *what) {
+    (void)hipStreamSynchronize(st);
+    abort_rows(s, txns);
+    return hip_fail(ctx, e, what);
+  };
+  hipError_t e = hipMemcpyAsync(s->step_dev, s->step_host, sizeof(StepInputs),
+                                hipMemcpyHostToDevice, st);
+  if (e != hipSuccess) return fail(e, "step inputs");
+  for (auto &t : txns)
+    if (t.installs) {
+      e = hipMemcpyAsync(s->page_table + (size_t)t.lane * s->max_pages + t.pos / 16, &t.page, 4,
+                         hipMemcpyHostToDevice, st);
+      if (e != hipSuccess) return fail(e, "page table");
+      e = hipStreamSynchronize(st);  // t.page is pageable host memory
+      if (e != hipSuccess) return fail(e, "page table sync");
+    }
+  const uint64_t W = (c.vocab_size + 63) / 64;
+  if (elig_host) {
+    e = hipMemcpyAsync(s->elig_words, elig_host, (size_t)count * W * 8, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) return fail(e, "eligibility words");
+  }
+  const bool elig = elig_host != nullptr;
+  hipGraphExec_t exec = nullptr;
+  if (s->opt.use_graph) {
+    for (auto &g : s->graphs)
+      if (g.rows == count && g.head == head && g.elig == elig) exec = g.exec;
+    if (!exec) {
+      hipGraph_t graph;
+      e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
+      if (e != hipSuccess) return fail(e, "begin capture");
+      hipError_t e2 = enqueue_step(s, (int)count, head, elig, st);
+      e = hipStreamEndCapture(st, &graph);
+      if (e2 != hipSuccess) return fail(e2, "capture step");
+      if (e != hipSuccess) return fail(e, "end capture");
+      e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(graph);
+      if (e != hipSuccess) return fail(e, "graph instantiate");
+      s->graphs.push_back({count, head, elig, exec});
+    }
+    e = hipGraphLaunch(exec, st);
+    if (e != hipSuccess) return fail(e, "graph launch");
+  } else {
+    e = enqueue_step(s, (int)count, head, elig, st);
+    if (e != hipSuccess) return fail(e, "enqueue step");
+  }
+  if (head) {
+    e = hipMemcpyAsync(s->res_host, s->arg_result, count * sizeof(gk::ArgmaxResult),
+                       hipMemcpyDeviceToHost, st);
+    if (e != hipSuccess) return fail(e, "result copy");
+    if (logits_host) {
+      e = hipMemcpyAsync(logits_host, s->logits, (size_t)count * c.vocab_size * 4,
+                         hipMemcpyDeviceToHost, st);
+      if (e != hipSuccess) return fail(e, "logits copy");
+    }
+  }
+  e = hipStreamSynchronize(st);
+  if (e != hipSuccess) return fail(e, "step sync");
+  if (s->inject_failure) {
+    abort_rows(s, txns);
+    return GLACIER_HIP_DEVICE_ERROR;
+  }
+  if (head)
+    for (uint32_t i = 0; i < count; ++i)
+      if (s->res_host[i].status != 0) {
+        const int st_code = s->res_host[i].status;
+        abort_rows(s, txns);
+        return st_code;
+      }
+  return GLACIER_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
+                                                const glacier_hip_session_options_t *opts) {
+  if (!m || !opts) return nullptr;
+  glacier_hip_context *ctx = m->ctx;
+  for (bool b : m->layer_set)
+    if (!b) {
+      ctx->last_error = "model layers not set";
+      return nullptr;
+    }
+  if (!m->globals_set) {
+    ctx->last_error = "model globals not set";
+    return nullptr;
+  }
+  const auto &c = m->cfg;
+  if (opts->max_lanes == 0 || opts->max_lanes > 32 || opts->max_positions == 0 ||
+      (opts->kv_dtype != GLACIER_HIP_F32 && opts->kv_dtype != GLACIER_HIP_F16)) {
+    ctx->last_error = "session options invalid";
+    return nullptr;
+  }
+  auto *s = new glacier_hip_session();
+  s->model = m;
+  s->opt = *opts;
+  s->max_pages = (opts->max_positions + 15) / 16;
+  s->total_pages = opts->total_pages ? opts->total_pages : opts->max_lanes * s->max_pages;
+  s->lanes.resize(opts->max_lanes);
+  for (uint32_t p = s->total_pages; p-- > 0;) s->free_pages.push_back((int32_t)p);
+  const uint32_t M = opts->max_lanes;
+  const size_t kvd = (size_t)c.num_kv_heads * c.head_dim;
+  const size_t elem = opts->kv_dtype == GLACIER_HIP_F16 ? 2 : 4;
+  const size_t page_bytes = (size_t)c.num_layers * 2 * 16 * kvd * elem;
+  const size_t Kmax = std::max(c.dim, c.hidden_dim);
+  const size_t Gmax = Kmax / 32;
+  // partial workspace: max over the projections of S * M * N
+  auto part_floats = [&](uint32_t N, uint32_t K) {
+    const int S = gk::choose_splits((int)N / 16, (int)K / 128, (int)M);
+    return S > 1 ? (size_t)S * M * N : (size_t)0;
+  };
+  const uint32_t nqkv = c.dim + 2 * (uint32_t)kvd;
+  size_t pf = std::max({part_floats(nqkv, c.dim), part_floats(c.dim, c.dim),
+                        part_floats(2 * c.hidden_dim, c.dim), part_floats(c.dim, c.hidden_dim),
+                        part_floats(c.vocab_size, c.dim), (size_t)1});
+  const size_t nb_max = std::max<size_t>(c.vocab_size, 2 * c.hidden_dim) / 16;
+  const size_t W = (c.vocab_size + 63) / 64;
+  const size_t att = gk::attention_scratch_floats((int)M, (int)c.num_heads, (int)c.head_dim,
+                                                  (int)opts->max_positions);
+  bool ok = true;
+  auto A = [&](void **p, size_t bytes) {
+    if (ok && hipMalloc(p, bytes) != hipSuccess) ok = false;
+  };
+  A(&s->kv_pool, page_bytes * s->total_pages);
+  A((void **)&s->page_table, (size_t)M * s->max_pages * 4);
+  A((void **)&s->rope_cos, (size_t)opts->max_positions * c.head_dim / 2 * 4);
+  A((void **)&s->rope_sin, (size_t)opts->max_positions * c.head_dim / 2 * 4);
+  A((void **)&s->x_res, (size_t)M * c.dim * 4);
+  A((void **)&s->h, (size_t)M * c.dim * 4);
+  A((void **)&s->q, (size_t)M * c.dim * 4);
+  A((void **)&s->attn, (size_t)M * c.dim * 4);
+  A((void **)&s->act, (size_t)M * c.hidden_dim * 4);
+  A((void **)&s->logits, (size_t)M * c.vocab_size * 4);
+  A((void **)&s->act_q, Gmax * 3 * M * 32);
+  A((void **)&s->act_meta, Gmax * M * sizeof(gk::ActMeta));
+  A((void **)&s->partial, pf * 4);
+  A((void **)&s->counters, nb_max * 4);
+  A((void **)&s->att_scratch, std::max<size_t>(att, 1) * 4);
+  A(&s->arg_scratch, gk::argmax_scratch_bytes((int)M, (long)c.vocab_size));
+  A((void **)&s->arg_counters, (size_t)M * 4);
+  A((void **)&s->arg_result, (size_t)M * sizeof(gk::ArgmaxResult));
+  A((void **)&s->elig_words, (size_t)M * W * 8);
+  A((void **)&s->step_dev, sizeof(StepInputs));
+  if (ok && hipHostMalloc((void **)&s->step_host, sizeof(StepInputs)) != hipSuccess) ok = false;
+  if (ok && hipHostMalloc((void **)&s->res_host, M * sizeof(gk::ArgmaxResult)) != hipSuccess) ok = false;
+  if (ok) {
+    ok = hipMemset(s->counters, 0, nb_max * 4) == hipSuccess &&
+         hipMemset(s->arg_counters, 0, (size_t)M * 4) == hipSuccess &&
+         hipMemset(s->kv_pool, 0, page_bytes * s->total_pages) == hipSuccess;
+    std::vector<int32_t> pt((size_t)M * s->max_pages, 0);
+    ok = ok && hipMemcpy(s->page_table, pt.data(), pt.size() * 4, hipMemcpyHostToDevice) == hipSuccess;
+    // RopeTable.init (generate.zig:790-806), f32 libm on the host
+    const size_t half = c.head_dim / 2;
+    std::vector<float> cs(opts->max_positions * half), sn(opts->max_positions * half);
+    for (size_t pos = 0; pos < opts->max_positions; ++pos)
+      for (size_t pair = 0; pair < half; ++pair) {
+        const float exponent = (float)(2 * pair) / (float)c.head_dim;
+        const float freq = 1.0f / powf(c.rope_theta, exponent);
+        const float angle = (float)pos * freq;
+        cs[pos * half + pair] = cosf(angle);
+        sn[pos * half + pair] = sinf(angle);
+      }
+    ok = ok && hipMemcpy(s->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice) == hipSuccess &&
+         hipMemcpy(s->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice) == hipSuccess;
+  }
+  if (!ok) {
+    ctx->last_error = "session allocation failed";
+    destroy_session(s);
+    return nullptr;
+  }
+  return s;
+}
+
+void glacier_hip_session_destroy(glacier_hip_session *s) {
+  if (!s) return;
+  (void)hipStreamSynchronize(s->model->ctx->stream);
+  destroy_session(s);
+}
+
+int glacier_hip_session_lane_begin(glacier_hip_session *s, uint32_t lane, uint64_t seed) {
+  if (!s) return GLACIER_HIP_INVALID_HANDLE;
+  if (lane >= s->lanes.size()) return GLACIER_HIP_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> lk(s->model->ctx->mu);
+  reset_lane(s, s->lanes[lane], seed);
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_session_inject_failure(glacier_hip_session *s, int enable) {
+  if (!s) return GLACIER_HIP_INVALID_HANDLE;
+  s->inject_failure = enable != 0;
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_session_prefill(glacier_hip_session *s, uint32_t lane, const uint32_t *tokens,
+                                uint32_t n, uint32_t *first_token, float *logits_host) {
+  if (!s || !tokens || !first_token) return GLACIER_HIP_INVALID_ARGUMENT;
+  if (lane >= s->lanes.size() || !s->lanes[lane].active) return GLACIER_HIP_INVALID_ARGUMENT;
+  const auto &c = s->model->cfg;
+  Lane &ln = s->lanes[lane];
+  if (n == 0) return GLACIER_HIP_SHAPE_MISMATCH;
+  for (uint32_t i = 0; i < n; ++i)
+    if (tokens[i] >= c.vocab_size) return GLACIER_HIP_SHAPE_MISMATCH;
+  if (ln.len + n > s->opt.max_positions) return GLACIER_HIP_CACHE_FULL;
+  std::lock_guard<std::mutex> lk(s->model->ctx->mu);
+  std::vector<RowTxn> txns;
+  for (uint32_t i = 0; i < n; ++i) {
+    const bool last = i + 1 == n;
+    int rc = run_step(s, &lane, &tokens[i], 1, last, nullptr, last ? logits_host : nullptr, txns);
+    if (rc) return rc;  // rows of earlier prompt tokens stay committed (cache.commit per token)
+    commit_rows(s, txns);
+  }
+  *first_token = (uint32_t)s->res_host[0].index;
+  ln.sampling_calls += 1;
+  ln.output.push_back(*first_token);
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_session_decode_step(glacier_hip_session *s, const uint32_t *lanes,
+                                    const uint32_t *tokens, uint32_t count,
+                                    const uint64_t *eligible_words_host, uint32_t *next_tokens,
+                                    float *logits_host) {
+  if (!s || !lanes || !tokens || !next_tokens) return GLACIER_HIP_INVALID_ARGUMENT;
+  if (count == 0 || count > s->lanes.size()) return GLACIER_HIP_SHAPE_MISMATCH;
+  const auto &c = s->model->cfg;
+  for (uint32_t i = 0; i < count; ++i) {
+    if (lanes[i] >= s->lanes.size() || !s->lanes[lanes[i]].active) return GLACIER_HIP_INVALID_ARGUMENT;
+    for (uint32_t j = 0; j < i; ++j)
+      if (lanes[j] == lanes[i]) return GLACIER_HIP_INVALID_ARGUMENT;
+    if (tokens[i] >= c.vocab_size) return GLACIER_HIP_SHAPE_MISMATCH;
+    if (s->lanes[lanes[i]].len + 1 > s->opt.max_positions) return GLACIER_HIP_CACHE_FULL;
+  }
+  std::lock_guard<std::mutex> lk(s->model->ctx->mu);
+  std::vector<RowTxn> txns;
+  int rc = run_step(s, lanes, tokens, count, true, eligible_words_host, logits_host, txns);
+  if (rc) return rc;
+  // publish: KV root + length, sampler counter, output word (all or nothing)
+  for (uint32_t i = 0; i < count; ++i) next_tokens[i] = (uint32_t)s->res_host[i].index;
+  commit_rows(s, txns);
+  for (uint32_t i = 0; i < count; ++i) {
+    Lane &ln = s->lanes[lanes[i]];
+    // the eligible (posthead) branch does not count a sampler call
+    // (generate.zig:5574-5598); the greedy sampler does (:5593)
+    if (!eligible_words_host) ln.sampling_calls += 1;
+    ln.output.push_back(next_tokens[i]);
+  }
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_session_lane_root(glacier_hip_session *s, uint32_t lane,
+                                  glacier_hip_page_map_root_t *out) {
+  if (!s || !out || lane >= s->lanes.size()) return GLACIER_HIP_INVALID_ARGUMENT;
+  *out = s->lanes[lane].root;
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_session_lane_state(glacier_hip_session *s, uint32_t lane,
+                                   glacier_hip_lane_state_t *out) {
+  if (!s || !out || lane >= s->lanes.size()) return GLACIER_HIP_INVALID_ARGUMENT;
+  const Lane &ln = s->lanes[lane];
+  out->kv_positions = ln.len;
+  out->published_tokens = ln.output.size();
+  out->sampling_calls = ln.sampling_calls;
+  memcpy(out->rng_state, ln.rng, sizeof ln.rng);
+  // tokenSequenceSha256 (generate.zig:3193-3203)
+  gh::Sha256 h;
+  h.update("glacier-output-token-state-v1\0", 30);
+  h.u64(ln.output.size());
+  for (uint32_t t : ln.output) h.u32(t);
+  h.final(out->output_sha256);
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_session_read_kv_row(glacier_hip_session *s, uint32_t lane, uint32_t layer,
+                                    int value, uint32_t position, float *out_host) {
+  if (!s || !out_host || lane >= s->lanes.size()) return GLACIER_HIP_INVALID_ARGUMENT;
+  const auto &c = s->model->cfg;
+  const Lane &ln = s->lanes[lane];
+  if (layer >= c.num_layers || position >= ln.len) return GLACIER_HIP_SHAPE_MISMATCH;
+  const int32_t page = ln.page_of[position / 16];
+  if (page < 0) return GLACIER_HIP_INVALID_TRANSACTION;
+  const size_t kvd = (size_t)c.num_kv_heads * c.head_dim;
+  const size_t elem = s->opt.kv_dtype == GLACIER_HIP_F16 ? 2 : 4;
+  const size_t off = ((((size_t)page * c.num_layers + layer) * 2 + (value ? 1 : 0)) * 16 +
+                      position % 16) * kvd;
+  glacier_hip_context *ctx = s->model->ctx;
+  std::vector<uint8_t> raw(kvd * elem);
+  GH_CHECK(ctx, hipMemcpy(raw.data(), (char *)s->kv_pool + off * elem, kvd * elem,
+                          hipMemcpyDeviceToHost));
+  for (size_t i = 0; i < kvd; ++i) {
+    if (elem == 4) memcpy(&out_host[i], &raw[4 * i], 4);
+    else {
+      uint16_t hv;
+      memcpy(&hv, &raw[2 * i], 2);
+      out_host[i] = gh::f16_to_f32(hv);
+    }
+  }
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_session_lane_kv_sha256(glacier_hip_session *s, uint32_t lane, uint8_t out[32]) {
+  if (!s || !out || lane >= s->lanes.size()) return GLACIER_HIP_INVALID_ARGUMENT;
+  const auto &c = s->model->cfg;
+  const Lane &ln = s->lanes[lane];
+  const size_t kvd = (size_t)c.num_kv_heads * c.head_dim;
+  gh::Sha256 h;
+  h.update("glacier-logical-kv-state-v1\0", 28);
+  h.u64(c.num_layers);
+  h.u64(kvd);
+  h.u64(ln.len);
+  std::vector<float> row(kvd);
+  for (uint32_t l = 0; l < c.num_layers; ++l)
+    for (int v = 0; v < 2; ++v)
+      for (uint64_t p = 0; p < ln.len; ++p) {
+        int rc = glacier_hip_session_read_kv_row(s, lane, l, v, (uint32_t)p, row.data());
+        if (rc) return rc;
+        for (float f : row) {
+          uint32_t b;
+          memcpy(&b, &f, 4);
+          h.u32(b);
+        }
+      }
+  h.final(out);
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_session_page_of(glacier_hip_session *s, uint32_t lane, uint32_t logical_page,
+                                int32_t *physical_out) {
+  if (!s || !physical_out || lane >= s->lanes.size()) return GLACIER_HIP_INVALID_ARGUMENT;
+  const Lane &ln = s->lanes[lane];
+  if (logical_page >= ln.page_of.size()) return GLACIER_HIP_SHAPE_MISMATCH;
+  *physical_out = ln.page_of[logical_page];
+  return GLACIER_HIP_OK;
+}
+
+}  // extern "C"

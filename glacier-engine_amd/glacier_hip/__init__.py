@@ -1,0 +1,441 @@
+"""ctypes mirror of include/glacier_hip.h (the gfx950 device backend).
+
+Loads the in-tree libglacier_hip.so and raises if it is missing: there is no
+CPU fallback. Device memory for tests and benchmarks is plain torch tensors;
+their addresses cross the ABI as raw pointers.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(HERE), "libglacier_hip.so")
+
+OK = 0
+SHAPE_MISMATCH = 1
+DTYPE_UNSUPPORTED = 2
+INVALID_ARGUMENT = 3
+OUT_OF_MEMORY = 4
+DEVICE_ERROR = 5
+INVALID_MASK = 6
+ELIGIBLE_NAN = 7
+CACHE_FULL = 8
+NO_DEVICE = 9
+INVALID_HANDLE = 10
+BUSY = 13
+
+F32, F16, BF16 = 0, 1, 2
+ACT_Q8, ACT_F32, ACT_AUTO = 0, 1, 2
+
+
+class GlacierHipError(RuntimeError):
+    def __init__(self, code, what):
+        super().__init__(f"{what}: status {code}")
+        self.code = code
+
+
+class DeviceInfo(C.Structure):
+    _fields_ = [("name", C.c_char * 64), ("arch", C.c_char * 32),
+                ("compute_units", C.c_uint32), ("wavefront_size", C.c_uint32),
+                ("total_global_bytes", C.c_uint64), ("max_single_allocation_bytes", C.c_uint64),
+                ("lds_bytes_per_block", C.c_uint32), ("l2_bytes", C.c_uint32),
+                ("clock_khz", C.c_uint32), ("memory_clock_khz", C.c_uint32),
+                ("memory_bus_width_bits", C.c_uint32), ("device_ordinal", C.c_uint32)]
+
+
+class AllocationLimits(C.Structure):
+    _fields_ = [("max_single_allocation_bytes", C.c_uint64), ("max_total_device_bytes", C.c_uint64),
+                ("allocation_granularity_bytes", C.c_uint64), ("max_queue_slots", C.c_uint64)]
+
+
+class Capability(C.Structure):
+    _fields_ = [("abi_version", C.c_uint64), ("backend_kind", C.c_uint64),
+                ("device_class", C.c_uint64), ("operation_profile_bits", C.c_uint64),
+                ("operator_bits", C.c_uint64), ("element_type_bits", C.c_uint64),
+                ("numerical_policy_bits", C.c_uint64), ("feature_bits", C.c_uint64),
+                ("max_single_allocation_bytes", C.c_uint64), ("max_total_device_bytes", C.c_uint64),
+                ("max_queue_slots", C.c_uint64), ("backend_sha256", C.c_uint8 * 32),
+                ("device_sha256", C.c_uint8 * 32), ("driver_sha256", C.c_uint8 * 32),
+                ("placement_sha256", C.c_uint8 * 32), ("capability_sha256", C.c_uint8 * 32)]
+
+
+class BufferToken(C.Structure):
+    _fields_ = [("id", C.c_uint64), ("requested_bytes", C.c_uint64), ("charged_bytes", C.c_uint64)]
+
+
+class BufferInfo(C.Structure):
+    _fields_ = [("id", C.c_uint64), ("requested_bytes", C.c_uint64), ("charged_bytes", C.c_uint64),
+                ("device_address", C.c_uint64)]
+
+
+class AllocationQuote(C.Structure):
+    _fields_ = [("requested_bytes", C.c_uint64), ("charged_bytes", C.c_uint64),
+                ("context_epoch", C.c_uint64)]
+
+
+class ArgmaxResult(C.Structure):
+    _fields_ = [("token_index", C.c_uint64), ("eligible_rows", C.c_uint64),
+                ("status", C.c_int32), ("reserved", C.c_int32)]
+
+
+class ModelConfig(C.Structure):
+    _fields_ = [("num_layers", C.c_uint32), ("dim", C.c_uint32), ("hidden_dim", C.c_uint32),
+                ("num_heads", C.c_uint32), ("num_kv_heads", C.c_uint32), ("head_dim", C.c_uint32),
+                ("vocab_size", C.c_uint32), ("group_size", C.c_uint32),
+                ("rms_eps", C.c_float), ("rope_theta", C.c_float)]
+
+
+_P = C.c_void_p
+
+
+class LayerHost(C.Structure):
+    _fields_ = [(n, _P) for n in (
+        "input_norm", "post_attn_norm", "wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down",
+        "sq", "sk", "sv", "so", "s_gate", "s_up", "s_down", "bq", "bk", "bv")]
+
+
+class SessionOptions(C.Structure):
+    _fields_ = [("max_lanes", C.c_uint32), ("max_positions", C.c_uint32),
+                ("total_pages", C.c_uint32), ("kv_dtype", C.c_int32),
+                ("layer_activation", C.c_int32), ("head_activation", C.c_int32),
+                ("use_graph", C.c_int32), ("reserved", C.c_int32)]
+
+
+class PageMapRoot(C.Structure):
+    _fields_ = [("cache_instance", C.c_uint64), ("generation", C.c_uint64),
+                ("committed_len", C.c_uint64), ("committed_pages", C.c_uint64),
+                ("ownership_sha256", C.c_uint8 * 32)]
+
+
+class LaneState(C.Structure):
+    _fields_ = [("kv_positions", C.c_uint64), ("published_tokens", C.c_uint64),
+                ("sampling_calls", C.c_uint64), ("rng_state", C.c_uint64 * 4),
+                ("output_sha256", C.c_uint8 * 32)]
+
+
+# (name, restype, argtypes) for every exported symbol of include/glacier_hip.h
+_SIGS = [
+    ("glacier_hip_abi_version", C.c_uint64, []),
+    ("glacier_hip_init", _P, [C.c_int]),
+    ("glacier_hip_deinit", C.c_int, [_P]),
+    ("glacier_hip_device_info", C.c_int, [_P, C.POINTER(DeviceInfo)]),
+    ("glacier_hip_allocation_limits", C.c_int, [_P, C.POINTER(AllocationLimits)]),
+    ("glacier_hip_last_error", C.c_char_p, [_P]),
+    ("glacier_hip_synchronize", C.c_int, [_P]),
+    ("glacier_hip_device_capability_v1", C.c_int, [_P, C.POINTER(Capability)]),
+    ("glacier_hip_buffer_create", C.c_int, [_P, C.c_uint64, C.POINTER(BufferToken)]),
+    ("glacier_hip_buffer_info", C.c_int, [_P, C.POINTER(BufferToken), C.POINTER(BufferInfo)]),
+    ("glacier_hip_buffer_release", C.c_int, [_P, C.POINTER(BufferToken)]),
+    ("glacier_hip_live_buffer_count", C.c_int, [_P, C.POINTER(C.c_uint64)]),
+    ("glacier_hip_allocation_quote", C.c_int, [_P, C.c_uint64, C.POINTER(AllocationQuote)]),
+    ("glacier_hip_allocation_allocate", C.c_int,
+     [_P, C.POINTER(AllocationQuote), C.POINTER(BufferToken)]),
+    ("glacier_hip_allocation_free", C.c_int, [_P, C.POINTER(BufferToken)]),
+    ("glacier_hip_int4_weight_create", _P,
+     [_P, _P, C.c_uint64, _P, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32]),
+    ("glacier_hip_int4_weight_create_f16scales", _P,
+     [_P, _P, C.c_uint64, _P, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32]),
+    ("glacier_hip_int4_weight_destroy", None, [_P]),
+    ("glacier_hip_live_weight_count", C.c_int, [_P, C.POINTER(C.c_uint64)]),
+    ("glacier_hip_int4_weight_device_bytes", C.c_uint64, [_P]),
+    ("glacier_hip_int4_matvec_dispatch", C.c_int, [_P, _P, _P, C.c_uint64, _P, C.c_uint64]),
+    ("glacier_hip_int4_gemv", C.c_int, [_P, _P, _P, C.c_int, C.c_uint32, _P, _P, C.c_int, _P]),
+    ("glacier_hip_rmsnorm", C.c_int, [_P, _P, _P, C.c_uint32, C.c_uint32, C.c_float, _P, _P]),
+    ("glacier_hip_paged_attention", C.c_int,
+     [_P, _P, _P, C.c_int, _P, C.c_uint32, _P, C.c_uint32, C.c_uint32, C.c_uint32,
+      C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, _P, _P]),
+    ("glacier_hip_argmax", C.c_int, [_P, _P, C.c_uint64, C.c_uint32, _P, _P]),
+    ("glacier_hip_eligible_argmax", C.c_int,
+     [_P, _P, C.c_uint64, _P, C.c_uint64, C.c_uint32, C.POINTER(ArgmaxResult), _P]),
+    ("glacier_hip_model_create", _P, [_P, C.POINTER(ModelConfig)]),
+    ("glacier_hip_model_set_layer", C.c_int, [_P, C.c_uint32, C.POINTER(LayerHost)]),
+    ("glacier_hip_model_set_globals", C.c_int, [_P, _P, _P, _P, _P]),
+    ("glacier_hip_model_init_random", C.c_int, [_P, C.c_uint64]),
+    ("glacier_hip_model_destroy", None, [_P]),
+    ("glacier_hip_model_weight_bytes", C.c_uint64, [_P]),
+    ("glacier_hip_session_create", _P, [_P, C.POINTER(SessionOptions)]),
+    ("glacier_hip_session_destroy", None, [_P]),
+    ("glacier_hip_session_lane_begin", C.c_int, [_P, C.c_uint32, C.c_uint64]),
+    ("glacier_hip_session_prefill", C.c_int, [_P, C.c_uint32, _P, C.c_uint32, _P, _P]),
+    ("glacier_hip_session_decode_step", C.c_int, [_P, _P, _P, C.c_uint32, _P, _P, _P]),
+    ("glacier_hip_session_lane_root", C.c_int, [_P, C.c_uint32, C.POINTER(PageMapRoot)]),
+    ("glacier_hip_session_lane_state", C.c_int, [_P, C.c_uint32, C.POINTER(LaneState)]),
+    ("glacier_hip_session_lane_kv_sha256", C.c_int, [_P, C.c_uint32, _P]),
+    ("glacier_hip_session_read_kv_row", C.c_int,
+     [_P, C.c_uint32, C.c_uint32, C.c_int, C.c_uint32, _P]),
+    ("glacier_hip_session_page_of", C.c_int, [_P, C.c_uint32, C.c_uint32, C.POINTER(C.c_int32)]),
+    ("glacier_hip_session_inject_failure", C.c_int, [_P, C.c_int]),
+    ("glacier_hip_synth_int4", None, [C.c_uint64, C.c_uint64, _P, C.c_uint64]),
+    ("glacier_hip_synth_scales_f16", None, [C.c_uint64, C.c_uint64, C.c_float, _P, C.c_uint64]),
+    ("glacier_hip_synth_normal_f32", None, [C.c_uint64, C.c_uint64, C.c_float, _P, C.c_uint64]),
+    ("glacier_hip_synth_tokens", None, [C.c_uint64, C.c_uint64, C.c_uint32, _P, C.c_uint64]),
+    ("glacier_hip_synth_tensor_id", C.c_uint64, [C.c_uint32, C.c_uint32]),
+    ("glacier_hip_f16_to_f32", C.c_float, [C.c_uint16]),
+]
+
+_lib = None
+
+
+def lib():
+    """Load libglacier_hip.so; raise when it has not been built."""
+    global _lib
+    if _lib is None:
+        # One HIP runtime per process: torch ships its own libamdhip64 (soname
+        # libamdhip64.so.7). Loading torch first lets this library bind to that
+        # same runtime by soname; loading /opt/rocm's copy first would leave two
+        # runtimes competing for the device.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python glacier-engine_amd/build.py` "
+                "(there is no CPU fallback)")
+        L = C.CDLL(LIB_PATH)
+        for name, res, args in _SIGS:
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def exported_symbols():
+    return [s[0] for s in _SIGS]
+
+
+def ptr(a):
+    """Raw address of a numpy array or a torch tensor (None -> NULL)."""
+    if a is None:
+        return None
+    if isinstance(a, np.ndarray):
+        return a.ctypes.data
+    return a.data_ptr()
+
+
+def check(rc, what, ctx=None):
+    if rc != OK:
+        msg = what
+        if ctx is not None:
+            err = lib().glacier_hip_last_error(ctx)
+            if err:
+                msg += f" ({err.decode()})"
+        raise GlacierHipError(rc, msg)
+
+
+# ---- synthetic generator (host) ------------------------------------------------------
+def synth_int4(seed, tensor_id, nbytes):
+    out = np.empty(nbytes, dtype=np.uint8)
+    lib().glacier_hip_synth_int4(seed, tensor_id, ptr(out), nbytes)
+    return out
+
+
+def synth_scales_f16(seed, tensor_id, count, sigma=0.02):
+    out = np.empty(count, dtype=np.uint16)
+    lib().glacier_hip_synth_scales_f16(seed, tensor_id, sigma, ptr(out), count)
+    return out
+
+
+def synth_normal_f32(seed, tensor_id, count, sigma=0.02):
+    out = np.empty(count, dtype=np.float32)
+    lib().glacier_hip_synth_normal_f32(seed, tensor_id, sigma, ptr(out), count)
+    return out
+
+
+def synth_tokens(seed, tensor_id, vocab, count):
+    out = np.empty(count, dtype=np.uint32)
+    lib().glacier_hip_synth_tokens(seed, tensor_id, vocab, ptr(out), count)
+    return out
+
+
+def tensor_id(layer, which):
+    return lib().glacier_hip_synth_tensor_id(layer, which)
+
+
+GLOBAL_LAYER = 0xFFFFFF
+# per-layer tensor slots used by glacier_hip_model_init_random
+SLOT = dict(input_norm=0, post_attn_norm=1, wq=2, sq=3, wk=4, sk=5, wv=6, sv=7, wo=8, so=9,
+            w_gate=10, s_gate=11, w_up=12, s_up=13, w_down=14, s_down=15,
+            embedding=20, final_norm=21, lm_head=22, lm_head_scales=23)
+
+
+def random_model_host(cfg, seed):
+    """Host tensors identical to what glacier_hip_model_init_random uploads.
+
+    Returns a dict with per-layer dicts (packed uint8 codes in the reference
+    row-major layout, float32 scales that are exact fp16 values, f32 norms)
+    and the global tensors."""
+    D, F, V = cfg["dim"], cfg["hidden_dim"], cfg["vocab_size"]
+    kvd = cfg["num_kv_heads"] * cfg["head_dim"]
+    f16 = lambda a: a.view(np.float16).astype(np.float32)
+    shapes = dict(q=(D, D), k=(kvd, D), v=(kvd, D), o=(D, D), gate=(F, D), up=(F, D),
+                  down=(D, F))
+    layers = []
+    for l in range(cfg["num_layers"]):
+        t = lambda which: tensor_id(l, which)
+        L = dict(input_norm=synth_normal_f32(seed, t(0), D),
+                 post_attn_norm=synth_normal_f32(seed, t(1), D))
+        for i, name in enumerate(["q", "k", "v", "o", "gate", "up", "down"]):
+            n, k = shapes[name]
+            L["w_" + name] = synth_int4(seed, t(2 + 2 * i), n * k // 2)
+            L["s_" + name] = f16(synth_scales_f16(seed, t(3 + 2 * i), n * k // 32))
+        layers.append(L)
+    G = GLOBAL_LAYER
+    return dict(
+        layers=layers,
+        embedding=synth_normal_f32(seed, tensor_id(G, 20), V * D),
+        final_norm=synth_normal_f32(seed, tensor_id(G, 21), D),
+        lm_head=synth_int4(seed, tensor_id(G, 22), V * D // 2),
+        lm_head_scales=f16(synth_scales_f16(seed, tensor_id(G, 23), V * D // 32)),
+    )
+
+
+# ---- thin object wrappers -------------------------------------------------------------
+class Context:
+    def __init__(self, device=0):
+        self.L = lib()
+        self.h = self.L.glacier_hip_init(device)
+        if not self.h:
+            raise GlacierHipError(NO_DEVICE, "glacier_hip_init: " +
+                                  (self.L.glacier_hip_last_error(None) or b"").decode())
+
+    def close(self):
+        if self.h:
+            check(self.L.glacier_hip_deinit(self.h), "deinit", self.h)
+            self.h = None
+
+    def info(self):
+        d = DeviceInfo()
+        check(self.L.glacier_hip_device_info(self.h, C.byref(d)), "device_info", self.h)
+        return d
+
+    def sync(self):
+        check(self.L.glacier_hip_synchronize(self.h), "synchronize", self.h)
+
+    def weight(self, packed, scales, in_f, out_f, group=32):
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        if scales.dtype == np.uint16:
+            w = self.L.glacier_hip_int4_weight_create_f16scales(
+                self.h, ptr(packed), packed.size, ptr(scales), scales.size, group, in_f, out_f)
+        else:
+            scales = np.ascontiguousarray(scales, dtype=np.float32)
+            w = self.L.glacier_hip_int4_weight_create(
+                self.h, ptr(packed), packed.size, ptr(scales), scales.size, group, in_f, out_f)
+        if not w:
+            raise GlacierHipError(INVALID_ARGUMENT, "int4_weight_create: " +
+                                  self.L.glacier_hip_last_error(self.h).decode())
+        return w
+
+
+class Model:
+    def __init__(self, ctx, cfg):
+        self.ctx = ctx
+        self.cfg = dict(cfg)
+        c = ModelConfig(**{k: cfg[k] for k, _ in ModelConfig._fields_})
+        self.h = lib().glacier_hip_model_create(ctx.h, C.byref(c))
+        if not self.h:
+            raise GlacierHipError(INVALID_ARGUMENT, "model_create: " +
+                                  lib().glacier_hip_last_error(ctx.h).decode())
+
+    def init_random(self, seed):
+        check(lib().glacier_hip_model_init_random(self.h, seed), "model_init_random", self.ctx.h)
+
+    def set_from_host(self, host):
+        for l, L in enumerate(host["layers"]):
+            keep = {k: np.ascontiguousarray(v) for k, v in L.items()}
+            lh = LayerHost(
+                input_norm=ptr(keep["input_norm"]), post_attn_norm=ptr(keep["post_attn_norm"]),
+                wq=ptr(keep["w_q"]), wk=ptr(keep["w_k"]), wv=ptr(keep["w_v"]), wo=ptr(keep["w_o"]),
+                w_gate=ptr(keep["w_gate"]), w_up=ptr(keep["w_up"]), w_down=ptr(keep["w_down"]),
+                sq=ptr(keep["s_q"]), sk=ptr(keep["s_k"]), sv=ptr(keep["s_v"]), so=ptr(keep["s_o"]),
+                s_gate=ptr(keep["s_gate"]), s_up=ptr(keep["s_up"]), s_down=ptr(keep["s_down"]),
+                bq=ptr(keep.get("bq")), bk=ptr(keep.get("bk")), bv=ptr(keep.get("bv")))
+            check(lib().glacier_hip_model_set_layer(self.h, l, C.byref(lh)), "set_layer", self.ctx.h)
+        check(lib().glacier_hip_model_set_globals(
+            self.h, ptr(host["embedding"]), ptr(host["final_norm"]), ptr(host["lm_head"]),
+            ptr(np.ascontiguousarray(host["lm_head_scales"], dtype=np.float32))),
+            "set_globals", self.ctx.h)
+
+    def weight_bytes(self):
+        return lib().glacier_hip_model_weight_bytes(self.h)
+
+    def close(self):
+        if self.h:
+            lib().glacier_hip_model_destroy(self.h)
+            self.h = None
+
+
+class Session:
+    def __init__(self, model, max_lanes, max_positions, kv_dtype=F32, total_pages=0,
+                 layer_activation=ACT_AUTO, head_activation=ACT_AUTO, use_graph=True):
+        self.model = model
+        o = SessionOptions(max_lanes=max_lanes, max_positions=max_positions,
+                           total_pages=total_pages, kv_dtype=kv_dtype,
+                           layer_activation=layer_activation, head_activation=head_activation,
+                           use_graph=1 if use_graph else 0)
+        self.h = lib().glacier_hip_session_create(model.h, C.byref(o))
+        if not self.h:
+            raise GlacierHipError(INVALID_ARGUMENT, "session_create: " +
+                                  lib().glacier_hip_last_error(model.ctx.h).decode())
+        self.vocab = model.cfg["vocab_size"]
+
+    def begin(self, lane, seed=0):
+        check(lib().glacier_hip_session_lane_begin(self.h, lane, seed), "lane_begin")
+
+    def prefill(self, lane, tokens, want_logits=False):
+        toks = np.ascontiguousarray(tokens, dtype=np.uint32)
+        first = np.zeros(1, dtype=np.uint32)
+        logits = np.empty(self.vocab, dtype=np.float32) if want_logits else None
+        rc = lib().glacier_hip_session_prefill(self.h, lane, ptr(toks), toks.size, ptr(first),
+                                               ptr(logits))
+        check(rc, "prefill", self.model.ctx.h)
+        return (int(first[0]), logits) if want_logits else int(first[0])
+
+    def step(self, lanes, tokens, eligible=None, want_logits=False, raise_on_error=True):
+        lanes = np.ascontiguousarray(lanes, dtype=np.uint32)
+        toks = np.ascontiguousarray(tokens, dtype=np.uint32)
+        nxt = np.zeros(lanes.size, dtype=np.uint32)
+        logits = np.empty((lanes.size, self.vocab), dtype=np.float32) if want_logits else None
+        el = None if eligible is None else np.ascontiguousarray(eligible, dtype=np.uint64)
+        rc = lib().glacier_hip_session_decode_step(self.h, ptr(lanes), ptr(toks), lanes.size,
+                                                   ptr(el), ptr(nxt), ptr(logits))
+        if raise_on_error:
+            check(rc, "decode_step", self.model.ctx.h)
+            return (nxt, logits) if want_logits else nxt
+        return rc, nxt
+
+    def root(self, lane):
+        r = PageMapRoot()
+        check(lib().glacier_hip_session_lane_root(self.h, lane, C.byref(r)), "lane_root")
+        return r
+
+    def state(self, lane):
+        s = LaneState()
+        check(lib().glacier_hip_session_lane_state(self.h, lane, C.byref(s)), "lane_state")
+        return s
+
+    def kv_sha256(self, lane):
+        out = (C.c_uint8 * 32)()
+        check(lib().glacier_hip_session_lane_kv_sha256(self.h, lane, out), "kv_sha256")
+        return bytes(out)
+
+    def kv_row(self, lane, layer, value, pos, kv_dim):
+        out = np.empty(kv_dim, dtype=np.float32)
+        check(lib().glacier_hip_session_read_kv_row(self.h, lane, layer, value, pos, ptr(out)),
+              "read_kv_row")
+        return out
+
+    def page_of(self, lane, logical_page):
+        v = C.c_int32()
+        check(lib().glacier_hip_session_page_of(self.h, lane, logical_page, C.byref(v)), "page_of")
+        return v.value
+
+    def inject_failure(self, enable):
+        check(lib().glacier_hip_session_inject_failure(self.h, 1 if enable else 0), "inject")
+
+    def close(self):
+        if self.h:
+            lib().glacier_hip_session_destroy(self.h)
+            self.h = None

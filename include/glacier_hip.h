@@ -1,0 +1,365 @@
+/*
+ * glacier_hip.h — C ABI of the MI355X (gfx950) device backend for Glacier
+ * Engine's text token loop.
+ *
+ * Conventions follow the reference's Metal extern set
+ * (src/backends/metal/backend.zig:506-670): opaque context / weight handles,
+ * `int` status returns with 0 = ok, caller-owned buffers with explicit
+ * lengths, no ownership transfer of caller pointers, a destroy for every
+ * create, and live-object counts for zero-orphan checks
+ * (backend.zig:2182-2235). The header uses C types only so that a Zig host
+ * can `@cImport` it; HIP streams are passed as `void *` (NULL = the
+ * context's own stream).
+ *
+ * "dev" pointers are device (HBM) addresses; "host" pointers are host
+ * memory. Every entry point validates shapes, alignment and handles on the
+ * host before it launches anything and publishes nothing on error.
+ */
+#ifndef GLACIER_HIP_H
+#define GLACIER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes -------------------------------------------------------- */
+enum glacier_hip_status {
+    GLACIER_HIP_OK = 0,
+    GLACIER_HIP_SHAPE_MISMATCH = 1,      /* TensorError.ShapeMismatch */
+    GLACIER_HIP_DTYPE_UNSUPPORTED = 2,   /* TensorError.DTypeUnsupported */
+    GLACIER_HIP_INVALID_ARGUMENT = 3,
+    GLACIER_HIP_OUT_OF_MEMORY = 4,
+    GLACIER_HIP_DEVICE_ERROR = 5,        /* a HIP runtime call failed */
+    GLACIER_HIP_INVALID_MASK = 6,        /* EligibleArgmaxError.InvalidEligibleMask */
+    GLACIER_HIP_ELIGIBLE_NAN = 7,        /* EligibleArgmaxError.EligibleLogitNaN */
+    GLACIER_HIP_CACHE_FULL = 8,          /* GenerateError.CacheFull / paged CacheFull */
+    GLACIER_HIP_NO_DEVICE = 9,
+    GLACIER_HIP_INVALID_HANDLE = 10,
+    GLACIER_HIP_TRANSACTION_ACTIVE = 11, /* paged_kv_cache Error.TransactionActive */
+    GLACIER_HIP_INVALID_TRANSACTION = 12,/* paged_kv_cache Error.InvalidTransaction */
+    GLACIER_HIP_BUSY = 13,               /* concurrent submission rejected (int4_executor.zig:2267) */
+    GLACIER_HIP_UNSUPPORTED = 14,
+};
+
+/* ---- element types / activation modes ------------------------------------ */
+enum glacier_hip_dtype {
+    GLACIER_HIP_F32 = 0,
+    GLACIER_HIP_F16 = 1,
+    GLACIER_HIP_BF16 = 2,
+};
+
+/* How the INT4 GEMV treats activations.
+ *  Q8   — the reference's blockwise Q8 path (int4_matmul.zig:335-420): per
+ *         32-element group s = max|x|/127, q = clamp(round(x/s), +-127), exact
+ *         integer dot per group, f32 across groups.
+ *  F32  — the reference's f32-activation path (int4_matmul.zig:215-311),
+ *         computed to ~2^-22 relative accuracy (three 7-bit digit planes).
+ *  AUTO — the reference's x86 dispatch (int4_matmul.zig:372-374,461-463):
+ *         F32 when out_f > 65536 or in_f > 16384, else Q8. */
+enum glacier_hip_activation {
+    GLACIER_HIP_ACT_Q8 = 0,
+    GLACIER_HIP_ACT_F32 = 1,
+    GLACIER_HIP_ACT_AUTO = 2,
+};
+
+/* ---- opaque handles ------------------------------------------------------ */
+typedef struct glacier_hip_context glacier_hip_context;
+typedef struct glacier_hip_int4_weight glacier_hip_int4_weight;
+typedef struct glacier_hip_model glacier_hip_model;
+typedef struct glacier_hip_session glacier_hip_session;
+
+/* ---- context (backend.zig:506-531: init / deinit / device_info /
+ *      allocation_limits) -------------------------------------------------- */
+typedef struct {
+    char name[64];
+    char arch[32];             /* "gfx950" */
+    uint32_t compute_units;
+    uint32_t wavefront_size;
+    uint64_t total_global_bytes;
+    uint64_t max_single_allocation_bytes;
+    uint32_t lds_bytes_per_block;
+    uint32_t l2_bytes;
+    uint32_t clock_khz;
+    uint32_t memory_clock_khz;
+    uint32_t memory_bus_width_bits;
+    uint32_t device_ordinal;
+} glacier_hip_device_info_t;
+
+typedef struct {
+    uint64_t max_single_allocation_bytes;
+    uint64_t max_total_device_bytes;
+    uint64_t allocation_granularity_bytes;
+    uint64_t max_queue_slots;
+} glacier_hip_allocation_limits_t;
+
+glacier_hip_context *glacier_hip_init(int device_ordinal);
+int glacier_hip_deinit(glacier_hip_context *ctx);
+int glacier_hip_device_info(glacier_hip_context *ctx, glacier_hip_device_info_t *out);
+int glacier_hip_allocation_limits(glacier_hip_context *ctx, glacier_hip_allocation_limits_t *out);
+/* Last HIP error string recorded on this context ("" if none). */
+const char *glacier_hip_last_error(glacier_hip_context *ctx);
+/* Synchronize the context stream. */
+int glacier_hip_synchronize(glacier_hip_context *ctx);
+
+/* ---- device capability (device_capability_contract.zig:132-150,
+ *      capabilityRootV1 :331-350) ------------------------------------------ */
+typedef struct {
+    uint64_t abi_version;            /* 0x4744434100000001 */
+    uint64_t backend_kind;           /* 3 = portable_compute */
+    uint64_t device_class;           /* 2 = accelerator */
+    uint64_t operation_profile_bits; /* matvec_int4_f32_bounded (1<<2) */
+    uint64_t operator_bits;
+    uint64_t element_type_bits;
+    uint64_t numerical_policy_bits;
+    uint64_t feature_bits;
+    uint64_t max_single_allocation_bytes;
+    uint64_t max_total_device_bytes;
+    uint64_t max_queue_slots;
+    uint8_t backend_sha256[32];
+    uint8_t device_sha256[32];
+    uint8_t driver_sha256[32];
+    uint8_t placement_sha256[32];
+    uint8_t capability_sha256[32];   /* sealed root over every field above */
+} glacier_hip_device_capability_v1_t;
+
+int glacier_hip_device_capability_v1(glacier_hip_context *ctx,
+                                     glacier_hip_device_capability_v1_t *out);
+
+/* ---- buffers (backend.zig:532-550) and the allocation lease adapter
+ *      (device_allocation_lease.zig:323-348: quote is side-effect free,
+ *      a failed allocate creates nothing, a failed free leaves it live) ---- */
+typedef struct {
+    uint64_t id;                 /* 0 = none */
+    uint64_t requested_bytes;
+    uint64_t charged_bytes;      /* granularity-rounded */
+} glacier_hip_buffer_token_t;
+
+typedef struct {
+    uint64_t id;
+    uint64_t requested_bytes;
+    uint64_t charged_bytes;
+    uint64_t device_address;     /* HBM address, for kernels and tests */
+} glacier_hip_buffer_info_t;
+
+typedef struct {
+    uint64_t requested_bytes;
+    uint64_t charged_bytes;
+    uint64_t context_epoch;      /* binds the quote to this context */
+} glacier_hip_allocation_quote_t;
+
+int glacier_hip_buffer_create(glacier_hip_context *ctx, uint64_t requested_length,
+                              glacier_hip_buffer_token_t *out);
+int glacier_hip_buffer_info(glacier_hip_context *ctx, const glacier_hip_buffer_token_t *token,
+                            glacier_hip_buffer_info_t *out);
+int glacier_hip_buffer_release(glacier_hip_context *ctx, const glacier_hip_buffer_token_t *token);
+int glacier_hip_live_buffer_count(glacier_hip_context *ctx, uint64_t *out);
+int glacier_hip_allocation_quote(glacier_hip_context *ctx, uint64_t requested_bytes,
+                                 glacier_hip_allocation_quote_t *out);
+int glacier_hip_allocation_allocate(glacier_hip_context *ctx,
+                                    const glacier_hip_allocation_quote_t *quote,
+                                    glacier_hip_buffer_token_t *out);
+int glacier_hip_allocation_free(glacier_hip_context *ctx, const glacier_hip_buffer_token_t *token);
+
+/* ---- persistent INT4 weights (backend.zig:570-598) -----------------------
+ * `packed` is the reference's row-major layout [out_f * in_f / 2] bytes, low
+ * nibble = even element, code u decodes to (u - 7) * scale (quant.zig:50-54,
+ * int4_matmul.zig:22-25). Scales are row-major [out_f][in_f / group]. The
+ * weight is re-laid out on the device into 16-row x 128-column MFMA tiles;
+ * the arithmetic is unchanged. Requirements: group_size == 32,
+ * out_f % 16 == 0, in_f % 128 == 0. */
+glacier_hip_int4_weight *glacier_hip_int4_weight_create(
+    glacier_hip_context *ctx, const uint8_t *packed, uint64_t packed_bytes,
+    const float *scales, uint64_t scale_count, uint32_t group_size,
+    uint32_t in_features, uint32_t out_features);
+/* Same with IEEE fp16 scales (the reference's optional fp16 mirror,
+ * int4_weights.zig:346-384). */
+glacier_hip_int4_weight *glacier_hip_int4_weight_create_f16scales(
+    glacier_hip_context *ctx, const uint8_t *packed, uint64_t packed_bytes,
+    const uint16_t *scales_f16, uint64_t scale_count, uint32_t group_size,
+    uint32_t in_features, uint32_t out_features);
+void glacier_hip_int4_weight_destroy(glacier_hip_int4_weight *weight);
+int glacier_hip_live_weight_count(glacier_hip_context *ctx, uint64_t *out);
+/* Bytes the weight occupies in HBM (codes + fp16 scales). */
+uint64_t glacier_hip_int4_weight_device_bytes(const glacier_hip_int4_weight *weight);
+
+/* Synchronous host-buffer matvec (glacier_metal_int4_matvec_dispatch,
+ * backend.zig:599-606): y[out_f] = W x, one row, F32 activation semantics. */
+int glacier_hip_int4_matvec_dispatch(glacier_hip_context *ctx, glacier_hip_int4_weight *weight,
+                                     const float *input, uint64_t input_count,
+                                     float *output, uint64_t output_count);
+
+/* Device-resident batched GEMV: y[m][out_f] = x[m][in_f] W^T (+ bias[out_f]),
+ * m in 1..32. x is f32 or bf16 (x_dtype), y is f32. Replaces
+ * linearInt4WeightQ8 / linearInt4Weight (int4_matmul.zig:422-531, 2957-2981)
+ * for one projection. Asynchronous on `stream`. */
+int glacier_hip_int4_gemv(glacier_hip_context *ctx, glacier_hip_int4_weight *weight,
+                          const void *x_dev, int x_dtype, uint32_t m,
+                          const float *bias_dev, float *y_dev, int activation,
+                          void *stream);
+
+/* ---- fused RMSNorm (kernels.zig:141-220) -------------------------------- */
+int glacier_hip_rmsnorm(glacier_hip_context *ctx, const float *x_dev, const float *w_dev,
+                        uint32_t rows, uint32_t dim, float eps, float *out_dev, void *stream);
+
+/* ---- paged-KV GQA decode attention (forward.zig:478-533,
+ *      paged_attention.zig:108-210) ----------------------------------------
+ * One query row per lane. kv_pool_dev holds pages laid out as the reference's
+ * page payload (paged_kv_cache.zig:1421-1444):
+ *   page[layer][K=0,V=1][16 positions][num_kv_heads * head_dim]
+ * in f32 or f16 (kv_dtype). page_table_dev is [lanes][max_pages_per_lane]
+ * int32 physical page ids; ctx_lens_dev[lanes] int32 = attended positions
+ * (the new row included). q_dev/out_dev are [lanes][num_heads * head_dim]. */
+int glacier_hip_paged_attention(glacier_hip_context *ctx, const float *q_dev,
+                                const void *kv_pool_dev, int kv_dtype,
+                                const int32_t *page_table_dev, uint32_t max_pages_per_lane,
+                                const int32_t *ctx_lens_dev, uint32_t lanes,
+                                uint32_t layer, uint32_t num_layers, uint32_t num_heads,
+                                uint32_t num_kv_heads, uint32_t head_dim,
+                                uint32_t max_ctx, float *out_dev, void *stream);
+
+/* ---- greedy samplers (sampling.zig:194-206, :55-105) ---------------------
+ * rows independent logit rows of length n. Results are written to host
+ * memory after the call synchronizes the stream. */
+typedef struct {
+    uint64_t token_index;
+    uint64_t eligible_rows;
+    int32_t status;              /* GLACIER_HIP_OK / _INVALID_MASK / _ELIGIBLE_NAN */
+    int32_t reserved;
+} glacier_hip_argmax_result_t;
+
+int glacier_hip_argmax(glacier_hip_context *ctx, const float *logits_dev, uint64_t n,
+                       uint32_t rows, uint64_t *index_host, void *stream);
+/* words_dev: [rows][word_count] u64 LSB-first eligibility bits;
+ * word_count must equal ceil(n / 64) (checked on the host). */
+int glacier_hip_eligible_argmax(glacier_hip_context *ctx, const float *logits_dev, uint64_t n,
+                                const uint64_t *words_dev, uint64_t word_count, uint32_t rows,
+                                glacier_hip_argmax_result_t *results_host, void *stream);
+
+/* ---- model: Llama/Qwen pre-norm decoder with INT4 projections ------------
+ * (forward.zig:36-81 LayerWeights/LayerConfig, loader.zig:31 ModelConfig) */
+typedef struct {
+    uint32_t num_layers, dim, hidden_dim, num_heads, num_kv_heads, head_dim;
+    uint32_t vocab_size, group_size;
+    float rms_eps, rope_theta;
+} glacier_hip_model_config_t;
+
+/* Host-side tensors of one layer in the reference's layouts. Biases may be
+ * NULL. Scales are f32 (fp16 values are accepted exactly). */
+typedef struct {
+    const float *input_norm, *post_attn_norm;              /* [dim] */
+    const uint8_t *wq, *wk, *wv, *wo, *w_gate, *w_up, *w_down;
+    const float *sq, *sk, *sv, *so, *s_gate, *s_up, *s_down;
+    const float *bq, *bk, *bv;
+} glacier_hip_layer_host_t;
+
+glacier_hip_model *glacier_hip_model_create(glacier_hip_context *ctx,
+                                            const glacier_hip_model_config_t *cfg);
+int glacier_hip_model_set_layer(glacier_hip_model *model, uint32_t layer,
+                                const glacier_hip_layer_host_t *w);
+int glacier_hip_model_set_globals(glacier_hip_model *model, const float *token_embedding,
+                                  const float *final_norm, const uint8_t *lm_head_packed,
+                                  const float *lm_head_scales);
+/* Random-init every tensor from `seed` with the synthetic generator below
+ * (host-generated, then uploaded). */
+int glacier_hip_model_init_random(glacier_hip_model *model, uint64_t seed);
+void glacier_hip_model_destroy(glacier_hip_model *model);
+uint64_t glacier_hip_model_weight_bytes(const glacier_hip_model *model);
+
+/* ---- sessions: paged KV pool + lanes, the per-token step -----------------
+ * A session owns a pool of KV pages (each holds 16 positions of every layer,
+ * paged_kv_cache.zig:1-8) and up to max_lanes request-local page tables.
+ * Each decode step runs one token for each listed lane: embedding gather ->
+ * layers -> final norm -> LM head -> greedy argmax (optionally eligible).
+ * The per-token publication is atomic (paged_token_txn.zig:346-600): the
+ * kernels write K/V rows into a provisional row of the lane's current page;
+ * only after the argmax result is read back does the host commit, per lane,
+ * the KV length + page-map root, the sampling counter and the output token.
+ * On any error nothing of that step is committed. */
+typedef struct {
+    uint32_t max_lanes;
+    uint32_t max_positions;      /* per lane */
+    uint32_t total_pages;        /* pool size; 0 = max_lanes * ceil(max_positions/16) */
+    int32_t kv_dtype;            /* GLACIER_HIP_F32 or GLACIER_HIP_F16 */
+    int32_t layer_activation;    /* GLACIER_HIP_ACT_*; AUTO = reference x86 dispatch */
+    int32_t head_activation;     /* usually AUTO (=> F32 for V > 65536) */
+    int32_t use_graph;           /* capture the decode step in a hipGraph */
+    int32_t reserved;
+} glacier_hip_session_options_t;
+
+typedef struct {
+    uint64_t cache_instance;
+    uint64_t generation;
+    uint64_t committed_len;
+    uint64_t committed_pages;
+    uint8_t ownership_sha256[32];
+} glacier_hip_page_map_root_t;     /* PageMapRootV1 (paged_kv_cache.zig:64-71) */
+
+typedef struct {
+    uint64_t kv_positions;
+    uint64_t published_tokens;
+    uint64_t sampling_calls;
+    uint64_t rng_state[4];       /* DefaultPrng state; greedy never advances it */
+    uint8_t output_sha256[32];   /* tokenSequenceSha256 (generate.zig:3193) */
+} glacier_hip_lane_state_t;
+
+glacier_hip_session *glacier_hip_session_create(glacier_hip_model *model,
+                                                const glacier_hip_session_options_t *opts);
+void glacier_hip_session_destroy(glacier_hip_session *s);
+/* Start a request on `lane` (resets its cache and counters). */
+int glacier_hip_session_lane_begin(glacier_hip_session *s, uint32_t lane, uint64_t seed);
+/* Prefill: run `n` prompt tokens on `lane` and produce the first greedy
+ * token (generate.zig:5080-5160). logits_host: optional [vocab]. */
+int glacier_hip_session_prefill(glacier_hip_session *s, uint32_t lane, const uint32_t *tokens,
+                                uint32_t n, uint32_t *first_token, float *logits_host);
+/* One decode step for `count` lanes: lanes[i] consumes tokens[i] at its next
+ * position. next_tokens receives the greedy result per lane. logits_host:
+ * optional [count][vocab]. eligible_words_host: optional
+ * [count][ceil(vocab/64)] masks (sampling.zig:55-105 semantics). */
+int glacier_hip_session_decode_step(glacier_hip_session *s, const uint32_t *lanes,
+                                    const uint32_t *tokens, uint32_t count,
+                                    const uint64_t *eligible_words_host,
+                                    uint32_t *next_tokens, float *logits_host);
+int glacier_hip_session_lane_root(glacier_hip_session *s, uint32_t lane,
+                                  glacier_hip_page_map_root_t *out);
+int glacier_hip_session_lane_state(glacier_hip_session *s, uint32_t lane,
+                                   glacier_hip_lane_state_t *out);
+/* Logical KV digest of a lane (logicalKvPrefixSha256, generate.zig:3150),
+ * computed over K/V values widened to f32 bit patterns. */
+int glacier_hip_session_lane_kv_sha256(glacier_hip_session *s, uint32_t lane, uint8_t out[32]);
+/* Copy one K or V row (f32) of a lane out of the paged pool. */
+int glacier_hip_session_read_kv_row(glacier_hip_session *s, uint32_t lane, uint32_t layer,
+                                    int value, uint32_t position, float *out_host);
+/* Physical page of a lane's logical page (-1 if not installed). */
+int glacier_hip_session_page_of(glacier_hip_session *s, uint32_t lane, uint32_t logical_page,
+                                int32_t *physical_out);
+/* Test hook: make the next decode step fail after its kernels ran but before
+ * commit (forces the abort path, as a failed sink/ack would). */
+int glacier_hip_session_inject_failure(glacier_hip_session *s, int enable);
+
+/* ---- synthetic random-init generator (host, deterministic) ---------------
+ * Counter-based SplitMix64 streams keyed by (seed, tensor id):
+ *  - INT4 codes: uniform nibbles u in 0..15 (decode u - 7 in [-7, 8]);
+ *  - scales: fp16(|N(0, sigma)|) via Box-Muller in double;
+ *  - f32 tensors: N(0, sigma);
+ *  - token ids: uniform in [0, vocab). */
+void glacier_hip_synth_int4(uint64_t seed, uint64_t tensor_id, uint8_t *packed, uint64_t bytes);
+void glacier_hip_synth_scales_f16(uint64_t seed, uint64_t tensor_id, float sigma,
+                                  uint16_t *out, uint64_t count);
+void glacier_hip_synth_normal_f32(uint64_t seed, uint64_t tensor_id, float sigma,
+                                  float *out, uint64_t count);
+void glacier_hip_synth_tokens(uint64_t seed, uint64_t tensor_id, uint32_t vocab,
+                              uint32_t *out, uint64_t count);
+/* Tensor ids used by glacier_hip_model_init_random. */
+uint64_t glacier_hip_synth_tensor_id(uint32_t layer, uint32_t which);
+float glacier_hip_f16_to_f32(uint16_t h);
+
+/* Version of this ABI. */
+uint64_t glacier_hip_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,211 @@
+"""End-to-end token loop on the GPU against the CPU oracle (serial reference
+mode of prepared_text_session.zig:81-105: Q8 layer projections, f32 head,
+greedy), through the C ABI.
+
+Bars: identical greedy token sequences; logits within 1e-2 max-relative
+error (max |gpu - oracle| / max |oracle|); page-map roots, output digests and
+sampler counters exactly as the reference's transaction rules produce them.
+"""
+import hashlib
+import struct
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(num_layers=2, dim=256, hidden_dim=512, num_heads=4, num_kv_heads=2, head_dim=64,
+            vocab_size=4096, group_size=32, rms_eps=1e-6, rope_theta=1e6)
+SEED = 0x5EED
+
+
+@pytest.fixture(scope="module")
+def tiny(gh, gctx, ora):
+    host = gh.random_model_host(TINY, SEED)
+    om = ora.OracleModel(TINY, host)
+    m = gh.Model(gctx, TINY)
+    m.init_random(SEED)
+    yield host, om, m
+    m.close()
+
+
+def _run_gpu(sess, lane, prompt, max_new, logits_at=()):
+    first, lg0 = sess.prefill(lane, prompt, want_logits=True)
+    toks = [first]
+    logits = {0: lg0}
+    for s in range(1, max_new):
+        nxt, lg = sess.step([lane], [toks[-1]], want_logits=True)
+        toks.append(int(nxt[0]))
+        if s in logits_at:
+            logits[s] = lg[0]
+    return toks, logits
+
+
+def _rel(a, b):
+    return float(np.max(np.abs(a - b)) / np.max(np.abs(b)))
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_tiny_greedy_matches_oracle(gh, tiny, use_graph):
+    host, om, m = tiny
+    prompt = gh.synth_tokens(SEED, 99, TINY["vocab_size"], 20)
+    max_new = 24
+    want, wl, kv_sha, out_sha = om.generate(prompt, max_new, logits_steps=[0, max_new - 1])
+    sess = gh.Session(m, max_lanes=1, max_positions=64, use_graph=use_graph)
+    try:
+        sess.begin(0, seed=7)
+        toks, logits = _run_gpu(sess, 0, prompt, max_new, logits_at=(max_new - 1,))
+        print("gpu", toks, "\noracle", want.tolist(), flush=True)
+        assert toks == want.tolist()
+        assert _rel(logits[0], wl[0]) < 1e-2
+        assert _rel(logits[max_new - 1], wl[1]) < 1e-2
+        print("logit rel err", _rel(logits[0], wl[0]), _rel(logits[max_new - 1], wl[1]))
+        st = sess.state(0)
+        assert bytes(st.output_sha256) == out_sha
+        assert st.sampling_calls == max_new and st.published_tokens == max_new
+        assert st.kv_positions == len(prompt) + max_new - 1
+        assert list(st.rng_state) == gh_xoshiro(7)
+    finally:
+        sess.close()
+
+
+def gh_xoshiro(seed):
+    import oracle
+
+    return oracle.xoshiro256_init(seed)
+
+
+def test_page_roots_follow_reference_chain(gh, tiny, ora):
+    host, om, m = tiny
+    sess = gh.Session(m, max_lanes=2, max_positions=64)
+    try:
+        sess.begin(0)
+        r0 = sess.root(0)
+        inst = r0.cache_instance
+        kvd = TINY["num_kv_heads"] * TINY["head_dim"]
+        assert bytes(r0.ownership_sha256) == ora.empty_ownership_digest(inst, TINY["num_layers"], kvd, 64)
+        prompt = gh.synth_tokens(SEED, 5, TINY["vocab_size"], 17)
+        tok = sess.prefill(0, prompt)
+        digest = ora.empty_ownership_digest(inst, TINY["num_layers"], kvd, 64)
+        for page in range(2):  # rows 0 and 16 installed pages 0 and 1 (generations 1, 2)
+            digest = ora.append_ownership_digest(digest, inst, page, page + 1)
+        r = sess.root(0)
+        assert (r.committed_len, r.committed_pages, r.generation) == (17, 2, 1 + 17)
+        assert bytes(r.ownership_sha256) == digest
+        # the logical KV digest of the device rows (generate.zig:3150-3172)
+        h = hashlib.sha256(b"glacier-logical-kv-state-v1\x00" +
+                           struct.pack("<3Q", TINY["num_layers"], kvd, 17))
+        for l in range(TINY["num_layers"]):
+            for v in (0, 1):
+                for p in range(17):
+                    h.update(sess.kv_row(0, l, v, p, kvd).astype("<f4").tobytes())
+        assert sess.kv_sha256(0) == h.digest()
+        assert sess.page_of(0, 0) >= 0 and sess.page_of(0, 2) == -1
+    finally:
+        sess.close()
+
+
+def test_failed_step_publishes_nothing(gh, tiny):
+    host, om, m = tiny
+    sess = gh.Session(m, max_lanes=1, max_positions=64)
+    try:
+        sess.begin(0)
+        prompt = gh.synth_tokens(SEED, 6, TINY["vocab_size"], 15)
+        t0 = sess.prefill(0, prompt)
+        before_root, before_state = sess.root(0), sess.state(0)
+        sess.inject_failure(True)
+        rc, _ = sess.step([0], [t0], raise_on_error=False)
+        assert rc == gh.DEVICE_ERROR
+        sess.inject_failure(False)
+        after_root, after_state = sess.root(0), sess.state(0)
+        assert bytes(after_root) == bytes(before_root)  # row 15 -> page 0, no install
+        assert bytes(after_state) == bytes(before_state)
+        # the retried step (it installs page 1 at row 16 next) matches a clean run
+        t1 = int(sess.step([0], [t0])[0])
+        t2 = int(sess.step([0], [t1])[0])
+        clean = gh.Session(m, max_lanes=1, max_positions=64)
+        clean.begin(0)
+        c0 = clean.prefill(0, prompt)
+        c1 = int(clean.step([0], [c0])[0])
+        c2 = int(clean.step([0], [c1])[0])
+        assert (t0, t1, t2) == (c0, c1, c2)
+        assert sess.root(0).committed_pages == clean.root(0).committed_pages
+        clean.close()
+        # an abort on a page-installing row releases the page and its generation
+        pages_before = sess.root(0).committed_pages
+        sess.inject_failure(False)
+        for _ in range(15):
+            t2 = int(sess.step([0], [t2])[0])
+        assert sess.root(0).committed_len == 32
+        sess.inject_failure(True)
+        rc, _ = sess.step([0], [t2], raise_on_error=False)
+        assert rc == gh.DEVICE_ERROR and sess.page_of(0, 2) == -1
+        sess.inject_failure(False)
+        sess.step([0], [t2])
+        assert sess.root(0).committed_pages == pages_before + 1
+    finally:
+        sess.close()
+
+
+def test_multi_lane_matches_independent_runs(gh, tiny):
+    host, om, m = tiny
+    prompts = [gh.synth_tokens(SEED, 40 + i, TINY["vocab_size"], n) for i, n in enumerate([5, 16, 33])]
+    max_new = 10
+    wants = [om.generate(p, max_new)[0].tolist() for p in prompts]
+    sess = gh.Session(m, max_lanes=3, max_positions=64)
+    try:
+        toks = []
+        for i, p in enumerate(prompts):
+            sess.begin(i)
+            toks.append([sess.prefill(i, p)])
+        for _ in range(max_new - 1):
+            nxt = sess.step([2, 0, 1], [toks[2][-1], toks[0][-1], toks[1][-1]])
+            toks[2].append(int(nxt[0]))
+            toks[0].append(int(nxt[1]))
+            toks[1].append(int(nxt[2]))
+        assert toks == wants
+    finally:
+        sess.close()
+
+
+def test_eligible_step_matches_masked_argmax(gh, tiny, ora):
+    host, om, m = tiny
+    V = TINY["vocab_size"]
+    sess = gh.Session(m, max_lanes=1, max_positions=64)
+    try:
+        sess.begin(0)
+        t0 = sess.prefill(0, gh.synth_tokens(SEED, 8, V, 9))
+        rng = np.random.default_rng(3)
+        bits = rng.random(V) < 0.05
+        words = np.zeros(V // 64, np.uint64)
+        for i in np.nonzero(bits)[0]:
+            words[i // 64] |= np.uint64(1) << np.uint64(i % 64)
+        calls = sess.state(0).sampling_calls
+        nxt, lg = sess.step([0], [t0], eligible=words[None], want_logits=True)
+        rc, idx, rows = ora.argmax_eligible(lg[0], words)
+        assert rc == 0 and int(nxt[0]) == idx and bits[idx]
+        assert sess.state(0).sampling_calls == calls  # posthead path counts no sampler call
+        bad = words.copy()
+        bad[:] = 0
+        rc, _ = sess.step([0], [int(nxt[0])], eligible=bad[None], raise_on_error=False)
+        assert rc == gh.INVALID_MASK
+        assert sess.root(0).committed_len == 10
+    finally:
+        sess.close()
+
+
+def test_cache_full_is_rejected_before_launch(gh, tiny):
+    host, om, m = tiny
+    sess = gh.Session(m, max_lanes=2, max_positions=32, total_pages=2)
+    try:
+        sess.begin(0)
+        sess.begin(1)
+        t = sess.prefill(0, gh.synth_tokens(SEED, 9, TINY["vocab_size"], 17))  # takes both pages
+        with pytest.raises(gh.GlacierHipError) as e:
+            sess.prefill(1, [1, 2])
+        assert e.value.code == gh.CACHE_FULL
+        assert sess.root(1).committed_len == 0
+        assert sess.root(0).committed_len == 17
+        sess.step([0], [t])
+    finally:
+        sess.close()
