@@ -1,0 +1,214 @@
+#!/usr/bin/env python3
+"""Headline benchmark: Qwen2.5-7B-shaped INT4 decode on one MI355X.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+One "step" is one greedy decode token of the batch-1 lane (the full token
+loop: embedding gather, 28 layers, final norm, LM head, argmax, per-token
+commit). `value` = tokens/s over exactly K timed steps with the weights and
+KV already resident in HBM. The same JSON line carries:
+  * lanes32     32 concurrent lanes decoding together (tokens/s, aggregate);
+  * gemv        the INT4 GEMV kernel timed alone on the BASELINE config-2
+                shapes and on the 7B gate/up projection, with HIP events on
+                the launch stream;
+  * roofline    for the dominant kernel (the fused 7B gate/up GEMV, 53% of a
+                token's weight bytes): algorithmic bytes / average duration;
+  * cpu_baseline the CPU oracle (the reference algorithm restated in C) on the
+                same model, timed on this host's cores over a bounded sample.
+Weights are random-init from a fixed seed (no checkpoints exist offline).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "glacier-engine_amd")]
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+SEED = 0x474C4143
+CFG_7B = dict(num_layers=28, dim=3584, hidden_dim=18944, num_heads=28, num_kv_heads=4,
+              head_dim=128, vocab_size=152064, group_size=32, rms_eps=1e-6, rope_theta=1e6)
+# BASELINE config 2 GEMV shapes [N, K] plus the fused 7B gate/up projection
+GEMV_SHAPES = [(4096, 4096), (11008, 4096), (4096, 11008), (18944, 3584), (152064, 3584)]
+GATE_UP = (2 * 18944, 3584)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemv_bytes(n, k, m, act_bytes=4):
+    # algorithmic bytes: packed codes + fp16 scales + activations + f32 outputs
+    return n * k // 2 + 2 * n * k // 32 + m * k * act_bytes + m * n * 4
+
+
+def time_gemv(gh, ctx, torch, n, k, m, reps, act):
+    L = gh.lib()
+    packed = gh.synth_int4(SEED, n * 7 + k, n * k // 2)
+    s16 = gh.synth_scales_f16(SEED, n * 11 + k, n * k // 32)
+    w = ctx.weight(packed, s16, k, n)
+    del packed, s16
+    try:
+        stream = torch.cuda.Stream()  # non-null handle: our launches and the events share it
+        x = torch.randn((m, k), device="cuda", dtype=torch.float32)
+        y = torch.empty((m, n), device="cuda", dtype=torch.float32)
+        planes = torch.empty(L.glacier_hip_activation_bytes(m, k, act), dtype=torch.uint8, device="cuda")
+        torch.cuda.synchronize()
+        gh.check(L.glacier_hip_activation_prepare(ctx.h, x.data_ptr(), gh.F32, m, k, act,
+                                                  planes.data_ptr(), stream.cuda_stream), "prepare")
+        for _ in range(5):
+            gh.check(L.glacier_hip_int4_gemv_prepared(ctx.h, w, planes.data_ptr(), m, act, None,
+                                                      y.data_ptr(), stream.cuda_stream), "gemv")
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            L.glacier_hip_int4_gemv_prepared(ctx.h, w, planes.data_ptr(), m, act, None,
+                                             y.data_ptr(), stream.cuda_stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1000.0 / reps
+        b = gemv_bytes(n, k, m)
+        return dict(N=n, K=k, M=m, act="q8" if act == gh.ACT_Q8 else "f32", us=round(us, 2),
+                    bytes=b, gbs=round(b / us / 1e3, 1), frac=round(b / us / 1e3 / HBM_PEAK_GBS, 4))
+    finally:
+        L.glacier_hip_int4_weight_destroy(w)
+
+
+def auto_act(gh, n, k):
+    return gh.ACT_F32 if (n > 65536 or k > 16384) else gh.ACT_Q8
+
+
+def decode_batch1(gh, sess, prompt, warmup, steps):
+    tok = sess.prefill(0, prompt)
+    for _ in range(warmup):
+        tok = int(sess.step([0], [tok])[0])
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tok = int(sess.step([0], [tok])[0])
+    dt = time.perf_counter() - t0
+    return steps / dt, dt
+
+
+def decode_lanes(gh, sess, lanes, prompts, warmup, steps):
+    toks = []
+    for i in range(lanes):
+        sess.begin(i, seed=i)
+        toks.append(sess.prefill(i, prompts[i]))
+    ids = list(range(lanes))
+    for _ in range(warmup):
+        toks = [int(t) for t in sess.step(ids, toks)]
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        toks = [int(t) for t in sess.step(ids, toks)]
+    dt = time.perf_counter() - t0
+    return lanes * steps / dt, dt
+
+
+def cpu_baseline(host, prompt_tok, budget_s=15.0):
+    import oracle
+
+    oracle.build()
+    cores = len(os.sched_getaffinity(0))
+    cores = min(cores, 16)
+    oracle.set_threads(cores)
+    om = oracle.OracleModel(CFG_7B, host)
+    t0 = time.perf_counter()
+    om.generate(np.array([prompt_tok], np.uint32), 1)
+    one = time.perf_counter() - t0
+    n = max(2, min(64, int(budget_s / max(one, 1e-3))))
+    t0 = time.perf_counter()
+    om.generate(np.array([prompt_tok], np.uint32), n)
+    dt = time.perf_counter() - t0
+    return dict(value=round(n / dt, 3), unit="tokens/s", cores=cores, kind="port",
+                sample=f"oracle greedy run of the same 7B model: 1-token prompt + {n} tokens "
+                       f"({dt:.1f} s), Q8 layers / f32 head, {cores} threads row-split")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--prompt", type=int, default=128)
+    ap.add_argument("--lanes", type=int, default=32)
+    ap.add_argument("--lane-prompt", type=int, default=64)
+    ap.add_argument("--gemv-reps", type=int, default=50)
+    ap.add_argument("--gemv-only", action="store_true", help="only the GEMV kernel timing")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {a.gpus}); this build has no "
+              "multi-GPU path: lanes would shard across GPUs with no exchange.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import glacier_hip as gh
+
+    ctx = gh.Context(0)
+    info = ctx.info()
+    log(f"device {info.arch.decode()} CUs={info.compute_units}")
+
+    # ---- GEMV kernel alone ----
+    gemv = []
+    n, k = GATE_UP
+    dom = time_gemv(gh, ctx, torch, n, k, 1, a.gemv_reps * 2, gh.ACT_Q8)
+    log("gemv gate/up", dom)
+    if not a.gemv_only:
+        for (n, k) in GEMV_SHAPES:
+            for m in (1, 8):
+                r = time_gemv(gh, ctx, torch, n, k, m, a.gemv_reps, auto_act(gh, n, k))
+                log("gemv", r)
+                gemv.append(r)
+    roofline = dict(bound="hbm", achieved=dom["gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=dom["frac"], traffic=None)
+    if a.gemv_only:
+        print(json.dumps(dict(metric="int4 gemv HBM GB/s (7B gate/up, M=1)", value=dom["gbs"],
+                              unit="GB/s", roofline=roofline, gemv=[dom])))
+        return
+
+    # ---- 7B model ----
+    t0 = time.perf_counter()
+    host = gh.random_model_host(CFG_7B, SEED)
+    model = gh.Model(ctx, CFG_7B)
+    model.set_from_host(host)
+    log(f"7B model built in {time.perf_counter() - t0:.1f}s, {model.weight_bytes() / 1e9:.2f} GB in HBM")
+    prompt = gh.synth_tokens(SEED, 0x50524F4D, CFG_7B["vocab_size"], a.prompt)
+    max_pos = max(a.prompt, a.lane_prompt) + a.warmup + a.steps + 8
+    sess = gh.Session(model, max_lanes=max(1, a.lanes), max_positions=max_pos, kv_dtype=gh.F16)
+    sess.begin(0, seed=1)
+    tps1, dt1 = decode_batch1(gh, sess, prompt, a.warmup, a.steps)
+    log(f"batch-1 decode {tps1:.1f} tok/s ({dt1 * 1e3 / a.steps:.3f} ms/token)")
+    lanes = None
+    if a.lanes > 1:
+        prompts = [gh.synth_tokens(SEED, 0x4C414E45 + i, CFG_7B["vocab_size"], a.lane_prompt)
+                   for i in range(a.lanes)]
+        tpsL, dtL = decode_lanes(gh, sess, a.lanes, prompts, a.warmup, a.steps)
+        lanes = dict(value=round(tpsL, 1), unit="tokens/s", lanes=a.lanes,
+                     ms_per_step=round(dtL * 1e3 / a.steps, 3), prompt_len=a.lane_prompt,
+                     context_range=[a.lane_prompt, a.lane_prompt + a.warmup + a.steps])
+        log(f"{a.lanes}-lane decode {tpsL:.1f} tok/s")
+    sess.close()
+    model.close()
+    cpu = None if a.no_cpu_baseline else cpu_baseline(host, int(prompt[0]))
+    if cpu:
+        log("cpu baseline", cpu)
+    out = dict(
+        metric="decode tok/s at batch 1 (7B INT4)", value=round(tps1, 2), unit="tokens/s",
+        n_gpus=1, steps=a.steps, warmup=a.warmup, ms_per_step=round(dt1 * 1e3 / a.steps, 4),
+        higher_is_better=True, scaling="weak", vs_baseline=None, dtype="int8xint4 (Q8) / f32",
+        data="synthetic random-init weights (seed 0x474C4143), uniform random prompt ids",
+        config=dict(workload="Qwen2.5-7B-shaped INT4 g32 greedy decode, batch 1",
+                    prompt_len=a.prompt, kv="fp16 paged, 16 positions/page",
+                    parallelism="single GPU"),
+        roofline=roofline, cpu_baseline=cpu, lanes32=lanes, gemv=[dom] + gemv)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

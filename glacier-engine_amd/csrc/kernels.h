@@ -4,12 +4,12 @@
 //
 // INT4 weight tiles (replaces the reference's row-major packed layout,
 // int4_weights.zig:79-107; arithmetic unchanged):
-//   codes  uint4  [NB = N/16][KQ = K/128][64 lanes]
-//          lane l -> output row n = 16*nb + (l & 15), k-chunk c = l >> 4;
-//          u32 word j (0..3) covers group g = 4*kq + j, columns
-//          k = 32*g + 8*c + b (low nibble of byte b) and k + 4 (high nibble).
+//   codes  uint4   [NB = N/16][KQ = K/128][64 lanes]
+//          lane l = 16*j + n -> output row 16*nb + n, group g = 4*kq + j;
+//          u32 word w (0..3) covers columns k = 32*g + 8*w + b (low nibble of
+//          byte b) and k + 4 (high nibble), b = 0..3.
 //          Code u decodes to (u - 7) (int4_matmul.zig:22-25).
-//   scales uint2  [NB][KQ][16] = fp16 w_scale[n][4*kq + j], j = 0..3.
+//   scales uint16  [NB][KQ][64 lanes] = fp16 w_scale[row][g], same lane order.
 //
 // Activation digit planes (A operand of v_mfma_i32_16x16x32_i8):
 //   q      int8   [G][D][M][32]   (D = digit planes: 1 for Q8, 3 for F32)
@@ -58,12 +58,24 @@ struct GemvArgs {
   const float *bias;        // [N] logical order (EPI_PLAIN/QKV), may be null
   float *y;                 // EPI_PLAIN/RESID: [M][N]; SWIGLU: [M][N/2]
   const float *resid;       // EPI_RESID
-  int S;                    // K splits
-  float *partial;           // [S][M][N] (S > 1)
-  uint32_t *counters;       // [NB] zero-initialised, self-resetting
   int epi;
+  int prefetch;             // quads in flight per wave (4 or 8); 0 = default
+  int target_waves;         // launch-shape heuristic input; 0 = default
+  int ksplit_override;      // force the K split (tuning); 0 = heuristic
+  int rb_override;          // row blocks per workgroup with ksplit_override
+  int ksplit;               // set by launch_gemv
+  int force_mfma;           // use the MFMA path even for M <= 2 (tuning / tests)
   QkvArgs qkv;
 };
+
+// Launch shape of one GEMV: RB row blocks per workgroup, KS waves per row
+// block splitting K, activation planes in LDS when they fit.
+struct GemvShape {
+  int ksplit, rb, waves, grid;
+  bool lds_a;
+  size_t lds_bytes;
+};
+GemvShape plan_gemv(int N, int K, int M, int D, int target_waves = 0);
 
 // Prepare activation planes from x [M][K] (f32 or bf16), optionally
 // RMS-normalised with weight `norm_w` first (kernels.zig:141-220).
@@ -73,8 +85,6 @@ hipError_t launch_prep_act(const void *x, int x_bf16, const float *norm_w, float
 
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t st);
 
-// Choose the split count for a GEMV of NB row blocks and KQ quads.
-int choose_splits(int NB, int KQ, int M);
 
 hipError_t launch_rmsnorm(const float *x, const float *w, int rows, int dim, float eps,
                           float *out, hipStream_t st);

@@ -16,9 +16,18 @@
 #include <hip/hip_fp16.h>
 #include <math.h>
 
+#include <algorithm>
+
 namespace gk {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+// Streaming 16-byte load of weight codes (read once per token).
+static __device__ __forceinline__ uint4 load_stream(const uint4 *p) {
+  const v4u v = __builtin_nontemporal_load((const v4u *)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 static __device__ __forceinline__ float h2f(uint32_t bits16) {
   return __half2float(__ushort_as_half((unsigned short)bits16));
@@ -43,12 +52,51 @@ static __device__ __forceinline__ float load_x(const void *x, int bf16, size_t i
   return ((const float *)x)[i];
 }
 
+// Converts the 32-element group held by a 32-lane half-wave (one value per
+// lane, hl = lane within the half-wave) into D digit bytes per lane and the
+// group's meta. q layout [G][D][M][32], meta [G][M].
+template <int D>
+static __device__ __forceinline__ void quantize_group(float v, int hl, int g, int m, int M,
+                                                      int8_t *act_q, ActMeta *meta) {
+  float amax = fabsf(v);
+  for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
+  const float scale = amax / 127.0f;
+  const float inv_s = scale == 0.0f ? 0.0f : 1.0f / scale;
+  const float y = v * inv_s;
+  float q0f = roundf(y);
+  q0f = fminf(fmaxf(q0f, -127.0f), 127.0f);
+  int qd[3] = {(int)q0f, 0, 0};
+  if (D == 3) {
+    const float r1 = (y - q0f) * 128.0f;
+    const float q1f = roundf(r1);
+    const float r2 = (r1 - q1f) * 128.0f;
+    qd[1] = (int)q1f;
+    qd[2] = (int)roundf(r2);
+  }
+  int comb = 0;  // 128-adic combination of the digits; one reduction gives sum_d 128^(D-1-d) sum q_d
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    act_q[(((size_t)g * D + d) * M + m) * 32 + hl] = (int8_t)qd[d];
+    comb = comb * 128 + qd[d];
+  }
+  int sum = comb;
+  for (int o = 16; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 32);
+  if (hl == 0) {
+    ActMeta mm;
+    mm.scale = D == 3 ? scale * (1.0f / 16384.0f) : scale;
+    mm.corr = 7 * sum;
+    meta[(size_t)g * M + m] = mm;
+  }
+}
+
+// grid = (ceil(G / 8), M): each block converts 8 groups of one row; with a
+// norm weight every block first reduces the row's full sum of squares.
 template <int D>
 __global__ __launch_bounds__(256) void prep_act_kernel(const void *x, int x_bf16,
                                                        const float *norm_w, float eps, int M,
                                                        int K, int8_t *act_q, ActMeta *meta,
                                                        float *normed_out) {
-  const int m = blockIdx.x;
+  const int m = blockIdx.y;
   const int t = threadIdx.x;
   const size_t row = (size_t)m * K;
   __shared__ float red[8];
@@ -73,7 +121,9 @@ __global__ __launch_bounds__(256) void prep_act_kernel(const void *x, int x_bf16
   // One 32-lane half-wave per 32-element group.
   const int half = t >> 5, hl = t & 31;
   const int G = K >> 5;
-  for (int g = half; g < G; g += 8) {
+  {
+    const int g = blockIdx.x * 8 + half;
+    if (g >= G) return;
     const int k = (g << 5) + hl;
     float v = load_x(x, x_bf16, row + k);
     if (norm_w) {
@@ -81,70 +131,62 @@ __global__ __launch_bounds__(256) void prep_act_kernel(const void *x, int x_bf16
       v = tt * norm_w[k];
     }
     if (normed_out) normed_out[row + k] = v;
-    float amax = fabsf(v);
-    for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
-    const float scale = amax / 127.0f;
-    const float inv_s = scale == 0.0f ? 0.0f : 1.0f / scale;
-    const float y = v * inv_s;
-    float q0f = roundf(y);
-    q0f = fminf(fmaxf(q0f, -127.0f), 127.0f);
-    int q0 = (int)q0f;
-    int qd[3] = {q0, 0, 0};
-    if (D == 3) {
-      float r1 = (y - q0f) * 128.0f;
-      float q1f = roundf(r1);
-      float r2 = (r1 - q1f) * 128.0f;
-      float q2f = roundf(r2);
-      qd[1] = (int)q1f;
-      qd[2] = (int)q2f;
-    }
-    int sum = 0;
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-      act_q[(((size_t)g * D + d) * M + m) * 32 + hl] = (int8_t)qd[d];
-      int sd = qd[d];
-      for (int o = 16; o > 0; o >>= 1) sd += __shfl_xor(sd, o, 32);
-      sum = sum * 128 + sd;
-    }
-    if (hl == 0) {
-      ActMeta mm;
-      mm.scale = D == 3 ? scale * (1.0f / 16384.0f) : scale;
-      mm.corr = 7 * sum;
-      meta[(size_t)g * M + m] = mm;
-    }
+    quantize_group<D>(v, hl, g, m, M, act_q, meta);
   }
 }
 
 hipError_t launch_prep_act(const void *x, int x_bf16, const float *norm_w, float eps, int M,
                            int K, int D, int8_t *act_q, ActMeta *meta, float *normed_out,
                            hipStream_t st) {
+  const dim3 grid((K / 32 + 7) / 8, M);
   if (D == 1)
-    hipLaunchKernelGGL(prep_act_kernel<1>, dim3(M), dim3(256), 0, st, x, x_bf16, norm_w, eps,
-                       M, K, act_q, meta, normed_out);
+    hipLaunchKernelGGL(prep_act_kernel<1>, grid, dim3(256), 0, st, x, x_bf16, norm_w, eps, M,
+                       K, act_q, meta, normed_out);
   else
-    hipLaunchKernelGGL(prep_act_kernel<3>, dim3(M), dim3(256), 0, st, x, x_bf16, norm_w, eps,
-                       M, K, act_q, meta, normed_out);
+    hipLaunchKernelGGL(prep_act_kernel<3>, grid, dim3(256), 0, st, x, x_bf16, norm_w, eps, M,
+                       K, act_q, meta, normed_out);
   return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
-// K1: INT4 GEMV on i8 MFMA
+// K1: INT4 GEMV
 // ---------------------------------------------------------------------------
-static constexpr int kLdsBudget = 40 * 1024;
+// Tile = 16 rows x 128 columns (4 groups of 32): 1 KB of codes as 64 lanes x
+// 16 B, lane (j, n) = 16 * j + n holding group j of row n, plus 64 fp16
+// scales in the same lane order. A workgroup of W = RB * KS waves owns RB
+// row blocks; the KS waves of a row block split its K range and reduce their
+// partial sums through LDS in a fixed order (deterministic, no workgroup ever
+// waits on another). Activation planes are staged in LDS when they fit.
+//
+// M <= 2 (decode): every lane dots its whole group with v_dot4_i32_i8 (exact
+// integer per group) and applies the group's f32 scales itself; the four
+// lanes of a row are summed once at the end.
+// M > 2: v_mfma_i32_16x16x32_i8 per group, B operand = k-chunk c of the
+// group gathered with one coalesced dword load per group.
+static constexpr int kTargetWaves = 8192;
+static constexpr size_t kLdsLimit = 64 * 1024;
 
-static size_t act_slice_bytes(int quads, int M, int D) {
-  return (size_t)quads * 4 * ((size_t)D * M * 32 + (size_t)M * sizeof(ActMeta));
+static size_t planes_bytes(int groups, int M, int D) {
+  return (size_t)groups * ((size_t)D * M * 32 + (size_t)M * sizeof(ActMeta));
 }
 
-int choose_splits(int NB, int KQ, int M) {
-  // Enough waves to cover 256 CUs x 8, at least two quads per split, and
-  // an activation slice that fits the LDS budget.
-  int S = (2048 + NB - 1) / NB;
-  int max_s = KQ >= 4 ? KQ / 2 : 1;
-  if (S > max_s) S = max_s;
-  if (S < 1) S = 1;
-  while (S < KQ && act_slice_bytes((KQ + S - 1) / S, M, 3) > (size_t)kLdsBudget) ++S;
-  return S;
+GemvShape plan_gemv(int N, int K, int M, int D, int target_waves) {
+  GemvShape p;
+  const int NB = N / 16, KQ = K / 128;
+  if (target_waves <= 0) target_waves = kTargetWaves;
+  int ks = (target_waves + NB - 1) / NB;
+  const int max_ks = KQ >= 4 ? std::min(16, KQ / 2) : 1;
+  ks = std::max(1, std::min(ks, max_ks));
+  int rb = std::max(1, std::min(16 / ks, 4));
+  p.ksplit = ks;
+  p.rb = rb;
+  p.waves = ks * rb;
+  const size_t red = (size_t)p.waves * ((M + 15) / 16) * 4 * 64 * sizeof(float);
+  const size_t planes = planes_bytes(K / 32, M, D);
+  p.lds_a = planes <= kLdsLimit;
+  p.lds_bytes = std::max(p.lds_a ? planes : 0, red);
+  p.grid = (NB + rb - 1) / rb;
+  return p;
 }
 
 static __device__ __forceinline__ float silu_mul(float g, float u) {
@@ -154,35 +196,56 @@ static __device__ __forceinline__ float silu_mul(float g, float u) {
   return t * u;
 }
 
-template <int D, int MT>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+template <int D, int MT, int U, bool LDS_A, bool DOT4, int LB>
+__global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int NB = a.N >> 4, KQ = a.K >> 7;
-  const int s = blockIdx.y;
-  const int kq0 = (s * KQ) / a.S, kq1 = ((s + 1) * KQ) / a.S;
-  const int nq = kq1 - kq0;
+  const int KS = a.ksplit;
+  const int NB = a.N >> 4, KQ = a.K >> 7, G = a.K >> 5;
   const int M = a.M;
-
-  // Stage this split's activation slice in LDS.
-  const size_t qbytes = (size_t)nq * 4 * D * M * 32;
-  const size_t mbytes = (size_t)nq * 4 * M * sizeof(ActMeta);
-  {
-    const uint4 *src = (const uint4 *)(a.act_q + (size_t)kq0 * 4 * D * M * 32);
-    uint4 *dst = (uint4 *)smem;
-    for (size_t i = threadIdx.x; i < qbytes / 16; i += 256) dst[i] = src[i];
-    const uint2 *msrc = (const uint2 *)(a.act_meta + (size_t)kq0 * 4 * M);
-    uint2 *mdst = (uint2 *)(smem + qbytes);
-    for (size_t i = threadIdx.x; i < mbytes / 8; i += 256) mdst[i] = msrc[i];
-  }
-  __syncthreads();
-  const int8_t *sq = (const int8_t *)smem;
-  const ActMeta *sm = (const ActMeta *)(smem + qbytes);
-
-  const int nb = blockIdx.x * 4 + wave;
-  if (nb >= NB) return;
+  const int ks = wave % KS;
+  const int nb = blockIdx.x * (int)(blockDim.x >> 6) / KS + wave / KS;
+  const int kq0 = (ks * KQ) / KS, kq1 = ((ks + 1) * KQ) / KS;
+  const int nq = kq1 - kq0;
   const int n_local = lane & 15, c = lane >> 4;
+
+  // The first U quads of weights are requested before the activation planes
+  // are staged, so the staging latency hides under the weight fetch.
+  const size_t tile0 = (size_t)min(nb, NB - 1) * KQ + kq0;
+  const uint4 *cp = a.codes + tile0 * 64 + lane;                       // DOT4: own 16 B
+  const uint32_t *cw = (const uint32_t *)a.codes + tile0 * 256 + n_local * 4 + c;  // MFMA
+  const uint16_t *spp = (const uint16_t *)a.scales + tile0 * 64;
+  uint4 wb[U];
+  uint16_t sb[U];
+  float4 sbm[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    if (u < nq) {
+      if (DOT4) {
+        wb[u] = load_stream(cp + (size_t)u * 64);
+        sb[u] = spp[(size_t)u * 64 + lane];
+      } else {
+        const uint32_t *w0 = cw + (size_t)u * 256;
+        wb[u] = make_uint4(w0[0], w0[64], w0[128], w0[192]);
+        const uint16_t *s0 = spp + (size_t)u * 64 + n_local;
+        sbm[u] = make_float4(h2f(s0[0]), h2f(s0[16]), h2f(s0[32]), h2f(s0[48]));
+      }
+    }
+
+  const size_t qbytes = (size_t)G * D * M * 32;
+  const size_t mbytes = (size_t)G * M * sizeof(ActMeta);
+  if (LDS_A) {
+    const uint4 *src = (const uint4 *)a.act_q;
+    uint4 *dst = (uint4 *)smem;
+    for (size_t i = threadIdx.x; i < qbytes / 16; i += blockDim.x) dst[i] = src[i];
+    const uint2 *msrc = (const uint2 *)a.act_meta;
+    uint2 *mdst = (uint2 *)(smem + qbytes);
+    for (size_t i = threadIdx.x; i < mbytes / 8; i += blockDim.x) mdst[i] = msrc[i];
+    __syncthreads();
+  }
+  const int8_t *aq = LDS_A ? (const int8_t *)smem : a.act_q;
+  const ActMeta *am = LDS_A ? (const ActMeta *)(smem + qbytes) : a.act_meta;
 
   float acc[MT][4];
 #pragma unroll
@@ -190,63 +253,91 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[mt][r] = 0.0f;
 
-  const uint4 *cp = a.codes + ((size_t)nb * KQ + kq0) * 64 + lane;
-  const uint2 *sp = a.scales + ((size_t)nb * KQ + kq0) * 16 + n_local;
-  constexpr int U = 4;
-  uint4 wb[U];
-  uint2 sb[U];
+  if (nb < NB) {
+    const v4i zero = {0, 0, 0, 0};
+    for (int q = 0; q < nq; q += U) {
+      uint4 wc[U];
+      uint16_t sc[U];
+      float4 scm[U];
 #pragma unroll
-  for (int u = 0; u < U; ++u)
-    if (u < nq) {
-      wb[u] = cp[(size_t)u * 64];
-      sb[u] = sp[(size_t)u * 16];
-    }
-  const v4i zero = {0, 0, 0, 0};
-  for (int q = 0; q < nq; q += U) {
-    uint4 wc[U];
-    uint2 sc[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      wc[u] = wb[u];
-      sc[u] = sb[u];
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (q + U + u < nq) {
-        wb[u] = cp[(size_t)(q + U + u) * 64];
-        sb[u] = sp[(size_t)(q + U + u) * 16];
+      for (int u = 0; u < U; ++u) {
+        wc[u] = wb[u];
+        if (DOT4) sc[u] = sb[u]; else scm[u] = sbm[u];
       }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (q + u >= nq) break;
-      const uint32_t wj[4] = {wc[u].x, wc[u].y, wc[u].z, wc[u].w};
-      const float wsj[4] = {h2f(sc[u].x & 0xFFFFu), h2f(sc[u].x >> 16), h2f(sc[u].y & 0xFFFFu),
-                            h2f(sc[u].y >> 16)};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int gl = (q + u) * 4 + j;  // group index within the slice
-        const long b = unpack_codes(wj[j]);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const int ma = mt * 16 + n_local;
-          v4i dd[D];
-#pragma unroll
-          for (int d = 0; d < D; ++d) {
-            long av = 0;
-            if (ma < M) av = *(const long *)(sq + (((size_t)gl * D + d) * M + ma) * 32 + c * 8);
-            dd[d] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b, zero, 0, 0, 0);
+      for (int u = 0; u < U; ++u)
+        if (q + U + u < nq) {
+          if (DOT4) {
+            wb[u] = load_stream(cp + (size_t)(q + U + u) * 64);
+            sb[u] = spp[(size_t)(q + U + u) * 64 + lane];
+          } else {
+            const uint32_t *w0 = cw + (size_t)(q + U + u) * 256;
+            wb[u] = make_uint4(w0[0], w0[64], w0[128], w0[192]);
+            const uint16_t *s0 = spp + (size_t)(q + U + u) * 64 + n_local;
+            sbm[u] = make_float4(h2f(s0[0]), h2f(s0[16]), h2f(s0[32]), h2f(s0[48]));
           }
+        }
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int m = mt * 16 + c * 4 + r;
-            if (m < M) {
-              int T = dd[0][r];
-              if (D == 3) T = dd[0][r] * 16384 + dd[1][r] * 128 + dd[2][r];
-              const ActMeta mm = sm[(size_t)gl * M + m];
-              const float v = (float)(T - mm.corr);
-              float tt = v * wsj[j];
-              tt = tt * mm.scale;
-              acc[mt][r] += tt;
+      for (int u = 0; u < U; ++u) {
+        if (q + u >= nq) break;
+        if constexpr (DOT4) {
+          // lane (j = c, n): all 32 codes of group g of row n
+          const int g = (kq0 + q + u) * 4 + c;
+          const uint32_t wj[4] = {wc[u].x, wc[u].y, wc[u].z, wc[u].w};
+          const float ws = h2f(sc[u]);
+#pragma unroll
+          for (int m = 0; m < 2; ++m) {
+            if (m >= M) break;
+            int T = 0;
+#pragma unroll
+            for (int d = 0; d < D; ++d) {
+              const int4 q0 = *(const int4 *)(aq + (((size_t)g * D + d) * M + m) * 32);
+              const int4 q1 = *(const int4 *)(aq + (((size_t)g * D + d) * M + m) * 32 + 16);
+              const int qa[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+              int t = 0;
+#pragma unroll
+              for (int w = 0; w < 4; ++w) {
+                t = __builtin_amdgcn_sdot4((int)(wj[w] & 0x0F0F0F0Fu), qa[2 * w], t, false);
+                t = __builtin_amdgcn_sdot4((int)((wj[w] >> 4) & 0x0F0F0F0Fu), qa[2 * w + 1], t, false);
+              }
+              T = T * 128 + t;
+            }
+            const ActMeta mm = am[(size_t)g * M + m];
+            const float v = (float)(T - mm.corr);
+            float tt = v * ws;
+            tt = tt * mm.scale;
+            acc[0][m] += tt;
+          }
+        } else {
+          const uint32_t wj[4] = {wc[u].x, wc[u].y, wc[u].z, wc[u].w};
+          const float wsj[4] = {scm[u].x, scm[u].y, scm[u].z, scm[u].w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int g = (kq0 + q + u) * 4 + j;  // absolute group index
+            const long b = unpack_codes(wj[j]);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              const int ma = mt * 16 + n_local;
+              v4i dd[D];
+#pragma unroll
+              for (int d = 0; d < D; ++d) {
+                long av = 0;
+                if (ma < M) av = *(const long *)(aq + (((size_t)g * D + d) * M + ma) * 32 + c * 8);
+                dd[d] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b, zero, 0, 0, 0);
+              }
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int m = mt * 16 + c * 4 + r;
+                if (m < M) {
+                  int T = dd[0][r];
+                  if constexpr (D == 3) T = dd[0][r] * 16384 + dd[1][r] * 128 + dd[2][r];
+                  const ActMeta mm = am[(size_t)g * M + m];
+                  const float v = (float)(T - mm.corr);
+                  float tt = v * wsj[j];
+                  tt = tt * mm.scale;
+                  acc[mt][r] += tt;
+                }
+              }
             }
           }
         }
@@ -254,37 +345,42 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     }
   }
 
-  // ---- split-K: deterministic last-arriving finisher ----
-  const int N = a.N;
-  const int n = nb * 16 + n_local;
-  if (a.S > 1) {
+  if constexpr (DOT4) {
+    // acc[0][m] of lane (j, n) sums the groups j, j + 4, ... of row n; add
+    // the four lanes of the row so lanes j = 0 hold m = 0.. M-1 as (c=0, r=m)
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = mt * 16 + c * 4 + r;
-        if (m < M) a.partial[((size_t)s * M + m) * N + n] = acc[mt][r];
-      }
-    __threadfence();
-    int last = 0;
-    if (lane == 0) last = (atomicAdd(&a.counters[nb], 1u) == (unsigned)(a.S - 1));
-    last = __shfl(last, 0);
-    if (!last) return;
-    __threadfence();
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = mt * 16 + c * 4 + r;
-        float tot = 0.0f;
-        if (m < M)
-          for (int ss = 0; ss < a.S; ++ss) tot += __builtin_nontemporal_load(&a.partial[((size_t)ss * M + m) * N + n]);
-        acc[mt][r] = tot;
-      }
-    if (lane == 0) a.counters[nb] = 0u;
+    for (int m = 0; m < 2; ++m) {
+      float v = acc[0][m];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      acc[0][m] = v;
+    }
   }
 
-  // ---- fused epilogues ----
+  // ---- split-K reduction through LDS, fixed order over ks ----
+  if (KS > 1) {
+    if (LDS_A) __syncthreads();  // the planes region is reused below
+    float *red = (float *)smem;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[((wave * MT + mt) * 4 + r) * 64 + lane] = acc[mt][r];
+    __syncthreads();
+    if (ks != 0) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float tot = acc[mt][r];
+        for (int s2 = 1; s2 < KS; ++s2) tot += red[(((wave + s2) * MT + mt) * 4 + r) * 64 + lane];
+        acc[mt][r] = tot;
+      }
+  }
+  if (nb >= NB) return;
+
+  // ---- fused epilogues: lane (c, n) owns rows m = 16 mt + 4 c + r of column n ----
+  const int N = a.N;
+  const int n = nb * 16 + n_local;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -364,21 +460,48 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     }
 }
 
-hipError_t launch_gemv(const GemvArgs &a, hipStream_t st) {
-  const int NB = a.N / 16, KQ = a.K / 128;
-  const int maxq = (KQ + a.S - 1) / a.S;
-  const size_t lds = act_slice_bytes(maxq, a.M, a.D);
-  dim3 grid((NB + 3) / 4, a.S);
+hipError_t launch_gemv(const GemvArgs &a0, hipStream_t st) {
+  GemvArgs a = a0;
   const int MT = (a.M + 15) / 16;
-  if (MT > 2) return hipErrorInvalidValue;
-#define GK_LAUNCH(DD, MM) \
-  hipLaunchKernelGGL((gemv_kernel<DD, MM>), grid, dim3(256), lds, st, a)
-  if (a.D == 1) {
-    if (MT == 1) GK_LAUNCH(1, 1); else GK_LAUNCH(1, 2);
-  } else {
-    if (MT == 1) GK_LAUNCH(3, 1); else GK_LAUNCH(3, 2);
+  if (MT > 2 || a.N % 16 || a.K % 128 || !a.act_q || !a.act_meta) return hipErrorInvalidValue;
+  GemvShape p = plan_gemv(a.N, a.K, a.M, a.D, a.target_waves);
+  if (a.ksplit_override > 0) {
+    p.ksplit = a.ksplit_override;
+    p.rb = a.rb_override > 0 ? a.rb_override : std::max(1, std::min(16 / p.ksplit, 4));
+    p.waves = p.ksplit * p.rb;
+    p.grid = (a.N / 16 + p.rb - 1) / p.rb;
+    const size_t red = (size_t)p.waves * MT * 4 * 64 * sizeof(float);
+    p.lds_bytes = std::max(p.lds_a ? planes_bytes(a.K / 32, a.M, a.D) : 0, red);
   }
-#undef GK_LAUNCH
+  a.ksplit = p.ksplit;
+  const int U = a.prefetch ? a.prefetch : 4;
+  dim3 grid(p.grid), block(64 * p.waves);
+  const bool dot4 = a.M <= 2 && !a.force_mfma;
+  const bool small = p.waves <= 4;
+  const size_t lds = p.lds_bytes;
+#define GK_KERNEL(DD, MM, UU, LL, T4, LBB) gemv_kernel<DD, MM, UU, LL, T4, LBB>
+#define GK_GO(DD, MM, UU, LL, T4)                                                              \
+  do {                                                                                       \
+    if (small) hipLaunchKernelGGL((GK_KERNEL(DD, MM, UU, LL, T4, 256)), grid, block, lds, st, a); \
+    else hipLaunchKernelGGL((GK_KERNEL(DD, MM, UU, LL, T4, 1024)), grid, block, lds, st, a);      \
+  } while (0)
+#define GK_PATH(DD, LL)                                          \
+  do {                                                          \
+    if (MT == 2) GK_GO(DD, 2, 4, LL, false);                    \
+    else if (dot4) {                                            \
+      if (U == 8) GK_GO(DD, 1, 8, LL, true); else GK_GO(DD, 1, 4, LL, true);   \
+    } else {                                                    \
+      if (U == 8) GK_GO(DD, 1, 8, LL, false); else GK_GO(DD, 1, 4, LL, false); \
+    }                                                           \
+  } while (0)
+  if (a.D == 1) {
+    if (p.lds_a) GK_PATH(1, true); else GK_PATH(1, false);
+  } else {
+    if (p.lds_a) GK_PATH(3, true); else GK_PATH(3, false);
+  }
+#undef GK_PATH
+#undef GK_GO
+#undef GK_KERNEL
   return hipGetLastError();
 }
 
@@ -427,89 +550,137 @@ hipError_t launch_gather_rows(const float *table, const int32_t *ids, int M, int
 // ---------------------------------------------------------------------------
 // K3: paged GQA decode attention
 // ---------------------------------------------------------------------------
-static constexpr int kChunk = 256;
+// grid (chunks, kv heads, rows). A workgroup serves the G = Hq / Hkv query
+// heads that share one KV head over one context chunk. HD/8 threads cooperate
+// on a position (one 16-byte fp16 load each), so K and V rows are read fully
+// coalesced straight from the lane's pages. One chunk: the output is written
+// directly with the weights normalised first (forward.zig:515-528); several
+// chunks: (max, sum, unnormalised output) records are merged by the combine
+// kernel with the usual log-sum-exp rescaling.
+static constexpr int kMaxChunk = 512;
 static constexpr int kMaxGroup = 8;
 
+int attention_chunk(int max_ctx, int num_kv_heads, int M) {
+  int ch = kMaxChunk;
+  if (max_ctx > 2 * kMaxChunk)
+    while (ch > 128 && ((max_ctx + ch - 1) / ch) * num_kv_heads * M < 256) ch /= 2;
+  return ch;
+}
+
 size_t attention_scratch_floats(int M, int num_heads, int head_dim, int max_ctx) {
-  const int nch = (max_ctx + kChunk - 1) / kChunk;
+  // sized for the smallest chunk the planner can pick
+  const int nch = (max_ctx + 127) / 128;
   return (size_t)M * num_heads * nch * (2 + head_dim);
 }
 
 template <int HD, int F16>
-__global__ __launch_bounds__(256) void attn_chunk_kernel(
+static __device__ __forceinline__ void load8(const void *pool, size_t idx, float *v) {
+  if (F16) {
+    const uint4 raw = *(const uint4 *)((const __half *)pool + idx);
+    const __half *hp = (const __half *)&raw;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = __half2float(hp[e]);
+  } else {
+    const float4 r0 = *(const float4 *)((const float *)pool + idx);
+    const float4 r1 = *(const float4 *)((const float *)pool + idx + 4);
+    v[0] = r0.x; v[1] = r0.y; v[2] = r0.z; v[3] = r0.w;
+    v[4] = r1.x; v[5] = r1.y; v[6] = r1.z; v[7] = r1.w;
+  }
+}
+
+template <int HD, int F16, int HPW>
+__global__ __launch_bounds__(256) void attn_decode_kernel(
     const float *q, const void *kv_pool, const int32_t *page_table, int max_pages,
     const int32_t *lane_of_row, const int32_t *ctx_len, int layer, int num_layers, int Hq,
-    int Hkv, int n_chunks_max, int max_ctx, float *scratch, float *out) {
-  const int ch = blockIdx.x, h = blockIdx.y, m = blockIdx.z, t = threadIdx.x;
-  // lengths beyond the launch's capacity are clamped, never read past it
+    int Hkv, int chunk, int n_chunks_max, int max_ctx, float *scratch, float *out) {
+  constexpr int TPP = HD / 8;        // threads per position
+  constexpr int PPP = 256 / TPP;     // positions per pass
+  constexpr int PPW = 64 / TPP;      // positions per wave
+  const int ch = blockIdx.x, m = blockIdx.z, t = threadIdx.x;
+  // HPW == 1: one query head per workgroup (blockIdx.y = query head);
+  // otherwise all G query heads of one KV head (blockIdx.y = KV head).
+  const int Gfull = Hq / Hkv;
+  const int h = HPW == 1 ? (int)blockIdx.y / Gfull : (int)blockIdx.y;
+  const int qh0 = HPW == 1 ? (int)blockIdx.y : h * Gfull;
+  const int G = HPW == 1 ? 1 : Gfull;
   const int ctx = min(ctx_len[m], max_ctx);
-  const int j0 = ch * kChunk;
+  const int j0 = ch * chunk;
   if (j0 >= ctx) return;
-  const int nvalid = min(kChunk, ctx - j0);
-  const int nchunks = (ctx + kChunk - 1) / kChunk;
-  const int G = Hq / Hkv;
+  const int n = min(chunk, ctx - j0);
+  const int nch = (ctx + chunk - 1) / chunk;
   const int kv_dim = Hkv * HD;
   const int lane_id = lane_of_row[m];
-  __shared__ float sq[kMaxGroup][HD];
-  __shared__ float sp[kMaxGroup][kChunk];
-  __shared__ float smax[kMaxGroup], ssum[kMaxGroup];
-  __shared__ int spage[kChunk / 16];
+  __shared__ float sq[HPW][HD];
+  __shared__ float ss[HPW][kMaxChunk];
+  __shared__ float red[4][HPW][HD];
+  __shared__ float smax[HPW], ssum[HPW];
+  __shared__ int spage[kMaxChunk / 16];
   for (int i = t; i < G * HD; i += 256)
-    sq[i / HD][i % HD] = q[(size_t)m * Hq * HD + (size_t)(h * G) * HD + i];
-  if (t < (nvalid + 15) / 16) spage[t] = page_table[(size_t)lane_id * max_pages + (j0 / 16) + t];
+    sq[i / HD][i % HD] = q[(size_t)m * Hq * HD + (size_t)qh0 * HD + i];
+  for (int i = t; i < (n + 15) / 16; i += 256)
+    spage[i] = page_table[(size_t)lane_id * max_pages + (j0 / 16) + i];
   __syncthreads();
 
+  const int sub = t % TPP, pp = t / TPP;
   const float scale = 1.0f / sqrtf((float)HD);
-  if (t < nvalid) {
-    const int j = j0 + t;
-    const size_t base =
-        ((((size_t)spage[t >> 4] * num_layers + layer) * 2 + 0) * 16 + (j & 15)) * kv_dim +
-        (size_t)h * HD;
-    float dot[kMaxGroup];
+  const size_t lay = (size_t)num_layers;
+  // ---- scores ----
+  {
+    float qf[HPW][8];
 #pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g) dot[g] = 0.0f;
-    for (int d = 0; d < HD; d += 8) {
-      float kv[8];
-      if (F16) {
-        const uint4 raw = *(const uint4 *)((const __half *)kv_pool + base + d);
-        const __half *hp = (const __half *)&raw;
+    for (int g = 0; g < HPW; ++g)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) kv[e] = __half2float(hp[e]);
-      } else {
-        const float4 r0 = *(const float4 *)((const float *)kv_pool + base + d);
-        const float4 r1 = *(const float4 *)((const float *)kv_pool + base + d + 4);
-        kv[0] = r0.x; kv[1] = r0.y; kv[2] = r0.z; kv[3] = r0.w;
-        kv[4] = r1.x; kv[5] = r1.y; kv[6] = r1.z; kv[7] = r1.w;
+      for (int e = 0; e < 8; ++e) qf[g][e] = g < G ? sq[g][sub * 8 + e] : 0.0f;
+    constexpr int B = 8;  // rows in flight per thread
+    for (int i0 = pp; i0 < n; i0 += B * PPP) {
+      float kv[B][8];
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        const int i = i0 + b * PPP;
+        if (i < n) {
+          const int j = j0 + i;
+          const size_t idx =
+              ((((size_t)spage[i >> 4] * lay + layer) * 2 + 0) * 16 + (j & 15)) * kv_dim +
+              (size_t)h * HD + sub * 8;
+          load8<HD, F16>(kv_pool, idx, kv[b]);
+        }
       }
 #pragma unroll
-      for (int g = 0; g < kMaxGroup; ++g)
-        if (g < G)
+      for (int b = 0; b < B; ++b) {
+        const int i = i0 + b * PPP;
+        if (i >= n) break;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) dot[g] = fmaf(sq[g][d + e], kv[e], dot[g]);
+        for (int g = 0; g < HPW; ++g) {
+          if (g >= G) break;
+          float d = 0.0f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) d = fmaf(qf[g][e], kv[b][e], d);
+#pragma unroll
+          for (int o = TPP / 2; o > 0; o >>= 1) d += __shfl_xor(d, o);
+          if (sub == 0) ss[g][i] = d * scale;
+        }
+      }
     }
-#pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g)
-      if (g < G) sp[g][t] = dot[g] * scale;
-  } else {
-#pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g)
-      if (g < G) sp[g][t] = -INFINITY;
   }
   __syncthreads();
-  // softmax statistics per query head: wave w handles heads w, w + 4
+  // ---- softmax statistics: wave w handles heads w, w + 4 ----
   {
     const int w = t >> 6, l = t & 63;
     for (int g = w; g < G; g += 4) {
       float mx = -INFINITY;
-      for (int i = l; i < kChunk; i += 64) mx = fmaxf(mx, sp[g][i]);
+      for (int i = l; i < n; i += 64) mx = fmaxf(mx, ss[g][i]);
       for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
       float sum = 0.0f;
-      for (int i = l; i < kChunk; i += 64) {
-        const float e = i < nvalid ? expf(sp[g][i] - mx) : 0.0f;
-        sp[g][i] = e;
+      for (int i = l; i < n; i += 64) {
+        const float e = expf(ss[g][i] - mx);
+        ss[g][i] = e;
         sum += e;
       }
       for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+      if (nch == 1) {
+        const float inv = 1.0f / sum;
+        for (int i = l; i < n; i += 64) ss[g][i] = ss[g][i] * inv;
+      }
       if (l == 0) {
         smax[g] = mx;
         ssum[g] = sum;
@@ -517,62 +688,89 @@ __global__ __launch_bounds__(256) void attn_chunk_kernel(
     }
   }
   __syncthreads();
-  if (nchunks == 1) {
-    // single chunk: normalise the weights first, as forward.zig:515-528 does
-    for (int i = t; i < G * kChunk; i += 256) {
-      const int g = i / kChunk, jj = i % kChunk;
-      sp[g][jj] = sp[g][jj] * (1.0f / ssum[g]);
-    }
-    __syncthreads();
-  }
-  // P.V: thread -> (d, part)
-  constexpr int PARTS = 256 / HD;
-  const int d = t % HD, part = t / HD;
-  float o[kMaxGroup];
+  // ---- weighted V ----
+  float acc[HPW][8];
 #pragma unroll
-  for (int g = 0; g < kMaxGroup; ++g) o[g] = 0.0f;
-  for (int i = part; i < nvalid; i += PARTS) {
-    const int j = j0 + i;
-    const size_t vidx =
-        ((((size_t)spage[i >> 4] * num_layers + layer) * 2 + 1) * 16 + (j & 15)) * kv_dim +
-        (size_t)h * HD + d;
-    const float v = F16 ? __half2float(((const __half *)kv_pool)[vidx]) : ((const float *)kv_pool)[vidx];
+  for (int g = 0; g < HPW; ++g)
 #pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g)
-      if (g < G) o[g] = fmaf(sp[g][i], v, o[g]);
-  }
-  __syncthreads();  // sp reused below as the part-reduction buffer
-  float *red = &sp[0][0];
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
+  {
+    constexpr int B = 8;
+    for (int i0 = pp; i0 < n; i0 += B * PPP) {
+      float v[B][8];
 #pragma unroll
-  for (int g = 0; g < kMaxGroup; ++g)
-    if (g < G) red[(part * kMaxGroup + g) * HD + d] = o[g];
-  __syncthreads();
-  if (part == 0) {
-    for (int g = 0; g < G; ++g) {
-      float acc = red[g * HD + d];
-      for (int p = 1; p < PARTS; ++p) acc += red[(p * kMaxGroup + g) * HD + d];
-      const int qh = h * G + g;
-      if (nchunks == 1) {
-        out[((size_t)m * Hq + qh) * HD + d] = acc;
-      } else {
-        float *rec = scratch + (((size_t)m * Hq + qh) * n_chunks_max + ch) * (2 + HD);
-        if (d == 0) {
-          rec[0] = smax[g];
-          rec[1] = ssum[g];
+      for (int b = 0; b < B; ++b) {
+        const int i = i0 + b * PPP;
+        if (i < n) {
+          const int j = j0 + i;
+          const size_t idx =
+              ((((size_t)spage[i >> 4] * lay + layer) * 2 + 1) * 16 + (j & 15)) * kv_dim +
+              (size_t)h * HD + sub * 8;
+          load8<HD, F16>(kv_pool, idx, v[b]);
         }
-        rec[2 + d] = acc;
       }
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        const int i = i0 + b * PPP;
+        if (i >= n) break;
+#pragma unroll
+        for (int g = 0; g < HPW; ++g) {
+          if (g >= G) break;
+          const float w = ss[g][i];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(w, v[b][e], acc[g][e]);
+        }
+      }
+    }
+  }
+  // reduce over the positions of a wave (lanes sub + TPP * k), then over waves
+#pragma unroll
+  for (int g = 0; g < HPW; ++g) {
+    if (g >= G) break;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = acc[g][e];
+#pragma unroll
+      for (int o = TPP; o < 64; o <<= 1) v += __shfl_xor(v, o);
+      acc[g][e] = v;
+    }
+  }
+  const int w = t >> 6, l = t & 63;
+  if (l < TPP) {
+#pragma unroll
+    for (int g = 0; g < HPW; ++g) {
+      if (g >= G) break;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) red[w][g][l * 8 + e] = acc[g][e];
+    }
+  }
+  __syncthreads();
+  (void)PPW;
+  for (int o = t; o < G * HD; o += 256) {
+    const int g = o / HD, d = o % HD;
+    const float sum = ((red[0][g][d] + red[1][g][d]) + red[2][g][d]) + red[3][g][d];
+    const int qh = qh0 + g;
+    if (nch == 1) {
+      out[((size_t)m * Hq + qh) * HD + d] = sum;
+    } else {
+      float *rec = scratch + (((size_t)m * Hq + qh) * n_chunks_max + ch) * (2 + HD);
+      if (d == 0) {
+        rec[0] = smax[g];
+        rec[1] = ssum[g];
+      }
+      rec[2 + d] = sum;
     }
   }
 }
 
 template <int HD>
 __global__ __launch_bounds__(HD) void attn_combine_kernel(const int32_t *ctx_len, int Hq,
-                                                          int n_chunks_max, int max_ctx,
-                                                          const float *scratch, float *out) {
+                                                          int chunk, int n_chunks_max,
+                                                          int max_ctx, const float *scratch,
+                                                          float *out) {
   const int qh = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
   const int ctx = min(ctx_len[m], max_ctx);
-  const int nch = (ctx + kChunk - 1) / kChunk;
+  const int nch = (ctx + chunk - 1) / chunk;
   if (nch <= 1) return;
   const float *rec0 = scratch + ((size_t)m * Hq + qh) * n_chunks_max * (2 + HD);
   float mx = -INFINITY;
@@ -594,12 +792,22 @@ hipError_t launch_attention(const float *q, const void *kv_pool, int kv_f16,
                             float *scratch, float *out, hipStream_t st) {
   if (num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > kMaxGroup)
     return hipErrorInvalidValue;
-  const int nch = (max_ctx + kChunk - 1) / kChunk;
-  dim3 grid(nch, num_kv_heads, M);
-#define GK_ATT(HD, F)                                                                        \
-  hipLaunchKernelGGL((attn_chunk_kernel<HD, F>), grid, dim3(256), 0, st, q, kv_pool,          \
-                     page_table, max_pages, lane_of_row, ctx_len, layer, num_layers,          \
-                     num_heads, num_kv_heads, nch, max_ctx, scratch, out)
+  const int chunk = attention_chunk(max_ctx, num_kv_heads, M);
+  const int nch = (max_ctx + chunk - 1) / chunk;
+  // few workgroups (batch-1 decode): one query head each, K/V re-read from L2
+  const bool per_head = nch * num_kv_heads * M < 64;
+  dim3 grid(nch, per_head ? num_heads : num_kv_heads, M);
+#define GK_ATT(HD, F)                                                                           \
+  do {                                                                                          \
+    if (per_head)                                                                               \
+      hipLaunchKernelGGL((attn_decode_kernel<HD, F, 1>), grid, dim3(256), 0, st, q, kv_pool,    \
+                         page_table, max_pages, lane_of_row, ctx_len, layer, num_layers,        \
+                         num_heads, num_kv_heads, chunk, nch, max_ctx, scratch, out);           \
+    else                                                                                        \
+      hipLaunchKernelGGL((attn_decode_kernel<HD, F, kMaxGroup>), grid, dim3(256), 0, st, q,     \
+                         kv_pool, page_table, max_pages, lane_of_row, ctx_len, layer,           \
+                         num_layers, num_heads, num_kv_heads, chunk, nch, max_ctx, scratch, out); \
+  } while (0)
   if (head_dim == 64) {
     if (kv_f16) GK_ATT(64, 1); else GK_ATT(64, 0);
   } else if (head_dim == 128) {
@@ -612,10 +820,10 @@ hipError_t launch_attention(const float *q, const void *kv_pool, int kv_f16,
   if (e != hipSuccess || nch <= 1) return e;
   if (head_dim == 64)
     hipLaunchKernelGGL((attn_combine_kernel<64>), dim3(num_heads, M), dim3(64), 0, st, ctx_len,
-                       num_heads, nch, max_ctx, scratch, out);
+                       num_heads, chunk, nch, max_ctx, scratch, out);
   else
     hipLaunchKernelGGL((attn_combine_kernel<128>), dim3(num_heads, M), dim3(128), 0, st,
-                       ctx_len, num_heads, nch, max_ctx, scratch, out);
+                       ctx_len, num_heads, chunk, nch, max_ctx, scratch, out);
   return hipGetLastError();
 }
 

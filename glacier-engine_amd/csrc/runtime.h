@@ -27,6 +27,8 @@ struct glacier_hip_context {
   // scratch for the stand-alone kernel entry points
   void *scratch = nullptr;
   size_t scratch_bytes = 0;
+  void *planes = nullptr;  // activation planes of glacier_hip_int4_gemv
+  size_t planes_bytes = 0;
   uint32_t *counters = nullptr;  // zeroed once, self-resetting
   size_t counter_count = 0;
   gk::ArgmaxResult *results_host = nullptr;  // pinned

@@ -32,10 +32,11 @@ int resolve_activation(int activation, uint32_t out_f, uint32_t in_f) {
 
 void repack_tiles(const std::vector<RowSrc> &rows, uint32_t K, std::vector<uint32_t> &codes,
                   std::vector<uint16_t> &scales) {
+  // Tile layout of kernels.h: lane 16*j + n holds group 4*kq + j of row n.
   const size_t N = rows.size();
   const size_t NB = N / 16, KQ = K / 128, G = K / 32;
   codes.assign(NB * KQ * 64 * 4, 0u);
-  scales.assign(NB * KQ * 16 * 4, 0u);
+  scales.assign(NB * KQ * 64, 0u);
   parallel_for(NB, [&](size_t b0, size_t b1) {
     for (size_t nb = b0; nb < b1; ++nb)
       for (int nl = 0; nl < 16; ++nl) {
@@ -43,22 +44,22 @@ void repack_tiles(const std::vector<RowSrc> &rows, uint32_t K, std::vector<uint3
         const uint8_t *rp = src.packed ? src.packed + src.row * (K / 2) : nullptr;
         for (size_t g = 0; g < G; ++g) {
           const size_t kq = g / 4, j = g % 4;
+          const size_t lane = j * 16 + (size_t)nl;
           uint16_t sh = 0;
           if (src.scales_f16) sh = src.scales_f16[src.row * G + g];
           else if (src.scales_f32) sh = f32_to_f16(src.scales_f32[src.row * G + g]);
-          scales[((nb * KQ + kq) * 16 + nl) * 4 + j] = sh;
-          for (int c = 0; c < 4; ++c) {
+          scales[(nb * KQ + kq) * 64 + lane] = sh;
+          for (int w = 0; w < 4; ++w) {
             uint32_t word = 0x77777777u;  // code 7 decodes to 0 for absent rows
             if (rp) {
-              const uint8_t *b = rp + g * 16 + c * 4;  // columns 32g + 8c .. +8
+              const uint8_t *b = rp + g * 16 + w * 4;  // columns 32g + 8w .. +8
               uint8_t code[8];
               for (int t = 0; t < 8; ++t) code[t] = (b[t / 2] >> (4 * (t & 1))) & 0xF;
               word = 0;
               for (int bb = 0; bb < 4; ++bb)
                 word |= (uint32_t)(code[bb] | (code[bb + 4] << 4)) << (8 * bb);
             }
-            const size_t lane = (size_t)c * 16 + nl;
-            codes[((nb * KQ + kq) * 64 + lane) * 4 + j] = word;
+            codes[((nb * KQ + kq) * 64 + lane) * 4 + w] = word;
           }
         }
       }
@@ -153,6 +154,7 @@ int glacier_hip_deinit(glacier_hip_context *ctx) {
   if (!ctx->buffers.empty() || ctx->live_weights != 0) return GLACIER_HIP_BUSY;
   (void)hipStreamSynchronize(ctx->stream);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
+  if (ctx->planes) (void)hipFree(ctx->planes);
   if (ctx->counters) (void)hipFree(ctx->counters);
   if (ctx->results_host) (void)hipHostFree(ctx->results_host);
   (void)hipStreamDestroy(ctx->stream);
@@ -413,6 +415,47 @@ uint64_t glacier_hip_int4_weight_device_bytes(const glacier_hip_int4_weight *w) 
   return w ? w->device_bytes : 0;
 }
 
+// Activation planes: int8 [G][D][m][32] followed (256-aligned) by ActMeta [G][m].
+static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
+static size_t planes_q_bytes(uint32_t m, uint32_t in_f, int D) { return (size_t)(in_f / 32) * D * m * 32; }
+static size_t planes_bytes(uint32_t m, uint32_t in_f, int D) {
+  return al256(planes_q_bytes(m, in_f, D)) + (size_t)(in_f / 32) * m * sizeof(gk::ActMeta);
+}
+
+static int act_digits(int activation) {
+  if (activation == GLACIER_HIP_ACT_Q8) return 1;
+  if (activation == GLACIER_HIP_ACT_F32) return 3;
+  return 0;
+}
+
+static int gemv_launch(glacier_hip_context *ctx, glacier_hip_int4_weight *w, const void *planes,
+                       uint32_t m, int D, const float *bias_dev, float *y_dev, hipStream_t st) {
+  const int N = (int)w->out_f, K = (int)w->in_f;
+  gk::GemvArgs a{};
+  a.codes = w->codes;
+  a.scales = w->scales;
+  a.N = N;
+  a.K = K;
+  a.act_q = (const int8_t *)planes;
+  a.act_meta = (const gk::ActMeta *)((const char *)planes + al256(planes_q_bytes(m, (uint32_t)K, D)));
+  a.M = (int)m;
+  a.D = D;
+  a.bias = bias_dev;
+  a.y = y_dev;
+  a.epi = gk::EPI_PLAIN;
+  GH_CHECK(ctx, gk::launch_gemv(a, st));
+  return GLACIER_HIP_OK;
+}
+
+static int prepare_launch(glacier_hip_context *ctx, const void *x_dev, int x_dtype, uint32_t m,
+                          uint32_t in_f, int D, void *planes, hipStream_t st) {
+  GH_CHECK(ctx, gk::launch_prep_act(x_dev, x_dtype == GLACIER_HIP_BF16, nullptr, 0.0f, (int)m,
+                                    (int)in_f, D, (int8_t *)planes,
+                                    (gk::ActMeta *)((char *)planes + al256(planes_q_bytes(m, in_f, D))),
+                                    nullptr, st));
+  return GLACIER_HIP_OK;
+}
+
 static int gemv_common(glacier_hip_context *ctx, glacier_hip_int4_weight *w, const void *x_dev,
                        int x_dtype, uint32_t m, const float *bias_dev, float *y_dev,
                        int activation, hipStream_t st) {
@@ -420,38 +463,19 @@ static int gemv_common(glacier_hip_context *ctx, glacier_hip_int4_weight *w, con
   if (w->ctx != ctx) return GLACIER_HIP_INVALID_HANDLE;
   if (m == 0 || m > 32) return GLACIER_HIP_SHAPE_MISMATCH;
   if (x_dtype != GLACIER_HIP_F32 && x_dtype != GLACIER_HIP_BF16) return GLACIER_HIP_DTYPE_UNSUPPORTED;
-  const int act = gh::resolve_activation(activation, w->out_f, w->in_f);
-  if (act != GLACIER_HIP_ACT_Q8 && act != GLACIER_HIP_ACT_F32) return GLACIER_HIP_INVALID_ARGUMENT;
-  const int D = act == GLACIER_HIP_ACT_Q8 ? 1 : 3;
-  const int N = (int)w->out_f, K = (int)w->in_f;
-  const int NB = N / 16, KQ = K / 128, G = K / 32;
-  const int S = gk::choose_splits(NB, KQ, (int)m);
-  const size_t q_bytes = (size_t)G * D * m * 32;
-  const size_t meta_bytes = (size_t)G * m * sizeof(gk::ActMeta);
-  const size_t part_bytes = S > 1 ? (size_t)S * m * N * sizeof(float) : 0;
-  auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
-  int rc = gh::ensure_scratch(ctx, al(q_bytes) + al(meta_bytes) + al(part_bytes), (size_t)NB);
+  const int D = act_digits(gh::resolve_activation(activation, w->out_f, w->in_f));
+  if (!D) return GLACIER_HIP_INVALID_ARGUMENT;
+  const size_t pb = planes_bytes(m, w->in_f, D);
+  if (pb > ctx->planes_bytes) {
+    if (ctx->planes) GH_CHECK(ctx, hipFree(ctx->planes));
+    ctx->planes = nullptr;
+    ctx->planes_bytes = 0;
+    GH_CHECK(ctx, hipMalloc(&ctx->planes, pb));
+    ctx->planes_bytes = pb;
+  }
+  int rc = prepare_launch(ctx, x_dev, x_dtype, m, w->in_f, D, ctx->planes, st);
   if (rc) return rc;
-  char *base = (char *)ctx->scratch;
-  gk::GemvArgs a{};
-  a.codes = w->codes;
-  a.scales = w->scales;
-  a.N = N;
-  a.K = K;
-  a.act_q = (int8_t *)base;
-  a.act_meta = (gk::ActMeta *)(base + al(q_bytes));
-  a.M = (int)m;
-  a.D = D;
-  a.bias = bias_dev;
-  a.y = y_dev;
-  a.S = S;
-  a.partial = (float *)(base + al(q_bytes) + al(meta_bytes));
-  a.counters = ctx->counters;
-  a.epi = gk::EPI_PLAIN;
-  GH_CHECK(ctx, gk::launch_prep_act(x_dev, x_dtype == GLACIER_HIP_BF16, nullptr, 0.0f, (int)m, K,
-                                    D, (int8_t *)a.act_q, (gk::ActMeta *)a.act_meta, nullptr, st));
-  GH_CHECK(ctx, gk::launch_gemv(a, st));
-  return GLACIER_HIP_OK;
+  return gemv_launch(ctx, w, ctx->planes, m, D, bias_dev, y_dev, st);
 }
 
 int glacier_hip_int4_gemv(glacier_hip_context *ctx, glacier_hip_int4_weight *w, const void *x_dev,
@@ -460,6 +484,38 @@ int glacier_hip_int4_gemv(glacier_hip_context *ctx, glacier_hip_int4_weight *w, 
   if (!ctx) return GLACIER_HIP_INVALID_HANDLE;
   std::lock_guard<std::mutex> lk(ctx->mu);
   return gemv_common(ctx, w, x_dev, x_dtype, m, bias_dev, y_dev, activation,
+                     stream ? (hipStream_t)stream : ctx->stream);
+}
+
+uint64_t glacier_hip_activation_bytes(uint32_t m, uint32_t in_f, int activation) {
+  const int D = act_digits(activation);
+  if (!D || in_f % 128 != 0 || m == 0) return 0;
+  return planes_bytes(m, in_f, D);
+}
+
+int glacier_hip_activation_prepare(glacier_hip_context *ctx, const void *x_dev, int x_dtype,
+                                   uint32_t m, uint32_t in_f, int activation, void *act_dev,
+                                   void *stream) {
+  if (!ctx || !x_dev || !act_dev) return GLACIER_HIP_INVALID_ARGUMENT;
+  const int D = act_digits(activation);
+  if (!D) return GLACIER_HIP_INVALID_ARGUMENT;
+  if (m == 0 || m > 32 || in_f == 0 || in_f % 128 != 0) return GLACIER_HIP_SHAPE_MISMATCH;
+  if (x_dtype != GLACIER_HIP_F32 && x_dtype != GLACIER_HIP_BF16) return GLACIER_HIP_DTYPE_UNSUPPORTED;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  return prepare_launch(ctx, x_dev, x_dtype, m, in_f, D, act_dev,
+                        stream ? (hipStream_t)stream : ctx->stream);
+}
+
+int glacier_hip_int4_gemv_prepared(glacier_hip_context *ctx, glacier_hip_int4_weight *w,
+                                   const void *act_dev, uint32_t m, int activation,
+                                   const float *bias_dev, float *y_dev, void *stream) {
+  if (!ctx || !w || !act_dev || !y_dev) return GLACIER_HIP_INVALID_ARGUMENT;
+  if (w->ctx != ctx) return GLACIER_HIP_INVALID_HANDLE;
+  const int D = act_digits(activation);
+  if (!D) return GLACIER_HIP_INVALID_ARGUMENT;
+  if (m == 0 || m > 32) return GLACIER_HIP_SHAPE_MISMATCH;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  return gemv_launch(ctx, w, act_dev, m, D, bias_dev, y_dev,
                      stream ? (hipStream_t)stream : ctx->stream);
 }
 

@@ -106,8 +106,6 @@ struct glacier_hip_session {
         *logits = nullptr;
   int8_t *act_q = nullptr;
   gk::ActMeta *act_meta = nullptr;
-  float *partial = nullptr;
-  uint32_t *counters = nullptr;
   float *att_scratch = nullptr;
   void *arg_scratch = nullptr;
   uint32_t *arg_counters = nullptr;
@@ -344,9 +342,11 @@ int head_D(const glacier_hip_session *s) {
   return gh::resolve_activation(s->opt.head_activation, c.vocab_size, c.dim) == GLACIER_HIP_ACT_Q8 ? 1 : 3;
 }
 
+// One projection: activation conversion (RMSNorm + Q8 / digit planes) then
+// the GEMV with its epilogue.
 hipError_t run_proj(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, int rows,
                     const float *x, const float *norm_w, int epi, const float *bias, float *y,
-                    const float *resid, hipStream_t st) {
+                    const float *resid, const gk::QkvArgs *qkv, hipStream_t st) {
   const auto &c = s->model->cfg;
   hipError_t e = gk::launch_prep_act(x, 0, norm_w, c.rms_eps, rows, (int)w->in_f, D, s->act_q,
                                      s->act_meta, nullptr, st);
@@ -363,26 +363,8 @@ hipError_t run_proj(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, i
   a.bias = bias;
   a.y = y;
   a.resid = resid;
-  a.S = gk::choose_splits(a.N / 16, a.K / 128, rows);
-  a.partial = s->partial;
-  a.counters = s->counters;
   a.epi = epi;
-  if (epi == gk::EPI_QKV) {
-    gk::QkvArgs &q = a.qkv;
-    q.q_out = s->q;
-    q.kv_pool = s->kv_pool;
-    q.kv_f16 = s->opt.kv_dtype == GLACIER_HIP_F16;
-    q.page_table = s->page_table;
-    q.max_pages = (int)s->max_pages;
-    q.lane_of_row = s->step_dev->lane_of_row;
-    q.pos_of_row = s->step_dev->pos_of_row;
-    q.rope_cos = s->rope_cos;
-    q.rope_sin = s->rope_sin;
-    q.num_layers = (int)c.num_layers;
-    q.num_heads = (int)c.num_heads;
-    q.num_kv_heads = (int)c.num_kv_heads;
-    q.head_dim = (int)c.head_dim;
-  }
+  if (qkv) a.qkv = *qkv;
   return gk::launch_gemv(a, st);
 }
 
@@ -390,51 +372,30 @@ hipError_t run_proj(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, i
 hipError_t enqueue_step(glacier_hip_session *s, int rows, bool head, bool elig, hipStream_t st) {
   glacier_hip_model *m = s->model;
   const auto &c = m->cfg;
-  const int D = (int)c.dim, F = (int)c.hidden_dim;
+  const int D = (int)c.dim;
   hipError_t e = gk::launch_gather_rows(m->embed, s->step_dev->tokens, rows, D, s->x_res, st);
   if (e != hipSuccess) return e;
+  gk::QkvArgs q{};
+  q.q_out = s->q;
+  q.kv_pool = s->kv_pool;
+  q.kv_f16 = s->opt.kv_dtype == GLACIER_HIP_F16;
+  q.page_table = s->page_table;
+  q.max_pages = (int)s->max_pages;
+  q.lane_of_row = s->step_dev->lane_of_row;
+  q.pos_of_row = s->step_dev->pos_of_row;
+  q.rope_cos = s->rope_cos;
+  q.rope_sin = s->rope_sin;
+  q.num_layers = (int)c.num_layers;
+  q.num_heads = (int)c.num_heads;
+  q.num_kv_heads = (int)c.num_kv_heads;
+  q.head_dim = (int)c.head_dim;
   for (uint32_t l = 0; l < c.num_layers; ++l) {
     const LayerDev &L = m->layers[l];
-    gk::GemvArgs dummy{};
-    (void)dummy;
-    // QKV (+RoPE, KV row write)
-    {
-      const int Dq = layer_D(s, L.qkv->out_f, L.qkv->in_f);
-      e = gk::launch_prep_act(s->x_res, 0, L.in_norm, c.rms_eps, rows, D, Dq, s->act_q,
-                              s->act_meta, nullptr, st);
-      if (e != hipSuccess) return e;
-      gk::GemvArgs a{};
-      a.codes = L.qkv->codes;
-      a.scales = L.qkv->scales;
-      a.N = (int)L.qkv->out_f;
-      a.K = D;
-      a.act_q = s->act_q;
-      a.act_meta = s->act_meta;
-      a.M = rows;
-      a.D = Dq;
-      a.bias = L.qkv_bias;
-      a.S = gk::choose_splits(a.N / 16, a.K / 128, rows);
-      a.partial = s->partial;
-      a.counters = s->counters;
-      a.epi = gk::EPI_QKV;
-      gk::QkvArgs &q = a.qkv;
-      q.q_out = s->q;
-      q.kv_pool = s->kv_pool;
-      q.kv_f16 = s->opt.kv_dtype == GLACIER_HIP_F16;
-      q.page_table = s->page_table;
-      q.max_pages = (int)s->max_pages;
-      q.lane_of_row = s->step_dev->lane_of_row;
-      q.pos_of_row = s->step_dev->pos_of_row;
-      q.rope_cos = s->rope_cos;
-      q.rope_sin = s->rope_sin;
-      q.layer = (int)l;
-      q.num_layers = (int)c.num_layers;
-      q.num_heads = (int)c.num_heads;
-      q.num_kv_heads = (int)c.num_kv_heads;
-      q.head_dim = (int)c.head_dim;
-      e = gk::launch_gemv(a, st);
-      if (e != hipSuccess) return e;
-    }
+    q.layer = (int)l;
+    // RMSNorm -> QKV (+RoPE, KV row write into the lane's page)
+    e = run_proj(s, L.qkv, layer_D(s, L.qkv->out_f, L.qkv->in_f), rows, s->x_res, L.in_norm,
+                 gk::EPI_QKV, L.qkv_bias, nullptr, nullptr, &q, st);
+    if (e != hipSuccess) return e;
     e = gk::launch_attention(s->q, s->kv_pool, s->opt.kv_dtype == GLACIER_HIP_F16, s->page_table,
                              (int)s->max_pages, s->step_dev->lane_of_row, s->step_dev->ctx_len,
                              rows, (int)l, (int)c.num_layers, (int)c.num_heads,
@@ -442,19 +403,18 @@ hipError_t enqueue_step(glacier_hip_session *s, int rows, bool head, bool elig, 
                              s->att_scratch, s->attn, st);
     if (e != hipSuccess) return e;
     e = run_proj(s, L.o, layer_D(s, L.o->out_f, L.o->in_f), rows, s->attn, nullptr,
-                 gk::EPI_RESID, nullptr, s->h, s->x_res, st);
+                 gk::EPI_RESID, nullptr, s->h, s->x_res, nullptr, st);
     if (e != hipSuccess) return e;
     e = run_proj(s, L.gu, layer_D(s, L.gu->out_f / 2, L.gu->in_f), rows, s->h, L.post_norm,
-                 gk::EPI_SWIGLU, nullptr, s->act, nullptr, st);
+                 gk::EPI_SWIGLU, nullptr, s->act, nullptr, nullptr, st);
     if (e != hipSuccess) return e;
     e = run_proj(s, L.down, layer_D(s, L.down->out_f, L.down->in_f), rows, s->act, nullptr,
-                 gk::EPI_RESID, nullptr, s->x_res, s->h, st);
+                 gk::EPI_RESID, nullptr, s->x_res, s->h, nullptr, st);
     if (e != hipSuccess) return e;
-    (void)F;
   }
   if (!head) return hipSuccess;
   e = run_proj(s, m->head, head_D(s), rows, s->x_res, m->final_norm, gk::EPI_PLAIN, nullptr,
-               s->logits, nullptr, st);
+               s->logits, nullptr, nullptr, st);
   if (e != hipSuccess) return e;
   const long V = (long)c.vocab_size;
   const long W = (V + 63) / 64;
@@ -464,7 +424,7 @@ hipError_t enqueue_step(glacier_hip_session *s, int rows, bool head, bool elig, 
 
 void destroy_session(glacier_hip_session *s) {
   void *ptrs[] = {s->kv_pool, s->page_table, s->rope_cos, s->rope_sin, s->x_res, s->h, s->q,
-                  s->attn, s->act, s->logits, s->act_q, s->act_meta, s->partial, s->counters,
+                  s->attn, s->act, s->logits, s->act_q, s->act_meta,
                   s->att_scratch, s->arg_scratch, s->arg_counters, s->arg_result, s->elig_words,
                   s->step_dev};
   for (void *p : ptrs)
@@ -711,16 +671,6 @@ glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
   const size_t page_bytes = (size_t)c.num_layers * 2 * 16 * kvd * elem;
   const size_t Kmax = std::max(c.dim, c.hidden_dim);
   const size_t Gmax = Kmax / 32;
-  // partial workspace: max over the projections of S * M * N
-  auto part_floats = [&](uint32_t N, uint32_t K) {
-    const int S = gk::choose_splits((int)N / 16, (int)K / 128, (int)M);
-    return S > 1 ? (size_t)S * M * N : (size_t)0;
-  };
-  const uint32_t nqkv = c.dim + 2 * (uint32_t)kvd;
-  size_t pf = std::max({part_floats(nqkv, c.dim), part_floats(c.dim, c.dim),
-                        part_floats(2 * c.hidden_dim, c.dim), part_floats(c.dim, c.hidden_dim),
-                        part_floats(c.vocab_size, c.dim), (size_t)1});
-  const size_t nb_max = std::max<size_t>(c.vocab_size, 2 * c.hidden_dim) / 16;
   const size_t W = (c.vocab_size + 63) / 64;
   const size_t att = gk::attention_scratch_floats((int)M, (int)c.num_heads, (int)c.head_dim,
                                                   (int)opts->max_positions);
@@ -740,8 +690,6 @@ glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
   A((void **)&s->logits, (size_t)M * c.vocab_size * 4);
   A((void **)&s->act_q, Gmax * 3 * M * 32);
   A((void **)&s->act_meta, Gmax * M * sizeof(gk::ActMeta));
-  A((void **)&s->partial, pf * 4);
-  A((void **)&s->counters, nb_max * 4);
   A((void **)&s->att_scratch, std::max<size_t>(att, 1) * 4);
   A(&s->arg_scratch, gk::argmax_scratch_bytes((int)M, (long)c.vocab_size));
   A((void **)&s->arg_counters, (size_t)M * 4);
@@ -751,8 +699,7 @@ glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
   if (ok && hipHostMalloc((void **)&s->step_host, sizeof(StepInputs)) != hipSuccess) ok = false;
   if (ok && hipHostMalloc((void **)&s->res_host, M * sizeof(gk::ArgmaxResult)) != hipSuccess) ok = false;
   if (ok) {
-    ok = hipMemset(s->counters, 0, nb_max * 4) == hipSuccess &&
-         hipMemset(s->arg_counters, 0, (size_t)M * 4) == hipSuccess &&
+    ok = hipMemset(s->arg_counters, 0, (size_t)M * 4) == hipSuccess &&
          hipMemset(s->kv_pool, 0, page_bytes * s->total_pages) == hipSuccess;
     std::vector<int32_t> pt((size_t)M * s->max_pages, 0);
     ok = ok && hipMemcpy(s->page_table, pt.data(), pt.size() * 4, hipMemcpyHostToDevice) == hipSuccess;

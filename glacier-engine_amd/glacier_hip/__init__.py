@@ -141,6 +141,10 @@ _SIGS = [
     ("glacier_hip_int4_weight_device_bytes", C.c_uint64, [_P]),
     ("glacier_hip_int4_matvec_dispatch", C.c_int, [_P, _P, _P, C.c_uint64, _P, C.c_uint64]),
     ("glacier_hip_int4_gemv", C.c_int, [_P, _P, _P, C.c_int, C.c_uint32, _P, _P, C.c_int, _P]),
+    ("glacier_hip_activation_bytes", C.c_uint64, [C.c_uint32, C.c_uint32, C.c_int]),
+    ("glacier_hip_activation_prepare", C.c_int,
+     [_P, _P, C.c_int, C.c_uint32, C.c_uint32, C.c_int, _P, _P]),
+    ("glacier_hip_int4_gemv_prepared", C.c_int, [_P, _P, _P, C.c_uint32, C.c_int, _P, _P, _P]),
     ("glacier_hip_rmsnorm", C.c_int, [_P, _P, _P, C.c_uint32, C.c_uint32, C.c_float, _P, _P]),
     ("glacier_hip_paged_attention", C.c_int,
      [_P, _P, _P, C.c_int, _P, C.c_uint32, _P, C.c_uint32, C.c_uint32, C.c_uint32,

@@ -200,6 +200,21 @@ int glacier_hip_int4_gemv(glacier_hip_context *ctx, glacier_hip_int4_weight *wei
                           const float *bias_dev, float *y_dev, int activation,
                           void *stream);
 
+/* The same projection in two phases, as the reference splits it into
+ * quantizeQ8Activation (int4_matmul.zig:537-560, glacier_q8_activation_quantize
+ * int4_neon.c:453-486) and linearInt4WeightQ8Prepared (int4_matmul.zig:771):
+ * the activation is converted once into device "digit planes" that several
+ * projections with the same in_f can share. activation must be Q8 or F32
+ * (F32 = three digit planes). act_dev must hold
+ * glacier_hip_activation_bytes(m, in_f, activation) bytes. */
+uint64_t glacier_hip_activation_bytes(uint32_t m, uint32_t in_f, int activation);
+int glacier_hip_activation_prepare(glacier_hip_context *ctx, const void *x_dev, int x_dtype,
+                                   uint32_t m, uint32_t in_f, int activation,
+                                   void *act_dev, void *stream);
+int glacier_hip_int4_gemv_prepared(glacier_hip_context *ctx, glacier_hip_int4_weight *weight,
+                                   const void *act_dev, uint32_t m, int activation,
+                                   const float *bias_dev, float *y_dev, void *stream);
+
 /* ---- fused RMSNorm (kernels.zig:141-220) -------------------------------- */
 int glacier_hip_rmsnorm(glacier_hip_context *ctx, const float *x_dev, const float *w_dev,
                         uint32_t rows, uint32_t dim, float eps, float *out_dev, void *stream);

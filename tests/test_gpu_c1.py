@@ -1,0 +1,66 @@
+"""BASELINE config 1 on the GPU: Qwen2.5-0.5B-shaped INT4 random-init model,
+128-token prompt, 128 greedy tokens, page size 16, f32 paged KV, against the
+oracle's committed run (tests/golden/make_c1_golden.py).
+
+Bars: the identical greedy token sequence and output digest; logits within
+1e-2 max-relative error (max |gpu - oracle| over the stored 4096 sampled +
+top-32 indices, divided by the oracle's max |logit|) at steps 0, 1, 64, 127.
+"""
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+C1 = dict(num_layers=24, dim=896, hidden_dim=4864, num_heads=14, num_kv_heads=2, head_dim=64,
+          vocab_size=151936, group_size=32, rms_eps=1e-6, rope_theta=1e6)
+
+
+@pytest.mark.parametrize("variant", ["spec", "unitnorm"])
+def test_c1_greedy_128_matches_oracle(gh, gctx, variant):
+    name = "c1_qwen05b.npz" if variant == "spec" else "c1_qwen05b_unitnorm.npz"
+    fx = np.load(os.path.join(HERE, "golden", name))
+    seed = int(fx["seed"][0])
+    m = gh.Model(gctx, C1)
+    if variant == "spec":
+        m.init_random(seed)
+    else:
+        host = gh.random_model_host(C1, seed)
+        for L in host["layers"]:
+            L["input_norm"] = (L["input_norm"] + 1.0).astype(np.float32)
+            L["post_attn_norm"] = (L["post_attn_norm"] + 1.0).astype(np.float32)
+        host["final_norm"] = (host["final_norm"] + 1.0).astype(np.float32)
+        m.set_from_host(host)
+        del host
+    sess = gh.Session(m, max_lanes=1, max_positions=256, kv_dtype=gh.F32)
+    try:
+        sess.begin(0)
+        steps = fx["steps"].tolist()
+        first, lg = sess.prefill(0, fx["prompt"], want_logits=True)
+        toks, logits = [first], {0: lg}
+        for s in range(1, len(fx["tokens"])):
+            if s in steps:
+                nxt, lg = sess.step([0], [toks[-1]], want_logits=True)
+                logits[s] = lg[0]
+            else:
+                nxt = sess.step([0], [toks[-1]])
+            toks.append(int(nxt[0]))
+        want = fx["tokens"].tolist()
+        n_same = next((i for i, (a, b) in enumerate(zip(toks, want)) if a != b), len(want))
+        print(f"{variant}: first divergence at {n_same}; distinct oracle tokens {len(set(want))}",
+              flush=True)
+        for i, s in enumerate(steps):
+            got = logits[s]
+            err = max(np.max(np.abs(got[fx["sample_idx"]] - fx["sample_logits"][i])),
+                      np.max(np.abs(got[fx["top_idx"][i]] - fx["top_val"][i]))) / fx["max_abs"][i]
+            print(f"  step {s}: logit max-rel err {err:.2e}", flush=True)
+            assert err < 1e-2
+        assert toks == want
+        st = sess.state(0)
+        assert bytes(st.output_sha256) == fx["output_sha256"].tobytes()
+        assert st.kv_positions == 128 + 127
+    finally:
+        sess.close()
+        m.close()

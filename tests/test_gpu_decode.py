@@ -19,14 +19,44 @@ TINY = dict(num_layers=2, dim=256, hidden_dim=512, num_heads=4, num_kv_heads=2, 
 SEED = 0x5EED
 
 
+def unit_norm(host):
+    """RMSNorm weights 1 + N(0, 0.02): with the config's N(0, 0.02) norms a
+    random-init model repeats one greedy token, which makes token identity a
+    weak check; unit-centred norms give varied greedy sequences."""
+    for L in host["layers"]:
+        L["input_norm"] = (L["input_norm"] + 1.0).astype(np.float32)
+        L["post_attn_norm"] = (L["post_attn_norm"] + 1.0).astype(np.float32)
+    host["final_norm"] = (host["final_norm"] + 1.0).astype(np.float32)
+    return host
+
+
 @pytest.fixture(scope="module")
 def tiny(gh, gctx, ora):
+    host = unit_norm(gh.random_model_host(TINY, SEED))
+    om = ora.OracleModel(TINY, host)
+    m = gh.Model(gctx, TINY)
+    m.set_from_host(host)
+    yield host, om, m
+    m.close()
+
+
+def test_init_random_equals_host_generator(gh, gctx, ora):
+    """glacier_hip_model_init_random uploads exactly random_model_host's tensors."""
     host = gh.random_model_host(TINY, SEED)
     om = ora.OracleModel(TINY, host)
     m = gh.Model(gctx, TINY)
     m.init_random(SEED)
-    yield host, om, m
-    m.close()
+    sess = gh.Session(m, max_lanes=1, max_positions=64)
+    try:
+        prompt = gh.synth_tokens(SEED, 98, TINY["vocab_size"], 12)
+        want, wl, _, _ = om.generate(prompt, 6, logits_steps=[0])
+        sess.begin(0)
+        toks, logits = _run_gpu(sess, 0, prompt, 6)
+        assert toks == want.tolist()
+        assert _rel(logits[0], wl[0]) < 1e-2
+    finally:
+        sess.close()
+        m.close()
 
 
 def _run_gpu(sess, lane, prompt, max_new, logits_at=()):
@@ -56,6 +86,7 @@ def test_tiny_greedy_matches_oracle(gh, tiny, use_graph):
         sess.begin(0, seed=7)
         toks, logits = _run_gpu(sess, 0, prompt, max_new, logits_at=(max_new - 1,))
         print("gpu", toks, "\noracle", want.tolist(), flush=True)
+        assert len(set(want.tolist())) > max_new // 2  # a discriminative sequence
         assert toks == want.tolist()
         assert _rel(logits[0], wl[0]) < 1e-2
         assert _rel(logits[max_new - 1], wl[1]) < 1e-2

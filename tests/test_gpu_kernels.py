@@ -47,7 +47,7 @@ SMALL = [(16, 128), (48, 256), (896, 896), (128, 896), (896, 4864), (9728, 896)]
 
 
 @pytest.mark.parametrize("out_f,in_f", SMALL)
-@pytest.mark.parametrize("m", [1, 2, 4, 8])
+@pytest.mark.parametrize("m", [1, 2, 4, 8, 16, 32])
 def test_gemv_q8_matches_oracle(gh, gctx, ora, out_f, in_f, m):
     packed, s16, s32 = _weights(gh, 100 + out_f + in_f, out_f, in_f)
     w = gctx.weight(packed, s16, in_f, out_f)
@@ -219,11 +219,13 @@ def _paged_case(rng, lanes_ctx, Hkv, hd, num_layers, layer, fp16):
 
 @pytest.mark.parametrize("fp16", [False, True])
 @pytest.mark.parametrize("geom", [(14, 2, 64), (28, 4, 128)])
-def test_paged_attention_matches_oracle(gh, gctx, ora, fp16, geom):
+@pytest.mark.parametrize("ctxs", [[1, 17, 256, 257, 700],  # few workgroups: one query head each
+                                  [5, 16, 33, 64, 100, 129, 200, 256, 300, 333, 400, 511,
+                                   512, 513, 600, 1030]])  # many: GQA-shared workgroups
+def test_paged_attention_matches_oracle(gh, gctx, ora, fp16, geom, ctxs):
     torch = _torch()
     Hq, Hkv, hd = geom
-    rng = np.random.default_rng(Hq + fp16)
-    ctxs = [1, 17, 256, 257, 700]
+    rng = np.random.default_rng(Hq + fp16 + len(ctxs))
     L, layer = 3, 2
     pool, pt = _paged_case(rng, ctxs, Hkv, hd, L, layer, fp16)
     q = rng.standard_normal((len(ctxs), Hq * hd)).astype(np.float32)
