@@ -41,16 +41,28 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def gemv_bytes(n, k, m, act_bytes=4):
-    # algorithmic bytes: packed codes + fp16 scales + activations + f32 outputs
-    return n * k // 2 + 2 * n * k // 32 + m * k * act_bytes + m * n * 4
+def gemv_bytes(n, k, m, digits=1):
+    """Algorithmic HBM bytes of one prepared GEMV launch: packed codes (K/2 per
+    row) + fp16 group scales (K/16 per row) + the activation planes it reads
+    (`digits` int8 bytes per element plus an 8-byte scale/correction per
+    32-element group, per row of M) + the f32 outputs."""
+    return n * k // 2 + n * k // 16 + m * k * digits + m * (k // 32) * 8 + m * n * 4
+
+
+MALL_BYTES = 256 << 20   # MI355X Infinity Cache; rotated weight copies must exceed it
 
 
 def time_gemv(gh, ctx, torch, n, k, m, reps, act):
+    """Cold GEMV timing: the launches rotate over enough weight copies (same
+    content, separate HBM allocations) that the 256 MB MALL cannot serve a
+    repeat, which is the condition of every projection in a decode token (a 7B
+    model is ~4.5 GB of weights). HIP events on the launch stream."""
     L = gh.lib()
     packed = gh.synth_int4(SEED, n * 7 + k, n * k // 2)
     s16 = gh.synth_scales_f16(SEED, n * 11 + k, n * k // 32)
-    w = ctx.weight(packed, s16, k, n)
+    wbytes = n * k // 2 + n * k // 16
+    copies = max(2, -(-3 * MALL_BYTES // wbytes))
+    ws = [ctx.weight(packed, s16, k, n) for _ in range(copies)]
     del packed, s16
     try:
         stream = torch.cuda.Stream()  # non-null handle: our launches and the events share it
@@ -60,23 +72,38 @@ def time_gemv(gh, ctx, torch, n, k, m, reps, act):
         torch.cuda.synchronize()
         gh.check(L.glacier_hip_activation_prepare(ctx.h, x.data_ptr(), gh.F32, m, k, act,
                                                   planes.data_ptr(), stream.cuda_stream), "prepare")
-        for _ in range(5):
-            gh.check(L.glacier_hip_int4_gemv_prepared(ctx.h, w, planes.data_ptr(), m, act, None,
-                                                      y.data_ptr(), stream.cuda_stream), "gemv")
+
+        def go(i):
+            return L.glacier_hip_int4_gemv_prepared(ctx.h, ws[i % copies], planes.data_ptr(), m, act,
+                                                    None, y.data_ptr(), stream.cuda_stream)
+        for i in range(copies):
+            gh.check(go(i), "gemv", ctx.h)
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for _ in range(reps):
-            L.glacier_hip_int4_gemv_prepared(ctx.h, w, planes.data_ptr(), m, act, None,
-                                             y.data_ptr(), stream.cuda_stream)
-        e1.record(stream)
+        # the launches are captured into a graph so that host submission cost
+        # (ctypes + launch, several us) does not hide the kernels' own time
+        reps = max(reps, copies) // copies * copies
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for i in range(reps):
+                go(i)
+        iters = 5
+        with torch.cuda.stream(stream):
+            g.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(iters):
+                g.replay()
+            e1.record(stream)
         torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1000.0 / reps
-        b = gemv_bytes(n, k, m)
+        us = e0.elapsed_time(e1) * 1000.0 / (reps * iters)
+        del g
+        b = gemv_bytes(n, k, m, 1 if act == gh.ACT_Q8 else 3)
         return dict(N=n, K=k, M=m, act="q8" if act == gh.ACT_Q8 else "f32", us=round(us, 2),
-                    bytes=b, gbs=round(b / us / 1e3, 1), frac=round(b / us / 1e3 / HBM_PEAK_GBS, 4))
+                    bytes=b, gbs=round(b / us / 1e3, 1), frac=round(b / us / 1e3 / HBM_PEAK_GBS, 4),
+                    weight_copies=copies)
     finally:
-        L.glacier_hip_int4_weight_destroy(w)
+        for w in ws:
+            L.glacier_hip_int4_weight_destroy(w)
 
 
 def auto_act(gh, n, k):

@@ -59,8 +59,7 @@ struct GemvArgs {
   float *y;                 // EPI_PLAIN/RESID: [M][N]; SWIGLU: [M][N/2]
   const float *resid;       // EPI_RESID
   int epi;
-  int prefetch;             // quads in flight per wave (4 or 8); 0 = default
-  int target_waves;         // launch-shape heuristic input; 0 = default
+  int prefetch;             // quads in flight per wave (4 or 8); 0 = heuristic
   int ksplit_override;      // force the K split (tuning); 0 = heuristic
   int rb_override;          // row blocks per workgroup with ksplit_override
   int ksplit;               // set by launch_gemv
@@ -69,13 +68,14 @@ struct GemvArgs {
 };
 
 // Launch shape of one GEMV: RB row blocks per workgroup, KS waves per row
-// block splitting K, activation planes in LDS when they fit.
+// block splitting K, U quads in flight per wave, activation planes in LDS
+// when they fit.
 struct GemvShape {
-  int ksplit, rb, waves, grid;
+  int ksplit, rb, waves, grid, unroll;
   bool lds_a;
   size_t lds_bytes;
 };
-GemvShape plan_gemv(int N, int K, int M, int D, int target_waves = 0);
+GemvShape plan_gemv(int N, int K, int M, int D);
 
 // Prepare activation planes from x [M][K] (f32 or bf16), optionally
 // RMS-normalised with weight `norm_w` first (kernels.zig:141-220).

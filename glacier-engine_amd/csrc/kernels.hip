@@ -1,8 +1,9 @@
 // kernels.hip — hand-written gfx950 kernels for Glacier's text token loop.
 //
-//  K1  gemv_kernel     INT4 x (Q8 | f32-as-3-digit) GEMV on v_mfma_i32_16x16x32_i8,
-//                      split-K with a deterministic last-arriving finisher and
-//                      fused epilogues (residual, SwiGLU, RoPE + paged KV write).
+//  K1  gemv_kernel     INT4 x (Q8 | f32-as-3-digit) GEMV: v_dot4_i32_i8 for one
+//                      or two rows, v_mfma_i32_16x16x32_i8 above; split-K
+//                      reduced inside the workgroup through LDS; fused
+//                      epilogues (residual, SwiGLU, RoPE + paged KV write).
 //  K4  prep_act_kernel RMSNorm (kernels.zig:141-220) fused with the activation
 //                      quantiser (int4_matmul.zig:380-398).
 //  K3  attn_*          paged-KV GQA decode attention (split over context chunks).
@@ -163,24 +164,39 @@ hipError_t launch_prep_act(const void *x, int x_bf16, const float *norm_w, float
 // lanes of a row are summed once at the end.
 // M > 2: v_mfma_i32_16x16x32_i8 per group, B operand = k-chunk c of the
 // group gathered with one coalesced dword load per group.
-static constexpr int kTargetWaves = 8192;
+//
+// Launch shape (measured cold, weights rotated through more than the 256 MB
+// MALL): a wave owns at most 16 quads of its row block; K is split further
+// while the doubled grid stays below 4096 waves and every wave keeps >= 2
+// quads. Row blocks per workgroup fill it to 4 waves (8 when the activation
+// planes are 3 digits deep: every workgroup stages the whole plane set in
+// LDS, so fewer, larger workgroups stage less). The resident-wave budget
+// decides U: the dot4 kernel holds 6 waves/SIMD at U=4 and 4 at U=8, so a
+// grid between those two capacities (4096..6144 waves on 256 CUs) runs one
+// round at U=4 but two at U=8; elsewhere U=8 keeps more bytes in flight.
 static constexpr size_t kLdsLimit = 64 * 1024;
 
 static size_t planes_bytes(int groups, int M, int D) {
   return (size_t)groups * ((size_t)D * M * 32 + (size_t)M * sizeof(ActMeta));
 }
 
-GemvShape plan_gemv(int N, int K, int M, int D, int target_waves) {
+GemvShape plan_gemv(int N, int K, int M, int D) {
   GemvShape p;
   const int NB = N / 16, KQ = K / 128;
-  if (target_waves <= 0) target_waves = kTargetWaves;
-  int ks = (target_waves + NB - 1) / NB;
-  const int max_ks = KQ >= 4 ? std::min(16, KQ / 2) : 1;
-  ks = std::max(1, std::min(ks, max_ks));
-  int rb = std::max(1, std::min(16 / ks, 4));
+  const bool mfma = M > 2;
+  const int max_ks = std::max(1, std::min(16, KQ / 2));
+  int ks = 1;
+  while (ks * 2 <= max_ks && (KQ + ks - 1) / ks > 16) ks *= 2;
+  while (ks * 2 <= max_ks && NB * ks * 2 < 4096 && KQ >= 4 * ks) ks *= 2;
+  const int rb = std::min(4, std::max(1, (D == 3 ? 8 : 4) / ks));
   p.ksplit = ks;
   p.rb = rb;
   p.waves = ks * rb;
+  const long total = (long)NB * ks;
+  if (mfma)
+    p.unroll = (p.waves <= 4 && total <= 3072) ? 8 : 4;
+  else
+    p.unroll = (total > 4096 && total <= 6144) ? 4 : 8;
   const size_t red = (size_t)p.waves * ((M + 15) / 16) * 4 * 64 * sizeof(float);
   const size_t planes = planes_bytes(K / 32, M, D);
   p.lds_a = planes <= kLdsLimit;
@@ -464,20 +480,24 @@ hipError_t launch_gemv(const GemvArgs &a0, hipStream_t st) {
   GemvArgs a = a0;
   const int MT = (a.M + 15) / 16;
   if (MT > 2 || a.N % 16 || a.K % 128 || !a.act_q || !a.act_meta) return hipErrorInvalidValue;
-  GemvShape p = plan_gemv(a.N, a.K, a.M, a.D, a.target_waves);
+  GemvShape p = plan_gemv(a.N, a.K, a.M, a.D);
   if (a.ksplit_override > 0) {
     p.ksplit = a.ksplit_override;
-    p.rb = a.rb_override > 0 ? a.rb_override : std::max(1, std::min(16 / p.ksplit, 4));
+    p.rb = a.rb_override > 0 ? a.rb_override : std::max(1, 4 / p.ksplit);
     p.waves = p.ksplit * p.rb;
+    if (p.waves > 16 || p.ksplit > a.K / 128) return hipErrorInvalidValue;
     p.grid = (a.N / 16 + p.rb - 1) / p.rb;
     const size_t red = (size_t)p.waves * MT * 4 * 64 * sizeof(float);
     p.lds_bytes = std::max(p.lds_a ? planes_bytes(a.K / 32, a.M, a.D) : 0, red);
   }
   a.ksplit = p.ksplit;
-  const int U = a.prefetch ? a.prefetch : 4;
   dim3 grid(p.grid), block(64 * p.waves);
   const bool dot4 = a.M <= 2 && !a.force_mfma;
   const bool small = p.waves <= 4;
+  // the MFMA kernel at U=8 needs more than the 128 VGPRs a 1024-thread
+  // workgroup allows; it only runs with small workgroups
+  int U = a.prefetch ? a.prefetch : p.unroll;
+  if (U != 8 || (!dot4 && !small)) U = 4;
   const size_t lds = p.lds_bytes;
 #define GK_KERNEL(DD, MM, UU, LL, T4, LBB) gemv_kernel<DD, MM, UU, LL, T4, LBB>
 #define GK_GO(DD, MM, UU, LL, T4)                                                              \
