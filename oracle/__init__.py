@@ -39,7 +39,7 @@ class Model(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in ("num_layers", "dim", "hidden_dim", "num_heads",
                                           "num_kv_heads", "head_dim", "vocab_size", "group_size")] + \
         [("rms_eps", C.c_float), ("rope_theta", C.c_float), ("token_embedding", _P),
-         ("final_norm", _P), ("lm_head", Int4Weight), ("layers", _P)]
+         ("final_norm", _P), ("lm_head", Int4Weight), ("layers", _P), ("kv_fp16", C.c_uint32)]
 
 
 class Ledger(C.Structure):
@@ -259,7 +259,7 @@ def xoshiro256_init(seed):
 class OracleModel:
     """Keeps the numpy tensors alive while the C model struct points at them."""
 
-    def __init__(self, cfg, host):
+    def __init__(self, cfg, host, kv_fp16=False):
         self.cfg = cfg
         self.host = host
         self._keep = []
@@ -291,7 +291,7 @@ class OracleModel:
                        cfg["num_kv_heads"], cfg["head_dim"], cfg["vocab_size"], cfg["group_size"],
                        cfg["rms_eps"], cfg["rope_theta"], arr(host["embedding"]),
                        arr(host["final_norm"]), w(host["lm_head"], host["lm_head_scales"]),
-                       C.cast(layers, _P))
+                       C.cast(layers, _P), 1 if kv_fp16 else 0)
 
     def generate(self, prompt, max_new, logits_steps=()):
         prompt = np.ascontiguousarray(prompt, dtype=np.uint32)

@@ -590,6 +590,11 @@ int go_forward_layer(const go_model *m, size_t li, const float *x_row,
     if ((rc = project(h_norm, L->wv, L->bv, v, kv_dim, dim, gs))) goto done;
     /* RoPE on k, append row, RoPE on q (:1712-1735) */
     go_rope_apply(rope_cos, rope_sin, hd / 2, k, pos, m->num_kv_heads, hd);
+    if (m->kv_fp16)
+        for (size_t i = 0; i < kv_dim; i++) {
+            k[i] = go_f16_to_f32(go_f32_to_f16(k[i]));
+            v[i] = go_f16_to_f32(go_f32_to_f16(v[i]));
+        }
     memcpy(k_cache + pos * kv_dim, k, kv_dim * sizeof(float));
     memcpy(v_cache + pos * kv_dim, v, kv_dim * sizeof(float));
     go_rope_apply(rope_cos, rope_sin, hd / 2, q, pos, m->num_heads, hd);

@@ -138,6 +138,10 @@ typedef struct {
     const float *final_norm;      /* [dim] */
     go_int4_weight lm_head;       /* [vocab, dim] */
     const go_layer *layers;       /* [num_layers] */
+    uint32_t kv_fp16;             /* 0: f32 KV rows as the reference stores
+                                   * them (paged_kv_cache.zig:1-8); 1: rows
+                                   * rounded to fp16 on store (the fp16 page
+                                   * pools of the GPU path) */
 } go_model;
 
 /* Greedy generate. tokens_out gets max_new tokens. If logits_steps/logits_out

@@ -18,7 +18,11 @@ norm weights the residual stream is dominated by the attention average and
 greedy decoding repeats one token, which makes token identity a weak check;
 the unit-norm variant produces a varied sequence.
 
-Run: python tests/golden/make_c1_golden.py [spec|unitnorm]  (~2 min each on 8 cores)
+A third fixture, c1_qwen05b_unitnorm_kvf16.npz, is the unit-norm model with
+fp16 KV pages (BASELINE configs 3 and 5 ask for fp16 KV; the reference stores
+f32): the oracle rounds every K/V row to fp16 on store.
+
+Run: python tests/golden/make_c1_golden.py [spec|unitnorm|unitnorm_kvf16]  (~2 min each on 8 cores)
 """
 import os
 import sys
@@ -55,11 +59,11 @@ def main(variant):
     oracle.set_threads(os.cpu_count() or 1)
     t = time.time()
     host = gh.random_model_host(C1, SEED)
-    if variant == "unitnorm":
+    if variant.startswith("unitnorm"):
         host = unit_norm(host)
     prompt = gh.synth_tokens(SEED, PROMPT_ID, C1["vocab_size"], PROMPT_LEN)
     print(f"weights generated in {time.time() - t:.1f}s", flush=True)
-    om = oracle.OracleModel(C1, host)
+    om = oracle.OracleModel(C1, host, kv_fp16=variant.endswith("kvf16"))
     t = time.time()
     toks, logits, kv_sha, out_sha = om.generate(prompt, MAX_NEW, logits_steps=STEPS)
     print(f"oracle generate in {time.time() - t:.1f}s", flush=True)
@@ -68,7 +72,8 @@ def main(variant):
     top_idx = np.argsort(-logits, axis=1)[:, :32].astype(np.int32)
     top_val = np.take_along_axis(logits, top_idx, axis=1)
     np.savez_compressed(
-        os.path.join(HERE, "c1_qwen05b.npz" if variant == "spec" else "c1_qwen05b_unitnorm.npz"), tokens=toks, prompt=prompt,
+        os.path.join(HERE, "c1_qwen05b.npz" if variant == "spec" else f"c1_qwen05b_{variant}.npz"),
+        tokens=toks, prompt=prompt,
         steps=np.array(STEPS, np.int32), sample_idx=idx, sample_logits=logits[:, idx],
         top_idx=top_idx, top_val=top_val, max_abs=np.abs(logits).max(1),
         kv_sha256=np.frombuffer(kv_sha, np.uint8), output_sha256=np.frombuffer(out_sha, np.uint8),

@@ -18,9 +18,9 @@ C1 = dict(num_layers=24, dim=896, hidden_dim=4864, num_heads=14, num_kv_heads=2,
           vocab_size=151936, group_size=32, rms_eps=1e-6, rope_theta=1e6)
 
 
-@pytest.mark.parametrize("variant", ["spec", "unitnorm"])
+@pytest.mark.parametrize("variant", ["spec", "unitnorm", "unitnorm_kvf16"])
 def test_c1_greedy_128_matches_oracle(gh, gctx, variant):
-    name = "c1_qwen05b.npz" if variant == "spec" else "c1_qwen05b_unitnorm.npz"
+    name = "c1_qwen05b.npz" if variant == "spec" else f"c1_qwen05b_{variant}.npz"
     fx = np.load(os.path.join(HERE, "golden", name))
     seed = int(fx["seed"][0])
     m = gh.Model(gctx, C1)
@@ -34,7 +34,8 @@ def test_c1_greedy_128_matches_oracle(gh, gctx, variant):
         host["final_norm"] = (host["final_norm"] + 1.0).astype(np.float32)
         m.set_from_host(host)
         del host
-    sess = gh.Session(m, max_lanes=1, max_positions=256, kv_dtype=gh.F32)
+    kv = gh.F16 if variant.endswith("kvf16") else gh.F32
+    sess = gh.Session(m, max_lanes=1, max_positions=256, kv_dtype=kv)
     try:
         sess.begin(0)
         steps = fx["steps"].tolist()

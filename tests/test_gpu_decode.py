@@ -100,6 +100,38 @@ def test_tiny_greedy_matches_oracle(gh, tiny, use_graph):
         sess.close()
 
 
+def test_tiny_greedy_fp16_kv_matches_oracle(gh, gctx, tiny, ora):
+    """fp16 page pools (the configs' KV dtype): the oracle rounds every stored
+    K/V row to fp16 (round to nearest even) and otherwise runs unchanged.
+
+    Logit bar 5e-2 here, not 1e-2: a K/V element whose f32 value lies within
+    the GPU/CPU summation-order difference (~1e-7 relative) of an fp16
+    rounding midpoint rounds the other way (a 5e-4 relative step), and this
+    2-layer, 256-wide model turns such steps into Q8 activation flips that
+    move its logits by percents (perturbing the oracle's embeddings by 1e-5
+    relative moves its step-0 logits by 3.2e-2). The C1-shaped fixture
+    c1_qwen05b_unitnorm_kvf16.npz holds fp16 KV to the 1e-2 bar."""
+    host, _, m = tiny
+    om16 = ora.OracleModel(TINY, host, kv_fp16=True)
+    prompt = gh.synth_tokens(SEED, 99, TINY["vocab_size"], 20)
+    max_new = 24
+    want, wl, kv_sha, out_sha = om16.generate(prompt, max_new, logits_steps=[0, max_new - 1])
+    sess = gh.Session(m, max_lanes=1, max_positions=64, kv_dtype=gh.F16)
+    try:
+        sess.begin(0)
+        toks, logits = _run_gpu(sess, 0, prompt, max_new, logits_at=(max_new - 1,))
+        assert toks == want.tolist()
+        assert _rel(logits[0], wl[0]) < 5e-2
+        assert _rel(logits[max_new - 1], wl[1]) < 5e-2
+        assert bytes(sess.state(0).output_sha256) == out_sha
+        # every stored element is an fp16 value widened to f32
+        kvd = TINY["num_kv_heads"] * TINY["head_dim"]
+        row = sess.kv_row(0, 1, 0, len(prompt), kvd)
+        assert np.array_equal(row, row.astype(np.float16).astype(np.float32))
+    finally:
+        sess.close()
+
+
 def gh_xoshiro(seed):
     import oracle
 
