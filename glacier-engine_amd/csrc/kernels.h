@@ -85,6 +85,15 @@ hipError_t launch_prep_act(const void *x, int x_bf16, const float *norm_w, float
 
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t st);
 
+// Prefill GEMM (K2) for M > 32 activation rows: same arguments and epilogues
+// as launch_gemv (prefetch / ksplit / force_mfma fields are ignored). Block
+// tile (32*mt) x (32*nt) rows x weight rows, 4 waves.
+struct GemmShape {
+  int mt, nt, m_tiles, n_tiles, grid;
+};
+GemmShape plan_gemm(int N, int M);
+hipError_t launch_gemm(const GemvArgs &a, hipStream_t st);
+
 
 hipError_t launch_rmsnorm(const float *x, const float *w, int rows, int dim, float eps,
                           float *out, hipStream_t st);

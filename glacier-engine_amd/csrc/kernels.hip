@@ -13,6 +13,7 @@
 // rounds where the reference rounds; explicit fmaf() marks the places where a
 // fused multiply-add is intended.
 #include "kernels.h"
+#include "epilogue.h"
 
 #include <hip/hip_fp16.h>
 #include <math.h>
@@ -205,13 +206,6 @@ GemvShape plan_gemv(int N, int K, int M, int D) {
   return p;
 }
 
-static __device__ __forceinline__ float silu_mul(float g, float u) {
-  // kernels.zig:465-520: g * (1 / (1 + exp(-g))) * u
-  float sig = 1.0f / (1.0f + expf(-g));
-  float t = g * sig;
-  return t * u;
-}
-
 template <int D, int MT, int U, bool LDS_A, bool DOT4, int LB>
 __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -395,84 +389,16 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
   if (nb >= NB) return;
 
   // ---- fused epilogues: lane (c, n) owns rows m = 16 mt + 4 c + r of column n ----
-  const int N = a.N;
-  const int n = nb * 16 + n_local;
+  const bool paired = a.epi == EPI_SWIGLU || a.epi == EPI_QKV;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = mt * 16 + c * 4 + r;
       const float tot = acc[mt][r];
-      if (a.epi == EPI_SWIGLU || a.epi == EPI_QKV) {
-        // partner row (n_local ^ 8) lives in lane ^ 8 with the same (c, r)
-        const float partner = __shfl_xor(tot, 8);
-        if (m >= M) continue;
-        if (a.epi == EPI_SWIGLU) {
-          if (n_local < 8) {
-            const int j = nb * 8 + n_local;
-            a.y[(size_t)m * (N / 2) + j] = silu_mul(tot, partner);
-          }
-          continue;
-        }
-        const QkvArgs &Q = a.qkv;
-        const int hd = Q.head_dim;
-        const int nbq = Q.num_heads * hd / 16, nbk = Q.num_kv_heads * hd / 16;
-        const int kv_dim = Q.num_kv_heads * hd;
-        const int pos = Q.pos_of_row[m];
-        const int lane_id = Q.lane_of_row[m];
-        const int page = Q.page_table[(size_t)lane_id * Q.max_pages + pos / 16];
-        const size_t page_base =
-            (((size_t)page * Q.num_layers + Q.layer) * 2) * 16 * (size_t)kv_dim;
-        const size_t krow = page_base + (size_t)(pos % 16) * kv_dim;
-        const size_t vrow = page_base + (size_t)(16 + pos % 16) * kv_dim;
-        if (nb < nbq + nbk) {
-          if (n_local >= 8) continue;
-          const bool is_q = nb < nbq;
-          const int rel = is_q ? nb : nb - nbq;
-          const int bph = hd / 16;  // row blocks per head
-          const int head = rel / bph, p = (rel % bph) * 8 + n_local;
-          const int i0 = head * hd + p, i1 = i0 + hd / 2;
-          float x0 = tot, x1 = partner;
-          if (a.bias) {
-            const int off = is_q ? 0 : Q.num_heads * hd;
-            x0 = a.bias[off + i0] + x0;
-            x1 = a.bias[off + i1] + x1;
-          }
-          // RopeTable.apply (generate.zig:813-830)
-          const float cs = Q.rope_cos[(size_t)pos * (hd / 2) + p];
-          const float sn = Q.rope_sin[(size_t)pos * (hd / 2) + p];
-          const float a0 = x0 * cs, b0 = x1 * sn, a1 = x0 * sn, b1 = x1 * cs;
-          const float y0 = a0 - b0, y1 = a1 + b1;
-          if (is_q) {
-            float *qo = Q.q_out + (size_t)m * Q.num_heads * hd;
-            qo[i0] = y0;
-            qo[i1] = y1;
-          } else if (Q.kv_f16) {
-            __half *kp = (__half *)Q.kv_pool;
-            kp[krow + i0] = __float2half_rn(y0);
-            kp[krow + i1] = __float2half_rn(y1);
-          } else {
-            float *kp = (float *)Q.kv_pool;
-            kp[krow + i0] = y0;
-            kp[krow + i1] = y1;
-          }
-        } else {
-          const int idx = (nb - nbq - nbk) * 16 + n_local;
-          float v = tot;
-          if (a.bias) v = a.bias[Q.num_heads * hd + kv_dim + idx] + v;
-          if (Q.kv_f16)
-            ((__half *)Q.kv_pool)[vrow + idx] = __float2half_rn(v);
-          else
-            ((float *)Q.kv_pool)[vrow + idx] = v;
-        }
-        continue;
-      }
-      if (m >= M) continue;
-      if (a.epi == EPI_RESID) {
-        a.y[(size_t)m * N + n] = a.resid[(size_t)m * N + n] + tot;
-      } else {
-        a.y[(size_t)m * N + n] = a.bias ? a.bias[n] + tot : tot;
-      }
+      // partner row (n_local ^ 8) lives in lane ^ 8 with the same (c, r)
+      const float partner = paired ? __shfl_xor(tot, 8) : 0.0f;
+      if (m < M) store_output(a, nb, n_local, m, tot, partner);
     }
 }
 
