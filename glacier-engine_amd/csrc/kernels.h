@@ -102,8 +102,9 @@ hipError_t launch_gather_rows(const float *table, const int32_t *ids, int M, int
                               float *out, hipStream_t st);
 
 // Paged GQA decode attention. Writes out [M][Hq*hd]. Scratch must hold
-// attention_scratch_floats(...) floats.
-size_t attention_scratch_floats(int M, int num_heads, int head_dim, int max_ctx);
+// attention_scratch_floats(...) floats for any M up to max_rows.
+size_t attention_scratch_floats(int max_rows, int num_heads, int num_kv_heads, int head_dim,
+                                int max_ctx);
 hipError_t launch_attention(const float *q, const void *kv_pool, int kv_f16,
                             const int32_t *page_table, int max_pages, const int32_t *lane_of_row,
                             const int32_t *ctx_len, int M, int layer, int num_layers,

@@ -513,10 +513,16 @@ int attention_chunk(int max_ctx, int num_kv_heads, int M) {
   return ch;
 }
 
-size_t attention_scratch_floats(int M, int num_heads, int head_dim, int max_ctx) {
-  // sized for the smallest chunk the planner can pick
-  const int nch = (max_ctx + 127) / 128;
-  return (size_t)M * num_heads * nch * (2 + head_dim);
+size_t attention_scratch_floats(int max_rows, int num_heads, int num_kv_heads, int head_dim,
+                                int max_ctx) {
+  // the largest chunk-record set the planner produces for any row count
+  size_t most = 0;
+  for (int M = 1; M <= max_rows; ++M) {
+    const int ch = attention_chunk(max_ctx, num_kv_heads, M);
+    const size_t nch = (size_t)(max_ctx + ch - 1) / ch;
+    most = std::max(most, (size_t)M * num_heads * nch * (2 + head_dim));
+  }
+  return most;
 }
 
 template <int HD, int F16>

@@ -443,7 +443,8 @@ static int gemv_launch(glacier_hip_context *ctx, glacier_hip_int4_weight *w, con
   a.bias = bias_dev;
   a.y = y_dev;
   a.epi = gk::EPI_PLAIN;
-  GH_CHECK(ctx, gk::launch_gemv(a, st));
+  // up to 32 rows: the decode GEMV (K1); more: the MFMA prefill GEMM (K2)
+  GH_CHECK(ctx, m <= 32 ? gk::launch_gemv(a, st) : gk::launch_gemm(a, st));
   return GLACIER_HIP_OK;
 }
 
@@ -461,7 +462,7 @@ static int gemv_common(glacier_hip_context *ctx, glacier_hip_int4_weight *w, con
                        int activation, hipStream_t st) {
   if (!ctx || !w || !x_dev || !y_dev) return GLACIER_HIP_INVALID_ARGUMENT;
   if (w->ctx != ctx) return GLACIER_HIP_INVALID_HANDLE;
-  if (m == 0 || m > 32) return GLACIER_HIP_SHAPE_MISMATCH;
+  if (m == 0 || m > GLACIER_HIP_MAX_ROWS) return GLACIER_HIP_SHAPE_MISMATCH;
   if (x_dtype != GLACIER_HIP_F32 && x_dtype != GLACIER_HIP_BF16) return GLACIER_HIP_DTYPE_UNSUPPORTED;
   const int D = act_digits(gh::resolve_activation(activation, w->out_f, w->in_f));
   if (!D) return GLACIER_HIP_INVALID_ARGUMENT;
@@ -499,7 +500,7 @@ int glacier_hip_activation_prepare(glacier_hip_context *ctx, const void *x_dev, 
   if (!ctx || !x_dev || !act_dev) return GLACIER_HIP_INVALID_ARGUMENT;
   const int D = act_digits(activation);
   if (!D) return GLACIER_HIP_INVALID_ARGUMENT;
-  if (m == 0 || m > 32 || in_f == 0 || in_f % 128 != 0) return GLACIER_HIP_SHAPE_MISMATCH;
+  if (m == 0 || m > GLACIER_HIP_MAX_ROWS || in_f == 0 || in_f % 128 != 0) return GLACIER_HIP_SHAPE_MISMATCH;
   if (x_dtype != GLACIER_HIP_F32 && x_dtype != GLACIER_HIP_BF16) return GLACIER_HIP_DTYPE_UNSUPPORTED;
   std::lock_guard<std::mutex> lk(ctx->mu);
   return prepare_launch(ctx, x_dev, x_dtype, m, in_f, D, act_dev,
@@ -513,7 +514,7 @@ int glacier_hip_int4_gemv_prepared(glacier_hip_context *ctx, glacier_hip_int4_we
   if (w->ctx != ctx) return GLACIER_HIP_INVALID_HANDLE;
   const int D = act_digits(activation);
   if (!D) return GLACIER_HIP_INVALID_ARGUMENT;
-  if (m == 0 || m > 32) return GLACIER_HIP_SHAPE_MISMATCH;
+  if (m == 0 || m > GLACIER_HIP_MAX_ROWS) return GLACIER_HIP_SHAPE_MISMATCH;
   std::lock_guard<std::mutex> lk(ctx->mu);
   return gemv_launch(ctx, w, act_dev, m, D, bias_dev, y_dev,
                      stream ? (hipStream_t)stream : ctx->stream);
@@ -572,7 +573,8 @@ int glacier_hip_paged_attention(glacier_hip_context *ctx, const float *q_dev,
   std::lock_guard<std::mutex> lk(ctx->mu);
   hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
   // lane_of_row = identity: row i attends with page-table row i
-  const size_t sc = gk::attention_scratch_floats((int)lanes, (int)num_heads, (int)head_dim, (int)max_ctx);
+  const size_t sc = gk::attention_scratch_floats((int)lanes, (int)num_heads, (int)num_kv_heads,
+                                                 (int)head_dim, (int)max_ctx);
   int rc = gh::ensure_scratch(ctx, sc * 4 + 256 + lanes * 4, 1);
   if (rc) return rc;
   int32_t *ident = (int32_t *)((char *)ctx->scratch + ((sc * 4 + 255) & ~(size_t)255));

@@ -84,11 +84,16 @@ struct Lane {
   std::vector<uint32_t> output;
 };
 
-struct StepInputs {  // uploaded once per step, in one copy
+struct StepInputs {  // uploaded once per decode step, in one copy
   int32_t tokens[64];
   int32_t lane_of_row[64];
   int32_t pos_of_row[64];
   int32_t ctx_len[64];
+};
+
+// Device arrays describing the activation rows of one launch sequence.
+struct RowPtrs {
+  const int32_t *tokens, *lane_of_row, *pos_of_row, *ctx_len;
 };
 
 struct glacier_hip_session {
@@ -96,6 +101,8 @@ struct glacier_hip_session {
   glacier_hip_session_options_t opt{};
   uint32_t max_pages = 0;  // per lane
   uint32_t total_pages = 0;
+  uint32_t rows_cap = 0;   // max(max_lanes, prefill_chunk): rows of the scratch buffers
+  uint32_t prefill_chunk = 0;
   std::vector<int32_t> free_pages;
   std::vector<Lane> lanes;
   // device
@@ -112,8 +119,11 @@ struct glacier_hip_session {
   gk::ArgmaxResult *arg_result = nullptr;
   uint64_t *elig_words = nullptr;
   StepInputs *step_dev = nullptr;
+  int32_t *pf_dev = nullptr;     // prefill rows: tokens, lane, pos, ctx [4][prefill_chunk]
   // host pinned
   StepInputs *step_host = nullptr;
+  int32_t *pf_host = nullptr;
+  int32_t *pt_host = nullptr;    // mirror of page_table [max_lanes][max_pages]
   gk::ArgmaxResult *res_host = nullptr;
   bool inject_failure = false;
   // graph cache: key = (rows, with_head, eligible)
@@ -343,7 +353,7 @@ int head_D(const glacier_hip_session *s) {
 }
 
 // One projection: activation conversion (RMSNorm + Q8 / digit planes) then
-// the GEMV with its epilogue.
+// the GEMV (up to 32 rows) or the MFMA GEMM (prompt chunks) with its epilogue.
 hipError_t run_proj(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, int rows,
                     const float *x, const float *norm_w, int epi, const float *bias, float *y,
                     const float *resid, const gk::QkvArgs *qkv, hipStream_t st) {
@@ -365,15 +375,16 @@ hipError_t run_proj(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, i
   a.resid = resid;
   a.epi = epi;
   if (qkv) a.qkv = *qkv;
-  return gk::launch_gemv(a, st);
+  return rows <= 32 ? gk::launch_gemv(a, st) : gk::launch_gemm(a, st);
 }
 
-// The full launch sequence of one token step for `rows` activation rows.
-hipError_t enqueue_step(glacier_hip_session *s, int rows, bool head, bool elig, hipStream_t st) {
+// Embedding gather and every decoder layer for `rows` activation rows
+// (generate.zig:1511-1967 per row; K/V rows land in the rows' pages).
+hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, hipStream_t st) {
   glacier_hip_model *m = s->model;
   const auto &c = m->cfg;
   const int D = (int)c.dim;
-  hipError_t e = gk::launch_gather_rows(m->embed, s->step_dev->tokens, rows, D, s->x_res, st);
+  hipError_t e = gk::launch_gather_rows(m->embed, rp.tokens, rows, D, s->x_res, st);
   if (e != hipSuccess) return e;
   gk::QkvArgs q{};
   q.q_out = s->q;
@@ -381,8 +392,8 @@ hipError_t enqueue_step(glacier_hip_session *s, int rows, bool head, bool elig, 
   q.kv_f16 = s->opt.kv_dtype == GLACIER_HIP_F16;
   q.page_table = s->page_table;
   q.max_pages = (int)s->max_pages;
-  q.lane_of_row = s->step_dev->lane_of_row;
-  q.pos_of_row = s->step_dev->pos_of_row;
+  q.lane_of_row = rp.lane_of_row;
+  q.pos_of_row = rp.pos_of_row;
   q.rope_cos = s->rope_cos;
   q.rope_sin = s->rope_sin;
   q.num_layers = (int)c.num_layers;
@@ -397,10 +408,10 @@ hipError_t enqueue_step(glacier_hip_session *s, int rows, bool head, bool elig, 
                  gk::EPI_QKV, L.qkv_bias, nullptr, nullptr, &q, st);
     if (e != hipSuccess) return e;
     e = gk::launch_attention(s->q, s->kv_pool, s->opt.kv_dtype == GLACIER_HIP_F16, s->page_table,
-                             (int)s->max_pages, s->step_dev->lane_of_row, s->step_dev->ctx_len,
-                             rows, (int)l, (int)c.num_layers, (int)c.num_heads,
-                             (int)c.num_kv_heads, (int)c.head_dim, (int)s->opt.max_positions,
-                             s->att_scratch, s->attn, st);
+                             (int)s->max_pages, rp.lane_of_row, rp.ctx_len, rows, (int)l,
+                             (int)c.num_layers, (int)c.num_heads, (int)c.num_kv_heads,
+                             (int)c.head_dim, (int)s->opt.max_positions, s->att_scratch, s->attn,
+                             st);
     if (e != hipSuccess) return e;
     e = run_proj(s, L.o, layer_D(s, L.o->out_f, L.o->in_f), rows, s->attn, nullptr,
                  gk::EPI_RESID, nullptr, s->h, s->x_res, nullptr, st);
@@ -412,9 +423,16 @@ hipError_t enqueue_step(glacier_hip_session *s, int rows, bool head, bool elig, 
                  gk::EPI_RESID, nullptr, s->x_res, s->h, nullptr, st);
     if (e != hipSuccess) return e;
   }
-  if (!head) return hipSuccess;
-  e = run_proj(s, m->head, head_D(s), rows, s->x_res, m->final_norm, gk::EPI_PLAIN, nullptr,
-               s->logits, nullptr, nullptr, st);
+  return hipSuccess;
+}
+
+// Final RMSNorm + LM head + (eligible) argmax for `rows` rows starting at x.
+hipError_t enqueue_head(glacier_hip_session *s, int rows, const float *x, bool elig,
+                        hipStream_t st) {
+  glacier_hip_model *m = s->model;
+  const auto &c = m->cfg;
+  hipError_t e = run_proj(s, m->head, head_D(s), rows, x, m->final_norm, gk::EPI_PLAIN, nullptr,
+                          s->logits, nullptr, nullptr, st);
   if (e != hipSuccess) return e;
   const long V = (long)c.vocab_size;
   const long W = (V + 63) / 64;
@@ -422,14 +440,25 @@ hipError_t enqueue_step(glacier_hip_session *s, int rows, bool head, bool elig, 
                            s->arg_counters, s->arg_result, st);
 }
 
+// The full launch sequence of one decode step for `rows` lanes.
+hipError_t enqueue_step(glacier_hip_session *s, int rows, bool head, bool elig, hipStream_t st) {
+  const RowPtrs rp{s->step_dev->tokens, s->step_dev->lane_of_row, s->step_dev->pos_of_row,
+                   s->step_dev->ctx_len};
+  hipError_t e = enqueue_layers(s, rows, rp, st);
+  if (e != hipSuccess || !head) return e;
+  return enqueue_head(s, rows, s->x_res, elig, st);
+}
+
 void destroy_session(glacier_hip_session *s) {
   void *ptrs[] = {s->kv_pool, s->page_table, s->rope_cos, s->rope_sin, s->x_res, s->h, s->q,
                   s->attn, s->act, s->logits, s->act_q, s->act_meta,
                   s->att_scratch, s->arg_scratch, s->arg_counters, s->arg_result, s->elig_words,
-                  s->step_dev};
+                  s->step_dev, s->pf_dev};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   if (s->step_host) (void)hipHostFree(s->step_host);
+  if (s->pf_host) (void)hipHostFree(s->pf_host);
+  if (s->pt_host) (void)hipHostFree(s->pt_host);
   if (s->res_host) (void)hipHostFree(s->res_host);
   for (auto &g : s->graphs) (void)hipGraphExecDestroy(g.exec);
   delete s;
@@ -478,6 +507,23 @@ struct RowTxn {
   glacier_hip_page_map_root_t after;
 };
 
+void abort_rows(glacier_hip_session *s, std::vector<RowTxn> &txns) {
+  // abortRow (paged_kv_cache.zig:1146-1160): a newly installed page loses
+  // its ownership generation; nothing else changes. Installs are undone
+  // newest first so the free list returns to its order before the step.
+  for (size_t i = txns.size(); i-- > 0;) {
+    const RowTxn &t = txns[i];
+    Lane &ln = s->lanes[t.lane];
+    if (t.installs) {
+      ln.page_of[t.pos / 16] = -1;
+      ln.page_gen[t.pos / 16] = 0;
+      s->pt_host[(size_t)t.lane * s->max_pages + t.pos / 16] = 0;
+      s->free_pages.push_back(t.page);
+    }
+  }
+  txns.clear();
+}
+
 // beginRow (paged_kv_cache.zig:1006-1072) for every participating lane.
 int begin_rows(glacier_hip_session *s, const uint32_t *lanes, uint32_t count,
                std::vector<RowTxn> &txns) {
@@ -492,13 +538,7 @@ int begin_rows(glacier_hip_session *s, const uint32_t *lanes, uint32_t count,
     if (t.installs) {
       if (s->free_pages.empty()) {
         // roll back the installs made so far in this step
-        for (auto &u : txns)
-          if (u.installs) {
-            s->free_pages.push_back(u.page);
-            s->lanes[u.lane].page_of[u.pos / 16] = -1;
-            s->lanes[u.lane].page_gen[u.pos / 16] = 0;
-          }
-        txns.clear();
+        abort_rows(s, txns);
         return GLACIER_HIP_CACHE_FULL;
       }
       t.page = s->free_pages.back();
@@ -506,6 +546,7 @@ int begin_rows(glacier_hip_session *s, const uint32_t *lanes, uint32_t count,
       t.gen = ln.next_page_generation;
       ln.page_of[page] = t.page;
       ln.page_gen[page] = t.gen;
+      s->pt_host[(size_t)lanes[i] * s->max_pages + page] = t.page;
     } else {
       t.page = ln.page_of[page];
       t.gen = ln.page_gen[page];
@@ -524,18 +565,49 @@ int begin_rows(glacier_hip_session *s, const uint32_t *lanes, uint32_t count,
   return GLACIER_HIP_OK;
 }
 
-void abort_rows(glacier_hip_session *s, std::vector<RowTxn> &txns) {
-  // abortRow (paged_kv_cache.zig:1146-1160): a newly installed page loses
-  // its ownership generation; nothing else changes.
-  for (auto &t : txns) {
-    Lane &ln = s->lanes[t.lane];
-    if (t.installs) {
-      ln.page_of[t.pos / 16] = -1;
-      ln.page_gen[t.pos / 16] = 0;
-      s->free_pages.push_back(t.page);
-    }
-  }
+// beginRow for `n` consecutive rows of one lane (a prompt chunk): row i's
+// transaction starts from row i - 1's staged root, exactly as n sequential
+// per-token transactions would (generate.zig:5080-5118 commits per token).
+int begin_chunk(glacier_hip_session *s, uint32_t lane, uint32_t n, std::vector<RowTxn> &txns) {
   txns.clear();
+  txns.reserve(n);  // `before` points into txns
+  Lane &ln = s->lanes[lane];
+  const glacier_hip_page_map_root_t *before = &ln.root;
+  uint64_t page_gen = ln.next_page_generation;
+  for (uint32_t i = 0; i < n; ++i) {
+    RowTxn t{};
+    t.lane = lane;
+    t.pos = ln.len + i;
+    const uint64_t page = t.pos / 16;
+    t.installs = t.pos % 16 == 0;
+    if (t.installs) {
+      if (s->free_pages.empty()) {
+        abort_rows(s, txns);
+        return GLACIER_HIP_CACHE_FULL;
+      }
+      t.page = s->free_pages.back();
+      s->free_pages.pop_back();
+      t.gen = page_gen++;
+      ln.page_of[page] = t.page;
+      ln.page_gen[page] = t.gen;
+      s->pt_host[(size_t)lane * s->max_pages + page] = t.page;
+    } else {
+      t.page = ln.page_of[page];
+      t.gen = ln.page_gen[page];
+    }
+    t.after.cache_instance = ln.instance;
+    t.after.generation = ln.next_root_generation + i;
+    t.after.committed_len = t.pos + 1;
+    t.after.committed_pages = before->committed_pages + (t.installs ? 1 : 0);
+    if (t.installs)
+      appendOwnershipDigest(before->ownership_sha256, ln.instance, page, t.gen,
+                            t.after.ownership_sha256);
+    else
+      memcpy(t.after.ownership_sha256, before->ownership_sha256, 32);
+    txns.push_back(t);
+    before = &txns.back().after;
+  }
+  return GLACIER_HIP_OK;
 }
 
 void commit_rows(glacier_hip_session *s, std::vector<RowTxn> &txns) {
@@ -547,6 +619,35 @@ void commit_rows(glacier_hip_session *s, std::vector<RowTxn> &txns) {
     ln.len = t.pos + 1;
   }
   txns.clear();
+}
+
+// Copies the page-table entries installed by `txns` from the pinned host
+// mirror (runs of consecutive logical pages of one lane go in one copy). The
+// mirror is only rewritten after the step's stream synchronisation.
+hipError_t upload_page_entries(glacier_hip_session *s, const std::vector<RowTxn> &txns,
+                               hipStream_t st) {
+  size_t i = 0;
+  while (i < txns.size()) {
+    if (!txns[i].installs) {
+      ++i;
+      continue;
+    }
+    const uint32_t lane = txns[i].lane;
+    const uint64_t p0 = txns[i].pos / 16;
+    uint64_t p1 = p0 + 1;
+    size_t j = i + 1;
+    for (; j < txns.size() && txns[j].lane == lane; ++j)
+      if (txns[j].installs) {
+        if (txns[j].pos / 16 != p1) break;
+        ++p1;
+      }
+    const size_t off = (size_t)lane * s->max_pages + p0;
+    hipError_t e = hipMemcpyAsync(s->page_table + off, s->pt_host + off, (p1 - p0) * 4,
+                                  hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) return e;
+    i = j;
+  }
+  return hipSuccess;
 }
 
 // Execute one step for `count` rows; on success results are in res_host.
@@ -572,14 +673,8 @@ int run_step(glacier_hip_session *s, const uint32_t *lanes, const uint32_t *toke
   hipError_t e = hipMemcpyAsync(s->step_dev, s->step_host, sizeof(StepInputs),
                                 hipMemcpyHostToDevice, st);
   if (e != hipSuccess) return fail(e, "step inputs");
-  for (auto &t : txns)
-    if (t.installs) {
-      e = hipMemcpyAsync(s->page_table + (size_t)t.lane * s->max_pages + t.pos / 16, &t.page, 4,
-                         hipMemcpyHostToDevice, st);
-      if (e != hipSuccess) return fail(e, "page table");
-      e = hipStreamSynchronize(st);  // t.page is pageable host memory
-      if (e != hipSuccess) return fail(e, "page table sync");
-    }
+  e = upload_page_entries(s, txns, st);
+  if (e != hipSuccess) return fail(e, "page table");
   const uint64_t W = (c.vocab_size + 63) / 64;
   if (elig_host) {
     e = hipMemcpyAsync(s->elig_words, elig_host, (size_t)count * W * 8, hipMemcpyHostToDevice, st);
@@ -635,6 +730,65 @@ int run_step(glacier_hip_session *s, const uint32_t *lanes, const uint32_t *toke
   return GLACIER_HIP_OK;
 }
 
+// One prompt chunk of `n` rows of one lane: all layers over the rows at
+// once; with `head`, the last row's final norm, LM head and argmax.
+int run_prefill_chunk(glacier_hip_session *s, uint32_t lane, const uint32_t *tokens, uint32_t n,
+                      bool head, float *logits_host, std::vector<RowTxn> &txns) {
+  glacier_hip_context *ctx = s->model->ctx;
+  const auto &c = s->model->cfg;
+  hipStream_t st = ctx->stream;
+  int rc = begin_chunk(s, lane, n, txns);
+  if (rc) return rc;
+  const uint32_t C = s->prefill_chunk;
+  int32_t *tok = s->pf_host, *lor = s->pf_host + C, *por = s->pf_host + 2 * C,
+          *ctl = s->pf_host + 3 * C;
+  for (uint32_t i = 0; i < n; ++i) {
+    tok[i] = (int32_t)tokens[i];
+    lor[i] = (int32_t)lane;
+    por[i] = (int32_t)txns[i].pos;
+    ctl[i] = (int32_t)txns[i].pos + 1;
+  }
+  auto fail = [&](hipError_t e, const char *what) {
+    (void)hipStreamSynchronize(st);
+    abort_rows(s, txns);
+    return hip_fail(ctx, e, what);
+  };
+  hipError_t e = hipSuccess;
+  for (int k = 0; k < 4 && e == hipSuccess; ++k)
+    e = hipMemcpyAsync(s->pf_dev + (size_t)k * C, s->pf_host + (size_t)k * C, (size_t)n * 4,
+                       hipMemcpyHostToDevice, st);
+  if (e != hipSuccess) return fail(e, "prefill inputs");
+  e = upload_page_entries(s, txns, st);
+  if (e != hipSuccess) return fail(e, "page table");
+  const RowPtrs rp{s->pf_dev, s->pf_dev + C, s->pf_dev + 2 * C, s->pf_dev + 3 * C};
+  e = enqueue_layers(s, (int)n, rp, st);
+  if (e != hipSuccess) return fail(e, "prefill layers");
+  if (head) {
+    e = enqueue_head(s, 1, s->x_res + (size_t)(n - 1) * c.dim, false, st);
+    if (e != hipSuccess) return fail(e, "prefill head");
+    e = hipMemcpyAsync(s->res_host, s->arg_result, sizeof(gk::ArgmaxResult),
+                       hipMemcpyDeviceToHost, st);
+    if (e != hipSuccess) return fail(e, "result copy");
+    if (logits_host) {
+      e = hipMemcpyAsync(logits_host, s->logits, (size_t)c.vocab_size * 4, hipMemcpyDeviceToHost,
+                         st);
+      if (e != hipSuccess) return fail(e, "logits copy");
+    }
+  }
+  e = hipStreamSynchronize(st);
+  if (e != hipSuccess) return fail(e, "prefill sync");
+  if (s->inject_failure) {
+    abort_rows(s, txns);
+    return GLACIER_HIP_DEVICE_ERROR;
+  }
+  if (head && s->res_host[0].status != 0) {
+    const int st_code = s->res_host[0].status;
+    abort_rows(s, txns);
+    return st_code;
+  }
+  return GLACIER_HIP_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -654,6 +808,7 @@ glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
   }
   const auto &c = m->cfg;
   if (opts->max_lanes == 0 || opts->max_lanes > 32 || opts->max_positions == 0 ||
+      opts->prefill_chunk < 0 || opts->prefill_chunk > 8192 ||
       (opts->kv_dtype != GLACIER_HIP_F32 && opts->kv_dtype != GLACIER_HIP_F16)) {
     ctx->last_error = "session options invalid";
     return nullptr;
@@ -665,21 +820,25 @@ glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
   s->total_pages = opts->total_pages ? opts->total_pages : opts->max_lanes * s->max_pages;
   s->lanes.resize(opts->max_lanes);
   for (uint32_t p = s->total_pages; p-- > 0;) s->free_pages.push_back((int32_t)p);
-  const uint32_t M = opts->max_lanes;
+  s->prefill_chunk = opts->prefill_chunk ? (uint32_t)opts->prefill_chunk
+                                         : std::min<uint32_t>(opts->max_positions, 2048);
+  s->rows_cap = std::max(opts->max_lanes, s->prefill_chunk);
+  const uint32_t L = opts->max_lanes;  // lanes: page tables, logits, masks
+  const uint32_t M = s->rows_cap;      // activation rows: decode lanes or a prompt chunk
   const size_t kvd = (size_t)c.num_kv_heads * c.head_dim;
   const size_t elem = opts->kv_dtype == GLACIER_HIP_F16 ? 2 : 4;
   const size_t page_bytes = (size_t)c.num_layers * 2 * 16 * kvd * elem;
   const size_t Kmax = std::max(c.dim, c.hidden_dim);
   const size_t Gmax = Kmax / 32;
   const size_t W = (c.vocab_size + 63) / 64;
-  const size_t att = gk::attention_scratch_floats((int)M, (int)c.num_heads, (int)c.head_dim,
-                                                  (int)opts->max_positions);
+  const size_t att = gk::attention_scratch_floats((int)M, (int)c.num_heads, (int)c.num_kv_heads,
+                                                  (int)c.head_dim, (int)opts->max_positions);
   bool ok = true;
   auto A = [&](void **p, size_t bytes) {
     if (ok && hipMalloc(p, bytes) != hipSuccess) ok = false;
   };
   A(&s->kv_pool, page_bytes * s->total_pages);
-  A((void **)&s->page_table, (size_t)M * s->max_pages * 4);
+  A((void **)&s->page_table, (size_t)L * s->max_pages * 4);
   A((void **)&s->rope_cos, (size_t)opts->max_positions * c.head_dim / 2 * 4);
   A((void **)&s->rope_sin, (size_t)opts->max_positions * c.head_dim / 2 * 4);
   A((void **)&s->x_res, (size_t)M * c.dim * 4);
@@ -687,22 +846,29 @@ glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
   A((void **)&s->q, (size_t)M * c.dim * 4);
   A((void **)&s->attn, (size_t)M * c.dim * 4);
   A((void **)&s->act, (size_t)M * c.hidden_dim * 4);
-  A((void **)&s->logits, (size_t)M * c.vocab_size * 4);
+  A((void **)&s->logits, (size_t)L * c.vocab_size * 4);
   A((void **)&s->act_q, Gmax * 3 * M * 32);
   A((void **)&s->act_meta, Gmax * M * sizeof(gk::ActMeta));
   A((void **)&s->att_scratch, std::max<size_t>(att, 1) * 4);
-  A(&s->arg_scratch, gk::argmax_scratch_bytes((int)M, (long)c.vocab_size));
-  A((void **)&s->arg_counters, (size_t)M * 4);
-  A((void **)&s->arg_result, (size_t)M * sizeof(gk::ArgmaxResult));
-  A((void **)&s->elig_words, (size_t)M * W * 8);
+  A(&s->arg_scratch, gk::argmax_scratch_bytes((int)L, (long)c.vocab_size));
+  A((void **)&s->arg_counters, (size_t)L * 4);
+  A((void **)&s->arg_result, (size_t)L * sizeof(gk::ArgmaxResult));
+  A((void **)&s->elig_words, (size_t)L * W * 8);
   A((void **)&s->step_dev, sizeof(StepInputs));
-  if (ok && hipHostMalloc((void **)&s->step_host, sizeof(StepInputs)) != hipSuccess) ok = false;
-  if (ok && hipHostMalloc((void **)&s->res_host, M * sizeof(gk::ArgmaxResult)) != hipSuccess) ok = false;
+  A((void **)&s->pf_dev, (size_t)4 * s->prefill_chunk * 4);
+  auto H = [&](void **p, size_t bytes) {
+    if (ok && hipHostMalloc(p, bytes) != hipSuccess) ok = false;
+  };
+  H((void **)&s->step_host, sizeof(StepInputs));
+  H((void **)&s->pf_host, (size_t)4 * s->prefill_chunk * 4);
+  H((void **)&s->pt_host, (size_t)L * s->max_pages * 4);
+  H((void **)&s->res_host, L * sizeof(gk::ArgmaxResult));
   if (ok) {
-    ok = hipMemset(s->arg_counters, 0, (size_t)M * 4) == hipSuccess &&
+    ok = hipMemset(s->arg_counters, 0, (size_t)L * 4) == hipSuccess &&
          hipMemset(s->kv_pool, 0, page_bytes * s->total_pages) == hipSuccess;
-    std::vector<int32_t> pt((size_t)M * s->max_pages, 0);
-    ok = ok && hipMemcpy(s->page_table, pt.data(), pt.size() * 4, hipMemcpyHostToDevice) == hipSuccess;
+    memset(s->pt_host, 0, (size_t)L * s->max_pages * 4);
+    ok = ok && hipMemcpy(s->page_table, s->pt_host, (size_t)L * s->max_pages * 4,
+                         hipMemcpyHostToDevice) == hipSuccess;
     // RopeTable.init (generate.zig:790-806), f32 libm on the host
     const size_t half = c.head_dim / 2;
     std::vector<float> cs(opts->max_positions * half), sn(opts->max_positions * half);
@@ -757,11 +923,14 @@ int glacier_hip_session_prefill(glacier_hip_session *s, uint32_t lane, const uin
   if (ln.len + n > s->opt.max_positions) return GLACIER_HIP_CACHE_FULL;
   std::lock_guard<std::mutex> lk(s->model->ctx->mu);
   std::vector<RowTxn> txns;
-  for (uint32_t i = 0; i < n; ++i) {
-    const bool last = i + 1 == n;
-    int rc = run_step(s, &lane, &tokens[i], 1, last, nullptr, last ? logits_host : nullptr, txns);
-    if (rc) return rc;  // rows of earlier prompt tokens stay committed (cache.commit per token)
+  for (uint32_t done = 0; done < n;) {
+    const uint32_t rows = std::min(n - done, s->prefill_chunk);
+    const bool last = done + rows == n;
+    int rc = run_prefill_chunk(s, lane, tokens + done, rows, last, last ? logits_host : nullptr,
+                               txns);
+    if (rc) return rc;  // rows of earlier chunks stay committed (cache.commit per token)
     commit_rows(s, txns);
+    done += rows;
   }
   *first_token = (uint32_t)s->res_host[0].index;
   ln.sampling_calls += 1;

@@ -191,10 +191,14 @@ int glacier_hip_int4_matvec_dispatch(glacier_hip_context *ctx, glacier_hip_int4_
                                      const float *input, uint64_t input_count,
                                      float *output, uint64_t output_count);
 
-/* Device-resident batched GEMV: y[m][out_f] = x[m][in_f] W^T (+ bias[out_f]),
- * m in 1..32. x is f32 or bf16 (x_dtype), y is f32. Replaces
- * linearInt4WeightQ8 / linearInt4Weight (int4_matmul.zig:422-531, 2957-2981)
- * for one projection. Asynchronous on `stream`. */
+/* Device-resident batched projection: y[m][out_f] = x[m][in_f] W^T
+ * (+ bias[out_f]), m in 1..GLACIER_HIP_MAX_ROWS. x is f32 or bf16 (x_dtype),
+ * y is f32. Replaces linearInt4WeightQ8 / linearInt4Weight
+ * (int4_matmul.zig:422-531, 2957-2981) for one projection over m rows: up to
+ * 32 rows run the decode GEMV, more rows (prompt chunks, the packed batch of
+ * forwardLayerPackedBatch, generate.zig:2105) the MFMA GEMM; both compute
+ * every row with the same per-group arithmetic. Asynchronous on `stream`. */
+#define GLACIER_HIP_MAX_ROWS 65536u
 int glacier_hip_int4_gemv(glacier_hip_context *ctx, glacier_hip_int4_weight *weight,
                           const void *x_dev, int x_dtype, uint32_t m,
                           const float *bias_dev, float *y_dev, int activation,
@@ -301,7 +305,8 @@ typedef struct {
     int32_t layer_activation;    /* GLACIER_HIP_ACT_*; AUTO = reference x86 dispatch */
     int32_t head_activation;     /* usually AUTO (=> F32 for V > 65536) */
     int32_t use_graph;           /* capture the decode step in a hipGraph */
-    int32_t reserved;
+    int32_t prefill_chunk;       /* prompt rows per prefill launch sequence;
+                                  * 0 = min(max_positions, 2048) */
 } glacier_hip_session_options_t;
 
 typedef struct {
@@ -326,7 +331,13 @@ void glacier_hip_session_destroy(glacier_hip_session *s);
 /* Start a request on `lane` (resets its cache and counters). */
 int glacier_hip_session_lane_begin(glacier_hip_session *s, uint32_t lane, uint64_t seed);
 /* Prefill: run `n` prompt tokens on `lane` and produce the first greedy
- * token (generate.zig:5080-5160). logits_host: optional [vocab]. */
+ * token (generate.zig:5080-5160). logits_host: optional [vocab]. The prompt
+ * runs in chunks of up to prefill_chunk rows: every projection of a chunk is
+ * one MFMA GEMM over its rows, attention is causal per row over the lane's
+ * pages, and only the last prompt row goes through the LM head. Each row is
+ * computed as the reference's token-at-a-time prefill computes it; a chunk's
+ * KV rows commit together once the chunk has run, and rows of earlier chunks
+ * stay committed if a later chunk fails (the reference commits per token). */
 int glacier_hip_session_prefill(glacier_hip_session *s, uint32_t lane, const uint32_t *tokens,
                                 uint32_t n, uint32_t *first_token, float *logits_host);
 /* One decode step for `count` lanes: lanes[i] consumes tokens[i] at its next
