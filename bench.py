@@ -11,6 +11,10 @@ KV already resident in HBM. The same JSON line carries:
   * gemv        the INT4 GEMV kernel timed alone on the BASELINE config-2
                 shapes and on the 7B gate/up projection, with HIP events on
                 the launch stream;
+  * prefill     config 4: 7B time to first token at T = 512 and 2048 and the
+                int8 MFMA rate it implies;
+  * attention   config 3: paged GQA decode attention alone, 4 lanes at
+                contexts 512..8192, GB/s;
   * roofline    for the dominant kernel (the fused 7B gate/up GEMV, 53% of a
                 token's weight bytes): algorithmic bytes / average duration;
   * cpu_baseline the CPU oracle (the reference algorithm restated in C) on the
@@ -29,6 +33,7 @@ sys.path[:0] = [ROOT, os.path.join(ROOT, "glacier-engine_amd")]
 import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_OPS = 5.0e15   # MI355X dense int8 MFMA
 SEED = 0x474C4143
 CFG_7B = dict(num_layers=28, dim=3584, hidden_dim=18944, num_heads=28, num_kv_heads=4,
               head_dim=128, vocab_size=152064, group_size=32, rms_eps=1e-6, rope_theta=1e6)
@@ -136,6 +141,104 @@ def decode_lanes(gh, sess, lanes, prompts, warmup, steps):
     return lanes * steps / dt, dt
 
 
+def layer_params(cfg):
+    d, f, kvd = cfg["dim"], cfg["hidden_dim"], cfg["num_kv_heads"] * cfg["head_dim"]
+    qkv, o, gu, down = d * (d + 2 * kvd), d * d, 2 * f * d, d * f
+    return qkv, o, gu, down
+
+
+def bench_prefill(gh, model, lengths, reps=3):
+    """time to first token of a fresh lane for prompts of T
+    uniform random ids (wall clock around the synchronous prefill call: all
+    28 layers over the prompt in one 2048-row chunk, then the last row's LM
+    head and argmax). MFMA figures: the algorithmic contraction is
+    2 * T * (layer weights) int8 multiply-adds (plus one head row); the
+    executed count triples the down projection, whose 18944-wide input runs
+    as three 7-bit digit planes (the reference's f32-activation path for
+    in_f > 16384)."""
+    cfg = model.cfg
+    qkv, o, gu, down = layer_params(cfg)
+    L = cfg["num_layers"]
+    out = []
+    for T in lengths:
+        sess = gh.Session(model, max_lanes=1, max_positions=T + 8, kv_dtype=gh.F16,
+                          prefill_chunk=min(T, 2048))
+        try:
+            prompt = gh.synth_tokens(SEED, 0x50524546 + T, cfg["vocab_size"], T)
+            times = []
+            for r in range(reps + 1):
+                sess.begin(0, seed=r)
+                t0 = time.perf_counter()
+                sess.prefill(0, prompt)
+                times.append(time.perf_counter() - t0)
+            ttft = float(np.median(times[1:]))
+            algo = 2.0 * T * L * (qkv + o + gu + down) + 2.0 * cfg["dim"] * cfg["vocab_size"]
+            execd = 2.0 * T * L * (qkv + o + gu + 3 * down) + 2.0 * cfg["dim"] * cfg["vocab_size"]
+            out.append(dict(T=T, ttft_ms=round(ttft * 1e3, 2), tokens_per_s=round(T / ttft, 1),
+                            int8_mfma_algorithmic_tops=round(algo / ttft / 1e12, 1),
+                            int8_mfma_executed_tops=round(execd / ttft / 1e12, 1),
+                            mfma_frac_of_5000_tops=round(execd / ttft / INT8_PEAK_OPS, 4)))
+            log("prefill", out[-1])
+        finally:
+            sess.close()
+    return out
+
+
+def bench_attention(gh, ctx, torch, reps=20):
+    """paged GQA decode attention alone at Qwen2.5-7B head
+    geometry (28 q / 4 kv heads, hd 128), fp16 KV in 16-position pages of a
+    28-layer payload, pages scattered by a seeded permutation, 4 lanes at
+    contexts 512 / 2048 / 4096 / 8192. HIP events on the launch stream around
+    a captured graph of `reps` launches. Algorithmic bytes: K and V of every
+    attended position (2 * ctx * 4 * 128 * 2 B per lane) + q/out rows + page
+    table entries."""
+    L = gh.lib()
+    Hq, Hkv, hd, layers, layer = 28, 4, 128, 28, 27
+    ctxs = [512, 2048, 4096, 8192]
+    pages = [c // 16 for c in ctxs]
+    total = sum(pages)
+    g = torch.Generator().manual_seed(SEED)
+    perm = torch.randperm(total, generator=g).to(torch.int32)
+    pt = torch.zeros((len(ctxs), max(pages)), dtype=torch.int32)
+    off = 0
+    for i, p in enumerate(pages):
+        pt[i, :p] = perm[off:off + p]
+        off += p
+    pool = torch.randn((total, layers, 2, 16, Hkv * hd), dtype=torch.float16, device="cuda")
+    q = torch.randn((len(ctxs), Hq * hd), dtype=torch.float32, device="cuda")
+    out = torch.empty_like(q)
+    ptd = pt.cuda()
+    cl = torch.tensor(ctxs, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.Stream()
+
+    def go():
+        gh.check(L.glacier_hip_paged_attention(ctx.h, q.data_ptr(), pool.data_ptr(), gh.F16,
+                                               ptd.data_ptr(), pt.shape[1], cl.data_ptr(), len(ctxs),
+                                               layer, layers, Hq, Hkv, hd, max(ctxs),
+                                               out.data_ptr(), stream.cuda_stream), "attention")
+    go()
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr, stream=stream):
+        for _ in range(reps):
+            go()
+    with torch.cuda.stream(stream):
+        gr.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(5):
+            gr.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / (reps * 5)
+    b = sum(2 * c * Hkv * hd * 2 for c in ctxs) + len(ctxs) * Hq * hd * 4 * 2 + sum(pages) * 4
+    res = dict(contexts=ctxs, us=round(us, 2), bytes=b, gbs=round(b / us / 1e3, 1),
+               frac=round(b / us / 1e3 / HBM_PEAK_GBS, 4), kv="fp16, 28-layer pages")
+    log("attention", res)
+    del gr, pool
+    return res
+
+
 def cpu_baseline(host, prompt_tok, budget_s=15.0):
     import oracle
 
@@ -166,8 +269,19 @@ def main():
     ap.add_argument("--lane-prompt", type=int, default=64)
     ap.add_argument("--gemv-reps", type=int, default=50)
     ap.add_argument("--gemv-only", action="store_true", help="only the GEMV kernel timing")
+    ap.add_argument("--sections", default="gemv,decode,lanes,prefill,attention,cpu",
+                    help="comma list of gemv, decode, lanes, prefill, attention, cpu "
+                         "(profiling runs select one; the JSON line needs decode)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-attention", action="store_true")
     a = ap.parse_args()
+    secs = set(a.sections.split(","))
+    if "lanes" not in secs:
+        a.lanes = 1
+    a.no_prefill = a.no_prefill or "prefill" not in secs
+    a.no_attention = a.no_attention or "attention" not in secs
+    a.no_cpu_baseline = a.no_cpu_baseline or "cpu" not in secs
     if a.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {a.gpus}); this build has no "
               "multi-GPU path: lanes would shard across GPUs with no exchange.", file=sys.stderr)
@@ -184,16 +298,18 @@ def main():
     # ---- GEMV kernel alone ----
     gemv = []
     n, k = GATE_UP
-    dom = time_gemv(gh, ctx, torch, n, k, 1, a.gemv_reps * 2, gh.ACT_Q8)
-    log("gemv gate/up", dom)
-    if not a.gemv_only:
+    dom = None
+    if "gemv" in secs or a.gemv_only:
+        dom = time_gemv(gh, ctx, torch, n, k, 1, a.gemv_reps * 2, gh.ACT_Q8)
+        log("gemv gate/up", dom)
+    if not a.gemv_only and "gemv" in secs:
         for (n, k) in GEMV_SHAPES:
             for m in (1, 8):
                 r = time_gemv(gh, ctx, torch, n, k, m, a.gemv_reps, auto_act(gh, n, k))
                 log("gemv", r)
                 gemv.append(r)
     roofline = dict(bound="hbm", achieved=dom["gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=dom["frac"], traffic=None)
+                    frac=dom["frac"], traffic=None) if dom else None
     if a.gemv_only:
         print(json.dumps(dict(metric="int4 gemv HBM GB/s (7B gate/up, M=1)", value=dom["gbs"],
                               unit="GB/s", roofline=roofline, gemv=[dom])))
@@ -209,8 +325,10 @@ def main():
     max_pos = max(a.prompt, a.lane_prompt) + a.warmup + a.steps + 8
     sess = gh.Session(model, max_lanes=max(1, a.lanes), max_positions=max_pos, kv_dtype=gh.F16)
     sess.begin(0, seed=1)
-    tps1, dt1 = decode_batch1(gh, sess, prompt, a.warmup, a.steps)
-    log(f"batch-1 decode {tps1:.1f} tok/s ({dt1 * 1e3 / a.steps:.3f} ms/token)")
+    tps1, dt1 = 0.0, 0.0
+    if "decode" in secs:
+        tps1, dt1 = decode_batch1(gh, sess, prompt, a.warmup, a.steps)
+        log(f"batch-1 decode {tps1:.1f} tok/s ({dt1 * 1e3 / a.steps:.3f} ms/token)")
     lanes = None
     if a.lanes > 1:
         prompts = [gh.synth_tokens(SEED, 0x4C414E45 + i, CFG_7B["vocab_size"], a.lane_prompt)
@@ -221,19 +339,22 @@ def main():
                      context_range=[a.lane_prompt, a.lane_prompt + a.warmup + a.steps])
         log(f"{a.lanes}-lane decode {tpsL:.1f} tok/s")
     sess.close()
+    prefill = bench_prefill(gh, model, [512, 2048]) if not a.no_prefill else None
     model.close()
+    attn = bench_attention(gh, ctx, torch) if not a.no_attention else None
     cpu = None if a.no_cpu_baseline else cpu_baseline(host, int(prompt[0]))
     if cpu:
         log("cpu baseline", cpu)
     out = dict(
         metric="decode tok/s at batch 1 (7B INT4)", value=round(tps1, 2), unit="tokens/s",
-        n_gpus=1, steps=a.steps, warmup=a.warmup, ms_per_step=round(dt1 * 1e3 / a.steps, 4),
+        n_gpus=1, steps=a.steps, warmup=a.warmup, ms_per_step=round(dt1 * 1e3 / max(a.steps, 1), 4),
         higher_is_better=True, scaling="weak", vs_baseline=None, dtype="int8xint4 (Q8) / f32",
         data="synthetic random-init weights (seed 0x474C4143), uniform random prompt ids",
         config=dict(workload="Qwen2.5-7B-shaped INT4 g32 greedy decode, batch 1",
                     prompt_len=a.prompt, kv="fp16 paged, 16 positions/page",
                     parallelism="single GPU"),
-        roofline=roofline, cpu_baseline=cpu, lanes32=lanes, gemv=[dom] + gemv)
+        roofline=roofline, cpu_baseline=cpu, lanes32=lanes, prefill=prefill, attention=attn,
+        gemv=([dom] if dom else []) + gemv)
     print(json.dumps(out))
 
 

@@ -63,8 +63,21 @@ struct GemvArgs {
   int ksplit_override;      // force the K split (tuning); 0 = heuristic
   int rb_override;          // row blocks per workgroup with ksplit_override
   int ksplit;               // set by launch_gemv
+  int ksplit_lds_off;       // set by launch_gemv: LDS offset of the SwiGLU plane buffer
   int force_mfma;           // use the MFMA path even for M <= 2 (tuning / tests)
   QkvArgs qkv;
+  // Fused input stage: with x_in set, every workgroup builds the activation
+  // planes of x_in [M][K] (f32) in LDS itself, RMS-normalised with norm_w
+  // first when norm_w is set (act_q / act_meta are then unused).
+  const float *x_in;
+  const float *norm_w;
+  float eps;
+  // EPI_SWIGLU only: also (or instead, with y == null) emit the SwiGLU output
+  // as digit planes [G][out_D][M][32] + meta [G][M] of width N/2, ready as
+  // the next projection's input.
+  int8_t *out_q;
+  ActMeta *out_meta;
+  int out_D;
 };
 
 // Launch shape of one GEMV: RB row blocks per workgroup, KS waves per row
@@ -76,6 +89,9 @@ struct GemvShape {
   size_t lds_bytes;
 };
 GemvShape plan_gemv(int N, int K, int M, int D);
+// Whether launch_gemv can build the planes of an M x K input in LDS (fused
+// input stage) for this projection.
+bool gemv_fused_input_ok(int N, int K, int M, int D);
 
 // Prepare activation planes from x [M][K] (f32 or bf16), optionally
 // RMS-normalised with weight `norm_w` first (kernels.zig:141-220).

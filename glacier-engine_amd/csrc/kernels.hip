@@ -184,26 +184,46 @@ static size_t planes_bytes(int groups, int M, int D) {
 GemvShape plan_gemv(int N, int K, int M, int D) {
   GemvShape p;
   const int NB = N / 16, KQ = K / 128;
-  const bool mfma = M > 2;
-  const int max_ks = std::max(1, std::min(16, KQ / 2));
-  int ks = 1;
-  while (ks * 2 <= max_ks && (KQ + ks - 1) / ks > 16) ks *= 2;
-  while (ks * 2 <= max_ks && NB * ks * 2 < 4096 && KQ >= 4 * ks) ks *= 2;
-  const int rb = std::min(4, std::max(1, (D == 3 ? 8 : 4) / ks));
+  int ks, rb;
+  if (M <= 2) {
+    // From cold-cache sweeps of the 7B decode shapes: about 4096 waves or
+    // more keep HBM busy (split K until there, keeping >= 4 quads per wave),
+    // workgroups of about 8 waves, 4 quads in flight per wave.
+    ks = std::max(1, std::min(std::min(16, std::max(1, KQ / 4)), (4096 + NB - 1) / NB));
+    rb = std::max(1, std::min(8, 8 / ks));
+    p.unroll = 4;
+  } else {
+    const int max_ks = std::max(1, std::min(16, KQ / 2));
+    ks = 1;
+    while (ks * 2 <= max_ks && (KQ + ks - 1) / ks > 16) ks *= 2;
+    while (ks * 2 <= max_ks && NB * ks * 2 < 4096 && KQ >= 4 * ks) ks *= 2;
+    rb = std::min(4, std::max(1, (D == 3 ? 8 : 4) / ks));
+    p.unroll = (ks * rb <= 4 && (long)NB * ks <= 3072) ? 8 : 4;
+  }
   p.ksplit = ks;
   p.rb = rb;
   p.waves = ks * rb;
-  const long total = (long)NB * ks;
-  if (mfma)
-    p.unroll = (p.waves <= 4 && total <= 3072) ? 8 : 4;
-  else
-    p.unroll = (total > 4096 && total <= 6144) ? 4 : 8;
   const size_t red = (size_t)p.waves * ((M + 15) / 16) * 4 * 64 * sizeof(float);
-  const size_t planes = planes_bytes(K / 32, M, D);
+  const size_t planes = planes_bytes(K / 32, M, D) + (size_t)M * sizeof(float);
   p.lds_a = planes <= kLdsLimit;
   p.lds_bytes = std::max(p.lds_a ? planes : 0, red);
   p.grid = (NB + rb - 1) / rb;
   return p;
+}
+
+// LDS of the fused input stage: planes, inverse RMS per row, per-wave
+// partial sums (up to 16 waves) and the staged input rows.
+static __host__ __device__ __forceinline__ size_t fused_rows_offset(int groups, int M, int D) {
+  const size_t planes = (size_t)groups * ((size_t)D * M * 32 + (size_t)M * 8);
+  return (planes + (size_t)M * 4 + (size_t)M * 16 * 4 + 15) & ~(size_t)15;
+}
+static size_t fused_stage_bytes(int K, int M, int D) {
+  return fused_rows_offset(K / 32, M, D) + (size_t)M * K * 4;
+}
+
+bool gemv_fused_input_ok(int N, int K, int M, int D) {
+  (void)N;
+  return M <= 4 && fused_stage_bytes(K, M, D) <= kLdsLimit;
 }
 
 template <int D, int MT, int U, bool LDS_A, bool DOT4, int LB>
@@ -246,12 +266,53 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
   const size_t qbytes = (size_t)G * D * M * 32;
   const size_t mbytes = (size_t)G * M * sizeof(ActMeta);
   if (LDS_A) {
-    const uint4 *src = (const uint4 *)a.act_q;
-    uint4 *dst = (uint4 *)smem;
-    for (size_t i = threadIdx.x; i < qbytes / 16; i += blockDim.x) dst[i] = src[i];
-    const uint2 *msrc = (const uint2 *)a.act_meta;
-    uint2 *mdst = (uint2 *)(smem + qbytes);
-    for (size_t i = threadIdx.x; i < mbytes / 8; i += blockDim.x) mdst[i] = msrc[i];
+    if (a.x_in) {
+      // Fused input stage: RMSNorm (kernels.zig:141-220) and the group
+      // quantiser (int4_matmul.zig:380-398) of the whole input into LDS. The
+      // rows are first copied into LDS with one wide load per thread, so the
+      // reduction and the quantiser never wait on HBM/L2 round trips.
+      const int nthr = blockDim.x, nw = nthr >> 6;
+      float *inv = (float *)(smem + qbytes + mbytes);
+      float *ssw = inv + M;                       // [M][nw] per-wave partial sums
+      float *xs = (float *)(smem + fused_rows_offset(G, M, D));  // [M][K] the input rows
+      const float4 *src4 = (const float4 *)a.x_in;
+      float4 *xs4 = (float4 *)xs;
+      for (int i = threadIdx.x; i < M * (a.K >> 2); i += nthr) xs4[i] = src4[i];
+      __syncthreads();
+      if (a.norm_w) {
+        for (int m = 0; m < M; ++m) {
+          float ss = 0.0f;
+          for (int i = threadIdx.x; i < a.K; i += nthr) ss = fmaf(xs[m * a.K + i], xs[m * a.K + i], ss);
+          for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+          if (lane == 0) ssw[m * nw + wave] = ss;
+        }
+        __syncthreads();
+        if (threadIdx.x < M) {
+          float tot = 0.0f;
+          for (int w = 0; w < nw; ++w) tot += ssw[threadIdx.x * nw + w];
+          inv[threadIdx.x] = 1.0f / sqrtf(tot / (float)a.K + a.eps);
+        }
+        __syncthreads();
+      }
+      const int half = threadIdx.x >> 5, hl = threadIdx.x & 31, nh = nthr >> 5;
+      for (int gi = half; gi < G * M; gi += nh) {
+        const int m = gi % M, g = gi / M;
+        const int k = (g << 5) + hl;
+        float v = xs[m * a.K + k];
+        if (a.norm_w) {
+          const float tt = v * inv[m];
+          v = tt * a.norm_w[k];
+        }
+        quantize_group<D>(v, hl, g, m, M, (int8_t *)smem, (ActMeta *)(smem + qbytes));
+      }
+    } else {
+      const uint4 *src = (const uint4 *)a.act_q;
+      uint4 *dst = (uint4 *)smem;
+      for (size_t i = threadIdx.x; i < qbytes / 16; i += blockDim.x) dst[i] = src[i];
+      const uint2 *msrc = (const uint2 *)a.act_meta;
+      uint2 *mdst = (uint2 *)(smem + qbytes);
+      for (size_t i = threadIdx.x; i < mbytes / 8; i += blockDim.x) mdst[i] = msrc[i];
+    }
     __syncthreads();
   }
   const int8_t *aq = LDS_A ? (const int8_t *)smem : a.act_q;
@@ -368,6 +429,9 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
   }
 
   // ---- split-K reduction through LDS, fixed order over ks ----
+  // (no early return: the SwiGLU plane epilogue below synchronises the
+  // whole workgroup again)
+  const bool lead = ks == 0 && nb < NB;
   if (KS > 1) {
     if (LDS_A) __syncthreads();  // the planes region is reused below
     float *red = (float *)smem;
@@ -376,20 +440,26 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) red[((wave * MT + mt) * 4 + r) * 64 + lane] = acc[mt][r];
     __syncthreads();
-    if (ks != 0) return;
+    if (ks == 0) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float tot = acc[mt][r];
-        for (int s2 = 1; s2 < KS; ++s2) tot += red[(((wave + s2) * MT + mt) * 4 + r) * 64 + lane];
-        acc[mt][r] = tot;
-      }
+        for (int r = 0; r < 4; ++r) {
+          float tot = acc[mt][r];
+          for (int s2 = 1; s2 < KS; ++s2) tot += red[(((wave + s2) * MT + mt) * 4 + r) * 64 + lane];
+          acc[mt][r] = tot;
+        }
+    }
   }
-  if (nb >= NB) return;
 
   // ---- fused epilogues: lane (c, n) owns rows m = 16 mt + 4 c + r of column n ----
   const bool paired = a.epi == EPI_SWIGLU || a.epi == EPI_QKV;
+  const bool emit_planes = a.epi == EPI_SWIGLU && a.out_q;
+  // SwiGLU outputs of this workgroup's rb row blocks: [M][8 * rb] floats
+  // after the reduction area
+  const int RB = (int)(blockDim.x >> 6) / KS;
+  float *actbuf = (float *)(smem + a.ksplit_lds_off);
+  const int nb_wg0 = blockIdx.x * RB;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -398,15 +468,60 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
       const float tot = acc[mt][r];
       // partner row (n_local ^ 8) lives in lane ^ 8 with the same (c, r)
       const float partner = paired ? __shfl_xor(tot, 8) : 0.0f;
-      if (m < M) store_output(a, nb, n_local, m, tot, partner);
+      if (!lead || m >= M) continue;
+      if (emit_planes) {
+        if (n_local < 8) {
+          const float v = silu_mul(tot, partner);
+          actbuf[m * (8 * RB) + (nb - nb_wg0) * 8 + n_local] = v;
+          if (a.y) a.y[(size_t)m * (a.N / 2) + nb * 8 + n_local] = v;
+        }
+      } else {
+        store_output(a, nb, n_local, m, tot, partner);
+      }
     }
+  if (!emit_planes) return;
+  __syncthreads();
+  // Groups of 32 consecutive SwiGLU outputs = 4 row blocks; each half-wave
+  // quantises one (group, row) into the next projection's planes.
+  const int half = threadIdx.x >> 5, hl = threadIdx.x & 31, nh = blockDim.x >> 5;
+  const int groups = RB / 4;
+  const int Gout = a.N / 64;
+  for (int gi = half; gi < groups * M; gi += nh) {
+    const int m = gi % M, gl = gi / M;
+    const int g = nb_wg0 / 4 + gl;
+    if (g >= Gout) continue;
+    const float v = actbuf[m * (8 * RB) + gl * 32 + hl];
+    if (a.out_D == 1)
+      quantize_group<1>(v, hl, g, m, M, a.out_q, a.out_meta);
+    else
+      quantize_group<3>(v, hl, g, m, M, a.out_q, a.out_meta);
+  }
 }
 
 hipError_t launch_gemv(const GemvArgs &a0, hipStream_t st) {
   GemvArgs a = a0;
   const int MT = (a.M + 15) / 16;
-  if (MT > 2 || a.N % 16 || a.K % 128 || !a.act_q || !a.act_meta) return hipErrorInvalidValue;
+  if (MT > 2 || a.N % 16 || a.K % 128 || (!a.x_in && (!a.act_q || !a.act_meta)))
+    return hipErrorInvalidValue;
+  const bool emit_planes = a.epi == EPI_SWIGLU && a.out_q;
+  if (emit_planes && ((a.N / 16) % 4 || !a.out_meta || (a.out_D != 1 && a.out_D != 3)))
+    return hipErrorInvalidValue;
   GemvShape p = plan_gemv(a.N, a.K, a.M, a.D);
+  if (a.x_in) {
+    if (!gemv_fused_input_ok(a.N, a.K, a.M, a.D)) return hipErrorInvalidValue;
+    p.lds_a = true;
+    p.lds_bytes = std::max(p.lds_bytes, fused_stage_bytes(a.K, a.M, a.D));
+  }
+  if (emit_planes && p.rb % 4) {
+    // the workgroup must own whole 32-wide output groups (4 row blocks)
+    p.rb = 4;
+    while (p.ksplit * p.rb > 16) p.ksplit /= 2;
+    p.waves = p.ksplit * p.rb;
+    p.grid = (a.N / 16 + p.rb - 1) / p.rb;
+    const size_t red = (size_t)p.waves * MT * 4 * 64 * sizeof(float);
+    p.lds_bytes = std::max(p.lds_a ? planes_bytes(a.K / 32, a.M, a.D) + a.M * 4 : 0, red);
+    if (a.x_in) p.lds_bytes = std::max(p.lds_bytes, fused_stage_bytes(a.K, a.M, a.D));
+  }
   if (a.ksplit_override > 0) {
     p.ksplit = a.ksplit_override;
     p.rb = a.rb_override > 0 ? a.rb_override : std::max(1, 4 / p.ksplit);
@@ -414,9 +529,13 @@ hipError_t launch_gemv(const GemvArgs &a0, hipStream_t st) {
     if (p.waves > 16 || p.ksplit > a.K / 128) return hipErrorInvalidValue;
     p.grid = (a.N / 16 + p.rb - 1) / p.rb;
     const size_t red = (size_t)p.waves * MT * 4 * 64 * sizeof(float);
-    p.lds_bytes = std::max(p.lds_a ? planes_bytes(a.K / 32, a.M, a.D) : 0, red);
+    p.lds_bytes = std::max(p.lds_a ? planes_bytes(a.K / 32, a.M, a.D) + a.M * 4 : 0, red);
+    if (a.x_in) p.lds_bytes = std::max(p.lds_bytes, fused_stage_bytes(a.K, a.M, a.D));
+    if (emit_planes && p.rb % 4) return hipErrorInvalidValue;
   }
   a.ksplit = p.ksplit;
+  a.ksplit_lds_off = (int)((p.lds_bytes + 15) & ~(size_t)15);
+  if (emit_planes) p.lds_bytes = a.ksplit_lds_off + (size_t)a.M * 8 * p.rb * sizeof(float);
   dim3 grid(p.grid), block(64 * p.waves);
   const bool dot4 = a.M <= 2 && !a.force_mfma;
   const bool small = p.waves <= 4;

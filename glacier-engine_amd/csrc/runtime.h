@@ -32,6 +32,7 @@ struct glacier_hip_context {
   uint32_t *counters = nullptr;  // zeroed once, self-resetting
   size_t counter_count = 0;
   gk::ArgmaxResult *results_host = nullptr;  // pinned
+  int32_t *ident = nullptr;  // device 0..63: row i -> page-table row i
 };
 
 struct glacier_hip_int4_weight {

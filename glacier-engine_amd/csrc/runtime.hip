@@ -139,6 +139,13 @@ glacier_hip_context *glacier_hip_init(int device_ordinal) {
     what = "hipHostMalloc";
     e = hipHostMalloc((void **)&ctx->results_host, sizeof(gk::ArgmaxResult) * 64);
   }
+  if (e == hipSuccess) {
+    what = "identity rows";
+    int32_t h[64];
+    for (int i = 0; i < 64; ++i) h[i] = i;
+    e = hipMalloc((void **)&ctx->ident, sizeof h);
+    if (e == hipSuccess) e = hipMemcpy(ctx->ident, h, sizeof h, hipMemcpyHostToDevice);
+  }
   if (e != hipSuccess) {
     g_init_error = std::string(what) + ": " + hipGetErrorString(e);
     delete ctx;
@@ -157,6 +164,7 @@ int glacier_hip_deinit(glacier_hip_context *ctx) {
   if (ctx->planes) (void)hipFree(ctx->planes);
   if (ctx->counters) (void)hipFree(ctx->counters);
   if (ctx->results_host) (void)hipHostFree(ctx->results_host);
+  if (ctx->ident) (void)hipFree(ctx->ident);
   (void)hipStreamDestroy(ctx->stream);
   delete ctx;
   return GLACIER_HIP_OK;
@@ -575,19 +583,13 @@ int glacier_hip_paged_attention(glacier_hip_context *ctx, const float *q_dev,
   // lane_of_row = identity: row i attends with page-table row i
   const size_t sc = gk::attention_scratch_floats((int)lanes, (int)num_heads, (int)num_kv_heads,
                                                  (int)head_dim, (int)max_ctx);
-  int rc = gh::ensure_scratch(ctx, sc * 4 + 256 + lanes * 4, 1);
+  int rc = gh::ensure_scratch(ctx, sc * 4, 1);
   if (rc) return rc;
-  int32_t *ident = (int32_t *)((char *)ctx->scratch + ((sc * 4 + 255) & ~(size_t)255));
-  std::vector<int32_t> h(lanes);
-  for (uint32_t i = 0; i < lanes; ++i) h[i] = (int32_t)i;
-  GH_CHECK(ctx, hipMemcpyAsync(ident, h.data(), lanes * 4, hipMemcpyHostToDevice, st));
   GH_CHECK(ctx, gk::launch_attention(q_dev, kv_pool_dev, kv_dtype == GLACIER_HIP_F16, page_table_dev,
-                                     (int)max_pages_per_lane, ident, ctx_lens_dev, (int)lanes,
+                                     (int)max_pages_per_lane, ctx->ident, ctx_lens_dev, (int)lanes,
                                      (int)layer, (int)num_layers, (int)num_heads,
                                      (int)num_kv_heads, (int)head_dim, (int)max_ctx,
                                      (float *)ctx->scratch, out_dev, st));
-  // `h` must outlive the async copy
-  GH_CHECK(ctx, hipStreamSynchronize(st));
   return GLACIER_HIP_OK;
 }
 

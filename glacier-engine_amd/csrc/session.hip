@@ -113,6 +113,9 @@ struct glacier_hip_session {
         *logits = nullptr;
   int8_t *act_q = nullptr;
   gk::ActMeta *act_meta = nullptr;
+  int8_t *act_q2 = nullptr;         // planes emitted by the gate/up epilogue for down
+  gk::ActMeta *act_meta2 = nullptr;
+  uint32_t planes2_rows = 0;        // rows act_q2 / act_meta2 hold
   float *att_scratch = nullptr;
   void *arg_scratch = nullptr;
   uint32_t *arg_counters = nullptr;
@@ -352,22 +355,33 @@ int head_D(const glacier_hip_session *s) {
   return gh::resolve_activation(s->opt.head_activation, c.vocab_size, c.dim) == GLACIER_HIP_ACT_Q8 ? 1 : 3;
 }
 
-// One projection: activation conversion (RMSNorm + Q8 / digit planes) then
-// the GEMV (up to 32 rows) or the MFMA GEMM (prompt chunks) with its epilogue.
+// One projection over `rows` activation rows. Input x (f32 [rows][K], with
+// an optional RMSNorm weight) is converted into int8 digit planes (Q8 or the
+// 3-digit f32 representation) and multiplied by the INT4 weight with the
+// given epilogue. Decode-sized projections build the planes inside the GEMV
+// (fused input stage); otherwise a separate conversion kernel writes them to
+// HBM first. With x == null the planes are already in `planes_q/planes_m`
+// (emitted by the previous projection's epilogue). The fused input stage is
+// requested where it measured faster than a separate conversion launch: the
+// O projection (no norm) and the LM head (cold, measured on gfx950), not QKV
+// or gate/up, whose every workgroup would repeat the whole-row RMSNorm.
+struct PlanesOut {
+  int8_t *q;
+  gk::ActMeta *meta;
+  int D;
+};
+
 hipError_t run_proj(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, int rows,
                     const float *x, const float *norm_w, int epi, const float *bias, float *y,
-                    const float *resid, const gk::QkvArgs *qkv, hipStream_t st) {
+                    const float *resid, const gk::QkvArgs *qkv, hipStream_t st,
+                    const int8_t *planes_q = nullptr, const gk::ActMeta *planes_m = nullptr,
+                    const PlanesOut *emit = nullptr, bool fuse_input = false) {
   const auto &c = s->model->cfg;
-  hipError_t e = gk::launch_prep_act(x, 0, norm_w, c.rms_eps, rows, (int)w->in_f, D, s->act_q,
-                                     s->act_meta, nullptr, st);
-  if (e != hipSuccess) return e;
   gk::GemvArgs a{};
   a.codes = w->codes;
   a.scales = w->scales;
   a.N = (int)w->out_f;
   a.K = (int)w->in_f;
-  a.act_q = s->act_q;
-  a.act_meta = s->act_meta;
   a.M = rows;
   a.D = D;
   a.bias = bias;
@@ -375,7 +389,27 @@ hipError_t run_proj(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, i
   a.resid = resid;
   a.epi = epi;
   if (qkv) a.qkv = *qkv;
-  return rows <= 32 ? gk::launch_gemv(a, st) : gk::launch_gemm(a, st);
+  const bool decode = rows <= 32;
+  if (x && decode && fuse_input && gk::gemv_fused_input_ok(a.N, a.K, rows, D)) {
+    a.x_in = x;
+    a.norm_w = norm_w;
+    a.eps = c.rms_eps;
+  } else if (x) {
+    hipError_t e = gk::launch_prep_act(x, 0, norm_w, c.rms_eps, rows, a.K, D, s->act_q,
+                                       s->act_meta, nullptr, st);
+    if (e != hipSuccess) return e;
+    a.act_q = s->act_q;
+    a.act_meta = s->act_meta;
+  } else {
+    a.act_q = planes_q;
+    a.act_meta = planes_m;
+  }
+  if (emit && decode) {
+    a.out_q = emit->q;
+    a.out_meta = emit->meta;
+    a.out_D = emit->D;
+  }
+  return decode ? gk::launch_gemv(a, st) : gk::launch_gemm(a, st);
 }
 
 // Embedding gather and every decoder layer for `rows` activation rows
@@ -414,13 +448,25 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
                              st);
     if (e != hipSuccess) return e;
     e = run_proj(s, L.o, layer_D(s, L.o->out_f, L.o->in_f), rows, s->attn, nullptr,
-                 gk::EPI_RESID, nullptr, s->h, s->x_res, nullptr, st);
+                 gk::EPI_RESID, nullptr, s->h, s->x_res, nullptr, st, nullptr, nullptr, nullptr,
+                 true);
     if (e != hipSuccess) return e;
-    e = run_proj(s, L.gu, layer_D(s, L.gu->out_f / 2, L.gu->in_f), rows, s->h, L.post_norm,
-                 gk::EPI_SWIGLU, nullptr, s->act, nullptr, nullptr, st);
-    if (e != hipSuccess) return e;
-    e = run_proj(s, L.down, layer_D(s, L.down->out_f, L.down->in_f), rows, s->act, nullptr,
-                 gk::EPI_RESID, nullptr, s->x_res, s->h, nullptr, st);
+    const int Dd = layer_D(s, L.down->out_f, L.down->in_f);
+    if (rows <= 32 && (uint32_t)rows <= s->planes2_rows) {
+      // gate/up writes the SwiGLU output straight into down's input planes
+      const PlanesOut po{s->act_q2, s->act_meta2, Dd};
+      e = run_proj(s, L.gu, layer_D(s, L.gu->out_f / 2, L.gu->in_f), rows, s->h, L.post_norm,
+                   gk::EPI_SWIGLU, nullptr, nullptr, nullptr, nullptr, st, nullptr, nullptr, &po);
+      if (e != hipSuccess) return e;
+      e = run_proj(s, L.down, Dd, rows, nullptr, nullptr, gk::EPI_RESID, nullptr, s->x_res, s->h,
+                   nullptr, st, s->act_q2, s->act_meta2);
+    } else {
+      e = run_proj(s, L.gu, layer_D(s, L.gu->out_f / 2, L.gu->in_f), rows, s->h, L.post_norm,
+                   gk::EPI_SWIGLU, nullptr, s->act, nullptr, nullptr, st);
+      if (e != hipSuccess) return e;
+      e = run_proj(s, L.down, Dd, rows, s->act, nullptr, gk::EPI_RESID, nullptr, s->x_res, s->h,
+                   nullptr, st);
+    }
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
@@ -432,7 +478,7 @@ hipError_t enqueue_head(glacier_hip_session *s, int rows, const float *x, bool e
   glacier_hip_model *m = s->model;
   const auto &c = m->cfg;
   hipError_t e = run_proj(s, m->head, head_D(s), rows, x, m->final_norm, gk::EPI_PLAIN, nullptr,
-                          s->logits, nullptr, nullptr, st);
+                          s->logits, nullptr, nullptr, st, nullptr, nullptr, nullptr, true);
   if (e != hipSuccess) return e;
   const long V = (long)c.vocab_size;
   const long W = (V + 63) / 64;
@@ -451,7 +497,7 @@ hipError_t enqueue_step(glacier_hip_session *s, int rows, bool head, bool elig, 
 
 void destroy_session(glacier_hip_session *s) {
   void *ptrs[] = {s->kv_pool, s->page_table, s->rope_cos, s->rope_sin, s->x_res, s->h, s->q,
-                  s->attn, s->act, s->logits, s->act_q, s->act_meta,
+                  s->attn, s->act, s->logits, s->act_q, s->act_meta, s->act_q2, s->act_meta2,
                   s->att_scratch, s->arg_scratch, s->arg_counters, s->arg_result, s->elig_words,
                   s->step_dev, s->pf_dev};
   for (void *p : ptrs)
@@ -849,6 +895,11 @@ glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
   A((void **)&s->logits, (size_t)L * c.vocab_size * 4);
   A((void **)&s->act_q, Gmax * 3 * M * 32);
   A((void **)&s->act_meta, Gmax * M * sizeof(gk::ActMeta));
+  // the gate/up epilogue emits planes for every decode-path launch: up to 32
+  // rows (decode lanes, or a prompt chunk that short)
+  s->planes2_rows = std::min<uint32_t>(M, 32);
+  A((void **)&s->act_q2, (size_t)(c.hidden_dim / 32) * 3 * s->planes2_rows * 32);
+  A((void **)&s->act_meta2, (size_t)(c.hidden_dim / 32) * s->planes2_rows * sizeof(gk::ActMeta));
   A((void **)&s->att_scratch, std::max<size_t>(att, 1) * 4);
   A(&s->arg_scratch, gk::argmax_scratch_bytes((int)L, (long)c.vocab_size));
   A((void **)&s->arg_counters, (size_t)L * 4);

@@ -230,7 +230,9 @@ int glacier_hip_rmsnorm(glacier_hip_context *ctx, const float *x_dev, const floa
  *   page[layer][K=0,V=1][16 positions][num_kv_heads * head_dim]
  * in f32 or f16 (kv_dtype). page_table_dev is [lanes][max_pages_per_lane]
  * int32 physical page ids; ctx_lens_dev[lanes] int32 = attended positions
- * (the new row included). q_dev/out_dev are [lanes][num_heads * head_dim]. */
+ * (the new row included). q_dev/out_dev are [lanes][num_heads * head_dim],
+ * lanes <= 64. Asynchronous on `stream`; after a first call with the same or
+ * larger sizes it only launches kernels (capturable in a HIP graph). */
 int glacier_hip_paged_attention(glacier_hip_context *ctx, const float *q_dev,
                                 const void *kv_pool_dev, int kv_dtype,
                                 const int32_t *page_table_dev, uint32_t max_pages_per_lane,

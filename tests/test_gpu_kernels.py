@@ -238,6 +238,7 @@ def test_paged_attention_matches_oracle(gh, gctx, ora, fp16, geom, ctxs):
         gctx.h, qd.data_ptr(), pdv.data_ptr(), gh.F16 if fp16 else gh.F32, ptd.data_ptr(),
         pt.shape[1], cl.data_ptr(), len(ctxs), layer, L, Hq, Hkv, hd, max(ctxs), out.data_ptr(), None)
     gh.check(rc, "paged_attention", gctx.h)
+    gctx.sync()  # the entry point is asynchronous on the context stream
     got = out.cpu().numpy()
     pool_host = pool.view(np.uint16) if fp16 else pool
     for i, c in enumerate(ctxs):
@@ -258,3 +259,33 @@ def test_rmsnorm_matches_oracle(gh, gctx, ora):
     gctx.sync()
     want = ora.rmsnorm(x, w, 1e-6)
     assert np.max(np.abs(out.cpu().numpy() - want) / (np.abs(want) + 1e-3)) < 1e-5
+
+
+def test_paged_attention_c3_config_matches_oracle(gh, gctx, ora):
+    """BASELINE config 3 geometry: 28 q / 4 kv heads, hd 128, fp16 KV in
+    scattered 16-position pages, 4 lanes at contexts 512, 2048, 4096, 8192
+    (above the reference's 4096 cap, which the oracle lifts unchanged)."""
+    torch = _torch()
+    Hq, Hkv, hd = 28, 4, 128
+    ctxs = [512, 2048, 4096, 8192]
+    rng = np.random.default_rng(0xC3)
+    L, layer = 2, 1
+    pool, pt = _paged_case(rng, ctxs, Hkv, hd, L, layer, True)
+    q = rng.standard_normal((len(ctxs), Hq * hd)).astype(np.float32)
+    qd = torch.from_numpy(q).cuda()
+    pdv = torch.from_numpy(pool.view(np.uint16)).cuda()
+    ptd = torch.from_numpy(pt).cuda()
+    cl = torch.from_numpy(np.array(ctxs, np.int32)).cuda()
+    out = torch.empty((len(ctxs), Hq * hd), dtype=torch.float32, device="cuda")
+    rc = gh.lib().glacier_hip_paged_attention(
+        gctx.h, qd.data_ptr(), pdv.data_ptr(), gh.F16, ptd.data_ptr(), pt.shape[1], cl.data_ptr(),
+        len(ctxs), layer, L, Hq, Hkv, hd, max(ctxs), out.data_ptr(), None)
+    gh.check(rc, "paged_attention", gctx.h)
+    gctx.sync()  # the entry point is asynchronous on the context stream
+    got = out.cpu().numpy()
+    for i, c in enumerate(ctxs):
+        want = ora.attention_paged(q[i], pool.view(np.uint16), True, pt[i], c, layer, L, Hq, Hkv,
+                                   hd)[0]
+        err = np.max(np.abs(got[i] - want))
+        print(f"c3 ctx={c} abs={err:.2e}", flush=True)
+        assert err < 2e-5
