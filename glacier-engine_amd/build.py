@@ -15,7 +15,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "libglacier_hip.so")
-SOURCES = ["kernels.hip", "gemm.hip", "runtime.hip", "session.hip", "host_util.cpp"]
+SOURCES = ["kernels.hip", "gemm.hip", "runtime.hip", "session.hip", "host_util.cpp",
+           "lane_weave.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 

@@ -114,6 +114,55 @@ class LaneState(C.Structure):
                 ("output_sha256", C.c_uint8 * 32)]
 
 
+CLAIM_FIELDS = ("capsule_bytes", "kv_bytes", "activation_bytes", "partial_bytes", "logits_bytes",
+                "output_journal_bytes", "staging_bytes", "device_bytes", "io_bytes",
+                "queue_slots")
+
+
+class Claim(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in CLAIM_FIELDS]
+
+
+class Limits(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("host_bytes",) + CLAIM_FIELDS]
+
+
+class RequestSpec(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("tenant_key", "request_key", "request_generation",
+                                          "resource_owner_key", "weight", "work_quanta",
+                                          "deadline_tick")] + [("claim", Claim)]
+
+
+class LaneHandle(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("scheduler_epoch", "slot_index", "slot_generation",
+                                          "tenant_key", "request_key", "request_generation")]
+
+
+class BankReceipt(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("bank_epoch", "slot_index", "generation", "owner_key")] + \
+        [("claim", Claim), ("integrity", C.c_uint64)]
+
+
+class LaneEvent(C.Structure):
+    _fields_ = [("abi_version", C.c_uint64), ("scheduler_epoch", C.c_uint64),
+                ("event_sequence", C.c_uint64), ("kind", C.c_uint32),
+                ("rejection_reason", C.c_uint32)] + \
+        [(n, C.c_uint8 * 32) for n in ("previous_sha256", "event_sha256", "state_before_sha256",
+                                       "state_after_sha256")] + \
+        [("logical_tick_before", C.c_uint64), ("logical_tick_after", C.c_uint64)] + \
+        [(n, C.c_uint32) for n in ("cursor_before", "cursor_after", "level_before",
+                                   "level_after")] + \
+        [("handle", LaneHandle), ("spec", RequestSpec), ("resource_receipt", BankReceipt),
+         ("resource_receipt_sha256", C.c_uint8 * 32)] + \
+        [(n, C.c_uint64) for n in ("remaining_before", "remaining_after", "wait_quanta",
+                                   "maximum_service_gap")] + \
+        [(n, C.c_uint32) for n in ("active_before", "active_after", "finished_before",
+                                   "finished_after")] + \
+        [("bank_used_before", Claim), ("bank_used_after", Claim)]
+
+
+_LW = [C.POINTER(LaneEvent)]
+
 # (name, restype, argtypes) for every exported symbol of include/glacier_hip.h
 _SIGS = [
     ("glacier_hip_abi_version", C.c_uint64, []),
@@ -176,6 +225,21 @@ _SIGS = [
     ("glacier_hip_synth_tokens", None, [C.c_uint64, C.c_uint64, C.c_uint32, _P, C.c_uint64]),
     ("glacier_hip_synth_tensor_id", C.c_uint64, [C.c_uint32, C.c_uint32]),
     ("glacier_hip_f16_to_f32", C.c_float, [C.c_uint16]),
+    ("glacier_hip_lane_weave_create", _P,
+     [C.c_uint32, C.POINTER(Limits), C.c_uint64, C.c_uint64, _P, C.c_uint32, C.c_uint64,
+      C.c_uint64]),
+    ("glacier_hip_lane_weave_destroy", None, [_P]),
+    ("glacier_hip_lane_weave_admit", C.c_int,
+     [_P, C.POINTER(RequestSpec), C.POINTER(C.c_int), C.POINTER(LaneHandle)] + _LW),
+    ("glacier_hip_lane_weave_serve_one", C.c_int, [_P] + _LW),
+    ("glacier_hip_lane_weave_plan_wave", C.c_int, [_P, C.c_uint32, _P, C.POINTER(C.c_uint32)]),
+    ("glacier_hip_lane_weave_retire", C.c_int, [_P, C.POINTER(LaneHandle)] + _LW),
+    ("glacier_hip_lane_weave_cancel", C.c_int, [_P, C.POINTER(LaneHandle)] + _LW),
+    ("glacier_hip_lane_weave_close", C.c_int, [_P] + _LW),
+    ("glacier_hip_lane_weave_slot", C.c_int,
+     [_P, C.c_uint32, C.POINTER(LaneHandle), C.POINTER(C.c_uint32), C.POINTER(C.c_uint64)]),
+    ("glacier_hip_lane_weave_chain_head", C.c_int, [_P, _P]),
+    ("glacier_hip_lane_weave_state_sha256", C.c_int, [_P, _P]),
 ]
 
 _lib = None
@@ -444,3 +508,91 @@ class Session:
         if self.h:
             lib().glacier_hip_session_destroy(self.h)
             self.h = None
+
+
+STALE_HANDLE, NO_RUNNABLE, INCOMPLETE_DRAIN, SCHEDULER_CLOSED, SCHEDULER_POISONED = 15, 16, 17, 18, 19
+
+
+def _claim(d):
+    c = Claim()
+    for k, v in (d or {}).items():
+        setattr(c, k, v)
+    return c
+
+
+class LaneWeave:
+    """Python face of glacier_hip_lane_weave_* (host scheduler; no GPU)."""
+
+    def __init__(self, capacity, bank_limits=None, bank_epoch=1, scheduler_epoch=1,
+                 challenge=None, max_weight=64, max_projection_quanta=1_000_000,
+                 max_projection_operations=1_000_000):
+        lim = Limits(*([2**64 - 1] * 11))
+        for k, v in (bank_limits or {}).items():
+            setattr(lim, k, v)
+        ch = (C.c_uint8 * 32)(*(challenge or (bytes([0xA5]) + bytes(31))))
+        self.h = lib().glacier_hip_lane_weave_create(capacity, C.byref(lim), bank_epoch,
+                                                     scheduler_epoch, ch, max_weight,
+                                                     max_projection_quanta,
+                                                     max_projection_operations)
+        if not self.h:
+            raise GlacierHipError(INVALID_ARGUMENT, "lane_weave_create")
+
+    def close_handle(self):
+        if self.h:
+            lib().glacier_hip_lane_weave_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close_handle()
+        except Exception:
+            pass
+
+    @staticmethod
+    def spec(tenant_key, request_key, request_generation, resource_owner_key, weight,
+             work_quanta, deadline_tick, claim):
+        return RequestSpec(tenant_key, request_key, request_generation, resource_owner_key,
+                           weight, work_quanta, deadline_tick, _claim(claim))
+
+    def admit(self, spec):
+        ok, h, e = C.c_int(0), LaneHandle(), LaneEvent()
+        check(lib().glacier_hip_lane_weave_admit(self.h, C.byref(spec), C.byref(ok), C.byref(h),
+                                                 C.byref(e)), "lane_weave_admit")
+        return bool(ok.value), (h if ok.value else None), e
+
+    def _ev(self, fn, *args):
+        e = LaneEvent()
+        rc = fn(self.h, *args, C.byref(e))
+        return rc, e
+
+    def serve_one(self):
+        rc, e = self._ev(lib().glacier_hip_lane_weave_serve_one)
+        check(rc, "lane_weave_serve_one")
+        return e
+
+    def plan_wave(self, max_count):
+        out = (C.c_uint32 * max(1, max_count))()
+        n = C.c_uint32(0)
+        check(lib().glacier_hip_lane_weave_plan_wave(self.h, max_count, out, C.byref(n)),
+              "lane_weave_plan_wave")
+        return [int(out[i]) for i in range(n.value)]
+
+    def retire(self, handle):
+        return self._ev(lib().glacier_hip_lane_weave_retire, C.byref(handle))
+
+    def cancel(self, handle):
+        return self._ev(lib().glacier_hip_lane_weave_cancel, C.byref(handle))
+
+    def close(self):
+        return self._ev(lib().glacier_hip_lane_weave_close)
+
+    def slot(self, i):
+        h, st, rem = LaneHandle(), C.c_uint32(), C.c_uint64()
+        check(lib().glacier_hip_lane_weave_slot(self.h, i, C.byref(h), C.byref(st),
+                                                C.byref(rem)), "lane_weave_slot")
+        return h, int(st.value), int(rem.value)
+
+    def chain_head(self):
+        out = (C.c_uint8 * 32)()
+        check(lib().glacier_hip_lane_weave_chain_head(self.h, out), "chain_head")
+        return bytes(out)

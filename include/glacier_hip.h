@@ -42,6 +42,11 @@ enum glacier_hip_status {
     GLACIER_HIP_INVALID_TRANSACTION = 12,/* paged_kv_cache Error.InvalidTransaction */
     GLACIER_HIP_BUSY = 13,               /* concurrent submission rejected (int4_executor.zig:2267) */
     GLACIER_HIP_UNSUPPORTED = 14,
+    GLACIER_HIP_STALE_HANDLE = 15,       /* LaneWeave Error.StaleHandle */
+    GLACIER_HIP_NO_RUNNABLE = 16,        /* LaneWeave Error.NoRunnableRequest */
+    GLACIER_HIP_INCOMPLETE_DRAIN = 17,   /* LaneWeave Error.IncompleteDrain */
+    GLACIER_HIP_SCHEDULER_CLOSED = 18,   /* LaneWeave Error.SchedulerClosed */
+    GLACIER_HIP_SCHEDULER_POISONED = 19, /* LaneWeave Error.InvariantViolation / BankDrift */
 };
 
 /* ---- element types / activation modes ------------------------------------ */
@@ -366,6 +371,118 @@ int glacier_hip_session_page_of(glacier_hip_session *s, uint32_t lane, uint32_t 
 /* Test hook: make the next decode step fail after its kernels ran but before
  * commit (forces the abort path, as a failed sink/ack would). */
 int glacier_hip_session_inject_failure(glacier_hip_session *s, int enable);
+
+/* ---- LaneWeave QoS v1 multi-request scheduler ----------------------------
+ * The reference's deterministic interleaved weighted round-robin scheduler
+ * (src/core/lane_weave_qos.zig:576-2830) over its own dedicated flat
+ * ResourceBank (src/core/resource_bank.zig:867-3200): admission reserves and
+ * commits the request's claim before any request state exists and rejects
+ * (no_slot / duplicate_tenant / resource_limit / projection_limit /
+ * deadline_infeasible) without touching the Bank; one service quantum is one
+ * decode token of one lane; every committed decision is an Event-v1 record
+ * chained by SHA-256 (eventSha256 :4004-4038, initialRoot :4040-4064) with
+ * the reference's field order, domains and little-endian encoding.
+ *
+ * A decode wave batches the next quanta of distinct lanes:
+ * glacier_hip_lane_weave_plan_wave simulates the IWRR selections that the
+ * next serve_one calls will make (stopping before a lane would repeat), the
+ * caller runs those lanes' tokens in one device step, then commits them with
+ * serve_one in the same order; the committed event chain is the one a serial
+ * caller would produce. Layouts below are the reference's fields in order;
+ * events are values, not live handles. */
+typedef struct {
+    uint64_t capsule_bytes, kv_bytes, activation_bytes, partial_bytes, logits_bytes;
+    uint64_t output_journal_bytes, staging_bytes, device_bytes, io_bytes, queue_slots;
+} glacier_hip_claim_t;                 /* resource_bank.zig:61-72 */
+
+typedef struct {
+    uint64_t host_bytes, capsule_bytes, kv_bytes, activation_bytes, partial_bytes;
+    uint64_t logits_bytes, output_journal_bytes, staging_bytes, device_bytes, io_bytes;
+    uint64_t queue_slots;
+} glacier_hip_limits_t;                /* resource_bank.zig:101-113 (UINT64_MAX = unlimited) */
+
+typedef struct {
+    uint64_t tenant_key, request_key, request_generation, resource_owner_key;
+    uint64_t weight;                   /* u16 in the reference: 1..max_weight */
+    uint64_t work_quanta;
+    uint64_t deadline_tick;            /* absolute logical tick; 0 = none */
+    glacier_hip_claim_t claim;
+} glacier_hip_request_spec_t;          /* RequestSpec lane_weave_qos.zig:96-106 */
+
+typedef struct {
+    uint64_t scheduler_epoch;
+    uint64_t slot_index;               /* u32 in the reference */
+    uint64_t slot_generation, tenant_key, request_key, request_generation;
+} glacier_hip_lane_handle_t;           /* Handle :109-116 */
+
+typedef struct {
+    uint64_t bank_epoch;
+    uint64_t slot_index;               /* u32 in the reference */
+    uint64_t generation, owner_key;
+    glacier_hip_claim_t claim;
+    uint64_t integrity;
+} glacier_hip_bank_receipt_t;          /* Receipt resource_bank.zig:506-513 */
+
+enum glacier_hip_lane_event_kind {
+    GLACIER_HIP_EVENT_ADMISSION_ACCEPTED = 0, GLACIER_HIP_EVENT_ADMISSION_REJECTED = 1,
+    GLACIER_HIP_EVENT_SERVICE = 2, GLACIER_HIP_EVENT_CANCEL = 3, GLACIER_HIP_EVENT_RETIRE = 4,
+    GLACIER_HIP_EVENT_CLOSE = 5,
+};
+enum glacier_hip_lane_rejection {
+    GLACIER_HIP_REJECT_NONE = 0, GLACIER_HIP_REJECT_NO_SLOT = 1,
+    GLACIER_HIP_REJECT_DUPLICATE_TENANT = 2, GLACIER_HIP_REJECT_RESOURCE_LIMIT = 3,
+    GLACIER_HIP_REJECT_PROJECTION_LIMIT = 4, GLACIER_HIP_REJECT_DEADLINE_INFEASIBLE = 5,
+};
+
+typedef struct {
+    uint64_t abi_version, scheduler_epoch, event_sequence;
+    uint32_t kind, rejection_reason;
+    uint8_t previous_sha256[32], event_sha256[32];
+    uint8_t state_before_sha256[32], state_after_sha256[32];
+    uint64_t logical_tick_before, logical_tick_after;
+    uint32_t cursor_before, cursor_after, level_before, level_after;
+    glacier_hip_lane_handle_t handle;
+    glacier_hip_request_spec_t spec;
+    glacier_hip_bank_receipt_t resource_receipt;
+    uint8_t resource_receipt_sha256[32];
+    uint64_t remaining_before, remaining_after, wait_quanta, maximum_service_gap;
+    uint32_t active_before, active_after, finished_before, finished_after;
+    glacier_hip_claim_t bank_used_before, bank_used_after;
+} glacier_hip_lane_event_t;            /* EventV1 :303-332 */
+
+typedef struct glacier_hip_lane_weave glacier_hip_lane_weave;
+
+/* Scheduler.init over a fresh dedicated Bank of `capacity` slots
+ * (:634-735): NULL on an invalid configuration (zero capacity / epoch /
+ * weight / budgets, all-zero challenge). */
+glacier_hip_lane_weave *glacier_hip_lane_weave_create(
+    uint32_t capacity, const glacier_hip_limits_t *bank_limits, uint64_t bank_epoch,
+    uint64_t scheduler_epoch, const uint8_t challenge[32], uint32_t max_weight,
+    uint64_t max_projection_quanta, uint64_t max_projection_operations);
+void glacier_hip_lane_weave_destroy(glacier_hip_lane_weave *lw);
+/* admit (:742-900). *admitted = 1 with handle_out set, or 0 (a rejection
+ * event, Bank untouched). A malformed spec returns INVALID_ARGUMENT and emits
+ * nothing. */
+int glacier_hip_lane_weave_admit(glacier_hip_lane_weave *lw, const glacier_hip_request_spec_t *spec,
+                                 int *admitted, glacier_hip_lane_handle_t *handle_out,
+                                 glacier_hip_lane_event_t *event_out);
+/* serveOne (:1196-1270): commit the next IWRR quantum. */
+int glacier_hip_lane_weave_serve_one(glacier_hip_lane_weave *lw, glacier_hip_lane_event_t *event_out);
+/* The slots the next serve_one calls select, in order, up to max_count and
+ * stopping before a slot would repeat; nothing is mutated. */
+int glacier_hip_lane_weave_plan_wave(glacier_hip_lane_weave *lw, uint32_t max_count,
+                                     uint32_t *slots_out, uint32_t *count_out);
+int glacier_hip_lane_weave_retire(glacier_hip_lane_weave *lw, const glacier_hip_lane_handle_t *h,
+                                  glacier_hip_lane_event_t *event_out);
+int glacier_hip_lane_weave_cancel(glacier_hip_lane_weave *lw, const glacier_hip_lane_handle_t *h,
+                                  glacier_hip_lane_event_t *event_out);
+int glacier_hip_lane_weave_close(glacier_hip_lane_weave *lw, glacier_hip_lane_event_t *event_out);
+/* Handle of a slot (handleFor :2665) and whether it is free / active / finished (0/1/2). */
+int glacier_hip_lane_weave_slot(glacier_hip_lane_weave *lw, uint32_t slot,
+                                glacier_hip_lane_handle_t *handle_out, uint32_t *state_out,
+                                uint64_t *remaining_out);
+int glacier_hip_lane_weave_chain_head(glacier_hip_lane_weave *lw, uint8_t out[32]);
+int glacier_hip_lane_weave_state_sha256(glacier_hip_lane_weave *lw, uint8_t out[32]);
 
 /* ---- synthetic random-init generator (host, deterministic) ---------------
  * Counter-based SplitMix64 streams keyed by (seed, tensor id):

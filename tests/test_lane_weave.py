@@ -1,0 +1,260 @@
+"""LaneWeave QoS v1 (BASELINE config 5's scheduler): the oracle restatement
+and the product scheduler (glacier_hip_lane_weave_*, host C++ in
+libglacier_hip.so) against the reference's own known answers, and against
+each other on random traces.
+
+Reference known answers (src/core/lane_weave_qos.zig):
+  * IWRR golden order and final close-event SHA-256 (:4436-4474)
+  * deadline_infeasible before Bank mutation (:4476-4493)
+  * projection budgets: quanta, operations, scan (:4495-4554)
+  * resource capacity (:4556-4570)
+  * stale handle after slot reuse (:4572-4586)
+"""
+import random
+
+import pytest
+
+from oracle import lane_weave as lw
+
+GOLDEN_ORDER = [1, 2, 3, 2, 3, 3, 3, 1, 2, 3, 2, 3, 3, 3]
+GOLDEN_CLOSE = "9cffc54d7a146c3a69cebb386a189dd1d3efffec3fba25c8ecadef8ab3c96785"
+
+
+# ---------------------------------------------------------------- oracle ----
+def test_oracle_iwrr_golden_order_and_close_hash():
+    f = lw.test_fixture(3, 4)
+    for key, weight, work in ((1, 1, 2), (2, 2, 4), (3, 4, 8)):
+        ok, _, ev = f.admit(lw.test_spec(key, weight, work, 0))
+        assert ok and ev["kind"] == lw.ADMISSION_ACCEPTED
+    order = []
+    for _ in GOLDEN_ORDER:
+        ev = f.serve_one()
+        assert ev["kind"] == lw.SERVICE
+        assert ev["wait_quanta"] <= ev["maximum_service_gap"]
+        assert ev["event_sha256"] == lw.event_sha256(ev)
+        order.append(ev["handle"]["tenant_key"])
+    assert order == GOLDEN_ORDER
+    for i in range(3):
+        f.retire(f.handle_for(i))
+    final = f.close()
+    assert final["kind"] == lw.CLOSE
+    assert final["event_sha256"].hex() == GOLDEN_CLOSE
+    assert lw.claim_is_zero(f.bank.used) and f.bank.committed_receipts() == 0
+
+
+def _bank_state(f):
+    return (dict(f.bank.used), [dict(s) for s in f.bank.slots], f.bank.next_generation)
+
+
+def test_oracle_rejects_infeasible_deadline_before_bank_mutation():
+    f = lw.test_fixture(2, 2)
+    assert f.admit(lw.test_spec(1, 1, 2, 2))[0]
+    before = _bank_state(f)
+    ok, _, ev = f.admit(lw.test_spec(2, 1, 1, 1))
+    assert not ok and ev["rejection_reason"] == lw.DEADLINE_INFEASIBLE
+    assert _bank_state(f) == before
+
+
+@pytest.mark.parametrize("cap,mw,pq,po,spec", [
+    (1, 1, 2, 100, (1, 1, 3, 10)),     # quanta budget
+    (8, 8, 100, 32, (1, 1, 4, 20)),    # operation budget
+    (8, 8, 100, 1, (1, 1, 1, 0)),      # scan budget
+])
+def test_oracle_projection_budgets_reject_before_bank_mutation(cap, mw, pq, po, spec):
+    f = lw.test_fixture(cap, mw, pq, po)
+    before = _bank_state(f)
+    ok, _, ev = f.admit(lw.test_spec(*spec))
+    assert not ok and ev["rejection_reason"] == lw.PROJECTION_LIMIT
+    assert _bank_state(f) == before
+
+
+def test_oracle_rejects_resource_capacity():
+    f = lw.test_fixture(2, 2)
+    sp = lw.test_spec(1, 1, 1, 0)
+    sp["claim"]["kv_bytes"] = (1 << 20) + 1
+    before = _bank_state(f)
+    ok, _, ev = f.admit(sp)
+    assert not ok and ev["rejection_reason"] == lw.RESOURCE_LIMIT
+    assert _bank_state(f) == before
+
+
+def test_oracle_stale_handle_cannot_cancel_reused_slot():
+    f = lw.test_fixture(1, 1)
+    ok, first, _ = f.admit(lw.test_spec(1, 1, 1, 0))
+    f.cancel(first)
+    ok, second, _ = f.admit(lw.test_spec(2, 1, 1, 0))
+    assert second["slot_generation"] != first["slot_generation"]
+    with pytest.raises(lw.LaneWeaveError, match="StaleHandle"):
+        f.cancel(first)
+    f.cancel(second)
+    f.close()
+
+
+# --------------------------------------------------------------- product ----
+FIXTURE_LIMITS = lambda cap: dict(host_bytes=1 << 20, kv_bytes=1 << 20, queue_slots=cap)  # noqa: E731
+
+
+def _product(gh, cap, mw, pq=10_000, po=1_000_000):
+    return gh.LaneWeave(cap, FIXTURE_LIMITS(cap), bank_epoch=0x42414E4B,
+                        scheduler_epoch=0x51534553, challenge=bytes([0xA5]) + bytes(31),
+                        max_weight=mw, max_projection_quanta=pq, max_projection_operations=po)
+
+
+def _pspec(gh, sp):
+    return gh.LaneWeave.spec(sp["tenant_key"], sp["request_key"], sp["request_generation"],
+                             sp["resource_owner_key"], sp["weight"], sp["work_quanta"],
+                             sp["deadline_tick"], {k: v for k, v in sp["claim"].items() if v})
+
+
+def test_product_iwrr_golden_order_and_close_hash(gh):
+    p = _product(gh, 3, 4)
+    for key, weight, work in ((1, 1, 2), (2, 2, 4), (3, 4, 8)):
+        ok, _, ev = p.admit(_pspec(gh, lw.test_spec(key, weight, work, 0)))
+        assert ok and ev.kind == lw.ADMISSION_ACCEPTED
+    order = []
+    for _ in GOLDEN_ORDER:
+        ev = p.serve_one()
+        assert ev.kind == lw.SERVICE and ev.wait_quanta <= ev.maximum_service_gap
+        order.append(ev.handle.tenant_key)
+    assert order == GOLDEN_ORDER
+    for i in range(3):
+        rc, _ = p.retire(p.slot(i)[0])
+        assert rc == 0
+    rc, final = p.close()
+    assert rc == 0 and bytes(final.event_sha256).hex() == GOLDEN_CLOSE
+
+
+@pytest.mark.parametrize("cap,mw,pq,po,first,spec,reason", [
+    (2, 2, 10_000, 1_000_000, (1, 1, 2, 2), (2, 1, 1, 1), lw.DEADLINE_INFEASIBLE),
+    (1, 1, 2, 100, None, (1, 1, 3, 10), lw.PROJECTION_LIMIT),
+    (8, 8, 100, 32, None, (1, 1, 4, 20), lw.PROJECTION_LIMIT),
+    (8, 8, 100, 1, None, (1, 1, 1, 0), lw.PROJECTION_LIMIT),
+])
+def test_product_rejections_match_reference(gh, cap, mw, pq, po, first, spec, reason):
+    p = _product(gh, cap, mw, pq, po)
+    if first:
+        assert p.admit(_pspec(gh, lw.test_spec(*first)))[0]
+    ok, h, ev = p.admit(_pspec(gh, lw.test_spec(*spec)))
+    assert not ok and h is None
+    assert ev.kind == lw.ADMISSION_REJECTED and ev.rejection_reason == reason
+    assert list(ev.bank_used_before.__reduce__()[1]) == list(ev.bank_used_after.__reduce__()[1])
+
+
+def test_product_resource_limit_and_stale_handle(gh):
+    p = _product(gh, 2, 2)
+    sp = lw.test_spec(1, 1, 1, 0)
+    sp["claim"]["kv_bytes"] = (1 << 20) + 1
+    ok, _, ev = p.admit(_pspec(gh, sp))
+    assert not ok and ev.rejection_reason == lw.RESOURCE_LIMIT
+    q = _product(gh, 1, 1)
+    ok, first, _ = q.admit(_pspec(gh, lw.test_spec(1, 1, 1, 0)))
+    assert q.cancel(first)[0] == 0
+    ok, second, _ = q.admit(_pspec(gh, lw.test_spec(2, 1, 1, 0)))
+    assert second.slot_generation != first.slot_generation
+    assert q.cancel(first)[0] == gh.STALE_HANDLE
+    assert q.cancel(second)[0] == 0
+    assert q.close()[0] == 0
+
+
+def test_product_rejects_malformed_spec_without_event(gh):
+    p = _product(gh, 2, 2)
+    head = p.chain_head()
+    bad = lw.test_spec(1, 3, 1, 0)  # weight above max_weight
+    with pytest.raises(gh.GlacierHipError):
+        p.admit(_pspec(gh, bad))
+    assert p.chain_head() == head
+
+
+def _random_trace(seed, cap=6, steps=400):
+    """A random mix of admissions (weights, deadlines, oversize claims,
+    duplicate tenants), services, retires and cancels."""
+    rng = random.Random(seed)
+    ops, next_key = [], 1
+    for _ in range(steps):
+        r = rng.random()
+        if r < 0.25:
+            key = next_key if rng.random() < 0.9 else max(1, next_key - 1)
+            next_key += 1
+            deadline = 0 if rng.random() < 0.6 else rng.randint(1, 60)
+            ops.append(("admit", key, rng.randint(1, 4), rng.randint(1, 12), deadline,
+                        rng.random() < 0.05))
+        elif r < 0.85:
+            ops.append(("serve",))
+        elif r < 0.95:
+            ops.append(("retire", rng.randrange(cap)))
+        else:
+            ops.append(("cancel", rng.randrange(cap)))
+    return ops
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_product_matches_oracle_on_random_traces(gh, seed):
+    cap, mw = 6, 4
+    o = lw.test_fixture(cap, mw, 200, 100_000)
+    p = _product(gh, cap, mw, 200, 100_000)
+    n_events = 0
+    for op in _random_trace(seed, cap):
+        if op[0] == "admit":
+            _, key, weight, work, deadline, big = op
+            sp = lw.test_spec(key, weight, work, deadline)
+            if big:
+                sp["claim"]["kv_bytes"] = 1 << 19
+            try:
+                o_ok, o_h, o_ev = o.admit(sp)
+            except lw.LaneWeaveError:  # e.g. a deadline already in the past
+                with pytest.raises(gh.GlacierHipError):
+                    p.admit(_pspec(gh, sp))
+                continue
+            p_ok, p_h, p_ev = p.admit(_pspec(gh, sp))
+            assert o_ok == p_ok
+            assert bytes(p_ev.event_sha256) == o_ev["event_sha256"]
+        elif op[0] == "serve":
+            plan = p.plan_wave(cap)
+            try:
+                o_ev = o.serve_one()
+            except lw.LaneWeaveError:
+                with pytest.raises(gh.GlacierHipError):
+                    p.serve_one()
+                assert plan == []
+                continue
+            p_ev = p.serve_one()
+            assert plan and plan[0] == p_ev.handle.slot_index
+            assert bytes(p_ev.event_sha256) == o_ev["event_sha256"]
+        else:
+            idx = op[1]
+            handle = o.handle_for(idx)
+            try:
+                o_ev = o.retire(handle) if op[0] == "retire" else o.cancel(handle)
+            except lw.LaneWeaveError:
+                ph = p.slot(idx)[0]
+                rc, _ = p.retire(ph) if op[0] == "retire" else p.cancel(ph)
+                assert rc == gh.STALE_HANDLE
+                continue
+            ph = p.slot(idx)[0]
+            rc, p_ev = p.retire(ph) if op[0] == "retire" else p.cancel(ph)
+            assert rc == 0 and bytes(p_ev.event_sha256) == o_ev["event_sha256"]
+        n_events += 1
+        assert p.chain_head() == o.chain_head
+    assert n_events > 100
+
+
+@pytest.mark.parametrize("weights", [(1, 1, 1, 1), (1, 2, 4, 3), (4, 4, 1, 2, 3, 1, 2)])
+def test_plan_wave_is_the_next_serial_selections(gh, weights):
+    """A planned wave lists exactly the slots the following serve_one calls
+    select, with no slot twice; committing it reproduces the serial chain."""
+    cap = len(weights)
+    p = _product(gh, cap, 4)
+    o = lw.test_fixture(cap, 4)
+    for i, w in enumerate(weights):
+        sp = lw.test_spec(i + 1, w, 3 + 2 * i, 0)
+        assert p.admit(_pspec(gh, sp))[0] and o.admit(sp)[0]
+    while True:
+        plan = p.plan_wave(cap)
+        if not plan:
+            break
+        assert len(set(plan)) == len(plan)
+        for slot in plan:
+            ev = p.serve_one()
+            assert ev.handle.slot_index == slot
+            assert bytes(ev.event_sha256) == o.serve_one()["event_sha256"]
+    assert p.chain_head() == o.chain_head
