@@ -7,7 +7,10 @@ One "step" is one greedy decode token of the batch-1 lane (the full token
 loop: embedding gather, 28 layers, final norm, LM head, argmax, per-token
 commit). `value` = tokens/s over exactly K timed steps with the weights and
 KV already resident in HBM. The same JSON line carries:
-  * lanes32     32 concurrent lanes decoding together (tokens/s, aggregate);
+  * lanes32     32 concurrent lanes decoding together at short context
+                (tokens/s, aggregate);
+  * c5_laneweave config 5: 32 lanes under LaneWeave weighted IWRR, prompts
+                U[64, 4096], 256 tokens each through the eligible argmax;
   * gemv        the INT4 GEMV kernel timed alone on the BASELINE config-2
                 shapes and on the 7B gate/up projection, with HIP events on
                 the launch stream;
@@ -124,6 +127,75 @@ def decode_batch1(gh, sess, prompt, warmup, steps):
         tok = int(sess.step([0], [tok])[0])
     dt = time.perf_counter() - t0
     return steps / dt, dt
+
+
+def bench_c5(gh, model, lanes=32, gen=256, prompt_lo=64, prompt_hi=4096, max_weight=4):
+    """32 concurrent lanes under LaneWeave weighted IWRR
+    (weights 1..4 by lane, max_weight 4), prompt lengths uniform in
+    [64, 4096] by seed, each lane generating `gen` greedy tokens through the
+    eligible argmax over an all-ones full-vocab mask, KV paged at 16 fp16
+    positions. Every lane is admitted (its KV claim charged to the scheduler's
+    Bank) and prefilled; then decode waves run until every lane's quanta are
+    served: each wave batches the next IWRR quanta of distinct lanes into one
+    device step and commits them in scheduler order. Decode tok/s counts the
+    tokens of the waves over their wall time; end-to-end adds prefill."""
+    cfg = model.cfg
+    rng = np.random.default_rng(SEED ^ 0xC5)
+    plens = [int(x) for x in rng.integers(prompt_lo, prompt_hi + 1, size=lanes)]
+    weights = [1 + (i % max_weight) for i in range(lanes)]
+    V = cfg["vocab_size"]
+    W = (V + 63) // 64
+    kvd = cfg["num_kv_heads"] * cfg["head_dim"]
+    page_bytes = cfg["num_layers"] * 2 * 16 * kvd * 2
+    pages = [-(-(p + gen) // 16) for p in plens]
+    sess = gh.Session(model, max_lanes=lanes, max_positions=prompt_hi + gen + 8, kv_dtype=gh.F16,
+                      total_pages=sum(pages), prefill_chunk=2048)
+    sched = gh.LaneWeave(lanes, dict(host_bytes=sum(pages) * page_bytes,
+                                     kv_bytes=sum(pages) * page_bytes, queue_slots=lanes),
+                         bank_epoch=0x42414E4B, scheduler_epoch=0x51534553, max_weight=max_weight)
+    try:
+        tokens = np.zeros(lanes, np.uint32)
+        t0 = time.perf_counter()
+        for i in range(lanes):
+            spec = gh.LaneWeave.spec(i + 1, 10 * (i + 1), 1, 100 * (i + 1), weights[i], gen - 1, 0,
+                                     dict(kv_bytes=pages[i] * page_bytes, queue_slots=1))
+            ok, _, _ = sched.admit(spec)
+            assert ok, "admission rejected"
+            sess.begin(i, seed=i)
+            prompt = gh.synth_tokens(SEED, 0x4C414E45 + i, V, plens[i])
+            tokens[i] = sess.prefill(i, prompt)
+        t_prefill = time.perf_counter() - t0
+        elig = np.full((lanes, W), np.uint64(0xFFFFFFFFFFFFFFFF), np.uint64)
+        if V % 64:
+            elig[:, -1] = np.uint64((1 << (V % 64)) - 1)
+        t1 = time.perf_counter()
+        n_tok, waves = 0, 0
+        while True:
+            try:
+                slots, evs = sched.wave(sess, list(range(lanes)), tokens, elig)
+            except gh.GlacierHipError as e:
+                if e.code == gh.NO_RUNNABLE:
+                    break
+                raise
+            waves += 1
+            n_tok += len(slots)
+            for ev in evs:
+                if ev.remaining_after == 0:
+                    assert sched.retire(ev.handle)[0] == 0
+        t_decode = time.perf_counter() - t1
+        rc, cev = sched.close()
+        assert rc == 0
+        res = dict(lanes=lanes, tokens_per_lane=gen, weights="1..4 by lane",
+                   prompt_len_min=min(plens), prompt_len_max=max(plens),
+                   prompt_tokens=sum(plens), prefill_s=round(t_prefill, 2),
+                   decode_tokens=n_tok, waves=waves, mean_wave=round(n_tok / max(waves, 1), 2),
+                   decode_s=round(t_decode, 2), decode_tokens_per_s=round(n_tok / t_decode, 1),
+                   end_to_end_tokens_per_s=round((n_tok + lanes) / (t_prefill + t_decode), 1),
+                   event_chain_head=bytes(cev.event_sha256).hex())
+        log("c5", res)
+        return res
+    finally:
+        sess.close()
 
 
 def decode_lanes(gh, sess, lanes, prompts, warmup, steps):
@@ -269,8 +341,8 @@ def main():
     ap.add_argument("--lane-prompt", type=int, default=64)
     ap.add_argument("--gemv-reps", type=int, default=50)
     ap.add_argument("--gemv-only", action="store_true", help="only the GEMV kernel timing")
-    ap.add_argument("--sections", default="gemv,decode,lanes,prefill,attention,cpu",
-                    help="comma list of gemv, decode, lanes, prefill, attention, cpu "
+    ap.add_argument("--sections", default="gemv,decode,lanes,c5,prefill,attention,cpu",
+                    help="comma list of gemv, decode, lanes, c5, prefill, attention, cpu "
                          "(profiling runs select one; the JSON line needs decode)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
@@ -339,12 +411,17 @@ def main():
                      context_range=[a.lane_prompt, a.lane_prompt + a.warmup + a.steps])
         log(f"{a.lanes}-lane decode {tpsL:.1f} tok/s")
     sess.close()
+    c5 = bench_c5(gh, model) if "c5" in secs else None
     prefill = bench_prefill(gh, model, [512, 2048]) if not a.no_prefill else None
     model.close()
     attn = bench_attention(gh, ctx, torch) if not a.no_attention else None
     cpu = None if a.no_cpu_baseline else cpu_baseline(host, int(prompt[0]))
     if cpu:
         log("cpu baseline", cpu)
+        if c5:
+            # the reference serves one lane per quantum with the serial token
+            # loop (F10): its multi-lane rate is its single-lane rate
+            c5["vs_cpu_reference"] = round(c5["decode_tokens_per_s"] / cpu["value"], 1)
     out = dict(
         metric="decode tok/s at batch 1 (7B INT4)", value=round(tps1, 2), unit="tokens/s",
         n_gpus=1, steps=a.steps, warmup=a.warmup, ms_per_step=round(dt1 * 1e3 / max(a.steps, 1), 4),
@@ -353,7 +430,8 @@ def main():
         config=dict(workload="Qwen2.5-7B-shaped INT4 g32 greedy decode, batch 1",
                     prompt_len=a.prompt, kv="fp16 paged, 16 positions/page",
                     parallelism="single GPU"),
-        roofline=roofline, cpu_baseline=cpu, lanes32=lanes, prefill=prefill, attention=attn,
+        roofline=roofline, cpu_baseline=cpu, lanes32=lanes, c5_laneweave=c5, prefill=prefill,
+        attention=attn,
         gemv=([dom] if dom else []) + gemv)
     print(json.dumps(out))
 

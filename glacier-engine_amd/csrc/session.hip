@@ -1107,3 +1107,50 @@ int glacier_hip_session_page_of(glacier_hip_session *s, uint32_t lane, uint32_t 
 }
 
 }  // extern "C"
+
+extern "C" int glacier_hip_session_lane_weave_wave(
+    glacier_hip_session *s, glacier_hip_lane_weave *lw, const uint32_t *lane_of_slot,
+    uint32_t slot_count, uint32_t *tokens_by_lane, const uint64_t *eligible_by_lane,
+    uint32_t max_count, uint32_t *slots_out, glacier_hip_lane_event_t *events_out,
+    uint32_t *count_out) {
+  if (!s || !lw || !lane_of_slot || !tokens_by_lane || !count_out)
+    return GLACIER_HIP_INVALID_ARGUMENT;
+  *count_out = 0;
+  const uint32_t L = (uint32_t)s->lanes.size();
+  if (max_count == 0 || max_count > L) return GLACIER_HIP_SHAPE_MISMATCH;
+  std::vector<uint32_t> plan(max_count);
+  uint32_t n = 0;
+  int rc = glacier_hip_lane_weave_plan_wave(lw, max_count, plan.data(), &n);
+  if (rc) return rc;
+  if (n == 0) return GLACIER_HIP_NO_RUNNABLE;
+  std::vector<uint32_t> lanes(n), toks(n), next(n);
+  for (uint32_t i = 0; i < n; ++i) {
+    if (plan[i] >= slot_count || lane_of_slot[plan[i]] >= L) return GLACIER_HIP_SHAPE_MISMATCH;
+    lanes[i] = lane_of_slot[plan[i]];
+    toks[i] = tokens_by_lane[lanes[i]];
+  }
+  const uint64_t W = (s->model->cfg.vocab_size + 63) / 64;
+  std::vector<uint64_t> elig;
+  if (eligible_by_lane) {
+    elig.resize((size_t)n * W);
+    for (uint32_t i = 0; i < n; ++i)
+      memcpy(&elig[(size_t)i * W], eligible_by_lane + (size_t)lanes[i] * W, W * 8);
+  }
+  // the device step commits its KV rows, tokens and sampler counters only on
+  // success; then the scheduler commits the same quanta in plan order
+  rc = glacier_hip_session_decode_step(s, lanes.data(), toks.data(), n,
+                                       eligible_by_lane ? elig.data() : nullptr, next.data(),
+                                       nullptr);
+  if (rc) return rc;
+  for (uint32_t i = 0; i < n; ++i) {
+    glacier_hip_lane_event_t ev;
+    rc = glacier_hip_lane_weave_serve_one(lw, &ev);
+    if (rc) return rc;
+    if (ev.handle.slot_index != plan[i]) return GLACIER_HIP_SCHEDULER_POISONED;
+    tokens_by_lane[lanes[i]] = next[i];
+    if (slots_out) slots_out[i] = plan[i];
+    if (events_out) events_out[i] = ev;
+    *count_out = i + 1;
+  }
+  return GLACIER_HIP_OK;
+}

@@ -240,6 +240,8 @@ _SIGS = [
      [_P, C.c_uint32, C.POINTER(LaneHandle), C.POINTER(C.c_uint32), C.POINTER(C.c_uint64)]),
     ("glacier_hip_lane_weave_chain_head", C.c_int, [_P, _P]),
     ("glacier_hip_lane_weave_state_sha256", C.c_int, [_P, _P]),
+    ("glacier_hip_session_lane_weave_wave", C.c_int,
+     [_P, _P, _P, C.c_uint32, _P, _P, C.c_uint32, _P, _P, C.POINTER(C.c_uint32)]),
 ]
 
 _lib = None
@@ -591,6 +593,21 @@ class LaneWeave:
         check(lib().glacier_hip_lane_weave_slot(self.h, i, C.byref(h), C.byref(st),
                                                 C.byref(rem)), "lane_weave_slot")
         return h, int(st.value), int(rem.value)
+
+    def wave(self, sess, lane_of_slot, tokens_by_lane, eligible_by_lane=None, max_count=None):
+        """One decode wave through glacier_hip_session_lane_weave_wave.
+        tokens_by_lane (uint32 array) is updated in place; returns
+        (slots, events)."""
+        los = np.ascontiguousarray(lane_of_slot, dtype=np.uint32)
+        mc = max_count or len(los)
+        slots = np.zeros(mc, dtype=np.uint32)
+        evs = (LaneEvent * mc)()
+        n = C.c_uint32(0)
+        rc = lib().glacier_hip_session_lane_weave_wave(sess.h, self.h, ptr(los), los.size,
+                                                       ptr(tokens_by_lane), ptr(eligible_by_lane),
+                                                       mc, ptr(slots), evs, C.byref(n))
+        check(rc, "lane_weave_wave", sess.model.ctx.h)
+        return slots[:n.value].tolist(), [evs[i] for i in range(n.value)]
 
     def chain_head(self):
         out = (C.c_uint8 * 32)()

@@ -484,6 +484,25 @@ int glacier_hip_lane_weave_slot(glacier_hip_lane_weave *lw, uint32_t slot,
 int glacier_hip_lane_weave_chain_head(glacier_hip_lane_weave *lw, uint8_t out[32]);
 int glacier_hip_lane_weave_state_sha256(glacier_hip_lane_weave *lw, uint8_t out[32]);
 
+/* One LaneWeave decode wave (the multi-request service loop of
+ * prepared_text_session.zig:1840-1885 with one token per service quantum):
+ * plan the next quanta of distinct lanes (at most max_count), run those
+ * lanes' tokens as ONE batched decode step on the device, then commit the
+ * quanta with serve_one in plan order. lane_of_slot[slot] names the session
+ * lane of each scheduler slot (slot_count entries). tokens_by_lane[lane] holds
+ * each lane's last token and receives its next one. eligible_by_lane:
+ * optional [session max_lanes][ceil(vocab/64)] masks (eligible argmax,
+ * sampling.zig:55-105). slots_out / events_out (optional) receive the
+ * committed slots and their Event-v1 records; count_out the number of quanta.
+ * A failed device step commits nothing: no KV row, token, sampler counter or
+ * scheduler event. NO_RUNNABLE when no lane is runnable. */
+int glacier_hip_session_lane_weave_wave(glacier_hip_session *s, glacier_hip_lane_weave *lw,
+                                        const uint32_t *lane_of_slot, uint32_t slot_count,
+                                        uint32_t *tokens_by_lane,
+                                        const uint64_t *eligible_by_lane, uint32_t max_count,
+                                        uint32_t *slots_out, glacier_hip_lane_event_t *events_out,
+                                        uint32_t *count_out);
+
 /* ---- synthetic random-init generator (host, deterministic) ---------------
  * Counter-based SplitMix64 streams keyed by (seed, tensor id):
  *  - INT4 codes: uniform nibbles u in 0..15 (decode u - 7 in [-7, 8]);

@@ -272,3 +272,66 @@ def test_cache_full_is_rejected_before_launch(gh, tiny):
         sess.step([0], [t])
     finally:
         sess.close()
+
+
+def test_lane_weave_waves_match_serial_oracle(gh, gctx, tiny, ora):
+    """BASELINE config 5 in miniature: four lanes with LaneWeave weights
+    (1, 2, 1, 3), eligible argmax over an all-ones mask, decoded in waves of
+    distinct lanes. Each lane's greedy tokens equal the oracle's independent
+    run of that lane, and the scheduler's event chain equals the oracle
+    scheduler's serial chain (admissions, every service quantum in order,
+    retirements, close)."""
+    from oracle import lane_weave as olw
+
+    host, om, m = tiny
+    weights = [1, 2, 1, 3]
+    prompts = [gh.synth_tokens(SEED, 300 + i, TINY["vocab_size"], 5 + 7 * i) for i in range(4)]
+    quanta = [6, 9, 4, 8]
+    cap = len(weights)
+    V = TINY["vocab_size"]
+    W = (V + 63) // 64
+    lim = dict(host_bytes=1 << 30, kv_bytes=1 << 30, queue_slots=cap)
+    sched = gh.LaneWeave(cap, lim, bank_epoch=7, scheduler_epoch=9, max_weight=4)
+    ref = olw.Scheduler(olw.Bank(cap, olw.limits(**lim), 7), cap, 9, bytes([0xA5]) + bytes(31), 4)
+    sess = gh.Session(m, max_lanes=cap, max_positions=64)
+    try:
+        tokens = np.zeros(cap, np.uint32)
+        got = [[] for _ in range(cap)]
+        for i in range(cap):
+            sp = dict(tenant_key=i + 1, request_key=10 * (i + 1), request_generation=1,
+                      resource_owner_key=100 * (i + 1), weight=weights[i], work_quanta=quanta[i],
+                      deadline_tick=0, claim=olw.claim(kv_bytes=4096, queue_slots=1))
+            ok, _, ev = sched.admit(gh.LaneWeave.spec(**{**sp, "claim": {"kv_bytes": 4096,
+                                                                          "queue_slots": 1}}))
+            assert ok and bytes(ev.event_sha256) == ref.admit(sp)[2]["event_sha256"]
+            sess.begin(i)
+            tokens[i] = sess.prefill(i, prompts[i])
+            got[i].append(int(tokens[i]))
+        elig = np.full((cap, W), ~np.uint64(0), np.uint64)
+        elig[:, -1] = (np.uint64(1) << np.uint64(V % 64)) - np.uint64(1) if V % 64 else elig[:, -1]
+        waves = 0
+        while True:
+            try:
+                slots, evs = sched.wave(sess, list(range(cap)), tokens, elig)
+            except gh.GlacierHipError as e:
+                assert e.code == gh.NO_RUNNABLE
+                break
+            waves += 1
+            assert len(set(slots)) == len(slots)
+            # the wave commits all its quanta first; lanes are retired after
+            for slot, ev in zip(slots, evs):
+                got[slot].append(int(tokens[slot]))
+                assert bytes(ev.event_sha256) == ref.serve_one()["event_sha256"]
+            for slot, ev in zip(slots, evs):
+                if ev.remaining_after == 0:
+                    want_retire = ref.retire(ref.handle_for(slot))["event_sha256"]
+                    rc, rev = sched.retire(ev.handle)
+                    assert rc == 0 and bytes(rev.event_sha256) == want_retire
+        rc, cev = sched.close()
+        assert rc == 0 and bytes(cev.event_sha256) == ref.close()["event_sha256"]
+        assert waves < sum(quanta)  # lanes really were batched
+        for i in range(cap):
+            want = om.generate(prompts[i], quanta[i] + 1)[0].tolist()
+            assert got[i] == want, (i, got[i], want)
+    finally:
+        sess.close()
