@@ -114,6 +114,20 @@ def time_gemv(gh, ctx, torch, n, k, m, reps, act):
             L.glacier_hip_int4_weight_destroy(w)
 
 
+def measured_traffic():
+    """HBM bytes per launch of the gate/up GEMV from the committed
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE summary (copy-kernel calibrated),
+    or None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "gemv_gate_up_7b_m1_pmc.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch"):
+                return int(line.split("=")[1])
+    except OSError:
+        pass
+    return None
+
+
 def auto_act(gh, n, k):
     return gh.ACT_F32 if (n > 65536 or k > 16384) else gh.ACT_Q8
 
@@ -347,7 +361,20 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-attention", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only a 1 GiB device-to-device copy, 5 times (HBM counter calibration "
+                         "under rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
     a = ap.parse_args()
+    if a.copy_probe:
+        import torch
+
+        src = torch.ones(1 << 30, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps(dict(copy_bytes=1 << 30, copies=5)))
+        return
     secs = set(a.sections.split(","))
     if "lanes" not in secs:
         a.lanes = 1
@@ -381,7 +408,7 @@ def main():
                 log("gemv", r)
                 gemv.append(r)
     roofline = dict(bound="hbm", achieved=dom["gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=dom["frac"], traffic=None) if dom else None
+                    frac=dom["frac"], traffic=measured_traffic()) if dom else None
     if a.gemv_only:
         print(json.dumps(dict(metric="int4 gemv HBM GB/s (7B gate/up, M=1)", value=dom["gbs"],
                               unit="GB/s", roofline=roofline, gemv=[dom])))

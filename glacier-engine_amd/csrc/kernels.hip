@@ -625,10 +625,13 @@ hipError_t launch_gather_rows(const float *table, const int32_t *ids, int M, int
 static constexpr int kMaxChunk = 512;
 static constexpr int kMaxGroup = 8;
 
+// Chunk length: short contexts stay one chunk (no combine launch); long ones
+// are split until (chunks x KV heads x rows) >= 2048 work items or chunks of
+// 64 positions, so a few long lanes still spread over the whole chip.
 int attention_chunk(int max_ctx, int num_kv_heads, int M) {
   int ch = kMaxChunk;
   if (max_ctx > 2 * kMaxChunk)
-    while (ch > 128 && ((max_ctx + ch - 1) / ch) * num_kv_heads * M < 256) ch /= 2;
+    while (ch > 64 && ((max_ctx + ch - 1) / ch) * num_kv_heads * M < 2048) ch /= 2;
   return ch;
 }
 
