@@ -127,6 +127,14 @@ hipError_t launch_attention(const float *q, const void *kv_pool, int kv_f16,
                             int num_heads, int num_kv_heads, int head_dim, int max_ctx,
                             float *scratch, float *out, hipStream_t st);
 
+// fp16-KV attention with an explicit launch shape: wp positions per wave,
+// nw waves per workgroup (tuning; launch_attention picks the shape).
+hipError_t launch_attention_f16(const float *q, const void *kv_pool, const int32_t *page_table,
+                                int max_pages, const int32_t *lane_of_row, const int32_t *ctx_len,
+                                int M, int layer, int num_layers, int num_heads, int num_kv_heads,
+                                int head_dim, int max_ctx, float *scratch, float *out,
+                                hipStream_t st, int wp, int nw);
+
 // Argmax over rows x n. Eligible variant when words != null. Results to
 // `result` [rows] = {index (u64), eligible_rows (u64), status (i32), pad}.
 struct ArgmaxResult {

@@ -623,6 +623,8 @@ hipError_t launch_gather_rows(const float *table, const int32_t *ids, int M, int
 // chunks: (max, sum, unnormalised output) records are merged by the combine
 // kernel with the usual log-sum-exp rescaling.
 static constexpr int kMaxChunk = 512;
+static constexpr int kF16Chunk = 256;     // positions per workgroup, fp16-KV kernel
+static constexpr int kMaxRecords = 1024;  // chunk records one combine merges
 static constexpr int kMaxGroup = 8;
 
 // Chunk length: short contexts stay one chunk (no combine launch); long ones
@@ -638,7 +640,9 @@ int attention_chunk(int max_ctx, int num_kv_heads, int M) {
 size_t attention_scratch_floats(int max_rows, int num_heads, int num_kv_heads, int head_dim,
                                 int max_ctx) {
   // the largest chunk-record set the planner produces for any row count
-  size_t most = 0;
+  // fp16 KV: launch_attention uses 256-position workgroups
+  size_t most = (size_t)max_rows * num_heads * ((max_ctx + kF16Chunk - 1) / kF16Chunk) *
+                (2 + head_dim);
   for (int M = 1; M <= max_rows; ++M) {
     const int ch = attention_chunk(max_ctx, num_kv_heads, M);
     const size_t nch = (size_t)(max_ctx + ch - 1) / ch;
@@ -699,7 +703,57 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   const float scale = 1.0f / sqrtf((float)HD);
   const size_t lay = (size_t)num_layers;
   // ---- scores ----
-  {
+  if constexpr (F16 && HPW == kMaxGroup) {
+    // fp16 KV: S[head][pos] = q . k on v_mfma_f32_16x16x16_f16, one 16-position
+    // tile (one page) per MFMA column block, query heads as MFMA rows. q is
+    // split into fp16 hi + lo parts (q = hi + lo to ~2^-22 relative); the
+    // fp16 x fp16 products are exact in the f32 accumulator, so the score is
+    // the f32 dot product up to summation order. Lane (c, j) loads 16-byte
+    // pieces 4*tt + c of position j's K row, which fixes the dims of k-chunk c
+    // in step s: 8 * (4 * (s / 2) + c) + 4 * (s % 2) + 0..3.
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    constexpr int S = HD / 16;
+    const int wv = t >> 6, l = t & 63, c = l >> 4, jr = l & 15;
+    h4 qhi[S], qlo[S];
+#pragma unroll
+    for (int st = 0; st < S; ++st) {
+      const int base = 8 * (4 * (st >> 1) + c) + 4 * (st & 1);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float v = jr < G ? sq[jr][base + e] : 0.0f;
+        const _Float16 hv = (_Float16)v;
+        qhi[st][e] = hv;
+        qlo[st][e] = (_Float16)(v - (float)hv);
+      }
+    }
+    for (int T = wv; T * 16 < n; T += 4) {
+      const int pl = T * 16 + jr;  // position within the chunk; page = spage[T]
+      const bool valid = pl < n;
+      const __half *krow = (const __half *)kv_pool +
+                           ((((size_t)spage[T] * lay + layer) * 2 + 0) * 16 + jr) * kv_dim +
+                           (size_t)h * HD;
+      uint4 kr[HD / 32];
+#pragma unroll
+      for (int tt = 0; tt < HD / 32; ++tt)
+        kr[tt] = valid ? *(const uint4 *)(krow + 8 * (4 * tt + c)) : make_uint4(0, 0, 0, 0);
+      f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int st = 0; st < S; ++st) {
+        const uint4 w = kr[st >> 1];
+        const uint2 bw = (st & 1) ? make_uint2(w.z, w.w) : make_uint2(w.x, w.y);
+        h4 b;
+        __builtin_memcpy(&b, &bw, 8);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(qhi[st], b, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(qlo[st], b, acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int head = 4 * c + r;
+        if (head < G && valid) ss[head][pl] = acc[r] * scale;
+      }
+    }
+  } else {
     float qf[HPW][8];
 #pragma unroll
     for (int g = 0; g < HPW; ++g)
@@ -837,26 +891,296 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// fp16-KV streaming attention: grid (chunks of 256 positions, KV heads,
+// rows); each of the 4 waves owns 64 positions (four 16-position tiles =
+// four pages). A wave issues all its K loads at once, computes the scores of
+// every query head of the group on MFMA (q split into fp16 hi + lo so the
+// products are exact in f32), runs the softmax over its positions, issues
+// all its V loads at once and accumulates P.V on VALU (16-byte V loads, 8
+// dims x 8 heads per lane). The waves' (max, sum, output) states merge by
+// log-sum-exp; one chunk writes the output, several write records for the
+// combine kernel. Softmax: exp(s - max) summed, output divided once by the
+// sum (forward.zig:515-528), with the max taken per wave and merged.
+// ---------------------------------------------------------------------------
+template <int HD, int WP, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_f16_kernel(
+    const float *q, const __half *pool, const int32_t *page_table, int max_pages,
+    const int32_t *lane_of_row, const int32_t *ctx_len, int layer, int num_layers, int Hq,
+    int Hkv, int n_chunks_max, int max_ctx, float *scratch, float *out) {
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  constexpr int S = HD / 16;   // MFMA steps over the head dim
+  constexpr int DL = HD / 8;   // lanes per V row in P.V (16 B each)
+  constexpr int PG = 64 / DL;  // position groups in P.V
+  constexpr int NT = WP / 16;  // 16-position tiles (pages) per wave
+  constexpr int CH = NW * WP;  // positions per workgroup
+  constexpr int NPOS = (WP + PG - 1) / PG;
+  const int t = threadIdx.x, wv = t >> 6, l = t & 63;
+  const int ch = blockIdx.x, h = blockIdx.y, m = blockIdx.z;
+  const int ctx = min(ctx_len[m], max_ctx);
+  const int j0 = ch * CH;
+  if (j0 >= ctx) return;
+  const int n = min(CH, ctx - j0);
+  const int nch = (ctx + CH - 1) / CH;
+  const int G = Hq / Hkv, qh0 = h * G;
+  const int kv_dim = Hkv * HD;
+  const int lane_id = lane_of_row[m];
+  const size_t lay = (size_t)num_layers;
+  __shared__ float ss[NW][kMaxGroup][WP];
+  __shared__ float pT[NW][WP][kMaxGroup];
+  __shared__ float so[NW][kMaxGroup][HD];
+  __shared__ float sm[NW][kMaxGroup], sl[NW][kMaxGroup];
+  const float scale = 1.0f / sqrtf((float)HD);
+  const int wbase = wv * WP;
+  const int wn = max(0, min(WP, n - wbase));
+  // this wave's page-table entries: tile T (16 positions) lives in ptab[T]
+  const int32_t *ptab = page_table + (size_t)lane_id * max_pages + (j0 + wbase) / 16;
+  const int c = l >> 4, jr = l & 15;
+  const int qg = l / DL, d8 = l % DL;
+  uint4 vr[NPOS];
+
+  // ---- one round of loads: q (straight into the MFMA operand), the K tiles
+  // and the V rows of this wave; then the scores on MFMA. Lane (c, jr) loads
+  // 16-byte pieces 4*tt + c of position jr's K row, so k-chunk c of step s
+  // covers dims 8 * (4 * (s / 2) + c) + 4 * (s % 2) + 0..3 ----
+  if (wn > 0) {
+    h4 qhi[S], qlo[S];
+    const float *qrow = q + ((size_t)m * Hq + qh0 + (jr < G ? jr : 0)) * HD;
+#pragma unroll
+    for (int st = 0; st < S; ++st) {
+      const int base = 8 * (4 * (st >> 1) + c) + 4 * (st & 1);
+      const float4 qv = jr < G ? *(const float4 *)(qrow + base) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float qa[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const _Float16 hv = (_Float16)qa[e];
+        qhi[st][e] = hv;
+        qlo[st][e] = (_Float16)(qa[e] - (float)hv);
+      }
+    }
+    uint4 kr[NT][HD / 32];
+#pragma unroll
+    for (int T = 0; T < NT; ++T) {
+      const bool valid = 16 * T + jr < wn;
+      const int page = 16 * T < wn ? ptab[T] : 0;
+      const __half *krow =
+          valid ? pool + ((((size_t)page * lay + layer) * 2 + 0) * 16 + jr) * kv_dim + (size_t)h * HD
+                : pool;
+#pragma unroll
+      for (int tt = 0; tt < HD / 32; ++tt)
+        kr[T][tt] = valid ? *(const uint4 *)(krow + 8 * (4 * tt + c)) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int T = 0; T < NT; ++T) {
+      if (16 * T >= wn) break;
+      f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int st = 0; st < S; ++st) {
+        const uint4 w = kr[T][st >> 1];
+        const uint2 bw = (st & 1) ? make_uint2(w.z, w.w) : make_uint2(w.x, w.y);
+        h4 b;
+        __builtin_memcpy(&b, &bw, 8);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(qhi[st], b, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(qlo[st], b, acc, 0, 0, 0);
+      }
+      const bool valid = 16 * T + jr < wn;
+      if (c < 2) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ss[wv][4 * c + r][16 * T + jr] = valid ? acc[r] * scale : -INFINITY;
+      }
+    }
+    // V rows now, so their latency hides under the softmax
+#pragma unroll
+    for (int i = 0; i < NPOS; ++i) {
+      const int pos = qg + i * PG;
+      const bool valid = pos < wn && pos < WP;
+      const int page = valid ? ptab[pos >> 4] : 0;
+      const __half *vrow =
+          valid ? pool + ((((size_t)page * lay + layer) * 2 + 1) * 16 + (pos & 15)) * kv_dim +
+                      (size_t)h * HD + 8 * d8
+                : pool;
+      vr[i] = valid ? *(const uint4 *)vrow : make_uint4(0, 0, 0, 0);
+    }
+  }
+  __syncthreads();
+  // ---- softmax over the wave's positions: lane (head l / 8, part l % 8) ----
+  {
+    constexpr int PP = WP / 8;  // positions per lane
+    const int hh = l >> 3, part = l & 7;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < PP; ++e) {
+      const int pos = part * PP + e;
+      if (pos < wn) mx = fmaxf(mx, ss[wv][hh][pos]);
+    }
+    for (int o = 1; o < 8; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    float sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < PP; ++e) {
+      const int pos = part * PP + e;
+      const float pe = pos < wn ? expf(ss[wv][hh][pos] - mx) : 0.0f;
+      pT[wv][pos][hh] = pe;
+      sum += pe;
+    }
+    for (int o = 1; o < 8; o <<= 1) sum += __shfl_xor(sum, o);
+    if (part == 0) {
+      sm[wv][hh] = mx;
+      sl[wv][hh] = sum;
+    }
+  }
+  __syncthreads();
+  // ---- P.V: lane (position group qg, 16-byte dim piece d8) ----
+  float acc[kMaxGroup][8];
+#pragma unroll
+  for (int g = 0; g < kMaxGroup; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
+  if (wn > 0) {
+#pragma unroll
+    for (int i = 0; i < NPOS; ++i) {
+      const int pos = qg + i * PG;
+      if (pos >= wn) break;
+      const __half *hp = (const __half *)&vr[i];
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = __half2float(hp[e]);
+      const float4 p0 = *(const float4 *)&pT[wv][pos][0];
+      const float4 p1 = *(const float4 *)&pT[wv][pos][4];
+      const float pg[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+      for (int g = 0; g < kMaxGroup; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pg[g], v[e], acc[g][e]);
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < kMaxGroup; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = acc[g][e];
+      for (int o = DL; o < 64; o <<= 1) v += __shfl_xor(v, o);
+      acc[g][e] = v;
+    }
+  if (l < DL) {
+#pragma unroll
+    for (int g = 0; g < kMaxGroup; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) so[wv][g][8 * l + e] = acc[g][e];
+  }
+  __syncthreads();
+  // ---- merge the waves (log-sum-exp) ----
+  for (int o = t; o < G * HD; o += 64 * NW) {
+    const int g = o / HD, d = o % HD;
+    float M = -INFINITY;
+    for (int w = 0; w < NW; ++w)
+      if (sl[w][g] > 0.0f) M = fmaxf(M, sm[w][g]);
+    float L = 0.0f, O = 0.0f;
+    for (int w = 0; w < NW; ++w)
+      if (sl[w][g] > 0.0f) {
+        const float f = expf(sm[w][g] - M);
+        L = fmaf(sl[w][g], f, L);
+        O = fmaf(so[w][g][d], f, O);
+      }
+    if (nch == 1) {
+      out[((size_t)m * Hq + qh0 + g) * HD + d] = O * (1.0f / L);
+    } else {
+      float *rec = scratch + (((size_t)m * Hq + qh0 + g) * n_chunks_max + ch) * (2 + HD);
+      if (d == 0) {
+        rec[0] = M;
+        rec[1] = L;
+      }
+      rec[2 + d] = O;
+    }
+  }
+}
+
+// Merge the chunk records of one (query head, row): every thread of the
+// workgroup takes part in each step, so the record count costs parallel
+// loads, not a serial chain.
 template <int HD>
-__global__ __launch_bounds__(HD) void attn_combine_kernel(const int32_t *ctx_len, int Hq,
-                                                          int chunk, int n_chunks_max,
-                                                          int max_ctx, const float *scratch,
-                                                          float *out) {
-  const int qh = blockIdx.x, m = blockIdx.y, d = threadIdx.x;
+__global__ __launch_bounds__(256) void attn_combine2_kernel(const int32_t *ctx_len, int Hq,
+                                                            int chunk, int n_chunks_max,
+                                                            int max_ctx, const float *scratch,
+                                                            float *out) {
+  const int qh = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
   const int ctx = min(ctx_len[m], max_ctx);
   const int nch = (ctx + chunk - 1) / chunk;
   if (nch <= 1) return;
   const float *rec0 = scratch + ((size_t)m * Hq + qh) * n_chunks_max * (2 + HD);
+  __shared__ float f[kMaxRecords];
+  __shared__ float red[4];
+  __shared__ float part[256 / HD][HD];
   float mx = -INFINITY;
-  for (int c = 0; c < nch; ++c) mx = fmaxf(mx, rec0[(size_t)c * (2 + HD)]);
-  float l = 0.0f, o = 0.0f;
-  for (int c = 0; c < nch; ++c) {
-    const float *rec = rec0 + (size_t)c * (2 + HD);
-    const float f = expf(rec[0] - mx);
-    l = fmaf(rec[1], f, l);
-    o = fmaf(rec[2 + d], f, o);
+  for (int c = t; c < nch; c += 256) mx = fmaxf(mx, rec0[(size_t)c * (2 + HD)]);
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((t & 63) == 0) red[t >> 6] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float lp = 0.0f;
+  for (int c = t; c < nch; c += 256) {
+    const float fc = expf(rec0[(size_t)c * (2 + HD)] - M);
+    f[c] = fc;
+    lp = fmaf(rec0[(size_t)c * (2 + HD) + 1], fc, lp);
   }
-  out[((size_t)m * Hq + qh) * HD + d] = o * (1.0f / l);
+  for (int o = 32; o > 0; o >>= 1) lp += __shfl_xor(lp, o);
+  if ((t & 63) == 0) red[t >> 6] = lp;
+  __syncthreads();
+  const float L = (red[0] + red[1]) + (red[2] + red[3]);
+  constexpr int NG = 256 / HD;
+  const int d = t % HD, g = t / HD;
+  float o = 0.0f;
+  for (int c = g; c < nch; c += NG) o = fmaf(rec0[(size_t)c * (2 + HD) + 2 + d], f[c], o);
+  part[g][d] = o;
+  __syncthreads();
+  if (g == 0) {
+    float tot = part[0][d];
+    for (int i = 1; i < NG; ++i) tot += part[i][d];
+    out[((size_t)m * Hq + qh) * HD + d] = tot * (1.0f / L);
+  }
+}
+
+hipError_t launch_attention_f16(const float *q, const void *kv_pool, const int32_t *page_table,
+                                int max_pages, const int32_t *lane_of_row, const int32_t *ctx_len,
+                                int M, int layer, int num_layers, int num_heads, int num_kv_heads,
+                                int head_dim, int max_ctx, float *scratch, float *out,
+                                hipStream_t st, int wp, int nw) {
+  if (num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > kMaxGroup)
+    return hipErrorInvalidValue;
+  const int chunk = wp * nw;
+  if (chunk > kF16Chunk || chunk % 16) return hipErrorInvalidValue;
+  const int nch = (max_ctx + chunk - 1) / chunk;
+  if (nch > kMaxRecords) return hipErrorInvalidValue;
+  dim3 grid(nch, num_kv_heads, M);
+  const __half *pool = (const __half *)kv_pool;
+#define GK_F16(HD, WP, NW)                                                                   \
+  hipLaunchKernelGGL((attn_f16_kernel<HD, WP, NW>), grid, dim3(64 * NW), 0, st, q, pool,     \
+                     page_table, max_pages, lane_of_row, ctx_len, layer, num_layers,         \
+                     num_heads, num_kv_heads, nch, max_ctx, scratch, out)
+#define GK_F16_HD(WP, NW)                                        \
+  do {                                                          \
+    if (head_dim == 64) GK_F16(64, WP, NW);                     \
+    else if (head_dim == 128) GK_F16(128, WP, NW);              \
+    else return hipErrorInvalidValue;                           \
+  } while (0)
+  if (wp == 64 && nw == 4) GK_F16_HD(64, 4);
+  else if (wp == 32 && nw == 4) GK_F16_HD(32, 4);
+  else if (wp == 32 && nw == 8) GK_F16_HD(32, 8);
+  else if (wp == 16 && nw == 8) GK_F16_HD(16, 8);
+  else if (wp == 16 && nw == 4) GK_F16_HD(16, 4);
+  else return hipErrorInvalidValue;
+#undef GK_F16_HD
+#undef GK_F16
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || nch <= 1) return e;
+  if (head_dim == 64)
+    hipLaunchKernelGGL((attn_combine2_kernel<64>), dim3(num_heads, M), dim3(256), 0, st, ctx_len,
+                       num_heads, chunk, nch, max_ctx, scratch, out);
+  else
+    hipLaunchKernelGGL((attn_combine2_kernel<128>), dim3(num_heads, M), dim3(256), 0, st, ctx_len,
+                       num_heads, chunk, nch, max_ctx, scratch, out);
+  return hipGetLastError();
 }
 
 hipError_t launch_attention(const float *q, const void *kv_pool, int kv_f16,
@@ -866,10 +1190,16 @@ hipError_t launch_attention(const float *q, const void *kv_pool, int kv_f16,
                             float *scratch, float *out, hipStream_t st) {
   if (num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > kMaxGroup)
     return hipErrorInvalidValue;
+  if (kv_f16)
+    return launch_attention_f16(q, kv_pool, page_table, max_pages, lane_of_row, ctx_len, M, layer,
+                                num_layers, num_heads, num_kv_heads, head_dim, max_ctx, scratch,
+                                out, st, 64, 4);
   const int chunk = attention_chunk(max_ctx, num_kv_heads, M);
+  if ((max_ctx + chunk - 1) / chunk > kMaxRecords) return hipErrorInvalidValue;
   const int nch = (max_ctx + chunk - 1) / chunk;
-  // few workgroups (batch-1 decode): one query head each, K/V re-read from L2
-  const bool per_head = nch * num_kv_heads * M < 64;
+  // few workgroups (batch-1 decode, f32 KV): one query head each; fp16 KV
+  // always groups the query heads of a KV head (MFMA scores)
+  const bool per_head = !kv_f16 && nch * num_kv_heads * M < 64;
   dim3 grid(nch, per_head ? num_heads : num_kv_heads, M);
 #define GK_ATT(HD, F)                                                                           \
   do {                                                                                          \
@@ -893,10 +1223,10 @@ hipError_t launch_attention(const float *q, const void *kv_pool, int kv_f16,
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || nch <= 1) return e;
   if (head_dim == 64)
-    hipLaunchKernelGGL((attn_combine_kernel<64>), dim3(num_heads, M), dim3(64), 0, st, ctx_len,
+    hipLaunchKernelGGL((attn_combine2_kernel<64>), dim3(num_heads, M), dim3(256), 0, st, ctx_len,
                        num_heads, chunk, nch, max_ctx, scratch, out);
   else
-    hipLaunchKernelGGL((attn_combine_kernel<128>), dim3(num_heads, M), dim3(128), 0, st,
+    hipLaunchKernelGGL((attn_combine2_kernel<128>), dim3(num_heads, M), dim3(256), 0, st,
                        ctx_len, num_heads, chunk, nch, max_ctx, scratch, out);
   return hipGetLastError();
 }
