@@ -18,6 +18,36 @@
 
 namespace gk {
 
+// Greedy candidate order (sampling.zig:194-206): a larger value wins, equal
+// values go to the lower index, a NaN never wins; bi < 0 means "none yet".
+static __device__ __forceinline__ bool arg_better(float v, long i, float bv, long bi) {
+  if (isnan(v)) return false;
+  if (bi < 0) return true;
+  return v > bv || (v == bv && i < bi);
+}
+
+static __device__ __forceinline__ void arg_merge(ArgPartial &p, const ArgPartial &q) {
+  if (q.i >= 0 && arg_better(q.v, q.i, p.v, p.i)) {
+    p.v = q.v;
+    p.i = q.i;
+  }
+  p.nan_flag |= q.nan_flag;
+  p.rows += q.rows;
+  p.bad_mask |= q.bad_mask;
+  p.nan0 |= q.nan0;
+}
+
+static __device__ __forceinline__ ArgPartial arg_shfl_xor(const ArgPartial &p, int o) {
+  ArgPartial q;
+  q.v = __shfl_xor(p.v, o);
+  q.i = __shfl_xor(p.i, o);
+  q.nan_flag = __shfl_xor(p.nan_flag, o);
+  q.rows = __shfl_xor(p.rows, o);
+  q.bad_mask = __shfl_xor(p.bad_mask, o);
+  q.nan0 = __shfl_xor(p.nan0, o);
+  return q;
+}
+
 static __device__ __forceinline__ float silu_mul(float g, float u) {
   // kernels.zig:465-520: g * (1 / (1 + exp(-g))) * u
   float sig = 1.0f / (1.0f + expf(-g));

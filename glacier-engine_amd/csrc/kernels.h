@@ -27,6 +27,20 @@ struct ActMeta {
   int32_t corr;
 };
 
+// Greedy candidate of one span of logits (sampling.zig:55-105, 194-206):
+// best (value, lowest index) among its eligible non-NaN entries (i = -1:
+// none), whether an eligible entry was NaN, how many entries were eligible,
+// whether mask bits beyond the vocabulary were set, and whether logit 0 is
+// NaN (the unmasked scan starts from index 0 and never leaves a NaN there).
+struct ArgPartial {
+  float v;
+  int nan_flag;
+  long i;
+  unsigned long long rows;
+  int bad_mask;
+  int nan0;
+};
+
 enum Epilogue : int {
   EPI_PLAIN = 0,   // y = sum (+ bias)
   EPI_RESID = 1,   // y = resid + sum
@@ -78,6 +92,13 @@ struct GemvArgs {
   int8_t *out_q;
   ActMeta *out_meta;
   int out_D;
+  // EPI_PLAIN only, fused greedy head (a reference LM head fused with its
+  // argmax over row tiles): every workgroup also reduces its logits of each
+  // activation row m to one candidate arg_parts[m * grid + workgroup],
+  // honouring the eligibility bits arg_words [M][arg_word_count] when set.
+  ArgPartial *arg_parts;
+  const uint64_t *arg_words;
+  long arg_word_count;
 };
 
 // Launch shape of one GEMV: RB row blocks per workgroup, KS waves per row
@@ -144,6 +165,14 @@ struct ArgmaxResult {
   int32_t pad;
 };
 size_t argmax_scratch_bytes(int rows, long n);
+// Candidates one fused-head GEMV writes per activation row (its grid size).
+int gemv_argmax_parts(int N, int K, int M, int D);
+// Final reduction of the fused head's candidates: parts [rows][nparts]; the
+// eligible variant (words != null) also counts the eligible rows and checks
+// the bits beyond n, as launch_argmax does.
+hipError_t launch_argmax_parts(const ArgPartial *parts, int nparts, long n, int rows,
+                               const uint64_t *words, long word_count, ArgmaxResult *result,
+                               hipStream_t st);
 hipError_t launch_argmax(const float *logits, long n, int rows, const uint64_t *words,
                          long word_count, void *scratch, uint32_t *counters,
                          ArgmaxResult *result, hipStream_t st);

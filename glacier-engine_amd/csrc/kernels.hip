@@ -19,6 +19,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 namespace gk {
 
@@ -105,9 +106,28 @@ __global__ __launch_bounds__(256) void prep_act_kernel(const void *x, int x_bf16
   float inv = 1.0f;
   if (norm_w) {
     float ss = 0.0f;
-    for (int i = t; i < K; i += 256) {
-      float v = load_x(x, x_bf16, row + i);
-      ss = fmaf(v, v, ss);
+    if (!x_bf16 && (K & 3) == 0) {
+      // every load of a pass is issued before the first is used: one memory
+      // round trip per 8192 elements instead of one per 256
+      constexpr int U = 8;
+      const float4 *x4 = (const float4 *)((const float *)x + row);
+      const int K4 = K >> 2;
+      for (int base = 0; base < K4; base += 256 * U) {
+        float4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int i = base + t + 256 * u;
+          v[u] = i < K4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          ss = fmaf(v[u].w, v[u].w, fmaf(v[u].z, v[u].z, fmaf(v[u].y, v[u].y, fmaf(v[u].x, v[u].x, ss))));
+      }
+    } else {
+      for (int i = t; i < K; i += 256) {
+        float v = load_x(x, x_bf16, row + i);
+        ss = fmaf(v, v, ss);
+      }
     }
     for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
     if ((t & 63) == 0) red[t >> 6] = ss;
@@ -212,13 +232,13 @@ GemvShape plan_gemv(int N, int K, int M, int D) {
 }
 
 // LDS of the fused input stage: planes, inverse RMS per row, per-wave
-// partial sums (up to 16 waves) and the staged input rows.
+// partial sums (up to 16 waves), the staged input rows and norm weights.
 static __host__ __device__ __forceinline__ size_t fused_rows_offset(int groups, int M, int D) {
   const size_t planes = (size_t)groups * ((size_t)D * M * 32 + (size_t)M * 8);
   return (planes + (size_t)M * 4 + (size_t)M * 16 * 4 + 15) & ~(size_t)15;
 }
 static size_t fused_stage_bytes(int K, int M, int D) {
-  return fused_rows_offset(K / 32, M, D) + (size_t)M * K * 4;
+  return fused_rows_offset(K / 32, M, D) + (size_t)(M + 1) * K * 4;  // rows + norm weights
 }
 
 bool gemv_fused_input_ok(int N, int K, int M, int D) {
@@ -269,20 +289,43 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
     if (a.x_in) {
       // Fused input stage: RMSNorm (kernels.zig:141-220) and the group
       // quantiser (int4_matmul.zig:380-398) of the whole input into LDS. The
-      // rows are first copied into LDS with one wide load per thread, so the
-      // reduction and the quantiser never wait on HBM/L2 round trips.
+      // rows and the norm weights are first copied into LDS with every load
+      // of a pass in flight at once, so the stage costs one L2 round trip and
+      // the reduction and the quantiser never wait on memory.
       const int nthr = blockDim.x, nw = nthr >> 6;
       float *inv = (float *)(smem + qbytes + mbytes);
       float *ssw = inv + M;                       // [M][nw] per-wave partial sums
-      float *xs = (float *)(smem + fused_rows_offset(G, M, D));  // [M][K] the input rows
-      const float4 *src4 = (const float4 *)a.x_in;
-      float4 *xs4 = (float4 *)xs;
-      for (int i = threadIdx.x; i < M * (a.K >> 2); i += nthr) xs4[i] = src4[i];
+      float *xs = (float *)(smem + fused_rows_offset(G, M, D));  // [M][K] rows, then [K] norm
+      const float *nws = xs + (size_t)M * a.K;
+      {
+        constexpr int SU = 8;
+        const int n4 = M * (a.K >> 2), w4 = a.norm_w ? (a.K >> 2) : 0;
+        const float4 *src4 = (const float4 *)a.x_in;
+        const float4 *nrm4 = (const float4 *)a.norm_w;
+        float4 *xs4 = (float4 *)xs;
+        for (int base = 0; base < n4 + w4; base += nthr * SU) {
+          float4 v[SU];
+#pragma unroll
+          for (int u = 0; u < SU; ++u) {
+            const int i = base + (int)threadIdx.x + nthr * u;
+            v[u] = i < n4 ? src4[i] : (i < n4 + w4 ? nrm4[i - n4] : make_float4(0.f, 0.f, 0.f, 0.f));
+          }
+#pragma unroll
+          for (int u = 0; u < SU; ++u) {
+            const int i = base + (int)threadIdx.x + nthr * u;
+            if (i < n4 + w4) xs4[i] = v[u];
+          }
+        }
+      }
       __syncthreads();
       if (a.norm_w) {
+        const float4 *xs4 = (const float4 *)xs;
         for (int m = 0; m < M; ++m) {
           float ss = 0.0f;
-          for (int i = threadIdx.x; i < a.K; i += nthr) ss = fmaf(xs[m * a.K + i], xs[m * a.K + i], ss);
+          for (int i = threadIdx.x; i < (a.K >> 2); i += nthr) {
+            const float4 v = xs4[m * (a.K >> 2) + i];
+            ss = fmaf(v.w, v.w, fmaf(v.z, v.z, fmaf(v.y, v.y, fmaf(v.x, v.x, ss))));
+          }
           for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
           if (lane == 0) ssw[m * nw + wave] = ss;
         }
@@ -301,7 +344,7 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
         float v = xs[m * a.K + k];
         if (a.norm_w) {
           const float tt = v * inv[m];
-          v = tt * a.norm_w[k];
+          v = tt * nws[k];
         }
         quantize_group<D>(v, hl, g, m, M, (int8_t *)smem, (ActMeta *)(smem + qbytes));
       }
@@ -479,6 +522,50 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
         store_output(a, nb, n_local, m, tot, partner);
       }
     }
+  if (a.arg_parts) {
+    // Fused greedy head: this workgroup's best eligible logit of each row m
+    // (arg_better order), reduced over its 16-row blocks and then its waves.
+    __syncthreads();  // the reduction / planes area of smem is reused
+    ArgPartial *wpart = (ArgPartial *)smem;  // [waves][M]
+    const int nwv = (int)(blockDim.x >> 6);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = mt * 16 + c * 4 + r;
+        ArgPartial p;
+        p.v = 0.0f;
+        p.i = -1;
+        p.nan_flag = 0;
+        p.rows = 0;
+        p.bad_mask = 0;
+        p.nan0 = 0;
+        if (lead && m < M) {
+          const int nrow = nb * 16 + n_local;
+          const float v = a.bias ? a.bias[nrow] + acc[mt][r] : acc[mt][r];
+          const bool elig =
+              !a.arg_words ||
+              ((a.arg_words[(size_t)m * a.arg_word_count + (nrow >> 6)] >> (nrow & 63)) & 1ull);
+          if (elig) {
+            if (isnan(v)) p.nan_flag = 1;
+            else {
+              p.v = v;
+              p.i = nrow;
+            }
+          }
+          if (nrow == 0 && isnan(v)) p.nan0 = 1;
+        }
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) arg_merge(p, arg_shfl_xor(p, o));
+        if (n_local == 0 && m < M) wpart[wave * M + m] = p;
+      }
+    __syncthreads();
+    for (int m = threadIdx.x; m < M; m += blockDim.x) {
+      ArgPartial p = wpart[m];
+      for (int w = 1; w < nwv; ++w) arg_merge(p, wpart[w * M + m]);
+      a.arg_parts[(size_t)m * gridDim.x + blockIdx.x] = p;
+    }
+  }
   if (!emit_planes) return;
   __syncthreads();
   // Groups of 32 consecutive SwiGLU outputs = 4 row blocks; each half-wave
@@ -506,6 +593,7 @@ hipError_t launch_gemv(const GemvArgs &a0, hipStream_t st) {
   const bool emit_planes = a.epi == EPI_SWIGLU && a.out_q;
   if (emit_planes && ((a.N / 16) % 4 || !a.out_meta || (a.out_D != 1 && a.out_D != 3)))
     return hipErrorInvalidValue;
+  if (a.arg_parts && (a.epi != EPI_PLAIN || !a.y)) return hipErrorInvalidValue;
   GemvShape p = plan_gemv(a.N, a.K, a.M, a.D);
   if (a.x_in) {
     if (!gemv_fused_input_ok(a.N, a.K, a.M, a.D)) return hipErrorInvalidValue;
@@ -532,6 +620,12 @@ hipError_t launch_gemv(const GemvArgs &a0, hipStream_t st) {
     p.lds_bytes = std::max(p.lds_a ? planes_bytes(a.K / 32, a.M, a.D) + a.M * 4 : 0, red);
     if (a.x_in) p.lds_bytes = std::max(p.lds_bytes, fused_stage_bytes(a.K, a.M, a.D));
     if (emit_planes && p.rb % 4) return hipErrorInvalidValue;
+  }
+  if (a.arg_parts) {
+    // one candidate per (wave, row) in LDS; the candidate array holds one
+    // entry per workgroup of the planned grid
+    if (a.ksplit_override > 0) return hipErrorInvalidValue;
+    p.lds_bytes = std::max(p.lds_bytes, (size_t)p.waves * a.M * sizeof(ArgPartial));
   }
   a.ksplit = p.ksplit;
   a.ksplit_lds_off = (int)((p.lds_bytes + 15) & ~(size_t)15);
@@ -623,7 +717,7 @@ hipError_t launch_gather_rows(const float *table, const int32_t *ids, int M, int
 // chunks: (max, sum, unnormalised output) records are merged by the combine
 // kernel with the usual log-sum-exp rescaling.
 static constexpr int kMaxChunk = 512;
-static constexpr int kF16Chunk = 256;     // positions per workgroup, fp16-KV kernel
+static constexpr int kF16MinChunk = 64;   // fewest positions per fp16-KV workgroup
 static constexpr int kMaxRecords = 1024;  // chunk records one combine merges
 static constexpr int kMaxGroup = 8;
 
@@ -640,8 +734,8 @@ int attention_chunk(int max_ctx, int num_kv_heads, int M) {
 size_t attention_scratch_floats(int max_rows, int num_heads, int num_kv_heads, int head_dim,
                                 int max_ctx) {
   // the largest chunk-record set the planner produces for any row count
-  // fp16 KV: launch_attention uses 256-position workgroups
-  size_t most = (size_t)max_rows * num_heads * ((max_ctx + kF16Chunk - 1) / kF16Chunk) *
+  // fp16 KV: workgroups of at least kF16MinChunk positions
+  size_t most = (size_t)max_rows * num_heads * ((max_ctx + kF16MinChunk - 1) / kF16MinChunk) *
                 (2 + head_dim);
   for (int M = 1; M <= max_rows; ++M) {
     const int ch = attention_chunk(max_ctx, num_kv_heads, M);
@@ -892,31 +986,39 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// fp16-KV streaming attention: grid (chunks of 256 positions, KV heads,
-// rows); each of the 4 waves owns 64 positions (four 16-position tiles =
-// four pages). A wave issues all its K loads at once, computes the scores of
-// every query head of the group on MFMA (q split into fp16 hi + lo so the
-// products are exact in f32), runs the softmax over its positions, issues
-// all its V loads at once and accumulates P.V on VALU (16-byte V loads, 8
-// dims x 8 heads per lane). The waves' (max, sum, output) states merge by
-// log-sum-exp; one chunk writes the output, several write records for the
-// combine kernel. Softmax: exp(s - max) summed, output divided once by the
-// sum (forward.zig:515-528), with the max taken per wave and merged.
+// fp16-KV streaming attention: grid (chunks, KV heads, rows); a workgroup of
+// NW waves owns NW * NT pages of one (row, KV head) and each wave NT pages
+// (16 positions each). A wave reads its page ids once (wave-uniform scalar
+// loads), then issues every K and V load of its pages together, and keeps
+// the whole softmax in registers:
+//   scores  S^T[pos][head] = K . Q^T on v_mfma_f32_16x16x16f16, q split into
+//           fp16 hi + lo so every product is exact in f32; lane (c, j) ends
+//           with head j's scores of positions 4c + r (r = 0..3) of a page,
+//   softmax max / exp / sum per head over the wave's positions (in-lane, then
+//           two cross-row shuffles),
+//   P.V     on v_mfma_f32_16x16x4f32 (f32 operands): those same registers are
+//           the A operand (k = the four positions 4c + r for fixed r), and
+//           lane (c, j) supplies V[4c + r][DPL * j + b] from one 16-byte (hd
+//           128) or 8-byte (hd 64) load of a V row, so V is read row-major
+//           and fully coalesced.
+// The waves' (max, sum, output) states merge by log-sum-exp in LDS; one chunk
+// writes the output normalised once by the sum (forward.zig:515-528), several
+// write (max, sum, output) records for the combine kernel.
 // ---------------------------------------------------------------------------
-template <int HD, int WP, int NW>
+template <int HD, int NT, int NW>
 __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(
     const float *q, const __half *pool, const int32_t *page_table, int max_pages,
     const int32_t *lane_of_row, const int32_t *ctx_len, int layer, int num_layers, int Hq,
     int Hkv, int n_chunks_max, int max_ctx, float *scratch, float *out) {
   typedef _Float16 h4 __attribute__((ext_vector_type(4)));
   typedef float f4 __attribute__((ext_vector_type(4)));
-  constexpr int S = HD / 16;   // MFMA steps over the head dim
-  constexpr int DL = HD / 8;   // lanes per V row in P.V (16 B each)
-  constexpr int PG = 64 / DL;  // position groups in P.V
-  constexpr int NT = WP / 16;  // 16-position tiles (pages) per wave
-  constexpr int CH = NW * WP;  // positions per workgroup
-  constexpr int NPOS = (WP + PG - 1) / PG;
-  const int t = threadIdx.x, wv = t >> 6, l = t & 63;
+  constexpr int S = HD / 16;    // f16 MFMA steps over the head dim
+  constexpr int DPL = HD / 16;  // dims per lane in P.V (one MFMA block each)
+  constexpr int WP = 16 * NT;   // positions per wave
+  constexpr int CH = NW * WP;   // positions per workgroup
+  typedef typename std::conditional<DPL == 8, uint4, uint2>::type vrow_t;
+  const int t = threadIdx.x, l = t & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
   const int ch = blockIdx.x, h = blockIdx.y, m = blockIdx.z;
   const int ctx = min(ctx_len[m], max_ctx);
   const int j0 = ch * CH;
@@ -925,32 +1027,53 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(
   const int nch = (ctx + CH - 1) / CH;
   const int G = Hq / Hkv, qh0 = h * G;
   const int kv_dim = Hkv * HD;
-  const int lane_id = lane_of_row[m];
   const size_t lay = (size_t)num_layers;
-  __shared__ float ss[NW][kMaxGroup][WP];
-  __shared__ float pT[NW][WP][kMaxGroup];
   __shared__ float so[NW][kMaxGroup][HD];
-  __shared__ float sm[NW][kMaxGroup], sl[NW][kMaxGroup];
+  __shared__ float sm[NW][16], sl[NW][16];
   const float scale = 1.0f / sqrtf((float)HD);
   const int wbase = wv * WP;
   const int wn = max(0, min(WP, n - wbase));
-  // this wave's page-table entries: tile T (16 positions) lives in ptab[T]
-  const int32_t *ptab = page_table + (size_t)lane_id * max_pages + (j0 + wbase) / 16;
-  const int c = l >> 4, jr = l & 15;
-  const int qg = l / DL, d8 = l % DL;
-  uint4 vr[NPOS];
+  const int c = l >> 4, j = l & 15;
 
-  // ---- one round of loads: q (straight into the MFMA operand), the K tiles
-  // and the V rows of this wave; then the scores on MFMA. Lane (c, jr) loads
-  // 16-byte pieces 4*tt + c of position jr's K row, so k-chunk c of step s
-  // covers dims 8 * (4 * (s / 2) + c) + 4 * (s % 2) + 0..3 ----
+  f4 o[DPL];
+#pragma unroll
+  for (int b = 0; b < DPL; ++b) o[b] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  float mx = -INFINITY, sum = 0.0f;
   if (wn > 0) {
+    // page ids of this wave's pages (wave-uniform)
+    const int32_t *ptab = page_table + (size_t)lane_of_row[m] * max_pages + (j0 + wbase) / 16;
+    int pg[NT];
+#pragma unroll
+    for (int T = 0; T < NT; ++T) pg[T] = 16 * T < wn ? ptab[T] : 0;
+    // K: lane (c, j) loads 16-byte pieces 4 * tt + c of position j of each
+    // page; V: lane (c, j) loads dims DPL*j .. DPL*j + DPL-1 of positions
+    // 4c + r (r = 0..3) of each page
+    uint4 kr[NT][HD / 32];
+    vrow_t vr[NT][4];
+#pragma unroll
+    for (int T = 0; T < NT; ++T) {
+      const size_t pbase = ((size_t)pg[T] * lay + layer) * 2;
+      const bool kval = 16 * T + j < wn;
+      const __half *krow = pool + ((pbase + 0) * 16 + j) * kv_dim + (size_t)h * HD;
+#pragma unroll
+      for (int tt = 0; tt < HD / 32; ++tt)
+        kr[T][tt] = kval ? *(const uint4 *)(krow + 8 * (4 * tt + c)) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int pos = 4 * c + r;
+        const __half *vrow = pool + ((pbase + 1) * 16 + pos) * kv_dim + (size_t)h * HD + DPL * j;
+        if (16 * T + pos < wn) vr[T][r] = *(const vrow_t *)vrow;
+        else __builtin_memset(&vr[T][r], 0, sizeof(vrow_t));
+      }
+    }
+    // q as the B operand (after the K/V loads are in flight): lane (c, j)
+    // holds head j's dims of k-chunk c
     h4 qhi[S], qlo[S];
-    const float *qrow = q + ((size_t)m * Hq + qh0 + (jr < G ? jr : 0)) * HD;
+    const float *qrow = q + ((size_t)m * Hq + qh0 + (j < G ? j : 0)) * HD;
 #pragma unroll
     for (int st = 0; st < S; ++st) {
       const int base = 8 * (4 * (st >> 1) + c) + 4 * (st & 1);
-      const float4 qv = jr < G ? *(const float4 *)(qrow + base) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 qv = j < G ? *(const float4 *)(qrow + base) : make_float4(0.f, 0.f, 0.f, 0.f);
       const float qa[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -959,123 +1082,71 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(
         qlo[st][e] = (_Float16)(qa[e] - (float)hv);
       }
     }
-    uint4 kr[NT][HD / 32];
+    // scores: S^T = K . Q^T, one 16x16 tile per page
+    f4 sc[NT];
 #pragma unroll
     for (int T = 0; T < NT; ++T) {
-      const bool valid = 16 * T + jr < wn;
-      const int page = 16 * T < wn ? ptab[T] : 0;
-      const __half *krow =
-          valid ? pool + ((((size_t)page * lay + layer) * 2 + 0) * 16 + jr) * kv_dim + (size_t)h * HD
-                : pool;
-#pragma unroll
-      for (int tt = 0; tt < HD / 32; ++tt)
-        kr[T][tt] = valid ? *(const uint4 *)(krow + 8 * (4 * tt + c)) : make_uint4(0, 0, 0, 0);
-    }
-#pragma unroll
-    for (int T = 0; T < NT; ++T) {
-      if (16 * T >= wn) break;
       f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int st = 0; st < S; ++st) {
         const uint4 w = kr[T][st >> 1];
         const uint2 bw = (st & 1) ? make_uint2(w.z, w.w) : make_uint2(w.x, w.y);
-        h4 b;
-        __builtin_memcpy(&b, &bw, 8);
-        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(qhi[st], b, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(qlo[st], b, acc, 0, 0, 0);
+        h4 a;
+        __builtin_memcpy(&a, &bw, 8);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qhi[st], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qlo[st], acc, 0, 0, 0);
       }
-      const bool valid = 16 * T + jr < wn;
-      if (c < 2) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) ss[wv][4 * c + r][16 * T + jr] = valid ? acc[r] * scale : -INFINITY;
+      for (int r = 0; r < 4; ++r) {
+        const float v = acc[r] * scale;
+        sc[T][r] = 16 * T + 4 * c + r < wn ? v : -INFINITY;
+        mx = fmaxf(mx, sc[T][r]);
       }
     }
-    // V rows now, so their latency hides under the softmax
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
 #pragma unroll
-    for (int i = 0; i < NPOS; ++i) {
-      const int pos = qg + i * PG;
-      const bool valid = pos < wn && pos < WP;
-      const int page = valid ? ptab[pos >> 4] : 0;
-      const __half *vrow =
-          valid ? pool + ((((size_t)page * lay + layer) * 2 + 1) * 16 + (pos & 15)) * kv_dim +
-                      (size_t)h * HD + 8 * d8
-                : pool;
-      vr[i] = valid ? *(const uint4 *)vrow : make_uint4(0, 0, 0, 0);
-    }
+    for (int T = 0; T < NT; ++T)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = expf(sc[T][r] - mx);
+        sc[T][r] = p;
+        sum += p;
+      }
+    sum += __shfl_xor(sum, 16);
+    sum += __shfl_xor(sum, 32);
+    // P.V: A = P[head][pos 4c + r] (this lane's own registers), B = V
+#pragma unroll
+    for (int T = 0; T < NT; ++T)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const __half *hv = (const __half *)&vr[T][r];
+#pragma unroll
+        for (int b = 0; b < DPL; ++b)
+          o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(sc[T][r], __half2float(hv[b]), o[b], 0, 0, 0);
+      }
   }
-  __syncthreads();
-  // ---- softmax over the wave's positions: lane (head l / 8, part l % 8) ----
-  {
-    constexpr int PP = WP / 8;  // positions per lane
-    const int hh = l >> 3, part = l & 7;
-    float mx = -INFINITY;
+  // lane (c, j) holds O[head 4c + r][dim DPL * j + b]
+  if (c < 2) {
 #pragma unroll
-    for (int e = 0; e < PP; ++e) {
-      const int pos = part * PP + e;
-      if (pos < wn) mx = fmaxf(mx, ss[wv][hh][pos]);
-    }
-    for (int o = 1; o < 8; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    float sum = 0.0f;
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int e = 0; e < PP; ++e) {
-      const int pos = part * PP + e;
-      const float pe = pos < wn ? expf(ss[wv][hh][pos] - mx) : 0.0f;
-      pT[wv][pos][hh] = pe;
-      sum += pe;
-    }
-    for (int o = 1; o < 8; o <<= 1) sum += __shfl_xor(sum, o);
-    if (part == 0) {
-      sm[wv][hh] = mx;
-      sl[wv][hh] = sum;
-    }
+      for (int b = 0; b < DPL; ++b) so[wv][4 * c + r][DPL * j + b] = o[b][r];
   }
-  __syncthreads();
-  // ---- P.V: lane (position group qg, 16-byte dim piece d8) ----
-  float acc[kMaxGroup][8];
-#pragma unroll
-  for (int g = 0; g < kMaxGroup; ++g)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[g][e] = 0.0f;
-  if (wn > 0) {
-#pragma unroll
-    for (int i = 0; i < NPOS; ++i) {
-      const int pos = qg + i * PG;
-      if (pos >= wn) break;
-      const __half *hp = (const __half *)&vr[i];
-      float v[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = __half2float(hp[e]);
-      const float4 p0 = *(const float4 *)&pT[wv][pos][0];
-      const float4 p1 = *(const float4 *)&pT[wv][pos][4];
-      const float pg[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-#pragma unroll
-      for (int g = 0; g < kMaxGroup; ++g)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(pg[g], v[e], acc[g][e]);
-    }
-  }
-#pragma unroll
-  for (int g = 0; g < kMaxGroup; ++g)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float v = acc[g][e];
-      for (int o = DL; o < 64; o <<= 1) v += __shfl_xor(v, o);
-      acc[g][e] = v;
-    }
-  if (l < DL) {
-#pragma unroll
-    for (int g = 0; g < kMaxGroup; ++g)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) so[wv][g][8 * l + e] = acc[g][e];
+  if (c == 0) {
+    sm[wv][j] = mx;
+    sl[wv][j] = sum;
   }
   __syncthreads();
   // ---- merge the waves (log-sum-exp) ----
-  for (int o = t; o < G * HD; o += 64 * NW) {
-    const int g = o / HD, d = o % HD;
+  for (int oi = t; oi < G * HD; oi += 64 * NW) {
+    const int g = oi / HD, d = oi % HD;
     float M = -INFINITY;
+#pragma unroll
     for (int w = 0; w < NW; ++w)
       if (sl[w][g] > 0.0f) M = fmaxf(M, sm[w][g]);
     float L = 0.0f, O = 0.0f;
+#pragma unroll
     for (int w = 0; w < NW; ++w)
       if (sl[w][g] > 0.0f) {
         const float f = expf(sm[w][g] - M);
@@ -1096,48 +1167,81 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(
 }
 
 // Merge the chunk records of one (query head, row): every thread of the
-// workgroup takes part in each step, so the record count costs parallel
-// loads, not a serial chain.
+// workgroup takes part in each step and issues all of its record loads of a
+// step before using them, so the record count costs a few parallel memory
+// round trips, not a serial chain.
+static constexpr int kCombineThreads = 512;
 template <int HD>
-__global__ __launch_bounds__(256) void attn_combine2_kernel(const int32_t *ctx_len, int Hq,
-                                                            int chunk, int n_chunks_max,
-                                                            int max_ctx, const float *scratch,
-                                                            float *out) {
+__global__ __launch_bounds__(kCombineThreads) void attn_combine2_kernel(
+    const int32_t *ctx_len, int Hq, int chunk, int n_chunks_max, int max_ctx,
+    const float *scratch, float *out) {
+  constexpr int NTH = kCombineThreads, NG = NTH / HD, U = 8, RPT = kMaxRecords / NTH;
   const int qh = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
   const int ctx = min(ctx_len[m], max_ctx);
   const int nch = (ctx + chunk - 1) / chunk;
   if (nch <= 1) return;
   const float *rec0 = scratch + ((size_t)m * Hq + qh) * n_chunks_max * (2 + HD);
   __shared__ float f[kMaxRecords];
-  __shared__ float red[4];
-  __shared__ float part[256 / HD][HD];
+  __shared__ float redm[NTH / 64], redl[NTH / 64];
+  __shared__ float part[NG][HD];
+  float mc[RPT], lc[RPT];
   float mx = -INFINITY;
-  for (int c = t; c < nch; c += 256) mx = fmaxf(mx, rec0[(size_t)c * (2 + HD)]);
+#pragma unroll
+  for (int u = 0; u < RPT; ++u) {
+    const int c = t + NTH * u;
+    mc[u] = c < nch ? rec0[(size_t)c * (2 + HD)] : -INFINITY;
+    lc[u] = c < nch ? rec0[(size_t)c * (2 + HD) + 1] : 0.0f;
+    mx = fmaxf(mx, mc[u]);
+  }
   for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-  if ((t & 63) == 0) red[t >> 6] = mx;
+  if ((t & 63) == 0) redm[t >> 6] = mx;
   __syncthreads();
-  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  __syncthreads();
+  float M = redm[0];
+#pragma unroll
+  for (int w = 1; w < NTH / 64; ++w) M = fmaxf(M, redm[w]);
   float lp = 0.0f;
-  for (int c = t; c < nch; c += 256) {
-    const float fc = expf(rec0[(size_t)c * (2 + HD)] - M);
-    f[c] = fc;
-    lp = fmaf(rec0[(size_t)c * (2 + HD) + 1], fc, lp);
+#pragma unroll
+  for (int u = 0; u < RPT; ++u) {
+    const int c = t + NTH * u;
+    if (c < nch) {
+      const float fc = expf(mc[u] - M);
+      f[c] = fc;
+      lp = fmaf(lc[u], fc, lp);
+    }
   }
   for (int o = 32; o > 0; o >>= 1) lp += __shfl_xor(lp, o);
-  if ((t & 63) == 0) red[t >> 6] = lp;
+  if ((t & 63) == 0) redl[t >> 6] = lp;
   __syncthreads();
-  const float L = (red[0] + red[1]) + (red[2] + red[3]);
-  constexpr int NG = 256 / HD;
+  float L = 0.0f;
+#pragma unroll
+  for (int w = 0; w < NTH / 64; ++w) L += redl[w];
   const int d = t % HD, g = t / HD;
-  float o = 0.0f;
-  for (int c = g; c < nch; c += NG) o = fmaf(rec0[(size_t)c * (2 + HD) + 2 + d], f[c], o);
-  part[g][d] = o;
+  float o[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) o[u] = 0.0f;
+  for (int c0 = g; c0 < nch; c0 += NG * U) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + NG * u;
+      v[u] = c < nch ? rec0[(size_t)c * (2 + HD) + 2 + d] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + NG * u;
+      if (c < nch) o[u] = fmaf(v[u], f[c], o[u]);
+    }
+  }
+  float tot = 0.0f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) tot += o[u];
+  part[g][d] = tot;
   __syncthreads();
   if (g == 0) {
-    float tot = part[0][d];
-    for (int i = 1; i < NG; ++i) tot += part[i][d];
-    out[((size_t)m * Hq + qh) * HD + d] = tot * (1.0f / L);
+    float acc = part[0][d];
+#pragma unroll
+    for (int i = 1; i < NG; ++i) acc += part[i][d];
+    out[((size_t)m * Hq + qh) * HD + d] = acc * (1.0f / L);
   }
 }
 
@@ -1149,36 +1253,36 @@ hipError_t launch_attention_f16(const float *q, const void *kv_pool, const int32
   if (num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > kMaxGroup)
     return hipErrorInvalidValue;
   const int chunk = wp * nw;
-  if (chunk > kF16Chunk || chunk % 16) return hipErrorInvalidValue;
+  if (chunk < kF16MinChunk || wp % 16) return hipErrorInvalidValue;
   const int nch = (max_ctx + chunk - 1) / chunk;
   if (nch > kMaxRecords) return hipErrorInvalidValue;
   dim3 grid(nch, num_kv_heads, M);
   const __half *pool = (const __half *)kv_pool;
-#define GK_F16(HD, WP, NW)                                                                   \
-  hipLaunchKernelGGL((attn_f16_kernel<HD, WP, NW>), grid, dim3(64 * NW), 0, st, q, pool,     \
+#define GK_F16(HD, NT, NW)                                                                   \
+  hipLaunchKernelGGL((attn_f16_kernel<HD, NT, NW>), grid, dim3(64 * NW), 0, st, q, pool,     \
                      page_table, max_pages, lane_of_row, ctx_len, layer, num_layers,         \
                      num_heads, num_kv_heads, nch, max_ctx, scratch, out)
-#define GK_F16_HD(WP, NW)                                        \
+#define GK_F16_HD(NT, NW)                                        \
   do {                                                          \
-    if (head_dim == 64) GK_F16(64, WP, NW);                     \
-    else if (head_dim == 128) GK_F16(128, WP, NW);              \
+    if (head_dim == 64) GK_F16(64, NT, NW);                     \
+    else if (head_dim == 128) GK_F16(128, NT, NW);              \
     else return hipErrorInvalidValue;                           \
   } while (0)
-  if (wp == 64 && nw == 4) GK_F16_HD(64, 4);
-  else if (wp == 32 && nw == 4) GK_F16_HD(32, 4);
-  else if (wp == 32 && nw == 8) GK_F16_HD(32, 8);
-  else if (wp == 16 && nw == 8) GK_F16_HD(16, 8);
-  else if (wp == 16 && nw == 4) GK_F16_HD(16, 4);
+  if (wp == 16 && nw == 4) GK_F16_HD(1, 4);
+  else if (wp == 16 && nw == 8) GK_F16_HD(1, 8);
+  else if (wp == 16 && nw == 16) GK_F16_HD(1, 16);
+  else if (wp == 32 && nw == 4) GK_F16_HD(2, 4);
+  else if (wp == 32 && nw == 8) GK_F16_HD(2, 8);
   else return hipErrorInvalidValue;
 #undef GK_F16_HD
 #undef GK_F16
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || nch <= 1) return e;
   if (head_dim == 64)
-    hipLaunchKernelGGL((attn_combine2_kernel<64>), dim3(num_heads, M), dim3(256), 0, st, ctx_len,
+    hipLaunchKernelGGL((attn_combine2_kernel<64>), dim3(num_heads, M), dim3(kCombineThreads), 0, st, ctx_len,
                        num_heads, chunk, nch, max_ctx, scratch, out);
   else
-    hipLaunchKernelGGL((attn_combine2_kernel<128>), dim3(num_heads, M), dim3(256), 0, st, ctx_len,
+    hipLaunchKernelGGL((attn_combine2_kernel<128>), dim3(num_heads, M), dim3(kCombineThreads), 0, st, ctx_len,
                        num_heads, chunk, nch, max_ctx, scratch, out);
   return hipGetLastError();
 }
@@ -1190,10 +1294,16 @@ hipError_t launch_attention(const float *q, const void *kv_pool, int kv_f16,
                             float *scratch, float *out, hipStream_t st) {
   if (num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > kMaxGroup)
     return hipErrorInvalidValue;
-  if (kv_f16)
+  if (kv_f16) {
+    // one page per wave; workgroups of 16 waves when the whole context fits
+    // one (no combine), else 4 waves for few (row, KV head) pairs and 8 for
+    // many, which keeps about 1000 or more workgroups on long contexts
+    // (measured on 1-16 rows at contexts 150-8192)
+    const int nw = max_ctx <= 256 ? 16 : (M * num_kv_heads < 16 ? 4 : 8);
     return launch_attention_f16(q, kv_pool, page_table, max_pages, lane_of_row, ctx_len, M, layer,
                                 num_layers, num_heads, num_kv_heads, head_dim, max_ctx, scratch,
-                                out, st, 64, 4);
+                                out, st, 16, nw);
+  }
   const int chunk = attention_chunk(max_ctx, num_kv_heads, M);
   if ((max_ctx + chunk - 1) / chunk > kMaxRecords) return hipErrorInvalidValue;
   const int nch = (max_ctx + chunk - 1) / chunk;
@@ -1223,10 +1333,10 @@ hipError_t launch_attention(const float *q, const void *kv_pool, int kv_f16,
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || nch <= 1) return e;
   if (head_dim == 64)
-    hipLaunchKernelGGL((attn_combine2_kernel<64>), dim3(num_heads, M), dim3(256), 0, st, ctx_len,
+    hipLaunchKernelGGL((attn_combine2_kernel<64>), dim3(num_heads, M), dim3(kCombineThreads), 0, st, ctx_len,
                        num_heads, chunk, nch, max_ctx, scratch, out);
   else
-    hipLaunchKernelGGL((attn_combine2_kernel<128>), dim3(num_heads, M), dim3(256), 0, st,
+    hipLaunchKernelGGL((attn_combine2_kernel<128>), dim3(num_heads, M), dim3(kCombineThreads), 0, st,
                        ctx_len, num_heads, chunk, nch, max_ctx, scratch, out);
   return hipGetLastError();
 }
@@ -1234,115 +1344,48 @@ hipError_t launch_attention(const float *q, const void *kv_pool, int kv_f16,
 // ---------------------------------------------------------------------------
 // K5: argmax / eligible argmax
 // ---------------------------------------------------------------------------
-// Candidate order: larger value wins; equal values -> lower index. NaN
-// candidates never win (sampling.zig:194-206 strict '>' scan); index 0's NaN
-// case is settled by the finisher.
-struct Cand {
-  float v;
-  long i;
-};
-static __device__ __forceinline__ bool better(float v, long i, float bv, long bi) {
-  if (isnan(v)) return false;
-  if (bi < 0) return true;
-  return v > bv || (v == bv && i < bi);
-}
-
+// Candidate order and merge: arg_better / arg_merge (epilogue.h). A block
+// owns 8192 logits of one row; each thread issues all 32 of its loads (and
+// the block's 128 mask words go to LDS) before comparing, so a block costs
+// one memory round trip. The last block of a row (atomic counter, which it
+// resets) merges the row's partials and writes the result.
 static constexpr int kArgBlock = 256;
 static constexpr int kArgPerBlock = 8192;  // 128 mask words per block
 
 size_t argmax_scratch_bytes(int rows, long n) {
   const long blocks = (n + kArgPerBlock - 1) / kArgPerBlock;
-  return (size_t)rows * blocks * 32;
+  return (size_t)rows * blocks * sizeof(ArgPartial);
 }
 
-struct ArgPartial {
-  float v;
-  int nan_flag;
-  long i;
-  unsigned long long rows;
-  int bad_mask;
-  int pad;
-};
+static __device__ __forceinline__ ArgPartial arg_none() {
+  ArgPartial p;
+  p.v = 0.0f;
+  p.i = -1;
+  p.nan_flag = 0;
+  p.rows = 0;
+  p.bad_mask = 0;
+  p.nan0 = 0;
+  return p;
+}
 
-__global__ __launch_bounds__(kArgBlock) void argmax_kernel(const float *logits, long n,
-                                                           const uint64_t *words,
-                                                           long word_count,
-                                                           ArgPartial *parts,
-                                                           uint32_t *counters,
-                                                           ArgmaxResult *result) {
-  const int row = blockIdx.y, blk = blockIdx.x, t = threadIdx.x;
-  const long nblocks = gridDim.x;
-  const float *lr = logits + (size_t)row * n;
-  const uint64_t *wr = words ? words + (size_t)row * word_count : nullptr;
-  const long e0 = (long)blk * kArgPerBlock, e1 = min(n, e0 + kArgPerBlock);
-  float bv = 0.0f;
-  long bi = -1;
-  int nan_flag = 0;
-  for (long e = e0 + t; e < e1; e += kArgBlock) {
-    if (wr && !((wr[e >> 6] >> (e & 63)) & 1ull)) continue;
-    const float v = lr[e];
-    if (isnan(v)) nan_flag = 1;
-    if (better(v, e, bv, bi)) {
-      bv = v;
-      bi = e;
-    }
-  }
-  unsigned long long cnt = 0;
-  int bad = 0;
-  if (wr) {
-    const long w0 = e0 >> 6, w1 = (e1 + 63) >> 6;
-    for (long w = w0 + t; w < w1; w += kArgBlock) cnt += __popcll(wr[w]);
-    if (blk == nblocks - 1 && t == 0 && (n & 63)) {
-      const uint64_t tail = (1ull << (n & 63)) - 1ull;
-      if (wr[word_count - 1] & ~tail) bad = 1;
-    }
-  }
-  // wave reduction
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(bv, o);
-    const long oi = __shfl_xor(bi, o);
-    if (oi >= 0 && better(ov, oi, bv, bi)) {
-      bv = ov;
-      bi = oi;
-    }
-    nan_flag |= __shfl_xor(nan_flag, o);
-    cnt += __shfl_xor(cnt, o);
-    bad |= __shfl_xor(bad, o);
-  }
-  __shared__ ArgPartial wp[kArgBlock / 64];
-  if ((t & 63) == 0) wp[t >> 6] = ArgPartial{bv, nan_flag, bi, cnt, bad, 0};
+// Reduce one partial per thread over a 256-thread block; thread 0 gets it.
+static __device__ ArgPartial arg_block_reduce(ArgPartial p) {
+  __shared__ ArgPartial wpart[kArgBlock / 64];
+  const int t = threadIdx.x;
+  for (int o = 32; o > 0; o >>= 1) arg_merge(p, arg_shfl_xor(p, o));
+  __syncthreads();  // wpart may still be read by a previous call
+  if ((t & 63) == 0) wpart[t >> 6] = p;
   __syncthreads();
-  if (t != 0) return;
-  ArgPartial p = wp[0];
-  for (int w = 1; w < kArgBlock / 64; ++w) {
-    const ArgPartial q = wp[w];
-    if (q.i >= 0 && better(q.v, q.i, p.v, p.i)) {
-      p.v = q.v;
-      p.i = q.i;
-    }
-    p.nan_flag |= q.nan_flag;
-    p.rows += q.rows;
-    p.bad_mask |= q.bad_mask;
-  }
-  parts[(size_t)row * nblocks + blk] = p;
-  __threadfence();
-  if (atomicAdd(&counters[row], 1u) != (unsigned)(nblocks - 1)) return;
-  __threadfence();
-  ArgPartial r = parts[(size_t)row * nblocks];
-  for (long b = 1; b < nblocks; ++b) {
-    const ArgPartial q = parts[(size_t)row * nblocks + b];
-    if (q.i >= 0 && better(q.v, q.i, r.v, r.i)) {
-      r.v = q.v;
-      r.i = q.i;
-    }
-    r.nan_flag |= q.nan_flag;
-    r.rows += q.rows;
-    r.bad_mask |= q.bad_mask;
-  }
-  counters[row] = 0u;
+  ArgPartial r = wpart[0];
+  for (int w = 1; w < kArgBlock / 64; ++w) arg_merge(r, wpart[w]);
+  return r;
+}
+
+static __device__ void arg_write_result(const ArgPartial &r, bool masked, long n,
+                                        ArgmaxResult *res_out) {
   ArgmaxResult res;
   res.pad = 0;
-  if (wr) {
+  if (masked) {
     res.eligible_rows = r.rows;
     if (r.bad_mask || r.rows == 0 || r.rows > (unsigned long long)n) {
       res.status = 6;  // GLACIER_HIP_INVALID_MASK
@@ -1358,9 +1401,73 @@ __global__ __launch_bounds__(kArgBlock) void argmax_kernel(const float *logits, 
     res.eligible_rows = (uint64_t)n;
     res.status = 0;
     // a NaN at index 0 is the initial best and is never displaced
-    res.index = (isnan(lr[0]) || r.i < 0) ? 0 : (uint64_t)r.i;
+    res.index = (r.nan0 || r.i < 0) ? 0 : (uint64_t)r.i;
   }
-  result[row] = res;
+  *res_out = res;
+}
+
+__global__ __launch_bounds__(kArgBlock) void argmax_kernel(const float *logits, long n,
+                                                           const uint64_t *words,
+                                                           long word_count,
+                                                           ArgPartial *parts,
+                                                           uint32_t *counters,
+                                                           ArgmaxResult *result) {
+  constexpr int PER = kArgPerBlock / kArgBlock;
+  const int row = blockIdx.y, blk = blockIdx.x, t = threadIdx.x;
+  const long nblocks = gridDim.x;
+  const float *lr = logits + (size_t)row * n;
+  const uint64_t *wr = words ? words + (size_t)row * word_count : nullptr;
+  const long e0 = (long)blk * kArgPerBlock, e1 = min(n, e0 + kArgPerBlock);
+  __shared__ uint64_t sw[kArgPerBlock / 64];
+  __shared__ int last;
+  uint64_t myword = 0;
+  if (wr && t < kArgPerBlock / 64) {
+    const long wi = (e0 >> 6) + t;
+    myword = wi < word_count ? wr[wi] : 0ull;
+  }
+  float v[PER];
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const long e = e0 + t + (long)kArgBlock * u;
+    v[u] = e < e1 ? lr[e] : 0.0f;
+  }
+  if (wr && t < kArgPerBlock / 64) sw[t] = myword;
+  __syncthreads();
+  ArgPartial p = arg_none();
+#pragma unroll
+  for (int u = 0; u < PER; ++u) {
+    const long e = e0 + t + (long)kArgBlock * u;
+    if (e >= e1) break;
+    if (wr && !((sw[(e - e0) >> 6] >> (e & 63)) & 1ull)) continue;
+    if (isnan(v[u])) p.nan_flag = 1;
+    if (arg_better(v[u], e, p.v, p.i)) {
+      p.v = v[u];
+      p.i = e;
+    }
+  }
+  if (blk == 0 && t == 0 && isnan(v[0])) p.nan0 = 1;
+  if (wr && t < kArgPerBlock / 64) {
+    const long wi = (e0 >> 6) + t, w1 = (e1 + 63) >> 6;
+    if (wi < w1) p.rows = __popcll(myword);
+    if (wi == word_count - 1 && (n & 63) && (myword & ~((1ull << (n & 63)) - 1ull)))
+      p.bad_mask = 1;
+  }
+  const ArgPartial bp = arg_block_reduce(p);
+  if (t == 0) {
+    parts[(size_t)row * nblocks + blk] = bp;
+    __threadfence();
+    last = atomicAdd(&counters[row], 1u) == (unsigned)(nblocks - 1);
+  }
+  __syncthreads();
+  if (!last) return;
+  __threadfence();
+  ArgPartial q = arg_none();
+  for (long b = t; b < nblocks; b += kArgBlock) arg_merge(q, parts[(size_t)row * nblocks + b]);
+  const ArgPartial r = arg_block_reduce(q);
+  if (t == 0) {
+    counters[row] = 0u;
+    arg_write_result(r, wr != nullptr, n, &result[row]);
+  }
 }
 
 hipError_t launch_argmax(const float *logits, long n, int rows, const uint64_t *words,
@@ -1369,6 +1476,61 @@ hipError_t launch_argmax(const float *logits, long n, int rows, const uint64_t *
   const long blocks = (n + kArgPerBlock - 1) / kArgPerBlock;
   hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)blocks, rows), dim3(kArgBlock), 0, st,
                      logits, n, words, word_count, (ArgPartial *)scratch, counters, result);
+  return hipGetLastError();
+}
+
+// Fused-head finisher: one block per row merges the candidates the head
+// GEMV wrote and, for the eligible variant, counts the mask bits and checks
+// those beyond n; all loads of a pass are issued before they are used.
+__global__ __launch_bounds__(kArgBlock) void argmax_parts_kernel(const ArgPartial *parts,
+                                                                 int nparts, long n,
+                                                                 const uint64_t *words,
+                                                                 long word_count,
+                                                                 ArgmaxResult *result) {
+  constexpr int U = 8;
+  const int row = blockIdx.x, t = threadIdx.x;
+  const ArgPartial *pr = parts + (size_t)row * nparts;
+  const uint64_t *wr = words ? words + (size_t)row * word_count : nullptr;
+  ArgPartial p = arg_none();
+  for (int base = 0; base < nparts; base += kArgBlock * U) {
+    ArgPartial q[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = base + t + kArgBlock * u;
+      q[u] = i < nparts ? pr[i] : arg_none();
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) arg_merge(p, q[u]);
+  }
+  if (wr) {
+    for (long base = 0; base < word_count; base += (long)kArgBlock * U) {
+      uint64_t w[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const long i = base + t + (long)kArgBlock * u;
+        w[u] = i < word_count ? wr[i] : 0ull;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const long i = base + t + (long)kArgBlock * u;
+        if (i < (n + 63) / 64) p.rows += __popcll(w[u]);
+        if (i == word_count - 1 && (n & 63) && (w[u] & ~((1ull << (n & 63)) - 1ull)))
+          p.bad_mask = 1;
+      }
+    }
+  }
+  const ArgPartial r = arg_block_reduce(p);
+  if (t == 0) arg_write_result(r, wr != nullptr, n, &result[row]);
+}
+
+int gemv_argmax_parts(int N, int K, int M, int D) { return plan_gemv(N, K, M, D).grid; }
+
+hipError_t launch_argmax_parts(const ArgPartial *parts, int nparts, long n, int rows,
+                               const uint64_t *words, long word_count, ArgmaxResult *result,
+                               hipStream_t st) {
+  if (rows <= 0 || nparts <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(argmax_parts_kernel, dim3(rows), dim3(kArgBlock), 0, st, parts, nparts, n,
+                     words, word_count, result);
   return hipGetLastError();
 }
 

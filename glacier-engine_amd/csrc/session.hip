@@ -375,7 +375,9 @@ hipError_t run_proj(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, i
                     const float *x, const float *norm_w, int epi, const float *bias, float *y,
                     const float *resid, const gk::QkvArgs *qkv, hipStream_t st,
                     const int8_t *planes_q = nullptr, const gk::ActMeta *planes_m = nullptr,
-                    const PlanesOut *emit = nullptr, bool fuse_input = false) {
+                    const PlanesOut *emit = nullptr, bool fuse_input = false,
+                    gk::ArgPartial *arg_parts = nullptr, const uint64_t *arg_words = nullptr,
+                    long arg_word_count = 0) {
   const auto &c = s->model->cfg;
   gk::GemvArgs a{};
   a.codes = w->codes;
@@ -403,6 +405,12 @@ hipError_t run_proj(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, i
   } else {
     a.act_q = planes_q;
     a.act_meta = planes_m;
+  }
+  if (arg_parts) {
+    if (!decode) return hipErrorInvalidValue;
+    a.arg_parts = arg_parts;
+    a.arg_words = arg_words;
+    a.arg_word_count = arg_word_count;
   }
   if (emit && decode) {
     a.out_q = emit->q;
@@ -448,8 +456,7 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
                              st);
     if (e != hipSuccess) return e;
     e = run_proj(s, L.o, layer_D(s, L.o->out_f, L.o->in_f), rows, s->attn, nullptr,
-                 gk::EPI_RESID, nullptr, s->h, s->x_res, nullptr, st, nullptr, nullptr, nullptr,
-                 true);
+                 gk::EPI_RESID, nullptr, s->h, s->x_res, nullptr, st);
     if (e != hipSuccess) return e;
     const int Dd = layer_D(s, L.down->out_f, L.down->in_f);
     if (rows <= 32 && (uint32_t)rows <= s->planes2_rows) {
@@ -473,17 +480,30 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
 }
 
 // Final RMSNorm + LM head + (eligible) argmax for `rows` rows starting at x.
+// Decode-sized row counts fuse the argmax into the head GEMV (each
+// workgroup reduces its logits to one candidate per row) and finish with a
+// one-block-per-row merge; longer row sets scan the logits afterwards.
 hipError_t enqueue_head(glacier_hip_session *s, int rows, const float *x, bool elig,
                         hipStream_t st) {
   glacier_hip_model *m = s->model;
   const auto &c = m->cfg;
-  hipError_t e = run_proj(s, m->head, head_D(s), rows, x, m->final_norm, gk::EPI_PLAIN, nullptr,
-                          s->logits, nullptr, nullptr, st, nullptr, nullptr, nullptr, true);
-  if (e != hipSuccess) return e;
   const long V = (long)c.vocab_size;
   const long W = (V + 63) / 64;
-  return gk::launch_argmax(s->logits, V, rows, elig ? s->elig_words : nullptr, W, s->arg_scratch,
-                           s->arg_counters, s->arg_result, st);
+  const uint64_t *words = elig ? s->elig_words : nullptr;
+  if (rows <= 32) {
+    gk::ArgPartial *parts = (gk::ArgPartial *)s->arg_scratch;
+    hipError_t e = run_proj(s, m->head, head_D(s), rows, x, m->final_norm, gk::EPI_PLAIN,
+                            nullptr, s->logits, nullptr, nullptr, st, nullptr, nullptr, nullptr,
+                            false, parts, words, W);
+    if (e != hipSuccess) return e;
+    const int nparts = gk::gemv_argmax_parts((int)V, (int)c.dim, rows, head_D(s));
+    return gk::launch_argmax_parts(parts, nparts, V, rows, words, W, s->arg_result, st);
+  }
+  hipError_t e = run_proj(s, m->head, head_D(s), rows, x, m->final_norm, gk::EPI_PLAIN, nullptr,
+                          s->logits, nullptr, nullptr, st);
+  if (e != hipSuccess) return e;
+  return gk::launch_argmax(s->logits, V, rows, words, W, s->arg_scratch, s->arg_counters,
+                           s->arg_result, st);
 }
 
 // The full launch sequence of one decode step for `rows` lanes.
@@ -901,7 +921,12 @@ glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
   A((void **)&s->act_q2, (size_t)(c.hidden_dim / 32) * 3 * s->planes2_rows * 32);
   A((void **)&s->act_meta2, (size_t)(c.hidden_dim / 32) * s->planes2_rows * sizeof(gk::ActMeta));
   A((void **)&s->att_scratch, std::max<size_t>(att, 1) * 4);
-  A(&s->arg_scratch, gk::argmax_scratch_bytes((int)L, (long)c.vocab_size));
+  size_t arg_bytes = gk::argmax_scratch_bytes((int)L, (long)c.vocab_size);
+  for (uint32_t r = 1; r <= std::min<uint32_t>(L, 32); ++r)
+    arg_bytes = std::max(arg_bytes, (size_t)r * sizeof(gk::ArgPartial) *
+                                        gk::gemv_argmax_parts((int)c.vocab_size, (int)c.dim,
+                                                              (int)r, head_D(s)));
+  A(&s->arg_scratch, arg_bytes);
   A((void **)&s->arg_counters, (size_t)L * 4);
   A((void **)&s->arg_result, (size_t)L * sizeof(gk::ArgmaxResult));
   A((void **)&s->elig_words, (size_t)L * W * 8);

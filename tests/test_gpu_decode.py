@@ -257,6 +257,50 @@ def test_eligible_step_matches_masked_argmax(gh, tiny, ora):
         sess.close()
 
 
+@pytest.mark.parametrize("lanes", [2, 4])
+def test_fused_head_argmax_matches_logit_scan(gh, tiny, ora, lanes):
+    """The LM head reduces its logits to per-workgroup candidates and a
+    one-block merge picks the token (dot4 head at 2 rows, MFMA head at 4):
+    the token equals the oracle's (eligible) argmax over the logits the same
+    step returns, for dense, sparse, first-only and last-only masks."""
+    host, om, m = tiny
+    V = TINY["vocab_size"]
+    W = V // 64
+    sess = gh.Session(m, max_lanes=lanes, max_positions=64)
+    try:
+        last = []
+        for lane in range(lanes):
+            sess.begin(lane)
+            last.append(sess.prefill(lane, gh.synth_tokens(SEED + lane, 6 + lane, V, 9)))
+        rng = np.random.default_rng(11)
+        masks = []
+        for k in range(lanes):
+            w = np.zeros(W, np.uint64)
+            kind = k % 4
+            if kind == 0:
+                w[:] = ~np.uint64(0)
+            elif kind == 1:
+                for i in np.nonzero(rng.random(V) < 0.01)[0]:
+                    w[i // 64] |= np.uint64(1) << np.uint64(i % 64)
+            elif kind == 2:
+                w[0] = np.uint64(1)
+            else:
+                w[-1] = np.uint64(1) << np.uint64(63)
+            masks.append(w)
+        for step in range(3):
+            el = np.stack(masks) if step != 1 else None
+            nxt, lg = sess.step(list(range(lanes)), last, eligible=el, want_logits=True)
+            for k in range(lanes):
+                if el is None:
+                    assert int(nxt[k]) == ora.argmax(lg[k])
+                else:
+                    rc, idx, rows = ora.argmax_eligible(lg[k], masks[k])
+                    assert rc == 0 and int(nxt[k]) == idx
+            last = [int(t) for t in nxt]
+    finally:
+        sess.close()
+
+
 def test_cache_full_is_rejected_before_launch(gh, tiny):
     host, om, m = tiny
     sess = gh.Session(m, max_lanes=2, max_positions=32, total_pages=2)
