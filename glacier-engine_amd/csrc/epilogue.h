@@ -55,27 +55,96 @@ static __device__ __forceinline__ float silu_mul(float g, float u) {
   return t * u;
 }
 
-// Stores one output value `tot` of activation row m, weight row block nb,
-// row n_local; `partner` is the value of row n_local ^ 8 (only read by the
-// SwiGLU and QKV epilogues). Rows m >= M are never passed in.
-static __device__ __forceinline__ void store_output(const GemvArgs &a, int nb, int n_local, int m,
-                                                    float tot, float partner) {
-  const int N = a.N;
-  if (a.epi == EPI_SWIGLU) {
-    if (n_local < 8) a.y[(size_t)m * (N / 2) + nb * 8 + n_local] = silu_mul(tot, partner);
-    return;
-  }
-  if (a.epi == EPI_QKV) {
+// Inputs the epilogue reads besides the dot product, for one output (row m,
+// weight row block nb, row n_local): the residual, bias values, the RoPE
+// factors and the KV page slot of the row's position. Loading them is
+// separate from storing so the decode GEMV can request them early: the
+// first level (epi_load1) has no dependence on other loads, the second
+// (epi_load2: page id and RoPE factors of the row's position) needs pos and
+// lane_id from the first.
+struct EpiIn {
+  float resid, b0, b1, cs, sn;
+  int pos, lane_id, page;
+};
+
+static __device__ __forceinline__ void epi_load1(EpiIn &e, const GemvArgs &a, int epi, int nb,
+                                                 int n_local, int m) {
+  e.resid = e.b0 = e.b1 = e.cs = e.sn = 0.0f;
+  e.pos = e.lane_id = e.page = 0;
+  const int n = nb * 16 + n_local;
+  if (epi == EPI_QKV) {
+    // every lane of a row block loads (RoPE partner rows n_local >= 8 read
+    // their pair's entries and ignore them), so no branch splits the wave
     const QkvArgs &Q = a.qkv;
     const int hd = Q.head_dim;
     const int nbq = Q.num_heads * hd / 16, nbk = Q.num_kv_heads * hd / 16;
     const int kv_dim = Q.num_kv_heads * hd;
-    const int pos = Q.pos_of_row[m];
-    const int lane_id = Q.lane_of_row[m];
-    const int page = Q.page_table[(size_t)lane_id * Q.max_pages + pos / 16];
-    const size_t page_base = (((size_t)page * Q.num_layers + Q.layer) * 2) * 16 * (size_t)kv_dim;
-    const size_t krow = page_base + (size_t)(pos % 16) * kv_dim;
-    const size_t vrow = page_base + (size_t)(16 + pos % 16) * kv_dim;
+    e.pos = Q.pos_of_row[m];
+    e.lane_id = Q.lane_of_row[m];
+    if (a.bias) {
+      if (nb < nbq + nbk) {
+        const bool is_q = nb < nbq;
+        const int rel = is_q ? nb : nb - nbq;
+        const int bph = hd / 16;  // row blocks per head
+        const int head = rel / bph, p = (rel % bph) * 8 + (n_local & 7);
+        const int i0 = head * hd + p, i1 = i0 + hd / 2;
+        const int off = is_q ? 0 : Q.num_heads * hd;
+        e.b0 = a.bias[off + i0];
+        e.b1 = a.bias[off + i1];
+      } else {
+        e.b0 = a.bias[Q.num_heads * hd + kv_dim + (nb - nbq - nbk) * 16 + n_local];
+      }
+    }
+  } else if (epi == EPI_RESID) {
+    e.resid = a.resid[(size_t)m * a.N + n];
+  } else if (epi == EPI_PLAIN) {
+    if (a.bias) e.b0 = a.bias[n];
+  }
+}
+
+static __device__ __forceinline__ void epi_load2(EpiIn &e, const GemvArgs &a, int epi, int nb,
+                                                 int n_local) {
+  if (epi != EPI_QKV) return;
+  const QkvArgs &Q = a.qkv;
+  const int hd = Q.head_dim;
+  const int nbq = Q.num_heads * hd / 16, nbk = Q.num_kv_heads * hd / 16;
+  e.page = Q.page_table[(size_t)e.lane_id * Q.max_pages + e.pos / 16];
+  if (nb < nbq + nbk) {
+    const int rel = nb < nbq ? nb : nb - nbq;
+    const int p = (rel % (hd / 16)) * 8 + (n_local & 7);
+    e.cs = Q.rope_cos[(size_t)e.pos * (hd / 2) + p];
+    e.sn = Q.rope_sin[(size_t)e.pos * (hd / 2) + p];
+  }
+}
+
+static __device__ __forceinline__ EpiIn epi_load(const GemvArgs &a, int epi, int nb, int n_local,
+                                                 int m) {
+  EpiIn e;
+  epi_load1(e, a, epi, nb, n_local, m);
+  epi_load2(e, a, epi, nb, n_local);
+  return e;
+}
+
+// Stores one output value `tot` of activation row m, weight row block nb,
+// row n_local with epilogue type epi; `partner` is the value of row
+// n_local ^ 8 (only read by the SwiGLU and QKV epilogues), e its epi_load
+// inputs. Rows m >= M are never passed in.
+static __device__ __forceinline__ void store_output(const GemvArgs &a, int epi, int nb,
+                                                    int n_local, int m, float tot, float partner,
+                                                    const EpiIn &e) {
+  const int N = a.N;
+  if (epi == EPI_SWIGLU) {
+    if (n_local < 8) a.y[(size_t)m * (N / 2) + nb * 8 + n_local] = silu_mul(tot, partner);
+    return;
+  }
+  if (epi == EPI_QKV) {
+    const QkvArgs &Q = a.qkv;
+    const int hd = Q.head_dim;
+    const int nbq = Q.num_heads * hd / 16, nbk = Q.num_kv_heads * hd / 16;
+    const int kv_dim = Q.num_kv_heads * hd;
+    const size_t page_base = (((size_t)e.page * Q.num_layers + Q.layer) * 2) * 16 * (size_t)kv_dim;
+    const size_t krow = page_base + (size_t)(e.pos % 16) * kv_dim;
+    const size_t vrow = page_base + (size_t)(16 + e.pos % 16) * kv_dim;
     if (nb < nbq + nbk) {
       if (n_local >= 8) return;
       const bool is_q = nb < nbq;
@@ -85,14 +154,11 @@ static __device__ __forceinline__ void store_output(const GemvArgs &a, int nb, i
       const int i0 = head * hd + p, i1 = i0 + hd / 2;
       float x0 = tot, x1 = partner;
       if (a.bias) {
-        const int off = is_q ? 0 : Q.num_heads * hd;
-        x0 = a.bias[off + i0] + x0;
-        x1 = a.bias[off + i1] + x1;
+        x0 = e.b0 + x0;
+        x1 = e.b1 + x1;
       }
       // RopeTable.apply (generate.zig:813-830)
-      const float cs = Q.rope_cos[(size_t)pos * (hd / 2) + p];
-      const float sn = Q.rope_sin[(size_t)pos * (hd / 2) + p];
-      const float a0 = x0 * cs, b0 = x1 * sn, a1 = x0 * sn, b1 = x1 * cs;
+      const float a0 = x0 * e.cs, b0 = x1 * e.sn, a1 = x0 * e.sn, b1 = x1 * e.cs;
       const float y0 = a0 - b0, y1 = a1 + b1;
       if (is_q) {
         float *qo = Q.q_out + (size_t)m * Q.num_heads * hd;
@@ -110,7 +176,7 @@ static __device__ __forceinline__ void store_output(const GemvArgs &a, int nb, i
     } else {
       const int idx = (nb - nbq - nbk) * 16 + n_local;
       float v = tot;
-      if (a.bias) v = a.bias[Q.num_heads * hd + kv_dim + idx] + v;
+      if (a.bias) v = e.b0 + v;
       if (Q.kv_f16)
         ((__half *)Q.kv_pool)[vrow + idx] = __float2half_rn(v);
       else
@@ -119,10 +185,10 @@ static __device__ __forceinline__ void store_output(const GemvArgs &a, int nb, i
     return;
   }
   const int n = nb * 16 + n_local;
-  if (a.epi == EPI_RESID)
-    a.y[(size_t)m * N + n] = a.resid[(size_t)m * N + n] + tot;
+  if (epi == EPI_RESID)
+    a.y[(size_t)m * N + n] = e.resid + tot;
   else
-    a.y[(size_t)m * N + n] = a.bias ? a.bias[n] + tot : tot;
+    a.y[(size_t)m * N + n] = a.bias ? e.b0 + tot : tot;
 }
 
 }  // namespace gk

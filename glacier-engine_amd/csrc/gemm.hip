@@ -169,7 +169,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemvArgs p, int m_tiles) {
         const float partner = paired ? __shfl_xor(tot, 8) : 0.0f;
         const int m = m0 + 16 * mt + 4 * c + r;
         const int nb = nb0 + nt;
-        if (m < p.M && nb < NB) store_output(p, nb, n_local, m, tot, partner);
+        if (m < p.M && nb < NB)
+          store_output(p, p.epi, nb, n_local, m, tot, partner, epi_load(p, p.epi, nb, n_local, m));
       }
 }
 

@@ -27,6 +27,14 @@ struct ActMeta {
   int32_t corr;
 };
 
+// Destination of emitted activation planes (see the layout above): a
+// producer quantises its outputs straight into the next projection's input.
+struct PlanesDst {
+  int8_t *q;
+  ActMeta *meta;
+  int D;
+};
+
 // Greedy candidate of one span of logits (sampling.zig:55-105, 194-206):
 // best (value, lowest index) among its eligible non-NaN entries (i = -1:
 // none), whether an eligible entry was NaN, how many entries were eligible,
@@ -80,18 +88,26 @@ struct GemvArgs {
   int ksplit_lds_off;       // set by launch_gemv: LDS offset of the SwiGLU plane buffer
   int force_mfma;           // use the MFMA path even for M <= 2 (tuning / tests)
   QkvArgs qkv;
-  // Fused input stage: with x_in set, every workgroup builds the activation
-  // planes of x_in [M][K] (f32) in LDS itself, RMS-normalised with norm_w
-  // first when norm_w is set (act_q / act_meta are then unused).
-  const float *x_in;
-  const float *norm_w;
-  float eps;
   // EPI_SWIGLU only: also (or instead, with y == null) emit the SwiGLU output
   // as digit planes [G][out_D][M][32] + meta [G][M] of width N/2, ready as
   // the next projection's input.
   int8_t *out_q;
   ActMeta *out_meta;
   int out_D;
+  // EPI_RESID: also write ss_out [M][grid], each workgroup's sum of y^2 per
+  // row, from which the next projection finishes its RMSNorm (deferred).
+  float *ss_out;
+  // Input mode: with x_in set the kernel builds its planes in LDS from
+  // x_in [M][K] (f32), times norm_w when set, instead of reading act_q /
+  // act_meta (needs the planes to fit in LDS).
+  const float *x_in;
+  const float *norm_w;
+  // Deferred RMSNorm of the input: the kernel sums in_ss [M][in_ss_count]
+  // and scales every output of row m by 1 / sqrt(sum / K + in_eps) before
+  // the epilogue (the planes were quantised without that per-row factor).
+  const float *in_ss;
+  int in_ss_count;
+  float in_eps;
   // EPI_PLAIN only, fused greedy head (a reference LM head fused with its
   // argmax over row tiles): every workgroup also reduces its logits of each
   // activation row m to one candidate arg_parts[m * grid + workgroup],
@@ -110,9 +126,10 @@ struct GemvShape {
   size_t lds_bytes;
 };
 GemvShape plan_gemv(int N, int K, int M, int D);
-// Whether launch_gemv can build the planes of an M x K input in LDS (fused
-// input stage) for this projection.
-bool gemv_fused_input_ok(int N, int K, int M, int D);
+// The shape launch_gemv uses for these arguments (plan_gemv adjusted for
+// emitted planes / fused stages / overrides); grid = workgroup count, which
+// is also the number of ss_out partials per row. Returns false if invalid.
+bool gemv_launch_shape(const GemvArgs &a, GemvShape *out);
 
 // Prepare activation planes from x [M][K] (f32 or bf16), optionally
 // RMS-normalised with weight `norm_w` first (kernels.zig:141-220).
@@ -135,8 +152,11 @@ hipError_t launch_gemm(const GemvArgs &a, hipStream_t st);
 hipError_t launch_rmsnorm(const float *x, const float *w, int rows, int dim, float eps,
                           float *out, hipStream_t st);
 
-hipError_t launch_gather_rows(const float *table, const int32_t *ids, int M, int dim,
-                              float *out, hipStream_t st);
+// Embedding rows out[m] = table[ids[m]]; with ss_out set also
+// gather_ss_parts(dim) partial sums of squares per row (deferred RMSNorm).
+int gather_ss_parts(int dim);
+hipError_t launch_gather_rows(const float *table, const int32_t *ids, int M, int dim, float *out,
+                              hipStream_t st, float *ss_out = nullptr);
 
 // Paged GQA decode attention. Writes out [M][Hq*hd]. Scratch must hold
 // attention_scratch_floats(...) floats for any M up to max_rows.
@@ -146,7 +166,8 @@ hipError_t launch_attention(const float *q, const void *kv_pool, int kv_f16,
                             const int32_t *page_table, int max_pages, const int32_t *lane_of_row,
                             const int32_t *ctx_len, int M, int layer, int num_layers,
                             int num_heads, int num_kv_heads, int head_dim, int max_ctx,
-                            float *scratch, float *out, hipStream_t st);
+                            float *scratch, float *out, hipStream_t st,
+                            PlanesDst emit = PlanesDst{nullptr, nullptr, 1});
 
 // fp16-KV attention with an explicit launch shape: wp positions per wave,
 // nw waves per workgroup (tuning; launch_attention picks the shape).
@@ -154,7 +175,8 @@ hipError_t launch_attention_f16(const float *q, const void *kv_pool, const int32
                                 int max_pages, const int32_t *lane_of_row, const int32_t *ctx_len,
                                 int M, int layer, int num_layers, int num_heads, int num_kv_heads,
                                 int head_dim, int max_ctx, float *scratch, float *out,
-                                hipStream_t st, int wp, int nw);
+                                hipStream_t st, int wp, int nw,
+                                PlanesDst emit = PlanesDst{nullptr, nullptr, 1});
 
 // Argmax over rows x n. Eligible variant when words != null. Results to
 // `result` [rows] = {index (u64), eligible_rows (u64), status (i32), pad}.

@@ -92,6 +92,15 @@ static __device__ __forceinline__ void quantize_group(float v, int hl, int g, in
   }
 }
 
+// Quantises one 32-value group (one value per lane of a half-wave) into
+// the planes pd describes, when it is set.
+static __device__ __forceinline__ void emit_group(const PlanesDst &pd, float v, int hl, int g,
+                                                  int m, int M) {
+  if (!pd.q) return;
+  if (pd.D == 1) quantize_group<1>(v, hl, g, m, M, pd.q, pd.meta);
+  else quantize_group<3>(v, hl, g, m, M, pd.q, pd.meta);
+}
+
 // grid = (ceil(G / 8), M): each block converts 8 groups of one row; with a
 // norm weight every block first reduces the row's full sum of squares.
 template <int D>
@@ -196,6 +205,7 @@ hipError_t launch_prep_act(const void *x, int x_bf16, const float *norm_w, float
 // grid between those two capacities (4096..6144 waves on 256 CUs) runs one
 // round at U=4 but two at U=8; elsewhere U=8 keeps more bytes in flight.
 static constexpr size_t kLdsLimit = 64 * 1024;
+static constexpr int kMaxSsParts = 256;  // deferred-RMSNorm partial sums per row
 
 static size_t planes_bytes(int groups, int M, int D) {
   return (size_t)groups * ((size_t)D * M * 32 + (size_t)M * sizeof(ActMeta));
@@ -231,23 +241,12 @@ GemvShape plan_gemv(int N, int K, int M, int D) {
   return p;
 }
 
-// LDS of the fused input stage: planes, inverse RMS per row, per-wave
-// partial sums (up to 16 waves), the staged input rows and norm weights.
-static __host__ __device__ __forceinline__ size_t fused_rows_offset(int groups, int M, int D) {
-  const size_t planes = (size_t)groups * ((size_t)D * M * 32 + (size_t)M * 8);
-  return (planes + (size_t)M * 4 + (size_t)M * 16 * 4 + 15) & ~(size_t)15;
-}
-static size_t fused_stage_bytes(int K, int M, int D) {
-  return fused_rows_offset(K / 32, M, D) + (size_t)(M + 1) * K * 4;  // rows + norm weights
-}
-
-bool gemv_fused_input_ok(int N, int K, int M, int D) {
-  (void)N;
-  return M <= 4 && fused_stage_bytes(K, M, D) <= kLdsLimit;
-}
-
-template <int D, int MT, int U, bool LDS_A, bool DOT4, int LB>
+// EPI >= 0: the epilogue type as a compile-time constant (so a launch only
+// carries its own epilogue's loads and branches); EPI < 0: a.epi at run time.
+// XIN: input mode (planes built in LDS from a.x_in, deferred RMSNorm).
+template <int D, int MT, int U, bool LDS_A, bool DOT4, int LB, int EPI, bool XIN>
 __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
+  const int epi = EPI >= 0 ? EPI : a.epi;
   extern __shared__ __align__(16) unsigned char smem[];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -283,80 +282,172 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
       }
     }
 
+  // Epilogue inputs of the (at most two) rows of a dot4 launch: the first
+  // level now, with the weights and the input staging in flight; the second
+  // level (page slot, RoPE factors) after the staging barrier, under the
+  // weight stream.
+  // (every lane loads, with the row block clamped into range, so no branch
+  // splits the wave and the loads issue back to back)
+  EpiIn epre[2];
+  const int nb_c = min(nb, NB - 1);
+  if constexpr (DOT4) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+      if (ks == 0 && m < M) epi_load1(epre[m], a, epi, nb_c, n_local, m);
+  }
+  // Requests before any wait: the deferred-RMSNorm partial sums of this
+  // wave's first input row (row = wave), then the first pass of the input
+  // staging; the weights above are already in flight, so all three
+  // latencies overlap.
+  const int nthr = (int)blockDim.x;
   const size_t qbytes = (size_t)G * D * M * 32;
   const size_t mbytes = (size_t)G * M * sizeof(ActMeta);
-  if (LDS_A) {
-    if (a.x_in) {
-      // Fused input stage: RMSNorm (kernels.zig:141-220) and the group
-      // quantiser (int4_matmul.zig:380-398) of the whole input into LDS. The
-      // rows and the norm weights are first copied into LDS with every load
-      // of a pass in flight at once, so the stage costs one L2 round trip and
-      // the reduction and the quantiser never wait on memory.
-      const int nthr = blockDim.x, nw = nthr >> 6;
-      float *inv = (float *)(smem + qbytes + mbytes);
-      float *ssw = inv + M;                       // [M][nw] per-wave partial sums
-      float *xs = (float *)(smem + fused_rows_offset(G, M, D));  // [M][K] rows, then [K] norm
-      const float *nws = xs + (size_t)M * a.K;
-      {
-        constexpr int SU = 8;
-        const int n4 = M * (a.K >> 2), w4 = a.norm_w ? (a.K >> 2) : 0;
-        const float4 *src4 = (const float4 *)a.x_in;
-        const float4 *nrm4 = (const float4 *)a.norm_w;
-        float4 *xs4 = (float4 *)xs;
-        for (int base = 0; base < n4 + w4; base += nthr * SU) {
-          float4 v[SU];
+  __shared__ float sinv[32];
+  if constexpr (XIN) {
+    static_assert(LDS_A, "input mode builds the planes in LDS");
+    constexpr int XU = 2, PU = kMaxSsParts / 64;
+    const int nwv = (int)(blockDim.x >> 6);
+    float ssv[PU];
+    // (loads are clamped into range rather than branched around, so they
+    // all issue back to back)
+    if (a.in_ss && wave < M) {
+      const float *src = a.in_ss + (size_t)wave * a.in_ss_count;
 #pragma unroll
-          for (int u = 0; u < SU; ++u) {
-            const int i = base + (int)threadIdx.x + nthr * u;
-            v[u] = i < n4 ? src4[i] : (i < n4 + w4 ? nrm4[i - n4] : make_float4(0.f, 0.f, 0.f, 0.f));
-          }
+      for (int u = 0; u < PU; ++u) ssv[u] = src[min(lane + 64 * u, a.in_ss_count - 1)];
+    }
+    // 8 consecutive elements of x (and of the norm weight) per thread, so
+    // the 4 threads of a 32-element group quantise it together
+    const int nchunk = M * (a.K >> 3);
+    float4 xr[XU][2], wr[XU][2];
 #pragma unroll
-          for (int u = 0; u < SU; ++u) {
-            const int i = base + (int)threadIdx.x + nthr * u;
-            if (i < n4 + w4) xs4[i] = v[u];
-          }
-        }
-      }
-      __syncthreads();
-      if (a.norm_w) {
-        const float4 *xs4 = (const float4 *)xs;
-        for (int m = 0; m < M; ++m) {
-          float ss = 0.0f;
-          for (int i = threadIdx.x; i < (a.K >> 2); i += nthr) {
-            const float4 v = xs4[m * (a.K >> 2) + i];
-            ss = fmaf(v.w, v.w, fmaf(v.z, v.z, fmaf(v.y, v.y, fmaf(v.x, v.x, ss))));
-          }
-          for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-          if (lane == 0) ssw[m * nw + wave] = ss;
-        }
-        __syncthreads();
-        if (threadIdx.x < M) {
-          float tot = 0.0f;
-          for (int w = 0; w < nw; ++w) tot += ssw[threadIdx.x * nw + w];
-          inv[threadIdx.x] = 1.0f / sqrtf(tot / (float)a.K + a.eps);
-        }
-        __syncthreads();
-      }
-      const int half = threadIdx.x >> 5, hl = threadIdx.x & 31, nh = nthr >> 5;
-      for (int gi = half; gi < G * M; gi += nh) {
-        const int m = gi % M, g = gi / M;
-        const int k = (g << 5) + hl;
-        float v = xs[m * a.K + k];
+    for (int u = 0; u < XU; ++u)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) xr[u][h] = wr[u][h] = make_float4(1.f, 1.f, 1.f, 1.f);
+    auto load_chunks = [&](int base) {
+#pragma unroll
+      for (int u = 0; u < XU; ++u) {
+        const int c8 = min(base + (int)threadIdx.x + nthr * u, nchunk - 1);
+        const float4 *xp = (const float4 *)(a.x_in + (size_t)c8 * 8);
+        xr[u][0] = xp[0];
+        xr[u][1] = xp[1];
         if (a.norm_w) {
-          const float tt = v * inv[m];
-          v = tt * nws[k];
+          const float4 *wp = (const float4 *)(a.norm_w + (size_t)(c8 * 8) % a.K);
+          wr[u][0] = wp[0];
+          wr[u][1] = wp[1];
         }
-        quantize_group<D>(v, hl, g, m, M, (int8_t *)smem, (ActMeta *)(smem + qbytes));
       }
-    } else {
-      const uint4 *src = (const uint4 *)a.act_q;
-      uint4 *dst = (uint4 *)smem;
-      for (size_t i = threadIdx.x; i < qbytes / 16; i += blockDim.x) dst[i] = src[i];
-      const uint2 *msrc = (const uint2 *)a.act_meta;
-      uint2 *mdst = (uint2 *)(smem + qbytes);
-      for (size_t i = threadIdx.x; i < mbytes / 8; i += blockDim.x) mdst[i] = msrc[i];
+    };
+    load_chunks(0);
+    // 1/rms of each input row from the producer's partial sums of squares
+    // (wave w reduces rows w, w + waves, ...; fixed order)
+    if (a.in_ss) {
+      for (int m = wave; m < M; m += nwv) {
+        if (m != wave) {
+          const float *src = a.in_ss + (size_t)m * a.in_ss_count;
+#pragma unroll
+          for (int u = 0; u < PU; ++u) ssv[u] = src[min(lane + 64 * u, a.in_ss_count - 1)];
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int u = 0; u < PU; ++u) ss += lane + 64 * u < a.in_ss_count ? ssv[u] : 0.0f;
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        if (lane == 0) sinv[m] = 1.0f / sqrtf(ss / (float)a.K + a.in_eps);
+      }
+    }
+    // Group quantiser (int4_matmul.zig:380-398) of x * norm_w: the RMSNorm
+    // factor is a per-row scalar that cancels in q = round(v * 127 / max|v|),
+    // so it is applied to the outputs instead (sinv).
+    for (int base = 0; base < nchunk; base += nthr * XU) {
+      if (base > 0) load_chunks(base);
+#pragma unroll
+      for (int u = 0; u < XU; ++u) {
+        const int c8 = base + (int)threadIdx.x + nthr * u;
+        const bool valid = c8 < nchunk;  // uniform over the 4 threads of a group
+        float v[8] = {xr[u][0].x, xr[u][0].y, xr[u][0].z, xr[u][0].w,
+                      xr[u][1].x, xr[u][1].y, xr[u][1].z, xr[u][1].w};
+        if (a.norm_w) {
+          const float w8[8] = {wr[u][0].x, wr[u][0].y, wr[u][0].z, wr[u][0].w,
+                               wr[u][1].x, wr[u][1].y, wr[u][1].z, wr[u][1].w};
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[i] = v[i] * w8[i];
+        }
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+        amax = fmaxf(amax, __shfl_xor(amax, 1));
+        amax = fmaxf(amax, __shfl_xor(amax, 2));
+        const float scale = amax / 127.0f;
+        const float inv_s = scale == 0.0f ? 0.0f : 1.0f / scale;
+        uint64_t packed[D];
+#pragma unroll
+        for (int d = 0; d < D; ++d) packed[d] = 0;
+        int csum = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float y = v[i] * inv_s;
+          float q0f = roundf(y);
+          q0f = fminf(fmaxf(q0f, -127.0f), 127.0f);
+          int qd[3] = {(int)q0f, 0, 0};
+          if (D == 3) {
+            const float r1 = (y - q0f) * 128.0f;
+            const float q1f = roundf(r1);
+            const float r2 = (r1 - q1f) * 128.0f;
+            qd[1] = (int)q1f;
+            qd[2] = (int)roundf(r2);
+          }
+          int comb = 0;
+#pragma unroll
+          for (int d = 0; d < D; ++d) {
+            packed[d] |= (uint64_t)(uint8_t)(int8_t)qd[d] << (8 * i);
+            comb = comb * 128 + qd[d];
+          }
+          csum += comb;
+        }
+        csum += __shfl_xor(csum, 1);
+        csum += __shfl_xor(csum, 2);
+        if (valid) {
+          const int e = c8 * 8, m = e / a.K, g = (e % a.K) >> 5, part = (e >> 3) & 3;
+#pragma unroll
+          for (int d = 0; d < D; ++d)
+            *(uint64_t *)(smem + (((size_t)g * D + d) * M + m) * 32 + part * 8) = packed[d];
+          if (part == 0) {
+            ActMeta mm;
+            mm.scale = D == 3 ? scale * (1.0f / 16384.0f) : scale;
+            mm.corr = 7 * csum;
+            ((ActMeta *)(smem + qbytes))[(size_t)g * M + m] = mm;
+          }
+        }
+      }
     }
     __syncthreads();
+  } else if (LDS_A) {
+    // copy the producer's planes and meta into LDS: the first pass (all of
+    // it for decode shapes) issues its five loads before the first store
+    const int n16 = (int)(qbytes / 16), n8 = (int)(mbytes / 8);
+    const uint4 *src = (const uint4 *)a.act_q;
+    uint4 *dst = (uint4 *)smem;
+    const uint2 *msrc = (const uint2 *)a.act_meta;
+    uint2 *mdst = (uint2 *)(smem + qbytes);
+    const int t = (int)threadIdx.x;
+    const uint4 v0 = src[min(t, n16 - 1)];
+    const uint4 v1 = src[min(t + nthr, n16 - 1)];
+    const uint4 v2 = src[min(t + 2 * nthr, n16 - 1)];
+    const uint4 v3 = src[min(t + 3 * nthr, n16 - 1)];
+    const uint2 mv = msrc[min(t, n8 - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    if (t < n16) dst[t] = v0;
+    if (t + nthr < n16) dst[t + nthr] = v1;
+    if (t + 2 * nthr < n16) dst[t + 2 * nthr] = v2;
+    if (t + 3 * nthr < n16) dst[t + 3 * nthr] = v3;
+    if (t < n8) mdst[t] = mv;
+    for (int i = t + 4 * nthr; i < n16; i += nthr) dst[i] = src[i];
+    for (int i = t + nthr; i < n8; i += nthr) mdst[i] = msrc[i];
+    __syncthreads();
+  }
+  if constexpr (DOT4) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+      if (ks == 0 && m < M) epi_load2(epre[m], a, epi, nb_c, n_local);
   }
   const int8_t *aq = LDS_A ? (const int8_t *)smem : a.act_q;
   const ActMeta *am = LDS_A ? (const ActMeta *)(smem + qbytes) : a.act_meta;
@@ -495,13 +586,25 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
     }
   }
 
+  if (XIN && a.in_ss) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = mt * 16 + c * 4 + r;
+        if (m < M) acc[mt][r] *= sinv[m];
+      }
+  }
+
   // ---- fused epilogues: lane (c, n) owns rows m = 16 mt + 4 c + r of column n ----
-  const bool paired = a.epi == EPI_SWIGLU || a.epi == EPI_QKV;
-  const bool emit_planes = a.epi == EPI_SWIGLU && a.out_q;
+  const bool paired = epi == EPI_SWIGLU || epi == EPI_QKV;
+  const bool emit_planes = epi == EPI_SWIGLU && a.out_q;
+  const bool resid_ss = epi == EPI_RESID && a.ss_out;
   // SwiGLU outputs of this workgroup's rb row blocks: [M][8 * rb] floats
-  // after the reduction area
+  // after the reduction area; residual sums of squares: [waves][M]
   const int RB = (int)(blockDim.x >> 6) / KS;
   float *actbuf = (float *)(smem + a.ksplit_lds_off);
+  float *sspart = (float *)(smem + a.ksplit_lds_off);
   const int nb_wg0 = blockIdx.x * RB;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -511,6 +614,20 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
       const float tot = acc[mt][r];
       // partner row (n_local ^ 8) lives in lane ^ 8 with the same (c, r)
       const float partner = paired ? __shfl_xor(tot, 8) : 0.0f;
+      if (resid_ss) {
+        // residual output y = resid + tot, and this wave's sum of y^2 of row m
+        float y = 0.0f;
+        if (lead && m < M) {
+          const EpiIn e = DOT4 ? epre[m & 1] : epi_load(a, epi, nb, n_local, m);
+          y = e.resid + tot;
+          a.y[(size_t)m * a.N + nb * 16 + n_local] = y;
+        }
+        float sq = y * y;
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) sq += __shfl_xor(sq, o);
+        if (n_local == 0 && m < M) sspart[wave * M + m] = sq;
+        continue;
+      }
       if (!lead || m >= M) continue;
       if (emit_planes) {
         if (n_local < 8) {
@@ -519,9 +636,20 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
           if (a.y) a.y[(size_t)m * (a.N / 2) + nb * 8 + n_local] = v;
         }
       } else {
-        store_output(a, nb, n_local, m, tot, partner);
+        store_output(a, epi, nb, n_local, m, tot, partner,
+                     DOT4 ? epre[m & 1] : epi_load(a, epi, nb, n_local, m));
       }
     }
+  if (resid_ss) {
+    // this workgroup's sum of y^2 per row (the deferred RMSNorm of the next
+    // projection), waves added in a fixed order
+    __syncthreads();
+    for (int m = threadIdx.x; m < M; m += blockDim.x) {
+      float tot = 0.0f;
+      for (int w = 0; w < (int)(blockDim.x >> 6); ++w) tot += sspart[w * M + m];
+      a.ss_out[(size_t)m * gridDim.x + blockIdx.x] = tot;
+    }
+  }
   if (a.arg_parts) {
     // Fused greedy head: this workgroup's best eligible logit of each row m
     // (arg_better order), reduced over its 16-row blocks and then its waves.
@@ -585,79 +713,108 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
   }
 }
 
-hipError_t launch_gemv(const GemvArgs &a0, hipStream_t st) {
-  GemvArgs a = a0;
+// Launch shape for these arguments; also fills the fields launch_gemv
+// derives (ksplit, LDS offsets). False when the arguments are invalid.
+static bool gemv_shape(GemvArgs &a, GemvShape &p) {
   const int MT = (a.M + 15) / 16;
-  if (MT > 2 || a.N % 16 || a.K % 128 || (!a.x_in && (!a.act_q || !a.act_meta)))
-    return hipErrorInvalidValue;
+  if (MT > 2 || a.N % 16 || a.K % 128 || (!a.x_in && (!a.act_q || !a.act_meta))) return false;
   const bool emit_planes = a.epi == EPI_SWIGLU && a.out_q;
+  const bool resid_ss = a.epi == EPI_RESID && a.ss_out;
+  // the workgroup must own whole 32-wide output groups (4 row blocks)
   if (emit_planes && ((a.N / 16) % 4 || !a.out_meta || (a.out_D != 1 && a.out_D != 3)))
-    return hipErrorInvalidValue;
-  if (a.arg_parts && (a.epi != EPI_PLAIN || !a.y)) return hipErrorInvalidValue;
-  GemvShape p = plan_gemv(a.N, a.K, a.M, a.D);
-  if (a.x_in) {
-    if (!gemv_fused_input_ok(a.N, a.K, a.M, a.D)) return hipErrorInvalidValue;
-    p.lds_a = true;
-    p.lds_bytes = std::max(p.lds_bytes, fused_stage_bytes(a.K, a.M, a.D));
-  }
+    return false;
+  if (a.ss_out && (a.epi != EPI_RESID || !a.y || !a.resid)) return false;
+  if (a.arg_parts && (a.epi != EPI_PLAIN || !a.y)) return false;
+  if (a.in_ss && (!a.x_in || a.in_ss_count <= 0 || a.in_ss_count > kMaxSsParts || a.M > 32))
+    return false;
+  p = plan_gemv(a.N, a.K, a.M, a.D);
   if (emit_planes && p.rb % 4) {
-    // the workgroup must own whole 32-wide output groups (4 row blocks)
     p.rb = 4;
     while (p.ksplit * p.rb > 16) p.ksplit /= 2;
     p.waves = p.ksplit * p.rb;
     p.grid = (a.N / 16 + p.rb - 1) / p.rb;
     const size_t red = (size_t)p.waves * MT * 4 * 64 * sizeof(float);
     p.lds_bytes = std::max(p.lds_a ? planes_bytes(a.K / 32, a.M, a.D) + a.M * 4 : 0, red);
-    if (a.x_in) p.lds_bytes = std::max(p.lds_bytes, fused_stage_bytes(a.K, a.M, a.D));
   }
   if (a.ksplit_override > 0) {
+    if (a.arg_parts) return false;
     p.ksplit = a.ksplit_override;
     p.rb = a.rb_override > 0 ? a.rb_override : std::max(1, 4 / p.ksplit);
     p.waves = p.ksplit * p.rb;
-    if (p.waves > 16 || p.ksplit > a.K / 128) return hipErrorInvalidValue;
+    if (p.waves > 16 || p.ksplit > a.K / 128) return false;
     p.grid = (a.N / 16 + p.rb - 1) / p.rb;
     const size_t red = (size_t)p.waves * MT * 4 * 64 * sizeof(float);
     p.lds_bytes = std::max(p.lds_a ? planes_bytes(a.K / 32, a.M, a.D) + a.M * 4 : 0, red);
-    if (a.x_in) p.lds_bytes = std::max(p.lds_bytes, fused_stage_bytes(a.K, a.M, a.D));
-    if (emit_planes && p.rb % 4) return hipErrorInvalidValue;
+    if (emit_planes && p.rb % 4) return false;
   }
-  if (a.arg_parts) {
-    // one candidate per (wave, row) in LDS; the candidate array holds one
-    // entry per workgroup of the planned grid
-    if (a.ksplit_override > 0) return hipErrorInvalidValue;
+  // input mode: the planes are built in LDS, so they must fit there
+  if (a.x_in && !p.lds_a) return false;
+  if (resid_ss && p.grid > kMaxSsParts) return false;
+  if (a.arg_parts)  // one candidate per (wave, row) in LDS
     p.lds_bytes = std::max(p.lds_bytes, (size_t)p.waves * a.M * sizeof(ArgPartial));
-  }
   a.ksplit = p.ksplit;
   a.ksplit_lds_off = (int)((p.lds_bytes + 15) & ~(size_t)15);
   if (emit_planes) p.lds_bytes = a.ksplit_lds_off + (size_t)a.M * 8 * p.rb * sizeof(float);
+  if (resid_ss) p.lds_bytes = a.ksplit_lds_off + (size_t)p.waves * a.M * sizeof(float);
+  return true;
+}
+
+bool gemv_launch_shape(const GemvArgs &a0, GemvShape *out) {
+  GemvArgs a = a0;
+  GemvShape p;
+  if (!gemv_shape(a, p)) return false;
+  *out = p;
+  return true;
+}
+
+hipError_t launch_gemv(const GemvArgs &a0, hipStream_t st) {
+  GemvArgs a = a0;
+  GemvShape p;
+  if (!gemv_shape(a, p)) return hipErrorInvalidValue;
+  const int MT = (a.M + 15) / 16;
   dim3 grid(p.grid), block(64 * p.waves);
   const bool dot4 = a.M <= 2 && !a.force_mfma;
   const bool small = p.waves <= 4;
-  // the MFMA kernel at U=8 needs more than the 128 VGPRs a 1024-thread
-  // workgroup allows; it only runs with small workgroups
+  // U = 8 (quads in flight per wave) only for the MFMA kernel with small
+  // workgroups: it needs more than the 128 VGPRs a 1024-thread workgroup
+  // allows; the dot4 decode kernel measured best at U = 4
   int U = a.prefetch ? a.prefetch : p.unroll;
-  if (U != 8 || (!dot4 && !small)) U = 4;
+  if (U != 8 || dot4 || !small) U = 4;
   const size_t lds = p.lds_bytes;
-#define GK_KERNEL(DD, MM, UU, LL, T4, LBB) gemv_kernel<DD, MM, UU, LL, T4, LBB>
-#define GK_GO(DD, MM, UU, LL, T4)                                                              \
-  do {                                                                                       \
-    if (small) hipLaunchKernelGGL((GK_KERNEL(DD, MM, UU, LL, T4, 256)), grid, block, lds, st, a); \
-    else hipLaunchKernelGGL((GK_KERNEL(DD, MM, UU, LL, T4, 1024)), grid, block, lds, st, a);      \
+#define GK_KERNEL(DD, MM, UU, LL, T4, LBB, EE, XX) gemv_kernel<DD, MM, UU, LL, T4, LBB, EE, XX>
+#define GK_GO(DD, MM, UU, LL, T4, EE, XX)                                                           \
+  do {                                                                                          \
+    if (small)                                                                                  \
+      hipLaunchKernelGGL((GK_KERNEL(DD, MM, UU, LL, T4, 256, EE, XX)), grid, block, lds, st, a);  \
+    else                                                                                        \
+      hipLaunchKernelGGL((GK_KERNEL(DD, MM, UU, LL, T4, 1024, EE, XX)), grid, block, lds, st, a); \
   } while (0)
-#define GK_PATH(DD, LL)                                          \
-  do {                                                          \
-    if (MT == 2) GK_GO(DD, 2, 4, LL, false);                    \
-    else if (dot4) {                                            \
-      if (U == 8) GK_GO(DD, 1, 8, LL, true); else GK_GO(DD, 1, 4, LL, true);   \
-    } else {                                                    \
-      if (U == 8) GK_GO(DD, 1, 8, LL, false); else GK_GO(DD, 1, 4, LL, false); \
-    }                                                           \
+  // dot4 (decode) launches carry their epilogue type at compile time
+#define GK_DOT4(DD, LL, XX)                                                \
+  do {                                                                     \
+    switch (a.epi) {                                                       \
+      case EPI_PLAIN: GK_GO(DD, 1, 4, LL, true, EPI_PLAIN, XX); break;     \
+      case EPI_RESID: GK_GO(DD, 1, 4, LL, true, EPI_RESID, XX); break;     \
+      case EPI_SWIGLU: GK_GO(DD, 1, 4, LL, true, EPI_SWIGLU, XX); break;   \
+      default: GK_GO(DD, 1, 4, LL, true, EPI_QKV, XX); break;              \
+    }                                                                      \
   } while (0)
-  if (a.D == 1) {
-    if (p.lds_a) GK_PATH(1, true); else GK_PATH(1, false);
+#define GK_PATH(DD, LL, XX)                                                                      \
+  do {                                                                                          \
+    if (MT == 2) GK_GO(DD, 2, 4, LL, false, -1, XX);                                            \
+    else if (dot4) GK_DOT4(DD, LL, XX);                                                         \
+    else if (U == 8 && small)                                                                   \
+      hipLaunchKernelGGL((GK_KERNEL(DD, 1, 8, LL, false, 256, -1, XX)), grid, block, lds, st, a); \
+    else GK_GO(DD, 1, 4, LL, false, -1, XX);                                                    \
+  } while (0)
+  if (a.x_in) {
+    if (a.D == 1) GK_PATH(1, true, true); else GK_PATH(3, true, true);
+  } else if (a.D == 1) {
+    if (p.lds_a) GK_PATH(1, true, false); else GK_PATH(1, false, false);
   } else {
-    if (p.lds_a) GK_PATH(3, true); else GK_PATH(3, false);
+    if (p.lds_a) GK_PATH(3, true, false); else GK_PATH(3, false, false);
   }
+#undef GK_DOT4
 #undef GK_PATH
 #undef GK_GO
 #undef GK_KERNEL
@@ -692,17 +849,35 @@ hipError_t launch_rmsnorm(const float *x, const float *w, int rows, int dim, flo
   return hipGetLastError();
 }
 
-__global__ void gather_rows_kernel(const float *table, const int32_t *ids, int dim, float *out) {
-  const int m = blockIdx.y;
+// Embedding gather (generate.zig:3653-3663): one element per thread, a
+// block covers 256 columns of one row; with ss_out set it also writes the
+// block's sum of x^2 to ss_out [M][gridDim.x] (the next projection's
+// deferred RMSNorm).
+__global__ __launch_bounds__(256) void gather_rows_kernel(const float *table, const int32_t *ids,
+                                                         int dim, float *out, float *ss_out) {
+  const int m = blockIdx.y, t = threadIdx.x;
+  const int i = blockIdx.x * 256 + t;
   const size_t src = (size_t)ids[m] * dim;
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < dim; i += gridDim.x * blockDim.x)
-    out[(size_t)m * dim + i] = table[src + i];
+  float v = 0.0f;
+  if (i < dim) {
+    v = table[src + i];
+    out[(size_t)m * dim + i] = v;
+  }
+  if (!ss_out) return;
+  __shared__ float red[4];
+  float sq = v * v;
+  for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o);
+  if ((t & 63) == 0) red[t >> 6] = sq;
+  __syncthreads();
+  if (t == 0) ss_out[(size_t)m * gridDim.x + blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-hipError_t launch_gather_rows(const float *table, const int32_t *ids, int M, int dim,
-                              float *out, hipStream_t st) {
-  hipLaunchKernelGGL(gather_rows_kernel, dim3((dim + 255) / 256, M), dim3(256), 0, st, table,
-                     ids, dim, out);
+int gather_ss_parts(int dim) { return (dim + 255) / 256; }
+
+hipError_t launch_gather_rows(const float *table, const int32_t *ids, int M, int dim, float *out,
+                              hipStream_t st, float *ss_out) {
+  hipLaunchKernelGGL(gather_rows_kernel, dim3(gather_ss_parts(dim), M), dim3(256), 0, st, table,
+                     ids, dim, out, ss_out);
   return hipGetLastError();
 }
 
@@ -764,7 +939,8 @@ template <int HD, int F16, int HPW>
 __global__ __launch_bounds__(256) void attn_decode_kernel(
     const float *q, const void *kv_pool, const int32_t *page_table, int max_pages,
     const int32_t *lane_of_row, const int32_t *ctx_len, int layer, int num_layers, int Hq,
-    int Hkv, int chunk, int n_chunks_max, int max_ctx, float *scratch, float *out) {
+    int Hkv, int chunk, int n_chunks_max, int max_ctx, float *scratch, float *out,
+    PlanesDst pd) {
   constexpr int TPP = HD / 8;        // threads per position
   constexpr int PPP = 256 / TPP;     // positions per pass
   constexpr int PPW = 64 / TPP;      // positions per wave
@@ -974,6 +1150,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     const int qh = qh0 + g;
     if (nch == 1) {
       out[((size_t)m * Hq + qh) * HD + d] = sum;
+      emit_group(pd, sum, t & 31, (qh * HD + d) >> 5, m, (int)gridDim.z);
     } else {
       float *rec = scratch + (((size_t)m * Hq + qh) * n_chunks_max + ch) * (2 + HD);
       if (d == 0) {
@@ -1009,7 +1186,7 @@ template <int HD, int NT, int NW>
 __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(
     const float *q, const __half *pool, const int32_t *page_table, int max_pages,
     const int32_t *lane_of_row, const int32_t *ctx_len, int layer, int num_layers, int Hq,
-    int Hkv, int n_chunks_max, int max_ctx, float *scratch, float *out) {
+    int Hkv, int n_chunks_max, int max_ctx, float *scratch, float *out, PlanesDst pd) {
   typedef _Float16 h4 __attribute__((ext_vector_type(4)));
   typedef float f4 __attribute__((ext_vector_type(4)));
   constexpr int S = HD / 16;    // f16 MFMA steps over the head dim
@@ -1154,7 +1331,9 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(
         O = fmaf(so[w][g][d], f, O);
       }
     if (nch == 1) {
-      out[((size_t)m * Hq + qh0 + g) * HD + d] = O * (1.0f / L);
+      const float v = O * (1.0f / L);
+      out[((size_t)m * Hq + qh0 + g) * HD + d] = v;
+      emit_group(pd, v, t & 31, ((qh0 + g) * HD + d) >> 5, m, (int)gridDim.z);
     } else {
       float *rec = scratch + (((size_t)m * Hq + qh0 + g) * n_chunks_max + ch) * (2 + HD);
       if (d == 0) {
@@ -1174,7 +1353,7 @@ static constexpr int kCombineThreads = 512;
 template <int HD>
 __global__ __launch_bounds__(kCombineThreads) void attn_combine2_kernel(
     const int32_t *ctx_len, int Hq, int chunk, int n_chunks_max, int max_ctx,
-    const float *scratch, float *out) {
+    const float *scratch, float *out, PlanesDst pd) {
   constexpr int NTH = kCombineThreads, NG = NTH / HD, U = 8, RPT = kMaxRecords / NTH;
   const int qh = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
   const int ctx = min(ctx_len[m], max_ctx);
@@ -1241,7 +1420,9 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine2_kernel(
     float acc = part[0][d];
 #pragma unroll
     for (int i = 1; i < NG; ++i) acc += part[i][d];
-    out[((size_t)m * Hq + qh) * HD + d] = acc * (1.0f / L);
+    const float v = acc * (1.0f / L);
+    out[((size_t)m * Hq + qh) * HD + d] = v;
+    emit_group(pd, v, t & 31, (qh * HD + d) >> 5, m, (int)gridDim.y);
   }
 }
 
@@ -1249,7 +1430,7 @@ hipError_t launch_attention_f16(const float *q, const void *kv_pool, const int32
                                 int max_pages, const int32_t *lane_of_row, const int32_t *ctx_len,
                                 int M, int layer, int num_layers, int num_heads, int num_kv_heads,
                                 int head_dim, int max_ctx, float *scratch, float *out,
-                                hipStream_t st, int wp, int nw) {
+                                hipStream_t st, int wp, int nw, PlanesDst emit) {
   if (num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > kMaxGroup)
     return hipErrorInvalidValue;
   const int chunk = wp * nw;
@@ -1261,7 +1442,7 @@ hipError_t launch_attention_f16(const float *q, const void *kv_pool, const int32
 #define GK_F16(HD, NT, NW)                                                                   \
   hipLaunchKernelGGL((attn_f16_kernel<HD, NT, NW>), grid, dim3(64 * NW), 0, st, q, pool,     \
                      page_table, max_pages, lane_of_row, ctx_len, layer, num_layers,         \
-                     num_heads, num_kv_heads, nch, max_ctx, scratch, out)
+                     num_heads, num_kv_heads, nch, max_ctx, scratch, out, emit)
 #define GK_F16_HD(NT, NW)                                        \
   do {                                                          \
     if (head_dim == 64) GK_F16(64, NT, NW);                     \
@@ -1280,10 +1461,10 @@ hipError_t launch_attention_f16(const float *q, const void *kv_pool, const int32
   if (e != hipSuccess || nch <= 1) return e;
   if (head_dim == 64)
     hipLaunchKernelGGL((attn_combine2_kernel<64>), dim3(num_heads, M), dim3(kCombineThreads), 0, st, ctx_len,
-                       num_heads, chunk, nch, max_ctx, scratch, out);
+                       num_heads, chunk, nch, max_ctx, scratch, out, emit);
   else
     hipLaunchKernelGGL((attn_combine2_kernel<128>), dim3(num_heads, M), dim3(kCombineThreads), 0, st, ctx_len,
-                       num_heads, chunk, nch, max_ctx, scratch, out);
+                       num_heads, chunk, nch, max_ctx, scratch, out, emit);
   return hipGetLastError();
 }
 
@@ -1291,7 +1472,7 @@ hipError_t launch_attention(const float *q, const void *kv_pool, int kv_f16,
                             const int32_t *page_table, int max_pages, const int32_t *lane_of_row,
                             const int32_t *ctx_len, int M, int layer, int num_layers,
                             int num_heads, int num_kv_heads, int head_dim, int max_ctx,
-                            float *scratch, float *out, hipStream_t st) {
+                            float *scratch, float *out, hipStream_t st, PlanesDst emit) {
   if (num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > kMaxGroup)
     return hipErrorInvalidValue;
   if (kv_f16) {
@@ -1302,7 +1483,7 @@ hipError_t launch_attention(const float *q, const void *kv_pool, int kv_f16,
     const int nw = max_ctx <= 256 ? 16 : (M * num_kv_heads < 16 ? 4 : 8);
     return launch_attention_f16(q, kv_pool, page_table, max_pages, lane_of_row, ctx_len, M, layer,
                                 num_layers, num_heads, num_kv_heads, head_dim, max_ctx, scratch,
-                                out, st, 16, nw);
+                                out, st, 16, nw, emit);
   }
   const int chunk = attention_chunk(max_ctx, num_kv_heads, M);
   if ((max_ctx + chunk - 1) / chunk > kMaxRecords) return hipErrorInvalidValue;
@@ -1316,11 +1497,12 @@ hipError_t launch_attention(const float *q, const void *kv_pool, int kv_f16,
     if (per_head)                                                                               \
       hipLaunchKernelGGL((attn_decode_kernel<HD, F, 1>), grid, dim3(256), 0, st, q, kv_pool,    \
                          page_table, max_pages, lane_of_row, ctx_len, layer, num_layers,        \
-                         num_heads, num_kv_heads, chunk, nch, max_ctx, scratch, out);           \
+                         num_heads, num_kv_heads, chunk, nch, max_ctx, scratch, out, emit);     \
     else                                                                                        \
       hipLaunchKernelGGL((attn_decode_kernel<HD, F, kMaxGroup>), grid, dim3(256), 0, st, q,     \
                          kv_pool, page_table, max_pages, lane_of_row, ctx_len, layer,           \
-                         num_layers, num_heads, num_kv_heads, chunk, nch, max_ctx, scratch, out); \
+                         num_layers, num_heads, num_kv_heads, chunk, nch, max_ctx, scratch, out, \
+                         emit);                                                                 \
   } while (0)
   if (head_dim == 64) {
     if (kv_f16) GK_ATT(64, 1); else GK_ATT(64, 0);
@@ -1334,10 +1516,10 @@ hipError_t launch_attention(const float *q, const void *kv_pool, int kv_f16,
   if (e != hipSuccess || nch <= 1) return e;
   if (head_dim == 64)
     hipLaunchKernelGGL((attn_combine2_kernel<64>), dim3(num_heads, M), dim3(kCombineThreads), 0, st, ctx_len,
-                       num_heads, chunk, nch, max_ctx, scratch, out);
+                       num_heads, chunk, nch, max_ctx, scratch, out, emit);
   else
     hipLaunchKernelGGL((attn_combine2_kernel<128>), dim3(num_heads, M), dim3(kCombineThreads), 0, st,
-                       ctx_len, num_heads, chunk, nch, max_ctx, scratch, out);
+                       ctx_len, num_heads, chunk, nch, max_ctx, scratch, out, emit);
   return hipGetLastError();
 }
 

@@ -116,6 +116,7 @@ struct glacier_hip_session {
   int8_t *act_q2 = nullptr;         // planes emitted by the gate/up epilogue for down
   gk::ActMeta *act_meta2 = nullptr;
   uint32_t planes2_rows = 0;        // rows act_q2 / act_meta2 hold
+  float *ss_parts = nullptr;        // deferred RMSNorm partial sums [32][1024]
   float *att_scratch = nullptr;
   void *arg_scratch = nullptr;
   uint32_t *arg_counters = nullptr;
@@ -355,30 +356,37 @@ int head_D(const glacier_hip_session *s) {
   return gh::resolve_activation(s->opt.head_activation, c.vocab_size, c.dim) == GLACIER_HIP_ACT_Q8 ? 1 : 3;
 }
 
-// One projection over `rows` activation rows. Input x (f32 [rows][K], with
-// an optional RMSNorm weight) is converted into int8 digit planes (Q8 or the
-// 3-digit f32 representation) and multiplied by the INT4 weight with the
-// given epilogue. Decode-sized projections build the planes inside the GEMV
-// (fused input stage); otherwise a separate conversion kernel writes them to
-// HBM first. With x == null the planes are already in `planes_q/planes_m`
-// (emitted by the previous projection's epilogue). The fused input stage is
-// requested where it measured faster than a separate conversion launch: the
-// O projection (no norm) and the LM head (cold, measured on gfx950), not QKV
-// or gate/up, whose every workgroup would repeat the whole-row RMSNorm.
-struct PlanesOut {
-  int8_t *q;
-  gk::ActMeta *meta;
-  int D;
+// One projection over `rows` activation rows with the given epilogue. The
+// input is an f32 matrix x (optionally RMS-normalised with norm_w) or int8
+// digit planes a producer already emitted. An f32 input is converted into
+// planes (Q8, or the 3-digit f32 representation) either by a separate
+// kernel or, for decode-sized row sets whose planes fit in LDS, by the GEMV
+// itself while its weights stream in; in that input mode the RMSNorm is
+// deferred: the planes are quantised from x * w and the per-row 1/rms factor
+// (which cancels in the group quantiser, q = round(v * 127 / max|v|)) is
+// applied to the outputs from the producer's partial sums of squares.
+struct ProjIn {
+  const float *x = nullptr;
+  const float *norm_w = nullptr;
+  const float *ss = nullptr;  // producer's partial sums of x^2 [rows][ss_count]
+  int ss_count = 0;
+  const int8_t *planes_q = nullptr;
+  const gk::ActMeta *planes_m = nullptr;
+};
+struct ProjOut {
+  float *y = nullptr;
+  const float *resid = nullptr;
+  const float *bias = nullptr;
+  const gk::QkvArgs *qkv = nullptr;
+  gk::PlanesDst emit{nullptr, nullptr, 1};  // EPI_SWIGLU: next projection's planes
+  float *ss_out = nullptr;                  // EPI_RESID: partial sums of y^2
+  gk::ArgPartial *arg_parts = nullptr;      // EPI_PLAIN: fused greedy head
+  const uint64_t *arg_words = nullptr;
+  long arg_word_count = 0;
 };
 
-hipError_t run_proj(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, int rows,
-                    const float *x, const float *norm_w, int epi, const float *bias, float *y,
-                    const float *resid, const gk::QkvArgs *qkv, hipStream_t st,
-                    const int8_t *planes_q = nullptr, const gk::ActMeta *planes_m = nullptr,
-                    const PlanesOut *emit = nullptr, bool fuse_input = false,
-                    gk::ArgPartial *arg_parts = nullptr, const uint64_t *arg_words = nullptr,
-                    long arg_word_count = 0) {
-  const auto &c = s->model->cfg;
+gk::GemvArgs proj_args(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, int rows,
+                       int epi, const ProjIn &in, const ProjOut &out) {
   gk::GemvArgs a{};
   a.codes = w->codes;
   a.scales = w->scales;
@@ -386,48 +394,86 @@ hipError_t run_proj(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, i
   a.K = (int)w->in_f;
   a.M = rows;
   a.D = D;
-  a.bias = bias;
-  a.y = y;
-  a.resid = resid;
   a.epi = epi;
-  if (qkv) a.qkv = *qkv;
+  a.bias = out.bias;
+  a.y = out.y;
+  a.resid = out.resid;
+  if (out.qkv) a.qkv = *out.qkv;
+  a.act_q = in.planes_q;
+  a.act_meta = in.planes_m;
+  a.out_q = out.emit.q;
+  a.out_meta = out.emit.meta;
+  a.out_D = out.emit.D;
+  a.ss_out = out.ss_out;
+  a.arg_parts = out.arg_parts;
+  a.arg_words = out.arg_words;
+  a.arg_word_count = out.arg_word_count;
+  a.in_eps = s->model->cfg.rms_eps;
+  return a;
+}
+
+// GEMV arguments in input mode (planes built in LDS, deferred RMSNorm), or
+// false when this projection cannot run that way.
+bool input_mode_args(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, int rows, int epi,
+                     const ProjIn &in, const ProjOut &out, gk::GemvArgs *a) {
+  if (!in.x || rows > 32 || (in.norm_w && !in.ss)) return false;
+  *a = proj_args(s, w, D, rows, epi, in, out);
+  a->x_in = in.x;
+  a->norm_w = in.norm_w;
+  a->in_ss = in.ss;
+  a->in_ss_count = in.ss_count;
+  gk::GemvShape p;
+  return gk::gemv_launch_shape(*a, &p);
+}
+
+// Workgroups (= ss_out partials per row) of a decode projection.
+int proj_grid(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, int rows, int epi,
+              const ProjIn &in, const ProjOut &out) {
+  gk::GemvArgs a;
+  if (!input_mode_args(s, w, D, rows, epi, in, out, &a)) {
+    a = proj_args(s, w, D, rows, epi, in, out);
+    if (in.x) {  // the separate conversion kernel fills these
+      a.act_q = s->act_q;
+      a.act_meta = s->act_meta;
+    }
+  }
+  gk::GemvShape p;
+  return gk::gemv_launch_shape(a, &p) ? p.grid : -1;
+}
+
+hipError_t run_proj(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, int rows, int epi,
+                    const ProjIn &in, const ProjOut &out, hipStream_t st) {
   const bool decode = rows <= 32;
-  if (x && decode && fuse_input && gk::gemv_fused_input_ok(a.N, a.K, rows, D)) {
-    a.x_in = x;
-    a.norm_w = norm_w;
-    a.eps = c.rms_eps;
-  } else if (x) {
-    hipError_t e = gk::launch_prep_act(x, 0, norm_w, c.rms_eps, rows, a.K, D, s->act_q,
-                                       s->act_meta, nullptr, st);
+  // partial sums, plane emission and the fused head are GEMV-only
+  if (!decode && (out.emit.q || out.ss_out || out.arg_parts)) return hipErrorInvalidValue;
+  gk::GemvArgs a;
+  if (input_mode_args(s, w, D, rows, epi, in, out, &a)) return gk::launch_gemv(a, st);
+  a = proj_args(s, w, D, rows, epi, in, out);
+  if (in.x) {
+    hipError_t e = gk::launch_prep_act(in.x, 0, in.norm_w, s->model->cfg.rms_eps, rows,
+                                       (int)w->in_f, D, s->act_q, s->act_meta, nullptr, st);
     if (e != hipSuccess) return e;
     a.act_q = s->act_q;
     a.act_meta = s->act_meta;
-  } else {
-    a.act_q = planes_q;
-    a.act_meta = planes_m;
-  }
-  if (arg_parts) {
-    if (!decode) return hipErrorInvalidValue;
-    a.arg_parts = arg_parts;
-    a.arg_words = arg_words;
-    a.arg_word_count = arg_word_count;
-  }
-  if (emit && decode) {
-    a.out_q = emit->q;
-    a.out_meta = emit->meta;
-    a.out_D = emit->D;
   }
   return decode ? gk::launch_gemv(a, st) : gk::launch_gemm(a, st);
 }
 
 // Embedding gather and every decoder layer for `rows` activation rows
 // (generate.zig:1511-1967 per row; K/V rows land in the rows' pages).
+//
+// Decode-sized row sets (rows <= 32) run a chain with no conversion kernels:
+// the gather and each residual projection (O, down) also write per-workgroup
+// sums of squares of their output, from which the next RMSNorm'd projection
+// (QKV, gate/up, LM head) finishes its deferred norm while it quantises its
+// input in LDS; attention writes the O projection's planes and gate/up the
+// down projection's. Longer row sets (prefill chunks) convert each input
+// with a separate kernel.
 hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, hipStream_t st) {
   glacier_hip_model *m = s->model;
   const auto &c = m->cfg;
   const int D = (int)c.dim;
-  hipError_t e = gk::launch_gather_rows(m->embed, rp.tokens, rows, D, s->x_res, st);
-  if (e != hipSuccess) return e;
+  const bool chain = rows <= 32 && (uint32_t)rows <= s->planes2_rows;
   gk::QkvArgs q{};
   q.q_out = s->q;
   q.kv_pool = s->kv_pool;
@@ -442,46 +488,95 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
   q.num_heads = (int)c.num_heads;
   q.num_kv_heads = (int)c.num_kv_heads;
   q.head_dim = (int)c.head_dim;
+  float *ss = chain ? s->ss_parts : nullptr;
+  hipError_t e = gk::launch_gather_rows(m->embed, rp.tokens, rows, D, s->x_res, st, ss);
+  if (e != hipSuccess) return e;
+  int ss_count = chain ? gk::gather_ss_parts(D) : 0;  // partial sums behind x_res
   for (uint32_t l = 0; l < c.num_layers; ++l) {
     const LayerDev &L = m->layers[l];
     q.layer = (int)l;
+    const int Dq = layer_D(s, L.qkv->out_f, L.qkv->in_f);
+    const int Do = layer_D(s, L.o->out_f, L.o->in_f);
+    const int Dg = layer_D(s, L.gu->out_f / 2, L.gu->in_f);
+    const int Dd = layer_D(s, L.down->out_f, L.down->in_f);
     // RMSNorm -> QKV (+RoPE, KV row write into the lane's page)
-    e = run_proj(s, L.qkv, layer_D(s, L.qkv->out_f, L.qkv->in_f), rows, s->x_res, L.in_norm,
-                 gk::EPI_QKV, L.qkv_bias, nullptr, nullptr, &q, st);
+    ProjIn qin;
+    qin.x = s->x_res;
+    qin.norm_w = L.in_norm;
+    qin.ss = ss;
+    qin.ss_count = ss_count;
+    ProjOut qout;
+    qout.bias = L.qkv_bias;
+    qout.qkv = &q;
+    e = run_proj(s, L.qkv, Dq, rows, gk::EPI_QKV, qin, qout, st);
     if (e != hipSuccess) return e;
+    // attention (chain: also the O projection's planes)
+    const gk::PlanesDst opd = chain ? gk::PlanesDst{s->act_q2, s->act_meta2, Do}
+                                    : gk::PlanesDst{nullptr, nullptr, 1};
     e = gk::launch_attention(s->q, s->kv_pool, s->opt.kv_dtype == GLACIER_HIP_F16, s->page_table,
                              (int)s->max_pages, rp.lane_of_row, rp.ctx_len, rows, (int)l,
                              (int)c.num_layers, (int)c.num_heads, (int)c.num_kv_heads,
                              (int)c.head_dim, (int)s->opt.max_positions, s->att_scratch, s->attn,
-                             st);
+                             st, opd);
     if (e != hipSuccess) return e;
-    e = run_proj(s, L.o, layer_D(s, L.o->out_f, L.o->in_f), rows, s->attn, nullptr,
-                 gk::EPI_RESID, nullptr, s->h, s->x_res, nullptr, st);
-    if (e != hipSuccess) return e;
-    const int Dd = layer_D(s, L.down->out_f, L.down->in_f);
-    if (rows <= 32 && (uint32_t)rows <= s->planes2_rows) {
-      // gate/up writes the SwiGLU output straight into down's input planes
-      const PlanesOut po{s->act_q2, s->act_meta2, Dd};
-      e = run_proj(s, L.gu, layer_D(s, L.gu->out_f / 2, L.gu->in_f), rows, s->h, L.post_norm,
-                   gk::EPI_SWIGLU, nullptr, nullptr, nullptr, nullptr, st, nullptr, nullptr, &po);
-      if (e != hipSuccess) return e;
-      e = run_proj(s, L.down, Dd, rows, nullptr, nullptr, gk::EPI_RESID, nullptr, s->x_res, s->h,
-                   nullptr, st, s->act_q2, s->act_meta2);
+    // O projection + residual (chain: partial sums of h for gate/up's norm)
+    ProjIn oin;
+    ProjOut oout;
+    oout.y = s->h;
+    oout.resid = s->x_res;
+    oout.ss_out = ss;
+    if (chain) {
+      oin.planes_q = s->act_q2;
+      oin.planes_m = s->act_meta2;
     } else {
-      e = run_proj(s, L.gu, layer_D(s, L.gu->out_f / 2, L.gu->in_f), rows, s->h, L.post_norm,
-                   gk::EPI_SWIGLU, nullptr, s->act, nullptr, nullptr, st);
-      if (e != hipSuccess) return e;
-      e = run_proj(s, L.down, Dd, rows, s->act, nullptr, gk::EPI_RESID, nullptr, s->x_res, s->h,
-                   nullptr, st);
+      oin.x = s->attn;
     }
+    if (chain) {
+      ss_count = proj_grid(s, L.o, Do, rows, gk::EPI_RESID, oin, oout);
+      if (ss_count <= 0) return hipErrorInvalidValue;
+    }
+    e = run_proj(s, L.o, Do, rows, gk::EPI_RESID, oin, oout, st);
+    if (e != hipSuccess) return e;
+    // gate/up + SwiGLU (decode sizes: emitted straight into down's planes)
+    ProjIn gin;
+    gin.x = s->h;
+    gin.norm_w = L.post_norm;
+    gin.ss = ss;
+    gin.ss_count = ss_count;
+    ProjOut gout;
+    if (rows <= 32 && (uint32_t)rows <= s->planes2_rows)
+      gout.emit = gk::PlanesDst{s->act_q2, s->act_meta2, Dd};
+    else
+      gout.y = s->act;
+    e = run_proj(s, L.gu, Dg, rows, gk::EPI_SWIGLU, gin, gout, st);
+    if (e != hipSuccess) return e;
+    // down + residual (chain: partial sums of x_res for the next norm)
+    ProjIn din;
+    ProjOut dout;
+    dout.y = s->x_res;
+    dout.resid = s->h;
+    const bool last = l + 1 == c.num_layers;  // the LM head converts x_res itself
+    dout.ss_out = last ? nullptr : ss;
+    if (gout.emit.q) {
+      din.planes_q = s->act_q2;
+      din.planes_m = s->act_meta2;
+    } else {
+      din.x = s->act;
+    }
+    if (chain && !last) {
+      ss_count = proj_grid(s, L.down, Dd, rows, gk::EPI_RESID, din, dout);
+      if (ss_count <= 0) return hipErrorInvalidValue;
+    }
+    e = run_proj(s, L.down, Dd, rows, gk::EPI_RESID, din, dout, st);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
 }
 
 // Final RMSNorm + LM head + (eligible) argmax for `rows` rows starting at x.
-// Decode-sized row counts fuse the argmax into the head GEMV (each
-// workgroup reduces its logits to one candidate per row) and finish with a
+// Decode-
+// sized row counts fuse the argmax into the head GEMV (each workgroup
+// reduces its logits to one candidate per row) and finish with a
 // one-block-per-row merge; longer row sets scan the logits afterwards.
 hipError_t enqueue_head(glacier_hip_session *s, int rows, const float *x, bool elig,
                         hipStream_t st) {
@@ -490,17 +585,24 @@ hipError_t enqueue_head(glacier_hip_session *s, int rows, const float *x, bool e
   const long V = (long)c.vocab_size;
   const long W = (V + 63) / 64;
   const uint64_t *words = elig ? s->elig_words : nullptr;
+  // The head converts its input with the separate kernel: in input mode
+  // its ~1200 workgroups would each repeat the 3-digit quantisation of the
+  // row, which measured slower than one extra launch.
+  ProjIn in;
+  in.x = x;
+  in.norm_w = m->final_norm;
+  ProjOut out;
+  out.y = s->logits;
   if (rows <= 32) {
-    gk::ArgPartial *parts = (gk::ArgPartial *)s->arg_scratch;
-    hipError_t e = run_proj(s, m->head, head_D(s), rows, x, m->final_norm, gk::EPI_PLAIN,
-                            nullptr, s->logits, nullptr, nullptr, st, nullptr, nullptr, nullptr,
-                            false, parts, words, W);
+    out.arg_parts = (gk::ArgPartial *)s->arg_scratch;
+    out.arg_words = words;
+    out.arg_word_count = W;
+    hipError_t e = run_proj(s, m->head, head_D(s), rows, gk::EPI_PLAIN, in, out, st);
     if (e != hipSuccess) return e;
     const int nparts = gk::gemv_argmax_parts((int)V, (int)c.dim, rows, head_D(s));
-    return gk::launch_argmax_parts(parts, nparts, V, rows, words, W, s->arg_result, st);
+    return gk::launch_argmax_parts(out.arg_parts, nparts, V, rows, words, W, s->arg_result, st);
   }
-  hipError_t e = run_proj(s, m->head, head_D(s), rows, x, m->final_norm, gk::EPI_PLAIN, nullptr,
-                          s->logits, nullptr, nullptr, st);
+  hipError_t e = run_proj(s, m->head, head_D(s), rows, gk::EPI_PLAIN, in, out, st);
   if (e != hipSuccess) return e;
   return gk::launch_argmax(s->logits, V, rows, words, W, s->arg_scratch, s->arg_counters,
                            s->arg_result, st);
@@ -518,7 +620,8 @@ hipError_t enqueue_step(glacier_hip_session *s, int rows, bool head, bool elig, 
 void destroy_session(glacier_hip_session *s) {
   void *ptrs[] = {s->kv_pool, s->page_table, s->rope_cos, s->rope_sin, s->x_res, s->h, s->q,
                   s->attn, s->act, s->logits, s->act_q, s->act_meta, s->act_q2, s->act_meta2,
-                  s->att_scratch, s->arg_scratch, s->arg_counters, s->arg_result, s->elig_words,
+                  s->att_scratch, s->ss_parts, s->arg_scratch, s->arg_counters, s->arg_result,
+                  s->elig_words,
                   s->step_dev, s->pf_dev};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
@@ -918,9 +1021,12 @@ glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
   // the gate/up epilogue emits planes for every decode-path launch: up to 32
   // rows (decode lanes, or a prompt chunk that short)
   s->planes2_rows = std::min<uint32_t>(M, 32);
-  A((void **)&s->act_q2, (size_t)(c.hidden_dim / 32) * 3 * s->planes2_rows * 32);
-  A((void **)&s->act_meta2, (size_t)(c.hidden_dim / 32) * s->planes2_rows * sizeof(gk::ActMeta));
+  // act_q2 also holds the O projection's planes, emitted by attention
+  const size_t G2 = std::max<size_t>(c.hidden_dim, (size_t)c.num_heads * c.head_dim) / 32;
+  A((void **)&s->act_q2, G2 * 3 * s->planes2_rows * 32);
+  A((void **)&s->act_meta2, G2 * s->planes2_rows * sizeof(gk::ActMeta));
   A((void **)&s->att_scratch, std::max<size_t>(att, 1) * 4);
+  A((void **)&s->ss_parts, (size_t)32 * 1024 * sizeof(float));
   size_t arg_bytes = gk::argmax_scratch_bytes((int)L, (long)c.vocab_size);
   for (uint32_t r = 1; r <= std::min<uint32_t>(L, 32); ++r)
     arg_bytes = std::max(arg_bytes, (size_t)r * sizeof(gk::ArgPartial) *
