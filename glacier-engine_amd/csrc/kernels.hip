@@ -219,7 +219,9 @@ GemvShape plan_gemv(int N, int K, int M, int D) {
     // From cold-cache sweeps of the 7B decode shapes: about 4096 waves or
     // more keep HBM busy (split K until there, keeping >= 4 quads per wave),
     // workgroups of about 8 waves, 4 quads in flight per wave.
-    ks = std::max(1, std::min(std::min(16, std::max(1, KQ / 4)), (4096 + NB - 1) / NB));
+    // (K split capped at 8 waves: the 3-digit down projection measured best
+    // there.)
+    ks = std::max(1, std::min(std::min(8, std::max(1, KQ / 4)), (4096 + NB - 1) / NB));
     rb = std::max(1, std::min(8, 8 / ks));
     p.unroll = 4;
   } else {
@@ -728,6 +730,18 @@ static bool gemv_shape(GemvArgs &a, GemvShape &p) {
   if (a.in_ss && (!a.x_in || a.in_ss_count <= 0 || a.in_ss_count > kMaxSsParts || a.M > 32))
     return false;
   p = plan_gemv(a.N, a.K, a.M, a.D);
+  if (a.x_in && a.M <= 2) {
+    // input mode: every workgroup quantises the whole input row, so fewer,
+    // wider workgroups (8 waves; the K split only for short row counts)
+    // measured faster on the 7B QKV and gate/up shapes
+    const int NB = a.N / 16, KQ = a.K / 128;
+    p.ksplit = NB >= 1024 ? 1 : std::max(1, std::min(4, KQ / 4));
+    p.rb = 8 / p.ksplit;
+    p.waves = p.ksplit * p.rb;
+    p.grid = (NB + p.rb - 1) / p.rb;
+    const size_t red = (size_t)p.waves * MT * 4 * 64 * sizeof(float);
+    p.lds_bytes = std::max(p.lds_a ? planes_bytes(a.K / 32, a.M, a.D) + a.M * 4 : 0, red);
+  }
   if (emit_planes && p.rb % 4) {
     p.rb = 4;
     while (p.ksplit * p.rb > 16) p.ksplit /= 2;
