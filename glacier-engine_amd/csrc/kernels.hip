@@ -36,13 +36,18 @@ static __device__ __forceinline__ float h2f(uint32_t bits16) {
   return __half2float(__ushort_as_half((unsigned short)bits16));
 }
 
-// Eight 4-bit codes of one u32 -> eight int8 lanes k0..k7 (low nibbles are
-// k0..k3, high nibbles k4..k7 in the device tile layout).
-static __device__ __forceinline__ long unpack_codes(uint32_t w) {
-  uint32_t lo = w & 0x0F0F0F0Fu;
-  uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
+// Eight 4-bit codes of one u32 (low nibbles k0..k3, high nibbles k4..k7 in
+// the device tile layout) -> eight signed int8 lanes (u - 7), k0..k7. Per
+// byte u + 0x79 stays below 0x100 and flipping bit 7 of (u + 121) gives
+// u - 7 in two's complement, so an integer dot with these lanes is the
+// group dot of the dequantised codes itself (no correction term).
+static __device__ __forceinline__ long signed_codes(uint32_t w) {
+  const uint32_t lo = ((w & 0x0F0F0F0Fu) + 0x79797979u) ^ 0x80808080u;
+  const uint32_t hi = (((w >> 4) & 0x0F0F0F0Fu) + 0x79797979u) ^ 0x80808080u;
   return (long)(((uint64_t)hi << 32) | (uint64_t)lo);
 }
+
+static constexpr int kMagic = 0x4B400000;  // bits of 12582912.0f = 1.5 * 2^23
 
 // ---------------------------------------------------------------------------
 // K4: activation planes (+ optional RMSNorm)
@@ -204,7 +209,10 @@ hipError_t launch_prep_act(const void *x, int x_bf16, const float *norm_w, float
 // decides U: the dot4 kernel holds 6 waves/SIMD at U=4 and 4 at U=8, so a
 // grid between those two capacities (4096..6144 waves on 256 CUs) runs one
 // round at U=4 but two at U=8; elsewhere U=8 keeps more bytes in flight.
-static constexpr size_t kLdsLimit = 64 * 1024;
+// Activation planes are staged in LDS when they fit in 144 KB of the 160 KB
+// a gfx950 workgroup may use (the rest holds the epilogue buffers; launches
+// above 64 KB raise the kernel's dynamic-LDS limit first).
+static constexpr size_t kLdsLimit = 144 * 1024;
 static constexpr int kMaxSsParts = 256;  // deferred-RMSNorm partial sums per row
 
 static size_t planes_bytes(int groups, int M, int D) {
@@ -229,6 +237,9 @@ GemvShape plan_gemv(int N, int K, int M, int D) {
     ks = 1;
     while (ks * 2 <= max_ks && (KQ + ks - 1) / ks > 16) ks *= 2;
     while (ks * 2 <= max_ks && NB * ks * 2 < 4096 && KQ >= 4 * ks) ks *= 2;
+    // at most 8 waves per workgroup: the MFMA kernel needs more than the
+    // 128 VGPRs per wave a 16-wave workgroup leaves (it spilled there)
+    ks = std::min(ks, 8);
     rb = std::min(4, std::max(1, (D == 3 ? 8 : 4) / ks));
     p.unroll = (ks * rb <= 4 && (long)NB * ks <= 3072) ? 8 : 4;
   }
@@ -246,7 +257,9 @@ GemvShape plan_gemv(int N, int K, int M, int D) {
 // EPI >= 0: the epilogue type as a compile-time constant (so a launch only
 // carries its own epilogue's loads and branches); EPI < 0: a.epi at run time.
 // XIN: input mode (planes built in LDS from a.x_in, deferred RMSNorm).
-template <int D, int MT, int U, bool LDS_A, bool DOT4, int LB, int EPI, bool XIN>
+// MR: rows the dot4 path accumulates per lane (2, or 16 for the batched
+// dot4 path on one-digit planes).
+template <int D, int MT, int U, bool LDS_A, bool DOT4, int LB, int EPI, bool XIN, int MR = 2>
 __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
   const int epi = EPI >= 0 ? EPI : a.epi;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -292,7 +305,7 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
   // splits the wave and the loads issue back to back)
   EpiIn epre[2];
   const int nb_c = min(nb, NB - 1);
-  if constexpr (DOT4) {
+  if constexpr (DOT4 && MR == 2) {
 #pragma unroll
     for (int m = 0; m < 2; ++m)
       if (ks == 0 && m < M) epi_load1(epre[m], a, epi, nb_c, n_local, m);
@@ -446,7 +459,7 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
     for (int i = t + nthr; i < n8; i += nthr) mdst[i] = msrc[i];
     __syncthreads();
   }
-  if constexpr (DOT4) {
+  if constexpr (DOT4 && MR == 2) {
 #pragma unroll
     for (int m = 0; m < 2; ++m)
       if (ks == 0 && m < M) epi_load2(epre[m], a, epi, nb_c, n_local);
@@ -459,6 +472,9 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[mt][r] = 0.0f;
+  float accm[MR];  // batched dot4: per-lane sums of every row
+#pragma unroll
+  for (int m = 0; m < MR; ++m) accm[m] = 0.0f;
 
   if (nb < NB) {
     const v4i zero = {0, 0, 0, 0};
@@ -487,7 +503,34 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (q + u >= nq) break;
-        if constexpr (DOT4) {
+        if constexpr (DOT4 && MR > 2) {
+          // batched dot4 (one-digit planes): the codes become signed once
+          // per group and serve every row; each row's dot starts from the
+          // bits of 1.5 * 2^23, so fma(that as f32, ws, -12582912 * ws) is
+          // RN(T * ws) in one instruction (|T| < 2^22)
+          const int g = (kq0 + q + u) * 4 + c;
+          const uint32_t wj[4] = {wc[u].x, wc[u].y, wc[u].z, wc[u].w};
+          int sw[8];
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const long sc2 = signed_codes(wj[w]);
+            sw[2 * w] = (int)(uint32_t)sc2;
+            sw[2 * w + 1] = (int)(uint32_t)((uint64_t)sc2 >> 32);
+          }
+          const float ws = h2f(sc[u]), wcorr = -12582912.0f * ws;
+#pragma unroll
+          for (int m = 0; m < MR; ++m) {
+            if (m >= M) break;
+            const int4 q0 = *(const int4 *)(aq + ((size_t)g * M + m) * 32);
+            const int4 q1 = *(const int4 *)(aq + ((size_t)g * M + m) * 32 + 16);
+            const int qa[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+            int t = kMagic;
+#pragma unroll
+            for (int w = 0; w < 8; ++w) t = __builtin_amdgcn_sdot4(sw[w], qa[w], t, false);
+            const float tw = fmaf(__int_as_float(t), ws, wcorr);
+            accm[m] = fmaf(tw, am[(size_t)g * M + m].scale, accm[m]);
+          }
+        } else if constexpr (DOT4) {
           // lane (j = c, n): all 32 codes of group g of row n
           const int g = (kq0 + q + u) * 4 + c;
           const uint32_t wj[4] = {wc[u].x, wc[u].y, wc[u].z, wc[u].w};
@@ -516,33 +559,64 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
             acc[0][m] += tt;
           }
         } else {
+          // MFMA: one v_mfma_i32_16x16x32_i8 per (group, 16-row tile, digit)
+          // on signed codes, so the result is the group dot T itself. With
+          // one digit the accumulator starts at the bits of 1.5 * 2^23: the
+          // sum read as f32 is 12582912 + T exactly (|T| < 2^22), and
+          // fma(that, ws, -12582912 * ws) = RN(T * ws) in one instruction
+          // (-12582912 * ws is exact for an fp16 ws). Three digits chain
+          // through 7-bit shifts to the exact 128-adic T and convert.
           const uint32_t wj[4] = {wc[u].x, wc[u].y, wc[u].z, wc[u].w};
           const float wsj[4] = {scm[u].x, scm[u].y, scm[u].z, scm[u].w};
+          const v4i magic = {kMagic, kMagic, kMagic, kMagic};
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int g = (kq0 + q + u) * 4 + j;  // absolute group index
-            const long b = unpack_codes(wj[j]);
+            const long b = signed_codes(wj[j]);
+            const float ws = wsj[j], wcorr = -12582912.0f * wsj[j];
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
               const int ma = mt * 16 + n_local;
-              v4i dd[D];
+              long av[D];
 #pragma unroll
               for (int d = 0; d < D; ++d) {
-                long av = 0;
-                if (ma < M) av = *(const long *)(aq + (((size_t)g * D + d) * M + ma) * 32 + c * 8);
-                dd[d] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, b, zero, 0, 0, 0);
+                av[d] = 0;
+                if (ma < M) av[d] = *(const long *)(aq + (((size_t)g * D + d) * M + ma) * 32 + c * 8);
               }
+              // activation scales of rows mr .. mr + 3
+              const int mr = mt * 16 + c * 4;
+              float as[4];
+              if (mr + 3 < M && (((size_t)g * M) & 1) == 0) {  // 16-byte aligned pairs
+                const float4 m01 = *(const float4 *)(am + (size_t)g * M + mr);
+                const float4 m23 = *(const float4 *)(am + (size_t)g * M + mr + 2);
+                as[0] = m01.x;
+                as[1] = m01.z;
+                as[2] = m23.x;
+                as[3] = m23.z;
+              } else {
 #pragma unroll
-              for (int r = 0; r < 4; ++r) {
-                const int m = mt * 16 + c * 4 + r;
-                if (m < M) {
+                for (int r = 0; r < 4; ++r) as[r] = mr + r < M ? am[(size_t)g * M + mr + r].scale : 0.0f;
+              }
+              if constexpr (D == 1) {
+                const v4i dd = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[0], b, magic, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                  const float t = fmaf(__int_as_float(dd[r]), ws, wcorr);
+                  acc[mt][r] = fmaf(t, as[r], acc[mt][r]);
+                }
+              } else {
+                // independent MFMAs per digit (no accumulator chain between
+                // them), combined as the exact 128-adic integer
+                v4i dd[D];
+#pragma unroll
+                for (int d = 0; d < D; ++d)
+                  dd[d] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[d], b, zero, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
                   int T = dd[0][r];
-                  if constexpr (D == 3) T = dd[0][r] * 16384 + dd[1][r] * 128 + dd[2][r];
-                  const ActMeta mm = am[(size_t)g * M + m];
-                  const float v = (float)(T - mm.corr);
-                  float tt = v * wsj[j];
-                  tt = tt * mm.scale;
-                  acc[mt][r] += tt;
+#pragma unroll
+                  for (int d = 1; d < D; ++d) T = (T << 7) + dd[d][r];
+                  acc[mt][r] = fmaf((float)T * ws, as[r], acc[mt][r]);
                 }
               }
             }
@@ -552,7 +626,26 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
     }
   }
 
-  if constexpr (DOT4) {
+  if constexpr (DOT4 && MR > 2) {
+    // accm[m] of lane (j, n) sums the groups j, j + 4, ... of row n; after
+    // adding the four lanes of the row, lane (c, n) keeps rows 4c .. 4c + 3
+    // in acc[0][r] (the epilogue's row mapping m = 4c + r)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      float v = accm[m];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      accm[m] = v;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float v = 0.0f;
+#pragma unroll
+      for (int m = r; m < MR; m += 4)
+        if (m == 4 * c + r) v = accm[m];
+      acc[0][r] = v;
+    }
+  } else if constexpr (DOT4) {
     // acc[0][m] of lane (j, n) sums the groups j, j + 4, ... of row n; add
     // the four lanes of the row so lanes j = 0 hold m = 0.. M-1 as (c=0, r=m)
 #pragma unroll
@@ -620,7 +713,7 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
         // residual output y = resid + tot, and this wave's sum of y^2 of row m
         float y = 0.0f;
         if (lead && m < M) {
-          const EpiIn e = DOT4 ? epre[m & 1] : epi_load(a, epi, nb, n_local, m);
+          const EpiIn e = (DOT4 && MR == 2) ? epre[m & 1] : epi_load(a, epi, nb, n_local, m);
           y = e.resid + tot;
           a.y[(size_t)m * a.N + nb * 16 + n_local] = y;
         }
@@ -639,7 +732,7 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
         }
       } else {
         store_output(a, epi, nb, n_local, m, tot, partner,
-                     DOT4 ? epre[m & 1] : epi_load(a, epi, nb, n_local, m));
+                     (DOT4 && MR == 2) ? epre[m & 1] : epi_load(a, epi, nb, n_local, m));
       }
     }
   if (resid_ss) {
@@ -715,6 +808,11 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
   }
 }
 
+// 3..16 rows of one-digit planes that fit in LDS run the batched dot4 kernel.
+static bool dot4_rows_ok(const GemvArgs &a, const GemvShape &p) {
+  return a.M > 2 && a.M <= 16 && a.D == 1 && p.lds_a && !a.force_mfma;
+}
+
 // Launch shape for these arguments; also fills the fields launch_gemv
 // derives (ksplit, LDS offsets). False when the arguments are invalid.
 static bool gemv_shape(GemvArgs &a, GemvShape &p) {
@@ -730,7 +828,18 @@ static bool gemv_shape(GemvArgs &a, GemvShape &p) {
   if (a.in_ss && (!a.x_in || a.in_ss_count <= 0 || a.in_ss_count > kMaxSsParts || a.M > 32))
     return false;
   p = plan_gemv(a.N, a.K, a.M, a.D);
-  if (a.x_in && a.M <= 2) {
+  if (dot4_rows_ok(a, p)) {
+    // the batched dot4 kernel streams like the decode one: its launch shape
+    const GemvShape d = plan_gemv(a.N, a.K, 2, a.D);
+    p.ksplit = d.ksplit;
+    p.rb = d.rb;
+    p.waves = d.waves;
+    p.grid = d.grid;
+    p.unroll = 4;
+    const size_t red = (size_t)p.waves * MT * 4 * 64 * sizeof(float);
+    p.lds_bytes = std::max(planes_bytes(a.K / 32, a.M, a.D) + a.M * 4, red);
+  }
+  if (a.x_in && (a.M <= 2 || dot4_rows_ok(a, p))) {
     // input mode: every workgroup quantises the whole input row, so fewer,
     // wider workgroups (8 waves; the K split only for short row counts)
     // measured faster on the 7B QKV and gate/up shapes
@@ -761,6 +870,21 @@ static bool gemv_shape(GemvArgs &a, GemvShape &p) {
     p.lds_bytes = std::max(p.lds_a ? planes_bytes(a.K / 32, a.M, a.D) + a.M * 4 : 0, red);
     if (emit_planes && p.rb % 4) return false;
   }
+  if ((a.M > 2 || a.force_mfma) && !dot4_rows_ok(a, p) && p.waves > 8) {
+    // the MFMA kernel runs at most 8 waves per workgroup (VGPR budget)
+    if (a.ksplit_override > 0) return false;
+    while (p.ksplit > 1 && p.ksplit * p.rb > 8) p.ksplit /= 2;
+    if (p.ksplit * p.rb > 8) return false;
+    p.waves = p.ksplit * p.rb;
+    const size_t red = (size_t)p.waves * MT * 4 * 64 * sizeof(float);
+    p.lds_bytes = std::max(p.lds_a ? planes_bytes(a.K / 32, a.M, a.D) + a.M * 4 : 0, red);
+  }
+  if (dot4_rows_ok(a, p) && p.waves > 8) {
+    // the batched dot4 kernel runs at most 8 waves per workgroup
+    while (p.ksplit > 1 && p.ksplit * p.rb > 8) p.ksplit /= 2;
+    if (p.ksplit * p.rb > 8) return false;
+    p.waves = p.ksplit * p.rb;
+  }
   // input mode: the planes are built in LDS, so they must fit there
   if (a.x_in && !p.lds_a) return false;
   if (resid_ss && p.grid > kMaxSsParts) return false;
@@ -788,6 +912,7 @@ hipError_t launch_gemv(const GemvArgs &a0, hipStream_t st) {
   const int MT = (a.M + 15) / 16;
   dim3 grid(p.grid), block(64 * p.waves);
   const bool dot4 = a.M <= 2 && !a.force_mfma;
+  const bool dot4_rows = dot4_rows_ok(a, p);
   const bool small = p.waves <= 4;
   // U = 8 (quads in flight per wave) only for the MFMA kernel with small
   // workgroups: it needs more than the 128 VGPRs a 1024-thread workgroup
@@ -796,12 +921,18 @@ hipError_t launch_gemv(const GemvArgs &a0, hipStream_t st) {
   if (U != 8 || dot4 || !small) U = 4;
   const size_t lds = p.lds_bytes;
 #define GK_KERNEL(DD, MM, UU, LL, T4, LBB, EE, XX) gemv_kernel<DD, MM, UU, LL, T4, LBB, EE, XX>
+#define GK_LAUNCH(KERNEL)                                                                       \
+  do {                                                                                          \
+    if (lds > 64 * 1024)                                                                        \
+      (void)hipFuncSetAttribute((const void *)KERNEL, hipFuncAttributeMaxDynamicSharedMemorySize, \
+                                (int)lds);                                                      \
+    hipLaunchKernelGGL(KERNEL, grid, block, lds, st, a);                                        \
+  } while (0)
+  // dot4 workgroups up to 16 waves; MFMA workgroups up to 8 (VGPR budget)
 #define GK_GO(DD, MM, UU, LL, T4, EE, XX)                                                           \
   do {                                                                                          \
-    if (small)                                                                                  \
-      hipLaunchKernelGGL((GK_KERNEL(DD, MM, UU, LL, T4, 256, EE, XX)), grid, block, lds, st, a);  \
-    else                                                                                        \
-      hipLaunchKernelGGL((GK_KERNEL(DD, MM, UU, LL, T4, 1024, EE, XX)), grid, block, lds, st, a); \
+    if (small) GK_LAUNCH((GK_KERNEL(DD, MM, UU, LL, T4, 256, EE, XX)));                          \
+    else GK_LAUNCH((GK_KERNEL(DD, MM, UU, LL, T4, ((T4) ? 1024 : 512), EE, XX)));               \
   } while (0)
   // dot4 (decode) launches carry their epilogue type at compile time
 #define GK_DOT4(DD, LL, XX)                                                \
@@ -813,15 +944,25 @@ hipError_t launch_gemv(const GemvArgs &a0, hipStream_t st) {
       default: GK_GO(DD, 1, 4, LL, true, EPI_QKV, XX); break;              \
     }                                                                      \
   } while (0)
+#define GK_DOT4_ROWS(XX)                                                                          \
+  do {                                                                                           \
+    switch (a.epi) {                                                                             \
+      case EPI_PLAIN: GK_LAUNCH((gemv_kernel<1, 1, 4, true, true, 512, EPI_PLAIN, XX, 16>)); break;   \
+      case EPI_RESID: GK_LAUNCH((gemv_kernel<1, 1, 4, true, true, 512, EPI_RESID, XX, 16>)); break;   \
+      case EPI_SWIGLU: GK_LAUNCH((gemv_kernel<1, 1, 4, true, true, 512, EPI_SWIGLU, XX, 16>)); break; \
+      default: GK_LAUNCH((gemv_kernel<1, 1, 4, true, true, 512, EPI_QKV, XX, 16>)); break;            \
+    }                                                                                            \
+  } while (0)
 #define GK_PATH(DD, LL, XX)                                                                      \
   do {                                                                                          \
     if (MT == 2) GK_GO(DD, 2, 4, LL, false, -1, XX);                                            \
     else if (dot4) GK_DOT4(DD, LL, XX);                                                         \
-    else if (U == 8 && small)                                                                   \
-      hipLaunchKernelGGL((GK_KERNEL(DD, 1, 8, LL, false, 256, -1, XX)), grid, block, lds, st, a); \
+    else if (U == 8 && small) GK_LAUNCH((GK_KERNEL(DD, 1, 8, LL, false, 256, -1, XX)));       \
     else GK_GO(DD, 1, 4, LL, false, -1, XX);                                                    \
   } while (0)
-  if (a.x_in) {
+  if (dot4_rows) {
+    if (a.x_in) GK_DOT4_ROWS(true); else GK_DOT4_ROWS(false);
+  } else if (a.x_in) {
     if (a.D == 1) GK_PATH(1, true, true); else GK_PATH(3, true, true);
   } else if (a.D == 1) {
     if (p.lds_a) GK_PATH(1, true, false); else GK_PATH(1, false, false);
@@ -829,8 +970,10 @@ hipError_t launch_gemv(const GemvArgs &a0, hipStream_t st) {
     if (p.lds_a) GK_PATH(3, true, false); else GK_PATH(3, false, false);
   }
 #undef GK_DOT4
+#undef GK_DOT4_ROWS
 #undef GK_PATH
 #undef GK_GO
+#undef GK_LAUNCH
 #undef GK_KERNEL
   return hipGetLastError();
 }
@@ -1719,7 +1862,26 @@ __global__ __launch_bounds__(kArgBlock) void argmax_parts_kernel(const ArgPartia
   if (t == 0) arg_write_result(r, wr != nullptr, n, &result[row]);
 }
 
-int gemv_argmax_parts(int N, int K, int M, int D) { return plan_gemv(N, K, M, D).grid; }
+int gemv_argmax_parts(int N, int K, int M, int D) {
+  // the grid of the fused-head launch itself (gemv_shape adjusts the plain
+  // plan per path); the shape only tests these pointers for null
+  static int8_t q_tag;
+  static ActMeta meta_tag;
+  static float y_tag;
+  static ArgPartial part_tag;
+  GemvArgs a{};
+  a.N = N;
+  a.K = K;
+  a.M = M;
+  a.D = D;
+  a.epi = EPI_PLAIN;
+  a.act_q = &q_tag;
+  a.act_meta = &meta_tag;
+  a.y = &y_tag;
+  a.arg_parts = &part_tag;
+  GemvShape p;
+  return gemv_shape(a, p) ? p.grid : -1;
+}
 
 hipError_t launch_argmax_parts(const ArgPartial *parts, int nparts, long n, int rows,
                                const uint64_t *words, long word_count, ArgmaxResult *result,

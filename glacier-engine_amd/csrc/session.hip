@@ -1030,8 +1030,9 @@ glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
   size_t arg_bytes = gk::argmax_scratch_bytes((int)L, (long)c.vocab_size);
   for (uint32_t r = 1; r <= std::min<uint32_t>(L, 32); ++r)
     arg_bytes = std::max(arg_bytes, (size_t)r * sizeof(gk::ArgPartial) *
-                                        gk::gemv_argmax_parts((int)c.vocab_size, (int)c.dim,
-                                                              (int)r, head_D(s)));
+                                        std::max(0, gk::gemv_argmax_parts((int)c.vocab_size,
+                                                                          (int)c.dim, (int)r,
+                                                                          head_D(s))));
   A(&s->arg_scratch, arg_bytes);
   A((void **)&s->arg_counters, (size_t)L * 4);
   A((void **)&s->arg_result, (size_t)L * sizeof(gk::ArgmaxResult));
