@@ -49,6 +49,31 @@ static __device__ __forceinline__ long signed_codes(uint32_t w) {
 
 static constexpr int kMagic = 0x4B400000;  // bits of 12582912.0f = 1.5 * 2^23
 
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
+
+// Even lanes: (own u16) | (u16 of the next lane) << 16; DPP quad_perm
+// [1, 0, 3, 2] reads the neighbour's value without a trip through LDS.
+static __device__ __forceinline__ uint32_t scale_pair(uint32_t s) {
+  const uint32_t nb = (uint32_t)__builtin_amdgcn_mov_dpp((int)s, 0xB1, 0xF, 0xF, false);
+  return (s & 0xFFFFu) | (nb << 16);
+}
+
+// 4 x 4 transpose of u32 words across the four 16-lane rows of a wave: on
+// entry lane (c, n) = 16c + n holds words 0..3 of its tile slot (group c of
+// weight row n, one coalesced 16-byte load per lane); on return it holds
+// word c of groups 0..3 of row n, which is the B operand layout of
+// v_mfma_i32_16x16x32_i8 for each of the four groups (lane (c, n) = codes
+// 8c .. 8c + 7 of row n). The 32-lane swap exchanges the upper rows of one
+// register with the lower rows of the other, the 16-lane swap the odd rows
+// of one with the even rows of the other.
+static __device__ __forceinline__ uint4 quad_transpose(uint4 v) {
+  const v2u a = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
+  const v2u b = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
+  const v2u c = __builtin_amdgcn_permlane16_swap(a.x, b.x, false, false);
+  const v2u d = __builtin_amdgcn_permlane16_swap(a.y, b.y, false, false);
+  return make_uint4(c.x, c.y, d.x, d.y);
+}
+
 // ---------------------------------------------------------------------------
 // K4: activation planes (+ optional RMSNorm)
 // ---------------------------------------------------------------------------
@@ -277,24 +302,19 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
   // The first U quads of weights are requested before the activation planes
   // are staged, so the staging latency hides under the weight fetch.
   const size_t tile0 = (size_t)min(nb, NB - 1) * KQ + kq0;
-  const uint4 *cp = a.codes + tile0 * 64 + lane;                       // DOT4: own 16 B
-  const uint32_t *cw = (const uint32_t *)a.codes + tile0 * 256 + n_local * 4 + c;  // MFMA
+  // (every lane loads its own 16-byte tile slot; the MFMA path transposes
+  // the words across lanes at use)
+  const uint4 *cp = a.codes + tile0 * 64 + lane;
   const uint16_t *spp = (const uint16_t *)a.scales + tile0 * 64;
+  // (the scales too: one u16 per lane in its slot's order; the MFMA path
+  // redistributes them across lanes at use)
   uint4 wb[U];
-  uint16_t sb[U];
-  float4 sbm[U];
+  uint32_t sb[U];
 #pragma unroll
   for (int u = 0; u < U; ++u)
     if (u < nq) {
-      if (DOT4) {
-        wb[u] = load_stream(cp + (size_t)u * 64);
-        sb[u] = spp[(size_t)u * 64 + lane];
-      } else {
-        const uint32_t *w0 = cw + (size_t)u * 256;
-        wb[u] = make_uint4(w0[0], w0[64], w0[128], w0[192]);
-        const uint16_t *s0 = spp + (size_t)u * 64 + n_local;
-        sbm[u] = make_float4(h2f(s0[0]), h2f(s0[16]), h2f(s0[32]), h2f(s0[48]));
-      }
+      wb[u] = load_stream(cp + (size_t)u * 64);
+      sb[u] = spp[(size_t)u * 64 + lane];
     }
 
   // Epilogue inputs of the (at most two) rows of a dot4 launch: the first
@@ -480,29 +500,35 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
     const v4i zero = {0, 0, 0, 0};
     for (int q = 0; q < nq; q += U) {
       uint4 wc[U];
-      uint16_t sc[U];
-      float4 scm[U];
+      uint32_t sc[U];
+      if constexpr (DOT4) {
+        // all U quads move to the working registers, then U new ones are
+        // requested
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        wc[u] = wb[u];
-        if (DOT4) sc[u] = sb[u]; else scm[u] = sbm[u];
-      }
+        for (int u = 0; u < U; ++u) {
+          wc[u] = wb[u];
+          sc[u] = sb[u];
+        }
 #pragma unroll
-      for (int u = 0; u < U; ++u)
-        if (q + U + u < nq) {
-          if (DOT4) {
+        for (int u = 0; u < U; ++u)
+          if (q + U + u < nq) {
             wb[u] = load_stream(cp + (size_t)(q + U + u) * 64);
             sb[u] = spp[(size_t)(q + U + u) * 64 + lane];
-          } else {
-            const uint32_t *w0 = cw + (size_t)(q + U + u) * 256;
-            wb[u] = make_uint4(w0[0], w0[64], w0[128], w0[192]);
-            const uint16_t *s0 = spp + (size_t)(q + U + u) * 64 + n_local;
-            sbm[u] = make_float4(h2f(s0[0]), h2f(s0[16]), h2f(s0[32]), h2f(s0[48]));
           }
-        }
+      }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (q + u >= nq) break;
+        if constexpr (!DOT4) {
+          // MFMA: each slot is refilled as soon as it is taken, so only U + 1
+          // quads occupy registers
+          wc[u] = wb[u];
+          sc[u] = sb[u];
+          if (q + U + u < nq) {
+            wb[u] = load_stream(cp + (size_t)(q + U + u) * 64);
+            sb[u] = spp[(size_t)(q + U + u) * 64 + lane];
+          }
+        }
         if constexpr (DOT4 && MR > 2) {
           // batched dot4 (one-digit planes): the codes become signed once
           // per group and serve every row; each row's dot starts from the
@@ -560,67 +586,65 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
           }
         } else {
           // MFMA: one v_mfma_i32_16x16x32_i8 per (group, 16-row tile, digit)
-          // on signed codes, so the result is the group dot T itself. With
+          // with the weights as the A operand and the activations as B, so
+          // lane (c, m) holds D[n = 4c + r][m]: one activation scale per lane
+          // and group, the weight scales of rows 4c .. 4c + 3 in one 8-byte
+          // load. The codes are signed, so D is the group dot T itself. With
           // one digit the accumulator starts at the bits of 1.5 * 2^23: the
           // sum read as f32 is 12582912 + T exactly (|T| < 2^22), and
           // fma(that, ws, -12582912 * ws) = RN(T * ws) in one instruction
-          // (-12582912 * ws is exact for an fp16 ws). Three digits chain
-          // through 7-bit shifts to the exact 128-adic T and convert.
-          const uint32_t wj[4] = {wc[u].x, wc[u].y, wc[u].z, wc[u].w};
-          const float wsj[4] = {scm[u].x, scm[u].y, scm[u].z, scm[u].w};
+          // (-12582912 * ws is exact for an fp16 ws). Three digits run
+          // independent MFMAs combined as the exact 128-adic T.
+          const uint4 wt = quad_transpose(wc[u]);
+          const uint32_t wj[4] = {wt.x, wt.y, wt.z, wt.w};
           const v4i magic = {kMagic, kMagic, kMagic, kMagic};
+          // lane L holds the scale of slot L; pair it with slot L ^ 1, then
+          // fetch the pairs (16 j + 4 c, +1) and (16 j + 4 c + 2, +3)
+          const uint32_t sp = scale_pair(sc[u]);
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int g = (kq0 + q + u) * 4 + j;  // absolute group index
             const long b = signed_codes(wj[j]);
-            const float ws = wsj[j], wcorr = -12582912.0f * wsj[j];
+            const uint32_t s01 = __builtin_amdgcn_ds_bpermute((16 * j + 4 * c) * 4, (int)sp);
+            const uint32_t s23 = __builtin_amdgcn_ds_bpermute((16 * j + 4 * c + 2) * 4, (int)sp);
+            const float ws[4] = {h2f(s01 & 0xFFFFu), h2f(s01 >> 16), h2f(s23 & 0xFFFFu),
+                                 h2f(s23 >> 16)};
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-              const int ma = mt * 16 + n_local;
+              // activation row of this lane, clamped: columns m >= M of the
+              // tile compute a copy of row M - 1 and are never stored (no
+              // branch splits the wave around the loads)
+              const int ma = min(mt * 16 + n_local, M - 1);
               long av[D];
 #pragma unroll
-              for (int d = 0; d < D; ++d) {
-                av[d] = 0;
-                if (ma < M) av[d] = *(const long *)(aq + (((size_t)g * D + d) * M + ma) * 32 + c * 8);
-              }
-              // activation scales of rows mr .. mr + 3
-              const int mr = mt * 16 + c * 4;
-              float as[4];
-              if (mr + 3 < M && (((size_t)g * M) & 1) == 0) {  // 16-byte aligned pairs
-                const float4 m01 = *(const float4 *)(am + (size_t)g * M + mr);
-                const float4 m23 = *(const float4 *)(am + (size_t)g * M + mr + 2);
-                as[0] = m01.x;
-                as[1] = m01.z;
-                as[2] = m23.x;
-                as[3] = m23.z;
-              } else {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) as[r] = mr + r < M ? am[(size_t)g * M + mr + r].scale : 0.0f;
-              }
+              for (int d = 0; d < D; ++d)
+                av[d] = *(const long *)(aq + (((size_t)g * D + d) * M + ma) * 32 + c * 8);
+              const float as = am[(size_t)g * M + ma].scale;
               if constexpr (D == 1) {
-                const v4i dd = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[0], b, magic, 0, 0, 0);
+                const v4i dd = __builtin_amdgcn_mfma_i32_16x16x32_i8(b, av[0], magic, 0, 0, 0);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                  const float t = fmaf(__int_as_float(dd[r]), ws, wcorr);
-                  acc[mt][r] = fmaf(t, as[r], acc[mt][r]);
+                  const float t = fmaf(__int_as_float(dd[r]), ws[r], -12582912.0f * ws[r]);
+                  acc[mt][r] = fmaf(t, as, acc[mt][r]);
                 }
               } else {
-                // independent MFMAs per digit (no accumulator chain between
-                // them), combined as the exact 128-adic integer
                 v4i dd[D];
 #pragma unroll
                 for (int d = 0; d < D; ++d)
-                  dd[d] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[d], b, zero, 0, 0, 0);
+                  dd[d] = __builtin_amdgcn_mfma_i32_16x16x32_i8(b, av[d], zero, 0, 0, 0);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                   int T = dd[0][r];
 #pragma unroll
                   for (int d = 1; d < D; ++d) T = (T << 7) + dd[d][r];
-                  acc[mt][r] = fmaf((float)T * ws, as[r], acc[mt][r]);
+                  acc[mt][r] = fmaf((float)T * ws[r], as, acc[mt][r]);
                 }
               }
             }
           }
+          // keep each quad's LDS reads and MFMA results within the quad
+          // (hoisting them across quads costs occupancy)
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
     }
@@ -661,7 +685,31 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
   // (no early return: the SwiGLU plane epilogue below synchronises the
   // whole workgroup again)
   const bool lead = ks == 0 && nb < NB;
-  if (KS > 1) {
+  if constexpr (!DOT4) {
+    // The MFMA tiles hold D[n][m] (lane (c, m): n = 4c + r). Every wave
+    // writes them to LDS in the epilogue's layout (lane (c, n): rows
+    // m = 4c + r), and the first wave of each row block adds the K split's
+    // waves in a fixed order.
+    if (LDS_A) __syncthreads();  // the planes region is reused below
+    float *red = (float *)smem;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        red[((wave * MT + mt) * 4 + (n_local & 3)) * 64 + (n_local >> 2) * 16 + 4 * c + r] =
+            acc[mt][r];
+    __syncthreads();
+    if (ks == 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float tot = red[((wave * MT + mt) * 4 + r) * 64 + lane];
+          for (int s2 = 1; s2 < KS; ++s2) tot += red[(((wave + s2) * MT + mt) * 4 + r) * 64 + lane];
+          acc[mt][r] = tot;
+        }
+    }
+  } else if (KS > 1) {
     if (LDS_A) __syncthreads();  // the planes region is reused below
     float *red = (float *)smem;
 #pragma unroll
@@ -808,9 +856,11 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
   }
 }
 
-// 3..16 rows of one-digit planes that fit in LDS run the batched dot4 kernel.
+// 3..5 rows of one-digit planes that fit in LDS run the batched dot4 kernel
+// (its cost grows with every row; from 8 rows on the MFMA kernel measured
+// faster on the 7B shapes, about even at 5).
 static bool dot4_rows_ok(const GemvArgs &a, const GemvShape &p) {
-  return a.M > 2 && a.M <= 16 && a.D == 1 && p.lds_a && !a.force_mfma;
+  return a.M > 2 && a.M <= 5 && a.D == 1 && p.lds_a && !a.force_mfma;
 }
 
 // Launch shape for these arguments; also fills the fields launch_gemv

@@ -413,10 +413,15 @@ gk::GemvArgs proj_args(glacier_hip_session *s, glacier_hip_int4_weight *w, int D
 }
 
 // GEMV arguments in input mode (planes built in LDS, deferred RMSNorm), or
-// false when this projection cannot run that way.
+// false when this projection cannot run that way. Every workgroup quantises
+// the whole input, so the mode only pays for a few rows: from 8 rows on the
+// separate conversion kernel plus the plain GEMV measured faster (7B QKV and
+// gate/up), about even at 4-5.
+constexpr int kInputModeRows = 4;
+
 bool input_mode_args(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, int rows, int epi,
                      const ProjIn &in, const ProjOut &out, gk::GemvArgs *a) {
-  if (!in.x || rows > 32 || (in.norm_w && !in.ss)) return false;
+  if (!in.x || rows > kInputModeRows || (in.norm_w && !in.ss)) return false;
   *a = proj_args(s, w, D, rows, epi, in, out);
   a->x_in = in.x;
   a->norm_w = in.norm_w;
@@ -465,10 +470,11 @@ hipError_t run_proj(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, i
 // Decode-sized row sets (rows <= 32) run a chain with no conversion kernels:
 // the gather and each residual projection (O, down) also write per-workgroup
 // sums of squares of their output, from which the next RMSNorm'd projection
-// (QKV, gate/up, LM head) finishes its deferred norm while it quantises its
-// input in LDS; attention writes the O projection's planes and gate/up the
-// down projection's. Longer row sets (prefill chunks) convert each input
-// with a separate kernel.
+// (QKV, gate/up) finishes its deferred norm while it quantises its input in
+// LDS (up to kInputModeRows rows; more rows convert with the separate
+// kernel); attention writes the O projection's planes and gate/up the down
+// projection's. Longer row sets (prefill chunks) convert each input with a
+// separate kernel.
 hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, hipStream_t st) {
   glacier_hip_model *m = s->model;
   const auto &c = m->cfg;
@@ -488,10 +494,11 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
   q.num_heads = (int)c.num_heads;
   q.num_kv_heads = (int)c.num_kv_heads;
   q.head_dim = (int)c.head_dim;
-  float *ss = chain ? s->ss_parts : nullptr;
+  // deferred RMSNorm partial sums, for consumers that run in input mode
+  float *ss = chain && rows <= kInputModeRows ? s->ss_parts : nullptr;
   hipError_t e = gk::launch_gather_rows(m->embed, rp.tokens, rows, D, s->x_res, st, ss);
   if (e != hipSuccess) return e;
-  int ss_count = chain ? gk::gather_ss_parts(D) : 0;  // partial sums behind x_res
+  int ss_count = ss ? gk::gather_ss_parts(D) : 0;  // partial sums behind x_res
   for (uint32_t l = 0; l < c.num_layers; ++l) {
     const LayerDev &L = m->layers[l];
     q.layer = (int)l;
@@ -531,7 +538,7 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
     } else {
       oin.x = s->attn;
     }
-    if (chain) {
+    if (ss) {
       ss_count = proj_grid(s, L.o, Do, rows, gk::EPI_RESID, oin, oout);
       if (ss_count <= 0) return hipErrorInvalidValue;
     }
@@ -563,7 +570,7 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
     } else {
       din.x = s->act;
     }
-    if (chain && !last) {
+    if (ss && !last) {
       ss_count = proj_grid(s, L.down, Dd, rows, gk::EPI_RESID, din, dout);
       if (ss_count <= 0) return hipErrorInvalidValue;
     }
