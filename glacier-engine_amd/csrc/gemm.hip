@@ -7,26 +7,30 @@
 // scaled by the weight and activation group scales and summed in f32.
 //
 // One v_mfma_i32_16x16x32_i8 covers exactly one group of a 16x16 output tile.
-// The weight codes are turned into signed int8 (u - 7) in registers, so the
-// MFMA result is the group dot itself (no correction term). The MFMA
-// accumulator input is preset to 0x4B400000, the bit pattern of 1.5 * 2^23:
-// for |T| < 2^22 the integer sum 0x4B400000 + T read as f32 is exactly
-// 12582912 + T, so  fma(that, ws, -12582912 * ws)  yields RN(T * ws) (the
-// reference's f32(T) * s_w) in one instruction with no int->float convert;
-// -12582912 * ws is exact because ws is an fp16 value. The activation scale is
-// then applied with one fma into the running sum. Three-digit (f32
-// activation) planes chain three MFMAs with a 7-bit shift between them, which
-// gives the exact 128-adic integer T; |T| can exceed 2^22 there, so that path
-// converts explicitly.
+// The weight codes are made signed (u - 7) in registers, so the MFMA result
+// is the group dot T itself; with one digit the accumulator starts at the
+// bits of 1.5 * 2^23 and fma(that as f32, ws, -12582912 * ws) = RN(T * ws)
+// (int4_ops.h), then one fma applies the activation scale into the running
+// sum. Three-digit (f32 activation) planes run three independent MFMAs and
+// combine them as the exact 128-adic integer.
 //
-// Block = 4 waves in a 2 x 2 arrangement, a wave owns MT x NT 16x16 output
-// tiles, loads straight from HBM/L2 (A rows of one group are 512 contiguous
-// bytes per tile, B codes 256 contiguous bytes per tile) and keeps the next
-// group's operands in flight while it computes the current one. Block ids are
-// remapped so that the blocks of one weight column tile run on one XCD
-// (hardware places block b on XCD b % 8), which keeps that tile in the XCD's
-// L2 for every row tile that reads it.
+// The per-group scaling (two fmas per output and group against one MFMA per
+// 16 x 16 x 32 group tile) bounds this kernel by VALU issue, not by the
+// matrix cores; the layout keeps everything else off that path:
+//   * workgroup = 4 waves over a 64-row x 256-column output tile; each wave
+//     owns 4 weight row blocks (64 columns) x the 4 activation row tiles;
+//   * weights: each lane loads its own 16-byte tile slot per row block and
+//     quad (1 KB per wave, fully coalesced), two quads in flight; the words
+//     are transposed across lanes into MFMA operands (quad_transpose) and
+//     the lane-ordered fp16 scales gathered per column (column_gather);
+//   * activations: the workgroup stages each quad's digit planes (64 rows x
+//     128 columns x D) and their scales in LDS, double buffered, one barrier
+//     per quad; every wave reads its operands from there;
+//   * block ids are remapped so that the row tiles of one weight column tile
+//     run on one XCD (hardware places block b on XCD b % 8), which keeps the
+//     tile's weights in that XCD's L2 for every row tile that reads them.
 #include "epilogue.h"
+#include "int4_ops.h"
 #include "kernels.h"
 
 #include <algorithm>
@@ -35,162 +39,234 @@ namespace gk {
 
 namespace {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
+constexpr int kBM = 64;              // activation rows per workgroup
+constexpr int kWaves = 4;            // waves per workgroup, side by side in N
+constexpr int kU = 2;                // weight quads in flight per wave
 
-constexpr int kMagic = 0x4B400000;        // bits of 12582912.0f = 1.5 * 2^23
-constexpr float kMagicF = 12582912.0f;
-
-// 8 codes (u32 word: low nibbles k0..3, high nibbles k4..7) -> 8 signed bytes
-// (u - 7). Per byte, u + 0x79 stays below 0x100, and flipping bit 7 of
-// (u + 121) gives (u - 7) in two's complement.
-__device__ __forceinline__ long signed_codes(uint32_t w) {
-  const uint32_t lo = ((w & 0x0F0F0F0Fu) + 0x79797979u) ^ 0x80808080u;
-  const uint32_t hi = (((w >> 4) & 0x0F0F0F0Fu) + 0x79797979u) ^ 0x80808080u;
-  return (long)(((uint64_t)hi << 32) | (uint64_t)lo);
-}
-
-__device__ __forceinline__ float h2f(uint32_t bits16) {
-  return __half2float(__ushort_as_half((unsigned short)bits16));
-}
-
-template <int D, int MT, int NT>
-struct GroupOps {
-  long a[MT][D];
-  uint32_t w[NT];
-  uint32_t s[NT];
-  float as[MT][4];
+template <int D>
+struct ActStage {
+  static constexpr int kActBytes = 4 * D * kBM * 32;    // [4 groups][D][kBM rows][32]
+  static constexpr int kBufBytes = kActBytes + 4 * kBM * 4;  // + scales [4][kBM]
+  static constexpr int kUnits = kActBytes / 16 / 256;    // 16-byte loads per thread
 };
 
-template <int D, int MT, int NT>
-__device__ __forceinline__ void load_group(const GemvArgs &p, int g, int m0, int nb0, int KQ,
-                                           int NB, int n_local, int c, GroupOps<D, MT, NT> &o) {
-  const int M = p.M;
-  const uint32_t *codes = (const uint32_t *)p.codes;
-  const uint16_t *scales = (const uint16_t *)p.scales;
-  const int kq = g >> 2, j = g & 3;
+// One thread's share of a quad's activation staging.
+template <int D>
+struct ActRegs {
+  uint4 v[ActStage<D>::kUnits];
+  float sc;
+};
+
+// Loads quad kq's activation planes (rows m0 .. m0 + kBM - 1, clamped to
+// M - 1) and scales into registers; one 16-byte unit per thread and pass.
+template <int D>
+__device__ __forceinline__ ActRegs<D> act_load(const GemvArgs &p, int kq, int m0) {
+  ActRegs<D> r;
+  const int M = p.M, t = threadIdx.x;
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int nb = nb0 + nt;
-    if (nb < NB) {
-      const size_t lane_slot = ((size_t)nb * KQ + kq) * 64 + 16 * j + n_local;
-      o.w[nt] = codes[lane_slot * 4 + c];
-      o.s[nt] = scales[lane_slot];
-    } else {
-      o.w[nt] = 0x77777777u;  // code 7 decodes to 0
-      o.s[nt] = 0;
-    }
+  for (int i = 0; i < ActStage<D>::kUnits; ++i) {
+    const int u = t + 256 * i;  // unit: ((j * D + d) * kBM + row) * 2 + half
+    const int half = u & 1, row = (u >> 1) % kBM, jd = (u >> 1) / kBM;
+    const int m = min(m0 + row, M - 1);
+    const size_t src = ((size_t)(4 * kq) * D + jd) * M + m;  // group 4kq + j, digit d
+    r.v[i] = *(const uint4 *)(p.act_q + src * 32 + 16 * half);
   }
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = m0 + 16 * mt + n_local;
-#pragma unroll
-    for (int d = 0; d < D; ++d)
-      o.a[mt][d] = m < M ? *(const long *)(p.act_q + (((size_t)g * D + d) * M + m) * 32 + 8 * c)
-                         : 0l;
-    const int mr = m0 + 16 * mt + 4 * c;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) o.as[mt][r] = mr + r < M ? p.act_meta[(size_t)g * M + mr + r].scale : 0.0f;
-  }
+  const int j = t / kBM, row = t % kBM;
+  r.sc = p.act_meta[(size_t)(4 * kq + j) * M + min(m0 + row, M - 1)].scale;
+  return r;
 }
 
-template <int D, int MT, int NT>
-__global__ __launch_bounds__(256) void gemm_kernel(GemvArgs p, int m_tiles) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+template <int D>
+__device__ __forceinline__ void act_store(unsigned char *buf, const ActRegs<D> &r) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < ActStage<D>::kUnits; ++i) ((uint4 *)buf)[t + 256 * i] = r.v[i];
+  ((float *)(buf + ActStage<D>::kActBytes))[t] = r.sc;
+}
+
+// kRB: 16-row weight blocks per wave (the workgroup covers 4 kRB of them).
+template <int D, int kRB>
+__global__ __launch_bounds__(256, kRB == 4 ? 2 : 4) void gemm_kernel(GemvArgs p, int m_tiles) {
+  using S = ActStage<D>;
+  constexpr int kNBW = kWaves * kRB;  // weight row blocks per workgroup
+  __shared__ __align__(16) unsigned char lds[2 * S::kBufBytes];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform
   const int n_local = lane & 15, c = lane >> 4;
-  const int NB = p.N >> 4, KQ = p.K >> 7, G = p.K >> 5;
+  const int NB = p.N >> 4, KQ = p.K >> 7;
   // XCD-aware block order: XCD x runs logical blocks [first_x, first_x + cnt_x)
   const int nblk = gridDim.x, b = blockIdx.x;
   const int xcd = b & 7, idx = b >> 3;
   const int logical = xcd * (nblk >> 3) + min(xcd, nblk & 7) + idx;
   const int n_tile = logical / m_tiles, m_tile = logical % m_tiles;
-  const int m0 = m_tile * (32 * MT) + (wave & 1) * (16 * MT);
-  const int nb0 = n_tile * (2 * NT) + (wave >> 1) * NT;
-  if (m0 >= p.M || nb0 >= NB) return;
+  const int m0 = m_tile * kBM;
+  const int nb0 = n_tile * kNBW + wave * kRB;  // this wave's first row block
 
-  float acc[MT][NT][4];
+  // weight slots of this wave's row blocks: one per-lane base pointer plus
+  // uniform tile offsets (row blocks past NB are clamped into range, compute
+  // on a copy and are never stored)
+  const uint4 *cp = p.codes + lane;
+  const uint16_t *spp = (const uint16_t *)p.scales + lane;
+  size_t toff[kRB];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int rb = 0; rb < kRB; ++rb) toff[rb] = (size_t)min(nb0 + rb, NB - 1) * KQ * 64;
+  uint4 wb[kU][kRB];
+  uint32_t sb[kU][kRB];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
+  for (int u = 0; u < kU; ++u)
+    if (u < KQ) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) acc[mt][nt][r] = 0.0f;
+      for (int rb = 0; rb < kRB; ++rb) {
+        wb[u][rb] = load_stream(cp + toff[rb] + (size_t)u * 64);
+        sb[u][rb] = spp[toff[rb] + (size_t)u * 64];
+      }
+    }
+  act_store<D>(lds, act_load<D>(p, 0, m0));
+  __syncthreads();
 
-  GroupOps<D, MT, NT> cur, nxt;
-  load_group<D, MT, NT>(p, 0, m0, nb0, KQ, NB, n_local, c, cur);
+  float acc[kRB][4][4];
+#pragma unroll
+  for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[rb][mt][r] = 0.0f;
   const v4i magic = {kMagic, kMagic, kMagic, kMagic};
   const v4i zero = {0, 0, 0, 0};
-  for (int g = 0; g < G; ++g) {
-    if (g + 1 < G) load_group<D, MT, NT>(p, g + 1, m0, nb0, KQ, NB, n_local, c, nxt);
-    long bs[NT];
-    float ws[NT], wc[NT];
+
+  for (int q0 = 0; q0 < KQ; q0 += kU) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      bs[nt] = signed_codes(cur.w[nt]);
-      ws[nt] = h2f(cur.s[nt]);
-      wc[nt] = -kMagicF * ws[nt];
-    }
+    for (int u = 0; u < kU; ++u) {
+      const int kq = q0 + u;
+      if (kq >= KQ) break;
+      // this quad's weights; the slot is refilled with quad kq + kU
+      uint4 wc[kRB];
+      uint32_t sc[kRB];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int rb = 0; rb < kRB; ++rb) {
+        wc[rb] = wb[u][rb];
+        sc[rb] = sb[u][rb];
+      }
+      // (branch-free: past the end the last quad is loaded again and never
+      // used, so the quad's work stays one block for the scheduler)
+      const int kn = min(kq + kU, KQ - 1);
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt) {
-        if constexpr (D == 1) {
-          const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(cur.a[mt][0], bs[nt], magic, 0, 0, 0);
+      for (int rb = 0; rb < kRB; ++rb) {
+        wb[u][rb] = load_stream(cp + toff[rb] + (size_t)kn * 64);
+        sb[u][rb] = spp[toff[rb] + (size_t)kn * 64];
+      }
+      // the next quad's activations, in flight while this one computes
+      // (the last quad stages a copy of itself into the idle buffer)
+      const ActRegs<D> nxt = act_load<D>(p, min(kq + 1, KQ - 1), m0);
+
+      // q0 is even, so this quad's buffer is u: constant LDS offsets
+      const unsigned char *buf = lds + u * S::kBufBytes;
+      uint4 wt[kRB];
+      float ws[kRB][4];  // [row block][group]: scale of this lane's column
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float t = fmaf(__int_as_float(d[r]), ws[nt], wc[nt]);
-            acc[mt][nt][r] = fmaf(t, cur.as[mt][r], acc[mt][nt][r]);
-          }
-        } else {
-          v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(cur.a[mt][0], bs[nt], zero, 0, 0, 0);
+      for (int rb = 0; rb < kRB; ++rb) wt[rb] = quad_transpose(wc[rb]);
 #pragma unroll
-          for (int dd = 1; dd < D; ++dd) {
+      for (int h = 0; h < kRB / 2; ++h) {
+        // two row blocks' u16 scales per register, all four groups' rows
+        uint32_t g4[4];
+        column_gather((sc[2 * h] & 0xFFFFu) | (sc[2 * h + 1] << 16), g4);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) d[r] = d[r] << 7;
-            d = __builtin_amdgcn_mfma_i32_16x16x32_i8(cur.a[mt][dd], bs[nt], d, 0, 0, 0);
-          }
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float t = (float)d[r] * ws[nt];
-            acc[mt][nt][r] = fmaf(t, cur.as[mt][r], acc[mt][nt][r]);
-          }
+        for (int j = 0; j < 4; ++j) {
+          ws[2 * h][j] = h2f(g4[j] & 0xFFFFu);
+          ws[2 * h + 1][j] = h2f(g4[j] >> 16);
         }
       }
-    cur = nxt;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        long bw[kRB];
+#pragma unroll
+        for (int rb = 0; rb < kRB; ++rb) {
+          const uint32_t w = j == 0 ? wt[rb].x : j == 1 ? wt[rb].y : j == 2 ? wt[rb].z : wt[rb].w;
+          bw[rb] = signed_codes(w);
+        }
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          long av[D];
+#pragma unroll
+          for (int d = 0; d < D; ++d)
+            av[d] = *(const long *)(buf + (((j * D + d) * kBM + mt * 16 + n_local) * 32 + 8 * c));
+          const float4 as4 = *(const float4 *)(buf + S::kActBytes + (j * kBM + mt * 16 + 4 * c) * 4);
+          const float as[4] = {as4.x, as4.y, as4.z, as4.w};
+#pragma unroll
+          for (int rb = 0; rb < kRB; ++rb) {
+            if constexpr (D == 1) {
+              const v4i dd = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[0], bw[rb], magic, 0, 0, 0);
+              const float wcorr = -kMagicF * ws[rb][j];
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const float t = fmaf(__int_as_float(dd[r]), ws[rb][j], wcorr);
+                acc[rb][mt][r] = fmaf(t, as[r], acc[rb][mt][r]);
+              }
+            } else {
+              v4i dd[D];
+#pragma unroll
+              for (int d = 0; d < D; ++d)
+                dd[d] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[d], bw[rb], zero, 0, 0, 0);
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                int T = dd[0][r];
+#pragma unroll
+                for (int d = 1; d < D; ++d) T = (T << 7) + dd[d][r];
+                acc[rb][mt][r] = fmaf((float)T * ws[rb][j], as[r], acc[rb][mt][r]);
+              }
+            }
+          }
+          // one activation tile's MFMAs at a time: their results are
+          // consumed before the next tile's are issued (register budget)
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      // publish the next quad's activations (the other buffer was last read
+      // before the previous barrier)
+      act_store<D>(lds + (u ^ 1) * S::kBufBytes, nxt);
+      __syncthreads();
+    }
   }
 
+  // Lane (c, n) holds rows m0 + 16 mt + 4c + r of column 16 nb + n; the
+  // SwiGLU / RoPE partner row n ^ 8 lives in lane ^ 8. The epilogue runs as
+  // a loop over each row block's 16 values parked in this thread's own LDS
+  // column (the staging buffers are free after the last barrier): unrolled
+  // over the large inlined epilogue it would index the accumulators
+  // dynamically and push them to scratch.
   const bool paired = p.epi == EPI_SWIGLU || p.epi == EPI_QKV;
+  float *park = (float *)lds + threadIdx.x;
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int rb = 0; rb < kRB; ++rb) {
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
+    for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float tot = acc[mt][nt][r];
-        const float partner = paired ? __shfl_xor(tot, 8) : 0.0f;
-        const int m = m0 + 16 * mt + 4 * c + r;
-        const int nb = nb0 + nt;
-        if (m < p.M && nb < NB)
-          store_output(p, p.epi, nb, n_local, m, tot, partner, epi_load(p, p.epi, nb, n_local, m));
-      }
+      for (int r = 0; r < 4; ++r) park[(mt * 4 + r) * 256] = acc[rb][mt][r];
+    const int nb = nb0 + rb;
+#pragma unroll 1
+    for (int i = 0; i < 16; ++i) {
+      const float tot = park[i * 256];
+      const float partner = paired ? __shfl_xor(tot, 8) : 0.0f;
+      const int m = m0 + 16 * (i >> 2) + 4 * c + (i & 3);
+      if (m < p.M && nb < NB)
+        store_output(p, p.epi, nb, n_local, m, tot, partner, epi_load(p, p.epi, nb, n_local, m));
+    }
+  }
 }
 
 }  // namespace
 
-GemmShape plan_gemm(int N, int M) {
+GemmShape plan_gemm(int N, int M, int D) {
   GemmShape s;
+  s.mt = kBM / 16;
+  s.m_tiles = (M + kBM - 1) / kBM;
+  // 2 row blocks per wave (4 workgroups per CU) for one-digit planes; the
+  // three-digit kernel with 4 (2 per CU) once that still fills the GPU
+  // (measured on the 7B shapes at 512 and 2048 rows)
   const int NB = N / 16;
-  // 128 x 64 block tiles while that still gives two workgroups per CU, else
-  // 64 x 64
-  const long big = (long)((M + 127) / 128) * ((NB + 3) / 4);
-  if (big >= 512) {
-    s.mt = 4;
-    s.nt = 2;
-  } else {
-    s.mt = 2;
-    s.nt = 2;
-  }
-  s.m_tiles = (M + 32 * s.mt - 1) / (32 * s.mt);
-  s.n_tiles = (NB + 2 * s.nt - 1) / (2 * s.nt);
+  const long big = (long)s.m_tiles * ((NB + 15) / 16);
+  s.nt = D == 3 && big >= 384 ? 16 : 8;
+  s.n_tiles = (NB + s.nt - 1) / s.nt;
   s.grid = s.m_tiles * s.n_tiles;
   return s;
 }
@@ -198,14 +274,18 @@ GemmShape plan_gemm(int N, int M) {
 hipError_t launch_gemm(const GemvArgs &a, hipStream_t st) {
   if (a.N % 16 || a.K % 128 || a.M < 1 || !a.act_q || !a.act_meta || (a.D != 1 && a.D != 3))
     return hipErrorInvalidValue;
-  const GemmShape s = plan_gemm(a.N, a.M);
+  GemmShape s = plan_gemm(a.N, a.M, a.D);
+  if (a.rb_override == 2 || a.rb_override == 4) {  // tuning: row blocks per wave
+    s.nt = 4 * a.rb_override;
+    s.n_tiles = (a.N / 16 + s.nt - 1) / s.nt;
+    s.grid = s.m_tiles * s.n_tiles;
+  }
   const dim3 grid(s.grid), block(256);
-#define GK_GEMM(DD, MM, NN) \
-  hipLaunchKernelGGL((gemm_kernel<DD, MM, NN>), grid, block, 0, st, a, s.m_tiles)
+#define GK_GEMM(DD, RB) hipLaunchKernelGGL((gemm_kernel<DD, RB>), grid, block, 0, st, a, s.m_tiles)
   if (a.D == 1) {
-    if (s.mt == 4) GK_GEMM(1, 4, 2); else GK_GEMM(1, 2, 2);
+    if (s.nt == 16) GK_GEMM(1, 4); else GK_GEMM(1, 2);
   } else {
-    if (s.mt == 4) GK_GEMM(3, 4, 2); else GK_GEMM(3, 2, 2);
+    if (s.nt == 16) GK_GEMM(3, 4); else GK_GEMM(3, 2);
   }
 #undef GK_GEMM
   return hipGetLastError();

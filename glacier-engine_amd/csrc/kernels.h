@@ -84,6 +84,7 @@ struct GemvArgs {
   int prefetch;             // quads in flight per wave (4 or 8); 0 = heuristic
   int ksplit_override;      // force the K split (tuning); 0 = heuristic
   int rb_override;          // row blocks per workgroup with ksplit_override
+                            // (GEMM: 2 or 4 forces the row blocks per wave)
   int ksplit;               // set by launch_gemv
   int ksplit_lds_off;       // set by launch_gemv: LDS offset of the SwiGLU plane buffer
   int force_mfma;           // use the MFMA path even for M <= 2 (tuning / tests)
@@ -141,11 +142,11 @@ hipError_t launch_gemv(const GemvArgs &a, hipStream_t st);
 
 // Prefill GEMM (K2) for M > 32 activation rows: same arguments and epilogues
 // as launch_gemv (prefetch / ksplit / force_mfma fields are ignored). Block
-// tile (32*mt) x (32*nt) rows x weight rows, 4 waves.
+// tile 16*mt activation rows x nt weight row blocks (16 rows each), 4 waves.
 struct GemmShape {
   int mt, nt, m_tiles, n_tiles, grid;
 };
-GemmShape plan_gemm(int N, int M);
+GemmShape plan_gemm(int N, int M, int D);
 hipError_t launch_gemm(const GemvArgs &a, hipStream_t st);
 
 
@@ -177,6 +178,14 @@ hipError_t launch_attention_f16(const float *q, const void *kv_pool, const int32
                                 int head_dim, int max_ctx, float *scratch, float *out,
                                 hipStream_t st, int wp, int nw,
                                 PlanesDst emit = PlanesDst{nullptr, nullptr, 1});
+
+// Causal prefill attention (fp16 KV) for one lane's chunk of T consecutive
+// positions pos0 .. pos0 + T - 1 whose K/V rows are already in the lane's
+// pages; q / out [T][Hq*hd] as launch_attention.
+hipError_t launch_attention_prefill(const float *q, const void *kv_pool, const int32_t *page_table,
+                                    int max_pages, int lane, int pos0, int T, int layer,
+                                    int num_layers, int num_heads, int num_kv_heads, int head_dim,
+                                    float *out, hipStream_t st);
 
 // Argmax over rows x n. Eligible variant when words != null. Results to
 // `result` [rows] = {index (u64), eligible_rows (u64), status (i32), pad}.

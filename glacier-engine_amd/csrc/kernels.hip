@@ -14,6 +14,7 @@
 // fused multiply-add is intended.
 #include "kernels.h"
 #include "epilogue.h"
+#include "int4_ops.h"
 
 #include <hip/hip_fp16.h>
 #include <math.h>
@@ -23,56 +24,6 @@
 
 namespace gk {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-
-// Streaming 16-byte load of weight codes (read once per token).
-static __device__ __forceinline__ uint4 load_stream(const uint4 *p) {
-  const v4u v = __builtin_nontemporal_load((const v4u *)p);
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
-
-static __device__ __forceinline__ float h2f(uint32_t bits16) {
-  return __half2float(__ushort_as_half((unsigned short)bits16));
-}
-
-// Eight 4-bit codes of one u32 (low nibbles k0..k3, high nibbles k4..k7 in
-// the device tile layout) -> eight signed int8 lanes (u - 7), k0..k7. Per
-// byte u + 0x79 stays below 0x100 and flipping bit 7 of (u + 121) gives
-// u - 7 in two's complement, so an integer dot with these lanes is the
-// group dot of the dequantised codes itself (no correction term).
-static __device__ __forceinline__ long signed_codes(uint32_t w) {
-  const uint32_t lo = ((w & 0x0F0F0F0Fu) + 0x79797979u) ^ 0x80808080u;
-  const uint32_t hi = (((w >> 4) & 0x0F0F0F0Fu) + 0x79797979u) ^ 0x80808080u;
-  return (long)(((uint64_t)hi << 32) | (uint64_t)lo);
-}
-
-static constexpr int kMagic = 0x4B400000;  // bits of 12582912.0f = 1.5 * 2^23
-
-typedef unsigned v2u __attribute__((ext_vector_type(2)));
-
-// Even lanes: (own u16) | (u16 of the next lane) << 16; DPP quad_perm
-// [1, 0, 3, 2] reads the neighbour's value without a trip through LDS.
-static __device__ __forceinline__ uint32_t scale_pair(uint32_t s) {
-  const uint32_t nb = (uint32_t)__builtin_amdgcn_mov_dpp((int)s, 0xB1, 0xF, 0xF, false);
-  return (s & 0xFFFFu) | (nb << 16);
-}
-
-// 4 x 4 transpose of u32 words across the four 16-lane rows of a wave: on
-// entry lane (c, n) = 16c + n holds words 0..3 of its tile slot (group c of
-// weight row n, one coalesced 16-byte load per lane); on return it holds
-// word c of groups 0..3 of row n, which is the B operand layout of
-// v_mfma_i32_16x16x32_i8 for each of the four groups (lane (c, n) = codes
-// 8c .. 8c + 7 of row n). The 32-lane swap exchanges the upper rows of one
-// register with the lower rows of the other, the 16-lane swap the odd rows
-// of one with the even rows of the other.
-static __device__ __forceinline__ uint4 quad_transpose(uint4 v) {
-  const v2u a = __builtin_amdgcn_permlane32_swap(v.x, v.z, false, false);
-  const v2u b = __builtin_amdgcn_permlane32_swap(v.y, v.w, false, false);
-  const v2u c = __builtin_amdgcn_permlane16_swap(a.x, b.x, false, false);
-  const v2u d = __builtin_amdgcn_permlane16_swap(a.y, b.y, false, false);
-  return make_uint4(c.x, c.y, d.x, d.y);
-}
 
 // ---------------------------------------------------------------------------
 // K4: activation planes (+ optional RMSNorm)
@@ -1672,6 +1623,198 @@ hipError_t launch_attention_f16(const float *q, const void *kv_pool, const int32
   else
     hipLaunchKernelGGL((attn_combine2_kernel<128>), dim3(num_heads, M), dim3(kCombineThreads), 0, st, ctx_len,
                        num_heads, chunk, nch, max_ctx, scratch, out, emit);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// K3b: causal prefill attention over one lane's chunk of T consecutive
+// positions pos0 .. pos0 + T - 1 (generate.zig:1511-1967 per row: softmax of
+// q . k / sqrt(hd) over the row's positions 0 .. pos, then the weighted sum
+// of v), fp16 KV pages.
+//
+// Workgroup = the G query heads of one KV head (one wave each) x 16 query
+// rows; it walks the key pages 0 .. (last row's position) / 16, staging each
+// page's K rows and V (transposed) in LDS, double buffered, one barrier per
+// page, so the G waves share every K/V read. Per page and wave:
+//   * S^T = K . Q^T as one 16 x 16 tile (keys x rows) with f16 MFMAs; Q is
+//     split into f16 hi + lo parts (K is exact in f16), so the scores carry
+//     f32 accuracy like the decode kernel's;
+//   * online softmax per row (column of S^T: the 16 keys of row j sit in
+//     lanes (c, j), c = 0..3, four per lane), causal mask on the diagonal;
+//   * O += P . V with P split into f16 hi + lo (the tile's A operand is the
+//     lane's own P registers) and V^T from LDS; O (16 rows x hd, f32) stays
+//     in registers, rescaled by each row's exp(m_old - m_new).
+// The last blocks (longest key ranges) are scheduled first. PPT: 16-byte
+// K (and V) pieces each thread stages per page (16 * hd / 8 pieces over
+// 64 * G threads).
+template <int HD, int PPT>
+__global__ __launch_bounds__(64 * kMaxGroup) void attn_prefill_kernel(
+    const float *q, const __half *pool, const int32_t *ptab, int pos0, int T, int layer,
+    int num_layers, int Hq, int Hkv, float *out) {
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  constexpr int S = HD / 16;   // 16-wide steps over the head dim (scores)
+  constexpr int NT = HD / 16;  // 16-wide output tiles over the head dim
+  constexpr int KP = HD + 8;   // K row stride in halves (padded)
+  constexpr int VP = 16 + 4;   // V^T row stride in halves (padded)
+  constexpr int PIECES = 16 * HD / 8;  // 16-byte pieces of one page's K (or V)
+  __shared__ __align__(16) _Float16 ks[2][16 * KP];
+  __shared__ __align__(16) _Float16 vt[2][HD * VP];
+  const int t = threadIdx.x, l = t & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int c = l >> 4, j = l & 15;
+  const int G = Hq / Hkv;
+  const int nqb = (T + 15) / 16;
+  const int i0 = (nqb - 1 - (int)blockIdx.x) * 16;  // longest blocks first
+  const int h = blockIdx.y;
+  const int qh = h * G + wv;
+  const int kv_dim = Hkv * HD;
+  const size_t lay = (size_t)num_layers;
+  const int last_pos = pos0 + min(i0 + 15, T - 1);
+  const int npages = last_pos / 16 + 1;
+  const float scale = 1.0f / sqrtf((float)HD);
+
+  // staging: thread t moves K and V pieces t + 64 G i (i < PPT) of a page;
+  // key positions past the last row's are zeroed (their page slots may hold
+  // anything, and a masked score still multiplies its V row)
+  const int nthr = (int)blockDim.x;
+  uint4 kreg[PPT], vreg[PPT];
+  auto fetch = [&](int kp) {
+    const size_t pbase = ((size_t)ptab[kp] * lay + layer) * 2;
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int pc = t + nthr * i, skey = pc / (HD / 8), spc = pc % (HD / 8);
+      kreg[i] = vreg[i] = make_uint4(0, 0, 0, 0);
+      if (pc < PIECES && 16 * kp + skey <= last_pos) {
+        const size_t off = (pbase * 16 + skey) * kv_dim + (size_t)h * HD + 8 * spc;
+        kreg[i] = *(const uint4 *)(pool + off);
+        vreg[i] = *(const uint4 *)(pool + off + 16 * (size_t)kv_dim);
+      }
+    }
+  };
+  auto stage = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) {
+      const int pc = t + nthr * i, skey = pc / (HD / 8), spc = pc % (HD / 8);
+      if (pc >= PIECES) continue;
+      *(uint4 *)&ks[b][skey * KP + 8 * spc] = kreg[i];
+      const _Float16 *vh = (const _Float16 *)&vreg[i];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vt[b][(8 * spc + e) * VP + skey] = vh[e];
+    }
+  };
+  fetch(0);
+  stage(0);
+
+  // Q^T as the B operand: lane (c, j) = row i0 + j, dims 16 st + 4c .. + 3
+  h4 qhi[S], qlo[S];
+  {
+    const float *qrow = q + ((size_t)min(i0 + j, T - 1) * Hq + qh) * HD;
+#pragma unroll
+    for (int st = 0; st < S; ++st) {
+      const float4 qv = *(const float4 *)(qrow + 16 * st + 4 * c);
+      const float qa[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const _Float16 hv = (_Float16)qa[e];
+        qhi[st][e] = hv;
+        qlo[st][e] = (_Float16)(qa[e] - (float)hv);
+      }
+    }
+  }
+  const int qpos = pos0 + i0 + j;  // position of this lane's score column
+  f4 o[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) o[nt] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  float mx = -INFINITY, sum = 0.0f;
+  __syncthreads();
+
+  for (int kp = 0; kp < npages; ++kp) {
+    const int b = kp & 1;
+    if (kp + 1 < npages) fetch(kp + 1);  // next page in flight
+    // scores S^T[key 4c + r][row j]
+    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int st = 0; st < S; ++st) {
+      const h4 a = *(const h4 *)&ks[b][j * KP + 16 * st + 4 * c];
+      acc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qhi[st], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qlo[st], acc, 0, 0, 0);
+    }
+    float sv[4], pm = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int kpos = 16 * kp + 4 * c + r;
+      sv[r] = kpos <= qpos ? acc[r] * scale : -INFINITY;
+      pm = fmaxf(pm, sv[r]);
+    }
+    pm = fmaxf(pm, __shfl_xor(pm, 16));
+    pm = fmaxf(pm, __shfl_xor(pm, 32));
+    const float mnew = fmaxf(mx, pm);  // finite: key 0 is in every row's range
+    const float alpha = expf(mx - mnew);
+    h4 phi, plo;
+    float ps = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float pv = expf(sv[r] - mnew);
+      ps += pv;
+      const _Float16 hv = (_Float16)pv;
+      phi[r] = hv;
+      plo[r] = (_Float16)(pv - (float)hv);
+    }
+    ps += __shfl_xor(ps, 16);
+    ps += __shfl_xor(ps, 32);
+    sum = sum * alpha + ps;
+    mx = mnew;
+    // O rows are rows 4c + r: their factors live in lanes 4c + r
+    float ar[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ar[r] = __shfl(alpha, 4 * c + r);
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[nt][r] *= ar[r];
+      const h4 bv = *(const h4 *)&vt[b][(16 * nt + j) * VP + 4 * c];
+      o[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi, bv, o[nt], 0, 0, 0);
+      o[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo, bv, o[nt], 0, 0, 0);
+    }
+    // publish the next page (the other buffer was last read before the
+    // previous barrier)
+    if (kp + 1 < npages) stage(b ^ 1);
+    __syncthreads();
+  }
+  // lane (c, j): O[row 4c + r][dim 16 nt + j]
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = i0 + 4 * c + r;
+    const float lr = __shfl(sum, 4 * c + r);
+    if (row < T) {
+      float *orow = out + ((size_t)row * Hq + qh) * HD;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) orow[16 * nt + j] = o[nt][r] / lr;
+    }
+  }
+}
+
+hipError_t launch_attention_prefill(const float *q, const void *kv_pool, const int32_t *page_table,
+                                    int max_pages, int lane, int pos0, int T, int layer,
+                                    int num_layers, int num_heads, int num_kv_heads, int head_dim,
+                                    float *out, hipStream_t st) {
+  if (T < 1 || lane < 0 || pos0 < 0 || num_heads % num_kv_heads != 0 ||
+      num_heads / num_kv_heads > kMaxGroup || (pos0 + T + 15) / 16 > max_pages)
+    return hipErrorInvalidValue;
+  const int G = num_heads / num_kv_heads;
+  if (head_dim != 64 && head_dim != 128) return hipErrorInvalidValue;
+  const dim3 grid((T + 15) / 16, num_kv_heads), block(64 * G);
+  const int32_t *ptab = page_table + (size_t)lane * max_pages;
+  const __half *pool = (const __half *)kv_pool;
+  const int ppt = (16 * head_dim / 8 + 64 * G - 1) / (64 * G);
+#define GK_PF(HD, P)                                                                              hipLaunchKernelGGL((attn_prefill_kernel<HD, P>), grid, block, 0, st, q, pool, ptab, pos0, T,                      layer, num_layers, num_heads, num_kv_heads, out)
+  if (head_dim == 64) {
+    if (ppt <= 1) GK_PF(64, 1); else GK_PF(64, 2);
+  } else {
+    if (ppt <= 1) GK_PF(128, 1); else if (ppt == 2) GK_PF(128, 2); else GK_PF(128, 4);
+  }
+#undef GK_PF
   return hipGetLastError();
 }
 

@@ -94,6 +94,9 @@ struct StepInputs {  // uploaded once per decode step, in one copy
 // Device arrays describing the activation rows of one launch sequence.
 struct RowPtrs {
   const int32_t *tokens, *lane_of_row, *pos_of_row, *ctx_len;
+  // a prefill chunk: every row is lane chunk_lane, rows at consecutive
+  // positions from chunk_pos0 (-1: rows of arbitrary lanes / positions)
+  int chunk_lane = -1, chunk_pos0 = 0;
 };
 
 struct glacier_hip_session {
@@ -520,11 +523,17 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
     // attention (chain: also the O projection's planes)
     const gk::PlanesDst opd = chain ? gk::PlanesDst{s->act_q2, s->act_meta2, Do}
                                     : gk::PlanesDst{nullptr, nullptr, 1};
-    e = gk::launch_attention(s->q, s->kv_pool, s->opt.kv_dtype == GLACIER_HIP_F16, s->page_table,
-                             (int)s->max_pages, rp.lane_of_row, rp.ctx_len, rows, (int)l,
-                             (int)c.num_layers, (int)c.num_heads, (int)c.num_kv_heads,
-                             (int)c.head_dim, (int)s->opt.max_positions, s->att_scratch, s->attn,
-                             st, opd);
+    if (rows > 32 && rp.chunk_lane >= 0 && s->opt.kv_dtype == GLACIER_HIP_F16)
+      e = gk::launch_attention_prefill(s->q, s->kv_pool, s->page_table, (int)s->max_pages,
+                                       rp.chunk_lane, rp.chunk_pos0, rows, (int)l,
+                                       (int)c.num_layers, (int)c.num_heads, (int)c.num_kv_heads,
+                                       (int)c.head_dim, s->attn, st);
+    else
+      e = gk::launch_attention(s->q, s->kv_pool, s->opt.kv_dtype == GLACIER_HIP_F16,
+                               s->page_table, (int)s->max_pages, rp.lane_of_row, rp.ctx_len, rows,
+                               (int)l, (int)c.num_layers, (int)c.num_heads, (int)c.num_kv_heads,
+                               (int)c.head_dim, (int)s->opt.max_positions, s->att_scratch,
+                               s->attn, st, opd);
     if (e != hipSuccess) return e;
     // O projection + residual (chain: partial sums of h for gate/up's norm)
     ProjIn oin;
@@ -936,7 +945,13 @@ int run_prefill_chunk(glacier_hip_session *s, uint32_t lane, const uint32_t *tok
   if (e != hipSuccess) return fail(e, "prefill inputs");
   e = upload_page_entries(s, txns, st);
   if (e != hipSuccess) return fail(e, "page table");
-  const RowPtrs rp{s->pf_dev, s->pf_dev + C, s->pf_dev + 2 * C, s->pf_dev + 3 * C};
+  RowPtrs rp{s->pf_dev, s->pf_dev + C, s->pf_dev + 2 * C, s->pf_dev + 3 * C};
+  bool consecutive = true;
+  for (uint32_t i = 1; i < n; ++i) consecutive = consecutive && por[i] == por[0] + (int32_t)i;
+  if (consecutive) {
+    rp.chunk_lane = (int)lane;
+    rp.chunk_pos0 = por[0];
+  }
   e = enqueue_layers(s, (int)n, rp, st);
   if (e != hipSuccess) return fail(e, "prefill layers");
   if (head) {
