@@ -39,55 +39,63 @@ namespace gk {
 
 namespace {
 
-constexpr int kBM = 64;              // activation rows per workgroup
 constexpr int kWaves = 4;            // waves per workgroup, side by side in N
 constexpr int kU = 2;                // weight quads in flight per wave
 
-template <int D>
+// Per-quad activation staging of a BM-row tile: digit planes
+// [4 groups][D][BM rows][32] then the scales [4][BM].
+template <int D, int BM>
 struct ActStage {
-  static constexpr int kActBytes = 4 * D * kBM * 32;    // [4 groups][D][kBM rows][32]
-  static constexpr int kBufBytes = kActBytes + 4 * kBM * 4;  // + scales [4][kBM]
-  static constexpr int kUnits = kActBytes / 16 / 256;    // 16-byte loads per thread
+  static constexpr int kActBytes = 4 * D * BM * 32;
+  static constexpr int kBufBytes = kActBytes + 4 * BM * 4;
+  static constexpr int kUnits = kActBytes / 16 / 256;  // 16-byte loads per thread
 };
 
 // One thread's share of a quad's activation staging.
-template <int D>
+template <int D, int BM>
 struct ActRegs {
-  uint4 v[ActStage<D>::kUnits];
+  uint4 v[ActStage<D, BM>::kUnits];
   float sc;
 };
 
-// Loads quad kq's activation planes (rows m0 .. m0 + kBM - 1, clamped to
+// Loads quad kq's activation planes (rows m0 .. m0 + BM - 1, clamped to
 // M - 1) and scales into registers; one 16-byte unit per thread and pass.
-template <int D>
-__device__ __forceinline__ ActRegs<D> act_load(const GemvArgs &p, int kq, int m0) {
-  ActRegs<D> r;
+template <int D, int BM>
+__device__ __forceinline__ ActRegs<D, BM> act_load(const GemvArgs &p, int kq, int m0) {
+  ActRegs<D, BM> r;
   const int M = p.M, t = threadIdx.x;
 #pragma unroll
-  for (int i = 0; i < ActStage<D>::kUnits; ++i) {
-    const int u = t + 256 * i;  // unit: ((j * D + d) * kBM + row) * 2 + half
-    const int half = u & 1, row = (u >> 1) % kBM, jd = (u >> 1) / kBM;
+  for (int i = 0; i < ActStage<D, BM>::kUnits; ++i) {
+    const int u = t + 256 * i;  // unit: ((j * D + d) * BM + row) * 2 + half
+    const int half = u & 1, row = (u >> 1) % BM, jd = (u >> 1) / BM;
     const int m = min(m0 + row, M - 1);
     const size_t src = ((size_t)(4 * kq) * D + jd) * M + m;  // group 4kq + j, digit d
     r.v[i] = *(const uint4 *)(p.act_q + src * 32 + 16 * half);
   }
-  const int j = t / kBM, row = t % kBM;
+  const int ts = t % (4 * BM);  // threads past 4 BM repeat another's scale
+  const int j = ts / BM, row = ts % BM;
   r.sc = p.act_meta[(size_t)(4 * kq + j) * M + min(m0 + row, M - 1)].scale;
   return r;
 }
 
-template <int D>
-__device__ __forceinline__ void act_store(unsigned char *buf, const ActRegs<D> &r) {
+template <int D, int BM>
+__device__ __forceinline__ void act_store(unsigned char *buf, const ActRegs<D, BM> &r) {
   const int t = threadIdx.x;
 #pragma unroll
-  for (int i = 0; i < ActStage<D>::kUnits; ++i) ((uint4 *)buf)[t + 256 * i] = r.v[i];
-  ((float *)(buf + ActStage<D>::kActBytes))[t] = r.sc;
+  for (int i = 0; i < ActStage<D, BM>::kUnits; ++i) ((uint4 *)buf)[t + 256 * i] = r.v[i];
+  // (duplicates store the same value to the same slot: no branch)
+  ((float *)(buf + ActStage<D, BM>::kActBytes))[t % (4 * BM)] = r.sc;
 }
 
-// kRB: 16-row weight blocks per wave (the workgroup covers 4 kRB of them).
-template <int D, int kRB>
-__global__ __launch_bounds__(256, kRB == 4 ? 2 : 4) void gemm_kernel(GemvArgs p, int m_tiles) {
-  using S = ActStage<D>;
+// kRB: 16-row weight blocks per wave (the workgroup covers 4 kRB of them);
+// BM: activation rows per workgroup (32 or 64). With ks_count > 1 the K
+// quads are split over blockIdx.y and each split writes its partial sums to
+// part [ks_count][M][N] (no epilogue; splitk_reduce_kernel finishes).
+template <int D, int kRB, int BM>
+__global__ __launch_bounds__(256, kRB == 4 ? 2 : 4) void gemm_kernel(GemvArgs p, int m_tiles,
+                                                                     int ks_count, float *part) {
+  using S = ActStage<D, BM>;
+  constexpr int MT = BM / 16;         // 16-row activation tiles per wave
   constexpr int kNBW = kWaves * kRB;  // weight row blocks per workgroup
   __shared__ __align__(16) unsigned char lds[2 * S::kBufBytes];
   const int lane = threadIdx.x & 63;
@@ -99,8 +107,11 @@ __global__ __launch_bounds__(256, kRB == 4 ? 2 : 4) void gemm_kernel(GemvArgs p,
   const int xcd = b & 7, idx = b >> 3;
   const int logical = xcd * (nblk >> 3) + min(xcd, nblk & 7) + idx;
   const int n_tile = logical / m_tiles, m_tile = logical % m_tiles;
-  const int m0 = m_tile * kBM;
+  const int m0 = m_tile * BM;
   const int nb0 = n_tile * kNBW + wave * kRB;  // this wave's first row block
+  // this split's quads kq0 .. kq0 + nq - 1
+  const int kq0 = (int)(((long)blockIdx.y * KQ) / ks_count);
+  const int nq = (int)(((long)(blockIdx.y + 1) * KQ) / ks_count) - kq0;
 
   // weight slots of this wave's row blocks: one per-lane base pointer plus
   // uniform tile offsets (row blocks past NB are clamped into range, compute
@@ -109,37 +120,37 @@ __global__ __launch_bounds__(256, kRB == 4 ? 2 : 4) void gemm_kernel(GemvArgs p,
   const uint16_t *spp = (const uint16_t *)p.scales + lane;
   size_t toff[kRB];
 #pragma unroll
-  for (int rb = 0; rb < kRB; ++rb) toff[rb] = (size_t)min(nb0 + rb, NB - 1) * KQ * 64;
+  for (int rb = 0; rb < kRB; ++rb) toff[rb] = ((size_t)min(nb0 + rb, NB - 1) * KQ + kq0) * 64;
   uint4 wb[kU][kRB];
   uint32_t sb[kU][kRB];
 #pragma unroll
-  for (int u = 0; u < kU; ++u)
-    if (u < KQ) {
+  for (int u = 0; u < kU; ++u) {
+    const int q = min(u, nq - 1);
 #pragma unroll
-      for (int rb = 0; rb < kRB; ++rb) {
-        wb[u][rb] = load_stream(cp + toff[rb] + (size_t)u * 64);
-        sb[u][rb] = spp[toff[rb] + (size_t)u * 64];
-      }
+    for (int rb = 0; rb < kRB; ++rb) {
+      wb[u][rb] = load_stream(cp + toff[rb] + (size_t)q * 64);
+      sb[u][rb] = spp[toff[rb] + (size_t)q * 64];
     }
-  act_store<D>(lds, act_load<D>(p, 0, m0));
+  }
+  act_store<D, BM>(lds, act_load<D, BM>(p, kq0, m0));
   __syncthreads();
 
-  float acc[kRB][4][4];
+  float acc[kRB][MT][4];
 #pragma unroll
   for (int rb = 0; rb < kRB; ++rb)
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[rb][mt][r] = 0.0f;
   const v4i magic = {kMagic, kMagic, kMagic, kMagic};
   const v4i zero = {0, 0, 0, 0};
 
-  for (int q0 = 0; q0 < KQ; q0 += kU) {
+  for (int q0 = 0; q0 < nq; q0 += kU) {
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-      const int kq = q0 + u;
-      if (kq >= KQ) break;
-      // this quad's weights; the slot is refilled with quad kq + kU
+      const int q = q0 + u;  // local quad index (absolute kq0 + q)
+      if (q >= nq) break;
+      // this quad's weights; the slot is refilled with quad q + kU
       uint4 wc[kRB];
       uint32_t sc[kRB];
 #pragma unroll
@@ -149,15 +160,15 @@ __global__ __launch_bounds__(256, kRB == 4 ? 2 : 4) void gemm_kernel(GemvArgs p,
       }
       // (branch-free: past the end the last quad is loaded again and never
       // used, so the quad's work stays one block for the scheduler)
-      const int kn = min(kq + kU, KQ - 1);
+      const int qn = min(q + kU, nq - 1);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) {
-        wb[u][rb] = load_stream(cp + toff[rb] + (size_t)kn * 64);
-        sb[u][rb] = spp[toff[rb] + (size_t)kn * 64];
+        wb[u][rb] = load_stream(cp + toff[rb] + (size_t)qn * 64);
+        sb[u][rb] = spp[toff[rb] + (size_t)qn * 64];
       }
       // the next quad's activations, in flight while this one computes
       // (the last quad stages a copy of itself into the idle buffer)
-      const ActRegs<D> nxt = act_load<D>(p, min(kq + 1, KQ - 1), m0);
+      const ActRegs<D, BM> nxt = act_load<D, BM>(p, kq0 + min(q + 1, nq - 1), m0);
 
       // q0 is even, so this quad's buffer is u: constant LDS offsets
       const unsigned char *buf = lds + u * S::kBufBytes;
@@ -185,12 +196,12 @@ __global__ __launch_bounds__(256, kRB == 4 ? 2 : 4) void gemm_kernel(GemvArgs p,
           bw[rb] = signed_codes(w);
         }
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
+        for (int mt = 0; mt < MT; ++mt) {
           long av[D];
 #pragma unroll
           for (int d = 0; d < D; ++d)
-            av[d] = *(const long *)(buf + (((j * D + d) * kBM + mt * 16 + n_local) * 32 + 8 * c));
-          const float4 as4 = *(const float4 *)(buf + S::kActBytes + (j * kBM + mt * 16 + 4 * c) * 4);
+            av[d] = *(const long *)(buf + (((j * D + d) * BM + mt * 16 + n_local) * 32 + 8 * c));
+          const float4 as4 = *(const float4 *)(buf + S::kActBytes + (j * BM + mt * 16 + 4 * c) * 4);
           const float as[4] = {as4.x, as4.y, as4.z, as4.w};
 #pragma unroll
           for (int rb = 0; rb < kRB; ++rb) {
@@ -223,28 +234,43 @@ __global__ __launch_bounds__(256, kRB == 4 ? 2 : 4) void gemm_kernel(GemvArgs p,
       }
       // publish the next quad's activations (the other buffer was last read
       // before the previous barrier)
-      act_store<D>(lds + (u ^ 1) * S::kBufBytes, nxt);
+      act_store<D, BM>(lds + (u ^ 1) * S::kBufBytes, nxt);
       __syncthreads();
     }
   }
 
-  // Lane (c, n) holds rows m0 + 16 mt + 4c + r of column 16 nb + n; the
-  // SwiGLU / RoPE partner row n ^ 8 lives in lane ^ 8. The epilogue runs as
-  // a loop over each row block's 16 values parked in this thread's own LDS
+  // Lane (c, n) holds rows m0 + 16 mt + 4c + r of column 16 nb + n.
+  if (ks_count > 1) {
+    // split K: this split's partial sums, part[split][m][n]
+    float *dst = part + (size_t)blockIdx.y * p.M * p.N;
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + 16 * mt + 4 * c + r, nb = nb0 + rb;
+          if (m < p.M && nb < NB) dst[(size_t)m * p.N + nb * 16 + n_local] = acc[rb][mt][r];
+        }
+    return;
+  }
+  // The SwiGLU / RoPE partner row n ^ 8 lives in lane ^ 8. The epilogue runs
+  // as a loop over each row block's values parked in this thread's own LDS
   // column (the staging buffers are free after the last barrier): unrolled
   // over the large inlined epilogue it would index the accumulators
   // dynamically and push them to scratch.
+  static_assert(MT * 4 * 256 * 4 <= 2 * S::kBufBytes, "parking area");
   const bool paired = p.epi == EPI_SWIGLU || p.epi == EPI_QKV;
   float *park = (float *)lds + threadIdx.x;
 #pragma unroll
   for (int rb = 0; rb < kRB; ++rb) {
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) park[(mt * 4 + r) * 256] = acc[rb][mt][r];
     const int nb = nb0 + rb;
 #pragma unroll 1
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < MT * 4; ++i) {
       const float tot = park[i * 256];
       const float partner = paired ? __shfl_xor(tot, 8) : 0.0f;
       const int m = m0 + 16 * (i >> 2) + 4 * c + (i & 3);
@@ -254,40 +280,91 @@ __global__ __launch_bounds__(256, kRB == 4 ? 2 : 4) void gemm_kernel(GemvArgs p,
   }
 }
 
+// Split-K finish: y = the fixed-order sum over splits of part[s][m][n],
+// through the same epilogue as the one-split kernel. One thread per output
+// (m, n); the SwiGLU / RoPE partner n ^ 8 is summed by the same thread.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemvArgs p, int ks_count,
+                                                            const float *part) {
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t MN = (size_t)p.M * p.N;
+  if (idx >= MN) return;
+  const int m = (int)(idx / p.N), n = (int)(idx % p.N);
+  const int nb = n >> 4, n_local = n & 15;
+  const bool paired = p.epi == EPI_SWIGLU || p.epi == EPI_QKV;
+  const size_t pi = (size_t)m * p.N + (n ^ 8);
+  float tot = part[idx], partner = paired ? part[pi] : 0.0f;
+  for (int s = 1; s < ks_count; ++s) {
+    tot += part[s * MN + idx];
+    if (paired) partner += part[s * MN + pi];
+  }
+  store_output(p, p.epi, nb, n_local, m, tot, partner, epi_load(p, p.epi, nb, n_local, m));
+}
+
 }  // namespace
 
-GemmShape plan_gemm(int N, int M, int D) {
+GemmShape plan_gemm(int N, int M, int K, int D, size_t ws_floats) {
   GemmShape s;
-  s.mt = kBM / 16;
-  s.m_tiles = (M + kBM - 1) / kBM;
+  const int bm = M <= 32 ? 32 : 64;
+  s.mt = bm / 16;
+  s.m_tiles = (M + bm - 1) / bm;
   // 2 row blocks per wave (4 workgroups per CU) for one-digit planes; the
   // three-digit kernel with 4 (2 per CU) once that still fills the GPU
   // (measured on the 7B shapes at 512 and 2048 rows)
-  const int NB = N / 16;
+  const int NB = N / 16, KQ = K / 128;
   const long big = (long)s.m_tiles * ((NB + 15) / 16);
   s.nt = D == 3 && big >= 384 ? 16 : 8;
   s.n_tiles = (NB + s.nt - 1) / s.nt;
   s.grid = s.m_tiles * s.n_tiles;
+  // split K over workgroups (at least 2 quads each) until about 512
+  // workgroups, as far as the partial sums fit the workspace
+  s.ks = 1;
+  while (s.grid * s.ks < 512 && 2 * s.ks <= KQ / 2 && s.ks < 16 &&
+         (size_t)(2 * s.ks) * M * N <= ws_floats)
+    s.ks *= 2;
   return s;
+}
+
+size_t gemm_splitk_floats(int N, int M, int K, int D) {
+  const GemmShape s = plan_gemm(N, M, K, D, (size_t)-1);
+  return s.ks > 1 ? (size_t)s.ks * M * N : 0;
 }
 
 hipError_t launch_gemm(const GemvArgs &a, hipStream_t st) {
   if (a.N % 16 || a.K % 128 || a.M < 1 || !a.act_q || !a.act_meta || (a.D != 1 && a.D != 3))
     return hipErrorInvalidValue;
-  GemmShape s = plan_gemm(a.N, a.M, a.D);
+  if (a.out_q || a.ss_out || a.arg_parts || a.x_in) return hipErrorInvalidValue;  // GEMV-only
+  GemmShape s = plan_gemm(a.N, a.M, a.K, a.D, a.splitk_ws ? a.splitk_ws_floats : 0);
   if (a.rb_override == 2 || a.rb_override == 4) {  // tuning: row blocks per wave
     s.nt = 4 * a.rb_override;
     s.n_tiles = (a.N / 16 + s.nt - 1) / s.nt;
     s.grid = s.m_tiles * s.n_tiles;
   }
-  const dim3 grid(s.grid), block(256);
-#define GK_GEMM(DD, RB) hipLaunchKernelGGL((gemm_kernel<DD, RB>), grid, block, 0, st, a, s.m_tiles)
-  if (a.D == 1) {
-    if (s.nt == 16) GK_GEMM(1, 4); else GK_GEMM(1, 2);
-  } else {
-    if (s.nt == 16) GK_GEMM(3, 4); else GK_GEMM(3, 2);
+  if (a.ksplit_override > 0) {  // tuning: K splits (needs the workspace)
+    if ((size_t)a.ksplit_override * a.M * a.N > (a.splitk_ws ? a.splitk_ws_floats : 0) &&
+        a.ksplit_override > 1)
+      return hipErrorInvalidValue;
+    s.ks = std::min(a.ksplit_override, a.K / 128);
   }
+  const dim3 grid(s.grid, s.ks), block(256);
+  float *part = s.ks > 1 ? a.splitk_ws : nullptr;
+#define GK_GEMM(DD, RB, BM) \
+  hipLaunchKernelGGL((gemm_kernel<DD, RB, BM>), grid, block, 0, st, a, s.m_tiles, s.ks, part)
+#define GK_GEMM_BM(DD, RB) \
+  do {                       \
+    if (s.mt == 2) GK_GEMM(DD, RB, 32); else GK_GEMM(DD, RB, 64); \
+  } while (0)
+  if (a.D == 1) {
+    if (s.nt == 16) GK_GEMM_BM(1, 4); else GK_GEMM_BM(1, 2);
+  } else {
+    if (s.nt == 16) GK_GEMM_BM(3, 4); else GK_GEMM_BM(3, 2);
+  }
+#undef GK_GEMM_BM
 #undef GK_GEMM
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || s.ks == 1) return e;
+  const size_t MN = (size_t)a.M * a.N;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, st, a,
+                     s.ks, (const float *)part);
   return hipGetLastError();
 }
 

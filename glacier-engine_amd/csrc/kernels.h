@@ -116,6 +116,9 @@ struct GemvArgs {
   ArgPartial *arg_parts;
   const uint64_t *arg_words;
   long arg_word_count;
+  // GEMM split-K workspace (floats); null: no K split
+  float *splitk_ws;
+  size_t splitk_ws_floats;
 };
 
 // Launch shape of one GEMV: RB row blocks per workgroup, KS waves per row
@@ -140,13 +143,24 @@ hipError_t launch_prep_act(const void *x, int x_bf16, const float *norm_w, float
 
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t st);
 
-// Prefill GEMM (K2) for M > 32 activation rows: same arguments and epilogues
-// as launch_gemv (prefetch / ksplit / force_mfma fields are ignored). Block
-// tile 16*mt activation rows x nt weight row blocks (16 rows each), 4 waves.
+// Row counts up to this run the decode GEMV (K1, with its fused chain
+// stages); more rows run the MFMA GEMM (K2).
+constexpr int kGemvMaxRows = 16;
+
+// MFMA GEMM (K2) for more than 16 activation rows: same arguments and
+// epilogues as launch_gemv without the GEMV-only stages (plane emission,
+// partial sums of squares, fused argmax, input mode); prefetch / force_mfma
+// are ignored. Block tile 16*mt activation rows x nt weight row blocks (16
+// rows each), 4 waves; ks > 1 splits K over workgroups, which needs
+// splitk_ws (ks * M * N floats) and a second, fixed-order reduction kernel.
+// ksplit_override / rb_override force the splits / row blocks per wave
+// (tuning).
 struct GemmShape {
-  int mt, nt, m_tiles, n_tiles, grid;
+  int mt, nt, m_tiles, n_tiles, grid, ks;
 };
-GemmShape plan_gemm(int N, int M, int D);
+GemmShape plan_gemm(int N, int M, int K, int D, size_t ws_floats);
+// Workspace floats the GEMM would use for these sizes with no limit.
+size_t gemm_splitk_floats(int N, int M, int K, int D);
 hipError_t launch_gemm(const GemvArgs &a, hipStream_t st);
 
 

@@ -224,7 +224,7 @@ GemvShape plan_gemv(int N, int K, int M, int D) {
   p.waves = ks * rb;
   const size_t red = (size_t)p.waves * ((M + 15) / 16) * 4 * 64 * sizeof(float);
   const size_t planes = planes_bytes(K / 32, M, D) + (size_t)M * sizeof(float);
-  p.lds_a = planes <= kLdsLimit;
+  p.lds_a = planes <= kLdsLimit && (M <= 16 || planes <= 64 * 1024);
   p.lds_bytes = std::max(p.lds_a ? planes : 0, red);
   p.grid = (NB + rb - 1) / rb;
   return p;

@@ -29,6 +29,8 @@ struct glacier_hip_context {
   size_t scratch_bytes = 0;
   void *planes = nullptr;  // activation planes of glacier_hip_int4_gemv
   size_t planes_bytes = 0;
+  float *splitk = nullptr;  // GEMM split-K partial sums of glacier_hip_int4_gemv
+  size_t splitk_floats = 0;
   uint32_t *counters = nullptr;  // zeroed once, self-resetting
   size_t counter_count = 0;
   gk::ArgmaxResult *results_host = nullptr;  // pinned

@@ -162,6 +162,7 @@ int glacier_hip_deinit(glacier_hip_context *ctx) {
   (void)hipStreamSynchronize(ctx->stream);
   if (ctx->scratch) (void)hipFree(ctx->scratch);
   if (ctx->planes) (void)hipFree(ctx->planes);
+  if (ctx->splitk) (void)hipFree(ctx->splitk);
   if (ctx->counters) (void)hipFree(ctx->counters);
   if (ctx->results_host) (void)hipHostFree(ctx->results_host);
   if (ctx->ident) (void)hipFree(ctx->ident);
@@ -451,8 +452,24 @@ static int gemv_launch(glacier_hip_context *ctx, glacier_hip_int4_weight *w, con
   a.bias = bias_dev;
   a.y = y_dev;
   a.epi = gk::EPI_PLAIN;
-  // up to 32 rows: the decode GEMV (K1); more: the MFMA prefill GEMM (K2)
-  GH_CHECK(ctx, m <= 32 ? gk::launch_gemv(a, st) : gk::launch_gemm(a, st));
+  // up to kGemvMaxRows rows: the decode GEMV (K1); more: the MFMA GEMM (K2),
+  // with a workspace for its K split (grown on demand, capped at 64 MiB;
+  // a smaller one only lowers the split)
+  if (m <= (uint32_t)gk::kGemvMaxRows) {
+    GH_CHECK(ctx, gk::launch_gemv(a, st));
+    return GLACIER_HIP_OK;
+  }
+  const size_t need = std::min<size_t>(gk::gemm_splitk_floats(N, (int)m, K, D), 16u << 20);
+  if (need > ctx->splitk_floats) {
+    if (ctx->splitk) GH_CHECK(ctx, hipFree(ctx->splitk));
+    ctx->splitk = nullptr;
+    ctx->splitk_floats = 0;
+    GH_CHECK(ctx, hipMalloc((void **)&ctx->splitk, need * sizeof(float)));
+    ctx->splitk_floats = need;
+  }
+  a.splitk_ws = ctx->splitk;
+  a.splitk_ws_floats = ctx->splitk_floats;
+  GH_CHECK(ctx, gk::launch_gemm(a, st));
   return GLACIER_HIP_OK;
 }
 

@@ -119,6 +119,8 @@ struct glacier_hip_session {
   int8_t *act_q2 = nullptr;         // planes emitted by the gate/up epilogue for down
   gk::ActMeta *act_meta2 = nullptr;
   uint32_t planes2_rows = 0;        // rows act_q2 / act_meta2 hold
+  float *splitk_ws = nullptr;       // GEMM split-K partial sums
+  size_t splitk_floats = 0;
   float *ss_parts = nullptr;        // deferred RMSNorm partial sums [32][1024]
   float *att_scratch = nullptr;
   void *arg_scratch = nullptr;
@@ -412,6 +414,8 @@ gk::GemvArgs proj_args(glacier_hip_session *s, glacier_hip_int4_weight *w, int D
   a.arg_words = out.arg_words;
   a.arg_word_count = out.arg_word_count;
   a.in_eps = s->model->cfg.rms_eps;
+  a.splitk_ws = s->splitk_ws;
+  a.splitk_ws_floats = s->splitk_floats;
   return a;
 }
 
@@ -451,7 +455,7 @@ int proj_grid(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, int row
 
 hipError_t run_proj(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, int rows, int epi,
                     const ProjIn &in, const ProjOut &out, hipStream_t st) {
-  const bool decode = rows <= 32;
+  const bool decode = rows <= gk::kGemvMaxRows;
   // partial sums, plane emission and the fused head are GEMV-only
   if (!decode && (out.emit.q || out.ss_out || out.arg_parts)) return hipErrorInvalidValue;
   gk::GemvArgs a;
@@ -470,7 +474,8 @@ hipError_t run_proj(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, i
 // Embedding gather and every decoder layer for `rows` activation rows
 // (generate.zig:1511-1967 per row; K/V rows land in the rows' pages).
 //
-// Decode-sized row sets (rows <= 32) run a chain with no conversion kernels:
+// Decode-sized row sets (rows <= kGemvMaxRows) run a chain with no
+// conversion kernels:
 // the gather and each residual projection (O, down) also write per-workgroup
 // sums of squares of their output, from which the next RMSNorm'd projection
 // (QKV, gate/up) finishes its deferred norm while it quantises its input in
@@ -482,7 +487,7 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
   glacier_hip_model *m = s->model;
   const auto &c = m->cfg;
   const int D = (int)c.dim;
-  const bool chain = rows <= 32 && (uint32_t)rows <= s->planes2_rows;
+  const bool chain = rows <= gk::kGemvMaxRows && (uint32_t)rows <= s->planes2_rows;
   gk::QkvArgs q{};
   q.q_out = s->q;
   q.kv_pool = s->kv_pool;
@@ -560,7 +565,7 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
     gin.ss = ss;
     gin.ss_count = ss_count;
     ProjOut gout;
-    if (rows <= 32 && (uint32_t)rows <= s->planes2_rows)
+    if (chain)
       gout.emit = gk::PlanesDst{s->act_q2, s->act_meta2, Dd};
     else
       gout.y = s->act;
@@ -609,7 +614,7 @@ hipError_t enqueue_head(glacier_hip_session *s, int rows, const float *x, bool e
   in.norm_w = m->final_norm;
   ProjOut out;
   out.y = s->logits;
-  if (rows <= 32) {
+  if (rows <= gk::kGemvMaxRows) {
     out.arg_parts = (gk::ArgPartial *)s->arg_scratch;
     out.arg_words = words;
     out.arg_word_count = W;
@@ -637,7 +642,7 @@ void destroy_session(glacier_hip_session *s) {
   void *ptrs[] = {s->kv_pool, s->page_table, s->rope_cos, s->rope_sin, s->x_res, s->h, s->q,
                   s->attn, s->act, s->logits, s->act_q, s->act_meta, s->act_q2, s->act_meta2,
                   s->att_scratch, s->ss_parts, s->arg_scratch, s->arg_counters, s->arg_result,
-                  s->elig_words,
+                  s->elig_words, s->splitk_ws,
                   s->step_dev, s->pf_dev};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
@@ -1040,9 +1045,9 @@ glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
   A((void **)&s->logits, (size_t)L * c.vocab_size * 4);
   A((void **)&s->act_q, Gmax * 3 * M * 32);
   A((void **)&s->act_meta, Gmax * M * sizeof(gk::ActMeta));
-  // the gate/up epilogue emits planes for every decode-path launch: up to 32
-  // rows (decode lanes, or a prompt chunk that short)
-  s->planes2_rows = std::min<uint32_t>(M, 32);
+  // the gate/up epilogue emits planes for every decode-path launch: up to
+  // kGemvMaxRows rows (decode lanes, or a prompt chunk that short)
+  s->planes2_rows = std::min<uint32_t>(M, gk::kGemvMaxRows);
   // act_q2 also holds the O projection's planes, emitted by attention
   const size_t G2 = std::max<size_t>(c.hidden_dim, (size_t)c.num_heads * c.head_dim) / 32;
   A((void **)&s->act_q2, G2 * 3 * s->planes2_rows * 32);
@@ -1050,12 +1055,27 @@ glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
   A((void **)&s->att_scratch, std::max<size_t>(att, 1) * 4);
   A((void **)&s->ss_parts, (size_t)32 * 1024 * sizeof(float));
   size_t arg_bytes = gk::argmax_scratch_bytes((int)L, (long)c.vocab_size);
-  for (uint32_t r = 1; r <= std::min<uint32_t>(L, 32); ++r)
+  for (uint32_t r = 1; r <= std::min<uint32_t>(L, gk::kGemvMaxRows); ++r)
     arg_bytes = std::max(arg_bytes, (size_t)r * sizeof(gk::ArgPartial) *
                                         std::max(0, gk::gemv_argmax_parts((int)c.vocab_size,
                                                                           (int)c.dim, (int)r,
                                                                           head_D(s))));
   A(&s->arg_scratch, arg_bytes);
+  // GEMM split-K partial sums: the most any projection asks for at the row
+  // counts past the GEMV (decode lanes up to 32, a full prompt chunk),
+  // capped at 64 MiB (a smaller workspace only lowers a split)
+  {
+    size_t need = 0;
+    const LayerDev &L0 = m->layers[0];  // every layer has the same shapes
+    const glacier_hip_int4_weight *ws[] = {L0.qkv, L0.o, L0.gu, L0.down, m->head};
+    for (uint32_t rows : {(uint32_t)gk::kGemvMaxRows + 1, 24u, 32u, M})
+      if (rows > (uint32_t)gk::kGemvMaxRows && rows <= M)
+        for (const auto *w : ws)
+          for (int D : {1, 3})
+            need = std::max(need, gk::gemm_splitk_floats((int)w->out_f, (int)rows, (int)w->in_f, D));
+    s->splitk_floats = std::min<size_t>(need, 16u << 20);
+    if (s->splitk_floats) A((void **)&s->splitk_ws, s->splitk_floats * sizeof(float));
+  }
   A((void **)&s->arg_counters, (size_t)L * 4);
   A((void **)&s->arg_result, (size_t)L * sizeof(gk::ArgmaxResult));
   A((void **)&s->elig_words, (size_t)L * W * 8);

@@ -231,6 +231,30 @@ def test_multi_lane_matches_independent_runs(gh, tiny):
         sess.close()
 
 
+def test_wide_step_matches_independent_runs(gh, tiny):
+    """20 lanes in one step (past the 16-row GEMV: the split-K MFMA GEMM for
+    every projection, the separate conversion kernels, the plain argmax):
+    each lane's greedy tokens equal the oracle's run of that lane alone."""
+    host, om, m = tiny
+    lanes, max_new = 20, 4
+    prompts = [gh.synth_tokens(SEED, 70 + i, TINY["vocab_size"], 3 + (i % 7)) for i in range(lanes)]
+    wants = [om.generate(p, max_new)[0].tolist() for p in prompts]
+    sess = gh.Session(m, max_lanes=lanes, max_positions=32)
+    try:
+        toks = []
+        for i, p in enumerate(prompts):
+            sess.begin(i)
+            toks.append([sess.prefill(i, p)])
+        order = list(range(lanes))[::-1]
+        for _ in range(max_new - 1):
+            nxt = sess.step(order, [toks[i][-1] for i in order])
+            for k, i in enumerate(order):
+                toks[i].append(int(nxt[k]))
+        assert toks == wants
+    finally:
+        sess.close()
+
+
 def test_eligible_step_matches_masked_argmax(gh, tiny, ora):
     host, om, m = tiny
     V = TINY["vocab_size"]
@@ -257,12 +281,14 @@ def test_eligible_step_matches_masked_argmax(gh, tiny, ora):
         sess.close()
 
 
-@pytest.mark.parametrize("lanes", [2, 4])
+@pytest.mark.parametrize("lanes", [2, 4, 20])
 def test_fused_head_argmax_matches_logit_scan(gh, tiny, ora, lanes):
     """The LM head reduces its logits to per-workgroup candidates and a
-    one-block merge picks the token (dot4 head at 2 rows, MFMA head at 4):
-    the token equals the oracle's (eligible) argmax over the logits the same
-    step returns, for dense, sparse, first-only and last-only masks."""
+    one-block merge picks the token (dot4 head at 2 rows, MFMA head at 4;
+    past 16 rows the GEMM writes the logits and the separate argmax scans
+    them): the token equals the oracle's (eligible) argmax over the logits
+    the same step returns, for dense, sparse, first-only and last-only
+    masks."""
     host, om, m = tiny
     V = TINY["vocab_size"]
     W = V // 64

@@ -1,6 +1,7 @@
-"""GPU parity of the MFMA prefill GEMM (K2: projections over more than 32
-rows) against the CPU oracle, through the C ABI (glacier_hip_int4_gemv with
-m > 32), and of chunked prefill end to end.
+"""GPU parity of the MFMA GEMM (K2: projections over more than 16 rows,
+32-row tiles up to 32 rows with K split over workgroups, 64-row tiles above)
+against the CPU oracle, through the C ABI (glacier_hip_int4_gemv with
+m > 16), and of chunked prefill end to end.
 
 Tolerances: as the decode GEMV. Q8: every per-group integer dot is exact and
 the group term RN(T * s_w) is the reference's; the activation scale is folded
@@ -44,7 +45,7 @@ SHAPES = [(16, 128), (48, 256), (896, 896), (128, 896), (896, 4864), (9728, 896)
 
 
 @pytest.mark.parametrize("out_f,in_f", SHAPES)
-@pytest.mark.parametrize("m", [33, 64, 130, 300])
+@pytest.mark.parametrize("m", [17, 24, 32, 33, 64, 130, 300])
 def test_gemm_q8_matches_oracle(gh, gctx, ora, out_f, in_f, m):
     packed, s16, s32 = _weights(gh, 300 + out_f + in_f, out_f, in_f)
     w = gctx.weight(packed, s16, in_f, out_f)
@@ -60,7 +61,7 @@ def test_gemm_q8_matches_oracle(gh, gctx, ora, out_f, in_f, m):
 
 
 @pytest.mark.parametrize("out_f,in_f", [(48, 256), (896, 896), (512, 18944)])
-@pytest.mark.parametrize("m", [40, 129])
+@pytest.mark.parametrize("m", [20, 32, 40, 129])
 def test_gemm_f32_matches_oracle(gh, gctx, ora, out_f, in_f, m):
     packed, s16, s32 = _weights(gh, 400 + out_f + in_f, out_f, in_f)
     w = gctx.weight(packed, s16, in_f, out_f)
@@ -78,8 +79,9 @@ def test_gemm_f32_matches_oracle(gh, gctx, ora, out_f, in_f, m):
 @pytest.mark.parametrize("out_f,in_f,act", [(3584, 3584, "q8"), (4608, 3584, "q8"),
                                             (3584, 18944, "f32")])
 def test_gemm_rows_equal_gemv_rows_at_7b_prefill_size(gh, gctx, out_f, in_f, act):
-    """M = 2048 prompt rows: 32 rows spread over the chunk,
-    the first and the last included, equal the decode GEMV of those rows."""
+    """M = 2048 prompt rows: 16 rows spread over the chunk,
+    the first and the last included, equal the decode GEMV of those rows; and
+    24 of them through the 32-row split-K tiles."""
     a = gh.ACT_Q8 if act == "q8" else gh.ACT_F32
     packed, s16, _ = _weights(gh, 500 + out_f + in_f, out_f, in_f)
     w = gctx.weight(packed, s16, in_f, out_f)
@@ -87,12 +89,13 @@ def test_gemm_rows_equal_gemv_rows_at_7b_prefill_size(gh, gctx, out_f, in_f, act
         m = 2048
         x = np.random.default_rng(3).standard_normal((m, in_f)).astype(np.float32)
         big = _proj(gh, gctx, w, out_f, x, a)
-        rows = np.unique(np.concatenate([[0, 1, 15, 16, 127, 128, m - 1],
-                                         np.random.default_rng(4).choice(m, 25, replace=False)]))[:32]
-        small = _proj(gh, gctx, w, out_f, x[rows], a)
-        err = np.max(np.abs(big[rows] - small)) / np.max(np.abs(small))
-        print(f"gemm vs gemv {out_f}x{in_f} {act} rel={err:.3e}", flush=True)
-        assert err < (2e-6 if act == "q8" else 1e-5)
+        pick = np.unique(np.concatenate([[0, 1, 15, 16, 127, 128, m - 1],
+                                         np.random.default_rng(4).choice(m, 25, replace=False)]))
+        for rows in (pick[:16], pick[:24]):
+            small = _proj(gh, gctx, w, out_f, x[rows], a)
+            err = np.max(np.abs(big[rows] - small)) / np.max(np.abs(small))
+            print(f"gemm vs {len(rows)} rows {out_f}x{in_f} {act} rel={err:.3e}", flush=True)
+            assert err < (2e-6 if act == "q8" else 1e-5)
         assert np.all(np.isfinite(big))
     finally:
         gh.lib().glacier_hip_int4_weight_destroy(w)
