@@ -355,6 +355,9 @@ def main():
     ap.add_argument("--lane-prompt", type=int, default=64)
     ap.add_argument("--gemv-reps", type=int, default=50)
     ap.add_argument("--gemv-only", action="store_true", help="only the GEMV kernel timing")
+    ap.add_argument("--gemv-rows", type=int, default=1,
+                    help="with --gemv-only: activation rows of the timed gate/up launch (past "
+                         "16 rows the C ABI runs the MFMA GEMM; counter runs at prefill size)")
     ap.add_argument("--sections", default="gemv,decode,lanes,c5,prefill,attention,cpu",
                     help="comma list of gemv, decode, lanes, c5, prefill, attention, cpu "
                          "(profiling runs select one; the JSON line needs decode)")
@@ -399,7 +402,8 @@ def main():
     n, k = GATE_UP
     dom = None
     if "gemv" in secs or a.gemv_only:
-        dom = time_gemv(gh, ctx, torch, n, k, 1, a.gemv_reps * 2, gh.ACT_Q8)
+        rows = a.gemv_rows if a.gemv_only else 1
+        dom = time_gemv(gh, ctx, torch, n, k, rows, a.gemv_reps * 2, gh.ACT_Q8)
         log("gemv gate/up", dom)
     if not a.gemv_only and "gemv" in secs:
         for (n, k) in GEMV_SHAPES:
@@ -410,8 +414,8 @@ def main():
     roofline = dict(bound="hbm", achieved=dom["gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
                     frac=dom["frac"], traffic=measured_traffic()) if dom else None
     if a.gemv_only:
-        print(json.dumps(dict(metric="int4 gemv HBM GB/s (7B gate/up, M=1)", value=dom["gbs"],
-                              unit="GB/s", roofline=roofline, gemv=[dom])))
+        print(json.dumps(dict(metric=f"int4 gemv HBM GB/s (7B gate/up, M={dom['M']})",
+                              value=dom["gbs"], unit="GB/s", roofline=roofline, gemv=[dom])))
         return
 
     # ---- 7B model ----

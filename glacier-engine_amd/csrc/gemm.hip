@@ -1,6 +1,7 @@
-// gemm.hip — K2: INT4 x int8-digit prefill GEMM on gfx950 MFMA.
+// gemm.hip — K2: INT4 x int8-digit GEMM on gfx950 MFMA.
 //
-// y[M][N] = planes(x)[M][K] . W^T for prompt chunks (M > 32 rows), with the
+// y[M][N] = planes(x)[M][K] . W^T past 16 rows (wide decode batches, prompt
+// chunks), with the
 // same digit planes, tile layout and fused epilogues as the decode GEMV (K1):
 // the per-group arithmetic is the reference's Q8 dot
 // (int4_matmul.zig:365-418): an exact integer dot per 32-element group,
@@ -17,8 +18,9 @@
 // The per-group scaling (two fmas per output and group against one MFMA per
 // 16 x 16 x 32 group tile) bounds this kernel by VALU issue, not by the
 // matrix cores; the layout keeps everything else off that path:
-//   * workgroup = 4 waves over a 64-row x 256-column output tile; each wave
-//     owns 4 weight row blocks (64 columns) x the 4 activation row tiles;
+//   * workgroup = 4 waves over a BM-row (32 or 64) x 64 kRB-column output
+//     tile; each wave owns kRB (2 or 4) weight row blocks x the BM / 16
+//     activation row tiles;
 //   * weights: each lane loads its own 16-byte tile slot per row block and
 //     quad (1 KB per wave, fully coalesced), two quads in flight; the words
 //     are transposed across lanes into MFMA operands (quad_transpose) and
@@ -28,7 +30,11 @@
 //     per quad; every wave reads its operands from there;
 //   * block ids are remapped so that the row tiles of one weight column tile
 //     run on one XCD (hardware places block b on XCD b % 8), which keeps the
-//     tile's weights in that XCD's L2 for every row tile that reads them.
+//     tile's weights in that XCD's L2 for every row tile that reads them;
+//   * small grids (few row tiles x few column tiles, e.g. 32 decode rows of a
+//     3584-wide projection) split K over workgroups: each split writes its
+//     partial sums and splitk_reduce_kernel adds the splits in a fixed order
+//     and runs the epilogue (deterministic, no atomics).
 #include "epilogue.h"
 #include "int4_ops.h"
 #include "kernels.h"

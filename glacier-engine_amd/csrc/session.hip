@@ -528,7 +528,7 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
     // attention (chain: also the O projection's planes)
     const gk::PlanesDst opd = chain ? gk::PlanesDst{s->act_q2, s->act_meta2, Do}
                                     : gk::PlanesDst{nullptr, nullptr, 1};
-    if (rows > 32 && rp.chunk_lane >= 0 && s->opt.kv_dtype == GLACIER_HIP_F16)
+    if (rows > gk::kGemvMaxRows && rp.chunk_lane >= 0 && s->opt.kv_dtype == GLACIER_HIP_F16)
       e = gk::launch_attention_prefill(s->q, s->kv_pool, s->page_table, (int)s->max_pages,
                                        rp.chunk_lane, rp.chunk_pos0, rows, (int)l,
                                        (int)c.num_layers, (int)c.num_heads, (int)c.num_kv_heads,
