@@ -19,7 +19,7 @@
 // 16 x 16 x 32 group tile) bounds this kernel by VALU issue, not by the
 // matrix cores; the layout keeps everything else off that path:
 //   * workgroup = 4 waves over a BM-row (32 or 64) x 64 kRB-column output
-//     tile; each wave owns kRB (2 or 4) weight row blocks x the BM / 16
+//     tile; each wave owns kRB (1, 2 or 4) weight row blocks x the BM / 16
 //     activation row tiles;
 //   * weights: each lane loads its own 16-byte tile slot per row block and
 //     quad (1 KB per wave, fully coalesced), two quads in flight; the words
@@ -93,12 +93,12 @@ __device__ __forceinline__ void act_store(unsigned char *buf, const ActRegs<D, B
   ((float *)(buf + ActStage<D, BM>::kActBytes))[t % (4 * BM)] = r.sc;
 }
 
-// kRB: 16-row weight blocks per wave (the workgroup covers 4 kRB of them);
+// kRB: 16-row weight blocks per wave (1, 2 or 4; the workgroup covers 4 kRB);
 // BM: activation rows per workgroup (32 or 64). With ks_count > 1 the K
 // quads are split over blockIdx.y and each split writes its partial sums to
 // part [ks_count][M][N] (no epilogue; splitk_reduce_kernel finishes).
 template <int D, int kRB, int BM>
-__global__ __launch_bounds__(256, kRB == 4 ? 2 : 4) void gemm_kernel(GemvArgs p, int m_tiles,
+__global__ __launch_bounds__(256, kRB == 4 ? 2 : kRB == 2 ? 4 : 5) void gemm_kernel(GemvArgs p, int m_tiles,
                                                                      int ks_count, float *part) {
   using S = ActStage<D, BM>;
   constexpr int MT = BM / 16;         // 16-row activation tiles per wave
@@ -183,14 +183,15 @@ __global__ __launch_bounds__(256, kRB == 4 ? 2 : 4) void gemm_kernel(GemvArgs p,
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) wt[rb] = quad_transpose(wc[rb]);
 #pragma unroll
-      for (int h = 0; h < kRB / 2; ++h) {
+      for (int h = 0; h < (kRB + 1) / 2; ++h) {
         // two row blocks' u16 scales per register, all four groups' rows
         uint32_t g4[4];
-        column_gather((sc[2 * h] & 0xFFFFu) | (sc[2 * h + 1] << 16), g4);
+        const uint32_t hi = 2 * h + 1 < kRB ? sc[min(2 * h + 1, kRB - 1)] << 16 : 0u;
+        column_gather((sc[2 * h] & 0xFFFFu) | hi, g4);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           ws[2 * h][j] = h2f(g4[j] & 0xFFFFu);
-          ws[2 * h + 1][j] = h2f(g4[j] >> 16);
+          if (2 * h + 1 < kRB) ws[min(2 * h + 1, kRB - 1)][j] = h2f(g4[j] >> 16);
         }
       }
 #pragma unroll
@@ -313,18 +314,27 @@ GemmShape plan_gemm(int N, int M, int K, int D, size_t ws_floats) {
   const int bm = M <= 32 ? 32 : 64;
   s.mt = bm / 16;
   s.m_tiles = (M + bm - 1) / bm;
-  // 2 row blocks per wave (4 workgroups per CU) for one-digit planes; the
-  // three-digit kernel with 4 (2 per CU) once that still fills the GPU
-  // (measured on the 7B shapes at 512 and 2048 rows)
+  // Row blocks per wave and the workgroup target, from sweeps of the 7B
+  // shapes: 32-row tiles (decode lanes) 1 row block per wave for one-digit
+  // planes, 2 for three, toward about 1024 workgroups; 64-row tiles (prompt
+  // chunks) 2 for one digit (4 workgroups per CU), 4 for three once that
+  // still fills the GPU, toward about 512.
   const int NB = N / 16, KQ = K / 128;
   const long big = (long)s.m_tiles * ((NB + 15) / 16);
-  s.nt = D == 3 && big >= 384 ? 16 : 8;
+  int target;
+  if (bm == 32) {
+    s.nt = D == 1 ? 4 : 8;
+    target = 1024;
+  } else {
+    s.nt = D == 3 && big >= 384 ? 16 : 8;
+    target = 512;
+  }
   s.n_tiles = (NB + s.nt - 1) / s.nt;
   s.grid = s.m_tiles * s.n_tiles;
-  // split K over workgroups (at least 2 quads each) until about 512
-  // workgroups, as far as the partial sums fit the workspace
+  // split K over workgroups (at least 2 quads each) toward the target, as far
+  // as the partial sums fit the workspace
   s.ks = 1;
-  while (s.grid * s.ks < 512 && 2 * s.ks <= KQ / 2 && s.ks < 16 &&
+  while (s.grid * s.ks < target && 2 * s.ks <= KQ / 2 && s.ks < 16 &&
          (size_t)(2 * s.ks) * M * N <= ws_floats)
     s.ks *= 2;
   return s;
@@ -340,7 +350,7 @@ hipError_t launch_gemm(const GemvArgs &a, hipStream_t st) {
     return hipErrorInvalidValue;
   if (a.out_q || a.ss_out || a.arg_parts || a.x_in) return hipErrorInvalidValue;  // GEMV-only
   GemmShape s = plan_gemm(a.N, a.M, a.K, a.D, a.splitk_ws ? a.splitk_ws_floats : 0);
-  if (a.rb_override == 2 || a.rb_override == 4) {  // tuning: row blocks per wave
+  if (a.rb_override == 1 || a.rb_override == 2 || a.rb_override == 4) {  // tuning
     s.nt = 4 * a.rb_override;
     s.n_tiles = (a.N / 16 + s.nt - 1) / s.nt;
     s.grid = s.m_tiles * s.n_tiles;
@@ -360,9 +370,9 @@ hipError_t launch_gemm(const GemvArgs &a, hipStream_t st) {
     if (s.mt == 2) GK_GEMM(DD, RB, 32); else GK_GEMM(DD, RB, 64); \
   } while (0)
   if (a.D == 1) {
-    if (s.nt == 16) GK_GEMM_BM(1, 4); else GK_GEMM_BM(1, 2);
+    if (s.nt == 16) GK_GEMM_BM(1, 4); else if (s.nt == 8) GK_GEMM_BM(1, 2); else GK_GEMM_BM(1, 1);
   } else {
-    if (s.nt == 16) GK_GEMM_BM(3, 4); else GK_GEMM_BM(3, 2);
+    if (s.nt == 16) GK_GEMM_BM(3, 4); else if (s.nt == 8) GK_GEMM_BM(3, 2); else GK_GEMM_BM(3, 1);
   }
 #undef GK_GEMM_BM
 #undef GK_GEMM

@@ -525,10 +525,15 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
     qout.qkv = &q;
     e = run_proj(s, L.qkv, Dq, rows, gk::EPI_QKV, qin, qout, st);
     if (e != hipSuccess) return e;
-    // attention (chain: also the O projection's planes)
-    const gk::PlanesDst opd = chain ? gk::PlanesDst{s->act_q2, s->act_meta2, Do}
-                                    : gk::PlanesDst{nullptr, nullptr, 1};
-    if (rows > gk::kGemvMaxRows && rp.chunk_lane >= 0 && s->opt.kv_dtype == GLACIER_HIP_F16)
+    // attention: a prompt chunk of one lane past the GEMV size runs the
+    // prefill kernel, other steps the decode kernel, which for up to 32 rows
+    // also writes the O projection's planes
+    const bool pf_attn = rows > gk::kGemvMaxRows && rp.chunk_lane >= 0 &&
+                         s->opt.kv_dtype == GLACIER_HIP_F16;
+    const bool o_planes = !pf_attn && rows <= 32 && (uint32_t)rows <= s->planes2_rows;
+    const gk::PlanesDst opd = o_planes ? gk::PlanesDst{s->act_q2, s->act_meta2, Do}
+                                       : gk::PlanesDst{nullptr, nullptr, 1};
+    if (pf_attn)
       e = gk::launch_attention_prefill(s->q, s->kv_pool, s->page_table, (int)s->max_pages,
                                        rp.chunk_lane, rp.chunk_pos0, rows, (int)l,
                                        (int)c.num_layers, (int)c.num_heads, (int)c.num_kv_heads,
@@ -546,7 +551,7 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
     oout.y = s->h;
     oout.resid = s->x_res;
     oout.ss_out = ss;
-    if (chain) {
+    if (o_planes) {
       oin.planes_q = s->act_q2;
       oin.planes_m = s->act_meta2;
     } else {
@@ -1045,9 +1050,10 @@ glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
   A((void **)&s->logits, (size_t)L * c.vocab_size * 4);
   A((void **)&s->act_q, Gmax * 3 * M * 32);
   A((void **)&s->act_meta, Gmax * M * sizeof(gk::ActMeta));
-  // the gate/up epilogue emits planes for every decode-path launch: up to
-  // kGemvMaxRows rows (decode lanes, or a prompt chunk that short)
-  s->planes2_rows = std::min<uint32_t>(M, gk::kGemvMaxRows);
+  // the gate/up epilogue emits planes for every GEMV launch (up to
+  // kGemvMaxRows rows) and attention the O projection's for every step of
+  // up to 32 rows (decode lanes, or a prompt chunk that short)
+  s->planes2_rows = std::min<uint32_t>(M, 32);
   // act_q2 also holds the O projection's planes, emitted by attention
   const size_t G2 = std::max<size_t>(c.hidden_dim, (size_t)c.num_heads * c.head_dim) / 32;
   A((void **)&s->act_q2, G2 * 3 * s->planes2_rows * 32);
