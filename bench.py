@@ -12,8 +12,8 @@ KV already resident in HBM. The same JSON line carries:
   * c5_laneweave config 5: 32 lanes under LaneWeave weighted IWRR, prompts
                 U[64, 4096], 256 tokens each through the eligible argmax;
   * gemv        the INT4 GEMV kernel timed alone on the BASELINE config-2
-                shapes and on the 7B gate/up projection, with HIP events on
-                the launch stream;
+                shapes at M = 1, 2, 4 and 8 and on the 7B gate/up projection,
+                with HIP events on the launch stream;
   * prefill     config 4: 7B time to first token at T = 512 and 2048 and the
                 int8 MFMA rate it implies;
   * attention   config 3: paged GQA decode attention alone, 4 lanes at
@@ -407,7 +407,7 @@ def main():
         log("gemv gate/up", dom)
     if not a.gemv_only and "gemv" in secs:
         for (n, k) in GEMV_SHAPES:
-            for m in (1, 8):
+            for m in (1, 2, 4, 8):
                 r = time_gemv(gh, ctx, torch, n, k, m, a.gemv_reps, auto_act(gh, n, k))
                 log("gemv", r)
                 gemv.append(r)
