@@ -1474,20 +1474,32 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(
   }
   __syncthreads();
   // ---- merge the waves (log-sum-exp) ----
-  for (int oi = t; oi < G * HD; oi += 64 * NW) {
-    const int g = oi / HD, d = oi % HD;
+  // The weight of wave w for head g, exp(m_w - M) (0 for a wave without
+  // positions), is computed once per (wave, head); every output is then two
+  // short dot products over the waves, in wave order (the same arithmetic
+  // as evaluating the weights inside each output's loop, without its NW
+  // exponentials and branches per output).
+  __shared__ float fw[NW][kMaxGroup], mg[kMaxGroup];
+  for (int i = t; i < NW * G; i += 64 * NW) {
+    const int w = i / G, g = i % G;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < NW; ++w)
-      if (sl[w][g] > 0.0f) M = fmaxf(M, sm[w][g]);
+    for (int w2 = 0; w2 < NW; ++w2)
+      if (sl[w2][g] > 0.0f) M = fmaxf(M, sm[w2][g]);
+    fw[w][g] = sl[w][g] > 0.0f ? expf(sm[w][g] - M) : 0.0f;
+    if (w == 0) mg[g] = M;
+  }
+  __syncthreads();
+  for (int oi = t; oi < G * HD; oi += 64 * NW) {
+    const int g = oi / HD, d = oi % HD;
+    const float M = mg[g];
     float L = 0.0f, O = 0.0f;
 #pragma unroll
-    for (int w = 0; w < NW; ++w)
-      if (sl[w][g] > 0.0f) {
-        const float f = expf(sm[w][g] - M);
-        L = fmaf(sl[w][g], f, L);
-        O = fmaf(so[w][g][d], f, O);
-      }
+    for (int w = 0; w < NW; ++w) {
+      const float f = fw[w][g];
+      L = fmaf(sl[w][g], f, L);
+      O = fmaf(so[w][g][d], f, O);
+    }
     if (nch == 1) {
       const float v = O * (1.0f / L);
       out[((size_t)m * Hq + qh0 + g) * HD + d] = v;
