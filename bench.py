@@ -21,7 +21,10 @@ KV already resident in HBM. The same JSON line carries:
   * roofline    for the dominant kernel (the fused 7B gate/up GEMV, 53% of a
                 token's weight bytes): algorithmic bytes / average duration;
   * cpu_baseline the CPU oracle (the reference algorithm restated in C) on the
-                same model, timed on this host's cores over a bounded sample.
+                same model, timed on this host's cores over a bounded sample;
+                with the cpu section the gemv (M = 1), attention and prefill
+                entries also carry the oracle's rate on the same inputs (and
+                the GPU result's deviation from it) under "cpu".
 Weights are random-init from a fixed seed (no checkpoints exist offline).
 """
 import argparse
@@ -112,6 +115,52 @@ def time_gemv(gh, ctx, torch, n, k, m, reps, act):
     finally:
         for w in ws:
             L.glacier_hip_int4_weight_destroy(w)
+
+
+def cpu_gemv(gh, ctx, torch, n, k, act):
+    """Config-2 CPU leg for one shape at M = 1: the oracle's row-split
+    restatement of the reference's a2 (f32) / a3 (Q8) GEMV timed on every host
+    core (at most 16) and on 8 threads (the reference executor's cap), and the
+    GPU launch's result on the same inputs compared with it (max |diff| /
+    max |oracle|; the reference's own bar is 1e-3)."""
+    import oracle
+
+    oracle.build()
+    L = gh.lib()
+    packed = gh.synth_int4(SEED, n * 7 + k, n * k // 2)
+    s16 = gh.synth_scales_f16(SEED, n * 11 + k, n * k // 32)
+    s32 = s16.view(np.float16).astype(np.float32)
+    x = np.random.default_rng(n + k).standard_normal((1, k)).astype(np.float32)
+    w = ctx.weight(packed, s16, k, n)
+    try:
+        xd = torch.from_numpy(x).cuda()
+        yd = torch.empty((1, n), dtype=torch.float32, device="cuda")
+        gh.check(L.glacier_hip_int4_gemv(ctx.h, w, xd.data_ptr(), gh.F32, 1, None, yd.data_ptr(),
+                                         act, None), "gemv", ctx.h)
+        ctx.sync()
+        got = yd.cpu().numpy()
+    finally:
+        L.glacier_hip_int4_weight_destroy(w)
+    fn = oracle.linear_int4_q8 if act == gh.ACT_Q8 else oracle.linear_int4_f32
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    res = {}
+    want = None
+    for th in (cores, 8):
+        oracle.set_threads(th)
+        want = fn(x, packed, s32, n, k, 32)
+        reps = 1
+        t0 = time.perf_counter()
+        dt = 0.0
+        while dt < 0.2 and reps < 64:  # a few tenths of a second per thread count
+            fn(x, packed, s32, n, k, 32)
+            dt = time.perf_counter() - t0
+            reps += 1
+        res[th] = dt / (reps - 1)
+    b = gemv_bytes(n, k, 1, 1 if act == gh.ACT_Q8 else 3)
+    err = float(np.max(np.abs(got - want)) / np.max(np.abs(want)))
+    return dict(threads=cores, us=round(res[cores] * 1e6, 1), gbs=round(b / res[cores] / 1e9, 2),
+                us_8_threads=round(res[8] * 1e6, 1), gbs_8_threads=round(b / res[8] / 1e9, 2),
+                max_rel_vs_oracle=float(f"{err:.3g}"), kind="port")
 
 
 def measured_traffic():
@@ -270,7 +319,7 @@ def bench_prefill(gh, model, lengths, reps=3):
     return out
 
 
-def bench_attention(gh, ctx, torch, reps=20):
+def bench_attention(gh, ctx, torch, reps=20, cpu=False):
     """paged GQA decode attention alone at Qwen2.5-7B head
     geometry (28 q / 4 kv heads, hd 128), fp16 KV in 16-position pages of a
     28-layer payload, pages scattered by a seeded permutation, 4 lanes at
@@ -320,6 +369,24 @@ def bench_attention(gh, ctx, torch, reps=20):
     b = sum(2 * c * Hkv * hd * 2 for c in ctxs) + len(ctxs) * Hq * hd * 4 * 2 + sum(pages) * 4
     res = dict(contexts=ctxs, us=round(us, 2), bytes=b, gbs=round(b / us / 1e3, 1),
                frac=round(b / us / 1e3 / HBM_PEAK_GBS, 4), kv="fp16, 28-layer pages")
+    if cpu:
+        # config-3 CPU leg: the oracle's a7 (fp16 pages widened to f32, one
+        # thread, as the reference's attention) on the same pool and rows
+        import oracle
+
+        oracle.build()
+        go()
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        pool_h = pool.cpu().numpy()
+        qh = q.cpu().numpy()
+        t0 = time.perf_counter()
+        want = np.stack([oracle.attention_paged(qh[i], pool_h, True, pt[i].numpy(), ctxs[i], layer,
+                                                layers, Hq, Hkv, hd)[0] for i in range(len(ctxs))])
+        dt = time.perf_counter() - t0
+        res["cpu"] = dict(threads=1, us=round(dt * 1e6, 1), gbs=round(b / dt / 1e9, 3), kind="port",
+                          max_rel_vs_oracle=float(f"{np.max(np.abs(got - want)) / np.max(np.abs(want)):.3g}"))
+        del pool_h
     log("attention", res)
     del gr, pool
     return res
@@ -340,9 +407,16 @@ def cpu_baseline(host, prompt_tok, budget_s=15.0):
     t0 = time.perf_counter()
     om.generate(np.array([prompt_tok], np.uint32), n)
     dt = time.perf_counter() - t0
+    # config-4 leg: the reference prefills token at a time (generate.zig:5080);
+    # an 8-token prompt (plus the one head and argmax) gives its prompt rate
+    p8 = np.full(8, prompt_tok, np.uint32)
+    t0 = time.perf_counter()
+    om.generate(p8, 1)
+    dp = time.perf_counter() - t0
     return dict(value=round(n / dt, 3), unit="tokens/s", cores=cores, kind="port",
                 sample=f"oracle greedy run of the same 7B model: 1-token prompt + {n} tokens "
-                       f"({dt:.1f} s), Q8 layers / f32 head, {cores} threads row-split")
+                       f"({dt:.1f} s), Q8 layers / f32 head, {cores} threads row-split",
+                prefill_tokens_per_s=round(8 / dp, 3))
 
 
 def main():
@@ -409,6 +483,8 @@ def main():
         for (n, k) in GEMV_SHAPES:
             for m in (1, 2, 4, 8):
                 r = time_gemv(gh, ctx, torch, n, k, m, a.gemv_reps, auto_act(gh, n, k))
+                if m == 1 and not a.no_cpu_baseline:
+                    r["cpu"] = cpu_gemv(gh, ctx, torch, n, k, auto_act(gh, n, k))
                 log("gemv", r)
                 gemv.append(r)
     roofline = dict(bound="hbm", achieved=dom["gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
@@ -445,10 +521,14 @@ def main():
     c5 = bench_c5(gh, model) if "c5" in secs else None
     prefill = bench_prefill(gh, model, [512, 2048]) if not a.no_prefill else None
     model.close()
-    attn = bench_attention(gh, ctx, torch) if not a.no_attention else None
+    attn = bench_attention(gh, ctx, torch, cpu=not a.no_cpu_baseline) if not a.no_attention else None
     cpu = None if a.no_cpu_baseline else cpu_baseline(host, int(prompt[0]))
     if cpu:
         log("cpu baseline", cpu)
+        for pf in prefill or []:
+            pf["cpu"] = dict(threads=cpu["cores"], tokens_per_s=cpu["prefill_tokens_per_s"],
+                             ttft_s_estimate=round(pf["T"] / cpu["prefill_tokens_per_s"], 1),
+                             kind="port", sample="8-token prompt, token at a time")
         if c5:
             # the reference serves one lane per quantum with the serial token
             # loop (F10): its multi-lane rate is its single-lane rate
