@@ -79,4 +79,49 @@ static __device__ __forceinline__ void column_gather(uint32_t x, uint32_t out[4]
   out[3] = c.y;
 }
 
+// v combined with the value of lane ^ 16 (rows 0/1 and 2/3 of the wave) or
+// lane ^ 32 (the two halves), through the permlane swaps instead of LDS
+// permutes. A swap of v with itself leaves the pair's two values in r.x and
+// r.y of both lanes, so the commutative result is bit-identical to
+// v + shuffle_xor(v, 16 or 32).
+static __device__ __forceinline__ float xor16_add(float v) {
+  const v2u r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r.x) + __uint_as_float(r.y);
+}
+static __device__ __forceinline__ float xor32_add(float v) {
+  const v2u r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r.x) + __uint_as_float(r.y);
+}
+static __device__ __forceinline__ float xor16_max(float v) {
+  const v2u r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r.x), __uint_as_float(r.y));
+}
+static __device__ __forceinline__ float xor32_max(float v) {
+  const v2u r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r.x), __uint_as_float(r.y));
+}
+
+// Reductions over each 32-lane half of a wave (every lane of the half gets
+// the result): DPP row rotations by 8, 4, 2, 1 combine the 16 lanes of a row,
+// then a 16-lane swap of the value with itself puts the even row's and the
+// odd row's results side by side in every lane (rows 0/1 and 2/3 pair up,
+// which are exactly the two halves). Max and integer sums are exact in any
+// order, so the results equal a butterfly's.
+static __device__ __forceinline__ float half_wave_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x122, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x121, 0xF, 0xF, false)));
+  const v2u r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r.x), __uint_as_float(r.y));
+}
+static __device__ __forceinline__ int half_wave_sum(int v) {
+  v += __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false);
+  v += __builtin_amdgcn_mov_dpp(v, 0x124, 0xF, 0xF, false);
+  v += __builtin_amdgcn_mov_dpp(v, 0x122, 0xF, 0xF, false);
+  v += __builtin_amdgcn_mov_dpp(v, 0x121, 0xF, 0xF, false);
+  const v2u r = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+  return (int)(r.x + r.y);
+}
+
 }  // namespace gk

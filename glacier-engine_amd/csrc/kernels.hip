@@ -42,8 +42,7 @@ static __device__ __forceinline__ float load_x(const void *x, int bf16, size_t i
 template <int D>
 static __device__ __forceinline__ void quantize_group(float v, int hl, int g, int m, int M,
                                                       int8_t *act_q, ActMeta *meta) {
-  float amax = fabsf(v);
-  for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
+  const float amax = half_wave_max(fabsf(v));
   const float scale = amax / 127.0f;
   const float inv_s = scale == 0.0f ? 0.0f : 1.0f / scale;
   const float y = v * inv_s;
@@ -63,8 +62,7 @@ static __device__ __forceinline__ void quantize_group(float v, int hl, int g, in
     act_q[(((size_t)g * D + d) * M + m) * 32 + hl] = (int8_t)qd[d];
     comb = comb * 128 + qd[d];
   }
-  int sum = comb;
-  for (int o = 16; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 32);
+  const int sum = half_wave_sum(comb);
   if (hl == 0) {
     ActMeta mm;
     mm.scale = D == 3 ? scale * (1.0f / 16384.0f) : scale;
@@ -608,8 +606,7 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       float v = accm[m];
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
+      v = xor32_add(xor16_add(v));
       accm[m] = v;
     }
 #pragma unroll
@@ -626,8 +623,7 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       float v = acc[0][m];
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
+      v = xor32_add(xor16_add(v));
       acc[0][m] = v;
     }
   }
@@ -1375,6 +1371,15 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(
   for (int b = 0; b < DPL; ++b) o[b] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   float mx = -INFINITY, sum = 0.0f;
   if (wn > 0) {
+    // q first (it depends on nothing the page walk reads), as the B operand:
+    // lane (c, j) holds head j's dims of k-chunk c
+    const float *qrow = q + ((size_t)m * Hq + qh0 + (j < G ? j : 0)) * HD;
+    float4 qv[S];
+#pragma unroll
+    for (int st = 0; st < S; ++st) {
+      const int base = 8 * (4 * (st >> 1) + c) + 4 * (st & 1);
+      qv[st] = j < G ? *(const float4 *)(qrow + base) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     // page ids of this wave's pages (wave-uniform)
     const int32_t *ptab = page_table + (size_t)lane_of_row[m] * max_pages + (j0 + wbase) / 16;
     int pg[NT];
@@ -1401,15 +1406,11 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(
         else __builtin_memset(&vr[T][r], 0, sizeof(vrow_t));
       }
     }
-    // q as the B operand (after the K/V loads are in flight): lane (c, j)
-    // holds head j's dims of k-chunk c
+    // q split into f16 hi + lo (after the K/V loads are in flight)
     h4 qhi[S], qlo[S];
-    const float *qrow = q + ((size_t)m * Hq + qh0 + (j < G ? j : 0)) * HD;
 #pragma unroll
     for (int st = 0; st < S; ++st) {
-      const int base = 8 * (4 * (st >> 1) + c) + 4 * (st & 1);
-      const float4 qv = j < G ? *(const float4 *)(qrow + base) : make_float4(0.f, 0.f, 0.f, 0.f);
-      const float qa[4] = {qv.x, qv.y, qv.z, qv.w};
+      const float qa[4] = {qv[st].x, qv[st].y, qv[st].z, qv[st].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const _Float16 hv = (_Float16)qa[e];
@@ -1438,8 +1439,7 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(
         mx = fmaxf(mx, sc[T][r]);
       }
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = xor32_max(xor16_max(mx));
 #pragma unroll
     for (int T = 0; T < NT; ++T)
 #pragma unroll
@@ -1448,8 +1448,7 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(
         sc[T][r] = p;
         sum += p;
       }
-    sum += __shfl_xor(sum, 16);
-    sum += __shfl_xor(sum, 32);
+    sum = xor32_add(xor16_add(sum));
     // P.V: A = P[head][pos 4c + r] (this lane's own registers), B = V
 #pragma unroll
     for (int T = 0; T < NT; ++T)
@@ -1759,8 +1758,7 @@ __global__ __launch_bounds__(64 * kMaxGroup) void attn_prefill_kernel(
       sv[r] = kpos <= qpos ? acc[r] * scale : -INFINITY;
       pm = fmaxf(pm, sv[r]);
     }
-    pm = fmaxf(pm, __shfl_xor(pm, 16));
-    pm = fmaxf(pm, __shfl_xor(pm, 32));
+    pm = xor32_max(xor16_max(pm));
     const float mnew = fmaxf(mx, pm);  // finite: key 0 is in every row's range
     const float alpha = expf(mx - mnew);
     h4 phi, plo;
@@ -1773,8 +1771,7 @@ __global__ __launch_bounds__(64 * kMaxGroup) void attn_prefill_kernel(
       phi[r] = hv;
       plo[r] = (_Float16)(pv - (float)hv);
     }
-    ps += __shfl_xor(ps, 16);
-    ps += __shfl_xor(ps, 32);
+    ps = xor32_add(xor16_add(ps));
     sum = sum * alpha + ps;
     mx = mnew;
     // O rows are rows 4c + r: their factors live in lanes 4c + r
