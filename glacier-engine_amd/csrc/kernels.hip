@@ -837,12 +837,15 @@ static bool gemv_shape(GemvArgs &a, GemvShape &p) {
     p.lds_bytes = std::max(planes_bytes(a.K / 32, a.M, a.D) + a.M * 4, red);
   }
   if (a.x_in && (a.M <= 2 || dot4_rows_ok(a, p))) {
-    // input mode: every workgroup quantises the whole input row, so fewer,
-    // wider workgroups (8 waves; the K split only for short row counts)
-    // measured faster on the 7B QKV and gate/up shapes
+    // input mode: every workgroup quantises the whole input row, so fewer
+    // workgroups than the plane-reading shapes: 8 waves with the K split for
+    // short row counts (7B QKV), whole K per wave for tall ones, in
+    // workgroups of 4 row blocks for one input row (7B gate/up: 18.7 us
+    // against 20.4 with 8 row blocks) and 8 for more (22.7 against 23.4
+    // at two rows)
     const int NB = a.N / 16, KQ = a.K / 128;
     p.ksplit = NB >= 1024 ? 1 : std::max(1, std::min(4, KQ / 4));
-    p.rb = 8 / p.ksplit;
+    p.rb = NB >= 1024 && a.M == 1 ? 4 : 8 / p.ksplit;
     p.waves = p.ksplit * p.rb;
     p.grid = (NB + p.rb - 1) / p.rb;
     const size_t red = (size_t)p.waves * MT * 4 * 64 * sizeof(float);
