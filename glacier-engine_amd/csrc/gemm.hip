@@ -279,7 +279,7 @@ __global__ __launch_bounds__(256, kRB == 4 ? 2 : kRB == 2 ? 4 : 5) void gemm_ker
 #pragma unroll 1
     for (int i = 0; i < MT * 4; ++i) {
       const float tot = park[i * 256];
-      const float partner = paired ? __shfl_xor(tot, 8) : 0.0f;
+      const float partner = paired ? row_xor8(tot) : 0.0f;
       const int m = m0 + 16 * (i >> 2) + 4 * c + (i & 3);
       if (m < p.M && nb < NB)
         store_output(p, p.epi, nb, n_local, m, tot, partner, epi_load(p, p.epi, nb, n_local, m));

@@ -101,6 +101,41 @@ static __device__ __forceinline__ float xor32_max(float v) {
   return fmaxf(__uint_as_float(r.x), __uint_as_float(r.y));
 }
 
+// DPP lane exchanges inside a 16-lane row (no LDS round trip): the value of
+// lane ^ 8 (a rotation by 8 within the row), and of lane ^ 1 / lane ^ 2
+// (quad permutations [1, 0, 3, 2] / [2, 3, 0, 1]).
+static __device__ __forceinline__ float row_xor8(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, false));
+}
+static __device__ __forceinline__ float quad_xor1(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+static __device__ __forceinline__ float quad_xor2(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
+static __device__ __forceinline__ int quad_xor1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
+static __device__ __forceinline__ int quad_xor2(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false); }
+// Sum over the 16 lanes of each row by rotations 8, 4, 2, 1: every lane
+// gets the row's sum, each in its own (fixed) association order, so a
+// caller that needs one deterministic value reads it from one lane.
+static __device__ __forceinline__ float row16_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x122, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x121, 0xF, 0xF, false));
+  return v;
+}
+// Maximum over the whole wave (exact: every lane gets it).
+static __device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x122, 0xF, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x121, 0xF, 0xF, false)));
+  return xor32_max(xor16_max(v));
+}
+// Sum over the whole wave (lane 0's value is the deterministic one).
+static __device__ __forceinline__ float wave_sum(float v) { return xor32_add(xor16_add(row16_sum(v))); }
+
 // Reductions over each 32-lane half of a wave (every lane of the half gets
 // the result): DPP row rotations by 8, 4, 2, 1 combine the 16 lanes of a row,
 // then a 16-lane swap of the value with itself puts the even row's and the

@@ -117,7 +117,7 @@ __global__ __launch_bounds__(256) void prep_act_kernel(const void *x, int x_bf16
         ss = fmaf(v, v, ss);
       }
     }
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    ss = wave_sum(ss);
     if ((t & 63) == 0) red[t >> 6] = ss;
     __syncthreads();
     if (t == 0) {
@@ -334,7 +334,7 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
         float ss = 0.0f;
 #pragma unroll
         for (int u = 0; u < PU; ++u) ss += lane + 64 * u < a.in_ss_count ? ssv[u] : 0.0f;
-        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+        ss = wave_sum(ss);
         if (lane == 0) sinv[m] = 1.0f / sqrtf(ss / (float)a.K + a.in_eps);
       }
     }
@@ -358,8 +358,8 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
         float amax = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-        amax = fmaxf(amax, __shfl_xor(amax, 1));
-        amax = fmaxf(amax, __shfl_xor(amax, 2));
+        amax = fmaxf(amax, quad_xor1(amax));
+        amax = fmaxf(amax, quad_xor2(amax));
         const float scale = amax / 127.0f;
         const float inv_s = scale == 0.0f ? 0.0f : 1.0f / scale;
         uint64_t packed[D];
@@ -387,8 +387,8 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
           }
           csum += comb;
         }
-        csum += __shfl_xor(csum, 1);
-        csum += __shfl_xor(csum, 2);
+        csum += quad_xor1(csum);
+        csum += quad_xor2(csum);
         if (valid) {
           const int e = c8 * 8, m = e / a.K, g = (e % a.K) >> 5, part = (e >> 3) & 3;
 #pragma unroll
@@ -703,7 +703,7 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
       const int m = mt * 16 + c * 4 + r;
       const float tot = acc[mt][r];
       // partner row (n_local ^ 8) lives in lane ^ 8 with the same (c, r)
-      const float partner = paired ? __shfl_xor(tot, 8) : 0.0f;
+      const float partner = paired ? row_xor8(tot) : 0.0f;
       if (resid_ss) {
         // residual output y = resid + tot, and this wave's sum of y^2 of row m
         float y = 0.0f;
@@ -712,9 +712,8 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
           y = e.resid + tot;
           a.y[(size_t)m * a.N + nb * 16 + n_local] = y;
         }
-        float sq = y * y;
-#pragma unroll
-        for (int o = 1; o < 16; o <<= 1) sq += __shfl_xor(sq, o);
+        // the row of 16 lanes (c, n), n = 0..15, summed; lane n = 0 stores
+        const float sq = row16_sum(y * y);
         if (n_local == 0 && m < M) sspart[wave * M + m] = sq;
         continue;
       }
@@ -988,7 +987,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *x, const floa
   __shared__ float red[8];
   float ss = 0.0f;
   for (int i = t; i < dim; i += 256) ss = fmaf(xr[i], xr[i], ss);
-  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  ss = wave_sum(ss);
   if ((t & 63) == 0) red[t >> 6] = ss;
   __syncthreads();
   if (t == 0) red[4] = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)dim + eps);
@@ -1023,7 +1022,7 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const float *table, co
   if (!ss_out) return;
   __shared__ float red[4];
   float sq = v * v;
-  for (int o = 32; o > 0; o >>= 1) sq += __shfl_xor(sq, o);
+  sq = wave_sum(sq);
   if ((t & 63) == 0) red[t >> 6] = sq;
   __syncthreads();
   if (t == 0) ss_out[(size_t)m * gridDim.x + blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
@@ -1544,7 +1543,7 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine2_kernel(
     lc[u] = c < nch ? rec0[(size_t)c * (2 + HD) + 1] : 0.0f;
     mx = fmaxf(mx, mc[u]);
   }
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  mx = wave_max(mx);
   if ((t & 63) == 0) redm[t >> 6] = mx;
   __syncthreads();
   float M = redm[0];
@@ -1560,7 +1559,7 @@ __global__ __launch_bounds__(kCombineThreads) void attn_combine2_kernel(
       lp = fmaf(lc[u], fc, lp);
     }
   }
-  for (int o = 32; o > 0; o >>= 1) lp += __shfl_xor(lp, o);
+  lp = wave_sum(lp);
   if ((t & 63) == 0) redl[t >> 6] = lp;
   __syncthreads();
   float L = 0.0f;
