@@ -94,9 +94,9 @@ __device__ __forceinline__ void act_store(unsigned char *buf, const ActRegs<D, B
 }
 
 // kRB: 16-row weight blocks per wave (1, 2 or 4; the workgroup covers 4 kRB);
-// BM: activation rows per workgroup (32 or 64). With ks_count > 1 the K
-// quads are split over blockIdx.y and each split writes its partial sums to
-// part [ks_count][M][N] (no epilogue; splitk_reduce_kernel finishes).
+// BM: activation rows per workgroup (32 or 64). The K quads are split over
+// blockIdx.y (ks_count splits); with part set each split writes its partial
+// sums to part [ks_count][M][N] (no epilogue; a finishing kernel runs it).
 template <int D, int kRB, int BM>
 __global__ __launch_bounds__(256, kRB == 4 ? 2 : kRB == 2 ? 4 : 5) void gemm_kernel(GemvArgs p, int m_tiles,
                                                                      int ks_count, float *part) {
@@ -247,8 +247,9 @@ __global__ __launch_bounds__(256, kRB == 4 ? 2 : kRB == 2 ? 4 : 5) void gemm_ker
   }
 
   // Lane (c, n) holds rows m0 + 16 mt + 4c + r of column 16 nb + n.
-  if (ks_count > 1) {
-    // split K: this split's partial sums, part[split][m][n]
+  if (part) {
+    // split K (or a finishing pass that emits planes): this split's partial
+    // sums, part[split][m][n]
     float *dst = part + (size_t)blockIdx.y * p.M * p.N;
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb)
@@ -307,6 +308,94 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemvArgs p, int ks_c
   store_output(p, p.epi, nb, n_local, m, tot, partner, epi_load(p, p.epi, nb, n_local, m));
 }
 
+// Split-K finish of the gate/up GEMM that also emits the down projection's
+// digit planes: one thread per SwiGLU output (m, o), o < N / 2, whose gate
+// and up rows are device rows 16 (o / 8) + o % 8 and that + 8 (the
+// interleaved layout); every split sum in a fixed order, then the epilogue's
+// silu(g) * u. A half-wave holds 32 consecutive outputs of one row, which
+// is one quantisation group of the planes.
+template <int KS, int D>
+__global__ __launch_bounds__(256) void splitk_swiglu_emit_kernel(GemvArgs p, const float *part) {
+  const int No = p.N >> 1;
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t MN = (size_t)p.M * p.N;
+  if (idx >= (size_t)p.M * No) return;  // whole half-waves: No is a multiple of 32
+  const int m = (int)(idx / No), o = (int)(idx % No);
+  const size_t gi = (size_t)m * p.N + ((o >> 3) << 4) + (o & 7), ui = gi + 8;
+  float gv[KS], uv[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    gv[s] = part[s * MN + gi];
+    uv[s] = part[s * MN + ui];
+  }
+  float g = gv[0], u = uv[0];
+#pragma unroll
+  for (int s = 1; s < KS; ++s) {
+    g += gv[s];
+    u += uv[s];
+  }
+  const float v = silu_mul(g, u);
+  if (p.y) p.y[(size_t)m * No + o] = v;
+  quantize_group<D>(v, o & 31, o >> 5, m, p.M, p.out_q, p.out_meta);
+}
+
+// Split-K finish of a residual GEMM (O, down) that also produces the next
+// projection's input: y = resid + (fixed-order sum of the splits) is
+// written, then the row's RMSNorm with emit_norm_w (kernels.zig:141-220:
+// y / sqrt(mean(y^2) + eps) * w) and the group quantiser give the digit
+// planes prep_act_kernel would make from y. One 1024-thread workgroup per
+// row (N <= 4096, at most 4 outputs per thread, every load of the row
+// issued before the first add).
+constexpr int kEmitThreads = 1024;
+template <int KS, int D>
+__global__ __launch_bounds__(kEmitThreads) void splitk_resid_emit_kernel(GemvArgs p,
+                                                                         const float *part) {
+  constexpr int E = 4096 / kEmitThreads;
+  const int m = blockIdx.x, t = threadIdx.x, N = p.N;
+  const size_t MN = (size_t)p.M * N, row = (size_t)m * N;
+  __shared__ float red[kEmitThreads / 64 + 1];
+  float pv[KS][E], rv[E], y[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int n = min(t + kEmitThreads * e, N - 1);
+    rv[e] = p.resid[row + n];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) pv[s][e] = part[s * MN + row + n];
+  }
+  float ss = 0.0f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    float tot = pv[0][e];
+#pragma unroll
+    for (int s = 1; s < KS; ++s) tot += pv[s][e];
+    y[e] = rv[e] + tot;
+    const int n = t + kEmitThreads * e;
+    if (n < N) {
+      p.y[row + n] = y[e];
+      ss = fmaf(y[e], y[e], ss);
+    }
+  }
+  ss = wave_sum(ss);
+  if ((t & 63) == 0) red[t >> 6] = ss;
+  __syncthreads();
+  if (t == 0) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kEmitThreads / 64; ++w) sum += red[w];
+    red[kEmitThreads / 64] = 1.0f / sqrtf(sum / (float)N + p.in_eps);
+  }
+  __syncthreads();
+  const float inv = red[kEmitThreads / 64];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int n = t + kEmitThreads * e;
+    if (n < N) {  // whole half-waves: N is a multiple of 32
+      const float v = (y[e] * inv) * p.emit_norm_w[n];
+      quantize_group<D>(v, t & 31, n >> 5, m, p.M, p.out_q, p.out_meta);
+    }
+  }
+}
+
 }  // namespace
 
 GemmShape plan_gemm(int N, int M, int K, int D, size_t ws_floats) {
@@ -345,11 +434,13 @@ size_t gemm_splitk_floats(int N, int M, int K, int D) {
   return s.ks > 1 ? (size_t)s.ks * M * N : 0;
 }
 
-hipError_t launch_gemm(const GemvArgs &a, hipStream_t st) {
+// The launch shape of these arguments (plan_gemm plus the tuning
+// overrides); false when they are invalid.
+static bool gemm_plan(const GemvArgs &a, GemmShape &s) {
   if (a.N % 16 || a.K % 128 || a.M < 1 || !a.act_q || !a.act_meta || (a.D != 1 && a.D != 3))
-    return hipErrorInvalidValue;
-  if (a.out_q || a.ss_out || a.arg_parts || a.x_in) return hipErrorInvalidValue;  // GEMV-only
-  GemmShape s = plan_gemm(a.N, a.M, a.K, a.D, a.splitk_ws ? a.splitk_ws_floats : 0);
+    return false;
+  if (a.ss_out || a.arg_parts || a.x_in) return false;  // GEMV-only
+  s = plan_gemm(a.N, a.M, a.K, a.D, a.splitk_ws ? a.splitk_ws_floats : 0);
   if (a.rb_override == 1 || a.rb_override == 2 || a.rb_override == 4) {  // tuning
     s.nt = 4 * a.rb_override;
     s.n_tiles = (a.N / 16 + s.nt - 1) / s.nt;
@@ -358,11 +449,30 @@ hipError_t launch_gemm(const GemvArgs &a, hipStream_t st) {
   if (a.ksplit_override > 0) {  // tuning: K splits (needs the workspace)
     if ((size_t)a.ksplit_override * a.M * a.N > (a.splitk_ws ? a.splitk_ws_floats : 0) &&
         a.ksplit_override > 1)
-      return hipErrorInvalidValue;
+      return false;
     s.ks = std::min(a.ksplit_override, a.K / 128);
   }
+  return true;
+}
+
+bool gemm_emit_ok(const GemvArgs &a) {
+  GemmShape s;
+  if (!a.out_q || !a.out_meta || (a.out_D != 1 && a.out_D != 3) || !gemm_plan(a, s)) return false;
+  if (s.ks != 1 && s.ks != 2 && s.ks != 4 && s.ks != 8 && s.ks != 16) return false;
+  if (!a.splitk_ws || (size_t)s.ks * a.M * a.N > a.splitk_ws_floats) return false;
+  if (a.epi == EPI_SWIGLU) return (a.N / 2) % 32 == 0;
+  if (a.epi == EPI_RESID)
+    return a.emit_norm_w && a.resid && a.y && a.N % 32 == 0 && a.N <= 4096;
+  return false;
+}
+
+hipError_t launch_gemm(const GemvArgs &a, hipStream_t st) {
+  GemmShape s;
+  if (!gemm_plan(a, s)) return hipErrorInvalidValue;
+  const bool emit = a.out_q != nullptr;
+  if (emit && !gemm_emit_ok(a)) return hipErrorInvalidValue;
   const dim3 grid(s.grid, s.ks), block(256);
-  float *part = s.ks > 1 ? a.splitk_ws : nullptr;
+  float *part = s.ks > 1 || emit ? a.splitk_ws : nullptr;
 #define GK_GEMM(DD, RB, BM) \
   hipLaunchKernelGGL((gemm_kernel<DD, RB, BM>), grid, block, 0, st, a, s.m_tiles, s.ks, part)
 #define GK_GEMM_BM(DD, RB) \
@@ -377,7 +487,35 @@ hipError_t launch_gemm(const GemvArgs &a, hipStream_t st) {
 #undef GK_GEMM_BM
 #undef GK_GEMM
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || s.ks == 1) return e;
+  if (e != hipSuccess) return e;
+  if (emit) {
+    const float *pc = part;
+    const unsigned sw_grid = (unsigned)(((size_t)a.M * (a.N / 2) + 255) / 256);
+#define GK_EMIT(KS, DD)                                                                      \
+  do {                                                                                      \
+    if (a.epi == EPI_SWIGLU)                                                                \
+      hipLaunchKernelGGL((splitk_swiglu_emit_kernel<KS, DD>), dim3(sw_grid), dim3(256), 0, \
+                         st, a, pc);                                                        \
+    else                                                                                    \
+      hipLaunchKernelGGL((splitk_resid_emit_kernel<KS, DD>), dim3(a.M), dim3(kEmitThreads), \
+                         0, st, a, pc);                                                     \
+  } while (0)
+#define GK_EMIT_D(KS)                                  \
+  do {                                                \
+    if (a.out_D == 1) GK_EMIT(KS, 1); else GK_EMIT(KS, 3); \
+  } while (0)
+    switch (s.ks) {
+      case 1: GK_EMIT_D(1); break;
+      case 2: GK_EMIT_D(2); break;
+      case 4: GK_EMIT_D(4); break;
+      case 8: GK_EMIT_D(8); break;
+      default: GK_EMIT_D(16); break;
+    }
+#undef GK_EMIT_D
+#undef GK_EMIT
+    return hipGetLastError();
+  }
+  if (s.ks == 1) return e;
   const size_t MN = (size_t)a.M * a.N;
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, st, a,
                      s.ks, (const float *)part);

@@ -119,6 +119,11 @@ struct GemvArgs {
   // GEMM split-K workspace (floats); null: no K split
   float *splitk_ws;
   size_t splitk_ws_floats;
+  // GEMM with out_q set (launch_gemm, when gemm_emit_ok): the finishing
+  // pass also writes the next projection's digit planes [G][out_D][M][32] +
+  // meta. EPI_SWIGLU: the SwiGLU outputs (width N/2); EPI_RESID: y after
+  // the RMSNorm with these weights and in_eps (y itself is written too).
+  const float *emit_norm_w;
 };
 
 // Launch shape of one GEMV: RB row blocks per workgroup, KS waves per row
@@ -160,6 +165,10 @@ struct GemmShape {
 };
 GemmShape plan_gemm(int N, int M, int K, int D, size_t ws_floats);
 // Workspace floats the GEMM would use for these sizes with no limit.
+// True when launch_gemm can emit planes for these arguments (out_q set):
+// SwiGLU outputs or residual rows of at most 4096 in whole 32-wide groups,
+// a K split of 1, 2, 4, 8 or 16 and a workspace for its partial sums.
+bool gemm_emit_ok(const GemvArgs &a);
 size_t gemm_splitk_floats(int N, int M, int K, int D);
 hipError_t launch_gemm(const GemvArgs &a, hipStream_t st);
 

@@ -36,41 +36,6 @@ static __device__ __forceinline__ float load_x(const void *x, int bf16, size_t i
   return ((const float *)x)[i];
 }
 
-// Converts the 32-element group held by a 32-lane half-wave (one value per
-// lane, hl = lane within the half-wave) into D digit bytes per lane and the
-// group's meta. q layout [G][D][M][32], meta [G][M].
-template <int D>
-static __device__ __forceinline__ void quantize_group(float v, int hl, int g, int m, int M,
-                                                      int8_t *act_q, ActMeta *meta) {
-  const float amax = half_wave_max(fabsf(v));
-  const float scale = amax / 127.0f;
-  const float inv_s = scale == 0.0f ? 0.0f : 1.0f / scale;
-  const float y = v * inv_s;
-  float q0f = roundf(y);
-  q0f = fminf(fmaxf(q0f, -127.0f), 127.0f);
-  int qd[3] = {(int)q0f, 0, 0};
-  if (D == 3) {
-    const float r1 = (y - q0f) * 128.0f;
-    const float q1f = roundf(r1);
-    const float r2 = (r1 - q1f) * 128.0f;
-    qd[1] = (int)q1f;
-    qd[2] = (int)roundf(r2);
-  }
-  int comb = 0;  // 128-adic combination of the digits; one reduction gives sum_d 128^(D-1-d) sum q_d
-#pragma unroll
-  for (int d = 0; d < D; ++d) {
-    act_q[(((size_t)g * D + d) * M + m) * 32 + hl] = (int8_t)qd[d];
-    comb = comb * 128 + qd[d];
-  }
-  const int sum = half_wave_sum(comb);
-  if (hl == 0) {
-    ActMeta mm;
-    mm.scale = D == 3 ? scale * (1.0f / 16384.0f) : scale;
-    mm.corr = 7 * sum;
-    meta[(size_t)g * M + m] = mm;
-  }
-}
-
 // Quantises one 32-value group (one value per lane of a half-wave) into
 // the planes pd describes, when it is set.
 static __device__ __forceinline__ void emit_group(const PlanesDst &pd, float v, int hl, int g,

@@ -383,7 +383,8 @@ struct ProjOut {
   const float *resid = nullptr;
   const float *bias = nullptr;
   const gk::QkvArgs *qkv = nullptr;
-  gk::PlanesDst emit{nullptr, nullptr, 1};  // EPI_SWIGLU: next projection's planes
+  gk::PlanesDst emit{nullptr, nullptr, 1};  // next projection's planes (SwiGLU; GEMM: residual)
+  const float *emit_norm_w = nullptr;       // GEMM residual emission: the next RMSNorm
   float *ss_out = nullptr;                  // EPI_RESID: partial sums of y^2
   gk::ArgPartial *arg_parts = nullptr;      // EPI_PLAIN: fused greedy head
   const uint64_t *arg_words = nullptr;
@@ -409,6 +410,7 @@ gk::GemvArgs proj_args(glacier_hip_session *s, glacier_hip_int4_weight *w, int D
   a.out_q = out.emit.q;
   a.out_meta = out.emit.meta;
   a.out_D = out.emit.D;
+  a.emit_norm_w = out.emit_norm_w;
   a.ss_out = out.ss_out;
   a.arg_parts = out.arg_parts;
   a.arg_words = out.arg_words;
@@ -456,8 +458,9 @@ int proj_grid(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, int row
 hipError_t run_proj(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, int rows, int epi,
                     const ProjIn &in, const ProjOut &out, hipStream_t st) {
   const bool decode = rows <= gk::kGemvMaxRows;
-  // partial sums, plane emission and the fused head are GEMV-only
-  if (!decode && (out.emit.q || out.ss_out || out.arg_parts)) return hipErrorInvalidValue;
+  // partial sums and the fused head are GEMV-only (the GEMM emits planes
+  // when gemm_emit_ok says so)
+  if (!decode && (out.ss_out || out.arg_parts)) return hipErrorInvalidValue;
   gk::GemvArgs a;
   if (input_mode_args(s, w, D, rows, epi, in, out, &a)) return gk::launch_gemv(a, st);
   a = proj_args(s, w, D, rows, epi, in, out);
@@ -471,6 +474,19 @@ hipError_t run_proj(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, i
   return decode ? gk::launch_gemv(a, st) : gk::launch_gemm(a, st);
 }
 
+// Whether a GEMM-sized projection can finish by emitting the next
+// projection's planes (its inputs come from planes or the conversion kernel,
+// both into act_q, so that is what the check assumes).
+bool gemm_emit_ok(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, int rows, int epi,
+                  const ProjOut &out) {
+  if (rows <= gk::kGemvMaxRows) return false;
+  ProjIn in;
+  in.planes_q = s->act_q;
+  in.planes_m = s->act_meta;
+  const gk::GemvArgs a = proj_args(s, w, D, rows, epi, in, out);
+  return gk::gemm_emit_ok(a);
+}
+
 // Embedding gather and every decoder layer for `rows` activation rows
 // (generate.zig:1511-1967 per row; K/V rows land in the rows' pages).
 //
@@ -481,8 +497,10 @@ hipError_t run_proj(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, i
 // (QKV, gate/up) finishes its deferred norm while it quantises its input in
 // LDS (up to kInputModeRows rows; more rows convert with the separate
 // kernel); attention writes the O projection's planes and gate/up the down
-// projection's. Longer row sets (prefill chunks) convert each input with a
-// separate kernel.
+// projection's. Longer row sets run the GEMM; where its split-K partial
+// sums fit the workspace the finishing pass of O and down also writes the
+// next RMSNorm'd projection's planes and that of gate/up the down
+// projection's, otherwise each input is converted by a separate kernel.
 hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, hipStream_t st) {
   glacier_hip_model *m = s->model;
   const auto &c = m->cfg;
@@ -507,6 +525,7 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
   hipError_t e = gk::launch_gather_rows(m->embed, rp.tokens, rows, D, s->x_res, st, ss);
   if (e != hipSuccess) return e;
   int ss_count = ss ? gk::gather_ss_parts(D) : 0;  // partial sums behind x_res
+  bool x_planes = false;  // GEMM path: the previous down emitted this layer's QKV planes
   for (uint32_t l = 0; l < c.num_layers; ++l) {
     const LayerDev &L = m->layers[l];
     q.layer = (int)l;
@@ -516,10 +535,15 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
     const int Dd = layer_D(s, L.down->out_f, L.down->in_f);
     // RMSNorm -> QKV (+RoPE, KV row write into the lane's page)
     ProjIn qin;
-    qin.x = s->x_res;
-    qin.norm_w = L.in_norm;
-    qin.ss = ss;
-    qin.ss_count = ss_count;
+    if (x_planes) {
+      qin.planes_q = s->act_q;
+      qin.planes_m = s->act_meta;
+    } else {
+      qin.x = s->x_res;
+      qin.norm_w = L.in_norm;
+      qin.ss = ss;
+      qin.ss_count = ss_count;
+    }
     ProjOut qout;
     qout.bias = L.qkv_bias;
     qout.qkv = &q;
@@ -561,19 +585,39 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
       ss_count = proj_grid(s, L.o, Do, rows, gk::EPI_RESID, oin, oout);
       if (ss_count <= 0) return hipErrorInvalidValue;
     }
+    if (!chain) {  // GEMM: gate/up's planes from O's finishing pass
+      oout.emit = gk::PlanesDst{s->act_q, s->act_meta, Dg};
+      oout.emit_norm_w = L.post_norm;
+      if (!gemm_emit_ok(s, L.o, Do, rows, gk::EPI_RESID, oout)) {
+        oout.emit = gk::PlanesDst{nullptr, nullptr, 1};
+        oout.emit_norm_w = nullptr;
+      }
+    }
     e = run_proj(s, L.o, Do, rows, gk::EPI_RESID, oin, oout, st);
     if (e != hipSuccess) return e;
     // gate/up + SwiGLU (decode sizes: emitted straight into down's planes)
     ProjIn gin;
-    gin.x = s->h;
-    gin.norm_w = L.post_norm;
-    gin.ss = ss;
-    gin.ss_count = ss_count;
+    if (oout.emit.q) {
+      gin.planes_q = s->act_q;
+      gin.planes_m = s->act_meta;
+    } else {
+      gin.x = s->h;
+      gin.norm_w = L.post_norm;
+      gin.ss = ss;
+      gin.ss_count = ss_count;
+    }
     ProjOut gout;
-    if (chain)
+    if (chain) {
       gout.emit = gk::PlanesDst{s->act_q2, s->act_meta2, Dd};
-    else
-      gout.y = s->act;
+    } else {
+      // GEMM: down's planes from gate/up's finishing pass (into act_q, which
+      // gate/up has finished reading by then), else the SwiGLU rows
+      gout.emit = gk::PlanesDst{s->act_q, s->act_meta, Dd};
+      if (!gemm_emit_ok(s, L.gu, Dg, rows, gk::EPI_SWIGLU, gout)) {
+        gout.emit = gk::PlanesDst{nullptr, nullptr, 1};
+        gout.y = s->act;
+      }
+    }
     e = run_proj(s, L.gu, Dg, rows, gk::EPI_SWIGLU, gin, gout, st);
     if (e != hipSuccess) return e;
     // down + residual (chain: partial sums of x_res for the next norm)
@@ -584,14 +628,25 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
     const bool last = l + 1 == c.num_layers;  // the LM head converts x_res itself
     dout.ss_out = last ? nullptr : ss;
     if (gout.emit.q) {
-      din.planes_q = s->act_q2;
-      din.planes_m = s->act_meta2;
+      din.planes_q = gout.emit.q;
+      din.planes_m = gout.emit.meta;
     } else {
       din.x = s->act;
     }
     if (ss && !last) {
       ss_count = proj_grid(s, L.down, Dd, rows, gk::EPI_RESID, din, dout);
       if (ss_count <= 0) return hipErrorInvalidValue;
+    }
+    x_planes = false;
+    if (!chain && !last) {  // GEMM: the next layer's QKV planes from down's finishing pass
+      const LayerDev &N = m->layers[l + 1];
+      dout.emit = gk::PlanesDst{s->act_q, s->act_meta, layer_D(s, N.qkv->out_f, N.qkv->in_f)};
+      dout.emit_norm_w = N.in_norm;
+      x_planes = gemm_emit_ok(s, L.down, Dd, rows, gk::EPI_RESID, dout);
+      if (!x_planes) {
+        dout.emit = gk::PlanesDst{nullptr, nullptr, 1};
+        dout.emit_norm_w = nullptr;
+      }
     }
     e = run_proj(s, L.down, Dd, rows, gk::EPI_RESID, din, dout, st);
     if (e != hipSuccess) return e;
@@ -1077,8 +1132,12 @@ glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
     for (uint32_t rows : {(uint32_t)gk::kGemvMaxRows + 1, 24u, 32u, M})
       if (rows > (uint32_t)gk::kGemvMaxRows && rows <= M)
         for (const auto *w : ws)
-          for (int D : {1, 3})
+          for (int D : {1, 3}) {
             need = std::max(need, gk::gemm_splitk_floats((int)w->out_f, (int)rows, (int)w->in_f, D));
+            // plane emission from the finishing pass needs the partial sums
+            // even without a K split (decode lanes up to 32)
+            if (rows <= 32) need = std::max(need, (size_t)rows * w->out_f);
+          }
     s->splitk_floats = std::min<size_t>(need, 16u << 20);
     if (s->splitk_floats) A((void **)&s->splitk_ws, s->splitk_floats * sizeof(float));
   }
