@@ -343,37 +343,44 @@ __global__ __launch_bounds__(256) void splitk_swiglu_emit_kernel(GemvArgs p, con
 // projection's input: y = resid + (fixed-order sum of the splits) is
 // written, then the row's RMSNorm with emit_norm_w (kernels.zig:141-220:
 // y / sqrt(mean(y^2) + eps) * w) and the group quantiser give the digit
-// planes prep_act_kernel would make from y. One 1024-thread workgroup per
-// row (N <= 4096, at most 4 outputs per thread, every load of the row
-// issued before the first add).
-constexpr int kEmitThreads = 1024;
+// planes prep_act_kernel would make from y. One workgroup per row; each
+// thread owns 8 consecutive outputs (two 16-byte loads per split, all of a
+// thread's loads issued before the first add), so 4 threads (one quad) hold
+// a 32-wide group and reduce it with quad DPP exchanges.
+constexpr int kEmitThreads = 512;  // rows of up to 4096
 template <int KS, int D>
 __global__ __launch_bounds__(kEmitThreads) void splitk_resid_emit_kernel(GemvArgs p,
                                                                          const float *part) {
-  constexpr int E = 4096 / kEmitThreads;
   const int m = blockIdx.x, t = threadIdx.x, N = p.N;
   const size_t MN = (size_t)p.M * N, row = (size_t)m * N;
+  const bool act = 8 * t < N;  // N is a multiple of 32: whole quads
+  const int n0 = act ? 8 * t : 0;
   __shared__ float red[kEmitThreads / 64 + 1];
-  float pv[KS][E], rv[E], y[E];
+  float4 pv[KS][2], rv[2], wv[2];
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int n = min(t + kEmitThreads * e, N - 1);
-    rv[e] = p.resid[row + n];
+  for (int h = 0; h < 2; ++h) {
+    rv[h] = *(const float4 *)(p.resid + row + n0 + 4 * h);
+    wv[h] = *(const float4 *)(p.emit_norm_w + n0 + 4 * h);
 #pragma unroll
-    for (int s = 0; s < KS; ++s) pv[s][e] = part[s * MN + row + n];
+    for (int s = 0; s < KS; ++s) pv[s][h] = *(const float4 *)(part + s * MN + row + n0 + 4 * h);
   }
+  float y[8], w8[8];
   float ss = 0.0f;
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    float tot = pv[0][e];
+  for (int i = 0; i < 8; ++i) {
+    const int h = i >> 2, e = i & 3;
+    float tot = pv[0][h][e];
 #pragma unroll
-    for (int s = 1; s < KS; ++s) tot += pv[s][e];
-    y[e] = rv[e] + tot;
-    const int n = t + kEmitThreads * e;
-    if (n < N) {
-      p.y[row + n] = y[e];
-      ss = fmaf(y[e], y[e], ss);
-    }
+    for (int s = 1; s < KS; ++s) tot += pv[s][h][e];
+    y[i] = rv[h][e] + tot;
+    w8[i] = wv[h][e];
+    ss = fmaf(y[i], y[i], ss);
+  }
+  if (act) {
+    *(float4 *)(p.y + row + n0) = make_float4(y[0], y[1], y[2], y[3]);
+    *(float4 *)(p.y + row + n0 + 4) = make_float4(y[4], y[5], y[6], y[7]);
+  } else {
+    ss = 0.0f;
   }
   ss = wave_sum(ss);
   if ((t & 63) == 0) red[t >> 6] = ss;
@@ -386,12 +393,56 @@ __global__ __launch_bounds__(kEmitThreads) void splitk_resid_emit_kernel(GemvArg
   }
   __syncthreads();
   const float inv = red[kEmitThreads / 64];
+  // group quantiser (int4_matmul.zig:380-398), the same arithmetic as
+  // quantize_group, over the quad's 32 values
+  float v[8];
+  float amax = 0.0f;
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const int n = t + kEmitThreads * e;
-    if (n < N) {  // whole half-waves: N is a multiple of 32
-      const float v = (y[e] * inv) * p.emit_norm_w[n];
-      quantize_group<D>(v, t & 31, n >> 5, m, p.M, p.out_q, p.out_meta);
+  for (int i = 0; i < 8; ++i) {
+    v[i] = (y[i] * inv) * w8[i];
+    amax = fmaxf(amax, fabsf(v[i]));
+  }
+  amax = fmaxf(amax, quad_xor1(amax));
+  amax = fmaxf(amax, quad_xor2(amax));
+  const float scale = amax / 127.0f;
+  const float inv_s = scale == 0.0f ? 0.0f : 1.0f / scale;
+  uint64_t packed[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) packed[d] = 0;
+  int csum = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float yq = v[i] * inv_s;
+    float q0f = roundf(yq);
+    q0f = fminf(fmaxf(q0f, -127.0f), 127.0f);
+    int qd[3] = {(int)q0f, 0, 0};
+    if (D == 3) {
+      const float r1 = (yq - q0f) * 128.0f;
+      const float q1f = roundf(r1);
+      const float r2 = (r1 - q1f) * 128.0f;
+      qd[1] = (int)q1f;
+      qd[2] = (int)roundf(r2);
+    }
+    int comb = 0;
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      packed[d] |= (uint64_t)(uint8_t)(int8_t)qd[d] << (8 * i);
+      comb = comb * 128 + qd[d];
+    }
+    csum += comb;
+  }
+  csum += quad_xor1(csum);
+  csum += quad_xor2(csum);
+  if (act) {
+    const int g = n0 >> 5, qp = (n0 >> 3) & 3;
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      *(uint64_t *)(p.out_q + (((size_t)g * D + d) * p.M + m) * 32 + qp * 8) = packed[d];
+    if (qp == 0) {
+      ActMeta mm;
+      mm.scale = D == 3 ? scale * (1.0f / 16384.0f) : scale;
+      mm.corr = 7 * csum;
+      p.out_meta[(size_t)g * p.M + m] = mm;
     }
   }
 }
@@ -462,7 +513,7 @@ bool gemm_emit_ok(const GemvArgs &a) {
   if (!a.splitk_ws || (size_t)s.ks * a.M * a.N > a.splitk_ws_floats) return false;
   if (a.epi == EPI_SWIGLU) return (a.N / 2) % 32 == 0;
   if (a.epi == EPI_RESID)
-    return a.emit_norm_w && a.resid && a.y && a.N % 32 == 0 && a.N <= 4096;
+    return a.emit_norm_w && a.resid && a.y && a.N % 32 == 0 && a.N <= 8 * kEmitThreads;
   return false;
 }
 
