@@ -291,6 +291,9 @@ __global__ __launch_bounds__(256, kRB == 4 ? 2 : kRB == 2 ? 4 : 5) void gemm_ker
 // Split-K finish: y = the fixed-order sum over splits of part[s][m][n],
 // through the same epilogue as the one-split kernel. One thread per output
 // (m, n); the SwiGLU / RoPE partner n ^ 8 is summed by the same thread.
+// KS > 0: that many splits, every load issued before the first add; KS = 0:
+// ks_count splits in a loop.
+template <int KS>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemvArgs p, int ks_count,
                                                             const float *part) {
   const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -299,12 +302,32 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemvArgs p, int ks_c
   const int m = (int)(idx / p.N), n = (int)(idx % p.N);
   const int nb = n >> 4, n_local = n & 15;
   const bool paired = p.epi == EPI_SWIGLU || p.epi == EPI_QKV;
-  const size_t pi = (size_t)m * p.N + (n ^ 8);
-  float tot = part[idx], partner = paired ? part[pi] : 0.0f;
-  for (int s = 1; s < ks_count; ++s) {
-    tot += part[s * MN + idx];
-    if (paired) partner += part[s * MN + pi];
+  // the partner of an unpaired output is itself (loaded, never used)
+  const size_t pi = paired ? (size_t)m * p.N + (n ^ 8) : idx;
+  float tot, partner;
+  if constexpr (KS > 0) {
+    float tv[KS], pv[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      tv[s] = part[s * MN + idx];
+      pv[s] = part[s * MN + pi];
+    }
+    tot = tv[0];
+    partner = pv[0];
+#pragma unroll
+    for (int s = 1; s < KS; ++s) {
+      tot += tv[s];
+      partner += pv[s];
+    }
+  } else {
+    tot = part[idx];
+    partner = part[pi];
+    for (int s = 1; s < ks_count; ++s) {
+      tot += part[s * MN + idx];
+      partner += part[s * MN + pi];
+    }
   }
+  if (!paired) partner = 0.0f;
   store_output(p, p.epi, nb, n_local, m, tot, partner, epi_load(p, p.epi, nb, n_local, m));
 }
 
@@ -568,8 +591,15 @@ hipError_t launch_gemm(const GemvArgs &a, hipStream_t st) {
   }
   if (s.ks == 1) return e;
   const size_t MN = (size_t)a.M * a.N;
-  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, st, a,
-                     s.ks, (const float *)part);
+  const dim3 rg((unsigned)((MN + 255) / 256));
+  const float *pc = part;
+  switch (s.ks) {
+    case 2: hipLaunchKernelGGL((splitk_reduce_kernel<2>), rg, dim3(256), 0, st, a, s.ks, pc); break;
+    case 4: hipLaunchKernelGGL((splitk_reduce_kernel<4>), rg, dim3(256), 0, st, a, s.ks, pc); break;
+    case 8: hipLaunchKernelGGL((splitk_reduce_kernel<8>), rg, dim3(256), 0, st, a, s.ks, pc); break;
+    case 16: hipLaunchKernelGGL((splitk_reduce_kernel<16>), rg, dim3(256), 0, st, a, s.ks, pc); break;
+    default: hipLaunchKernelGGL((splitk_reduce_kernel<0>), rg, dim3(256), 0, st, a, s.ks, pc); break;
+  }
   return hipGetLastError();
 }
 
