@@ -1,7 +1,7 @@
 // gemm.hip — K2: INT4 x int8-digit GEMM on gfx950 MFMA.
 //
-// y[M][N] = planes(x)[M][K] . W^T past 16 rows (wide decode batches, prompt
-// chunks), with the
+// y[M][N] = planes(x)[M][K] . W^T past the decode GEMV's rows (decode
+// batches of 6 or more lanes, prompt chunks), with the
 // same digit planes, tile layout and fused epilogues as the decode GEMV (K1):
 // the per-group arithmetic is the reference's Q8 dot
 // (int4_matmul.zig:365-418): an exact integer dot per 32-element group,

@@ -149,13 +149,16 @@ hipError_t launch_prep_act(const void *x, int x_bf16, const float *norm_w, float
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t st);
 
 // Row counts up to this run the decode GEMV (K1, with its fused chain
-// stages); more rows run the MFMA GEMM (K2).
-constexpr int kGemvMaxRows = 16;
+// stages); more rows run the MFMA GEMM (K2). From 6 rows on the GEMM
+// measured faster on every 7B projection (gate/up at 8 rows: 28.6 us against
+// 36.2 for the GEMV's MFMA path, at 16 rows 31.3 against 54.2); at 4 rows the
+// GEMV's batched dot4 is (27.2 against 30.0).
+constexpr int kGemvMaxRows = 5;
 
-// MFMA GEMM (K2) for more than 16 activation rows: same arguments and
-// epilogues as launch_gemv without the GEMV-only stages (plane emission,
-// partial sums of squares, fused argmax, input mode); prefetch / force_mfma
-// are ignored. Block tile 16*mt activation rows x nt weight row blocks (16
+// MFMA GEMM (K2) for more than kGemvMaxRows activation rows: same arguments
+// and epilogues as launch_gemv without the GEMV-only stages (partial sums of
+// squares, fused argmax, input mode; planes only through the finishing pass,
+// gemm_emit_ok); prefetch / force_mfma are ignored. Block tile 16*mt activation rows x nt weight row blocks (16
 // rows each), 4 waves; ks > 1 splits K over workgroups, which needs
 // splitk_ws (ks * M * N floats) and a second, fixed-order reduction kernel.
 // ksplit_override / rb_override force the splits / row blocks per wave

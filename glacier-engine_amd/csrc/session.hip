@@ -427,6 +427,9 @@ gk::GemvArgs proj_args(glacier_hip_session *s, glacier_hip_int4_weight *w, int D
 // separate conversion kernel plus the plain GEMV measured faster (7B QKV and
 // gate/up), about even at 4-5.
 constexpr int kInputModeRows = 4;
+// A prompt chunk of more rows than this (one lane, consecutive positions)
+// runs the prefill attention kernel; shorter chunks the decode kernel.
+constexpr int kPrefillAttnRows = 16;
 
 bool input_mode_args(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, int rows, int epi,
                      const ProjIn &in, const ProjOut &out, gk::GemvArgs *a) {
@@ -552,7 +555,7 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
     // attention: a prompt chunk of one lane past the GEMV size runs the
     // prefill kernel, other steps the decode kernel, which for up to 32 rows
     // also writes the O projection's planes
-    const bool pf_attn = rows > gk::kGemvMaxRows && rp.chunk_lane >= 0 &&
+    const bool pf_attn = rows > kPrefillAttnRows && rp.chunk_lane >= 0 &&
                          s->opt.kv_dtype == GLACIER_HIP_F16;
     const bool o_planes = !pf_attn && rows <= 32 && (uint32_t)rows <= s->planes2_rows;
     const gk::PlanesDst opd = o_planes ? gk::PlanesDst{s->act_q2, s->act_meta2, Do}
@@ -1107,7 +1110,8 @@ glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
   A((void **)&s->act_meta, Gmax * M * sizeof(gk::ActMeta));
   // the gate/up epilogue emits planes for every GEMV launch (up to
   // kGemvMaxRows rows) and attention the O projection's for every step of
-  // up to 32 rows (decode lanes, or a prompt chunk that short)
+  // up to 32 rows (decode lanes, or a prompt chunk that short); GEMM steps
+  // emit into act_q
   s->planes2_rows = std::min<uint32_t>(M, 32);
   // act_q2 also holds the O projection's planes, emitted by attention
   const size_t G2 = std::max<size_t>(c.hidden_dim, (size_t)c.num_heads * c.head_dim) / 32;

@@ -200,7 +200,7 @@ int glacier_hip_int4_matvec_dispatch(glacier_hip_context *ctx, glacier_hip_int4_
  * (+ bias[out_f]), m in 1..GLACIER_HIP_MAX_ROWS. x is f32 or bf16 (x_dtype),
  * y is f32. Replaces linearInt4WeightQ8 / linearInt4Weight
  * (int4_matmul.zig:422-531, 2957-2981) for one projection over m rows: up to
- * 16 rows run the decode GEMV, more rows (wide decode batches, prompt chunks,
+ * 5 rows run the decode GEMV, more rows (decode batches, prompt chunks,
  * the packed batch of forwardLayerPackedBatch, generate.zig:2105) the MFMA
  * GEMM; both compute every row with the same per-group arithmetic.
  * Asynchronous on `stream`. */

@@ -1,7 +1,7 @@
-"""GPU parity of the MFMA GEMM (K2: projections over more than 16 rows,
+"""GPU parity of the MFMA GEMM (K2: projections over more than 5 rows,
 32-row tiles up to 32 rows with K split over workgroups, 64-row tiles above)
 against the CPU oracle, through the C ABI (glacier_hip_int4_gemv with
-m > 16), and of chunked prefill end to end.
+m > 5), and of chunked prefill end to end.
 
 Tolerances: as the decode GEMV. Q8: every per-group integer dot is exact and
 the group term RN(T * s_w) is the reference's; the activation scale is folded
