@@ -54,7 +54,8 @@ template <int D, int BM>
 struct ActStage {
   static constexpr int kActBytes = 4 * D * BM * 32;
   static constexpr int kBufBytes = kActBytes + 4 * BM * 4;
-  static constexpr int kUnits = kActBytes / 16 / 256;  // 16-byte loads per thread
+  static constexpr int kUnitCount = kActBytes / 16;            // 16-byte units
+  static constexpr int kUnits = (kUnitCount + 255) / 256;      // per thread
 };
 
 // One thread's share of a quad's activation staging.
@@ -65,14 +66,16 @@ struct ActRegs {
 };
 
 // Loads quad kq's activation planes (rows m0 .. m0 + BM - 1, clamped to
-// M - 1) and scales into registers; one 16-byte unit per thread and pass.
+// M - 1) and scales into registers; one 16-byte unit per thread and pass
+// (16-row tiles have fewer units than threads: the extra threads repeat the
+// last unit, branch-free).
 template <int D, int BM>
 __device__ __forceinline__ ActRegs<D, BM> act_load(const GemvArgs &p, int kq, int m0) {
   ActRegs<D, BM> r;
   const int M = p.M, t = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < ActStage<D, BM>::kUnits; ++i) {
-    const int u = t + 256 * i;  // unit: ((j * D + d) * BM + row) * 2 + half
+    const int u = min(t + 256 * i, ActStage<D, BM>::kUnitCount - 1);  // ((j * D + d) * BM + row) * 2 + half
     const int half = u & 1, row = (u >> 1) % BM, jd = (u >> 1) / BM;
     const int m = min(m0 + row, M - 1);
     const size_t src = ((size_t)(4 * kq) * D + jd) * M + m;  // group 4kq + j, digit d
@@ -88,13 +91,14 @@ template <int D, int BM>
 __device__ __forceinline__ void act_store(unsigned char *buf, const ActRegs<D, BM> &r) {
   const int t = threadIdx.x;
 #pragma unroll
-  for (int i = 0; i < ActStage<D, BM>::kUnits; ++i) ((uint4 *)buf)[t + 256 * i] = r.v[i];
+  for (int i = 0; i < ActStage<D, BM>::kUnits; ++i)
+    ((uint4 *)buf)[min(t + 256 * i, ActStage<D, BM>::kUnitCount - 1)] = r.v[i];
   // (duplicates store the same value to the same slot: no branch)
   ((float *)(buf + ActStage<D, BM>::kActBytes))[t % (4 * BM)] = r.sc;
 }
 
 // kRB: 16-row weight blocks per wave (1, 2 or 4; the workgroup covers 4 kRB);
-// BM: activation rows per workgroup (32 or 64). The K quads are split over
+// BM: activation rows per workgroup (16, 32 or 64). The K quads are split over
 // blockIdx.y (ks_count splits); with part set each split writes its partial
 // sums to part [ks_count][M][N] (no epilogue; a finishing kernel runs it).
 template <int D, int kRB, int BM>
@@ -474,18 +478,19 @@ __global__ __launch_bounds__(kEmitThreads) void splitk_resid_emit_kernel(GemvArg
 
 GemmShape plan_gemm(int N, int M, int K, int D, size_t ws_floats) {
   GemmShape s;
-  const int bm = M <= 32 ? 32 : 64;
+  const int bm = M <= 16 ? 16 : M <= 32 ? 32 : 64;
   s.mt = bm / 16;
   s.m_tiles = (M + bm - 1) / bm;
   // Row blocks per wave and the workgroup target, from sweeps of the 7B
-  // shapes: 32-row tiles (decode lanes) 1 row block per wave for one-digit
+  // shapes: 16- and 32-row tiles (decode lanes; 16 rows up to 16, so small
+  // batches do not pay for 32 rows of MFMA and scaling work) 1 row block per wave for one-digit
   // planes, 2 for three, toward about 1024 workgroups; 64-row tiles (prompt
   // chunks) 2 for one digit (4 workgroups per CU), 4 for three once that
   // still fills the GPU, toward about 512.
   const int NB = N / 16, KQ = K / 128;
   const long big = (long)s.m_tiles * ((NB + 15) / 16);
   int target;
-  if (bm == 32) {
+  if (bm <= 32) {
     s.nt = D == 1 ? 4 : 8;
     target = 1024;
   } else {
@@ -551,7 +556,9 @@ hipError_t launch_gemm(const GemvArgs &a, hipStream_t st) {
   hipLaunchKernelGGL((gemm_kernel<DD, RB, BM>), grid, block, 0, st, a, s.m_tiles, s.ks, part)
 #define GK_GEMM_BM(DD, RB) \
   do {                       \
-    if (s.mt == 2) GK_GEMM(DD, RB, 32); else GK_GEMM(DD, RB, 64); \
+    if (s.mt == 1) GK_GEMM(DD, RB, 16);                           \
+    else if (s.mt == 2) GK_GEMM(DD, RB, 32);                      \
+    else GK_GEMM(DD, RB, 64);                                     \
   } while (0)
   if (a.D == 1) {
     if (s.nt == 16) GK_GEMM_BM(1, 4); else if (s.nt == 8) GK_GEMM_BM(1, 2); else GK_GEMM_BM(1, 1);
