@@ -1,5 +1,6 @@
-"""GPU parity of the MFMA GEMM (K2: projections over more than 5 rows,
-32-row tiles up to 32 rows with K split over workgroups, 64-row tiles above)
+"""GPU parity of the MFMA GEMM (K2: projections over more than 5 rows, and
+3-digit ones from 3 rows; 16-row tiles up to 16 rows, 32-row tiles up to 32
+with K split over workgroups, 64-row tiles above)
 against the CPU oracle, through the C ABI (glacier_hip_int4_gemv with
 m > 5), and of chunked prefill end to end.
 
@@ -45,7 +46,7 @@ SHAPES = [(16, 128), (48, 256), (896, 896), (128, 896), (896, 4864), (9728, 896)
 
 
 @pytest.mark.parametrize("out_f,in_f", SHAPES)
-@pytest.mark.parametrize("m", [17, 24, 32, 33, 64, 130, 300])
+@pytest.mark.parametrize("m", [6, 9, 16, 17, 24, 32, 33, 64, 130, 300])
 def test_gemm_q8_matches_oracle(gh, gctx, ora, out_f, in_f, m):
     packed, s16, s32 = _weights(gh, 300 + out_f + in_f, out_f, in_f)
     w = gctx.weight(packed, s16, in_f, out_f)
@@ -61,7 +62,7 @@ def test_gemm_q8_matches_oracle(gh, gctx, ora, out_f, in_f, m):
 
 
 @pytest.mark.parametrize("out_f,in_f", [(48, 256), (896, 896), (512, 18944)])
-@pytest.mark.parametrize("m", [20, 32, 40, 129])
+@pytest.mark.parametrize("m", [3, 5, 11, 16, 20, 32, 40, 129])
 def test_gemm_f32_matches_oracle(gh, gctx, ora, out_f, in_f, m):
     packed, s16, s32 = _weights(gh, 400 + out_f + in_f, out_f, in_f)
     w = gctx.weight(packed, s16, in_f, out_f)
