@@ -10,11 +10,13 @@
 #include <limits.h>
 #include <string.h>
 
+#include <functional>
 #include <mutex>
 #include <vector>
 
 #include "../../include/glacier_hip.h"
 #include "host_util.h"
+#include "lane_weave.h"
 
 namespace {
 
@@ -648,10 +650,12 @@ int glacier_hip_lane_weave_admit(glacier_hip_lane_weave *lw, const glacier_hip_r
   return GLACIER_HIP_OK;
 }
 
-int glacier_hip_lane_weave_serve_one(glacier_hip_lane_weave *lw, glacier_hip_lane_event_t *out) {
-  // serveOne (:1196-1270)
-  if (!lw || !out) return GLACIER_HIP_INVALID_ARGUMENT;
-  std::lock_guard<std::mutex> lk(lw->mu);
+}  // extern "C"
+
+namespace {
+
+// serveOne (:1196-1270) with lw->mu held.
+int serve_one_locked(glacier_hip_lane_weave *lw, glacier_hip_lane_event_t *out) {
   if (lw->poisoned) return GLACIER_HIP_SCHEDULER_POISONED;
   if (lw->closed) return GLACIER_HIP_SCHEDULER_CLOSED;
   if (lw->tick == kU64Max) return GLACIER_HIP_SCHEDULER_POISONED;
@@ -698,35 +702,99 @@ int glacier_hip_lane_weave_serve_one(glacier_hip_lane_weave *lw, glacier_hip_lan
   return GLACIER_HIP_OK;
 }
 
-int glacier_hip_lane_weave_plan_wave(glacier_hip_lane_weave *lw, uint32_t max_count,
-                                     uint32_t *slots_out, uint32_t *count_out) {
-  if (!lw || !slots_out || !count_out) return GLACIER_HIP_INVALID_ARGUMENT;
-  std::lock_guard<std::mutex> lk(lw->mu);
+// The slots the next serve_one calls select (lw->mu held): replays the
+// serve_one transitions on copies of the mutable selection state (cursor,
+// level, tick, remaining quanta, last service) and stops before a slot would
+// repeat or before a quantum whose serve_one would poison the scheduler
+// (a deadline it cannot keep, a service gap over the budget), so every
+// planned quantum commits.
+int plan_wave_locked(glacier_hip_lane_weave *lw, uint32_t max_count, uint32_t *slots_out,
+                     uint32_t *count_out) {
   *count_out = 0;
   if (lw->poisoned) return GLACIER_HIP_SCHEDULER_POISONED;
   if (lw->closed) return GLACIER_HIP_SCHEDULER_CLOSED;
-  // Replays the serve_one transitions on copies of the mutable selection
-  // state: cursor, level, and which slots are still active (a slot whose last
-  // quantum is planned becomes inactive, which can change the round).
-  std::vector<uint8_t> active(lw->slots.size()), taken(lw->slots.size(), 0);
-  std::vector<uint64_t> remaining(lw->slots.size());
-  for (size_t i = 0; i < active.size(); ++i) {
+  const size_t n = lw->slots.size();
+  std::vector<uint8_t> active(n), taken(n, 0);
+  std::vector<uint64_t> remaining(n), last(n);
+  for (size_t i = 0; i < n; ++i) {
     active[i] = lw->slots[i].state == kActive;
     remaining[i] = lw->slots[i].remaining;
+    last[i] = lw->slots[i].last_service_tick;
   }
   uint32_t cur = lw->cursor;
   uint16_t lvl = lw->level;
-  while (*count_out < max_count) {
+  uint64_t tick = lw->tick;
+  while (*count_out < max_count && tick != kU64Max) {
     Selection sel;
     if (!lw->next_selection(cur, lvl, active, &sel)) break;
     if (taken[sel.index]) break;
+    const uint64_t after_tick = tick + 1;
+    bool keeps = after_tick - last[sel.index] <= lw->max_gap;
+    for (size_t j = 0; j < n && keeps; ++j) {
+      const uint64_t dl = lw->slots[j].spec.deadline_tick;
+      if (!active[j] || dl == 0) continue;
+      const bool completes = j == sel.index && remaining[j] == 1;
+      if ((completes && after_tick > dl) || (!completes && after_tick >= dl)) keeps = false;
+    }
+    if (!keeps) break;
     taken[sel.index] = 1;
     slots_out[(*count_out)++] = sel.index;
     if (--remaining[sel.index] == 0) active[sel.index] = 0;
+    last[sel.index] = after_tick;
+    tick = after_tick;
     cur = sel.cursor_after;
     lvl = sel.level_after;
   }
   return GLACIER_HIP_OK;
+}
+
+}  // namespace
+
+namespace gh {
+
+int lane_weave_run_wave(glacier_hip_lane_weave *lw, uint32_t max_count,
+                        const std::function<int(const uint32_t *, uint32_t)> &device_step,
+                        uint32_t *slots_out, glacier_hip_lane_event_t *events_out,
+                        uint32_t *count_out) {
+  std::lock_guard<std::mutex> lk(lw->mu);
+  *count_out = 0;
+  std::vector<uint32_t> plan(max_count);
+  uint32_t n = 0;
+  int rc = plan_wave_locked(lw, max_count, plan.data(), &n);
+  if (rc) return rc;
+  if (n == 0) return GLACIER_HIP_NO_RUNNABLE;
+  rc = device_step(plan.data(), n);
+  if (rc) return rc;  // nothing committed, the scheduler unchanged
+  for (uint32_t i = 0; i < n; ++i) {
+    glacier_hip_lane_event_t ev;
+    rc = serve_one_locked(lw, &ev);
+    if (rc || ev.handle.slot_index != plan[i]) {
+      // the device step has committed: the scheduler no longer matches it
+      lw->poisoned = true;
+      return GLACIER_HIP_SCHEDULER_POISONED;
+    }
+    if (slots_out) slots_out[i] = plan[i];
+    if (events_out) events_out[i] = ev;
+    *count_out = i + 1;
+  }
+  return GLACIER_HIP_OK;
+}
+
+}  // namespace gh
+
+extern "C" {
+
+int glacier_hip_lane_weave_serve_one(glacier_hip_lane_weave *lw, glacier_hip_lane_event_t *out) {
+  if (!lw || !out) return GLACIER_HIP_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> lk(lw->mu);
+  return serve_one_locked(lw, out);
+}
+
+int glacier_hip_lane_weave_plan_wave(glacier_hip_lane_weave *lw, uint32_t max_count,
+                                     uint32_t *slots_out, uint32_t *count_out) {
+  if (!lw || !slots_out || !count_out) return GLACIER_HIP_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> lk(lw->mu);
+  return plan_wave_locked(lw, max_count, slots_out, count_out);
 }
 
 int glacier_hip_lane_weave_retire(glacier_hip_lane_weave *lw, const glacier_hip_lane_handle_t *h,

@@ -16,6 +16,7 @@ struct glacier_hip_context {
   hipDeviceProp_t props{};
   uint64_t epoch = 0;  // binds allocation quotes to this context
   std::mutex mu;       // one submission at a time (int4_executor.zig:2267)
+  std::mutex buf_mu;   // buffer table (backend.zig:1682-1684 buffer mutex)
   std::string last_error;
   struct Buf {
     void *ptr;
@@ -24,15 +25,20 @@ struct glacier_hip_context {
   std::map<uint64_t, Buf> buffers;
   uint64_t next_buffer_id = 1;
   uint64_t live_weights = 0;
-  // scratch for the stand-alone kernel entry points
-  void *scratch = nullptr;
-  size_t scratch_bytes = 0;
-  void *planes = nullptr;  // activation planes of glacier_hip_int4_gemv
-  size_t planes_bytes = 0;
-  float *splitk = nullptr;  // GEMM split-K partial sums of glacier_hip_int4_gemv
-  size_t splitk_floats = 0;
-  uint32_t *counters = nullptr;  // zeroed once, self-resetting
-  size_t counter_count = 0;
+  // Scratch of the stand-alone kernel entry points, one set per stream: the
+  // host lock only orders the calls, so work queued on two streams must not
+  // share a buffer.
+  struct StreamScratch {
+    void *scratch = nullptr;  // attention partials / argmax candidates
+    size_t scratch_bytes = 0;
+    void *planes = nullptr;  // activation planes of glacier_hip_int4_gemv
+    size_t planes_bytes = 0;
+    float *splitk = nullptr;  // GEMM split-K partial sums of glacier_hip_int4_gemv
+    size_t splitk_floats = 0;
+    uint32_t *counters = nullptr;  // zeroed once, self-resetting
+    size_t counter_count = 0;
+  };
+  std::map<hipStream_t, StreamScratch> per_stream;
   gk::ArgmaxResult *results_host = nullptr;  // pinned
   int32_t *ident = nullptr;  // device 0..63: row i -> page-table row i
 };
@@ -72,8 +78,16 @@ glacier_hip_int4_weight *upload_weight(glacier_hip_context *ctx, uint32_t out_f,
                                        const std::vector<uint32_t> &codes,
                                        const std::vector<uint16_t> &scales);
 
-// Ensure ctx->scratch holds at least `bytes` and ctx->counters `count`.
-int ensure_scratch(glacier_hip_context *ctx, size_t bytes, size_t counters);
+// Ensure the stream's scratch holds at least `bytes` and its counters `count`.
+int ensure_scratch(glacier_hip_context *ctx, glacier_hip_context::StreamScratch &ss, size_t bytes,
+                   size_t counters);
+
+// The host side of a submission: one at a time per context, a second one
+// (from another thread) is rejected with GLACIER_HIP_BUSY rather than queued
+// (acquireSubmission, int4_executor.zig:2267-2270).
+#define GH_SUBMISSION(ctx)                                        \
+  std::unique_lock<std::mutex> _submission((ctx)->mu, std::try_to_lock); \
+  if (!_submission.owns_lock()) return GLACIER_HIP_BUSY
 
 // Run one projection on the device: prep (+ optional norm) then GEMV.
 struct ProjBuffers {

@@ -88,21 +88,22 @@ glacier_hip_int4_weight *upload_weight(glacier_hip_context *ctx, uint32_t out_f,
   return w;
 }
 
-int ensure_scratch(glacier_hip_context *ctx, size_t bytes, size_t counters) {
-  if (bytes > ctx->scratch_bytes) {
-    if (ctx->scratch) GH_CHECK(ctx, hipFree(ctx->scratch));
-    ctx->scratch = nullptr;
-    ctx->scratch_bytes = 0;
-    GH_CHECK(ctx, hipMalloc(&ctx->scratch, bytes));
-    ctx->scratch_bytes = bytes;
+int ensure_scratch(glacier_hip_context *ctx, glacier_hip_context::StreamScratch &ss, size_t bytes,
+                   size_t counters) {
+  if (bytes > ss.scratch_bytes) {
+    if (ss.scratch) GH_CHECK(ctx, hipFree(ss.scratch));
+    ss.scratch = nullptr;
+    ss.scratch_bytes = 0;
+    GH_CHECK(ctx, hipMalloc(&ss.scratch, bytes));
+    ss.scratch_bytes = bytes;
   }
-  if (counters > ctx->counter_count) {
-    if (ctx->counters) GH_CHECK(ctx, hipFree(ctx->counters));
-    ctx->counters = nullptr;
-    ctx->counter_count = 0;
-    GH_CHECK(ctx, hipMalloc(&ctx->counters, counters * sizeof(uint32_t)));
-    GH_CHECK(ctx, hipMemset(ctx->counters, 0, counters * sizeof(uint32_t)));
-    ctx->counter_count = counters;
+  if (counters > ss.counter_count) {
+    if (ss.counters) GH_CHECK(ctx, hipFree(ss.counters));
+    ss.counters = nullptr;
+    ss.counter_count = 0;
+    GH_CHECK(ctx, hipMalloc(&ss.counters, counters * sizeof(uint32_t)));
+    GH_CHECK(ctx, hipMemset(ss.counters, 0, counters * sizeof(uint32_t)));
+    ss.counter_count = counters;
   }
   return GLACIER_HIP_OK;
 }
@@ -159,11 +160,14 @@ glacier_hip_context *glacier_hip_init(int device_ordinal) {
 int glacier_hip_deinit(glacier_hip_context *ctx) {
   if (!ctx) return GLACIER_HIP_INVALID_HANDLE;
   if (!ctx->buffers.empty() || ctx->live_weights != 0) return GLACIER_HIP_BUSY;
-  (void)hipStreamSynchronize(ctx->stream);
-  if (ctx->scratch) (void)hipFree(ctx->scratch);
-  if (ctx->planes) (void)hipFree(ctx->planes);
-  if (ctx->splitk) (void)hipFree(ctx->splitk);
-  if (ctx->counters) (void)hipFree(ctx->counters);
+  (void)hipDeviceSynchronize();
+  for (auto &kv : ctx->per_stream) {
+    auto &ss = kv.second;
+    if (ss.scratch) (void)hipFree(ss.scratch);
+    if (ss.planes) (void)hipFree(ss.planes);
+    if (ss.splitk) (void)hipFree(ss.splitk);
+    if (ss.counters) (void)hipFree(ss.counters);
+  }
   if (ctx->results_host) (void)hipHostFree(ctx->results_host);
   if (ctx->ident) (void)hipFree(ctx->ident);
   (void)hipStreamDestroy(ctx->stream);
@@ -314,7 +318,7 @@ int glacier_hip_allocation_allocate(glacier_hip_context *ctx,
   if (quote->context_epoch != ctx->epoch || quote->requested_bytes == 0 ||
       quote->charged_bytes != charged_size(quote->requested_bytes))
     return GLACIER_HIP_INVALID_ARGUMENT;
-  std::lock_guard<std::mutex> lk(ctx->mu);
+  std::lock_guard<std::mutex> lk(ctx->buf_mu);
   void *p = nullptr;
   hipError_t e = hipMalloc(&p, quote->requested_bytes);
   if (e != hipSuccess) return hip_fail(ctx, e, "hipMalloc");  // nothing was created
@@ -333,7 +337,7 @@ int glacier_hip_allocation_free(glacier_hip_context *ctx, const glacier_hip_buff
 int glacier_hip_buffer_info(glacier_hip_context *ctx, const glacier_hip_buffer_token_t *token,
                             glacier_hip_buffer_info_t *out) {
   if (!ctx || !token || !out) return GLACIER_HIP_INVALID_ARGUMENT;
-  std::lock_guard<std::mutex> lk(ctx->mu);
+  std::lock_guard<std::mutex> lk(ctx->buf_mu);
   auto it = ctx->buffers.find(token->id);
   if (it == ctx->buffers.end() || it->second.requested != token->requested_bytes)
     return GLACIER_HIP_INVALID_HANDLE;
@@ -346,7 +350,7 @@ int glacier_hip_buffer_info(glacier_hip_context *ctx, const glacier_hip_buffer_t
 
 int glacier_hip_buffer_release(glacier_hip_context *ctx, const glacier_hip_buffer_token_t *token) {
   if (!ctx || !token) return GLACIER_HIP_INVALID_ARGUMENT;
-  std::lock_guard<std::mutex> lk(ctx->mu);
+  std::lock_guard<std::mutex> lk(ctx->buf_mu);
   auto it = ctx->buffers.find(token->id);
   if (it == ctx->buffers.end() || it->second.requested != token->requested_bytes)
     return GLACIER_HIP_INVALID_HANDLE;
@@ -358,7 +362,7 @@ int glacier_hip_buffer_release(glacier_hip_context *ctx, const glacier_hip_buffe
 
 int glacier_hip_live_buffer_count(glacier_hip_context *ctx, uint64_t *out) {
   if (!ctx || !out) return GLACIER_HIP_INVALID_ARGUMENT;
-  std::lock_guard<std::mutex> lk(ctx->mu);
+  std::lock_guard<std::mutex> lk(ctx->buf_mu);
   *out = ctx->buffers.size();
   return GLACIER_HIP_OK;
 }
@@ -461,16 +465,17 @@ static int gemv_launch(glacier_hip_context *ctx, glacier_hip_int4_weight *w, con
     GH_CHECK(ctx, gk::launch_gemv(a, st));
     return GLACIER_HIP_OK;
   }
+  auto &ss = ctx->per_stream[st];
   const size_t need = std::min<size_t>(gk::gemm_splitk_floats(N, (int)m, K, D), 16u << 20);
-  if (need > ctx->splitk_floats) {
-    if (ctx->splitk) GH_CHECK(ctx, hipFree(ctx->splitk));
-    ctx->splitk = nullptr;
-    ctx->splitk_floats = 0;
-    GH_CHECK(ctx, hipMalloc((void **)&ctx->splitk, need * sizeof(float)));
-    ctx->splitk_floats = need;
+  if (need > ss.splitk_floats) {
+    if (ss.splitk) GH_CHECK(ctx, hipFree(ss.splitk));
+    ss.splitk = nullptr;
+    ss.splitk_floats = 0;
+    GH_CHECK(ctx, hipMalloc((void **)&ss.splitk, need * sizeof(float)));
+    ss.splitk_floats = need;
   }
-  a.splitk_ws = ctx->splitk;
-  a.splitk_ws_floats = ctx->splitk_floats;
+  a.splitk_ws = ss.splitk;
+  a.splitk_ws_floats = ss.splitk_floats;
   GH_CHECK(ctx, gk::launch_gemm(a, st));
   return GLACIER_HIP_OK;
 }
@@ -493,24 +498,25 @@ static int gemv_common(glacier_hip_context *ctx, glacier_hip_int4_weight *w, con
   if (x_dtype != GLACIER_HIP_F32 && x_dtype != GLACIER_HIP_BF16) return GLACIER_HIP_DTYPE_UNSUPPORTED;
   const int D = act_digits(gh::resolve_activation(activation, w->out_f, w->in_f));
   if (!D) return GLACIER_HIP_INVALID_ARGUMENT;
+  auto &ss = ctx->per_stream[st];
   const size_t pb = planes_bytes(m, w->in_f, D);
-  if (pb > ctx->planes_bytes) {
-    if (ctx->planes) GH_CHECK(ctx, hipFree(ctx->planes));
-    ctx->planes = nullptr;
-    ctx->planes_bytes = 0;
-    GH_CHECK(ctx, hipMalloc(&ctx->planes, pb));
-    ctx->planes_bytes = pb;
+  if (pb > ss.planes_bytes) {
+    if (ss.planes) GH_CHECK(ctx, hipFree(ss.planes));
+    ss.planes = nullptr;
+    ss.planes_bytes = 0;
+    GH_CHECK(ctx, hipMalloc(&ss.planes, pb));
+    ss.planes_bytes = pb;
   }
-  int rc = prepare_launch(ctx, x_dev, x_dtype, m, w->in_f, D, ctx->planes, st);
+  int rc = prepare_launch(ctx, x_dev, x_dtype, m, w->in_f, D, ss.planes, st);
   if (rc) return rc;
-  return gemv_launch(ctx, w, ctx->planes, m, D, bias_dev, y_dev, st);
+  return gemv_launch(ctx, w, ss.planes, m, D, bias_dev, y_dev, st);
 }
 
 int glacier_hip_int4_gemv(glacier_hip_context *ctx, glacier_hip_int4_weight *w, const void *x_dev,
                           int x_dtype, uint32_t m, const float *bias_dev, float *y_dev,
                           int activation, void *stream) {
   if (!ctx) return GLACIER_HIP_INVALID_HANDLE;
-  std::lock_guard<std::mutex> lk(ctx->mu);
+  GH_SUBMISSION(ctx);
   return gemv_common(ctx, w, x_dev, x_dtype, m, bias_dev, y_dev, activation,
                      stream ? (hipStream_t)stream : ctx->stream);
 }
@@ -529,7 +535,7 @@ int glacier_hip_activation_prepare(glacier_hip_context *ctx, const void *x_dev, 
   if (!D) return GLACIER_HIP_INVALID_ARGUMENT;
   if (m == 0 || m > GLACIER_HIP_MAX_ROWS || in_f == 0 || in_f % 128 != 0) return GLACIER_HIP_SHAPE_MISMATCH;
   if (x_dtype != GLACIER_HIP_F32 && x_dtype != GLACIER_HIP_BF16) return GLACIER_HIP_DTYPE_UNSUPPORTED;
-  std::lock_guard<std::mutex> lk(ctx->mu);
+  GH_SUBMISSION(ctx);
   return prepare_launch(ctx, x_dev, x_dtype, m, in_f, D, act_dev,
                         stream ? (hipStream_t)stream : ctx->stream);
 }
@@ -542,7 +548,7 @@ int glacier_hip_int4_gemv_prepared(glacier_hip_context *ctx, glacier_hip_int4_we
   const int D = act_digits(activation);
   if (!D) return GLACIER_HIP_INVALID_ARGUMENT;
   if (m == 0 || m > GLACIER_HIP_MAX_ROWS) return GLACIER_HIP_SHAPE_MISMATCH;
-  std::lock_guard<std::mutex> lk(ctx->mu);
+  GH_SUBMISSION(ctx);
   return gemv_launch(ctx, w, act_dev, m, D, bias_dev, y_dev,
                      stream ? (hipStream_t)stream : ctx->stream);
 }
@@ -552,7 +558,7 @@ int glacier_hip_int4_matvec_dispatch(glacier_hip_context *ctx, glacier_hip_int4_
                                      uint64_t output_count) {
   if (!ctx || !w || !input || !output) return GLACIER_HIP_INVALID_ARGUMENT;
   if (input_count != w->in_f || output_count != w->out_f) return GLACIER_HIP_SHAPE_MISMATCH;
-  std::lock_guard<std::mutex> lk(ctx->mu);
+  GH_SUBMISSION(ctx);
   float *xd = nullptr, *yd = nullptr;
   GH_CHECK(ctx, hipMalloc(&xd, input_count * 4));
   hipError_t e = hipMalloc(&yd, output_count * 4);
@@ -597,18 +603,19 @@ int glacier_hip_paged_attention(glacier_hip_context *ctx, const float *q_dev,
       num_heads / num_kv_heads > 8 || (head_dim != 64 && head_dim != 128) ||
       layer >= num_layers || max_ctx == 0 || (max_ctx + 15) / 16 > max_pages_per_lane)
     return GLACIER_HIP_SHAPE_MISMATCH;
-  std::lock_guard<std::mutex> lk(ctx->mu);
+  GH_SUBMISSION(ctx);
   hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
   // lane_of_row = identity: row i attends with page-table row i
   const size_t sc = gk::attention_scratch_floats((int)lanes, (int)num_heads, (int)num_kv_heads,
                                                  (int)head_dim, (int)max_ctx);
-  int rc = gh::ensure_scratch(ctx, sc * 4, 1);
+  auto &ss = ctx->per_stream[st];
+  int rc = gh::ensure_scratch(ctx, ss, sc * 4, 1);
   if (rc) return rc;
   GH_CHECK(ctx, gk::launch_attention(q_dev, kv_pool_dev, kv_dtype == GLACIER_HIP_F16, page_table_dev,
                                      (int)max_pages_per_lane, ctx->ident, ctx_lens_dev, (int)lanes,
                                      (int)layer, (int)num_layers, (int)num_heads,
                                      (int)num_kv_heads, (int)head_dim, (int)max_ctx,
-                                     (float *)ctx->scratch, out_dev, st));
+                                     (float *)ss.scratch, out_dev, st));
   return GLACIER_HIP_OK;
 }
 
@@ -626,13 +633,14 @@ static int argmax_common(glacier_hip_context *ctx, const float *logits_dev, uint
   } else if (n == 0) {
     return GLACIER_HIP_SHAPE_MISMATCH;
   }
-  std::lock_guard<std::mutex> lk(ctx->mu);
+  GH_SUBMISSION(ctx);
   const size_t sb = gk::argmax_scratch_bytes((int)rows, (long)n);
-  int rc = gh::ensure_scratch(ctx, sb + 256 + rows * sizeof(gk::ArgmaxResult), rows);
+  auto &ss = ctx->per_stream[st];
+  int rc = gh::ensure_scratch(ctx, ss, sb + 256 + rows * sizeof(gk::ArgmaxResult), rows);
   if (rc) return rc;
-  auto *res_dev = (gk::ArgmaxResult *)((char *)ctx->scratch + ((sb + 255) & ~(size_t)255));
+  auto *res_dev = (gk::ArgmaxResult *)((char *)ss.scratch + ((sb + 255) & ~(size_t)255));
   GH_CHECK(ctx, gk::launch_argmax(logits_dev, (long)n, (int)rows, words_dev, (long)word_count,
-                                  ctx->scratch, ctx->counters, res_dev, st));
+                                  ss.scratch, ss.counters, res_dev, st));
   GH_CHECK(ctx, hipMemcpyAsync(ctx->results_host, res_dev, rows * sizeof(gk::ArgmaxResult),
                                hipMemcpyDeviceToHost, st));
   GH_CHECK(ctx, hipStreamSynchronize(st));

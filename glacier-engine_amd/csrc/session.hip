@@ -16,46 +16,18 @@
 #include <algorithm>
 
 #include "host_util.h"
+#include "lane_weave.h"
+#include "paged_kv.h"
 #include "runtime.h"
 
 using gh::hip_fail;
 
 namespace {
 
-constexpr uint64_t kPageRefAbi = 0x4750524600000001ull;
-
 struct LayerDev {
   float *in_norm = nullptr, *post_norm = nullptr, *qkv_bias = nullptr;
   glacier_hip_int4_weight *qkv = nullptr, *o = nullptr, *gu = nullptr, *down = nullptr;
 };
-
-void emptyOwnershipDigest(uint64_t inst, uint64_t L, uint64_t dim, uint64_t max_seq,
-                          uint8_t out[32]) {
-  // paged_kv_cache.zig:323-338
-  gh::Sha256 h;
-  h.update("glacier-paged-kv-ownership-v1\0", 30);
-  h.u64(inst);
-  h.u64(L);
-  h.u64(dim);
-  h.u64(max_seq);
-  h.u64(16);
-  h.final(out);
-}
-
-void appendOwnershipDigest(const uint8_t before[32], uint64_t inst, uint64_t page, uint64_t gen,
-                           uint8_t out[32]) {
-  // paged_kv_cache.zig:341-353
-  gh::Sha256 h;
-  h.update("glacier-paged-kv-root-append-v1\0", 32);
-  h.update(before, 32);
-  h.u64(kPageRefAbi);
-  h.u64(inst);
-  h.u64(page);
-  h.u64(gen);
-  h.final(out);
-}
-
-uint64_t g_next_cache_instance = 1;  // reserveCacheInstance (process-local, nonzero)
 
 }  // namespace
 
@@ -71,14 +43,7 @@ struct glacier_hip_model {
 };
 
 struct Lane {
-  bool active = false;
-  uint64_t instance = 0;
-  uint64_t len = 0;
-  std::vector<int32_t> page_of;   // logical page -> physical page, -1 = none
-  std::vector<uint64_t> page_gen; // ownership generation
-  uint64_t next_page_generation = 1;
-  uint64_t next_root_generation = 2;
-  glacier_hip_page_map_root_t root{};
+  gpk::Cache kv;                  // page map, generations, committed root
   uint64_t sampling_calls = 0;
   uint64_t rng[4] = {0, 0, 0, 0};
   std::vector<uint32_t> output;
@@ -106,7 +71,7 @@ struct glacier_hip_session {
   uint32_t total_pages = 0;
   uint32_t rows_cap = 0;   // max(max_lanes, prefill_chunk): rows of the scratch buffers
   uint32_t prefill_chunk = 0;
-  std::vector<int32_t> free_pages;
+  gpk::PagePool pool;
   std::vector<Lane> lanes;
   // device
   void *kv_pool = nullptr;
@@ -718,26 +683,7 @@ void destroy_session(glacier_hip_session *s) {
 }
 
 void reset_lane(glacier_hip_session *s, Lane &ln, uint64_t seed) {
-  // return pages to the pool
-  for (auto &p : ln.page_of)
-    if (p >= 0) {
-      s->free_pages.push_back(p);
-      p = -1;
-    }
-  ln.page_of.assign(s->max_pages, -1);
-  ln.page_gen.assign(s->max_pages, 0);
-  ln.active = true;
-  ln.instance = g_next_cache_instance++;
-  ln.len = 0;
-  ln.next_page_generation = 1;
-  ln.next_root_generation = 2;
-  const auto &c = s->model->cfg;
-  ln.root.cache_instance = ln.instance;
-  ln.root.generation = 1;
-  ln.root.committed_len = 0;
-  ln.root.committed_pages = 0;
-  emptyOwnershipDigest(ln.instance, c.num_layers, (uint64_t)c.num_kv_heads * c.head_dim,
-                       s->opt.max_positions, ln.root.ownership_sha256);
+  ln.kv.start(s->pool);  // a new request: fresh cache instance, pages back to the pool
   ln.sampling_calls = 0;
   // SplitMix64-seeded Xoshiro256 state (std.Random.DefaultPrng.init)
   uint64_t st = seed;
@@ -751,70 +697,58 @@ void reset_lane(glacier_hip_session *s, Lane &ln, uint64_t seed) {
   ln.output.clear();
 }
 
-struct RowTxn {
-  uint32_t lane;
-  uint64_t pos;
-  bool installs;
-  int32_t page;
-  uint64_t gen;
-  glacier_hip_page_map_root_t after;
-};
+using gpk::RowTxn;
+
+// Runs fn(lane, first, count) over the runs of consecutive rows of one lane.
+template <class F>
+int for_lane_runs(std::vector<RowTxn> &txns, F fn) {
+  int rc = GLACIER_HIP_OK;
+  for (size_t i = 0; i < txns.size();) {
+    size_t j = i + 1;
+    while (j < txns.size() && txns[j].lane == txns[i].lane) ++j;
+    const int r = fn(txns[i].lane, &txns[i], j - i);
+    if (r && !rc) rc = r;
+    i = j;
+  }
+  return rc;
+}
 
 void abort_rows(glacier_hip_session *s, std::vector<RowTxn> &txns) {
-  // abortRow (paged_kv_cache.zig:1146-1160): a newly installed page loses
-  // its ownership generation; nothing else changes. Installs are undone
-  // newest first so the free list returns to its order before the step.
-  for (size_t i = txns.size(); i-- > 0;) {
-    const RowTxn &t = txns[i];
-    Lane &ln = s->lanes[t.lane];
-    if (t.installs) {
-      ln.page_of[t.pos / 16] = -1;
-      ln.page_gen[t.pos / 16] = 0;
-      s->pt_host[(size_t)t.lane * s->max_pages + t.pos / 16] = 0;
-      s->free_pages.push_back(t.page);
-    }
-  }
+  // abortRow per lane: installed pages lose their ownership generation, the
+  // payloads stay with their logical pages and the consumed generations are
+  // not handed back
+  for_lane_runs(txns, [&](uint32_t lane, const RowTxn *t, size_t n) {
+    return s->lanes[lane].kv.abort(t, n);
+  });
   txns.clear();
 }
 
-// beginRow (paged_kv_cache.zig:1006-1072) for every participating lane.
+void note_installs(glacier_hip_session *s, const std::vector<RowTxn> &txns) {
+  for (const RowTxn &t : txns)
+    if (t.installs) s->pt_host[(size_t)t.lane * s->max_pages + t.pos / 16] = t.page;
+}
+
+// beginRow (paged_kv_cache.zig:1006-1072) for every participating lane;
+// nothing changes unless every lane can begin.
 int begin_rows(glacier_hip_session *s, const uint32_t *lanes, uint32_t count,
                std::vector<RowTxn> &txns) {
   txns.clear();
+  uint32_t need = 0;
   for (uint32_t i = 0; i < count; ++i) {
-    Lane &ln = s->lanes[lanes[i]];
-    RowTxn t{};
-    t.lane = lanes[i];
-    t.pos = ln.len;
-    const uint64_t page = ln.len / 16, row = ln.len % 16;
-    t.installs = row == 0;
-    if (t.installs) {
-      if (s->free_pages.empty()) {
-        // roll back the installs made so far in this step
-        abort_rows(s, txns);
-        return GLACIER_HIP_CACHE_FULL;
-      }
-      t.page = s->free_pages.back();
-      s->free_pages.pop_back();
-      t.gen = ln.next_page_generation;
-      ln.page_of[page] = t.page;
-      ln.page_gen[page] = t.gen;
-      s->pt_host[(size_t)lanes[i] * s->max_pages + page] = t.page;
-    } else {
-      t.page = ln.page_of[page];
-      t.gen = ln.page_gen[page];
-    }
-    t.after.cache_instance = ln.instance;
-    t.after.generation = ln.next_root_generation;
-    t.after.committed_len = ln.len + 1;
-    t.after.committed_pages = ln.root.committed_pages + (t.installs ? 1 : 0);
-    if (t.installs)
-      appendOwnershipDigest(ln.root.ownership_sha256, ln.instance, page, t.gen,
-                            t.after.ownership_sha256);
-    else
-      memcpy(t.after.ownership_sha256, ln.root.ownership_sha256, 32);
-    txns.push_back(t);
+    const gpk::Cache &kv = s->lanes[lanes[i]].kv;
+    if (kv.staged) return GLACIER_HIP_TRANSACTION_ACTIVE;
+    if (kv.len + 1 > kv.max_seq) return GLACIER_HIP_CACHE_FULL;
+    need += kv.pages_needed(1);
   }
+  if (need > s->pool.free.size()) return GLACIER_HIP_CACHE_FULL;
+  for (uint32_t i = 0; i < count; ++i) {
+    const int rc = s->lanes[lanes[i]].kv.begin(lanes[i], 1, s->pool, txns);
+    if (rc) {
+      abort_rows(s, txns);
+      return rc;
+    }
+  }
+  note_installs(s, txns);
   return GLACIER_HIP_OK;
 }
 
@@ -823,55 +757,18 @@ int begin_rows(glacier_hip_session *s, const uint32_t *lanes, uint32_t count,
 // per-token transactions would (generate.zig:5080-5118 commits per token).
 int begin_chunk(glacier_hip_session *s, uint32_t lane, uint32_t n, std::vector<RowTxn> &txns) {
   txns.clear();
-  txns.reserve(n);  // `before` points into txns
-  Lane &ln = s->lanes[lane];
-  const glacier_hip_page_map_root_t *before = &ln.root;
-  uint64_t page_gen = ln.next_page_generation;
-  for (uint32_t i = 0; i < n; ++i) {
-    RowTxn t{};
-    t.lane = lane;
-    t.pos = ln.len + i;
-    const uint64_t page = t.pos / 16;
-    t.installs = t.pos % 16 == 0;
-    if (t.installs) {
-      if (s->free_pages.empty()) {
-        abort_rows(s, txns);
-        return GLACIER_HIP_CACHE_FULL;
-      }
-      t.page = s->free_pages.back();
-      s->free_pages.pop_back();
-      t.gen = page_gen++;
-      ln.page_of[page] = t.page;
-      ln.page_gen[page] = t.gen;
-      s->pt_host[(size_t)lane * s->max_pages + page] = t.page;
-    } else {
-      t.page = ln.page_of[page];
-      t.gen = ln.page_gen[page];
-    }
-    t.after.cache_instance = ln.instance;
-    t.after.generation = ln.next_root_generation + i;
-    t.after.committed_len = t.pos + 1;
-    t.after.committed_pages = before->committed_pages + (t.installs ? 1 : 0);
-    if (t.installs)
-      appendOwnershipDigest(before->ownership_sha256, ln.instance, page, t.gen,
-                            t.after.ownership_sha256);
-    else
-      memcpy(t.after.ownership_sha256, before->ownership_sha256, 32);
-    txns.push_back(t);
-    before = &txns.back().after;
-  }
+  const int rc = s->lanes[lane].kv.begin(lane, n, s->pool, txns);
+  if (rc) return rc;
+  note_installs(s, txns);
   return GLACIER_HIP_OK;
 }
 
-void commit_rows(glacier_hip_session *s, std::vector<RowTxn> &txns) {
-  for (auto &t : txns) {
-    Lane &ln = s->lanes[t.lane];
-    if (t.installs) ln.next_page_generation++;
-    ln.next_root_generation++;
-    ln.root = t.after;
-    ln.len = t.pos + 1;
-  }
+int commit_rows(glacier_hip_session *s, std::vector<RowTxn> &txns) {
+  const int rc = for_lane_runs(txns, [&](uint32_t lane, const RowTxn *t, size_t n) {
+    return s->lanes[lane].kv.commit(t, n);
+  });
   txns.clear();
+  return rc;
 }
 
 // Copies the page-table entries installed by `txns` from the pinned host
@@ -1078,7 +975,9 @@ glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
   s->max_pages = (opts->max_positions + 15) / 16;
   s->total_pages = opts->total_pages ? opts->total_pages : opts->max_lanes * s->max_pages;
   s->lanes.resize(opts->max_lanes);
-  for (uint32_t p = s->total_pages; p-- > 0;) s->free_pages.push_back((int32_t)p);
+  s->pool.init(s->total_pages);
+  for (auto &ln : s->lanes)
+    ln.kv.init(c.num_layers, (uint64_t)c.num_kv_heads * c.head_dim, opts->max_positions);
   s->prefill_chunk = opts->prefill_chunk ? (uint32_t)opts->prefill_chunk
                                          : std::min<uint32_t>(opts->max_positions, 2048);
   s->rows_cap = std::max(opts->max_lanes, s->prefill_chunk);
@@ -1194,7 +1093,7 @@ void glacier_hip_session_destroy(glacier_hip_session *s) {
 int glacier_hip_session_lane_begin(glacier_hip_session *s, uint32_t lane, uint64_t seed) {
   if (!s) return GLACIER_HIP_INVALID_HANDLE;
   if (lane >= s->lanes.size()) return GLACIER_HIP_INVALID_ARGUMENT;
-  std::lock_guard<std::mutex> lk(s->model->ctx->mu);
+  GH_SUBMISSION(s->model->ctx);
   reset_lane(s, s->lanes[lane], seed);
   return GLACIER_HIP_OK;
 }
@@ -1208,14 +1107,14 @@ int glacier_hip_session_inject_failure(glacier_hip_session *s, int enable) {
 int glacier_hip_session_prefill(glacier_hip_session *s, uint32_t lane, const uint32_t *tokens,
                                 uint32_t n, uint32_t *first_token, float *logits_host) {
   if (!s || !tokens || !first_token) return GLACIER_HIP_INVALID_ARGUMENT;
-  if (lane >= s->lanes.size() || !s->lanes[lane].active) return GLACIER_HIP_INVALID_ARGUMENT;
+  if (lane >= s->lanes.size() || !s->lanes[lane].kv.active) return GLACIER_HIP_INVALID_ARGUMENT;
   const auto &c = s->model->cfg;
   Lane &ln = s->lanes[lane];
   if (n == 0) return GLACIER_HIP_SHAPE_MISMATCH;
   for (uint32_t i = 0; i < n; ++i)
     if (tokens[i] >= c.vocab_size) return GLACIER_HIP_SHAPE_MISMATCH;
-  if (ln.len + n > s->opt.max_positions) return GLACIER_HIP_CACHE_FULL;
-  std::lock_guard<std::mutex> lk(s->model->ctx->mu);
+  if (ln.kv.len + n > s->opt.max_positions) return GLACIER_HIP_CACHE_FULL;
+  GH_SUBMISSION(s->model->ctx);
   std::vector<RowTxn> txns;
   for (uint32_t done = 0; done < n;) {
     const uint32_t rows = std::min(n - done, s->prefill_chunk);
@@ -1223,7 +1122,7 @@ int glacier_hip_session_prefill(glacier_hip_session *s, uint32_t lane, const uin
     int rc = run_prefill_chunk(s, lane, tokens + done, rows, last, last ? logits_host : nullptr,
                                txns);
     if (rc) return rc;  // rows of earlier chunks stay committed (cache.commit per token)
-    commit_rows(s, txns);
+    if ((rc = commit_rows(s, txns))) return rc;  // staged under the lock: cannot fail
     done += rows;
   }
   *first_token = (uint32_t)s->res_host[0].index;
@@ -1240,19 +1139,19 @@ int glacier_hip_session_decode_step(glacier_hip_session *s, const uint32_t *lane
   if (count == 0 || count > s->lanes.size()) return GLACIER_HIP_SHAPE_MISMATCH;
   const auto &c = s->model->cfg;
   for (uint32_t i = 0; i < count; ++i) {
-    if (lanes[i] >= s->lanes.size() || !s->lanes[lanes[i]].active) return GLACIER_HIP_INVALID_ARGUMENT;
+    if (lanes[i] >= s->lanes.size() || !s->lanes[lanes[i]].kv.active) return GLACIER_HIP_INVALID_ARGUMENT;
     for (uint32_t j = 0; j < i; ++j)
       if (lanes[j] == lanes[i]) return GLACIER_HIP_INVALID_ARGUMENT;
     if (tokens[i] >= c.vocab_size) return GLACIER_HIP_SHAPE_MISMATCH;
-    if (s->lanes[lanes[i]].len + 1 > s->opt.max_positions) return GLACIER_HIP_CACHE_FULL;
+    if (s->lanes[lanes[i]].kv.len + 1 > s->opt.max_positions) return GLACIER_HIP_CACHE_FULL;
   }
-  std::lock_guard<std::mutex> lk(s->model->ctx->mu);
+  GH_SUBMISSION(s->model->ctx);
   std::vector<RowTxn> txns;
   int rc = run_step(s, lanes, tokens, count, true, eligible_words_host, logits_host, txns);
   if (rc) return rc;
   // publish: KV root + length, sampler counter, output word (all or nothing)
+  if ((rc = commit_rows(s, txns))) return rc;  // staged under the lock: cannot fail
   for (uint32_t i = 0; i < count; ++i) next_tokens[i] = (uint32_t)s->res_host[i].index;
-  commit_rows(s, txns);
   for (uint32_t i = 0; i < count; ++i) {
     Lane &ln = s->lanes[lanes[i]];
     // the eligible (posthead) branch does not count a sampler call
@@ -1266,7 +1165,7 @@ int glacier_hip_session_decode_step(glacier_hip_session *s, const uint32_t *lane
 int glacier_hip_session_lane_root(glacier_hip_session *s, uint32_t lane,
                                   glacier_hip_page_map_root_t *out) {
   if (!s || !out || lane >= s->lanes.size()) return GLACIER_HIP_INVALID_ARGUMENT;
-  *out = s->lanes[lane].root;
+  *out = s->lanes[lane].kv.root;
   return GLACIER_HIP_OK;
 }
 
@@ -1274,7 +1173,7 @@ int glacier_hip_session_lane_state(glacier_hip_session *s, uint32_t lane,
                                    glacier_hip_lane_state_t *out) {
   if (!s || !out || lane >= s->lanes.size()) return GLACIER_HIP_INVALID_ARGUMENT;
   const Lane &ln = s->lanes[lane];
-  out->kv_positions = ln.len;
+  out->kv_positions = ln.kv.len;
   out->published_tokens = ln.output.size();
   out->sampling_calls = ln.sampling_calls;
   memcpy(out->rng_state, ln.rng, sizeof ln.rng);
@@ -1292,8 +1191,8 @@ int glacier_hip_session_read_kv_row(glacier_hip_session *s, uint32_t lane, uint3
   if (!s || !out_host || lane >= s->lanes.size()) return GLACIER_HIP_INVALID_ARGUMENT;
   const auto &c = s->model->cfg;
   const Lane &ln = s->lanes[lane];
-  if (layer >= c.num_layers || position >= ln.len) return GLACIER_HIP_SHAPE_MISMATCH;
-  const int32_t page = ln.page_of[position / 16];
+  if (layer >= c.num_layers || position >= ln.kv.len) return GLACIER_HIP_SHAPE_MISMATCH;
+  const int32_t page = ln.kv.page_of[position / 16];
   if (page < 0) return GLACIER_HIP_INVALID_TRANSACTION;
   const size_t kvd = (size_t)c.num_kv_heads * c.head_dim;
   const size_t elem = s->opt.kv_dtype == GLACIER_HIP_F16 ? 2 : 4;
@@ -1323,11 +1222,11 @@ int glacier_hip_session_lane_kv_sha256(glacier_hip_session *s, uint32_t lane, ui
   h.update("glacier-logical-kv-state-v1\0", 28);
   h.u64(c.num_layers);
   h.u64(kvd);
-  h.u64(ln.len);
+  h.u64(ln.kv.len);
   std::vector<float> row(kvd);
   for (uint32_t l = 0; l < c.num_layers; ++l)
     for (int v = 0; v < 2; ++v)
-      for (uint64_t p = 0; p < ln.len; ++p) {
+      for (uint64_t p = 0; p < ln.kv.len; ++p) {
         int rc = glacier_hip_session_read_kv_row(s, lane, l, v, (uint32_t)p, row.data());
         if (rc) return rc;
         for (float f : row) {
@@ -1344,8 +1243,17 @@ int glacier_hip_session_page_of(glacier_hip_session *s, uint32_t lane, uint32_t 
                                 int32_t *physical_out) {
   if (!s || !physical_out || lane >= s->lanes.size()) return GLACIER_HIP_INVALID_ARGUMENT;
   const Lane &ln = s->lanes[lane];
-  if (logical_page >= ln.page_of.size()) return GLACIER_HIP_SHAPE_MISMATCH;
-  *physical_out = ln.page_of[logical_page];
+  if (logical_page >= ln.kv.page_of.size()) return GLACIER_HIP_SHAPE_MISMATCH;
+  *physical_out = ln.kv.page_of[logical_page];
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_session_page_generation(glacier_hip_session *s, uint32_t lane,
+                                        uint32_t logical_page, uint64_t *ownership_generation_out) {
+  if (!s || !ownership_generation_out || lane >= s->lanes.size()) return GLACIER_HIP_INVALID_ARGUMENT;
+  const Lane &ln = s->lanes[lane];
+  if (logical_page >= ln.kv.page_gen.size()) return GLACIER_HIP_SHAPE_MISMATCH;
+  *ownership_generation_out = ln.kv.page_gen[logical_page];
   return GLACIER_HIP_OK;
 }
 
@@ -1361,39 +1269,34 @@ extern "C" int glacier_hip_session_lane_weave_wave(
   *count_out = 0;
   const uint32_t L = (uint32_t)s->lanes.size();
   if (max_count == 0 || max_count > L) return GLACIER_HIP_SHAPE_MISMATCH;
-  std::vector<uint32_t> plan(max_count);
-  uint32_t n = 0;
-  int rc = glacier_hip_lane_weave_plan_wave(lw, max_count, plan.data(), &n);
-  if (rc) return rc;
-  if (n == 0) return GLACIER_HIP_NO_RUNNABLE;
-  std::vector<uint32_t> lanes(n), toks(n), next(n);
-  for (uint32_t i = 0; i < n; ++i) {
-    if (plan[i] >= slot_count || lane_of_slot[plan[i]] >= L) return GLACIER_HIP_SHAPE_MISMATCH;
-    lanes[i] = lane_of_slot[plan[i]];
-    toks[i] = tokens_by_lane[lanes[i]];
-  }
   const uint64_t W = (s->model->cfg.vocab_size + 63) / 64;
-  std::vector<uint64_t> elig;
-  if (eligible_by_lane) {
-    elig.resize((size_t)n * W);
-    for (uint32_t i = 0; i < n; ++i)
-      memcpy(&elig[(size_t)i * W], eligible_by_lane + (size_t)lanes[i] * W, W * 8);
-  }
-  // the device step commits its KV rows, tokens and sampler counters only on
-  // success; then the scheduler commits the same quanta in plan order
-  rc = glacier_hip_session_decode_step(s, lanes.data(), toks.data(), n,
-                                       eligible_by_lane ? elig.data() : nullptr, next.data(),
-                                       nullptr);
-  if (rc) return rc;
-  for (uint32_t i = 0; i < n; ++i) {
-    glacier_hip_lane_event_t ev;
-    rc = glacier_hip_lane_weave_serve_one(lw, &ev);
-    if (rc) return rc;
-    if (ev.handle.slot_index != plan[i]) return GLACIER_HIP_SCHEDULER_POISONED;
+  std::vector<uint32_t> lanes, next;
+  auto step = [&](const uint32_t *plan, uint32_t n) -> int {
+    lanes.resize(n);
+    next.resize(n);
+    std::vector<uint32_t> toks(n);
+    for (uint32_t i = 0; i < n; ++i) {
+      if (plan[i] >= slot_count || lane_of_slot[plan[i]] >= L) return GLACIER_HIP_SHAPE_MISMATCH;
+      lanes[i] = lane_of_slot[plan[i]];
+      toks[i] = tokens_by_lane[lanes[i]];
+    }
+    std::vector<uint64_t> elig;
+    if (eligible_by_lane) {
+      elig.resize((size_t)n * W);
+      for (uint32_t i = 0; i < n; ++i)
+        memcpy(&elig[(size_t)i * W], eligible_by_lane + (size_t)lanes[i] * W, W * 8);
+    }
+    // the device step commits its KV rows, tokens and sampler counters only
+    // on success; the scheduler then commits the same quanta in plan order
+    return glacier_hip_session_decode_step(s, lanes.data(), toks.data(), n,
+                                           eligible_by_lane ? elig.data() : nullptr, next.data(),
+                                           nullptr);
+  };
+  const int rc = gh::lane_weave_run_wave(lw, max_count, step, slots_out, events_out, count_out);
+  // tokens of the quanta the device step committed (all of them, unless the
+  // scheduler was poisoned after the commit)
+  for (uint32_t i = 0; i < (uint32_t)next.size() && (rc == GLACIER_HIP_OK ||
+                                                    rc == GLACIER_HIP_SCHEDULER_POISONED); ++i)
     tokens_by_lane[lanes[i]] = next[i];
-    if (slots_out) slots_out[i] = plan[i];
-    if (events_out) events_out[i] = ev;
-    *count_out = i + 1;
-  }
-  return GLACIER_HIP_OK;
+  return rc;
 }

@@ -23,7 +23,10 @@ ELIGIBLE_NAN = 7
 CACHE_FULL = 8
 NO_DEVICE = 9
 INVALID_HANDLE = 10
+TRANSACTION_ACTIVE = 11
+INVALID_TRANSACTION = 12
 BUSY = 13
+UNSUPPORTED = 14
 
 F32, F16, BF16 = 0, 1, 2
 ACT_Q8, ACT_F32, ACT_AUTO = 0, 1, 2
@@ -103,9 +106,27 @@ class SessionOptions(C.Structure):
 
 
 class PageMapRoot(C.Structure):
-    _fields_ = [("cache_instance", C.c_uint64), ("generation", C.c_uint64),
-                ("committed_len", C.c_uint64), ("committed_pages", C.c_uint64),
-                ("ownership_sha256", C.c_uint8 * 32)]
+    _fields_ = [("abi_version", C.c_uint64), ("cache_instance", C.c_uint64),
+                ("generation", C.c_uint64), ("committed_len", C.c_uint64),
+                ("committed_pages", C.c_uint64), ("ownership_sha256", C.c_uint8 * 32)]
+
+
+class PageRef(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("abi_version", "cache_instance", "logical_page",
+                                          "ownership_generation")]
+
+
+class RowTxnMark(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("abi_version", "cache_id", "cache_instance", "generation",
+                                          "base_len", "row_count", "root_before_generation",
+                                          "root_after_generation")] + [("page_ref", PageRef)]
+
+
+class ResidentLedger(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in (
+        "page_count_capacity", "allocated_pages", "committed_pages", "provisional_pages",
+        "reusable_pages", "page_map_bytes", "resident_tensor_payload_bytes",
+        "resident_allocation_bytes", "committed_tensor_payload_bytes")]
 
 
 class LaneState(C.Structure):
@@ -218,6 +239,21 @@ _SIGS = [
     ("glacier_hip_session_read_kv_row", C.c_int,
      [_P, C.c_uint32, C.c_uint32, C.c_int, C.c_uint32, _P]),
     ("glacier_hip_session_page_of", C.c_int, [_P, C.c_uint32, C.c_uint32, C.POINTER(C.c_int32)]),
+    ("glacier_hip_session_page_generation", C.c_int,
+     [_P, C.c_uint32, C.c_uint32, C.POINTER(C.c_uint64)]),
+    ("glacier_hip_kv_pages_create", _P, [C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32]),
+    ("glacier_hip_kv_pages_destroy", None, [_P]),
+    ("glacier_hip_kv_pages_begin_row", C.c_int, [_P, C.POINTER(RowTxnMark)]),
+    ("glacier_hip_kv_pages_commit_row", C.c_int, [_P, C.POINTER(RowTxnMark)]),
+    ("glacier_hip_kv_pages_abort_row", C.c_int, [_P, C.POINTER(RowTxnMark)]),
+    ("glacier_hip_kv_pages_staged_root", C.c_int,
+     [_P, C.POINTER(RowTxnMark), C.POINTER(PageMapRoot), C.POINTER(PageMapRoot)]),
+    ("glacier_hip_kv_pages_reset", C.c_int, [_P]),
+    ("glacier_hip_kv_pages_root", C.c_int, [_P, C.POINTER(PageMapRoot)]),
+    ("glacier_hip_kv_pages_page", C.c_int,
+     [_P, C.c_uint32, C.POINTER(C.c_int32), C.POINTER(C.c_uint64)]),
+    ("glacier_hip_kv_pages_validate_page_ref", C.c_int, [_P, C.POINTER(PageRef)]),
+    ("glacier_hip_kv_pages_ledger", C.c_int, [_P, C.POINTER(ResidentLedger)]),
     ("glacier_hip_session_inject_failure", C.c_int, [_P, C.c_int]),
     ("glacier_hip_synth_int4", None, [C.c_uint64, C.c_uint64, _P, C.c_uint64]),
     ("glacier_hip_synth_scales_f16", None, [C.c_uint64, C.c_uint64, C.c_float, _P, C.c_uint64]),
@@ -503,6 +539,12 @@ class Session:
         check(lib().glacier_hip_session_page_of(self.h, lane, logical_page, C.byref(v)), "page_of")
         return v.value
 
+    def page_generation(self, lane, logical_page):
+        v = C.c_uint64()
+        check(lib().glacier_hip_session_page_generation(self.h, lane, logical_page, C.byref(v)),
+              "page_generation")
+        return v.value
+
     def inject_failure(self, enable):
         check(lib().glacier_hip_session_inject_failure(self.h, 1 if enable else 0), "inject")
 
@@ -510,6 +552,61 @@ class Session:
         if self.h:
             lib().glacier_hip_session_destroy(self.h)
             self.h = None
+
+
+class KvPages:
+    """Host page map of one paged KV cache (glacier_hip_kv_pages_*): the
+    reference's PagedKVCache row transaction without a device."""
+
+    def __init__(self, num_layers, kv_dim, max_seq, pool_pages):
+        self.h = lib().glacier_hip_kv_pages_create(num_layers, kv_dim, max_seq, pool_pages)
+        if not self.h:
+            raise GlacierHipError(INVALID_ARGUMENT, "kv_pages_create")
+
+    def begin_row(self):
+        m = RowTxnMark()
+        rc = lib().glacier_hip_kv_pages_begin_row(self.h, C.byref(m))
+        return rc, m
+
+    def commit_row(self, mark):
+        return lib().glacier_hip_kv_pages_commit_row(self.h, C.byref(mark))
+
+    def abort_row(self, mark):
+        return lib().glacier_hip_kv_pages_abort_row(self.h, C.byref(mark))
+
+    def staged_roots(self, mark):
+        b, a = PageMapRoot(), PageMapRoot()
+        rc = lib().glacier_hip_kv_pages_staged_root(self.h, C.byref(mark), C.byref(b), C.byref(a))
+        return rc, b, a
+
+    def reset(self):
+        return lib().glacier_hip_kv_pages_reset(self.h)
+
+    def root(self):
+        r = PageMapRoot()
+        check(lib().glacier_hip_kv_pages_root(self.h, C.byref(r)), "kv_pages_root")
+        return r
+
+    def page(self, logical_page):
+        p, g = C.c_int32(), C.c_uint64()
+        check(lib().glacier_hip_kv_pages_page(self.h, logical_page, C.byref(p), C.byref(g)),
+              "kv_pages_page")
+        return p.value, g.value
+
+    def validate_page_ref(self, ref):
+        return lib().glacier_hip_kv_pages_validate_page_ref(self.h, C.byref(ref))
+
+    def ledger(self):
+        led = ResidentLedger()
+        check(lib().glacier_hip_kv_pages_ledger(self.h, C.byref(led)), "kv_pages_ledger")
+        return {n: getattr(led, n) for n, _ in ResidentLedger._fields_}
+
+    def close(self):
+        if self.h:
+            lib().glacier_hip_kv_pages_destroy(self.h)
+            self.h = None
+
+    __del__ = close
 
 
 STALE_HANDLE, NO_RUNNABLE, INCOMPLETE_DRAIN, SCHEDULER_CLOSED, SCHEDULER_POISONED = 15, 16, 17, 18, 19

@@ -318,12 +318,67 @@ typedef struct {
 } glacier_hip_session_options_t;
 
 typedef struct {
+    uint64_t abi_version;        /* 0x47504d5200000001 */
     uint64_t cache_instance;
     uint64_t generation;
     uint64_t committed_len;
     uint64_t committed_pages;
     uint8_t ownership_sha256[32];
 } glacier_hip_page_map_root_t;     /* PageMapRootV1 (paged_kv_cache.zig:64-71) */
+
+typedef struct {
+    uint64_t abi_version;        /* 0x4750524600000001 */
+    uint64_t cache_instance;
+    uint64_t logical_page;
+    uint64_t ownership_generation;
+} glacier_hip_page_ref_t;          /* PageRefV1 (paged_kv_cache.zig:55-60) */
+
+typedef struct {
+    uint64_t abi_version;        /* 0x4750525400000001 */
+    uint64_t cache_id;           /* identity of the page map that staged the row */
+    uint64_t cache_instance;
+    uint64_t generation;         /* row transaction generation */
+    uint64_t base_len;
+    uint64_t row_count;          /* 1 */
+    uint64_t root_before_generation;
+    uint64_t root_after_generation;
+    glacier_hip_page_ref_t page_ref;
+} glacier_hip_row_txn_mark_t;      /* RowTxnMark (paged_kv_cache.zig:255-265) */
+
+typedef struct {
+    uint64_t page_count_capacity, allocated_pages, committed_pages, provisional_pages;
+    uint64_t reusable_pages, page_map_bytes, resident_tensor_payload_bytes;
+    uint64_t resident_allocation_bytes, committed_tensor_payload_bytes;
+} glacier_hip_kv_resident_ledger_t; /* ResidentLedger (paged_kv_cache.zig:92-102), f32 payloads */
+
+/* ---- host page map of one paged KV cache (no device) ----------------------
+ * The page-map half of the reference's PagedKVCache (paged_kv_cache.zig:
+ * 511-1520) over a pool of `pool_pages` payload slots: beginRow (:1006-1072)
+ * consumes the next page ownership generation (on a page's row 0) and the
+ * next root generation whether or not the row commits; abortRow (:1146-1158)
+ * only clears the page's ownership generation, so a retry reuses the payload
+ * under a fresh generation; reset (:1162-1182) invalidates every root and
+ * page ref and keeps the payloads. Sessions run the same transaction for
+ * each lane over their device pool. One staged row at a time. */
+typedef struct glacier_hip_kv_pages glacier_hip_kv_pages;
+glacier_hip_kv_pages *glacier_hip_kv_pages_create(uint32_t num_layers, uint32_t kv_dim,
+                                                  uint32_t max_seq, uint32_t pool_pages);
+void glacier_hip_kv_pages_destroy(glacier_hip_kv_pages *p);
+int glacier_hip_kv_pages_begin_row(glacier_hip_kv_pages *p, glacier_hip_row_txn_mark_t *mark_out);
+int glacier_hip_kv_pages_commit_row(glacier_hip_kv_pages *p, const glacier_hip_row_txn_mark_t *mark);
+int glacier_hip_kv_pages_abort_row(glacier_hip_kv_pages *p, const glacier_hip_row_txn_mark_t *mark);
+/* prepareCommit (:1105-1118): the roots the staged row moves between. */
+int glacier_hip_kv_pages_staged_root(glacier_hip_kv_pages *p, const glacier_hip_row_txn_mark_t *mark,
+                                     glacier_hip_page_map_root_t *before,
+                                     glacier_hip_page_map_root_t *after);
+int glacier_hip_kv_pages_reset(glacier_hip_kv_pages *p);
+int glacier_hip_kv_pages_root(glacier_hip_kv_pages *p, glacier_hip_page_map_root_t *out);
+/* Payload slot (-1 = none) and ownership generation (0 = not owned) of a logical page. */
+int glacier_hip_kv_pages_page(glacier_hip_kv_pages *p, uint32_t logical_page,
+                              int32_t *physical_out, uint64_t *ownership_generation_out);
+/* validateCommittedPageRef (:944-957): OK or INVALID_TRANSACTION. */
+int glacier_hip_kv_pages_validate_page_ref(glacier_hip_kv_pages *p, const glacier_hip_page_ref_t *ref);
+int glacier_hip_kv_pages_ledger(glacier_hip_kv_pages *p, glacier_hip_kv_resident_ledger_t *out);
 
 typedef struct {
     uint64_t kv_positions;
@@ -366,9 +421,12 @@ int glacier_hip_session_lane_kv_sha256(glacier_hip_session *s, uint32_t lane, ui
 /* Copy one K or V row (f32) of a lane out of the paged pool. */
 int glacier_hip_session_read_kv_row(glacier_hip_session *s, uint32_t lane, uint32_t layer,
                                     int value, uint32_t position, float *out_host);
-/* Physical page of a lane's logical page (-1 if not installed). */
+/* Physical page holding a lane's logical page (-1 if none; an aborted
+ * install keeps its payload, with ownership generation 0). */
 int glacier_hip_session_page_of(glacier_hip_session *s, uint32_t lane, uint32_t logical_page,
                                 int32_t *physical_out);
+int glacier_hip_session_page_generation(glacier_hip_session *s, uint32_t lane,
+                                        uint32_t logical_page, uint64_t *ownership_generation_out);
 /* Test hook: make the next decode step fail after its kernels ran but before
  * commit (forces the abort path, as a failed sink/ack would). */
 int glacier_hip_session_inject_failure(glacier_hip_session *s, int enable);
@@ -495,8 +553,11 @@ int glacier_hip_lane_weave_state_sha256(glacier_hip_lane_weave *lw, uint8_t out[
  * optional [session max_lanes][ceil(vocab/64)] masks (eligible argmax,
  * sampling.zig:55-105). slots_out / events_out (optional) receive the
  * committed slots and their Event-v1 records; count_out the number of quanta.
- * A failed device step commits nothing: no KV row, token, sampler counter or
- * scheduler event. NO_RUNNABLE when no lane is runnable. */
+ * The scheduler stays locked from planning to commit, and the plan holds
+ * only quanta whose serve_one commits (it stops before a deadline or service
+ * gap the next quantum would break). A failed device step commits nothing:
+ * no KV row, token, sampler counter or scheduler event. NO_RUNNABLE when no
+ * lane is runnable. */
 int glacier_hip_session_lane_weave_wave(glacier_hip_session *s, glacier_hip_lane_weave *lw,
                                         const uint32_t *lane_of_slot, uint32_t slot_count,
                                         uint32_t *tokens_by_lane,

@@ -39,7 +39,8 @@ class Model(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in ("num_layers", "dim", "hidden_dim", "num_heads",
                                           "num_kv_heads", "head_dim", "vocab_size", "group_size")] + \
         [("rms_eps", C.c_float), ("rope_theta", C.c_float), ("token_embedding", _P),
-         ("final_norm", _P), ("lm_head", Int4Weight), ("layers", _P), ("kv_fp16", C.c_uint32)]
+         ("final_norm", _P), ("lm_head", Int4Weight), ("layers", _P), ("kv_fp16", C.c_uint32),
+         ("int4_activation_f32", C.c_uint32)]
 
 
 class Ledger(C.Structure):
@@ -76,6 +77,7 @@ def lib():
             "go_argmax": (sz, [_P, sz]),
             "go_argmax_eligible": (C.c_int, [_P, sz, _P, sz, C.POINTER(sz), C.POINTER(sz)]),
             "go_generate": (C.c_int, [C.POINTER(Model), _P, sz, sz, _P, _P, sz, _P, _P, _P]),
+            "go_forward_layer": (C.c_int, [C.POINTER(Model), sz, _P, _P, _P, sz, _P, _P, _P]),
             "go_sha256": (None, [_P, sz, _P]),
             "go_paged_capacity_ledger": (C.c_int, [C.c_uint64] * 3 + [C.POINTER(Ledger)]),
             "go_paged_empty_ownership_digest": (None, [C.c_uint64] * 4 + [_P]),
@@ -259,7 +261,7 @@ def xoshiro256_init(seed):
 class OracleModel:
     """Keeps the numpy tensors alive while the C model struct points at them."""
 
-    def __init__(self, cfg, host, kv_fp16=False):
+    def __init__(self, cfg, host, kv_fp16=False, act_f32=False):
         self.cfg = cfg
         self.host = host
         self._keep = []
@@ -291,7 +293,23 @@ class OracleModel:
                        cfg["num_kv_heads"], cfg["head_dim"], cfg["vocab_size"], cfg["group_size"],
                        cfg["rms_eps"], cfg["rope_theta"], arr(host["embedding"]),
                        arr(host["final_norm"]), w(host["lm_head"], host["lm_head_scales"]),
-                       C.cast(layers, _P), 1 if kv_fp16 else 0)
+                       C.cast(layers, _P), 1 if kv_fp16 else 0, 1 if act_f32 else 0)
+
+    def forward_layer(self, li, xs):
+        """go_forward_layer over rows xs[t] at positions t = 0..T-1 (token at a
+        time over a contiguous f32 KV cache); returns the layer outputs [T, dim]."""
+        xs = f32(xs)
+        T, D = xs.shape
+        kvd = self.cfg["num_kv_heads"] * self.cfg["head_dim"]
+        kc = np.zeros((T, kvd), np.float32)
+        vc = np.zeros((T, kvd), np.float32)
+        cs, sn = rope_table(T, self.cfg["head_dim"], self.cfg["rope_theta"])
+        out = np.zeros_like(xs)
+        for t in range(T):
+            rc = lib().go_forward_layer(C.byref(self.m), li, _p(xs[t]), _p(kc), _p(vc), t,
+                                        _p(cs), _p(sn), _p(out[t]))
+            assert rc == OK, rc
+        return out
 
     def generate(self, prompt, max_new, logits_steps=()):
         prompt = np.ascontiguousarray(prompt, dtype=np.uint32)

@@ -563,10 +563,14 @@ int go_argmax_eligible(const float *logits, size_t n, const uint64_t *words,
 /* ------------------------------------------------------------------------ */
 /* a9-a11: one layer and the greedy token loop                               */
 /* ------------------------------------------------------------------------ */
-static int project(const float *x, go_int4_weight w, const float *bias, float *out,
-                   size_t out_f, size_t in_f, size_t gs) {
-    /* generate.zig:3550-3600 linearInt4Decode with no pool and .q8 activation
-     * (prepared_text_session.zig:81-105 num_threads = 1) -> linearInt4WeightQ8 */
+static int project(const go_model *m, const float *x, go_int4_weight w, const float *bias,
+                   float *out, size_t out_f, size_t in_f, size_t gs) {
+    /* generate.zig:3550-3596 linearInt4Decode with no pool: the .q8 activation
+     * (the default, generate.zig:925; prepared_text_session.zig:81-105
+     * num_threads = 1) -> linearInt4WeightQ8 with its x86 dispatch; .f32 ->
+     * linearInt4Weight (int4_matmul.zig:2957-2981) -> linearInt4OnTheFly */
+    if (m->int4_activation_f32)
+        return go_linear_int4_f32(x, 1, w.packed, w.scales, bias, out, out_f, in_f, gs);
     return go_linear_int4_weight_q8(x, 1, w.packed, w.scales, bias, out, out_f, in_f, gs);
 }
 
@@ -585,9 +589,9 @@ int go_forward_layer(const go_model *m, size_t li, const float *x_row,
     /* generate.zig:1561 */
     go_rmsnorm(x_row, 1, dim, L->input_norm, m->rms_eps, h_norm);
     /* Q, K, V projections (:1668-1700) */
-    if ((rc = project(h_norm, L->wq, L->bq, q, dim, dim, gs))) goto done;
-    if ((rc = project(h_norm, L->wk, L->bk, k, kv_dim, dim, gs))) goto done;
-    if ((rc = project(h_norm, L->wv, L->bv, v, kv_dim, dim, gs))) goto done;
+    if ((rc = project(m, h_norm, L->wq, L->bq, q, dim, dim, gs))) goto done;
+    if ((rc = project(m, h_norm, L->wk, L->bk, k, kv_dim, dim, gs))) goto done;
+    if ((rc = project(m, h_norm, L->wv, L->bv, v, kv_dim, dim, gs))) goto done;
     /* RoPE on k, append row, RoPE on q (:1712-1735) */
     go_rope_apply(rope_cos, rope_sin, hd / 2, k, pos, m->num_kv_heads, hd);
     if (m->kv_fp16)
@@ -602,14 +606,14 @@ int go_forward_layer(const go_model *m, size_t li, const float *x_row,
     if ((rc = go_attention(q, 1, k_cache, v_cache, pos + 1, attn, m->num_heads,
                            m->num_kv_heads, hd))) goto done;
     /* O projection, residual, post-attention norm (:1763-1768) */
-    if ((rc = project(attn, L->wo, NULL, proj, dim, dim, gs))) goto done;
+    if ((rc = project(m, attn, L->wo, NULL, proj, dim, dim, gs))) goto done;
     for (size_t i = 0; i < dim; i++) h[i] = x_row[i] + proj[i];
     go_rmsnorm(h, 1, dim, L->post_attn_norm, m->rms_eps, mlp_norm);
     /* gate, up, SiLU * up, down, residual (:1844-1965, x86 branch) */
-    if ((rc = project(mlp_norm, L->w_gate, NULL, gate, hidden, dim, gs))) goto done;
-    if ((rc = project(mlp_norm, L->w_up, NULL, up, hidden, dim, gs))) goto done;
+    if ((rc = project(m, mlp_norm, L->w_gate, NULL, gate, hidden, dim, gs))) goto done;
+    if ((rc = project(m, mlp_norm, L->w_up, NULL, up, hidden, dim, gs))) goto done;
     go_silu_mul(gate, up, act, hidden);
-    if ((rc = project(act, L->w_down, NULL, proj, dim, hidden, gs))) goto done;
+    if ((rc = project(m, act, L->w_down, NULL, proj, dim, hidden, gs))) goto done;
     for (size_t i = 0; i < dim; i++) out_row[i] = h[i] + proj[i];
 done:
     free(buf);
@@ -665,7 +669,7 @@ int go_generate(const go_model *m, const uint32_t *prompt, size_t prompt_len,
             pos++;
         }
         go_rmsnorm(x, 1, dim, m->final_norm, m->rms_eps, fh);
-        rc = project(fh, m->lm_head, NULL, logits, V, dim, m->group_size);
+        rc = project(m, fh, m->lm_head, NULL, logits, V, dim, m->group_size);
         if (rc) goto out;
         for (size_t i = 0; i < n_logits_steps; i++)
             if (logits_steps[i] == (int32_t)step)

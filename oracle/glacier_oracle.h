@@ -142,6 +142,9 @@ typedef struct {
                                    * them (paged_kv_cache.zig:1-8); 1: rows
                                    * rounded to fp16 on store (the fp16 page
                                    * pools of the GPU path) */
+    uint32_t int4_activation_f32; /* 0: .q8 (generate.zig:925 default, with the
+                                   * x86 f32 fallbacks); 1: .f32 for every
+                                   * projection and the head */
 } go_model;
 
 /* Greedy generate. tokens_out gets max_new tokens. If logits_steps/logits_out

@@ -169,43 +169,114 @@ def test_page_roots_follow_reference_chain(gh, tiny, ora):
 
 
 def test_failed_step_publishes_nothing(gh, tiny):
+    """A failed step publishes nothing (KV length, root, sampler counter, RNG,
+    output digest unchanged), and its row transaction consumes the page and
+    root generations as the reference's beginRow does (paged_kv_cache.zig:
+    1011-1072); abortRow only clears the page's ownership generation
+    (:1146-1158), so the retry reuses the payload under a fresh generation
+    (:1946-1985). The lane's root after every step equals the oracle page
+    map's replay of the same begin / abort / commit sequence."""
+    from oracle import paged_kv as opk
+
     host, om, m = tiny
+    kvd = TINY["num_kv_heads"] * TINY["head_dim"]
     sess = gh.Session(m, max_lanes=1, max_positions=64)
+
+    def same(root, cache):
+        r = cache.root()
+        return (root.abi_version, root.cache_instance, root.generation, root.committed_len,
+                root.committed_pages, bytes(root.ownership_sha256)) == r.key()
+
     try:
         sess.begin(0)
+        ref = opk.PagedKVCache(TINY["num_layers"], kvd, 64, instance=sess.root(0).cache_instance)
         prompt = gh.synth_tokens(SEED, 6, TINY["vocab_size"], 15)
         t0 = sess.prefill(0, prompt)
-        before_root, before_state = sess.root(0), sess.state(0)
+        for _ in range(15):
+            ref.commit_row(ref.begin_row())
+        assert same(sess.root(0), ref)
+        before_root, before_state = bytes(sess.root(0)), bytes(sess.state(0))
+        # row 15 (inside page 0) fails after its kernels ran
         sess.inject_failure(True)
         rc, _ = sess.step([0], [t0], raise_on_error=False)
         assert rc == gh.DEVICE_ERROR
         sess.inject_failure(False)
-        after_root, after_state = sess.root(0), sess.state(0)
-        assert bytes(after_root) == bytes(before_root)  # row 15 -> page 0, no install
-        assert bytes(after_state) == bytes(before_state)
-        # the retried step (it installs page 1 at row 16 next) matches a clean run
+        ref.abort_row(ref.begin_row())
+        assert bytes(sess.root(0)) == before_root and bytes(sess.state(0)) == before_state
+        assert same(sess.root(0), ref)
+        # the retry commits under root generation 1 + 15 + 2, not + 1
         t1 = int(sess.step([0], [t0])[0])
-        t2 = int(sess.step([0], [t1])[0])
+        ref.commit_row(ref.begin_row())
+        assert same(sess.root(0), ref) and sess.root(0).generation == 18
+        t2 = int(sess.step([0], [t1])[0])  # row 16 installs page 1
+        ref.commit_row(ref.begin_row())
+        assert same(sess.root(0), ref)
         clean = gh.Session(m, max_lanes=1, max_positions=64)
         clean.begin(0)
         c0 = clean.prefill(0, prompt)
         c1 = int(clean.step([0], [c0])[0])
         c2 = int(clean.step([0], [c1])[0])
-        assert (t0, t1, t2) == (c0, c1, c2)
-        assert sess.root(0).committed_pages == clean.root(0).committed_pages
         clean.close()
-        # an abort on a page-installing row releases the page and its generation
-        pages_before = sess.root(0).committed_pages
-        sess.inject_failure(False)
+        assert (t0, t1, t2) == (c0, c1, c2)  # an abort changes no token
         for _ in range(15):
             t2 = int(sess.step([0], [t2])[0])
-        assert sess.root(0).committed_len == 32
+            ref.commit_row(ref.begin_row())
+        assert sess.root(0).committed_len == 32 and same(sess.root(0), ref)
+        # row 32 installs page 2 and fails: the payload stays with logical page 2
         sess.inject_failure(True)
         rc, _ = sess.step([0], [t2], raise_on_error=False)
-        assert rc == gh.DEVICE_ERROR and sess.page_of(0, 2) == -1
+        assert rc == gh.DEVICE_ERROR
         sess.inject_failure(False)
-        sess.step([0], [t2])
-        assert sess.root(0).committed_pages == pages_before + 1
+        mark = ref.begin_row()
+        aborted_gen = mark.ownership_generation
+        ref.abort_row(mark)
+        assert same(sess.root(0), ref)
+        page = sess.page_of(0, 2)
+        assert page >= 0 and sess.page_generation(0, 2) == 0
+        t3 = int(sess.step([0], [t2])[0])
+        mark = ref.begin_row()
+        ref.commit_row(mark)
+        assert sess.page_of(0, 2) == page                      # payload reused
+        assert sess.page_generation(0, 2) == mark.ownership_generation != aborted_gen
+        assert same(sess.root(0), ref)
+        assert sess.state(0).kv_positions == 33
+        del t3
+    finally:
+        sess.close()
+
+
+@pytest.mark.parametrize("lanes", [3, 4, 5])
+def test_f32_activation_lanes_match_oracle(gh, tiny, ora, lanes):
+    """Sessions with layer_activation = head_activation = F32 (the reference's
+    int4_activation = .f32, generate.zig:925,3550-3596; the oracle's f32
+    mode) decoding 3-5 lanes together: every projection and the LM head run
+    on three-digit planes at 3-5 rows. Tokens equal the oracle's; logits
+    within 1e-2 max-relative at the last step."""
+    host, _, m = tiny
+    om = ora.OracleModel(TINY, host, act_f32=True)
+    V = TINY["vocab_size"]
+    prompts = [gh.synth_tokens(SEED, 60 + i, V, 9 + 5 * i) for i in range(lanes)]
+    max_new = 8
+    wants = [om.generate(p, max_new, logits_steps=[max_new - 1]) for p in prompts]
+    sess = gh.Session(m, max_lanes=lanes, max_positions=64, layer_activation=gh.ACT_F32,
+                      head_activation=gh.ACT_F32)
+    try:
+        toks = []
+        for i, p in enumerate(prompts):
+            sess.begin(i)
+            toks.append([sess.prefill(i, p)])
+        order = list(range(lanes))[::-1]
+        last = None
+        for step in range(1, max_new):
+            nxt, lg = sess.step(order, [toks[i][-1] for i in order], want_logits=True)
+            for j, i in enumerate(order):
+                toks[i].append(int(nxt[j]))
+            last = lg
+        for j, i in enumerate(order):
+            assert toks[i] == wants[i][0].tolist(), i
+            rel = _rel(last[j], wants[i][1][0])
+            print("lane", i, "logit rel", rel)
+            assert rel < 1e-2
     finally:
         sess.close()
 
@@ -403,5 +474,47 @@ def test_lane_weave_waves_match_serial_oracle(gh, gctx, tiny, ora):
         for i in range(cap):
             want = om.generate(prompts[i], quanta[i] + 1)[0].tolist()
             assert got[i] == want, (i, got[i], want)
+    finally:
+        sess.close()
+
+
+def test_concurrent_submission_is_rejected_busy(gh, tiny):
+    """One submission at a time per context: a second submission from another
+    thread while one is in flight returns BUSY instead of queueing
+    (acquireSubmission, int4_executor.zig:2267-2270; the reference's test
+    'executor rejects concurrent submissions and remains reusable' :6029), and
+    the context is usable again afterwards."""
+    import threading
+
+    host, om, m = tiny
+    sess = gh.Session(m, max_lanes=2, max_positions=2048, prefill_chunk=16)
+    try:
+        sess.begin(0)
+        sess.begin(1)
+        t1 = sess.prefill(1, gh.synth_tokens(SEED, 71, TINY["vocab_size"], 4))
+        long_prompt = gh.synth_tokens(SEED, 70, TINY["vocab_size"], 2000)
+        started, done = threading.Event(), threading.Event()
+        out = {}
+
+        def run():
+            started.set()
+            out["tok"] = sess.prefill(0, long_prompt)  # 125 chunks under one lease
+            done.set()
+
+        th = threading.Thread(target=run)
+        th.start()
+        started.wait()
+        codes = []
+        while not done.is_set():  # steps that slip in before the prefill takes the lease succeed
+            rc, _ = sess.step([1], [t1], raise_on_error=False)
+            codes.append(rc)
+        th.join()
+        busy = sum(c == gh.BUSY for c in codes)
+        print("attempts", len(codes), "busy", busy)
+        assert busy >= 1
+        assert all(c in (gh.BUSY, gh.OK) for c in codes)
+        # the lease is released: both lanes step again
+        nxt = sess.step([0, 1], [out["tok"], t1])
+        assert len(nxt) == 2
     finally:
         sess.close()

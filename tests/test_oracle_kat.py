@@ -376,3 +376,80 @@ def test_ownership_digest_formulas(ora):
 def test_xoshiro_seeding_splitmix_known_answer(ora):
     # SplitMix64 with seed 0: first output 0xe220a8397b1dcdaf (published sequence)
     assert ora.xoshiro256_init(0)[0] == 0xE220A8397B1DCDAF
+
+
+# ---- a9: the layer composition ------------------------------------------------------
+def test_forward_layer_f32_matches_reference_layer_composition(ora):
+    """go_forward_layer in the reference's int4_activation = .f32 mode against
+    tests/golden/layer_qwen05b.npz: one Qwen2.5-0.5B-shaped layer over 8
+    positions composed by tests/golden/make_layer_golden.py from the
+    reference's own rmsnorm / rope / softmax / silu
+    (tools/reference_layer0.py, composition of its main() :107-170) on the
+    dequantized weights. Pins RoPE before the KV append, GQA h // group, the
+    q/k/v biases, both residuals, the post-attention norm and SiLU(gate) * up.
+    Bar 1e-5 max-relative (f32 against f32, different summation order)."""
+    import os
+    import sys
+
+    sys.path.insert(0, os.path.join(os.path.dirname(__file__), "golden"))
+    import layer_case
+
+    layer, _, x = layer_case.make()
+    cfg = layer_case.CFG
+    D, V = cfg["dim"], cfg["vocab_size"]
+    host = dict(layers=[layer], embedding=np.zeros((V, D), np.float32),
+                final_norm=np.ones(D, np.float32),
+                lm_head=np.full(V * D // 2, 0x77, np.uint8),
+                lm_head_scales=np.zeros(V * D // 32, np.float32))
+    fx = np.load(os.path.join(os.path.dirname(__file__), "golden", "layer_qwen05b.npz"))
+    assert int(fx["seed"]) == layer_case.SEED and int(fx["T"]) == layer_case.T
+    om = ora.OracleModel(cfg, host, act_f32=True)
+    got = om.forward_layer(0, x)
+    rel = float(np.max(np.abs(got - fx["out"])) / np.max(np.abs(fx["out"])))
+    assert rel < 1e-5, rel
+    # the default .q8 mode stays close (Q8 activations, int4_matmul.zig:3375)
+    q8 = ora.OracleModel(cfg, host).forward_layer(0, x)
+    rel_q8 = float(np.max(np.abs(q8 - fx["out"])) / np.max(np.abs(fx["out"])))
+    assert 1e-5 < rel_q8 < 5e-2, rel_q8
+
+
+def _q8_brute(x, packed, scales, out_f, in_f):
+    """Closed form of linearInt4Q8OnTheFly (int4_matmul.zig:365-418): per
+    32-group s = max|x|/127, q = clamp(round_half_away(x * (1/s)), +-127), exact
+    integer group dots, acc += (f32(dot) * w_scale) * s in group order."""
+    x = x.astype(np.float32)
+    G = in_f // 32
+    xs = x.reshape(G, 32)
+    s = (np.max(np.abs(xs), axis=1) / np.float32(127)).astype(np.float32)
+    inv = np.where(s > 0, np.float32(1) / np.where(s > 0, s, 1), 0).astype(np.float32)
+    v = (xs * inv[:, None]).astype(np.float32)
+    q = np.clip(np.sign(v) * np.floor(np.abs(v) + np.float32(0.5)), -127, 127).astype(np.int64)
+    codes = np.empty(out_f * in_f, np.int64)
+    codes[0::2] = packed & 0xF
+    codes[1::2] = packed >> 4
+    w = (codes - 7).reshape(out_f, G, 32)
+    dots = np.einsum("ogk,gk->og", w, q)
+    ws = scales.reshape(out_f, G).astype(np.float32)
+    acc = np.zeros(out_f, np.float32)
+    for g in range(G):
+        t = (dots[:, g].astype(np.float32) * ws[:, g]).astype(np.float32)
+        acc = (acc + (t * s[g]).astype(np.float32)).astype(np.float32)
+    return acc
+
+
+@pytest.mark.parametrize("in_f", [16384, 16416])
+def test_q8_wide_input_fallback_boundary(ora, in_f):
+    """int4_matmul.zig:372-374: Q8 activations up to in_f = 16384 (512 groups
+    of 32); past it the exact f32 path (linearInt4OnTheFly)."""
+    rng = np.random.default_rng(in_f)
+    out_f = 16
+    x = rng.standard_normal(in_f).astype(np.float32)
+    packed = rng.integers(0, 256, out_f * in_f // 2, dtype=np.uint8)
+    scales = np.abs(rng.normal(0, 0.02, out_f * in_f // 32)).astype(np.float16).astype(np.float32)
+    got = ora.linear_int4_q8(x, packed, scales, out_f, in_f, 32)[0]
+    f32 = ora.linear_int4_f32(x, packed, scales, out_f, in_f, 32)[0]
+    if in_f > 16384:
+        assert np.array_equal(got, f32)
+    else:
+        assert np.array_equal(got, _q8_brute(x, packed, scales, out_f, in_f))
+        assert not np.array_equal(got, f32)
