@@ -192,6 +192,29 @@ def decode_batch1(gh, sess, prompt, warmup, steps):
     return steps / dt, dt
 
 
+def c5_workload(cfg, lanes=32, gen=256, prompt_lo=64, prompt_hi=4096, max_weight=4):
+    """The config-5 admission set: prompt lengths U[prompt_lo, prompt_hi] by
+    seed, LaneWeave weights 1..max_weight by lane, each lane's request spec
+    (gen - 1 decode quanta; its fp16 KV pages charged to the scheduler's Bank)
+    and the Bank / scheduler parameters. Model-free: the scheduler's event
+    chain depends on nothing else."""
+    rng = np.random.default_rng(SEED ^ 0xC5)
+    plens = [int(x) for x in rng.integers(prompt_lo, prompt_hi + 1, size=lanes)]
+    weights = [1 + (i % max_weight) for i in range(lanes)]
+    kvd = cfg["num_kv_heads"] * cfg["head_dim"]
+    page_bytes = cfg["num_layers"] * 2 * 16 * kvd * 2
+    pages = [-(-(p + gen) // 16) for p in plens]
+    specs = [dict(tenant_key=i + 1, request_key=10 * (i + 1), request_generation=1,
+                  resource_owner_key=100 * (i + 1), weight=weights[i], work_quanta=gen - 1,
+                  deadline_tick=0, claim=dict(kv_bytes=pages[i] * page_bytes, queue_slots=1))
+             for i in range(lanes)]
+    bank = dict(host_bytes=sum(pages) * page_bytes, kv_bytes=sum(pages) * page_bytes,
+                queue_slots=lanes)
+    return dict(lanes=lanes, gen=gen, plens=plens, weights=weights, pages=pages,
+                page_bytes=page_bytes, specs=specs, bank=bank, bank_epoch=0x42414E4B,
+                scheduler_epoch=0x51534553, max_weight=max_weight, prompt_hi=prompt_hi)
+
+
 def bench_c5(gh, model, lanes=32, gen=256, prompt_lo=64, prompt_hi=4096, max_weight=4):
     """32 concurrent lanes under LaneWeave weighted IWRR
     (weights 1..4 by lane, max_weight 4), prompt lengths uniform in
@@ -203,25 +226,22 @@ def bench_c5(gh, model, lanes=32, gen=256, prompt_lo=64, prompt_hi=4096, max_wei
     device step and commits them in scheduler order. Decode tok/s counts the
     tokens of the waves over their wall time; end-to-end adds prefill."""
     cfg = model.cfg
-    rng = np.random.default_rng(SEED ^ 0xC5)
-    plens = [int(x) for x in rng.integers(prompt_lo, prompt_hi + 1, size=lanes)]
-    weights = [1 + (i % max_weight) for i in range(lanes)]
+    wl = c5_workload(cfg, lanes, gen, prompt_lo, prompt_hi, max_weight)
+    plens, weights, pages = wl["plens"], wl["weights"], wl["pages"]
     V = cfg["vocab_size"]
     W = (V + 63) // 64
-    kvd = cfg["num_kv_heads"] * cfg["head_dim"]
-    page_bytes = cfg["num_layers"] * 2 * 16 * kvd * 2
-    pages = [-(-(p + gen) // 16) for p in plens]
     sess = gh.Session(model, max_lanes=lanes, max_positions=prompt_hi + gen + 8, kv_dtype=gh.F16,
                       total_pages=sum(pages), prefill_chunk=2048)
-    sched = gh.LaneWeave(lanes, dict(host_bytes=sum(pages) * page_bytes,
-                                     kv_bytes=sum(pages) * page_bytes, queue_slots=lanes),
-                         bank_epoch=0x42414E4B, scheduler_epoch=0x51534553, max_weight=max_weight)
+    sched = gh.LaneWeave(lanes, wl["bank"], bank_epoch=wl["bank_epoch"],
+                         scheduler_epoch=wl["scheduler_epoch"], max_weight=max_weight)
     try:
         tokens = np.zeros(lanes, np.uint32)
         t0 = time.perf_counter()
         for i in range(lanes):
-            spec = gh.LaneWeave.spec(i + 1, 10 * (i + 1), 1, 100 * (i + 1), weights[i], gen - 1, 0,
-                                     dict(kv_bytes=pages[i] * page_bytes, queue_slots=1))
+            sp = wl["specs"][i]
+            spec = gh.LaneWeave.spec(sp["tenant_key"], sp["request_key"], sp["request_generation"],
+                                     sp["resource_owner_key"], sp["weight"], sp["work_quanta"],
+                                     sp["deadline_tick"], sp["claim"])
             ok, _, _ = sched.admit(spec)
             assert ok, "admission rejected"
             sess.begin(i, seed=i)

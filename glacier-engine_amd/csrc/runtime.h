@@ -41,6 +41,24 @@ struct glacier_hip_context {
   std::map<hipStream_t, StreamScratch> per_stream;
   gk::ArgmaxResult *results_host = nullptr;  // pinned
   int32_t *ident = nullptr;  // device 0..63: row i -> page-table row i
+  // asynchronous registered dispatches, by command generation
+  struct AsyncCmd {
+    uint8_t binding[32];
+    uint64_t buf[4];  // packed, scales, input, output buffer ids
+    hipEvent_t start = nullptr, end = nullptr;
+    uint64_t alloc_before = 0;
+    bool observed = false;  // the final completion record is fixed once seen
+    glacier_hip_async_completion_t final{};
+  };
+  // every device allocation of the product (buffers, weights, sessions,
+  // scratch): requested and granularity-charged bytes
+  std::mutex dev_mu;
+  std::map<void *, uint64_t> dev_allocs;
+  uint64_t dev_requested = 0, dev_charged = 0;
+  std::map<uint64_t, AsyncCmd> commands;
+  uint64_t next_command_generation = 1;
+  uint64_t nonce[4] = {0, 0, 0, 0};
+  hipEvent_t origin = nullptr;  // recorded at init: the zero of the GPU times
 };
 
 struct glacier_hip_int4_weight {
@@ -52,6 +70,16 @@ struct glacier_hip_int4_weight {
 };
 
 namespace gh {
+
+// Allocation granularity the lease adapter charges (hipMalloc rounds large
+// buffers to 2 MiB pages).
+constexpr uint64_t kGranularity = 2ull << 20;
+inline uint64_t charged_bytes(uint64_t requested) {
+  return requested == 0 ? 0 : (requested + kGranularity - 1) / kGranularity * kGranularity;
+}
+// hipMalloc / hipFree with the context's device-byte accounting.
+hipError_t dev_malloc(glacier_hip_context *ctx, void **p, size_t bytes);
+void dev_free(glacier_hip_context *ctx, void *p);
 
 // Record a HIP failure on the context and map it to a status code.
 int hip_fail(glacier_hip_context *ctx, hipError_t e, const char *what);

@@ -19,8 +19,41 @@ int hip_fail(glacier_hip_context *ctx, hipError_t e, const char *what) {
   if (ctx) {
     ctx->last_error = std::string(what) + ": " + hipGetErrorString(e);
   }
+  // the failure is reported through the status code; clear the thread's last
+  // error so that the launch checks (hipGetLastError) of later calls do not
+  // report it again
+  (void)hipGetLastError();
   if (e == hipErrorOutOfMemory) return GLACIER_HIP_OUT_OF_MEMORY;
   return GLACIER_HIP_DEVICE_ERROR;
+}
+
+hipError_t dev_malloc(glacier_hip_context *ctx, void **p, size_t bytes) {
+  *p = nullptr;
+  const hipError_t e = hipMalloc(p, bytes);
+  if (e != hipSuccess) {
+    *p = nullptr;
+    (void)hipGetLastError();  // handled here: later launch checks must not see it
+    return e;
+  }
+  std::lock_guard<std::mutex> lk(ctx->dev_mu);
+  ctx->dev_allocs[*p] = bytes;
+  ctx->dev_requested += bytes;
+  ctx->dev_charged += charged_bytes(bytes);
+  return hipSuccess;
+}
+
+void dev_free(glacier_hip_context *ctx, void *p) {
+  if (!p) return;
+  {
+    std::lock_guard<std::mutex> lk(ctx->dev_mu);
+    auto it = ctx->dev_allocs.find(p);
+    if (it != ctx->dev_allocs.end()) {
+      ctx->dev_requested -= it->second;
+      ctx->dev_charged -= charged_bytes(it->second);
+      ctx->dev_allocs.erase(it);
+    }
+  }
+  (void)hipFree(p);
 }
 
 int resolve_activation(int activation, uint32_t out_f, uint32_t in_f) {
@@ -74,12 +107,13 @@ glacier_hip_int4_weight *upload_weight(glacier_hip_context *ctx, uint32_t out_f,
   w->out_f = out_f;
   w->in_f = in_f;
   const size_t cb = codes.size() * 4, sb = scales.size() * 2;
-  if (hipMalloc(&w->codes, cb) != hipSuccess || hipMalloc(&w->scales, sb) != hipSuccess ||
+  if (gh::dev_malloc(ctx, (void **)&w->codes, cb) != hipSuccess ||
+      gh::dev_malloc(ctx, (void **)&w->scales, sb) != hipSuccess ||
       hipMemcpy(w->codes, codes.data(), cb, hipMemcpyHostToDevice) != hipSuccess ||
       hipMemcpy(w->scales, scales.data(), sb, hipMemcpyHostToDevice) != hipSuccess) {
     ctx->last_error = "int4 weight upload failed";
-    if (w->codes) (void)hipFree(w->codes);
-    if (w->scales) (void)hipFree(w->scales);
+    gh::dev_free(ctx, w->codes);
+    gh::dev_free(ctx, w->scales);
     delete w;
     return nullptr;
   }
@@ -91,17 +125,17 @@ glacier_hip_int4_weight *upload_weight(glacier_hip_context *ctx, uint32_t out_f,
 int ensure_scratch(glacier_hip_context *ctx, glacier_hip_context::StreamScratch &ss, size_t bytes,
                    size_t counters) {
   if (bytes > ss.scratch_bytes) {
-    if (ss.scratch) GH_CHECK(ctx, hipFree(ss.scratch));
+    gh::dev_free(ctx, ss.scratch);
     ss.scratch = nullptr;
     ss.scratch_bytes = 0;
-    GH_CHECK(ctx, hipMalloc(&ss.scratch, bytes));
+    GH_CHECK(ctx, gh::dev_malloc(ctx, &ss.scratch, bytes));
     ss.scratch_bytes = bytes;
   }
   if (counters > ss.counter_count) {
-    if (ss.counters) GH_CHECK(ctx, hipFree(ss.counters));
+    gh::dev_free(ctx, ss.counters);
     ss.counters = nullptr;
     ss.counter_count = 0;
-    GH_CHECK(ctx, hipMalloc(&ss.counters, counters * sizeof(uint32_t)));
+    GH_CHECK(ctx, gh::dev_malloc(ctx, (void **)&ss.counters, counters * sizeof(uint32_t)));
     GH_CHECK(ctx, hipMemset(ss.counters, 0, counters * sizeof(uint32_t)));
     ss.counter_count = counters;
   }
@@ -144,7 +178,7 @@ glacier_hip_context *glacier_hip_init(int device_ordinal) {
     what = "identity rows";
     int32_t h[64];
     for (int i = 0; i < 64; ++i) h[i] = i;
-    e = hipMalloc((void **)&ctx->ident, sizeof h);
+    e = gh::dev_malloc(ctx, (void **)&ctx->ident, sizeof h);
     if (e == hipSuccess) e = hipMemcpy(ctx->ident, h, sizeof h, hipMemcpyHostToDevice);
   }
   if (e != hipSuccess) {
@@ -154,22 +188,41 @@ glacier_hip_context *glacier_hip_init(int device_ordinal) {
   }
   static uint64_t epoch_counter = 0x6c61636965720000ull;
   ctx->epoch = ++epoch_counter;
+  {  // command tokens carry a nonce of this context
+    gh::Sha256 h;
+    h.update("glacier-hip-command-nonce-v1", 28);
+    h.u64(ctx->epoch);
+    h.u64((uint64_t)(uintptr_t)ctx);
+    h.u64((uint64_t)device_ordinal);
+    uint8_t d[32];
+    h.final(d);
+    memcpy(ctx->nonce, d, 32);
+  }
+  if (hipEventCreate(&ctx->origin) != hipSuccess ||
+      hipEventRecord(ctx->origin, ctx->stream) != hipSuccess) {
+    g_init_error = "origin event";
+    (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return nullptr;
+  }
   return ctx;
 }
 
 int glacier_hip_deinit(glacier_hip_context *ctx) {
   if (!ctx) return GLACIER_HIP_INVALID_HANDLE;
-  if (!ctx->buffers.empty() || ctx->live_weights != 0) return GLACIER_HIP_BUSY;
+  if (!ctx->buffers.empty() || ctx->live_weights != 0 || !ctx->commands.empty())
+    return GLACIER_HIP_BUSY;
   (void)hipDeviceSynchronize();
   for (auto &kv : ctx->per_stream) {
     auto &ss = kv.second;
-    if (ss.scratch) (void)hipFree(ss.scratch);
-    if (ss.planes) (void)hipFree(ss.planes);
-    if (ss.splitk) (void)hipFree(ss.splitk);
-    if (ss.counters) (void)hipFree(ss.counters);
+    gh::dev_free(ctx, ss.scratch);
+    gh::dev_free(ctx, ss.planes);
+    gh::dev_free(ctx, ss.splitk);
+    gh::dev_free(ctx, ss.counters);
   }
   if (ctx->results_host) (void)hipHostFree(ctx->results_host);
-  if (ctx->ident) (void)hipFree(ctx->ident);
+  gh::dev_free(ctx, ctx->ident);
+  if (ctx->origin) (void)hipEventDestroy(ctx->origin);
   (void)hipStreamDestroy(ctx->stream);
   delete ctx;
   return GLACIER_HIP_OK;
@@ -204,11 +257,16 @@ int glacier_hip_device_info(glacier_hip_context *ctx, glacier_hip_device_info_t 
   return GLACIER_HIP_OK;
 }
 
-static const uint64_t kGranularity = 2ull << 20;  // hipMalloc rounds large buffers to 2 MiB
+using gh::kGranularity;
+static uint64_t charged_size(uint64_t requested) { return gh::charged_bytes(requested); }
 
-static uint64_t charged_size(uint64_t requested) {
-  if (requested == 0) return 0;
-  return (requested + kGranularity - 1) / kGranularity * kGranularity;
+int glacier_hip_live_device_bytes(glacier_hip_context *ctx, uint64_t *requested_out,
+                                  uint64_t *charged_out) {
+  if (!ctx) return GLACIER_HIP_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> lk(ctx->dev_mu);
+  if (requested_out) *requested_out = ctx->dev_requested;
+  if (charged_out) *charged_out = ctx->dev_charged;
+  return GLACIER_HIP_OK;
 }
 
 int glacier_hip_allocation_limits(glacier_hip_context *ctx, glacier_hip_allocation_limits_t *out) {
@@ -256,7 +314,9 @@ int glacier_hip_device_capability_v1(glacier_hip_context *ctx,
   out->element_type_bits = (1ull << 0) | (1ull << 2);
   out->numerical_policy_bits = 1ull << 1;
   // allocation | dispatch | completion_fence | persistent_weights
-  out->feature_bits = (1ull << 0) | (1ull << 1) | (1ull << 2) | (1ull << 3);
+  out->feature_bits = (1ull << 0) | (1ull << 1) | (1ull << 2) | (1ull << 3) | (1ull << 4) |
+                     (1ull << 5);  // allocation, dispatch, completion fence, persistent
+                                   // weights, command GPU times, allocated bytes
   out->max_single_allocation_bytes = ctx->props.totalGlobalMem;
   out->max_total_device_bytes = ctx->props.totalGlobalMem;
   out->max_queue_slots = 1;
@@ -320,7 +380,7 @@ int glacier_hip_allocation_allocate(glacier_hip_context *ctx,
     return GLACIER_HIP_INVALID_ARGUMENT;
   std::lock_guard<std::mutex> lk(ctx->buf_mu);
   void *p = nullptr;
-  hipError_t e = hipMalloc(&p, quote->requested_bytes);
+  hipError_t e = gh::dev_malloc(ctx, &p, quote->requested_bytes);
   if (e != hipSuccess) return hip_fail(ctx, e, "hipMalloc");  // nothing was created
   const uint64_t id = ctx->next_buffer_id++;
   ctx->buffers[id] = {p, quote->requested_bytes, quote->charged_bytes};
@@ -354,8 +414,10 @@ int glacier_hip_buffer_release(glacier_hip_context *ctx, const glacier_hip_buffe
   auto it = ctx->buffers.find(token->id);
   if (it == ctx->buffers.end() || it->second.requested != token->requested_bytes)
     return GLACIER_HIP_INVALID_HANDLE;
-  hipError_t e = hipFree(it->second.ptr);
-  if (e != hipSuccess) return hip_fail(ctx, e, "hipFree");  // the buffer stays live
+  for (const auto &kv : ctx->commands)  // a live command still uses it
+    for (uint64_t id : kv.second.buf)
+      if (id == token->id) return GLACIER_HIP_BUSY;
+  gh::dev_free(ctx, it->second.ptr);
   ctx->buffers.erase(it);
   return GLACIER_HIP_OK;
 }
@@ -418,8 +480,8 @@ glacier_hip_int4_weight *glacier_hip_int4_weight_create_f16scales(
 
 void glacier_hip_int4_weight_destroy(glacier_hip_int4_weight *w) {
   if (!w) return;
-  if (w->codes) (void)hipFree(w->codes);
-  if (w->scales) (void)hipFree(w->scales);
+  gh::dev_free(w->ctx, w->codes);
+  gh::dev_free(w->ctx, w->scales);
   if (w->ctx && w->ctx->live_weights) w->ctx->live_weights--;
   delete w;
 }
@@ -468,10 +530,10 @@ static int gemv_launch(glacier_hip_context *ctx, glacier_hip_int4_weight *w, con
   auto &ss = ctx->per_stream[st];
   const size_t need = std::min<size_t>(gk::gemm_splitk_floats(N, (int)m, K, D), 16u << 20);
   if (need > ss.splitk_floats) {
-    if (ss.splitk) GH_CHECK(ctx, hipFree(ss.splitk));
+    gh::dev_free(ctx, ss.splitk);
     ss.splitk = nullptr;
     ss.splitk_floats = 0;
-    GH_CHECK(ctx, hipMalloc((void **)&ss.splitk, need * sizeof(float)));
+    GH_CHECK(ctx, gh::dev_malloc(ctx, (void **)&ss.splitk, need * sizeof(float)));
     ss.splitk_floats = need;
   }
   a.splitk_ws = ss.splitk;
@@ -501,10 +563,10 @@ static int gemv_common(glacier_hip_context *ctx, glacier_hip_int4_weight *w, con
   auto &ss = ctx->per_stream[st];
   const size_t pb = planes_bytes(m, w->in_f, D);
   if (pb > ss.planes_bytes) {
-    if (ss.planes) GH_CHECK(ctx, hipFree(ss.planes));
+    gh::dev_free(ctx, ss.planes);
     ss.planes = nullptr;
     ss.planes_bytes = 0;
-    GH_CHECK(ctx, hipMalloc(&ss.planes, pb));
+    GH_CHECK(ctx, gh::dev_malloc(ctx, &ss.planes, pb));
     ss.planes_bytes = pb;
   }
   int rc = prepare_launch(ctx, x_dev, x_dtype, m, w->in_f, D, ss.planes, st);
@@ -560,10 +622,10 @@ int glacier_hip_int4_matvec_dispatch(glacier_hip_context *ctx, glacier_hip_int4_
   if (input_count != w->in_f || output_count != w->out_f) return GLACIER_HIP_SHAPE_MISMATCH;
   GH_SUBMISSION(ctx);
   float *xd = nullptr, *yd = nullptr;
-  GH_CHECK(ctx, hipMalloc(&xd, input_count * 4));
-  hipError_t e = hipMalloc(&yd, output_count * 4);
+  GH_CHECK(ctx, gh::dev_malloc(ctx, (void **)&xd, input_count * 4));
+  hipError_t e = gh::dev_malloc(ctx, (void **)&yd, output_count * 4);
   if (e != hipSuccess) {
-    (void)hipFree(xd);
+    gh::dev_free(ctx, xd);
     return hip_fail(ctx, e, "hipMalloc");
   }
   int rc = GLACIER_HIP_OK;
@@ -575,9 +637,243 @@ int glacier_hip_int4_matvec_dispatch(glacier_hip_context *ctx, glacier_hip_int4_
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) rc = hip_fail(ctx, e, "copy out");
   }
-  (void)hipFree(xd);
-  (void)hipFree(yd);
+  gh::dev_free(ctx, xd);
+  gh::dev_free(ctx, yd);
   return rc;
+}
+
+// ---- asynchronous registered-buffer dispatch --------------------------------
+static const uint64_t kAsyncSubmissionAbi = 0x474d415300000001ull;  // backend.zig:26
+static const uint64_t kAsyncCompletionAbi = 0x474d414300000001ull;  // backend.zig:27
+
+static bool binding_zero(const uint8_t b[32]) {
+  for (int i = 0; i < 32; ++i)
+    if (b[i]) return false;
+  return true;
+}
+
+static uint64_t live_buffer_bytes(const glacier_hip_context *ctx) {
+  uint64_t n = 0;
+  for (const auto &kv : ctx->buffers) n += kv.second.charged;
+  return n;
+}
+
+// The command of `token` + `binding` (held under ctx->buf_mu), or null.
+static glacier_hip_context::AsyncCmd *find_command(glacier_hip_context *ctx,
+                                                   const glacier_hip_command_token_t *t,
+                                                   const uint8_t binding[32]) {
+  if (memcmp(t->context_nonce, ctx->nonce, sizeof ctx->nonce) != 0) return nullptr;
+  auto it = ctx->commands.find(t->generation);
+  if (it == ctx->commands.end() || memcmp(it->second.binding, binding, 32) != 0) return nullptr;
+  return &it->second;
+}
+
+// The completion record of a command; once the command has ended the record
+// is fixed (every later poll returns the same bytes, as finalize compares).
+static void completion_of(glacier_hip_context *ctx, uint64_t gen,
+                          glacier_hip_context::AsyncCmd &c, bool wait,
+                          glacier_hip_async_completion_t *out) {
+  if (c.observed) {
+    *out = c.final;
+    return;
+  }
+  glacier_hip_async_completion_t r;
+  memset(&r, 0, sizeof r);
+  r.abi_version = kAsyncCompletionAbi;
+  memcpy(r.token.context_nonce, ctx->nonce, sizeof ctx->nonce);
+  r.token.generation = gen;
+  memcpy(r.submission_binding, c.binding, 32);
+  r.current_allocated_before = c.alloc_before;
+  const hipError_t e = wait ? hipEventSynchronize(c.end) : hipEventQuery(c.end);
+  if (e != hipSuccess) (void)hipGetLastError();  // reported in the record, not later
+  if (e == hipErrorNotReady) {
+    r.state = GLACIER_HIP_COMMAND_PENDING;
+    r.current_allocated_after = c.alloc_before;
+    *out = r;
+    return;
+  }
+  r.current_allocated_after = live_buffer_bytes(ctx);
+  if (e != hipSuccess) {
+    r.state = GLACIER_HIP_COMMAND_ERROR;
+    r.error_code = (int64_t)e;
+    r.error_present = 1;
+    r.error_domain_kind = 2;  // other
+  } else {
+    float ms0 = 0.0f, ms1 = 0.0f;
+    if (hipEventElapsedTime(&ms0, ctx->origin, c.start) == hipSuccess &&
+        hipEventElapsedTime(&ms1, ctx->origin, c.end) == hipSuccess) {
+      r.gpu_start_time = ms0 * 1e-3;
+      r.gpu_end_time = ms1 * 1e-3;
+    }
+    r.state = GLACIER_HIP_COMMAND_COMPLETED;
+  }
+  c.final = r;
+  c.observed = true;
+  *out = r;
+}
+
+int glacier_hip_int4_registered_buffers_submit_async(
+    glacier_hip_context *ctx, const glacier_hip_buffer_token_t *ptok,
+    const glacier_hip_buffer_token_t *stok, const glacier_hip_buffer_token_t *itok,
+    const glacier_hip_buffer_token_t *otok, const uint8_t *packed, uint64_t packed_bytes,
+    const float *scales, uint64_t scale_count, const float *input, uint64_t input_count,
+    uint32_t group_size, uint32_t in_f, uint32_t out_f, const uint8_t binding[32],
+    glacier_hip_async_submission_t *sub) {
+  if (sub) {
+    memset(sub, 0, sizeof *sub);
+    sub->abi_version = kAsyncSubmissionAbi;
+    sub->disposition = 2;  // submitted_or_ambiguous until the queue accepted it
+  }
+  if (!ctx || !ptok || !stok || !itok || !otok || !packed || !scales || !input || !binding ||
+      !sub || binding_zero(binding))
+    return GLACIER_HIP_INVALID_ARGUMENT;
+  if (group_size != 32 || out_f == 0 || in_f == 0 || out_f % 16 || in_f % 128)
+    return GLACIER_HIP_SHAPE_MISMATCH;
+  const uint64_t n = (uint64_t)out_f * in_f;
+  if (packed_bytes < n / 2 || scale_count < n / 32 || input_count != in_f)
+    return GLACIER_HIP_SHAPE_MISMATCH;
+  GH_SUBMISSION(ctx);
+  std::lock_guard<std::mutex> bl(ctx->buf_mu);
+  const glacier_hip_buffer_token_t *toks[4] = {ptok, stok, itok, otok};
+  const uint64_t need[4] = {n / 2, scale_count * 4, (uint64_t)in_f * 4, (uint64_t)out_f * 4};
+  void *ptr[4];
+  for (int i = 0; i < 4; ++i) {
+    auto it = ctx->buffers.find(toks[i]->id);
+    if (it == ctx->buffers.end() || it->second.requested != toks[i]->requested_bytes)
+      return GLACIER_HIP_INVALID_HANDLE;
+    if (it->second.requested < need[i]) return GLACIER_HIP_SHAPE_MISMATCH;
+    for (int j = 0; j < i; ++j)
+      if (toks[j]->id == toks[i]->id) return GLACIER_HIP_INVALID_ARGUMENT;
+    ptr[i] = it->second.ptr;
+  }
+  // the registered weight buffers receive the device tile layout (codes,
+  // then fp16 scales: half the f32 scale buffer)
+  std::vector<gh::RowSrc> rows(out_f);
+  for (uint32_t r = 0; r < out_f; ++r) rows[r] = {packed, scales, nullptr, r};
+  std::vector<uint32_t> codes;
+  std::vector<uint16_t> sc16;
+  gh::repack_tiles(rows, in_f, codes, sc16);
+  GH_CHECK(ctx, hipMemcpy(ptr[0], codes.data(), codes.size() * 4, hipMemcpyHostToDevice));
+  GH_CHECK(ctx, hipMemcpy(ptr[1], sc16.data(), sc16.size() * 2, hipMemcpyHostToDevice));
+  GH_CHECK(ctx, hipMemcpy(ptr[2], input, (size_t)in_f * 4, hipMemcpyHostToDevice));
+  glacier_hip_int4_weight view;
+  view.ctx = ctx;
+  view.out_f = out_f;
+  view.in_f = in_f;
+  view.codes = (uint4 *)ptr[0];
+  view.scales = (uint2 *)ptr[1];
+  glacier_hip_context::AsyncCmd c;
+  memcpy(c.binding, binding, 32);
+  for (int i = 0; i < 4; ++i) c.buf[i] = toks[i]->id;
+  c.alloc_before = live_buffer_bytes(ctx);
+  GH_CHECK(ctx, hipEventCreate(&c.start));
+  hipError_t e = hipEventCreate(&c.end);
+  if (e != hipSuccess) {
+    (void)hipEventDestroy(c.start);
+    return hip_fail(ctx, e, "hipEventCreate");
+  }
+  int rc = GLACIER_HIP_OK;
+  if ((e = hipEventRecord(c.start, ctx->stream)) != hipSuccess) rc = hip_fail(ctx, e, "record");
+  if (!rc) rc = gemv_common(ctx, &view, ptr[2], GLACIER_HIP_F32, 1, nullptr, (float *)ptr[3],
+                            GLACIER_HIP_ACT_F32, ctx->stream);
+  if (!rc && (e = hipEventRecord(c.end, ctx->stream)) != hipSuccess) rc = hip_fail(ctx, e, "record");
+  if (rc) {  // nothing was queued that outlives this call
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipEventDestroy(c.start);
+    (void)hipEventDestroy(c.end);
+    return rc;
+  }
+  const uint64_t gen = ctx->next_command_generation++;
+  ctx->commands[gen] = c;
+  memcpy(sub->token.context_nonce, ctx->nonce, sizeof ctx->nonce);
+  sub->token.generation = gen;
+  memcpy(sub->submission_binding, binding, 32);
+  sub->disposition = 1;  // submitted
+  return GLACIER_HIP_OK;
+}
+
+static int poll_or_wait(glacier_hip_context *ctx, const glacier_hip_command_token_t *t,
+                        const uint8_t binding[32], glacier_hip_async_completion_t *out, bool wait) {
+  if (!ctx || !t || !binding || !out || t->generation == 0 || binding_zero(binding))
+    return GLACIER_HIP_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> bl(ctx->buf_mu);
+  auto *c = find_command(ctx, t, binding);
+  if (!c) return GLACIER_HIP_INVALID_HANDLE;
+  completion_of(ctx, t->generation, *c, wait, out);
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_registered_dispatch_poll(glacier_hip_context *ctx,
+                                         const glacier_hip_command_token_t *t,
+                                         const uint8_t binding[32],
+                                         glacier_hip_async_completion_t *out) {
+  return poll_or_wait(ctx, t, binding, out, false);
+}
+
+int glacier_hip_registered_dispatch_wait(glacier_hip_context *ctx,
+                                         const glacier_hip_command_token_t *t,
+                                         const uint8_t binding[32],
+                                         glacier_hip_async_completion_t *out) {
+  return poll_or_wait(ctx, t, binding, out, true);
+}
+
+static bool expected_ok(const glacier_hip_command_token_t *t, const uint8_t binding[32],
+                        const glacier_hip_async_completion_t *x) {
+  return x && x->abi_version == kAsyncCompletionAbi && x->reserved == 0 &&
+         memcmp(&x->token, t, sizeof *t) == 0 && memcmp(x->submission_binding, binding, 32) == 0;
+}
+
+int glacier_hip_registered_dispatch_finalize(glacier_hip_context *ctx,
+                                             const glacier_hip_command_token_t *t,
+                                             const uint8_t binding[32],
+                                             const glacier_hip_async_completion_t *expected) {
+  if (!ctx || !t || !binding || t->generation == 0 || binding_zero(binding) ||
+      !expected_ok(t, binding, expected))
+    return GLACIER_HIP_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> bl(ctx->buf_mu);
+  auto *c = find_command(ctx, t, binding);
+  if (!c) return GLACIER_HIP_INVALID_HANDLE;
+  glacier_hip_async_completion_t exact;
+  completion_of(ctx, t->generation, *c, false, &exact);
+  if ((exact.state != GLACIER_HIP_COMMAND_COMPLETED && exact.state != GLACIER_HIP_COMMAND_ERROR) ||
+      memcmp(&exact, expected, sizeof exact) != 0)
+    return GLACIER_HIP_INVALID_TRANSACTION;
+  (void)hipEventDestroy(c->start);
+  (void)hipEventDestroy(c->end);
+  ctx->commands.erase(t->generation);
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_int4_registered_output_read(glacier_hip_context *ctx,
+                                            const glacier_hip_command_token_t *t,
+                                            const uint8_t binding[32],
+                                            const glacier_hip_async_completion_t *expected,
+                                            const glacier_hip_buffer_token_t *otok,
+                                            float *output, uint64_t output_count) {
+  if (!ctx || !t || !binding || t->generation == 0 || binding_zero(binding) ||
+      !expected_ok(t, binding, expected) || !otok || !output || output_count == 0 ||
+      output_count > UINT64_MAX / 4)
+    return GLACIER_HIP_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> bl(ctx->buf_mu);
+  auto *c = find_command(ctx, t, binding);
+  if (!c) return GLACIER_HIP_INVALID_HANDLE;
+  glacier_hip_async_completion_t exact;
+  completion_of(ctx, t->generation, *c, false, &exact);
+  if (exact.state != GLACIER_HIP_COMMAND_COMPLETED || memcmp(&exact, expected, sizeof exact) != 0)
+    return GLACIER_HIP_INVALID_TRANSACTION;
+  auto it = ctx->buffers.find(otok->id);
+  if (otok->id != c->buf[3] || it == ctx->buffers.end() ||
+      it->second.requested != otok->requested_bytes || output_count * 4 > it->second.requested)
+    return GLACIER_HIP_SHAPE_MISMATCH;
+  GH_CHECK(ctx, hipMemcpy(output, it->second.ptr, output_count * 4, hipMemcpyDeviceToHost));
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_live_command_count(glacier_hip_context *ctx, uint64_t *out) {
+  if (!ctx || !out) return GLACIER_HIP_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> bl(ctx->buf_mu);
+  *out = ctx->commands.size();
+  return GLACIER_HIP_OK;
 }
 
 int glacier_hip_rmsnorm(glacier_hip_context *ctx, const float *x_dev, const float *w_dev,
@@ -616,6 +912,26 @@ int glacier_hip_paged_attention(glacier_hip_context *ctx, const float *q_dev,
                                      (int)layer, (int)num_layers, (int)num_heads,
                                      (int)num_kv_heads, (int)head_dim, (int)max_ctx,
                                      (float *)ss.scratch, out_dev, st));
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_paged_attention_prefill(glacier_hip_context *ctx, const float *q_dev,
+                                        const void *kv_pool_dev, const int32_t *page_table_dev,
+                                        uint32_t max_pages, uint32_t pos0, uint32_t T,
+                                        uint32_t layer, uint32_t num_layers, uint32_t num_heads,
+                                        uint32_t num_kv_heads, uint32_t head_dim, float *out_dev,
+                                        void *stream) {
+  if (!ctx || !q_dev || !kv_pool_dev || !page_table_dev || !out_dev)
+    return GLACIER_HIP_INVALID_ARGUMENT;
+  if (T == 0 || num_kv_heads == 0 || num_heads % num_kv_heads != 0 ||
+      num_heads / num_kv_heads > 8 || (head_dim != 64 && head_dim != 128) ||
+      layer >= num_layers || (uint64_t)pos0 + T > (uint64_t)max_pages * 16 || pos0 > (1u << 30))
+    return GLACIER_HIP_SHAPE_MISMATCH;
+  GH_SUBMISSION(ctx);
+  GH_CHECK(ctx, gk::launch_attention_prefill(q_dev, kv_pool_dev, page_table_dev, (int)max_pages, 0,
+                                             (int)pos0, (int)T, (int)layer, (int)num_layers,
+                                             (int)num_heads, (int)num_kv_heads, (int)head_dim,
+                                             out_dev, stream ? (hipStream_t)stream : ctx->stream));
   return GLACIER_HIP_OK;
 }
 

@@ -14,10 +14,12 @@
 #include <string.h>
 
 #include <algorithm>
+#include <array>
 
 #include "host_util.h"
 #include "lane_weave.h"
 #include "paged_kv.h"
+#include "publication.h"
 #include "runtime.h"
 
 using gh::hip_fail;
@@ -47,6 +49,23 @@ struct Lane {
   uint64_t sampling_calls = 0;
   uint64_t rng[4] = {0, 0, 0, 0};
   std::vector<uint32_t> output;
+  // staged publication (paged_token_txn.zig): the prompt length, a first
+  // token held back for the first wave, the lane's KV state chain
+  uint64_t prompt_len = 0;
+  bool first_pending = false;
+  uint32_t first_token = 0;
+  bool chain_init = false;
+  uint8_t chain[32] = {};
+  bool retired = false;           // a terminal token was published
+};
+
+// A staged publication wave between step_prepare and commit / abort.
+struct PreparedWave {
+  bool active = false, first = false, elig = false;
+  std::vector<gpk::RowTxn> txns;
+  std::vector<uint32_t> lanes, slots, tokens;
+  glacier_hip_token_proposal_v1_t proposal{};
+  uint8_t sha[32] = {};
 };
 
 struct StepInputs {  // uploaded once per decode step, in one copy
@@ -100,6 +119,7 @@ struct glacier_hip_session {
   int32_t *pt_host = nullptr;    // mirror of page_table [max_lanes][max_pages]
   gk::ArgmaxResult *res_host = nullptr;
   bool inject_failure = false;
+  PreparedWave prep;
   // graph cache: key = (rows, with_head, eligible)
   struct GraphEntry {
     uint32_t rows;
@@ -113,7 +133,7 @@ struct glacier_hip_session {
 // model
 // ---------------------------------------------------------------------------
 static int upload_f32(glacier_hip_context *ctx, float **dst, const float *src, size_t n) {
-  if (!*dst) GH_CHECK(ctx, hipMalloc(dst, n * 4));
+  if (!*dst) GH_CHECK(ctx, gh::dev_malloc(ctx, (void **)dst, n * 4));
   if (src) GH_CHECK(ctx, hipMemcpy(*dst, src, n * 4, hipMemcpyHostToDevice));
   else GH_CHECK(ctx, hipMemset(*dst, 0, n * 4));
   return GLACIER_HIP_OK;
@@ -283,18 +303,54 @@ int glacier_hip_model_init_random(glacier_hip_model *m, uint64_t seed) {
 void glacier_hip_model_destroy(glacier_hip_model *m) {
   if (!m) return;
   for (auto &L : m->layers) {
-    if (L.in_norm) (void)hipFree(L.in_norm);
-    if (L.post_norm) (void)hipFree(L.post_norm);
-    if (L.qkv_bias) (void)hipFree(L.qkv_bias);
+    gh::dev_free(m->ctx, L.in_norm);
+    gh::dev_free(m->ctx, L.post_norm);
+    gh::dev_free(m->ctx, L.qkv_bias);
     glacier_hip_int4_weight_destroy(L.qkv);
     glacier_hip_int4_weight_destroy(L.o);
     glacier_hip_int4_weight_destroy(L.gu);
     glacier_hip_int4_weight_destroy(L.down);
   }
-  if (m->embed) (void)hipFree(m->embed);
-  if (m->final_norm) (void)hipFree(m->final_norm);
+  gh::dev_free(m->ctx, m->embed);
+  gh::dev_free(m->ctx, m->final_norm);
   glacier_hip_int4_weight_destroy(m->head);
   delete m;
+}
+
+int glacier_hip_model_quote(glacier_hip_context *ctx, const glacier_hip_model_config_t *cfg,
+                            int with_qkv_bias, glacier_hip_allocation_quote_t *out) {
+  // the allocations set_layer (x num_layers) and set_globals make
+  if (!ctx || !cfg || !out) return GLACIER_HIP_INVALID_ARGUMENT;
+  const auto &c = *cfg;
+  if (c.num_layers == 0 || c.dim == 0 || c.hidden_dim == 0 || c.vocab_size == 0)
+    return GLACIER_HIP_SHAPE_MISMATCH;
+  const uint64_t D = c.dim, F = c.hidden_dim, V = c.vocab_size;
+  const uint64_t kvd = (uint64_t)c.num_kv_heads * c.head_dim;
+  uint64_t req = 0, chg = 0;
+  auto add = [&](uint64_t b) {
+    req += b;
+    chg += gh::charged_bytes(b);
+  };
+  auto weight = [&](uint64_t N, uint64_t K) {  // tile codes + fp16 scales
+    add(N * K / 2);
+    add(N * K / 16);
+  };
+  for (uint32_t l = 0; l < c.num_layers; ++l) {
+    add(D * 4);
+    add(D * 4);
+    weight(D + 2 * kvd, D);
+    if (with_qkv_bias) add((D + 2 * kvd) * 4);
+    weight(D, D);
+    weight(2 * F, D);
+    weight(D, F);
+  }
+  add(V * D * 4);
+  add(D * 4);
+  weight(V, D);
+  out->requested_bytes = req;
+  out->charged_bytes = chg;
+  out->context_epoch = ctx->epoch;
+  return GLACIER_HIP_OK;
 }
 
 uint64_t glacier_hip_model_weight_bytes(const glacier_hip_model *m) {
@@ -672,8 +728,7 @@ void destroy_session(glacier_hip_session *s) {
                   s->att_scratch, s->ss_parts, s->arg_scratch, s->arg_counters, s->arg_result,
                   s->elig_words, s->splitk_ws,
                   s->step_dev, s->pf_dev};
-  for (void *p : ptrs)
-    if (p) (void)hipFree(p);
+  for (void *p : ptrs) gh::dev_free(s->model->ctx, p);
   if (s->step_host) (void)hipHostFree(s->step_host);
   if (s->pf_host) (void)hipHostFree(s->pf_host);
   if (s->pt_host) (void)hipHostFree(s->pt_host);
@@ -685,6 +740,10 @@ void destroy_session(glacier_hip_session *s) {
 void reset_lane(glacier_hip_session *s, Lane &ln, uint64_t seed) {
   ln.kv.start(s->pool);  // a new request: fresh cache instance, pages back to the pool
   ln.sampling_calls = 0;
+  ln.prompt_len = 0;
+  ln.first_pending = ln.chain_init = ln.retired = false;
+  ln.first_token = 0;
+  memset(ln.chain, 0, 32);
   // SplitMix64-seeded Xoshiro256 state (std.Random.DefaultPrng.init)
   uint64_t st = seed;
   for (int i = 0; i < 4; ++i) {
@@ -945,12 +1004,123 @@ int run_prefill_chunk(glacier_hip_session *s, uint32_t lane, const uint32_t *tok
   return GLACIER_HIP_OK;
 }
 
+// logicalKvPrefixSha256 (generate.zig:3150-3172; hashLogicalPrefix
+// paged_kv_cache.zig:1532-1555) over the committed rows, K/V values widened to
+// f32 bit patterns: each committed page is copied once, then hashed in the
+// canonical layer / K-then-V / position order.
+int logical_kv_sha256(glacier_hip_session *s, uint32_t lane, uint8_t out[32]) {
+  const auto &c = s->model->cfg;
+  const Lane &ln = s->lanes[lane];
+  glacier_hip_context *ctx = s->model->ctx;
+  const size_t kvd = (size_t)c.num_kv_heads * c.head_dim, L = c.num_layers;
+  const size_t elem = s->opt.kv_dtype == GLACIER_HIP_F16 ? 2 : 4;
+  const size_t page_elems = L * 2 * 16 * kvd;
+  const uint64_t len = ln.kv.len, pages = (len + 15) / 16;
+  std::vector<uint8_t> raw(pages * page_elems * elem);
+  for (uint64_t p = 0; p < pages; ++p) {
+    const int32_t phys = ln.kv.page_of[p];
+    if (phys < 0) return GLACIER_HIP_INVALID_TRANSACTION;
+    GH_CHECK(ctx, hipMemcpy(raw.data() + p * page_elems * elem,
+                            (char *)s->kv_pool + (size_t)phys * page_elems * elem,
+                            page_elems * elem, hipMemcpyDeviceToHost));
+  }
+  gh::Sha256 h;
+  h.update("glacier-logical-kv-state-v1\0", 28);
+  h.u64(L);
+  h.u64(kvd);
+  h.u64(len);
+  for (size_t l = 0; l < L; ++l)
+    for (int v = 0; v < 2; ++v)
+      for (uint64_t pos = 0; pos < len; ++pos) {
+        const uint8_t *row = raw.data() +
+                             ((((pos / 16) * L + l) * 2 + v) * 16 + pos % 16) * kvd * elem;
+        for (size_t i = 0; i < kvd; ++i) {
+          uint32_t b;
+          if (elem == 4) {
+            memcpy(&b, row + 4 * i, 4);
+          } else {
+            uint16_t hv;
+            memcpy(&hv, row + 2 * i, 2);
+            const float f = gh::f16_to_f32(hv);
+            memcpy(&b, &f, 4);
+          }
+          h.u32(b);
+        }
+      }
+  h.final(out);
+  return GLACIER_HIP_OK;
+}
+
+// logicalRowTxnSha256 (paged_kv_cache.zig:1366-1384) of each staged row: the
+// row's K and V of every layer (one strided copy), widened to f32 bits.
+int row_payload_sha256(glacier_hip_session *s, const std::vector<RowTxn> &txns,
+                       std::vector<std::array<uint8_t, 32>> &out) {
+  const auto &c = s->model->cfg;
+  glacier_hip_context *ctx = s->model->ctx;
+  const size_t kvd = (size_t)c.num_kv_heads * c.head_dim, L = c.num_layers;
+  const size_t elem = s->opt.kv_dtype == GLACIER_HIP_F16 ? 2 : 4;
+  std::vector<uint8_t> raw(2 * L * kvd * elem);
+  out.resize(txns.size());
+  for (size_t i = 0; i < txns.size(); ++i) {
+    const RowTxn &t = txns[i];
+    // rows (layer l, K/V v) of the page sit 16 * kvd elements apart
+    const size_t off = ((size_t)t.page * L * 2 * 16 + t.pos % 16) * kvd * elem;
+    GH_CHECK(ctx, hipMemcpy2D(raw.data(), kvd * elem, (char *)s->kv_pool + off, 16 * kvd * elem,
+                              kvd * elem, 2 * L, hipMemcpyDeviceToHost));
+    gh::Sha256 h;
+    h.update("glacier-paged-kv-row-v1", sizeof("glacier-paged-kv-row-v1"));
+    h.u64(L);
+    h.u64(kvd);
+    h.u64(t.mark.base_len);
+    for (size_t r = 0; r < 2 * L * kvd; ++r) {
+      uint32_t b;
+      if (elem == 4) {
+        memcpy(&b, &raw[4 * r], 4);
+      } else {
+        uint16_t hv;
+        memcpy(&hv, &raw[2 * r], 2);
+        const float f = gh::f16_to_f32(hv);
+        memcpy(&b, &f, 4);
+      }
+      h.u32(b);
+    }
+    h.final(out[i].data());
+  }
+  return GLACIER_HIP_OK;
+}
+
+// capacityLedger().allocation_capacity_bytes of a lane's cache
+// (paged_kv_cache.zig capacity ledger: f32 page payloads + 16-byte entries).
+uint64_t lane_capacity_bytes(const glacier_hip_session *s) {
+  const auto &c = s->model->cfg;
+  const uint64_t pages = (s->opt.max_positions + 15) / 16;
+  const uint64_t payload = (uint64_t)c.num_layers * 2 * 16 * c.num_kv_heads * c.head_dim * 4;
+  return pages * payload + pages * 16;
+}
+
+void copy_root(const glacier_hip_page_map_root_t &r, glacier_hip_root_transition_v1_t &t,
+               bool before) {
+  if (before) {
+    t.root_before_generation = r.generation;
+    t.root_before_len = r.committed_len;
+    t.root_before_pages = r.committed_pages;
+    memcpy(t.root_before_ownership_sha256, r.ownership_sha256, 32);
+  } else {
+    t.root_after_generation = r.generation;
+    t.root_after_len = r.committed_len;
+    t.root_after_pages = r.committed_pages;
+    memcpy(t.root_after_ownership_sha256, r.ownership_sha256, 32);
+  }
+}
+
 }  // namespace
 
-extern "C" {
-
-glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
-                                                const glacier_hip_session_options_t *opts) {
+// Creates the session, or with `quote` set only adds up the device bytes its
+// allocations would take (requested and granularity-charged) and creates
+// nothing: the quote and the allocation come from the same list.
+static glacier_hip_session *session_create_impl(glacier_hip_model *m,
+                                                const glacier_hip_session_options_t *opts,
+                                                uint64_t *quote) {
   if (!m || !opts) return nullptr;
   glacier_hip_context *ctx = m->ctx;
   for (bool b : m->layer_set)
@@ -993,7 +1163,12 @@ glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
                                                   (int)c.head_dim, (int)opts->max_positions);
   bool ok = true;
   auto A = [&](void **p, size_t bytes) {
-    if (ok && hipMalloc(p, bytes) != hipSuccess) ok = false;
+    if (quote) {
+      quote[0] += bytes;
+      quote[1] += gh::charged_bytes(bytes);
+    } else if (ok && gh::dev_malloc(ctx, p, bytes) != hipSuccess) {
+      ok = false;
+    }
   };
   A(&s->kv_pool, page_bytes * s->total_pages);
   A((void **)&s->page_table, (size_t)L * s->max_pages * 4);
@@ -1049,6 +1224,10 @@ glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
   A((void **)&s->elig_words, (size_t)L * W * 8);
   A((void **)&s->step_dev, sizeof(StepInputs));
   A((void **)&s->pf_dev, (size_t)4 * s->prefill_chunk * 4);
+  if (quote) {  // host-pinned staging is not device memory
+    delete s;
+    return nullptr;
+  }
   auto H = [&](void **p, size_t bytes) {
     if (ok && hipHostMalloc(p, bytes) != hipSuccess) ok = false;
   };
@@ -1077,11 +1256,31 @@ glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
          hipMemcpy(s->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice) == hipSuccess;
   }
   if (!ok) {
+    (void)hipGetLastError();
     ctx->last_error = "session allocation failed";
     destroy_session(s);
     return nullptr;
   }
   return s;
+}
+
+extern "C" {
+
+glacier_hip_session *glacier_hip_session_create(glacier_hip_model *m,
+                                                const glacier_hip_session_options_t *opts) {
+  return session_create_impl(m, opts, nullptr);
+}
+
+int glacier_hip_session_quote(glacier_hip_model *m, const glacier_hip_session_options_t *opts,
+                              glacier_hip_allocation_quote_t *out) {
+  if (!m || !opts || !out) return GLACIER_HIP_INVALID_ARGUMENT;
+  uint64_t q[2] = {0, 0};
+  (void)session_create_impl(m, opts, q);
+  if (q[0] == 0) return GLACIER_HIP_INVALID_ARGUMENT;  // options the session would refuse
+  out->requested_bytes = q[0];
+  out->charged_bytes = q[1];
+  out->context_epoch = m->ctx->epoch;
+  return GLACIER_HIP_OK;
 }
 
 void glacier_hip_session_destroy(glacier_hip_session *s) {
@@ -1094,6 +1293,7 @@ int glacier_hip_session_lane_begin(glacier_hip_session *s, uint32_t lane, uint64
   if (!s) return GLACIER_HIP_INVALID_HANDLE;
   if (lane >= s->lanes.size()) return GLACIER_HIP_INVALID_ARGUMENT;
   GH_SUBMISSION(s->model->ctx);
+  if (s->prep.active) return GLACIER_HIP_TRANSACTION_ACTIVE;
   reset_lane(s, s->lanes[lane], seed);
   return GLACIER_HIP_OK;
 }
@@ -1104,8 +1304,8 @@ int glacier_hip_session_inject_failure(glacier_hip_session *s, int enable) {
   return GLACIER_HIP_OK;
 }
 
-int glacier_hip_session_prefill(glacier_hip_session *s, uint32_t lane, const uint32_t *tokens,
-                                uint32_t n, uint32_t *first_token, float *logits_host) {
+static int prefill_impl(glacier_hip_session *s, uint32_t lane, const uint32_t *tokens, uint32_t n,
+                        uint32_t *first_token, float *logits_host, bool staged) {
   if (!s || !tokens || !first_token) return GLACIER_HIP_INVALID_ARGUMENT;
   if (lane >= s->lanes.size() || !s->lanes[lane].kv.active) return GLACIER_HIP_INVALID_ARGUMENT;
   const auto &c = s->model->cfg;
@@ -1115,6 +1315,8 @@ int glacier_hip_session_prefill(glacier_hip_session *s, uint32_t lane, const uin
     if (tokens[i] >= c.vocab_size) return GLACIER_HIP_SHAPE_MISMATCH;
   if (ln.kv.len + n > s->opt.max_positions) return GLACIER_HIP_CACHE_FULL;
   GH_SUBMISSION(s->model->ctx);
+  if (s->prep.active) return GLACIER_HIP_TRANSACTION_ACTIVE;
+  if (ln.first_pending || ln.retired || !ln.output.empty()) return GLACIER_HIP_INVALID_TRANSACTION;
   std::vector<RowTxn> txns;
   for (uint32_t done = 0; done < n;) {
     const uint32_t rows = std::min(n - done, s->prefill_chunk);
@@ -1126,9 +1328,26 @@ int glacier_hip_session_prefill(glacier_hip_session *s, uint32_t lane, const uin
     done += rows;
   }
   *first_token = (uint32_t)s->res_host[0].index;
-  ln.sampling_calls += 1;
-  ln.output.push_back(*first_token);
+  ln.prompt_len = ln.kv.len;
+  if (staged) {  // held for the first publication wave
+    ln.first_pending = true;
+    ln.first_token = *first_token;
+  } else {
+    ln.sampling_calls += 1;
+    ln.output.push_back(*first_token);
+  }
   return GLACIER_HIP_OK;
+}
+
+int glacier_hip_session_prefill(glacier_hip_session *s, uint32_t lane, const uint32_t *tokens,
+                                uint32_t n, uint32_t *first_token, float *logits_host) {
+  return prefill_impl(s, lane, tokens, n, first_token, logits_host, false);
+}
+
+int glacier_hip_session_prefill_staged(glacier_hip_session *s, uint32_t lane,
+                                       const uint32_t *tokens, uint32_t n, uint32_t *first_token,
+                                       float *logits_host) {
+  return prefill_impl(s, lane, tokens, n, first_token, logits_host, true);
 }
 
 int glacier_hip_session_decode_step(glacier_hip_session *s, const uint32_t *lanes,
@@ -1146,6 +1365,10 @@ int glacier_hip_session_decode_step(glacier_hip_session *s, const uint32_t *lane
     if (s->lanes[lanes[i]].kv.len + 1 > s->opt.max_positions) return GLACIER_HIP_CACHE_FULL;
   }
   GH_SUBMISSION(s->model->ctx);
+  if (s->prep.active) return GLACIER_HIP_TRANSACTION_ACTIVE;
+  for (uint32_t i = 0; i < count; ++i)  // a held first token publishes through a wave first
+    if (s->lanes[lanes[i]].first_pending || s->lanes[lanes[i]].retired)
+      return GLACIER_HIP_INVALID_TRANSACTION;
   std::vector<RowTxn> txns;
   int rc = run_step(s, lanes, tokens, count, true, eligible_words_host, logits_host, txns);
   if (rc) return rc;
@@ -1215,28 +1438,7 @@ int glacier_hip_session_read_kv_row(glacier_hip_session *s, uint32_t lane, uint3
 
 int glacier_hip_session_lane_kv_sha256(glacier_hip_session *s, uint32_t lane, uint8_t out[32]) {
   if (!s || !out || lane >= s->lanes.size()) return GLACIER_HIP_INVALID_ARGUMENT;
-  const auto &c = s->model->cfg;
-  const Lane &ln = s->lanes[lane];
-  const size_t kvd = (size_t)c.num_kv_heads * c.head_dim;
-  gh::Sha256 h;
-  h.update("glacier-logical-kv-state-v1\0", 28);
-  h.u64(c.num_layers);
-  h.u64(kvd);
-  h.u64(ln.kv.len);
-  std::vector<float> row(kvd);
-  for (uint32_t l = 0; l < c.num_layers; ++l)
-    for (int v = 0; v < 2; ++v)
-      for (uint64_t p = 0; p < ln.kv.len; ++p) {
-        int rc = glacier_hip_session_read_kv_row(s, lane, l, v, (uint32_t)p, row.data());
-        if (rc) return rc;
-        for (float f : row) {
-          uint32_t b;
-          memcpy(&b, &f, 4);
-          h.u32(b);
-        }
-      }
-  h.final(out);
-  return GLACIER_HIP_OK;
+  return logical_kv_sha256(s, lane, out);
 }
 
 int glacier_hip_session_page_of(glacier_hip_session *s, uint32_t lane, uint32_t logical_page,
@@ -1254,6 +1456,187 @@ int glacier_hip_session_page_generation(glacier_hip_session *s, uint32_t lane,
   const Lane &ln = s->lanes[lane];
   if (logical_page >= ln.kv.page_gen.size()) return GLACIER_HIP_SHAPE_MISMATCH;
   *ownership_generation_out = ln.kv.page_gen[logical_page];
+  return GLACIER_HIP_OK;
+}
+
+}  // extern "C"
+
+extern "C" {
+
+int glacier_hip_session_step_prepare(glacier_hip_session *s, const uint32_t *lanes,
+                                     const uint32_t *tokens, uint32_t count,
+                                     const uint64_t *eligible_words_host,
+                                     const glacier_hip_publication_binding_t *binding,
+                                     glacier_hip_token_proposal_v1_t *proposal_out,
+                                     uint8_t proposal_sha256_out[32], uint32_t *next_tokens,
+                                     float *logits_host) {
+  // Batch.begin's lane validation and proposal (paged_token_txn.zig:346-471,
+  // validateAndBuildLane :832-944, rootTransition :813-872)
+  if (!s || !lanes || !binding || !proposal_out || !proposal_sha256_out || !next_tokens)
+    return GLACIER_HIP_INVALID_ARGUMENT;
+  if (count == 0 || count > GLACIER_HIP_PUBLICATION_WIDTH || count > s->lanes.size())
+    return GLACIER_HIP_SHAPE_MISMATCH;
+  const auto &c = s->model->cfg;
+  uint32_t mask = 0;
+  int first = -1;
+  for (uint32_t i = 0; i < count; ++i) {
+    if (lanes[i] >= s->lanes.size() || !s->lanes[lanes[i]].kv.active) return GLACIER_HIP_INVALID_ARGUMENT;
+    for (uint32_t j = 0; j < i; ++j)
+      if (lanes[j] == lanes[i]) return GLACIER_HIP_INVALID_ARGUMENT;
+    const uint32_t slot = binding->lane_index[i];
+    if (slot >= GLACIER_HIP_PUBLICATION_WIDTH || (mask >> slot & 1)) return GLACIER_HIP_INVALID_ARGUMENT;
+    mask |= 1u << slot;
+    const Lane &ln = s->lanes[lanes[i]];
+    if (ln.retired) return GLACIER_HIP_INVALID_TRANSACTION;
+    const int kind = ln.first_pending ? 1 : 0;
+    if (!kind && !ln.chain_init) return GLACIER_HIP_INVALID_TRANSACTION;  // no first wave yet
+    if (first >= 0 && first != kind) return GLACIER_HIP_INVALID_TRANSACTION;  // one kind per wave
+    first = kind;
+    if (!kind) {
+      if (!tokens || tokens[i] >= c.vocab_size) return GLACIER_HIP_SHAPE_MISMATCH;
+      if (ln.kv.len + 1 > s->opt.max_positions) return GLACIER_HIP_CACHE_FULL;
+      if (ln.kv.len + 1 != ln.prompt_len + ln.output.size()) return GLACIER_HIP_INVALID_TRANSACTION;
+    }
+  }
+  GH_SUBMISSION(s->model->ctx);
+  if (s->prep.active) return GLACIER_HIP_TRANSACTION_ACTIVE;
+  PreparedWave &P = s->prep;
+  P.txns.clear();
+  P.lanes.assign(lanes, lanes + count);
+  P.slots.assign(binding->lane_index, binding->lane_index + count);
+  P.tokens.assign(count, 0);
+  P.first = first == 1;
+  P.elig = eligible_words_host != nullptr;
+  std::vector<std::array<uint8_t, 32>> digests;
+  if (!P.first) {
+    int rc = run_step(s, lanes, tokens, count, true, eligible_words_host, logits_host, P.txns);
+    if (rc) return rc;
+    rc = row_payload_sha256(s, P.txns, digests);
+    if (rc) {
+      abort_rows(s, P.txns);
+      return rc;
+    }
+    for (uint32_t i = 0; i < count; ++i) P.tokens[i] = (uint32_t)s->res_host[i].index;
+  } else {
+    for (uint32_t i = 0; i < count; ++i) P.tokens[i] = s->lanes[lanes[i]].first_token;
+  }
+  glacier_hip_token_proposal_v1_t &pr = P.proposal;
+  gpub::empty_proposal(pr);
+  pr.execution_abi = binding->execution_abi;
+  pr.request_epoch = binding->request_epoch;
+  pr.transaction_sequence = binding->transaction_sequence;
+  pr.resource_permit_generation = binding->resource_permit_generation;
+  pr.live_mask = mask;
+  pr.live_lane_count = count;
+  pr.kv_capacity_bytes = binding->kv_capacity_bytes;
+  pr.receipt = binding->receipt;
+  for (uint32_t i = 0; i < count; ++i) {
+    Lane &ln = s->lanes[lanes[i]];
+    glacier_hip_lane_proposal_v1_t &lp = pr.lanes[P.slots[i]];
+    glacier_hip_root_transition_v1_t &t = lp.kv_transition;
+    lp.lane_index = P.slots[i];
+    lp.step_index = ln.output.size();
+    lp.prompt_len = ln.prompt_len;
+    lp.kv_capacity_bytes = lane_capacity_bytes(s);
+    if (P.first) {  // initialRootTransition (:790-811)
+      uint8_t kv_sha[32];
+      int rc = logical_kv_sha256(s, lanes[i], kv_sha);
+      if (rc) return rc;
+      const glacier_hip_page_map_root_t &r = ln.kv.root;
+      lp.has_kv_transition = 0;
+      lp.kv_before = lp.kv_after = ln.kv.len;
+      t.cache_instance = r.cache_instance;
+      copy_root(r, t, true);
+      copy_root(r, t, false);
+      memcpy(t.initial_logical_kv_sha256, kv_sha, 32);
+      gpub::initial_state_chain(kv_sha, r, t.state_chain_before);
+      memcpy(t.state_chain_after, t.state_chain_before, 32);
+    } else {
+      const RowTxn &rt = P.txns[i];
+      lp.has_kv_transition = 1;
+      lp.kv_before = rt.mark.base_len;
+      lp.kv_after = rt.mark.base_len + 1;
+      t.cache_instance = rt.mark.cache_instance;
+      t.row_txn_generation = rt.mark.generation;
+      copy_root(rt.before, t, true);
+      copy_root(rt.after, t, false);
+      t.logical_page = rt.mark.page_ref.logical_page;
+      t.page_ownership_generation = rt.mark.page_ref.ownership_generation;
+      t.installs_new_page = rt.installs ? 1 : 0;
+      memcpy(t.row_payload_sha256, digests[i].data(), 32);
+      memcpy(t.state_chain_before, ln.chain, 32);
+      gpub::appended_state_chain(ln.chain, rt.before, rt.after, rt.mark, digests[i].data(),
+                                 t.state_chain_after);
+    }
+    lp.output_before = ln.output.size();
+    lp.output_after = ln.output.size() + 1;
+    memcpy(lp.rng_before, ln.rng, sizeof ln.rng);
+    memcpy(lp.rng_after, ln.rng, sizeof ln.rng);  // greedy: the RNG never advances
+    lp.sampling_calls_before = ln.sampling_calls;
+    // the greedy sampler counts a call (generate.zig:5593), the eligible
+    // posthead branch does not (:5574-5598); the first token is greedy
+    lp.sampling_calls_after = ln.sampling_calls + ((P.first || !P.elig) ? 1 : 0);
+    lp.token_id = P.tokens[i];
+    lp.terminal = binding->terminal[i] ? 1 : 0;
+  }
+  gpub::proposal_sha256(pr, P.sha);
+  P.active = true;
+  *proposal_out = pr;
+  memcpy(proposal_sha256_out, P.sha, 32);
+  for (uint32_t i = 0; i < count; ++i) next_tokens[i] = P.tokens[i];
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_session_step_abort(glacier_hip_session *s) {
+  // Batch.abort / rollback (:565-600): every staged row aborts; nothing else
+  // was touched
+  if (!s) return GLACIER_HIP_INVALID_ARGUMENT;
+  GH_SUBMISSION(s->model->ctx);
+  if (!s->prep.active) return GLACIER_HIP_INVALID_TRANSACTION;
+  if (!s->prep.first) abort_rows(s, s->prep.txns);
+  s->prep.active = false;
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_session_step_commit(glacier_hip_session *s, const glacier_hip_prepare_ack_v1_t *ack,
+                                    glacier_hip_commit_receipt_v1_t *receipt_out) {
+  // Batch.prepare's ack checks (:503-515) then Batch.commit (:519-563)
+  if (!s || !ack) return GLACIER_HIP_INVALID_ARGUMENT;
+  GH_SUBMISSION(s->model->ctx);
+  PreparedWave &P = s->prep;
+  if (!P.active) return GLACIER_HIP_INVALID_TRANSACTION;
+  if (ack->abi_version != gpub::kPrepareAckAbi || ack->sink_epoch == 0 ||
+      ack->reservation_id == 0 || memcmp(ack->proposal_sha256, P.sha, 32) != 0) {
+    if (!P.first) abort_rows(s, P.txns);
+    P.active = false;
+    return GLACIER_HIP_INVALID_TRANSACTION;
+  }
+  if (!P.first) {
+    const int rc = commit_rows(s, P.txns);  // staged under the session's rule: cannot fail
+    if (rc) {
+      P.active = false;
+      return rc;
+    }
+  }
+  for (size_t i = 0; i < P.lanes.size(); ++i) {
+    Lane &ln = s->lanes[P.lanes[i]];
+    const glacier_hip_lane_proposal_v1_t &lp = P.proposal.lanes[P.slots[i]];
+    memcpy(ln.rng, lp.rng_after, sizeof ln.rng);
+    ln.sampling_calls = lp.sampling_calls_after;
+    ln.output.push_back(lp.token_id);
+    memcpy(ln.chain, lp.kv_transition.state_chain_after, 32);
+    ln.chain_init = true;
+    ln.first_pending = false;
+    if (lp.terminal) ln.retired = true;
+  }
+  if (receipt_out) {
+    memset(receipt_out, 0, sizeof *receipt_out);
+    receipt_out->abi_version = gpub::kCommitReceiptAbi;
+    memcpy(receipt_out->proposal_sha256, P.sha, 32);
+    receipt_out->prepare_ack = *ack;
+    gpub::commit_sha256(P.sha, *ack, receipt_out->commit_sha256);
+  }
+  P.active = false;
   return GLACIER_HIP_OK;
 }
 

@@ -184,6 +184,84 @@ class LaneEvent(C.Structure):
 
 _LW = [C.POINTER(LaneEvent)]
 
+PUBLICATION_WIDTH = 4
+
+
+class RootTransition(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in (
+        "abi_version", "kv_row_txn_abi", "page_map_root_abi", "page_ref_abi", "cache_instance",
+        "row_txn_generation", "root_before_generation", "root_after_generation",
+        "root_before_len", "root_after_len", "root_before_pages", "root_after_pages")] + \
+        [("root_before_ownership_sha256", C.c_uint8 * 32),
+         ("root_after_ownership_sha256", C.c_uint8 * 32),
+         ("logical_page", C.c_uint64), ("page_ownership_generation", C.c_uint64),
+         ("installs_new_page", C.c_uint32), ("reserved", C.c_uint32),
+         ("initial_logical_kv_sha256", C.c_uint8 * 32), ("row_payload_sha256", C.c_uint8 * 32),
+         ("state_chain_before", C.c_uint8 * 32), ("state_chain_after", C.c_uint8 * 32)]
+
+
+class LaneProposal(C.Structure):
+    _fields_ = [("lane_index", C.c_uint32), ("has_kv_transition", C.c_uint32)] + \
+        [(n, C.c_uint64) for n in ("step_index", "prompt_len", "kv_before", "kv_after",
+                                   "kv_capacity_bytes")] + \
+        [("kv_transition", RootTransition), ("output_before", C.c_uint64),
+         ("output_after", C.c_uint64), ("rng_before", C.c_uint64 * 4),
+         ("rng_after", C.c_uint64 * 4), ("sampling_calls_before", C.c_uint64),
+         ("sampling_calls_after", C.c_uint64), ("token_id", C.c_uint32), ("terminal", C.c_uint32)]
+
+
+class TokenProposal(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in (
+        "abi_version", "resource_bank_abi", "resource_publication_fence_abi", "paged_kv_abi",
+        "page_map_root_abi", "page_ref_abi", "page_transition_abi", "kv_row_txn_abi",
+        "execution_abi", "request_epoch", "transaction_sequence", "resource_permit_generation")] + \
+        [("live_mask", C.c_uint32), ("live_lane_count", C.c_uint32),
+         ("kv_capacity_bytes", C.c_uint64), ("receipt", BankReceipt),
+         ("lanes", LaneProposal * PUBLICATION_WIDTH)]
+
+
+class PrepareAck(C.Structure):
+    _fields_ = [("abi_version", C.c_uint64), ("proposal_sha256", C.c_uint8 * 32),
+                ("sink_epoch", C.c_uint64), ("reservation_id", C.c_uint64)]
+
+
+class CommitReceipt(C.Structure):
+    _fields_ = [("abi_version", C.c_uint64), ("proposal_sha256", C.c_uint8 * 32),
+                ("prepare_ack", PrepareAck), ("commit_sha256", C.c_uint8 * 32)]
+
+
+class PublicationBinding(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("execution_abi", "request_epoch",
+                                          "transaction_sequence", "resource_permit_generation",
+                                          "kv_capacity_bytes")] + \
+        [("receipt", BankReceipt), ("lane_index", C.c_uint32 * PUBLICATION_WIDTH),
+         ("terminal", C.c_uint32 * PUBLICATION_WIDTH)]
+
+
+PREPARE_ACK_ABI = 0x4750544100000001
+
+
+class CommandToken(C.Structure):
+    _fields_ = [("context_nonce", C.c_uint64 * 4), ("generation", C.c_uint64)]
+
+
+class AsyncSubmission(C.Structure):
+    _fields_ = [("abi_version", C.c_uint64), ("token", CommandToken),
+                ("submission_binding", C.c_uint8 * 32), ("disposition", C.c_uint32),
+                ("reserved", C.c_uint32)]
+
+
+class AsyncCompletion(C.Structure):
+    _fields_ = [("abi_version", C.c_uint64), ("token", CommandToken),
+                ("submission_binding", C.c_uint8 * 32), ("current_allocated_before", C.c_uint64),
+                ("current_allocated_after", C.c_uint64), ("gpu_start_time", C.c_double),
+                ("gpu_end_time", C.c_double), ("error_code", C.c_int64)] + \
+        [(n, C.c_uint32) for n in ("state", "command_status", "error_domain_kind",
+                                   "error_present", "callback_fault", "reserved")]
+
+
+COMMAND_PENDING, COMMAND_COMPLETED, COMMAND_ERROR, COMMAND_UNKNOWN = 1, 2, 3, 4
+
 # (name, restype, argtypes) for every exported symbol of include/glacier_hip.h
 _SIGS = [
     ("glacier_hip_abi_version", C.c_uint64, []),
@@ -202,6 +280,7 @@ _SIGS = [
     ("glacier_hip_allocation_allocate", C.c_int,
      [_P, C.POINTER(AllocationQuote), C.POINTER(BufferToken)]),
     ("glacier_hip_allocation_free", C.c_int, [_P, C.POINTER(BufferToken)]),
+    ("glacier_hip_live_device_bytes", C.c_int, [_P, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
     ("glacier_hip_int4_weight_create", _P,
      [_P, _P, C.c_uint64, _P, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32]),
     ("glacier_hip_int4_weight_create_f16scales", _P,
@@ -210,6 +289,20 @@ _SIGS = [
     ("glacier_hip_live_weight_count", C.c_int, [_P, C.POINTER(C.c_uint64)]),
     ("glacier_hip_int4_weight_device_bytes", C.c_uint64, [_P]),
     ("glacier_hip_int4_matvec_dispatch", C.c_int, [_P, _P, _P, C.c_uint64, _P, C.c_uint64]),
+    ("glacier_hip_int4_registered_buffers_submit_async", C.c_int,
+     [_P] + [C.POINTER(BufferToken)] * 4 + [_P, C.c_uint64, _P, C.c_uint64, _P, C.c_uint64,
+                                            C.c_uint32, C.c_uint32, C.c_uint32, _P,
+                                            C.POINTER(AsyncSubmission)]),
+    ("glacier_hip_registered_dispatch_poll", C.c_int,
+     [_P, C.POINTER(CommandToken), _P, C.POINTER(AsyncCompletion)]),
+    ("glacier_hip_registered_dispatch_wait", C.c_int,
+     [_P, C.POINTER(CommandToken), _P, C.POINTER(AsyncCompletion)]),
+    ("glacier_hip_registered_dispatch_finalize", C.c_int,
+     [_P, C.POINTER(CommandToken), _P, C.POINTER(AsyncCompletion)]),
+    ("glacier_hip_int4_registered_output_read", C.c_int,
+     [_P, C.POINTER(CommandToken), _P, C.POINTER(AsyncCompletion), C.POINTER(BufferToken), _P,
+      C.c_uint64]),
+    ("glacier_hip_live_command_count", C.c_int, [_P, C.POINTER(C.c_uint64)]),
     ("glacier_hip_int4_gemv", C.c_int, [_P, _P, _P, C.c_int, C.c_uint32, _P, _P, C.c_int, _P]),
     ("glacier_hip_activation_bytes", C.c_uint64, [C.c_uint32, C.c_uint32, C.c_int]),
     ("glacier_hip_activation_prepare", C.c_int,
@@ -219,6 +312,9 @@ _SIGS = [
     ("glacier_hip_paged_attention", C.c_int,
      [_P, _P, _P, C.c_int, _P, C.c_uint32, _P, C.c_uint32, C.c_uint32, C.c_uint32,
       C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, _P, _P]),
+    ("glacier_hip_paged_attention_prefill", C.c_int,
+     [_P, _P, _P, _P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+      C.c_uint32, C.c_uint32, _P, _P]),
     ("glacier_hip_argmax", C.c_int, [_P, _P, C.c_uint64, C.c_uint32, _P, _P]),
     ("glacier_hip_eligible_argmax", C.c_int,
      [_P, _P, C.c_uint64, _P, C.c_uint64, C.c_uint32, C.POINTER(ArgmaxResult), _P]),
@@ -228,6 +324,10 @@ _SIGS = [
     ("glacier_hip_model_init_random", C.c_int, [_P, C.c_uint64]),
     ("glacier_hip_model_destroy", None, [_P]),
     ("glacier_hip_model_weight_bytes", C.c_uint64, [_P]),
+    ("glacier_hip_model_quote", C.c_int,
+     [_P, C.POINTER(ModelConfig), C.c_int, C.POINTER(AllocationQuote)]),
+    ("glacier_hip_session_quote", C.c_int,
+     [_P, C.POINTER(SessionOptions), C.POINTER(AllocationQuote)]),
     ("glacier_hip_session_create", _P, [_P, C.POINTER(SessionOptions)]),
     ("glacier_hip_session_destroy", None, [_P]),
     ("glacier_hip_session_lane_begin", C.c_int, [_P, C.c_uint32, C.c_uint64]),
@@ -255,6 +355,15 @@ _SIGS = [
     ("glacier_hip_kv_pages_validate_page_ref", C.c_int, [_P, C.POINTER(PageRef)]),
     ("glacier_hip_kv_pages_ledger", C.c_int, [_P, C.POINTER(ResidentLedger)]),
     ("glacier_hip_session_inject_failure", C.c_int, [_P, C.c_int]),
+    ("glacier_hip_session_prefill_staged", C.c_int, [_P, C.c_uint32, _P, C.c_uint32, _P, _P]),
+    ("glacier_hip_session_step_prepare", C.c_int,
+     [_P, _P, _P, C.c_uint32, _P, C.POINTER(PublicationBinding), C.POINTER(TokenProposal), _P,
+      _P, _P]),
+    ("glacier_hip_session_step_commit", C.c_int,
+     [_P, C.POINTER(PrepareAck), C.POINTER(CommitReceipt)]),
+    ("glacier_hip_session_step_abort", C.c_int, [_P]),
+    ("glacier_hip_token_proposal_sha256", C.c_int, [C.POINTER(TokenProposal), _P]),
+    ("glacier_hip_token_commit_sha256", C.c_int, [_P, C.POINTER(PrepareAck), _P]),
     ("glacier_hip_synth_int4", None, [C.c_uint64, C.c_uint64, _P, C.c_uint64]),
     ("glacier_hip_synth_scales_f16", None, [C.c_uint64, C.c_uint64, C.c_float, _P, C.c_uint64]),
     ("glacier_hip_synth_normal_f32", None, [C.c_uint64, C.c_uint64, C.c_float, _P, C.c_uint64]),
@@ -538,6 +647,36 @@ class Session:
         v = C.c_int32()
         check(lib().glacier_hip_session_page_of(self.h, lane, logical_page, C.byref(v)), "page_of")
         return v.value
+
+    def prefill_staged(self, lane, tokens):
+        toks = np.ascontiguousarray(tokens, dtype=np.uint32)
+        first = np.zeros(1, dtype=np.uint32)
+        check(lib().glacier_hip_session_prefill_staged(self.h, lane, ptr(toks), toks.size,
+                                                       ptr(first), None),
+              "prefill_staged", self.model.ctx.h)
+        return int(first[0])
+
+    def step_prepare(self, lanes, tokens, binding, eligible=None):
+        """Returns (rc, proposal, proposal_sha256 bytes, next tokens)."""
+        lanes = np.ascontiguousarray(lanes, dtype=np.uint32)
+        toks = np.ascontiguousarray(tokens if tokens is not None else np.zeros(lanes.size),
+                                    dtype=np.uint32)
+        nxt = np.zeros(lanes.size, dtype=np.uint32)
+        el = None if eligible is None else np.ascontiguousarray(eligible, dtype=np.uint64)
+        prop = TokenProposal()
+        sha = (C.c_uint8 * 32)()
+        rc = lib().glacier_hip_session_step_prepare(self.h, ptr(lanes), ptr(toks), lanes.size,
+                                                    ptr(el), C.byref(binding), C.byref(prop),
+                                                    sha, ptr(nxt), None)
+        return rc, prop, bytes(sha), nxt
+
+    def step_commit(self, ack):
+        rec = CommitReceipt()
+        rc = lib().glacier_hip_session_step_commit(self.h, C.byref(ack), C.byref(rec))
+        return rc, rec
+
+    def step_abort(self):
+        return lib().glacier_hip_session_step_abort(self.h)
 
     def page_generation(self, lane, logical_page):
         v = C.c_uint64()

@@ -167,6 +167,14 @@ int glacier_hip_allocation_allocate(glacier_hip_context *ctx,
                                     const glacier_hip_allocation_quote_t *quote,
                                     glacier_hip_buffer_token_t *out);
 int glacier_hip_allocation_free(glacier_hip_context *ctx, const glacier_hip_buffer_token_t *token);
+/* Device bytes the context holds for every object it created (buffers,
+ * weights, models, sessions, scratch): requested and charged at the
+ * allocation granularity. Models and sessions quote their exact charge
+ * (glacier_hip_model_quote / glacier_hip_session_quote) without allocating,
+ * so a host charges its ResourceBank before it creates them
+ * (device_allocation_lease.zig:1-14). */
+int glacier_hip_live_device_bytes(glacier_hip_context *ctx, uint64_t *requested_out,
+                                  uint64_t *charged_out);
 
 /* ---- persistent INT4 weights (backend.zig:570-598) -----------------------
  * `packed` is the reference's row-major layout [out_f * in_f / 2] bytes, low
@@ -196,14 +204,88 @@ int glacier_hip_int4_matvec_dispatch(glacier_hip_context *ctx, glacier_hip_int4_
                                      const float *input, uint64_t input_count,
                                      float *output, uint64_t output_count);
 
+/* ---- asynchronous registered-buffer dispatch (backend.zig:600-668;
+ *      shim.m registered_buffers_submit_async .. int4_registered_output_read)
+ * submit_async copies a reference-layout INT4 weight, its f32 scales and an
+ * f32 input into four registered buffers (buffer_create tokens), queues the
+ * f32-semantics matvec into the output buffer on the context stream and
+ * returns a command token bound to the caller's 32-byte submission binding.
+ * poll / wait report the command (pending, completed, error) with GPU start
+ * and end times (seconds from the context's creation); output_read copies the
+ * output after completion; finalize retires a completed command whose exact
+ * completion record the caller presents. Until finalize the command keeps
+ * its buffers alive (buffer_release returns BUSY). Status codes: OK,
+ * INVALID_ARGUMENT (malformed call), INVALID_HANDLE (no such live command for
+ * this token and binding), INVALID_TRANSACTION (not completed, or the
+ * completion record differs), SHAPE_MISMATCH (buffer too small / not the
+ * command's output). */
+typedef struct {
+    uint64_t context_nonce[4];
+    uint64_t generation;             /* 0 = none */
+} glacier_hip_command_token_t;          /* MetalCommandToken (backend.zig:101-112) */
+
+enum glacier_hip_command_state {
+    GLACIER_HIP_COMMAND_PENDING = 1, GLACIER_HIP_COMMAND_COMPLETED = 2,
+    GLACIER_HIP_COMMAND_ERROR = 3, GLACIER_HIP_COMMAND_UNKNOWN = 4,
+};
+
+typedef struct {
+    uint64_t abi_version;            /* 0x474d415300000001 */
+    glacier_hip_command_token_t token;
+    uint8_t submission_binding[32];
+    uint32_t disposition;            /* 1 submitted, 2 submitted_or_ambiguous */
+    uint32_t reserved;
+} glacier_hip_async_submission_t;       /* MetalAsyncSubmission (:135-142) */
+
+typedef struct {
+    uint64_t abi_version;            /* 0x474d414300000001 */
+    glacier_hip_command_token_t token;
+    uint8_t submission_binding[32];
+    uint64_t current_allocated_before, current_allocated_after;  /* live buffer bytes */
+    double gpu_start_time, gpu_end_time;
+    int64_t error_code;              /* hipError_t of a failed command */
+    uint32_t state;                  /* glacier_hip_command_state */
+    uint32_t command_status, error_domain_kind, error_present, callback_fault, reserved;
+} glacier_hip_async_completion_t;       /* MetalAsyncCompletion (:144-159) */
+
+int glacier_hip_int4_registered_buffers_submit_async(
+    glacier_hip_context *ctx, const glacier_hip_buffer_token_t *packed_token,
+    const glacier_hip_buffer_token_t *scales_token, const glacier_hip_buffer_token_t *input_token,
+    const glacier_hip_buffer_token_t *output_token, const uint8_t *packed_weights,
+    uint64_t packed_bytes, const float *scales, uint64_t scale_count, const float *input,
+    uint64_t input_count, uint32_t group_size, uint32_t in_features, uint32_t out_features,
+    const uint8_t submission_binding[32], glacier_hip_async_submission_t *submission);
+int glacier_hip_registered_dispatch_poll(glacier_hip_context *ctx,
+                                         const glacier_hip_command_token_t *token,
+                                         const uint8_t submission_binding[32],
+                                         glacier_hip_async_completion_t *completion);
+int glacier_hip_registered_dispatch_wait(glacier_hip_context *ctx,
+                                         const glacier_hip_command_token_t *token,
+                                         const uint8_t submission_binding[32],
+                                         glacier_hip_async_completion_t *completion);
+int glacier_hip_registered_dispatch_finalize(glacier_hip_context *ctx,
+                                             const glacier_hip_command_token_t *token,
+                                             const uint8_t submission_binding[32],
+                                             const glacier_hip_async_completion_t *expected);
+int glacier_hip_int4_registered_output_read(glacier_hip_context *ctx,
+                                            const glacier_hip_command_token_t *token,
+                                            const uint8_t submission_binding[32],
+                                            const glacier_hip_async_completion_t *expected,
+                                            const glacier_hip_buffer_token_t *output_token,
+                                            float *output, uint64_t output_count);
+/* Submitted commands not yet finalized (backend.zig:664). */
+int glacier_hip_live_command_count(glacier_hip_context *ctx, uint64_t *out);
+
 /* Device-resident batched projection: y[m][out_f] = x[m][in_f] W^T
  * (+ bias[out_f]), m in 1..GLACIER_HIP_MAX_ROWS. x is f32 or bf16 (x_dtype),
  * y is f32. Replaces linearInt4WeightQ8 / linearInt4Weight
- * (int4_matmul.zig:422-531, 2957-2981) for one projection over m rows: up to
- * 5 rows run the decode GEMV, more rows (decode batches, prompt chunks,
- * the packed batch of forwardLayerPackedBatch, generate.zig:2105) the MFMA
- * GEMM; both compute every row with the same per-group arithmetic.
- * Asynchronous on `stream`. */
+ * (int4_matmul.zig:422-531, 2957-2981) for one projection over m rows: Q8
+ * activations up to 5 rows and F32 ones up to 2 rows run the decode GEMV;
+ * more rows (decode batches, prompt chunks, the packed batch of
+ * forwardLayerPackedBatch, generate.zig:2105) the MFMA GEMM; both compute
+ * every row with the same per-group arithmetic. Asynchronous on `stream`;
+ * each stream has its own activation planes and split-K workspace (grown on
+ * the first call with larger sizes; later calls only launch kernels). */
 #define GLACIER_HIP_MAX_ROWS 65536u
 int glacier_hip_int4_gemv(glacier_hip_context *ctx, glacier_hip_int4_weight *weight,
                           const void *x_dev, int x_dtype, uint32_t m,
@@ -246,6 +328,20 @@ int glacier_hip_paged_attention(glacier_hip_context *ctx, const float *q_dev,
                                 uint32_t layer, uint32_t num_layers, uint32_t num_heads,
                                 uint32_t num_kv_heads, uint32_t head_dim,
                                 uint32_t max_ctx, float *out_dev, void *stream);
+
+/* Causal attention for a chunk of T query rows of one lane at positions
+ * pos0 .. pos0 + T - 1 (attentionMultiHead with q_seq = T and query_start =
+ * pos0, forward.zig:478-533 / paged_attention.zig:108-210): row i attends to
+ * positions 0 .. pos0 + i, whose K/V rows are already in the lane's pages.
+ * fp16 pools only (the prompt-chunk kernel); page_table_dev is that lane's
+ * int32[max_pages] physical page ids; q_dev / out_dev [T][num_heads * head_dim].
+ * Asynchronous on `stream`; launches only (no scratch). */
+int glacier_hip_paged_attention_prefill(glacier_hip_context *ctx, const float *q_dev,
+                                        const void *kv_pool_dev, const int32_t *page_table_dev,
+                                        uint32_t max_pages, uint32_t pos0, uint32_t T,
+                                        uint32_t layer, uint32_t num_layers, uint32_t num_heads,
+                                        uint32_t num_kv_heads, uint32_t head_dim, float *out_dev,
+                                        void *stream);
 
 /* ---- greedy samplers (sampling.zig:194-206, :55-105) ---------------------
  * rows independent logit rows of length n. Results are written to host
@@ -294,6 +390,10 @@ int glacier_hip_model_set_globals(glacier_hip_model *model, const float *token_e
 int glacier_hip_model_init_random(glacier_hip_model *model, uint64_t seed);
 void glacier_hip_model_destroy(glacier_hip_model *model);
 uint64_t glacier_hip_model_weight_bytes(const glacier_hip_model *model);
+/* The device bytes a model of `cfg` takes once every layer and the globals
+ * are set (side-effect free). */
+int glacier_hip_model_quote(glacier_hip_context *ctx, const glacier_hip_model_config_t *cfg,
+                            int with_qkv_bias, glacier_hip_allocation_quote_t *out);
 
 /* ---- sessions: paged KV pool + lanes, the per-token step -----------------
  * A session owns a pool of KV pages (each holds 16 positions of every layer,
@@ -391,6 +491,10 @@ typedef struct {
 glacier_hip_session *glacier_hip_session_create(glacier_hip_model *model,
                                                 const glacier_hip_session_options_t *opts);
 void glacier_hip_session_destroy(glacier_hip_session *s);
+/* The device bytes glacier_hip_session_create would allocate for these
+ * options (side-effect free; computed from the same allocation list). */
+int glacier_hip_session_quote(glacier_hip_model *model, const glacier_hip_session_options_t *opts,
+                              glacier_hip_allocation_quote_t *out);
 /* Start a request on `lane` (resets its cache and counters). */
 int glacier_hip_session_lane_begin(glacier_hip_session *s, uint32_t lane, uint64_t seed);
 /* Prefill: run `n` prompt tokens on `lane` and produce the first greedy
@@ -564,6 +668,116 @@ int glacier_hip_session_lane_weave_wave(glacier_hip_session *s, glacier_hip_lane
                                         const uint64_t *eligible_by_lane, uint32_t max_count,
                                         uint32_t *slots_out, glacier_hip_lane_event_t *events_out,
                                         uint32_t *count_out);
+
+/* ---- staged per-token publication (paged_token_txn.zig:346-600) ----------
+ * The reference publishes a decode wave in three phases: the engine stages
+ * every lane's token transition as a proposal (KV row / page-map root
+ * transition, RNG, sampler counter, output word, token, terminal flag) sealed
+ * by proposalSha256; the host's sink reserves it (prepare -> ack); then the
+ * engine commits, a step with no failure path, and hands the sink one receipt.
+ * step_prepare runs the device step with the KV rows left provisional and
+ * returns the proposal; step_commit checks the sink's ack and publishes;
+ * step_abort (a rejected or abandoned proposal) publishes nothing: the rows
+ * are aborted (their generations stay consumed) and the RNG, sampler counter
+ * and outputs are unchanged. Records keep the reference's fields in order
+ * (u8/bool fields widened to u32); proposalSha256 hashes them with the
+ * reference's widths. A wave holds 1..GLACIER_HIP_PUBLICATION_WIDTH lanes
+ * (the reference's fixed B4 width). The Bank receipt, fence permit and
+ * sequence are the host's (its ResourceBank), passed in the binding. */
+#define GLACIER_HIP_PUBLICATION_WIDTH 4
+
+typedef struct {
+    uint64_t abi_version;            /* 0x4750545200000001 */
+    uint64_t kv_row_txn_abi, page_map_root_abi, page_ref_abi;
+    uint64_t cache_instance, row_txn_generation;
+    uint64_t root_before_generation, root_after_generation;
+    uint64_t root_before_len, root_after_len, root_before_pages, root_after_pages;
+    uint8_t root_before_ownership_sha256[32], root_after_ownership_sha256[32];
+    uint64_t logical_page, page_ownership_generation;
+    uint32_t installs_new_page, reserved;
+    uint8_t initial_logical_kv_sha256[32];  /* first wave only */
+    uint8_t row_payload_sha256[32];         /* logicalRowTxnSha256 of the staged row */
+    uint8_t state_chain_before[32], state_chain_after[32];
+} glacier_hip_root_transition_v1_t;     /* RootTransitionV1 (paged_token_txn.zig:61-89) */
+
+typedef struct {
+    uint32_t lane_index, has_kv_transition;
+    uint64_t step_index, prompt_len, kv_before, kv_after, kv_capacity_bytes;
+    glacier_hip_root_transition_v1_t kv_transition;
+    uint64_t output_before, output_after;
+    uint64_t rng_before[4], rng_after[4];
+    uint64_t sampling_calls_before, sampling_calls_after;
+    uint32_t token_id, terminal;
+} glacier_hip_lane_proposal_v1_t;       /* LaneProposalV1 (:91-108) */
+
+typedef struct {
+    uint64_t abi_version;            /* 0x4750545800000001 */
+    uint64_t resource_bank_abi, resource_publication_fence_abi, paged_kv_abi;
+    uint64_t page_map_root_abi, page_ref_abi, page_transition_abi, kv_row_txn_abi;
+    uint64_t execution_abi, request_epoch, transaction_sequence, resource_permit_generation;
+    uint32_t live_mask, live_lane_count;
+    uint64_t kv_capacity_bytes;
+    glacier_hip_bank_receipt_t receipt;
+    glacier_hip_lane_proposal_v1_t lanes[GLACIER_HIP_PUBLICATION_WIDTH];
+} glacier_hip_token_proposal_v1_t;      /* ProposalV1 (:110-131) */
+
+typedef struct {
+    uint64_t abi_version;            /* 0x4750544100000001 */
+    uint8_t proposal_sha256[32];
+    uint64_t sink_epoch;             /* nonzero */
+    uint64_t reservation_id;         /* nonzero */
+} glacier_hip_prepare_ack_v1_t;         /* PrepareAckV1 (:133-138) */
+
+typedef struct {
+    uint64_t abi_version;            /* 0x4750544300000001 */
+    uint8_t proposal_sha256[32];
+    glacier_hip_prepare_ack_v1_t prepare_ack;
+    uint8_t commit_sha256[32];       /* commitSha256 (:1132-1148) */
+} glacier_hip_commit_receipt_v1_t;      /* CommitReceiptV1 (:140-146); its proposal is prepare's */
+
+/* The host publication session's side of a wave (Session.init / Batch.begin,
+ * :262-471): its execution ABI, request epoch, sequence, the fence permit's
+ * generation, the cohort's KV capacity and its Bank receipt, and for each
+ * wave lane (in the order of the step's lanes) its publication slot and
+ * whether this token ends its request. */
+typedef struct {
+    uint64_t execution_abi, request_epoch, transaction_sequence, resource_permit_generation;
+    uint64_t kv_capacity_bytes;
+    glacier_hip_bank_receipt_t receipt;
+    uint32_t lane_index[GLACIER_HIP_PUBLICATION_WIDTH];
+    uint32_t terminal[GLACIER_HIP_PUBLICATION_WIDTH];
+} glacier_hip_publication_binding_t;
+
+/* Prefill for staged publication: the prompt rows commit as in
+ * glacier_hip_session_prefill, the first greedy token is computed and held
+ * back for the first wave (published by step_prepare/step_commit). */
+int glacier_hip_session_prefill_staged(glacier_hip_session *s, uint32_t lane,
+                                       const uint32_t *tokens, uint32_t n,
+                                       uint32_t *first_token, float *logits_host);
+/* Stage one wave of `count` lanes (1..4). Either every lane holds a staged
+ * first token (the first wave: no KV row, an initial transition over the
+ * lane's logical KV digest; tokens[] unused) or every lane has published it
+ * (a decode wave: lanes[i] consumes tokens[i], its row stays provisional).
+ * next_tokens receives the proposed tokens; nothing is published. Until
+ * commit or abort every other step on the session is TRANSACTION_ACTIVE. */
+int glacier_hip_session_step_prepare(glacier_hip_session *s, const uint32_t *lanes,
+                                     const uint32_t *tokens, uint32_t count,
+                                     const uint64_t *eligible_words_host,
+                                     const glacier_hip_publication_binding_t *binding,
+                                     glacier_hip_token_proposal_v1_t *proposal_out,
+                                     uint8_t proposal_sha256_out[32], uint32_t *next_tokens,
+                                     float *logits_host);
+/* Publish the prepared wave after the sink's ack (abi, nonzero epoch and
+ * reservation, the proposal's digest). An invalid ack aborts the wave and
+ * returns INVALID_TRANSACTION. */
+int glacier_hip_session_step_commit(glacier_hip_session *s, const glacier_hip_prepare_ack_v1_t *ack,
+                                    glacier_hip_commit_receipt_v1_t *receipt_out);
+int glacier_hip_session_step_abort(glacier_hip_session *s);
+/* proposalSha256 / commitSha256 of a record (pure host functions). */
+int glacier_hip_token_proposal_sha256(const glacier_hip_token_proposal_v1_t *proposal,
+                                      uint8_t out[32]);
+int glacier_hip_token_commit_sha256(const uint8_t proposal_sha256[32],
+                                    const glacier_hip_prepare_ack_v1_t *ack, uint8_t out[32]);
 
 /* ---- synthetic random-init generator (host, deterministic) ---------------
  * Counter-based SplitMix64 streams keyed by (seed, tensor id):

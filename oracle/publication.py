@@ -1,0 +1,120 @@
+"""Restatement of the per-token publication digests of the reference.
+
+TEST INFRASTRUCTURE ONLY: the checker for the product's staged publication
+(glacier_hip_session_step_prepare / _commit, csrc/publication.cpp). Only
+tests/ use it.
+
+Follows /root/reference/src/paged_token_txn.zig:
+  hashRoot             :762-772
+  initialStateChain    :774-786
+  appendedStateChain   :788-808
+  proposalSha256       :1064-1130  (ProposalV1 :110-131, LaneProposalV1 :91-108,
+                                    RootTransitionV1 :61-89; u8 fields live_mask,
+                                    live_lane_count, bools as one byte)
+  commitSha256         :1132-1148
+and src/paged_kv_cache.zig logicalRowTxnSha256 :1366-1384 (row payload digest).
+Integers little-endian, SHA-256 from hashlib. A record here is the ctypes
+structure of the product's header read field by field, so the byte layout
+this module hashes is written from the reference's field list, not from the
+product's code.
+"""
+import hashlib
+import struct
+
+PAGE_MAP_ROOT_ABI = 0x47504D5200000001
+PAGE_REF_ABI = 0x4750524600000001
+
+
+def _u64(v):
+    return struct.pack("<Q", v)
+
+
+def _u32(v):
+    return struct.pack("<I", v)
+
+
+def _u8(v):
+    return struct.pack("<B", v)
+
+
+def root_bytes(generation, committed_len, committed_pages, ownership, cache_instance):
+    """hashRoot: abi, instance, generation, len, pages, ownership digest."""
+    return (_u64(PAGE_MAP_ROOT_ABI) + _u64(cache_instance) + _u64(generation) +
+            _u64(committed_len) + _u64(committed_pages) + bytes(ownership))
+
+
+def initial_state_chain(logical_kv_sha256, root):
+    return hashlib.sha256(b"glacier-paged-token-kv-chain-seed-v1\x00" + bytes(logical_kv_sha256) +
+                          root).digest()
+
+
+def appended_state_chain(chain_before, root_before, root_after, cache_instance, logical_page,
+                         ownership_generation, row_txn_generation, row_payload_sha256):
+    return hashlib.sha256(
+        b"glacier-paged-token-kv-chain-append-v1\x00" + bytes(chain_before) + root_before +
+        root_after + _u64(PAGE_REF_ABI) + _u64(cache_instance) + _u64(logical_page) +
+        _u64(ownership_generation) + _u64(row_txn_generation) + bytes(row_payload_sha256)).digest()
+
+
+def row_payload_sha256(num_layers, dim, base_len, rows_f32):
+    """logicalRowTxnSha256: rows_f32 = [K_0, V_0, K_1, V_1, ...] f32 rows."""
+    h = hashlib.sha256(b"glacier-paged-kv-row-v1\x00" + _u64(num_layers) + _u64(dim) +
+                       _u64(base_len))
+    for r in rows_f32:
+        h.update(bytes(memoryview(r.astype("<f4")).cast("B")))
+    return h.digest()
+
+
+_PROPOSAL_HEAD = ("abi_version", "resource_bank_abi", "resource_publication_fence_abi",
+                  "paged_kv_abi", "page_map_root_abi", "page_ref_abi", "page_transition_abi",
+                  "kv_row_txn_abi", "execution_abi", "request_epoch", "transaction_sequence",
+                  "resource_permit_generation")
+_CLAIM = ("capsule_bytes", "kv_bytes", "activation_bytes", "partial_bytes", "logits_bytes",
+          "output_journal_bytes", "staging_bytes", "device_bytes", "io_bytes", "queue_slots")
+_TRANSITION_U64 = ("abi_version", "kv_row_txn_abi", "page_map_root_abi", "page_ref_abi",
+                   "cache_instance", "row_txn_generation", "root_before_generation",
+                   "root_after_generation", "root_before_len", "root_after_len",
+                   "root_before_pages", "root_after_pages")
+
+
+def proposal_sha256(p):
+    """proposalSha256 over a ProposalV1 record (any object with the fields)."""
+    b = bytearray(b"glacier-paged-token-txn-proposal-v1\x00")
+    for f in _PROPOSAL_HEAD:
+        b += _u64(getattr(p, f))
+    b += _u8(p.live_mask) + _u8(p.live_lane_count) + _u64(p.kv_capacity_bytes)
+    r = p.receipt
+    b += _u64(r.bank_epoch) + _u32(r.slot_index) + _u64(r.generation) + _u64(r.owner_key)
+    for f in _CLAIM:
+        b += _u64(getattr(r.claim, f))
+    b += _u64(r.integrity)
+    for lane in p.lanes:
+        b += _u32(lane.lane_index)
+        for f in ("step_index", "prompt_len", "kv_before", "kv_after", "kv_capacity_bytes"):
+            b += _u64(getattr(lane, f))
+        b += _u8(1 if lane.has_kv_transition else 0)
+        t = lane.kv_transition
+        for f in _TRANSITION_U64:
+            b += _u64(getattr(t, f))
+        b += bytes(t.root_before_ownership_sha256) + bytes(t.root_after_ownership_sha256)
+        b += _u64(t.logical_page) + _u64(t.page_ownership_generation)
+        b += _u8(1 if t.installs_new_page else 0)
+        b += (bytes(t.initial_logical_kv_sha256) + bytes(t.row_payload_sha256) +
+              bytes(t.state_chain_before) + bytes(t.state_chain_after))
+        b += _u64(lane.output_before) + _u64(lane.output_after)
+        for w in lane.rng_before:
+            b += _u64(w)
+        for w in lane.rng_after:
+            b += _u64(w)
+        b += _u64(lane.sampling_calls_before) + _u64(lane.sampling_calls_after)
+        b += _u32(lane.token_id) + _u8(1 if lane.terminal else 0)
+    return hashlib.sha256(bytes(b)).digest()
+
+
+COMMIT_RECEIPT_ABI = 0x4750544300000001
+
+
+def commit_sha256(proposal_sha, ack_abi, ack_proposal_sha, sink_epoch, reservation_id):
+    return hashlib.sha256(b"glacier-paged-token-txn-commit-v1\x00" + _u64(COMMIT_RECEIPT_ABI) +
+                          bytes(proposal_sha) + _u64(ack_abi) + bytes(ack_proposal_sha) +
+                          _u64(sink_epoch) + _u64(reservation_id)).digest()

@@ -9,8 +9,10 @@ the group term RN(T * s_w) is the reference's; the activation scale is folded
 into the running sum with one fused multiply-add (one rounding fewer per
 group than the reference's separate multiply and add) and the across-group
 order differs -> 2e-6 of max|y|. F32 (three 7-bit digit planes) -> 1e-5.
-At the config sizes (M = 2048) rows are checked against the decode GEMV on
-the same rows, which the oracle pins at small sizes.
+At the config sizes (M = 2048, the 7B prefill projections) a sample of the
+rows is checked directly against the oracle (linear_int4_q8 /
+linear_int4_f32), and the same rows recomputed as 16- and 24-row GEMMs must
+agree with the 2048-row one.
 """
 import numpy as np
 import pytest
@@ -79,10 +81,11 @@ def test_gemm_f32_matches_oracle(gh, gctx, ora, out_f, in_f, m):
 
 @pytest.mark.parametrize("out_f,in_f,act", [(3584, 3584, "q8"), (4608, 3584, "q8"),
                                             (3584, 18944, "f32")])
-def test_gemm_rows_equal_gemv_rows_at_7b_prefill_size(gh, gctx, out_f, in_f, act):
-    """M = 2048 prompt rows: 16 rows spread over the chunk,
-    the first and the last included, equal the decode GEMV of those rows; and
-    24 of them through the 32-row split-K tiles."""
+def test_gemm_at_7b_prefill_size_matches_oracle(gh, gctx, ora, out_f, in_f, act):
+    """M = 2048 prompt rows (the 7B QKV, O-shaped and the
+    3-digit down projection): 32 rows spread over the chunk, the first and
+    the last included, match the oracle; the first 16 and 24 of them run
+    again as 16-row and 32-row (split-K) GEMMs agree with the 2048-row one."""
     a = gh.ACT_Q8 if act == "q8" else gh.ACT_F32
     packed, s16, _ = _weights(gh, 500 + out_f + in_f, out_f, in_f)
     w = gctx.weight(packed, s16, in_f, out_f)
@@ -92,11 +95,18 @@ def test_gemm_rows_equal_gemv_rows_at_7b_prefill_size(gh, gctx, out_f, in_f, act
         big = _proj(gh, gctx, w, out_f, x, a)
         pick = np.unique(np.concatenate([[0, 1, 15, 16, 127, 128, m - 1],
                                          np.random.default_rng(4).choice(m, 25, replace=False)]))
+        bar = 2e-6 if act == "q8" else 1e-5
+        fn = ora.linear_int4_q8 if act == "q8" else ora.linear_int4_f32
+        want = fn(x[pick], packed, s16.view(np.float16).astype(np.float32), out_f, in_f, 32)
+        err = np.max(np.abs(big[pick] - want)) / np.max(np.abs(want))
+        print(f"gemm 2048 rows {out_f}x{in_f} {act} vs oracle on {len(pick)} rows rel={err:.3e}",
+              flush=True)
+        assert err < bar
         for rows in (pick[:16], pick[:24]):
             small = _proj(gh, gctx, w, out_f, x[rows], a)
             err = np.max(np.abs(big[rows] - small)) / np.max(np.abs(small))
             print(f"gemm vs {len(rows)} rows {out_f}x{in_f} {act} rel={err:.3e}", flush=True)
-            assert err < (2e-6 if act == "q8" else 1e-5)
+            assert err < bar
         assert np.all(np.isfinite(big))
     finally:
         gh.lib().glacier_hip_int4_weight_destroy(w)

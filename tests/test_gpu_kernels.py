@@ -289,3 +289,37 @@ def test_paged_attention_c3_config_matches_oracle(gh, gctx, ora):
         err = np.max(np.abs(got[i] - want))
         print(f"c3 ctx={c} abs={err:.2e}", flush=True)
         assert err < 2e-5
+
+
+@pytest.mark.parametrize("geom", [(28, 4, 128), (14, 2, 64)])
+@pytest.mark.parametrize("pos0,T", [(0, 512), (768, 256), (5, 37)])
+def test_prefill_attention_matches_oracle(gh, gctx, ora, geom, pos0, T):
+    """The prompt-chunk kernel (causal attention of T consecutive query rows
+    over one lane's fp16 pages, glacier_hip_paged_attention_prefill) against
+    the oracle's attentionMultiHead with q_seq = T, query_start = pos0, at
+    the 7B geometry (28 q / 4 kv heads, hd 128) and the
+    0.5B one, chunks starting at page boundaries and inside a page; pages
+    scattered by a seeded permutation. Bar 2e-5 absolute on N(0, 1) inputs
+    (the oracle reads the same fp16 KV)."""
+    torch = _torch()
+    Hq, Hkv, hd = geom
+    rng = np.random.default_rng(pos0 + T + Hq)
+    L, layer = 2, 1
+    kv_seq = pos0 + T
+    pool, pt = _paged_case(rng, [kv_seq], Hkv, hd, L, layer, True)
+    q = rng.standard_normal((T, Hq * hd)).astype(np.float32)
+    qd = torch.from_numpy(q).cuda()
+    pdv = torch.from_numpy(pool.view(np.uint16)).cuda()
+    ptd = torch.from_numpy(np.ascontiguousarray(pt[0])).cuda()
+    out = torch.empty((T, Hq * hd), dtype=torch.float32, device="cuda")
+    print(f"prefill attention {Hq}/{Hkv}x{hd} pos0={pos0} T={T}", flush=True)
+    rc = gh.lib().glacier_hip_paged_attention_prefill(
+        gctx.h, qd.data_ptr(), pdv.data_ptr(), ptd.data_ptr(), pt.shape[1], pos0, T, layer, L,
+        Hq, Hkv, hd, out.data_ptr(), None)
+    gh.check(rc, "paged_attention_prefill", gctx.h)
+    gctx.sync()
+    got = out.cpu().numpy()
+    want = ora.attention_paged(q, pool.view(np.uint16), True, pt[0], kv_seq, layer, L, Hq, Hkv, hd)
+    err = float(np.max(np.abs(got - want)))
+    print(f"  abs {err:.2e}", flush=True)
+    assert err < 2e-5

@@ -258,3 +258,51 @@ def test_plan_wave_is_the_next_serial_selections(gh, weights):
             assert ev.handle.slot_index == slot
             assert bytes(ev.event_sha256) == o.serve_one()["event_sha256"]
     assert p.chain_head() == o.chain_head
+
+
+def test_c5_schedule_replays_on_oracle(gh):
+    """BASELINE config 5's scheduler trace, model-free: the 32 admissions of
+    bench.c5_workload, decode waves (the next IWRR quanta of distinct lanes,
+    served in plan order), the retire of each lane once its last quantum is
+    served, then close. The product's event chain equals the oracle's event
+    for event, and its close event is the chain head the bench's device
+    waves report (the device step does not change the schedule)."""
+    import bench
+
+    wl = bench.c5_workload(bench.CFG_7B)
+    lanes = wl["lanes"]
+    p = gh.LaneWeave(lanes, wl["bank"], bank_epoch=wl["bank_epoch"],
+                     scheduler_epoch=wl["scheduler_epoch"], max_weight=wl["max_weight"])
+    o = lw.Scheduler(lw.Bank(lanes, lw.limits(**wl["bank"]), wl["bank_epoch"]), lanes,
+                     wl["scheduler_epoch"], bytes([0xA5]) + bytes(31), wl["max_weight"],
+                     1_000_000, 1_000_000)
+    for sp in wl["specs"]:
+        o_ok, _, o_ev = o.admit(dict(sp, claim=lw.claim(**sp["claim"])))
+        p_ok, _, p_ev = p.admit(_pspec(gh, dict(sp, claim=lw.claim(**sp["claim"]))))
+        assert o_ok and p_ok and bytes(p_ev.event_sha256) == o_ev["event_sha256"]
+    waves = quanta = 0
+    while True:
+        plan = p.plan_wave(lanes)
+        if not plan:
+            break
+        waves += 1
+        finished = []
+        for slot in plan:
+            p_ev, o_ev = p.serve_one(), o.serve_one()
+            assert p_ev.handle.slot_index == slot
+            assert bytes(p_ev.event_sha256) == o_ev["event_sha256"]
+            quanta += 1
+            if p_ev.remaining_after == 0:
+                finished.append(slot)
+        for slot in finished:
+            rc, p_ev = p.retire(p.slot(slot)[0])
+            o_ev = o.retire(o.handle_for(slot))
+            assert rc == 0 and bytes(p_ev.event_sha256) == o_ev["event_sha256"]
+    rc, p_close = p.close()
+    o_close = o.close()
+    assert rc == 0 and bytes(p_close.event_sha256) == o_close["event_sha256"]
+    assert quanta == lanes * (wl["gen"] - 1)
+    print("waves", waves, "close", bytes(p_close.event_sha256).hex())
+    # the chain head of the bench's config-5 run on the GPU (device waves)
+    assert bytes(p_close.event_sha256).hex() == \
+        "7d027cdf284a5173360b19e40f9ba7099533958d46b50fd56d83b44e4b36c06f"

@@ -278,3 +278,66 @@ def test_product_pool_exhaustion_is_cache_full_without_mutation(gh):
     assert rc == gh.CACHE_FULL
     assert bytes(p.root()) == root and p.ledger() == led
     assert p.page(1) == (-1, 0)
+
+
+# ---------------------------------------------------------------------------------
+# per-token publication digests (paged_token_txn.zig:762-808, 1064-1148)
+# ---------------------------------------------------------------------------------
+def _random_proposal(gh, rng):
+    p = gh.TokenProposal()
+    for f, _ in gh.TokenProposal._fields_:
+        if f in ("receipt", "lanes"):
+            continue
+        setattr(p, f, int(rng.integers(0, 1 << 63)) if f not in ("live_mask", "live_lane_count")
+                else int(rng.integers(0, 16)))
+    for f, _ in gh.BankReceipt._fields_:
+        if f == "claim":
+            for g, _ in gh.Claim._fields_:
+                setattr(p.receipt.claim, g, int(rng.integers(0, 1 << 62)))
+        else:
+            setattr(p.receipt, f, int(rng.integers(0, 1 << 32 if f == "slot_index" else 1 << 62)))
+    for lane in p.lanes:
+        for f, t in gh.LaneProposal._fields_:
+            if f == "kv_transition":
+                for g, tt in gh.RootTransition._fields_:
+                    if tt == C.c_uint64:
+                        setattr(lane.kv_transition, g, int(rng.integers(0, 1 << 62)))
+                    elif tt == C.c_uint32:
+                        setattr(lane.kv_transition, g, int(rng.integers(0, 2)))
+                    else:
+                        getattr(lane.kv_transition, g)[:] = rng.integers(0, 256, 32).tolist()
+            elif f in ("rng_before", "rng_after"):
+                getattr(lane, f)[:] = [int(x) for x in rng.integers(0, 1 << 62, 4)]
+            elif t == C.c_uint32:
+                setattr(lane, f, int(rng.integers(0, 1 << 31)) if f in ("lane_index", "token_id")
+                        else int(rng.integers(0, 2)))
+            else:
+                setattr(lane, f, int(rng.integers(0, 1 << 62)))
+    return p
+
+
+import ctypes as C  # noqa: E402
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_product_proposal_and_commit_digests_equal_oracle(gh, seed):
+    """The product's proposalSha256 / commitSha256 (csrc/publication.cpp)
+    equal the oracle's restatement (oracle/publication.py, written from the
+    reference's field list) on random records; a one-byte change of any lane
+    field changes the digest."""
+    import numpy as np
+
+    from oracle import publication as opub
+
+    rng = np.random.default_rng(seed)
+    p = _random_proposal(gh, rng)
+    out = (C.c_uint8 * 32)()
+    assert gh.lib().glacier_hip_token_proposal_sha256(C.byref(p), out) == 0
+    sha = bytes(out)
+    assert sha == opub.proposal_sha256(p)
+    p.lanes[3].token_id ^= 1
+    assert gh.lib().glacier_hip_token_proposal_sha256(C.byref(p), out) == 0
+    assert bytes(out) != sha and bytes(out) == opub.proposal_sha256(p)
+    ack = gh.PrepareAck(gh.PREPARE_ACK_ABI, (C.c_uint8 * 32)(*sha), 0x50414745, 7)
+    assert gh.lib().glacier_hip_token_commit_sha256((C.c_uint8 * 32)(*sha), C.byref(ack), out) == 0
+    assert bytes(out) == opub.commit_sha256(sha, gh.PREPARE_ACK_ABI, sha, 0x50414745, 7)
