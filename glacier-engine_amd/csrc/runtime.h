@@ -59,6 +59,9 @@ struct glacier_hip_context {
   uint64_t next_command_generation = 1;
   uint64_t nonce[4] = {0, 0, 0, 0};
   hipEvent_t origin = nullptr;  // recorded at init: the zero of the GPU times
+  // device address of this device's no-allocation GEMV scratch (null when
+  // hipGetSymbolAddress failed at init; the entry point then refuses)
+  void *noalloc_scratch = nullptr;
 };
 
 struct glacier_hip_int4_weight {

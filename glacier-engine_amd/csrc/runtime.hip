@@ -13,6 +13,15 @@
 
 using gh::hip_fail;
 
+// Scratch of glacier_hip_int4_gemv_noalloc: activation planes, then the
+// GEMM's split-K partial sums. One array per GPU for the life of the
+// process; host code reaches it only through the address
+// hipGetSymbolAddress returns on that device (glacier_hip_init).
+static constexpr size_t kNoAllocPlanesBytes = 4u << 20;
+static constexpr size_t kNoAllocSplitkBytes = 12u << 20;
+static constexpr uint32_t kNoAllocMaxRows = 64;
+static __device__ __align__(256) uint8_t scratch[kNoAllocPlanesBytes + kNoAllocSplitkBytes];
+
 namespace gh {
 
 int hip_fail(glacier_hip_context *ctx, hipError_t e, const char *what) {
@@ -173,6 +182,18 @@ glacier_hip_context *glacier_hip_init(int device_ordinal) {
   if (e == hipSuccess) {
     what = "hipHostMalloc";
     e = hipHostMalloc((void **)&ctx->results_host, sizeof(gk::ArgmaxResult) * 64);
+  }
+  if (e == hipSuccess) {
+    // the no-allocation GEMV's scratch on this (current) device
+    static std::mutex sym_mu;
+    static void *sym_ptr[64] = {};
+    std::lock_guard<std::mutex> lk(sym_mu);
+    if (device_ordinal < 64 && !sym_ptr[device_ordinal]) {
+      void *p = nullptr;
+      if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) == hipSuccess) sym_ptr[device_ordinal] = p;
+      else (void)hipGetLastError();  // reported by the entry point
+    }
+    if (device_ordinal < 64) ctx->noalloc_scratch = sym_ptr[device_ordinal];
   }
   if (e == hipSuccess) {
     what = "identity rows";
@@ -503,8 +524,11 @@ static int act_digits(int activation) {
   return 0;
 }
 
+// ws == null: the stream's split-K workspace, grown on demand; else the
+// caller's (ws_floats floats; a smaller workspace only lowers the K split).
 static int gemv_launch(glacier_hip_context *ctx, glacier_hip_int4_weight *w, const void *planes,
-                       uint32_t m, int D, const float *bias_dev, float *y_dev, hipStream_t st) {
+                       uint32_t m, int D, const float *bias_dev, float *y_dev, hipStream_t st,
+                       float *ws = nullptr, size_t ws_floats = 0) {
   const int N = (int)w->out_f, K = (int)w->in_f;
   gk::GemvArgs a{};
   a.codes = w->codes;
@@ -527,17 +551,22 @@ static int gemv_launch(glacier_hip_context *ctx, glacier_hip_int4_weight *w, con
     GH_CHECK(ctx, gk::launch_gemv(a, st));
     return GLACIER_HIP_OK;
   }
-  auto &ss = ctx->per_stream[st];
-  const size_t need = std::min<size_t>(gk::gemm_splitk_floats(N, (int)m, K, D), 16u << 20);
-  if (need > ss.splitk_floats) {
-    gh::dev_free(ctx, ss.splitk);
-    ss.splitk = nullptr;
-    ss.splitk_floats = 0;
-    GH_CHECK(ctx, gh::dev_malloc(ctx, (void **)&ss.splitk, need * sizeof(float)));
-    ss.splitk_floats = need;
+  if (ws) {
+    a.splitk_ws = ws;
+    a.splitk_ws_floats = ws_floats;
+  } else {
+    auto &ss = ctx->per_stream[st];
+    const size_t need = std::min<size_t>(gk::gemm_splitk_floats(N, (int)m, K, D), 16u << 20);
+    if (need > ss.splitk_floats) {
+      gh::dev_free(ctx, ss.splitk);
+      ss.splitk = nullptr;
+      ss.splitk_floats = 0;
+      GH_CHECK(ctx, gh::dev_malloc(ctx, (void **)&ss.splitk, need * sizeof(float)));
+      ss.splitk_floats = need;
+    }
+    a.splitk_ws = ss.splitk;
+    a.splitk_ws_floats = ss.splitk_floats;
   }
-  a.splitk_ws = ss.splitk;
-  a.splitk_ws_floats = ss.splitk_floats;
   GH_CHECK(ctx, gk::launch_gemm(a, st));
   return GLACIER_HIP_OK;
 }
@@ -581,6 +610,33 @@ int glacier_hip_int4_gemv(glacier_hip_context *ctx, glacier_hip_int4_weight *w, 
   GH_SUBMISSION(ctx);
   return gemv_common(ctx, w, x_dev, x_dtype, m, bias_dev, y_dev, activation,
                      stream ? (hipStream_t)stream : ctx->stream);
+}
+
+int glacier_hip_int4_gemv_noalloc(glacier_hip_context *ctx, glacier_hip_int4_weight *w,
+                                  const void *x_dev, int x_dtype, uint32_t m, const float *bias_dev,
+                                  float *y_dev, int activation, void *stream) {
+  if (!ctx) return GLACIER_HIP_INVALID_HANDLE;
+  if (!w || !x_dev || !y_dev) return GLACIER_HIP_INVALID_ARGUMENT;
+  if (w->ctx != ctx) return GLACIER_HIP_INVALID_HANDLE;
+  if (x_dtype != GLACIER_HIP_F32 && x_dtype != GLACIER_HIP_BF16) return GLACIER_HIP_DTYPE_UNSUPPORTED;
+  const int D = act_digits(gh::resolve_activation(activation, w->out_f, w->in_f));
+  if (!D) return GLACIER_HIP_INVALID_ARGUMENT;
+  GH_SUBMISSION(ctx);
+  if (m == 0 || m > kNoAllocMaxRows || planes_bytes(m, w->in_f, D) > kNoAllocPlanesBytes) {
+    ctx->last_error = "int4_gemv_noalloc: more rows than its fixed scratch holds (at most 64 "
+                      "rows and 4 MiB of activation planes)";
+    return GLACIER_HIP_SHAPE_MISMATCH;
+  }
+  if (!ctx->noalloc_scratch) {
+    ctx->last_error = "int4_gemv_noalloc: no scratch address on this device";
+    return GLACIER_HIP_DEVICE_ERROR;
+  }
+  hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
+  uint8_t *planes = (uint8_t *)ctx->noalloc_scratch;
+  int rc = prepare_launch(ctx, x_dev, x_dtype, m, w->in_f, D, planes, st);
+  if (rc) return rc;
+  return gemv_launch(ctx, w, planes, m, D, bias_dev, y_dev, st,
+                     (float *)(planes + kNoAllocPlanesBytes), kNoAllocSplitkBytes / sizeof(float));
 }
 
 uint64_t glacier_hip_activation_bytes(uint32_t m, uint32_t in_f, int activation) {

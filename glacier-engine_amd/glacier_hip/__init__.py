@@ -304,6 +304,8 @@ _SIGS = [
       C.c_uint64]),
     ("glacier_hip_live_command_count", C.c_int, [_P, C.POINTER(C.c_uint64)]),
     ("glacier_hip_int4_gemv", C.c_int, [_P, _P, _P, C.c_int, C.c_uint32, _P, _P, C.c_int, _P]),
+    ("glacier_hip_int4_gemv_noalloc", C.c_int,
+     [_P, _P, _P, C.c_int, C.c_uint32, _P, _P, C.c_int, _P]),
     ("glacier_hip_activation_bytes", C.c_uint64, [C.c_uint32, C.c_uint32, C.c_int]),
     ("glacier_hip_activation_prepare", C.c_int,
      [_P, _P, C.c_int, C.c_uint32, C.c_uint32, C.c_int, _P, _P]),

@@ -292,6 +292,23 @@ int glacier_hip_int4_gemv(glacier_hip_context *ctx, glacier_hip_int4_weight *wei
                           const float *bias_dev, float *y_dev, int activation,
                           void *stream);
 
+/* glacier_hip_int4_gemv without any allocation. No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). Its
+ * activation planes and GEMM split-K partial sums live in one fixed 16 MiB
+ * array per GPU (4 MiB of planes, 12 MiB of partial sums), held from the
+ * library's load until the process ends; m is at most 64 rows and the planes
+ * of m x in_f at most 4 MiB (SHAPE_MISMATCH otherwise, nothing launched).
+ * Same arithmetic as glacier_hip_int4_gemv (a smaller workspace may lower a
+ * K split, which reorders only the f32 sum across splits). Every call on one
+ * GPU shares that array: calls that overlap on a GPU (from several threads
+ * or contexts, or on several streams) race; each call leaves its contents
+ * behind and needs nothing cleared. Asynchronous on `stream`. */
+int glacier_hip_int4_gemv_noalloc(glacier_hip_context *ctx, glacier_hip_int4_weight *weight,
+                                  const void *x_dev, int x_dtype, uint32_t m,
+                                  const float *bias_dev, float *y_dev, int activation,
+                                  void *stream);
+
 /* The same projection in two phases, as the reference splits it into
  * quantizeQ8Activation (int4_matmul.zig:537-560, glacier_q8_activation_quantize
  * int4_neon.c:453-486) and linearInt4WeightQ8Prepared (int4_matmul.zig:771):
