@@ -43,6 +43,8 @@ INT8_PEAK_OPS = 5.0e15   # MI355X dense int8 MFMA
 SEED = 0x474C4143
 CFG_7B = dict(num_layers=28, dim=3584, hidden_dim=18944, num_heads=28, num_kv_heads=4,
               head_dim=128, vocab_size=152064, group_size=32, rms_eps=1e-6, rope_theta=1e6)
+CFG_05B = dict(num_layers=24, dim=896, hidden_dim=4864, num_heads=14, num_kv_heads=2,
+               head_dim=64, vocab_size=151936, group_size=32, rms_eps=1e-6, rope_theta=1e6)
 # BASELINE config 2 GEMV shapes [N, K] plus the fused 7B gate/up projection
 GEMV_SHAPES = [(4096, 4096), (11008, 4096), (4096, 11008), (18944, 3584), (152064, 3584)]
 GATE_UP = (2 * 18944, 3584)
@@ -63,58 +65,80 @@ def gemv_bytes(n, k, m, digits=1):
 MALL_BYTES = 256 << 20   # MI355X Infinity Cache; rotated weight copies must exceed it
 
 
-def time_gemv(gh, ctx, torch, n, k, m, reps, act):
-    """Cold GEMV timing: the launches rotate over enough weight copies (same
-    content, separate HBM allocations) that the 256 MB MALL cannot serve a
-    repeat, which is the condition of every projection in a decode token (a 7B
-    model is ~4.5 GB of weights). HIP events on the launch stream."""
-    L = gh.lib()
-    packed = gh.synth_int4(SEED, n * 7 + k, n * k // 2)
-    s16 = gh.synth_scales_f16(SEED, n * 11 + k, n * k // 32)
-    wbytes = n * k // 2 + n * k // 16
-    copies = max(2, -(-3 * MALL_BYTES // wbytes))
-    ws = [ctx.weight(packed, s16, k, n) for _ in range(copies)]
-    del packed, s16
-    try:
-        stream = torch.cuda.Stream()  # non-null handle: our launches and the events share it
-        x = torch.randn((m, k), device="cuda", dtype=torch.float32)
-        y = torch.empty((m, n), device="cuda", dtype=torch.float32)
-        planes = torch.empty(L.glacier_hip_activation_bytes(m, k, act), dtype=torch.uint8, device="cuda")
-        torch.cuda.synchronize()
-        gh.check(L.glacier_hip_activation_prepare(ctx.h, x.data_ptr(), gh.F32, m, k, act,
-                                                  planes.data_ptr(), stream.cuda_stream), "prepare")
+class ColdWeights:
+    """Copies of one [n, k] weight (same content, separate HBM allocations),
+    enough that the 256 MB MALL cannot serve a repeat: the condition of every
+    projection in a decode token (a 7B model is ~4.5 GB of weights)."""
 
-        def go(i):
-            return L.glacier_hip_int4_gemv_prepared(ctx.h, ws[i % copies], planes.data_ptr(), m, act,
-                                                    None, y.data_ptr(), stream.cuda_stream)
-        for i in range(copies):
-            gh.check(go(i), "gemv", ctx.h)
-        torch.cuda.synchronize()
-        # the launches are captured into a graph so that host submission cost
-        # (ctypes + launch, several us) does not hide the kernels' own time
-        reps = max(reps, copies) // copies * copies
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=stream):
-            for i in range(reps):
-                go(i)
-        iters = 5
-        with torch.cuda.stream(stream):
+    def __init__(self, gh, ctx, n, k):
+        self.gh, self.n, self.k = gh, n, k
+        packed = gh.synth_int4(SEED, n * 7 + k, n * k // 2)
+        s16 = gh.synth_scales_f16(SEED, n * 11 + k, n * k // 32)
+        wbytes = n * k // 2 + n * k // 16
+        self.copies = max(2, -(-3 * MALL_BYTES // wbytes))
+        self.ws = [ctx.weight(packed, s16, k, n) for _ in range(self.copies)]
+
+    def close(self):
+        for w in self.ws:
+            self.gh.lib().glacier_hip_int4_weight_destroy(w)
+        self.ws = []
+
+
+def time_gemv(gh, ctx, torch, cw, m, reps, act, end_to_end_bf16=False):
+    """Cold GEMV timing over the weight copies `cw`, HIP events on the launch
+    stream around a captured graph. Prepared launches (activation planes made
+    once, untimed: the decode chain produces them inside the previous kernel)
+    with Q8 or 3-digit f32 planes; or, with end_to_end_bf16, the whole
+    glacier_hip_int4_gemv call on bf16 activations (the conversion launch
+    included, BASELINE config 2's bf16 leg)."""
+    L = gh.lib()
+    n, k, copies = cw.n, cw.k, cw.copies
+    ws = cw.ws
+    stream = torch.cuda.Stream()  # non-null handle: our launches and the events share it
+    dt = torch.bfloat16 if end_to_end_bf16 else torch.float32
+    x = torch.randn((m, k), device="cuda", dtype=torch.float32).to(dt)
+    y = torch.empty((m, n), device="cuda", dtype=torch.float32)
+    planes = torch.empty(L.glacier_hip_activation_bytes(m, k, act), dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    gh.check(L.glacier_hip_activation_prepare(ctx.h, x.data_ptr(), gh.BF16 if end_to_end_bf16
+                                              else gh.F32, m, k, act, planes.data_ptr(),
+                                              stream.cuda_stream), "prepare")
+
+    def go(i):
+        if end_to_end_bf16:
+            return L.glacier_hip_int4_gemv(ctx.h, ws[i % copies], x.data_ptr(), gh.BF16, m, None,
+                                           y.data_ptr(), act, stream.cuda_stream)
+        return L.glacier_hip_int4_gemv_prepared(ctx.h, ws[i % copies], planes.data_ptr(), m, act,
+                                                None, y.data_ptr(), stream.cuda_stream)
+    for i in range(copies):
+        gh.check(go(i), "gemv", ctx.h)
+    torch.cuda.synchronize()
+    # the launches are captured into a graph so that host submission cost
+    # (ctypes + launch, several us) does not hide the kernels' own time
+    reps = max(reps, copies) // copies * copies
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(reps):
+            go(i)
+    iters = 5
+    with torch.cuda.stream(stream):
+        g.replay()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(iters):
             g.replay()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for _ in range(iters):
-                g.replay()
-            e1.record(stream)
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1000.0 / (reps * iters)
-        del g
+        e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / (reps * iters)
+    del g
+    if end_to_end_bf16:  # BASELINE config 2's byte count with a = 2
+        b = n * k // 2 + n * k // 16 + m * k * 2 + m * n * 4
+        mode = "bf16_in_" + ("q8" if act == gh.ACT_Q8 else "f32")
+    else:
         b = gemv_bytes(n, k, m, 1 if act == gh.ACT_Q8 else 3)
-        return dict(N=n, K=k, M=m, act="q8" if act == gh.ACT_Q8 else "f32", us=round(us, 2),
-                    bytes=b, gbs=round(b / us / 1e3, 1), frac=round(b / us / 1e3 / HBM_PEAK_GBS, 4),
-                    weight_copies=copies)
-    finally:
-        for w in ws:
-            L.glacier_hip_int4_weight_destroy(w)
+        mode = "q8" if act == gh.ACT_Q8 else "f32"
+    return dict(N=n, K=k, M=m, act=mode, us=round(us, 2), bytes=b, gbs=round(b / us / 1e3, 1),
+                frac=round(b / us / 1e3 / HBM_PEAK_GBS, 4), weight_copies=copies)
 
 
 def cpu_gemv(gh, ctx, torch, n, k, act):
@@ -175,6 +199,109 @@ def measured_traffic():
     except OSError:
         pass
     return None
+
+
+def int4_weights(cfg):
+    """INT4 weights of a model (every projection and the LM head)."""
+    d, f, v = cfg["dim"], cfg["hidden_dim"], cfg["vocab_size"]
+    kvd = cfg["num_kv_heads"] * cfg["head_dim"]
+    return cfg["num_layers"] * (d * (d + 2 * kvd) + d * d + 3 * f * d) + v * d
+
+
+def kv_bytes_per_position(cfg, elem):
+    """K and V of every layer for one position (what attention reads)."""
+    return 2 * cfg["num_layers"] * cfg["num_kv_heads"] * cfg["head_dim"] * elem
+
+
+def step_roofline(cfg, tokens_per_s, steps_per_s, kv_positions_per_step, kv_elem):
+    """HBM roofline of a decode step: the INT4 weights (0.5625 B each: codes
+    + fp16 group scales) once per step, the K/V every lane reads, the
+    embedding rows; achieved = bytes per step x steps per second."""
+    wb = int4_weights(cfg) * 9 // 16
+    b = wb + kv_positions_per_step * kv_bytes_per_position(cfg, kv_elem) + \
+        (tokens_per_s / steps_per_s) * cfg["dim"] * 4
+    gbs = b * steps_per_s / 1e9
+    return dict(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                frac=round(gbs / HBM_PEAK_GBS, 4), bytes_per_step=int(b), weight_bytes=wb)
+
+
+def host_info(ctx):
+    info = ctx.info()
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    rocm = "unknown"
+    try:
+        rocm = open("/opt/rocm/.info/version").read().strip()
+    except OSError:
+        pass
+    import torch
+
+    return dict(cpu_model=cpu, host_cores_available=len(os.sched_getaffinity(0)),
+                rocm_version=rocm, torch=torch.__version__,
+                gpu=dict(name=info.name.decode(), arch=info.arch.decode(),
+                         compute_units=info.compute_units,
+                         hbm_bytes=info.total_global_bytes))
+
+
+def bench_c1(gh, ctx, steps=128, prompt_len=128, cpu=True):
+    """the Qwen2.5-0.5B-shaped INT4 model (random init from
+    the seed), batch 1, f32 paged KV as the reference stores it, a 128-token
+    prompt then 128 greedy tokens (the first from the prompt's logits, 127
+    decode steps timed). A warm-up request on another lane captures the
+    decode graph first. CPU leg: the oracle's serial greedy loop (the
+    reference's oracle mode) on a short sample, 1 thread and all cores."""
+    cfg = CFG_05B
+    model = gh.Model(ctx, cfg)
+    model.init_random(SEED)
+    sess = gh.Session(model, max_lanes=2, max_positions=prompt_len + steps + 8, kv_dtype=gh.F32)
+    try:
+        prompt = gh.synth_tokens(SEED, 0x50524F4D, cfg["vocab_size"], prompt_len)
+        sess.begin(1, seed=2)
+        t = sess.prefill(1, prompt)
+        for _ in range(8):
+            t = int(sess.step([1], [t])[0])
+        sess.begin(0, seed=1)
+        tok = sess.prefill(0, prompt)
+        t0 = time.perf_counter()
+        for _ in range(steps - 1):
+            tok = int(sess.step([0], [tok])[0])
+        dt = time.perf_counter() - t0
+    finally:
+        sess.close()
+        model.close()
+    tps = (steps - 1) / dt
+    mean_ctx = prompt_len + steps / 2
+    res = dict(workload="Qwen2.5-0.5B-shaped INT4 g32, batch 1, 128-token prompt, 128 greedy "
+                        "tokens, f32 paged KV", tokens_per_s=round(tps, 1),
+               ms_per_token=round(dt * 1e3 / (steps - 1), 4),
+               roofline=step_roofline(cfg, tps, tps, mean_ctx, 4))
+    if not cpu:
+        log("c1", res)
+        return res
+    # CPU leg: the oracle on a bounded sample (8-token prompt, 8 tokens)
+    import oracle
+
+    oracle.build()
+    host = gh.random_model_host(cfg, SEED)
+    om = oracle.OracleModel(cfg, host)
+    p8 = gh.synth_tokens(SEED, 0x50524F4D, cfg["vocab_size"], 8)
+    cpu = {}
+    for th in (1, min(len(os.sched_getaffinity(0)), 16)):
+        oracle.set_threads(th)
+        t0 = time.perf_counter()
+        om.generate(p8, 8)
+        cpu[th] = 16 / (time.perf_counter() - t0)  # 16 token forwards (8 prompt, 8 generated)
+    res["cpu"] = dict(kind="port", sample="oracle greedy loop, 8-token prompt + 8 tokens",
+                      tokens_per_s_1_thread=round(cpu[1], 2),
+                      threads=max(cpu), tokens_per_s=round(cpu[max(cpu)], 2))
+    log("c1", res)
+    return res
 
 
 def auto_act(gh, n, k):
@@ -253,6 +380,8 @@ def bench_c5(gh, model, lanes=32, gen=256, prompt_lo=64, prompt_hi=4096, max_wei
             elig[:, -1] = np.uint64((1 << (V % 64)) - 1)
         t1 = time.perf_counter()
         n_tok, waves = 0, 0
+        served = [0] * lanes
+        kv_positions = 0  # positions attended, summed over every served quantum
         while True:
             try:
                 slots, evs = sched.wave(sess, list(range(lanes)), tokens, elig)
@@ -262,6 +391,9 @@ def bench_c5(gh, model, lanes=32, gen=256, prompt_lo=64, prompt_hi=4096, max_wei
                 raise
             waves += 1
             n_tok += len(slots)
+            for sl in slots:
+                served[sl] += 1
+                kv_positions += plens[sl] + served[sl]
             for ev in evs:
                 if ev.remaining_after == 0:
                     assert sched.retire(ev.handle)[0] == 0
@@ -273,6 +405,8 @@ def bench_c5(gh, model, lanes=32, gen=256, prompt_lo=64, prompt_hi=4096, max_wei
                    prompt_tokens=sum(plens), prefill_s=round(t_prefill, 2),
                    decode_tokens=n_tok, waves=waves, mean_wave=round(n_tok / max(waves, 1), 2),
                    decode_s=round(t_decode, 2), decode_tokens_per_s=round(n_tok / t_decode, 1),
+                   roofline=step_roofline(cfg, n_tok / t_decode, waves / t_decode,
+                                          kv_positions / max(waves, 1), 2),
                    end_to_end_tokens_per_s=round((n_tok + lanes) / (t_prefill + t_decode), 1),
                    event_chain_head=bytes(cev.event_sha256).hex())
         log("c5", res)
@@ -452,8 +586,8 @@ def main():
     ap.add_argument("--gemv-rows", type=int, default=1,
                     help="with --gemv-only: activation rows of the timed gate/up launch (past "
                          "16 rows the C ABI runs the MFMA GEMM; counter runs at prefill size)")
-    ap.add_argument("--sections", default="gemv,decode,lanes,c5,prefill,attention,cpu",
-                    help="comma list of gemv, decode, lanes, c5, prefill, attention, cpu "
+    ap.add_argument("--sections", default="gemv,decode,lanes,c5,c1,prefill,attention,cpu",
+                    help="comma list of gemv, decode, lanes, c5, c1, prefill, attention, cpu "
                          "(profiling runs select one; the JSON line needs decode)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
@@ -497,16 +631,30 @@ def main():
     dom = None
     if "gemv" in secs or a.gemv_only:
         rows = a.gemv_rows if a.gemv_only else 1
-        dom = time_gemv(gh, ctx, torch, n, k, rows, a.gemv_reps * 2, gh.ACT_Q8)
+        cw = ColdWeights(gh, ctx, n, k)
+        dom = time_gemv(gh, ctx, torch, cw, rows, a.gemv_reps * 2, gh.ACT_Q8)
+        cw.close()
         log("gemv gate/up", dom)
     if not a.gemv_only and "gemv" in secs:
         for (n, k) in GEMV_SHAPES:
-            for m in (1, 2, 4, 8):
-                r = time_gemv(gh, ctx, torch, n, k, m, a.gemv_reps, auto_act(gh, n, k))
-                if m == 1 and not a.no_cpu_baseline:
-                    r["cpu"] = cpu_gemv(gh, ctx, torch, n, k, auto_act(gh, n, k))
-                log("gemv", r)
-                gemv.append(r)
+            cw = ColdWeights(gh, ctx, n, k)
+            try:
+                for m in (1, 2, 4, 8):
+                    # the reference's x86 dispatch (Q8, f32 for the head), then
+                    # the other activation mode, then the bf16-input call
+                    for act in (auto_act(gh, n, k), gh.ACT_F32 if auto_act(gh, n, k) == gh.ACT_Q8
+                                else gh.ACT_Q8):
+                        r = time_gemv(gh, ctx, torch, cw, m, a.gemv_reps, act)
+                        if m == 1 and act == auto_act(gh, n, k) and not a.no_cpu_baseline:
+                            r["cpu"] = cpu_gemv(gh, ctx, torch, n, k, act)
+                        log("gemv", r)
+                        gemv.append(r)
+                    r = time_gemv(gh, ctx, torch, cw, m, a.gemv_reps, auto_act(gh, n, k),
+                                  end_to_end_bf16=True)
+                    log("gemv", r)
+                    gemv.append(r)
+            finally:
+                cw.close()
     roofline = dict(bound="hbm", achieved=dom["gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
                     frac=dom["frac"], traffic=measured_traffic()) if dom else None
     if a.gemv_only:
@@ -515,6 +663,13 @@ def main():
         return
 
     # ---- 7B model ----
+    need_7b = bool(secs & {"decode", "lanes", "c5", "prefill", "cpu"})
+    if not need_7b:  # kernel-only sections (profiling runs)
+        attn = bench_attention(gh, ctx, torch, cpu=False) if not a.no_attention else None
+        c1 = bench_c1(gh, ctx, cpu=False) if "c1" in secs else None
+        print(json.dumps(dict(metric="sections " + a.sections, attention=attn, c1_qwen05b=c1,
+                              gemv=([dom] if dom else []) + gemv, host=host_info(ctx))))
+        return
     t0 = time.perf_counter()
     host = gh.random_model_host(CFG_7B, SEED)
     model = gh.Model(ctx, CFG_7B)
@@ -533,15 +688,19 @@ def main():
         prompts = [gh.synth_tokens(SEED, 0x4C414E45 + i, CFG_7B["vocab_size"], a.lane_prompt)
                    for i in range(a.lanes)]
         tpsL, dtL = decode_lanes(gh, sess, a.lanes, prompts, a.warmup, a.steps)
+        steps_per_s = a.steps / dtL
+        mean_ctx = a.lane_prompt + a.warmup + a.steps / 2 + 1
         lanes = dict(value=round(tpsL, 1), unit="tokens/s", lanes=a.lanes,
                      ms_per_step=round(dtL * 1e3 / a.steps, 3), prompt_len=a.lane_prompt,
-                     context_range=[a.lane_prompt, a.lane_prompt + a.warmup + a.steps])
+                     context_range=[a.lane_prompt, a.lane_prompt + a.warmup + a.steps],
+                     roofline=step_roofline(CFG_7B, tpsL, steps_per_s, a.lanes * mean_ctx, 2))
         log(f"{a.lanes}-lane decode {tpsL:.1f} tok/s")
     sess.close()
     c5 = bench_c5(gh, model) if "c5" in secs else None
     prefill = bench_prefill(gh, model, [512, 2048]) if not a.no_prefill else None
     model.close()
     attn = bench_attention(gh, ctx, torch, cpu=not a.no_cpu_baseline) if not a.no_attention else None
+    c1 = bench_c1(gh, ctx, cpu=not a.no_cpu_baseline) if "c1" in secs else None
     cpu = None if a.no_cpu_baseline else cpu_baseline(host, int(prompt[0]))
     if cpu:
         log("cpu baseline", cpu)
@@ -561,8 +720,10 @@ def main():
         config=dict(workload="Qwen2.5-7B-shaped INT4 g32 greedy decode, batch 1",
                     prompt_len=a.prompt, kv="fp16 paged, 16 positions/page",
                     parallelism="single GPU"),
-        roofline=roofline, cpu_baseline=cpu, lanes32=lanes, c5_laneweave=c5, prefill=prefill,
-        attention=attn,
+        roofline=roofline, cpu_baseline=cpu, host=host_info(ctx),
+        decode_roofline=step_roofline(CFG_7B, tps1, tps1, a.prompt + a.warmup + a.steps / 2 + 1, 2)
+        if tps1 else None,
+        lanes32=lanes, c5_laneweave=c5, c1_qwen05b=c1, prefill=prefill, attention=attn,
         gemv=([dom] if dom else []) + gemv)
     print(json.dumps(out))
 
