@@ -696,6 +696,18 @@ def main():
                      roofline=step_roofline(CFG_7B, tpsL, steps_per_s, a.lanes * mean_ctx, 2))
         log(f"{a.lanes}-lane decode {tpsL:.1f} tok/s")
     sess.close()
+    f32kv = None
+    if "decode" in secs:
+        # the same batch-1 decode on f32 KV pages, the reference's storage
+        s32 = gh.Session(model, max_lanes=1, max_positions=max_pos, kv_dtype=gh.F32)
+        s32.begin(0, seed=1)
+        tps32, dt32 = decode_batch1(gh, s32, prompt, a.warmup, a.steps)
+        s32.close()
+        f32kv = dict(value=round(tps32, 2), unit="tokens/s",
+                     ms_per_step=round(dt32 * 1e3 / a.steps, 4), kv="f32 paged",
+                     roofline=step_roofline(CFG_7B, tps32, tps32,
+                                            a.prompt + a.warmup + a.steps / 2 + 1, 4))
+        log(f"batch-1 decode, f32 KV {tps32:.1f} tok/s")
     c5 = bench_c5(gh, model) if "c5" in secs else None
     prefill = bench_prefill(gh, model, [512, 2048]) if not a.no_prefill else None
     model.close()
@@ -723,7 +735,7 @@ def main():
         roofline=roofline, cpu_baseline=cpu, host=host_info(ctx),
         decode_roofline=step_roofline(CFG_7B, tps1, tps1, a.prompt + a.warmup + a.steps / 2 + 1, 2)
         if tps1 else None,
-        lanes32=lanes, c5_laneweave=c5, c1_qwen05b=c1, prefill=prefill, attention=attn,
+        decode_f32_kv=f32kv, lanes32=lanes, c5_laneweave=c5, c1_qwen05b=c1, prefill=prefill, attention=attn,
         gemv=([dom] if dom else []) + gemv)
     print(json.dumps(out))
 
