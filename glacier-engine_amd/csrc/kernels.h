@@ -134,7 +134,7 @@ struct GemvShape {
   bool lds_a;
   size_t lds_bytes;
 };
-GemvShape plan_gemv(int N, int K, int M, int D);
+GemvShape plan_gemv(int N, int K, int M, int D, bool small_wg = true);
 // The shape launch_gemv uses for these arguments (plan_gemv adjusted for
 // emitted planes / fused stages / overrides); grid = workgroup count, which
 // is also the number of ss_out partials per row. Returns false if invalid.

@@ -158,18 +158,38 @@ static size_t planes_bytes(int groups, int M, int D) {
   return (size_t)groups * ((size_t)D * M * 32 + (size_t)M * sizeof(ActMeta));
 }
 
-GemvShape plan_gemv(int N, int K, int M, int D) {
+// Launch shape of the 1-2 row dot4 GEMV (and, with small_wg = false, of
+// the 3-5 row batched dot4 kernel). From cold-cache sweeps at M = 1, 2 with
+// one- and three-digit planes on the 7B and C2 shapes:
+//  * K split until the grid holds about 4096 waves, keeping >= 4 quads per
+//    wave, at most 8 split waves (the 3-digit down projection, 224 row
+//    blocks, measured best there), 4 quads in flight per wave;
+//  * 512-4095 row blocks: workgroups of 4 waves (11008x4096: 7.8 us
+//    against 9.6 with 6 waves; 18944x3584: 9.4 against 11.1; the fused
+//    gate/up: 15.1 against 16.3 with 8);
+//  * 257-511 row blocks: 4 split waves x 2 row blocks, so the grid stays
+//    within one workgroup per CU (4608x3584: 5.7 us against 6.5 with 288
+//    workgroups of 7 waves);
+//  * otherwise workgroups of about 8 waves.
+static void plan_rows2(int NB, int KQ, bool small_wg, int &ks, int &rb) {
+  ks = std::max(1, std::min(std::min(8, std::max(1, KQ / 4)), (4096 + NB - 1) / NB));
+  rb = std::max(1, std::min(8, 8 / ks));
+  if (!small_wg) return;
+  if (NB >= 512 && NB < 4096) {
+    ks = std::min(ks, 4);
+    rb = std::max(1, 4 / ks);
+  } else if (NB > 256 && NB < 512 && KQ >= 16) {
+    ks = 4;
+    rb = 2;
+  }
+}
+
+GemvShape plan_gemv(int N, int K, int M, int D, bool small_wg) {
   GemvShape p;
   const int NB = N / 16, KQ = K / 128;
   int ks, rb;
   if (M <= 2) {
-    // From cold-cache sweeps of the 7B decode shapes: about 4096 waves or
-    // more keep HBM busy (split K until there, keeping >= 4 quads per wave),
-    // workgroups of about 8 waves, 4 quads in flight per wave.
-    // (K split capped at 8 waves: the 3-digit down projection measured best
-    // there.)
-    ks = std::max(1, std::min(std::min(8, std::max(1, KQ / 4)), (4096 + NB - 1) / NB));
-    rb = std::max(1, std::min(8, 8 / ks));
+    plan_rows2(NB, KQ, small_wg, ks, rb);
     p.unroll = 4;
   } else {
     const int max_ks = std::max(1, std::min(16, KQ / 2));
@@ -791,7 +811,7 @@ static bool gemv_shape(GemvArgs &a, GemvShape &p) {
   p = plan_gemv(a.N, a.K, a.M, a.D);
   if (dot4_rows_ok(a, p)) {
     // the batched dot4 kernel streams like the decode one: its launch shape
-    const GemvShape d = plan_gemv(a.N, a.K, 2, a.D);
+    const GemvShape d = plan_gemv(a.N, a.K, 2, a.D, false);
     p.ksplit = d.ksplit;
     p.rb = d.rb;
     p.waves = d.waves;
