@@ -319,6 +319,46 @@ def decode_batch1(gh, sess, prompt, warmup, steps):
     return steps / dt, dt
 
 
+def decode_eligible(gh, model, prompt, warmup, steps, density=0.01):
+    """Batch-1 greedy decode with a caller-certified eligibility mask of the
+    given density on every step (a fresh random mask per step from a fixed
+    set), in the posthead domain (every logit, then the masked argmax) and
+    the prehead domain (LM-head row blocks with no eligible token stream no
+    weights). Same session, same tokens."""
+    V = model.cfg["vocab_size"]
+    rng = np.random.default_rng(SEED)
+    masks = []
+    for _ in range(8):
+        bits = rng.random(V) < density
+        bits[int(rng.integers(V))] = True
+        words = np.zeros(-(-V // 64), np.uint64)
+        idx = np.nonzero(bits)[0]
+        np.bitwise_or.at(words, idx // 64, np.left_shift(np.uint64(1), (idx % 64).astype(np.uint64)))
+        masks.append(words[None])
+    blocks = sum(1 for b in range(V // 16)
+                 if (int(masks[0][0][b // 4]) >> ((b % 4) * 16)) & 0xFFFF)
+    out = dict(density=density, head_blocks_streamed_frac=round(blocks / (V // 16), 4))
+    for mode, name in ((gh.HEAD_DOMAIN_POSTHEAD, "posthead"), (gh.HEAD_DOMAIN_PREHEAD, "prehead")):
+        sess = gh.Session(model, max_lanes=1, max_positions=len(prompt) + warmup + steps + 8,
+                          kv_dtype=gh.F16)
+        sess.set_head_domain(mode)
+        sess.begin(0, seed=1)
+        tok = sess.prefill(0, prompt)
+        toks = []
+        for i in range(warmup):
+            tok = int(sess.step([0], [tok], eligible=masks[i % 8])[0])
+        t0 = time.perf_counter()
+        for i in range(steps):
+            tok = int(sess.step([0], [tok], eligible=masks[i % 8])[0])
+            toks.append(tok)
+        dt = time.perf_counter() - t0
+        sess.close()
+        out[name] = dict(tokens_per_s=round(steps / dt, 1), ms_per_token=round(dt * 1e3 / steps, 4))
+        out[name + "_tokens"] = toks
+    out["same_tokens"] = out.pop("posthead_tokens") == out.pop("prehead_tokens")
+    return out
+
+
 def c5_workload(cfg, lanes=32, gen=256, prompt_lo=64, prompt_hi=4096, max_weight=4):
     """The config-5 admission set: prompt lengths U[prompt_lo, prompt_hi] by
     seed, LaneWeave weights 1..max_weight by lane, each lane's request spec
@@ -696,7 +736,7 @@ def main():
                      roofline=step_roofline(CFG_7B, tpsL, steps_per_s, a.lanes * mean_ctx, 2))
         log(f"{a.lanes}-lane decode {tpsL:.1f} tok/s")
     sess.close()
-    f32kv = None
+    f32kv = elig = None
     if "decode" in secs:
         # the same batch-1 decode on f32 KV pages, the reference's storage
         s32 = gh.Session(model, max_lanes=1, max_positions=max_pos, kv_dtype=gh.F32)
@@ -708,6 +748,8 @@ def main():
                      roofline=step_roofline(CFG_7B, tps32, tps32,
                                             a.prompt + a.warmup + a.steps / 2 + 1, 4))
         log(f"batch-1 decode, f32 KV {tps32:.1f} tok/s")
+        elig = decode_eligible(gh, model, prompt, a.warmup, min(a.steps, 32))
+        log("batch-1 decode with a 1% eligibility mask", elig)
     c5 = bench_c5(gh, model) if "c5" in secs else None
     prefill = bench_prefill(gh, model, [512, 2048]) if not a.no_prefill else None
     model.close()
@@ -735,7 +777,7 @@ def main():
         roofline=roofline, cpu_baseline=cpu, host=host_info(ctx),
         decode_roofline=step_roofline(CFG_7B, tps1, tps1, a.prompt + a.warmup + a.steps / 2 + 1, 2)
         if tps1 else None,
-        decode_f32_kv=f32kv, lanes32=lanes, c5_laneweave=c5, c1_qwen05b=c1, prefill=prefill, attention=attn,
+        decode_f32_kv=f32kv, decode_eligible=elig, lanes32=lanes, c5_laneweave=c5, c1_qwen05b=c1, prefill=prefill, attention=attn,
         gemv=([dom] if dom else []) + gemv)
     print(json.dumps(out))
 

@@ -116,6 +116,11 @@ struct GemvArgs {
   ArgPartial *arg_parts;
   const uint64_t *arg_words;
   long arg_word_count;
+  // With arg_parts and arg_words: a row block none of whose 16 rows is
+  // eligible for any activation row streams no weights (its logits are never
+  // computed and never candidates) -- the prehead domain mode. y may be null
+  // with arg_parts (no logits are stored).
+  int prehead;
   // GEMM split-K workspace (floats); null: no K split
   float *splitk_ws;
   size_t splitk_ws_floats;

@@ -230,7 +230,21 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
   const int ks = wave % KS;
   const int nb = blockIdx.x * (int)(blockDim.x >> 6) / KS + wave / KS;
   const int kq0 = (ks * KQ) / KS, kq1 = ((ks + 1) * KQ) / KS;
-  const int nq = kq1 - kq0;
+  // Prehead eligibility (int4_executor.zig:968-1150 skips empty rows4 tiles):
+  // a row block none of whose 16 rows is eligible for any activation row
+  // streams no weights; its accumulators stay 0 and no row of it becomes a
+  // candidate.
+  // (compiled only into the head's variants: a plain or run-time epilogue)
+  bool skip_block = false;
+  if ((EPI == EPI_PLAIN || EPI < 0) && a.prehead) {
+    const int nbq = min(nb, NB - 1);
+    uint32_t any = 0;
+    for (int m = 0; m < M; ++m)
+      any |= (uint32_t)(a.arg_words[(size_t)m * a.arg_word_count + (nbq >> 2)] >> ((nbq & 3) * 16)) &
+             0xFFFFu;
+    skip_block = any == 0;
+  }
+  const int nq = skip_block ? 0 : kq1 - kq0;
   const int n_local = lane & 15, c = lane >> 4;
 
   // The first U quads of weights are requested before the activation planes
@@ -709,7 +723,7 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
           actbuf[m * (8 * RB) + (nb - nb_wg0) * 8 + n_local] = v;
           if (a.y) a.y[(size_t)m * (a.N / 2) + nb * 8 + n_local] = v;
         }
-      } else {
+      } else if (epi != EPI_PLAIN || a.y) {  // (a fused head may store no logits)
         store_output(a, epi, nb, n_local, m, tot, partner,
                      (DOT4 && MR == 2) ? epre[m & 1] : epi_load(a, epi, nb, n_local, m));
       }
@@ -805,7 +819,8 @@ static bool gemv_shape(GemvArgs &a, GemvShape &p) {
   if (emit_planes && ((a.N / 16) % 4 || !a.out_meta || (a.out_D != 1 && a.out_D != 3)))
     return false;
   if (a.ss_out && (a.epi != EPI_RESID || !a.y || !a.resid)) return false;
-  if (a.arg_parts && (a.epi != EPI_PLAIN || !a.y)) return false;
+  if (a.arg_parts && a.epi != EPI_PLAIN) return false;
+  if (a.prehead && (!a.arg_parts || !a.arg_words || a.arg_word_count < (a.N + 63) / 64)) return false;
   if (a.in_ss && (!a.x_in || a.in_ss_count <= 0 || a.in_ss_count > kMaxSsParts || a.M > 32))
     return false;
   p = plan_gemv(a.N, a.K, a.M, a.D);

@@ -3,6 +3,7 @@
 // points (GEMV, RMSNorm, paged attention, argmax). The model/session token
 // loop lives in session.hip.
 #include <math.h>
+#include <cmath>
 #include <string.h>
 
 #include <algorithm>
@@ -1045,6 +1046,123 @@ int glacier_hip_eligible_argmax(glacier_hip_context *ctx, const float *logits_de
   if (!words_dev) return GLACIER_HIP_INVALID_ARGUMENT;
   return argmax_common(ctx, logits_dev, n, words_dev, word_count, rows, results_host,
                        stream ? (hipStream_t)stream : (ctx ? ctx->stream : nullptr));
+}
+
+// The reference's eligible-greedy counts (EligibleGreedyContext.run,
+// int4_executor.zig:986-1150, totals :1939-1966): per 64-row tile, a fully
+// eligible tile is one run of all its rows; otherwise each maximal run of
+// 4-row groups holding an eligible row is one run of 4 rows per group.
+// device_rows: the 16-row blocks this device streams (any eligible row).
+static void eligible_counts(const uint64_t *words, uint64_t out_f,
+                            glacier_hip_eligible_greedy_result_t &r) {
+  r.eligible_rows = r.producer_rows = r.producer_runs = r.device_rows = 0;
+  const uint64_t tiles = (out_f + 63) / 64;
+  for (uint64_t t = 0; t < tiles; ++t) {
+    const uint64_t row_count = std::min<uint64_t>(64, out_f - 64 * t);
+    const uint64_t valid = row_count == 64 ? ~0ull : (1ull << row_count) - 1;
+    const uint64_t e = words[t] & valid;
+    r.eligible_rows += (uint64_t)__builtin_popcountll(e);
+    if (!e) continue;
+    if (e == valid) {
+      r.producer_rows += row_count;
+      r.producer_runs += 1;
+      continue;
+    }
+    bool in_run = false;
+    for (uint64_t g = 0; g < row_count / 4; ++g) {
+      if ((e >> (4 * g)) & 0xFull) {
+        r.producer_rows += 4;
+        if (!in_run) r.producer_runs += 1;
+        in_run = true;
+      } else {
+        in_run = false;
+      }
+    }
+  }
+  for (uint64_t b = 0; b < out_f / 16; ++b)
+    if ((words[b / 4] >> ((b % 4) * 16)) & 0xFFFFull) r.device_rows += 16;
+  r.skipped_rows = out_f - r.producer_rows;
+  r.overcomputed_rows = r.producer_rows - r.eligible_rows;
+}
+
+int glacier_hip_int4_eligible_greedy(glacier_hip_context *ctx, glacier_hip_int4_weight *w,
+                                     const float *x_dev, uint32_t in_f,
+                                     const uint64_t *words_host, uint64_t word_count,
+                                     int activation, glacier_hip_eligible_greedy_result_t *out,
+                                     void *stream) {
+  if (!ctx || !w || !x_dev || !words_host || !out) return GLACIER_HIP_INVALID_ARGUMENT;
+  if (w->ctx != ctx) return GLACIER_HIP_INVALID_HANDLE;
+  int D;
+  if (activation == GLACIER_HIP_ACT_AUTO || activation == GLACIER_HIP_ACT_Q8) D = 1;
+  else if (activation == GLACIER_HIP_ACT_F32) D = 3;
+  else return GLACIER_HIP_INVALID_ARGUMENT;
+  // validation before any write (int4_executor.zig:1870-1890): geometry,
+  // eligibility words (validateEligibleWords), a finite input
+  const uint64_t V = w->out_f;
+  if (in_f != w->in_f || V % 4) return GLACIER_HIP_SHAPE_MISMATCH;
+  const uint64_t W = V / 64 + (V % 64 != 0);
+  if (word_count != W) return GLACIER_HIP_SHAPE_MISMATCH;
+  if (V % 64 && (words_host[W - 1] >> (V % 64)) != 0) return GLACIER_HIP_SHAPE_MISMATCH;
+  glacier_hip_eligible_greedy_result_t r{};
+  eligible_counts(words_host, V, r);
+  if (r.eligible_rows == 0) return GLACIER_HIP_SHAPE_MISMATCH;
+  GH_SUBMISSION(ctx);
+  hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
+  {
+    std::vector<float> xh(in_f);
+    GH_CHECK(ctx, hipMemcpyAsync(xh.data(), x_dev, (size_t)in_f * 4, hipMemcpyDeviceToHost, st));
+    GH_CHECK(ctx, hipStreamSynchronize(st));
+    for (float v : xh)
+      if (!std::isfinite(v)) return GLACIER_HIP_SHAPE_MISMATCH;
+  }
+  const int nparts = gk::gemv_argmax_parts((int)V, (int)in_f, 1, D);
+  if (nparts <= 0) return GLACIER_HIP_SHAPE_MISMATCH;
+  auto &ss = ctx->per_stream[st];
+  const size_t pb = planes_bytes(1, in_f, D);
+  if (pb > ss.planes_bytes) {
+    gh::dev_free(ctx, ss.planes);
+    ss.planes = nullptr;
+    ss.planes_bytes = 0;
+    GH_CHECK(ctx, gh::dev_malloc(ctx, &ss.planes, pb));
+    ss.planes_bytes = pb;
+  }
+  // scratch: eligibility words | candidates | merged result
+  const size_t wb = al256(W * 8), cb = al256((size_t)nparts * sizeof(gk::ArgPartial));
+  int rc = gh::ensure_scratch(ctx, ss, wb + cb + sizeof(gk::ArgmaxResult), 1);
+  if (rc) return rc;
+  auto *words_dev = (uint64_t *)ss.scratch;
+  auto *parts = (gk::ArgPartial *)((char *)ss.scratch + wb);
+  auto *res_dev = (gk::ArgmaxResult *)((char *)ss.scratch + wb + cb);
+  GH_CHECK(ctx, hipMemcpyAsync(words_dev, words_host, W * 8, hipMemcpyHostToDevice, st));
+  rc = prepare_launch(ctx, x_dev, GLACIER_HIP_F32, 1, in_f, D, ss.planes, st);
+  if (rc) return rc;
+  gk::GemvArgs a{};
+  a.codes = w->codes;
+  a.scales = w->scales;
+  a.N = (int)V;
+  a.K = (int)in_f;
+  a.act_q = (const int8_t *)ss.planes;
+  a.act_meta = (const gk::ActMeta *)((const char *)ss.planes + al256(planes_q_bytes(1, in_f, D)));
+  a.M = 1;
+  a.D = D;
+  a.epi = gk::EPI_PLAIN;
+  a.arg_parts = parts;
+  a.arg_words = words_dev;
+  a.arg_word_count = (long)W;
+  a.prehead = 1;
+  GH_CHECK(ctx, gk::launch_gemv(a, st));
+  GH_CHECK(ctx, gk::launch_argmax_parts(parts, nparts, (long)V, 1, words_dev, (long)W, res_dev, st));
+  GH_CHECK(ctx, hipMemcpyAsync(ctx->results_host, res_dev, sizeof(gk::ArgmaxResult),
+                               hipMemcpyDeviceToHost, st));
+  GH_CHECK(ctx, hipStreamSynchronize(st));
+  const gk::ArgmaxResult &g = ctx->results_host[0];
+  // an eligible NaN (or any mask the host checks missed) is the reference's
+  // ShapeMismatch (int4_executor.zig:1933-1938)
+  if (g.status != GLACIER_HIP_OK || g.index >= V || g.eligible_rows != r.eligible_rows)
+    return GLACIER_HIP_SHAPE_MISMATCH;
+  r.token_index = g.index;
+  *out = r;
+  return GLACIER_HIP_OK;
 }
 
 // ---- synthetic generator ----------------------------------------------------

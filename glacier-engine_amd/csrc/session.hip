@@ -90,6 +90,10 @@ struct glacier_hip_session {
   uint32_t total_pages = 0;
   uint32_t rows_cap = 0;   // max(max_lanes, prefill_chunk): rows of the scratch buffers
   uint32_t prefill_chunk = 0;
+  // eligible-step head domain: GLACIER_HIP_HEAD_DOMAIN_POSTHEAD (every
+  // logit, then the masked argmax) or _PREHEAD (row blocks with no eligible
+  // token stream no weights)
+  int head_domain = GLACIER_HIP_HEAD_DOMAIN_POSTHEAD;
   gpk::PagePool pool;
   std::vector<Lane> lanes;
   // device
@@ -120,10 +124,10 @@ struct glacier_hip_session {
   gk::ArgmaxResult *res_host = nullptr;
   bool inject_failure = false;
   PreparedWave prep;
-  // graph cache: key = (rows, with_head, eligible)
+  // graph cache: key = (rows, with_head, eligible, prehead)
   struct GraphEntry {
     uint32_t rows;
-    bool head, elig;
+    bool head, elig, pre;
     hipGraphExec_t exec;
   };
   std::vector<GraphEntry> graphs;
@@ -410,6 +414,7 @@ struct ProjOut {
   gk::ArgPartial *arg_parts = nullptr;      // EPI_PLAIN: fused greedy head
   const uint64_t *arg_words = nullptr;
   long arg_word_count = 0;
+  bool prehead = false;                     // skip row blocks with no eligible row
 };
 
 gk::GemvArgs proj_args(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, int rows,
@@ -436,6 +441,7 @@ gk::GemvArgs proj_args(glacier_hip_session *s, glacier_hip_int4_weight *w, int D
   a.arg_parts = out.arg_parts;
   a.arg_words = out.arg_words;
   a.arg_word_count = out.arg_word_count;
+  a.prehead = out.prehead ? 1 : 0;
   a.in_eps = s->model->cfg.rms_eps;
   a.splitk_ws = s->splitk_ws;
   a.splitk_ws_floats = s->splitk_floats;
@@ -683,7 +689,7 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
 // sized row counts fuse the argmax into the head GEMV (each workgroup
 // reduces its logits to one candidate per row) and finish with a
 // one-block-per-row merge; longer row sets scan the logits afterwards.
-hipError_t enqueue_head(glacier_hip_session *s, int rows, const float *x, bool elig,
+hipError_t enqueue_head(glacier_hip_session *s, int rows, const float *x, bool elig, bool pre,
                         hipStream_t st) {
   glacier_hip_model *m = s->model;
   const auto &c = m->cfg;
@@ -702,6 +708,7 @@ hipError_t enqueue_head(glacier_hip_session *s, int rows, const float *x, bool e
     out.arg_parts = (gk::ArgPartial *)s->arg_scratch;
     out.arg_words = words;
     out.arg_word_count = W;
+    out.prehead = elig && pre;
     hipError_t e = run_proj(s, m->head, head_D(s), rows, gk::EPI_PLAIN, in, out, st);
     if (e != hipSuccess) return e;
     const int nparts = gk::gemv_argmax_parts((int)V, (int)c.dim, rows, head_D(s));
@@ -714,12 +721,13 @@ hipError_t enqueue_head(glacier_hip_session *s, int rows, const float *x, bool e
 }
 
 // The full launch sequence of one decode step for `rows` lanes.
-hipError_t enqueue_step(glacier_hip_session *s, int rows, bool head, bool elig, hipStream_t st) {
+hipError_t enqueue_step(glacier_hip_session *s, int rows, bool head, bool elig, bool pre,
+                        hipStream_t st) {
   const RowPtrs rp{s->step_dev->tokens, s->step_dev->lane_of_row, s->step_dev->pos_of_row,
                    s->step_dev->ctx_len};
   hipError_t e = enqueue_layers(s, rows, rp, st);
   if (e != hipSuccess || !head) return e;
-  return enqueue_head(s, rows, s->x_res, elig, st);
+  return enqueue_head(s, rows, s->x_res, elig, pre, st);
 }
 
 void destroy_session(glacier_hip_session *s) {
@@ -866,6 +874,10 @@ int run_step(glacier_hip_session *s, const uint32_t *lanes, const uint32_t *toke
   glacier_hip_context *ctx = s->model->ctx;
   const auto &c = s->model->cfg;
   hipStream_t st = ctx->stream;
+  // prehead never computes the logits of skipped rows
+  // (generate.zig:423-426: full-vocabulary logits never exist)
+  if (logits_host && elig_host && s->head_domain == GLACIER_HIP_HEAD_DOMAIN_PREHEAD)
+    return GLACIER_HIP_INVALID_ARGUMENT;
   int rc = begin_rows(s, lanes, count, txns);
   if (rc) return rc;
   for (uint32_t i = 0; i < count; ++i) {
@@ -890,27 +902,28 @@ int run_step(glacier_hip_session *s, const uint32_t *lanes, const uint32_t *toke
     if (e != hipSuccess) return fail(e, "eligibility words");
   }
   const bool elig = elig_host != nullptr;
+  const bool pre = elig && s->head_domain == GLACIER_HIP_HEAD_DOMAIN_PREHEAD;
   hipGraphExec_t exec = nullptr;
   if (s->opt.use_graph) {
     for (auto &g : s->graphs)
-      if (g.rows == count && g.head == head && g.elig == elig) exec = g.exec;
+      if (g.rows == count && g.head == head && g.elig == elig && g.pre == pre) exec = g.exec;
     if (!exec) {
       hipGraph_t graph;
       e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
       if (e != hipSuccess) return fail(e, "begin capture");
-      hipError_t e2 = enqueue_step(s, (int)count, head, elig, st);
+      hipError_t e2 = enqueue_step(s, (int)count, head, elig, pre, st);
       e = hipStreamEndCapture(st, &graph);
       if (e2 != hipSuccess) return fail(e2, "capture step");
       if (e != hipSuccess) return fail(e, "end capture");
       e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
       (void)hipGraphDestroy(graph);
       if (e != hipSuccess) return fail(e, "graph instantiate");
-      s->graphs.push_back({count, head, elig, exec});
+      s->graphs.push_back({count, head, elig, pre, exec});
     }
     e = hipGraphLaunch(exec, st);
     if (e != hipSuccess) return fail(e, "graph launch");
   } else {
-    e = enqueue_step(s, (int)count, head, elig, st);
+    e = enqueue_step(s, (int)count, head, elig, pre, st);
     if (e != hipSuccess) return fail(e, "enqueue step");
   }
   if (head) {
@@ -979,7 +992,7 @@ int run_prefill_chunk(glacier_hip_session *s, uint32_t lane, const uint32_t *tok
   e = enqueue_layers(s, (int)n, rp, st);
   if (e != hipSuccess) return fail(e, "prefill layers");
   if (head) {
-    e = enqueue_head(s, 1, s->x_res + (size_t)(n - 1) * c.dim, false, st);
+    e = enqueue_head(s, 1, s->x_res + (size_t)(n - 1) * c.dim, false, false, st);
     if (e != hipSuccess) return fail(e, "prefill head");
     e = hipMemcpyAsync(s->res_host, s->arg_result, sizeof(gk::ArgmaxResult),
                        hipMemcpyDeviceToHost, st);
@@ -1447,6 +1460,14 @@ int glacier_hip_session_page_of(glacier_hip_session *s, uint32_t lane, uint32_t 
   const Lane &ln = s->lanes[lane];
   if (logical_page >= ln.kv.page_of.size()) return GLACIER_HIP_SHAPE_MISMATCH;
   *physical_out = ln.kv.page_of[logical_page];
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_session_set_head_domain(glacier_hip_session *s, int mode) {
+  if (!s || (mode != GLACIER_HIP_HEAD_DOMAIN_POSTHEAD && mode != GLACIER_HIP_HEAD_DOMAIN_PREHEAD))
+    return GLACIER_HIP_INVALID_ARGUMENT;
+  GH_SUBMISSION(s->model->ctx);
+  s->head_domain = mode;
   return GLACIER_HIP_OK;
 }
 

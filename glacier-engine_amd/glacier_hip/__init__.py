@@ -82,6 +82,18 @@ class ArgmaxResult(C.Structure):
                 ("status", C.c_int32), ("reserved", C.c_int32)]
 
 
+class EligibleGreedyResult(C.Structure):
+    """glacier_hip_eligible_greedy_result_t (EligibleGreedyResult,
+    int4_executor.zig:786-801, plus the rows this device streamed)."""
+    _fields_ = [("token_index", C.c_uint64), ("eligible_rows", C.c_uint64),
+                ("producer_rows", C.c_uint64), ("skipped_rows", C.c_uint64),
+                ("overcomputed_rows", C.c_uint64), ("producer_runs", C.c_uint64),
+                ("device_rows", C.c_uint64)]
+
+
+HEAD_DOMAIN_POSTHEAD, HEAD_DOMAIN_PREHEAD = 0, 1
+
+
 class ModelConfig(C.Structure):
     _fields_ = [("num_layers", C.c_uint32), ("dim", C.c_uint32), ("hidden_dim", C.c_uint32),
                 ("num_heads", C.c_uint32), ("num_kv_heads", C.c_uint32), ("head_dim", C.c_uint32),
@@ -320,6 +332,8 @@ _SIGS = [
     ("glacier_hip_argmax", C.c_int, [_P, _P, C.c_uint64, C.c_uint32, _P, _P]),
     ("glacier_hip_eligible_argmax", C.c_int,
      [_P, _P, C.c_uint64, _P, C.c_uint64, C.c_uint32, C.POINTER(ArgmaxResult), _P]),
+    ("glacier_hip_int4_eligible_greedy", C.c_int,
+     [_P, _P, _P, C.c_uint32, _P, C.c_uint64, C.c_int, C.POINTER(EligibleGreedyResult), _P]),
     ("glacier_hip_model_create", _P, [_P, C.POINTER(ModelConfig)]),
     ("glacier_hip_model_set_layer", C.c_int, [_P, C.c_uint32, C.POINTER(LayerHost)]),
     ("glacier_hip_model_set_globals", C.c_int, [_P, _P, _P, _P, _P]),
@@ -343,6 +357,7 @@ _SIGS = [
     ("glacier_hip_session_page_of", C.c_int, [_P, C.c_uint32, C.c_uint32, C.POINTER(C.c_int32)]),
     ("glacier_hip_session_page_generation", C.c_int,
      [_P, C.c_uint32, C.c_uint32, C.POINTER(C.c_uint64)]),
+    ("glacier_hip_session_set_head_domain", C.c_int, [_P, C.c_int]),
     ("glacier_hip_kv_pages_create", _P, [C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32]),
     ("glacier_hip_kv_pages_destroy", None, [_P]),
     ("glacier_hip_kv_pages_begin_row", C.c_int, [_P, C.POINTER(RowTxnMark)]),
@@ -685,6 +700,9 @@ class Session:
         check(lib().glacier_hip_session_page_generation(self.h, lane, logical_page, C.byref(v)),
               "page_generation")
         return v.value
+
+    def set_head_domain(self, mode):
+        check(lib().glacier_hip_session_set_head_domain(self.h, mode), "set_head_domain")
 
     def inject_failure(self, enable):
         check(lib().glacier_hip_session_inject_failure(self.h, 1 if enable else 0), "inject")

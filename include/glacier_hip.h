@@ -378,6 +378,39 @@ int glacier_hip_eligible_argmax(glacier_hip_context *ctx, const float *logits_de
                                 const uint64_t *words_dev, uint64_t word_count, uint32_t rows,
                                 glacier_hip_argmax_result_t *results_host, void *stream);
 
+/* Prehead eligible greedy projection: Executor.runGreedyArgmaxEligible
+ * (int4_executor.zig:1859-1967) with the EligibleGreedyContext tile walk
+ * (:968-1150) and its result (EligibleGreedyResult, :786-801). The argmax of
+ * x . W^T over the rows whose bit is set in words_host (LSB-first, exactly
+ * ceil(out_f / 64) words, no bits past out_f, at least one set), lowest
+ * index on ties. Row blocks of 16 with no eligible row stream no weights;
+ * full-vocabulary logits never exist. x_dev: [in_f] f32 on the device,
+ * every element finite; activation GLACIER_HIP_ACT_AUTO or _Q8 (the
+ * reference executor's Q8 arithmetic) or _F32. As in the reference, every
+ * failure -- a wrong word count, bits past out_f, an empty mask, a
+ * non-finite input, an eligible NaN logit -- is GLACIER_HIP_SHAPE_MISMATCH,
+ * and a rejected call writes nothing. The counts are the reference's:
+ * producer_rows = 4 x (4-row groups holding an eligible row; a fully
+ * eligible 64-row tile counts whole), producer_runs = maximal runs of such
+ * groups per 64-row tile, skipped = out_f - producer_rows, overcomputed =
+ * producer_rows - eligible_rows; device_rows is what this device streamed
+ * (16-row blocks holding an eligible row). Synchronous. */
+typedef struct {
+    uint64_t token_index;
+    uint64_t eligible_rows;
+    uint64_t producer_rows;
+    uint64_t skipped_rows;
+    uint64_t overcomputed_rows;
+    uint64_t producer_runs;
+    uint64_t device_rows;
+} glacier_hip_eligible_greedy_result_t;
+
+int glacier_hip_int4_eligible_greedy(glacier_hip_context *ctx, glacier_hip_int4_weight *w,
+                                     const float *x_dev, uint32_t in_f,
+                                     const uint64_t *words_host, uint64_t word_count,
+                                     int activation, glacier_hip_eligible_greedy_result_t *out,
+                                     void *stream);
+
 /* ---- model: Llama/Qwen pre-norm decoder with INT4 projections ------------
  * (forward.zig:36-81 LayerWeights/LayerConfig, loader.zig:31 ModelConfig) */
 typedef struct {
@@ -548,6 +581,15 @@ int glacier_hip_session_page_of(glacier_hip_session *s, uint32_t lane, uint32_t 
                                 int32_t *physical_out);
 int glacier_hip_session_page_generation(glacier_hip_session *s, uint32_t lane,
                                         uint32_t logical_page, uint64_t *ownership_generation_out);
+/* Head domain of eligible steps (GreedyOutputMode, generate.zig:415-426):
+ * POSTHEAD computes every logit, then applies the mask (domain_posthead);
+ * PREHEAD applies it before the head's dot products: a 16-row block with no
+ * eligible row for any lane of a fused-head step (up to 5 lanes) streams no
+ * weights (domain_prehead). Tokens are identical; in PREHEAD an eligible step
+ * cannot return logits (INVALID_ARGUMENT). Wider steps scan full logits. */
+#define GLACIER_HIP_HEAD_DOMAIN_POSTHEAD 0
+#define GLACIER_HIP_HEAD_DOMAIN_PREHEAD 1
+int glacier_hip_session_set_head_domain(glacier_hip_session *s, int mode);
 /* Test hook: make the next decode step fail after its kernels ran but before
  * commit (forces the abort path, as a failed sink/ack would). */
 int glacier_hip_session_inject_failure(glacier_hip_session *s, int enable);
