@@ -1048,9 +1048,10 @@ hipError_t launch_gather_rows(const float *table, const int32_t *ids, int M, int
 // chunks: (max, sum, unnormalised output) records are merged by the combine
 // kernel with the usual log-sum-exp rescaling.
 static constexpr int kMaxChunk = 512;
-static constexpr int kF16MinChunk = 64;   // fewest positions per fp16-KV workgroup
 static constexpr int kMaxRecords = 1024;  // chunk records one combine merges
 static constexpr int kMaxGroup = 8;
+static constexpr long kAttnMaxGrid = 4096;  // fp16 attention: workgroups per launch at most
+static constexpr int kF16MinChunk = 64;      // fewest positions per fp16-KV work item
 
 // Chunk length: short contexts stay one chunk (no combine launch); long ones
 // are split until (chunks x KV heads x rows) >= 2048 work items or chunks of
@@ -1064,10 +1065,10 @@ int attention_chunk(int max_ctx, int num_kv_heads, int M) {
 
 size_t attention_scratch_floats(int max_rows, int num_heads, int num_kv_heads, int head_dim,
                                 int max_ctx) {
-  // the largest chunk-record set the planner produces for any row count
-  // fp16 KV: workgroups of at least kF16MinChunk positions
+  // fp16 KV: a chunk record per kF16MinChunk positions and (row, query head)
   size_t most = (size_t)max_rows * num_heads * ((max_ctx + kF16MinChunk - 1) / kF16MinChunk) *
                 (2 + head_dim);
+  // f32 KV: the largest chunk-record set the planner produces for any row count
   for (int M = 1; M <= max_rows; ++M) {
     const int ch = attention_chunk(max_ctx, num_kv_heads, M);
     const size_t nch = (size_t)(max_ctx + ch - 1) / ch;
@@ -1319,200 +1320,240 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// fp16-KV streaming attention: grid (chunks, KV heads, rows); a workgroup of
-// NW waves owns NW * NT pages of one (row, KV head) and each wave NT pages
-// (16 positions each). A wave reads its page ids once (wave-uniform scalar
-// loads), then issues every K and V load of its pages together, and keeps
-// the whole softmax in registers:
+// fp16-KV streaming attention. The work list is every (row, KV head, chunk
+// of CH = NW * NT * 16 positions) with each row's chunks counted from its own
+// context length, rows in order; workgroup b takes items b, b + grid, ...,
+// so no chunk past a row's context is ever launched for it. A wave owns NT
+// pages of its chunk (16 positions each): it reads their page ids once
+// (wave-uniform scalar loads), issues every K and V load of them together
+// and keeps the softmax in registers:
 //   scores  S^T[pos][head] = K . Q^T on v_mfma_f32_16x16x16f16, q split into
 //           fp16 hi + lo so every product is exact in f32; lane (c, j) ends
 //           with head j's scores of positions 4c + r (r = 0..3) of a page,
 //   softmax max / exp / sum per head over the wave's positions (in-lane, then
 //           two cross-row shuffles),
-//   P.V     on v_mfma_f32_16x16x4f32 (f32 operands): those same registers are
-//           the A operand (k = the four positions 4c + r for fixed r), and
-//           lane (c, j) supplies V[4c + r][DPL * j + b] from one 16-byte (hd
-//           128) or 8-byte (hd 64) load of a V row, so V is read row-major
-//           and fully coalesced.
-// The waves' (max, sum, output) states merge by log-sum-exp in LDS; one chunk
-// writes the output normalised once by the sum (forward.zig:515-528), several
-// write (max, sum, output) records for the combine kernel.
+//   P.V     on v_mfma_f32_16x16x16f16 as well: the A operand is P[head j]
+//           [positions 4c .. 4c+3], which is exactly what lane (c, j) holds,
+//           split into fp16 hi + lo (V is exact in fp16, so the products
+//           are exact in f32); lane (c, j) supplies V[4c + r][DPL * j + e]
+//           for output block e from the DPL consecutive dims it read of each
+//           of its four V rows (one 16-byte load per row at hd 128), so V is
+//           read row-major and fully coalesced.
+// The waves' (max, sum, output) states merge by log-sum-exp in LDS. A row
+// whose context is one chunk writes its output normalised once by the sum
+// (forward.zig:515-528); otherwise every chunk writes a (max, sum, output)
+// record per query head for the combine kernel.
 // ---------------------------------------------------------------------------
 template <int HD, int NT, int NW>
 __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(
     const float *q, const __half *pool, const int32_t *page_table, int max_pages,
-    const int32_t *lane_of_row, const int32_t *ctx_len, int layer, int num_layers, int Hq,
+    const int32_t *lane_of_row, const int32_t *ctx_len, int M, int layer, int num_layers, int Hq,
     int Hkv, int n_chunks_max, int max_ctx, float *scratch, float *out, PlanesDst pd) {
   typedef _Float16 h4 __attribute__((ext_vector_type(4)));
   typedef float f4 __attribute__((ext_vector_type(4)));
   constexpr int S = HD / 16;    // f16 MFMA steps over the head dim
-  constexpr int DPL = HD / 16;  // dims per lane in P.V (one MFMA block each)
+  constexpr int DPL = HD / 16;  // dims per lane and V row = output blocks of P.V
   constexpr int WP = 16 * NT;   // positions per wave
-  constexpr int CH = NW * WP;   // positions per workgroup
+  constexpr int CH = NW * WP;   // positions per work item
+  constexpr int NTH = 64 * NW;
   typedef typename std::conditional<DPL == 8, uint4, uint2>::type vrow_t;
   const int t = threadIdx.x, l = t & 63;
   const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int ch = blockIdx.x, h = blockIdx.y, m = blockIdx.z;
-  const int ctx = min(ctx_len[m], max_ctx);
-  const int j0 = ch * CH;
-  if (j0 >= ctx) return;
-  const int n = min(CH, ctx - j0);
-  const int nch = (ctx + CH - 1) / CH;
-  const int G = Hq / Hkv, qh0 = h * G;
+  const int G = Hq / Hkv;
   const int kv_dim = Hkv * HD;
   const size_t lay = (size_t)num_layers;
   __shared__ float so[NW][kMaxGroup][HD];
   __shared__ float sm[NW][16], sl[NW][16];
+  __shared__ float fw[NW][kMaxGroup], mg[kMaxGroup];
   const float scale = 1.0f / sqrtf((float)HD);
   const int wbase = wv * WP;
-  const int wn = max(0, min(WP, n - wbase));
   const int c = l >> 4, j = l & 15;
 
-  f4 o[DPL];
+  // the work list (every wave holds it; lane r describes row r, M <= 64)
+  const int cl = l < M ? min(ctx_len[l], max_ctx) : 0;
+  const int ln = l < M ? lane_of_row[l] : 0;
+  const int nchl = (cl + CH - 1) / CH;
+  int incl = nchl * Hkv;
 #pragma unroll
-  for (int b = 0; b < DPL; ++b) o[b] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-  float mx = -INFINITY, sum = 0.0f;
-  if (wn > 0) {
-    // q first (it depends on nothing the page walk reads), as the B operand:
-    // lane (c, j) holds head j's dims of k-chunk c
-    const float *qrow = q + ((size_t)m * Hq + qh0 + (j < G ? j : 0)) * HD;
-    float4 qv[S];
+  for (int o = 1; o < 64; o <<= 1) {
+    const int v = __shfl_up(incl, o, 64);
+    if (l >= o) incl += v;
+  }
+  const int total = __builtin_amdgcn_readfirstlane(__shfl(incl, 63, 64));
+
+  for (int item = blockIdx.x; item < total; item += gridDim.x) {
+    // the item's row: the lanes whose running count is <= item precede it
+    const int k = __popcll(__ballot(incl <= item));
+    const int m = __builtin_amdgcn_readfirstlane(k);
+    const int ctx = __builtin_amdgcn_readfirstlane(__shfl(cl, k, 64));
+    const int lane = __builtin_amdgcn_readfirstlane(__shfl(ln, k, 64));
+    const int before = __builtin_amdgcn_readfirstlane(__shfl(incl, k > 0 ? k - 1 : 0, 64));
+    const int nch = (ctx + CH - 1) / CH;
+    const int r = item - (m > 0 ? before : 0);
+    const int h = r / nch, ch = r - h * nch;
+    const int qh0 = h * G;
+    const int j0 = ch * CH;
+    const int n = min(CH, ctx - j0);
+    const int wn = max(0, min(WP, n - wbase));
+
+    f4 o[DPL];
 #pragma unroll
-    for (int st = 0; st < S; ++st) {
-      const int base = 8 * (4 * (st >> 1) + c) + 4 * (st & 1);
-      qv[st] = j < G ? *(const float4 *)(qrow + base) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    // page ids of this wave's pages (wave-uniform)
-    const int32_t *ptab = page_table + (size_t)lane_of_row[m] * max_pages + (j0 + wbase) / 16;
-    int pg[NT];
-#pragma unroll
-    for (int T = 0; T < NT; ++T) pg[T] = 16 * T < wn ? ptab[T] : 0;
-    // K: lane (c, j) loads 16-byte pieces 4 * tt + c of position j of each
-    // page; V: lane (c, j) loads dims DPL*j .. DPL*j + DPL-1 of positions
-    // 4c + r (r = 0..3) of each page
-    uint4 kr[NT][HD / 32];
-    vrow_t vr[NT][4];
-#pragma unroll
-    for (int T = 0; T < NT; ++T) {
-      const size_t pbase = ((size_t)pg[T] * lay + layer) * 2;
-      const bool kval = 16 * T + j < wn;
-      const __half *krow = pool + ((pbase + 0) * 16 + j) * kv_dim + (size_t)h * HD;
-#pragma unroll
-      for (int tt = 0; tt < HD / 32; ++tt)
-        kr[T][tt] = kval ? *(const uint4 *)(krow + 8 * (4 * tt + c)) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int pos = 4 * c + r;
-        const __half *vrow = pool + ((pbase + 1) * 16 + pos) * kv_dim + (size_t)h * HD + DPL * j;
-        if (16 * T + pos < wn) vr[T][r] = *(const vrow_t *)vrow;
-        else __builtin_memset(&vr[T][r], 0, sizeof(vrow_t));
-      }
-    }
-    // q split into f16 hi + lo (after the K/V loads are in flight)
-    h4 qhi[S], qlo[S];
-#pragma unroll
-    for (int st = 0; st < S; ++st) {
-      const float qa[4] = {qv[st].x, qv[st].y, qv[st].z, qv[st].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const _Float16 hv = (_Float16)qa[e];
-        qhi[st][e] = hv;
-        qlo[st][e] = (_Float16)(qa[e] - (float)hv);
-      }
-    }
-    // scores: S^T = K . Q^T, one 16x16 tile per page
-    f4 sc[NT];
-#pragma unroll
-    for (int T = 0; T < NT; ++T) {
-      f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int e = 0; e < DPL; ++e) o[e] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    float mx = -INFINITY, sum = 0.0f;
+    if (wn > 0) {
+      // q first (it depends on nothing the page walk reads), as the B operand:
+      // lane (c, j) holds head j's dims of k-chunk c
+      const float *qrow = q + ((size_t)m * Hq + qh0 + (j < G ? j : 0)) * HD;
+      float4 qv[S];
 #pragma unroll
       for (int st = 0; st < S; ++st) {
-        const uint4 w = kr[T][st >> 1];
-        const uint2 bw = (st & 1) ? make_uint2(w.z, w.w) : make_uint2(w.x, w.y);
-        h4 a;
-        __builtin_memcpy(&a, &bw, 8);
-        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qhi[st], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qlo[st], acc, 0, 0, 0);
+        const int base = 8 * (4 * (st >> 1) + c) + 4 * (st & 1);
+        qv[st] = j < G ? *(const float4 *)(qrow + base) : make_float4(0.f, 0.f, 0.f, 0.f);
       }
+      // page ids of this wave's pages (wave-uniform)
+      const int32_t *ptab = page_table + (size_t)lane * max_pages + (j0 + wbase) / 16;
+      int pg[NT];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float v = acc[r] * scale;
-        sc[T][r] = 16 * T + 4 * c + r < wn ? v : -INFINITY;
-        mx = fmaxf(mx, sc[T][r]);
+      for (int T = 0; T < NT; ++T) pg[T] = 16 * T < wn ? ptab[T] : 0;
+      // K: lane (c, j) loads 16-byte pieces 4 * tt + c of position j of each
+      // page; V: lane (c, j) loads dims DPL*j .. DPL*j + DPL-1 of positions
+      // 4c + r (r = 0..3) of each page
+      uint4 kr[NT][HD / 32];
+      vrow_t vr[NT][4];
+#pragma unroll
+      for (int T = 0; T < NT; ++T) {
+        const size_t pbase = ((size_t)pg[T] * lay + layer) * 2;
+        const bool kval = 16 * T + j < wn;
+        const __half *krow = pool + ((pbase + 0) * 16 + j) * kv_dim + (size_t)h * HD;
+#pragma unroll
+        for (int tt = 0; tt < HD / 32; ++tt)
+          kr[T][tt] = kval ? *(const uint4 *)(krow + 8 * (4 * tt + c)) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int pos = 4 * c + rr;
+          const __half *vrow = pool + ((pbase + 1) * 16 + pos) * kv_dim + (size_t)h * HD + DPL * j;
+          if (16 * T + pos < wn) vr[T][rr] = *(const vrow_t *)vrow;
+          else __builtin_memset(&vr[T][rr], 0, sizeof(vrow_t));
+        }
+      }
+      // q split into f16 hi + lo (after the K/V loads are in flight)
+      h4 qhi[S], qlo[S];
+#pragma unroll
+      for (int st = 0; st < S; ++st) {
+        const float qa[4] = {qv[st].x, qv[st].y, qv[st].z, qv[st].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const _Float16 hv = (_Float16)qa[e];
+          qhi[st][e] = hv;
+          qlo[st][e] = (_Float16)(qa[e] - (float)hv);
+        }
+      }
+      // scores: S^T = K . Q^T, one 16x16 tile per page
+      f4 sc[NT];
+#pragma unroll
+      for (int T = 0; T < NT; ++T) {
+        f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int st = 0; st < S; ++st) {
+          const uint4 w = kr[T][st >> 1];
+          const uint2 bw = (st & 1) ? make_uint2(w.z, w.w) : make_uint2(w.x, w.y);
+          h4 a;
+          __builtin_memcpy(&a, &bw, 8);
+          acc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qhi[st], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qlo[st], acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const float v = acc[rr] * scale;
+          sc[T][rr] = 16 * T + 4 * c + rr < wn ? v : -INFINITY;
+          mx = fmaxf(mx, sc[T][rr]);
+        }
+      }
+      mx = xor32_max(xor16_max(mx));
+#pragma unroll
+      for (int T = 0; T < NT; ++T)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const float p = expf(sc[T][rr] - mx);
+          sc[T][rr] = p;
+          sum += p;
+        }
+      sum = xor32_add(xor16_add(sum));
+      // P.V: A = P[head j][pos 4c .. 4c+3] (this lane's own registers, fp16
+      // hi + lo), B_e = V[pos 4c + r][dim DPL * j + e]
+#pragma unroll
+      for (int T = 0; T < NT; ++T) {
+        h4 phi, plo;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const _Float16 hv = (_Float16)sc[T][rr];
+          phi[rr] = hv;
+          plo[rr] = (_Float16)(sc[T][rr] - (float)hv);
+        }
+        const _Float16 *v0 = (const _Float16 *)&vr[T][0];
+        const _Float16 *v1 = (const _Float16 *)&vr[T][1];
+        const _Float16 *v2 = (const _Float16 *)&vr[T][2];
+        const _Float16 *v3 = (const _Float16 *)&vr[T][3];
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) {
+          const h4 bv = {v0[e], v1[e], v2[e], v3[e]};
+          o[e] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi, bv, o[e], 0, 0, 0);
+          o[e] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo, bv, o[e], 0, 0, 0);
+        }
       }
     }
-    mx = xor32_max(xor16_max(mx));
+    // lane (c, j) holds O[head 4c + r][dim DPL * j + e]
+    if (c < 2) {
 #pragma unroll
-    for (int T = 0; T < NT; ++T)
+      for (int rr = 0; rr < 4; ++rr)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float p = expf(sc[T][r] - mx);
-        sc[T][r] = p;
-        sum += p;
-      }
-    sum = xor32_add(xor16_add(sum));
-    // P.V: A = P[head][pos 4c + r] (this lane's own registers), B = V
-#pragma unroll
-    for (int T = 0; T < NT; ++T)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const __half *hv = (const __half *)&vr[T][r];
-#pragma unroll
-        for (int b = 0; b < DPL; ++b)
-          o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(sc[T][r], __half2float(hv[b]), o[b], 0, 0, 0);
-      }
-  }
-  // lane (c, j) holds O[head 4c + r][dim DPL * j + b]
-  if (c < 2) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int b = 0; b < DPL; ++b) so[wv][4 * c + r][DPL * j + b] = o[b][r];
-  }
-  if (c == 0) {
-    sm[wv][j] = mx;
-    sl[wv][j] = sum;
-  }
-  __syncthreads();
-  // ---- merge the waves (log-sum-exp) ----
-  // The weight of wave w for head g, exp(m_w - M) (0 for a wave without
-  // positions), is computed once per (wave, head); every output is then two
-  // short dot products over the waves, in wave order (the same arithmetic
-  // as evaluating the weights inside each output's loop, without its NW
-  // exponentials and branches per output).
-  __shared__ float fw[NW][kMaxGroup], mg[kMaxGroup];
-  for (int i = t; i < NW * G; i += 64 * NW) {
-    const int w = i / G, g = i % G;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w2 = 0; w2 < NW; ++w2)
-      if (sl[w2][g] > 0.0f) M = fmaxf(M, sm[w2][g]);
-    fw[w][g] = sl[w][g] > 0.0f ? expf(sm[w][g] - M) : 0.0f;
-    if (w == 0) mg[g] = M;
-  }
-  __syncthreads();
-  for (int oi = t; oi < G * HD; oi += 64 * NW) {
-    const int g = oi / HD, d = oi % HD;
-    const float M = mg[g];
-    float L = 0.0f, O = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const float f = fw[w][g];
-      L = fmaf(sl[w][g], f, L);
-      O = fmaf(so[w][g][d], f, O);
+        for (int e = 0; e < DPL; ++e) so[wv][4 * c + rr][DPL * j + e] = o[e][rr];
     }
-    if (nch == 1) {
-      const float v = O * (1.0f / L);
-      out[((size_t)m * Hq + qh0 + g) * HD + d] = v;
-      emit_group(pd, v, t & 31, ((qh0 + g) * HD + d) >> 5, m, (int)gridDim.z);
-    } else {
-      float *rec = scratch + (((size_t)m * Hq + qh0 + g) * n_chunks_max + ch) * (2 + HD);
-      if (d == 0) {
-        rec[0] = M;
-        rec[1] = L;
-      }
-      rec[2 + d] = O;
+    if (c == 0) {
+      sm[wv][j] = mx;
+      sl[wv][j] = sum;
     }
+    __syncthreads();
+    // ---- merge the waves (log-sum-exp) ----
+    // The weight of wave w for head g, exp(m_w - M) (0 for a wave without
+    // positions), is computed once per (wave, head); every output is then two
+    // short dot products over the waves, in wave order.
+    for (int i = t; i < NW * G; i += NTH) {
+      const int w = i / G, g = i % G;
+      float Mx = -INFINITY;
+#pragma unroll
+      for (int w2 = 0; w2 < NW; ++w2)
+        if (sl[w2][g] > 0.0f) Mx = fmaxf(Mx, sm[w2][g]);
+      fw[w][g] = sl[w][g] > 0.0f ? expf(sm[w][g] - Mx) : 0.0f;
+      if (w == 0) mg[g] = Mx;
+    }
+    __syncthreads();
+    constexpr int RS = 2 + HD;  // floats per record
+    const size_t hstride = (size_t)n_chunks_max * RS;
+    float *rbase = scratch + ((size_t)m * Hq + qh0) * hstride;
+    for (int oi = t; oi < G * HD; oi += NTH) {
+      const int g = oi / HD, d = oi % HD;
+      float L = 0.0f, O = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float f = fw[w][g];
+        L = fmaf(sl[w][g], f, L);
+        O = fmaf(so[w][g][d], f, O);
+      }
+      if (nch == 1) {
+        const float v = O * (1.0f / L);
+        out[((size_t)m * Hq + qh0 + g) * HD + d] = v;
+        emit_group(pd, v, t & 31, ((qh0 + g) * HD + d) >> 5, m, M);
+      } else {
+        float *rec = rbase + g * hstride + (size_t)ch * RS;
+        if (d == 0) {
+          rec[0] = mg[g];
+          rec[1] = L;
+        }
+        rec[2 + d] = O;
+      }
+    }
+    __syncthreads();  // LDS is reused by the next item
   }
 }
 
@@ -1602,17 +1643,20 @@ hipError_t launch_attention_f16(const float *q, const void *kv_pool, const int32
                                 int M, int layer, int num_layers, int num_heads, int num_kv_heads,
                                 int head_dim, int max_ctx, float *scratch, float *out,
                                 hipStream_t st, int wp, int nw, PlanesDst emit) {
-  if (num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > kMaxGroup)
+  if (num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > kMaxGroup || M < 1 || M > 64 ||
+      max_ctx < 1)
     return hipErrorInvalidValue;
   const int chunk = wp * nw;
   if (chunk < kF16MinChunk || wp % 16) return hipErrorInvalidValue;
-  const int nch = (max_ctx + chunk - 1) / chunk;
+  const int nch = (max_ctx + chunk - 1) / chunk;  // record slots per (row, query head)
   if (nch > kMaxRecords) return hipErrorInvalidValue;
-  dim3 grid(nch, num_kv_heads, M);
+  // one workgroup per work item up to a cap; the rest loop over the list
+  const long items = (long)nch * num_kv_heads * M;
+  const unsigned grid = (unsigned)std::min<long>(items, kAttnMaxGrid);
   const __half *pool = (const __half *)kv_pool;
 #define GK_F16(HD, NT, NW)                                                                   \
-  hipLaunchKernelGGL((attn_f16_kernel<HD, NT, NW>), grid, dim3(64 * NW), 0, st, q, pool,     \
-                     page_table, max_pages, lane_of_row, ctx_len, layer, num_layers,         \
+  hipLaunchKernelGGL((attn_f16_kernel<HD, NT, NW>), dim3(grid), dim3(64 * NW), 0, st, q, pool, \
+                     page_table, max_pages, lane_of_row, ctx_len, M, layer, num_layers,      \
                      num_heads, num_kv_heads, nch, max_ctx, scratch, out, emit)
 #define GK_F16_HD(NT, NW)                                        \
   do {                                                          \
@@ -1631,11 +1675,11 @@ hipError_t launch_attention_f16(const float *q, const void *kv_pool, const int32
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || nch <= 1) return e;
   if (head_dim == 64)
-    hipLaunchKernelGGL((attn_combine2_kernel<64>), dim3(num_heads, M), dim3(kCombineThreads), 0, st, ctx_len,
-                       num_heads, chunk, nch, max_ctx, scratch, out, emit);
+    hipLaunchKernelGGL((attn_combine2_kernel<64>), dim3(num_heads, M), dim3(kCombineThreads), 0,
+                       st, ctx_len, num_heads, chunk, nch, max_ctx, scratch, out, emit);
   else
-    hipLaunchKernelGGL((attn_combine2_kernel<128>), dim3(num_heads, M), dim3(kCombineThreads), 0, st, ctx_len,
-                       num_heads, chunk, nch, max_ctx, scratch, out, emit);
+    hipLaunchKernelGGL((attn_combine2_kernel<128>), dim3(num_heads, M), dim3(kCombineThreads), 0,
+                       st, ctx_len, num_heads, chunk, nch, max_ctx, scratch, out, emit);
   return hipGetLastError();
 }
 
@@ -1837,14 +1881,19 @@ hipError_t launch_attention(const float *q, const void *kv_pool, int kv_f16,
   if (num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > kMaxGroup)
     return hipErrorInvalidValue;
   if (kv_f16) {
-    // one page per wave; workgroups of 16 waves when the whole context fits
-    // one (no combine), else 4 waves for few (row, KV head) pairs and 8 for
-    // many, which keeps about 1000 or more workgroups on long contexts
-    // (measured on 1-16 rows at contexts 150-8192)
-    const int nw = max_ctx <= 256 ? 16 : (M * num_kv_heads < 16 ? 4 : 8);
+    // contexts up to 256 positions: one work item per (row, KV head) of 8
+    // waves x 2 pages, no combine launch; longer ones: 64-position items of
+    // 4 waves x 1 page for few (row, KV head) pairs (batch-1 decode), else
+    // 128-position items of 4 waves x 2 pages (measured at 1-32 rows,
+    // contexts 16-8192)
+    int wp = 32, nw = 8;
+    if (max_ctx > 256) {
+      wp = M * num_kv_heads < 16 ? 16 : 32;
+      nw = 4;
+    }
     return launch_attention_f16(q, kv_pool, page_table, max_pages, lane_of_row, ctx_len, M, layer,
                                 num_layers, num_heads, num_kv_heads, head_dim, max_ctx, scratch,
-                                out, st, 16, nw, emit);
+                                out, st, wp, nw, emit);
   }
   const int chunk = attention_chunk(max_ctx, num_kv_heads, M);
   if ((max_ctx + chunk - 1) / chunk > kMaxRecords) return hipErrorInvalidValue;
