@@ -21,6 +21,7 @@
 #include "paged_kv.h"
 #include "publication.h"
 #include "runtime.h"
+#include "runtime_image.h"
 
 using gh::hip_fail;
 
@@ -367,6 +368,212 @@ uint64_t glacier_hip_model_weight_bytes(const glacier_hip_model *m) {
 }
 
 }  // extern "C"
+
+
+// ---------------------------------------------------------------------------
+// prepared runtime image -> device model (loader.zig:193-390)
+// ---------------------------------------------------------------------------
+namespace gri {
+const Image *image_of(const glacier_hip_glrt_image *h);
+}
+
+namespace {
+
+struct Int4View {
+  const uint8_t *packed = nullptr;
+  const float *s32 = nullptr;     // f32 scales (may be null)
+  const uint16_t *s16 = nullptr;  // f16 scale mirror (may be null)
+  uint64_t scales = 0;
+};
+
+// preparedRaw (loader.zig:785-809)
+uint32_t prepared_raw(const gri::Image &img, uint32_t layer, uint32_t kind, uint64_t n,
+                      bool required, const float **out) {
+  *out = nullptr;
+  const glacier_hip_glrt_record_t *r = gri::find(img, layer, kind, gri::kTensor);
+  if (!r) return required ? GLACIER_HIP_GLRT_MISSING_TENSOR : GLACIER_HIP_GLRT_OK;
+  if (r->encoding != gri::kRawF32 || r->packed_layout != gri::kLayoutNone || r->group_size != 0 ||
+      r->out_f != 1 || r->in_f != n || r->num_elements != n)
+    return GLACIER_HIP_GLRT_BAD_PAYLOAD;
+  uint64_t len = 0;
+  *out = (const float *)gri::stream(img, *r, gri::kRaw, &len);
+  return len == n * 4 ? GLACIER_HIP_GLRT_OK : GLACIER_HIP_GLRT_BAD_PAYLOAD;
+}
+
+// preparedInt4 (loader.zig:811-868), then what this device runs: row-major
+// nibbles, group 32, and f32 or f16 (non-rows4) scales
+uint32_t prepared_int4(const gri::Image &img, uint32_t layer, uint32_t kind, uint64_t out_f,
+                       uint64_t in_f, bool require_f32, Int4View *v) {
+  const glacier_hip_glrt_record_t *r = gri::find(img, layer, kind, gri::kTensor);
+  if (!r) return GLACIER_HIP_GLRT_MISSING_TENSOR;
+  const uint64_t n = out_f * in_f;
+  if (r->encoding != gri::kInt4 || r->group_size == 0 || r->out_f != out_f || r->in_f != in_f ||
+      r->num_elements != n)
+    return GLACIER_HIP_GLRT_BAD_PAYLOAD;
+  uint64_t lp, l32, l16, l16r;
+  v->packed = gri::stream(img, *r, gri::kPacked, &lp);
+  v->s32 = (const float *)gri::stream(img, *r, gri::kScalesF32, &l32);
+  v->s16 = (const uint16_t *)gri::stream(img, *r, gri::kScalesF16, &l16);
+  gri::stream(img, *r, gri::kScalesF16Rows4, &l16r);
+  const uint64_t sc = (n + r->group_size - 1) / r->group_size;
+  if (lp != (n + 1) / 2 || (l32 && l32 != sc * 4) || (l16 && l16 != sc * 2) ||
+      (l16r && l16r != sc * 2) || (!l32 && !l16 && !l16r) || (require_f32 && l32 != sc * 4))
+    return GLACIER_HIP_GLRT_BAD_PAYLOAD;
+  if (r->packed_layout == gri::kRows4K16 && (out_f % 4 || in_f % 16 || l16r != sc * 2))
+    return GLACIER_HIP_GLRT_BAD_PAYLOAD;
+  if (r->packed_layout == gri::kLayoutNone) return GLACIER_HIP_GLRT_BAD_PAYLOAD;
+  // the device's tile layout is built from row-major nibbles and group-32
+  // scales (f32 or the plain f16 mirror)
+  if (r->packed_layout != gri::kRowMajor || r->group_size != 32 || (!l32 && !l16))
+    return GLACIER_HIP_GLRT_UNSUPPORTED;
+  v->scales = sc;
+  return GLACIER_HIP_GLRT_OK;
+}
+
+// isExpectedPreparedRecord (loader.zig:731-768)
+bool expected_record(const glacier_hip_glrt_info_t &c, const glacier_hip_glrt_record_t &r) {
+  if (r.role == gri::kMlpGateUpPair) return r.layer_idx != gri::kGlobalLayer && r.layer_idx < c.layers;
+  if (r.role != gri::kTensor) return false;
+  if (r.layer_idx == gri::kGlobalLayer)
+    return r.kind == gri::kFinalNorm || r.kind == gri::kEmbedding ||
+           (r.kind == gri::kLmHead && !c.tie_embeddings);
+  if (r.layer_idx >= c.layers) return false;
+  switch (r.kind) {
+    case gri::kInputNorm: case gri::kAttnQ: case gri::kAttnK: case gri::kAttnV: case gri::kAttnO:
+    case gri::kAttnQBias: case gri::kAttnKBias: case gri::kAttnVBias: case gri::kAttnOBias:
+    case gri::kPostAttnNorm: case gri::kMlpGate: case gri::kMlpUp: case gri::kMlpDown:
+      return true;
+    default:
+      return false;
+  }
+}
+
+// f16 scales for the tile layout: the mirror when present, else f32 -> f16
+// (round to nearest even), counting the values fp16 does not hold exactly
+const uint16_t *scales_f16(const Int4View &v, std::vector<uint16_t> &buf, uint64_t *inexact) {
+  if (v.s16) return v.s16;
+  buf.resize(v.scales);
+  for (uint64_t i = 0; i < v.scales; ++i) {
+    buf[i] = gh::f32_to_f16(v.s32[i]);
+    if (gh::f16_to_f32(buf[i]) != v.s32[i]) ++*inexact;
+  }
+  return buf.data();
+}
+
+}  // namespace
+
+extern "C" glacier_hip_model *glacier_hip_model_load_glrt(glacier_hip_context *ctx,
+                                                          const glacier_hip_glrt_image *handle,
+                                                          glacier_hip_glrt_load_report_t *report) {
+  glacier_hip_glrt_load_report_t rep{};
+  glacier_hip_model *m = nullptr;
+  auto fail = [&](uint32_t e, const char *what) -> glacier_hip_model * {
+    rep.error = e;
+    if (report) *report = rep;
+    if (ctx) ctx->last_error = std::string("glrt load: ") + gri::error_name(e) + " (" + what + ")";
+    glacier_hip_model_destroy(m);
+    return nullptr;
+  };
+  const gri::Image *img = gri::image_of(handle);
+  if (!ctx || !img) return fail(GLACIER_HIP_GLRT_BAD_PAYLOAD, "null context or image");
+  const glacier_hip_glrt_info_t &c = img->info;
+  // validatePreparedConfig (loader.zig:618-654)
+  if ((uint64_t)c.heads * c.head_dim != c.dim || c.kv_heads > c.heads || c.heads % c.kv_heads)
+    return fail(GLACIER_HIP_GLRT_BAD_PAYLOAD, "config");
+  // validatePreparedRecordSet (loader.zig:656-716): expected records only,
+  // and one homogeneous MLP layout (separate gate/up is what this device runs)
+  for (const auto &r : img->records)
+    if (!expected_record(c, r)) return fail(GLACIER_HIP_GLRT_BAD_PAYLOAD, "unexpected record");
+  for (uint32_t l = 0; l < c.layers; ++l) {
+    const bool gate = gri::find(*img, l, gri::kMlpGate, gri::kTensor) != nullptr;
+    const bool up = gri::find(*img, l, gri::kMlpUp, gri::kTensor) != nullptr;
+    const bool pair = gri::find(*img, l, 0, gri::kMlpGateUpPair) != nullptr;
+    if (pair) {
+      if (gate || up) return fail(GLACIER_HIP_GLRT_BAD_PAYLOAD, "gate/up pair beside gate or up");
+      return fail(GLACIER_HIP_GLRT_UNSUPPORTED, "PairNibble gate/up");
+    }
+    if (!gate || !up) return fail(GLACIER_HIP_GLRT_MISSING_TENSOR, "gate/up");
+  }
+  rep.separate_mlp = 1;
+  const uint64_t D = c.dim, F = c.hidden_dim, V = c.vocab, kvd = (uint64_t)c.kv_heads * c.head_dim;
+  glacier_hip_model_config_t mc{};
+  mc.num_layers = c.layers;
+  mc.dim = c.dim;
+  mc.hidden_dim = c.hidden_dim;
+  mc.num_heads = c.heads;
+  mc.num_kv_heads = c.kv_heads;
+  mc.head_dim = c.head_dim;
+  mc.vocab_size = c.vocab;
+  mc.group_size = 32;
+  mc.rms_eps = c.rms_eps;
+  mc.rope_theta = c.rope_theta;
+  m = glacier_hip_model_create(ctx, &mc);
+  if (!m) return fail(GLACIER_HIP_GLRT_UNSUPPORTED, "model shape");
+  std::vector<uint16_t> sbuf[7];
+  uint32_t e;
+  for (uint32_t l = 0; l < c.layers; ++l) {
+    glacier_hip_layer_host_t w{};
+    const float *bo = nullptr;
+    if ((e = prepared_raw(*img, l, gri::kInputNorm, D, true, &w.input_norm)) ||
+        (e = prepared_raw(*img, l, gri::kPostAttnNorm, D, true, &w.post_attn_norm)) ||
+        (e = prepared_raw(*img, l, gri::kAttnQBias, D, false, &w.bq)) ||
+        (e = prepared_raw(*img, l, gri::kAttnKBias, kvd, false, &w.bk)) ||
+        (e = prepared_raw(*img, l, gri::kAttnVBias, kvd, false, &w.bv)) ||
+        (e = prepared_raw(*img, l, gri::kAttnOBias, D, false, &bo)))
+      return fail(e, "layer norms / biases");
+    if (bo) return fail(GLACIER_HIP_GLRT_UNSUPPORTED, "attn_o bias");
+    const uint32_t kinds[7] = {gri::kAttnQ, gri::kAttnK, gri::kAttnV, gri::kAttnO,
+                               gri::kMlpGate, gri::kMlpUp, gri::kMlpDown};
+    const uint64_t outs[7] = {D, kvd, kvd, D, F, F, D}, ins[7] = {D, D, D, D, D, D, F};
+    Int4View v[7];
+    const uint16_t *s16[7];
+    for (int i = 0; i < 7; ++i) {
+      if ((e = prepared_int4(*img, l, kinds[i], outs[i], ins[i], false, &v[i])))
+        return fail(e, "layer projection");
+      s16[i] = scales_f16(v[i], sbuf[i], &rep.inexact_scales);
+      rep.int4_records++;
+    }
+    w.wq = v[0].packed; w.wk = v[1].packed; w.wv = v[2].packed; w.wo = v[3].packed;
+    w.w_gate = v[4].packed; w.w_up = v[5].packed; w.w_down = v[6].packed;
+    int rc = set_layer_impl(m, l, w, s16);
+    if (rc) return fail(GLACIER_HIP_GLRT_BAD_PAYLOAD, "device upload");
+    rep.raw_records += 2 + (w.bq != nullptr) + (w.bk != nullptr) + (w.bv != nullptr);
+  }
+  const float *final_norm = nullptr;
+  if ((e = prepared_raw(*img, gri::kGlobalLayer, gri::kFinalNorm, D, true, &final_norm)))
+    return fail(e, "final_norm");
+  // the token embedding is INT4 with f32 scales; dequantizeRow
+  // (int4_matmul.zig:3164-3194) per element: NIBBLE_TO_OFFSET[u] * scale
+  Int4View emb, head;
+  if ((e = prepared_int4(*img, gri::kGlobalLayer, gri::kEmbedding, V, D, true, &emb)))
+    return fail(e, "embedding");
+  if (c.tie_embeddings) {
+    head = emb;
+  } else if ((e = prepared_int4(*img, gri::kGlobalLayer, gri::kLmHead, V, D, false, &head))) {
+    return fail(e, "lm_head");
+  }
+  std::vector<float> table(V * D);
+  gh::parallel_for(V, [&](size_t r0, size_t r1) {
+    for (size_t r = r0; r < r1; ++r)
+      for (size_t k = 0; k < D; ++k) {
+        const size_t idx = r * D + k;
+        const uint8_t b = emb.packed[idx / 2];
+        const int u = (idx & 1) ? b >> 4 : b & 0xF;
+        table[idx] = (float)(u - 7) * emb.s32[idx / 32];
+      }
+  }, 256);
+  std::vector<float> head_s(head.scales);
+  std::vector<uint16_t> hbuf;
+  const uint16_t *h16 = scales_f16(head, hbuf, &rep.inexact_scales);
+  for (uint64_t i = 0; i < head.scales; ++i) head_s[i] = gh::f16_to_f32(h16[i]);
+  rep.int4_records += c.tie_embeddings ? 1 : 2;
+  rep.raw_records += 1;
+  int rc = glacier_hip_model_set_globals(m, table.data(), final_norm, head.packed, head_s.data());
+  if (rc) return fail(GLACIER_HIP_GLRT_BAD_PAYLOAD, "device upload");
+  rep.uploaded_bytes = m->bytes ? m->bytes : glacier_hip_model_weight_bytes(m);
+  if (report) *report = rep;
+  return m;
+}
 
 // ---------------------------------------------------------------------------
 // session

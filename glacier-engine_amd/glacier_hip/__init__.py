@@ -27,6 +27,8 @@ TRANSACTION_ACTIVE = 11
 INVALID_TRANSACTION = 12
 BUSY = 13
 UNSUPPORTED = 14
+BAD_IMAGE = 20
+NOT_FOUND = 21
 
 F32, F16, BF16 = 0, 1, 2
 ACT_Q8, ACT_F32, ACT_AUTO = 0, 1, 2
@@ -272,6 +274,48 @@ class AsyncCompletion(C.Structure):
                                    "error_present", "callback_fault", "reserved")]
 
 
+class GlrtOpenOptions(C.Structure):
+    _fields_ = [("verify_payload_crc", C.c_int32), ("verify_payload_digest", C.c_int32),
+                ("allow_v1", C.c_int32), ("check_source_fingerprint", C.c_int32),
+                ("expected_source_fingerprint", C.c_uint8 * 32)]
+
+
+class GlrtInfo(C.Structure):
+    _fields_ = [("error", C.c_uint32), ("version", C.c_uint32), ("record_count", C.c_uint64),
+                ("data_offset", C.c_uint64), ("file_size", C.c_uint64),
+                ("source_fingerprint", C.c_uint8 * 32), ("abi_fingerprint", C.c_uint8 * 32)] + \
+        [(n, C.c_uint32) for n in ("dim", "hidden_dim", "layers", "vocab", "heads", "head_dim",
+                                   "kv_heads", "tie_embeddings")] + \
+        [("rms_eps", C.c_float), ("rope_theta", C.c_float)]
+
+
+class GlrtRecord(C.Structure):
+    _fields_ = [("layer_idx", C.c_uint32), ("kind", C.c_uint32), ("role", C.c_uint16),
+                ("encoding", C.c_uint16), ("packed_layout", C.c_uint16),
+                ("pair_nibble_layout", C.c_uint16)] + \
+        [(n, C.c_uint32) for n in ("group_size", "out_f", "in_f", "flags", "payload_crc32",
+                                   "reserved")] + \
+        [("num_elements", C.c_uint64), ("offset", C.c_uint64 * 5), ("length", C.c_uint64 * 5),
+         ("payload_digest", C.c_uint8 * 32)]
+
+
+class GlrtLoadReport(C.Structure):
+    _fields_ = [("error", C.c_uint32), ("separate_mlp", C.c_uint32), ("int4_records", C.c_uint64),
+                ("raw_records", C.c_uint64), ("inexact_scales", C.c_uint64),
+                ("uploaded_bytes", C.c_uint64)]
+
+
+# glacier_hip_glrt_error, by the reference's error names
+GLRT_ERRORS = ["Ok", "TruncatedHeader", "BadMagic", "BadVersion", "BadHeaderSize", "BadRecordSize",
+               "BadAlignment", "BadConfig", "BadReservedField", "HeaderCrcMismatch",
+               "LegacyVersionDisabled", "BadHeader", "BadBounds", "SourceFingerprintMismatch",
+               "AbiFingerprintMismatch", "IndexCrcMismatch", "TruncatedIndex", "BadTensorKind",
+               "BadEncoding", "BadPackedLayout", "BadRole", "BadPairNibbleLayout", "BadFlags",
+               "BadVersionedRecord", "MissingDigest", "BadTensorShape", "MissingScales",
+               "OverlappingPayload", "DuplicateRecord", "CrcMismatch", "DigestMismatch",
+               "FileError", "MissingTensor", "BadPayload", "NoLayers", "Unsupported"]
+
+
 COMMAND_PENDING, COMMAND_COMPLETED, COMMAND_ERROR, COMMAND_UNKNOWN = 1, 2, 3, 4
 
 # (name, restype, argtypes) for every exported symbol of include/glacier_hip.h
@@ -404,6 +448,15 @@ _SIGS = [
     ("glacier_hip_lane_weave_state_sha256", C.c_int, [_P, _P]),
     ("glacier_hip_session_lane_weave_wave", C.c_int,
      [_P, _P, _P, C.c_uint32, _P, _P, C.c_uint32, _P, _P, C.POINTER(C.c_uint32)]),
+    ("glacier_hip_glrt_open", C.c_int,
+     [C.c_char_p, C.POINTER(GlrtOpenOptions), C.POINTER(_P), C.POINTER(GlrtInfo)]),
+    ("glacier_hip_glrt_close", None, [_P]),
+    ("glacier_hip_glrt_record_at", C.c_int, [_P, C.c_uint64, C.POINTER(GlrtRecord)]),
+    ("glacier_hip_glrt_find", C.c_int, [_P, C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(GlrtRecord)]),
+    ("glacier_hip_glrt_stream", C.c_int,
+     [_P, C.POINTER(GlrtRecord), C.c_uint32, C.POINTER(_P), C.POINTER(C.c_uint64)]),
+    ("glacier_hip_glrt_identity", C.c_int, [_P, _P, C.POINTER(C.c_uint64)]),
+    ("glacier_hip_model_load_glrt", _P, [_P, _P, C.POINTER(GlrtLoadReport)]),
 ]
 
 _lib = None
@@ -524,6 +577,65 @@ def random_model_host(cfg, seed):
     )
 
 
+class GlrtError(GlacierHipError):
+    """A prepared runtime image that failed validation; .reason is the
+    reference's error name."""
+
+    def __init__(self, code, reason, what):
+        super().__init__(code, f"{what}: {reason}")
+        self.reason = reason
+
+
+class GlrtImage:
+    """A validated .glrt image (glacier_hip_glrt_open); host only."""
+
+    def __init__(self, path, verify_payload_crc=True, verify_payload_digest=True, allow_v1=True,
+                 expected_source=None):
+        o = GlrtOpenOptions(verify_payload_crc=int(verify_payload_crc),
+                            verify_payload_digest=int(verify_payload_digest),
+                            allow_v1=int(allow_v1), check_source_fingerprint=int(expected_source is not None))
+        if expected_source is not None:
+            o.expected_source_fingerprint[:] = list(expected_source)
+        self.info = GlrtInfo()
+        h = _P()
+        rc = lib().glacier_hip_glrt_open(os.fsencode(path), C.byref(o), C.byref(h), C.byref(self.info))
+        if rc != OK:
+            raise GlrtError(rc, GLRT_ERRORS[self.info.error], "glrt_open")
+        self.h = h
+
+    def record_at(self, i):
+        r = GlrtRecord()
+        check(lib().glacier_hip_glrt_record_at(self.h, i, C.byref(r)), "glrt_record_at")
+        return r
+
+    def records(self):
+        return [self.record_at(i) for i in range(self.info.record_count)]
+
+    def find(self, layer, kind, role=0):
+        r = GlrtRecord()
+        rc = lib().glacier_hip_glrt_find(self.h, layer, kind, role, C.byref(r))
+        if rc == NOT_FOUND:
+            return None
+        check(rc, "glrt_find")
+        return r
+
+    def stream(self, record, s):
+        p, n = _P(), C.c_uint64()
+        check(lib().glacier_hip_glrt_stream(self.h, C.byref(record), s, C.byref(p), C.byref(n)),
+              "glrt_stream")
+        return C.string_at(p.value, n.value) if n.value else b""
+
+    def identity(self):
+        d, n = (C.c_uint8 * 32)(), C.c_uint64()
+        check(lib().glacier_hip_glrt_identity(self.h, d, C.byref(n)), "glrt_identity")
+        return bytes(d), n.value
+
+    def close(self):
+        if self.h:
+            lib().glacier_hip_glrt_close(self.h)
+            self.h = None
+
+
 # ---- thin object wrappers -------------------------------------------------------------
 class Context:
     def __init__(self, device=0):
@@ -589,6 +701,21 @@ class Model:
             self.h, ptr(host["embedding"]), ptr(host["final_norm"]), ptr(host["lm_head"]),
             ptr(np.ascontiguousarray(host["lm_head_scales"], dtype=np.float32))),
             "set_globals", self.ctx.h)
+
+    @classmethod
+    def load_glrt(cls, ctx, image):
+        """glacier_hip_model_load_glrt: a device model from a validated image."""
+        m = cls.__new__(cls)
+        m.ctx = ctx
+        i = image.info
+        m.cfg = dict(num_layers=i.layers, dim=i.dim, hidden_dim=i.hidden_dim, num_heads=i.heads,
+                     num_kv_heads=i.kv_heads, head_dim=i.head_dim, vocab_size=i.vocab,
+                     group_size=32, rms_eps=i.rms_eps, rope_theta=i.rope_theta)
+        m.report = GlrtLoadReport()
+        m.h = lib().glacier_hip_model_load_glrt(ctx.h, image.h, C.byref(m.report))
+        if not m.h:
+            raise GlrtError(INVALID_ARGUMENT, GLRT_ERRORS[m.report.error], "model_load_glrt")
+        return m
 
     def weight_bytes(self):
         return lib().glacier_hip_model_weight_bytes(self.h)

@@ -47,6 +47,9 @@ enum glacier_hip_status {
     GLACIER_HIP_INCOMPLETE_DRAIN = 17,   /* LaneWeave Error.IncompleteDrain */
     GLACIER_HIP_SCHEDULER_CLOSED = 18,   /* LaneWeave Error.SchedulerClosed */
     GLACIER_HIP_SCHEDULER_POISONED = 19, /* LaneWeave Error.InvariantViolation / BankDrift */
+    GLACIER_HIP_BAD_IMAGE = 20,          /* a prepared runtime image failed validation
+                                          * (the reason: glacier_hip_glrt_info_t.error) */
+    GLACIER_HIP_NOT_FOUND = 21,          /* no record with that key */
 };
 
 /* ---- element types / activation modes ------------------------------------ */
@@ -837,6 +840,129 @@ int glacier_hip_token_proposal_sha256(const glacier_hip_token_proposal_v1_t *pro
                                       uint8_t out[32]);
 int glacier_hip_token_commit_sha256(const uint8_t proposal_sha256[32],
                                     const glacier_hip_prepare_ack_v1_t *ack, uint8_t out[32]);
+
+/* ---- prepared runtime images (.glrt) -------------------------------------
+ * src/model/runtime_image.zig (MappedImage, :770-1049) and the prepared-model
+ * loader src/loader.zig:193-390 (loadPreparedWithOptions). An image is read
+ * through a read-only file mapping and validated fail-closed before anything
+ * is uploaded: header (magic, version, sizes, reserved bytes, CRC32), ABI
+ * fingerprint (this backend runs the portable row-major INT4 + f32-scale
+ * execution layout: GLRT v2 "row-major-f32-v2", v1 "row-major-f32-v1"),
+ * index CRC32, every record descriptor (encoding / layout / shape / stream
+ * bounds, 64-byte alignment, no overlap, no duplicates) and, by default,
+ * each record's payload CRC32 and (v2) descriptor+payload SHA-256. */
+typedef struct glacier_hip_glrt_image glacier_hip_glrt_image;
+
+/* Failure reasons, named after the reference's errors. */
+enum glacier_hip_glrt_error {
+    GLACIER_HIP_GLRT_OK = 0,
+    GLACIER_HIP_GLRT_TRUNCATED_HEADER = 1,
+    GLACIER_HIP_GLRT_BAD_MAGIC = 2,
+    GLACIER_HIP_GLRT_BAD_VERSION = 3,
+    GLACIER_HIP_GLRT_BAD_HEADER_SIZE = 4,
+    GLACIER_HIP_GLRT_BAD_RECORD_SIZE = 5,
+    GLACIER_HIP_GLRT_BAD_ALIGNMENT = 6,
+    GLACIER_HIP_GLRT_BAD_CONFIG = 7,
+    GLACIER_HIP_GLRT_BAD_RESERVED_FIELD = 8,
+    GLACIER_HIP_GLRT_HEADER_CRC_MISMATCH = 9,
+    GLACIER_HIP_GLRT_LEGACY_VERSION_DISABLED = 10,
+    GLACIER_HIP_GLRT_BAD_HEADER = 11,
+    GLACIER_HIP_GLRT_BAD_BOUNDS = 12,
+    GLACIER_HIP_GLRT_SOURCE_FINGERPRINT_MISMATCH = 13,
+    GLACIER_HIP_GLRT_ABI_FINGERPRINT_MISMATCH = 14,
+    GLACIER_HIP_GLRT_INDEX_CRC_MISMATCH = 15,
+    GLACIER_HIP_GLRT_TRUNCATED_INDEX = 16,
+    GLACIER_HIP_GLRT_BAD_TENSOR_KIND = 17,
+    GLACIER_HIP_GLRT_BAD_ENCODING = 18,
+    GLACIER_HIP_GLRT_BAD_PACKED_LAYOUT = 19,
+    GLACIER_HIP_GLRT_BAD_ROLE = 20,
+    GLACIER_HIP_GLRT_BAD_PAIR_NIBBLE_LAYOUT = 21,
+    GLACIER_HIP_GLRT_BAD_FLAGS = 22,
+    GLACIER_HIP_GLRT_BAD_VERSIONED_RECORD = 23,
+    GLACIER_HIP_GLRT_MISSING_DIGEST = 24,
+    GLACIER_HIP_GLRT_BAD_TENSOR_SHAPE = 25,
+    GLACIER_HIP_GLRT_MISSING_SCALES = 26,
+    GLACIER_HIP_GLRT_OVERLAPPING_PAYLOAD = 27,
+    GLACIER_HIP_GLRT_DUPLICATE_RECORD = 28,
+    GLACIER_HIP_GLRT_CRC_MISMATCH = 29,
+    GLACIER_HIP_GLRT_DIGEST_MISMATCH = 30,
+    GLACIER_HIP_GLRT_FILE_ERROR = 31,        /* open / stat / mmap failed */
+    /* loader (loader.zig LoaderError) */
+    GLACIER_HIP_GLRT_MISSING_TENSOR = 32,
+    GLACIER_HIP_GLRT_BAD_PAYLOAD = 33,
+    GLACIER_HIP_GLRT_NO_LAYERS = 34,
+    GLACIER_HIP_GLRT_UNSUPPORTED = 35,       /* valid, but not a shape this device runs */
+};
+
+typedef struct {
+    int32_t verify_payload_crc;      /* OpenOptions defaults: 1 */
+    int32_t verify_payload_digest;   /* 1 */
+    int32_t allow_v1;                /* 1 */
+    int32_t check_source_fingerprint;/* 0: any source */
+    uint8_t expected_source_fingerprint[32];
+} glacier_hip_glrt_open_options_t;
+
+typedef struct {
+    uint32_t error;                  /* glacier_hip_glrt_error of a failed open/load */
+    uint32_t version;                /* 1 or 2 */
+    uint64_t record_count, data_offset, file_size;
+    uint8_t source_fingerprint[32], abi_fingerprint[32];
+    uint32_t dim, hidden_dim, layers, vocab, heads, head_dim, kv_heads;
+    uint32_t tie_embeddings;
+    float rms_eps, rope_theta;
+} glacier_hip_glrt_info_t;
+
+/* One decoded record (Record, runtime_image.zig:300-323). Streams: 0 packed
+ * weights, 1 f32 scales, 2 f16 scales, 3 f16 rows4 scales, 4 raw f32. */
+typedef struct {
+    uint32_t layer_idx, kind;        /* kind: format.zig TensorKind */
+    uint16_t role, encoding, packed_layout, pair_nibble_layout;
+    uint32_t group_size, out_f, in_f, flags, payload_crc32, reserved;
+    uint64_t num_elements;
+    uint64_t offset[5], length[5];
+    uint8_t payload_digest[32];
+} glacier_hip_glrt_record_t;
+
+/* Opens and validates `path` (opts NULL = the defaults). On failure returns
+ * GLACIER_HIP_BAD_IMAGE with info->error set and *out NULL. Host only. */
+int glacier_hip_glrt_open(const char *path, const glacier_hip_glrt_open_options_t *opts,
+                          glacier_hip_glrt_image **out, glacier_hip_glrt_info_t *info);
+void glacier_hip_glrt_close(glacier_hip_glrt_image *image);
+int glacier_hip_glrt_record_at(const glacier_hip_glrt_image *image, uint64_t index,
+                               glacier_hip_glrt_record_t *out);
+/* findWithRole (:898-911): GLACIER_HIP_NOT_FOUND when absent. */
+int glacier_hip_glrt_find(const glacier_hip_glrt_image *image, uint32_t layer_idx, uint32_t kind,
+                          uint32_t role, glacier_hip_glrt_record_t *out);
+/* A view into the mapping (valid until close); empty streams give len 0. */
+int glacier_hip_glrt_stream(const glacier_hip_glrt_image *image,
+                            const glacier_hip_glrt_record_t *record, uint32_t stream,
+                            const void **data, uint64_t *len);
+/* identityV1 (:860-870): SHA-256 over every byte of the container. */
+int glacier_hip_glrt_identity(const glacier_hip_glrt_image *image, uint8_t container_sha256[32],
+                              uint64_t *container_bytes);
+
+/* Loader report: the loader-level failure reason (info.error codes), and
+ * how many INT4 scales were taken from f32 values that fp16 does not hold
+ * exactly (the device stores fp16 scales; an image with an f16 scale
+ * mirror is uploaded from the mirror). */
+typedef struct {
+    uint32_t error;
+    uint32_t separate_mlp;           /* 1: separate gate/up records (the only layout loaded) */
+    uint64_t int4_records, raw_records;
+    uint64_t inexact_scales;
+    uint64_t uploaded_bytes;         /* device bytes of the model */
+} glacier_hip_glrt_load_report_t;
+
+/* loadPreparedWithOptions (loader.zig:202-306) onto the device: validates
+ * the prepared record set (config, expected records only, required norms,
+ * separate gate/up per layer, optional q/k/v biases), dequantizes the INT4
+ * token embedding to f32 rows (dequantizeRow, int4_matmul.zig:3164-3194),
+ * uploads every projection into the device tile layout and the LM head (or
+ * the tied embedding matrix). Returns NULL on failure with report->error
+ * set (and the context's last_error). */
+glacier_hip_model *glacier_hip_model_load_glrt(glacier_hip_context *ctx,
+                                               const glacier_hip_glrt_image *image,
+                                               glacier_hip_glrt_load_report_t *report);
 
 /* ---- synthetic random-init generator (host, deterministic) ---------------
  * Counter-based SplitMix64 streams keyed by (seed, tensor id):
