@@ -16,7 +16,8 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "libglacier_hip.so")
 SOURCES = ["kernels.hip", "gemm.hip", "runtime.hip", "session.hip", "host_util.cpp",
-           "lane_weave.cpp", "paged_kv.cpp", "publication.cpp", "runtime_image.cpp"]
+           "lane_weave.cpp", "paged_kv.cpp", "publication.cpp", "runtime_image.cpp",
+           "page_image.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 

@@ -21,6 +21,7 @@
 #include "paged_kv.h"
 #include "publication.h"
 #include "runtime.h"
+#include "page_image.h"
 #include "runtime_image.h"
 
 using gh::hip_fail;
@@ -1684,6 +1685,219 @@ int glacier_hip_session_page_generation(glacier_hip_session *s, uint32_t lane,
   const Lane &ln = s->lanes[lane];
   if (logical_page >= ln.kv.page_gen.size()) return GLACIER_HIP_SHAPE_MISMATCH;
   *ownership_generation_out = ln.kv.page_gen[logical_page];
+  return GLACIER_HIP_OK;
+}
+
+
+// ---- checkpoint page images (continuation_paged_kv_restore.zig) ----------
+
+int glacier_hip_session_encode_page_image(glacier_hip_session *s, uint32_t lane,
+                                          uint32_t logical_page,
+                                          const uint8_t challenge_sha256[32], uint8_t *out,
+                                          uint64_t out_capacity, uint64_t *out_len,
+                                          glacier_hip_page_image_v1_t *info) {
+  if (!s) return GLACIER_HIP_INVALID_HANDLE;
+  if (!challenge_sha256 || !out || !out_len || lane >= s->lanes.size())
+    return GLACIER_HIP_INVALID_ARGUMENT;
+  GH_SUBMISSION(s->model->ctx);
+  const auto &c = s->model->cfg;
+  const Lane &ln = s->lanes[lane];
+  glacier_hip_page_image_v1_t tmp{};
+  glacier_hip_page_image_v1_t &hd = info ? *info : tmp;
+  memset(&hd, 0, sizeof hd);
+  auto reject = [&](uint32_t e) {
+    hd.error = e;
+    return GLACIER_HIP_INVALID_CHECKPOINT;
+  };
+  // encodePageImageV1 (:174-261): a committed page of the current root
+  bool zero = true;
+  for (int i = 0; i < 32; ++i) zero = zero && challenge_sha256[i] == 0;
+  if (zero || !ln.kv.active) return reject(GLACIER_HIP_PAGE_IMAGE_INVALID_PAGE_IMAGE);
+  const gpk::Root root = ln.kv.root;
+  if (logical_page >= root.committed_pages) return reject(GLACIER_HIP_PAGE_IMAGE_INVALID_PAGE_IMAGE);
+  const uint64_t start = (uint64_t)logical_page * 16;
+  if (start >= root.committed_len) return reject(GLACIER_HIP_PAGE_IMAGE_INVALID_PAGE_IMAGE);
+  const uint64_t rows = std::min<uint64_t>(16, root.committed_len - start);
+  const uint64_t L = c.num_layers, kvd = (uint64_t)c.num_kv_heads * c.head_dim;
+  const uint64_t need = gpi::encoded_bytes(L, kvd, rows);
+  if (!need) return reject(GLACIER_HIP_PAGE_IMAGE_INVALID_PAGE_IMAGE);
+  if (out_capacity < need) return reject(GLACIER_HIP_PAGE_IMAGE_CAPACITY_EXCEEDED);
+  const int32_t phys = ln.kv.page_of[logical_page];
+  if (phys < 0 || ln.kv.page_gen[logical_page] == 0)
+    return reject(GLACIER_HIP_PAGE_IMAGE_INVALID_PAGE_IMAGE);
+  // read the page back, then lay its committed rows out canonically:
+  // (layer, K then V, row, dim) little-endian f32; fp16 widens exactly
+  const size_t elem = s->opt.kv_dtype == GLACIER_HIP_F16 ? 2 : 4;
+  const size_t page_elems = L * 2 * 16 * kvd;
+  std::vector<uint8_t> raw(page_elems * elem);
+  glacier_hip_context *ctx = s->model->ctx;
+  GH_CHECK(ctx, hipMemcpy(raw.data(), (char *)s->kv_pool + (size_t)phys * page_elems * elem,
+                          page_elems * elem, hipMemcpyDeviceToHost));
+  std::vector<uint8_t> canon(L * 2 * rows * kvd * 4);
+  size_t w = 0;
+  for (uint64_t l = 0; l < L; ++l)
+    for (int v = 0; v < 2; ++v)
+      for (uint64_t r = 0; r < rows; ++r) {
+        const uint8_t *src = raw.data() + (((l * 2 + v) * 16 + r) * kvd) * elem;
+        for (uint64_t i = 0; i < kvd; ++i, w += 4) {
+          float f;
+          if (elem == 4) {
+            memcpy(&f, src + 4 * i, 4);
+          } else {
+            uint16_t hv;
+            memcpy(&hv, src + 2 * i, 2);
+            f = gh::f16_to_f32(hv);
+          }
+          uint32_t b;
+          memcpy(&b, &f, 4);
+          for (int k = 0; k < 4; ++k) canon[w + k] = (uint8_t)(b >> (8 * k));
+        }
+      }
+  glacier_hip_page_ref_t ref{gpk::kPageRefAbi, ln.kv.instance, logical_page,
+                             ln.kv.page_gen[logical_page]};
+  const uint32_t e = gpi::encode(root, L, kvd, ln.kv.max_seq, ref, rows, canon.data(),
+                                 canon.size(), challenge_sha256, out, out_capacity, out_len);
+  if (e) return reject(e);
+  gpi::decode(out, *out_len, challenge_sha256, &hd);
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_session_restore_checkpoint(glacier_hip_session *s, uint32_t lane,
+                                           const uint8_t *const *images,
+                                           const uint64_t *image_lens, uint32_t count,
+                                           const uint8_t challenge_sha256[32], uint64_t seed,
+                                           glacier_hip_checkpoint_restore_v1_t *out,
+                                           glacier_hip_page_ref_t *target_refs) {
+  if (!s) return GLACIER_HIP_INVALID_HANDLE;
+  if (!images || !image_lens || !challenge_sha256 || !out || lane >= s->lanes.size() ||
+      count == 0)
+    return GLACIER_HIP_INVALID_ARGUMENT;
+  for (uint32_t i = 0; i < count; ++i)
+    if (!images[i]) return GLACIER_HIP_INVALID_ARGUMENT;
+  GH_SUBMISSION(s->model->ctx);
+  if (s->prep.active) return GLACIER_HIP_TRANSACTION_ACTIVE;
+  memset(out, 0, sizeof *out);
+  out->abi_version = gpi::kCheckpointRestoreAbi;
+  const auto &c = s->model->cfg;
+  const uint64_t L = c.num_layers, kvd = (uint64_t)c.num_kv_heads * c.head_dim;
+  Lane &ln = s->lanes[lane];
+  // the restore target is a fresh request (PagedKVCache.initForCheckpoint)
+  reset_lane(s, ln, seed);
+  auto reject = [&](uint32_t e) {
+    out->error = e;
+    return GLACIER_HIP_INVALID_CHECKPOINT;
+  };
+  // ---- decode every image (restoreAndCommitV1's loop, :405-447) ----
+  std::vector<glacier_hip_page_image_v1_t> hd(count);
+  for (uint32_t i = 0; i < count; ++i) {
+    const uint32_t e = gpi::decode(images[i], image_lens[i], challenge_sha256, &hd[i]);
+    if (e) return reject(e);
+    if (hd[i].source_ref.logical_page != i) return reject(GLACIER_HIP_PAGE_IMAGE_INVALID_RESTORE_PLAN);
+    if (i > 0 && (memcmp(&hd[i].source_root, &hd[0].source_root, sizeof hd[0].source_root) != 0 ||
+                  hd[i].num_layers != hd[0].num_layers || hd[i].dim != hd[0].dim ||
+                  hd[i].max_seq != hd[0].max_seq))
+      return reject(GLACIER_HIP_PAGE_IMAGE_FOREIGN_CHECKPOINT);
+  }
+  const glacier_hip_page_map_root_t src = hd[0].source_root;
+  out->source_root = src;
+  // ---- restoreCheckpointV1 validation (paged_kv_cache.zig:614-684) ----
+  if (hd[0].num_layers != L || hd[0].dim != kvd || hd[0].max_seq != ln.kv.max_seq)
+    return reject(GLACIER_HIP_PAGE_IMAGE_INVALID_CHECKPOINT);
+  if (ln.kv.instance == src.cache_instance) {  // initForCheckpoint: a different instance
+    ln.kv.instance = gpk::next_cache_instance();
+    ln.kv.root.cache_instance = ln.kv.instance;
+    gpk::empty_ownership_digest(ln.kv.instance, L, kvd, ln.kv.max_seq, ln.kv.root.ownership_sha256);
+  }
+  if (src.committed_len > ln.kv.max_seq || src.committed_pages > ln.kv.page_of.size() ||
+      src.committed_pages != count)
+    return reject(GLACIER_HIP_PAGE_IMAGE_INVALID_CHECKPOINT);
+  uint8_t own[32];
+  gpk::empty_ownership_digest(src.cache_instance, L, kvd, ln.kv.max_seq, own);
+  for (uint32_t i = 0; i < count; ++i) {
+    const glacier_hip_page_ref_t &f = hd[i].source_ref;
+    const uint64_t rows = std::min<uint64_t>(16, src.committed_len - (uint64_t)i * 16);
+    if (f.cache_instance != src.cache_instance || f.ownership_generation == 0 ||
+        hd[i].committed_rows != rows)
+      return reject(GLACIER_HIP_PAGE_IMAGE_INVALID_CHECKPOINT);
+    gpk::append_ownership_digest(own, f.cache_instance, f.logical_page, f.ownership_generation, own);
+  }
+  if (memcmp(own, src.ownership_sha256, 32) != 0)
+    return reject(GLACIER_HIP_PAGE_IMAGE_INVALID_CHECKPOINT);
+  // ---- build the device pages (an fp16 pool takes only exact values) ----
+  const bool f16 = s->opt.kv_dtype == GLACIER_HIP_F16;
+  const size_t elem = f16 ? 2 : 4;
+  const size_t page_elems = L * 2 * 16 * kvd;
+  std::vector<uint8_t> pages((size_t)count * page_elems * elem, 0);
+  for (uint32_t i = 0; i < count; ++i) {
+    const uint8_t *rd = images[i] + hd[i].payload_offset;
+    uint8_t *dst = pages.data() + (size_t)i * page_elems * elem;
+    for (uint64_t l = 0; l < L; ++l)
+      for (int v = 0; v < 2; ++v)
+        for (uint64_t r = 0; r < hd[i].committed_rows; ++r)
+          for (uint64_t k = 0; k < kvd; ++k, rd += 4) {
+            const uint32_t b = (uint32_t)rd[0] | ((uint32_t)rd[1] << 8) | ((uint32_t)rd[2] << 16) |
+                               ((uint32_t)rd[3] << 24);
+            const size_t at = ((l * 2 + v) * 16 + r) * kvd + k;
+            if (!f16) {
+              memcpy(dst + 4 * at, &b, 4);
+            } else {
+              float f;
+              memcpy(&f, &b, 4);
+              const uint16_t hv = gh::f32_to_f16(f);
+              const float back = gh::f16_to_f32(hv);
+              if (memcmp(&back, &f, 4) != 0 && !(back != back && f != f))
+                return reject(GLACIER_HIP_PAGE_IMAGE_INVALID_CHECKPOINT);
+              memcpy(dst + 2 * at, &hv, 2);
+            }
+          }
+  }
+  if (s->pool.free.size() < count) return GLACIER_HIP_CACHE_FULL;
+  // ---- install: pool pages, HBM rows, page table, page map ----
+  glacier_hip_context *ctx = s->model->ctx;
+  std::vector<int32_t> phys(count);
+  for (uint32_t i = 0; i < count; ++i) {
+    phys[i] = s->pool.free.back();
+    s->pool.free.pop_back();
+  }
+  auto undo = [&]() {
+    for (uint32_t i = 0; i < count; ++i) s->pool.free.push_back(phys[count - 1 - i]);
+  };
+  for (uint32_t i = 0; i < count; ++i) {
+    if (hipMemcpy((char *)s->kv_pool + (size_t)phys[i] * page_elems * elem,
+                  pages.data() + (size_t)i * page_elems * elem, page_elems * elem,
+                  hipMemcpyHostToDevice) != hipSuccess) {
+      undo();
+      ctx->last_error = "restore: page upload failed";
+      return GLACIER_HIP_DEVICE_ERROR;
+    }
+    s->pt_host[(size_t)lane * s->max_pages + i] = phys[i];
+  }
+  if (hipMemcpy(s->page_table + (size_t)lane * s->max_pages, s->pt_host + (size_t)lane * s->max_pages,
+                (size_t)count * 4, hipMemcpyHostToDevice) != hipSuccess) {
+    undo();
+    ctx->last_error = "restore: page table upload failed";
+    return GLACIER_HIP_DEVICE_ERROR;
+  }
+  uint8_t tgt[32];
+  memcpy(tgt, ln.kv.root.ownership_sha256, 32);
+  for (uint32_t i = 0; i < count; ++i) {
+    ln.kv.page_of[i] = phys[i];
+    ln.kv.page_gen[i] = (uint64_t)i + 1;
+    gpk::append_ownership_digest(tgt, ln.kv.instance, i, (uint64_t)i + 1, tgt);
+    if (target_refs) target_refs[i] = {gpk::kPageRefAbi, ln.kv.instance, i, (uint64_t)i + 1};
+  }
+  ln.kv.len = src.committed_len;
+  ln.kv.next_page_generation = (uint64_t)count + 1;
+  ln.kv.root.cache_instance = ln.kv.instance;
+  ln.kv.root.generation = 2;
+  ln.kv.root.committed_len = src.committed_len;
+  ln.kv.root.committed_pages = src.committed_pages;
+  memcpy(ln.kv.root.ownership_sha256, tgt, 32);
+  ln.kv.next_root_generation = 3;
+  ln.prompt_len = src.committed_len;
+  out->target_root = ln.kv.root;
+  out->restored_pages = count;
+  out->restored_payload_bytes = (uint64_t)count * L * 2 * 16 * kvd * 4;
   return GLACIER_HIP_OK;
 }
 

@@ -29,6 +29,7 @@ BUSY = 13
 UNSUPPORTED = 14
 BAD_IMAGE = 20
 NOT_FOUND = 21
+INVALID_CHECKPOINT = 22
 
 F32, F16, BF16 = 0, 1, 2
 ACT_Q8, ACT_F32, ACT_AUTO = 0, 1, 2
@@ -305,6 +306,28 @@ class GlrtLoadReport(C.Structure):
                 ("uploaded_bytes", C.c_uint64)]
 
 
+class PageImageInfo(C.Structure):
+    _fields_ = [("error", C.c_uint32), ("reserved", C.c_uint32), ("source_root", PageMapRoot),
+                ("num_layers", C.c_uint64), ("dim", C.c_uint64), ("max_seq", C.c_uint64),
+                ("source_ref", PageRef), ("committed_rows", C.c_uint64),
+                ("payload_element_count", C.c_uint64), ("payload_offset", C.c_uint64),
+                ("challenge_sha256", C.c_uint8 * 32), ("image_sha256", C.c_uint8 * 32)]
+
+
+class CheckpointRestore(C.Structure):
+    _fields_ = [("abi_version", C.c_uint64), ("source_root", PageMapRoot),
+                ("target_root", PageMapRoot), ("restored_pages", C.c_uint64),
+                ("restored_payload_bytes", C.c_uint64), ("error", C.c_uint32),
+                ("reserved", C.c_uint32)]
+
+
+# glacier_hip_page_image_error, by the reference's error names
+PAGE_IMAGE_ERRORS = ["Ok", "InvalidLength", "InvalidMagic", "InvalidAbi", "InvalidFlags",
+                     "InvalidPageImage", "CapacityExceeded", "UnsafeDestination",
+                     "ForeignCheckpoint", "InvalidCheckpoint", "InvalidRestorePlan",
+                     "ArithmeticOverflow"]
+
+
 # glacier_hip_glrt_error, by the reference's error names
 GLRT_ERRORS = ["Ok", "TruncatedHeader", "BadMagic", "BadVersion", "BadHeaderSize", "BadRecordSize",
                "BadAlignment", "BadConfig", "BadReservedField", "HeaderCrcMismatch",
@@ -448,6 +471,17 @@ _SIGS = [
     ("glacier_hip_lane_weave_state_sha256", C.c_int, [_P, _P]),
     ("glacier_hip_session_lane_weave_wave", C.c_int,
      [_P, _P, _P, C.c_uint32, _P, _P, C.c_uint32, _P, _P, C.POINTER(C.c_uint32)]),
+    ("glacier_hip_page_image_bytes", C.c_uint64, [C.c_uint64, C.c_uint64, C.c_uint64]),
+    ("glacier_hip_page_image_encode_canonical", C.c_int,
+     [C.POINTER(PageMapRoot), C.c_uint64, C.c_uint64, C.c_uint64, C.POINTER(PageRef), C.c_uint64,
+      _P, C.c_uint64, _P, _P, C.c_uint64, C.POINTER(C.c_uint64), C.POINTER(PageImageInfo)]),
+    ("glacier_hip_page_image_decode", C.c_int, [_P, C.c_uint64, _P, C.POINTER(PageImageInfo)]),
+    ("glacier_hip_session_encode_page_image", C.c_int,
+     [_P, C.c_uint32, C.c_uint32, _P, _P, C.c_uint64, C.POINTER(C.c_uint64),
+      C.POINTER(PageImageInfo)]),
+    ("glacier_hip_session_restore_checkpoint", C.c_int,
+     [_P, C.c_uint32, C.POINTER(C.c_char_p), C.POINTER(C.c_uint64), C.c_uint32, _P, C.c_uint64,
+      C.POINTER(CheckpointRestore), C.POINTER(PageRef)]),
     ("glacier_hip_glrt_open", C.c_int,
      [C.c_char_p, C.POINTER(GlrtOpenOptions), C.POINTER(_P), C.POINTER(GlrtInfo)]),
     ("glacier_hip_glrt_close", None, [_P]),
@@ -575,6 +609,40 @@ def random_model_host(cfg, seed):
         lm_head=synth_int4(seed, tensor_id(G, 22), V * D // 2),
         lm_head_scales=f16(synth_scales_f16(seed, tensor_id(G, 23), V * D // 32)),
     )
+
+
+class PageImageError(GlacierHipError):
+    """A rejected page image or checkpoint restore; .reason is the
+    reference's error name."""
+
+    def __init__(self, code, reason, what):
+        super().__init__(code, f"{what}: {reason}")
+        self.reason = reason
+
+
+def page_image_decode(image, challenge):
+    """glacier_hip_page_image_decode -> PageImageInfo (PageImageError on rejection)."""
+    info = PageImageInfo()
+    buf = C.create_string_buffer(bytes(image), len(image))
+    rc = lib().glacier_hip_page_image_decode(buf, len(image), bytes(challenge), C.byref(info))
+    if rc != OK:
+        raise PageImageError(rc, PAGE_IMAGE_ERRORS[info.error], "page_image_decode")
+    return info
+
+
+def page_image_encode_canonical(source_root, num_layers, dim, max_seq, source_ref, committed_rows,
+                                payload, challenge):
+    need = lib().glacier_hip_page_image_bytes(num_layers, dim, committed_rows) or 256
+    out = C.create_string_buffer(need)
+    n = C.c_uint64()
+    info = PageImageInfo()
+    buf = C.create_string_buffer(bytes(payload), len(payload))
+    rc = lib().glacier_hip_page_image_encode_canonical(
+        C.byref(source_root), num_layers, dim, max_seq, C.byref(source_ref), committed_rows, buf,
+        len(payload), bytes(challenge), out, need, C.byref(n), C.byref(info))
+    if rc != OK:
+        raise PageImageError(rc, PAGE_IMAGE_ERRORS[info.error], "page_image_encode_canonical")
+    return out.raw[:n.value]
 
 
 class GlrtError(GlacierHipError):
@@ -833,6 +901,37 @@ class Session:
 
     def inject_failure(self, enable):
         check(lib().glacier_hip_session_inject_failure(self.h, 1 if enable else 0), "inject")
+
+    def encode_page_image(self, lane, logical_page, challenge):
+        """glacier_hip_session_encode_page_image -> (image bytes, PageImageInfo)."""
+        cfg = self.model.cfg
+        need = lib().glacier_hip_page_image_bytes(cfg["num_layers"],
+                                                  cfg["num_kv_heads"] * cfg["head_dim"], 16)
+        out = C.create_string_buffer(need)
+        n = C.c_uint64()
+        info = PageImageInfo()
+        rc = lib().glacier_hip_session_encode_page_image(self.h, lane, logical_page, bytes(challenge),
+                                                         out, need, C.byref(n), C.byref(info))
+        if rc != OK:
+            if rc == INVALID_CHECKPOINT:
+                raise PageImageError(rc, PAGE_IMAGE_ERRORS[info.error], "encode_page_image")
+            check(rc, "encode_page_image", self.model.ctx.h)
+        return out.raw[:n.value], info
+
+    def restore_checkpoint(self, lane, images, challenge, seed=0):
+        """glacier_hip_session_restore_checkpoint -> (CheckpointRestore, target refs)."""
+        n = len(images)
+        arr = (C.c_char_p * n)(*[bytes(i) for i in images])
+        lens = (C.c_uint64 * n)(*[len(i) for i in images])
+        out = CheckpointRestore()
+        refs = (PageRef * max(n, 1))()
+        rc = lib().glacier_hip_session_restore_checkpoint(self.h, lane, arr, lens, n,
+                                                          bytes(challenge), seed, C.byref(out), refs)
+        if rc != OK:
+            if rc == INVALID_CHECKPOINT:
+                raise PageImageError(rc, PAGE_IMAGE_ERRORS[out.error], "restore_checkpoint")
+            check(rc, "restore_checkpoint", self.model.ctx.h)
+        return out, [refs[i] for i in range(n)]
 
     def close(self):
         if self.h:

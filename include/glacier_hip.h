@@ -50,6 +50,8 @@ enum glacier_hip_status {
     GLACIER_HIP_BAD_IMAGE = 20,          /* a prepared runtime image failed validation
                                           * (the reason: glacier_hip_glrt_info_t.error) */
     GLACIER_HIP_NOT_FOUND = 21,          /* no record with that key */
+    GLACIER_HIP_INVALID_CHECKPOINT = 22, /* a page image or checkpoint restore was rejected
+                                          * (the reason: glacier_hip_page_image_v1_t.error) */
 };
 
 /* ---- element types / activation modes ------------------------------------ */
@@ -840,6 +842,95 @@ int glacier_hip_token_proposal_sha256(const glacier_hip_token_proposal_v1_t *pro
                                       uint8_t out[32]);
 int glacier_hip_token_commit_sha256(const uint8_t proposal_sha256[32],
                                     const glacier_hip_prepare_ack_v1_t *ack, uint8_t out[32]);
+
+/* ---- paged-KV checkpoint page images ------------------------------------
+ * src/continuation_paged_kv_restore.zig (PageImageV1, :18-360) and
+ * PagedKVCache.restoreCheckpointV1 (paged_kv_cache.zig:570-762). A page
+ * image is one committed page of a lane in the portable layout: a 208-byte
+ * header (magic "GCKVPG01", ABI 0x4743_4b50_0000_0001, length, flags, the
+ * source PageMapRootV1, num_layers, kv dim, max_seq, the page's PageRefV1,
+ * committed rows, element count, challenge), the committed rows as
+ * little-endian f32 in (layer, K/V, row, dim) order, and SHA-256 of
+ * "glacier-continuation-paged-kv-page-image-v1\0" ++ everything before it.
+ * The device pages are read back (fp16 pages widen to f32 exactly) or
+ * written (restore) by these entry points; the host keeps the bytes. */
+enum glacier_hip_page_image_error {
+    GLACIER_HIP_PAGE_IMAGE_OK = 0,
+    GLACIER_HIP_PAGE_IMAGE_INVALID_LENGTH = 1,
+    GLACIER_HIP_PAGE_IMAGE_INVALID_MAGIC = 2,
+    GLACIER_HIP_PAGE_IMAGE_INVALID_ABI = 3,
+    GLACIER_HIP_PAGE_IMAGE_INVALID_FLAGS = 4,
+    GLACIER_HIP_PAGE_IMAGE_INVALID_PAGE_IMAGE = 5,
+    GLACIER_HIP_PAGE_IMAGE_CAPACITY_EXCEEDED = 6,
+    GLACIER_HIP_PAGE_IMAGE_UNSAFE_DESTINATION = 7,
+    GLACIER_HIP_PAGE_IMAGE_FOREIGN_CHECKPOINT = 8,
+    GLACIER_HIP_PAGE_IMAGE_INVALID_CHECKPOINT = 9,
+    GLACIER_HIP_PAGE_IMAGE_INVALID_RESTORE_PLAN = 10,
+    GLACIER_HIP_PAGE_IMAGE_ARITHMETIC_OVERFLOW = 11,
+};
+
+typedef struct {
+    uint32_t error;                  /* glacier_hip_page_image_error of a failed call */
+    uint32_t reserved;
+    glacier_hip_page_map_root_t source_root;
+    uint64_t num_layers, dim, max_seq;
+    glacier_hip_page_ref_t source_ref;
+    uint64_t committed_rows, payload_element_count;
+    uint64_t payload_offset;         /* byte offset of the canonical f32 rows (208) */
+    uint8_t challenge_sha256[32];
+    uint8_t image_sha256[32];
+} glacier_hip_page_image_v1_t;
+
+typedef struct {
+    uint64_t abi_version;            /* 0x4750435200000001 (checkpoint_restore_abi) */
+    glacier_hip_page_map_root_t source_root;
+    glacier_hip_page_map_root_t target_root;
+    uint64_t restored_pages;
+    uint64_t restored_payload_bytes; /* f32 page payloads, as the reference counts them */
+    uint32_t error;                  /* glacier_hip_page_image_error of a failed restore */
+    uint32_t reserved;
+} glacier_hip_checkpoint_restore_v1_t;
+
+/* encodedPageImageBytesV1 (:68-97); 0 for an invalid geometry. */
+uint64_t glacier_hip_page_image_bytes(uint64_t num_layers, uint64_t dim, uint64_t committed_rows);
+/* encodeCanonicalPageImageV1 (:101-170) from caller-owned canonical bytes.
+ * info (may be NULL) receives the failure reason. Host only. */
+int glacier_hip_page_image_encode_canonical(const glacier_hip_page_map_root_t *source_root,
+                                            uint64_t num_layers, uint64_t dim, uint64_t max_seq,
+                                            const glacier_hip_page_ref_t *source_ref,
+                                            uint64_t committed_rows,
+                                            const uint8_t *canonical_f32_le, uint64_t canonical_len,
+                                            const uint8_t challenge_sha256[32], uint8_t *out,
+                                            uint64_t out_capacity, uint64_t *out_len,
+                                            glacier_hip_page_image_v1_t *info);
+/* decodePageImageV1 (:263-360). Host only. */
+int glacier_hip_page_image_decode(const uint8_t *image, uint64_t len,
+                                  const uint8_t expected_challenge_sha256[32],
+                                  glacier_hip_page_image_v1_t *out);
+/* encodePageImageV1 (:174-261) for one committed page of a session lane:
+ * the page is read back from HBM. info (may be NULL) receives the header. */
+int glacier_hip_session_encode_page_image(glacier_hip_session *session, uint32_t lane,
+                                          uint32_t logical_page,
+                                          const uint8_t challenge_sha256[32], uint8_t *out,
+                                          uint64_t out_capacity, uint64_t *out_len,
+                                          glacier_hip_page_image_v1_t *info);
+/* Restore a checkpoint into `lane`, which is begun afresh (lane_begin with
+ * `seed`; a cache instance different from the source's): every image is
+ * decoded against the challenge, must carry logical page = its index, the
+ * same source root and geometry (ForeignCheckpoint otherwise), the session's
+ * layer count, kv dim and max_positions (InvalidCheckpoint otherwise); the
+ * source ownership chain is verified; only then are pool pages taken and the
+ * rows written to HBM (zeros past the committed rows; an fp16 pool accepts
+ * only values fp16 holds exactly). The lane's page map then has target refs
+ * (this instance, page i, generation i + 1), root generation 2 and the next
+ * root generation 3 (restoreCheckpointV1). target_refs may be NULL. On
+ * failure the lane is left begun and empty. */
+int glacier_hip_session_restore_checkpoint(glacier_hip_session *session, uint32_t lane,
+                                           const uint8_t *const *images,
+                                           const uint64_t *image_lens, uint32_t count,
+                                           const uint8_t challenge_sha256[32], uint64_t seed,
+                                           glacier_hip_checkpoint_restore_v1_t *out,
+                                           glacier_hip_page_ref_t *target_refs);
 
 /* ---- prepared runtime images (.glrt) -------------------------------------
  * src/model/runtime_image.zig (MappedImage, :770-1049) and the prepared-model
