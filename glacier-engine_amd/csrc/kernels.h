@@ -210,6 +210,41 @@ hipError_t launch_attention_f16(const float *q, const void *kv_pool, const int32
                                 hipStream_t st, int wp, int nw,
                                 PlanesDst emit = PlanesDst{nullptr, nullptr, 1});
 
+// Batch-1 decode with fp16 KV: attention fused with the O projection.
+// Workgroup (row-block group bg, KV head h) computes the attention of the
+// G = Hq / Hkv query heads of KV head h over row 0's whole context, quantises
+// it (the O projection's Q8 planes of that K slice, in LDS) and writes
+// parts[h][n] = W_o[n, slice h] . attn[slice h] for its NW row blocks of 16
+// rows. With y set, the last of a group's Hkv workgroups to finish (a
+// counter per group) also writes the projection with its residual,
+// y[n] = resid[n] + ((parts[0][n] + parts[1][n]) + ...), and the group's
+// sum of y^2 to ss_out[bg] (the next RMSNorm's partial sums), then resets
+// its counter to 0.
+struct AttnOArgs {
+  const float *q;              // [Hq * head_dim] row 0's queries
+  const void *kv_pool;         // fp16 pages [page][L][2][16][kv_dim]
+  const int32_t *page_table;   // [lanes][max_pages]
+  int max_pages;
+  const int32_t *lane_of_row;  // [1]
+  const int32_t *ctx_len;      // [1]
+  int layer, num_layers, num_heads, num_kv_heads, head_dim, max_ctx;
+  const uint4 *codes;          // O weights, device tile layout, N x K (K = Hq * head_dim)
+  const uint2 *scales;
+  int N, K;
+  float *parts;                // [num_kv_heads][N]
+  const float *resid;          // [N]  (with y)
+  float *y;                    // [N]  null: parts only
+  float *ss_out;               // [attn_o_groups(N)]
+  unsigned *counters;          // [attn_o_groups(N)], 0 between launches
+};
+constexpr int kMaxAttnOHeads = 8;  // KV heads (partial vectors) at most
+// Whether launch_attn_o supports these shapes (head_dim 64 or 128, a K
+// slice per KV head of whole 128-column quads).
+bool attn_o_ok(const AttnOArgs &a);
+// Row-block groups of the fused launch (= ss_out partials, counters).
+int attn_o_groups(int N);
+hipError_t launch_attn_o(const AttnOArgs &a, hipStream_t st);
+
 // Causal prefill attention (fp16 KV) for one lane's chunk of T consecutive
 // positions pos0 .. pos0 + T - 1 whose K/V rows are already in the lane's
 // pages; q / out [T][Hq*hd] as launch_attention.

@@ -1344,30 +1344,214 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 // (forward.zig:515-528); otherwise every chunk writes a (max, sum, output)
 // record per query head for the combine kernel.
 // ---------------------------------------------------------------------------
+// LDS of one fp16 attention work item: every wave's (output, max, sum)
+// state and the log-sum-exp merge weights.
+template <int HD, int NW>
+struct AttnF16Lds {
+  float so[NW][kMaxGroup][HD];
+  float sm[NW][16], sl[NW][16];
+  float fw[NW][kMaxGroup], mg[kMaxGroup];
+};
+
+// One work item of fp16-KV attention: positions j0 .. j0 + n - 1 of one
+// row's context for KV head h (qrow = the row's q at its first query head
+// h * G, ptab = the row's page table at page j0 / 16). Every thread of the
+// NW-wave workgroup calls it; on return (after two barriers) each wave's
+// state is in s.so / s.sm / s.sl and the merge weights in s.fw / s.mg, so
+// the merged output of query head g, dim d is
+//   O = sum_w s.so[w][g][d] * s.fw[w][g],  L = sum_w s.sl[w][g] * s.fw[w][g],
+// with maximum s.mg[g] (waves added in order). The caller must pass a
+// barrier before the next call reuses s.
 template <int HD, int NT, int NW>
-__global__ __launch_bounds__(64 * NW) void attn_f16_kernel(
-    const float *q, const __half *pool, const int32_t *page_table, int max_pages,
-    const int32_t *lane_of_row, const int32_t *ctx_len, int M, int layer, int num_layers, int Hq,
-    int Hkv, int n_chunks_max, int max_ctx, float *scratch, float *out, PlanesDst pd) {
+static __device__ __forceinline__ void attn_f16_item(const float *qrow, const __half *pool,
+                                                     const int32_t *ptab, int n, int layer,
+                                                     size_t lay, int kv_dim, int h, int G,
+                                                     AttnF16Lds<HD, NW> &s) {
   typedef _Float16 h4 __attribute__((ext_vector_type(4)));
   typedef float f4 __attribute__((ext_vector_type(4)));
   constexpr int S = HD / 16;    // f16 MFMA steps over the head dim
   constexpr int DPL = HD / 16;  // dims per lane and V row = output blocks of P.V
   constexpr int WP = 16 * NT;   // positions per wave
-  constexpr int CH = NW * WP;   // positions per work item
   constexpr int NTH = 64 * NW;
   typedef typename std::conditional<DPL == 8, uint4, uint2>::type vrow_t;
   const int t = threadIdx.x, l = t & 63;
   const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
-  const int G = Hq / Hkv;
-  const int kv_dim = Hkv * HD;
-  const size_t lay = (size_t)num_layers;
-  __shared__ float so[NW][kMaxGroup][HD];
-  __shared__ float sm[NW][16], sl[NW][16];
-  __shared__ float fw[NW][kMaxGroup], mg[kMaxGroup];
   const float scale = 1.0f / sqrtf((float)HD);
   const int wbase = wv * WP;
   const int c = l >> 4, j = l & 15;
+  const int wn = max(0, min(WP, n - wbase));
+
+  f4 o[DPL];
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) o[e] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  float mx = -INFINITY, sum = 0.0f;
+  if (wn > 0) {
+    // q first (it depends on nothing the page walk reads), as the B operand:
+    // lane (c, j) holds head j's dims of k-chunk c
+    const float *qr = qrow + (size_t)(j < G ? j : 0) * HD;
+    float4 qv[S];
+#pragma unroll
+    for (int st = 0; st < S; ++st) {
+      const int base = 8 * (4 * (st >> 1) + c) + 4 * (st & 1);
+      qv[st] = j < G ? *(const float4 *)(qr + base) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    // page ids of this wave's pages (wave-uniform)
+    const int32_t *pt = ptab + wbase / 16;
+    int pg[NT];
+#pragma unroll
+    for (int T = 0; T < NT; ++T) pg[T] = 16 * T < wn ? pt[T] : 0;
+    // K: lane (c, j) loads 16-byte pieces 4 * tt + c of position j of each
+    // page; V: lane (c, j) loads dims DPL*j .. DPL*j + DPL-1 of positions
+    // 4c + r (r = 0..3) of each page
+    uint4 kr[NT][HD / 32];
+    vrow_t vr[NT][4];
+#pragma unroll
+    for (int T = 0; T < NT; ++T) {
+      const size_t pbase = ((size_t)pg[T] * lay + layer) * 2;
+      const bool kval = 16 * T + j < wn;
+      const __half *krow = pool + ((pbase + 0) * 16 + j) * kv_dim + (size_t)h * HD;
+#pragma unroll
+      for (int tt = 0; tt < HD / 32; ++tt)
+        kr[T][tt] = kval ? *(const uint4 *)(krow + 8 * (4 * tt + c)) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int pos = 4 * c + rr;
+        const __half *vrow = pool + ((pbase + 1) * 16 + pos) * kv_dim + (size_t)h * HD + DPL * j;
+        if (16 * T + pos < wn) vr[T][rr] = *(const vrow_t *)vrow;
+        else __builtin_memset(&vr[T][rr], 0, sizeof(vrow_t));
+      }
+    }
+    // q split into f16 hi + lo (after the K/V loads are in flight)
+    h4 qhi[S], qlo[S];
+#pragma unroll
+    for (int st = 0; st < S; ++st) {
+      const float qa[4] = {qv[st].x, qv[st].y, qv[st].z, qv[st].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const _Float16 hv = (_Float16)qa[e];
+        qhi[st][e] = hv;
+        qlo[st][e] = (_Float16)(qa[e] - (float)hv);
+      }
+    }
+    // scores: S^T = K . Q^T, one 16x16 tile per page
+    f4 sc[NT];
+#pragma unroll
+    for (int T = 0; T < NT; ++T) {
+      f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int st = 0; st < S; ++st) {
+        const uint4 w = kr[T][st >> 1];
+        const uint2 bw = (st & 1) ? make_uint2(w.z, w.w) : make_uint2(w.x, w.y);
+        h4 a;
+        __builtin_memcpy(&a, &bw, 8);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qhi[st], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qlo[st], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const float v = acc[rr] * scale;
+        sc[T][rr] = 16 * T + 4 * c + rr < wn ? v : -INFINITY;
+        mx = fmaxf(mx, sc[T][rr]);
+      }
+    }
+    mx = xor32_max(xor16_max(mx));
+#pragma unroll
+    for (int T = 0; T < NT; ++T)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const float p = expf(sc[T][rr] - mx);
+        sc[T][rr] = p;
+        sum += p;
+      }
+    sum = xor32_add(xor16_add(sum));
+    // P.V: A = P[head j][pos 4c .. 4c+3] (this lane's own registers, fp16
+    // hi + lo), B_e = V[pos 4c + r][dim DPL * j + e]
+#pragma unroll
+    for (int T = 0; T < NT; ++T) {
+      h4 phi, plo;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const _Float16 hv = (_Float16)sc[T][rr];
+        phi[rr] = hv;
+        plo[rr] = (_Float16)(sc[T][rr] - (float)hv);
+      }
+      const _Float16 *v0 = (const _Float16 *)&vr[T][0];
+      const _Float16 *v1 = (const _Float16 *)&vr[T][1];
+      const _Float16 *v2 = (const _Float16 *)&vr[T][2];
+      const _Float16 *v3 = (const _Float16 *)&vr[T][3];
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) {
+        const h4 bv = {v0[e], v1[e], v2[e], v3[e]};
+        o[e] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi, bv, o[e], 0, 0, 0);
+        o[e] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo, bv, o[e], 0, 0, 0);
+      }
+    }
+  }
+  // lane (c, j) holds O[head 4c + r][dim DPL * j + e]
+  if (c < 2) {
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) s.so[wv][4 * c + rr][DPL * j + e] = o[e][rr];
+  }
+  if (c == 0) {
+    s.sm[wv][j] = mx;
+    s.sl[wv][j] = sum;
+  }
+  __syncthreads();
+  // ---- merge the waves (log-sum-exp) ----
+  // The weight of wave w for head g, exp(m_w - M) (0 for a wave without
+  // positions), is computed once per (wave, head); every output is then two
+  // short dot products over the waves, in wave order.
+  for (int i = t; i < NW * G; i += NTH) {
+    const int w = i / G, g = i % G;
+    float Mx = -INFINITY;
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2)
+      if (s.sl[w2][g] > 0.0f) Mx = fmaxf(Mx, s.sm[w2][g]);
+    s.fw[w][g] = s.sl[w][g] > 0.0f ? expf(s.sm[w][g] - Mx) : 0.0f;
+    if (w == 0) s.mg[g] = Mx;
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// fp16-KV streaming attention. The work list is every (row, KV head, chunk
+// of CH = NW * NT * 16 positions) with each row's chunks counted from its own
+// context length, rows in order; workgroup b takes items b, b + grid, ...,
+// so no chunk past a row's context is ever launched for it. A wave owns NT
+// pages of its chunk (16 positions each): it reads their page ids once
+// (wave-uniform scalar loads), issues every K and V load of them together
+// and keeps the softmax in registers:
+//   scores  S^T[pos][head] = K . Q^T on v_mfma_f32_16x16x16f16, q split into
+//           fp16 hi + lo so every product is exact in f32; lane (c, j) ends
+//           with head j's scores of positions 4c + r (r = 0..3) of a page,
+//   softmax max / exp / sum per head over the wave's positions (in-lane, then
+//           two cross-row shuffles),
+//   P.V     on v_mfma_f32_16x16x16f16 as well: the A operand is P[head j]
+//           [positions 4c .. 4c+3], which is exactly what lane (c, j) holds,
+//           split into fp16 hi + lo (V is exact in fp16, so the products
+//           are exact in f32); lane (c, j) supplies V[4c + r][DPL * j + e]
+//           for output block e from the DPL consecutive dims it read of each
+//           of its four V rows (one 16-byte load per row at hd 128), so V is
+//           read row-major and fully coalesced.
+// The waves' (max, sum, output) states merge by log-sum-exp in LDS. A row
+// whose context is one chunk writes its output normalised once by the sum
+// (forward.zig:515-528); otherwise every chunk writes a (max, sum, output)
+// record per query head for the combine kernel.
+// ---------------------------------------------------------------------------
+template <int HD, int NT, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_f16_kernel(
+    const float *q, const __half *pool, const int32_t *page_table, int max_pages,
+    const int32_t *lane_of_row, const int32_t *ctx_len, int M, int layer, int num_layers, int Hq,
+    int Hkv, int n_chunks_max, int max_ctx, float *scratch, float *out, PlanesDst pd) {
+  constexpr int WP = 16 * NT;   // positions per wave
+  constexpr int CH = NW * WP;   // positions per work item
+  constexpr int NTH = 64 * NW;
+  const int t = threadIdx.x, l = t & 63;
+  const int G = Hq / Hkv;
+  const int kv_dim = Hkv * HD;
+  __shared__ AttnF16Lds<HD, NW> s;
 
   // the work list (every wave holds it; lane r describes row r, M <= 64)
   const int cl = l < M ? min(ctx_len[l], max_ctx) : 0;
@@ -1393,141 +1577,9 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(
     const int h = r / nch, ch = r - h * nch;
     const int qh0 = h * G;
     const int j0 = ch * CH;
-    const int n = min(CH, ctx - j0);
-    const int wn = max(0, min(WP, n - wbase));
-
-    f4 o[DPL];
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) o[e] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-    float mx = -INFINITY, sum = 0.0f;
-    if (wn > 0) {
-      // q first (it depends on nothing the page walk reads), as the B operand:
-      // lane (c, j) holds head j's dims of k-chunk c
-      const float *qrow = q + ((size_t)m * Hq + qh0 + (j < G ? j : 0)) * HD;
-      float4 qv[S];
-#pragma unroll
-      for (int st = 0; st < S; ++st) {
-        const int base = 8 * (4 * (st >> 1) + c) + 4 * (st & 1);
-        qv[st] = j < G ? *(const float4 *)(qrow + base) : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-      // page ids of this wave's pages (wave-uniform)
-      const int32_t *ptab = page_table + (size_t)lane * max_pages + (j0 + wbase) / 16;
-      int pg[NT];
-#pragma unroll
-      for (int T = 0; T < NT; ++T) pg[T] = 16 * T < wn ? ptab[T] : 0;
-      // K: lane (c, j) loads 16-byte pieces 4 * tt + c of position j of each
-      // page; V: lane (c, j) loads dims DPL*j .. DPL*j + DPL-1 of positions
-      // 4c + r (r = 0..3) of each page
-      uint4 kr[NT][HD / 32];
-      vrow_t vr[NT][4];
-#pragma unroll
-      for (int T = 0; T < NT; ++T) {
-        const size_t pbase = ((size_t)pg[T] * lay + layer) * 2;
-        const bool kval = 16 * T + j < wn;
-        const __half *krow = pool + ((pbase + 0) * 16 + j) * kv_dim + (size_t)h * HD;
-#pragma unroll
-        for (int tt = 0; tt < HD / 32; ++tt)
-          kr[T][tt] = kval ? *(const uint4 *)(krow + 8 * (4 * tt + c)) : make_uint4(0, 0, 0, 0);
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int pos = 4 * c + rr;
-          const __half *vrow = pool + ((pbase + 1) * 16 + pos) * kv_dim + (size_t)h * HD + DPL * j;
-          if (16 * T + pos < wn) vr[T][rr] = *(const vrow_t *)vrow;
-          else __builtin_memset(&vr[T][rr], 0, sizeof(vrow_t));
-        }
-      }
-      // q split into f16 hi + lo (after the K/V loads are in flight)
-      h4 qhi[S], qlo[S];
-#pragma unroll
-      for (int st = 0; st < S; ++st) {
-        const float qa[4] = {qv[st].x, qv[st].y, qv[st].z, qv[st].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const _Float16 hv = (_Float16)qa[e];
-          qhi[st][e] = hv;
-          qlo[st][e] = (_Float16)(qa[e] - (float)hv);
-        }
-      }
-      // scores: S^T = K . Q^T, one 16x16 tile per page
-      f4 sc[NT];
-#pragma unroll
-      for (int T = 0; T < NT; ++T) {
-        f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int st = 0; st < S; ++st) {
-          const uint4 w = kr[T][st >> 1];
-          const uint2 bw = (st & 1) ? make_uint2(w.z, w.w) : make_uint2(w.x, w.y);
-          h4 a;
-          __builtin_memcpy(&a, &bw, 8);
-          acc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qhi[st], acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qlo[st], acc, 0, 0, 0);
-        }
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const float v = acc[rr] * scale;
-          sc[T][rr] = 16 * T + 4 * c + rr < wn ? v : -INFINITY;
-          mx = fmaxf(mx, sc[T][rr]);
-        }
-      }
-      mx = xor32_max(xor16_max(mx));
-#pragma unroll
-      for (int T = 0; T < NT; ++T)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const float p = expf(sc[T][rr] - mx);
-          sc[T][rr] = p;
-          sum += p;
-        }
-      sum = xor32_add(xor16_add(sum));
-      // P.V: A = P[head j][pos 4c .. 4c+3] (this lane's own registers, fp16
-      // hi + lo), B_e = V[pos 4c + r][dim DPL * j + e]
-#pragma unroll
-      for (int T = 0; T < NT; ++T) {
-        h4 phi, plo;
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const _Float16 hv = (_Float16)sc[T][rr];
-          phi[rr] = hv;
-          plo[rr] = (_Float16)(sc[T][rr] - (float)hv);
-        }
-        const _Float16 *v0 = (const _Float16 *)&vr[T][0];
-        const _Float16 *v1 = (const _Float16 *)&vr[T][1];
-        const _Float16 *v2 = (const _Float16 *)&vr[T][2];
-        const _Float16 *v3 = (const _Float16 *)&vr[T][3];
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) {
-          const h4 bv = {v0[e], v1[e], v2[e], v3[e]};
-          o[e] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi, bv, o[e], 0, 0, 0);
-          o[e] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo, bv, o[e], 0, 0, 0);
-        }
-      }
-    }
-    // lane (c, j) holds O[head 4c + r][dim DPL * j + e]
-    if (c < 2) {
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) so[wv][4 * c + rr][DPL * j + e] = o[e][rr];
-    }
-    if (c == 0) {
-      sm[wv][j] = mx;
-      sl[wv][j] = sum;
-    }
-    __syncthreads();
-    // ---- merge the waves (log-sum-exp) ----
-    // The weight of wave w for head g, exp(m_w - M) (0 for a wave without
-    // positions), is computed once per (wave, head); every output is then two
-    // short dot products over the waves, in wave order.
-    for (int i = t; i < NW * G; i += NTH) {
-      const int w = i / G, g = i % G;
-      float Mx = -INFINITY;
-#pragma unroll
-      for (int w2 = 0; w2 < NW; ++w2)
-        if (sl[w2][g] > 0.0f) Mx = fmaxf(Mx, sm[w2][g]);
-      fw[w][g] = sl[w][g] > 0.0f ? expf(sm[w][g] - Mx) : 0.0f;
-      if (w == 0) mg[g] = Mx;
-    }
-    __syncthreads();
+    attn_f16_item<HD, NT, NW>(q + ((size_t)m * Hq + qh0) * HD, pool,
+                              page_table + (size_t)lane * max_pages + j0 / 16, min(CH, ctx - j0),
+                              layer, (size_t)num_layers, kv_dim, h, G, s);
     constexpr int RS = 2 + HD;  // floats per record
     const size_t hstride = (size_t)n_chunks_max * RS;
     float *rbase = scratch + ((size_t)m * Hq + qh0) * hstride;
@@ -1536,9 +1588,9 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(
       float L = 0.0f, O = 0.0f;
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
-        const float f = fw[w][g];
-        L = fmaf(sl[w][g], f, L);
-        O = fmaf(so[w][g][d], f, O);
+        const float f = s.fw[w][g];
+        L = fmaf(s.sl[w][g], f, L);
+        O = fmaf(s.so[w][g][d], f, O);
       }
       if (nch == 1) {
         const float v = O * (1.0f / L);
@@ -1547,13 +1599,188 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(
       } else {
         float *rec = rbase + g * hstride + (size_t)ch * RS;
         if (d == 0) {
-          rec[0] = mg[g];
+          rec[0] = s.mg[g];
           rec[1] = L;
         }
         rec[2 + d] = O;
       }
     }
     __syncthreads();  // LDS is reused by the next item
+  }
+}
+
+// Batch-1 decode: the attention of KV head h fused with h's K slice of the
+// O projection (AttnOArgs). Workgroup (bg, h) first requests its wave's O
+// weights (row block bg * NW + wave, the KQS quads of slice h) and its rows'
+// residuals, then runs the attention items of row 0's context for KV head h
+// (CH positions each; more than one merge in registers by log-sum-exp),
+// quantises the G * hd outputs into Q8 planes in LDS exactly as the O
+// projection's input planes are quantised (int4_matmul.zig:380-398), and
+// each wave forms its row block's partial dot over the slice with the
+// GEMV's group arithmetic ((f32(T - corr) * w_scale) * a_scale, groups in
+// order). With a.y set, the group's Hkv workgroups meet at a counter: each
+// publishes its partial vector (agent-scope stores, completed before a
+// barrier, then the counter increment) and the last to arrive reads the
+// Hkv vectors with agent-scope loads and adds them in head order, whatever
+// the arrival order, so the result is reproducible.
+// With the round-robin placement of workgroups on the 8 XCDs, blockIdx % Hkv
+// = h puts every workgroup of one KV head on the same 8 / Hkv XCDs, whose L2s
+// then serve its K/V rows after the first read.
+template <int HD, int NT, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_o_kernel(AttnOArgs a) {
+  constexpr int WP = 16 * NT, CH = NW * WP, NTH = 64 * NW, RG = 16 * NW;
+  constexpr int KQM = kMaxGroup * HD / 128;  // quads of the largest slice
+  constexpr int KO = (kMaxGroup * HD + NTH - 1) / NTH;
+  static_assert(RG <= NTH, "one thread per row of the group in the epilogue");
+  const int t = threadIdx.x, l = t & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int Hkv = a.num_kv_heads;
+  const int h = blockIdx.x % Hkv, bg = blockIdx.x / Hkv;
+  const int G = a.num_heads / Hkv, SL = G * HD;
+  const int KQ = a.K >> 7, KQS = SL >> 7, NB = a.N >> 4;
+  const int nb = bg * NW + wv;
+  const int n_local = l & 15, c = l >> 4;
+  // this wave's O weights first: they depend on nothing else
+  const size_t tile0 = (size_t)min(nb, NB - 1) * KQ + (size_t)h * KQS;
+  const uint4 *cp = a.codes + tile0 * 64 + l;
+  const uint16_t *sp = (const uint16_t *)a.scales + tile0 * 64 + l;
+  uint4 wq[KQM];
+  uint32_t wsc[KQM];
+#pragma unroll
+  for (int i = 0; i < KQM; ++i)
+    if (i < KQS) {
+      wq[i] = load_stream(cp + (size_t)i * 64);
+      wsc[i] = sp[(size_t)i * 64];
+    }
+  // the residual of this thread's epilogue row (read by the last workgroup)
+  const int r0 = bg * RG, nrows = min(RG, a.N - r0);
+  const float resid = a.y && t < nrows ? a.resid[r0 + t] : 0.0f;
+  const int ctx = __builtin_amdgcn_readfirstlane(min(a.ctx_len[0], a.max_ctx));
+  const int lane = __builtin_amdgcn_readfirstlane(a.lane_of_row[0]);
+  __shared__ AttnF16Lds<HD, NW> s;
+  __shared__ __align__(16) int8_t aq[kMaxGroup * HD];
+  __shared__ ActMeta am[kMaxGroup * HD / 32];
+  __shared__ float wsq[NW];
+  __shared__ int last;
+  float orun[KO], lrun[KO], mrun[KO];
+#pragma unroll
+  for (int k = 0; k < KO; ++k) {
+    orun[k] = 0.0f;
+    lrun[k] = 0.0f;
+    mrun[k] = -INFINITY;
+  }
+  const __half *pool = (const __half *)a.kv_pool;
+  const int32_t *prow = a.page_table + (size_t)lane * a.max_pages;
+  const int nch = (ctx + CH - 1) / CH;
+  for (int ch = 0; ch < nch; ++ch) {
+    const int j0 = ch * CH;
+    attn_f16_item<HD, NT, NW>(a.q + (size_t)h * SL, pool, prow + j0 / 16, min(CH, ctx - j0),
+                              a.layer, (size_t)a.num_layers, Hkv * HD, h, G, s);
+#pragma unroll
+    for (int k = 0; k < KO; ++k) {
+      const int oi = t + NTH * k;
+      if (oi >= SL) break;
+      const int g = oi / HD, d = oi % HD;
+      float L = 0.0f, O = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float f = s.fw[w][g];
+        L = fmaf(s.sl[w][g], f, L);
+        O = fmaf(s.so[w][g][d], f, O);
+      }
+      const float mx = s.mg[g];
+      if (ch == 0) {
+        orun[k] = O;
+        lrun[k] = L;
+        mrun[k] = mx;
+      } else {
+        const float mn = fmaxf(mrun[k], mx);
+        const float fa = expf(mrun[k] - mn), fb = expf(mx - mn);
+        orun[k] = orun[k] * fa + O * fb;
+        lrun[k] = lrun[k] * fa + L * fb;
+        mrun[k] = mn;
+      }
+    }
+    __syncthreads();  // s is reused by the next item
+  }
+  // the O projection's planes of this slice (a half-wave = one group of 32;
+  // SL is a multiple of 128, so a half-wave is wholly in or out of range)
+#pragma unroll
+  for (int k = 0; k < KO; ++k) {
+    const int oi = t + NTH * k;
+    if (oi >= SL) break;
+    const float v = nch > 0 ? orun[k] * (1.0f / lrun[k]) : 0.0f;
+    quantize_group<1>(v, t & 31, oi >> 5, 0, 1, aq, am);
+  }
+  __syncthreads();
+  if (nb < NB) {
+    // lane (c, n): group 4 i + c of the slice, row n of the block
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < KQM; ++i) {
+      if (i >= KQS) break;
+      const int g = 4 * i + c;
+      const uint32_t wj[4] = {wq[i].x, wq[i].y, wq[i].z, wq[i].w};
+      const int4 q0 = *(const int4 *)(aq + g * 32);
+      const int4 q1 = *(const int4 *)(aq + g * 32 + 16);
+      const int qa[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+      int T = 0;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        T = __builtin_amdgcn_sdot4((int)(wj[w] & 0x0F0F0F0Fu), qa[2 * w], T, false);
+        T = __builtin_amdgcn_sdot4((int)((wj[w] >> 4) & 0x0F0F0F0Fu), qa[2 * w + 1], T, false);
+      }
+      const ActMeta mm = am[g];
+      const float v = (float)(T - mm.corr);
+      float tt = v * h2f(wsc[i]);
+      tt = tt * mm.scale;
+      acc += tt;
+    }
+    acc = xor32_add(xor16_add(acc));
+    // (agent-scope stores: written through to the device-coherent level, so
+    // the other XCDs' workgroups read them without an L2 write-back)
+    if (c == 0)
+      __hip_atomic_store(a.parts + (size_t)h * a.N + nb * 16 + n_local, acc, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+  if (!a.y) return;
+  // publish this slice: every wave waits for its stores to complete before
+  // the barrier, after which one thread counts the group's arrival
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __syncthreads();
+  if (t == 0)
+    last = __hip_atomic_fetch_add(a.counters + bg, 1u, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(Hkv - 1);
+  __syncthreads();
+  if (!last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  float y = 0.0f;
+  if (t < nrows) {
+    const int n = r0 + t;
+    float pv[kMaxAttnOHeads];  // every slice requested before the first add
+#pragma unroll
+    for (int h2 = 0; h2 < kMaxAttnOHeads; ++h2)
+      pv[h2] = h2 < Hkv ? __hip_atomic_load(a.parts + (size_t)h2 * a.N + n, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT)
+                        : 0.0f;
+    float p = pv[0];
+#pragma unroll
+    for (int h2 = 1; h2 < kMaxAttnOHeads; ++h2)
+      if (h2 < Hkv) p += pv[h2];
+    y = resid + p;
+    a.y[n] = y;
+  }
+  const float sq = wave_sum(y * y);
+  if (l == 0) wsq[wv] = sq;
+  __syncthreads();
+  if (t == 0) {
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) tot += wsq[w];
+    a.ss_out[bg] = tot;
+    // ready for the next launch
+    __hip_atomic_store(a.counters + bg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -1680,6 +1907,34 @@ hipError_t launch_attention_f16(const float *q, const void *kv_pool, const int32
   else
     hipLaunchKernelGGL((attn_combine2_kernel<128>), dim3(num_heads, M), dim3(kCombineThreads), 0,
                        st, ctx_len, num_heads, chunk, nch, max_ctx, scratch, out, emit);
+  return hipGetLastError();
+}
+
+static constexpr int kAttnONT = 2, kAttnONW = 8;  // 256 positions per item
+
+int attn_o_groups(int N) { return (N / 16 + kAttnONW - 1) / kAttnONW; }
+
+bool attn_o_ok(const AttnOArgs &a) {
+  const int hd = a.head_dim;
+  if ((hd != 64 && hd != 128) || a.num_kv_heads < 1 || a.num_kv_heads > kMaxAttnOHeads ||
+      a.num_heads % a.num_kv_heads)
+    return false;
+  const int G = a.num_heads / a.num_kv_heads;
+  if (a.y && (!a.resid || !a.ss_out || !a.counters)) return false;
+  return G <= kMaxGroup && (G * hd) % 128 == 0 && a.K == a.num_heads * hd && a.N > 0 &&
+         a.N % 16 == 0 && a.max_ctx >= 1 && a.max_pages >= 1 && a.codes && a.scales && a.parts &&
+         a.q && a.kv_pool && a.page_table && a.lane_of_row && a.ctx_len;
+}
+
+hipError_t launch_attn_o(const AttnOArgs &a, hipStream_t st) {
+  if (!attn_o_ok(a)) return hipErrorInvalidValue;
+  const unsigned grid = (unsigned)(attn_o_groups(a.N) * a.num_kv_heads);
+  if (a.head_dim == 64)
+    hipLaunchKernelGGL((attn_o_kernel<64, kAttnONT, kAttnONW>), dim3(grid), dim3(64 * kAttnONW), 0,
+                       st, a);
+  else
+    hipLaunchKernelGGL((attn_o_kernel<128, kAttnONT, kAttnONW>), dim3(grid),
+                       dim3(64 * kAttnONW), 0, st, a);
   return hipGetLastError();
 }
 

@@ -972,6 +972,44 @@ int glacier_hip_paged_attention(glacier_hip_context *ctx, const float *q_dev,
   return GLACIER_HIP_OK;
 }
 
+int glacier_hip_paged_attention_o(glacier_hip_context *ctx, const float *q_dev,
+                                  const void *kv_pool_dev, const int32_t *page_table_dev,
+                                  uint32_t max_pages, const int32_t *ctx_len_dev, uint32_t layer,
+                                  uint32_t num_layers, uint32_t num_heads, uint32_t num_kv_heads,
+                                  uint32_t head_dim, uint32_t max_ctx,
+                                  const glacier_hip_int4_weight *o_weight, float *parts_dev,
+                                  void *stream) {
+  if (!ctx || !q_dev || !kv_pool_dev || !page_table_dev || !ctx_len_dev || !o_weight ||
+      !parts_dev)
+    return GLACIER_HIP_INVALID_ARGUMENT;
+  if (o_weight->ctx != ctx) return GLACIER_HIP_INVALID_HANDLE;
+  gk::AttnOArgs a{};
+  a.q = q_dev;
+  a.kv_pool = kv_pool_dev;
+  a.page_table = page_table_dev;
+  a.max_pages = (int)max_pages;
+  a.lane_of_row = ctx->ident;  // row 0 attends with page-table row 0
+  a.ctx_len = ctx_len_dev;
+  a.layer = (int)layer;
+  a.num_layers = (int)num_layers;
+  a.num_heads = (int)num_heads;
+  a.num_kv_heads = (int)num_kv_heads;
+  a.head_dim = (int)head_dim;
+  a.max_ctx = (int)max_ctx;
+  a.codes = o_weight->codes;
+  a.scales = o_weight->scales;
+  a.N = (int)o_weight->out_f;
+  a.K = (int)o_weight->in_f;
+  a.parts = parts_dev;
+  if (layer >= num_layers || max_ctx == 0 || max_pages == 0 || (max_ctx + 15) / 16 > max_pages ||
+      max_ctx > (1u << 24) || num_heads > 1024 || !gk::attn_o_ok(a))
+    return GLACIER_HIP_SHAPE_MISMATCH;
+  GH_SUBMISSION(ctx);
+  hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
+  GH_CHECK(ctx, gk::launch_attn_o(a, st));
+  return GLACIER_HIP_OK;
+}
+
 int glacier_hip_paged_attention_prefill(glacier_hip_context *ctx, const float *q_dev,
                                         const void *kv_pool_dev, const int32_t *page_table_dev,
                                         uint32_t max_pages, uint32_t pos0, uint32_t T,

@@ -112,6 +112,9 @@ struct glacier_hip_session {
   float *splitk_ws = nullptr;       // GEMM split-K partial sums
   size_t splitk_floats = 0;
   float *ss_parts = nullptr;        // deferred RMSNorm partial sums [32][1024]
+  float *o_parts = nullptr;         // fused attention + O: [num_kv_heads][dim]
+  unsigned *o_counters = nullptr;   // fused attention + O: arrivals per row group (0 at rest)
+  int attn_o = -1;                  // fused attention + O usable: -1 not yet known, 0, 1
   float *att_scratch = nullptr;
   void *arg_scratch = nullptr;
   uint32_t *arg_counters = nullptr;
@@ -126,10 +129,10 @@ struct glacier_hip_session {
   gk::ArgmaxResult *res_host = nullptr;
   bool inject_failure = false;
   PreparedWave prep;
-  // graph cache: key = (rows, with_head, eligible, prehead)
+  // graph cache: key = (rows, with_head, eligible, prehead, fused attention + O)
   struct GraphEntry {
     uint32_t rows;
-    bool head, elig, pre;
+    bool head, elig, pre, fused;
     hipGraphExec_t exec;
   };
   std::vector<GraphEntry> graphs;
@@ -739,7 +742,65 @@ bool gemm_emit_ok(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, int
 // sums fit the workspace the finishing pass of O and down also writes the
 // next RMSNorm'd projection's planes and that of gate/up the down
 // projection's, otherwise each input is converted by a separate kernel.
-hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, hipStream_t st) {
+// Arguments of the fused attention + O projection launch for row 0 of rp at
+// layer l: the O projection plus the residual x_res into h, with its
+// partial sums of squares (one per row group) into ss.
+gk::AttnOArgs attn_o_args(glacier_hip_session *s, const RowPtrs &rp, uint32_t l, float *ss) {
+  const auto &c = s->model->cfg;
+  const glacier_hip_int4_weight *o = s->model->layers[l].o;
+  gk::AttnOArgs a{};
+  a.q = s->q;
+  a.kv_pool = s->kv_pool;
+  a.page_table = s->page_table;
+  a.max_pages = (int)s->max_pages;
+  a.lane_of_row = rp.lane_of_row;
+  a.ctx_len = rp.ctx_len;
+  a.layer = (int)l;
+  a.num_layers = (int)c.num_layers;
+  a.num_heads = (int)c.num_heads;
+  a.num_kv_heads = (int)c.num_kv_heads;
+  a.head_dim = (int)c.head_dim;
+  a.max_ctx = (int)s->opt.max_positions;
+  a.codes = o->codes;
+  a.scales = o->scales;
+  a.N = (int)o->out_f;
+  a.K = (int)o->in_f;
+  a.parts = s->o_parts;
+  a.resid = s->x_res;
+  a.y = s->h;
+  a.ss_out = ss;
+  a.counters = s->o_counters;
+  return a;
+}
+
+// Largest context (positions) a fused one-lane step is used for: one work
+// item of the fused kernel (longer contexts run correctly but serially
+// inside each workgroup, slower than the two launches).
+constexpr uint32_t kFusedMaxCtx = 256;
+
+// Whether one-lane decode steps can run attention and the O projection as
+// one launch: fp16 KV, Q8 inputs for O, shapes the fused kernel takes, and
+// its row groups within the partial sums gate/up reads; not when the
+// session options ask for two launches.
+bool attn_o_usable(glacier_hip_session *s) {
+  if (s->attn_o >= 0) return s->attn_o == 1;
+  const auto &c = s->model->cfg;
+  bool ok = !s->opt.split_attention_o && s->opt.kv_dtype == GLACIER_HIP_F16 &&
+            s->planes2_rows >= 1 && s->o_parts && s->o_counters && s->ss_parts;
+  const RowPtrs rp{s->step_dev->tokens, s->step_dev->lane_of_row, s->step_dev->pos_of_row,
+                   s->step_dev->ctx_len};
+  for (uint32_t l = 0; ok && l < c.num_layers; ++l) {
+    const LayerDev &L = s->model->layers[l];
+    ok = layer_D(s, L.o->out_f, L.o->in_f) == 1 && L.o->out_f == c.dim &&
+         gk::attn_o_ok(attn_o_args(s, rp, l, s->ss_parts)) &&
+         gk::attn_o_groups((int)c.dim) <= 1024;
+  }
+  s->attn_o = ok ? 1 : 0;
+  return ok;
+}
+
+hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, hipStream_t st,
+                          bool fused = false) {
   glacier_hip_model *m = s->model;
   const auto &c = m->cfg;
   const int D = (int)c.dim;
@@ -787,77 +848,93 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
     qout.qkv = &q;
     e = run_proj(s, L.qkv, Dq, rows, gk::EPI_QKV, qin, qout, st);
     if (e != hipSuccess) return e;
-    // attention: a prompt chunk of one lane past the GEMV size runs the
-    // prefill kernel, other steps the decode kernel, which for up to 32 rows
-    // also writes the O projection's planes
-    const bool pf_attn = rows > kPrefillAttnRows && rp.chunk_lane >= 0 &&
-                         s->opt.kv_dtype == GLACIER_HIP_F16;
-    const bool o_planes = !pf_attn && rows <= 32 && (uint32_t)rows <= s->planes2_rows;
-    const gk::PlanesDst opd = o_planes ? gk::PlanesDst{s->act_q2, s->act_meta2, Do}
-                                       : gk::PlanesDst{nullptr, nullptr, 1};
-    if (pf_attn)
-      e = gk::launch_attention_prefill(s->q, s->kv_pool, s->page_table, (int)s->max_pages,
-                                       rp.chunk_lane, rp.chunk_pos0, rows, (int)l,
-                                       (int)c.num_layers, (int)c.num_heads, (int)c.num_kv_heads,
-                                       (int)c.head_dim, s->attn, st);
-    else
-      e = gk::launch_attention(s->q, s->kv_pool, s->opt.kv_dtype == GLACIER_HIP_F16,
-                               s->page_table, (int)s->max_pages, rp.lane_of_row, rp.ctx_len, rows,
-                               (int)l, (int)c.num_layers, (int)c.num_heads, (int)c.num_kv_heads,
-                               (int)c.head_dim, (int)s->opt.max_positions, s->att_scratch,
-                               s->attn, st, opd);
-    if (e != hipSuccess) return e;
-    // O projection + residual (chain: partial sums of h for gate/up's norm)
-    ProjIn oin;
-    ProjOut oout;
-    oout.y = s->h;
-    oout.resid = s->x_res;
-    oout.ss_out = ss;
-    if (o_planes) {
-      oin.planes_q = s->act_q2;
-      oin.planes_m = s->act_meta2;
-    } else {
-      oin.x = s->attn;
-    }
-    if (ss) {
-      ss_count = proj_grid(s, L.o, Do, rows, gk::EPI_RESID, oin, oout);
-      if (ss_count <= 0) return hipErrorInvalidValue;
-    }
-    if (!chain) {  // GEMM: gate/up's planes from O's finishing pass
-      oout.emit = gk::PlanesDst{s->act_q, s->act_meta, Dg};
-      oout.emit_norm_w = L.post_norm;
-      if (!gemm_emit_ok(s, L.o, Do, rows, gk::EPI_RESID, oout)) {
-        oout.emit = gk::PlanesDst{nullptr, nullptr, 1};
-        oout.emit_norm_w = nullptr;
-      }
-    }
-    e = run_proj(s, L.o, Do, rows, gk::EPI_RESID, oin, oout, st);
-    if (e != hipSuccess) return e;
-    // gate/up + SwiGLU (decode sizes: emitted straight into down's planes)
-    ProjIn gin;
-    if (oout.emit.q) {
-      gin.planes_q = s->act_q;
-      gin.planes_m = s->act_meta;
-    } else {
+    ProjOut gout;
+    if (fused) {
+      // one lane: attention + the O projection (+ residual, partial sums of
+      // h for gate/up's norm) in one launch, then gate/up as in the chain
+      e = gk::launch_attn_o(attn_o_args(s, rp, l, ss), st);
+      if (e != hipSuccess) return e;
+      ss_count = gk::attn_o_groups((int)c.dim);
+      ProjIn gin;
       gin.x = s->h;
       gin.norm_w = L.post_norm;
       gin.ss = ss;
       gin.ss_count = ss_count;
-    }
-    ProjOut gout;
-    if (chain) {
       gout.emit = gk::PlanesDst{s->act_q2, s->act_meta2, Dd};
+      e = run_proj(s, L.gu, Dg, rows, gk::EPI_SWIGLU, gin, gout, st);
+      if (e != hipSuccess) return e;
     } else {
-      // GEMM: down's planes from gate/up's finishing pass (into act_q, which
-      // gate/up has finished reading by then), else the SwiGLU rows
-      gout.emit = gk::PlanesDst{s->act_q, s->act_meta, Dd};
-      if (!gemm_emit_ok(s, L.gu, Dg, rows, gk::EPI_SWIGLU, gout)) {
-        gout.emit = gk::PlanesDst{nullptr, nullptr, 1};
-        gout.y = s->act;
+      // attention: a prompt chunk of one lane past the GEMV size runs the
+      // prefill kernel, other steps the decode kernel, which for up to 32 rows
+      // also writes the O projection's planes
+      const bool pf_attn = rows > kPrefillAttnRows && rp.chunk_lane >= 0 &&
+                           s->opt.kv_dtype == GLACIER_HIP_F16;
+      const bool o_planes = !pf_attn && rows <= 32 && (uint32_t)rows <= s->planes2_rows;
+      const gk::PlanesDst opd = o_planes ? gk::PlanesDst{s->act_q2, s->act_meta2, Do}
+                                         : gk::PlanesDst{nullptr, nullptr, 1};
+      if (pf_attn)
+        e = gk::launch_attention_prefill(s->q, s->kv_pool, s->page_table, (int)s->max_pages,
+                                         rp.chunk_lane, rp.chunk_pos0, rows, (int)l,
+                                         (int)c.num_layers, (int)c.num_heads, (int)c.num_kv_heads,
+                                         (int)c.head_dim, s->attn, st);
+      else
+        e = gk::launch_attention(s->q, s->kv_pool, s->opt.kv_dtype == GLACIER_HIP_F16,
+                                 s->page_table, (int)s->max_pages, rp.lane_of_row, rp.ctx_len, rows,
+                                 (int)l, (int)c.num_layers, (int)c.num_heads, (int)c.num_kv_heads,
+                                 (int)c.head_dim, (int)s->opt.max_positions, s->att_scratch,
+                                 s->attn, st, opd);
+      if (e != hipSuccess) return e;
+      // O projection + residual (chain: partial sums of h for gate/up's norm)
+      ProjIn oin;
+      ProjOut oout;
+      oout.y = s->h;
+      oout.resid = s->x_res;
+      oout.ss_out = ss;
+      if (o_planes) {
+        oin.planes_q = s->act_q2;
+        oin.planes_m = s->act_meta2;
+      } else {
+        oin.x = s->attn;
       }
+      if (ss) {
+        ss_count = proj_grid(s, L.o, Do, rows, gk::EPI_RESID, oin, oout);
+        if (ss_count <= 0) return hipErrorInvalidValue;
+      }
+      if (!chain) {  // GEMM: gate/up's planes from O's finishing pass
+        oout.emit = gk::PlanesDst{s->act_q, s->act_meta, Dg};
+        oout.emit_norm_w = L.post_norm;
+        if (!gemm_emit_ok(s, L.o, Do, rows, gk::EPI_RESID, oout)) {
+          oout.emit = gk::PlanesDst{nullptr, nullptr, 1};
+          oout.emit_norm_w = nullptr;
+        }
+      }
+      e = run_proj(s, L.o, Do, rows, gk::EPI_RESID, oin, oout, st);
+      if (e != hipSuccess) return e;
+      // gate/up + SwiGLU (decode sizes: emitted straight into down's planes)
+      ProjIn gin;
+      if (oout.emit.q) {
+        gin.planes_q = s->act_q;
+        gin.planes_m = s->act_meta;
+      } else {
+        gin.x = s->h;
+        gin.norm_w = L.post_norm;
+        gin.ss = ss;
+        gin.ss_count = ss_count;
+      }
+      if (chain) {
+        gout.emit = gk::PlanesDst{s->act_q2, s->act_meta2, Dd};
+      } else {
+        // GEMM: down's planes from gate/up's finishing pass (into act_q, which
+        // gate/up has finished reading by then), else the SwiGLU rows
+        gout.emit = gk::PlanesDst{s->act_q, s->act_meta, Dd};
+        if (!gemm_emit_ok(s, L.gu, Dg, rows, gk::EPI_SWIGLU, gout)) {
+          gout.emit = gk::PlanesDst{nullptr, nullptr, 1};
+          gout.y = s->act;
+        }
+      }
+      e = run_proj(s, L.gu, Dg, rows, gk::EPI_SWIGLU, gin, gout, st);
+      if (e != hipSuccess) return e;
     }
-    e = run_proj(s, L.gu, Dg, rows, gk::EPI_SWIGLU, gin, gout, st);
-    if (e != hipSuccess) return e;
     // down + residual (chain: partial sums of x_res for the next norm)
     ProjIn din;
     ProjOut dout;
@@ -930,10 +1007,10 @@ hipError_t enqueue_head(glacier_hip_session *s, int rows, const float *x, bool e
 
 // The full launch sequence of one decode step for `rows` lanes.
 hipError_t enqueue_step(glacier_hip_session *s, int rows, bool head, bool elig, bool pre,
-                        hipStream_t st) {
+                        bool fused, hipStream_t st) {
   const RowPtrs rp{s->step_dev->tokens, s->step_dev->lane_of_row, s->step_dev->pos_of_row,
                    s->step_dev->ctx_len};
-  hipError_t e = enqueue_layers(s, rows, rp, st);
+  hipError_t e = enqueue_layers(s, rows, rp, st, fused);
   if (e != hipSuccess || !head) return e;
   return enqueue_head(s, rows, s->x_res, elig, pre, st);
 }
@@ -941,7 +1018,9 @@ hipError_t enqueue_step(glacier_hip_session *s, int rows, bool head, bool elig, 
 void destroy_session(glacier_hip_session *s) {
   void *ptrs[] = {s->kv_pool, s->page_table, s->rope_cos, s->rope_sin, s->x_res, s->h, s->q,
                   s->attn, s->act, s->logits, s->act_q, s->act_meta, s->act_q2, s->act_meta2,
-                  s->att_scratch, s->ss_parts, s->arg_scratch, s->arg_counters, s->arg_result,
+                  s->att_scratch, s->ss_parts, s->o_parts, s->o_counters, s->arg_scratch,
+                  s->arg_counters,
+                  s->arg_result,
                   s->elig_words, s->splitk_ws,
                   s->step_dev, s->pf_dev};
   for (void *p : ptrs) gh::dev_free(s->model->ctx, p);
@@ -1111,27 +1190,29 @@ int run_step(glacier_hip_session *s, const uint32_t *lanes, const uint32_t *toke
   }
   const bool elig = elig_host != nullptr;
   const bool pre = elig && s->head_domain == GLACIER_HIP_HEAD_DOMAIN_PREHEAD;
+  const bool fused = count == 1 && txns[0].pos + 1 <= kFusedMaxCtx && attn_o_usable(s);
   hipGraphExec_t exec = nullptr;
   if (s->opt.use_graph) {
     for (auto &g : s->graphs)
-      if (g.rows == count && g.head == head && g.elig == elig && g.pre == pre) exec = g.exec;
+      if (g.rows == count && g.head == head && g.elig == elig && g.pre == pre && g.fused == fused)
+        exec = g.exec;
     if (!exec) {
       hipGraph_t graph;
       e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
       if (e != hipSuccess) return fail(e, "begin capture");
-      hipError_t e2 = enqueue_step(s, (int)count, head, elig, pre, st);
+      hipError_t e2 = enqueue_step(s, (int)count, head, elig, pre, fused, st);
       e = hipStreamEndCapture(st, &graph);
       if (e2 != hipSuccess) return fail(e2, "capture step");
       if (e != hipSuccess) return fail(e, "end capture");
       e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
       (void)hipGraphDestroy(graph);
       if (e != hipSuccess) return fail(e, "graph instantiate");
-      s->graphs.push_back({count, head, elig, pre, exec});
+      s->graphs.push_back({count, head, elig, pre, fused, exec});
     }
     e = hipGraphLaunch(exec, st);
     if (e != hipSuccess) return fail(e, "graph launch");
   } else {
-    e = enqueue_step(s, (int)count, head, elig, pre, st);
+    e = enqueue_step(s, (int)count, head, elig, pre, fused, st);
     if (e != hipSuccess) return fail(e, "enqueue step");
   }
   if (head) {
@@ -1414,6 +1495,8 @@ static glacier_hip_session *session_create_impl(glacier_hip_model *m,
   A((void **)&s->act_meta2, G2 * s->planes2_rows * sizeof(gk::ActMeta));
   A((void **)&s->att_scratch, std::max<size_t>(att, 1) * 4);
   A((void **)&s->ss_parts, (size_t)32 * 1024 * sizeof(float));
+  A((void **)&s->o_parts, (size_t)c.num_kv_heads * c.dim * sizeof(float));
+  A((void **)&s->o_counters, (size_t)gk::attn_o_groups((int)c.dim) * sizeof(unsigned));
   size_t arg_bytes = gk::argmax_scratch_bytes((int)L, (long)c.vocab_size);
   for (uint32_t r = 1; r <= std::min<uint32_t>(L, gk::kGemvMaxRows); ++r)
     arg_bytes = std::max(arg_bytes, (size_t)r * sizeof(gk::ArgPartial) *
@@ -1458,6 +1541,8 @@ static glacier_hip_session *session_create_impl(glacier_hip_model *m,
   H((void **)&s->res_host, L * sizeof(gk::ArgmaxResult));
   if (ok) {
     ok = hipMemset(s->arg_counters, 0, (size_t)L * 4) == hipSuccess &&
+         hipMemset(s->o_counters, 0,
+                   (size_t)gk::attn_o_groups((int)c.dim) * sizeof(unsigned)) == hipSuccess &&
          hipMemset(s->kv_pool, 0, page_bytes * s->total_pages) == hipSuccess;
     memset(s->pt_host, 0, (size_t)L * s->max_pages * 4);
     ok = ok && hipMemcpy(s->page_table, s->pt_host, (size_t)L * s->max_pages * 4,

@@ -117,7 +117,8 @@ class SessionOptions(C.Structure):
     _fields_ = [("max_lanes", C.c_uint32), ("max_positions", C.c_uint32),
                 ("total_pages", C.c_uint32), ("kv_dtype", C.c_int32),
                 ("layer_activation", C.c_int32), ("head_activation", C.c_int32),
-                ("use_graph", C.c_int32), ("prefill_chunk", C.c_int32)]
+                ("use_graph", C.c_int32), ("prefill_chunk", C.c_int32),
+                ("split_attention_o", C.c_int32)]
 
 
 class PageMapRoot(C.Structure):
@@ -393,6 +394,9 @@ _SIGS = [
     ("glacier_hip_paged_attention", C.c_int,
      [_P, _P, _P, C.c_int, _P, C.c_uint32, _P, C.c_uint32, C.c_uint32, C.c_uint32,
       C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, _P, _P]),
+    ("glacier_hip_paged_attention_o", C.c_int,
+     [_P, _P, _P, _P, C.c_uint32, _P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+      C.c_uint32, C.c_uint32, _P, _P, _P]),
     ("glacier_hip_paged_attention_prefill", C.c_int,
      [_P, _P, _P, _P, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
       C.c_uint32, C.c_uint32, _P, _P]),
@@ -797,12 +801,13 @@ class Model:
 class Session:
     def __init__(self, model, max_lanes, max_positions, kv_dtype=F32, total_pages=0,
                  layer_activation=ACT_AUTO, head_activation=ACT_AUTO, use_graph=True,
-                 prefill_chunk=0):
+                 prefill_chunk=0, split_attention_o=False):
         self.model = model
         o = SessionOptions(max_lanes=max_lanes, max_positions=max_positions,
                            total_pages=total_pages, kv_dtype=kv_dtype,
                            layer_activation=layer_activation, head_activation=head_activation,
-                           use_graph=1 if use_graph else 0, prefill_chunk=prefill_chunk)
+                           use_graph=1 if use_graph else 0, prefill_chunk=prefill_chunk,
+                           split_attention_o=1 if split_attention_o else 0)
         self.h = lib().glacier_hip_session_create(model.h, C.byref(o))
         if not self.h:
             raise GlacierHipError(INVALID_ARGUMENT, "session_create: " +

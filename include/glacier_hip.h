@@ -365,6 +365,26 @@ int glacier_hip_paged_attention_prefill(glacier_hip_context *ctx, const float *q
                                         uint32_t num_kv_heads, uint32_t head_dim, float *out_dev,
                                         void *stream);
 
+/* Attention of one decode row fused with the O projection (the one-lane
+ * decode step's launch; the reference runs attention then the O matvec,
+ * forward.zig:478-533 and generate.zig:1561): for row 0 (page-table row 0,
+ * ctx_len_dev[0] attended positions of fp16 pages at `layer`) every KV head
+ * h computes the attention of its num_heads / num_kv_heads query heads,
+ * quantises that slice of the attention output to Q8 groups of 32 (the O
+ * projection's activation quantiser, int4_matmul.zig:380-398) and writes
+ * parts_dev[h][n] = sum over the slice of W_o[n][k] * a[k] (Q8 group
+ * arithmetic of glacier_hip_int4_gemv). The sum over h is the O projection
+ * of the attention output. num_kv_heads <= 8, head_dim 64 or 128, a slice
+ * of whole 128-column tiles; o_weight is [out_f][num_heads * head_dim].
+ * Asynchronous on `stream`; launches only. */
+int glacier_hip_paged_attention_o(glacier_hip_context *ctx, const float *q_dev,
+                                  const void *kv_pool_dev, const int32_t *page_table_dev,
+                                  uint32_t max_pages, const int32_t *ctx_len_dev, uint32_t layer,
+                                  uint32_t num_layers, uint32_t num_heads, uint32_t num_kv_heads,
+                                  uint32_t head_dim, uint32_t max_ctx,
+                                  const glacier_hip_int4_weight *o_weight, float *parts_dev,
+                                  void *stream);
+
 /* ---- greedy samplers (sampling.zig:194-206, :55-105) ---------------------
  * rows independent logit rows of length n. Results are written to host
  * memory after the call synchronizes the stream. */
@@ -470,6 +490,9 @@ typedef struct {
     int32_t use_graph;           /* capture the decode step in a hipGraph */
     int32_t prefill_chunk;       /* prompt rows per prefill launch sequence;
                                   * 0 = min(max_positions, 2048) */
+    int32_t split_attention_o;   /* 0: a one-lane decode step at a context of up to
+                                  * 256 positions (fp16 KV) runs attention and the O
+                                  * projection as one launch; 1: always two */
 } glacier_hip_session_options_t;
 
 typedef struct {
