@@ -227,6 +227,12 @@ struct AttnOArgs {
   int max_pages;
   const int32_t *lane_of_row;  // [1]
   const int32_t *ctx_len;      // [1]
+  // optional: row 0 packed in one line, {lane, ctx_len, -, -, then the
+  // first row0_pages entries of its page-table row}; read instead of
+  // lane_of_row / ctx_len, and instead of the page table when the context
+  // fits those pages
+  const int32_t *row0;
+  int row0_pages;
   int layer, num_layers, num_heads, num_kv_heads, head_dim, max_ctx;
   const uint4 *codes;          // O weights, device tile layout, N x K (K = Hq * head_dim)
   const uint2 *scales;

@@ -1361,12 +1361,19 @@ struct AttnF16Lds {
 // the merged output of query head g, dim d is
 //   O = sum_w s.so[w][g][d] * s.fw[w][g],  L = sum_w s.sl[w][g] * s.fw[w][g],
 // with maximum s.mg[g] (waves added in order). The caller must pass a
-// barrier before the next call reuses s.
-template <int HD, int NT, int NW>
+// barrier before the next call reuses s. after_issue() runs in every wave
+// once the item's q, K and V loads are requested and before any of them is
+// waited for: loads the caller requests there return after the item's
+// (vector loads complete in issue order), so they never delay it.
+struct AttnNoHook {
+  __device__ void operator()() const {}
+};
+template <int HD, int NT, int NW, class Hook = AttnNoHook>
 static __device__ __forceinline__ void attn_f16_item(const float *qrow, const __half *pool,
                                                      const int32_t *ptab, int n, int layer,
                                                      size_t lay, int kv_dim, int h, int G,
-                                                     AttnF16Lds<HD, NW> &s) {
+                                                     AttnF16Lds<HD, NW> &s,
+                                                     const Hook &after_issue = Hook()) {
   typedef _Float16 h4 __attribute__((ext_vector_type(4)));
   typedef float f4 __attribute__((ext_vector_type(4)));
   constexpr int S = HD / 16;    // f16 MFMA steps over the head dim
@@ -1385,47 +1392,63 @@ static __device__ __forceinline__ void attn_f16_item(const float *qrow, const __
 #pragma unroll
   for (int e = 0; e < DPL; ++e) o[e] = f4{0.0f, 0.0f, 0.0f, 0.0f};
   float mx = -INFINITY, sum = 0.0f;
+  float4 qv[S];
+  uint4 kr[NT][HD / 32];
+  vrow_t vr[NT][4];
   if (wn > 0) {
     // q first (it depends on nothing the page walk reads), as the B operand:
     // lane (c, j) holds head j's dims of k-chunk c
+    // (every load of the item is unconditional, from an address clamped into
+    // range: a conditional load whose lanes are zeroed instead makes the
+    // compiler wait for it before the next one, serialising the batch;
+    // validity is applied by value when the data is used)
     const float *qr = qrow + (size_t)(j < G ? j : 0) * HD;
-    float4 qv[S];
 #pragma unroll
     for (int st = 0; st < S; ++st) {
       const int base = 8 * (4 * (st >> 1) + c) + 4 * (st & 1);
-      qv[st] = j < G ? *(const float4 *)(qr + base) : make_float4(0.f, 0.f, 0.f, 0.f);
+      qv[st] = *(const float4 *)(qr + base);
     }
     // page ids of this wave's pages (wave-uniform)
     const int32_t *pt = ptab + wbase / 16;
     int pg[NT];
 #pragma unroll
-    for (int T = 0; T < NT; ++T) pg[T] = 16 * T < wn ? pt[T] : 0;
+    // (an unconditional load from a wave-uniform clamped index is a scalar
+    // load; a conditional one becomes a vector load, which completes only
+    // after every vector load issued before it, q's included)
+    for (int T = 0; T < NT; ++T) pg[T] = pt[16 * T < wn ? T : 0];
     // K: lane (c, j) loads 16-byte pieces 4 * tt + c of position j of each
     // page; V: lane (c, j) loads dims DPL*j .. DPL*j + DPL-1 of positions
-    // 4c + r (r = 0..3) of each page
-    uint4 kr[NT][HD / 32];
-    vrow_t vr[NT][4];
+    // 4c + r (r = 0..3) of each page. Pages past the item read page 0 and
+    // positions past it stay inside their page, so every load is in range;
+    // their scores are masked and their V rows zeroed before use.
 #pragma unroll
     for (int T = 0; T < NT; ++T) {
       const size_t pbase = ((size_t)pg[T] * lay + layer) * 2;
-      const bool kval = 16 * T + j < wn;
       const __half *krow = pool + ((pbase + 0) * 16 + j) * kv_dim + (size_t)h * HD;
 #pragma unroll
-      for (int tt = 0; tt < HD / 32; ++tt)
-        kr[T][tt] = kval ? *(const uint4 *)(krow + 8 * (4 * tt + c)) : make_uint4(0, 0, 0, 0);
+      for (int tt = 0; tt < HD / 32; ++tt) kr[T][tt] = *(const uint4 *)(krow + 8 * (4 * tt + c));
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int pos = 4 * c + rr;
         const __half *vrow = pool + ((pbase + 1) * 16 + pos) * kv_dim + (size_t)h * HD + DPL * j;
-        if (16 * T + pos < wn) vr[T][rr] = *(const vrow_t *)vrow;
-        else __builtin_memset(&vr[T][rr], 0, sizeof(vrow_t));
+        vr[T][rr] = *(const vrow_t *)vrow;
       }
     }
-    // q split into f16 hi + lo (after the K/V loads are in flight)
+  }
+  if constexpr (!std::is_same<Hook, AttnNoHook>::value) {
+    // (the scheduler would otherwise hoist the hook's loads above the item's)
+    __builtin_amdgcn_sched_barrier(0);
+    after_issue();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (wn > 0) {
+    // q split into f16 hi + lo (after the K/V loads are in flight); lanes of
+    // heads past G hold zeros
     h4 qhi[S], qlo[S];
 #pragma unroll
     for (int st = 0; st < S; ++st) {
-      const float qa[4] = {qv[st].x, qv[st].y, qv[st].z, qv[st].w};
+      const float qa[4] = {j < G ? qv[st].x : 0.0f, j < G ? qv[st].y : 0.0f,
+                           j < G ? qv[st].z : 0.0f, j < G ? qv[st].w : 0.0f};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const _Float16 hv = (_Float16)qa[e];
@@ -1475,6 +1498,11 @@ static __device__ __forceinline__ void attn_f16_item(const float *qrow, const __
         phi[rr] = hv;
         plo[rr] = (_Float16)(sc[T][rr] - (float)hv);
       }
+      // V rows past the item are zeroed (P is 0 there, but a stale row
+      // might hold an infinity)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        if (16 * T + 4 * c + rr >= wn) __builtin_memset(&vr[T][rr], 0, sizeof(vrow_t));
       const _Float16 *v0 = (const _Float16 *)&vr[T][0];
       const _Float16 *v1 = (const _Float16 *)&vr[T][1];
       const _Float16 *v2 = (const _Float16 *)&vr[T][2];
@@ -1640,23 +1668,30 @@ __global__ __launch_bounds__(64 * NW) void attn_o_kernel(AttnOArgs a) {
   const int KQ = a.K >> 7, KQS = SL >> 7, NB = a.N >> 4;
   const int nb = bg * NW + wv;
   const int n_local = l & 15, c = l >> 4;
-  // this wave's O weights first: they depend on nothing else
+  // the row's context and lane first: the page walk waits for them
+  const int ctx = __builtin_amdgcn_readfirstlane(min(a.row0 ? a.row0[1] : a.ctx_len[0], a.max_ctx));
+  const int lane = __builtin_amdgcn_readfirstlane(a.row0 ? a.row0[0] : a.lane_of_row[0]);
+  // this wave's O weights (tile slot i of quads h * KQS + i, clamped into
+  // the slice so every slot loads) and its epilogue row's residual are
+  // requested once the first attention item's loads are: vector loads
+  // complete in issue order, so requested earlier they would hold up the
+  // page walk
   const size_t tile0 = (size_t)min(nb, NB - 1) * KQ + (size_t)h * KQS;
   const uint4 *cp = a.codes + tile0 * 64 + l;
   const uint16_t *sp = (const uint16_t *)a.scales + tile0 * 64 + l;
   uint4 wq[KQM];
   uint32_t wsc[KQM];
-#pragma unroll
-  for (int i = 0; i < KQM; ++i)
-    if (i < KQS) {
-      wq[i] = load_stream(cp + (size_t)i * 64);
-      wsc[i] = sp[(size_t)i * 64];
-    }
-  // the residual of this thread's epilogue row (read by the last workgroup)
   const int r0 = bg * RG, nrows = min(RG, a.N - r0);
-  const float resid = a.y && t < nrows ? a.resid[r0 + t] : 0.0f;
-  const int ctx = __builtin_amdgcn_readfirstlane(min(a.ctx_len[0], a.max_ctx));
-  const int lane = __builtin_amdgcn_readfirstlane(a.lane_of_row[0]);
+  float resid = 0.0f;
+  auto load_weights = [&]() {
+#pragma unroll
+    for (int i = 0; i < KQM; ++i) {
+      const int ic = min(i, KQS - 1);
+      wq[i] = load_stream(cp + (size_t)ic * 64);
+      wsc[i] = sp[(size_t)ic * 64];
+    }
+    resid = a.y ? a.resid[r0 + min(t, nrows - 1)] : 0.0f;
+  };
   __shared__ AttnF16Lds<HD, NW> s;
   __shared__ __align__(16) int8_t aq[kMaxGroup * HD];
   __shared__ ActMeta am[kMaxGroup * HD / 32];
@@ -1670,12 +1705,17 @@ __global__ __launch_bounds__(64 * NW) void attn_o_kernel(AttnOArgs a) {
     mrun[k] = -INFINITY;
   }
   const __half *pool = (const __half *)a.kv_pool;
-  const int32_t *prow = a.page_table + (size_t)lane * a.max_pages;
+  const int32_t *prow = a.row0 && ctx <= 16 * a.row0_pages
+                            ? a.row0 + 4
+                            : a.page_table + (size_t)lane * a.max_pages;
   const int nch = (ctx + CH - 1) / CH;
+  if (nch == 0) load_weights();
   for (int ch = 0; ch < nch; ++ch) {
     const int j0 = ch * CH;
     attn_f16_item<HD, NT, NW>(a.q + (size_t)h * SL, pool, prow + j0 / 16, min(CH, ctx - j0),
-                              a.layer, (size_t)a.num_layers, Hkv * HD, h, G, s);
+                              a.layer, (size_t)a.num_layers, Hkv * HD, h, G, s, [&]() {
+                                if (ch == 0) load_weights();
+                              });
 #pragma unroll
     for (int k = 0; k < KO; ++k) {
       const int oi = t + NTH * k;

@@ -70,7 +70,12 @@ struct PreparedWave {
   uint8_t sha[32] = {};
 };
 
+constexpr int kRow0Pages = 28;  // page ids of row 0 carried in the step inputs
 struct StepInputs {  // uploaded once per decode step, in one copy
+  // row 0 in one 128-byte line: lane, context length, position, 0, then its
+  // first kRow0Pages page ids, so the one-lane attention reads everything
+  // its page walk needs in one memory round trip
+  alignas(128) int32_t row0[4 + kRow0Pages];
   int32_t tokens[64];
   int32_t lane_of_row[64];
   int32_t pos_of_row[64];
@@ -80,6 +85,7 @@ struct StepInputs {  // uploaded once per decode step, in one copy
 // Device arrays describing the activation rows of one launch sequence.
 struct RowPtrs {
   const int32_t *tokens, *lane_of_row, *pos_of_row, *ctx_len;
+  const int32_t *row0 = nullptr;  // StepInputs::row0, or null
   // a prefill chunk: every row is lane chunk_lane, rows at consecutive
   // positions from chunk_pos0 (-1: rows of arbitrary lanes / positions)
   int chunk_lane = -1, chunk_pos0 = 0;
@@ -755,6 +761,8 @@ gk::AttnOArgs attn_o_args(glacier_hip_session *s, const RowPtrs &rp, uint32_t l,
   a.max_pages = (int)s->max_pages;
   a.lane_of_row = rp.lane_of_row;
   a.ctx_len = rp.ctx_len;
+  a.row0 = rp.row0;
+  a.row0_pages = rp.row0 ? (int)std::min<uint32_t>(kRow0Pages, s->max_pages) : 0;
   a.layer = (int)l;
   a.num_layers = (int)c.num_layers;
   a.num_heads = (int)c.num_heads;
@@ -1009,7 +1017,7 @@ hipError_t enqueue_head(glacier_hip_session *s, int rows, const float *x, bool e
 hipError_t enqueue_step(glacier_hip_session *s, int rows, bool head, bool elig, bool pre,
                         bool fused, hipStream_t st) {
   const RowPtrs rp{s->step_dev->tokens, s->step_dev->lane_of_row, s->step_dev->pos_of_row,
-                   s->step_dev->ctx_len};
+                   s->step_dev->ctx_len, s->step_dev->row0};
   hipError_t e = enqueue_layers(s, rows, rp, st, fused);
   if (e != hipSuccess || !head) return e;
   return enqueue_head(s, rows, s->x_res, elig, pre, st);
@@ -1172,6 +1180,16 @@ int run_step(glacier_hip_session *s, const uint32_t *lanes, const uint32_t *toke
     s->step_host->lane_of_row[i] = (int32_t)lanes[i];
     s->step_host->pos_of_row[i] = (int32_t)txns[i].pos;
     s->step_host->ctx_len[i] = (int32_t)txns[i].pos + 1;
+  }
+  {
+    int32_t *r0 = s->step_host->row0;
+    r0[0] = (int32_t)lanes[0];
+    r0[1] = (int32_t)txns[0].pos + 1;
+    r0[2] = (int32_t)txns[0].pos;
+    r0[3] = 0;
+    const uint32_t np = std::min<uint32_t>(kRow0Pages, s->max_pages);
+    const int32_t *pr = s->pt_host + (size_t)lanes[0] * s->max_pages;
+    for (uint32_t k = 0; k < np; ++k) r0[4 + k] = pr[k];
   }
   auto fail = [&](hipError_t e, const char *what) {
     (void)hipStreamSynchronize(st);
