@@ -22,6 +22,8 @@
 #include "publication.h"
 #include "runtime.h"
 #include "page_image.h"
+
+#include <map>
 #include "runtime_image.h"
 
 using gh::hip_fail;
@@ -135,11 +137,16 @@ struct glacier_hip_session {
   gk::ArgmaxResult *res_host = nullptr;
   bool inject_failure = false;
   PreparedWave prep;
-  // graph cache: key = (rows, with_head, eligible, prehead, fused attention + O)
+  // sealed step plans: key = (rows, with_head, eligible, prehead, fused
+  // attention + O). The step's launches are captured once (every host-side
+  // check and launch-shape choice made then); use_graph 1 replays the
+  // recorded kernel launches, 2 the instantiated graph.
   struct GraphEntry {
     uint32_t rows;
     bool head, elig, pre, fused;
-    hipGraphExec_t exec;
+    hipGraph_t graph;                            // kept: `launches` point into it
+    hipGraphExec_t exec;                         // use_graph 2
+    std::vector<hipKernelNodeParams> launches;   // use_graph 1, in dependency order
   };
   std::vector<GraphEntry> graphs;
 };
@@ -1036,7 +1043,10 @@ void destroy_session(glacier_hip_session *s) {
   if (s->pf_host) (void)hipHostFree(s->pf_host);
   if (s->pt_host) (void)hipHostFree(s->pt_host);
   if (s->res_host) (void)hipHostFree(s->res_host);
-  for (auto &g : s->graphs) (void)hipGraphExecDestroy(g.exec);
+  for (auto &g : s->graphs) {
+    if (g.exec) (void)hipGraphExecDestroy(g.exec);
+    if (g.graph) (void)hipGraphDestroy(g.graph);
+  }
   delete s;
 }
 
@@ -1162,6 +1172,41 @@ hipError_t upload_page_entries(glacier_hip_session *s, const std::vector<RowTxn>
   return hipSuccess;
 }
 
+// The kernel launches of a captured step in dependency order (a chain for a
+// one-stream capture); false if the graph holds any other kind of node.
+bool record_launches(hipGraph_t g, std::vector<hipKernelNodeParams> &out) {
+  size_t n = 0;
+  if (hipGraphGetNodes(g, nullptr, &n) != hipSuccess || n == 0) return false;
+  std::vector<hipGraphNode_t> nodes(n);
+  if (hipGraphGetNodes(g, nodes.data(), &n) != hipSuccess) return false;
+  std::map<hipGraphNode_t, size_t> indeg;
+  std::vector<hipGraphNode_t> ready;
+  for (hipGraphNode_t v : nodes) {
+    hipGraphNodeType t;
+    size_t d = 0;
+    if (hipGraphNodeGetType(v, &t) != hipSuccess || t != hipGraphNodeTypeKernel ||
+        hipGraphNodeGetDependencies(v, nullptr, &d) != hipSuccess)
+      return false;
+    indeg[v] = d;
+    if (d == 0) ready.push_back(v);
+  }
+  out.clear();
+  while (!ready.empty()) {
+    hipGraphNode_t v = ready.front();
+    ready.erase(ready.begin());
+    hipKernelNodeParams p{};
+    if (hipGraphKernelNodeGetParams(v, &p) != hipSuccess) return false;
+    out.push_back(p);
+    size_t m = 0;
+    if (hipGraphNodeGetDependentNodes(v, nullptr, &m) != hipSuccess) return false;
+    std::vector<hipGraphNode_t> next(m);
+    if (m && hipGraphNodeGetDependentNodes(v, next.data(), &m) != hipSuccess) return false;
+    for (hipGraphNode_t w : next)
+      if (--indeg[w] == 0) ready.push_back(w);
+  }
+  return out.size() == n;
+}
+
 // Execute one step for `count` rows; on success results are in res_host.
 int run_step(glacier_hip_session *s, const uint32_t *lanes, const uint32_t *tokens,
              uint32_t count, bool head, const uint64_t *elig_host, float *logits_host,
@@ -1209,26 +1254,43 @@ int run_step(glacier_hip_session *s, const uint32_t *lanes, const uint32_t *toke
   const bool elig = elig_host != nullptr;
   const bool pre = elig && s->head_domain == GLACIER_HIP_HEAD_DOMAIN_PREHEAD;
   const bool fused = count == 1 && txns[0].pos + 1 <= kFusedMaxCtx && attn_o_usable(s);
-  hipGraphExec_t exec = nullptr;
   if (s->opt.use_graph) {
+    glacier_hip_session::GraphEntry *plan = nullptr;
     for (auto &g : s->graphs)
       if (g.rows == count && g.head == head && g.elig == elig && g.pre == pre && g.fused == fused)
-        exec = g.exec;
-    if (!exec) {
-      hipGraph_t graph;
+        plan = &g;
+    if (!plan) {
+      glacier_hip_session::GraphEntry g{count, head, elig, pre, fused, nullptr, nullptr, {}};
       e = hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal);
       if (e != hipSuccess) return fail(e, "begin capture");
       hipError_t e2 = enqueue_step(s, (int)count, head, elig, pre, fused, st);
-      e = hipStreamEndCapture(st, &graph);
-      if (e2 != hipSuccess) return fail(e2, "capture step");
-      if (e != hipSuccess) return fail(e, "end capture");
-      e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-      (void)hipGraphDestroy(graph);
-      if (e != hipSuccess) return fail(e, "graph instantiate");
-      s->graphs.push_back({count, head, elig, pre, fused, exec});
+      e = hipStreamEndCapture(st, &g.graph);
+      if (e2 != hipSuccess || e != hipSuccess) {
+        if (g.graph) (void)hipGraphDestroy(g.graph);
+        return fail(e2 != hipSuccess ? e2 : e, e2 != hipSuccess ? "capture step" : "end capture");
+      }
+      // replay the recorded launches (use_graph 1) unless the step holds a
+      // node that is not a kernel launch; else the instantiated graph
+      if (s->opt.use_graph != 1 || !record_launches(g.graph, g.launches)) {
+        g.launches.clear();
+        e = hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+          (void)hipGraphDestroy(g.graph);
+          return fail(e, "graph instantiate");
+        }
+      }
+      s->graphs.push_back(std::move(g));
+      plan = &s->graphs.back();
     }
-    e = hipGraphLaunch(exec, st);
-    if (e != hipSuccess) return fail(e, "graph launch");
+    if (plan->exec) {
+      e = hipGraphLaunch(plan->exec, st);
+      if (e != hipSuccess) return fail(e, "graph launch");
+    } else {
+      for (const hipKernelNodeParams &p : plan->launches) {
+        e = hipLaunchKernel(p.func, p.gridDim, p.blockDim, p.kernelParams, p.sharedMemBytes, st);
+        if (e != hipSuccess) return fail(e, "plan launch");
+      }
+    }
   } else {
     e = enqueue_step(s, (int)count, head, elig, pre, fused, st);
     if (e != hipSuccess) return fail(e, "enqueue step");

@@ -806,7 +806,7 @@ class Session:
         o = SessionOptions(max_lanes=max_lanes, max_positions=max_positions,
                            total_pages=total_pages, kv_dtype=kv_dtype,
                            layer_activation=layer_activation, head_activation=head_activation,
-                           use_graph=1 if use_graph else 0, prefill_chunk=prefill_chunk,
+                           use_graph=int(use_graph), prefill_chunk=prefill_chunk,
                            split_attention_o=1 if split_attention_o else 0)
         self.h = lib().glacier_hip_session_create(model.h, C.byref(o))
         if not self.h:

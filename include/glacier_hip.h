@@ -487,7 +487,10 @@ typedef struct {
     int32_t kv_dtype;            /* GLACIER_HIP_F32 or GLACIER_HIP_F16 */
     int32_t layer_activation;    /* GLACIER_HIP_ACT_*; AUTO = reference x86 dispatch */
     int32_t head_activation;     /* usually AUTO (=> F32 for V > 65536) */
-    int32_t use_graph;           /* capture the decode step in a hipGraph */
+    int32_t use_graph;           /* sealed step plans: 0 = plan and launch every step;
+                                  * 1 = capture each step shape once and replay its
+                                  * recorded kernel launches; 2 = replay the captured
+                                  * hipGraph */
     int32_t prefill_chunk;       /* prompt rows per prefill launch sequence;
                                   * 0 = min(max_positions, 2048) */
     int32_t split_attention_o;   /* 0: a one-lane decode step at a context of up to
