@@ -81,13 +81,11 @@ struct GemvArgs {
   float *y;                 // EPI_PLAIN/RESID: [M][N]; SWIGLU: [M][N/2]
   const float *resid;       // EPI_RESID
   int epi;
-  int prefetch;             // quads in flight per wave (4 or 8); 0 = heuristic
   int ksplit_override;      // force the K split (tuning); 0 = heuristic
   int rb_override;          // row blocks per workgroup with ksplit_override
                             // (GEMM: 2 or 4 forces the row blocks per wave)
   int ksplit;               // set by launch_gemv
   int ksplit_lds_off;       // set by launch_gemv: LDS offset of the SwiGLU plane buffer
-  int force_mfma;           // use the MFMA path even for M <= 2 (tuning / tests)
   QkvArgs qkv;
   // EPI_SWIGLU only: also (or instead, with y == null) emit the SwiGLU output
   // as digit planes [G][out_D][M][32] + meta [G][M] of width N/2, ready as
@@ -139,7 +137,7 @@ struct GemvShape {
   bool lds_a;
   size_t lds_bytes;
 };
-GemvShape plan_gemv(int N, int K, int M, int D, bool small_wg = true);
+GemvShape plan_gemv(int N, int K, int M, int D);
 // The shape launch_gemv uses for these arguments (plan_gemv adjusted for
 // emitted planes / fused stages / overrides); grid = workgroup count, which
 // is also the number of ss_out partials per row. Returns false if invalid.
@@ -154,16 +152,18 @@ hipError_t launch_prep_act(const void *x, int x_bf16, const float *norm_w, float
 hipError_t launch_gemv(const GemvArgs &a, hipStream_t st);
 
 // Row counts up to this run the decode GEMV (K1, with its fused chain
-// stages); more rows run the MFMA GEMM (K2). From 6 rows on the GEMM
-// measured faster on every 7B projection (gate/up at 8 rows: 28.6 us against
-// 36.2 for the GEMV's MFMA path, at 16 rows 31.3 against 54.2); at 4 rows the
-// GEMV's batched dot4 is (27.2 against 30.0).
-constexpr int kGemvMaxRows = 5;
+// stages); more rows run the MFMA GEMM (K2). From 3 rows on the GEMM
+// chain measured faster for the whole 7B decode step (3, 4, 5 lanes: 2.22,
+// 2.27, 2.28 ms per step against 2.82, 2.91, 2.90 with the GEMV's batched
+// dot4 at up to 5 rows) and on the C2 shapes at 4 rows except the smallest
+// (11008x4096: 12.5 us against 16.2, 18944x3584: 15.2 against 17.0;
+// 4096x4096: 8.8 against 8.2).
+constexpr int kGemvMaxRows = 2;
 
 // MFMA GEMM (K2) for more than kGemvMaxRows activation rows: same arguments
 // and epilogues as launch_gemv without the GEMV-only stages (partial sums of
 // squares, fused argmax, input mode; planes only through the finishing pass,
-// gemm_emit_ok); prefetch / force_mfma are ignored. Block tile 16*mt activation rows x nt weight row blocks (16
+// gemm_emit_ok). Block tile 16*mt activation rows x nt weight row blocks (16
 // rows each), 4 waves; ks > 1 splits K over workgroups, which needs
 // splitk_ws (ks * M * N floats) and a second, fixed-order reduction kernel.
 // ksplit_override / rb_override force the splits / row blocks per wave

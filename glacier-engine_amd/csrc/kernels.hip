@@ -1,9 +1,10 @@
 // kernels.hip — hand-written gfx950 kernels for Glacier's text token loop.
 //
-//  K1  gemv_kernel     INT4 x (Q8 | f32-as-3-digit) GEMV: v_dot4_i32_i8 for one
-//                      or two rows, v_mfma_i32_16x16x32_i8 above; split-K
-//                      reduced inside the workgroup through LDS; fused
-//                      epilogues (residual, SwiGLU, RoPE + paged KV write).
+//  K1  gemv_kernel     INT4 x (Q8 | f32-as-3-digit) GEMV for one or two rows
+//                      (v_dot4_i32_i8; more rows run the GEMM, gemm.hip);
+//                      split-K reduced inside the workgroup through LDS;
+//                      fused epilogues (residual, SwiGLU, RoPE + paged KV
+//                      write, greedy candidates).
 //  K4  prep_act_kernel RMSNorm (kernels.zig:141-220) fused with the activation
 //                      quantiser (int4_matmul.zig:380-398).
 //  K3  attn_*          paged-KV GQA decode attention (split over context chunks).
@@ -133,21 +134,10 @@ hipError_t launch_prep_act(const void *x, int x_bf16, const float *norm_w, float
 // partial sums through LDS in a fixed order (deterministic, no workgroup ever
 // waits on another). Activation planes are staged in LDS when they fit.
 //
-// M <= 2 (decode): every lane dots its whole group with v_dot4_i32_i8 (exact
-// integer per group) and applies the group's f32 scales itself; the four
-// lanes of a row are summed once at the end.
-// M > 2: v_mfma_i32_16x16x32_i8 per group, B operand = k-chunk c of the
-// group gathered with one coalesced dword load per group.
-//
-// Launch shape (measured cold, weights rotated through more than the 256 MB
-// MALL): a wave owns at most 16 quads of its row block; K is split further
-// while the doubled grid stays below 4096 waves and every wave keeps >= 2
-// quads. Row blocks per workgroup fill it to 4 waves (8 when the activation
-// planes are 3 digits deep: every workgroup stages the whole plane set in
-// LDS, so fewer, larger workgroups stage less). The resident-wave budget
-// decides U: the dot4 kernel holds 6 waves/SIMD at U=4 and 4 at U=8, so a
-// grid between those two capacities (4096..6144 waves on 256 CUs) runs one
-// round at U=4 but two at U=8; elsewhere U=8 keeps more bytes in flight.
+// Every lane dots its whole group with v_dot4_i32_i8 (exact integer per
+// group) and applies the group's f32 scales itself; the four lanes of a row
+// are summed once at the end. 4 quads per wave are in flight (8 measured
+// slower on every 7B shape).
 // Activation planes are staged in LDS when they fit in 144 KB of the 160 KB
 // a gfx950 workgroup may use (the rest holds the epilogue buffers; launches
 // above 64 KB raise the kernel's dynamic-LDS limit first).
@@ -158,8 +148,7 @@ static size_t planes_bytes(int groups, int M, int D) {
   return (size_t)groups * ((size_t)D * M * 32 + (size_t)M * sizeof(ActMeta));
 }
 
-// Launch shape of the 1-2 row dot4 GEMV (and, with small_wg = false, of
-// the 3-5 row batched dot4 kernel). From cold-cache sweeps at M = 1, 2 with
+// Launch shape of the GEMV. From cold-cache sweeps at M = 1, 2 with
 // one- and three-digit planes on the 7B and C2 shapes:
 //  * K split until the grid holds about 4096 waves, keeping >= 4 quads per
 //    wave, at most 8 split waves (the 3-digit down projection, 224 row
@@ -171,10 +160,9 @@ static size_t planes_bytes(int groups, int M, int D) {
 //    within one workgroup per CU (4608x3584: 5.7 us against 6.5 with 288
 //    workgroups of 7 waves);
 //  * otherwise workgroups of about 8 waves.
-static void plan_rows2(int NB, int KQ, bool small_wg, int &ks, int &rb) {
+static void plan_rows2(int NB, int KQ, int &ks, int &rb) {
   ks = std::max(1, std::min(std::min(8, std::max(1, KQ / 4)), (4096 + NB - 1) / NB));
   rb = std::max(1, std::min(8, 8 / ks));
-  if (!small_wg) return;
   if (NB >= 512 && NB < 4096) {
     ks = std::min(ks, 4);
     rb = std::max(1, 4 / ks);
@@ -184,30 +172,18 @@ static void plan_rows2(int NB, int KQ, bool small_wg, int &ks, int &rb) {
   }
 }
 
-GemvShape plan_gemv(int N, int K, int M, int D, bool small_wg) {
+GemvShape plan_gemv(int N, int K, int M, int D) {
   GemvShape p;
   const int NB = N / 16, KQ = K / 128;
   int ks, rb;
-  if (M <= 2) {
-    plan_rows2(NB, KQ, small_wg, ks, rb);
-    p.unroll = 4;
-  } else {
-    const int max_ks = std::max(1, std::min(16, KQ / 2));
-    ks = 1;
-    while (ks * 2 <= max_ks && (KQ + ks - 1) / ks > 16) ks *= 2;
-    while (ks * 2 <= max_ks && NB * ks * 2 < 4096 && KQ >= 4 * ks) ks *= 2;
-    // at most 8 waves per workgroup: the MFMA kernel needs more than the
-    // 128 VGPRs per wave a 16-wave workgroup leaves (it spilled there)
-    ks = std::min(ks, 8);
-    rb = std::min(4, std::max(1, (D == 3 ? 8 : 4) / ks));
-    p.unroll = (ks * rb <= 4 && (long)NB * ks <= 3072) ? 8 : 4;
-  }
+  plan_rows2(NB, KQ, ks, rb);
+  p.unroll = 4;
   p.ksplit = ks;
   p.rb = rb;
   p.waves = ks * rb;
-  const size_t red = (size_t)p.waves * ((M + 15) / 16) * 4 * 64 * sizeof(float);
+  const size_t red = (size_t)p.waves * 4 * 64 * sizeof(float);
   const size_t planes = planes_bytes(K / 32, M, D) + (size_t)M * sizeof(float);
-  p.lds_a = planes <= kLdsLimit && (M <= 16 || planes <= 64 * 1024);
+  p.lds_a = planes <= kLdsLimit;
   p.lds_bytes = std::max(p.lds_a ? planes : 0, red);
   p.grid = (NB + rb - 1) / rb;
   return p;
@@ -216,10 +192,12 @@ GemvShape plan_gemv(int N, int K, int M, int D, bool small_wg) {
 // EPI >= 0: the epilogue type as a compile-time constant (so a launch only
 // carries its own epilogue's loads and branches); EPI < 0: a.epi at run time.
 // XIN: input mode (planes built in LDS from a.x_in, deferred RMSNorm).
-// MR: rows the dot4 path accumulates per lane (2, or 16 for the batched
-// dot4 path on one-digit planes).
-template <int D, int MT, int U, bool LDS_A, bool DOT4, int LB, int EPI, bool XIN, int MR = 2>
+template <int D, bool LDS_A, int LB, int EPI, bool XIN>
 __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
+  // one or two activation rows, each lane dotting its own group (dot4), U
+  // quads of weights in flight per wave
+  constexpr int MT = 1, U = 4, MR = 2;
+  constexpr bool DOT4 = true;
   const int epi = EPI >= 0 ? EPI : a.epi;
   extern __shared__ __align__(16) unsigned char smem[];
   const int lane = threadIdx.x & 63;
@@ -440,12 +418,8 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[mt][r] = 0.0f;
-  float accm[MR];  // batched dot4: per-lane sums of every row
-#pragma unroll
-  for (int m = 0; m < MR; ++m) accm[m] = 0.0f;
 
   if (nb < NB) {
-    const v4i zero = {0, 0, 0, 0};
     for (int q = 0; q < nq; q += U) {
       uint4 wc[U];
       uint32_t sc[U];
@@ -467,44 +441,7 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         if (q + u >= nq) break;
-        if constexpr (!DOT4) {
-          // MFMA: each slot is refilled as soon as it is taken, so only U + 1
-          // quads occupy registers
-          wc[u] = wb[u];
-          sc[u] = sb[u];
-          if (q + U + u < nq) {
-            wb[u] = load_stream(cp + (size_t)(q + U + u) * 64);
-            sb[u] = spp[(size_t)(q + U + u) * 64 + lane];
-          }
-        }
-        if constexpr (DOT4 && MR > 2) {
-          // batched dot4 (one-digit planes): the codes become signed once
-          // per group and serve every row; each row's dot starts from the
-          // bits of 1.5 * 2^23, so fma(that as f32, ws, -12582912 * ws) is
-          // RN(T * ws) in one instruction (|T| < 2^22)
-          const int g = (kq0 + q + u) * 4 + c;
-          const uint32_t wj[4] = {wc[u].x, wc[u].y, wc[u].z, wc[u].w};
-          int sw[8];
-#pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            const long sc2 = signed_codes(wj[w]);
-            sw[2 * w] = (int)(uint32_t)sc2;
-            sw[2 * w + 1] = (int)(uint32_t)((uint64_t)sc2 >> 32);
-          }
-          const float ws = h2f(sc[u]), wcorr = -12582912.0f * ws;
-#pragma unroll
-          for (int m = 0; m < MR; ++m) {
-            if (m >= M) break;
-            const int4 q0 = *(const int4 *)(aq + ((size_t)g * M + m) * 32);
-            const int4 q1 = *(const int4 *)(aq + ((size_t)g * M + m) * 32 + 16);
-            const int qa[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-            int t = kMagic;
-#pragma unroll
-            for (int w = 0; w < 8; ++w) t = __builtin_amdgcn_sdot4(sw[w], qa[w], t, false);
-            const float tw = fmaf(__int_as_float(t), ws, wcorr);
-            accm[m] = fmaf(tw, am[(size_t)g * M + m].scale, accm[m]);
-          }
-        } else if constexpr (DOT4) {
+        {
           // lane (j = c, n): all 32 codes of group g of row n
           const int g = (kq0 + q + u) * 4 + c;
           const uint32_t wj[4] = {wc[u].x, wc[u].y, wc[u].z, wc[u].w};
@@ -532,91 +469,12 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
             tt = tt * mm.scale;
             acc[0][m] += tt;
           }
-        } else {
-          // MFMA: one v_mfma_i32_16x16x32_i8 per (group, 16-row tile, digit)
-          // with the weights as the A operand and the activations as B, so
-          // lane (c, m) holds D[n = 4c + r][m]: one activation scale per lane
-          // and group, the weight scales of rows 4c .. 4c + 3 in one 8-byte
-          // load. The codes are signed, so D is the group dot T itself. With
-          // one digit the accumulator starts at the bits of 1.5 * 2^23: the
-          // sum read as f32 is 12582912 + T exactly (|T| < 2^22), and
-          // fma(that, ws, -12582912 * ws) = RN(T * ws) in one instruction
-          // (-12582912 * ws is exact for an fp16 ws). Three digits run
-          // independent MFMAs combined as the exact 128-adic T.
-          const uint4 wt = quad_transpose(wc[u]);
-          const uint32_t wj[4] = {wt.x, wt.y, wt.z, wt.w};
-          const v4i magic = {kMagic, kMagic, kMagic, kMagic};
-          // lane L holds the scale of slot L; pair it with slot L ^ 1, then
-          // fetch the pairs (16 j + 4 c, +1) and (16 j + 4 c + 2, +3)
-          const uint32_t sp = scale_pair(sc[u]);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int g = (kq0 + q + u) * 4 + j;  // absolute group index
-            const long b = signed_codes(wj[j]);
-            const uint32_t s01 = __builtin_amdgcn_ds_bpermute((16 * j + 4 * c) * 4, (int)sp);
-            const uint32_t s23 = __builtin_amdgcn_ds_bpermute((16 * j + 4 * c + 2) * 4, (int)sp);
-            const float ws[4] = {h2f(s01 & 0xFFFFu), h2f(s01 >> 16), h2f(s23 & 0xFFFFu),
-                                 h2f(s23 >> 16)};
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-              // activation row of this lane, clamped: columns m >= M of the
-              // tile compute a copy of row M - 1 and are never stored (no
-              // branch splits the wave around the loads)
-              const int ma = min(mt * 16 + n_local, M - 1);
-              long av[D];
-#pragma unroll
-              for (int d = 0; d < D; ++d)
-                av[d] = *(const long *)(aq + (((size_t)g * D + d) * M + ma) * 32 + c * 8);
-              const float as = am[(size_t)g * M + ma].scale;
-              if constexpr (D == 1) {
-                const v4i dd = __builtin_amdgcn_mfma_i32_16x16x32_i8(b, av[0], magic, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                  const float t = fmaf(__int_as_float(dd[r]), ws[r], -12582912.0f * ws[r]);
-                  acc[mt][r] = fmaf(t, as, acc[mt][r]);
-                }
-              } else {
-                v4i dd[D];
-#pragma unroll
-                for (int d = 0; d < D; ++d)
-                  dd[d] = __builtin_amdgcn_mfma_i32_16x16x32_i8(b, av[d], zero, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                  int T = dd[0][r];
-#pragma unroll
-                  for (int d = 1; d < D; ++d) T = (T << 7) + dd[d][r];
-                  acc[mt][r] = fmaf((float)T * ws[r], as, acc[mt][r]);
-                }
-              }
-            }
-          }
-          // keep each quad's LDS reads and MFMA results within the quad
-          // (hoisting them across quads costs occupancy)
-          __builtin_amdgcn_sched_barrier(0);
         }
       }
     }
   }
 
-  if constexpr (DOT4 && MR > 2) {
-    // accm[m] of lane (j, n) sums the groups j, j + 4, ... of row n; after
-    // adding the four lanes of the row, lane (c, n) keeps rows 4c .. 4c + 3
-    // in acc[0][r] (the epilogue's row mapping m = 4c + r)
-#pragma unroll
-    for (int m = 0; m < MR; ++m) {
-      float v = accm[m];
-      v = xor32_add(xor16_add(v));
-      accm[m] = v;
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float v = 0.0f;
-#pragma unroll
-      for (int m = r; m < MR; m += 4)
-        if (m == 4 * c + r) v = accm[m];
-      acc[0][r] = v;
-    }
-  } else if constexpr (DOT4) {
+  {
     // acc[0][m] of lane (j, n) sums the groups j, j + 4, ... of row n; add
     // the four lanes of the row so lanes j = 0 hold m = 0.. M-1 as (c=0, r=m)
 #pragma unroll
@@ -631,31 +489,7 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
   // (no early return: the SwiGLU plane epilogue below synchronises the
   // whole workgroup again)
   const bool lead = ks == 0 && nb < NB;
-  if constexpr (!DOT4) {
-    // The MFMA tiles hold D[n][m] (lane (c, m): n = 4c + r). Every wave
-    // writes them to LDS in the epilogue's layout (lane (c, n): rows
-    // m = 4c + r), and the first wave of each row block adds the K split's
-    // waves in a fixed order.
-    if (LDS_A) __syncthreads();  // the planes region is reused below
-    float *red = (float *)smem;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        red[((wave * MT + mt) * 4 + (n_local & 3)) * 64 + (n_local >> 2) * 16 + 4 * c + r] =
-            acc[mt][r];
-    __syncthreads();
-    if (ks == 0) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float tot = red[((wave * MT + mt) * 4 + r) * 64 + lane];
-          for (int s2 = 1; s2 < KS; ++s2) tot += red[(((wave + s2) * MT + mt) * 4 + r) * 64 + lane];
-          acc[mt][r] = tot;
-        }
-    }
-  } else if (KS > 1) {
+  if (KS > 1) {
     if (LDS_A) __syncthreads();  // the planes region is reused below
     float *red = (float *)smem;
 #pragma unroll
@@ -804,15 +638,12 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
 // 3..5 rows of one-digit planes that fit in LDS run the batched dot4 kernel
 // (its cost grows with every row; from 8 rows on the MFMA kernel measured
 // faster on the 7B shapes, about even at 5).
-static bool dot4_rows_ok(const GemvArgs &a, const GemvShape &p) {
-  return a.M > 2 && a.M <= 5 && a.D == 1 && p.lds_a && !a.force_mfma;
-}
-
 // Launch shape for these arguments; also fills the fields launch_gemv
 // derives (ksplit, LDS offsets). False when the arguments are invalid.
 static bool gemv_shape(GemvArgs &a, GemvShape &p) {
-  const int MT = (a.M + 15) / 16;
-  if (MT > 2 || a.N % 16 || a.K % 128 || (!a.x_in && (!a.act_q || !a.act_meta))) return false;
+  if (a.M < 1 || a.M > kGemvMaxRows || a.N % 16 || a.K % 128 ||
+      (!a.x_in && (!a.act_q || !a.act_meta)))
+    return false;
   const bool emit_planes = a.epi == EPI_SWIGLU && a.out_q;
   const bool resid_ss = a.epi == EPI_RESID && a.ss_out;
   // the workgroup must own whole 32-wide output groups (4 row blocks)
@@ -821,21 +652,10 @@ static bool gemv_shape(GemvArgs &a, GemvShape &p) {
   if (a.ss_out && (a.epi != EPI_RESID || !a.y || !a.resid)) return false;
   if (a.arg_parts && a.epi != EPI_PLAIN) return false;
   if (a.prehead && (!a.arg_parts || !a.arg_words || a.arg_word_count < (a.N + 63) / 64)) return false;
-  if (a.in_ss && (!a.x_in || a.in_ss_count <= 0 || a.in_ss_count > kMaxSsParts || a.M > 32))
-    return false;
+  if (a.in_ss && (!a.x_in || a.in_ss_count <= 0 || a.in_ss_count > kMaxSsParts)) return false;
   p = plan_gemv(a.N, a.K, a.M, a.D);
-  if (dot4_rows_ok(a, p)) {
-    // the batched dot4 kernel streams like the decode one: its launch shape
-    const GemvShape d = plan_gemv(a.N, a.K, 2, a.D, false);
-    p.ksplit = d.ksplit;
-    p.rb = d.rb;
-    p.waves = d.waves;
-    p.grid = d.grid;
-    p.unroll = 4;
-    const size_t red = (size_t)p.waves * MT * 4 * 64 * sizeof(float);
-    p.lds_bytes = std::max(planes_bytes(a.K / 32, a.M, a.D) + a.M * 4, red);
-  }
-  if (a.x_in && (a.M <= 2 || dot4_rows_ok(a, p))) {
+  const size_t red0 = (size_t)4 * 64 * sizeof(float);  // per wave
+  if (a.x_in) {
     // input mode: every workgroup quantises the whole input row, so fewer
     // workgroups than the plane-reading shapes: 8 waves with the K split for
     // short row counts (7B QKV), whole K per wave for tall ones, in
@@ -847,16 +667,16 @@ static bool gemv_shape(GemvArgs &a, GemvShape &p) {
     p.rb = NB >= 1024 && a.M == 1 ? 4 : 8 / p.ksplit;
     p.waves = p.ksplit * p.rb;
     p.grid = (NB + p.rb - 1) / p.rb;
-    const size_t red = (size_t)p.waves * MT * 4 * 64 * sizeof(float);
-    p.lds_bytes = std::max(p.lds_a ? planes_bytes(a.K / 32, a.M, a.D) + a.M * 4 : 0, red);
+    p.lds_bytes = std::max(p.lds_a ? planes_bytes(a.K / 32, a.M, a.D) + a.M * 4 : 0,
+                           p.waves * red0);
   }
   if (emit_planes && p.rb % 4) {
     p.rb = 4;
     while (p.ksplit * p.rb > 16) p.ksplit /= 2;
     p.waves = p.ksplit * p.rb;
     p.grid = (a.N / 16 + p.rb - 1) / p.rb;
-    const size_t red = (size_t)p.waves * MT * 4 * 64 * sizeof(float);
-    p.lds_bytes = std::max(p.lds_a ? planes_bytes(a.K / 32, a.M, a.D) + a.M * 4 : 0, red);
+    p.lds_bytes = std::max(p.lds_a ? planes_bytes(a.K / 32, a.M, a.D) + a.M * 4 : 0,
+                           p.waves * red0);
   }
   if (a.ksplit_override > 0) {
     if (a.arg_parts) return false;
@@ -865,24 +685,9 @@ static bool gemv_shape(GemvArgs &a, GemvShape &p) {
     p.waves = p.ksplit * p.rb;
     if (p.waves > 16 || p.ksplit > a.K / 128) return false;
     p.grid = (a.N / 16 + p.rb - 1) / p.rb;
-    const size_t red = (size_t)p.waves * MT * 4 * 64 * sizeof(float);
-    p.lds_bytes = std::max(p.lds_a ? planes_bytes(a.K / 32, a.M, a.D) + a.M * 4 : 0, red);
+    p.lds_bytes = std::max(p.lds_a ? planes_bytes(a.K / 32, a.M, a.D) + a.M * 4 : 0,
+                           p.waves * red0);
     if (emit_planes && p.rb % 4) return false;
-  }
-  if ((a.M > 2 || a.force_mfma) && !dot4_rows_ok(a, p) && p.waves > 8) {
-    // the MFMA kernel runs at most 8 waves per workgroup (VGPR budget)
-    if (a.ksplit_override > 0) return false;
-    while (p.ksplit > 1 && p.ksplit * p.rb > 8) p.ksplit /= 2;
-    if (p.ksplit * p.rb > 8) return false;
-    p.waves = p.ksplit * p.rb;
-    const size_t red = (size_t)p.waves * MT * 4 * 64 * sizeof(float);
-    p.lds_bytes = std::max(p.lds_a ? planes_bytes(a.K / 32, a.M, a.D) + a.M * 4 : 0, red);
-  }
-  if (dot4_rows_ok(a, p) && p.waves > 8) {
-    // the batched dot4 kernel runs at most 8 waves per workgroup
-    while (p.ksplit > 1 && p.ksplit * p.rb > 8) p.ksplit /= 2;
-    if (p.ksplit * p.rb > 8) return false;
-    p.waves = p.ksplit * p.rb;
   }
   // input mode: the planes are built in LDS, so they must fit there
   if (a.x_in && !p.lds_a) return false;
@@ -908,18 +713,9 @@ hipError_t launch_gemv(const GemvArgs &a0, hipStream_t st) {
   GemvArgs a = a0;
   GemvShape p;
   if (!gemv_shape(a, p)) return hipErrorInvalidValue;
-  const int MT = (a.M + 15) / 16;
   dim3 grid(p.grid), block(64 * p.waves);
-  const bool dot4 = a.M <= 2 && !a.force_mfma;
-  const bool dot4_rows = dot4_rows_ok(a, p);
   const bool small = p.waves <= 4;
-  // U = 8 (quads in flight per wave) only for the MFMA kernel with small
-  // workgroups: it needs more than the 128 VGPRs a 1024-thread workgroup
-  // allows; the dot4 decode kernel measured best at U = 4
-  int U = a.prefetch ? a.prefetch : p.unroll;
-  if (U != 8 || dot4 || !small) U = 4;
   const size_t lds = p.lds_bytes;
-#define GK_KERNEL(DD, MM, UU, LL, T4, LBB, EE, XX) gemv_kernel<DD, MM, UU, LL, T4, LBB, EE, XX>
 #define GK_LAUNCH(KERNEL)                                                                       \
   do {                                                                                          \
     if (lds > 64 * 1024)                                                                        \
@@ -927,53 +723,32 @@ hipError_t launch_gemv(const GemvArgs &a0, hipStream_t st) {
                                 (int)lds);                                                      \
     hipLaunchKernelGGL(KERNEL, grid, block, lds, st, a);                                        \
   } while (0)
-  // dot4 workgroups up to 16 waves; MFMA workgroups up to 8 (VGPR budget)
-#define GK_GO(DD, MM, UU, LL, T4, EE, XX)                                                           \
+  // workgroups of up to 4 waves (256-thread bound) or up to 16 (1024)
+#define GK_GO(DD, LL, EE, XX)                                                                   \
   do {                                                                                          \
-    if (small) GK_LAUNCH((GK_KERNEL(DD, MM, UU, LL, T4, 256, EE, XX)));                          \
-    else GK_LAUNCH((GK_KERNEL(DD, MM, UU, LL, T4, ((T4) ? 1024 : 512), EE, XX)));               \
+    if (small) GK_LAUNCH((gemv_kernel<DD, LL, 256, EE, XX>));                                   \
+    else GK_LAUNCH((gemv_kernel<DD, LL, 1024, EE, XX>));                                        \
   } while (0)
-  // dot4 (decode) launches carry their epilogue type at compile time
+  // the epilogue type is a template parameter
 #define GK_DOT4(DD, LL, XX)                                                \
   do {                                                                     \
     switch (a.epi) {                                                       \
-      case EPI_PLAIN: GK_GO(DD, 1, 4, LL, true, EPI_PLAIN, XX); break;     \
-      case EPI_RESID: GK_GO(DD, 1, 4, LL, true, EPI_RESID, XX); break;     \
-      case EPI_SWIGLU: GK_GO(DD, 1, 4, LL, true, EPI_SWIGLU, XX); break;   \
-      default: GK_GO(DD, 1, 4, LL, true, EPI_QKV, XX); break;              \
+      case EPI_PLAIN: GK_GO(DD, LL, EPI_PLAIN, XX); break;                 \
+      case EPI_RESID: GK_GO(DD, LL, EPI_RESID, XX); break;                 \
+      case EPI_SWIGLU: GK_GO(DD, LL, EPI_SWIGLU, XX); break;               \
+      default: GK_GO(DD, LL, EPI_QKV, XX); break;                          \
     }                                                                      \
   } while (0)
-#define GK_DOT4_ROWS(XX)                                                                          \
-  do {                                                                                           \
-    switch (a.epi) {                                                                             \
-      case EPI_PLAIN: GK_LAUNCH((gemv_kernel<1, 1, 4, true, true, 512, EPI_PLAIN, XX, 16>)); break;   \
-      case EPI_RESID: GK_LAUNCH((gemv_kernel<1, 1, 4, true, true, 512, EPI_RESID, XX, 16>)); break;   \
-      case EPI_SWIGLU: GK_LAUNCH((gemv_kernel<1, 1, 4, true, true, 512, EPI_SWIGLU, XX, 16>)); break; \
-      default: GK_LAUNCH((gemv_kernel<1, 1, 4, true, true, 512, EPI_QKV, XX, 16>)); break;            \
-    }                                                                                            \
-  } while (0)
-#define GK_PATH(DD, LL, XX)                                                                      \
-  do {                                                                                          \
-    if (MT == 2) GK_GO(DD, 2, 4, LL, false, -1, XX);                                            \
-    else if (dot4) GK_DOT4(DD, LL, XX);                                                         \
-    else if (U == 8 && small) GK_LAUNCH((GK_KERNEL(DD, 1, 8, LL, false, 256, -1, XX)));       \
-    else GK_GO(DD, 1, 4, LL, false, -1, XX);                                                    \
-  } while (0)
-  if (dot4_rows) {
-    if (a.x_in) GK_DOT4_ROWS(true); else GK_DOT4_ROWS(false);
-  } else if (a.x_in) {
-    if (a.D == 1) GK_PATH(1, true, true); else GK_PATH(3, true, true);
+  if (a.x_in) {
+    if (a.D == 1) GK_DOT4(1, true, true); else GK_DOT4(3, true, true);
   } else if (a.D == 1) {
-    if (p.lds_a) GK_PATH(1, true, false); else GK_PATH(1, false, false);
+    if (p.lds_a) GK_DOT4(1, true, false); else GK_DOT4(1, false, false);
   } else {
-    if (p.lds_a) GK_PATH(3, true, false); else GK_PATH(3, false, false);
+    if (p.lds_a) GK_DOT4(3, true, false); else GK_DOT4(3, false, false);
   }
 #undef GK_DOT4
-#undef GK_DOT4_ROWS
-#undef GK_PATH
 #undef GK_GO
 #undef GK_LAUNCH
-#undef GK_KERNEL
   return hipGetLastError();
 }
 

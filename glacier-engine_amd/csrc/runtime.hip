@@ -545,10 +545,8 @@ static int gemv_launch(glacier_hip_context *ctx, glacier_hip_int4_weight *w, con
   a.epi = gk::EPI_PLAIN;
   // up to kGemvMaxRows rows: the decode GEMV (K1); more: the MFMA GEMM (K2),
   // with a workspace for its K split (grown on demand, capped at 64 MiB;
-  // a smaller one only lowers the split). Three-digit planes go to the GEMM
-  // from 3 rows: the GEMV's MFMA path for them measured slower there (7B
-  // down at 4 rows 31.8 us against 21.1, LM head 123.8 against ~100)
-  if (m <= (uint32_t)gk::kGemvMaxRows && (D == 1 || m <= 2)) {
+  // a smaller one only lowers the split)
+  if (m <= (uint32_t)gk::kGemvMaxRows) {
     GH_CHECK(ctx, gk::launch_gemv(a, st));
     return GLACIER_HIP_OK;
   }

@@ -284,9 +284,9 @@ int glacier_hip_live_command_count(glacier_hip_context *ctx, uint64_t *out);
 /* Device-resident batched projection: y[m][out_f] = x[m][in_f] W^T
  * (+ bias[out_f]), m in 1..GLACIER_HIP_MAX_ROWS. x is f32 or bf16 (x_dtype),
  * y is f32. Replaces linearInt4WeightQ8 / linearInt4Weight
- * (int4_matmul.zig:422-531, 2957-2981) for one projection over m rows: Q8
- * activations up to 5 rows and F32 ones up to 2 rows run the decode GEMV;
- * more rows (decode batches, prompt chunks, the packed batch of
+ * (int4_matmul.zig:422-531, 2957-2981) for one projection over m rows: up
+ * to 2 rows run the decode GEMV; more rows (decode batches, prompt chunks,
+ * the packed batch of
  * forwardLayerPackedBatch, generate.zig:2105) the MFMA GEMM; both compute
  * every row with the same per-group arithmetic. Asynchronous on `stream`;
  * each stream has its own activation planes and split-K workspace (grown on
@@ -615,7 +615,7 @@ int glacier_hip_session_page_generation(glacier_hip_session *s, uint32_t lane,
 /* Head domain of eligible steps (GreedyOutputMode, generate.zig:415-426):
  * POSTHEAD computes every logit, then applies the mask (domain_posthead);
  * PREHEAD applies it before the head's dot products: a 16-row block with no
- * eligible row for any lane of a fused-head step (up to 5 lanes) streams no
+ * eligible row for any lane of a fused-head step (up to 2 lanes) streams no
  * weights (domain_prehead). Tokens are identical; in PREHEAD an eligible step
  * cannot return logits (INVALID_ARGUMENT). Wider steps scan full logits. */
 #define GLACIER_HIP_HEAD_DOMAIN_POSTHEAD 0

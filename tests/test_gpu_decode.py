@@ -355,9 +355,8 @@ def test_eligible_step_matches_masked_argmax(gh, tiny, ora):
 @pytest.mark.parametrize("lanes", [2, 4, 20])
 def test_fused_head_argmax_matches_logit_scan(gh, tiny, ora, lanes):
     """The LM head reduces its logits to per-workgroup candidates and a
-    one-block merge picks the token (dot4 head at 2 rows, MFMA head at 4;
-    past 5 rows the GEMM writes the logits and the separate argmax scans
-    them): the token equals the oracle's (eligible) argmax over the logits
+    one-block merge picks the token (the GEMV head at 1-2 rows; from 3 rows
+    the GEMM writes the logits and the separate argmax scans them): the token equals the oracle's (eligible) argmax over the logits
     the same step returns, for dense, sparse, first-only and last-only
     masks."""
     host, om, m = tiny

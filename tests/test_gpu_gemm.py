@@ -1,4 +1,4 @@
-"""GPU parity of the MFMA GEMM (K2: projections over more than 5 rows, and
+"""GPU parity of the MFMA GEMM (K2: projections over more than 2 rows, and
 3-digit ones from 3 rows; 16-row tiles up to 16 rows, 32-row tiles up to 32
 with K split over workgroups, 64-row tiles above)
 against the CPU oracle, through the C ABI (glacier_hip_int4_gemv with

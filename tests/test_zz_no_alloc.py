@@ -1,7 +1,7 @@
 """glacier_hip_int4_gemv_noalloc (the GEMV entry point that allocates
 nothing: its planes and split-K partial sums live in a fixed per-GPU array)
 against glacier_hip_int4_gemv, through the C ABI, on two calls in a row with
-the second smaller, for the GEMV (<= 5 rows) and GEMM (split-K) paths in Q8
+the second smaller, for the GEMV (<= 2 rows) and GEMM (split-K) paths in Q8
 and f32 activation modes. Bars as the GEMV tests: Q8 2e-6, f32 1e-5 of
 max |y| (the two entry points run the same kernels; only a K split may
 differ). The context's device bytes do not move across the calls."""
