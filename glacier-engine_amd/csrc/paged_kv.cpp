@@ -49,6 +49,7 @@ void Cache::init(uint64_t L, uint64_t d, uint64_t seq) {
   const size_t pages = (seq + kPagePositions - 1) / kPagePositions;
   page_of.assign(pages, -1);
   page_gen.assign(pages, 0);
+  page_payload_bytes = L * 2 * kPagePositions * d * 4;  // f32 rows unless the owner says otherwise
   active = false;
 }
 
@@ -66,6 +67,7 @@ void Cache::release(PagePool &pool) {
 void Cache::start(PagePool &pool) {
   release(pool);
   active = true;
+  retired = false;
   instance = next_cache_instance();
   len = 0;
   next_page_generation = 1;
@@ -88,7 +90,7 @@ uint32_t Cache::pages_needed(uint32_t n) const {
 int Cache::begin(uint32_t lane, uint32_t n, PagePool &pool, std::vector<RowTxn> &out) {
   // validateNextRowState (paged_kv_cache.zig:1386-1419), for every row
   // before any state changes
-  if (!active || n == 0) return GLACIER_HIP_INVALID_TRANSACTION;
+  if (!active || retired || n == 0) return GLACIER_HIP_INVALID_TRANSACTION;
   if (staged) return GLACIER_HIP_TRANSACTION_ACTIVE;
   if (len + n > max_seq) return GLACIER_HIP_CACHE_FULL;
   if (root.committed_len != len || root.cache_instance != instance) return GLACIER_HIP_INVALID_TRANSACTION;
@@ -151,7 +153,7 @@ int Cache::begin(uint32_t lane, uint32_t n, PagePool &pool, std::vector<RowTxn> 
   return GLACIER_HIP_OK;
 }
 
-static bool same_mark(const Mark &a, const Mark &b) { return memcmp(&a, &b, sizeof a) == 0; }
+bool same_mark(const Mark &a, const Mark &b) { return memcmp(&a, &b, sizeof a) == 0; }
 
 int Cache::commit(const RowTxn *txns, size_t n) {
   // commitPreparedAssumeValid (:1122-1135) after prepareCommit's checks
@@ -192,7 +194,7 @@ int Cache::abort(const RowTxn *txns, size_t n) {
 
 int Cache::reset() {
   // reset (:1162-1182): every page ref and root becomes stale, payloads stay
-  if (!active) return GLACIER_HIP_INVALID_TRANSACTION;
+  if (!active || retired) return GLACIER_HIP_INVALID_TRANSACTION;
   if (staged) return GLACIER_HIP_TRANSACTION_ACTIVE;
   for (auto &g : page_gen) g = 0;
   root = Root{};
@@ -216,16 +218,15 @@ int Cache::validate_page_ref(const glacier_hip_page_ref_t &ref) const {
 }
 
 void Cache::ledger(glacier_hip_kv_resident_ledger_t *o) const {
-  // allocationCommitmentLedger (:840-892) with f32 payload accounting
+  // allocationCommitmentLedger (:840-892)
   memset(o, 0, sizeof *o);
-  uint64_t allocated = 0;
-  for (int32_t p : page_of) allocated += p >= 0;
+  const uint64_t allocated = allocated_pages();
   uint64_t provisional = 0;
   // a staged row that installed a page holds it provisionally
   if (staged)
     for (uint64_t pos = len; pos < len + staged; ++pos)
       if (pos % kPagePositions == 0) ++provisional;
-  const uint64_t page_payload = layers * 2 * kPagePositions * dim * 4;
+  const uint64_t page_payload = page_payload_bytes;
   o->page_count_capacity = page_of.size();
   o->allocated_pages = allocated;
   o->committed_pages = root.committed_pages;
@@ -234,7 +235,99 @@ void Cache::ledger(glacier_hip_kv_resident_ledger_t *o) const {
   o->page_map_bytes = page_of.size() * 16;
   o->resident_tensor_payload_bytes = allocated * page_payload;
   o->resident_allocation_bytes = o->page_map_bytes + o->resident_tensor_payload_bytes;
-  o->committed_tensor_payload_bytes = layers * 2 * len * dim * 4;
+  o->committed_tensor_payload_bytes = layers * 2 * len * dim * (page_payload / (layers * 2 * kPagePositions * dim));
+}
+
+uint64_t Cache::allocated_pages() const {
+  uint64_t n = 0;
+  for (int32_t p : page_of) n += p >= 0;
+  return n;
+}
+
+int Cache::plan_next_row(glacier_hip_row_allocation_plan_t *o) const {
+  // planNextRowAllocation (:962-990) after validateNextRowState (:1386-1419)
+  if (retired) return GLACIER_HIP_LEASE_CACHE_RETIRED;
+  if (!active) return GLACIER_HIP_LEASE_INVALID_TRANSACTION;
+  if (staged) return GLACIER_HIP_LEASE_TRANSACTION_ACTIVE;
+  if (len >= max_seq) return GLACIER_HIP_LEASE_CACHE_FULL;
+  if (root.committed_len != len || root.cache_instance != instance) return GLACIER_HIP_LEASE_INVALID_ROOT;
+  const uint64_t p = len / kPagePositions, row = len % kPagePositions;
+  if (p >= page_of.size()) return GLACIER_HIP_LEASE_CACHE_FULL;
+  if (root.committed_pages != p + (row != 0)) return GLACIER_HIP_LEASE_INVALID_ROOT;
+  const bool installs = row == 0;
+  if (installs ? page_gen[p] != 0 : (page_of[p] < 0 || page_gen[p] == 0))
+    return GLACIER_HIP_LEASE_INVALID_ROOT;
+  memset(o, 0, sizeof *o);
+  o->abi_version = 0x4750415000000001ull;  // row_allocation_plan_abi
+  o->cache_id = (uint64_t)(uintptr_t)this;
+  o->cache_instance = instance;
+  o->base_len = len;
+  o->logical_page = p;
+  o->row_in_page = row;
+  o->root_generation = root.generation;
+  o->row_txn_generation = next_row_txn_generation;
+  o->root_after_generation = next_root_generation;
+  o->page_ownership_generation = page_gen[p];
+  o->next_page_ownership_generation = next_page_generation;
+  o->allocated_pages = allocated_pages();
+  o->page_payload_present = page_of[p] >= 0;
+  o->allocation_bytes = installs && page_of[p] < 0 ? page_payload_bytes : 0;
+  return GLACIER_HIP_LEASE_OK;
+}
+
+int Cache::plan_retirement(RetirePlan *o) const {
+  // planRetirementReclaim (:1187-1214) with validateRetirementCommitment:
+  // committed pages own payload and a generation, later pages own none
+  if (retired) return GLACIER_HIP_LEASE_CACHE_RETIRED;
+  if (!active) return GLACIER_HIP_LEASE_INVALID_TRANSACTION;
+  if (staged) return GLACIER_HIP_LEASE_TRANSACTION_ACTIVE;
+  if (root.cache_instance != instance || root.committed_len != len ||
+      root.committed_pages != (len + kPagePositions - 1) / kPagePositions)
+    return GLACIER_HIP_LEASE_INVALID_ROOT;
+  for (size_t p = 0; p < page_of.size(); ++p) {
+    const bool committed = p < root.committed_pages;
+    if (committed ? (page_of[p] < 0 || page_gen[p] == 0) : page_gen[p] != 0)
+      return GLACIER_HIP_LEASE_INVALID_ROOT;
+  }
+  *o = RetirePlan{};
+  o->cache_id = (uint64_t)(uintptr_t)this;
+  o->cache_instance = instance;
+  o->root = root;
+  o->committed_len = len;
+  o->allocated_pages = allocated_pages();
+  o->page_payload_bytes = page_payload_bytes;
+  o->payload_bytes_to_free = o->allocated_pages * page_payload_bytes;
+  o->next_root_generation = next_root_generation;
+  return GLACIER_HIP_LEASE_OK;
+}
+
+int Cache::reclaim_retired(const RetirePlan &plan, PagePool &pool, uint64_t *freed_bytes) {
+  // reclaimRetiredAfterCommit (:1216-1250)
+  RetirePlan want;
+  if (int rc = plan_retirement(&want)) return rc;
+  if (memcmp(&want, &plan, sizeof plan) != 0) return GLACIER_HIP_LEASE_INVALID_TRANSACTION;
+  for (auto &p : page_of)
+    if (p >= 0) {
+      pool.free.push_back(p);
+      p = -1;
+    }
+  for (auto &g : page_gen) g = 0;
+  root = Root{};
+  root.abi_version = kPageMapRootAbi;
+  root.cache_instance = instance;
+  root.generation = next_root_generation++;
+  empty_ownership_digest(instance, layers, dim, max_seq, root.ownership_sha256);
+  len = 0;
+  retired = true;
+  *freed_bytes = plan.payload_bytes_to_free;
+  return GLACIER_HIP_LEASE_OK;
+}
+
+bool Cache::claim_leased(uint64_t inst, uintptr_t owner) {
+  if (!inst || !owner || retired || leased_instance || leased_owner) return false;
+  leased_instance = inst;
+  leased_owner = owner;
+  return true;
 }
 
 }  // namespace gpk
@@ -244,11 +337,35 @@ void Cache::ledger(glacier_hip_kv_resident_ledger_t *o) const {
 // row transaction the sessions run for their lanes, for hosts that stage rows
 // themselves and for tests.
 // ---------------------------------------------------------------------------
-struct glacier_hip_kv_pages {
-  gpk::PagePool pool;
-  gpk::Cache cache;
-  std::vector<gpk::RowTxn> staged;
-};
+namespace gpk {
+// logicalKvSha256 (paged_kv_cache.zig:1347-1350, hashLogicalPrefix :1532-1555)
+// of a host page map's committed rows.
+int host_kv_sha256(const glacier_hip_kv_pages *p, uint8_t out[32]) {
+  const Cache &c = p->cache;
+  if (c.retired) return GLACIER_HIP_LEASE_CACHE_RETIRED;
+  const size_t L = c.layers, d = c.dim;
+  gh::Sha256 h;
+  h.update("glacier-logical-kv-state-v1\0", 28);
+  h.u64(L);
+  h.u64(d);
+  h.u64(c.len);
+  for (size_t l = 0; l < L; ++l)
+    for (int v = 0; v < 2; ++v)
+      for (uint64_t pos = 0; pos < c.len; ++pos) {
+        const int32_t phys = c.page_of[pos / kPagePositions];
+        if (phys < 0) return GLACIER_HIP_LEASE_INVALID_ROOT;
+        const float *row = p->rows.data() +
+                           ((((size_t)phys * L + l) * 2 + v) * kPagePositions + pos % kPagePositions) * d;
+        for (size_t i = 0; i < d; ++i) {
+          uint32_t b;
+          memcpy(&b, row + i, 4);
+          h.u32(b);
+        }
+      }
+  h.final(out);
+  return GLACIER_HIP_LEASE_OK;
+}
+}  // namespace gpk
 
 extern "C" {
 
@@ -260,7 +377,34 @@ glacier_hip_kv_pages *glacier_hip_kv_pages_create(uint32_t num_layers, uint32_t 
   p->pool.init(pool_pages);
   p->cache.init(num_layers, kv_dim, max_seq);
   p->cache.start(p->pool);
+  p->rows.assign((size_t)pool_pages * num_layers * 2 * gpk::kPagePositions * kv_dim, 0.f);
   return p;
+}
+
+int glacier_hip_kv_pages_append_row(glacier_hip_kv_pages *p, const glacier_hip_row_txn_mark_t *mark,
+                                    uint32_t layer, const float *k, const float *v) {
+  // appendRowTxn (paged_kv_cache.zig:1074-1103): the staged row's K and V at one layer
+  if (!p || !mark || !k || !v) return GLACIER_HIP_INVALID_ARGUMENT;
+  if (p->staged.size() != 1 || !gpk::same_mark(p->staged[0].mark, *mark))
+    return GLACIER_HIP_INVALID_TRANSACTION;
+  if (layer >= p->cache.layers) return GLACIER_HIP_SHAPE_MISMATCH;
+  const gpk::RowTxn &t = p->staged[0];
+  const size_t L = p->cache.layers, d = p->cache.dim, r = t.pos % gpk::kPagePositions;
+  float *base = p->rows.data() + (((size_t)t.page * L + layer) * 2) * gpk::kPagePositions * d;
+  memcpy(base + r * d, k, d * 4);
+  memcpy(base + (gpk::kPagePositions + r) * d, v, d * 4);
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_kv_pages_kv_sha256(glacier_hip_kv_pages *p, uint8_t out[32]) {
+  if (!p || !out) return GLACIER_HIP_INVALID_ARGUMENT;
+  return gpk::host_kv_sha256(p, out) ? GLACIER_HIP_INVALID_TRANSACTION : GLACIER_HIP_OK;
+}
+
+int glacier_hip_kv_pages_is_retired(glacier_hip_kv_pages *p, int32_t *out) {
+  if (!p || !out) return GLACIER_HIP_INVALID_ARGUMENT;
+  *out = p->cache.retired;
+  return GLACIER_HIP_OK;
 }
 
 void glacier_hip_kv_pages_destroy(glacier_hip_kv_pages *p) { delete p; }

@@ -64,6 +64,14 @@ struct RowTxn {
   Root before{}, after{};
 };
 
+// RetirementReclaimPlanV1 (paged_kv_cache.zig:135-146)
+struct RetirePlan {
+  uint64_t cache_id = 0, cache_instance = 0;
+  Root root{};
+  uint64_t committed_len = 0, allocated_pages = 0, page_payload_bytes = 0;
+  uint64_t payload_bytes_to_free = 0, next_root_generation = 0;
+};
+
 class Cache {
  public:
   void init(uint64_t layers, uint64_t dim, uint64_t max_seq);
@@ -86,6 +94,21 @@ class Cache {
 
   int validate_page_ref(const glacier_hip_page_ref_t &ref) const;
   void ledger(glacier_hip_kv_resident_ledger_t *out) const;
+  uint64_t allocated_pages() const;
+
+  // planNextRowAllocation (paged_kv_cache.zig:962-990): the next row's page
+  // and the payload bytes it would take from the pool; lease status codes.
+  int plan_next_row(glacier_hip_row_allocation_plan_t *out) const;
+  // planRetirementReclaim (:1187-1214) / reclaimRetiredAfterCommit
+  // (:1216-1250): every payload goes back to the pool, the root becomes an
+  // empty one under a fresh generation and the map is retired for good.
+  int plan_retirement(RetirePlan *out) const;
+  int reclaim_retired(const RetirePlan &plan, PagePool &pool, uint64_t *freed_bytes);
+  // claimLeasedCoordinator / isLeasedCoordinator (:910-932)
+  bool claim_leased(uint64_t instance, uintptr_t owner);
+  bool is_leased(uint64_t instance, uintptr_t owner) const {
+    return instance && owner && leased_instance == instance && leased_owner == owner;
+  }
 
   bool active = false;
   uint64_t instance = 0, len = 0, layers = 0, dim = 0, max_seq = 0;
@@ -94,6 +117,25 @@ class Cache {
   std::vector<uint64_t> page_gen;  // ownership generation (0 = not owned)
   Root root{};
   uint32_t staged = 0;             // rows begun and not yet committed / aborted
+  uint64_t page_payload_bytes = 0; // one page's K and V rows over every layer
+  bool retired = false;
+  uint64_t leased_instance = 0;    // the lease coordinator that owns the map
+  uintptr_t leased_owner = 0;
 };
 
+bool same_mark(const Mark &a, const Mark &b);
+
+}  // namespace gpk
+
+// A host page map with its own pool (no device), behind glacier_hip_kv_pages_*.
+struct glacier_hip_kv_pages {
+  gpk::PagePool pool;
+  gpk::Cache cache;
+  std::vector<gpk::RowTxn> staged;
+  std::vector<float> rows;  // [pool page][layer][K, V][16][kv_dim], written by append_row
+};
+
+namespace gpk {
+// logicalKvSha256 of a host page map's committed rows; lease status codes.
+int host_kv_sha256(const glacier_hip_kv_pages *p, uint8_t out[32]);
 }  // namespace gpk

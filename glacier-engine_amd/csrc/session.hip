@@ -18,6 +18,7 @@
 
 #include "host_util.h"
 #include "lane_weave.h"
+#include "leased_kv.h"
 #include "paged_kv.h"
 #include "publication.h"
 #include "runtime.h"
@@ -61,6 +62,7 @@ struct Lane {
   bool chain_init = false;
   uint8_t chain[32] = {};
   bool retired = false;           // a terminal token was published
+  glacier_hip_leased_kv *lease = nullptr;  // page payloads charged through a LeaseTree
 };
 
 // A staged publication wave between step_prepare and commit / abort.
@@ -1031,6 +1033,12 @@ hipError_t enqueue_step(glacier_hip_session *s, int rows, bool head, bool elig, 
 }
 
 void destroy_session(glacier_hip_session *s) {
+  for (Lane &ln : s->lanes)
+    if (ln.lease) {  // the coordinator outlives the lane: every later call on it is refused
+      ln.lease->lease.orphan();
+      ln.lease->detach = nullptr;
+      ln.lease = nullptr;
+    }
   void *ptrs[] = {s->kv_pool, s->page_table, s->rope_cos, s->rope_sin, s->x_res, s->h, s->q,
                   s->attn, s->act, s->logits, s->act_q, s->act_meta, s->act_q2, s->act_meta2,
                   s->att_scratch, s->ss_parts, s->o_parts, s->o_counters, s->arg_scratch,
@@ -1090,9 +1098,18 @@ void abort_rows(glacier_hip_session *s, std::vector<RowTxn> &txns) {
   // payloads stay with their logical pages and the consumed generations are
   // not handed back
   for_lane_runs(txns, [&](uint32_t lane, const RowTxn *t, size_t n) {
+    if (s->lanes[lane].lease) s->lanes[lane].lease->lease.end_rows();
     return s->lanes[lane].kv.abort(t, n);
   });
   txns.clear();
+}
+
+// A lease refusing a step's new pages, in the session's status domain.
+int lease_refusal(int rc) {
+  return rc == GLACIER_HIP_LEASE_CAPACITY_EXCEEDED || rc == GLACIER_HIP_LEASE_INVALID_CLAIM ||
+                 rc == GLACIER_HIP_LEASE_NODES_EXHAUSTED || rc == GLACIER_HIP_LEASE_CLAIM_OVERFLOW
+             ? GLACIER_HIP_OUT_OF_MEMORY
+             : GLACIER_HIP_INVALID_TRANSACTION;
 }
 
 void note_installs(glacier_hip_session *s, const std::vector<RowTxn> &txns) {
@@ -1113,12 +1130,26 @@ int begin_rows(glacier_hip_session *s, const uint32_t *lanes, uint32_t count,
     need += kv.pages_needed(1);
   }
   if (need > s->pool.free.size()) return GLACIER_HIP_CACHE_FULL;
+  // leased lanes: every new page payload is charged before any map takes one
+  for (uint32_t i = 0; i < count; ++i) {
+    glacier_hip_leased_kv *l = s->lanes[lanes[i]].lease;
+    if (!l) continue;
+    if (int rc = l->lease.reserve_rows(1)) {
+      for (uint32_t j = 0; j < i; ++j)
+        if (s->lanes[lanes[j]].lease) s->lanes[lanes[j]].lease->lease.settle_rows(false);
+      return lease_refusal(rc);
+    }
+  }
   for (uint32_t i = 0; i < count; ++i) {
     const int rc = s->lanes[lanes[i]].kv.begin(lanes[i], 1, s->pool, txns);
+    glacier_hip_leased_kv *l = s->lanes[lanes[i]].lease;
     if (rc) {
+      for (uint32_t j = i; j < count; ++j)
+        if (s->lanes[lanes[j]].lease) s->lanes[lanes[j]].lease->lease.settle_rows(false);
       abort_rows(s, txns);
       return rc;
     }
+    if (l) l->lease.settle_rows(true);
   }
   note_installs(s, txns);
   return GLACIER_HIP_OK;
@@ -1129,7 +1160,11 @@ int begin_rows(glacier_hip_session *s, const uint32_t *lanes, uint32_t count,
 // per-token transactions would (generate.zig:5080-5118 commits per token).
 int begin_chunk(glacier_hip_session *s, uint32_t lane, uint32_t n, std::vector<RowTxn> &txns) {
   txns.clear();
+  glacier_hip_leased_kv *l = s->lanes[lane].lease;
+  if (l)
+    if (int rc = l->lease.reserve_rows(n)) return lease_refusal(rc);
   const int rc = s->lanes[lane].kv.begin(lane, n, s->pool, txns);
+  if (l) l->lease.settle_rows(rc == GLACIER_HIP_OK);
   if (rc) return rc;
   note_installs(s, txns);
   return GLACIER_HIP_OK;
@@ -1137,6 +1172,7 @@ int begin_chunk(glacier_hip_session *s, uint32_t lane, uint32_t n, std::vector<R
 
 int commit_rows(glacier_hip_session *s, std::vector<RowTxn> &txns) {
   const int rc = for_lane_runs(txns, [&](uint32_t lane, const RowTxn *t, size_t n) {
+    if (s->lanes[lane].lease) s->lanes[lane].lease->lease.end_rows();
     return s->lanes[lane].kv.commit(t, n);
   });
   txns.clear();
@@ -1530,6 +1566,9 @@ static glacier_hip_session *session_create_impl(glacier_hip_model *m,
   s->pool.init(s->total_pages);
   for (auto &ln : s->lanes)
     ln.kv.init(c.num_layers, (uint64_t)c.num_kv_heads * c.head_dim, opts->max_positions);
+  for (auto &ln : s->lanes)
+    ln.kv.page_payload_bytes = (uint64_t)c.num_layers * 2 * 16 * c.num_kv_heads * c.head_dim *
+                               (opts->kv_dtype == GLACIER_HIP_F16 ? 2 : 4);
   s->prefill_chunk = opts->prefill_chunk ? (uint32_t)opts->prefill_chunk
                                          : std::min<uint32_t>(opts->max_positions, 2048);
   s->rows_cap = std::max(opts->max_lanes, s->prefill_chunk);
@@ -1680,6 +1719,7 @@ int glacier_hip_session_lane_begin(glacier_hip_session *s, uint32_t lane, uint64
   if (lane >= s->lanes.size()) return GLACIER_HIP_INVALID_ARGUMENT;
   GH_SUBMISSION(s->model->ctx);
   if (s->prep.active) return GLACIER_HIP_TRANSACTION_ACTIVE;
+  if (s->lanes[lane].lease) return GLACIER_HIP_INVALID_TRANSACTION;  // one request per lease
   reset_lane(s, s->lanes[lane], seed);
   return GLACIER_HIP_OK;
 }
@@ -1946,6 +1986,7 @@ int glacier_hip_session_restore_checkpoint(glacier_hip_session *s, uint32_t lane
   const auto &c = s->model->cfg;
   const uint64_t L = c.num_layers, kvd = (uint64_t)c.num_kv_heads * c.head_dim;
   Lane &ln = s->lanes[lane];
+  if (ln.lease) return GLACIER_HIP_INVALID_TRANSACTION;
   // the restore target is a fresh request (PagedKVCache.initForCheckpoint)
   reset_lane(s, ln, seed);
   auto reject = [&](uint32_t e) {
@@ -2289,4 +2330,53 @@ extern "C" int glacier_hip_session_lane_weave_wave(
                                                     rc == GLACIER_HIP_SCHEDULER_POISONED); ++i)
     tokens_by_lane[lanes[i]] = next[i];
   return rc;
+}
+
+// ---------------------------------------------------------------------------
+// Leased lanes (leased_paged_kv_cache.zig over a device session lane)
+// ---------------------------------------------------------------------------
+namespace {
+void detach_lane(glacier_hip_leased_kv *c) {
+  auto *s = (glacier_hip_session *)c->owner;
+  if (!s || c->lane >= s->lanes.size()) return;
+  Lane &ln = s->lanes[c->lane];
+  if (ln.lease != c) return;
+  ln.lease = nullptr;
+  ln.kv.leased_instance = 0;  // the lane may start a new request
+  ln.kv.leased_owner = 0;
+}
+}  // namespace
+
+extern "C" int glacier_hip_leased_kv_create_for_lane(
+    glacier_hip_lease_bank *b, glacier_hip_lease_tree_t *tree, const glacier_hip_lease_node_t *scope,
+    glacier_hip_session *s, uint32_t lane, glacier_hip_page_lease_binding_t *bindings,
+    uint32_t binding_count, uint64_t request_epoch, uint64_t session_id, uint64_t *sequence,
+    glacier_hip_leased_kv **out) {
+  if (!b || !tree || !scope || !s || !bindings || !sequence || !out || lane >= s->lanes.size())
+    return GLACIER_HIP_LEASE_INVALID_ARGUMENT;
+  GH_SUBMISSION(s->model->ctx);
+  Lane &ln = s->lanes[lane];
+  if (s->prep.active || ln.lease || !ln.kv.active) return GLACIER_HIP_LEASE_INVALID_COORDINATOR;
+  auto *c = new (std::nothrow) glacier_hip_leased_kv();
+  if (!c) return GLACIER_HIP_LEASE_INVALID_CONFIGURATION;
+  glb::Target t;
+  t.cache = &ln.kv;
+  t.pool = &s->pool;
+  t.kv_sha256 = [s, lane](uint8_t o[32]) {
+    if (s->lanes[lane].kv.retired) return (int)GLACIER_HIP_LEASE_CACHE_RETIRED;
+    return logical_kv_sha256(s, lane, o) ? (int)GLACIER_HIP_LEASE_DEVICE_ERROR
+                                         : (int)GLACIER_HIP_LEASE_OK;
+  };
+  const int rc = c->lease.init(&b->bank, tree, *scope, t, bindings, binding_count, request_epoch,
+                               session_id, sequence);
+  if (rc) {
+    delete c;
+    return rc;
+  }
+  c->owner = s;
+  c->lane = lane;
+  c->detach = detach_lane;
+  ln.lease = c;
+  *out = c;
+  return GLACIER_HIP_LEASE_OK;
 }

@@ -198,6 +198,112 @@ class LaneEvent(C.Structure):
         [("bank_used_before", Claim), ("bank_used_after", Claim)]
 
 
+# ---- leased paged KV (glacier_hip_lease_* / glacier_hip_leased_kv_*) ---------
+LEASE_STATUS = ["OK", "InvalidArgument", "InvalidConfiguration", "InvalidClaim", "ClaimOverflow",
+                "CapacityExceeded", "ReservationSlotsExhausted", "LeaseNodesExhausted",
+                "StaleReservation", "InvalidTransition", "InvalidCoordinator",
+                "InvalidBindingStorage", "InvalidBinding", "InvalidLeasedPlan",
+                "InvalidLeasedTransaction", "AlreadyTerminal", "TerminalRequired",
+                "InvalidTerminalSeal", "ReclaimPending", "ReclaimComplete", "InvalidFreedPayload",
+                "InvalidRoot", "CacheRetired", "OutOfMemory", "CacheFull", "TransactionActive",
+                "InvalidTransaction", "DeviceError"]
+
+
+class LeaseTree(C.Structure):
+    _fields_ = [("abi_version", C.c_uint64), ("parent", BankReceipt)] + \
+        [(n, C.c_uint64) for n in ("tree_key", "authority_key", "identity_generation", "generation",
+                                   "structural_revision")] + \
+        [("ceiling", Claim), ("current", Claim), ("active_nodes", C.c_uint32),
+         ("reserved0", C.c_uint32), ("state_digest", C.c_uint64), ("integrity", C.c_uint64)]
+
+
+class LeaseNode(C.Structure):
+    _fields_ = [("abi_version", C.c_uint64), ("parent", BankReceipt), ("tree_key", C.c_uint64),
+                ("tree_identity_generation", C.c_uint64), ("node_index", C.c_uint32),
+                ("reserved0", C.c_uint32), ("generation", C.c_uint64),
+                ("parent_index", C.c_uint32), ("reserved1", C.c_uint32)] + \
+        [(n, C.c_uint64) for n in ("parent_generation", "node_key", "tenant_key", "binding_key")] + \
+        [("kind", C.c_uint32), ("reserved2", C.c_uint32), ("ceiling", Claim), ("claim", Claim),
+         ("integrity", C.c_uint64)]
+
+
+class LeaseBankSnapshot(C.Structure):
+    _fields_ = [("used", Claim), ("peak", Claim)] + [(n, C.c_uint64) for n in (
+        "peak_host_bytes", "active_reservations", "committed_receipts", "active_lease_trees",
+        "active_lease_scopes", "active_lease_nodes", "reserved_unmaterialized_allocations",
+        "live_allocations", "quiescing_allocations", "free_authorized_allocations",
+        "successful_reservations", "successful_commits", "cancellations", "releases",
+        "rejected_capacity", "rejected_slots", "lease_tree_opens", "lease_scope_opens",
+        "lease_allocation_reserves", "lease_allocation_materializations", "lease_allocation_aborts",
+        "lease_reclaim_prepares", "lease_reclaim_authorizations", "lease_reclaim_cancels",
+        "lease_reclaim_commits", "lease_tree_closes", "rejected_lease_capacity",
+        "rejected_lease_nodes")]
+
+
+class PageLeaseBinding(C.Structure):
+    _fields_ = [("abi_version", C.c_uint64), ("state", C.c_uint32), ("has_leaf", C.c_uint32),
+                ("cache_instance", C.c_uint64), ("logical_page", C.c_uint64),
+                ("payload_bytes", C.c_uint64), ("scope_index", C.c_uint32),
+                ("reserved0", C.c_uint32), ("scope_generation", C.c_uint64), ("leaf", LeaseNode),
+                ("integrity", C.c_uint64)]
+
+
+class BindingSummary(C.Structure):
+    _fields_ = [("count", C.c_uint32), ("reserved0", C.c_uint32), ("payload_bytes", C.c_uint64),
+                ("digest", C.c_uint8 * 32)]
+
+
+class RowAllocationPlan(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in (
+        "abi_version", "cache_id", "cache_instance", "base_len", "logical_page", "row_in_page",
+        "root_generation", "row_txn_generation", "root_after_generation",
+        "page_ownership_generation", "next_page_ownership_generation", "allocated_pages")] + \
+        [("page_payload_present", C.c_uint32), ("reserved0", C.c_uint32),
+         ("allocation_bytes", C.c_uint64)]
+
+
+class LeasedRowPlan(C.Structure):
+    _fields_ = [("abi_version", C.c_uint64), ("coordinator_instance", C.c_uint64),
+                ("tree", LeaseTree), ("publication_sequence", C.c_uint64),
+                ("cache_plan", RowAllocationPlan), ("bindings", BindingSummary),
+                ("integrity", C.c_uint64)]
+
+
+class LeasedRowTxn(C.Structure):
+    _fields_ = [("abi_version", C.c_uint64), ("coordinator_instance", C.c_uint64),
+                ("generation", C.c_uint64), ("mark", RowTxnMark),
+                ("installed_new_binding", C.c_uint32), ("reserved0", C.c_uint32),
+                ("bindings_digest", C.c_uint8 * 32), ("integrity", C.c_uint64)]
+
+
+class TerminalSeal(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("abi_version", "coordinator_instance", "cache_id",
+                                          "cache_instance")] + \
+        [("scope_index", C.c_uint32), ("reserved0", C.c_uint32)] + \
+        [(n, C.c_uint64) for n in ("scope_generation", "tree_identity_generation",
+                                   "tree_generation", "tree_structural_revision",
+                                   "tree_state_digest")] + \
+        [("root", PageMapRoot), ("logical_kv_sha256", C.c_uint8 * 32),
+         ("bindings", BindingSummary), ("transaction_sequence", C.c_uint64),
+         ("terminal_reason", C.c_uint32), ("terminal_token", C.c_uint32),
+         ("generation", C.c_uint64), ("digest", C.c_uint8 * 32)]
+
+
+class FreedPayload(C.Structure):
+    _fields_ = [("abi_version", C.c_uint64), ("coordinator_instance", C.c_uint64),
+                ("generation", C.c_uint64), ("terminal_seal_digest", C.c_uint8 * 32),
+                ("permit_generation", C.c_uint64), ("root_before", PageMapRoot),
+                ("root_after", PageMapRoot), ("binding_count", C.c_uint32),
+                ("reserved0", C.c_uint32), ("payload_bytes", C.c_uint64),
+                ("bindings_digest", C.c_uint8 * 32), ("integrity", C.c_uint64)]
+
+
+class ReclaimReceipt(C.Structure):
+    _fields_ = [("abi_version", C.c_uint64), ("coordinator_instance", C.c_uint64),
+                ("generation", C.c_uint64), ("freed", FreedPayload), ("tree_after", LeaseTree),
+                ("integrity", C.c_uint64)]
+
+
 _LW = [C.POINTER(LaneEvent)]
 
 PUBLICATION_WIDTH = 4
@@ -495,6 +601,54 @@ _SIGS = [
      [_P, C.POINTER(GlrtRecord), C.c_uint32, C.POINTER(_P), C.POINTER(C.c_uint64)]),
     ("glacier_hip_glrt_identity", C.c_int, [_P, _P, C.POINTER(C.c_uint64)]),
     ("glacier_hip_model_load_glrt", _P, [_P, _P, C.POINTER(GlrtLoadReport)]),
+    ("glacier_hip_lease_bank_create", _P, [C.c_uint32, C.c_uint32, C.POINTER(Limits), C.c_uint64]),
+    ("glacier_hip_lease_bank_destroy", None, [_P]),
+    ("glacier_hip_lease_bank_reserve", C.c_int,
+     [_P, C.c_uint64, C.POINTER(Claim), C.POINTER(BankReceipt)]),
+    ("glacier_hip_lease_bank_commit", C.c_int, [_P, C.POINTER(BankReceipt), C.POINTER(BankReceipt)]),
+    ("glacier_hip_lease_bank_cancel", C.c_int, [_P, C.POINTER(BankReceipt)]),
+    ("glacier_hip_lease_bank_release", C.c_int, [_P, C.POINTER(BankReceipt)]),
+    ("glacier_hip_lease_tree_open", C.c_int,
+     [_P, C.POINTER(BankReceipt), C.c_uint64, C.c_uint64, C.POINTER(Claim), C.POINTER(LeaseTree)]),
+    ("glacier_hip_lease_scope_open", C.c_int,
+     [_P, C.POINTER(LeaseTree), C.c_uint64, C.c_uint64, C.POINTER(Claim), C.POINTER(LeaseNode)]),
+    ("glacier_hip_lease_tree_close", C.c_int, [_P, C.POINTER(LeaseTree)]),
+    ("glacier_hip_lease_tree_validate", C.c_int, [_P, C.POINTER(LeaseTree)]),
+    ("glacier_hip_lease_node_validate", C.c_int, [_P, C.POINTER(LeaseTree), C.POINTER(LeaseNode)]),
+    ("glacier_hip_lease_session_bind", C.c_int, [_P, C.POINTER(LeaseTree), C.c_uint64, C.c_uint64]),
+    ("glacier_hip_lease_session_close", C.c_int,
+     [_P, C.POINTER(BankReceipt), C.c_uint64, C.c_uint64, C.c_uint64]),
+    ("glacier_hip_lease_bank_snapshot", C.c_int, [_P, C.POINTER(LeaseBankSnapshot)]),
+    ("glacier_hip_leased_kv_create", C.c_int,
+     [_P, C.POINTER(LeaseTree), C.POINTER(LeaseNode), _P, C.POINTER(PageLeaseBinding), C.c_uint32,
+      C.c_uint64, C.c_uint64, C.POINTER(C.c_uint64), C.POINTER(_P)]),
+    ("glacier_hip_leased_kv_create_for_lane", C.c_int,
+     [_P, C.POINTER(LeaseTree), C.POINTER(LeaseNode), _P, C.c_uint32, C.POINTER(PageLeaseBinding),
+      C.c_uint32, C.c_uint64, C.c_uint64, C.POINTER(C.c_uint64), C.POINTER(_P)]),
+    ("glacier_hip_leased_kv_destroy", None, [_P]),
+    ("glacier_hip_leased_kv_plan_next_row", C.c_int, [_P, C.POINTER(LeasedRowPlan)]),
+    ("glacier_hip_leased_kv_begin_row", C.c_int,
+     [_P, C.POINTER(LeasedRowPlan), C.POINTER(LeasedRowTxn)]),
+    ("glacier_hip_leased_kv_commit_row", C.c_int,
+     [_P, C.POINTER(LeasedRowTxn), C.POINTER(PageMapRoot)]),
+    ("glacier_hip_leased_kv_abort_row", C.c_int, [_P, C.POINTER(LeasedRowTxn)]),
+    ("glacier_hip_leased_kv_binding_summary", C.c_int, [_P, C.POINTER(BindingSummary)]),
+    ("glacier_hip_leased_kv_lifecycle", C.c_int, [_P, C.POINTER(C.c_uint32)]),
+    ("glacier_hip_leased_kv_root", C.c_int, [_P, C.POINTER(PageMapRoot)]),
+    ("glacier_hip_leased_kv_kv_sha256", C.c_int, [_P, _P]),
+    ("glacier_hip_leased_kv_seal_terminal", C.c_int,
+     [_P, C.POINTER(PageMapRoot), _P, C.c_uint64, C.c_uint32, C.c_uint32,
+      C.POINTER(TerminalSeal)]),
+    ("glacier_hip_leased_kv_begin_reclaim", C.c_int,
+     [_P, C.POINTER(TerminalSeal), C.c_uint64, C.POINTER(FreedPayload)]),
+    ("glacier_hip_leased_kv_commit_reclaim", C.c_int,
+     [_P, C.POINTER(FreedPayload), C.POINTER(ReclaimReceipt)]),
+    ("glacier_hip_leased_kv_reclaim_for_teardown", C.c_int, [_P, C.c_uint64]),
+    ("glacier_hip_kv_pages_append_row", C.c_int,
+     [_P, C.POINTER(RowTxnMark), C.c_uint32, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
+    ("glacier_hip_kv_pages_kv_sha256", C.c_int, [_P, _P]),
+    ("glacier_hip_kv_pages_is_retired", C.c_int, [_P, C.POINTER(C.c_int32)]),
+    ("glacier_hip_kv_pages_set_pool_capacity", C.c_int, [_P, C.c_uint32]),
 ]
 
 _lib = None
@@ -991,6 +1145,22 @@ class KvPages:
         check(lib().glacier_hip_kv_pages_ledger(self.h, C.byref(led)), "kv_pages_ledger")
         return {n: getattr(led, n) for n, _ in ResidentLedger._fields_}
 
+    def page_count(self):
+        return self.ledger()["page_count_capacity"]
+
+    def kv_sha256(self):
+        b = (C.c_uint8 * 32)()
+        check(lib().glacier_hip_kv_pages_kv_sha256(self.h, b), "kv_pages_kv_sha256")
+        return bytes(b)
+
+    def is_retired(self):
+        v = C.c_int32()
+        check(lib().glacier_hip_kv_pages_is_retired(self.h, C.byref(v)), "kv_pages_is_retired")
+        return bool(v.value)
+
+    def set_pool_capacity(self, pages):
+        return lib().glacier_hip_kv_pages_set_pool_capacity(self.h, pages)
+
     def close(self):
         if self.h:
             lib().glacier_hip_kv_pages_destroy(self.h)
@@ -1100,3 +1270,203 @@ class LaneWeave:
         out = (C.c_uint8 * 32)()
         check(lib().glacier_hip_lane_weave_chain_head(self.h, out), "chain_head")
         return bytes(out)
+
+
+class LeaseError(Exception):
+    """A lease verb's status, by the reference's error name (e.g. 'InvalidBinding')."""
+
+    def __init__(self, code, what):
+        self.code = code
+        self.reason = LEASE_STATUS[code] if 0 <= code < len(LEASE_STATUS) else f"status {code}"
+        super().__init__(f"{what}: {self.reason}")
+
+
+def lease_check(rc, what):
+    if rc != 0:
+        raise LeaseError(rc, what)
+
+
+def make_claim(**kw):
+    c = Claim()
+    for k, v in kw.items():
+        setattr(c, k, v)
+    return c
+
+
+def make_limits(**kw):
+    lim = Limits(*([2**64 - 1] * len(Limits._fields_)))
+    for k, v in kw.items():
+        setattr(lim, k, v)
+    return lim
+
+
+class LeaseBank:
+    """ResourceBank receipts with LeaseTree page ownership (glacier_hip_lease_*)."""
+
+    def __init__(self, slots, nodes, epoch, **limits):
+        self.h = lib().glacier_hip_lease_bank_create(slots, nodes, C.byref(make_limits(**limits)),
+                                                     epoch)
+        if not self.h:
+            raise LeaseError(1, "lease_bank_create")
+
+    def reserve(self, owner_key, **claim):
+        r = BankReceipt()
+        lease_check(lib().glacier_hip_lease_bank_reserve(self.h, owner_key,
+                                                         C.byref(make_claim(**claim)), C.byref(r)),
+                    "reserve")
+        return r
+
+    def commit(self, reservation):
+        r = BankReceipt()
+        lease_check(lib().glacier_hip_lease_bank_commit(self.h, C.byref(reservation), C.byref(r)),
+                    "commit")
+        return r
+
+    def release(self, receipt):
+        lease_check(lib().glacier_hip_lease_bank_release(self.h, C.byref(receipt)), "release")
+
+    def open_tree(self, receipt, tree_key, authority_key, **ceiling):
+        t = LeaseTree()
+        lease_check(lib().glacier_hip_lease_tree_open(self.h, C.byref(receipt), tree_key,
+                                                      authority_key, C.byref(make_claim(**ceiling)),
+                                                      C.byref(t)), "open_tree")
+        return t
+
+    def open_scope(self, tree, scope_key, tenant_key, **ceiling):
+        """Adds a scope; `tree` (a LeaseTree) is replaced in place."""
+        n = LeaseNode()
+        lease_check(lib().glacier_hip_lease_scope_open(self.h, C.byref(tree), scope_key, tenant_key,
+                                                       C.byref(make_claim(**ceiling)), C.byref(n)),
+                    "open_scope")
+        return n
+
+    def close_tree(self, tree):
+        lease_check(lib().glacier_hip_lease_tree_close(self.h, C.byref(tree)), "close_tree")
+
+    def validate_tree(self, tree):
+        return lib().glacier_hip_lease_tree_validate(self.h, C.byref(tree))
+
+    def bind_session(self, tree, request_epoch, session_id):
+        lease_check(lib().glacier_hip_lease_session_bind(self.h, C.byref(tree), request_epoch,
+                                                         session_id), "bind_session")
+
+    def close_session(self, receipt, request_epoch, session_id, next_sequence):
+        lease_check(lib().glacier_hip_lease_session_close(self.h, C.byref(receipt), request_epoch,
+                                                          session_id, next_sequence),
+                    "close_session")
+
+    def snapshot(self):
+        s = LeaseBankSnapshot()
+        lease_check(lib().glacier_hip_lease_bank_snapshot(self.h, C.byref(s)), "snapshot")
+        out = {n: getattr(s, n) for n, _ in LeaseBankSnapshot._fields_[2:]}
+        out["used"] = {n: getattr(s.used, n) for n in CLAIM_FIELDS}
+        out["peak"] = {n: getattr(s.peak, n) for n in CLAIM_FIELDS}
+        return out
+
+    def close(self):
+        if self.h:
+            lib().glacier_hip_lease_bank_destroy(self.h)
+            self.h = None
+
+    __del__ = close
+
+
+class LeasedKV:
+    """One lane's page map leased through a LeaseTree (glacier_hip_leased_kv_*).
+    `tree` and `sequence` are the cohort's shared cells (a LeaseTree and a
+    ctypes c_uint64); `bindings` is created here, one entry per logical page."""
+
+    def __init__(self, bank, tree, scope, target, request_epoch, session_id, sequence, lane=None,
+                 binding_count=None):
+        self.bank, self.tree, self.sequence, self.target = bank, tree, sequence, target
+        n = binding_count if binding_count is not None else target.page_count()
+        self.bindings = (PageLeaseBinding * max(n, 1))()
+        self.h = _P()
+        if lane is None:
+            rc = lib().glacier_hip_leased_kv_create(bank.h, C.byref(tree), C.byref(scope), target.h,
+                                                    self.bindings, n, request_epoch, session_id,
+                                                    C.byref(sequence), C.byref(self.h))
+        else:
+            rc = lib().glacier_hip_leased_kv_create_for_lane(
+                bank.h, C.byref(tree), C.byref(scope), target.h, lane, self.bindings, n,
+                request_epoch, session_id, C.byref(sequence), C.byref(self.h))
+        lease_check(rc, "leased_kv_create")
+
+    def plan_next_row(self):
+        p = LeasedRowPlan()
+        lease_check(lib().glacier_hip_leased_kv_plan_next_row(self.h, C.byref(p)), "plan_next_row")
+        return p
+
+    def begin_row(self, plan):
+        t = LeasedRowTxn()
+        lease_check(lib().glacier_hip_leased_kv_begin_row(self.h, C.byref(plan), C.byref(t)),
+                    "begin_row")
+        return t
+
+    def commit_row(self, txn):
+        r = PageMapRoot()
+        lease_check(lib().glacier_hip_leased_kv_commit_row(self.h, C.byref(txn), C.byref(r)),
+                    "commit_row")
+        return r
+
+    def abort_row(self, txn):
+        lease_check(lib().glacier_hip_leased_kv_abort_row(self.h, C.byref(txn)), "abort_row")
+
+    def append_row(self, txn, layer, k, v):
+        kk = (C.c_float * len(k))(*k)
+        vv = (C.c_float * len(v))(*v)
+        check(lib().glacier_hip_kv_pages_append_row(self.target.h, C.byref(txn.mark), layer, kk, vv),
+              "append_row")
+
+    def binding_summary(self):
+        s = BindingSummary()
+        lease_check(lib().glacier_hip_leased_kv_binding_summary(self.h, C.byref(s)),
+                    "binding_summary")
+        return s
+
+    def lifecycle(self):
+        v = C.c_uint32()
+        lease_check(lib().glacier_hip_leased_kv_lifecycle(self.h, C.byref(v)), "lifecycle")
+        return ["live", "terminal_retained", "freed_pending_uncharge", "reclaimed"][v.value]
+
+    def root(self):
+        r = PageMapRoot()
+        lease_check(lib().glacier_hip_leased_kv_root(self.h, C.byref(r)), "root")
+        return r
+
+    def kv_sha256(self):
+        b = (C.c_uint8 * 32)()
+        lease_check(lib().glacier_hip_leased_kv_kv_sha256(self.h, b), "kv_sha256")
+        return bytes(b)
+
+    def seal_terminal(self, root, kv_sha256, sequence, reason, token):
+        s = TerminalSeal()
+        kv = (C.c_uint8 * 32)(*kv_sha256)
+        lease_check(lib().glacier_hip_leased_kv_seal_terminal(self.h, C.byref(root), kv, sequence,
+                                                              reason, token, C.byref(s)),
+                    "seal_terminal")
+        return s
+
+    def begin_reclaim(self, seal, expected_sequence):
+        f = FreedPayload()
+        lease_check(lib().glacier_hip_leased_kv_begin_reclaim(self.h, C.byref(seal),
+                                                              expected_sequence, C.byref(f)),
+                    "begin_reclaim")
+        return f
+
+    def commit_reclaim(self, freed):
+        r = ReclaimReceipt()
+        lease_check(lib().glacier_hip_leased_kv_commit_reclaim(self.h, C.byref(freed), C.byref(r)),
+                    "commit_reclaim")
+        return r
+
+    def reclaim_for_teardown(self, expected_sequence):
+        lease_check(lib().glacier_hip_leased_kv_reclaim_for_teardown(self.h, expected_sequence),
+                    "reclaim_for_teardown")
+
+    def close(self):
+        if self.h:
+            lib().glacier_hip_leased_kv_destroy(self.h)
+            self.h = None
+
+    __del__ = close

@@ -1098,6 +1098,292 @@ void glacier_hip_synth_tokens(uint64_t seed, uint64_t tensor_id, uint32_t vocab,
 uint64_t glacier_hip_synth_tensor_id(uint32_t layer, uint32_t which);
 float glacier_hip_f16_to_f32(uint16_t h);
 
+/* ---- leased paged KV: page payloads charged through a LeaseTree ----------
+ * The reference's LeaseTree-backed page ownership (leased_paged_kv_cache.zig)
+ * over its ResourceBank (core/resource_bank.zig). A lease bank holds
+ * receipt slots (reserve :976-1044, commit :1046-1076, release :3166-3184)
+ * and a LeaseTree per committed receipt: a tree (openLeaseTree :1368-1446)
+ * carries zero-charge scopes, one per lane (openLeaseScope :1448-1514), and
+ * one allocation leaf per live page payload. A leaf is reserved and charged
+ * before the page map takes the payload (reserveAllocationsForSession
+ * :1534-1783), settled once it has (commitAllocationsAfterAllocate
+ * :1785-1823) or uncharged if it could not (abortAllocationsAfterFree
+ * :1909-1956). Terminal reclaim retires a whole scope (beginRetireSubtree
+ * :2227-2343, authorizeFree :2383-2452), frees the payloads, then uncharges
+ * (commitFreeAfterAllocatorFree :2454-2502). Publication sessions bind a
+ * request epoch and session id to a receipt and hand out one permit per
+ * sequence number (bindPublicationSessionWithLeaseTree :2731-2750,
+ * beginPublicationWithLeaseTree :2938-2960, commitPublicationAssumeValid
+ * :3076-3089, closePublicationSession :3104-3124).
+ *
+ * Tokens (tree, node, receipt) are values the caller passes back; every
+ * field must equal the bank's current state (a stale copy is rejected with
+ * GLACIER_HIP_LEASE_STALE_RESERVATION). Integrity words are this library's
+ * own keyed mixes of the token fields; they are not part of the reference's
+ * published formats. Every lease verb returns a glacier_hip_lease_status. */
+enum glacier_hip_lease_status {
+    GLACIER_HIP_LEASE_OK = 0,
+    GLACIER_HIP_LEASE_INVALID_ARGUMENT = 1,       /* NULL pointer / zero count */
+    /* resource_bank.zig:43-53 */
+    GLACIER_HIP_LEASE_INVALID_CONFIGURATION = 2,
+    GLACIER_HIP_LEASE_INVALID_CLAIM = 3,
+    GLACIER_HIP_LEASE_CLAIM_OVERFLOW = 4,
+    GLACIER_HIP_LEASE_CAPACITY_EXCEEDED = 5,
+    GLACIER_HIP_LEASE_SLOTS_EXHAUSTED = 6,        /* ReservationSlotsExhausted */
+    GLACIER_HIP_LEASE_NODES_EXHAUSTED = 7,        /* LeaseNodesExhausted */
+    GLACIER_HIP_LEASE_STALE_RESERVATION = 8,
+    GLACIER_HIP_LEASE_INVALID_TRANSITION = 9,
+    /* leased_paged_kv_cache.zig:37-51 */
+    GLACIER_HIP_LEASE_INVALID_COORDINATOR = 10,
+    GLACIER_HIP_LEASE_INVALID_BINDING_STORAGE = 11,
+    GLACIER_HIP_LEASE_INVALID_BINDING = 12,
+    GLACIER_HIP_LEASE_INVALID_LEASED_PLAN = 13,
+    GLACIER_HIP_LEASE_INVALID_LEASED_TRANSACTION = 14,
+    GLACIER_HIP_LEASE_ALREADY_TERMINAL = 15,
+    GLACIER_HIP_LEASE_TERMINAL_REQUIRED = 16,
+    GLACIER_HIP_LEASE_INVALID_TERMINAL_SEAL = 17,
+    GLACIER_HIP_LEASE_RECLAIM_PENDING = 18,
+    GLACIER_HIP_LEASE_RECLAIM_COMPLETE = 19,
+    GLACIER_HIP_LEASE_INVALID_FREED_PAYLOAD = 20,
+    /* the page map's errors (paged_kv_cache.zig) */
+    GLACIER_HIP_LEASE_INVALID_ROOT = 21,
+    GLACIER_HIP_LEASE_CACHE_RETIRED = 22,
+    GLACIER_HIP_LEASE_OUT_OF_MEMORY = 23,         /* no free payload in the pool */
+    GLACIER_HIP_LEASE_CACHE_FULL = 24,
+    GLACIER_HIP_LEASE_TRANSACTION_ACTIVE = 25,
+    GLACIER_HIP_LEASE_INVALID_TRANSACTION = 26,
+    GLACIER_HIP_LEASE_DEVICE_ERROR = 27,          /* a session lane's KV read failed */
+};
+
+typedef struct {
+    uint64_t abi_version;        /* 0x474c545200000001 */
+    glacier_hip_bank_receipt_t parent;
+    uint64_t tree_key, authority_key, identity_generation, generation, structural_revision;
+    glacier_hip_claim_t ceiling, current;
+    uint32_t active_nodes, reserved0;
+    uint64_t state_digest, integrity;
+} glacier_hip_lease_tree_t;        /* LeaseTreeV1 (resource_bank.zig:296-312) */
+
+enum { GLACIER_HIP_LEASE_NODE_SCOPE = 0, GLACIER_HIP_LEASE_NODE_ALLOCATION = 1 };
+typedef struct {
+    uint64_t abi_version;        /* 0x474c4e4400000001 */
+    glacier_hip_bank_receipt_t parent;
+    uint64_t tree_key, tree_identity_generation;
+    uint32_t node_index, reserved0;
+    uint64_t generation;
+    uint32_t parent_index, reserved1;   /* 0xffffffff for a scope */
+    uint64_t parent_generation, node_key, tenant_key, binding_key;
+    uint32_t kind, reserved2;
+    glacier_hip_claim_t ceiling, claim;
+    uint64_t integrity;
+} glacier_hip_lease_node_t;        /* LeaseNodeV1 (resource_bank.zig:314-330) */
+
+typedef struct {
+    glacier_hip_claim_t used, peak;
+    uint64_t peak_host_bytes, active_reservations, committed_receipts;
+    uint64_t active_lease_trees, active_lease_scopes, active_lease_nodes;
+    uint64_t reserved_unmaterialized_allocations, live_allocations;
+    uint64_t quiescing_allocations, free_authorized_allocations;
+    uint64_t successful_reservations, successful_commits, cancellations, releases;
+    uint64_t rejected_capacity, rejected_slots;
+    uint64_t lease_tree_opens, lease_scope_opens, lease_allocation_reserves;
+    uint64_t lease_allocation_materializations, lease_allocation_aborts;
+    uint64_t lease_reclaim_prepares, lease_reclaim_authorizations, lease_reclaim_cancels;
+    uint64_t lease_reclaim_commits, lease_tree_closes;
+    uint64_t rejected_lease_capacity, rejected_lease_nodes;
+} glacier_hip_lease_bank_snapshot_t;  /* SnapshotV3's accounting fields (resource_bank.zig:703-754) */
+
+typedef struct glacier_hip_lease_bank glacier_hip_lease_bank;
+/* Bank.initWithLeaseTree (:929-974): `slot_count` receipt slots, one tree
+ * root per slot, `node_count` lease nodes shared by every tree. */
+glacier_hip_lease_bank *glacier_hip_lease_bank_create(uint32_t slot_count, uint32_t node_count,
+                                                      const glacier_hip_limits_t *limits,
+                                                      uint64_t epoch);
+void glacier_hip_lease_bank_destroy(glacier_hip_lease_bank *b);
+/* reserve (:976-1044) then commit (:1046-1076); cancel (:1078-1095) a reservation. */
+int glacier_hip_lease_bank_reserve(glacier_hip_lease_bank *b, uint64_t owner_key,
+                                   const glacier_hip_claim_t *claim,
+                                   glacier_hip_bank_receipt_t *reservation_out);
+int glacier_hip_lease_bank_commit(glacier_hip_lease_bank *b,
+                                  const glacier_hip_bank_receipt_t *reservation,
+                                  glacier_hip_bank_receipt_t *receipt_out);
+int glacier_hip_lease_bank_cancel(glacier_hip_lease_bank *b,
+                                  const glacier_hip_bank_receipt_t *reservation);
+/* release (:3166-3184): no publication session, no live tree. */
+int glacier_hip_lease_bank_release(glacier_hip_lease_bank *b, const glacier_hip_bank_receipt_t *receipt);
+int glacier_hip_lease_tree_open(glacier_hip_lease_bank *b, const glacier_hip_bank_receipt_t *receipt,
+                                uint64_t tree_key, uint64_t authority_key,
+                                const glacier_hip_claim_t *ceiling, glacier_hip_lease_tree_t *tree_out);
+/* Adds a scope; *tree is replaced by the tree after the change. */
+int glacier_hip_lease_scope_open(glacier_hip_lease_bank *b, glacier_hip_lease_tree_t *tree,
+                                 uint64_t scope_key, uint64_t tenant_key,
+                                 const glacier_hip_claim_t *ceiling, glacier_hip_lease_node_t *scope_out);
+/* closeLeaseTree (:2582-2622): only empty scopes left, session unbound. */
+int glacier_hip_lease_tree_close(glacier_hip_lease_bank *b, const glacier_hip_lease_tree_t *tree);
+int glacier_hip_lease_tree_validate(glacier_hip_lease_bank *b, const glacier_hip_lease_tree_t *tree);
+int glacier_hip_lease_node_validate(glacier_hip_lease_bank *b, const glacier_hip_lease_tree_t *tree,
+                                    const glacier_hip_lease_node_t *node);
+int glacier_hip_lease_session_bind(glacier_hip_lease_bank *b, const glacier_hip_lease_tree_t *tree,
+                                   uint64_t request_epoch, uint64_t session_id);
+int glacier_hip_lease_session_close(glacier_hip_lease_bank *b, const glacier_hip_bank_receipt_t *receipt,
+                                    uint64_t request_epoch, uint64_t session_id,
+                                    uint64_t expected_next_sequence);
+int glacier_hip_lease_bank_snapshot(glacier_hip_lease_bank *b, glacier_hip_lease_bank_snapshot_t *out);
+
+/* The page-lease coordinator of one lane (LeasedPagedKVCache :292-1466).
+ * `bindings` is caller-owned storage, one entry per logical page of the
+ * lane's page map (bindingStorageBytes :94-101); `tree` and `sequence` are
+ * caller-owned cells shared by every lane of one cohort (the coordinators
+ * read and replace them). */
+enum { GLACIER_HIP_BINDING_FREE = 0, GLACIER_HIP_BINDING_LIVE = 1,
+       GLACIER_HIP_BINDING_FREED_PENDING_UNCHARGE = 2 };
+typedef struct {
+    uint64_t abi_version;        /* 0x4750_4c42_0000_0001 */
+    uint32_t state, has_leaf;
+    uint64_t cache_instance, logical_page, payload_bytes;
+    uint32_t scope_index, reserved0;
+    uint64_t scope_generation;
+    glacier_hip_lease_node_t leaf;
+    uint64_t integrity;
+} glacier_hip_page_lease_binding_t;  /* PageLeaseBindingV1 (:62-72) */
+
+typedef struct {
+    uint32_t count, reserved0;
+    uint64_t payload_bytes;
+    uint8_t digest[32];
+} glacier_hip_binding_summary_t;     /* BindingSummaryV1 (:74-78) */
+
+typedef struct {
+    uint64_t abi_version;        /* RowAllocationPlanV1 (paged_kv_cache.zig:113-128) */
+    uint64_t cache_id, cache_instance, base_len, logical_page, row_in_page;
+    uint64_t root_generation, row_txn_generation, root_after_generation;
+    uint64_t page_ownership_generation, next_page_ownership_generation, allocated_pages;
+    uint32_t page_payload_present, reserved0;
+    uint64_t allocation_bytes;
+} glacier_hip_row_allocation_plan_t;
+
+typedef struct {
+    uint64_t abi_version;        /* 0x4750_4c50_0000_0001 */
+    uint64_t coordinator_instance;
+    glacier_hip_lease_tree_t tree;
+    uint64_t publication_sequence;
+    glacier_hip_row_allocation_plan_t cache_plan;
+    glacier_hip_binding_summary_t bindings;
+    uint64_t integrity;
+} glacier_hip_leased_row_plan_t;     /* LeasedRowPlanV1 (:103-111) */
+
+typedef struct {
+    uint64_t abi_version;        /* 0x4750_4c52_0000_0001 */
+    uint64_t coordinator_instance, generation;
+    glacier_hip_row_txn_mark_t mark;
+    uint32_t installed_new_binding, reserved0;
+    uint8_t bindings_digest[32];
+    uint64_t integrity;
+} glacier_hip_leased_row_txn_t;      /* LeasedRowTxnV1 (:113-121) */
+
+enum { GLACIER_HIP_TERMINAL_EOS = 0, GLACIER_HIP_TERMINAL_MAX_TOKENS = 1,
+       GLACIER_HIP_TERMINAL_CANCELLED = 2 };
+typedef struct {
+    uint64_t abi_version;        /* 0x4750_4c53_0000_0001 */
+    uint64_t coordinator_instance, cache_id, cache_instance;
+    uint32_t scope_index, reserved0;
+    uint64_t scope_generation, tree_identity_generation, tree_generation;
+    uint64_t tree_structural_revision, tree_state_digest;
+    glacier_hip_page_map_root_t root;
+    uint8_t logical_kv_sha256[32];
+    glacier_hip_binding_summary_t bindings;
+    uint64_t transaction_sequence;
+    uint32_t terminal_reason, terminal_token;
+    uint64_t generation;
+    uint8_t digest[32];
+} glacier_hip_terminal_seal_t;       /* TerminalSealV1 (:150-171) */
+
+typedef struct {
+    uint64_t abi_version;        /* 0x4750_4c46_0000_0001 */
+    uint64_t coordinator_instance, generation;
+    uint8_t terminal_seal_digest[32];
+    uint64_t permit_generation;
+    glacier_hip_page_map_root_t root_before, root_after;
+    uint32_t binding_count, reserved0;
+    uint64_t payload_bytes;
+    uint8_t bindings_digest[32];
+    uint64_t integrity;
+} glacier_hip_freed_payload_t;       /* FreedPayloadV1 (:241-253) */
+
+typedef struct {
+    uint64_t abi_version;        /* 0x4750_4c43_0000_0002 */
+    uint64_t coordinator_instance, generation;
+    glacier_hip_freed_payload_t freed;
+    glacier_hip_lease_tree_t tree_after;
+    uint64_t integrity;
+} glacier_hip_reclaim_receipt_t;     /* ReclaimReceiptV1 (:255-262) */
+
+enum { GLACIER_HIP_LEASE_LIVE = 0, GLACIER_HIP_LEASE_TERMINAL_RETAINED = 1,
+       GLACIER_HIP_LEASE_FREED_PENDING_UNCHARGE = 2, GLACIER_HIP_LEASE_RECLAIMED = 3 };
+
+typedef struct glacier_hip_leased_kv glacier_hip_leased_kv;
+/* LeasedPagedKVCache.init (:311-357) over a host page map (which must be
+ * empty and not yet leased) or over one lane of a device session (begun and
+ * empty; its decode steps and prefills then charge each new page payload
+ * through the lease before the step takes it, and a failed step uncharges
+ * it). A page payload is page_payload_bytes of the map: f32 for host maps,
+ * the session's KV dtype for lanes. */
+int glacier_hip_leased_kv_create(glacier_hip_lease_bank *b, glacier_hip_lease_tree_t *tree,
+                                 const glacier_hip_lease_node_t *scope, glacier_hip_kv_pages *pages,
+                                 glacier_hip_page_lease_binding_t *bindings, uint32_t binding_count,
+                                 uint64_t request_epoch, uint64_t session_id, uint64_t *sequence,
+                                 glacier_hip_leased_kv **out);
+int glacier_hip_leased_kv_create_for_lane(glacier_hip_lease_bank *b, glacier_hip_lease_tree_t *tree,
+                                          const glacier_hip_lease_node_t *scope,
+                                          glacier_hip_session *s, uint32_t lane,
+                                          glacier_hip_page_lease_binding_t *bindings,
+                                          uint32_t binding_count, uint64_t request_epoch,
+                                          uint64_t session_id, uint64_t *sequence,
+                                          glacier_hip_leased_kv **out);
+/* Ends the coordinator object; a session lane is unleased (its pages stay). */
+void glacier_hip_leased_kv_destroy(glacier_hip_leased_kv *c);
+/* planNextRow (:453-480) / beginRowPlanned (:482-565) / commitRowTxn
+ * (:666-676) / abortRowTxn (:678-689), for host page maps. */
+int glacier_hip_leased_kv_plan_next_row(glacier_hip_leased_kv *c, glacier_hip_leased_row_plan_t *out);
+int glacier_hip_leased_kv_begin_row(glacier_hip_leased_kv *c, const glacier_hip_leased_row_plan_t *plan,
+                                    glacier_hip_leased_row_txn_t *txn_out);
+int glacier_hip_leased_kv_commit_row(glacier_hip_leased_kv *c, const glacier_hip_leased_row_txn_t *txn,
+                                     glacier_hip_page_map_root_t *root_out);
+int glacier_hip_leased_kv_abort_row(glacier_hip_leased_kv *c, const glacier_hip_leased_row_txn_t *txn);
+int glacier_hip_leased_kv_binding_summary(glacier_hip_leased_kv *c, glacier_hip_binding_summary_t *out);
+int glacier_hip_leased_kv_lifecycle(glacier_hip_leased_kv *c, uint32_t *out);
+int glacier_hip_leased_kv_root(glacier_hip_leased_kv *c, glacier_hip_page_map_root_t *out);
+int glacier_hip_leased_kv_kv_sha256(glacier_hip_leased_kv *c, uint8_t out[32]);
+/* sealTerminalForPublication (:691-757): binds the committed root and
+ * logical KV digest, then takes and commits the cohort's publication permit
+ * for `transaction_sequence` (the shared sequence cell advances). */
+int glacier_hip_leased_kv_seal_terminal(glacier_hip_leased_kv *c, const glacier_hip_page_map_root_t *root,
+                                        const uint8_t logical_kv_sha256[32],
+                                        uint64_t transaction_sequence, uint32_t reason,
+                                        uint32_t terminal_token, glacier_hip_terminal_seal_t *seal_out);
+/* beginTerminalReclaim (:852-867, beginReclaimExact :918-1036): retire the
+ * lane's scope, free every payload back to the pool (the map is retired),
+ * charges stay until commit_reclaim (commitReclaimAfterFree :1040-1080). */
+int glacier_hip_leased_kv_begin_reclaim(glacier_hip_leased_kv *c, const glacier_hip_terminal_seal_t *seal,
+                                        uint64_t expected_sequence, glacier_hip_freed_payload_t *out);
+int glacier_hip_leased_kv_commit_reclaim(glacier_hip_leased_kv *c, const glacier_hip_freed_payload_t *freed,
+                                         glacier_hip_reclaim_receipt_t *out);
+/* reclaimForTeardown (:894-916): abort a staged row, retire and uncharge. */
+int glacier_hip_leased_kv_reclaim_for_teardown(glacier_hip_leased_kv *c, uint64_t expected_sequence);
+
+/* Host rows of a host page map: the K and V rows of a staged row at one
+ * layer (appendRowTxn, paged_kv_cache.zig:1074-1103) and the logical KV
+ * digest of the committed rows (logicalKvSha256, the session lanes' digest
+ * over f32 rows). */
+int glacier_hip_kv_pages_append_row(glacier_hip_kv_pages *p, const glacier_hip_row_txn_mark_t *mark,
+                                    uint32_t layer, const float *k, const float *v);
+int glacier_hip_kv_pages_kv_sha256(glacier_hip_kv_pages *p, uint8_t out[32]);
+/* A retired map (after a leased reclaim) rejects every row. */
+int glacier_hip_kv_pages_is_retired(glacier_hip_kv_pages *p, int32_t *out);
+/* The payload pool as an allocator with a limit: at most `pages` payloads
+ * held by the map and free together (not below what the map holds). */
+int glacier_hip_kv_pages_set_pool_capacity(glacier_hip_kv_pages *p, uint32_t pages);
+
 /* Version of this ABI. */
 uint64_t glacier_hip_abi_version(void);
 
