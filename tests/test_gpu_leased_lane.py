@@ -1,0 +1,128 @@
+"""Leased session lanes (glacier_hip_leased_kv_create_for_lane): the device
+page payloads of one lane charged through a LeaseTree as the reference's
+LeasedPagedKVCache charges its allocator pages (leased_paged_kv_cache.zig
+:482-565), sealed (:691-757) and reclaimed back to the session's pool
+(:918-1080).
+
+A leased lane decodes exactly what an unleased lane decodes (same tokens,
+same KV digest); every page it takes is one exact kv_bytes leaf of its scope
+from the step that takes it; a step whose new page the lease refuses fails
+with OUT_OF_MEMORY and publishes nothing (root, charge and published tokens
+unchanged); seal + reclaim return the lane's pages to the pool and the
+charge to zero; the lane cannot start a new request while leased and can
+once the coordinator is gone."""
+import ctypes as C
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(num_layers=2, dim=256, hidden_dim=512, num_heads=4, num_kv_heads=2, head_dim=64,
+            vocab_size=4096, group_size=32, rms_eps=1e-6, rope_theta=1e6)
+SEED = 0x4C454153
+MAXPOS = 96
+PAGES = MAXPOS // 16
+PB = TINY["num_layers"] * 2 * 16 * TINY["num_kv_heads"] * TINY["head_dim"] * 2  # fp16 payload
+
+
+@pytest.fixture(scope="module")
+def model(gh, gctx):
+    m = gh.Model(gctx, TINY)
+    m.init_random(SEED)
+    yield m
+    m.close()
+
+
+def _cohort(gh, scope_pages):
+    bank = gh.LeaseBank(2, 16, 0x4C4C, kv_bytes=64 * PB, queue_slots=4)
+    parent = bank.commit(bank.reserve(1, queue_slots=1))
+    tree = bank.open_tree(parent, 2, 3, kv_bytes=16 * PB)
+    scope = bank.open_scope(tree, 4, 5, kv_bytes=scope_pages * PB)
+    seq = C.c_uint64(0)
+    bank.bind_session(tree, 6, 0x5E55)
+    return bank, parent, tree, scope, seq
+
+
+def _decode(sess, lane, prompt, n):
+    toks = [sess.prefill(lane, prompt)]
+    for _ in range(n):
+        toks.append(int(sess.step([lane], [toks[-1]])[0]))
+    return toks
+
+
+def test_leased_lane_charges_pages_and_reclaims(gh, model):
+    sess = gh.Session(model, max_lanes=2, max_positions=MAXPOS, kv_dtype=gh.F16)
+    try:
+        bank, parent, tree, scope, seq = _cohort(gh, PAGES)
+        prompt = gh.synth_tokens(SEED, 1, TINY["vocab_size"], 21)
+        sess.begin(0, seed=3)
+        sess.begin(1, seed=3)
+        print("leased lane: create", flush=True)
+        lk = gh.LeasedKV(bank, tree, scope, sess, 6, 0x5E55, seq, lane=0, binding_count=PAGES)
+        assert lib_rc(gh, sess, 0) == gh.INVALID_TRANSACTION  # no new request while leased
+        first = sess.prefill(0, prompt)
+        assert tree.current.kv_bytes == 2 * PB  # 21 rows: two pages, each charged once
+        s = lk.binding_summary()
+        assert (s.count, s.payload_bytes) == (2, 2 * PB)
+        toks = [first]
+        for i in range(16):  # to 37 positions: the third page from the step at row 32
+            toks.append(int(sess.step([0], [toks[-1]])[0]))
+            assert tree.current.kv_bytes == (3 if 21 + i + 1 > 32 else 2) * PB
+        assert toks == _decode(sess, 1, prompt, 16)  # the unleased lane decodes the same
+        assert sess.kv_sha256(0) == sess.kv_sha256(1) == lk.kv_sha256()
+        snap = bank.snapshot()
+        assert snap["used"]["kv_bytes"] == 3 * PB and snap["live_allocations"] == 3
+        # the prompt's two pages are one allocation wave, the decode page another
+        assert snap["lease_allocation_materializations"] == 2
+
+        root = lk.root()
+        seal = lk.seal_terminal(root, lk.kv_sha256(), 0, 0, toks[-1])
+        assert seq.value == 1 and seal.bindings.count == 3
+        rc, _ = sess.step([0], [toks[-1]], raise_on_error=False)
+        assert rc != gh.OK  # a sealed lane takes no more rows
+        freed = lk.begin_reclaim(seal, 1)
+        assert freed.payload_bytes == 3 * PB
+        assert all(sess.page_of(0, p) == -1 for p in range(PAGES))  # back in the pool
+        assert bank.snapshot()["used"]["kv_bytes"] == 3 * PB  # charged until the commit
+        lk.commit_reclaim(freed)
+        assert tree.current.kv_bytes == 0 and lk.lifecycle() == "reclaimed"
+        lk.close()
+        sess.begin(0, seed=3)  # unleased: a new request
+        assert _decode(sess, 0, prompt, 4) == toks[:5]
+        bank.close_session(parent, 6, 0x5E55, seq.value)
+        bank.close_tree(tree)
+        bank.release(parent)
+        assert not any(bank.snapshot()["used"].values())
+    finally:
+        sess.close()
+
+
+def lib_rc(gh, sess, lane):
+    return gh.lib().glacier_hip_session_lane_begin(sess.h, lane, 0)
+
+
+def test_refused_page_publishes_nothing(gh, model):
+    sess = gh.Session(model, max_lanes=1, max_positions=MAXPOS, kv_dtype=gh.F16)
+    try:
+        bank, parent, tree, scope, seq = _cohort(gh, 1)  # the scope holds one page
+        sess.begin(0, seed=9)
+        lk = gh.LeasedKV(bank, tree, scope, sess, 6, 0x5E55, seq, lane=0, binding_count=PAGES)
+        prompt = gh.synth_tokens(SEED, 2, TINY["vocab_size"], 14)
+        tok = sess.prefill(0, prompt)
+        tok = int(sess.step([0], [tok])[0])
+        tok = int(sess.step([0], [tok])[0])  # 16 rows: the page is full
+        root, state = sess.root(0), sess.state(0)
+        print("leased lane: refused page", flush=True)
+        rc, _ = sess.step([0], [tok], raise_on_error=False)
+        assert rc == gh.OUT_OF_MEMORY
+        after = sess.root(0)
+        assert (after.generation, after.committed_len) == (root.generation, root.committed_len)
+        assert sess.state(0).published_tokens == state.published_tokens
+        snap = bank.snapshot()
+        assert snap["used"]["kv_bytes"] == PB and snap["lease_allocation_reserves"] == 1
+        assert tree.current.kv_bytes == PB
+        lk.reclaim_for_teardown(seq.value)
+        assert tree.current.kv_bytes == 0
+        lk.close()
+    finally:
+        sess.close()
