@@ -22,6 +22,7 @@
 
 #include <random>
 #include <string>
+#include <atomic>
 #include <thread>
 #include <vector>
 
@@ -548,6 +549,143 @@ void mode_glrt(uint64_t seed, const char *tmp, int nvalid, int nimg, char **path
 
 }  // namespace
 
+// Leased page maps: random rows, aborts, pool limits, seals, reclaims and
+// renewals of two coordinators per tree; `threads` trees on one bank from
+// their own threads (the bank's lock). Invariant after every step: the
+// tree's kv charge equals the live bindings' bytes and the pages the maps hold.
+std::atomic<long> g_lease_ops{0};
+
+void lease_worker(glacier_hip_lease_bank *bank, uint64_t seed, int ops, int slot) {
+  std::mt19937_64 rng(seed);
+  glacier_hip_claim_t one{};
+  one.queue_slots = 1;
+  glacier_hip_bank_receipt_t res, parent;
+  if (glacier_hip_lease_bank_reserve(bank, 100 + slot, &one, &res) ||
+      glacier_hip_lease_bank_commit(bank, &res, &parent)) {
+    ++g_fail;
+    return;
+  }
+  glacier_hip_claim_t ceil{};
+  ceil.kv_bytes = 16 * 128;
+  glacier_hip_lease_tree_t tree;
+  glacier_hip_lease_node_t scope[2];
+  if (glacier_hip_lease_tree_open(bank, &parent, 7, 8, &ceil, &tree)) {
+    ++g_fail;
+    return;
+  }
+  ceil.kv_bytes = 8 * 128;
+  for (int i = 0; i < 2; ++i)
+    if (glacier_hip_lease_scope_open(bank, &tree, 20 + i, 30 + i, &ceil, &scope[i])) ++g_fail;
+  const uint64_t epoch = 5, sid = 0x5000 + slot;
+  uint64_t seq = 0;
+  if (glacier_hip_lease_session_bind(bank, &tree, epoch, sid)) ++g_fail;
+  glacier_hip_kv_pages *pages[2] = {};
+  glacier_hip_leased_kv *lk[2] = {};
+  std::vector<glacier_hip_page_lease_binding_t> bind[2];
+  glacier_hip_leased_row_txn_t txn[2];
+  bool staged[2] = {false, false}, sealed[2] = {false, false};
+  glacier_hip_terminal_seal_t seal[2];
+  auto renew = [&](int l) {
+    if (lk[l]) glacier_hip_leased_kv_destroy(lk[l]);
+    if (pages[l]) glacier_hip_kv_pages_destroy(pages[l]);
+    pages[l] = glacier_hip_kv_pages_create(1, 1, 64, 5);
+    bind[l].assign(4, glacier_hip_page_lease_binding_t{});
+    if (glacier_hip_leased_kv_create(bank, &tree, &scope[l], pages[l], bind[l].data(), 4, epoch,
+                                     sid, &seq, &lk[l]))
+      ++g_fail;
+    staged[l] = sealed[l] = false;
+  };
+  renew(0);
+  renew(1);
+  long done = 0;
+  for (int i = 0; i < ops; ++i) {
+    const int l = (int)(rng() % 2), r = (int)(rng() % 100);
+    if (r < 60) {
+      if (!staged[l]) {
+        glacier_hip_leased_row_plan_t plan;
+        if (!glacier_hip_leased_kv_plan_next_row(lk[l], &plan) &&
+            !glacier_hip_leased_kv_begin_row(lk[l], &plan, &txn[l])) {
+          const float k = (float)(rng() % 1000), v = -k;
+          if (glacier_hip_kv_pages_append_row(pages[l], &txn[l].mark, 0, &k, &v)) ++g_fail;
+          staged[l] = true;
+        }
+      } else {
+        if (glacier_hip_leased_kv_commit_row(lk[l], &txn[l], nullptr)) ++g_fail;
+        staged[l] = false;
+      }
+    } else if (r < 70 && staged[l]) {
+      if (glacier_hip_leased_kv_abort_row(lk[l], &txn[l])) ++g_fail;
+      staged[l] = false;
+    } else if (r < 78) {
+      glacier_hip_kv_pages_set_pool_capacity(pages[l], (uint32_t)(rng() % 6));
+    } else if (r < 84 && !staged[l] && !sealed[l]) {
+      glacier_hip_page_map_root_t root;
+      uint8_t kv[32];
+      if (!glacier_hip_leased_kv_root(lk[l], &root) && !glacier_hip_leased_kv_kv_sha256(lk[l], kv) &&
+          !glacier_hip_leased_kv_seal_terminal(lk[l], &root, kv, seq, 0, 1, &seal[l]))
+        sealed[l] = true;
+    } else if (r < 90 && sealed[l]) {
+      glacier_hip_freed_payload_t f;
+      if (!glacier_hip_leased_kv_begin_reclaim(lk[l], &seal[l], seq, &f) &&
+          glacier_hip_leased_kv_commit_reclaim(lk[l], &f, nullptr))
+        ++g_fail;
+    } else if (r < 94) {
+      if (glacier_hip_leased_kv_reclaim_for_teardown(lk[l], seq) == GLACIER_HIP_LEASE_OK) staged[l] = false;
+    } else {
+      uint32_t life;
+      glacier_hip_leased_kv_lifecycle(lk[l], &life);
+      if (life == GLACIER_HIP_LEASE_RECLAIMED) renew(l);
+    }
+    // invariant: charge == live bindings == pages held
+    uint64_t held = 0, bound = 0;
+    for (int j = 0; j < 2; ++j) {
+      glacier_hip_kv_resident_ledger_t led;
+      glacier_hip_kv_pages_ledger(pages[j], &led);
+      uint32_t life;
+      glacier_hip_leased_kv_lifecycle(lk[j], &life);
+      if (life != GLACIER_HIP_LEASE_FREED_PENDING_UNCHARGE) held += led.resident_tensor_payload_bytes;
+      for (const auto &b : bind[j])
+        if (b.state != GLACIER_HIP_BINDING_FREE) bound += b.payload_bytes;
+    }
+    if (tree.current.kv_bytes != held || bound != held) {
+      fprintf(stderr, "lease invariant: tree %llu held %llu bound %llu at op %d\n",
+              (unsigned long long)tree.current.kv_bytes, (unsigned long long)held,
+              (unsigned long long)bound, i);
+      ++g_fail;
+      break;
+    }
+    ++done;
+  }
+  g_lease_ops += done;
+  for (int l = 0; l < 2; ++l) {
+    if (glacier_hip_leased_kv_reclaim_for_teardown(lk[l], seq) != GLACIER_HIP_LEASE_OK) {
+      // a sealed lane is reclaimed through its seal
+      glacier_hip_freed_payload_t f;
+      if (!sealed[l] || glacier_hip_leased_kv_begin_reclaim(lk[l], &seal[l], seq, &f) ||
+          glacier_hip_leased_kv_commit_reclaim(lk[l], &f, nullptr))
+        ++g_fail;
+    }
+    glacier_hip_leased_kv_destroy(lk[l]);
+    glacier_hip_kv_pages_destroy(pages[l]);
+  }
+  if (tree.current.kv_bytes != 0 || glacier_hip_lease_session_close(bank, &parent, epoch, sid, seq) ||
+      glacier_hip_lease_tree_close(bank, &tree) || glacier_hip_lease_bank_release(bank, &parent))
+    ++g_fail;
+}
+
+void mode_lease(uint64_t seed, int ops, int threads) {
+  glacier_hip_limits_t lim;
+  memset(&lim, 0xff, sizeof lim);
+  glacier_hip_lease_bank *bank = glacier_hip_lease_bank_create(threads, 8 * threads, &lim, 77);
+  std::vector<std::thread> ts;
+  for (int t = 0; t < threads; ++t) ts.emplace_back(lease_worker, bank, seed + t, ops, t);
+  for (auto &t : ts) t.join();
+  glacier_hip_lease_bank_snapshot_t snap;
+  glacier_hip_lease_bank_snapshot(bank, &snap);
+  if (snap.used.kv_bytes || snap.used.queue_slots || snap.active_lease_nodes) ++g_fail;
+  glacier_hip_lease_bank_destroy(bank);
+}
+
 int main(int argc, char **argv) {
   if (argc < 2) {
     fprintf(stderr, "usage: %s mode args...\n", argv[0]);
@@ -559,6 +697,8 @@ int main(int argc, char **argv) {
   else if (mode == "laneweave" && argc == 4) mode_laneweave(strtoull(argv[2], 0, 0), atoi(argv[3]));
   else if (mode == "threads" && argc == 4) mode_threads(strtoull(argv[2], 0, 0), atoi(argv[3]));
   else if (mode == "pagedkv" && argc == 4) mode_pagedkv(strtoull(argv[2], 0, 0), atoi(argv[3]));
+  else if (mode == "lease" && argc == 5)
+    mode_lease(strtoull(argv[2], 0, 0), atoi(argv[3]), atoi(argv[4]));
   else if (mode == "glrt" && argc >= 6)
     mode_glrt(strtoull(argv[2], 0, 0), argv[3], atoi(argv[4]), argc - 5, argv + 5);
   else {
@@ -568,6 +708,7 @@ int main(int argc, char **argv) {
   if (mode == "laneweave" || mode == "threads")
     printf("admitted=%ld served=%ld waves=%ld failed_waves=%ld\n", g_n.admitted, g_n.served,
            g_n.waves, g_n.failed_waves);
+  if (mode == "lease") printf("lease_ops=%ld\n", g_lease_ops.load());
   if (mode == "pagedkv")
     printf("commits=%ld aborts=%ld resets=%ld images=%ld decoded=%ld refused=%ld\n", g_n.commits,
            g_n.aborts, g_n.resets, g_n.images, g_n.decoded, g_n.refused);

@@ -24,7 +24,7 @@ from glrt_images import int4_record, raw_record, reference_test_config, repair_c
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "glacier-engine_amd", "csrc")
 HOST_SOURCES = ["host_util.cpp", "lane_weave.cpp", "paged_kv.cpp", "publication.cpp",
-                "runtime_image.cpp", "page_image.cpp"]
+                "runtime_image.cpp", "page_image.cpp", "lease_bank.cpp", "leased_kv.cpp"]
 ENV = dict(os.environ, ASAN_OPTIONS="halt_on_error=1:detect_leaks=1",
            UBSAN_OPTIONS="halt_on_error=1:print_stacktrace=1",
            TSAN_OPTIONS="halt_on_error=1")
@@ -154,3 +154,15 @@ def test_runtime_image_reader_on_edited_images(binaries, tmp_path):
     opened, rejected = int(counts["opened"]), int(counts["rejected"])
     print(f"edited images: {opened} opened, {rejected} rejected")
     assert opened > 0 and rejected > 0
+
+
+def test_leased_page_maps_under_asan_ubsan_and_tsan(binaries):
+    """Leased page maps (lease_bank.cpp, leased_kv.cpp) under random rows,
+    aborts, pool limits, seals, reclaims and renewals: the tree's charge equals
+    the live bindings and the pages the maps hold after every step; four trees
+    on one bank from four threads under ThreadSanitizer."""
+    for seed in (1, 2, 3):
+        out = _run(binaries[0], "lease", seed, 3000, 1)
+        assert int(out.split("lease_ops=")[1]) == 3000
+    out = _run(binaries[1], "lease", 9, 1500, 4)
+    assert int(out.split("lease_ops=")[1]) == 6000
