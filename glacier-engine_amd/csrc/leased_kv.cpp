@@ -129,6 +129,19 @@ void seal_digest(const glacier_hip_terminal_seal_t &s, uint8_t out[32]) {
   h.final(out);
 }
 
+void seal_digest_v3(const glacier_hip_terminal_seal_t &s, const uint8_t proposal[32],
+                    const uint8_t commit[32], uint8_t out[32]) {
+  // terminalSealV3Digest: the seal's fields and the wave's proposal and commit digests
+  uint8_t base[32];
+  seal_digest(s, base);
+  gh::Sha256 h;
+  h.update("glacier-hip-terminal-seal-v3\0", 29);
+  h.update(base, 32);
+  h.update(proposal, 32);
+  h.update(commit, 32);
+  h.final(out);
+}
+
 void teardown_digest(uint64_t instance, uint64_t sequence, const Root &root, const uint8_t kv[32],
                      const Summary &b, uint8_t out[32]) {
   gh::Sha256 h;
@@ -494,13 +507,61 @@ int Leased::seal_terminal(const Root &expected_root, const uint8_t kv[32], uint6
   return GLACIER_HIP_LEASE_OK;
 }
 
+int Leased::finalize_wave_terminal(uint64_t sequence, uint32_t token, const uint8_t proposal[32],
+                                   const uint8_t commit[32]) {
+  if (int rc = validate_mutable()) return rc;
+  if (has_row || lane_active) return GLACIER_HIP_LEASE_INVALID_LEASED_TRANSACTION;
+  if (*this->sequence != sequence + 1) return GLACIER_HIP_LEASE_INVALID_TERMINAL_SEAL;
+  uint8_t digest[32];
+  if (int rc = target.kv_sha256(digest)) return rc;
+  Summary bs;
+  if (int rc = binding_summary(GLACIER_HIP_BINDING_LIVE, &bs)) return rc;
+  glacier_hip_terminal_seal_t s;
+  memset(&s, 0, sizeof s);
+  s.abi_version = kTerminalSealAbi;
+  s.coordinator_instance = instance;
+  s.cache_id = (uint64_t)(uintptr_t)target.cache;
+  s.cache_instance = target.cache->root.cache_instance;
+  s.scope_index = scope.node_index;
+  s.scope_generation = scope.generation;
+  s.tree_identity_generation = tree->identity_generation;
+  s.tree_generation = tree->generation;
+  s.tree_structural_revision = tree->structural_revision;
+  s.tree_state_digest = tree->state_digest;
+  s.root = target.cache->root;
+  memcpy(s.logical_kv_sha256, digest, 32);
+  s.bindings = bs;
+  s.transaction_sequence = sequence;
+  s.terminal_reason = GLACIER_HIP_TERMINAL_EOS;  // the wave binding carries a terminal flag
+  s.terminal_token = token;
+  s.generation = next_generation++;
+  memcpy(seal_proposal, proposal, 32);
+  memcpy(seal_commit, commit, 32);
+  seal_digest_v3(s, proposal, commit, s.digest);
+  seal = s;
+  seal_v3 = true;
+  has_seal = true;
+  return GLACIER_HIP_LEASE_OK;
+}
+
+int Leased::terminal_seal(glacier_hip_terminal_seal_t *out, uint8_t proposal[32],
+                          uint8_t commit[32]) const {
+  if (!leased_ok()) return GLACIER_HIP_LEASE_INVALID_COORDINATOR;
+  if (!has_seal) return GLACIER_HIP_LEASE_TERMINAL_REQUIRED;
+  *out = seal;
+  if (proposal) memcpy(proposal, seal_proposal, 32);
+  if (commit) memcpy(commit, seal_commit, 32);
+  return GLACIER_HIP_LEASE_OK;
+}
+
 int Leased::begin_reclaim(const glacier_hip_terminal_seal_t &sl, uint64_t expected_sequence,
                           glacier_hip_freed_payload_t *out) {
   // beginTerminalReclaim (:852-867) after validateTerminalSeal (:1112-1127)
   if (!leased_ok()) return GLACIER_HIP_LEASE_INVALID_COORDINATOR;
   if (!has_seal) return GLACIER_HIP_LEASE_TERMINAL_REQUIRED;
   uint8_t d[32];
-  seal_digest(sl, d);
+  if (seal_v3) seal_digest_v3(sl, seal_proposal, seal_commit, d);
+  else seal_digest(sl, d);
   if (sl.abi_version != kTerminalSealAbi || !same(d, sl.digest, 32) || !same(&sl, &seal, sizeof sl) ||
       sl.coordinator_instance != instance || sl.cache_id != (uint64_t)(uintptr_t)target.cache ||
       sl.scope_index != scope.node_index || sl.scope_generation != scope.generation)
@@ -752,6 +813,12 @@ int glacier_hip_leased_kv_commit_reclaim(glacier_hip_leased_kv *c, const glacier
                                          glacier_hip_reclaim_receipt_t *out) {
   if (!c || !freed) return GLACIER_HIP_LEASE_INVALID_ARGUMENT;
   return c->lease.commit_reclaim(*freed, out);
+}
+
+int glacier_hip_leased_kv_terminal_seal(glacier_hip_leased_kv *c, glacier_hip_terminal_seal_t *out,
+                                        uint8_t proposal_sha256[32], uint8_t commit_sha256[32]) {
+  if (!c || !out) return GLACIER_HIP_LEASE_INVALID_ARGUMENT;
+  return c->lease.terminal_seal(out, proposal_sha256, commit_sha256);
 }
 
 int glacier_hip_leased_kv_reclaim_for_teardown(glacier_hip_leased_kv *c, uint64_t expected_sequence) {

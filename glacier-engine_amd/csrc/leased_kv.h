@@ -86,6 +86,14 @@ class Leased {
                     glacier_hip_freed_payload_t *out);
   int commit_reclaim(const glacier_hip_freed_payload_t &freed, glacier_hip_reclaim_receipt_t *out);
   int reclaim_for_teardown(uint64_t expected_sequence);
+  // A staged publication wave's terminal lane (planTerminalForTokenTxn
+  // :759-808 + finalizeTerminalAssumePublished :810-850): after the wave's
+  // permit for `sequence` committed, the seal binds the lane's committed
+  // root, logical KV digest and bindings to the wave's proposal and commit
+  // digests.
+  int finalize_wave_terminal(uint64_t sequence, uint32_t token, const uint8_t proposal[32],
+                             const uint8_t commit[32]);
+  int terminal_seal(glacier_hip_terminal_seal_t *out, uint8_t proposal[32], uint8_t commit[32]) const;
 
   Bank *bank = nullptr;
   Tree *tree = nullptr;
@@ -109,8 +117,9 @@ class Leased {
 
   bool has_row = false, lane_active = false;
   glacier_hip_leased_row_txn_t row{};
-  bool has_seal = false;
+  bool has_seal = false, seal_v3 = false;
   glacier_hip_terminal_seal_t seal{};
+  uint8_t seal_proposal[32] = {}, seal_commit[32] = {};
   bool has_pending = false;
   glacier_hip_freed_payload_t pending_freed{};
   FreePermit pending_permit{};

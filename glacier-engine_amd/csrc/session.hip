@@ -72,6 +72,10 @@ struct PreparedWave {
   std::vector<uint32_t> lanes, slots, tokens;
   glacier_hip_token_proposal_v1_t proposal{};
   uint8_t sha[32] = {};
+  // leased lanes: the cohort's publication permit fences the whole wave
+  // (paged_lease_token_txn.zig: one Bank permit per B4 wave)
+  glacier_hip_leased_kv *cohort = nullptr;
+  glb::PubPermit permit{};
 };
 
 constexpr int kRow0Pages = 28;  // page ids of row 0 carried in the step inputs
@@ -2111,6 +2115,17 @@ int glacier_hip_session_restore_checkpoint(glacier_hip_session *s, uint32_t lane
 
 extern "C" {
 
+}  // extern "C"
+
+// abortPublication of a staged wave's permit (the sequence stays for the retry)
+static void release_permit(PreparedWave &P) {
+  if (!P.cohort) return;
+  (void)P.cohort->lease.bank->abort_publication(P.permit);
+  P.cohort = nullptr;
+}
+
+extern "C" {
+
 int glacier_hip_session_step_prepare(glacier_hip_session *s, const uint32_t *lanes,
                                      const uint32_t *tokens, uint32_t count,
                                      const uint64_t *eligible_words_host,
@@ -2168,12 +2183,41 @@ int glacier_hip_session_step_prepare(glacier_hip_session *s, const uint32_t *lan
   } else {
     for (uint32_t i = 0; i < count; ++i) P.tokens[i] = s->lanes[lanes[i]].first_token;
   }
+  // leased lanes publish under their cohort's permit for the binding's
+  // sequence: every leased lane of the wave shares one bank, tree and
+  // sequence cell, and the permit generation goes into the proposal
+  P.cohort = nullptr;
+  for (uint32_t i = 0; i < count; ++i) {
+    glacier_hip_leased_kv *l = s->lanes[lanes[i]].lease;
+    if (!l) continue;
+    const glb::Leased &a = l->lease;
+    if (P.cohort) {
+      const glb::Leased &b = P.cohort->lease;
+      if (a.bank != b.bank || a.tree != b.tree || a.sequence != b.sequence ||
+          a.request_epoch != b.request_epoch || a.session_id != b.session_id) {
+        if (!P.first) abort_rows(s, P.txns);
+        return GLACIER_HIP_INVALID_ARGUMENT;
+      }
+    } else {
+      P.cohort = l;
+    }
+  }
+  if (P.cohort) {
+    glb::Leased &a = P.cohort->lease;
+    if (binding->transaction_sequence != *a.sequence || binding->request_epoch != a.request_epoch ||
+        a.bank->begin_publication(*a.tree, a.request_epoch, a.session_id, *a.sequence, &P.permit)) {
+      if (!P.first) abort_rows(s, P.txns);
+      P.cohort = nullptr;
+      return GLACIER_HIP_INVALID_TRANSACTION;
+    }
+  }
   glacier_hip_token_proposal_v1_t &pr = P.proposal;
   gpub::empty_proposal(pr);
   pr.execution_abi = binding->execution_abi;
   pr.request_epoch = binding->request_epoch;
   pr.transaction_sequence = binding->transaction_sequence;
-  pr.resource_permit_generation = binding->resource_permit_generation;
+  pr.resource_permit_generation =
+      P.cohort ? P.permit.generation : binding->resource_permit_generation;
   pr.live_mask = mask;
   pr.live_lane_count = count;
   pr.kv_capacity_bytes = binding->kv_capacity_bytes;
@@ -2189,7 +2233,10 @@ int glacier_hip_session_step_prepare(glacier_hip_session *s, const uint32_t *lan
     if (P.first) {  // initialRootTransition (:790-811)
       uint8_t kv_sha[32];
       int rc = logical_kv_sha256(s, lanes[i], kv_sha);
-      if (rc) return rc;
+      if (rc) {
+        release_permit(P);
+        return rc;
+      }
       const glacier_hip_page_map_root_t &r = ln.kv.root;
       lp.has_kv_transition = 0;
       lp.kv_before = lp.kv_after = ln.kv.len;
@@ -2242,6 +2289,7 @@ int glacier_hip_session_step_abort(glacier_hip_session *s) {
   GH_SUBMISSION(s->model->ctx);
   if (!s->prep.active) return GLACIER_HIP_INVALID_TRANSACTION;
   if (!s->prep.first) abort_rows(s, s->prep.txns);
+  release_permit(s->prep);
   s->prep.active = false;
   return GLACIER_HIP_OK;
 }
@@ -2256,6 +2304,7 @@ int glacier_hip_session_step_commit(glacier_hip_session *s, const glacier_hip_pr
   if (ack->abi_version != gpub::kPrepareAckAbi || ack->sink_epoch == 0 ||
       ack->reservation_id == 0 || memcmp(ack->proposal_sha256, P.sha, 32) != 0) {
     if (!P.first) abort_rows(s, P.txns);
+    release_permit(P);
     P.active = false;
     return GLACIER_HIP_INVALID_TRANSACTION;
   }
@@ -2277,12 +2326,27 @@ int glacier_hip_session_step_commit(glacier_hip_session *s, const glacier_hip_pr
     ln.first_pending = false;
     if (lp.terminal) ln.retired = true;
   }
+  uint8_t commit_sha[32];
+  gpub::commit_sha256(P.sha, *ack, commit_sha);
+  if (P.cohort) {
+    // the wave's permit commits once (the cohort's sequence advances), then
+    // every leased lane whose terminal token this wave published is sealed
+    glb::Leased &a = P.cohort->lease;
+    if (a.bank->commit_publication(P.permit) == GLACIER_HIP_LEASE_OK) *a.sequence = P.permit.sequence + 1;
+    for (size_t i = 0; i < P.lanes.size(); ++i) {
+      const glacier_hip_lane_proposal_v1_t &lp = P.proposal.lanes[P.slots[i]];
+      glacier_hip_leased_kv *l = s->lanes[P.lanes[i]].lease;
+      if (l && lp.terminal)
+        (void)l->lease.finalize_wave_terminal(P.permit.sequence, lp.token_id, P.sha, commit_sha);
+    }
+    P.cohort = nullptr;
+  }
   if (receipt_out) {
     memset(receipt_out, 0, sizeof *receipt_out);
     receipt_out->abi_version = gpub::kCommitReceiptAbi;
     memcpy(receipt_out->proposal_sha256, P.sha, 32);
     receipt_out->prepare_ack = *ack;
-    gpub::commit_sha256(P.sha, *ack, receipt_out->commit_sha256);
+    memcpy(receipt_out->commit_sha256, commit_sha, 32);
   }
   P.active = false;
   return GLACIER_HIP_OK;

@@ -644,6 +644,7 @@ _SIGS = [
     ("glacier_hip_leased_kv_commit_reclaim", C.c_int,
      [_P, C.POINTER(FreedPayload), C.POINTER(ReclaimReceipt)]),
     ("glacier_hip_leased_kv_reclaim_for_teardown", C.c_int, [_P, C.c_uint64]),
+    ("glacier_hip_leased_kv_terminal_seal", C.c_int, [_P, C.POINTER(TerminalSeal), _P, _P]),
     ("glacier_hip_kv_pages_append_row", C.c_int,
      [_P, C.POINTER(RowTxnMark), C.c_uint32, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
     ("glacier_hip_kv_pages_kv_sha256", C.c_int, [_P, _P]),
@@ -1459,6 +1460,13 @@ class LeasedKV:
         lease_check(lib().glacier_hip_leased_kv_commit_reclaim(self.h, C.byref(freed), C.byref(r)),
                     "commit_reclaim")
         return r
+
+    def terminal_seal(self):
+        s = TerminalSeal()
+        p, c = (C.c_uint8 * 32)(), (C.c_uint8 * 32)()
+        lease_check(lib().glacier_hip_leased_kv_terminal_seal(self.h, C.byref(s), p, c),
+                    "terminal_seal")
+        return s, bytes(p), bytes(c)
 
     def reclaim_for_teardown(self, expected_sequence):
         lease_check(lib().glacier_hip_leased_kv_reclaim_for_teardown(self.h, expected_sequence),

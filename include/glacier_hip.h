@@ -1368,6 +1368,12 @@ int glacier_hip_leased_kv_begin_reclaim(glacier_hip_leased_kv *c, const glacier_
                                         uint64_t expected_sequence, glacier_hip_freed_payload_t *out);
 int glacier_hip_leased_kv_commit_reclaim(glacier_hip_leased_kv *c, const glacier_hip_freed_payload_t *freed,
                                          glacier_hip_reclaim_receipt_t *out);
+/* The lane's terminal seal: the one seal_terminal made, or the one a staged
+ * publication wave made when it published the lane's terminal token (then
+ * its digest also binds that wave's proposal and commit digests, returned
+ * here; zeros for a seal_terminal seal). TERMINAL_REQUIRED before either. */
+int glacier_hip_leased_kv_terminal_seal(glacier_hip_leased_kv *c, glacier_hip_terminal_seal_t *out,
+                                        uint8_t proposal_sha256[32], uint8_t commit_sha256[32]);
 /* reclaimForTeardown (:894-916): abort a staged row, retire and uncharge. */
 int glacier_hip_leased_kv_reclaim_for_teardown(glacier_hip_leased_kv *c, uint64_t expected_sequence);
 

@@ -10,7 +10,8 @@ from the step that takes it; a step whose new page the lease refuses fails
 with OUT_OF_MEMORY and publishes nothing (root, charge and published tokens
 unchanged); seal + reclaim return the lane's pages to the pool and the
 charge to zero; the lane cannot start a new request while leased and can
-once the coordinator is gone."""
+once the coordinator is gone. Staged publication waves over leased lanes
+take one cohort permit per wave (paged_lease_token_txn.zig)."""
 import ctypes as C
 
 import pytest
@@ -124,5 +125,100 @@ def test_refused_page_publishes_nothing(gh, model):
         lk.reclaim_for_teardown(seq.value)
         assert tree.current.kv_bytes == 0
         lk.close()
+    finally:
+        sess.close()
+
+
+def _wave_binding(gh, slots, seq, terminal=()):
+    b = gh.PublicationBinding()
+    b.execution_abi = 0x5042544553540001
+    b.request_epoch = 6
+    b.transaction_sequence = seq
+    b.resource_permit_generation = 999  # replaced by the cohort permit's generation
+    b.kv_capacity_bytes = 2 * PAGES * PB
+    b.receipt.bank_epoch = 0x4C4C
+    for i, sl in enumerate(slots):
+        b.lane_index[i] = sl
+        b.terminal[i] = 1 if sl in terminal else 0
+    return b
+
+
+def _ack(gh, sha, rid):
+    return gh.PrepareAck(gh.PREPARE_ACK_ABI, (C.c_uint8 * 32)(*sha), 0x50414745, rid)
+
+
+def test_leased_waves_publish_under_one_cohort_permit(gh, model):
+    """paged_lease_token_txn.zig: one Bank publication permit fences a whole
+    staged wave of leased lanes (its generation is the proposal's permit
+    generation); commit advances the cohort's sequence once, a sink rejection
+    or abort leaves it for the retry, a wrong sequence is refused before any
+    permit; a lane whose terminal token the wave publishes is sealed with the
+    wave's proposal and commit digests and reclaims from that seal."""
+    sess = gh.Session(model, max_lanes=2, max_positions=MAXPOS, kv_dtype=gh.F16)
+    try:
+        bank = gh.LeaseBank(2, 16, 0x4C4C, kv_bytes=64 * PB, queue_slots=4)
+        parent = bank.commit(bank.reserve(1, queue_slots=1))
+        tree = bank.open_tree(parent, 2, 3, kv_bytes=16 * PB)
+        scopes = [bank.open_scope(tree, 4 + i, 5 + i, kv_bytes=PAGES * PB) for i in range(2)]
+        seq = C.c_uint64(0)
+        bank.bind_session(tree, 6, 0x5E55)
+        lks = []
+        for lane in range(2):
+            sess.begin(lane, seed=lane)
+            lks.append(gh.LeasedKV(bank, tree, scopes[lane], sess, 6, 0x5E55, seq, lane=lane,
+                                   binding_count=PAGES))
+            sess.prefill_staged(lane, gh.synth_tokens(SEED, 10 + lane, TINY["vocab_size"], 20))
+        assert tree.current.kv_bytes == 4 * PB
+        print("leased waves: first tokens", flush=True)
+        rc, _, _, _ = sess.step_prepare([0, 1], None, _wave_binding(gh, [0, 1], 5))
+        assert rc == gh.INVALID_TRANSACTION and seq.value == 0  # not the cohort's sequence
+        rc, prop, sha, toks = sess.step_prepare([0, 1], None, _wave_binding(gh, [0, 1], 0))
+        assert rc == gh.OK and prop.resource_permit_generation == 1
+        rc, _ = sess.step_commit(_ack(gh, sha, 1))
+        assert rc == gh.OK and seq.value == 1
+        toks = [int(t) for t in toks]
+        # abort, then a rejected ack: the sequence stays, each retry takes a new permit
+        rc, prop, sha, _ = sess.step_prepare([0, 1], toks, _wave_binding(gh, [0, 1], 1))
+        assert rc == gh.OK and prop.resource_permit_generation == 2
+        assert sess.step_abort() == gh.OK and seq.value == 1
+        rc, prop, sha, _ = sess.step_prepare([0, 1], toks, _wave_binding(gh, [0, 1], 1))
+        assert rc == gh.OK and prop.resource_permit_generation == 3
+        rc, _ = sess.step_commit(_ack(gh, bytes(32), 2))
+        assert rc == gh.INVALID_TRANSACTION and seq.value == 1
+        for wave in range(12):
+            terminal = (1,) if wave == 11 else ()
+            rc, prop, sha, nxt = sess.step_prepare([0, 1], toks,
+                                                   _wave_binding(gh, [0, 1], seq.value, terminal))
+            assert rc == gh.OK
+            rc, rec = sess.step_commit(_ack(gh, sha, 10 + wave))
+            assert rc == gh.OK
+            toks = [int(t) for t in nxt]
+        assert seq.value == 13
+        # 20 prompt rows + 12 decode rows (the first-token wave writes none):
+        # 32 rows, two pages per lane
+        assert tree.current.kv_bytes == 4 * PB
+        seal, psha, csha = lks[1].terminal_seal()
+        assert psha == sha and csha == bytes(rec.commit_sha256)
+        assert seal.transaction_sequence == 12 and seal.terminal_token == toks[1]
+        assert seal.bindings.count == 2
+        assert lks[0].lifecycle() == "live" and lks[1].lifecycle() == "terminal_retained"
+        with pytest.raises(gh.LeaseError) as e:
+            lks[1].begin_reclaim(seal, 12)  # the reclaim comes after the terminal sequence
+        assert e.value.reason == "InvalidTerminalSeal"
+        freed = lks[1].begin_reclaim(seal, 13)
+        lks[1].commit_reclaim(freed)
+        assert tree.current.kv_bytes == 2 * PB
+        # lane 0 publishes on alone; then teardown
+        rc, prop, sha, nxt = sess.step_prepare([0], toks[:1], _wave_binding(gh, [0], 13))
+        assert rc == gh.OK
+        assert sess.step_commit(_ack(gh, sha, 99))[0] == gh.OK and seq.value == 14
+        lks[0].reclaim_for_teardown(seq.value)
+        assert tree.current.kv_bytes == 0
+        for lk in lks:
+            lk.close()
+        bank.close_session(parent, 6, 0x5E55, seq.value)
+        bank.close_tree(tree)
+        bank.release(parent)
+        assert not any(bank.snapshot()["used"].values())
     finally:
         sess.close()
