@@ -322,6 +322,36 @@ def decode_batch1(gh, sess, prompt, warmup, steps):
     return steps / dt, dt
 
 
+def decode_leased(gh, model, prompt, max_pos, warmup, steps):
+    """The batch-1 decode on a lane whose KV pages are charged through a
+    LeaseTree (each new page reserved and settled in the bank before the step
+    takes it), then sealed and reclaimed; the page-charge work rides the host
+    side of the step."""
+    import ctypes as C
+    pages = -(-max_pos // 16)
+    page_bytes = CFG_7B["num_layers"] * 2 * 16 * CFG_7B["num_kv_heads"] * CFG_7B["head_dim"] * 2
+    bank = gh.LeaseBank(1, pages + 4, 0x4C454153, kv_bytes=pages * page_bytes, queue_slots=1)
+    parent = bank.commit(bank.reserve(1, queue_slots=1))
+    tree = bank.open_tree(parent, 2, 3, kv_bytes=pages * page_bytes)
+    scope = bank.open_scope(tree, 4, 5, kv_bytes=pages * page_bytes)
+    seq = C.c_uint64(0)
+    bank.bind_session(tree, 6, 7)
+    sess = gh.Session(model, max_lanes=1, max_positions=max_pos, kv_dtype=gh.F16)
+    try:
+        sess.begin(0, seed=1)
+        lk = gh.LeasedKV(bank, tree, scope, sess, 6, 7, seq, lane=0, binding_count=pages)
+        tps, dt = decode_batch1(gh, sess, prompt, warmup, steps)
+        charged = tree.current.kv_bytes
+        seal = lk.seal_terminal(lk.root(), lk.kv_sha256(), seq.value, 0, 0)
+        lk.commit_reclaim(lk.begin_reclaim(seal, seq.value))
+        out = dict(tokens_per_s=round(tps, 2), ms_per_token=round(dt * 1e3 / steps, 4),
+                   pages_charged=charged // page_bytes, charge_after_reclaim=tree.current.kv_bytes)
+        lk.close()
+        return out
+    finally:
+        sess.close()
+
+
 def decode_eligible(gh, model, prompt, warmup, steps, density=0.01):
     """Batch-1 greedy decode with a caller-certified eligibility mask of the
     given density on every step (a fresh random mask per step from a fixed
@@ -739,7 +769,7 @@ def main():
                      roofline=step_roofline(CFG_7B, tpsL, steps_per_s, a.lanes * mean_ctx, 2))
         log(f"{a.lanes}-lane decode {tpsL:.1f} tok/s")
     sess.close()
-    f32kv = elig = None
+    f32kv = elig = leased = None
     if "decode" in secs:
         # the same batch-1 decode on f32 KV pages, the reference's storage
         s32 = gh.Session(model, max_lanes=1, max_positions=max_pos, kv_dtype=gh.F32)
@@ -753,6 +783,8 @@ def main():
         log(f"batch-1 decode, f32 KV {tps32:.1f} tok/s")
         elig = decode_eligible(gh, model, prompt, a.warmup, min(a.steps, 32))
         log("batch-1 decode with a 1% eligibility mask", elig)
+        leased = decode_leased(gh, model, prompt, max_pos, a.warmup, a.steps)
+        log("batch-1 decode on a leased lane", leased)
     c5 = bench_c5(gh, model) if "c5" in secs else None
     prefill = bench_prefill(gh, model, [512, 2048]) if not a.no_prefill else None
     model.close()
@@ -780,7 +812,7 @@ def main():
         roofline=roofline, cpu_baseline=cpu, host=host_info(ctx),
         decode_roofline=step_roofline(CFG_7B, tps1, tps1, a.prompt + a.warmup + a.steps / 2 + 1, 2)
         if tps1 else None,
-        decode_f32_kv=f32kv, decode_eligible=elig, lanes32=lanes, c5_laneweave=c5, c1_qwen05b=c1, prefill=prefill, attention=attn,
+        decode_f32_kv=f32kv, decode_eligible=elig, decode_leased=leased, lanes32=lanes, c5_laneweave=c5, c1_qwen05b=c1, prefill=prefill, attention=attn,
         gemv=([dom] if dom else []) + gemv)
     print(json.dumps(out))
 

@@ -417,8 +417,6 @@ int Leased::reserve_rows(uint32_t rows) {
   // page a row installs without a payload gets its leaf charged first
   if (int rc = validate_mutable()) return rc;
   if (lane_active || has_batch) return GLACIER_HIP_LEASE_INVALID_LEASED_TRANSACTION;
-  Summary bs;
-  if (int rc = binding_summary(GLACIER_HIP_BINDING_LIVE, &bs)) return rc;
   const gpk::Cache &c = *target.cache;
   std::vector<Spec> specs;
   batch_pages.clear();
@@ -431,6 +429,14 @@ int Leased::reserve_rows(uint32_t rows) {
     if (present) continue;
     specs.push_back(Spec{scope, p + 1, page_binding_key(c.instance, p), kv_claim(c.page_payload_bytes)});
     batch_pages.push_back(p);
+  }
+  // rows that take no new page keep the lane's binding set as it is (their
+  // pages' bindings were checked above); the full membership check
+  // (bindingSummaryForState) runs before any new page is charged, and again
+  // at seal and reclaim
+  if (!specs.empty()) {
+    Summary bs;
+    if (int rc = binding_summary(GLACIER_HIP_BINDING_LIVE, &bs)) return rc;
   }
   lane_active = true;
   if (specs.empty()) return GLACIER_HIP_LEASE_OK;
