@@ -1037,6 +1037,8 @@ hipError_t enqueue_step(glacier_hip_session *s, int rows, bool head, bool elig, 
 }
 
 void destroy_session(glacier_hip_session *s) {
+  if (s->prep.active && s->prep.cohort)  // a prepared wave's permit goes back to the bank
+    (void)s->prep.cohort->lease.bank->abort_publication(s->prep.permit);
   for (Lane &ln : s->lanes)
     if (ln.lease) {  // the coordinator outlives the lane: every later call on it is refused
       ln.lease->lease.orphan();
@@ -2405,6 +2407,14 @@ void detach_lane(glacier_hip_leased_kv *c) {
   if (!s || c->lane >= s->lanes.size()) return;
   Lane &ln = s->lanes[c->lane];
   if (ln.lease != c) return;
+  PreparedWave &P = s->prep;
+  if (P.active && std::find(P.lanes.begin(), P.lanes.end(), c->lane) != P.lanes.end()) {
+    // the lane's coordinator goes away inside a prepared wave: the wave aborts
+    if (!P.first) abort_rows(s, P.txns);
+    if (P.cohort) (void)P.cohort->lease.bank->abort_publication(P.permit);
+    P.cohort = nullptr;
+    P.active = false;
+  }
   ln.lease = nullptr;
   ln.kv.leased_instance = 0;  // the lane may start a new request
   ln.kv.leased_owner = 0;

@@ -222,3 +222,43 @@ def test_leased_waves_publish_under_one_cohort_permit(gh, model):
         assert not any(bank.snapshot()["used"].values())
     finally:
         sess.close()
+
+
+def test_coordinator_gone_mid_wave_aborts_the_wave(gh, model):
+    """A leased lane's coordinator destroyed between step_prepare and
+    step_commit aborts the prepared wave: its permit goes back to the bank
+    (the cohort's sequence stays), its rows are aborted, and the other lane
+    publishes the next wave at the same sequence."""
+    sess = gh.Session(model, max_lanes=2, max_positions=MAXPOS, kv_dtype=gh.F16)
+    try:
+        bank = gh.LeaseBank(2, 16, 0x4C4C, kv_bytes=64 * PB, queue_slots=4)
+        parent = bank.commit(bank.reserve(1, queue_slots=1))
+        tree = bank.open_tree(parent, 2, 3, kv_bytes=16 * PB)
+        scopes = [bank.open_scope(tree, 4 + i, 5 + i, kv_bytes=PAGES * PB) for i in range(2)]
+        seq = C.c_uint64(0)
+        bank.bind_session(tree, 6, 0x5E55)
+        lks = []
+        for lane in range(2):
+            sess.begin(lane, seed=lane)
+            lks.append(gh.LeasedKV(bank, tree, scopes[lane], sess, 6, 0x5E55, seq, lane=lane,
+                                   binding_count=PAGES))
+            sess.prefill_staged(lane, gh.synth_tokens(SEED, 20 + lane, TINY["vocab_size"], 18))
+        rc, _, sha, toks = sess.step_prepare([0, 1], None, _wave_binding(gh, [0, 1], 0))
+        assert rc == gh.OK and sess.step_commit(_ack(gh, sha, 1))[0] == gh.OK
+        toks = [int(t) for t in toks]
+        root1 = sess.root(1)
+        rc, _, sha, _ = sess.step_prepare([0, 1], toks, _wave_binding(gh, [0, 1], 1))
+        assert rc == gh.OK
+        print("coordinator gone mid-wave", flush=True)
+        lks[0].close()  # lane 0's coordinator goes away inside the prepared wave
+        rc, _ = sess.step_commit(_ack(gh, sha, 2))
+        assert rc == gh.INVALID_TRANSACTION and seq.value == 1
+        after = sess.root(1)
+        assert (after.generation, after.committed_len) == (root1.generation, root1.committed_len)
+        rc, _, sha, _ = sess.step_prepare([1], toks[1:], _wave_binding(gh, [1], 1))
+        assert rc == gh.OK and sess.step_commit(_ack(gh, sha, 3))[0] == gh.OK
+        assert seq.value == 2
+        lks[1].reclaim_for_teardown(seq.value)
+        lks[1].close()
+    finally:
+        sess.close()
