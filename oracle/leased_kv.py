@@ -406,7 +406,14 @@ class Bank:
         return batch, leaves
 
     def _pending(self, batch, kind):
+        # a decision token is the exact pending decision it names: a token
+        # whose fields were altered is a forgery (the reference's integrity
+        # word, validateLeaseAllocationBatchLocked :3816-3857), a consumed
+        # one no longer matches the tree's state
         root = self.roots[batch["slot"]]
+        if root is not None and root["pending"] == kind and root["pending_gen"] == batch["gen"] and \
+                (root["pending_claim"] != batch["claim"] or root["pending_count"] != batch["count"]):
+            fail("StaleReservation")
         if root is None or root["pending"] != kind or root["pending_gen"] != batch["gen"] or \
                 root["gen"] != batch["tree_gen"] or \
                 not self._session_ok(batch["slot"], batch["epoch"], batch["session"],

@@ -519,3 +519,62 @@ def test_random_operations_match_the_oracle(seed):
     got = _drive(Product(gh), ops)
     for i, (w, g) in enumerate(zip(want, got)):
         assert w == g, f"step {i}: {ops[i]}\noracle  {w}\nproduct {g}"
+
+
+def _oracle_lane(kv_limit, nodes, epoch):
+    bank = ol.Bank(1, nodes, epoch, kv_bytes=kv_limit)
+    receipt = bank.commit(bank.reserve(1, queue_slots=1))
+    tree = bank.open_tree(receipt, 1, 2, kv_bytes=128)
+    scope = bank.open_scope(tree, 3, 4, kv_bytes=128)
+    bank.bind_session(tree, 5, 0x5E55)
+    return bank, receipt, tree, scope
+
+
+def oreason(fn, *a):
+    with pytest.raises(ol.LeaseFailure) as e:
+        fn(*a)
+    return e.value.reason
+
+
+def test_oracle_aborted_reservation_stays_charged_until_abort():
+    """resource_bank.zig:6348-6435 on the oracle (the product runs the same
+    bank code through the leased-cache scenarios above)."""
+    bank, receipt, tree, scope = _oracle_lane(128, 3, 0x50324343)
+    batch, leaves = bank.reserve_allocations(tree, 5, 0x5E55, 0, [(scope, 6, 7, ol.Claim(kv_bytes=64))])
+    forged = dict(batch, claim=ol.Claim(kv_bytes=63))
+    assert oreason(bank.abort_allocations, forged, tree) == "StaleReservation"
+    assert bank.snapshot()["used"]["kv_bytes"] == 64
+    bank.abort_allocations(batch, tree)
+    assert tree.current.kv_bytes == 0
+    assert oreason(bank.abort_allocations, batch, tree) == "InvalidTransition"
+    assert oreason(bank._node, tree, leaves[0]) == "StaleReservation"
+    second, leaves2 = bank.reserve_allocations(tree, 5, 0x5E55, 0,
+                                               [(scope, 8, 9, ol.Claim(kv_bytes=32))])
+    assert leaves2[0].generation != leaves[0].generation
+    bank.abort_allocations(second, tree)
+    bank.close_session(receipt, 5, 0x5E55, 0)
+    bank.close_tree(tree)
+    bank.release(receipt)
+    snap = bank.snapshot()
+    assert not any(snap["used"].values()) and snap["lease_allocation_aborts"] == 2
+
+
+def test_oracle_capacity_and_node_exhaustion_are_atomic_and_distinct():
+    """resource_bank.zig:6437-6514 on the oracle: too many leaves for the
+    node pool, then a leaf past the bank's capacity, each refused with its
+    own error and counter and nothing charged."""
+    bank, receipt, tree, scope = _oracle_lane(64, 2, 0x50324344)
+    before = tree.key()
+    two = [(scope, 6, 7, ol.Claim(kv_bytes=16)), (scope, 8, 9, ol.Claim(kv_bytes=16))]
+    assert oreason(bank.reserve_allocations, tree, 5, 0x5E55, 0, two) == "LeaseNodesExhausted"
+    bank._tree(tree)
+    assert tree.key() == before
+    snap = bank.snapshot()
+    assert snap["used"]["kv_bytes"] == 0 and snap["rejected_lease_nodes"] == 1
+    big = [(scope, 10, 11, ol.Claim(kv_bytes=65))]
+    assert oreason(bank.reserve_allocations, tree, 5, 0x5E55, 0, big) == "CapacityExceeded"
+    snap = bank.snapshot()
+    assert snap["used"]["kv_bytes"] == 0 and snap["rejected_lease_capacity"] == 1
+    batch, _ = bank.reserve_allocations(tree, 5, 0x5E55, 0, [(scope, 12, 13, ol.Claim(kv_bytes=64))])
+    bank.commit_allocations(batch, tree)
+    assert bank.snapshot()["used"]["kv_bytes"] == 64
