@@ -578,3 +578,30 @@ def test_oracle_capacity_and_node_exhaustion_are_atomic_and_distinct():
     batch, _ = bank.reserve_allocations(tree, 5, 0x5E55, 0, [(scope, 12, 13, ol.Claim(kv_bytes=64))])
     bank.commit_allocations(batch, tree)
     assert bank.snapshot()["used"]["kv_bytes"] == 64
+
+
+def test_oracle_retire_cancel_and_forged_permit_keep_the_charge():
+    """resource_bank.zig:6516-6605 on the oracle: a cancelled retirement
+    keeps the charge and its ticket can no longer authorize; an authorized
+    one can no longer cancel; a forged free permit (the reference alters its
+    node-set digest, here its node count) is stale and uncharges nothing."""
+    bank, receipt, tree, scope = _oracle_lane(128, 3, 0x50324345)
+    batch, _ = bank.reserve_allocations(tree, 5, 0x5E55, 0, [(scope, 6, 7, ol.Claim(kv_bytes=64))])
+    bank.commit_allocations(batch, tree)
+    first = bank.begin_retire(tree, scope, 5, 0x5E55, 0)
+    bank.cancel_retire(first, tree)
+    assert bank.snapshot()["used"]["kv_bytes"] == 64
+    assert oreason(bank.authorize_free, first, tree) == "InvalidTransition"
+    second = bank.begin_retire(tree, scope, 5, 0x5E55, 0)
+    permit = bank.authorize_free(second, tree)
+    assert oreason(bank.cancel_retire, second, tree) == "InvalidTransition"
+    assert oreason(bank.commit_free, dict(permit, count=permit["count"] + 1), tree) == "StaleReservation"
+    assert bank.snapshot()["used"]["kv_bytes"] == 64
+    bank.commit_free(permit, tree)
+    bank.close_session(receipt, 5, 0x5E55, 0)
+    bank.close_tree(tree)
+    bank.release(receipt)
+    snap = bank.snapshot()
+    assert not any(snap["used"].values())
+    assert (snap["lease_reclaim_prepares"], snap["lease_reclaim_authorizations"],
+            snap["lease_reclaim_cancels"], snap["lease_reclaim_commits"]) == (2, 1, 1, 1)
