@@ -1552,15 +1552,32 @@ __global__ __launch_bounds__(64 * NW) void attn_o_kernel(AttnOArgs a) {
       acc += tt;
     }
     acc = xor32_add(xor16_add(acc));
-    // (agent-scope stores: written through to the device-coherent level, so
-    // the other XCDs' workgroups read them without an L2 write-back)
+    // agent-scope store: written through to the level all XCDs read (see
+    // the publication below)
     if (c == 0)
       __hip_atomic_store(a.parts + (size_t)h * a.N + nb * 16 + n_local, acc, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
   }
   if (!a.y) return;
-  // publish this slice: every wave waits for its stores to complete before
-  // the barrier, after which one thread counts the group's arrival
+  // Cross-workgroup publication of the Hkv slices. In the HIP language model
+  // this needs an agent-scope release on the counter increment and an
+  // agent-scope acquire in the last arriver; on gfx950 those lower to a
+  // write-back of the whole L2 and an L2 invalidate (measured +4.6 us per
+  // launch). The merge instead rests on how the gfx942-family memory model
+  // of the AMDGPU backend lowers agent-scope atomics, an ISA-level contract:
+  //  (1) an agent-scope atomic store carries the device scope bits, so the
+  //      XCD's L2 writes it through to the memory-side level every XCD
+  //      reads; (2) a store counts in vmcnt until that write is
+  //      acknowledged, so s_waitcnt vmcnt(0) returns only when every partial
+  //      row of this wave is there; (3) an agent-scope atomic load carries
+  //      the same scope bits and reads that level, never a stale L2 line.
+  // The counter (an agent-scope read-modify-write, coherent across XCDs in
+  // any lowering) is incremented only after every wave of the workgroup has
+  // passed (2) (the barrier below), so the last arriver's loads (3) see all
+  // Hkv slices. The built code shows the lowering: the slice stores and the
+  // merge loads are global_store_dword / global_load_dword with sc1. Plain stores or loads of `parts`, or dropping the wait,
+  // would break it; the workgroup-scope fences only keep the compiler from
+  // moving the accesses across the barrier.
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __syncthreads();

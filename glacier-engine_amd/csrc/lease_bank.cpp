@@ -591,19 +591,35 @@ int Bank::begin_publication(const Tree &t, uint64_t request_epoch, uint64_t sess
   return begin_publication_locked(t.parent, request_epoch, session_id, expected_sequence, out);
 }
 
+int Bank::validate_pub_permit_locked(const PubPermit &p, Slot **out) {
+  // validatePublicationPermit (:4133-4155): the permit is the committed
+  // slot's live one for this request epoch, session and sequence, and its
+  // integrity recomputes
+  Slot *s;
+  if (int rc = validate_receipt(p.receipt, &s)) return rc;
+  if (s->state != SlotState::Committed || !s->pub_active || s->pub_permit_integrity != p.integrity ||
+      s->pub_epoch != p.request_epoch || s->pub_session != p.session_id ||
+      s->pub_next != p.sequence || s->pub_permit_gen != p.generation ||
+      p.integrity != pub_permit_integrity(p.receipt, p.request_epoch, p.session_id, p.sequence,
+                                          p.generation))
+    return GLACIER_HIP_LEASE_INVALID_TRANSITION;
+  *out = s;
+  return GLACIER_HIP_LEASE_OK;
+}
+
+int Bank::validate_publication(const PubPermit &p) {
+  std::lock_guard<std::mutex> g(mu);
+  Slot *s;
+  return validate_pub_permit_locked(p, &s);
+}
+
 int Bank::commit_publication(const PubPermit &p) {
   // commitPublicationAssumeValid (:3076-3089): a permit that no longer
   // validates is reported instead of trapping
   std::lock_guard<std::mutex> g(mu);
   Slot *s;
-  if (int rc = validate_receipt(p.receipt, &s)) return rc;
-  if (!s->pub_active || s->pub_permit_integrity != p.integrity || s->pub_epoch != p.request_epoch ||
-      s->pub_session != p.session_id || s->pub_next != p.sequence ||
-      s->pub_permit_gen != p.generation ||
-      p.integrity != pub_permit_integrity(p.receipt, p.request_epoch, p.session_id, p.sequence,
-                                          p.generation) ||
-      p.sequence == UINT64_MAX)
-    return GLACIER_HIP_LEASE_INVALID_TRANSITION;
+  if (int rc = validate_pub_permit_locked(p, &s)) return rc;
+  if (p.sequence == UINT64_MAX) return GLACIER_HIP_LEASE_INVALID_TRANSITION;
   s->pub_active = false;
   s->pub_permit_integrity = 0;
   s->pub_next = p.sequence + 1;
@@ -611,12 +627,10 @@ int Bank::commit_publication(const PubPermit &p) {
 }
 
 int Bank::abort_publication(const PubPermit &p) {
-  // abortPublication (:3091-3102)
+  // abortPublication (:3091-3102): the same permit validation as commit
   std::lock_guard<std::mutex> g(mu);
   Slot *s;
-  if (int rc = validate_receipt(p.receipt, &s)) return rc;
-  if (!s->pub_active || s->pub_permit_integrity != p.integrity || s->pub_permit_gen != p.generation)
-    return GLACIER_HIP_LEASE_INVALID_TRANSITION;
+  if (int rc = validate_pub_permit_locked(p, &s)) return rc;
   s->pub_active = false;
   s->pub_permit_integrity = 0;
   return GLACIER_HIP_LEASE_OK;
@@ -1206,6 +1220,26 @@ int glacier_hip_lease_session_close(glacier_hip_lease_bank *b, const glacier_hip
                                     uint64_t expected_next_sequence) {
   if (!b || !r) return GLACIER_HIP_LEASE_INVALID_ARGUMENT;
   return b->bank.close_session(*r, request_epoch, session_id, expected_next_sequence);
+}
+
+int glacier_hip_lease_publication_begin(glacier_hip_lease_bank *b, const glacier_hip_lease_tree_t *tree,
+                                        uint64_t request_epoch, uint64_t session_id,
+                                        uint64_t expected_sequence,
+                                        glacier_hip_publication_permit_t *out) {
+  if (!b || !tree || !out) return GLACIER_HIP_LEASE_INVALID_ARGUMENT;
+  return b->bank.begin_publication(*tree, request_epoch, session_id, expected_sequence, out);
+}
+
+int glacier_hip_lease_publication_commit(glacier_hip_lease_bank *b,
+                                         const glacier_hip_publication_permit_t *p) {
+  if (!b || !p) return GLACIER_HIP_LEASE_INVALID_ARGUMENT;
+  return b->bank.commit_publication(*p);
+}
+
+int glacier_hip_lease_publication_abort(glacier_hip_lease_bank *b,
+                                        const glacier_hip_publication_permit_t *p) {
+  if (!b || !p) return GLACIER_HIP_LEASE_INVALID_ARGUMENT;
+  return b->bank.abort_publication(*p);
 }
 
 int glacier_hip_lease_bank_snapshot(glacier_hip_lease_bank *b, glacier_hip_lease_bank_snapshot_t *out) {

@@ -139,10 +139,7 @@ struct FreePermit {
 };
 
 // PublicationPermit (:646-654)
-struct PubPermit {
-  Receipt receipt;
-  uint64_t request_epoch, session_id, sequence, generation, integrity;
-};
+using PubPermit = glacier_hip_publication_permit_t;
 
 class Bank {
  public:
@@ -166,6 +163,7 @@ class Bank {
                     uint64_t expected_next_sequence);
   int begin_publication(const Tree &tree, uint64_t request_epoch, uint64_t session_id,
                         uint64_t expected_sequence, PubPermit *out);
+  int validate_publication(const PubPermit &permit);
   int commit_publication(const PubPermit &permit);
   int abort_publication(const PubPermit &permit);
 
@@ -197,6 +195,7 @@ class Bank {
   int validate_ticket_locked(const Ticket &k, RootSlot **out);
   int validate_free_permit_locked(const FreePermit &p, RootSlot **out);
   int validate_pending_locked(uint32_t slot, const RootSlot &root);
+  int validate_pub_permit_locked(const PubPermit &p, Slot **out);
   uint64_t state_digest(uint32_t slot, const RootSlot &root) const;
   uint64_t pending_digest(uint32_t slot, uint64_t tree_identity, uint64_t generation,
                           NState state) const;

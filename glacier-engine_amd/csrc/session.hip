@@ -1136,26 +1136,28 @@ int begin_rows(glacier_hip_session *s, const uint32_t *lanes, uint32_t count,
     need += kv.pages_needed(1);
   }
   if (need > s->pool.free.size()) return GLACIER_HIP_CACHE_FULL;
-  // leased lanes: every new page payload is charged before any map takes one
+  // lane by lane, as LeasedPagedKVCache.beginRowPlanned (leased_paged_kv_cache.zig:482-565):
+  // a leased lane's new page is charged, the map takes it and the charge
+  // settles before the next lane reserves, so lanes sharing one LeaseTree
+  // never leave two allocation batches pending on it. A lane that cannot
+  // begin aborts the rows begun before it (their pages stay charged with
+  // their logical pages, as abortRowTxn leaves them).
   for (uint32_t i = 0; i < count; ++i) {
     glacier_hip_leased_kv *l = s->lanes[lanes[i]].lease;
-    if (!l) continue;
-    if (int rc = l->lease.reserve_rows(1)) {
-      for (uint32_t j = 0; j < i; ++j)
-        if (s->lanes[lanes[j]].lease) s->lanes[lanes[j]].lease->lease.settle_rows(false);
-      return lease_refusal(rc);
+    int rc = GLACIER_HIP_OK;
+    if (l) {
+      const int lrc = l->lease.reserve_rows(1);
+      if (lrc) rc = lease_refusal(lrc);
     }
-  }
-  for (uint32_t i = 0; i < count; ++i) {
-    const int rc = s->lanes[lanes[i]].kv.begin(lanes[i], 1, s->pool, txns);
-    glacier_hip_leased_kv *l = s->lanes[lanes[i]].lease;
+    if (!rc) {
+      rc = s->lanes[lanes[i]].kv.begin(lanes[i], 1, s->pool, txns);
+      if (l) l->lease.settle_rows(rc == GLACIER_HIP_OK);
+    }
     if (rc) {
-      for (uint32_t j = i; j < count; ++j)
-        if (s->lanes[lanes[j]].lease) s->lanes[lanes[j]].lease->lease.settle_rows(false);
+      note_installs(s, txns);  // installed pages stay with their logical pages
       abort_rows(s, txns);
       return rc;
     }
-    if (l) l->lease.settle_rows(true);
   }
   note_installs(s, txns);
   return GLACIER_HIP_OK;
@@ -2310,9 +2312,19 @@ int glacier_hip_session_step_commit(glacier_hip_session *s, const glacier_hip_pr
     P.active = false;
     return GLACIER_HIP_INVALID_TRANSACTION;
   }
+  // the cohort's permit must still be the bank's live one before anything
+  // is published (commitPublicationAssumeValid may not fail after commit)
+  if (P.cohort && P.cohort->lease.bank->validate_publication(P.permit) != GLACIER_HIP_LEASE_OK) {
+    if (!P.first) abort_rows(s, P.txns);
+    P.cohort = nullptr;  // the bank no longer holds this permit
+    P.active = false;
+    s->model->ctx->last_error = "the wave's publication permit is no longer the bank's live permit";
+    return GLACIER_HIP_INVALID_TRANSACTION;
+  }
   if (!P.first) {
     const int rc = commit_rows(s, P.txns);  // staged under the session's rule: cannot fail
     if (rc) {
+      release_permit(P);
       P.active = false;
       return rc;
     }
@@ -2330,16 +2342,29 @@ int glacier_hip_session_step_commit(glacier_hip_session *s, const glacier_hip_pr
   }
   uint8_t commit_sha[32];
   gpub::commit_sha256(P.sha, *ack, commit_sha);
+  int status = GLACIER_HIP_OK;
   if (P.cohort) {
     // the wave's permit commits once (the cohort's sequence advances), then
-    // every leased lane whose terminal token this wave published is sealed
+    // every leased lane whose terminal token this wave published is sealed.
+    // The rows are published by now: a bank or seal refusal here is drift
+    // between the bank and the lanes (the reference traps), reported as
+    // GLACIER_HIP_SCHEDULER_POISONED after the wave's bookkeeping completes.
     glb::Leased &a = P.cohort->lease;
-    if (a.bank->commit_publication(P.permit) == GLACIER_HIP_LEASE_OK) *a.sequence = P.permit.sequence + 1;
+    if (a.bank->commit_publication(P.permit) == GLACIER_HIP_LEASE_OK) {
+      *a.sequence = P.permit.sequence + 1;
+    } else {
+      status = GLACIER_HIP_SCHEDULER_POISONED;
+      s->model->ctx->last_error = "the bank refused a validated publication permit at commit";
+    }
     for (size_t i = 0; i < P.lanes.size(); ++i) {
       const glacier_hip_lane_proposal_v1_t &lp = P.proposal.lanes[P.slots[i]];
       glacier_hip_leased_kv *l = s->lanes[P.lanes[i]].lease;
-      if (l && lp.terminal)
-        (void)l->lease.finalize_wave_terminal(P.permit.sequence, lp.token_id, P.sha, commit_sha);
+      if (l && lp.terminal && status == GLACIER_HIP_OK &&
+          l->lease.finalize_wave_terminal(P.permit.sequence, lp.token_id, P.sha, commit_sha) !=
+              GLACIER_HIP_LEASE_OK) {
+        status = GLACIER_HIP_SCHEDULER_POISONED;
+        s->model->ctx->last_error = "a published terminal token's lane could not be sealed";
+      }
     }
     P.cohort = nullptr;
   }
@@ -2351,7 +2376,7 @@ int glacier_hip_session_step_commit(glacier_hip_session *s, const glacier_hip_pr
     memcpy(receipt_out->commit_sha256, commit_sha, 32);
   }
   P.active = false;
-  return GLACIER_HIP_OK;
+  return status;
 }
 
 }  // extern "C"

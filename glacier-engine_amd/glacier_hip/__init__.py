@@ -209,6 +209,12 @@ LEASE_STATUS = ["OK", "InvalidArgument", "InvalidConfiguration", "InvalidClaim",
                 "InvalidTransaction", "DeviceError"]
 
 
+class PublicationPermit(C.Structure):
+    _fields_ = [("receipt", BankReceipt)] + \
+        [(n, C.c_uint64) for n in ("request_epoch", "session_id", "sequence", "generation",
+                                   "integrity")]
+
+
 class LeaseTree(C.Structure):
     _fields_ = [("abi_version", C.c_uint64), ("parent", BankReceipt)] + \
         [(n, C.c_uint64) for n in ("tree_key", "authority_key", "identity_generation", "generation",
@@ -619,6 +625,11 @@ _SIGS = [
     ("glacier_hip_lease_session_close", C.c_int,
      [_P, C.POINTER(BankReceipt), C.c_uint64, C.c_uint64, C.c_uint64]),
     ("glacier_hip_lease_bank_snapshot", C.c_int, [_P, C.POINTER(LeaseBankSnapshot)]),
+    ("glacier_hip_lease_publication_begin", C.c_int,
+     [_P, C.POINTER(LeaseTree), C.c_uint64, C.c_uint64, C.c_uint64,
+      C.POINTER(PublicationPermit)]),
+    ("glacier_hip_lease_publication_commit", C.c_int, [_P, C.POINTER(PublicationPermit)]),
+    ("glacier_hip_lease_publication_abort", C.c_int, [_P, C.POINTER(PublicationPermit)]),
     ("glacier_hip_leased_kv_create", C.c_int,
      [_P, C.POINTER(LeaseTree), C.POINTER(LeaseNode), _P, C.POINTER(PageLeaseBinding), C.c_uint32,
       C.c_uint64, C.c_uint64, C.POINTER(C.c_uint64), C.POINTER(_P)]),
@@ -1355,6 +1366,21 @@ class LeaseBank:
         lease_check(lib().glacier_hip_lease_session_close(self.h, C.byref(receipt), request_epoch,
                                                           session_id, next_sequence),
                     "close_session")
+
+    def begin_publication(self, tree, request_epoch, session_id, expected_sequence):
+        p = PublicationPermit()
+        lease_check(lib().glacier_hip_lease_publication_begin(
+            self.h, C.byref(tree), request_epoch, session_id, expected_sequence, C.byref(p)),
+            "begin_publication")
+        return p
+
+    def commit_publication(self, permit):
+        lease_check(lib().glacier_hip_lease_publication_commit(self.h, C.byref(permit)),
+                    "commit_publication")
+
+    def abort_publication(self, permit):
+        lease_check(lib().glacier_hip_lease_publication_abort(self.h, C.byref(permit)),
+                    "abort_publication")
 
     def snapshot(self):
         s = LeaseBankSnapshot()

@@ -1229,6 +1229,26 @@ int glacier_hip_lease_session_close(glacier_hip_lease_bank *b, const glacier_hip
                                     uint64_t request_epoch, uint64_t session_id,
                                     uint64_t expected_next_sequence);
 int glacier_hip_lease_bank_snapshot(glacier_hip_lease_bank *b, glacier_hip_lease_bank_snapshot_t *out);
+/* A publication fence permit (PublicationPermit, resource_bank.zig:2938-3102):
+ * one live permit per receipt slot; commit advances the slot's sequence,
+ * abort returns the permit and keeps the sequence. */
+typedef struct {
+    glacier_hip_bank_receipt_t receipt;
+    uint64_t request_epoch, session_id, sequence, generation, integrity;
+} glacier_hip_publication_permit_t;
+/* beginPublicationWithLeaseTree (:2938-2960): the tree has no pending batch,
+ * the session is bound at `expected_sequence` and no permit is live. */
+int glacier_hip_lease_publication_begin(glacier_hip_lease_bank *b, const glacier_hip_lease_tree_t *tree,
+                                        uint64_t request_epoch, uint64_t session_id,
+                                        uint64_t expected_sequence,
+                                        glacier_hip_publication_permit_t *permit_out);
+/* commitPublicationAssumeValid (:3076-3089) and abortPublication (:3091-3102),
+ * both behind validatePublicationPermit (:4133-4155): a stale, copied or
+ * forged permit is GLACIER_HIP_LEASE_INVALID_TRANSITION and changes nothing. */
+int glacier_hip_lease_publication_commit(glacier_hip_lease_bank *b,
+                                         const glacier_hip_publication_permit_t *permit);
+int glacier_hip_lease_publication_abort(glacier_hip_lease_bank *b,
+                                        const glacier_hip_publication_permit_t *permit);
 
 /* The page-lease coordinator of one lane (LeasedPagedKVCache :292-1466).
  * `bindings` is caller-owned storage, one entry per logical page of the

@@ -98,6 +98,65 @@ def test_leased_lane_charges_pages_and_reclaims(gh, model):
         sess.close()
 
 
+def test_two_leased_lanes_on_one_tree_take_pages_in_one_step(gh, model):
+    """Two leased lanes of one LeaseTree (one scope each) whose rows cross a
+    page boundary in the same decode step: each lane's page is reserved,
+    taken and settled before the next lane reserves (beginRowPlanned per
+    coordinator, leased_paged_kv_cache.zig:482-565), so the step succeeds and
+    both lanes decode as unleased lanes do. At the next boundary the second
+    lane's scope is full: the step fails, nothing is published on either
+    lane, and the first lane's new page stays charged with its logical page
+    (abortRowTxn), which that lane then continues onto."""
+    sess = gh.Session(model, max_lanes=4, max_positions=MAXPOS, kv_dtype=gh.F16)
+    try:
+        bank = gh.LeaseBank(2, 16, 0x4C4C, kv_bytes=64 * PB, queue_slots=4)
+        parent = bank.commit(bank.reserve(1, queue_slots=1))
+        tree = bank.open_tree(parent, 2, 3, kv_bytes=16 * PB)
+        scopes = [bank.open_scope(tree, 4, 5, kv_bytes=PAGES * PB),
+                  bank.open_scope(tree, 6, 7, kv_bytes=2 * PB)]
+        seq = C.c_uint64(0)
+        bank.bind_session(tree, 6, 0x5E55)
+        prompts = [gh.synth_tokens(SEED, 40 + i, TINY["vocab_size"], 15) for i in range(2)]
+        for lane in range(4):
+            sess.begin(lane, seed=lane % 2)
+        lks = [gh.LeasedKV(bank, tree, scopes[lane], sess, 6, 0x5E55, seq, lane=lane,
+                           binding_count=PAGES) for lane in range(2)]
+        toks = [sess.prefill(lane, prompts[lane]) for lane in range(2)]
+        ref = [sess.prefill(2 + lane, prompts[lane]) for lane in range(2)]
+        assert toks == ref and tree.current.kv_bytes == 2 * PB
+        print("two leased lanes: steps over a page boundary", flush=True)
+        for row in range(15, 32):  # row 16 takes a new page on both lanes in one step
+            toks = [int(t) for t in sess.step([0, 1], toks)]
+            ref = [int(t) for t in sess.step([2, 3], ref)]
+            assert toks == ref
+            assert tree.current.kv_bytes == (4 if row >= 16 else 2) * PB
+        assert lks[0].binding_summary().count == lks[1].binding_summary().count == 2
+        root0, root1, state1 = sess.root(0), sess.root(1), sess.state(1)
+        # row 32: lane 0's third page is charged and taken, lane 1's scope
+        # refuses its third: the step fails and publishes nothing
+        rc, _ = sess.step([0, 1], toks, raise_on_error=False)
+        assert rc == gh.OUT_OF_MEMORY
+        assert sess.root(0).committed_len == root0.committed_len == 32
+        assert sess.root(1).committed_len == root1.committed_len == 32
+        assert sess.state(1).published_tokens == state1.published_tokens
+        assert tree.current.kv_bytes == 5 * PB
+        assert lks[0].binding_summary().count == 3 and lks[1].binding_summary().count == 2
+        # lane 0 alone continues onto the page it already holds
+        assert int(sess.step([0], toks[:1])[0]) == int(sess.step([2], ref[:1])[0])
+        assert tree.current.kv_bytes == 5 * PB
+        assert sess.kv_sha256(0) == sess.kv_sha256(2)
+        for lk in lks:
+            lk.reclaim_for_teardown(seq.value)
+            lk.close()
+        assert tree.current.kv_bytes == 0
+        bank.close_session(parent, 6, 0x5E55, seq.value)
+        bank.close_tree(tree)
+        bank.release(parent)
+        assert not any(bank.snapshot()["used"].values())
+    finally:
+        sess.close()
+
+
 def lib_rc(gh, sess, lane):
     return gh.lib().glacier_hip_session_lane_begin(sess.h, lane, 0)
 
@@ -185,33 +244,33 @@ def test_leased_waves_publish_under_one_cohort_permit(gh, model):
         assert rc == gh.OK and prop.resource_permit_generation == 3
         rc, _ = sess.step_commit(_ack(gh, bytes(32), 2))
         assert rc == gh.INVALID_TRANSACTION and seq.value == 1
-        for wave in range(12):
-            terminal = (1,) if wave == 11 else ()
+        for wave in range(14):  # wave 12 writes row 32: both lanes take a page in one wave
+            terminal = (1,) if wave == 13 else ()
             rc, prop, sha, nxt = sess.step_prepare([0, 1], toks,
                                                    _wave_binding(gh, [0, 1], seq.value, terminal))
             assert rc == gh.OK
             rc, rec = sess.step_commit(_ack(gh, sha, 10 + wave))
             assert rc == gh.OK
             toks = [int(t) for t in nxt]
-        assert seq.value == 13
-        # 20 prompt rows + 12 decode rows (the first-token wave writes none):
-        # 32 rows, two pages per lane
-        assert tree.current.kv_bytes == 4 * PB
+        assert seq.value == 15
+        # 20 prompt rows + 14 decode rows (the first-token wave writes none):
+        # 34 rows, three pages per lane
+        assert tree.current.kv_bytes == 6 * PB
         seal, psha, csha = lks[1].terminal_seal()
         assert psha == sha and csha == bytes(rec.commit_sha256)
-        assert seal.transaction_sequence == 12 and seal.terminal_token == toks[1]
-        assert seal.bindings.count == 2
+        assert seal.transaction_sequence == 14 and seal.terminal_token == toks[1]
+        assert seal.bindings.count == 3
         assert lks[0].lifecycle() == "live" and lks[1].lifecycle() == "terminal_retained"
         with pytest.raises(gh.LeaseError) as e:
-            lks[1].begin_reclaim(seal, 12)  # the reclaim comes after the terminal sequence
+            lks[1].begin_reclaim(seal, 14)  # the reclaim comes after the terminal sequence
         assert e.value.reason == "InvalidTerminalSeal"
-        freed = lks[1].begin_reclaim(seal, 13)
+        freed = lks[1].begin_reclaim(seal, 15)
         lks[1].commit_reclaim(freed)
-        assert tree.current.kv_bytes == 2 * PB
+        assert tree.current.kv_bytes == 3 * PB
         # lane 0 publishes on alone; then teardown
-        rc, prop, sha, nxt = sess.step_prepare([0], toks[:1], _wave_binding(gh, [0], 13))
+        rc, prop, sha, nxt = sess.step_prepare([0], toks[:1], _wave_binding(gh, [0], 15))
         assert rc == gh.OK
-        assert sess.step_commit(_ack(gh, sha, 99))[0] == gh.OK and seq.value == 14
+        assert sess.step_commit(_ack(gh, sha, 99))[0] == gh.OK and seq.value == 16
         lks[0].reclaim_for_teardown(seq.value)
         assert tree.current.kv_bytes == 0
         for lk in lks:

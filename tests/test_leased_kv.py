@@ -605,3 +605,90 @@ def test_oracle_retire_cancel_and_forged_permit_keep_the_charge():
     assert not any(snap["used"].values())
     assert (snap["lease_reclaim_prepares"], snap["lease_reclaim_authorizations"],
             snap["lease_reclaim_cancels"], snap["lease_reclaim_commits"]) == (2, 1, 1, 1)
+
+
+def _bound_tree(gh, bank, owner, epoch, session):
+    parent = bank.commit(bank.reserve(owner, queue_slots=4))
+    tree = bank.open_tree(parent, owner + 1, owner + 2, queue_slots=4)
+    bank.bind_session(tree, epoch, session)
+    return parent, tree
+
+
+def _reason(gh, fn, *args):
+    with pytest.raises(gh.LeaseError) as e:
+        fn(*args)
+    return e.value.reason
+
+
+def test_publication_permit_lifecycle(gh):
+    """resource_bank.zig:5019-5077 ("publication session permits are exact and
+    single-use"), with the session bound through a LeaseTree: one live permit
+    per receipt, abort and commit each take it once, commit advances the
+    sequence, a retry gets a new generation."""
+    bank = gh.LeaseBank(1, 4, 21, queue_slots=4)
+    parent, tree = _bound_tree(gh, bank, 7, 99, 0x51)
+    assert _reason(gh, bank.bind_session, tree, 99, 0x51) == "InvalidTransition"
+    first = bank.begin_publication(tree, 99, 0x51, 0)
+    assert _reason(gh, bank.begin_publication, tree, 99, 0x51, 0) == "InvalidTransition"
+    assert _reason(gh, bank.close_session, parent, 99, 0x51, 0) == "InvalidTransition"
+    bank.abort_publication(first)
+    assert _reason(gh, bank.abort_publication, first) == "InvalidTransition"
+    retry = bank.begin_publication(tree, 99, 0x51, 0)
+    assert retry.generation != first.generation
+    bank.commit_publication(retry)
+    assert _reason(gh, bank.commit_publication, retry) == "InvalidTransition"
+    assert _reason(gh, bank.begin_publication, tree, 99, 0x51, 0) == "InvalidTransition"
+    second = bank.begin_publication(tree, 99, 0x51, 1)
+    bank.abort_publication(second)
+    bank.close_session(parent, 99, 0x51, 1)
+    bank.close_tree(tree)
+    bank.release(parent)
+    bank.close()
+
+
+def test_publication_permit_rejects_forged_identity(gh):
+    """resource_bank.zig:5126-5163 ("publication permit rejects wrong
+    coordinator and forged identity"): a permit copied with another session,
+    another sequence, epoch or generation, or a flipped integrity word is
+    refused by abort and by commit and changes nothing; the real permit
+    still aborts."""
+    bank = gh.LeaseBank(1, 4, 22, queue_slots=4)
+    parent, tree = _bound_tree(gh, bank, 8, 100, 0xA1)
+    assert _reason(gh, bank.begin_publication, tree, 100, 0xA2, 0) == "InvalidTransition"
+    permit = bank.begin_publication(tree, 100, 0xA1, 0)
+    for field, delta in (("session_id", 1), ("integrity", 1), ("sequence", 1),
+                         ("request_epoch", 1), ("generation", 1)):
+        forged = gh.PublicationPermit.from_buffer_copy(permit)
+        setattr(forged, field, getattr(forged, field) ^ delta)
+        assert _reason(gh, bank.abort_publication, forged) == "InvalidTransition", field
+        assert _reason(gh, bank.commit_publication, forged) == "InvalidTransition", field
+    bank.abort_publication(permit)
+    assert _reason(gh, bank.close_session, parent, 100, 0xA2, 0) == "InvalidTransition"
+    bank.close_session(parent, 100, 0xA1, 0)
+    bank.close_tree(tree)
+    bank.release(parent)
+    bank.close()
+
+
+def test_publication_close_is_terminal_and_prevents_replay(gh):
+    """resource_bank.zig:5165-5211 ("publication close is terminal for one
+    receipt and prevents replay ABA"): after close the receipt cannot bind
+    again; once the receipt is released a permit from it is a stale
+    reservation, even when a new receipt takes the same slot."""
+    bank = gh.LeaseBank(1, 4, 24, queue_slots=4)
+    parent, tree = _bound_tree(gh, bank, 9, 101, 0xB1)
+    stale = bank.begin_publication(tree, 101, 0xB1, 0)
+    bank.abort_publication(stale)
+    bank.close_session(parent, 101, 0xB1, 0)
+    assert _reason(gh, bank.bind_session, tree, 101, 0xB1) == "InvalidTransition"
+    bank.close_tree(tree)
+    bank.release(parent)
+    parent2, tree2 = _bound_tree(gh, bank, 10, 101, 0xB1)
+    current = bank.begin_publication(tree2, 101, 0xB1, 0)
+    assert current.receipt.generation != stale.receipt.generation
+    assert _reason(gh, bank.abort_publication, stale) == "StaleReservation"
+    bank.abort_publication(current)
+    bank.close_session(parent2, 101, 0xB1, 0)
+    bank.close_tree(tree2)
+    bank.release(parent2)
+    bank.close()
