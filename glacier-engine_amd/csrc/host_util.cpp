@@ -118,4 +118,12 @@ float f16_to_f32(uint16_t hv) {
   return f;
 }
 
+void token_sequence_sha256(const uint32_t *tokens, size_t count, uint8_t out[32]) {
+  Sha256 h;
+  h.update("glacier-output-token-state-v1\0", 30);
+  h.u64(count);
+  for (size_t i = 0; i < count; ++i) h.u32(tokens[i]);
+  h.final(out);
+}
+
 }  // namespace gh

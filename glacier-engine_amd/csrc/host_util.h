@@ -32,6 +32,10 @@ struct Sha256 {
   }
 };
 
+// tokenSequenceSha256 (generate.zig:3193-3203): domain, count (u64 LE),
+// then every token (u32 LE)
+void token_sequence_sha256(const uint32_t *tokens, size_t count, uint8_t out[32]);
+
 uint16_t f32_to_f16(float f);
 float f16_to_f32(uint16_t h);
 

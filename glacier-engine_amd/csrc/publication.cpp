@@ -169,4 +169,10 @@ int glacier_hip_token_commit_sha256(const uint8_t proposal_sha256[32],
   return GLACIER_HIP_OK;
 }
 
+int glacier_hip_token_sequence_sha256(const uint32_t *tokens, uint64_t count, uint8_t out[32]) {
+  if (!out || (count && !tokens)) return GLACIER_HIP_INVALID_ARGUMENT;
+  gh::token_sequence_sha256(tokens, (size_t)count, out);
+  return GLACIER_HIP_OK;
+}
+
 }  // extern "C"

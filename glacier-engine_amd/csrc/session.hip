@@ -1834,12 +1834,7 @@ int glacier_hip_session_lane_state(glacier_hip_session *s, uint32_t lane,
   out->published_tokens = ln.output.size();
   out->sampling_calls = ln.sampling_calls;
   memcpy(out->rng_state, ln.rng, sizeof ln.rng);
-  // tokenSequenceSha256 (generate.zig:3193-3203)
-  gh::Sha256 h;
-  h.update("glacier-output-token-state-v1\0", 30);
-  h.u64(ln.output.size());
-  for (uint32_t t : ln.output) h.u32(t);
-  h.final(out->output_sha256);
+  gh::token_sequence_sha256(ln.output.data(), ln.output.size(), out->output_sha256);
   return GLACIER_HIP_OK;
 }
 

@@ -564,6 +564,7 @@ _SIGS = [
     ("glacier_hip_session_step_abort", C.c_int, [_P]),
     ("glacier_hip_token_proposal_sha256", C.c_int, [C.POINTER(TokenProposal), _P]),
     ("glacier_hip_token_commit_sha256", C.c_int, [_P, C.POINTER(PrepareAck), _P]),
+    ("glacier_hip_token_sequence_sha256", C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p]),
     ("glacier_hip_synth_int4", None, [C.c_uint64, C.c_uint64, _P, C.c_uint64]),
     ("glacier_hip_synth_scales_f16", None, [C.c_uint64, C.c_uint64, C.c_float, _P, C.c_uint64]),
     ("glacier_hip_synth_normal_f32", None, [C.c_uint64, C.c_uint64, C.c_float, _P, C.c_uint64]),

@@ -868,6 +868,9 @@ int glacier_hip_token_proposal_sha256(const glacier_hip_token_proposal_v1_t *pro
                                       uint8_t out[32]);
 int glacier_hip_token_commit_sha256(const uint8_t proposal_sha256[32],
                                     const glacier_hip_prepare_ack_v1_t *ack, uint8_t out[32]);
+/* tokenSequenceSha256 (generate.zig:3193-3203): the output digest a lane's
+ * state reports, for a host that verifies a receipt's token journal. */
+int glacier_hip_token_sequence_sha256(const uint32_t *tokens, uint64_t count, uint8_t out[32]);
 
 /* ---- paged-KV checkpoint page images ------------------------------------
  * src/continuation_paged_kv_restore.zig (PageImageV1, :18-360) and

@@ -83,6 +83,7 @@ def lib():
             "go_paged_empty_ownership_digest": (None, [C.c_uint64] * 4 + [_P]),
             "go_paged_append_ownership_digest": (None, [_P] + [C.c_uint64] * 3 + [_P]),
             "go_token_sequence_sha256": (None, [_P, sz, _P]),
+            "go_logical_kv_sha256": (None, [_P, _P, sz, sz, sz, sz, _P]),
             "go_xoshiro256_init": (None, [C.c_uint64, _P]),
         }
         for name, (res, args) in sig.items():
@@ -242,6 +243,17 @@ def append_ownership_digest(before, inst, page, gen):
     b = np.frombuffer(before, dtype=np.uint8).copy()
     out = np.zeros(32, dtype=np.uint8)
     lib().go_paged_append_ownership_digest(_p(b), inst, page, gen, _p(out))
+    return out.tobytes()
+
+
+def logical_kv_sha256(k, v, positions):
+    """logicalKvPrefixSha256 of the first `positions` rows of k, v [L][max_seq][kv_dim]."""
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    assert k.shape == v.shape and k.ndim == 3 and positions <= k.shape[1]
+    out = np.zeros(32, dtype=np.uint8)
+    lib().go_logical_kv_sha256(_p(k), _p(v), k.shape[0], k.shape[1], k.shape[2], positions,
+                               _p(out))
     return out.tobytes()
 
 

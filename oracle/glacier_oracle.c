@@ -677,21 +677,7 @@ int go_generate(const go_model *m, const uint32_t *prompt, size_t prompt_len,
         next = (uint32_t)go_argmax(logits, V);
         tokens_out[step] = next;
     }
-    if (kv_sha256_out) {
-        /* generate.zig:3150-3172 over the committed prefix (pos rows) */
-        go_sha256_ctx c;
-        go_sha256_init(&c);
-        go_sha256_update(&c, "glacier-logical-kv-state-v1\0", 28);
-        hash_u64(&c, L);
-        hash_u64(&c, kv_dim);
-        hash_u64(&c, pos);
-        for (size_t l = 0; l < L; l++) {
-            const float *kl = kc + l * max_seq * kv_dim, *vl = vc + l * max_seq * kv_dim;
-            for (size_t i = 0; i < pos * kv_dim; i++) { uint32_t b; memcpy(&b, &kl[i], 4); hash_u32(&c, b); }
-            for (size_t i = 0; i < pos * kv_dim; i++) { uint32_t b; memcpy(&b, &vl[i], 4); hash_u32(&c, b); }
-        }
-        go_sha256_final(&c, kv_sha256_out);
-    }
+    if (kv_sha256_out) go_logical_kv_sha256(kc, vc, L, max_seq, kv_dim, pos, kv_sha256_out);
     if (output_sha256_out) go_token_sequence_sha256(tokens_out, max_new, output_sha256_out);
 out:
     free(kc); free(vc); free(rc_t); free(rs_t); free(x); free(nx); free(fh); free(logits);
@@ -821,6 +807,25 @@ void go_paged_append_ownership_digest(const uint8_t before[32], uint64_t inst,
     hash_u64(&c, inst);
     hash_u64(&c, logical_page);
     hash_u64(&c, gen);
+    go_sha256_final(&c, out);
+}
+
+/* logicalKvPrefixSha256 (generate.zig:3150-3172) over the committed prefix:
+ * domain, layer count, kv_dim and positions (u64 LE), then per layer the K
+ * rows and then the V rows of positions [0, pos) as f32 bit patterns. */
+void go_logical_kv_sha256(const float *k, const float *v, size_t L, size_t max_seq, size_t kv_dim,
+                          size_t pos, uint8_t out[32]) {
+    go_sha256_ctx c;
+    go_sha256_init(&c);
+    go_sha256_update(&c, "glacier-logical-kv-state-v1\0", 28);
+    hash_u64(&c, L);
+    hash_u64(&c, kv_dim);
+    hash_u64(&c, pos);
+    for (size_t l = 0; l < L; l++) {
+        const float *kl = k + l * max_seq * kv_dim, *vl = v + l * max_seq * kv_dim;
+        for (size_t i = 0; i < pos * kv_dim; i++) { uint32_t b; memcpy(&b, &kl[i], 4); hash_u32(&c, b); }
+        for (size_t i = 0; i < pos * kv_dim; i++) { uint32_t b; memcpy(&b, &vl[i], 4); hash_u32(&c, b); }
+    }
     go_sha256_final(&c, out);
 }
 

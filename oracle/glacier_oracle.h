@@ -193,6 +193,9 @@ void go_paged_append_ownership_digest(const uint8_t before[32],
                                       uint64_t ownership_generation,
                                       uint8_t out[32]);
 /* generate.zig:3193-3203 */
+/* logicalKvPrefixSha256 (generate.zig:3150-3172); k, v are [L][max_seq][kv_dim]. */
+void go_logical_kv_sha256(const float *k, const float *v, size_t L, size_t max_seq, size_t kv_dim,
+                          size_t pos, uint8_t out[32]);
 void go_token_sequence_sha256(const uint32_t *tokens, size_t n,
                               uint8_t out[32]);
 

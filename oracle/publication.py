@@ -43,17 +43,24 @@ def root_bytes(generation, committed_len, committed_pages, ownership, cache_inst
             _u64(committed_len) + _u64(committed_pages) + bytes(ownership))
 
 
+def initial_state_chain_preimage(logical_kv_sha256, root):
+    return b"glacier-paged-token-kv-chain-seed-v1\x00" + bytes(logical_kv_sha256) + root
+
+
 def initial_state_chain(logical_kv_sha256, root):
-    return hashlib.sha256(b"glacier-paged-token-kv-chain-seed-v1\x00" + bytes(logical_kv_sha256) +
-                          root).digest()
+    return hashlib.sha256(initial_state_chain_preimage(logical_kv_sha256, root)).digest()
 
 
-def appended_state_chain(chain_before, root_before, root_after, cache_instance, logical_page,
-                         ownership_generation, row_txn_generation, row_payload_sha256):
-    return hashlib.sha256(
-        b"glacier-paged-token-kv-chain-append-v1\x00" + bytes(chain_before) + root_before +
-        root_after + _u64(PAGE_REF_ABI) + _u64(cache_instance) + _u64(logical_page) +
-        _u64(ownership_generation) + _u64(row_txn_generation) + bytes(row_payload_sha256)).digest()
+def appended_state_chain_preimage(chain_before, root_before, root_after, cache_instance,
+                                  logical_page, ownership_generation, row_txn_generation,
+                                  row_payload_sha256):
+    return (b"glacier-paged-token-kv-chain-append-v1\x00" + bytes(chain_before) + root_before +
+            root_after + _u64(PAGE_REF_ABI) + _u64(cache_instance) + _u64(logical_page) +
+            _u64(ownership_generation) + _u64(row_txn_generation) + bytes(row_payload_sha256))
+
+
+def appended_state_chain(*args):
+    return hashlib.sha256(appended_state_chain_preimage(*args)).digest()
 
 
 def row_payload_sha256(num_layers, dim, base_len, rows_f32):
@@ -77,8 +84,8 @@ _TRANSITION_U64 = ("abi_version", "kv_row_txn_abi", "page_map_root_abi", "page_r
                    "root_before_pages", "root_after_pages")
 
 
-def proposal_sha256(p):
-    """proposalSha256 over a ProposalV1 record (any object with the fields)."""
+def proposal_preimage(p):
+    """The bytes proposalSha256 hashes for a ProposalV1 record (any object with the fields)."""
     b = bytearray(b"glacier-paged-token-txn-proposal-v1\x00")
     for f in _PROPOSAL_HEAD:
         b += _u64(getattr(p, f))
@@ -108,13 +115,21 @@ def proposal_sha256(p):
             b += _u64(w)
         b += _u64(lane.sampling_calls_before) + _u64(lane.sampling_calls_after)
         b += _u32(lane.token_id) + _u8(1 if lane.terminal else 0)
-    return hashlib.sha256(bytes(b)).digest()
+    return bytes(b)
+
+
+def proposal_sha256(p):
+    return hashlib.sha256(proposal_preimage(p)).digest()
 
 
 COMMIT_RECEIPT_ABI = 0x4750544300000001
 
 
-def commit_sha256(proposal_sha, ack_abi, ack_proposal_sha, sink_epoch, reservation_id):
-    return hashlib.sha256(b"glacier-paged-token-txn-commit-v1\x00" + _u64(COMMIT_RECEIPT_ABI) +
-                          bytes(proposal_sha) + _u64(ack_abi) + bytes(ack_proposal_sha) +
-                          _u64(sink_epoch) + _u64(reservation_id)).digest()
+def commit_preimage(proposal_sha, ack_abi, ack_proposal_sha, sink_epoch, reservation_id):
+    return (b"glacier-paged-token-txn-commit-v1\x00" + _u64(COMMIT_RECEIPT_ABI) +
+            bytes(proposal_sha) + _u64(ack_abi) + bytes(ack_proposal_sha) + _u64(sink_epoch) +
+            _u64(reservation_id))
+
+
+def commit_sha256(*args):
+    return hashlib.sha256(commit_preimage(*args)).digest()

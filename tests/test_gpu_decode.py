@@ -6,8 +6,6 @@ Bars: identical greedy token sequences; logits within 1e-2 max-relative
 error (max |gpu - oracle| / max |oracle|); page-map roots, output digests and
 sampler counters exactly as the reference's transaction rules produce them.
 """
-import hashlib
-import struct
 
 import numpy as np
 import pytest
@@ -155,14 +153,11 @@ def test_page_roots_follow_reference_chain(gh, tiny, ora):
         r = sess.root(0)
         assert (r.committed_len, r.committed_pages, r.generation) == (17, 2, 1 + 17)
         assert bytes(r.ownership_sha256) == digest
-        # the logical KV digest of the device rows (generate.zig:3150-3172)
-        h = hashlib.sha256(b"glacier-logical-kv-state-v1\x00" +
-                           struct.pack("<3Q", TINY["num_layers"], kvd, 17))
-        for l in range(TINY["num_layers"]):
-            for v in (0, 1):
-                for p in range(17):
-                    h.update(sess.kv_row(0, l, v, p, kvd).astype("<f4").tobytes())
-        assert sess.kv_sha256(0) == h.digest()
+        # the logical KV digest of the device rows (generate.zig:3150-3172) =
+        # the oracle's, which the reference's logical_kv_root vectors pin
+        rows = np.array([[[sess.kv_row(0, l, v, p, kvd) for p in range(17)] for v in (0, 1)]
+                         for l in range(TINY["num_layers"])], dtype=np.float32)
+        assert sess.kv_sha256(0) == ora.logical_kv_sha256(rows[:, 0], rows[:, 1], 17)
         assert sess.page_of(0, 0) >= 0 and sess.page_of(0, 2) == -1
     finally:
         sess.close()
