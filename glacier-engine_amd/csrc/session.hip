@@ -142,6 +142,11 @@ struct glacier_hip_session {
   int32_t *pt_host = nullptr;    // mirror of page_table [max_lanes][max_pages]
   gk::ArgmaxResult *res_host = nullptr;
   bool inject_failure = false;
+  // test tap: with a buffer, each decode step copies the residual after
+  // every layer into tap_x [num_layers][rows][dim] (direct launches only)
+  float *tap_x = nullptr;
+  uint32_t tap_rows = 0;
+  bool tap_now = false;
   PreparedWave prep;
   // sealed step plans: key = (rows, with_head, eligible, prehead, fused
   // attention + O). The step's launches are captured once (every host-side
@@ -986,6 +991,11 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
     }
     e = run_proj(s, L.down, Dd, rows, gk::EPI_RESID, din, dout, st);
     if (e != hipSuccess) return e;
+    if (s->tap_now) {
+      e = hipMemcpyAsync(s->tap_x + (size_t)l * rows * D, s->x_res, (size_t)rows * D * 4,
+                         hipMemcpyDeviceToDevice, st);
+      if (e != hipSuccess) return e;
+    }
   }
   return hipSuccess;
 }
@@ -1051,7 +1061,7 @@ void destroy_session(glacier_hip_session *s) {
                   s->arg_counters,
                   s->arg_result,
                   s->elig_words, s->splitk_ws,
-                  s->step_dev, s->pf_dev};
+                  s->step_dev, s->pf_dev, s->tap_x};
   for (void *p : ptrs) gh::dev_free(s->model->ctx, p);
   if (s->step_host) (void)hipHostFree(s->step_host);
   if (s->pf_host) (void)hipHostFree(s->pf_host);
@@ -1298,7 +1308,13 @@ int run_step(glacier_hip_session *s, const uint32_t *lanes, const uint32_t *toke
   const bool elig = elig_host != nullptr;
   const bool pre = elig && s->head_domain == GLACIER_HIP_HEAD_DOMAIN_PREHEAD;
   const bool fused = count == 1 && txns[0].pos + 1 <= kFusedMaxCtx && attn_o_usable(s);
-  if (s->opt.use_graph) {
+  s->tap_now = s->tap_x != nullptr;
+  if (s->tap_now) {  // a traced step launches directly (its copies are not plan nodes)
+    s->tap_rows = count;
+    e = enqueue_step(s, (int)count, head, elig, pre, fused, st);
+    s->tap_now = false;
+    if (e != hipSuccess) return fail(e, "enqueue traced step");
+  } else if (s->opt.use_graph) {
     glacier_hip_session::GraphEntry *plan = nullptr;
     for (auto &g : s->graphs)
       if (g.rows == count && g.head == head && g.elig == elig && g.pre == pre && g.fused == fused)
@@ -1735,6 +1751,33 @@ int glacier_hip_session_lane_begin(glacier_hip_session *s, uint32_t lane, uint64
 int glacier_hip_session_inject_failure(glacier_hip_session *s, int enable) {
   if (!s) return GLACIER_HIP_INVALID_HANDLE;
   s->inject_failure = enable != 0;
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_session_trace_layers(glacier_hip_session *s, int enable) {
+  if (!s) return GLACIER_HIP_INVALID_HANDLE;
+  GH_SUBMISSION(s->model->ctx);
+  glacier_hip_context *ctx = s->model->ctx;
+  if (enable && !s->tap_x) {
+    const auto &c = s->model->cfg;
+    const size_t n = (size_t)c.num_layers * s->lanes.size() * c.dim;
+    GH_CHECK(ctx, gh::dev_malloc(ctx, (void **)&s->tap_x, n * 4));
+  } else if (!enable && s->tap_x) {
+    gh::dev_free(ctx, s->tap_x);
+    s->tap_x = nullptr;
+  }
+  s->tap_rows = 0;
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_session_layer_trace(glacier_hip_session *s, float *out_host, uint32_t *rows_out) {
+  if (!s || !out_host || !rows_out) return GLACIER_HIP_INVALID_ARGUMENT;
+  GH_SUBMISSION(s->model->ctx);
+  if (!s->tap_x || !s->tap_rows) return GLACIER_HIP_INVALID_TRANSACTION;
+  const auto &c = s->model->cfg;
+  GH_CHECK(s->model->ctx, hipMemcpy(out_host, s->tap_x, (size_t)c.num_layers * s->tap_rows * c.dim * 4,
+                                    hipMemcpyDeviceToHost));
+  *rows_out = s->tap_rows;
   return GLACIER_HIP_OK;
 }
 

@@ -555,6 +555,8 @@ _SIGS = [
     ("glacier_hip_kv_pages_validate_page_ref", C.c_int, [_P, C.POINTER(PageRef)]),
     ("glacier_hip_kv_pages_ledger", C.c_int, [_P, C.POINTER(ResidentLedger)]),
     ("glacier_hip_session_inject_failure", C.c_int, [_P, C.c_int]),
+    ("glacier_hip_session_trace_layers", C.c_int, [_P, C.c_int]),
+    ("glacier_hip_session_layer_trace", C.c_int, [_P, _P, C.POINTER(C.c_uint32)]),
     ("glacier_hip_session_prefill_staged", C.c_int, [_P, C.c_uint32, _P, C.c_uint32, _P, _P]),
     ("glacier_hip_session_step_prepare", C.c_int,
      [_P, _P, _P, C.c_uint32, _P, C.POINTER(PublicationBinding), C.POINTER(TokenProposal), _P,
@@ -970,6 +972,7 @@ class Session:
                  layer_activation=ACT_AUTO, head_activation=ACT_AUTO, use_graph=True,
                  prefill_chunk=0, split_attention_o=False):
         self.model = model
+        self.max_lanes = max_lanes
         o = SessionOptions(max_lanes=max_lanes, max_positions=max_positions,
                            total_pages=total_pages, kv_dtype=kv_dtype,
                            layer_activation=layer_activation, head_activation=head_activation,
@@ -1073,6 +1076,19 @@ class Session:
 
     def inject_failure(self, enable):
         check(lib().glacier_hip_session_inject_failure(self.h, 1 if enable else 0), "inject")
+
+    def trace_layers(self, enable):
+        check(lib().glacier_hip_session_trace_layers(self.h, 1 if enable else 0), "trace_layers")
+
+    def layer_trace(self):
+        """The last traced step's residual after every layer: [num_layers, rows, dim]."""
+        c = self.model.cfg
+        buf = np.zeros(c["num_layers"] * self.max_lanes * c["dim"], np.float32)
+        rows = C.c_uint32()
+        check(lib().glacier_hip_session_layer_trace(self.h, buf.ctypes.data, C.byref(rows)),
+              "layer_trace")
+        n = rows.value
+        return buf[:c["num_layers"] * n * c["dim"]].reshape(c["num_layers"], n, c["dim"])
 
     def encode_page_image(self, lane, logical_page, challenge):
         """glacier_hip_session_encode_page_image -> (image bytes, PageImageInfo)."""

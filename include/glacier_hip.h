@@ -624,6 +624,16 @@ int glacier_hip_session_set_head_domain(glacier_hip_session *s, int mode);
 /* Test hook: make the next decode step fail after its kernels ran but before
  * commit (forces the abort path, as a failed sink/ack would). */
 int glacier_hip_session_inject_failure(glacier_hip_session *s, int enable);
+/* Test hook: with `enable`, every later decode step copies the residual
+ * stream after each layer (the output of forwardLayerCached,
+ * generate.zig:1511-1967) into a session buffer of num_layers x max_lanes x
+ * dim floats (allocated here through the allocation lease, freed when
+ * disabled or with the session); traced steps launch their kernels directly
+ * instead of replaying a sealed plan. layer_trace copies the last traced
+ * step's [num_layers][rows][dim] residuals to the host and its row count to
+ * *rows_out (rows in the step's lane order). */
+int glacier_hip_session_trace_layers(glacier_hip_session *s, int enable);
+int glacier_hip_session_layer_trace(glacier_hip_session *s, float *out_host, uint32_t *rows_out);
 
 /* ---- LaneWeave QoS v1 multi-request scheduler ----------------------------
  * The reference's deterministic interleaved weighted round-robin scheduler

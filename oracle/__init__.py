@@ -77,6 +77,7 @@ def lib():
             "go_argmax": (sz, [_P, sz]),
             "go_argmax_eligible": (C.c_int, [_P, sz, _P, sz, C.POINTER(sz), C.POINTER(sz)]),
             "go_generate": (C.c_int, [C.POINTER(Model), _P, sz, sz, _P, _P, sz, _P, _P, _P]),
+            "go_generate_forced": (C.c_int, [C.POINTER(Model), _P, sz, sz, _P, _P, _P, sz, _P]),
             "go_forward_layer": (C.c_int, [C.POINTER(Model), sz, _P, _P, _P, sz, _P, _P, _P]),
             "go_sha256": (None, [_P, sz, _P]),
             "go_paged_capacity_ledger": (C.c_int, [C.c_uint64] * 3 + [C.POINTER(Ledger)]),
@@ -322,6 +323,38 @@ class OracleModel:
                                         _p(cs), _p(sn), _p(out[t]))
             assert rc == OK, rc
         return out
+
+    def forward_layer_at(self, li, x, k_hist, v_hist):
+        """go_forward_layer for one token at position p = len(k_hist) over a
+        given K/V history of this layer ([p, kv_dim] rows, e.g. read back from
+        a device cache); returns (layer output, the K row, the V row)."""
+        x = f32(x)
+        p = len(k_hist)
+        kvd = self.cfg["num_kv_heads"] * self.cfg["head_dim"]
+        kc = np.zeros((p + 1, kvd), np.float32)
+        vc = np.zeros((p + 1, kvd), np.float32)
+        kc[:p], vc[:p] = k_hist, v_hist
+        cs, sn = rope_table(p + 1, self.cfg["head_dim"], self.cfg["rope_theta"])
+        out = np.zeros_like(x)
+        rc = lib().go_forward_layer(C.byref(self.m), li, _p(x), _p(kc), _p(vc), p, _p(cs),
+                                    _p(sn), _p(out))
+        assert rc == OK, rc
+        return out, kc[p].copy(), vc[p].copy()
+
+    def generate_forced(self, prompt, forced, logits_steps=()):
+        """Greedy argmax of every step with step s >= 1 fed forced[s - 1];
+        returns (argmax tokens, logits at logits_steps)."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        forced = np.ascontiguousarray(forced, dtype=np.uint32)
+        max_new = forced.size + 1
+        toks = np.zeros(max_new, dtype=np.uint32)
+        steps = np.ascontiguousarray(list(logits_steps) or [-1], dtype=np.int32)
+        logits = np.zeros((max(len(logits_steps), 1), self.cfg["vocab_size"]), dtype=np.float32)
+        rc = lib().go_generate_forced(C.byref(self.m), _p(prompt), prompt.size, max_new,
+                                      _p(forced), _p(toks), _p(steps), len(logits_steps),
+                                      _p(logits))
+        assert rc == OK, rc
+        return toks, logits
 
     def generate(self, prompt, max_new, logits_steps=()):
         prompt = np.ascontiguousarray(prompt, dtype=np.uint32)

@@ -631,10 +631,10 @@ static void hash_u32(go_sha256_ctx *c, uint32_t v) {
     go_sha256_update(c, b, 4);
 }
 
-int go_generate(const go_model *m, const uint32_t *prompt, size_t prompt_len,
-                size_t max_new, uint32_t *tokens_out, const int32_t *logits_steps,
-                size_t n_logits_steps, float *logits_out, uint8_t *kv_sha256_out,
-                uint8_t *output_sha256_out) {
+static int generate_impl(const go_model *m, const uint32_t *prompt, size_t prompt_len,
+                         size_t max_new, const uint32_t *forced, uint32_t *tokens_out,
+                         const int32_t *logits_steps, size_t n_logits_steps, float *logits_out,
+                         uint8_t *kv_sha256_out, uint8_t *output_sha256_out) {
     if (prompt_len == 0 || max_new == 0) return GO_SHAPE_MISMATCH;
     const size_t dim = m->dim, L = m->num_layers, hd = m->head_dim;
     const size_t kv_dim = (size_t)m->num_kv_heads * hd, V = m->vocab_size;
@@ -676,12 +676,31 @@ int go_generate(const go_model *m, const uint32_t *prompt, size_t prompt_len,
                 memcpy(logits_out + i * V, logits, V * sizeof(float));
         next = (uint32_t)go_argmax(logits, V);
         tokens_out[step] = next;
+        if (forced && step + 1 < max_new) next = forced[step];
     }
     if (kv_sha256_out) go_logical_kv_sha256(kc, vc, L, max_seq, kv_dim, pos, kv_sha256_out);
     if (output_sha256_out) go_token_sequence_sha256(tokens_out, max_new, output_sha256_out);
 out:
     free(kc); free(vc); free(rc_t); free(rs_t); free(x); free(nx); free(fh); free(logits);
     return rc;
+}
+
+int go_generate(const go_model *m, const uint32_t *prompt, size_t prompt_len,
+                size_t max_new, uint32_t *tokens_out, const int32_t *logits_steps,
+                size_t n_logits_steps, float *logits_out, uint8_t *kv_sha256_out,
+                uint8_t *output_sha256_out) {
+    return generate_impl(m, prompt, prompt_len, max_new, NULL, tokens_out, logits_steps,
+                         n_logits_steps, logits_out, kv_sha256_out, output_sha256_out);
+}
+
+int go_generate_forced(const go_model *m, const uint32_t *prompt, size_t prompt_len,
+                       size_t max_new, const uint32_t *forced, uint32_t *tokens_out,
+                       const int32_t *logits_steps, size_t n_logits_steps, float *logits_out) {
+    if (!forced) return GO_SHAPE_MISMATCH;
+    for (size_t i = 0; i + 1 < max_new; i++)
+        if (forced[i] >= m->vocab_size) return GO_SHAPE_MISMATCH;
+    return generate_impl(m, prompt, prompt_len, max_new, forced, tokens_out, logits_steps,
+                         n_logits_steps, logits_out, NULL, NULL);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -158,6 +158,12 @@ int go_generate(const go_model *m, const uint32_t *prompt, size_t prompt_len,
                 const int32_t *logits_steps, size_t n_logits_steps,
                 float *logits_out, uint8_t *kv_sha256_out,
                 uint8_t *output_sha256_out);
+/* go_generate with the decode inputs given: step s >= 1 is fed forced[s - 1]
+ * (max_new - 1 tokens) instead of the previous argmax; tokens_out still
+ * receives every step's argmax. For comparing two runs at the same context. */
+int go_generate_forced(const go_model *m, const uint32_t *prompt, size_t prompt_len,
+                       size_t max_new, const uint32_t *forced, uint32_t *tokens_out,
+                       const int32_t *logits_steps, size_t n_logits_steps, float *logits_out);
 
 /* One decoder layer at position pos over a contiguous f32 KV cache
  * k_cache/v_cache [max_seq, kv_dim] that already holds pos rows. Writes the

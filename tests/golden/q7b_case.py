@@ -17,6 +17,9 @@ PROMPT_ID = 0x37425052
 PROMPT_LEN = 16
 MAX_NEW = 32
 STEPS = [0, 1, 16, 31]
+# the shallow variant: the same geometry with two layers, 128 greedy tokens
+SHALLOW_LAYERS = 2
+SHALLOW_MAX_NEW = 128
 
 
 def _symmetric_lut():
@@ -35,16 +38,26 @@ def _symmetric(packed):
     return np.take(_LUT, packed)
 
 
-def make_host(gh):
-    host = gh.random_model_host(Q7B, SEED)
+def shallow_cfg():
+    return dict(Q7B, num_layers=SHALLOW_LAYERS)
+
+
+def symmetric_codes(host):
+    """Every INT4 tensor of a host model with nibble 15 replaced by 7."""
+    for L in host["layers"]:
+        for k in [k for k in L if k.startswith("w_")]:
+            L[k] = _symmetric(L[k])
+    host["lm_head"] = _symmetric(host["lm_head"])
+    return host
+
+
+def make_host(gh, cfg=Q7B):
+    host = gh.random_model_host(cfg, SEED)
     for L in host["layers"]:
         L["input_norm"] = (L["input_norm"] + 1.0).astype(np.float32)
         L["post_attn_norm"] = (L["post_attn_norm"] + 1.0).astype(np.float32)
-        for k in [k for k in L if k.startswith("w_")]:
-            L[k] = _symmetric(L[k])
     host["final_norm"] = (host["final_norm"] + 1.0).astype(np.float32)
-    host["lm_head"] = _symmetric(host["lm_head"])
-    return host
+    return symmetric_codes(host)
 
 
 def prompt(gh):

@@ -12,17 +12,35 @@ largest logit at step 0. So:
     tokens and the output digest equal the oracle's; logits within 1e-2
     max-relative (4096 sampled + top-32 indices) at steps 0, 1, 16 and 31.
     Every 7B projection and the head run at their real shapes.
-  * Q8 activations (the default and the headline's mode): the first four
-    greedy tokens equal the oracle's, and the step-0 / step-1 logits differ
-    from the oracle's by less than the oracle's own fp16-vs-f32-KV
-    difference at those steps. The Q8 kernels themselves are pinned at
-    2e-6 at these shapes (tests/test_gpu_c2.py, test_gpu_gemm.py).
+  * Q8 activations (the default and the headline's mode), 28 layers: the
+    first four greedy tokens equal the oracle's, and the step-0 / step-1
+    logits differ from the oracle's by less than the oracle differs from
+    itself when the prompt's embedding rows move by one ulp
+    (q7b_sym_kvf16_ulp.npz: 4.8% and 6.7% of the largest logit; the
+    perturbed oracle run leaves the sequence at step 8, as the GPU does).
+    The Q8 kernels themselves are pinned at 2e-6 at these shapes
+    (tests/test_gpu_c2.py, test_gpu_gemm.py).
   * 32 lanes decoding together (the GEMM path with the plane-emitting
     finishing passes) give every lane the tokens of its own batch-1 run (f32
     mode), and in Q8 mode the same first decode token.
   * config 4: 512- and 2048-token prompts prefilled as one chunk and in small
     chunks give the same first and next token, logits within 1e-2 and K/V
     rows within 1e-2 (f32 mode).
+  * the headline kernels held to the north-star bar at 7B shapes, Q8 mode:
+    - teacher-forced: a traced decode step (glacier_hip_session_trace_layers)
+      returns the residual after every one of the 28 layers; each layer's
+      output, and the K/V row it wrote, is compared with the oracle's
+      forwardLayerCached run on the GPU's own layer input and the GPU's own
+      K/V history (within 1e-2 max-relative), and the logits with the
+      oracle's head on the GPU's final residual. fp16 KV at 16 positions
+      runs the fused attention + O kernel, f32 KV and fp16 KV at 300
+      positions the attention kernel and the O GEMV;
+    - the same weights and geometry with two layers (tests/golden
+      q7b_l2sym*.npz), f32 and fp16 KV: the oracle's 128-token greedy
+      sequence (128 distinct tokens) decoded with the oracle's tokens fed
+      back; logits within 1e-2 at all 128 steps, or within twice the
+      oracle's own one-ulp sensitivity where that is larger, and the same
+      greedy token at every step but near ties.
 """
 import os
 import sys
@@ -34,17 +52,35 @@ pytestmark = pytest.mark.gpu
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(HERE, "golden"))
+sys.path.insert(0, HERE)
 import q7b_case  # noqa: E402
+from forced_decode import check_against_sensitivity, forced_decode, logit_err  # noqa: E402
 
 CFG = q7b_case.Q7B
 V = CFG["vocab_size"]
 
 
 @pytest.fixture(scope="module")
-def q7b(gh, gctx):
+def q7b_host(gh):
+    print("generating the 7B test weights", flush=True)
+    return q7b_case.make_host(gh)
+
+
+@pytest.fixture(scope="module")
+def q7b(gh, gctx, q7b_host):
     print("building the 7B test model", flush=True)
-    host = q7b_case.make_host(gh)
     m = gh.Model(gctx, CFG)
+    m.set_from_host(q7b_host)
+    yield m
+    m.close()
+
+
+@pytest.fixture(scope="module")
+def q7b_shallow(gh, gctx):
+    cfg = q7b_case.shallow_cfg()
+    print("building the two-layer 7B-geometry model", flush=True)
+    host = q7b_case.make_host(gh, cfg)
+    m = gh.Model(gctx, cfg)
     m.set_from_host(host)
     del host
     yield m
@@ -61,24 +97,21 @@ def _session(gh, q7b, lanes, max_pos, kv, f32, chunk=0):
                       layer_activation=act, head_activation=act, prefill_chunk=chunk)
 
 
-def _logit_err(got, fx, i):
-    return max(np.max(np.abs(got[fx["sample_idx"]] - fx["sample_logits"][i])),
-               np.max(np.abs(got[fx["top_idx"][i]] - fx["top_val"][i]))) / fx["max_abs"][i]
-
-
-def _run_fixture(gh, q7b, fx, kv, f32):
-    sess = _session(gh, q7b, 1, 64, kv, f32)
+def _run_fixture(gh, q7b, fx, kv, f32, max_pos=64):
+    sess = _session(gh, q7b, 1, max_pos, kv, f32)
     try:
         sess.begin(0)
         steps = fx["steps"].tolist()
         first, lg = sess.prefill(0, fx["prompt"], want_logits=True)
         toks, logits = [first], {0: lg}
         for s in range(1, len(fx["tokens"])):
-            nxt, lg = sess.step([0], [toks[-1]], want_logits=True)
-            toks.append(int(nxt[0]))
             if s in steps:
+                nxt, lg = sess.step([0], [toks[-1]], want_logits=True)
                 logits[s] = lg[0]
-        return toks, [_logit_err(logits[s], fx, i) for i, s in enumerate(steps)], \
+            else:  # the decode step as the bench runs it: no logits leave the device
+                nxt = sess.step([0], [toks[-1]])
+            toks.append(int(nxt[0]))
+        return toks, [logit_err(logits[s], fx, i) for i, s in enumerate(steps)], \
             bytes(sess.state(0).output_sha256)
     finally:
         sess.close()
@@ -101,8 +134,8 @@ def test_7b_f32_batch1_greedy_matches_oracle(gh, q7b, variant):
 @pytest.mark.parametrize("variant", ["sym_kvf16", "sym"])
 def test_7b_q8_batch1_within_model_sensitivity(gh, q7b, variant):
     fx = _fx(variant)
-    a, b = _fx("sym"), _fx("sym_kvf16")
-    # the oracle against itself under fp16 rounding of the stored K/V rows
+    a, b = _fx("sym_kvf16"), _fx("sym_kvf16_ulp")
+    # the oracle against itself with the prompt's embedding rows moved one ulp
     sens = [float(np.max(np.abs(a["sample_logits"][i] - b["sample_logits"][i])) / a["max_abs"][i])
             for i in range(2)]
     kv = gh.F16 if variant.endswith("kvf16") else gh.F32
@@ -110,7 +143,7 @@ def test_7b_q8_batch1_within_model_sensitivity(gh, q7b, variant):
     want = fx["tokens"].tolist()
     n_same = next((i for i, (x, y) in enumerate(zip(toks, want)) if x != y), len(want))
     print(f"{variant}: first divergence at {n_same}; logit max-rel {['%.2e' % e for e in errs]}; "
-          f"oracle fp16-KV sensitivity {['%.2e' % e for e in sens]}", flush=True)
+          f"oracle one-ulp input sensitivity {['%.2e' % e for e in sens]}", flush=True)
     assert toks[:4] == want[:4]
     assert errs[0] < sens[0] and errs[1] < sens[1]
 
@@ -193,3 +226,91 @@ def test_7b_prefill_one_chunk_equals_small_chunks(gh, q7b, T, small):
     assert (f1, n1) == (f2, n2)
     assert err < 1e-2
     assert kv_err < 1e-2
+
+
+@pytest.mark.parametrize("variant", ["l2sym_kvf16", "l2sym"])
+def test_7b_geometry_q8_128_steps_match_oracle(gh, q7b_shallow, variant):
+    """The headline's Q8 kernels at 7B shapes (input-mode QKV 3584->4608,
+    fused attention + O at 28/4/128 for fp16 KV, input-mode SwiGLU gate/up
+    37888, the 3-digit down at K = 18944, the fused head + argmax over
+    152064) on two layers, decoding the oracle's own 128-token greedy
+    sequence (each step is fed the oracle's previous token, so both sides
+    see the same context at every step). Q8 quantisation makes this random
+    model respond to last-bit changes of its input: the oracle fed the same
+    tokens with the prompt's embedding rows one ulp off moves its logits by
+    up to ~1.3e-2 of the largest and its argmax at a few near ties. So every
+    step's logits must be within 1e-2 max-relative of the oracle's, or within
+    twice that one-ulp sensitivity where it is larger (worst step and mean),
+    and every greedy token must equal the oracle's except at near ties (top-2
+    gap below twice the step's deviation). The sequence is discriminative
+    (128 distinct tokens)."""
+    fx = _fx(variant)
+    kv = gh.F16 if variant.endswith("kvf16") else gh.F32
+    want = fx["tokens"].tolist()
+    assert len(want) == 128 and len(set(want)) >= 32
+    sess = _session(gh, q7b_shallow, 1, 160, kv, False)
+    try:
+        errs, ties = forced_decode(sess, fx)
+    finally:
+        sess.close()
+    check_against_sensitivity(errs, ties, fx, f"{variant}, 128 forced steps")
+
+
+@pytest.mark.parametrize("kv,prompt_len", [("f16", 16), ("f32", 16), ("f16", 300)])
+def test_7b_q8_every_layer_matches_oracle_on_device_inputs(gh, ora, q7b, q7b_host, kv,
+                                                            prompt_len):
+    """Teacher-forced parity of the headline decode step (Q8 layers, f32
+    head) at the 7B shapes: each of the 28 layers' outputs on the GPU
+    equals forwardLayerCached (generate.zig:1511-1967, the oracle's
+    go_forward_layer) applied to the GPU's own input of that layer and the
+    GPU's own K/V history, within 1e-2 max-relative; so does the K/V row the
+    layer wrote, and the logits against the oracle's head on the GPU's final
+    residual, whose greedy token the GPU returns wherever the oracle's top-2
+    gap exceeds the logit deviation."""
+    f16 = kv == "f16"
+    kvd = CFG["num_kv_heads"] * CFG["head_dim"]
+    D = CFG["dim"]
+    om = ora.OracleModel(CFG, q7b_host, kv_fp16=f16, act_f32=False)
+    emb = q7b_host["embedding"].reshape(V, D)
+    sess = _session(gh, q7b, 1, prompt_len + 8, gh.F16 if f16 else gh.F32, False)
+    try:
+        sess.begin(0)
+        prompt = gh.synth_tokens(q7b_case.SEED, 0x54460000 + prompt_len, V, prompt_len)
+        tok = sess.prefill(0, prompt)
+        sess.trace_layers(True)
+        worst = dict(x=0.0, k=0.0, v=0.0, logits=0.0)
+        for step in range(2):
+            pos = prompt_len + step
+            print(f"kv={kv} ctx={pos + 1}: traced step", flush=True)
+            nxt, lg = sess.step([0], [tok], want_logits=True)
+            xs = sess.layer_trace()
+            assert xs.shape == (CFG["num_layers"], 1, D)
+            x_in = emb[tok]
+            for li in range(CFG["num_layers"]):
+                kh = np.stack([sess.kv_row(0, li, 0, p, kvd) for p in range(pos)])
+                vh = np.stack([sess.kv_row(0, li, 1, p, kvd) for p in range(pos)])
+                out, kr, vr = om.forward_layer_at(li, x_in, kh, vh)
+                errs = dict(
+                    x=float(np.max(np.abs(xs[li, 0] - out)) / np.max(np.abs(out))),
+                    k=float(np.max(np.abs(sess.kv_row(0, li, 0, pos, kvd) - kr)) /
+                            np.max(np.abs(kr))),
+                    v=float(np.max(np.abs(sess.kv_row(0, li, 1, pos, kvd) - vr)) /
+                            np.max(np.abs(vr))))
+                for k_, e in errs.items():
+                    worst[k_] = max(worst[k_], e)
+                assert max(errs.values()) < 1e-2, (step, li, errs)
+                x_in = xs[li, 0]
+            fin = ora.rmsnorm(xs[-1, 0], q7b_host["final_norm"], CFG["rms_eps"])
+            want_lg = ora.linear_int4_f32(fin, q7b_host["lm_head"], q7b_host["lm_head_scales"],
+                                          V, D, CFG["group_size"])[0]
+            dev = float(np.max(np.abs(lg[0] - want_lg)))
+            worst["logits"] = max(worst["logits"], dev / float(np.max(np.abs(want_lg))))
+            srt = np.sort(want_lg)
+            assert dev / np.max(np.abs(want_lg)) < 1e-2
+            if srt[-1] - srt[-2] > 2 * dev:
+                assert int(nxt[0]) == int(np.argmax(want_lg))
+            tok = int(nxt[0])
+        print(f"kv={kv} prompt={prompt_len}: worst max-rel over 28 layers x 2 steps: "
+              + ", ".join(f"{k_} {e:.2e}" for k_, e in worst.items()), flush=True)
+    finally:
+        sess.close()

@@ -5,8 +5,17 @@ oracle's committed run (tests/golden/make_c1_golden.py).
 Bars: the identical greedy token sequence and output digest; logits within
 1e-2 max-relative error (max |gpu - oracle| over the stored 4096 sampled +
 top-32 indices, divided by the oracle's max |logit|) at steps 0, 1, 64, 127.
+
+The discriminative Q8 fixture (c1_qwen05b_sym.npz: unit-centred norms,
+symmetric codes, 128 distinct greedy tokens, f32 KV) is decoded with the
+oracle's own tokens fed back (tests/forced_decode.py): logits within 1e-2 at
+all 128 steps, or within twice the oracle's own one-ulp sensitivity where
+that is larger (24 Q8 layers amplify a last-bit input change to several
+percent of the largest logit), and the same greedy token at every step
+except near ties (the oracle's top-2 gap below twice the step's deviation).
 """
 import os
+import sys
 
 import numpy as np
 import pytest
@@ -14,6 +23,8 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [HERE, os.path.join(HERE, "golden")]
+from forced_decode import check_against_sensitivity, forced_decode  # noqa: E402
 C1 = dict(num_layers=24, dim=896, hidden_dim=4864, num_heads=14, num_kv_heads=2, head_dim=64,
           vocab_size=151936, group_size=32, rms_eps=1e-6, rope_theta=1e6)
 
@@ -65,3 +76,27 @@ def test_c1_greedy_128_matches_oracle(gh, gctx, variant):
     finally:
         sess.close()
         m.close()
+
+
+def test_c1_discriminative_q8_128_steps_match_oracle(gh, gctx):
+    import q7b_case
+
+    fx = np.load(os.path.join(HERE, "golden", "c1_qwen05b_sym.npz"))
+    want = fx["tokens"].tolist()
+    assert len(want) == 128 and len(set(want)) >= 32
+    host = gh.random_model_host(C1, int(fx["seed"][0]))
+    for L in host["layers"]:
+        L["input_norm"] = (L["input_norm"] + 1.0).astype(np.float32)
+        L["post_attn_norm"] = (L["post_attn_norm"] + 1.0).astype(np.float32)
+    host["final_norm"] = (host["final_norm"] + 1.0).astype(np.float32)
+    host = q7b_case.symmetric_codes(host)
+    m = gh.Model(gctx, C1)
+    m.set_from_host(host)
+    del host
+    sess = gh.Session(m, max_lanes=1, max_positions=256, kv_dtype=gh.F32)
+    try:
+        errs, ties = forced_decode(sess, fx)
+    finally:
+        sess.close()
+        m.close()
+    check_against_sensitivity(errs, ties, fx, f"c1 sym ({len(set(want))} distinct tokens)")
