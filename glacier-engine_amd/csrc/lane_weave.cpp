@@ -10,6 +10,7 @@
 #include <limits.h>
 #include <string.h>
 
+#include <atomic>
 #include <functional>
 #include <mutex>
 #include <vector>
@@ -24,6 +25,7 @@ constexpr uint64_t kU64Max = ~0ull;
 constexpr uint64_t kBankAbi = 0x4752424B00000001ull;        // resource_bank.zig:12
 constexpr uint64_t kAbi = 0x474C575100000001ull;            // lane_weave_qos.zig:17
 constexpr uint64_t kEventAbi = 0x474C574500000001ull;       // :18
+constexpr uint64_t kPermitAbi = 0x474C575000000001ull;      // :19 service_permit_abi
 constexpr uint64_t kReservationDomain = 0x7265736572766531ull;  // resource_bank.zig:4159
 constexpr uint64_t kReceiptDomain = 0x7265636569707431ull;      // :4160
 
@@ -152,6 +154,39 @@ void receipt_sha256(const Receipt &r, uint8_t out[32]) {
   h_receipt(h, r);
   h.final(out);
 }
+
+using Permit = glacier_hip_service_permit_v1_t;
+
+// servicePermitSha256 (:3557-3581)
+void permit_sha256(const Permit &p, uint8_t out[32]) {
+  static const char dom[] = "glacier-lane-weave-qos-service-permit-v1";
+  gh::Sha256 h;
+  h.update(dom, sizeof dom);
+  h.u64(p.abi_version);
+  h.u64(p.scheduler_epoch);
+  h.u64(p.coordinator_id);
+  h.u64(p.coordinator_address);
+  h.u64(p.permit_generation);
+  h.u64(p.event_sequence);
+  h_handle(h, p.handle);
+  h.u64(p.logical_tick_before);
+  h.u32(p.cursor_before);
+  h_u16(h, (uint16_t)p.level_before);
+  h.u32(p.cursor_after);
+  h_u16(h, (uint16_t)p.level_after);
+  h.u64(p.remaining_before);
+  h.u64(p.wait_quanta);
+  h.u64(p.maximum_service_gap);
+  h.update(p.state_before_sha256, 32);
+  h.update(p.chain_head_before_sha256, 32);
+  h_receipt(h, p.resource_receipt);
+  h.update(p.resource_receipt_sha256, 32);
+  h.final(out);
+}
+
+// Scheduler lifetimes (nextServiceCoordinatorId :556-566): a permit of an
+// earlier scheduler at the same address is refused.
+std::atomic<uint64_t> g_next_coordinator{1};
 
 void event_sha256(const Event &e, uint8_t out[32]) {
   // eventSha256 (:4004-4038)
@@ -291,6 +326,10 @@ struct glacier_hip_lane_weave {
   uint64_t max_gap = 0;
   uint8_t chain_head[32] = {};
   bool poisoned = false, closed = false;
+  // prepared service (pending_service :676): one permit at most
+  uint64_t coordinator_id = 0, next_permit_generation = 1;
+  bool pending = false;
+  Permit pending_permit{};
 
   void counts(uint32_t *active, uint32_t *finished) const {
     *active = *finished = 0;
@@ -470,6 +509,7 @@ int finish_handle(glacier_hip_lane_weave *lw, const Handle *h, uint32_t kind, ui
   std::lock_guard<std::mutex> lk(lw->mu);
   if (lw->poisoned) return GLACIER_HIP_SCHEDULER_POISONED;
   if (lw->closed) return GLACIER_HIP_SCHEDULER_CLOSED;
+  if (lw->pending) return GLACIER_HIP_SERVICE_IN_FLIGHT;
   if (h->scheduler_epoch != lw->epoch || h->slot_index >= lw->slots.size())
     return GLACIER_HIP_STALE_HANDLE;
   const size_t i = (size_t)h->slot_index;
@@ -548,6 +588,7 @@ glacier_hip_lane_weave *glacier_hip_lane_weave_create(
   h_limits(h, *bank_limits);
   h.u64(lw->max_gap);
   h.final(lw->chain_head);
+  lw->coordinator_id = g_next_coordinator.fetch_add(1);
   return lw;
 }
 
@@ -561,6 +602,7 @@ int glacier_hip_lane_weave_admit(glacier_hip_lane_weave *lw, const glacier_hip_r
   std::lock_guard<std::mutex> lk(lw->mu);
   if (lw->poisoned) return GLACIER_HIP_SCHEDULER_POISONED;
   if (lw->closed) return GLACIER_HIP_SCHEDULER_CLOSED;
+  if (lw->pending) return GLACIER_HIP_SERVICE_IN_FLIGHT;
   const Spec &sp = *spec;
   uint64_t hb;
   // validateRequestSpec (:3145-3158)
@@ -655,32 +697,43 @@ int glacier_hip_lane_weave_admit(glacier_hip_lane_weave *lw, const glacier_hip_r
 namespace {
 
 // serveOne (:1196-1270) with lw->mu held.
-int serve_one_locked(glacier_hip_lane_weave *lw, glacier_hip_lane_event_t *out) {
-  if (lw->poisoned) return GLACIER_HIP_SCHEDULER_POISONED;
-  if (lw->closed) return GLACIER_HIP_SCHEDULER_CLOSED;
+// The selection serveOne / prepareService make (lw->mu held): the next IWRR
+// slot, its wait, and the checks that poison the scheduler (a deadline the
+// selection breaks :3340-3355, a service gap over the bound).
+int select_service_locked(glacier_hip_lane_weave *lw, Selection *sel, uint64_t *wait) {
   if (lw->tick == kU64Max) return GLACIER_HIP_SCHEDULER_POISONED;
   std::vector<uint8_t> active(lw->slots.size());
   for (size_t i = 0; i < active.size(); ++i) active[i] = lw->slots[i].state == kActive;
-  Selection sel;
-  if (!lw->next_selection(lw->cursor, lw->level, active, &sel)) return GLACIER_HIP_NO_RUNNABLE;
-  Slot &s = lw->slots[sel.index];
+  if (!lw->next_selection(lw->cursor, lw->level, active, sel)) return GLACIER_HIP_NO_RUNNABLE;
+  const Slot &s = lw->slots[sel->index];
   const uint64_t after_tick = lw->tick + 1;
-  // selectionPreservesDeadlines (:3340-3355)
   for (size_t j = 0; j < lw->slots.size(); ++j) {
     const Slot &o = lw->slots[j];
     if (o.state != kActive || o.spec.deadline_tick == 0) continue;
-    const bool completes = j == sel.index && o.remaining == 1;
+    const bool completes = j == sel->index && o.remaining == 1;
     if ((completes && after_tick > o.spec.deadline_tick) ||
         (!completes && after_tick >= o.spec.deadline_tick)) {
       lw->poisoned = true;
       return GLACIER_HIP_SCHEDULER_POISONED;
     }
   }
-  const uint64_t wait = after_tick - s.last_service_tick;
-  if (wait > lw->max_gap) {
+  *wait = after_tick - s.last_service_tick;
+  if (*wait > lw->max_gap) {
     lw->poisoned = true;
     return GLACIER_HIP_SCHEDULER_POISONED;
   }
+  return GLACIER_HIP_OK;
+}
+
+// serveOne (:1196-1270) with lw->mu held.
+int serve_one_locked(glacier_hip_lane_weave *lw, glacier_hip_lane_event_t *out) {
+  if (lw->poisoned) return GLACIER_HIP_SCHEDULER_POISONED;
+  if (lw->closed) return GLACIER_HIP_SCHEDULER_CLOSED;
+  Selection sel;
+  uint64_t wait = 0;
+  if (int rc = select_service_locked(lw, &sel, &wait)) return rc;
+  Slot &s = lw->slots[sel.index];
+  const uint64_t after_tick = lw->tick + 1;
   const auto b = lw->before();
   Event e{};
   e.handle = lw->handle_for(sel.index);
@@ -702,6 +755,113 @@ int serve_one_locked(glacier_hip_lane_weave *lw, glacier_hip_lane_event_t *out) 
   return GLACIER_HIP_OK;
 }
 
+// prepareService (:1127-1192) with lw->mu held: the next selection frozen
+// into a permit; nothing logical changes.
+int prepare_service_locked(glacier_hip_lane_weave *lw, Permit *out) {
+  if (lw->poisoned) return GLACIER_HIP_SCHEDULER_POISONED;
+  if (lw->closed) return GLACIER_HIP_SCHEDULER_CLOSED;
+  if (lw->pending) return GLACIER_HIP_SERVICE_IN_FLIGHT;
+  if (lw->next_permit_generation == 0 || lw->next_permit_generation == kU64Max)
+    return GLACIER_HIP_INVALID_TRANSACTION;  // GenerationOverflow
+  Selection sel;
+  uint64_t wait = 0;
+  if (int rc = select_service_locked(lw, &sel, &wait)) return rc;
+  const Slot &s = lw->slots[sel.index];
+  if (s.service_count == kU64Max) return GLACIER_HIP_INVALID_TRANSACTION;  // ServiceOverflow
+  Permit p;
+  memset(&p, 0, sizeof p);
+  p.abi_version = kPermitAbi;
+  p.scheduler_epoch = lw->epoch;
+  p.coordinator_id = lw->coordinator_id;
+  p.coordinator_address = (uint64_t)(uintptr_t)lw;
+  p.permit_generation = lw->next_permit_generation;
+  p.event_sequence = lw->next_seq;
+  p.handle = lw->handle_for(sel.index);
+  p.logical_tick_before = lw->tick;
+  p.cursor_before = lw->cursor;
+  p.level_before = lw->level;
+  p.cursor_after = sel.cursor_after;
+  p.level_after = sel.level_after;
+  p.remaining_before = s.remaining;
+  p.wait_quanta = wait;
+  p.maximum_service_gap = lw->max_gap;
+  lw->state_sha(p.state_before_sha256);
+  memcpy(p.chain_head_before_sha256, lw->chain_head, 32);
+  p.resource_receipt = s.receipt;
+  memcpy(p.resource_receipt_sha256, s.receipt_sha256, 32);
+  permit_sha256(p, p.permit_sha256);
+  lw->next_permit_generation += 1;
+  lw->pending = true;
+  lw->pending_permit = p;
+  *out = p;
+  return GLACIER_HIP_OK;
+}
+
+// validatePendingService (:2461-2487): exactly the pending permit, its digest
+// recomputing; a pending permit whose own digest no longer does poisons.
+int validate_pending_locked(glacier_hip_lane_weave *lw, const Permit &p) {
+  if (!lw->pending) return GLACIER_HIP_STALE_SERVICE_PERMIT;
+  uint8_t d[32];
+  permit_sha256(lw->pending_permit, d);
+  if (memcmp(d, lw->pending_permit.permit_sha256, 32) != 0) {
+    lw->poisoned = true;
+    return GLACIER_HIP_SCHEDULER_POISONED;
+  }
+  permit_sha256(p, d);
+  if (p.abi_version != kPermitAbi || p.scheduler_epoch != lw->epoch ||
+      p.coordinator_id != lw->coordinator_id ||
+      p.coordinator_address != (uint64_t)(uintptr_t)lw || p.permit_generation == 0 ||
+      memcmp(d, p.permit_sha256, 32) != 0 || memcmp(&p, &lw->pending_permit, sizeof p) != 0)
+    return GLACIER_HIP_STALE_SERVICE_PERMIT;
+  return GLACIER_HIP_OK;
+}
+
+// validateServiceBeforeState (:2512-2531): nothing logical moved since prepare.
+int validate_before_state_locked(glacier_hip_lane_weave *lw, const Permit &p) {
+  uint8_t st[32];
+  lw->state_sha(st);
+  if (memcmp(st, p.state_before_sha256, 32) != 0 || p.event_sequence != lw->next_seq ||
+      p.logical_tick_before != lw->tick || memcmp(p.chain_head_before_sha256, lw->chain_head, 32) != 0) {
+    lw->poisoned = true;
+    return GLACIER_HIP_SCHEDULER_POISONED;
+  }
+  return GLACIER_HIP_OK;
+}
+
+// commitService (:1272-1286 with validateServiceCommitLocked :2542-2600 and
+// commitServiceLocked :2617-2663): the serveOne transition of the permit's
+// selection, emitting the same Event-v1.
+int commit_service_locked(glacier_hip_lane_weave *lw, const Permit &p, Event *out) {
+  if (lw->poisoned) return GLACIER_HIP_SCHEDULER_POISONED;
+  if (lw->closed) return GLACIER_HIP_SCHEDULER_CLOSED;
+  if (int rc = validate_pending_locked(lw, p)) return rc;
+  if (int rc = validate_before_state_locked(lw, p)) return rc;
+  Selection sel;
+  uint64_t wait = 0;
+  int rc = select_service_locked(lw, &sel, &wait);
+  const Slot &s = lw->slots[p.handle.slot_index < lw->slots.size() ? p.handle.slot_index : 0];
+  if (rc || sel.index != p.handle.slot_index || sel.cursor_after != p.cursor_after ||
+      sel.level_after != p.level_after || wait != p.wait_quanta || s.state != kActive ||
+      s.generation != p.handle.slot_generation || s.remaining != p.remaining_before ||
+      memcmp(&s.receipt, &p.resource_receipt, sizeof s.receipt) != 0 ||
+      memcmp(s.receipt_sha256, p.resource_receipt_sha256, 32) != 0) {
+    lw->poisoned = true;
+    return GLACIER_HIP_SCHEDULER_POISONED;
+  }
+  lw->pending = false;
+  return serve_one_locked(lw, out);
+}
+
+// abortService (:1438-1452): the pending permit consumed, nothing logical changes.
+int abort_service_locked(glacier_hip_lane_weave *lw, const Permit &p) {
+  if (lw->poisoned) return GLACIER_HIP_SCHEDULER_POISONED;
+  if (lw->closed) return GLACIER_HIP_SCHEDULER_CLOSED;
+  if (int rc = validate_pending_locked(lw, p)) return rc;
+  if (int rc = validate_before_state_locked(lw, p)) return rc;
+  lw->pending = false;
+  return GLACIER_HIP_OK;
+}
+
 // The slots the next serve_one calls select (lw->mu held): replays the
 // serve_one transitions on copies of the mutable selection state (cursor,
 // level, tick, remaining quanta, last service) and stops before a slot would
@@ -713,6 +873,7 @@ int plan_wave_locked(glacier_hip_lane_weave *lw, uint32_t max_count, uint32_t *s
   *count_out = 0;
   if (lw->poisoned) return GLACIER_HIP_SCHEDULER_POISONED;
   if (lw->closed) return GLACIER_HIP_SCHEDULER_CLOSED;
+  if (lw->pending) return GLACIER_HIP_SERVICE_IN_FLIGHT;
   const size_t n = lw->slots.size();
   std::vector<uint8_t> active(n), taken(n, 0);
   std::vector<uint64_t> remaining(n), last(n);
@@ -752,8 +913,7 @@ int plan_wave_locked(glacier_hip_lane_weave *lw, uint32_t max_count, uint32_t *s
 
 namespace gh {
 
-int lane_weave_run_wave(glacier_hip_lane_weave *lw, uint32_t max_count,
-                        const std::function<int(const uint32_t *, uint32_t)> &device_step,
+int lane_weave_run_wave(glacier_hip_lane_weave *lw, uint32_t max_count, const WaveOps &ops,
                         uint32_t *slots_out, glacier_hip_lane_event_t *events_out,
                         uint32_t *count_out) {
   std::lock_guard<std::mutex> lk(lw->mu);
@@ -763,13 +923,35 @@ int lane_weave_run_wave(glacier_hip_lane_weave *lw, uint32_t max_count,
   int rc = plan_wave_locked(lw, max_count, plan.data(), &n);
   if (rc) return rc;
   if (n == 0) return GLACIER_HIP_NO_RUNNABLE;
-  rc = device_step(plan.data(), n);
-  if (rc) return rc;  // nothing committed, the scheduler unchanged
+  rc = ops.run(plan.data(), n);
+  if (rc) return rc;  // nothing published, the scheduler unchanged
+  if (ops.sink && (rc = ops.sink())) {
+    ops.abort(0);
+    return rc;
+  }
   for (uint32_t i = 0; i < n; ++i) {
+    Permit p;
+    rc = prepare_service_locked(lw, &p);
+    if (rc || p.handle.slot_index != plan[i]) {
+      if (!rc) (void)abort_service_locked(lw, p);
+      ops.abort(i);
+      lw->poisoned = true;
+      return GLACIER_HIP_SCHEDULER_POISONED;
+    }
+    rc = ops.publish(i);
+    if (rc) {
+      (void)abort_service_locked(lw, p);
+      ops.abort(i);
+      if (i > 0) {  // earlier quanta are published: the wave cannot be undone
+        lw->poisoned = true;
+        return GLACIER_HIP_SCHEDULER_POISONED;
+      }
+      return rc;
+    }
     glacier_hip_lane_event_t ev;
-    rc = serve_one_locked(lw, &ev);
-    if (rc || ev.handle.slot_index != plan[i]) {
-      // the device step has committed: the scheduler no longer matches it
+    rc = commit_service_locked(lw, p, &ev);
+    if (rc) {  // published but not served
+      ops.abort(i + 1);
       lw->poisoned = true;
       return GLACIER_HIP_SCHEDULER_POISONED;
     }
@@ -787,7 +969,36 @@ extern "C" {
 int glacier_hip_lane_weave_serve_one(glacier_hip_lane_weave *lw, glacier_hip_lane_event_t *out) {
   if (!lw || !out) return GLACIER_HIP_INVALID_ARGUMENT;
   std::lock_guard<std::mutex> lk(lw->mu);
+  if (!lw->poisoned && !lw->closed && lw->pending) return GLACIER_HIP_SERVICE_IN_FLIGHT;
   return serve_one_locked(lw, out);
+}
+
+int glacier_hip_lane_weave_prepare_service(glacier_hip_lane_weave *lw,
+                                           glacier_hip_service_permit_v1_t *out) {
+  if (!lw || !out) return GLACIER_HIP_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> lk(lw->mu);
+  return prepare_service_locked(lw, out);
+}
+
+int glacier_hip_lane_weave_commit_service(glacier_hip_lane_weave *lw,
+                                          const glacier_hip_service_permit_v1_t *p,
+                                          glacier_hip_lane_event_t *out) {
+  if (!lw || !p || !out) return GLACIER_HIP_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> lk(lw->mu);
+  return commit_service_locked(lw, *p, out);
+}
+
+int glacier_hip_lane_weave_abort_service(glacier_hip_lane_weave *lw,
+                                         const glacier_hip_service_permit_v1_t *p) {
+  if (!lw || !p) return GLACIER_HIP_INVALID_ARGUMENT;
+  std::lock_guard<std::mutex> lk(lw->mu);
+  return abort_service_locked(lw, *p);
+}
+
+int glacier_hip_service_permit_sha256(const glacier_hip_service_permit_v1_t *p, uint8_t out[32]) {
+  if (!p || !out) return GLACIER_HIP_INVALID_ARGUMENT;
+  permit_sha256(*p, out);
+  return GLACIER_HIP_OK;
 }
 
 int glacier_hip_lane_weave_plan_wave(glacier_hip_lane_weave *lw, uint32_t max_count,
@@ -813,6 +1024,7 @@ int glacier_hip_lane_weave_close(glacier_hip_lane_weave *lw, glacier_hip_lane_ev
   std::lock_guard<std::mutex> lk(lw->mu);
   if (lw->poisoned) return GLACIER_HIP_SCHEDULER_POISONED;
   if (lw->closed) return GLACIER_HIP_SCHEDULER_CLOSED;
+  if (lw->pending) return GLACIER_HIP_SERVICE_IN_FLIGHT;
   uint32_t a, f;
   lw->counts(&a, &f);
   if (a || f || !claim_zero(lw->used)) return GLACIER_HIP_INCOMPLETE_DRAIN;

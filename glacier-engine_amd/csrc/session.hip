@@ -2419,46 +2419,152 @@ int glacier_hip_session_step_commit(glacier_hip_session *s, const glacier_hip_pr
 
 }  // extern "C"
 
-extern "C" int glacier_hip_session_lane_weave_wave(
-    glacier_hip_session *s, glacier_hip_lane_weave *lw, const uint32_t *lane_of_slot,
-    uint32_t slot_count, uint32_t *tokens_by_lane, const uint64_t *eligible_by_lane,
-    uint32_t max_count, uint32_t *slots_out, glacier_hip_lane_event_t *events_out,
-    uint32_t *count_out) {
+namespace {
+
+// One LaneWeave wave (lane_weave_run_wave): the device step of the planned
+// lanes runs privately, an optional sink acknowledges the wave's stages, then
+// each quantum's row, sampler counter and output word publish under its
+// service permit.
+int lane_weave_wave_impl(glacier_hip_session *s, glacier_hip_lane_weave *lw,
+                         const uint32_t *lane_of_slot, uint32_t slot_count,
+                         uint32_t *tokens_by_lane, const uint64_t *eligible_by_lane,
+                         uint32_t max_count, glacier_hip_wave_sink_fn sink, void *sink_ctx,
+                         uint32_t *slots_out, glacier_hip_lane_event_t *events_out,
+                         uint32_t *count_out) {
   if (!s || !lw || !lane_of_slot || !tokens_by_lane || !count_out)
     return GLACIER_HIP_INVALID_ARGUMENT;
   *count_out = 0;
   const uint32_t L = (uint32_t)s->lanes.size();
   if (max_count == 0 || max_count > L) return GLACIER_HIP_SHAPE_MISMATCH;
-  const uint64_t W = (s->model->cfg.vocab_size + 63) / 64;
-  std::vector<uint32_t> lanes, next;
-  auto step = [&](const uint32_t *plan, uint32_t n) -> int {
+  const auto &c = s->model->cfg;
+  const uint64_t W = (c.vocab_size + 63) / 64;
+  GH_SUBMISSION(s->model->ctx);
+  if (s->prep.active) return GLACIER_HIP_TRANSACTION_ACTIVE;
+  std::vector<uint32_t> lanes, toks, next, slots;
+  std::vector<RowTxn> txns;
+  std::vector<uint8_t> published;
+  const bool elig = eligible_by_lane != nullptr;
+  gh::WaveOps ops;
+  ops.run = [&](const uint32_t *plan, uint32_t n) -> int {
     lanes.resize(n);
-    next.resize(n);
-    std::vector<uint32_t> toks(n);
+    toks.resize(n);
+    next.assign(n, 0);
+    slots.assign(plan, plan + n);
     for (uint32_t i = 0; i < n; ++i) {
       if (plan[i] >= slot_count || lane_of_slot[plan[i]] >= L) return GLACIER_HIP_SHAPE_MISMATCH;
       lanes[i] = lane_of_slot[plan[i]];
       toks[i] = tokens_by_lane[lanes[i]];
+      const Lane &ln = s->lanes[lanes[i]];
+      if (!ln.kv.active) return GLACIER_HIP_INVALID_ARGUMENT;
+      for (uint32_t j = 0; j < i; ++j)
+        if (lanes[j] == lanes[i]) return GLACIER_HIP_INVALID_ARGUMENT;
+      if (toks[i] >= c.vocab_size) return GLACIER_HIP_SHAPE_MISMATCH;
+      if (ln.kv.len + 1 > s->opt.max_positions) return GLACIER_HIP_CACHE_FULL;
+      if (ln.first_pending || ln.retired) return GLACIER_HIP_INVALID_TRANSACTION;
     }
-    std::vector<uint64_t> elig;
-    if (eligible_by_lane) {
-      elig.resize((size_t)n * W);
+    std::vector<uint64_t> words;
+    if (elig) {
+      words.resize((size_t)n * W);
       for (uint32_t i = 0; i < n; ++i)
-        memcpy(&elig[(size_t)i * W], eligible_by_lane + (size_t)lanes[i] * W, W * 8);
+        memcpy(&words[(size_t)i * W], eligible_by_lane + (size_t)lanes[i] * W, W * 8);
     }
-    // the device step commits its KV rows, tokens and sampler counters only
-    // on success; the scheduler then commits the same quanta in plan order
-    return glacier_hip_session_decode_step(s, lanes.data(), toks.data(), n,
-                                           eligible_by_lane ? elig.data() : nullptr, next.data(),
-                                           nullptr);
+    const int rc = run_step(s, lanes.data(), toks.data(), n, true, elig ? words.data() : nullptr,
+                            nullptr, txns);
+    if (rc) return rc;  // run_step aborted its rows
+    for (uint32_t i = 0; i < n; ++i) next[i] = (uint32_t)s->res_host[i].index;
+    published.assign(n, 0);
+    return GLACIER_HIP_OK;
   };
-  const int rc = gh::lane_weave_run_wave(lw, max_count, step, slots_out, events_out, count_out);
-  // tokens of the quanta the device step committed (all of them, unless the
-  // scheduler was poisoned after the commit)
-  for (uint32_t i = 0; i < (uint32_t)next.size() && (rc == GLACIER_HIP_OK ||
-                                                    rc == GLACIER_HIP_SCHEDULER_POISONED); ++i)
+  if (sink) {
+    ops.sink = [&]() -> int {
+      std::vector<std::array<uint8_t, 32>> digests;
+      if (int rc = row_payload_sha256(s, txns, digests)) return rc;
+      std::vector<glacier_hip_wave_stage_v1_t> stages(lanes.size());
+      for (size_t i = 0; i < lanes.size(); ++i) {
+        glacier_hip_wave_stage_v1_t &w = stages[i];
+        memset(&w, 0, sizeof w);
+        w.slot = slots[i];
+        w.lane = lanes[i];
+        const Lane &ln = s->lanes[lanes[i]];
+        glacier_hip_lane_proposal_v1_t &lp = w.stage;
+        gpub::empty_transition(lp.kv_transition);
+        const RowTxn &rt = txns[i];
+        glacier_hip_root_transition_v1_t &t = lp.kv_transition;
+        lp.lane_index = (uint32_t)i;
+        lp.step_index = ln.output.size();
+        lp.prompt_len = ln.prompt_len;
+        lp.kv_capacity_bytes = lane_capacity_bytes(s);
+        lp.has_kv_transition = 1;
+        lp.kv_before = rt.mark.base_len;
+        lp.kv_after = rt.mark.base_len + 1;
+        t.cache_instance = rt.mark.cache_instance;
+        t.row_txn_generation = rt.mark.generation;
+        copy_root(rt.before, t, true);
+        copy_root(rt.after, t, false);
+        t.logical_page = rt.mark.page_ref.logical_page;
+        t.page_ownership_generation = rt.mark.page_ref.ownership_generation;
+        t.installs_new_page = rt.installs ? 1 : 0;
+        memcpy(t.row_payload_sha256, digests[i].data(), 32);
+        if (ln.chain_init) {
+          memcpy(t.state_chain_before, ln.chain, 32);
+          gpub::appended_state_chain(ln.chain, rt.before, rt.after, rt.mark, digests[i].data(),
+                                     t.state_chain_after);
+        }
+        lp.output_before = ln.output.size();
+        lp.output_after = ln.output.size() + 1;
+        memcpy(lp.rng_before, ln.rng, sizeof ln.rng);
+        memcpy(lp.rng_after, ln.rng, sizeof ln.rng);  // greedy: the RNG never advances
+        lp.sampling_calls_before = ln.sampling_calls;
+        lp.sampling_calls_after = ln.sampling_calls + (elig ? 0 : 1);
+        lp.token_id = next[i];
+      }
+      return sink(sink_ctx, stages.data(), (uint32_t)stages.size()) ? GLACIER_HIP_SINK_REJECTED
+                                                                     : GLACIER_HIP_OK;
+    };
+  }
+  ops.publish = [&](uint32_t i) -> int {
+    // this quantum's KV row (root + length), sampler counter and output word
+    Lane &ln = s->lanes[lanes[i]];
+    if (ln.lease) ln.lease->lease.end_rows();
+    if (int rc = ln.kv.commit(&txns[i], 1)) return rc;
+    published[i] = 1;
+    // the eligible (posthead) branch does not count a sampler call
+    // (generate.zig:5574-5598); the greedy sampler does (:5593)
+    if (!elig) ln.sampling_calls += 1;
+    ln.output.push_back(next[i]);
     tokens_by_lane[lanes[i]] = next[i];
-  return rc;
+    return GLACIER_HIP_OK;
+  };
+  ops.abort = [&](uint32_t from) {
+    for (uint32_t i = from; i < (uint32_t)txns.size(); ++i) {
+      if (published[i]) continue;
+      Lane &ln = s->lanes[lanes[i]];
+      if (ln.lease) ln.lease->lease.end_rows();
+      (void)ln.kv.abort(&txns[i], 1);
+    }
+  };
+  return gh::lane_weave_run_wave(lw, max_count, ops, slots_out, events_out, count_out);
+}
+
+}  // namespace
+
+extern "C" int glacier_hip_session_lane_weave_wave(
+    glacier_hip_session *s, glacier_hip_lane_weave *lw, const uint32_t *lane_of_slot,
+    uint32_t slot_count, uint32_t *tokens_by_lane, const uint64_t *eligible_by_lane,
+    uint32_t max_count, uint32_t *slots_out, glacier_hip_lane_event_t *events_out,
+    uint32_t *count_out) {
+  return lane_weave_wave_impl(s, lw, lane_of_slot, slot_count, tokens_by_lane, eligible_by_lane,
+                              max_count, nullptr, nullptr, slots_out, events_out, count_out);
+}
+
+extern "C" int glacier_hip_session_lane_weave_wave_staged(
+    glacier_hip_session *s, glacier_hip_lane_weave *lw, const uint32_t *lane_of_slot,
+    uint32_t slot_count, uint32_t *tokens_by_lane, const uint64_t *eligible_by_lane,
+    uint32_t max_count, glacier_hip_wave_sink_fn sink, void *sink_ctx, uint32_t *slots_out,
+    glacier_hip_lane_event_t *events_out, uint32_t *count_out) {
+  if (!sink) return GLACIER_HIP_INVALID_ARGUMENT;
+  return lane_weave_wave_impl(s, lw, lane_of_slot, slot_count, tokens_by_lane, eligible_by_lane,
+                              max_count, sink, sink_ctx, slots_out, events_out, count_out);
 }
 
 // ---------------------------------------------------------------------------

@@ -338,6 +338,26 @@ class LaneProposal(C.Structure):
          ("sampling_calls_after", C.c_uint64), ("token_id", C.c_uint32), ("terminal", C.c_uint32)]
 
 
+class ServicePermit(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("abi_version", "scheduler_epoch", "coordinator_id",
+                                          "coordinator_address", "permit_generation",
+                                          "event_sequence")] + \
+        [("handle", LaneHandle), ("logical_tick_before", C.c_uint64)] + \
+        [(n, C.c_uint32) for n in ("cursor_before", "level_before", "cursor_after",
+                                   "level_after")] + \
+        [(n, C.c_uint64) for n in ("remaining_before", "wait_quanta", "maximum_service_gap")] + \
+        [("state_before_sha256", C.c_uint8 * 32), ("chain_head_before_sha256", C.c_uint8 * 32),
+         ("resource_receipt", BankReceipt), ("resource_receipt_sha256", C.c_uint8 * 32),
+         ("permit_sha256", C.c_uint8 * 32)]
+
+
+class WaveStage(C.Structure):
+    _fields_ = [("slot", C.c_uint32), ("lane", C.c_uint32), ("stage", LaneProposal)]
+
+
+WAVE_SINK = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(WaveStage), C.c_uint32)
+
+
 class TokenProposal(C.Structure):
     _fields_ = [(n, C.c_uint64) for n in (
         "abi_version", "resource_bank_abi", "resource_publication_fence_abi", "paged_kv_abi",
@@ -590,6 +610,13 @@ _SIGS = [
     ("glacier_hip_lane_weave_state_sha256", C.c_int, [_P, _P]),
     ("glacier_hip_session_lane_weave_wave", C.c_int,
      [_P, _P, _P, C.c_uint32, _P, _P, C.c_uint32, _P, _P, C.POINTER(C.c_uint32)]),
+    ("glacier_hip_session_lane_weave_wave_staged", C.c_int,
+     [_P, _P, _P, C.c_uint32, _P, _P, C.c_uint32, WAVE_SINK, _P, _P, _P, C.POINTER(C.c_uint32)]),
+    ("glacier_hip_lane_weave_prepare_service", C.c_int, [_P, C.POINTER(ServicePermit)]),
+    ("glacier_hip_lane_weave_commit_service", C.c_int,
+     [_P, C.POINTER(ServicePermit), C.POINTER(LaneEvent)]),
+    ("glacier_hip_lane_weave_abort_service", C.c_int, [_P, C.POINTER(ServicePermit)]),
+    ("glacier_hip_service_permit_sha256", C.c_int, [C.POINTER(ServicePermit), _P]),
     ("glacier_hip_page_image_bytes", C.c_uint64, [C.c_uint64, C.c_uint64, C.c_uint64]),
     ("glacier_hip_page_image_encode_canonical", C.c_int,
      [C.POINTER(PageMapRoot), C.c_uint64, C.c_uint64, C.c_uint64, C.POINTER(PageRef), C.c_uint64,
@@ -1199,6 +1226,7 @@ class KvPages:
 
 
 STALE_HANDLE, NO_RUNNABLE, INCOMPLETE_DRAIN, SCHEDULER_CLOSED, SCHEDULER_POISONED = 15, 16, 17, 18, 19
+SERVICE_IN_FLIGHT, STALE_SERVICE_PERMIT, SINK_REJECTED = 23, 24, 25
 
 
 def _claim(d):
@@ -1299,6 +1327,44 @@ class LaneWeave:
         out = (C.c_uint8 * 32)()
         check(lib().glacier_hip_lane_weave_chain_head(self.h, out), "chain_head")
         return bytes(out)
+
+    def prepare_service(self):
+        """prepareService -> (rc, ServicePermit)."""
+        p = ServicePermit()
+        rc = lib().glacier_hip_lane_weave_prepare_service(self.h, C.byref(p))
+        return rc, p
+
+    def commit_service(self, permit):
+        """commitService -> (rc, event)."""
+        return self._ev(lib().glacier_hip_lane_weave_commit_service, C.byref(permit))
+
+    def abort_service(self, permit):
+        return lib().glacier_hip_lane_weave_abort_service(self.h, C.byref(permit))
+
+    def state_sha256(self):
+        out = (C.c_uint8 * 32)()
+        check(lib().glacier_hip_lane_weave_state_sha256(self.h, out), "state_sha256")
+        return bytes(out)
+
+    def wave_staged(self, sess, lane_of_slot, tokens_by_lane, sink, eligible_by_lane=None,
+                    max_count=None):
+        """glacier_hip_session_lane_weave_wave_staged; sink(stages) returns
+        True to acknowledge the wave's stages (a list of WaveStage copies).
+        Returns (rc, slots, events)."""
+        los = np.ascontiguousarray(lane_of_slot, dtype=np.uint32)
+        mc = max_count or len(los)
+        slots = np.zeros(mc, dtype=np.uint32)
+        evs = (LaneEvent * mc)()
+        n = C.c_uint32(0)
+
+        def cb(_ctx, stages, count):
+            return 0 if sink([WaveStage.from_buffer_copy(stages[i]) for i in range(count)]) else 1
+
+        fn = WAVE_SINK(cb)
+        rc = lib().glacier_hip_session_lane_weave_wave_staged(
+            sess.h, self.h, ptr(los), los.size, ptr(tokens_by_lane), ptr(eligible_by_lane), mc, fn,
+            None, ptr(slots), evs, C.byref(n))
+        return rc, slots[:n.value].tolist(), [evs[i] for i in range(n.value)]
 
 
 class LeaseError(Exception):

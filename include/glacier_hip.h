@@ -52,6 +52,9 @@ enum glacier_hip_status {
     GLACIER_HIP_NOT_FOUND = 21,          /* no record with that key */
     GLACIER_HIP_INVALID_CHECKPOINT = 22, /* a page image or checkpoint restore was rejected
                                           * (the reason: glacier_hip_page_image_v1_t.error) */
+    GLACIER_HIP_SERVICE_IN_FLIGHT = 23,  /* LaneWeave Error.ServiceInFlight */
+    GLACIER_HIP_STALE_SERVICE_PERMIT = 24, /* LaneWeave Error.StaleServicePermit */
+    GLACIER_HIP_SINK_REJECTED = 25,      /* a publication sink refused a wave's stages */
 };
 
 /* ---- element types / activation modes ------------------------------------ */
@@ -747,6 +750,40 @@ int glacier_hip_lane_weave_slot(glacier_hip_lane_weave *lw, uint32_t slot,
 int glacier_hip_lane_weave_chain_head(glacier_hip_lane_weave *lw, uint8_t out[32]);
 int glacier_hip_lane_weave_state_sha256(glacier_hip_lane_weave *lw, uint8_t out[32]);
 
+/* ServicePermitV1 (lane_weave_qos.zig:122-142): the next IWRR selection
+ * frozen by prepareService without advancing the tick, cursor, request work,
+ * Bank charge or event chain; bound to this scheduler's lifetime (a
+ * process-wide coordinator id) and address. permit_sha256 is
+ * servicePermitSha256 (:3557-3581). */
+typedef struct {
+    uint64_t abi_version, scheduler_epoch, coordinator_id, coordinator_address;
+    uint64_t permit_generation, event_sequence;
+    glacier_hip_lane_handle_t handle;
+    uint64_t logical_tick_before;
+    uint32_t cursor_before, level_before;  /* level: u16 in the reference */
+    uint32_t cursor_after, level_after;
+    uint64_t remaining_before, wait_quanta, maximum_service_gap;
+    uint8_t state_before_sha256[32], chain_head_before_sha256[32];
+    glacier_hip_bank_receipt_t resource_receipt;
+    uint8_t resource_receipt_sha256[32], permit_sha256[32];
+} glacier_hip_service_permit_v1_t;
+/* prepareService (:1127-1192): one permit may be pending; while it is,
+ * prepare / serve_one / admit / cancel / retire / close / waves return
+ * GLACIER_HIP_SERVICE_IN_FLIGHT and change nothing. commitService
+ * (:1272-1286) consumes the pending permit and emits the service event
+ * serve_one would have emitted (byte-identical); abortService (:1438-1452)
+ * consumes it with no logical change. A permit that is not exactly the
+ * pending one (mutated, consumed, foreign, from an earlier scheduler) is
+ * GLACIER_HIP_STALE_SERVICE_PERMIT and consumes nothing. */
+int glacier_hip_lane_weave_prepare_service(glacier_hip_lane_weave *lw,
+                                           glacier_hip_service_permit_v1_t *permit_out);
+int glacier_hip_lane_weave_commit_service(glacier_hip_lane_weave *lw,
+                                          const glacier_hip_service_permit_v1_t *permit,
+                                          glacier_hip_lane_event_t *event_out);
+int glacier_hip_lane_weave_abort_service(glacier_hip_lane_weave *lw,
+                                         const glacier_hip_service_permit_v1_t *permit);
+int glacier_hip_service_permit_sha256(const glacier_hip_service_permit_v1_t *permit, uint8_t out[32]);
+
 /* One LaneWeave decode wave (the multi-request service loop of
  * prepared_text_session.zig:1840-1885 with one token per service quantum):
  * plan the next quanta of distinct lanes (at most max_count), run those
@@ -759,9 +796,15 @@ int glacier_hip_lane_weave_state_sha256(glacier_hip_lane_weave *lw, uint8_t out[
  * committed slots and their Event-v1 records; count_out the number of quanta.
  * The scheduler stays locked from planning to commit, and the plan holds
  * only quanta whose serve_one commits (it stops before a deadline or service
- * gap the next quantum would break). A failed device step commits nothing:
- * no KV row, token, sampler counter or scheduler event. NO_RUNNABLE when no
- * lane is runnable. */
+ * gap the next quantum would break). The device step runs privately (KV rows
+ * provisional); then each planned quantum publishes inside the reference's
+ * service transaction, in plan order: prepareService (its permit must select
+ * the planned slot), the lane's KV row, sampler counter and output word
+ * published, commitService (the quantum's Event-v1). A failed device step
+ * publishes nothing: no KV row, token, sampler counter or scheduler event; a
+ * permit that selects another slot aborts it (abortService), publishes
+ * nothing more and poisons the scheduler. NO_RUNNABLE when no lane is
+ * runnable; SERVICE_IN_FLIGHT while a caller's permit is pending. */
 int glacier_hip_session_lane_weave_wave(glacier_hip_session *s, glacier_hip_lane_weave *lw,
                                         const uint32_t *lane_of_slot, uint32_t slot_count,
                                         uint32_t *tokens_by_lane,
@@ -820,6 +863,32 @@ typedef struct {
     glacier_hip_bank_receipt_t receipt;
     glacier_hip_lane_proposal_v1_t lanes[GLACIER_HIP_PUBLICATION_WIDTH];
 } glacier_hip_token_proposal_v1_t;      /* ProposalV1 (:110-131) */
+
+/* A LaneWeave wave published through a sink: one stage per planned quantum,
+ * in plan order (the scheduler slot, the session lane, and the lane's token
+ * transition as a LaneProposalV1: the staged KV row's page-map root
+ * transition and row payload digest, output, RNG and sampler counters
+ * before / after, token; the state-chain fields are the lane's when it
+ * publishes staged waves, else zero). */
+typedef struct {
+    uint32_t slot, lane;
+    glacier_hip_lane_proposal_v1_t stage;
+} glacier_hip_wave_stage_v1_t;
+/* The sink acknowledges (0) or rejects (nonzero) the whole wave before any
+ * quantum publishes (the prepare -> ack of paged_token_txn.zig:503-515,
+ * taken once per wave). */
+typedef int (*glacier_hip_wave_sink_fn)(void *ctx, const glacier_hip_wave_stage_v1_t *stages,
+                                        uint32_t count);
+/* glacier_hip_session_lane_weave_wave with the wave's stages put to `sink`
+ * after the private device step and before the first service permit: a
+ * rejection aborts every staged row and returns GLACIER_HIP_SINK_REJECTED;
+ * no lane publishes, the scheduler's state and event chain do not move and
+ * the same quanta are planned again by the next wave. */
+int glacier_hip_session_lane_weave_wave_staged(
+    glacier_hip_session *s, glacier_hip_lane_weave *lw, const uint32_t *lane_of_slot,
+    uint32_t slot_count, uint32_t *tokens_by_lane, const uint64_t *eligible_by_lane,
+    uint32_t max_count, glacier_hip_wave_sink_fn sink, void *sink_ctx, uint32_t *slots_out,
+    glacier_hip_lane_event_t *events_out, uint32_t *count_out);
 
 typedef struct {
     uint64_t abi_version;            /* 0x4750544100000001 */

@@ -21,6 +21,7 @@ order and close-event SHA-256 (lane_weave_qos.zig:4436-4474), the deadline,
 projection-budget and resource-limit rejections (:4476-4570) and stale-handle
 fencing (:4572-4586).
 """
+import copy
 import hashlib
 import struct
 
@@ -43,6 +44,10 @@ LIMIT_FIELDS = ("host_bytes",) + CLAIM_FIELDS
 ADMISSION_ACCEPTED, ADMISSION_REJECTED, SERVICE, CANCEL, RETIRE, CLOSE = range(6)
 NONE, NO_SLOT, DUPLICATE_TENANT, RESOURCE_LIMIT, PROJECTION_LIMIT, DEADLINE_INFEASIBLE = range(6)
 FREE, ACTIVE, FINISHED = range(3)
+
+
+SERVICE_PERMIT_ABI = 0x474C575000000001  # service_permit_abi (lane_weave_qos.zig:19)
+_next_coordinator = [1]  # nextServiceCoordinatorId (:556-566)
 
 
 class LaneWeaveError(Exception):
@@ -334,6 +339,10 @@ class Scheduler:
         self.level = 1
         self.poisoned = False
         self.closed = False
+        self.pending_service = None
+        self.next_service_permit_generation = 1
+        self.service_coordinator_id = _next_coordinator[0]
+        _next_coordinator[0] += 1
         self.maximum_service_gap = (capacity - 1) * max_weight + 1
         h = hashlib.sha256(b"glacier-lane-weave-qos-root-v1\x00")
         _u64(h, ABI)
@@ -490,6 +499,7 @@ class Scheduler:
         """Returns (accepted: bool, handle or None, event)."""
         if self.closed:
             raise LaneWeaveError("SchedulerClosed")
+        self._require_no_service()
         self._valid_spec(sp)
         snap = self._snapshot_before()
 
@@ -535,9 +545,17 @@ class Scheduler:
         return select_iwrr([(s["state"] == ACTIVE, s["spec"]["weight"]) for s in self.slots],
                            self.cursor, self.level, self.max_weight)
 
+    def _require_no_service(self):
+        if self.pending_service is not None:
+            raise LaneWeaveError("ServiceInFlight")
+
     def serve_one(self):
         if self.closed:
             raise LaneWeaveError("SchedulerClosed")
+        self._require_no_service()
+        return self._serve_locked()
+
+    def _serve_locked(self):
         sel = self.next_selection()
         if sel is None:
             raise LaneWeaveError("NoRunnableRequest")
@@ -575,6 +593,7 @@ class Scheduler:
     def _finish(self, handle, kind, required_state):
         if self.closed:
             raise LaneWeaveError("SchedulerClosed")
+        self._require_no_service()
         i = handle["slot_index"]
         if handle["scheduler_epoch"] != self.epoch or i >= len(self.slots):
             raise LaneWeaveError("StaleHandle")
@@ -602,12 +621,120 @@ class Scheduler:
     def close(self):
         if self.closed:
             raise LaneWeaveError("SchedulerClosed")
+        self._require_no_service()
         a, f = self.counts()
         if a or f or not claim_is_zero(self.used):
             raise LaneWeaveError("IncompleteDrain")
         snap = self._snapshot_before()
         self.closed = True
         return self._emit(CLOSE, snap[0], snap[1], snap[2], snap[3], (0, 0), snap[5])
+
+    # ---- prepared service (prepareService :1127-1192, commitService
+    # :1272-1286, abortService :1438-1452) ----
+    def prepare_service(self):
+        if self.closed:
+            raise LaneWeaveError("SchedulerClosed")
+        self._require_no_service()
+        if self.logical_tick == U64_MAX:
+            raise LaneWeaveError("TickOverflow")
+        sel = self.next_selection()
+        if sel is None:
+            raise LaneWeaveError("NoRunnableRequest")
+        idx, cur_after, lvl_after = sel
+        s = self.slots[idx]
+        after_tick = self.logical_tick + 1
+        for j, o in enumerate(self.slots):  # selectionPreservesDeadlines
+            if o["state"] != ACTIVE or o["spec"]["deadline_tick"] == 0:
+                continue
+            completes = j == idx and o["remaining_quanta"] == 1
+            if (completes and after_tick > o["spec"]["deadline_tick"]) or (
+                    not completes and after_tick >= o["spec"]["deadline_tick"]):
+                self.poisoned = True
+                raise LaneWeaveError("InvariantViolation")
+        wait = after_tick - s["last_service_tick"]
+        if wait > self.maximum_service_gap:
+            self.poisoned = True
+            raise LaneWeaveError("InvariantViolation")
+        p = dict(abi_version=SERVICE_PERMIT_ABI, scheduler_epoch=self.epoch,
+                 coordinator_id=self.service_coordinator_id,
+                 coordinator_address=id(self) & U64_MAX,
+                 permit_generation=self.next_service_permit_generation,
+                 event_sequence=self.next_event_sequence, handle=self.handle_for(idx),
+                 logical_tick_before=self.logical_tick, cursor_before=self.cursor,
+                 level_before=self.level, cursor_after=cur_after, level_after=lvl_after,
+                 remaining_before=s["remaining_quanta"], wait_quanta=wait,
+                 maximum_service_gap=self.maximum_service_gap,
+                 state_before_sha256=self.state_sha256(),
+                 chain_head_before_sha256=self.chain_head, resource_receipt=dict(s["receipt"]),
+                 resource_receipt_sha256=s["receipt_sha256"])
+        p["permit_sha256"] = service_permit_sha256(p)
+        self.next_service_permit_generation += 1
+        self.pending_service = copy.deepcopy(p)
+        return p
+
+    def _validate_pending(self, p):
+        """validatePendingService (:2461-2487)."""
+        pend = self.pending_service
+        if pend is None:
+            raise LaneWeaveError("StaleServicePermit")
+        if pend["permit_sha256"] != service_permit_sha256(pend):
+            self.poisoned = True
+            raise LaneWeaveError("InvariantViolation")
+        if (p["abi_version"] != SERVICE_PERMIT_ABI or p["scheduler_epoch"] != self.epoch or
+                p["coordinator_id"] != self.service_coordinator_id or
+                p["coordinator_address"] != id(self) & U64_MAX or p["permit_generation"] == 0 or
+                p["permit_sha256"] != service_permit_sha256(p) or p != pend):
+            raise LaneWeaveError("StaleServicePermit")
+
+    def _validate_before_state(self, p):
+        """validateServiceBeforeState (:2512-2531)."""
+        if (p["state_before_sha256"] != self.state_sha256() or
+                p["event_sequence"] != self.next_event_sequence or
+                p["logical_tick_before"] != self.logical_tick or
+                p["chain_head_before_sha256"] != self.chain_head):
+            self.poisoned = True
+            raise LaneWeaveError("InvariantViolation")
+
+    def commit_service(self, p):
+        if self.closed:
+            raise LaneWeaveError("SchedulerClosed")
+        self._validate_pending(p)
+        self._validate_before_state(p)
+        sel = self.next_selection()
+        if sel is None or sel[0] != p["handle"]["slot_index"] or sel[1] != p["cursor_after"] or \
+                sel[2] != p["level_after"]:
+            self.poisoned = True
+            raise LaneWeaveError("InvariantViolation")
+        self.pending_service = None
+        return self._serve_locked()
+
+    def abort_service(self, p):
+        if self.closed:
+            raise LaneWeaveError("SchedulerClosed")
+        self._validate_pending(p)
+        self._validate_before_state(p)
+        self.pending_service = None
+
+
+def service_permit_sha256(p):
+    """servicePermitSha256 (lane_weave_qos.zig:3557-3581)."""
+    h = hashlib.sha256(b"glacier-lane-weave-qos-service-permit-v1\x00")
+    for f in ("abi_version", "scheduler_epoch", "coordinator_id", "coordinator_address",
+              "permit_generation", "event_sequence"):
+        _u64(h, p[f])
+    _handle(h, p["handle"])
+    _u64(h, p["logical_tick_before"])
+    _u32(h, p["cursor_before"])
+    _u16(h, p["level_before"])
+    _u32(h, p["cursor_after"])
+    _u16(h, p["level_after"])
+    for f in ("remaining_before", "wait_quanta", "maximum_service_gap"):
+        _u64(h, p[f])
+    h.update(p["state_before_sha256"])
+    h.update(p["chain_head_before_sha256"])
+    _receipt(h, p["resource_receipt"])
+    h.update(p["resource_receipt_sha256"])
+    return h.digest()
 
 
 def test_spec(key, weight, work, deadline):

@@ -149,7 +149,7 @@ void weave_trace(glacier_hip_lane_weave *lw, uint32_t capacity, std::mt19937_64 
   for (int op = 0; op < ops; ++op) {
     glacier_hip_lane_event_t ev;
     uint8_t before[32], after[32];
-    switch (rng() % 7) {
+    switch (rng() % 8) {
       case 0:
       case 1: {  // admit (sometimes malformed or infeasible)
         uint64_t w = rng() % 6;  // 0 and 5 are out of range for max_weight 4
@@ -181,29 +181,61 @@ void weave_trace(glacier_hip_lane_weave *lw, uint32_t capacity, std::mt19937_64 
         }
         break;
       }
-      case 3: {  // a wave whose device step fails changes nothing
+      case 3: {  // a wave whose device step fails or whose sink rejects changes nothing
         glacier_hip_lane_weave_state_sha256(lw, before);
-        uint32_t slots[64], n = 0;
+        uint32_t slots[64], n = 0, ran = 0, published = 0, aborted_from = ~0u;
         glacier_hip_lane_event_t evs[64];
-        const bool fail = rng() % 3 == 0;
-        int rc = gh::lane_weave_run_wave(
-            lw, 1 + rng() % capacity,
-            [&](const uint32_t *s, uint32_t k) {
-              for (uint32_t i = 0; i < k; ++i)
-                if (s[i] >= capacity) return (int)GLACIER_HIP_INVALID_ARGUMENT;
-              return fail ? (int)GLACIER_HIP_DEVICE_ERROR : (int)GLACIER_HIP_OK;
-            },
-            slots, evs, &n);
+        const bool fail = rng() % 3 == 0, reject = rng() % 4 == 0;
+        gh::WaveOps ops;
+        ops.run = [&](const uint32_t *s, uint32_t k) {
+          for (uint32_t i = 0; i < k; ++i)
+            if (s[i] >= capacity) return (int)GLACIER_HIP_INVALID_ARGUMENT;
+          ran = k;
+          return fail ? (int)GLACIER_HIP_DEVICE_ERROR : (int)GLACIER_HIP_OK;
+        };
+        if (reject) ops.sink = [&]() { return (int)GLACIER_HIP_SINK_REJECTED; };
+        ops.publish = [&](uint32_t i) {
+          if (i != published || i >= ran) {  // quanta publish once each, in plan order
+            ++g_fail;
+            return (int)GLACIER_HIP_INVALID_ARGUMENT;
+          }
+          ++published;
+          return (int)GLACIER_HIP_OK;
+        };
+        ops.abort = [&](uint32_t from) { aborted_from = from; };
+        int rc = gh::lane_weave_run_wave(lw, 1 + rng() % capacity, ops, slots, evs, &n);
         glacier_hip_lane_weave_state_sha256(lw, after);
         if (rc != GLACIER_HIP_OK) {
-          g_n.failed_waves += rc == GLACIER_HIP_DEVICE_ERROR;
-          CHECK(n == 0);
+          g_n.failed_waves += rc == GLACIER_HIP_DEVICE_ERROR || rc == GLACIER_HIP_SINK_REJECTED;
+          CHECK(n == 0 && published == 0);
+          if (rc == GLACIER_HIP_SINK_REJECTED) CHECK(aborted_from == 0);
           if (!concurrent) CHECK(memcmp(before, after, 32) == 0);
         } else {
+          CHECK(published == n && n == ran && aborted_from == ~0u);
           for (uint32_t i = 0; i < n; ++i) CHECK(evs[i].handle.slot_index == slots[i]);
           ++g_n.waves;
           g_n.served += n;
         }
+        break;
+      }
+      case 7: {  // a caller's prepared service, committed or aborted
+        glacier_hip_service_permit_v1_t p;
+        glacier_hip_lane_weave_state_sha256(lw, before);
+        int rc = glacier_hip_lane_weave_prepare_service(lw, &p);
+        if (rc) break;
+        glacier_hip_lane_weave_state_sha256(lw, after);
+        if (!concurrent) CHECK(memcmp(before, after, 32) == 0);
+        glacier_hip_service_permit_v1_t bad = p;
+        bad.remaining_before += 1;
+        CHECK(glacier_hip_lane_weave_commit_service(lw, &bad, &ev) == GLACIER_HIP_STALE_SERVICE_PERMIT);
+        if (rng() & 1) {
+          rc = glacier_hip_lane_weave_commit_service(lw, &p, &ev);
+          CHECK(rc == GLACIER_HIP_OK && ev.handle.slot_index == p.handle.slot_index);
+          ++g_n.served;
+        } else {
+          CHECK(glacier_hip_lane_weave_abort_service(lw, &p) == GLACIER_HIP_OK);
+        }
+        CHECK(glacier_hip_lane_weave_abort_service(lw, &p) == GLACIER_HIP_STALE_SERVICE_PERMIT);
         break;
       }
       case 4: {  // cancel or retire a known (maybe stale) handle
@@ -284,9 +316,11 @@ void mode_threads(uint64_t seed, int ops) {
     for (int i = 0; i < ops; ++i) {
       uint32_t slots[16], n = 0;
       glacier_hip_lane_event_t evs[16];
-      gh::lane_weave_run_wave(lw, 1 + rng() % capacity,
-                              [](const uint32_t *, uint32_t) { return (int)GLACIER_HIP_OK; },
-                              slots, evs, &n);
+      gh::WaveOps ops;
+      ops.run = [](const uint32_t *, uint32_t) { return (int)GLACIER_HIP_OK; };
+      ops.publish = [](uint32_t) { return (int)GLACIER_HIP_OK; };
+      ops.abort = [](uint32_t) {};
+      gh::lane_weave_run_wave(lw, 1 + rng() % capacity, ops, slots, evs, &n);
       uint8_t head[32];
       glacier_hip_lane_weave_chain_head(lw, head);
     }

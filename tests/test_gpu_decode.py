@@ -512,3 +512,108 @@ def test_concurrent_submission_is_rejected_busy(gh, tiny):
         assert len(nxt) == 2
     finally:
         sess.close()
+
+
+def test_lane_weave_wave_sink_rejection_publishes_nothing(gh, gctx, tiny, ora):
+    """LaneWeave waves publish each quantum inside the reference's service
+    transaction (prepareService -> publish -> commitService,
+    lane_weave_qos.zig:1127-1286) after the wave's stages are acknowledged:
+    a sink that rejects the wave leaves every lane unpublished (KV root,
+    length, outputs, sampler counter) and the scheduler's state and event
+    chain unmoved; the same quanta run again in the next wave, whose stages
+    carry the tokens and KV root transitions the lanes then publish. A
+    caller's pending permit holds waves off (SERVICE_IN_FLIGHT)."""
+    from oracle import lane_weave as olw
+
+    host, om, m = tiny
+    weights = [1, 2, 1, 3]
+    quanta = [3, 5, 2, 4]
+    cap = 4
+    prompts = [gh.synth_tokens(SEED, 400 + i, TINY["vocab_size"], 6 + 5 * i) for i in range(cap)]
+    lim = dict(host_bytes=1 << 30, kv_bytes=1 << 30, queue_slots=cap)
+    sched = gh.LaneWeave(cap, lim, bank_epoch=7, scheduler_epoch=9, max_weight=4)
+    ref = olw.Scheduler(olw.Bank(cap, olw.limits(**lim), 7), cap, 9, bytes([0xA5]) + bytes(31), 4)
+    sess = gh.Session(m, max_lanes=cap, max_positions=64)
+    try:
+        tokens = np.zeros(cap, np.uint32)
+        got = [[] for _ in range(cap)]
+        for i in range(cap):
+            sp = dict(tenant_key=i + 1, request_key=10 * (i + 1), request_generation=1,
+                      resource_owner_key=100 * (i + 1), weight=weights[i], work_quanta=quanta[i],
+                      deadline_tick=0, claim=olw.claim(kv_bytes=4096, queue_slots=1))
+            ok, _, ev = sched.admit(gh.LaneWeave.spec(**{**sp, "claim": {"kv_bytes": 4096,
+                                                                          "queue_slots": 1}}))
+            assert ok and bytes(ev.event_sha256) == ref.admit(sp)[2]["event_sha256"]
+            sess.begin(i)
+            tokens[i] = sess.prefill(i, prompts[i])
+            got[i].append(int(tokens[i]))
+        # a caller's permit holds the wave off
+        rc, permit = sched.prepare_service()
+        assert rc == gh.OK
+        rc, _, _ = sched.wave_staged(sess, list(range(cap)), tokens, lambda st: True)
+        assert rc == gh.SERVICE_IN_FLIGHT
+        assert sched.abort_service(permit) == gh.OK
+        # a rejected wave
+        head, state = sched.chain_head(), sched.state_sha256()
+        roots = [sess.root(i) for i in range(cap)]
+        states = [sess.state(i) for i in range(cap)]
+        plan = sched.plan_wave(cap)
+        seen = []
+        print("lane weave: rejected wave", flush=True)
+        rc, slots, evs = sched.wave_staged(sess, list(range(cap)), tokens,
+                                           lambda st: seen.append(st) or False)
+        assert rc == gh.SINK_REJECTED and slots == [] and evs == []
+        assert sched.chain_head() == head and sched.state_sha256() == state
+        for i in range(cap):
+            r, st = sess.root(i), sess.state(i)
+            assert r.committed_len == roots[i].committed_len
+            assert bytes(r.ownership_sha256) == bytes(roots[i].ownership_sha256)
+            assert (st.published_tokens, st.sampling_calls) == \
+                (states[i].published_tokens, states[i].sampling_calls)
+            assert int(tokens[i]) == got[i][-1]
+        rejected = seen[0]
+        assert [w.slot for w in rejected] == plan and [w.lane for w in rejected] == plan
+        # the same quanta, acknowledged
+        acked = []
+        rc, slots, evs = sched.wave_staged(sess, list(range(cap)), tokens,
+                                           lambda st: acked.append(st) or True)
+        assert rc == gh.OK and slots == plan
+        stages = acked[0]
+        for w, slot, ev in zip(stages, slots, evs):
+            st = w.stage
+            assert int(tokens[slot]) == st.token_id == \
+                next(x.stage.token_id for x in rejected if x.slot == slot)
+            r = sess.root(slot)
+            assert st.kv_after == r.committed_len and st.kv_before == r.committed_len - 1
+            assert st.kv_transition.root_after_generation == r.generation
+            assert bytes(st.kv_transition.root_after_ownership_sha256) == bytes(r.ownership_sha256)
+            assert st.output_after == sess.state(slot).published_tokens
+            assert bytes(ev.event_sha256) == ref.serve_one()["event_sha256"]
+            got[slot].append(int(tokens[slot]))
+        for slot, ev in zip(slots, evs):
+            if ev.remaining_after == 0:
+                rc, rev = sched.retire(ev.handle)
+                assert rc == 0 and bytes(rev.event_sha256) == \
+                    ref.retire(ref.handle_for(slot))["event_sha256"]
+        # the rest through plain waves
+        while True:
+            try:
+                slots, evs = sched.wave(sess, list(range(cap)), tokens)
+            except gh.GlacierHipError as e:
+                assert e.code == gh.NO_RUNNABLE
+                break
+            for slot, ev in zip(slots, evs):
+                got[slot].append(int(tokens[slot]))
+                assert bytes(ev.event_sha256) == ref.serve_one()["event_sha256"]
+            for slot, ev in zip(slots, evs):
+                if ev.remaining_after == 0:
+                    rc, rev = sched.retire(ev.handle)
+                    assert rc == 0 and bytes(rev.event_sha256) == \
+                        ref.retire(ref.handle_for(slot))["event_sha256"]
+        rc, cev = sched.close()
+        assert rc == 0 and bytes(cev.event_sha256) == ref.close()["event_sha256"]
+        for i in range(cap):
+            want = om.generate(prompts[i], quanta[i] + 1)[0].tolist()
+            assert got[i] == want, (i, got[i], want)
+    finally:
+        sess.close()

@@ -306,3 +306,215 @@ def test_c5_schedule_replays_on_oracle(gh):
     # the chain head of the bench's config-5 run on the GPU (device waves)
     assert bytes(p_close.event_sha256).hex() == \
         "7d027cdf284a5173360b19e40f9ba7099533958d46b50fd56d83b44e4b36c06f"
+
+
+# ------------------------------------------------------ prepared service ----
+# The reference's prepared-service tests (lane_weave_qos.zig:6156-6282,
+# :6652-6766) on the oracle and on the product. Permits are process-local
+# (coordinator id and address), so their digests are compared only with the
+# same implementation's recomputation.
+class _OracleSched:
+    def __init__(self, cap, mw):
+        self.f = lw.test_fixture(cap, mw)
+
+    def admit(self, key, weight, work):
+        ok, _, ev = self.f.admit(lw.test_spec(key, weight, work, 0))
+        assert ok
+        return ev["handle"]
+
+    def call(self, name, *args):
+        try:
+            return "OK", getattr(self.f, name)(*args)
+        except lw.LaneWeaveError as e:
+            return str(e), None
+
+    def state(self):
+        return self.f.state_sha256(), self.f.chain_head, dict(self.f.bank.used)
+
+    def event_sha(self, ev):
+        return ev["event_sha256"]
+
+    def mutate(self, p, field, how):
+        q = __import__("copy").deepcopy(p)
+        if field.startswith("handle."):
+            q["handle"][field[7:]] = (q["handle"][field[7:]] + 1) & lw.U64_MAX
+        elif field.startswith("resource_receipt."):
+            q["resource_receipt"][field[17:]] = (q["resource_receipt"][field[17:]] + 1) & lw.U64_MAX
+        elif field.endswith("sha256"):
+            q[field] = bytes([q[field][0] ^ 0xFF]) + q[field][1:]
+        else:
+            q[field] = (q[field] + 1) & lw.U64_MAX
+        if how == "resealed":
+            q["permit_sha256"] = lw.service_permit_sha256(q)
+        return q
+
+
+class _ProductSched:
+    names = {0: "OK", 16: "NoRunnableRequest", 18: "SchedulerClosed", 19: "InvariantViolation",
+             23: "ServiceInFlight", 24: "StaleServicePermit", 15: "StaleHandle",
+             17: "IncompleteDrain"}
+
+    def __init__(self, gh, cap, mw):
+        self.gh = gh
+        self.f = _product(gh, cap, mw)
+
+    def admit(self, key, weight, work):
+        ok, h, ev = self.f.admit(_pspec(self.gh, lw.test_spec(key, weight, work, 0)))
+        assert ok
+        return h
+
+    def call(self, name, *args):
+        f = self.f
+        if name == "prepare_service":
+            rc, p = f.prepare_service()
+            return self.names.get(rc, rc), p
+        if name in ("commit_service", "serve_one", "close"):
+            rc, ev = (f.commit_service(*args) if name == "commit_service" else
+                      f._ev(getattr(self.gh.lib(), "glacier_hip_lane_weave_" + name)))
+            return self.names.get(rc, rc), ev
+        if name == "abort_service":
+            return self.names.get(f.abort_service(*args), None), None
+        if name in ("cancel", "retire"):
+            rc, ev = getattr(f, name)(*args)
+            return self.names.get(rc, rc), ev
+        if name == "admit":
+            import ctypes as C
+            ok, h, e = C.c_int(0), self.gh.LaneHandle(), self.gh.LaneEvent()
+            rc = self.gh.lib().glacier_hip_lane_weave_admit(
+                f.h, C.byref(_pspec(self.gh, args[0])), C.byref(ok), C.byref(h), C.byref(e))
+            return self.names.get(rc, rc), e
+        raise AssertionError(name)
+
+    def state(self):
+        return self.f.state_sha256(), self.f.chain_head()
+
+    def event_sha(self, ev):
+        return bytes(ev.event_sha256)
+
+    def mutate(self, p, field, how):
+        import ctypes as C
+        q = self.gh.ServicePermit.from_buffer_copy(p)
+        if field.startswith("handle."):
+            setattr(q.handle, field[7:], getattr(q.handle, field[7:]) + 1)
+        elif field.startswith("resource_receipt."):
+            setattr(q.resource_receipt, field[17:], getattr(q.resource_receipt, field[17:]) + 1)
+        elif field.endswith("sha256"):
+            getattr(q, field)[0] ^= 0xFF
+        else:
+            setattr(q, field, (getattr(q, field) + 1) & ((1 << 64) - 1))
+        if how == "resealed":
+            out = (C.c_uint8 * 32)()
+            self.gh.lib().glacier_hip_service_permit_sha256(C.byref(q), out)
+            q.permit_sha256[:] = list(bytes(out))
+        return q
+
+
+@pytest.fixture(params=["oracle", "product"])
+def sched(request, gh):
+    return (lambda cap, mw: _OracleSched(cap, mw)) if request.param == "oracle" else \
+        (lambda cap, mw: _ProductSched(gh, cap, mw))
+
+
+def test_service_abort_preserves_state_and_refuses_stale_permits(sched):
+    """:6156-6211: prepare changes nothing; abort restores nothing because
+    nothing moved; a second permit has a later generation and another
+    digest; the aborted first permit is stale for commit and abort."""
+    s = sched(2, 2)
+    h = s.admit(1, 2, 3)
+    before = s.state()
+    rc, first = s.call("prepare_service")
+    assert rc == "OK" and s.state() == before
+    assert s.call("abort_service", first)[0] == "OK" and s.state() == before
+    rc, second = s.call("prepare_service")
+    assert rc == "OK"
+    g = (lambda p: p["permit_generation"]) if isinstance(first, dict) else \
+        (lambda p: p.permit_generation)
+    d = (lambda p: p["permit_sha256"]) if isinstance(first, dict) else \
+        (lambda p: bytes(p.permit_sha256))
+    assert g(second) > g(first) and d(second) != d(first)
+    assert s.call("commit_service", first)[0] == "StaleServicePermit"
+    assert s.call("abort_service", first)[0] == "StaleServicePermit"
+    assert s.call("abort_service", second)[0] == "OK"
+    assert s.call("cancel", h)[0] == "OK"
+    assert s.call("close")[0] == "OK"
+
+
+def test_prepared_commit_is_byte_identical_to_serve_one(sched):
+    """:6253-6282: prepareService + commitService emits the event serveOne
+    emits on an identical scheduler."""
+    a, b = sched(2, 2), sched(2, 2)
+    ha, hb = a.admit(1, 2, 2), b.admit(1, 2, 2)
+    rc, legacy = a.call("serve_one")
+    rc2, p = b.call("prepare_service")
+    rc3, prepared = b.call("commit_service", p)
+    assert (rc, rc2, rc3) == ("OK", "OK", "OK")
+    assert a.event_sha(legacy) == b.event_sha(prepared) and a.state() == b.state()
+    a.call("cancel", ha)
+    b.call("cancel", hb)
+
+
+def test_pending_service_blocks_every_logical_mutator(sched):
+    """:6652-6697."""
+    s = sched(2, 2)
+    h1, h2 = s.admit(1, 1, 2), s.admit(2, 2, 2)
+    rc, p = s.call("prepare_service")
+    before = s.state()
+    assert s.call("prepare_service")[0] == "ServiceInFlight"
+    assert s.call("serve_one")[0] == "ServiceInFlight"
+    assert s.call("admit", lw.test_spec(3, 1, 1, 0))[0] == "ServiceInFlight"
+    assert s.call("cancel", h1)[0] == "ServiceInFlight"
+    assert s.call("cancel", h2)[0] == "ServiceInFlight"
+    assert s.call("retire", h1)[0] == "ServiceInFlight"
+    assert s.call("close")[0] == "ServiceInFlight"
+    assert s.state() == before
+    assert s.call("abort_service", p)[0] == "OK"
+    assert s.call("cancel", h1)[0] == "OK" and s.call("cancel", h2)[0] == "OK"
+    assert s.call("close")[0] == "OK"
+
+
+MUTATIONS = ["abi_version", "scheduler_epoch", "coordinator_id", "coordinator_address",
+             "permit_generation", "event_sequence", "handle.request_key", "logical_tick_before",
+             "cursor_before", "level_before", "cursor_after", "level_after", "remaining_before",
+             "wait_quanta", "maximum_service_gap", "state_before_sha256",
+             "chain_head_before_sha256", "resource_receipt.owner_key", "resource_receipt_sha256",
+             "permit_sha256"]
+
+
+def test_mutated_and_foreign_permits_reject_without_consumption(sched):
+    """:6699-6766: each of the 20 single-field mutations is stale for commit;
+    a mutation resealed with its own digest is stale for abort; another
+    scheduler's permit is stale; the real permit then commits once."""
+    s, foreign = sched(1, 1), sched(1, 1)
+    h = s.admit(1, 1, 2)
+    fh = foreign.admit(1, 1, 2)
+    rc, p = s.call("prepare_service")
+    for field in MUTATIONS:
+        assert s.call("commit_service", s.mutate(p, field, "raw"))[0] == "StaleServicePermit", field
+    assert s.call("abort_service", s.mutate(p, "remaining_before", "resealed"))[0] == \
+        "StaleServicePermit"
+    assert foreign.call("commit_service", p)[0] == "StaleServicePermit"
+    assert s.call("commit_service", p)[0] == "OK"
+    assert s.call("commit_service", p)[0] == "StaleServicePermit"
+    assert s.call("abort_service", p)[0] == "StaleServicePermit"
+    assert s.call("cancel", h)[0] == "OK" and s.call("close")[0] == "OK"
+    rc, fp = foreign.call("prepare_service")
+    assert foreign.call("abort_service", fp)[0] == "OK"
+    assert foreign.call("cancel", fh)[0] == "OK" and foreign.call("close")[0] == "OK"
+
+
+def test_permit_of_an_earlier_scheduler_is_stale(sched):
+    """:6213-6251: a scheduler's lifetime fences its permits (a later
+    scheduler gets another coordinator id)."""
+    old = sched(1, 1)
+    old.admit(1, 1, 1)
+    rc, stale = old.call("prepare_service")
+    new = sched(1, 1)
+    h = new.admit(1, 1, 1)
+    rc, fresh = new.call("prepare_service")
+    cid = (lambda p: p["coordinator_id"]) if isinstance(fresh, dict) else \
+        (lambda p: p.coordinator_id)
+    assert cid(stale) != cid(fresh)
+    assert new.call("commit_service", stale)[0] == "StaleServicePermit"
+    assert new.call("abort_service", stale)[0] == "StaleServicePermit"
+    assert new.call("commit_service", fresh)[0] == "OK"
+    assert new.call("retire", h)[0] == "OK" and new.call("close")[0] == "OK"
