@@ -291,6 +291,72 @@ int Leased::binding_summary(uint32_t state, Summary *out) {
   return GLACIER_HIP_LEASE_OK;
 }
 
+static void hash_claim_fields(gh::Sha256 &h, const glacier_hip_claim_t &c) {
+  const uint64_t *f = &c.capsule_bytes;
+  for (int i = 0; i < 10; ++i) h.u64(f[i]);
+}
+
+// hashLeaseNode (:1597-1616)
+static void hash_lease_node(gh::Sha256 &h, const Node &n) {
+  h.u64(n.abi_version);
+  h.u64(n.parent.bank_epoch);
+  h.u32((uint32_t)n.parent.slot_index);
+  h.u64(n.parent.generation);
+  h.u64(n.parent.owner_key);
+  hash_claim_fields(h, n.parent.claim);
+  h.u64(n.parent.integrity);
+  h.u64(n.tree_key);
+  h.u64(n.tree_identity_generation);
+  h.u32(n.node_index);
+  h.u64(n.generation);
+  h.u32(n.parent_index);
+  h.u64(n.parent_generation);
+  h.u64(n.node_key);
+  h.u64(n.tenant_key);
+  h.u64(n.binding_key);
+  const uint8_t kind = (uint8_t)n.kind;
+  h.update(&kind, 1);
+  hash_claim_fields(h, n.ceiling);
+  hash_claim_fields(h, n.claim);
+  h.u64(n.integrity);
+}
+
+int Leased::allocation_set(uint32_t state, glacier_hip_allocation_set_v2_t *out) {
+  // allocationSetCommitmentForState (:1253-1291): the raw bindings with
+  // their LeaseNode leaves, after the binding summary's checks
+  Summary sum;
+  if (int rc = binding_summary(state, &sum)) return rc;
+  gh::Sha256 h;
+  static const char dom[] = "glacier-paged-lease-allocation-set-v2";
+  h.update(dom, sizeof dom);
+  h.u64(0x47504C4100000002ull);  // allocation_set_abi (:29)
+  h.u64(instance);
+  h.u64(target.cache->root.cache_instance);
+  h.u64(binding_count);
+  hash_lease_node(h, scope);
+  for (uint32_t i = 0; i < binding_count; ++i) {
+    const Binding &b = bindings[i];
+    if (b.state == GLACIER_HIP_BINDING_FREE) continue;
+    h.u64(i);
+    h.u64(b.abi_version);
+    const uint8_t st = (uint8_t)b.state;
+    h.update(&st, 1);
+    h.u64(b.cache_instance);
+    h.u64(b.logical_page);
+    h.u64(b.payload_bytes);
+    h.u32(b.scope_index);
+    h.u64(b.scope_generation);
+    h.u64(b.integrity);
+    hash_lease_node(h, b.leaf);
+  }
+  memset(out, 0, sizeof *out);
+  out->abi_version = 0x47504C4100000002ull;
+  out->count = sum.count;
+  out->payload_bytes = sum.payload_bytes;
+  h.final(out->sha256);
+  return GLACIER_HIP_LEASE_OK;
+}
+
 int Leased::lifecycle(uint32_t *out) const {
   // lifecycle (:423-430)
   *out = reclaimed     ? GLACIER_HIP_LEASE_RECLAIMED
@@ -513,8 +579,8 @@ int Leased::seal_terminal(const Root &expected_root, const uint8_t kv[32], uint6
   return GLACIER_HIP_LEASE_OK;
 }
 
-int Leased::finalize_wave_terminal(uint64_t sequence, uint32_t token, const uint8_t proposal[32],
-                                   const uint8_t commit[32]) {
+int Leased::finalize_wave_terminal(uint64_t sequence, uint32_t reason, uint32_t token,
+                                   const uint8_t proposal[32], const uint8_t commit[32]) {
   if (int rc = validate_mutable()) return rc;
   if (has_row || lane_active) return GLACIER_HIP_LEASE_INVALID_LEASED_TRANSACTION;
   if (*this->sequence != sequence + 1) return GLACIER_HIP_LEASE_INVALID_TERMINAL_SEAL;
@@ -538,7 +604,7 @@ int Leased::finalize_wave_terminal(uint64_t sequence, uint32_t token, const uint
   memcpy(s.logical_kv_sha256, digest, 32);
   s.bindings = bs;
   s.transaction_sequence = sequence;
-  s.terminal_reason = GLACIER_HIP_TERMINAL_EOS;  // the wave binding carries a terminal flag
+  s.terminal_reason = reason;
   s.terminal_token = token;
   s.generation = next_generation++;
   memcpy(seal_proposal, proposal, 32);
@@ -782,6 +848,12 @@ int glacier_hip_leased_kv_abort_row(glacier_hip_leased_kv *c, const glacier_hip_
 int glacier_hip_leased_kv_binding_summary(glacier_hip_leased_kv *c, glacier_hip_binding_summary_t *out) {
   if (!c || !out) return GLACIER_HIP_LEASE_INVALID_ARGUMENT;
   return c->lease.binding_summary(GLACIER_HIP_BINDING_LIVE, out);
+}
+
+int glacier_hip_leased_kv_allocation_set(glacier_hip_leased_kv *c,
+                                         glacier_hip_allocation_set_v2_t *out) {
+  if (!c || !out) return GLACIER_HIP_LEASE_INVALID_ARGUMENT;
+  return c->lease.allocation_set(GLACIER_HIP_BINDING_LIVE, out);
 }
 
 int glacier_hip_leased_kv_lifecycle(glacier_hip_leased_kv *c, uint32_t *out) {

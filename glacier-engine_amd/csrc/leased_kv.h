@@ -77,6 +77,8 @@ class Leased {
   void orphan() { target.cache = nullptr; }  // the session that held the lane is gone
 
   int binding_summary(uint32_t state, Summary *out);
+  // allocationSetCommitmentForState (:1253-1291)
+  int allocation_set(uint32_t state, glacier_hip_allocation_set_v2_t *out);
   int lifecycle(uint32_t *out) const;
   int root(Root *out) const;
   int kv_sha256(uint8_t out[32]) { return target.kv_sha256(out); }
@@ -90,9 +92,9 @@ class Leased {
   // :759-808 + finalizeTerminalAssumePublished :810-850): after the wave's
   // permit for `sequence` committed, the seal binds the lane's committed
   // root, logical KV digest and bindings to the wave's proposal and commit
-  // digests.
-  int finalize_wave_terminal(uint64_t sequence, uint32_t token, const uint8_t proposal[32],
-                             const uint8_t commit[32]);
+  // digests, with the token's terminal reason.
+  int finalize_wave_terminal(uint64_t sequence, uint32_t reason, uint32_t token,
+                             const uint8_t proposal[32], const uint8_t commit[32]);
   int terminal_seal(glacier_hip_terminal_seal_t *out, uint8_t proposal[32], uint8_t commit[32]) const;
 
   Bank *bank = nullptr;

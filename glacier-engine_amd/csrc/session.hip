@@ -63,6 +63,10 @@ struct Lane {
   uint8_t chain[32] = {};
   bool retired = false;           // a terminal token was published
   glacier_hip_leased_kv *lease = nullptr;  // page payloads charged through a LeaseTree
+  // leased v3 waves (paged_lease_token_txn.zig): the lane's chain runs under
+  // the v3 domains and its publication slot is fixed by its first v3 wave
+  bool chain_v3 = false;
+  int v3_slot = -1;
 };
 
 // A staged publication wave between step_prepare and commit / abort.
@@ -76,6 +80,11 @@ struct PreparedWave {
   // (paged_lease_token_txn.zig: one Bank permit per B4 wave)
   glacier_hip_leased_kv *cohort = nullptr;
   glb::PubPermit permit{};
+  // a v3 wave (every lane a leased lane of the cohort): the proposal hashed,
+  // and each lane's terminal reason (0 none, 1 + TerminalReason)
+  bool v3 = false;
+  glacier_hip_token_proposal_v3_t proposal_v3{};
+  std::vector<uint32_t> reasons;
 };
 
 constexpr int kRow0Pages = 28;  // page ids of row 0 carried in the step inputs
@@ -1078,7 +1087,8 @@ void reset_lane(glacier_hip_session *s, Lane &ln, uint64_t seed) {
   ln.kv.start(s->pool);  // a new request: fresh cache instance, pages back to the pool
   ln.sampling_calls = 0;
   ln.prompt_len = 0;
-  ln.first_pending = ln.chain_init = ln.retired = false;
+  ln.first_pending = ln.chain_init = ln.retired = ln.chain_v3 = false;
+  ln.v3_slot = -1;
   ln.first_token = 0;
   memset(ln.chain, 0, 32);
   // SplitMix64-seeded Xoshiro256 state (std.Random.DefaultPrng.init)
@@ -1450,14 +1460,16 @@ int run_prefill_chunk(glacier_hip_session *s, uint32_t lane, const uint32_t *tok
 // paged_kv_cache.zig:1532-1555) over the committed rows, K/V values widened to
 // f32 bit patterns: each committed page is copied once, then hashed in the
 // canonical layer / K-then-V / position order.
-int logical_kv_sha256(glacier_hip_session *s, uint32_t lane, uint8_t out[32]) {
+// `extra` = 1: the committed rows plus the lane's one staged row
+// (logicalKvTxnSha256 paged_kv_cache.zig, the canonical digest after a row).
+int logical_kv_sha256(glacier_hip_session *s, uint32_t lane, uint8_t out[32], uint64_t extra = 0) {
   const auto &c = s->model->cfg;
   const Lane &ln = s->lanes[lane];
   glacier_hip_context *ctx = s->model->ctx;
   const size_t kvd = (size_t)c.num_kv_heads * c.head_dim, L = c.num_layers;
   const size_t elem = s->opt.kv_dtype == GLACIER_HIP_F16 ? 2 : 4;
   const size_t page_elems = L * 2 * 16 * kvd;
-  const uint64_t len = ln.kv.len, pages = (len + 15) / 16;
+  const uint64_t len = ln.kv.len + extra, pages = (len + 15) / 16;
   std::vector<uint8_t> raw(pages * page_elems * elem);
   for (uint64_t p = 0; p < pages; ++p) {
     const int32_t phys = ln.kv.page_of[p];
@@ -2155,10 +2167,6 @@ int glacier_hip_session_restore_checkpoint(glacier_hip_session *s, uint32_t lane
 
 }  // extern "C"
 
-extern "C" {
-
-}  // extern "C"
-
 // abortPublication of a staged wave's permit (the sequence stays for the retry)
 static void release_permit(PreparedWave &P) {
   if (!P.cohort) return;
@@ -2166,25 +2174,76 @@ static void release_permit(PreparedWave &P) {
   P.cohort = nullptr;
 }
 
-extern "C" {
+// Leased lanes of the cohort `c` in this session (lanes whose coordinator
+// shares its bank, tree and publication sequence).
+static bool same_cohort(const glb::Leased &a, const glb::Leased &b) {
+  return a.bank == b.bank && a.tree == b.tree && a.sequence == b.sequence &&
+         a.request_epoch == b.request_epoch && a.session_id == b.session_id;
+}
 
-int glacier_hip_session_step_prepare(glacier_hip_session *s, const uint32_t *lanes,
-                                     const uint32_t *tokens, uint32_t count,
-                                     const uint64_t *eligible_words_host,
-                                     const glacier_hip_publication_binding_t *binding,
-                                     glacier_hip_token_proposal_v1_t *proposal_out,
-                                     uint8_t proposal_sha256_out[32], uint32_t *next_tokens,
-                                     float *logits_host) {
-  // Batch.begin's lane validation and proposal (paged_token_txn.zig:346-471,
-  // validateAndBuildLane :832-944, rootTransition :813-872)
-  if (!s || !lanes || !binding || !proposal_out || !proposal_sha256_out || !next_tokens)
-    return GLACIER_HIP_INVALID_ARGUMENT;
+// A v3 resource commitment's default slot (ResourceCommitmentV3 .{}, :141-160).
+static void empty_resource_v3(glacier_hip_resource_commitment_v3_t &r, uint32_t slot) {
+  memset(&r, 0, sizeof r);
+  r.abi_version = gpub::kResourceCommitmentAbi;
+  r.lane_index = slot;
+  r.lifecycle = GLACIER_HIP_LIFECYCLE_RECLAIMED;
+  r.allocation_set.abi_version = gpub::kAllocationSetAbi;
+}
+
+// collectResourceSnapshot's commitment of a cohort lane that is not in the
+// wave because an earlier wave published its terminal token (:834-860): its
+// sealed root and digest while its pages stay charged, the seal's root only
+// once they are reclaimed.
+static int retired_resource_v3(const Lane &ln, glacier_hip_leased_kv *l, uint32_t slot,
+                               glacier_hip_resource_commitment_v3_t &r) {
+  glb::Leased &a = l->lease;
+  empty_resource_v3(r, slot);
+  uint32_t life = 0;
+  if (a.lifecycle(&life)) return GLACIER_HIP_INVALID_TRANSACTION;
+  r.lifecycle = life;
+  r.coordinator_instance = a.instance;
+  r.cache_instance = ln.kv.root.cache_instance;
+  r.scope_index = a.scope.node_index;
+  r.scope_generation = a.scope.generation;
+  memcpy(r.kv_state_chain_after, ln.chain, 32);
+  glacier_hip_terminal_seal_t seal;
+  const bool sealed = a.terminal_seal(&seal, nullptr, nullptr) == GLACIER_HIP_LEASE_OK;
+  if (life == GLACIER_HIP_LIFECYCLE_TERMINAL_RETAINED) {
+    if (!sealed) return GLACIER_HIP_INVALID_TRANSACTION;
+    r.root = seal.root;
+    r.has_canonical_after = 1;
+    memcpy(r.canonical_after_sha256, seal.logical_kv_sha256, 32);
+    r.has_binding_summary = 1;
+    if (a.binding_summary(GLACIER_HIP_BINDING_LIVE, &r.binding_summary) ||
+        a.allocation_set(GLACIER_HIP_BINDING_LIVE, &r.allocation_set) ||
+        memcmp(&r.binding_summary, &seal.bindings, sizeof seal.bindings) != 0)
+      return GLACIER_HIP_INVALID_TRANSACTION;
+  } else if (life == GLACIER_HIP_LIFECYCLE_RECLAIMED) {
+    if (sealed) r.root = seal.root;
+  } else {
+    return GLACIER_HIP_INVALID_TRANSACTION;  // live without a wave, or mid-reclaim
+  }
+  return GLACIER_HIP_OK;
+}
+
+// Batch.begin (paged_token_txn.zig:346-471 for v1 waves,
+// paged_lease_token_txn.zig:1117-1250 for v3 waves): validate the lanes, run
+// the wave's device step privately, take the cohort's publication permit and
+// seal the proposal into s->prep.
+static int step_prepare_impl(glacier_hip_session *s, const uint32_t *lanes, const uint32_t *tokens,
+                             uint32_t count, const uint64_t *eligible_words_host,
+                             const glacier_hip_publication_binding_t *binding, bool v3,
+                             const uint32_t *terminal_reason, uint32_t *next_tokens,
+                             float *logits_host) {
+  if (!s || !lanes || !binding || !next_tokens) return GLACIER_HIP_INVALID_ARGUMENT;
   if (count == 0 || count > GLACIER_HIP_PUBLICATION_WIDTH || count > s->lanes.size())
     return GLACIER_HIP_SHAPE_MISMATCH;
   const auto &c = s->model->cfg;
   uint32_t mask = 0;
   int first = -1;
+  glacier_hip_leased_kv *cohort = nullptr;
   for (uint32_t i = 0; i < count; ++i) {
+    // validateAndBuildLane's checks (:832-944; v3 :663-733)
     if (lanes[i] >= s->lanes.size() || !s->lanes[lanes[i]].kv.active) return GLACIER_HIP_INVALID_ARGUMENT;
     for (uint32_t j = 0; j < i; ++j)
       if (lanes[j] == lanes[i]) return GLACIER_HIP_INVALID_ARGUMENT;
@@ -2202,6 +2261,34 @@ int glacier_hip_session_step_prepare(glacier_hip_session *s, const uint32_t *lan
       if (ln.kv.len + 1 > s->opt.max_positions) return GLACIER_HIP_CACHE_FULL;
       if (ln.kv.len + 1 != ln.prompt_len + ln.output.size()) return GLACIER_HIP_INVALID_TRANSACTION;
     }
+    // a lane's chain runs under one ABI's domains for its whole request
+    if (ln.chain_init && ln.chain_v3 != v3) return GLACIER_HIP_INVALID_TRANSACTION;
+    // leased lanes publish under their cohort's permit for the binding's
+    // sequence: every leased lane of the wave shares one bank, tree and
+    // sequence cell, and the permit generation goes into the proposal
+    if (ln.lease) {
+      if (cohort && !same_cohort(ln.lease->lease, cohort->lease)) return GLACIER_HIP_INVALID_ARGUMENT;
+      if (!cohort) cohort = ln.lease;
+    } else if (v3) {
+      return GLACIER_HIP_INVALID_ARGUMENT;  // v3 waves publish leased lanes only
+    }
+    if (v3) {
+      if (ln.v3_slot >= 0 && (uint32_t)ln.v3_slot != slot) return GLACIER_HIP_INVALID_ARGUMENT;
+      if (terminal_reason && terminal_reason[i] > 1 + GLACIER_HIP_TERMINAL_CANCELLED)
+        return GLACIER_HIP_INVALID_ARGUMENT;
+    }
+  }
+  if (v3) {
+    // the cohort's slots are fixed, and every cohort lane that is not
+    // retired joins every wave (Batch.begin's activeMask rule, :1127-1131)
+    for (uint32_t l = 0; l < s->lanes.size(); ++l) {
+      const Lane &o = s->lanes[l];
+      if (!o.lease || !same_cohort(o.lease->lease, cohort->lease) || o.v3_slot < 0) continue;
+      const bool in_wave = std::find(lanes, lanes + count, l) != lanes + count;
+      if (in_wave) continue;
+      if (mask >> o.v3_slot & 1) return GLACIER_HIP_INVALID_ARGUMENT;  // slot of another lane
+      if (!o.retired) return GLACIER_HIP_INVALID_TRANSACTION;
+    }
   }
   GH_SUBMISSION(s->model->ctx);
   if (s->prep.active) return GLACIER_HIP_TRANSACTION_ACTIVE;
@@ -2212,6 +2299,11 @@ int glacier_hip_session_step_prepare(glacier_hip_session *s, const uint32_t *lan
   P.tokens.assign(count, 0);
   P.first = first == 1;
   P.elig = eligible_words_host != nullptr;
+  P.v3 = v3;
+  P.reasons.assign(count, 0);
+  for (uint32_t i = 0; i < count; ++i)
+    P.reasons[i] = v3 ? (terminal_reason ? terminal_reason[i] : 0)
+                      : (binding->terminal[i] ? 1 + GLACIER_HIP_TERMINAL_EOS : 0);
   std::vector<std::array<uint8_t, 32>> digests;
   if (!P.first) {
     int rc = run_step(s, lanes, tokens, count, true, eligible_words_host, logits_host, P.txns);
@@ -2225,33 +2317,29 @@ int glacier_hip_session_step_prepare(glacier_hip_session *s, const uint32_t *lan
   } else {
     for (uint32_t i = 0; i < count; ++i) P.tokens[i] = s->lanes[lanes[i]].first_token;
   }
-  // leased lanes publish under their cohort's permit for the binding's
-  // sequence: every leased lane of the wave shares one bank, tree and
-  // sequence cell, and the permit generation goes into the proposal
+  auto fail = [&](int rc) {
+    if (!P.first) abort_rows(s, P.txns);
+    release_permit(P);
+    return rc;
+  };
   P.cohort = nullptr;
-  for (uint32_t i = 0; i < count; ++i) {
-    glacier_hip_leased_kv *l = s->lanes[lanes[i]].lease;
-    if (!l) continue;
-    const glb::Leased &a = l->lease;
-    if (P.cohort) {
-      const glb::Leased &b = P.cohort->lease;
-      if (a.bank != b.bank || a.tree != b.tree || a.sequence != b.sequence ||
-          a.request_epoch != b.request_epoch || a.session_id != b.session_id) {
-        if (!P.first) abort_rows(s, P.txns);
-        return GLACIER_HIP_INVALID_ARGUMENT;
-      }
-    } else {
-      P.cohort = l;
+  if (cohort) {
+    glb::Leased &a = cohort->lease;
+    if (binding->transaction_sequence != *a.sequence || binding->request_epoch != a.request_epoch)
+      return fail(GLACIER_HIP_INVALID_TRANSACTION);
+    if (v3) {
+      // collectResourceSnapshot's tree checks (:765-776): a live tree whose
+      // parent is the session's receipt and which charges KV bytes only
+      glb::Claim other = a.tree->ceiling, cur = a.tree->current;
+      other.kv_bytes = cur.kv_bytes = 0;
+      if (a.bank->validate_tree(*a.tree) != GLACIER_HIP_LEASE_OK ||
+          memcmp(&a.tree->parent, &binding->receipt, sizeof binding->receipt) != 0 ||
+          !glb::claim_zero(other) || !glb::claim_zero(cur))
+        return fail(GLACIER_HIP_INVALID_TRANSACTION);
     }
-  }
-  if (P.cohort) {
-    glb::Leased &a = P.cohort->lease;
-    if (binding->transaction_sequence != *a.sequence || binding->request_epoch != a.request_epoch ||
-        a.bank->begin_publication(*a.tree, a.request_epoch, a.session_id, *a.sequence, &P.permit)) {
-      if (!P.first) abort_rows(s, P.txns);
-      P.cohort = nullptr;
-      return GLACIER_HIP_INVALID_TRANSACTION;
-    }
+    if (a.bank->begin_publication(*a.tree, a.request_epoch, a.session_id, *a.sequence, &P.permit))
+      return fail(GLACIER_HIP_INVALID_TRANSACTION);
+    P.cohort = cohort;
   }
   glacier_hip_token_proposal_v1_t &pr = P.proposal;
   gpub::empty_proposal(pr);
@@ -2264,6 +2352,7 @@ int glacier_hip_session_step_prepare(glacier_hip_session *s, const uint32_t *lan
   pr.live_lane_count = count;
   pr.kv_capacity_bytes = binding->kv_capacity_bytes;
   pr.receipt = binding->receipt;
+  std::vector<std::array<uint8_t, 32>> canonical(count);
   for (uint32_t i = 0; i < count; ++i) {
     Lane &ln = s->lanes[lanes[i]];
     glacier_hip_lane_proposal_v1_t &lp = pr.lanes[P.slots[i]];
@@ -2272,23 +2361,27 @@ int glacier_hip_session_step_prepare(glacier_hip_session *s, const uint32_t *lan
     lp.step_index = ln.output.size();
     lp.prompt_len = ln.prompt_len;
     lp.kv_capacity_bytes = lane_capacity_bytes(s);
-    if (P.first) {  // initialRootTransition (:790-811)
-      uint8_t kv_sha[32];
-      int rc = logical_kv_sha256(s, lanes[i], kv_sha);
-      if (rc) {
-        release_permit(P);
-        return rc;
-      }
+    // the canonical logical-KV digest after the wave's row: a first wave's
+    // committed rows, a terminal row's committed rows plus its staged row
+    // (prepareTokenRow's require_canonical_after, :579-625)
+    if (P.first || (v3 && P.reasons[i])) {
+      if (int rc = logical_kv_sha256(s, lanes[i], canonical[i].data(), P.first ? 0 : 1))
+        return fail(rc);
+    }
+    if (P.first) {  // initialRootTransition (:790-811; v3 :579-606)
       const glacier_hip_page_map_root_t &r = ln.kv.root;
       lp.has_kv_transition = 0;
       lp.kv_before = lp.kv_after = ln.kv.len;
       t.cache_instance = r.cache_instance;
       copy_root(r, t, true);
       copy_root(r, t, false);
-      memcpy(t.initial_logical_kv_sha256, kv_sha, 32);
-      gpub::initial_state_chain(kv_sha, r, t.state_chain_before);
+      memcpy(t.initial_logical_kv_sha256, canonical[i].data(), 32);
+      if (v3)
+        gpub::initial_state_chain_v3(canonical[i].data(), r, t.state_chain_before);
+      else
+        gpub::initial_state_chain(canonical[i].data(), r, t.state_chain_before);
       memcpy(t.state_chain_after, t.state_chain_before, 32);
-    } else {
+    } else {  // rootTransition (:813-872; v3 :608-661)
       const RowTxn &rt = P.txns[i];
       lp.has_kv_transition = 1;
       lp.kv_before = rt.mark.base_len;
@@ -2302,8 +2395,12 @@ int glacier_hip_session_step_prepare(glacier_hip_session *s, const uint32_t *lan
       t.installs_new_page = rt.installs ? 1 : 0;
       memcpy(t.row_payload_sha256, digests[i].data(), 32);
       memcpy(t.state_chain_before, ln.chain, 32);
-      gpub::appended_state_chain(ln.chain, rt.before, rt.after, rt.mark, digests[i].data(),
-                                 t.state_chain_after);
+      if (v3)
+        gpub::appended_state_chain_v3(ln.chain, rt.before, rt.after, rt.mark, digests[i].data(),
+                                      t.state_chain_after);
+      else
+        gpub::appended_state_chain(ln.chain, rt.before, rt.after, rt.mark, digests[i].data(),
+                                   t.state_chain_after);
     }
     lp.output_before = ln.output.size();
     lp.output_after = ln.output.size() + 1;
@@ -2314,13 +2411,147 @@ int glacier_hip_session_step_prepare(glacier_hip_session *s, const uint32_t *lan
     // posthead branch does not (:5574-5598); the first token is greedy
     lp.sampling_calls_after = ln.sampling_calls + ((P.first || !P.elig) ? 1 : 0);
     lp.token_id = P.tokens[i];
-    lp.terminal = binding->terminal[i] ? 1 : 0;
+    lp.terminal = P.reasons[i] ? 1 : 0;
   }
-  gpub::proposal_sha256(pr, P.sha);
+  if (!v3) {
+    gpub::proposal_sha256(pr, P.sha);
+  } else {
+    // ProposalV3 (:162-180): the v1 lanes' fields plus each lane's output
+    // digest and terminal reason, the redacted tree commitment and one
+    // resource commitment per slot (collectResourceSnapshot :765-896)
+    glacier_hip_token_proposal_v3_t &q = P.proposal_v3;
+    memset(&q, 0, sizeof q);
+    q.abi_version = gpub::kProposalV3Abi;
+    q.resource_bank_abi = gpub::kResourceBankAbi;
+    q.resource_lease_tree_abi = gpub::kLeaseTreeAbi;
+    q.resource_publication_fence_abi = gpub::kPublicationFenceAbi;
+    q.leased_paged_kv_abi = gpub::kLeasedPagedKvAbi;
+    q.paged_kv_abi = gpk::kPagedKvAbi;
+    q.page_transition_abi = gpub::kPageTransitionV3Abi;
+    q.execution_abi = pr.execution_abi;
+    q.request_epoch = pr.request_epoch;
+    q.transaction_sequence = pr.transaction_sequence;
+    q.resource_permit_generation = pr.resource_permit_generation;
+    q.live_mask = mask;
+    q.live_lane_count = count;
+    q.parent_receipt = binding->receipt;
+    const glacier_hip_lease_tree_t &tree = *P.cohort->lease.tree;  // treeCommitment (:751-763)
+    q.tree.abi_version = gpub::kTreeCommitmentAbi;
+    q.tree.tree_key = tree.tree_key;
+    q.tree.identity_generation = tree.identity_generation;
+    q.tree.generation = tree.generation;
+    q.tree.structural_revision = tree.structural_revision;
+    q.tree.ceiling = tree.ceiling;
+    q.tree.current = tree.current;
+    q.tree.active_nodes = tree.active_nodes;
+    q.tree.state_digest = tree.state_digest;
+    q.tree.token_integrity = tree.integrity;
+    for (uint32_t l = 0; l < GLACIER_HIP_PUBLICATION_WIDTH; ++l) {
+      empty_resource_v3(q.resources[l], l);
+      glacier_hip_lane_proposal_v3_t &d = q.lanes[l];
+      const glacier_hip_lane_proposal_v1_t &sl = pr.lanes[l];
+      d.lane_index = sl.lane_index;
+      d.has_kv_transition = sl.has_kv_transition;
+      d.step_index = sl.step_index;
+      d.prompt_len = sl.prompt_len;
+      d.kv_before = sl.kv_before;
+      d.kv_after = sl.kv_after;
+      d.kv_transition = sl.kv_transition;
+      d.kv_transition.abi_version = gpub::kPageTransitionV3Abi;
+      d.output_before = sl.output_before;
+      d.output_after = sl.output_after;
+      memcpy(d.rng_before, sl.rng_before, sizeof d.rng_before);
+      memcpy(d.rng_after, sl.rng_after, sizeof d.rng_after);
+      d.sampling_calls_before = sl.sampling_calls_before;
+      d.sampling_calls_after = sl.sampling_calls_after;
+      d.token_id = sl.token_id;
+    }
+    for (uint32_t i = 0; i < count; ++i) {
+      Lane &ln = s->lanes[lanes[i]];
+      glb::Leased &a = ln.lease->lease;
+      const uint32_t slot = P.slots[i];
+      glacier_hip_lane_proposal_v3_t &d = q.lanes[slot];
+      d.terminal_reason = P.reasons[i];
+      {  // outputAfterSha256 (:566-577): the output with this token appended
+        std::vector<uint32_t> out(ln.output);
+        out.push_back(P.tokens[i]);
+        gh::token_sequence_sha256(out.data(), out.size(), d.output_sha256);
+      }
+      glacier_hip_resource_commitment_v3_t &r = q.resources[slot];
+      uint32_t life = 0;
+      if (a.lifecycle(&life) || life != GLACIER_HIP_LIFECYCLE_LIVE) return fail(GLACIER_HIP_INVALID_TRANSACTION);
+      r.lifecycle = life;
+      r.coordinator_instance = a.instance;
+      r.cache_instance = ln.kv.root.cache_instance;
+      r.scope_index = a.scope.node_index;
+      r.scope_generation = a.scope.generation;
+      r.root = P.first ? ln.kv.root : P.txns[i].after;
+      memcpy(r.kv_state_chain_after, d.kv_transition.state_chain_after, 32);
+      if (P.first || P.reasons[i]) {
+        r.has_canonical_after = 1;
+        memcpy(r.canonical_after_sha256, canonical[i].data(), 32);
+      }
+      if (P.reasons[i]) {
+        // the generation the lane's terminal seal takes (TerminalPlanV3)
+        r.has_terminal_generation = 1;
+        r.terminal_generation = a.next_generation;
+      }
+      r.has_binding_summary = 1;
+      if (a.binding_summary(GLACIER_HIP_BINDING_LIVE, &r.binding_summary) ||
+          a.allocation_set(GLACIER_HIP_BINDING_LIVE, &r.allocation_set))
+        return fail(GLACIER_HIP_INVALID_TRANSACTION);
+    }
+    for (uint32_t l = 0; l < s->lanes.size(); ++l) {  // retired cohort lanes
+      const Lane &o = s->lanes[l];
+      if (!o.lease || !same_cohort(o.lease->lease, P.cohort->lease) || o.v3_slot < 0 || !o.retired)
+        continue;
+      if (int rc = retired_resource_v3(o, o.lease, (uint32_t)o.v3_slot, q.resources[o.v3_slot]))
+        return fail(rc);
+    }
+    for (const auto &r : q.resources) {  // the snapshot's cross-checks (:862-882)
+      if (r.has_binding_summary != (r.allocation_set.count != 0) ||
+          (r.has_binding_summary && (r.binding_summary.count != r.allocation_set.count ||
+                                     r.binding_summary.payload_bytes != r.allocation_set.payload_bytes)))
+        return fail(GLACIER_HIP_INVALID_TRANSACTION);
+    }
+    gpub::proposal_v3_sha256(q, P.sha);
+  }
   P.active = true;
-  *proposal_out = pr;
-  memcpy(proposal_sha256_out, P.sha, 32);
   for (uint32_t i = 0; i < count; ++i) next_tokens[i] = P.tokens[i];
+  return GLACIER_HIP_OK;
+}
+
+extern "C" {
+
+int glacier_hip_session_step_prepare(glacier_hip_session *s, const uint32_t *lanes,
+                                     const uint32_t *tokens, uint32_t count,
+                                     const uint64_t *eligible_words_host,
+                                     const glacier_hip_publication_binding_t *binding,
+                                     glacier_hip_token_proposal_v1_t *proposal_out,
+                                     uint8_t proposal_sha256_out[32], uint32_t *next_tokens,
+                                     float *logits_host) {
+  if (!proposal_out || !proposal_sha256_out) return GLACIER_HIP_INVALID_ARGUMENT;
+  const int rc = step_prepare_impl(s, lanes, tokens, count, eligible_words_host, binding, false,
+                                   nullptr, next_tokens, logits_host);
+  if (rc) return rc;
+  *proposal_out = s->prep.proposal;
+  memcpy(proposal_sha256_out, s->prep.sha, 32);
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_session_step_prepare_v3(glacier_hip_session *s, const uint32_t *lanes,
+                                        const uint32_t *tokens, uint32_t count,
+                                        const uint64_t *eligible_words_host,
+                                        const glacier_hip_publication_binding_t *binding,
+                                        const uint32_t *terminal_reason,
+                                        glacier_hip_token_proposal_v3_t *proposal_out,
+                                        uint8_t proposal_sha256_out[32], uint32_t *next_tokens) {
+  if (!proposal_out || !proposal_sha256_out) return GLACIER_HIP_INVALID_ARGUMENT;
+  const int rc = step_prepare_impl(s, lanes, tokens, count, eligible_words_host, binding, true,
+                                   terminal_reason, next_tokens, nullptr);
+  if (rc) return rc;
+  *proposal_out = s->prep.proposal_v3;
+  memcpy(proposal_sha256_out, s->prep.sha, 32);
   return GLACIER_HIP_OK;
 }
 
@@ -2343,8 +2574,9 @@ int glacier_hip_session_step_commit(glacier_hip_session *s, const glacier_hip_pr
   GH_SUBMISSION(s->model->ctx);
   PreparedWave &P = s->prep;
   if (!P.active) return GLACIER_HIP_INVALID_TRANSACTION;
-  if (ack->abi_version != gpub::kPrepareAckAbi || ack->sink_epoch == 0 ||
-      ack->reservation_id == 0 || memcmp(ack->proposal_sha256, P.sha, 32) != 0) {
+  if (ack->abi_version != (P.v3 ? gpub::kPrepareAckV3Abi : gpub::kPrepareAckAbi) ||
+      ack->sink_epoch == 0 || ack->reservation_id == 0 ||
+      memcmp(ack->proposal_sha256, P.sha, 32) != 0) {
     if (!P.first) abort_rows(s, P.txns);
     release_permit(P);
     P.active = false;
@@ -2358,6 +2590,19 @@ int glacier_hip_session_step_commit(glacier_hip_session *s, const glacier_hip_pr
     P.active = false;
     s->model->ctx->last_error = "the wave's publication permit is no longer the bank's live permit";
     return GLACIER_HIP_INVALID_TRANSACTION;
+  }
+  if (P.v3) {  // each terminal lane's seal still takes the generation the proposal names
+    for (size_t i = 0; i < P.lanes.size(); ++i) {
+      const glacier_hip_resource_commitment_v3_t &r = P.proposal_v3.resources[P.slots[i]];
+      const glacier_hip_leased_kv *l = s->lanes[P.lanes[i]].lease;
+      if (r.has_terminal_generation && (!l || l->lease.next_generation != r.terminal_generation)) {
+        if (!P.first) abort_rows(s, P.txns);
+        release_permit(P);
+        P.active = false;
+        s->model->ctx->last_error = "a terminal lane's coordinator moved after the wave was proposed";
+        return GLACIER_HIP_INVALID_TRANSACTION;
+      }
+    }
   }
   if (!P.first) {
     const int rc = commit_rows(s, P.txns);  // staged under the session's rule: cannot fail
@@ -2375,11 +2620,16 @@ int glacier_hip_session_step_commit(glacier_hip_session *s, const glacier_hip_pr
     ln.output.push_back(lp.token_id);
     memcpy(ln.chain, lp.kv_transition.state_chain_after, 32);
     ln.chain_init = true;
+    ln.chain_v3 = P.v3;
+    if (P.v3) ln.v3_slot = (int)P.slots[i];
     ln.first_pending = false;
     if (lp.terminal) ln.retired = true;
   }
   uint8_t commit_sha[32];
-  gpub::commit_sha256(P.sha, *ack, commit_sha);
+  if (P.v3)
+    gpub::commit_v3_sha256(P.sha, *ack, commit_sha);
+  else
+    gpub::commit_sha256(P.sha, *ack, commit_sha);
   int status = GLACIER_HIP_OK;
   if (P.cohort) {
     // the wave's permit commits once (the cohort's sequence advances), then
@@ -2398,7 +2648,8 @@ int glacier_hip_session_step_commit(glacier_hip_session *s, const glacier_hip_pr
       const glacier_hip_lane_proposal_v1_t &lp = P.proposal.lanes[P.slots[i]];
       glacier_hip_leased_kv *l = s->lanes[P.lanes[i]].lease;
       if (l && lp.terminal && status == GLACIER_HIP_OK &&
-          l->lease.finalize_wave_terminal(P.permit.sequence, lp.token_id, P.sha, commit_sha) !=
+          l->lease.finalize_wave_terminal(P.permit.sequence, P.reasons[i] - 1, lp.token_id, P.sha,
+                                          commit_sha) !=
               GLACIER_HIP_LEASE_OK) {
         status = GLACIER_HIP_SCHEDULER_POISONED;
         s->model->ctx->last_error = "a published terminal token's lane could not be sealed";
@@ -2408,7 +2659,7 @@ int glacier_hip_session_step_commit(glacier_hip_session *s, const glacier_hip_pr
   }
   if (receipt_out) {
     memset(receipt_out, 0, sizeof *receipt_out);
-    receipt_out->abi_version = gpub::kCommitReceiptAbi;
+    receipt_out->abi_version = P.v3 ? gpub::kCommitReceiptV3Abi : gpub::kCommitReceiptAbi;
     memcpy(receipt_out->proposal_sha256, P.sha, 32);
     receipt_out->prepare_ack = *ack;
     memcpy(receipt_out->commit_sha256, commit_sha, 32);

@@ -387,6 +387,57 @@ class PublicationBinding(C.Structure):
 
 
 PREPARE_ACK_ABI = 0x4750544100000001
+PREPARE_ACK_V3_ABI = 0x47504C4100000003
+LIFECYCLE_LIVE, LIFECYCLE_TERMINAL_RETAINED, LIFECYCLE_FREED_PENDING_UNCHARGE, \
+    LIFECYCLE_RECLAIMED = 0, 1, 2, 3
+TERMINAL_EOS, TERMINAL_MAX_TOKENS, TERMINAL_CANCELLED = 0, 1, 2
+
+
+class AllocationSet(C.Structure):
+    _fields_ = [("abi_version", C.c_uint64), ("count", C.c_uint32), ("reserved", C.c_uint32),
+                ("payload_bytes", C.c_uint64), ("sha256", C.c_uint8 * 32)]
+
+
+class LeaseTreeCommitment(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in ("abi_version", "tree_key", "identity_generation",
+                                          "generation", "structural_revision")] + \
+        [("ceiling", Claim), ("current", Claim), ("active_nodes", C.c_uint32),
+         ("reserved", C.c_uint32), ("state_digest", C.c_uint64), ("token_integrity", C.c_uint64)]
+
+
+class ResourceCommitment(C.Structure):
+    _fields_ = [("abi_version", C.c_uint64), ("lane_index", C.c_uint32), ("lifecycle", C.c_uint32),
+                ("coordinator_instance", C.c_uint64), ("cache_instance", C.c_uint64),
+                ("scope_index", C.c_uint32), ("reserved0", C.c_uint32),
+                ("scope_generation", C.c_uint64), ("root", PageMapRoot),
+                ("kv_state_chain_after", C.c_uint8 * 32), ("has_canonical_after", C.c_uint32),
+                ("reserved1", C.c_uint32), ("canonical_after_sha256", C.c_uint8 * 32),
+                ("has_terminal_generation", C.c_uint32), ("reserved2", C.c_uint32),
+                ("terminal_generation", C.c_uint64), ("has_binding_summary", C.c_uint32),
+                ("reserved3", C.c_uint32), ("binding_summary", BindingSummary),
+                ("allocation_set", AllocationSet)]
+
+
+class LaneProposalV3(C.Structure):
+    _fields_ = [("lane_index", C.c_uint32), ("has_kv_transition", C.c_uint32)] + \
+        [(n, C.c_uint64) for n in ("step_index", "prompt_len", "kv_before", "kv_after")] + \
+        [("kv_transition", RootTransition), ("output_before", C.c_uint64),
+         ("output_after", C.c_uint64), ("output_sha256", C.c_uint8 * 32),
+         ("rng_before", C.c_uint64 * 4), ("rng_after", C.c_uint64 * 4),
+         ("sampling_calls_before", C.c_uint64), ("sampling_calls_after", C.c_uint64),
+         ("token_id", C.c_uint32), ("terminal_reason", C.c_uint32)]
+
+
+class TokenProposalV3(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in (
+        "abi_version", "resource_bank_abi", "resource_lease_tree_abi",
+        "resource_publication_fence_abi", "leased_paged_kv_abi", "paged_kv_abi",
+        "page_transition_abi", "execution_abi", "request_epoch", "transaction_sequence",
+        "resource_permit_generation")] + \
+        [("live_mask", C.c_uint32), ("live_lane_count", C.c_uint32),
+         ("parent_receipt", BankReceipt), ("tree", LeaseTreeCommitment),
+         ("resources", ResourceCommitment * PUBLICATION_WIDTH),
+         ("lanes", LaneProposalV3 * PUBLICATION_WIDTH)]
 
 
 class CommandToken(C.Structure):
@@ -587,6 +638,11 @@ _SIGS = [
     ("glacier_hip_token_proposal_sha256", C.c_int, [C.POINTER(TokenProposal), _P]),
     ("glacier_hip_token_commit_sha256", C.c_int, [_P, C.POINTER(PrepareAck), _P]),
     ("glacier_hip_token_sequence_sha256", C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p]),
+    ("glacier_hip_token_proposal_v3_sha256", C.c_int, [C.POINTER(TokenProposalV3), _P]),
+    ("glacier_hip_token_commit_v3_sha256", C.c_int, [_P, C.POINTER(PrepareAck), _P]),
+    ("glacier_hip_session_step_prepare_v3", C.c_int,
+     [_P, _P, _P, C.c_uint32, _P, C.POINTER(PublicationBinding), _P, C.POINTER(TokenProposalV3),
+      _P, _P]),
     ("glacier_hip_synth_int4", None, [C.c_uint64, C.c_uint64, _P, C.c_uint64]),
     ("glacier_hip_synth_scales_f16", None, [C.c_uint64, C.c_uint64, C.c_float, _P, C.c_uint64]),
     ("glacier_hip_synth_normal_f32", None, [C.c_uint64, C.c_uint64, C.c_float, _P, C.c_uint64]),
@@ -675,6 +731,7 @@ _SIGS = [
     ("glacier_hip_leased_kv_abort_row", C.c_int, [_P, C.POINTER(LeasedRowTxn)]),
     ("glacier_hip_leased_kv_binding_summary", C.c_int, [_P, C.POINTER(BindingSummary)]),
     ("glacier_hip_leased_kv_lifecycle", C.c_int, [_P, C.POINTER(C.c_uint32)]),
+    ("glacier_hip_leased_kv_allocation_set", C.c_int, [_P, C.POINTER(AllocationSet)]),
     ("glacier_hip_leased_kv_root", C.c_int, [_P, C.POINTER(PageMapRoot)]),
     ("glacier_hip_leased_kv_kv_sha256", C.c_int, [_P, _P]),
     ("glacier_hip_leased_kv_seal_terminal", C.c_int,
@@ -1084,6 +1141,24 @@ class Session:
                                                     sha, ptr(nxt), None)
         return rc, prop, bytes(sha), nxt
 
+    def step_prepare_v3(self, lanes, tokens, binding, terminal_reason=None, eligible=None):
+        """A wave of leased lanes of one cohort sealed as ProposalV3.
+        terminal_reason[i]: 0, or 1 + TERMINAL_* of lane i's token. Returns
+        (rc, proposal, proposal_sha256 bytes, next tokens)."""
+        lanes = np.ascontiguousarray(lanes, dtype=np.uint32)
+        toks = np.ascontiguousarray(tokens if tokens is not None else np.zeros(lanes.size),
+                                    dtype=np.uint32)
+        reasons = None if terminal_reason is None else \
+            np.ascontiguousarray(terminal_reason, dtype=np.uint32)
+        nxt = np.zeros(lanes.size, dtype=np.uint32)
+        el = None if eligible is None else np.ascontiguousarray(eligible, dtype=np.uint64)
+        prop = TokenProposalV3()
+        sha = (C.c_uint8 * 32)()
+        rc = lib().glacier_hip_session_step_prepare_v3(self.h, ptr(lanes), ptr(toks), lanes.size,
+                                                       ptr(el), C.byref(binding), ptr(reasons),
+                                                       C.byref(prop), sha, ptr(nxt))
+        return rc, prop, bytes(sha), nxt
+
     def step_commit(self, ack):
         rec = CommitReceipt()
         rc = lib().glacier_hip_session_step_commit(self.h, C.byref(ack), C.byref(rec))
@@ -1489,6 +1564,7 @@ class LeasedKV:
     def __init__(self, bank, tree, scope, target, request_epoch, session_id, sequence, lane=None,
                  binding_count=None):
         self.bank, self.tree, self.sequence, self.target = bank, tree, sequence, target
+        self.scope = scope
         n = binding_count if binding_count is not None else target.page_count()
         self.bindings = (PageLeaseBinding * max(n, 1))()
         self.h = _P()
@@ -1533,6 +1609,12 @@ class LeasedKV:
         lease_check(lib().glacier_hip_leased_kv_binding_summary(self.h, C.byref(s)),
                     "binding_summary")
         return s
+
+    def allocation_set(self):
+        a = AllocationSet()
+        lease_check(lib().glacier_hip_leased_kv_allocation_set(self.h, C.byref(a)),
+                    "allocation_set")
+        return a
 
     def lifecycle(self):
         v = C.c_uint32()

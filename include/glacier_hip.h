@@ -1355,6 +1355,95 @@ typedef struct {
     uint8_t digest[32];
 } glacier_hip_binding_summary_t;     /* BindingSummaryV1 (:74-78) */
 
+/* ---- leased publication waves: ProposalV3 (paged_lease_token_txn.zig) ----
+ * A staged wave over leased lanes hashes the v3 proposal: the v1 head minus
+ * the capacity word plus the LeaseTree and leased-KV ABIs, the cohort's
+ * parent receipt, a redacted commitment to the cohort's tree, one resource
+ * commitment per lane slot (lifecycle, coordinator and cache instances,
+ * scope, page-map root after the wave, KV state chain after, the canonical
+ * logical-KV digest after a first or terminal row, the terminal seal's
+ * generation, the lane's binding summary and allocation-set commitment) and
+ * LaneProposalV3 lanes (with the output digest after the token and the
+ * terminal reason). Leased lanes publishing v3 waves chain their KV state
+ * under the v3 domains. Layouts: the reference's fields in order, u8/bool
+ * widened to u32, the reference's widths hashed. */
+typedef struct {
+    uint64_t abi_version;            /* 0x47504c4100000002 */
+    uint32_t count, reserved;
+    uint64_t payload_bytes;
+    uint8_t sha256[32];
+} glacier_hip_allocation_set_v2_t;      /* AllocationSetCommitmentV2 (leased_paged_kv_cache.zig:85-90) */
+
+typedef struct {
+    uint64_t abi_version;            /* 0x47504c5400000003 */
+    uint64_t tree_key, identity_generation, generation, structural_revision;
+    glacier_hip_claim_t ceiling, current;
+    uint32_t active_nodes, reserved;
+    uint64_t state_digest, token_integrity;
+} glacier_hip_lease_tree_commitment_v3_t;  /* LeaseTreeCommitmentV3 (paged_lease_token_txn.zig:127-139) */
+
+enum { GLACIER_HIP_LIFECYCLE_LIVE = 0, GLACIER_HIP_LIFECYCLE_TERMINAL_RETAINED = 1,
+       GLACIER_HIP_LIFECYCLE_FREED_PENDING_UNCHARGE = 2, GLACIER_HIP_LIFECYCLE_RECLAIMED = 3 };
+
+typedef struct {
+    uint64_t abi_version;            /* 0x47504c4300000005 */
+    uint32_t lane_index, lifecycle;
+    uint64_t coordinator_instance, cache_instance;
+    uint32_t scope_index, reserved0;
+    uint64_t scope_generation;
+    glacier_hip_page_map_root_t root;
+    uint8_t kv_state_chain_after[32];
+    uint32_t has_canonical_after, reserved1;
+    uint8_t canonical_after_sha256[32];
+    uint32_t has_terminal_generation, reserved2;
+    uint64_t terminal_generation;
+    uint32_t has_binding_summary, reserved3;
+    glacier_hip_binding_summary_t binding_summary;
+    glacier_hip_allocation_set_v2_t allocation_set;
+} glacier_hip_resource_commitment_v3_t;  /* ResourceCommitmentV3 (:141-160) */
+
+typedef struct {
+    uint32_t lane_index, has_kv_transition;
+    uint64_t step_index, prompt_len, kv_before, kv_after;
+    glacier_hip_root_transition_v1_t kv_transition;  /* RootTransitionV3: the same fields */
+    uint64_t output_before, output_after;
+    uint8_t output_sha256[32];
+    uint64_t rng_before[4], rng_after[4];
+    uint64_t sampling_calls_before, sampling_calls_after;
+    uint32_t token_id;
+    uint32_t terminal_reason;        /* 0 none, 1 + TerminalReason */
+} glacier_hip_lane_proposal_v3_t;       /* LaneProposalV3 (:107-124) */
+
+typedef struct {
+    uint64_t abi_version;            /* 0x47504c5800000004 */
+    uint64_t resource_bank_abi, resource_lease_tree_abi, resource_publication_fence_abi;
+    uint64_t leased_paged_kv_abi, paged_kv_abi, page_transition_abi;
+    uint64_t execution_abi, request_epoch, transaction_sequence, resource_permit_generation;
+    uint32_t live_mask, live_lane_count;
+    glacier_hip_bank_receipt_t parent_receipt;
+    glacier_hip_lease_tree_commitment_v3_t tree;
+    glacier_hip_resource_commitment_v3_t resources[GLACIER_HIP_PUBLICATION_WIDTH];
+    glacier_hip_lane_proposal_v3_t lanes[GLACIER_HIP_PUBLICATION_WIDTH];
+} glacier_hip_token_proposal_v3_t;      /* ProposalV3 (:162-180) */
+
+/* proposalSha256 (:1013-1084) and commitSha256 (:1086-1098) of the v3 wave. */
+int glacier_hip_token_proposal_v3_sha256(const glacier_hip_token_proposal_v3_t *proposal,
+                                         uint8_t out[32]);
+int glacier_hip_token_commit_v3_sha256(const uint8_t proposal_sha256[32],
+                                       const glacier_hip_prepare_ack_v1_t *ack, uint8_t out[32]);
+/* step_prepare for a wave whose lanes are all leased lanes of one cohort,
+ * sealed as ProposalV3 (Batch.begin :1117-1250). terminal_reason[i]: 0, or
+ * 1 + the TerminalReason of lane i's token (eos / max_tokens / cancelled).
+ * The ack names the v3 digest; step_commit / step_abort finish the wave (the
+ * commit digest is commitSha256 v3, terminal seals bind both v3 digests). */
+int glacier_hip_session_step_prepare_v3(glacier_hip_session *s, const uint32_t *lanes,
+                                        const uint32_t *tokens, uint32_t count,
+                                        const uint64_t *eligible_words_host,
+                                        const glacier_hip_publication_binding_t *binding,
+                                        const uint32_t *terminal_reason,
+                                        glacier_hip_token_proposal_v3_t *proposal_out,
+                                        uint8_t proposal_sha256_out[32], uint32_t *next_tokens);
+
 typedef struct {
     uint64_t abi_version;        /* RowAllocationPlanV1 (paged_kv_cache.zig:113-128) */
     uint64_t cache_id, cache_instance, base_len, logical_page, row_in_page;
@@ -1454,6 +1543,11 @@ int glacier_hip_leased_kv_commit_row(glacier_hip_leased_kv *c, const glacier_hip
 int glacier_hip_leased_kv_abort_row(glacier_hip_leased_kv *c, const glacier_hip_leased_row_txn_t *txn);
 int glacier_hip_leased_kv_binding_summary(glacier_hip_leased_kv *c, glacier_hip_binding_summary_t *out);
 int glacier_hip_leased_kv_lifecycle(glacier_hip_leased_kv *c, uint32_t *out);
+/* allocationSetCommitment (:364-369, allocationSetCommitmentForState
+ * :1253-1291): the exact live allocation set, each non-free binding with its
+ * LeaseNode leaf, as AllocationSetCommitmentV2. */
+int glacier_hip_leased_kv_allocation_set(glacier_hip_leased_kv *c,
+                                         glacier_hip_allocation_set_v2_t *out);
 int glacier_hip_leased_kv_root(glacier_hip_leased_kv *c, glacier_hip_page_map_root_t *out);
 int glacier_hip_leased_kv_kv_sha256(glacier_hip_leased_kv *c, uint8_t out[32]);
 /* sealTerminalForPublication (:691-757): binds the committed root and

@@ -321,3 +321,188 @@ def test_coordinator_gone_mid_wave_aborts_the_wave(gh, model):
         lks[1].close()
     finally:
         sess.close()
+
+
+def _v3_binding(gh, parent, slots, seq):
+    b = _wave_binding(gh, slots, seq)
+    C.memmove(C.byref(b.receipt), C.byref(parent), C.sizeof(b.receipt))
+    return b
+
+
+def _ack3(gh, sha, rid):
+    return gh.PrepareAck(gh.PREPARE_ACK_V3_ABI, (C.c_uint8 * 32)(*sha), 0x50414745, rid)
+
+
+def _troot(opub, t, side):
+    return opub.root_bytes(getattr(t, f"root_{side}_generation"), getattr(t, f"root_{side}_len"),
+                           getattr(t, f"root_{side}_pages"),
+                           bytes(getattr(t, f"root_{side}_ownership_sha256")), t.cache_instance)
+
+
+def _rbytes(opub, r):
+    return opub.root_bytes(r.generation, r.committed_len, r.committed_pages,
+                           bytes(r.ownership_sha256), r.cache_instance)
+
+
+def test_leased_v3_waves_commit_tree_and_resources(gh, model):
+    """ProposalV3 (paged_lease_token_txn.zig:107-180, Batch.begin :1117-1250,
+    collectResourceSnapshot :765-896): each v3 wave's digest equals the
+    oracle's over the returned record; its tree commitment is the cohort
+    tree's redacted fields; each live lane's resource names its coordinator,
+    cache instance, scope, the page-map root and v3 KV chain after the wave,
+    the canonical logical-KV digest after a first or terminal row, the
+    terminal seal's generation, and its binding summary and allocation set
+    (equal to the coordinator's own and to the oracle's restatement over the
+    lane's sidecar); a terminal-retained lane is committed from its seal and
+    a reclaimed one by its seal's root. Slots are fixed, live lanes cannot
+    sit out, lanes chain under one ABI, and the v3 ack / commit digests are
+    the v3 ones."""
+    import oracle as ora
+    from oracle import publication as opub
+
+    V = TINY["vocab_size"]
+    sess = gh.Session(model, max_lanes=3, max_positions=MAXPOS, kv_dtype=gh.F16)
+    try:
+        bank = gh.LeaseBank(2, 16, 0x4C4C, kv_bytes=64 * PB, queue_slots=4)
+        parent = bank.commit(bank.reserve(1, queue_slots=1))
+        tree = bank.open_tree(parent, 2, 3, kv_bytes=16 * PB)
+        scopes = [bank.open_scope(tree, 4 + i, 5 + i, kv_bytes=PAGES * PB) for i in range(2)]
+        seq = C.c_uint64(0)
+        bank.bind_session(tree, 6, 0x5E55)
+        lks, outs = [], [[], []]
+        slots = [2, 0]  # lane 0 publishes in slot 2, lane 1 in slot 0
+        for lane in range(2):
+            sess.begin(lane, seed=lane)
+            lks.append(gh.LeasedKV(bank, tree, scopes[lane], sess, 6, 0x5E55, seq, lane=lane,
+                                   binding_count=PAGES))
+            sess.prefill_staged(lane, gh.synth_tokens(SEED, 30 + lane, V, 14))
+        sess.begin(2, seed=9)
+        sess.prefill_staged(2, gh.synth_tokens(SEED, 40, V, 5))
+        rc, *_ = sess.step_prepare_v3([2], None, _v3_binding(gh, parent, [1], 0))
+        assert rc == gh.INVALID_ARGUMENT  # v3 waves publish leased lanes only
+        bad = _v3_binding(gh, parent, slots, 0)
+        bad.receipt.integrity ^= 1
+        rc, *_ = sess.step_prepare_v3([0, 1], None, bad)
+        assert rc == gh.INVALID_TRANSACTION and seq.value == 0  # not the tree's parent
+
+        def check_wave(prop, sha, lanes, toks, first, reasons):
+            assert sha == opub.proposal_v3_sha256(prop)
+            assert prop.abi_version == opub.PROPOSAL_V3_ABI
+            assert prop.page_transition_abi == opub.PAGE_TRANSITION_V3_ABI
+            assert prop.live_lane_count == len(lanes)
+            assert prop.live_mask == sum(1 << slots[ln] for ln in lanes)
+            assert bytes(prop.parent_receipt) == bytes(parent)
+            t = prop.tree
+            assert (t.tree_key, t.identity_generation, t.generation, t.structural_revision,
+                    t.active_nodes, t.state_digest, t.token_integrity) == (
+                tree.tree_key, tree.identity_generation, tree.generation,
+                tree.structural_revision, tree.active_nodes, tree.state_digest, tree.integrity)
+            assert bytes(t.current) == bytes(tree.current)
+            for i, ln in enumerate(lanes):
+                sl = slots[ln]
+                r, lp = prop.resources[sl], prop.lanes[sl]
+                tr = lp.kv_transition
+                assert r.lane_index == sl and r.lifecycle == gh.LIFECYCLE_LIVE
+                assert r.scope_index == scopes[ln].node_index
+                assert r.scope_generation == scopes[ln].generation
+                assert r.cache_instance == sess.root(ln).cache_instance == tr.cache_instance
+                assert _rbytes(opub, r.root) == _troot(opub, tr, "after")
+                assert bytes(r.binding_summary) == bytes(lks[ln].binding_summary())
+                alloc = lks[ln].allocation_set()
+                assert bytes(r.allocation_set) == bytes(alloc)
+                assert bytes(alloc.sha256) == opub.allocation_set_sha256(
+                    r.coordinator_instance, r.cache_instance, lks[ln].scope, lks[ln].bindings)
+                assert bytes(lp.output_sha256) == ora.token_sequence_sha256(
+                    outs[ln] + [int(toks[i])])
+                assert lp.terminal_reason == reasons[i]
+                assert bool(r.has_terminal_generation) == bool(reasons[i])
+                assert bool(r.has_canonical_after) == (first or bool(reasons[i]))
+                if first:
+                    assert bytes(r.canonical_after_sha256) == sess.kv_sha256(ln)
+                    assert bytes(tr.state_chain_after) == opub.initial_state_chain_v3(
+                        bytes(r.canonical_after_sha256), _troot(opub, tr, "after"))
+                else:
+                    assert bytes(tr.state_chain_after) == opub.appended_state_chain_v3(
+                        bytes(tr.state_chain_before), _troot(opub, tr, "before"),
+                        _troot(opub, tr, "after"), tr.cache_instance, tr.logical_page,
+                        tr.page_ownership_generation, tr.row_txn_generation,
+                        bytes(tr.row_payload_sha256))
+                assert bytes(r.kv_state_chain_after) == bytes(tr.state_chain_after)
+
+        print("v3 leased waves: first tokens", flush=True)
+        rc, prop, sha, toks = sess.step_prepare_v3([0, 1], None, _v3_binding(gh, parent, slots, 0))
+        assert rc == gh.OK
+        check_wave(prop, sha, [0, 1], toks, True, [0, 0])
+        rc, _ = sess.step_commit(_ack(gh, sha, 1))  # a v1 ack does not acknowledge a v3 wave
+        assert rc == gh.INVALID_TRANSACTION and seq.value == 0
+        rc, prop, sha, toks = sess.step_prepare_v3([0, 1], None, _v3_binding(gh, parent, slots, 0))
+        assert rc == gh.OK
+        ack = _ack3(gh, sha, 1)
+        rc, rec = sess.step_commit(ack)
+        assert rc == gh.OK and seq.value == 1
+        assert bytes(rec.commit_sha256) == opub.commit_v3_sha256(
+            sha, ack.abi_version, sha, ack.sink_epoch, ack.reservation_id)
+        for ln in range(2):
+            outs[ln].append(int(toks[ln]))
+        toks = [int(t) for t in toks]
+        # slots are fixed, live lanes join every wave, lanes chain under one ABI
+        rc, *_ = sess.step_prepare_v3([0, 1], toks, _v3_binding(gh, parent, [0, 2], 1))
+        assert rc == gh.INVALID_ARGUMENT
+        rc, *_ = sess.step_prepare_v3([0], toks[:1], _v3_binding(gh, parent, [2], 1))
+        assert rc == gh.INVALID_TRANSACTION
+        rc, *_ = sess.step_prepare([0, 1], toks, _wave_binding(gh, slots, 1))
+        assert rc == gh.INVALID_TRANSACTION and seq.value == 1
+        for wave in range(4):  # wave 2 writes row 16: both lanes take a page
+            reasons = [0, 1 + gh.TERMINAL_MAX_TOKENS] if wave == 3 else [0, 0]
+            rc, prop, sha, nxt = sess.step_prepare_v3([0, 1], toks,
+                                                      _v3_binding(gh, parent, slots, seq.value),
+                                                      terminal_reason=reasons)
+            assert rc == gh.OK
+            check_wave(prop, sha, [0, 1], nxt, False, reasons)
+            rc, rec = sess.step_commit(_ack3(gh, sha, 10 + wave))
+            assert rc == gh.OK
+            for ln in range(2):
+                outs[ln].append(int(nxt[ln]))
+            toks = [int(t) for t in nxt]
+        assert seq.value == 5
+        term = prop.resources[slots[1]]
+        seal, psha, csha = lks[1].terminal_seal()
+        assert psha == sha and csha == bytes(rec.commit_sha256)
+        assert seal.terminal_reason == gh.TERMINAL_MAX_TOKENS and seal.terminal_token == toks[1]
+        assert seal.generation == term.terminal_generation
+        assert bytes(seal.logical_kv_sha256) == bytes(term.canonical_after_sha256)
+        assert bytes(seal.logical_kv_sha256) == sess.kv_sha256(1)
+        assert seal.coordinator_instance == term.coordinator_instance
+        chain1 = bytes(prop.lanes[slots[1]].kv_transition.state_chain_after)
+        # lane 1 retired: lane 0 publishes alone, lane 1 committed from its seal
+        rc, prop, sha, nxt = sess.step_prepare_v3([0], toks[:1], _v3_binding(gh, parent, [2], 5))
+        assert rc == gh.OK
+        check_wave(prop, sha, [0], nxt, False, [0])
+        r1 = prop.resources[0]
+        assert r1.lifecycle == gh.LIFECYCLE_TERMINAL_RETAINED
+        assert bytes(r1.root) == bytes(seal.root) and bytes(r1.kv_state_chain_after) == chain1
+        assert r1.has_canonical_after and r1.has_binding_summary and not r1.has_terminal_generation
+        assert bytes(r1.canonical_after_sha256) == bytes(seal.logical_kv_sha256)
+        assert bytes(r1.binding_summary) == bytes(seal.bindings)
+        assert sess.step_commit(_ack3(gh, sha, 20))[0] == gh.OK and seq.value == 6
+        outs[0].append(int(nxt[0]))
+        toks = [int(nxt[0])]
+        freed = lks[1].begin_reclaim(seal, 6)
+        lks[1].commit_reclaim(freed)
+        rc, prop, sha, nxt = sess.step_prepare_v3([0], toks, _v3_binding(gh, parent, [2], 6))
+        assert rc == gh.OK
+        check_wave(prop, sha, [0], nxt, False, [0])
+        r1 = prop.resources[0]
+        assert r1.lifecycle == gh.LIFECYCLE_RECLAIMED and bytes(r1.root) == bytes(seal.root)
+        assert not r1.has_binding_summary and r1.allocation_set.count == 0
+        assert r1.allocation_set.abi_version == opub.ALLOCATION_SET_ABI
+        assert sess.step_commit(_ack3(gh, sha, 21))[0] == gh.OK and seq.value == 7
+        lks[0].reclaim_for_teardown(seq.value)
+        assert tree.current.kv_bytes == 0
+        for lk in lks:
+            lk.close()
+        bank.close_session(parent, 6, 0x5E55, seq.value)
+        bank.close_tree(tree)
+        bank.release(parent)
+    finally:
+        sess.close()
