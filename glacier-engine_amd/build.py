@@ -17,7 +17,7 @@ BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "libglacier_hip.so")
 SOURCES = ["kernels.hip", "gemm.hip", "runtime.hip", "session.hip", "host_util.cpp",
            "lane_weave.cpp", "paged_kv.cpp", "publication.cpp", "runtime_image.cpp",
-           "page_image.cpp", "lease_bank.cpp", "leased_kv.cpp"]
+           "page_image.cpp", "lease_bank.cpp", "leased_kv.cpp", "glacier_container.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 

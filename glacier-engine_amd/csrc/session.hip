@@ -26,6 +26,7 @@
 
 #include <map>
 #include "runtime_image.h"
+#include "glacier_container.h"
 
 using gh::hip_fail;
 
@@ -608,6 +609,154 @@ extern "C" glacier_hip_model *glacier_hip_model_load_glrt(glacier_hip_context *c
   int rc = glacier_hip_model_set_globals(m, table.data(), final_norm, head.packed, head_s.data());
   if (rc) return fail(GLACIER_HIP_GLRT_BAD_PAYLOAD, "device upload");
   rep.uploaded_bytes = m->bytes ? m->bytes : glacier_hip_model_weight_bytes(m);
+  if (report) *report = rep;
+  return m;
+}
+
+// ---------------------------------------------------------------------------
+// portable .glacier container -> device model (loader.zig:1214-1592)
+// ---------------------------------------------------------------------------
+namespace gct {
+const Container *container_of(const glacier_hip_glacier *h);
+}
+
+extern "C" glacier_hip_model *glacier_hip_model_load_glacier(glacier_hip_context *ctx,
+                                                            const glacier_hip_glacier *handle,
+                                                            const glacier_hip_model_config_t *override,
+                                                            int tie_word_embeddings,
+                                                            glacier_hip_glacier_load_report_t *report) {
+  glacier_hip_glacier_load_report_t rep{};
+  glacier_hip_model *m = nullptr;
+  auto fail = [&](uint32_t e, const char *what) -> glacier_hip_model * {
+    rep.error = e;
+    if (report) *report = rep;
+    if (ctx) ctx->last_error = std::string("glacier load: ") + gct::error_name(e) + " (" + what + ")";
+    glacier_hip_model_destroy(m);
+    return nullptr;
+  };
+  const gct::Container *c = gct::container_of(handle);
+  if (!ctx || !c) return fail(GLACIER_HIP_GLAC_INVALID_ARGUMENT, "null context or container");
+  gct::Geometry geo;
+  if (uint32_t e = gct::derive_geometry(*c, &geo)) return fail(e, "geometry");
+  std::map<gct::GroupKey, gct::Group> groups;
+  if (uint32_t e = gct::materialize(*c, groups)) return fail(e, "tensor pages");
+  // the JSON sidecar's overrides on top of the page geometry (:1540-1556)
+  const glacier_hip_model_config_t o = override ? *override : glacier_hip_model_config_t{};
+  glacier_hip_model_config_t mc{};
+  mc.dim = o.dim ? o.dim : (uint32_t)geo.dim;
+  mc.hidden_dim = o.hidden_dim ? o.hidden_dim : (uint32_t)geo.hidden_dim;
+  mc.num_layers = o.num_layers ? o.num_layers : geo.num_layers;
+  mc.vocab_size = o.vocab_size ? o.vocab_size : (uint32_t)geo.vocab_size;
+  mc.rms_eps = o.rms_eps != 0.0f ? o.rms_eps : 1e-6f;
+  mc.rope_theta = o.rope_theta != 0.0f ? o.rope_theta : 10000.0f;
+  mc.num_heads = o.num_heads ? o.num_heads : (mc.dim >= 64 && mc.dim % 64 == 0 ? mc.dim / 64 : 1);
+  mc.head_dim = o.head_dim ? o.head_dim : (mc.dim >= 64 && mc.dim % 64 == 0 ? 64 : mc.dim);
+  mc.num_kv_heads = o.num_kv_heads ? o.num_kv_heads : mc.num_heads;
+  mc.group_size = 32;
+  rep.config = mc;
+  m = glacier_hip_model_create(ctx, &mc);
+  if (!m) return fail(GLACIER_HIP_GLAC_UNSUPPORTED, "model shape");
+  const uint64_t D = mc.dim, F = mc.hidden_dim, V = mc.vocab_size;
+  const uint64_t kvd = (uint64_t)mc.num_kv_heads * mc.head_dim;
+  auto find = [&](uint32_t layer, uint32_t kind) -> const gct::Group * {
+    auto it = groups.find({layer, kind});
+    return it == groups.end() ? nullptr : &it->second;
+  };
+  // a decoded (f32) tensor of n values; required ones are MissingTensor when absent
+  auto raw = [&](uint32_t layer, uint32_t kind, uint64_t n, bool required, const float **out) -> uint32_t {
+    *out = nullptr;
+    const gct::Group *g = find(layer, kind);
+    if (!g) return required ? GLACIER_HIP_GLAC_MISSING_TENSOR : GLACIER_HIP_GLAC_OK;
+    if (g->int4) return GLACIER_HIP_GLAC_UNSUPPORTED;  // a norm or bias must decode to values
+    if (g->values.size() != n) return GLACIER_HIP_GLAC_BAD_PAYLOAD;
+    *out = g->values.data();
+    return GLACIER_HIP_GLAC_OK;
+  };
+  // a merged INT4 tensor of out_f x in_f, group 32 (what this device runs)
+  auto int4 = [&](uint32_t layer, uint32_t kind, uint64_t out_f, uint64_t in_f,
+                  const gct::Group **out) -> uint32_t {
+    const gct::Group *g = find(layer, kind);
+    *out = g;
+    if (!g) return GLACIER_HIP_GLAC_MISSING_TENSOR;
+    if (!g->int4 || g->group_size != 32) return GLACIER_HIP_GLAC_UNSUPPORTED;
+    if (g->elements != out_f * in_f) return GLACIER_HIP_GLAC_BAD_PAYLOAD;
+    return GLACIER_HIP_GLAC_OK;
+  };
+  auto f16_scales = [&](const gct::Group &g, std::vector<uint16_t> &buf) {
+    buf.resize(g.scales.size());
+    for (size_t i = 0; i < g.scales.size(); ++i) {
+      buf[i] = gh::f32_to_f16(g.scales[i]);
+      if (gh::f16_to_f32(buf[i]) != g.scales[i]) ++rep.inexact_scales;
+    }
+    return buf.data();
+  };
+  std::vector<uint16_t> sbuf[7];
+  uint32_t e;
+  for (uint32_t l = 0; l < mc.num_layers; ++l) {
+    glacier_hip_layer_host_t w{};
+    const float *bo = nullptr;
+    const uint32_t kinds[7] = {gri::kAttnQ, gri::kAttnK, gri::kAttnV, gri::kAttnO,
+                               gri::kMlpGate, gri::kMlpUp, gri::kMlpDown};
+    const uint64_t outs[7] = {D, kvd, kvd, D, F, F, D}, ins[7] = {D, D, D, D, D, D, F};
+    const gct::Group *g[7];
+    const uint16_t *s16[7];
+    for (int i = 0; i < 7; ++i) {
+      if ((e = int4(l, kinds[i], outs[i], ins[i], &g[i]))) return fail(e, "layer projection");
+      s16[i] = f16_scales(*g[i], sbuf[i]);
+      rep.int4_tensors++;
+    }
+    if ((e = raw(l, gri::kInputNorm, D, true, &w.input_norm)) ||
+        (e = raw(l, gri::kPostAttnNorm, D, true, &w.post_attn_norm)) ||
+        (e = raw(l, gri::kAttnQBias, D, false, &w.bq)) ||
+        (e = raw(l, gri::kAttnKBias, kvd, false, &w.bk)) ||
+        (e = raw(l, gri::kAttnVBias, kvd, false, &w.bv)) ||
+        (e = raw(l, gri::kAttnOBias, D, false, &bo)))
+      return fail(e, "layer norms / biases");
+    if (bo) return fail(GLACIER_HIP_GLAC_UNSUPPORTED, "attn_o bias");
+    w.wq = g[0]->packed.data(); w.wk = g[1]->packed.data(); w.wv = g[2]->packed.data();
+    w.wo = g[3]->packed.data(); w.w_gate = g[4]->packed.data(); w.w_up = g[5]->packed.data();
+    w.w_down = g[6]->packed.data();
+    if (set_layer_impl(m, l, w, s16)) return fail(GLACIER_HIP_GLAC_BAD_PAYLOAD, "device upload");
+    rep.raw_tensors += 2 + (w.bq != nullptr) + (w.bk != nullptr) + (w.bv != nullptr);
+  }
+  // globals live at layer 0 (:1513-1530)
+  const float *final_norm = nullptr;
+  if ((e = raw(0, gri::kFinalNorm, D, true, &final_norm))) return fail(e, "final_norm");
+  const gct::Group *emb = find(0, gri::kEmbedding);
+  if (!emb) return fail(GLACIER_HIP_GLAC_MISSING_TENSOR, "embedding");
+  std::vector<float> table;
+  const float *table_p = nullptr;
+  if (emb->int4) {
+    if (emb->elements != V * D) return fail(GLACIER_HIP_GLAC_BAD_PAYLOAD, "embedding");
+    // the gather table: each element's code offset times its group's f32 scale
+    table.resize(V * D);
+    const uint32_t gs = emb->group_size;
+    gh::parallel_for(V, [&](size_t r0, size_t r1) {
+      for (size_t r = r0; r < r1; ++r)
+        for (size_t k = 0; k < D; ++k) {
+          const size_t idx = r * D + k;
+          const uint8_t b = emb->packed[idx / 2];
+          const int u = (idx & 1) ? b >> 4 : b & 0xF;
+          table[idx] = (float)(u - 7) * emb->scales[idx / gs];
+        }
+    }, 256);
+    table_p = table.data();
+  } else {
+    if (emb->values.size() != V * D) return fail(GLACIER_HIP_GLAC_BAD_PAYLOAD, "embedding");
+    table_p = emb->values.data();
+  }
+  const gct::Group *head = nullptr;
+  if ((e = int4(0, tie_word_embeddings ? gri::kEmbedding : gri::kLmHead, V, D, &head)))
+    return fail(e, tie_word_embeddings ? "tied head (INT4 embedding)" : "lm_head");
+  std::vector<uint16_t> hbuf;
+  const uint16_t *h16 = f16_scales(*head, hbuf);
+  std::vector<float> head_s(head->scales.size());
+  for (size_t i = 0; i < head_s.size(); ++i) head_s[i] = gh::f16_to_f32(h16[i]);
+  rep.int4_tensors += tie_word_embeddings ? 1 : (emb->int4 ? 2 : 1);
+  rep.raw_tensors += 1 + (emb->int4 ? 0 : 1);
+  if (glacier_hip_model_set_globals(m, table_p, final_norm, head->packed.data(), head_s.data()))
+    return fail(GLACIER_HIP_GLAC_BAD_PAYLOAD, "device upload");
+  rep.uploaded_bytes = glacier_hip_model_weight_bytes(m);
   if (report) *report = rep;
   return m;
 }

@@ -490,6 +490,45 @@ class GlrtLoadReport(C.Structure):
                 ("uploaded_bytes", C.c_uint64)]
 
 
+class GlacierHeader(C.Structure):
+    _fields_ = [("version", C.c_uint32), ("header_size", C.c_uint32)] + \
+        [(n, C.c_uint64) for n in ("meta_offset", "meta_len", "num_pages", "page_index_offset",
+                                   "page_data_offset")] + \
+        [("page_size_log2", C.c_uint32), ("reserved", C.c_uint32),
+         ("container_bytes", C.c_uint64)]
+
+
+class GlacierPage(C.Structure):
+    _fields_ = [("page_id", C.c_uint64), ("layer_idx", C.c_uint32), ("tensor_kind", C.c_uint32),
+                ("row_start", C.c_uint64), ("row_end", C.c_uint64), ("precision", C.c_uint32),
+                ("quant_group", C.c_uint32), ("data_offset", C.c_uint64),
+                ("data_len", C.c_uint64), ("crc32", C.c_uint32), ("reserved", C.c_uint32)]
+
+
+class GlacierAssembly(C.Structure):
+    _fields_ = [("error", C.c_uint32), ("num_layers", C.c_uint32)] + \
+        [(n, C.c_uint64) for n in ("dim", "hidden_dim", "vocab_size", "groups", "int4_groups")] + \
+        [("sha256", C.c_uint8 * 32)]
+
+
+class GlacierLoadReport(C.Structure):
+    _fields_ = [("error", C.c_uint32), ("int4_tensors", C.c_uint32), ("raw_tensors", C.c_uint32),
+                ("reserved", C.c_uint32), ("inexact_scales", C.c_uint64),
+                ("uploaded_bytes", C.c_uint64), ("config", ModelConfig)]
+
+
+GLACIER_ERRORS = [
+    "Ok", "TruncatedHeader", "BadMagic", "BadVersion", "BadHeaderSize", "BadPageSize",
+    "BadReservedField", "BadLayout", "MetadataTooLarge", "IndexTooLarge", "LayoutOverflow",
+    "TruncatedMeta", "TruncatedIndex", "BadMetadata", "BadTensorKind", "BadPrecision",
+    "BadPageId", "BadRowRange", "EmptyPage", "BadQuantGroup", "PageGeometryTooLarge",
+    "BadPageGeometry", "UnsupportedPrecision", "NonContiguousPayload", "TruncatedPage",
+    "TrailingBytes", "CrcMismatch", "BadQuantPayload", "BufferTooSmall", "EmptyStreamBuffer",
+    "FileError", "SizeMismatch", "BadGroupSize", "TruncatedScales", "TruncatedPacked",
+    "InvalidPayloadSize", "InvalidValue", "NoLayers", "MissingTensor", "BadPayload",
+    "Unsupported", "InvalidArgument"]
+
+
 class PageImageInfo(C.Structure):
     _fields_ = [("error", C.c_uint32), ("reserved", C.c_uint32), ("source_root", PageMapRoot),
                 ("num_layers", C.c_uint64), ("dim", C.c_uint64), ("max_seq", C.c_uint64),
@@ -693,6 +732,25 @@ _SIGS = [
      [_P, C.POINTER(GlrtRecord), C.c_uint32, C.POINTER(_P), C.POINTER(C.c_uint64)]),
     ("glacier_hip_glrt_identity", C.c_int, [_P, _P, C.POINTER(C.c_uint64)]),
     ("glacier_hip_model_load_glrt", _P, [_P, _P, C.POINTER(GlrtLoadReport)]),
+    ("glacier_hip_glacier_error_name", C.c_char_p, [C.c_uint32]),
+    ("glacier_hip_glacier_open", C.c_int, [C.c_char_p, C.POINTER(_P)]),
+    ("glacier_hip_glacier_close", None, [_P]),
+    ("glacier_hip_glacier_header", C.c_int, [_P, C.POINTER(GlacierHeader)]),
+    ("glacier_hip_glacier_page", C.c_int, [_P, C.c_uint64, C.POINTER(GlacierPage)]),
+    ("glacier_hip_glacier_metadata", C.c_int, [_P, C.POINTER(_P), C.POINTER(C.c_uint64)]),
+    ("glacier_hip_glacier_read_page", C.c_int, [_P, C.c_uint64, _P, C.c_uint64]),
+    ("glacier_hip_glacier_read_page_f32", C.c_int,
+     [_P, C.c_uint64, _P, C.c_uint64, C.POINTER(C.c_uint64)]),
+    ("glacier_hip_glacier_validate_crcs", C.c_int, [_P, C.c_uint64]),
+    ("glacier_hip_glacier_identity", C.c_int, [_P, _P, C.POINTER(C.c_uint64)]),
+    ("glacier_hip_glacier_source_fingerprint", C.c_int, [_P, _P]),
+    ("glacier_hip_glacier_assemble", C.c_int, [_P, C.POINTER(GlacierAssembly)]),
+    ("glacier_hip_qio_encode_f32", C.c_int,
+     [_P, C.c_uint64, C.c_uint32, C.c_uint32, _P, C.c_uint64, C.POINTER(C.c_uint64)]),
+    ("glacier_hip_qio_decode_f32", C.c_int,
+     [_P, C.c_uint64, _P, C.c_uint64, C.POINTER(C.c_uint64)]),
+    ("glacier_hip_model_load_glacier", _P,
+     [_P, _P, C.POINTER(ModelConfig), C.c_int, C.POINTER(GlacierLoadReport)]),
     ("glacier_hip_lease_bank_create", _P, [C.c_uint32, C.c_uint32, C.POINTER(Limits), C.c_uint64]),
     ("glacier_hip_lease_bank_destroy", None, [_P]),
     ("glacier_hip_lease_bank_reserve", C.c_int,
@@ -961,6 +1019,112 @@ class GlrtImage:
             self.h = None
 
 
+class GlacierError(GlacierHipError):
+    """A `.glacier` container or qio payload the reader refused; .reason is
+    the reference's error name."""
+
+    def __init__(self, code, what):
+        self.reason = GLACIER_ERRORS[code] if 0 <= code < len(GLACIER_ERRORS) else str(code)
+        super().__init__(code, f"{what}: {self.reason}")
+
+
+def _glac(rc, what):
+    if rc != 0:
+        raise GlacierError(rc, what)
+
+
+class Glacier:
+    """An admitted portable .glacier container (glacier_hip_glacier_open); host only."""
+
+    def __init__(self, path):
+        h = _P()
+        _glac(lib().glacier_hip_glacier_open(os.fsencode(path), C.byref(h)), "glacier_open")
+        self.h = h
+
+    def header(self):
+        x = GlacierHeader()
+        _glac(lib().glacier_hip_glacier_header(self.h, C.byref(x)), "glacier_header")
+        return x
+
+    def page(self, i):
+        x = GlacierPage()
+        _glac(lib().glacier_hip_glacier_page(self.h, i, C.byref(x)), "glacier_page")
+        return x
+
+    def pages(self):
+        return [self.page(i) for i in range(self.header().num_pages)]
+
+    def metadata(self):
+        p, n = _P(), C.c_uint64()
+        _glac(lib().glacier_hip_glacier_metadata(self.h, C.byref(p), C.byref(n)), "glacier_metadata")
+        return C.string_at(p.value, n.value) if n.value else b""
+
+    def read_page(self, i, capacity=None):
+        n = self.page(i).data_len if capacity is None else capacity
+        buf = (C.c_uint8 * max(n, 1))()
+        _glac(lib().glacier_hip_glacier_read_page(self.h, i, buf, n), "glacier_read_page")
+        return bytes(buf)[:self.page(i).data_len]
+
+    def read_page_f32(self, i):
+        pg = self.page(i)
+        out = np.zeros(max(pg.row_end - pg.row_start, 1), np.float32)
+        n = C.c_uint64()
+        _glac(lib().glacier_hip_glacier_read_page_f32(self.h, i, ptr(out), out.size, C.byref(n)),
+              "glacier_read_page_f32")
+        return out[:n.value]
+
+    def validate_crcs(self, buffer_bytes=64 * 1024):
+        _glac(lib().glacier_hip_glacier_validate_crcs(self.h, buffer_bytes), "glacier_validate_crcs")
+
+    def identity(self):
+        d, n = (C.c_uint8 * 32)(), C.c_uint64()
+        _glac(lib().glacier_hip_glacier_identity(self.h, d, C.byref(n)), "glacier_identity")
+        return bytes(d), n.value
+
+    def source_fingerprint(self):
+        d = (C.c_uint8 * 32)()
+        _glac(lib().glacier_hip_glacier_source_fingerprint(self.h, d), "glacier_source_fingerprint")
+        return bytes(d)
+
+    def assemble(self):
+        """The loader's host assembly: (error name, GlacierAssembly)."""
+        a = GlacierAssembly()
+        lib().glacier_hip_glacier_assemble(self.h, C.byref(a))
+        return GLACIER_ERRORS[a.error], a
+
+    def close(self):
+        if self.h:
+            lib().glacier_hip_glacier_close(self.h)
+            self.h = None
+
+
+def qio_encode_f32(src, precision, group_size):
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    n = C.c_uint64()
+    rc = lib().glacier_hip_qio_encode_f32(ptr(src) if src.size else None, src.size, precision,
+                                          group_size, None, 0, C.byref(n))
+    if rc != GLACIER_ERRORS.index("BufferTooSmall"):
+        _glac(rc, "qio_encode_f32")
+    buf = (C.c_uint8 * max(n.value, 1))()
+    _glac(lib().glacier_hip_qio_encode_f32(ptr(src) if src.size else None, src.size, precision,
+                                           group_size, buf, n.value, C.byref(n)), "qio_encode_f32")
+    return bytes(buf)[:n.value]
+
+
+def qio_decode_f32(payload):
+    payload = bytes(payload)
+    b = (C.c_uint8 * max(len(payload), 1)).from_buffer_copy(payload.ljust(1, b"\0"))
+    n = C.c_uint64()
+    rc = lib().glacier_hip_qio_decode_f32(b, len(payload), None, 0, C.byref(n))
+    if rc != GLACIER_ERRORS.index("BufferTooSmall"):
+        _glac(rc, "qio_decode_f32")
+        return np.zeros(0, np.float32)
+    out = np.zeros(max(n.value, 1), np.float32)
+    _glac(lib().glacier_hip_qio_decode_f32(b, len(payload), ptr(out), out.size, C.byref(n)),
+          "qio_decode_f32")
+    return out[:n.value]
+
+
 # ---- thin object wrappers -------------------------------------------------------------
 class Context:
     def __init__(self, device=0):
@@ -1040,6 +1204,23 @@ class Model:
         m.h = lib().glacier_hip_model_load_glrt(ctx.h, image.h, C.byref(m.report))
         if not m.h:
             raise GlrtError(INVALID_ARGUMENT, GLRT_ERRORS[m.report.error], "model_load_glrt")
+        return m
+
+    @classmethod
+    def load_glacier(cls, ctx, container, override=None, tie_word_embeddings=False):
+        """glacier_hip_model_load_glacier: a device model from an admitted
+        .glacier container; `override` holds ModelConfig fields (zero or
+        absent: the page geometry and the reference's defaults)."""
+        m = cls.__new__(cls)
+        m.ctx = ctx
+        o = ModelConfig(**(override or {}))
+        m.report = GlacierLoadReport()
+        m.h = lib().glacier_hip_model_load_glacier(ctx.h, container.h, C.byref(o),
+                                                   int(tie_word_embeddings), C.byref(m.report))
+        if not m.h:
+            raise GlacierError(m.report.error, "model_load_glacier")
+        c = m.report.config
+        m.cfg = {k: getattr(c, k) for k, _ in ModelConfig._fields_}
         return m
 
     def weight_bytes(self):

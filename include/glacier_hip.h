@@ -1163,6 +1163,136 @@ glacier_hip_model *glacier_hip_model_load_glrt(glacier_hip_context *ctx,
                                                const glacier_hip_glrt_image *image,
                                                glacier_hip_glrt_load_report_t *report);
 
+/* ---- portable .glacier source containers (src/model/format.zig) ----------
+ * Header (256 bytes) | JSON metadata | page index (64-byte PageEntry each) |
+ * page payloads; a quantized page's payload is the qio sub-header "QOIT"
+ * (u32 magic, u32 num_elements, u32 group_size, u8 precision 0 int8 /
+ * 1 int4, 3 zero bytes), f32 scales, then the packed codes (qio.zig:1-21).
+ * Admission, CRCs and identities follow FileReader (format.zig:379-662) and
+ * report the reference's error names (glacier_hip_glacier_error_name). */
+typedef struct glacier_hip_glacier glacier_hip_glacier;
+
+typedef struct {
+    uint32_t version, header_size;
+    uint64_t meta_offset, meta_len, num_pages, page_index_offset, page_data_offset;
+    uint32_t page_size_log2, reserved;
+    uint64_t container_bytes;
+} glacier_hip_glacier_header_t;    /* Header (format.zig:67-137) + the file size */
+
+typedef struct {
+    uint64_t page_id;
+    uint32_t layer_idx, tensor_kind;     /* TensorKind (format.zig:46-64) */
+    uint64_t row_start, row_end;         /* element range of the page's tensor */
+    uint32_t precision, quant_group;     /* core.Precision: fp16 0, bf16 1, int8 2, int4 3, int2 4, tri1p58 5, fp32 6 */
+    uint64_t data_offset, data_len;
+    uint32_t crc32, reserved;
+} glacier_hip_glacier_page_t;      /* PageEntry (format.zig:141-199) */
+
+enum {
+    GLACIER_HIP_GLAC_OK = 0,
+    GLACIER_HIP_GLAC_TRUNCATED_HEADER = 1, GLACIER_HIP_GLAC_BAD_MAGIC = 2,
+    GLACIER_HIP_GLAC_BAD_VERSION = 3, GLACIER_HIP_GLAC_BAD_HEADER_SIZE = 4,
+    GLACIER_HIP_GLAC_BAD_PAGE_SIZE = 5, GLACIER_HIP_GLAC_BAD_RESERVED_FIELD = 6,
+    GLACIER_HIP_GLAC_BAD_LAYOUT = 7, GLACIER_HIP_GLAC_METADATA_TOO_LARGE = 8,
+    GLACIER_HIP_GLAC_INDEX_TOO_LARGE = 9, GLACIER_HIP_GLAC_LAYOUT_OVERFLOW = 10,
+    GLACIER_HIP_GLAC_TRUNCATED_META = 11, GLACIER_HIP_GLAC_TRUNCATED_INDEX = 12,
+    GLACIER_HIP_GLAC_BAD_METADATA = 13, GLACIER_HIP_GLAC_BAD_TENSOR_KIND = 14,
+    GLACIER_HIP_GLAC_BAD_PRECISION = 15, GLACIER_HIP_GLAC_BAD_PAGE_ID = 16,
+    GLACIER_HIP_GLAC_BAD_ROW_RANGE = 17, GLACIER_HIP_GLAC_EMPTY_PAGE = 18,
+    GLACIER_HIP_GLAC_BAD_QUANT_GROUP = 19, GLACIER_HIP_GLAC_PAGE_GEOMETRY_TOO_LARGE = 20,
+    GLACIER_HIP_GLAC_BAD_PAGE_GEOMETRY = 21, GLACIER_HIP_GLAC_UNSUPPORTED_PRECISION = 22,
+    GLACIER_HIP_GLAC_NON_CONTIGUOUS_PAYLOAD = 23, GLACIER_HIP_GLAC_TRUNCATED_PAGE = 24,
+    GLACIER_HIP_GLAC_TRAILING_BYTES = 25, GLACIER_HIP_GLAC_CRC_MISMATCH = 26,
+    GLACIER_HIP_GLAC_BAD_QUANT_PAYLOAD = 27, GLACIER_HIP_GLAC_BUFFER_TOO_SMALL = 28,
+    GLACIER_HIP_GLAC_EMPTY_STREAM_BUFFER = 29, GLACIER_HIP_GLAC_FILE_ERROR = 30,
+    GLACIER_HIP_GLAC_SIZE_MISMATCH = 31,
+    /* qio / quant */
+    GLACIER_HIP_GLAC_BAD_GROUP_SIZE = 32, GLACIER_HIP_GLAC_TRUNCATED_SCALES = 33,
+    GLACIER_HIP_GLAC_TRUNCATED_PACKED = 34, GLACIER_HIP_GLAC_INVALID_PAYLOAD_SIZE = 35,
+    GLACIER_HIP_GLAC_INVALID_VALUE = 36,       /* encode: a non-finite source value */
+    /* loader (loader.zig:20-28) and this device's limits */
+    GLACIER_HIP_GLAC_NO_LAYERS = 37, GLACIER_HIP_GLAC_MISSING_TENSOR = 38,
+    GLACIER_HIP_GLAC_BAD_PAYLOAD = 39, GLACIER_HIP_GLAC_UNSUPPORTED = 40,
+    GLACIER_HIP_GLAC_INVALID_ARGUMENT = 41,
+};
+const char *glacier_hip_glacier_error_name(uint32_t code);
+
+/* FileReader.open (:383-478): strict admission of `path`; returns a
+ * GLACIER_HIP_GLAC_* code, *out set only on success. */
+int glacier_hip_glacier_open(const char *path, glacier_hip_glacier **out);
+void glacier_hip_glacier_close(glacier_hip_glacier *c);
+int glacier_hip_glacier_header(const glacier_hip_glacier *c, glacier_hip_glacier_header_t *out);
+int glacier_hip_glacier_page(const glacier_hip_glacier *c, uint64_t index,
+                             glacier_hip_glacier_page_t *out);
+/* The metadata blob (a view into the mapping, valid until close). */
+int glacier_hip_glacier_metadata(const glacier_hip_glacier *c, const void **data, uint64_t *len);
+/* readPage (:488-494): copies the page's payload after its CRC check. */
+int glacier_hip_glacier_read_page(const glacier_hip_glacier *c, uint64_t index, void *dst,
+                                  uint64_t dst_len);
+/* readPageDequant (:638-662) to f32: raw pages decoded, quantized pages
+ * schema-checked and dequantized; *count = the page's element count. */
+int glacier_hip_glacier_read_page_f32(const glacier_hip_glacier *c, uint64_t index, float *dst,
+                                      uint64_t capacity, uint64_t *count);
+/* validateAllPageCrcsWithBufferV1 (:503-531): every page's payload schema
+ * and CRC, read in chunks of buffer_bytes (0: EmptyStreamBuffer). */
+int glacier_hip_glacier_validate_crcs(const glacier_hip_glacier *c, uint64_t buffer_bytes);
+/* containerIdentityV1 (:536-575): SHA-256 of every byte of the file. */
+int glacier_hip_glacier_identity(const glacier_hip_glacier *c, uint8_t container_sha256[32],
+                                 uint64_t *container_bytes);
+/* sourceFingerprint (loader.zig:167-189): metadata and typed page entries,
+ * physical offsets omitted. */
+int glacier_hip_glacier_source_fingerprint(const glacier_hip_glacier *c, uint8_t out[32]);
+/* qio.encodePage over f32 source (qio.zig:72-112, quant.quantize
+ * quant.zig:36-112): precision 0 int8 / 1 int4; *len = payload bytes (with
+ * capacity too small nothing is written and BUFFER_TOO_SMALL returned). */
+int glacier_hip_qio_encode_f32(const float *src, uint64_t count, uint32_t precision,
+                               uint32_t group_size, uint8_t *out, uint64_t capacity,
+                               uint64_t *len);
+/* qio.decodePage to f32 (qio.zig:115-162, quant.dequantize :114-163). */
+int glacier_hip_qio_decode_f32(const uint8_t *payload, uint64_t len, float *out,
+                               uint64_t capacity, uint64_t *count);
+
+/* The loader's host-side assembly alone (no device): the geometry pass
+ * (loader.zig:1226-1268) and every (layer, kind) group materialised as the
+ * device loader takes them, summarised by a digest over the groups in
+ * (layer, kind) order: SHA-256 of "glacier-hip-assembly-v1\0", u64 group
+ * count, then per group u32 layer, u32 kind, u32 int4, u32 group size,
+ * u64 elements, then the packed nibbles and f32 scales (INT4 groups) or the
+ * f32 values (all LE). A test-facing summary of this library. */
+typedef struct {
+    uint32_t error;                  /* GLACIER_HIP_GLAC_* */
+    uint32_t num_layers;
+    uint64_t dim, hidden_dim, vocab_size;
+    uint64_t groups, int4_groups;
+    uint8_t sha256[32];
+} glacier_hip_glacier_assembly_t;
+int glacier_hip_glacier_assemble(const glacier_hip_glacier *c, glacier_hip_glacier_assembly_t *out);
+
+typedef struct {
+    uint32_t error;                  /* GLACIER_HIP_GLAC_* */
+    uint32_t int4_tensors, raw_tensors, reserved;
+    uint64_t inexact_scales;         /* f32 scales fp16 does not hold exactly */
+    uint64_t uploaded_bytes;
+    glacier_hip_model_config_t config;  /* the configuration loaded */
+} glacier_hip_glacier_load_report_t;
+
+/* loadWithOptions (loader.zig:1214-1592) with compact INT4 onto the device:
+ * model geometry from the page metadata (norm lengths, element counts),
+ * `override` fields that are non-zero replacing it as the reference's JSON
+ * sidecar does (heads default dim / 64 with head_dim 64, kv heads = heads,
+ * rms_eps 1e-6, rope_theta 10000), groups materialised in (layer, kind)
+ * order (INT4 pages of the projections, embedding and head merged by
+ * concatInt4Pages :1636-1720, the rest decoded to f32), then every layer
+ * uploaded into the device tile layout (f32 scales rounded to fp16) and the
+ * INT4 embedding dequantized for the gather. The device runs INT4 group-32
+ * projections and LM head: other encodings load as UNSUPPORTED. NULL on
+ * failure with report->error set. */
+glacier_hip_model *glacier_hip_model_load_glacier(glacier_hip_context *ctx,
+                                                  const glacier_hip_glacier *c,
+                                                  const glacier_hip_model_config_t *override,
+                                                  int tie_word_embeddings,
+                                                  glacier_hip_glacier_load_report_t *report);
+
 /* ---- synthetic random-init generator (host, deterministic) ---------------
  * Counter-based SplitMix64 streams keyed by (seed, tensor id):
  *  - INT4 codes: uniform nibbles u in 0..15 (decode u - 7 in [-7, 8]);
