@@ -18,8 +18,11 @@ KV already resident in HBM. The same JSON line carries:
                 int8 MFMA rate it implies;
   * attention   config 3: paged GQA decode attention alone, 4 lanes at
                 contexts 512..8192, GB/s;
-  * roofline    for the dominant kernel (the fused 7B gate/up GEMV, 53% of a
-                token's weight bytes): algorithmic bytes / average duration;
+  * roofline    for the dominant kernel: the 7B gate/up launch that runs in
+                the batch-1 token (53% of its weight bytes), algorithmic bytes
+                / its average launch duration from HIP events on the step
+                stream (in_token_kernels: gate/up, down, attention + O, QKV),
+                traffic from the committed counter summary;
   * cpu_baseline the CPU oracle (the reference algorithm restated in C) on the
                 same model, timed on this host's cores over a bounded sample;
                 with the cpu section the gemv (M = 1), attention and prefill
@@ -187,18 +190,23 @@ def cpu_gemv(gh, ctx, torch, n, k, act):
                 max_rel_vs_oracle=float(f"{err:.3g}"), kind="port")
 
 
-def measured_traffic():
-    """HBM bytes per launch of the gate/up GEMV from the committed
-    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE summary (copy-kernel calibrated),
-    or None when the summary is absent."""
-    path = os.path.join(ROOT, "profiles", "gemv_gate_up_7b_m1_pmc.md")
+def profile_value(name, key):
+    """A `key = value` line of a committed profiles/ summary (None when the
+    summary or the line is absent)."""
     try:
-        for line in open(path):
-            if line.startswith("traffic_bytes_per_launch"):
-                return int(line.split("=")[1])
-    except OSError:
+        for line in open(os.path.join(ROOT, "profiles", name)):
+            if line.startswith(key + " ="):
+                return float(line.split("=")[1])
+    except (OSError, ValueError):
         pass
     return None
+
+
+def measured_traffic(name):
+    """HBM bytes per launch from a committed rocprofv3 --pmc FETCH_SIZE /
+    WRITE_SIZE summary (copy-kernel calibrated), or None."""
+    v = profile_value(name, "traffic_bytes_per_launch")
+    return None if v is None else int(v)
 
 
 def int4_weights(cfg):
@@ -311,7 +319,10 @@ def auto_act(gh, n, k):
     return gh.ACT_F32 if (n > 65536 or k > 16384) else gh.ACT_Q8
 
 
-def decode_batch1(gh, sess, prompt, warmup, steps):
+def decode_batch1(gh, sess, prompt, warmup, steps, probe=None):
+    """Batch-1 greedy decode of lane 0: `warmup` untimed tokens, then exactly
+    `steps` timed ones. With `probe` (a step count), the in-token kernels are
+    then timed per launch (probe_in_token), after the timed region."""
     tok = sess.prefill(0, prompt)
     for _ in range(warmup):
         tok = int(sess.step([0], [tok])[0])
@@ -319,7 +330,85 @@ def decode_batch1(gh, sess, prompt, warmup, steps):
     for _ in range(steps):
         tok = int(sess.step([0], [tok])[0])
     dt = time.perf_counter() - t0
+    if probe:
+        return steps / dt, dt, probe_in_token(sess, tok, probe, len(prompt) + warmup + steps)
     return steps / dt, dt
+
+
+IN_TOKEN_KINDS = ("gate_up", "down", "attention", "qkv")
+
+
+def in_token_bytes(cfg, kind, ctx_len, kv_elem=2):
+    """Algorithmic HBM bytes of one batch-1 in-token launch of a layer: the
+    INT4 weights it streams (codes + fp16 group scales, 9/16 B per weight)
+    plus the activations it reads and writes once (f32 rows, 1- or 3-digit
+    int8 planes with an 8-byte scale/correction per 32-group, K/V rows)."""
+    D, F = cfg["dim"], cfg["hidden_dim"]
+    kvd = cfg["num_kv_heads"] * cfg["head_dim"]
+    w = lambda n, k: n * k // 2 + n * k // 16
+    if kind == "gate_up":  # x and the norm weight in; SwiGLU's 3-digit planes for down out
+        return w(2 * F, D) + 2 * D * 4 + F * 3 + F // 32 * 8
+    if kind == "down":  # 3-digit planes and the residual in; the new residual out
+        return w(D, F) + F * 3 + F // 32 * 8 + 2 * D * 4
+    if kind == "qkv":  # x and the norm weight in; q out, the K/V row into its page
+        return w(D + 2 * kvd, D) + 2 * D * 4 + D * 4 + 2 * kvd * kv_elem
+    # attention fused with O: q, the lane's K/V, the O weights and residual in; h out
+    return w(D, D) + D * 4 + ctx_len * 2 * kvd * kv_elem + 2 * D * 4
+
+
+def probe_in_token(sess, tok, steps, ctx0, reps=4):
+    """The batch-1 token's kernels timed with HIP events on the step stream,
+    after the timed region:
+      * gate/up and down: the last token's launches of all 28 layers (same
+        kernel, launch shape, inputs and per-layer weights, so every launch
+        streams its weights from HBM) replayed `reps` times back to back,
+        events around the run (glacier_hip_session_probe_replay): the
+        launch-to-launch duration a kernel trace reports;
+      * every kind: events around each launch of `steps` more tokens
+        (glacier_hip_session_probe_kernel), which adds each launch's
+        dispatch latency (avg_us_events)."""
+    out = {}
+    for kind in IN_TOKEN_KINDS:
+        sess.probe_kernel(kind)
+        for _ in range(steps):
+            tok = int(sess.step([0], [tok])[0])
+        us, n = sess.probe_read()
+        ctx = ctx0 + steps / 2
+        ctx0 += steps
+        b = in_token_bytes(CFG_7B, kind, ctx)
+        ev = us / max(n, 1)
+        r = dict(avg_us_events=round(ev, 2), launches_events=n, bytes_per_launch=int(b))
+        avg = ev
+        if kind in ("gate_up", "down"):
+            sess.probe_kernel(None)
+            avg = sess.probe_replay(kind, reps)
+            r.update(avg_us=round(avg, 2), launches=reps * CFG_7B["num_layers"])
+        else:
+            r.update(avg_us=round(ev, 2), launches=n)
+        r.update(gbs=round(b / avg / 1e3, 1), frac=round(b / avg / 1e3 / HBM_PEAK_GBS, 4))
+        out[kind] = r
+    sess.probe_kernel(None)
+    return out
+
+
+def decode_long_context(gh, model, prompt_len, warmup, steps):
+    """Batch-1 decode after a `prompt_len`-token prompt, fp16 and f32 KV:
+    the token whose attention reads ~2048 positions per layer."""
+    out = {}
+    for name, kv, elem in (("fp16_kv", gh.F16, 2), ("f32_kv", gh.F32, 4)):
+        sess = gh.Session(model, max_lanes=1, max_positions=prompt_len + warmup + steps + 8,
+                          kv_dtype=kv, prefill_chunk=2048)
+        try:
+            sess.begin(0, seed=1)
+            prompt = gh.synth_tokens(SEED, 0x4C4F4E47, model.cfg["vocab_size"], prompt_len)
+            tps, dt = decode_batch1(gh, sess, prompt, warmup, steps)
+        finally:
+            sess.close()
+        out[name] = dict(value=round(tps, 2), unit="tokens/s", ms_per_step=round(dt * 1e3 / steps, 4),
+                         roofline=step_roofline(model.cfg, tps, tps,
+                                                prompt_len + warmup + steps / 2 + 1, elem))
+    out.update(prompt_len=prompt_len, steps=steps)
+    return out
 
 
 def decode_leased(gh, model, prompt, max_pos, warmup, steps):
@@ -540,6 +629,9 @@ def bench_prefill(gh, model, lengths, reps=3):
                             int8_mfma_algorithmic_tops=round(algo / ttft / 1e12, 1),
                             int8_mfma_executed_tops=round(execd / ttft / 1e12, 1),
                             mfma_frac_of_5000_tops=round(execd / ttft / INT8_PEAK_OPS, 4)))
+            if T == 2048:  # the gate/up GEMM's VALU issue share, from its committed counters
+                out[-1]["gate_up_valu_issue_frac"] = profile_value("prefill_7b_t2048_pmc.md",
+                                                                   "valu_issue_fraction")
             log("prefill", out[-1])
         finally:
             sess.close()
@@ -662,6 +754,9 @@ def main():
     ap.add_argument("--sections", default="gemv,decode,lanes,c5,c1,prefill,attention,cpu",
                     help="comma list of gemv, decode, lanes, c5, c1, prefill, attention, cpu "
                          "(profiling runs select one; the JSON line needs decode)")
+    ap.add_argument("--probe-steps", type=int, default=8,
+                    help="tokens per in-token kernel timed with HIP events after the timed "
+                         "batch-1 region (0: none)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-attention", action="store_true")
@@ -728,15 +823,16 @@ def main():
                     gemv.append(r)
             finally:
                 cw.close()
+    # (replaced by the in-token gate/up launch when the decode section runs)
     roofline = dict(bound="hbm", achieved=dom["gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
-                    frac=dom["frac"], traffic=measured_traffic()) if dom else None
+                    frac=dom["frac"], traffic=None) if dom else None
     if a.gemv_only:
         print(json.dumps(dict(metric=f"int4 gemv HBM GB/s (7B gate/up, M={dom['M']})",
                               value=dom["gbs"], unit="GB/s", roofline=roofline, gemv=[dom])))
         return
 
     # ---- 7B model ----
-    need_7b = bool(secs & {"decode", "lanes", "c5", "prefill", "cpu"})
+    need_7b = bool(secs & {"decode", "decode1", "lanes", "c5", "prefill", "cpu"})
     if not need_7b:  # kernel-only sections (profiling runs)
         attn = bench_attention(gh, ctx, torch, cpu=False) if not a.no_attention else None
         c1 = bench_c1(gh, ctx, cpu=False) if "c1" in secs else None
@@ -749,13 +845,16 @@ def main():
     model.set_from_host(host)
     log(f"7B model built in {time.perf_counter() - t0:.1f}s, {model.weight_bytes() / 1e9:.2f} GB in HBM")
     prompt = gh.synth_tokens(SEED, 0x50524F4D, CFG_7B["vocab_size"], a.prompt)
-    max_pos = max(a.prompt, a.lane_prompt) + a.warmup + a.steps + 8
+    max_pos = max(a.prompt, a.lane_prompt) + a.warmup + a.steps + 8 + \
+        a.probe_steps * len(IN_TOKEN_KINDS)
     sess = gh.Session(model, max_lanes=max(1, a.lanes), max_positions=max_pos, kv_dtype=gh.F16)
     sess.begin(0, seed=1)
-    tps1, dt1 = 0.0, 0.0
-    if "decode" in secs:
-        tps1, dt1 = decode_batch1(gh, sess, prompt, a.warmup, a.steps)
+    tps1, dt1, in_token = 0.0, 0.0, None
+    if secs & {"decode", "decode1"}:  # decode1: the batch-1 token and its kernel probes only
+        r = decode_batch1(gh, sess, prompt, a.warmup, a.steps, probe=a.probe_steps)
+        tps1, dt1, in_token = r if a.probe_steps else (*r, None)
         log(f"batch-1 decode {tps1:.1f} tok/s ({dt1 * 1e3 / a.steps:.3f} ms/token)")
+        log("in-token kernels", in_token)
     lanes = None
     if a.lanes > 1:
         prompts = [gh.synth_tokens(SEED, 0x4C414E45 + i, CFG_7B["vocab_size"], a.lane_prompt)
@@ -769,7 +868,7 @@ def main():
                      roofline=step_roofline(CFG_7B, tpsL, steps_per_s, a.lanes * mean_ctx, 2))
         log(f"{a.lanes}-lane decode {tpsL:.1f} tok/s")
     sess.close()
-    f32kv = elig = leased = None
+    f32kv = elig = leased = long_ctx = None
     if "decode" in secs:
         # the same batch-1 decode on f32 KV pages, the reference's storage
         s32 = gh.Session(model, max_lanes=1, max_positions=max_pos, kv_dtype=gh.F32)
@@ -785,6 +884,8 @@ def main():
         log("batch-1 decode with a 1% eligibility mask", elig)
         leased = decode_leased(gh, model, prompt, max_pos, a.warmup, a.steps)
         log("batch-1 decode on a leased lane", leased)
+        long_ctx = decode_long_context(gh, model, 2048, a.warmup, min(a.steps, 32))
+        log("batch-1 decode at 2048 context", long_ctx)
     c5 = bench_c5(gh, model) if "c5" in secs else None
     prefill = bench_prefill(gh, model, [512, 2048]) if not a.no_prefill else None
     model.close()
@@ -801,6 +902,15 @@ def main():
             # the reference serves one lane per quantum with the serial token
             # loop (F10): its multi-lane rate is its single-lane rate
             c5["vs_cpu_reference"] = round(c5["decode_tokens_per_s"] / cpu["value"], 1)
+    if in_token:
+        # the line's roofline: the gate/up launch that runs in the token
+        # (input mode, deferred RMSNorm, SwiGLU emitting down's planes)
+        g = in_token["gate_up"]
+        roofline = dict(bound="hbm", achieved=g["gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
+                        frac=g["frac"], traffic=measured_traffic("gate_up_7b_in_token_pmc.md"),
+                        kernel="gemv_kernel<1, true, 256, EPI_SWIGLU, true> (7B gate/up in the "
+                               "batch-1 token)", avg_us=g["avg_us"],
+                        bytes_per_launch=g["bytes_per_launch"])
     out = dict(
         metric="decode tok/s at batch 1 (7B INT4)", value=round(tps1, 2), unit="tokens/s",
         n_gpus=1, steps=a.steps, warmup=a.warmup, ms_per_step=round(dt1 * 1e3 / max(a.steps, 1), 4),
@@ -809,10 +919,10 @@ def main():
         config=dict(workload="Qwen2.5-7B-shaped INT4 g32 greedy decode, batch 1",
                     prompt_len=a.prompt, kv="fp16 paged, 16 positions/page",
                     parallelism="single GPU"),
-        roofline=roofline, cpu_baseline=cpu, host=host_info(ctx),
+        roofline=roofline, in_token_kernels=in_token, cpu_baseline=cpu, host=host_info(ctx),
         decode_roofline=step_roofline(CFG_7B, tps1, tps1, a.prompt + a.warmup + a.steps / 2 + 1, 2)
         if tps1 else None,
-        decode_f32_kv=f32kv, decode_eligible=elig, decode_leased=leased, lanes32=lanes, c5_laneweave=c5, c1_qwen05b=c1, prefill=prefill, attention=attn,
+        decode_f32_kv=f32kv, decode_eligible=elig, decode_leased=leased, decode_2048=long_ctx, lanes32=lanes, c5_laneweave=c5, c1_qwen05b=c1, prefill=prefill, attention=attn,
         gemv=([dom] if dom else []) + gemv)
     print(json.dumps(out))
 

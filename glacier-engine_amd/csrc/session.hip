@@ -157,6 +157,20 @@ struct glacier_hip_session {
   float *tap_x = nullptr;
   uint32_t tap_rows = 0;
   bool tap_now = false;
+  // kernel probe: with a kind (GLACIER_HIP_PROBE_*), each decode step
+  // records HIP events on the step stream around that launch in every layer
+  // (direct launches, as the traced step) and adds their elapsed times
+  int probe_kind = -1;
+  bool probe_now = false;
+  std::vector<hipEvent_t> probe_ev;
+  uint32_t probe_used = 0;
+  double probe_ms = 0.0;
+  uint64_t probe_count = 0;
+  // probe replay: enqueue_layers launches only this kind (-1: every launch);
+  // the last decode step's shape, which a replay repeats
+  int probe_only = -1;
+  uint32_t last_rows = 0;
+  bool last_fused = false;
   PreparedWave prep;
   // sealed step plans: key = (rows, with_head, eligible, prehead, fused
   // attention + O). The step's launches are captured once (every host-side
@@ -1005,10 +1019,21 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
   q.head_dim = (int)c.head_dim;
   // deferred RMSNorm partial sums, for consumers that run in input mode
   float *ss = chain && rows <= kInputModeRows ? s->ss_parts : nullptr;
-  hipError_t e = gk::launch_gather_rows(m->embed, rp.tokens, rows, D, s->x_res, st, ss);
-  if (e != hipSuccess) return e;
+  // a probe replay launches one kind only; the others' outputs stay as the
+  // last step left them
+  auto keep = [&](int kind) { return s->probe_only < 0 || s->probe_only == kind; };
+  hipError_t e = hipSuccess;
+  if (s->probe_only < 0) {
+    e = gk::launch_gather_rows(m->embed, rp.tokens, rows, D, s->x_res, st, ss);
+    if (e != hipSuccess) return e;
+  }
   int ss_count = ss ? gk::gather_ss_parts(D) : 0;  // partial sums behind x_res
   bool x_planes = false;  // GEMM path: the previous down emitted this layer's QKV planes
+  auto mark = [&](int kind) -> hipError_t {
+    if (!s->probe_now || s->probe_kind != kind || s->probe_used >= s->probe_ev.size())
+      return hipSuccess;
+    return hipEventRecord(s->probe_ev[s->probe_used++], st);
+  };
   for (uint32_t l = 0; l < c.num_layers; ++l) {
     const LayerDev &L = m->layers[l];
     q.layer = (int)l;
@@ -1030,14 +1055,18 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
     ProjOut qout;
     qout.bias = L.qkv_bias;
     qout.qkv = &q;
-    e = run_proj(s, L.qkv, Dq, rows, gk::EPI_QKV, qin, qout, st);
+    if ((e = mark(GLACIER_HIP_PROBE_QKV)) != hipSuccess) return e;
+    if (keep(GLACIER_HIP_PROBE_QKV)) e = run_proj(s, L.qkv, Dq, rows, gk::EPI_QKV, qin, qout, st);
     if (e != hipSuccess) return e;
+    if ((e = mark(GLACIER_HIP_PROBE_QKV)) != hipSuccess) return e;
     ProjOut gout;
     if (fused) {
       // one lane: attention + the O projection (+ residual, partial sums of
       // h for gate/up's norm) in one launch, then gate/up as in the chain
-      e = gk::launch_attn_o(attn_o_args(s, rp, l, ss), st);
+      if ((e = mark(GLACIER_HIP_PROBE_ATTENTION)) != hipSuccess) return e;
+      if (keep(GLACIER_HIP_PROBE_ATTENTION)) e = gk::launch_attn_o(attn_o_args(s, rp, l, ss), st);
       if (e != hipSuccess) return e;
+      if ((e = mark(GLACIER_HIP_PROBE_ATTENTION)) != hipSuccess) return e;
       ss_count = gk::attn_o_groups((int)c.dim);
       ProjIn gin;
       gin.x = s->h;
@@ -1045,8 +1074,10 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
       gin.ss = ss;
       gin.ss_count = ss_count;
       gout.emit = gk::PlanesDst{s->act_q2, s->act_meta2, Dd};
-      e = run_proj(s, L.gu, Dg, rows, gk::EPI_SWIGLU, gin, gout, st);
+      if ((e = mark(GLACIER_HIP_PROBE_GATE_UP)) != hipSuccess) return e;
+      if (keep(GLACIER_HIP_PROBE_GATE_UP)) e = run_proj(s, L.gu, Dg, rows, gk::EPI_SWIGLU, gin, gout, st);
       if (e != hipSuccess) return e;
+      if ((e = mark(GLACIER_HIP_PROBE_GATE_UP)) != hipSuccess) return e;
     } else {
       // attention: a prompt chunk of one lane past the GEMV size runs the
       // prefill kernel, other steps the decode kernel, which for up to 32 rows
@@ -1056,7 +1087,10 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
       const bool o_planes = !pf_attn && rows <= 32 && (uint32_t)rows <= s->planes2_rows;
       const gk::PlanesDst opd = o_planes ? gk::PlanesDst{s->act_q2, s->act_meta2, Do}
                                          : gk::PlanesDst{nullptr, nullptr, 1};
-      if (pf_attn)
+      if ((e = mark(GLACIER_HIP_PROBE_ATTENTION)) != hipSuccess) return e;
+      if (!keep(GLACIER_HIP_PROBE_ATTENTION))
+        e = hipSuccess;
+      else if (pf_attn)
         e = gk::launch_attention_prefill(s->q, s->kv_pool, s->page_table, (int)s->max_pages,
                                          rp.chunk_lane, rp.chunk_pos0, rows, (int)l,
                                          (int)c.num_layers, (int)c.num_heads, (int)c.num_kv_heads,
@@ -1068,6 +1102,7 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
                                  (int)c.head_dim, (int)s->opt.max_positions, s->att_scratch,
                                  s->attn, st, opd);
       if (e != hipSuccess) return e;
+      if ((e = mark(GLACIER_HIP_PROBE_ATTENTION)) != hipSuccess) return e;
       // O projection + residual (chain: partial sums of h for gate/up's norm)
       ProjIn oin;
       ProjOut oout;
@@ -1092,8 +1127,10 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
           oout.emit_norm_w = nullptr;
         }
       }
-      e = run_proj(s, L.o, Do, rows, gk::EPI_RESID, oin, oout, st);
+      if ((e = mark(GLACIER_HIP_PROBE_O)) != hipSuccess) return e;
+      if (keep(GLACIER_HIP_PROBE_O)) e = run_proj(s, L.o, Do, rows, gk::EPI_RESID, oin, oout, st);
       if (e != hipSuccess) return e;
+      if ((e = mark(GLACIER_HIP_PROBE_O)) != hipSuccess) return e;
       // gate/up + SwiGLU (decode sizes: emitted straight into down's planes)
       ProjIn gin;
       if (oout.emit.q) {
@@ -1116,8 +1153,10 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
           gout.y = s->act;
         }
       }
-      e = run_proj(s, L.gu, Dg, rows, gk::EPI_SWIGLU, gin, gout, st);
+      if ((e = mark(GLACIER_HIP_PROBE_GATE_UP)) != hipSuccess) return e;
+      if (keep(GLACIER_HIP_PROBE_GATE_UP)) e = run_proj(s, L.gu, Dg, rows, gk::EPI_SWIGLU, gin, gout, st);
       if (e != hipSuccess) return e;
+      if ((e = mark(GLACIER_HIP_PROBE_GATE_UP)) != hipSuccess) return e;
     }
     // down + residual (chain: partial sums of x_res for the next norm)
     ProjIn din;
@@ -1147,8 +1186,10 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
         dout.emit_norm_w = nullptr;
       }
     }
-    e = run_proj(s, L.down, Dd, rows, gk::EPI_RESID, din, dout, st);
+    if ((e = mark(GLACIER_HIP_PROBE_DOWN)) != hipSuccess) return e;
+    if (keep(GLACIER_HIP_PROBE_DOWN)) e = run_proj(s, L.down, Dd, rows, gk::EPI_RESID, din, dout, st);
     if (e != hipSuccess) return e;
+    if ((e = mark(GLACIER_HIP_PROBE_DOWN)) != hipSuccess) return e;
     if (s->tap_now) {
       e = hipMemcpyAsync(s->tap_x + (size_t)l * rows * D, s->x_res, (size_t)rows * D * 4,
                          hipMemcpyDeviceToDevice, st);
@@ -1229,6 +1270,7 @@ void destroy_session(glacier_hip_session *s) {
     if (g.exec) (void)hipGraphExecDestroy(g.exec);
     if (g.graph) (void)hipGraphDestroy(g.graph);
   }
+  for (hipEvent_t ev : s->probe_ev) (void)hipEventDestroy(ev);
   delete s;
 }
 
@@ -1468,10 +1510,12 @@ int run_step(glacier_hip_session *s, const uint32_t *lanes, const uint32_t *toke
   const bool pre = elig && s->head_domain == GLACIER_HIP_HEAD_DOMAIN_PREHEAD;
   const bool fused = count == 1 && txns[0].pos + 1 <= kFusedMaxCtx && attn_o_usable(s);
   s->tap_now = s->tap_x != nullptr;
-  if (s->tap_now) {  // a traced step launches directly (its copies are not plan nodes)
-    s->tap_rows = count;
+  s->probe_now = s->probe_kind >= 0;
+  s->probe_used = 0;
+  if (s->tap_now || s->probe_now) {  // a traced or probed step launches directly
+    if (s->tap_now) s->tap_rows = count;
     e = enqueue_step(s, (int)count, head, elig, pre, fused, st);
-    s->tap_now = false;
+    s->tap_now = s->probe_now = false;
     if (e != hipSuccess) return fail(e, "enqueue traced step");
   } else if (s->opt.use_graph) {
     glacier_hip_session::GraphEntry *plan = nullptr;
@@ -1514,6 +1558,8 @@ int run_step(glacier_hip_session *s, const uint32_t *lanes, const uint32_t *toke
     e = enqueue_step(s, (int)count, head, elig, pre, fused, st);
     if (e != hipSuccess) return fail(e, "enqueue step");
   }
+  s->last_rows = count;
+  s->last_fused = fused;
   if (head) {
     e = hipMemcpyAsync(s->res_host, s->arg_result, count * sizeof(gk::ArgmaxResult),
                        hipMemcpyDeviceToHost, st);
@@ -1526,6 +1572,14 @@ int run_step(glacier_hip_session *s, const uint32_t *lanes, const uint32_t *toke
   }
   e = hipStreamSynchronize(st);
   if (e != hipSuccess) return fail(e, "step sync");
+  for (uint32_t i = 0; i + 1 < s->probe_used; i += 2) {
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, s->probe_ev[i], s->probe_ev[i + 1]) == hipSuccess) {
+      s->probe_ms += ms;
+      s->probe_count++;
+    }
+  }
+  s->probe_used = 0;
   if (s->inject_failure) {
     abort_rows(s, txns);
     return GLACIER_HIP_DEVICE_ERROR;
@@ -1939,6 +1993,62 @@ int glacier_hip_session_layer_trace(glacier_hip_session *s, float *out_host, uin
   GH_CHECK(s->model->ctx, hipMemcpy(out_host, s->tap_x, (size_t)c.num_layers * s->tap_rows * c.dim * 4,
                                     hipMemcpyDeviceToHost));
   *rows_out = s->tap_rows;
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_session_probe_kernel(glacier_hip_session *s, int kind) {
+  if (!s) return GLACIER_HIP_INVALID_HANDLE;
+  if (kind < -1 || kind > GLACIER_HIP_PROBE_DOWN) return GLACIER_HIP_INVALID_ARGUMENT;
+  GH_SUBMISSION(s->model->ctx);
+  glacier_hip_context *ctx = s->model->ctx;
+  const size_t need = 2 * (size_t)s->model->cfg.num_layers;
+  while (kind >= 0 && s->probe_ev.size() < need) {
+    hipEvent_t ev;
+    GH_CHECK(ctx, hipEventCreate(&ev));
+    s->probe_ev.push_back(ev);
+  }
+  s->probe_kind = kind;
+  s->probe_ms = 0.0;
+  s->probe_count = 0;
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_session_probe_replay(glacier_hip_session *s, int kind, uint32_t reps, double *avg_us) {
+  if (!s || !avg_us || reps == 0) return GLACIER_HIP_INVALID_ARGUMENT;
+  // only launches whose outputs are step scratch (the next step rewrites them)
+  if (kind != GLACIER_HIP_PROBE_GATE_UP && kind != GLACIER_HIP_PROBE_DOWN)
+    return GLACIER_HIP_INVALID_ARGUMENT;
+  GH_SUBMISSION(s->model->ctx);
+  if (s->prep.active) return GLACIER_HIP_TRANSACTION_ACTIVE;
+  if (s->last_rows == 0) return GLACIER_HIP_INVALID_TRANSACTION;  // no decode step yet
+  glacier_hip_context *ctx = s->model->ctx;
+  hipStream_t st = ctx->stream;
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  GH_CHECK(ctx, hipEventCreate(&ev[0]));
+  hipError_t e = hipEventCreate(&ev[1]);
+  const RowPtrs rp{s->step_dev->tokens, s->step_dev->lane_of_row, s->step_dev->pos_of_row,
+                   s->step_dev->ctx_len, s->step_dev->row0};
+  s->probe_only = kind;
+  if (e == hipSuccess) e = hipEventRecord(ev[0], st);
+  for (uint32_t r = 0; r < reps && e == hipSuccess; ++r)
+    e = enqueue_layers(s, (int)s->last_rows, rp, st, s->last_fused);
+  if (e == hipSuccess) e = hipEventRecord(ev[1], st);
+  s->probe_only = -1;
+  const hipError_t es = hipStreamSynchronize(st);
+  float ms = 0.0f;
+  if (e == hipSuccess) e = es;
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, ev[0], ev[1]);
+  (void)hipEventDestroy(ev[0]);
+  if (ev[1]) (void)hipEventDestroy(ev[1]);
+  if (e != hipSuccess) return hip_fail(ctx, e, "probe replay");
+  *avg_us = ms * 1000.0 / ((double)reps * s->model->cfg.num_layers);
+  return GLACIER_HIP_OK;
+}
+
+int glacier_hip_session_probe_read(glacier_hip_session *s, double *total_us, uint64_t *launches) {
+  if (!s || !total_us || !launches) return GLACIER_HIP_INVALID_ARGUMENT;
+  *total_us = s->probe_ms * 1000.0;
+  *launches = s->probe_count;
   return GLACIER_HIP_OK;
 }
 

@@ -666,6 +666,9 @@ _SIGS = [
     ("glacier_hip_kv_pages_ledger", C.c_int, [_P, C.POINTER(ResidentLedger)]),
     ("glacier_hip_session_inject_failure", C.c_int, [_P, C.c_int]),
     ("glacier_hip_session_trace_layers", C.c_int, [_P, C.c_int]),
+    ("glacier_hip_session_probe_kernel", C.c_int, [_P, C.c_int]),
+    ("glacier_hip_session_probe_replay", C.c_int, [_P, C.c_int, C.c_uint32, C.POINTER(C.c_double)]),
+    ("glacier_hip_session_probe_read", C.c_int, [_P, C.POINTER(C.c_double), C.POINTER(C.c_uint64)]),
     ("glacier_hip_session_layer_trace", C.c_int, [_P, _P, C.POINTER(C.c_uint32)]),
     ("glacier_hip_session_prefill_staged", C.c_int, [_P, C.c_uint32, _P, C.c_uint32, _P, _P]),
     ("glacier_hip_session_step_prepare", C.c_int,
@@ -1362,6 +1365,28 @@ class Session:
 
     def trace_layers(self, enable):
         check(lib().glacier_hip_session_trace_layers(self.h, 1 if enable else 0), "trace_layers")
+
+    PROBE = dict(qkv=0, attention=1, o=2, gate_up=3, down=4)
+
+    def probe_kernel(self, kind):
+        """Time one in-token launch per layer with HIP events (kind: a PROBE
+        key, or None to stop); resets the totals."""
+        check(lib().glacier_hip_session_probe_kernel(self.h, -1 if kind is None
+                                                     else self.PROBE[kind]), "probe_kernel")
+
+    def probe_replay(self, kind, reps=4):
+        """Average microseconds of the last step's `kind` (gate_up / down)
+        launches replayed back to back over every layer."""
+        us = C.c_double()
+        check(lib().glacier_hip_session_probe_replay(self.h, self.PROBE[kind], reps, C.byref(us)),
+              "probe_replay", self.model.ctx.h)
+        return us.value
+
+    def probe_read(self):
+        """(total microseconds, launches) since the last probe_kernel."""
+        us, n = C.c_double(), C.c_uint64()
+        check(lib().glacier_hip_session_probe_read(self.h, C.byref(us), C.byref(n)), "probe_read")
+        return us.value, n.value
 
     def layer_trace(self):
         """The last traced step's residual after every layer: [num_layers, rows, dim]."""

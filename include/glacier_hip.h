@@ -1561,6 +1561,21 @@ int glacier_hip_token_proposal_v3_sha256(const glacier_hip_token_proposal_v3_t *
                                          uint8_t out[32]);
 int glacier_hip_token_commit_v3_sha256(const uint8_t proposal_sha256[32],
                                        const glacier_hip_prepare_ack_v1_t *ack, uint8_t out[32]);
+/* Kernel probe (a measurement hook of this library, no reference
+ * counterpart): with kind >= 0 every later decode step launches directly
+ * and records HIP events on its stream around that launch of every layer,
+ * adding the elapsed times; -1 turns it off. Each call resets the totals. */
+enum { GLACIER_HIP_PROBE_QKV = 0, GLACIER_HIP_PROBE_ATTENTION = 1, GLACIER_HIP_PROBE_O = 2,
+       GLACIER_HIP_PROBE_GATE_UP = 3, GLACIER_HIP_PROBE_DOWN = 4 };
+int glacier_hip_session_probe_kernel(glacier_hip_session *s, int kind);
+int glacier_hip_session_probe_read(glacier_hip_session *s, double *total_us, uint64_t *launches);
+/* Replays the last decode step's gate/up or down launches of all layers
+ * (kind GLACIER_HIP_PROBE_GATE_UP / _DOWN: launches that write only step
+ * scratch) `reps` times back to back on the step stream, with the step's
+ * own inputs and each layer's weights, HIP events around the whole run;
+ * *avg_us = elapsed / (reps x layers). Lane state is not touched. */
+int glacier_hip_session_probe_replay(glacier_hip_session *s, int kind, uint32_t reps, double *avg_us);
+
 /* step_prepare for a wave whose lanes are all leased lanes of one cohort,
  * sealed as ProposalV3 (Batch.begin :1117-1250). terminal_reason[i]: 0, or
  * 1 + the TerminalReason of lane i's token (eos / max_tokens / cancelled).

@@ -617,3 +617,34 @@ def test_lane_weave_wave_sink_rejection_publishes_nothing(gh, gctx, tiny, ora):
             assert got[i] == want, (i, got[i], want)
     finally:
         sess.close()
+
+
+def test_kernel_probes_leave_the_lane_unchanged(gh, tiny):
+    """The measurement hooks (per-launch events, back-to-back replay of the
+    last step's gate/up and down launches) change no token: a lane probed
+    and replayed between its steps decodes the oracle's sequence."""
+    host, om, m = tiny
+    prompt = gh.synth_tokens(SEED, 131, TINY["vocab_size"], 19)
+    max_new = 12
+    want = om.generate(prompt, max_new)[0].tolist()
+    sess = gh.Session(m, max_lanes=1, max_positions=64)
+    try:
+        sess.begin(0)
+        with pytest.raises(gh.GlacierHipError):
+            sess.probe_replay("gate_up")  # no decode step yet
+        toks = [sess.prefill(0, prompt)]
+        kinds = ["gate_up", "down", "attention", "qkv", None]
+        for i in range(max_new - 1):
+            sess.probe_kernel(kinds[i % len(kinds)])
+            toks.append(int(sess.step([0], [toks[-1]])[0]))
+            if kinds[i % len(kinds)]:
+                us, n = sess.probe_read()
+                assert n == TINY["num_layers"] and us > 0
+            for k in ("gate_up", "down"):
+                assert sess.probe_replay(k, 2) > 0
+        sess.probe_kernel(None)
+        with pytest.raises(gh.GlacierHipError):
+            sess.probe_replay("qkv")  # writes lane state: not replayable
+        assert toks == want
+    finally:
+        sess.close()
