@@ -1,6 +1,9 @@
 // host_util.cpp — SHA-256 from FIPS 180-4 and IEEE binary16 conversion.
 #include "host_util.h"
 
+#include <cpuid.h>
+#include <immintrin.h>
+
 namespace gh {
 
 static const uint32_t K[64] = {
@@ -36,15 +39,77 @@ static void compress(uint32_t h[8], const uint8_t *p) {
   h[0] += a; h[1] += b; h[2] += c; h[3] += d; h[4] += e; h[5] += f; h[6] += g; h[7] += hh;
 }
 
+// The same compression with the x86 SHA extensions (SHA-256 rounds two at
+// a time, the message schedule in 4-word groups), used when the CPU has them.
+// State registers hold (A, B, E, F) and (C, D, G, H).
+__attribute__((target("sha,sse4.1,ssse3"))) static void compress_shani(uint32_t h[8],
+                                                                        const uint8_t *p,
+                                                                        size_t blocks) {
+  const __m128i bswap = _mm_set_epi64x(0x0c0d0e0f08090a0bLL, 0x0405060700010203LL);
+  __m128i tmp = _mm_shuffle_epi32(_mm_loadu_si128((const __m128i *)&h[0]), 0xB1);  // C D A B
+  __m128i s1 = _mm_shuffle_epi32(_mm_loadu_si128((const __m128i *)&h[4]), 0x1B);   // H G F E
+  __m128i s0 = _mm_alignr_epi8(tmp, s1, 8);                                         // A B E F
+  s1 = _mm_blend_epi16(s1, tmp, 0xF0);                                              // C D G H
+  for (; blocks; --blocks, p += 64) {
+    const __m128i save0 = s0, save1 = s1;
+    __m128i w[4];
+    for (int g = 0; g < 16; ++g) {
+      __m128i m;
+      if (g < 4) {
+        m = _mm_shuffle_epi8(_mm_loadu_si128((const __m128i *)(p + 16 * g)), bswap);
+      } else {  // W[t..t+3] = sigma1 terms + W[t-7..] + W[t-16..] + sigma0 terms
+        m = _mm_sha256msg1_epu32(w[g & 3], w[(g + 1) & 3]);
+        m = _mm_add_epi32(m, _mm_alignr_epi8(w[(g + 3) & 3], w[(g + 2) & 3], 4));
+        m = _mm_sha256msg2_epu32(m, w[(g + 3) & 3]);
+      }
+      w[g & 3] = m;
+      __m128i k = _mm_add_epi32(m, _mm_loadu_si128((const __m128i *)&K[4 * g]));
+      s1 = _mm_sha256rnds2_epu32(s1, s0, k);
+      s0 = _mm_sha256rnds2_epu32(s0, s1, _mm_shuffle_epi32(k, 0x0E));
+    }
+    s0 = _mm_add_epi32(s0, save0);
+    s1 = _mm_add_epi32(s1, save1);
+  }
+  tmp = _mm_shuffle_epi32(s0, 0x1B);       // F E B A
+  s1 = _mm_shuffle_epi32(s1, 0xB1);        // D C H G
+  s0 = _mm_blend_epi16(tmp, s1, 0xF0);     // D C B A
+  s1 = _mm_alignr_epi8(s1, tmp, 8);        // H G F E
+  _mm_storeu_si128((__m128i *)&h[0], s0);
+  _mm_storeu_si128((__m128i *)&h[4], s1);
+}
+
+static bool have_shani() {
+  static const bool yes = [] {
+    unsigned a, b, c, d;
+    if (!__get_cpuid(1, &a, &b, &c, &d) || !(c & bit_SSE4_1) || !(c & bit_SSSE3)) return false;
+    if (!__get_cpuid_count(7, 0, &a, &b, &c, &d)) return false;
+    return (b & (1u << 29)) != 0;  // CPUID.(7,0):EBX.SHA
+  }();
+  return yes;
+}
+
+static void compress_blocks(uint32_t h[8], const uint8_t *p, size_t blocks) {
+  if (have_shani()) {
+    compress_shani(h, p, blocks);
+    return;
+  }
+  for (; blocks; --blocks, p += 64) compress(h, p);
+}
+
 Sha256::Sha256() {
   static const uint32_t iv[8] = {0x6a09e667, 0xbb67ae85, 0x3c6ef372, 0xa54ff53a,
                                  0x510e527f, 0x9b05688c, 0x1f83d9ab, 0x5be0cd19};
   memcpy(h, iv, sizeof iv);
 }
 
-void Sha256::update(const void *data, size_t n) {
+void Sha256::update_blocks(const void *data, size_t n) {
   const uint8_t *p = (const uint8_t *)data;
   len += n;
+  if (fill == 0 && n >= 64) {  // whole blocks straight from the input
+    compress_blocks(h, p, n / 64);
+    p += n / 64 * 64;
+    n %= 64;
+  }
   while (n) {
     size_t take = std::min(64 - fill, n);
     memcpy(buf + fill, p, take);
@@ -52,7 +117,7 @@ void Sha256::update(const void *data, size_t n) {
     p += take;
     n -= take;
     if (fill == 64) {
-      compress(h, buf);
+      compress_blocks(h, buf, 1);
       fill = 0;
     }
   }

@@ -18,7 +18,18 @@ struct Sha256 {
   uint8_t buf[64];
   size_t fill = 0;
   Sha256();
-  void update(const void *data, size_t n);
+  // bytes that fit the partial block are buffered inline (most fields are a
+  // few bytes); whole blocks go to the compression
+  void update(const void *data, size_t n) {
+    if (n < 64 - fill) {
+      if (n) memcpy(buf + fill, data, n);
+      fill += n;
+      len += n;
+      return;
+    }
+    update_blocks(data, n);
+  }
+  void update_blocks(const void *data, size_t n);
   void final(uint8_t out[32]);
   void u64(uint64_t v) {
     uint8_t b[8];

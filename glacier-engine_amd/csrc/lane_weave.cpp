@@ -383,9 +383,12 @@ struct glacier_hip_lane_weave {
     uint32_t active, finished;
     Claim used;
   };
-  Before before() const {
+  Before before(const uint8_t *state = nullptr) const {  // state: its digest, if known
     Before b;
-    state_sha(b.state);
+    if (state)
+      memcpy(b.state, state, 32);
+    else
+      state_sha(b.state);
     b.tick = tick;
     b.cursor = cursor;
     b.level = level;
@@ -726,15 +729,24 @@ int select_service_locked(glacier_hip_lane_weave *lw, Selection *sel, uint64_t *
 }
 
 // serveOne (:1196-1270) with lw->mu held.
-int serve_one_locked(glacier_hip_lane_weave *lw, glacier_hip_lane_event_t *out) {
+int serve_one_locked(glacier_hip_lane_weave *lw, glacier_hip_lane_event_t *out,
+                     const Selection *pre = nullptr, uint64_t pre_wait = 0,
+                     const uint8_t *pre_state = nullptr) {
+  // (pre: the selection, wait and state digest a permit's commit has just
+  // validated against the current state)
   if (lw->poisoned) return GLACIER_HIP_SCHEDULER_POISONED;
   if (lw->closed) return GLACIER_HIP_SCHEDULER_CLOSED;
   Selection sel;
   uint64_t wait = 0;
-  if (int rc = select_service_locked(lw, &sel, &wait)) return rc;
+  if (pre) {
+    sel = *pre;
+    wait = pre_wait;
+  } else if (int rc = select_service_locked(lw, &sel, &wait)) {
+    return rc;
+  }
   Slot &s = lw->slots[sel.index];
   const uint64_t after_tick = lw->tick + 1;
-  const auto b = lw->before();
+  const auto b = lw->before(pre_state);
   Event e{};
   e.handle = lw->handle_for(sel.index);
   e.spec = s.spec;
@@ -817,9 +829,11 @@ int validate_pending_locked(glacier_hip_lane_weave *lw, const Permit &p) {
 }
 
 // validateServiceBeforeState (:2512-2531): nothing logical moved since prepare.
-int validate_before_state_locked(glacier_hip_lane_weave *lw, const Permit &p) {
+int validate_before_state_locked(glacier_hip_lane_weave *lw, const Permit &p,
+                                 uint8_t *state_out = nullptr) {
   uint8_t st[32];
   lw->state_sha(st);
+  if (state_out) memcpy(state_out, st, 32);
   if (memcmp(st, p.state_before_sha256, 32) != 0 || p.event_sequence != lw->next_seq ||
       p.logical_tick_before != lw->tick || memcmp(p.chain_head_before_sha256, lw->chain_head, 32) != 0) {
     lw->poisoned = true;
@@ -835,7 +849,8 @@ int commit_service_locked(glacier_hip_lane_weave *lw, const Permit &p, Event *ou
   if (lw->poisoned) return GLACIER_HIP_SCHEDULER_POISONED;
   if (lw->closed) return GLACIER_HIP_SCHEDULER_CLOSED;
   if (int rc = validate_pending_locked(lw, p)) return rc;
-  if (int rc = validate_before_state_locked(lw, p)) return rc;
+  uint8_t state[32];
+  if (int rc = validate_before_state_locked(lw, p, state)) return rc;
   Selection sel;
   uint64_t wait = 0;
   int rc = select_service_locked(lw, &sel, &wait);
@@ -849,7 +864,7 @@ int commit_service_locked(glacier_hip_lane_weave *lw, const Permit &p, Event *ou
     return GLACIER_HIP_SCHEDULER_POISONED;
   }
   lw->pending = false;
-  return serve_one_locked(lw, out);
+  return serve_one_locked(lw, out, &sel, wait, state);
 }
 
 // abortService (:1438-1452): the pending permit consumed, nothing logical changes.
