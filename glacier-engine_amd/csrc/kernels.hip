@@ -201,7 +201,10 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
   const int epi = EPI >= 0 ? EPI : a.epi;
   extern __shared__ __align__(16) unsigned char smem[];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // (wave-uniform by construction; readfirstlane tells the compiler, so the
+  // weight loop's bounds and branches are scalar and a load under a branch
+  // needs no merge that waits for its data)
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int KS = a.ksplit;
   const int NB = a.N >> 4, KQ = a.K >> 7, G = a.K >> 5;
   const int M = a.M;
@@ -225,41 +228,63 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
   const int nq = skip_block ? 0 : kq1 - kq0;
   const int n_local = lane & 15, c = lane >> 4;
 
-  // The first U quads of weights are requested before the activation planes
-  // are staged, so the staging latency hides under the weight fetch.
+  // Request order: the activation staging first (L2-resident, consumed
+  // first), then the first U quads of weights, then the first level of the
+  // epilogue inputs. Loads complete in issue order, so staging issued after
+  // the weights would wait out the weights' HBM latency before the next
+  // quads could be requested.
   const size_t tile0 = (size_t)min(nb, NB - 1) * KQ + kq0;
-  // (every lane loads its own 16-byte tile slot; the MFMA path transposes
-  // the words across lanes at use)
-  const uint4 *cp = a.codes + tile0 * 64 + lane;
-  const uint16_t *spp = (const uint16_t *)a.scales + tile0 * 64;
-  // (the scales too: one u16 per lane in its slot's order; the MFMA path
-  // redistributes them across lanes at use)
-  uint4 wb[U];
-  uint32_t sb[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u)
-    if (u < nq) {
-      wb[u] = load_stream(cp + (size_t)u * 64);
-      sb[u] = spp[(size_t)u * 64 + lane];
-    }
-
+  // (every lane loads its own 16-byte tile slot; a skipped row block reads
+  // the first tile, which stays cached, so no branch changes the number of
+  // loads in flight)
+  const size_t tq = nq > 0 ? tile0 : 0;
+  const uint4 *cp = a.codes + tq * 64 + lane;
+  // (the scales too: one u16 per lane in its slot's order, read as the dword
+  // that holds the lane's pair; a 16-bit load's register is merged with
+  // others, and the merge waits for the data, serialising the loads)
+  const uint32_t *spp = (const uint32_t *)a.scales + tq * 32 + (lane >> 1);
+  const int shalf = (lane & 1) * 16;
   // Epilogue inputs of the (at most two) rows of a dot4 launch: the first
-  // level now, with the weights and the input staging in flight; the second
-  // level (page slot, RoPE factors) after the staging barrier, under the
-  // weight stream.
+  // level with the weights in flight; the second level (page slot, RoPE
+  // factors) after the staging barrier, under the weight stream.
   // (every lane loads, with the row block clamped into range, so no branch
   // splits the wave and the loads issue back to back)
   EpiIn epre[2];
   const int nb_c = min(nb, NB - 1);
-  if constexpr (DOT4 && MR == 2) {
+  // Two register buffers of U quads alternate: the quads of one are dotted
+  // while the next U quads stream into the other, so a wave always has a
+  // buffer's loads in flight (refilling a single buffer drains it to zero
+  // first); both are requested before the staging wait.
+  // (a refill loads all U slots, a slot past the wave's last quad from the
+  // last quad again, computed and not added: loads under a per-slot branch
+  // leave the compiler a path with fewer loads in flight, and its waits are
+  // then counted for that path)
+  uint4 wb[U], wd[U];
+  uint32_t sb[U], sd[U];
+  // (scheduling barriers keep a refill after the dot of the buffer it
+  // overwrites: hoisted above it, the refill needs fresh registers and a
+  // wait for the data in flight)
+  auto fetch = [&](uint4(&w)[U], uint32_t(&sv)[U], int qb) {
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int m = 0; m < 2; ++m)
-      if (ks == 0 && m < M) epi_load1(epre[m], a, epi, nb_c, n_local, m);
-  }
-  // Requests before any wait: the deferred-RMSNorm partial sums of this
-  // wave's first input row (row = wave), then the first pass of the input
-  // staging; the weights above are already in flight, so all three
-  // latencies overlap.
+    for (int u = 0; u < U; ++u) {
+      const int uq = max(min(qb + u, nq - 1), 0);
+      w[u] = load_stream(cp + (size_t)uq * 64);
+      sv[u] = spp[(size_t)uq * 32];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto prefetch0 = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(wb, sb, 0);
+    fetch(wd, sd, U);
+    if constexpr (DOT4 && MR == 2) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+        if (ks == 0 && m < M) epi_load1(epre[m], a, epi, nb_c, n_local, m);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
   const int nthr = (int)blockDim.x;
   const size_t qbytes = (size_t)G * D * M * 32;
   const size_t mbytes = (size_t)G * M * sizeof(ActMeta);
@@ -299,6 +324,7 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
       }
     };
     load_chunks(0);
+    prefetch0();
     // 1/rms of each input row from the producer's partial sums of squares
     // (wave w reduces rows w, w + waves, ...; fixed order)
     if (a.in_ss) {
@@ -383,27 +409,33 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
     __syncthreads();
   } else if (LDS_A) {
     // copy the producer's planes and meta into LDS: the first pass (all of
-    // it for decode shapes) issues its five loads before the first store
+    // it at one or two rows up to K = 32768 with 512 threads) requests its
+    // loads before the weights and stores after them
+    constexpr int SP = 8, SM = 2;
     const int n16 = (int)(qbytes / 16), n8 = (int)(mbytes / 8);
     const uint4 *src = (const uint4 *)a.act_q;
     uint4 *dst = (uint4 *)smem;
     const uint2 *msrc = (const uint2 *)a.act_meta;
     uint2 *mdst = (uint2 *)(smem + qbytes);
     const int t = (int)threadIdx.x;
-    const uint4 v0 = src[min(t, n16 - 1)];
-    const uint4 v1 = src[min(t + nthr, n16 - 1)];
-    const uint4 v2 = src[min(t + 2 * nthr, n16 - 1)];
-    const uint4 v3 = src[min(t + 3 * nthr, n16 - 1)];
-    const uint2 mv = msrc[min(t, n8 - 1)];
-    __builtin_amdgcn_sched_barrier(0);
-    if (t < n16) dst[t] = v0;
-    if (t + nthr < n16) dst[t + nthr] = v1;
-    if (t + 2 * nthr < n16) dst[t + 2 * nthr] = v2;
-    if (t + 3 * nthr < n16) dst[t + 3 * nthr] = v3;
-    if (t < n8) mdst[t] = mv;
-    for (int i = t + 4 * nthr; i < n16; i += nthr) dst[i] = src[i];
-    for (int i = t + nthr; i < n8; i += nthr) mdst[i] = msrc[i];
+    // (named registers: an array of them is kept in scratch memory)
+#define GK_LDQ(i) const uint4 v##i = src[min(t + i * nthr, n16 - 1)]
+    GK_LDQ(0); GK_LDQ(1); GK_LDQ(2); GK_LDQ(3); GK_LDQ(4); GK_LDQ(5); GK_LDQ(6); GK_LDQ(7);
+#undef GK_LDQ
+    const uint2 m0 = msrc[min(t, n8 - 1)];
+    const uint2 m1 = msrc[min(t + nthr, n8 - 1)];
+    prefetch0();
+#define GK_STQ(i) \
+  if (t + i * nthr < n16) dst[t + i * nthr] = v##i
+    GK_STQ(0); GK_STQ(1); GK_STQ(2); GK_STQ(3); GK_STQ(4); GK_STQ(5); GK_STQ(6); GK_STQ(7);
+#undef GK_STQ
+    if (t < n8) mdst[t] = m0;
+    if (t + nthr < n8) mdst[t + nthr] = m1;
+    for (int i = t + SP * nthr; i < n16; i += nthr) dst[i] = src[i];
+    for (int i = t + SM * nthr; i < n8; i += nthr) mdst[i] = msrc[i];
     __syncthreads();
+  } else {
+    prefetch0();
   }
   if constexpr (DOT4 && MR == 2) {
 #pragma unroll
@@ -419,58 +451,60 @@ __global__ __launch_bounds__(LB) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[mt][r] = 0.0f;
 
-  if (nb < NB) {
-    for (int q = 0; q < nq; q += U) {
-      uint4 wc[U];
-      uint32_t sc[U];
-      if constexpr (DOT4) {
-        // all U quads move to the working registers, then U new ones are
-        // requested
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          wc[u] = wb[u];
-          sc[u] = sb[u];
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-          if (q + U + u < nq) {
-            wb[u] = load_stream(cp + (size_t)(q + U + u) * 64);
-            sb[u] = spp[(size_t)(q + U + u) * 64 + lane];
-          }
-      }
+  if (nb < NB && nq > 0) {
+    auto dot = [&](const uint4(&w)[U], const uint32_t(&sv)[U], int qb) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        if (q + u >= nq) break;
-        {
-          // lane (j = c, n): all 32 codes of group g of row n
-          const int g = (kq0 + q + u) * 4 + c;
-          const uint32_t wj[4] = {wc[u].x, wc[u].y, wc[u].z, wc[u].w};
-          const float ws = h2f(sc[u]);
+        const bool live = qb + u < nq;
+        // lane (j = c, n): all 32 codes of group g of row n (a slot past the
+        // end reads the last quad's planes: finite, and not added)
+        const int g = (kq0 + min(qb + u, nq - 1)) * 4 + c;
+        const uint32_t wj[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+        const float ws = h2f((uint16_t)(sv[u] >> shalf));
 #pragma unroll
-          for (int m = 0; m < 2; ++m) {
-            if (m >= M) break;
-            int T = 0;
+        for (int m = 0; m < 2; ++m) {
+          if (m > 0 && m >= M) break;
+          int T = 0;
 #pragma unroll
-            for (int d = 0; d < D; ++d) {
-              const int4 q0 = *(const int4 *)(aq + (((size_t)g * D + d) * M + m) * 32);
-              const int4 q1 = *(const int4 *)(aq + (((size_t)g * D + d) * M + m) * 32 + 16);
-              const int qa[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-              int t = 0;
+          for (int d = 0; d < D; ++d) {
+            const int4 q0 = *(const int4 *)(aq + (((size_t)g * D + d) * M + m) * 32);
+            const int4 q1 = *(const int4 *)(aq + (((size_t)g * D + d) * M + m) * 32 + 16);
+            const int qa[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+            int t = 0;
 #pragma unroll
-              for (int w = 0; w < 4; ++w) {
-                t = __builtin_amdgcn_sdot4((int)(wj[w] & 0x0F0F0F0Fu), qa[2 * w], t, false);
-                t = __builtin_amdgcn_sdot4((int)((wj[w] >> 4) & 0x0F0F0F0Fu), qa[2 * w + 1], t, false);
-              }
-              T = T * 128 + t;
+            for (int i = 0; i < 4; ++i) {
+              t = __builtin_amdgcn_sdot4((int)(wj[i] & 0x0F0F0F0Fu), qa[2 * i], t, false);
+              t = __builtin_amdgcn_sdot4((int)((wj[i] >> 4) & 0x0F0F0F0Fu), qa[2 * i + 1], t, false);
             }
-            const ActMeta mm = am[(size_t)g * M + m];
-            const float v = (float)(T - mm.corr);
-            float tt = v * ws;
-            tt = tt * mm.scale;
-            acc[0][m] += tt;
+            T = T * 128 + t;
           }
+          const ActMeta mm = am[(size_t)g * M + m];
+          const float v = (float)(T - mm.corr);
+          float tt = v * ws;
+          tt = tt * mm.scale;
+          acc[0][m] = live ? acc[0][m] + tt : acc[0][m];
         }
       }
+    };
+    // Buffers i (wb) and i + 1 (wd) are in flight at the top of each
+    // iteration. (a straight-line body with one exit: the compiler counts its
+    // waits along this one path, each dot waiting for its own buffer only)
+    const int nbuf = (nq + U - 1) / U;
+    int i = 0;
+    for (; i + 4 <= nbuf; i += 2) {
+      dot(wb, sb, i * U);
+      fetch(wb, sb, (i + 2) * U);
+      dot(wd, sd, (i + 1) * U);
+      fetch(wd, sd, (i + 3) * U);
+    }
+    const int rest = nbuf - i;  // 1..3
+    dot(wb, sb, i * U);
+    if (rest == 3) {
+      fetch(wb, sb, (i + 2) * U);
+      dot(wd, sd, (i + 1) * U);
+      dot(wb, sb, (i + 2) * U);
+    } else if (rest == 2) {
+      dot(wd, sd, (i + 1) * U);
     }
   }
 
