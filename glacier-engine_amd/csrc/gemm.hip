@@ -47,6 +47,7 @@ namespace {
 
 constexpr int kWaves = 4;            // waves per workgroup, side by side in N
 constexpr int kU = 2;                // weight quads in flight per wave
+constexpr int kFoldSplits = 4;       // K splits a folded tile adds at most
 
 // Per-quad activation staging of a BM-row tile: digit planes
 // [4 groups][D][BM rows][32] then the scales [4][BM].
@@ -100,10 +101,13 @@ __device__ __forceinline__ void act_store(unsigned char *buf, const ActRegs<D, B
 // kRB: 16-row weight blocks per wave (1, 2 or 4; the workgroup covers 4 kRB);
 // BM: activation rows per workgroup (16, 32 or 64). The K quads are split over
 // blockIdx.y (ks_count splits); with part set each split writes its partial
-// sums to part [ks_count][M][N] (no epilogue; a finishing kernel runs it).
+// sums to part [ks_count][M][N] (no epilogue; a finishing kernel runs it),
+// unless fold: then the splits of a tile meet at p.splitk_counters and the
+// last to arrive runs the epilogue (the SwiGLU plane emission included).
 template <int D, int kRB, int BM>
 __global__ __launch_bounds__(256, kRB == 4 ? 2 : kRB == 2 ? 4 : 5) void gemm_kernel(GemvArgs p, int m_tiles,
-                                                                     int ks_count, float *part) {
+                                                                     int ks_count, float *part,
+                                                                     int fold) {
   using S = ActStage<D, BM>;
   constexpr int MT = BM / 16;         // 16-row activation tiles per wave
   constexpr int kNBW = kWaves * kRB;  // weight row blocks per workgroup
@@ -251,7 +255,109 @@ __global__ __launch_bounds__(256, kRB == 4 ? 2 : kRB == 2 ? 4 : 5) void gemm_ker
   }
 
   // Lane (c, n) holds rows m0 + 16 mt + 4c + r of column 16 nb + n.
-  if (part) {
+  // (the fold is compiled into tiles of up to 32 rows only: in the 64-row
+  // prompt-chunk tiles its registers would spill the whole kernel)
+  if (BM <= 32 && fold) {
+    if (ks_count > 1) {
+      // Publish this split's partial sums; the tile's last split to arrive
+      // adds every split's in split order (the finishing kernel's order, so
+      // the sums are the same) and runs the epilogue. The publication is the
+      // cross-workgroup contract attn_o_kernel's merge documents:
+      // agent-scope stores written through to the level every XCD reads,
+      // waited for (s_waitcnt covers stores), then an agent-scope counter
+      // increment; the last arriver reads with agent-scope loads.
+      const size_t MN = (size_t)p.M * p.N;
+      float *dst = part + (size_t)blockIdx.y * MN;
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int m = m0 + 16 * mt + 4 * c + r, nb = nb0 + rb;
+            if (m < p.M && nb < NB)
+              __hip_atomic_store(dst + (size_t)m * p.N + nb * 16 + n_local, acc[rb][mt][r],
+                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+      __builtin_amdgcn_s_waitcnt(0);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __syncthreads();
+      __shared__ int tile_last;
+      if (threadIdx.x == 0)
+        tile_last = __hip_atomic_fetch_add(p.splitk_counters + blockIdx.x, 1u, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(ks_count - 1);
+      __syncthreads();
+      if (!tile_last) return;
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      // one (row block, row tile) at a time: its up to kFoldSplits splits'
+      // loads issued together, then added in split order
+#pragma unroll
+      for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          float v[kFoldSplits][4];
+#pragma unroll
+          for (int sp = 0; sp < kFoldSplits; ++sp)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int m = m0 + 16 * mt + 4 * c + r, nb = nb0 + rb;
+              const size_t idx = m < p.M && nb < NB ? (size_t)m * p.N + nb * 16 + n_local : 0;
+              v[sp][r] = sp < ks_count ? __hip_atomic_load(part + sp * MN + idx, __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT)
+                                       : 0.0f;
+            }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float tot = v[0][r];
+#pragma unroll
+            for (int sp = 1; sp < kFoldSplits; ++sp)
+              if (sp < ks_count) tot += v[sp][r];
+            acc[rb][mt][r] = tot;
+          }
+        }
+      if (threadIdx.x == 0)
+        __hip_atomic_store(p.splitk_counters + blockIdx.x, 0u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if constexpr (BM * 32 * kRB * 4 <= 2 * S::kBufBytes) {
+      if (p.epi == EPI_SWIGLU && p.out_q) {
+        // The SwiGLU plane emission of splitk_swiglu_emit_kernel for this
+        // tile: its 4 kRB row blocks hold 32 kRB SwiGLU outputs (kRB whole
+        // quantisation groups) of each activation row; silu(g) * u into LDS
+        // [BM][32 kRB], then a half-wave quantises each (row, group).
+        constexpr int NO = 32 * kRB;
+        float *stage = (float *)lds;
+        __syncthreads();  // the staging buffers were last read before the loop's end
+#pragma unroll
+        for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float tot = acc[rb][mt][r];
+              const float partner = row_xor8(tot);
+              if (n_local < 8)
+                stage[(16 * mt + 4 * c + r) * NO + (wave * kRB + rb) * 8 + n_local] =
+                    silu_mul(tot, partner);
+            }
+        __syncthreads();
+        const int No = p.N >> 1;
+        const int half = threadIdx.x >> 5, hl = threadIdx.x & 31;
+        for (int it = half; it < BM * kRB; it += 8) {
+          const int row = it / kRB, gl = it % kRB, m = m0 + row;
+          const int o = (n_tile * kNBW) * 8 + gl * 32 + hl;  // SwiGLU output index
+          if (m >= p.M || o >= No) continue;  // whole half-waves: No is a multiple of 32
+          const float v = stage[row * NO + gl * 32 + hl];
+          if (p.y) p.y[(size_t)m * No + o] = v;
+          if (p.out_D == 1)
+            quantize_group<1>(v, hl, o >> 5, m, p.M, p.out_q, p.out_meta);
+          else
+            quantize_group<3>(v, hl, o >> 5, m, p.M, p.out_q, p.out_meta);
+        }
+        return;
+      }
+    }
+  } else if (part) {
     // split K (or a finishing pass that emits planes): this split's partial
     // sums, part[split][m][n]
     float *dst = part + (size_t)blockIdx.y * p.M * p.N;
@@ -551,9 +657,23 @@ hipError_t launch_gemm(const GemvArgs &a, hipStream_t st) {
   const bool emit = a.out_q != nullptr;
   if (emit && !gemm_emit_ok(a)) return hipErrorInvalidValue;
   const dim3 grid(s.grid, s.ks), block(256);
-  float *part = s.ks > 1 || emit ? a.splitk_ws : nullptr;
-#define GK_GEMM(DD, RB, BM) \
-  hipLaunchKernelGGL((gemm_kernel<DD, RB, BM>), grid, block, 0, st, a, s.m_tiles, s.ks, part)
+  // the last-arriving split finishes its tile (no finishing kernel) when the
+  // counters cover the grid, the tile has at most 32 rows and kFoldSplits
+  // splits (their partial sums are read at once), and the epilogue is the
+  // tile's own: any but the residual plane emission (whole-row RMSNorm)
+  // (never when the emitted planes overlap the input planes: a finished
+  // tile would overwrite what the others still read)
+  const size_t in_bytes = (size_t)(a.K / 32) * a.D * a.M * 32;
+  const size_t out_bytes = emit ? (size_t)(a.N / 64) * a.out_D * a.M * 32 : 0;
+  const bool overlap = emit && (const int8_t *)a.out_q < a.act_q + in_bytes &&
+                       a.act_q < (const int8_t *)a.out_q + out_bytes;
+  const bool fold = a.splitk_counters && s.grid <= a.splitk_counter_count && s.mt <= 2 &&
+                    (!emit || (a.epi == EPI_SWIGLU && !overlap)) && (s.ks > 1 || emit) &&
+                    s.ks <= kFoldSplits;
+  float *part = s.ks > 1 || (emit && !fold) ? a.splitk_ws : nullptr;
+#define GK_GEMM(DD, RB, BM)                                                                      \
+  hipLaunchKernelGGL((gemm_kernel<DD, RB, BM>), grid, block, 0, st, a, s.m_tiles, s.ks, part, \
+                     fold ? 1 : 0)
 #define GK_GEMM_BM(DD, RB) \
   do {                       \
     if (s.mt == 1) GK_GEMM(DD, RB, 16);                           \
@@ -568,7 +688,7 @@ hipError_t launch_gemm(const GemvArgs &a, hipStream_t st) {
 #undef GK_GEMM_BM
 #undef GK_GEMM
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || fold) return e;
   if (emit) {
     const float *pc = part;
     const unsigned sw_grid = (unsigned)(((size_t)a.M * (a.N / 2) + 255) / 256);

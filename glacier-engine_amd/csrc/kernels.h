@@ -122,6 +122,13 @@ struct GemvArgs {
   // GEMM split-K workspace (floats); null: no K split
   float *splitk_ws;
   size_t splitk_ws_floats;
+  // GEMM split-K counters [splitk_counter_count], zero between launches:
+  // with them, a tile's K splits meet at a counter and the last to arrive
+  // adds the partial sums and runs the tile's epilogue, so no finishing
+  // kernel runs (for every epilogue but the residual plane emission, whose
+  // RMSNorm needs whole rows)
+  unsigned *splitk_counters;
+  int splitk_counter_count;
   // GEMM with out_q set (launch_gemm, when gemm_emit_ok): the finishing
   // pass also writes the next projection's digit planes [G][out_D][M][32] +
   // meta. EPI_SWIGLU: the SwiGLU outputs (width N/2); EPI_RESID: y after

@@ -135,6 +135,7 @@ struct glacier_hip_session {
   uint32_t planes2_rows = 0;        // rows act_q2 / act_meta2 hold
   float *splitk_ws = nullptr;       // GEMM split-K partial sums
   size_t splitk_floats = 0;
+  unsigned *splitk_counters = nullptr;  // GEMM split-K arrivals per tile (0 at rest)
   float *ss_parts = nullptr;        // deferred RMSNorm partial sums [32][1024]
   float *o_parts = nullptr;         // fused attention + O: [num_kv_heads][dim]
   unsigned *o_counters = nullptr;   // fused attention + O: arrivals per row group (0 at rest)
@@ -824,6 +825,10 @@ struct ProjOut {
   bool prehead = false;                     // skip row blocks with no eligible row
 };
 
+// GEMM tiles whose K splits can meet at a counter (the largest decode-lane
+// grids are about 1200 tiles)
+constexpr int kSplitkCounters = 4096;
+
 gk::GemvArgs proj_args(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, int rows,
                        int epi, const ProjIn &in, const ProjOut &out) {
   gk::GemvArgs a{};
@@ -852,6 +857,8 @@ gk::GemvArgs proj_args(glacier_hip_session *s, glacier_hip_int4_weight *w, int D
   a.in_eps = s->model->cfg.rms_eps;
   a.splitk_ws = s->splitk_ws;
   a.splitk_ws_floats = s->splitk_floats;
+  a.splitk_counters = s->splitk_counters;
+  a.splitk_counter_count = s->splitk_counters ? kSplitkCounters : 0;
   return a;
 }
 
@@ -1145,9 +1152,13 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
       if (chain) {
         gout.emit = gk::PlanesDst{s->act_q2, s->act_meta2, Dd};
       } else {
-        // GEMM: down's planes from gate/up's finishing pass (into act_q, which
-        // gate/up has finished reading by then), else the SwiGLU rows
-        gout.emit = gk::PlanesDst{s->act_q, s->act_meta, Dd};
+        // GEMM: down's planes from gate/up's finishing pass, else the SwiGLU
+        // rows; into act_q2 (free once O has read attention's planes) up to
+        // the rows it holds, so the last K split of each tile can emit its
+        // tile while the others still read act_q, else into act_q (which
+        // gate/up has finished reading by the finishing pass)
+        gout.emit = (uint32_t)rows <= s->planes2_rows ? gk::PlanesDst{s->act_q2, s->act_meta2, Dd}
+                                                      : gk::PlanesDst{s->act_q, s->act_meta, Dd};
         if (!gemm_emit_ok(s, L.gu, Dg, rows, gk::EPI_SWIGLU, gout)) {
           gout.emit = gk::PlanesDst{nullptr, nullptr, 1};
           gout.y = s->act;
@@ -1259,7 +1270,7 @@ void destroy_session(glacier_hip_session *s) {
                   s->att_scratch, s->ss_parts, s->o_parts, s->o_counters, s->arg_scratch,
                   s->arg_counters,
                   s->arg_result,
-                  s->elig_words, s->splitk_ws,
+                  s->elig_words, s->splitk_ws, s->splitk_counters,
                   s->step_dev, s->pf_dev, s->tap_x};
   for (void *p : ptrs) gh::dev_free(s->model->ctx, p);
   if (s->step_host) (void)hipHostFree(s->step_host);
@@ -1880,6 +1891,7 @@ static glacier_hip_session *session_create_impl(glacier_hip_model *m,
           }
     s->splitk_floats = std::min<size_t>(need, 16u << 20);
     if (s->splitk_floats) A((void **)&s->splitk_ws, s->splitk_floats * sizeof(float));
+    A((void **)&s->splitk_counters, (size_t)kSplitkCounters * sizeof(unsigned));
   }
   A((void **)&s->arg_counters, (size_t)L * 4);
   A((void **)&s->arg_result, (size_t)L * sizeof(gk::ArgmaxResult));
@@ -1901,6 +1913,8 @@ static glacier_hip_session *session_create_impl(glacier_hip_model *m,
     ok = hipMemset(s->arg_counters, 0, (size_t)L * 4) == hipSuccess &&
          hipMemset(s->o_counters, 0,
                    (size_t)gk::attn_o_groups((int)c.dim) * sizeof(unsigned)) == hipSuccess &&
+         hipMemset(s->splitk_counters, 0, (size_t)kSplitkCounters * sizeof(unsigned)) ==
+             hipSuccess &&
          hipMemset(s->kv_pool, 0, page_bytes * s->total_pages) == hipSuccess;
     memset(s->pt_host, 0, (size_t)L * s->max_pages * 4);
     ok = ok && hipMemcpy(s->page_table, s->pt_host, (size_t)L * s->max_pages * 4,
