@@ -229,7 +229,7 @@ hipError_t launch_attention_f16(const float *q, const void *kv_pool, const int32
 // its counter to 0.
 struct AttnOArgs {
   const float *q;              // [Hq * head_dim] row 0's queries
-  const void *kv_pool;         // fp16 pages [page][L][2][16][kv_dim]
+  const void *kv_pool;         // pages [page][L][2][16][kv_dim], fp16 (f32 with kv_f32)
   const int32_t *page_table;   // [lanes][max_pages]
   int max_pages;
   const int32_t *lane_of_row;  // [1]
@@ -249,10 +249,11 @@ struct AttnOArgs {
   float *y;                    // [N]  null: parts only
   float *ss_out;               // [attn_o_groups(N)]
   unsigned *counters;          // [attn_o_groups(N)], 0 between launches
+  int kv_f32;                  // 1: f32 KV pages (the reference's storage)
 };
 constexpr int kMaxAttnOHeads = 8;  // KV heads (partial vectors) at most
 // Whether launch_attn_o supports these shapes (head_dim 64 or 128, a K
-// slice per KV head of whole 128-column quads).
+// slice per KV head of whole 32-column groups).
 bool attn_o_ok(const AttnOArgs &a);
 // Row-block groups of the fused launch (= ss_out partials, counters).
 int attn_o_groups(int N);

@@ -1177,6 +1177,44 @@ struct AttnF16Lds {
 struct AttnNoHook {
   __device__ void operator()() const {}
 };
+
+typedef float attn_f4 __attribute__((ext_vector_type(4)));
+
+// The end of an attention work item: each wave's (output, max, sum) state
+// into s (lane (c, j) holds O[head 4c + r][dim (HD / 16) * j + e] in
+// o[e][r], and head j's max and sum), then the log-sum-exp weights of the
+// waves. The weight of wave w for head g, exp(m_w - M) (0 for a wave
+// without positions), is computed once per (wave, head); every output is
+// then two short dot products over the waves, in wave order.
+template <int HD, int NW>
+static __device__ __forceinline__ void attn_item_merge(const attn_f4 (&o)[HD / 16], float mx,
+                                                       float sum, int G, AttnF16Lds<HD, NW> &s) {
+  constexpr int DPL = HD / 16, NTH = 64 * NW;
+  const int t = threadIdx.x, l = t & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int c = l >> 4, j = l & 15;
+  if (c < 2) {
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) s.so[wv][4 * c + rr][DPL * j + e] = o[e][rr];
+  }
+  if (c == 0) {
+    s.sm[wv][j] = mx;
+    s.sl[wv][j] = sum;
+  }
+  __syncthreads();
+  for (int i = t; i < NW * G; i += NTH) {
+    const int w = i / G, g = i % G;
+    float Mx = -INFINITY;
+#pragma unroll
+    for (int w2 = 0; w2 < NW; ++w2)
+      if (s.sl[w2][g] > 0.0f) Mx = fmaxf(Mx, s.sm[w2][g]);
+    s.fw[w][g] = s.sl[w][g] > 0.0f ? expf(s.sm[w][g] - Mx) : 0.0f;
+    if (w == 0) s.mg[g] = Mx;
+  }
+  __syncthreads();
+}
 template <int HD, int NT, int NW, class Hook = AttnNoHook>
 static __device__ __forceinline__ void attn_f16_item(const float *qrow, const __half *pool,
                                                      const int32_t *ptab, int n, int layer,
@@ -1184,7 +1222,7 @@ static __device__ __forceinline__ void attn_f16_item(const float *qrow, const __
                                                      AttnF16Lds<HD, NW> &s,
                                                      const Hook &after_issue = Hook()) {
   typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-  typedef float f4 __attribute__((ext_vector_type(4)));
+  typedef attn_f4 f4;
   constexpr int S = HD / 16;    // f16 MFMA steps over the head dim
   constexpr int DPL = HD / 16;  // dims per lane and V row = output blocks of P.V
   constexpr int WP = 16 * NT;   // positions per wave
@@ -1324,32 +1362,138 @@ static __device__ __forceinline__ void attn_f16_item(const float *qrow, const __
       }
     }
   }
-  // lane (c, j) holds O[head 4c + r][dim DPL * j + e]
-  if (c < 2) {
+  attn_item_merge<HD, NW>(o, mx, sum, G, s);
+}
+
+// The same work item over f32 KV pages (the reference's KV storage), with
+// the same lane layout, softmax and merge as attn_f16_item, on
+// v_mfma_f32_16x16x4f32: every product is an f32 product, as in the
+// reference's f32 attention (forward.zig:478-533), only the summation order
+// differs.
+//   scores  S^T[pos][head] = K . Q^T, one MFMA per 4 dims: lane (c, j) gives
+//           K[pos j] and q[head j] at dim c * HD / 4 + st in step st (a
+//           dot product may take its dims in any order, so each lane reads
+//           a contiguous quarter of the K row and of q, as float4s); the
+//           result tile is laid out as attn_f16_item's (lane (c, j): head
+//           j's scores of positions 4c + r);
+//   P.V     four MFMAs per page and output block e, one per r = 0..3, over
+//           positions 4c + r: the A operand is P[head j][pos 4c + r], the
+//           lane's own register, the B operand V[4c + r][DPL * j + e] from
+//           the DPL consecutive dims the lane read of each of its four V
+//           rows; lane (c, j) ends with O[head 4c + r][dim DPL * j + e].
+// Every load is unconditional from an in-range address (as there). q is
+// staged in LDS (qs, kMaxGroup * HD floats) by the whole workgroup and read
+// a float4 per step: f32 K and V rows take twice the registers of fp16 ones.
+template <int HD, int NT, int NW, class Hook = AttnNoHook>
+static __device__ __forceinline__ void attn_f32_item(const float *qrow, const float *pool,
+                                                     const int32_t *ptab, int n, int layer,
+                                                     size_t lay, int kv_dim, int h, int G,
+                                                     AttnF16Lds<HD, NW> &s, float *qs,
+                                                     const Hook &after_issue = Hook()) {
+  typedef attn_f4 f4;
+  constexpr int QD = HD / 4;    // dims per lane of q and of a K row (one MFMA step each)
+  constexpr int DPL = HD / 16;  // dims per lane and V row = output blocks of P.V
+  constexpr int WP = 16 * NT;   // positions per wave
+  const int t = threadIdx.x, l = t & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+  const float scale = 1.0f / sqrtf((float)HD);
+  const int wbase = wv * WP;
+  const int c = l >> 4, j = l & 15;
+  const int wn = max(0, min(WP, n - wbase));
+
+  f4 o[DPL];
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr)
+  for (int e = 0; e < DPL; ++e) o[e] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+  float mx = -INFINITY, sum = 0.0f;
+  // q first (G * HD floats, a float4 per thread; HD is a multiple of 4)
+  constexpr int NTH = 64 * NW;
+  static_assert(kMaxGroup * HD / 4 <= NTH, "one float4 of q per thread");
+  const int nq4 = G * HD / 4;
+  const float4 qload = *(const float4 *)(qrow + 4 * min(t, nq4 - 1));
+  float4 kr[NT][QD / 4];
+  float4 vr[NT][4][DPL / 4];
+  if (wn > 0) {
+    const int32_t *pt = ptab + wbase / 16;
+    int pg[NT];
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) s.so[wv][4 * c + rr][DPL * j + e] = o[e][rr];
+    for (int T = 0; T < NT; ++T) pg[T] = pt[16 * T < wn ? T : 0];
+#pragma unroll
+    for (int T = 0; T < NT; ++T) {
+      const size_t pbase = ((size_t)pg[T] * lay + layer) * 2;
+      const float *krow = pool + ((pbase + 0) * 16 + j) * kv_dim + (size_t)h * HD + c * QD;
+#pragma unroll
+      for (int i = 0; i < QD / 4; ++i) kr[T][i] = *(const float4 *)(krow + 4 * i);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const float *vrow =
+            pool + ((pbase + 1) * 16 + 4 * c + rr) * kv_dim + (size_t)h * HD + DPL * j;
+#pragma unroll
+        for (int i = 0; i < DPL / 4; ++i) vr[T][rr][i] = *(const float4 *)(vrow + 4 * i);
+      }
+    }
   }
-  if (c == 0) {
-    s.sm[wv][j] = mx;
-    s.sl[wv][j] = sum;
+  if constexpr (!std::is_same<Hook, AttnNoHook>::value) {
+    __builtin_amdgcn_sched_barrier(0);
+    after_issue();
+    __builtin_amdgcn_sched_barrier(0);
   }
+  // (q's load was the first issued, so this wait leaves K and V in flight)
+  if (t < nq4) *(float4 *)(qs + 4 * t) = qload;
   __syncthreads();
-  // ---- merge the waves (log-sum-exp) ----
-  // The weight of wave w for head g, exp(m_w - M) (0 for a wave without
-  // positions), is computed once per (wave, head); every output is then two
-  // short dot products over the waves, in wave order.
-  for (int i = t; i < NW * G; i += NTH) {
-    const int w = i / G, g = i % G;
-    float Mx = -INFINITY;
+  if (wn > 0) {
+    // lanes of heads past G take q = 0 (their rows are never read)
+    const bool qon = j < G;
+    const float *qr = qs + (j < G ? j : 0) * HD + c * QD;
+    f4 sc[NT];
 #pragma unroll
-    for (int w2 = 0; w2 < NW; ++w2)
-      if (s.sl[w2][g] > 0.0f) Mx = fmaxf(Mx, s.sm[w2][g]);
-    s.fw[w][g] = s.sl[w][g] > 0.0f ? expf(s.sm[w][g] - Mx) : 0.0f;
-    if (w == 0) s.mg[g] = Mx;
+    for (int T = 0; T < NT; ++T) {
+      f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int i = 0; i < QD / 4; ++i) {
+        const float ka[4] = {kr[T][i].x, kr[T][i].y, kr[T][i].z, kr[T][i].w};
+        const float4 qv = *(const float4 *)(qr + 4 * i);
+        const float qa[4] = {qon ? qv.x : 0.0f, qon ? qv.y : 0.0f, qon ? qv.z : 0.0f,
+                             qon ? qv.w : 0.0f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[e], qa[e], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const float v = acc[rr] * scale;
+        sc[T][rr] = 16 * T + 4 * c + rr < wn ? v : -INFINITY;
+        mx = fmaxf(mx, sc[T][rr]);
+      }
+    }
+    mx = xor32_max(xor16_max(mx));
+#pragma unroll
+    for (int T = 0; T < NT; ++T)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const float p = expf(sc[T][rr] - mx);
+        sc[T][rr] = p;
+        sum += p;
+      }
+    sum = xor32_add(xor16_add(sum));
+#pragma unroll
+    for (int T = 0; T < NT; ++T) {
+      // V rows past the item are zeroed (P is 0 there, but a stale row
+      // might hold an infinity)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        if (16 * T + 4 * c + rr >= wn)
+#pragma unroll
+          for (int i = 0; i < DPL / 4; ++i) vr[T][rr][i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const float *vf = (const float *)&vr[T][rr][0];
+#pragma unroll
+        for (int e = 0; e < DPL; ++e)
+          o[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(sc[T][rr], vf[e], o[e], 0, 0, 0);
+      }
+    }
   }
-  __syncthreads();
+  attn_item_merge<HD, NW>(o, mx, sum, G, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -1450,6 +1594,7 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(
 // O projection (AttnOArgs). Workgroup (bg, h) first requests its wave's O
 // weights (row block bg * NW + wave, the KQS quads of slice h) and its rows'
 // residuals, then runs the attention items of row 0's context for KV head h
+// (attn_f16_item over fp16 pages, attn_f32_item over f32 pages)
 // (CH positions each; more than one merge in registers by log-sum-exp),
 // quantises the G * hd outputs into Q8 planes in LDS exactly as the O
 // projection's input planes are quantised (int4_matmul.zig:380-398), and
@@ -1463,7 +1608,7 @@ __global__ __launch_bounds__(64 * NW) void attn_f16_kernel(
 // With the round-robin placement of workgroups on the 8 XCDs, blockIdx % Hkv
 // = h puts every workgroup of one KV head on the same 8 / Hkv XCDs, whose L2s
 // then serve its K/V rows after the first read.
-template <int HD, int NT, int NW>
+template <int HD, int NT, int NW, bool KV32>
 __global__ __launch_bounds__(64 * NW) void attn_o_kernel(AttnOArgs a) {
   constexpr int WP = 16 * NT, CH = NW * WP, NTH = 64 * NW, RG = 16 * NW;
   constexpr int KQM = kMaxGroup * HD / 128;  // quads of the largest slice
@@ -1474,18 +1619,23 @@ __global__ __launch_bounds__(64 * NW) void attn_o_kernel(AttnOArgs a) {
   const int Hkv = a.num_kv_heads;
   const int h = blockIdx.x % Hkv, bg = blockIdx.x / Hkv;
   const int G = a.num_heads / Hkv, SL = G * HD;
-  const int KQ = a.K >> 7, KQS = SL >> 7, NB = a.N >> 4;
+  const int KQ = a.K >> 7, NB = a.N >> 4;
+  // slice h of the O input: groups g_first .. g_first + SG - 1, over quads
+  // q_first .. q_first + KQS - 1 (4 groups a quad; with head_dim 64 the
+  // first and last quad can be shared with the neighbouring slice)
+  const int SG = SL >> 5, g_first = h * SG, q_first = g_first >> 2;
+  const int KQS = ((g_first + SG + 3) >> 2) - q_first;
   const int nb = bg * NW + wv;
   const int n_local = l & 15, c = l >> 4;
   // the row's context and lane first: the page walk waits for them
   const int ctx = __builtin_amdgcn_readfirstlane(min(a.row0 ? a.row0[1] : a.ctx_len[0], a.max_ctx));
   const int lane = __builtin_amdgcn_readfirstlane(a.row0 ? a.row0[0] : a.lane_of_row[0]);
-  // this wave's O weights (tile slot i of quads h * KQS + i, clamped into
+  // this wave's O weights (tile slot i of quads q_first + i, clamped into
   // the slice so every slot loads) and its epilogue row's residual are
   // requested once the first attention item's loads are: vector loads
   // complete in issue order, so requested earlier they would hold up the
   // page walk
-  const size_t tile0 = (size_t)min(nb, NB - 1) * KQ + (size_t)h * KQS;
+  const size_t tile0 = (size_t)min(nb, NB - 1) * KQ + (size_t)q_first;
   const uint4 *cp = a.codes + tile0 * 64 + l;
   const uint16_t *sp = (const uint16_t *)a.scales + tile0 * 64 + l;
   uint4 wq[KQM];
@@ -1506,6 +1656,7 @@ __global__ __launch_bounds__(64 * NW) void attn_o_kernel(AttnOArgs a) {
   __shared__ ActMeta am[kMaxGroup * HD / 32];
   __shared__ float wsq[NW];
   __shared__ int last;
+  __shared__ __align__(16) float qs[KV32 ? kMaxGroup * HD : 4];  // f32 items' q
   float orun[KO], lrun[KO], mrun[KO];
 #pragma unroll
   for (int k = 0; k < KO; ++k) {
@@ -1513,7 +1664,6 @@ __global__ __launch_bounds__(64 * NW) void attn_o_kernel(AttnOArgs a) {
     lrun[k] = 0.0f;
     mrun[k] = -INFINITY;
   }
-  const __half *pool = (const __half *)a.kv_pool;
   const int32_t *prow = a.row0 && ctx <= 16 * a.row0_pages
                             ? a.row0 + 4
                             : a.page_table + (size_t)lane * a.max_pages;
@@ -1521,10 +1671,17 @@ __global__ __launch_bounds__(64 * NW) void attn_o_kernel(AttnOArgs a) {
   if (nch == 0) load_weights();
   for (int ch = 0; ch < nch; ++ch) {
     const int j0 = ch * CH;
-    attn_f16_item<HD, NT, NW>(a.q + (size_t)h * SL, pool, prow + j0 / 16, min(CH, ctx - j0),
-                              a.layer, (size_t)a.num_layers, Hkv * HD, h, G, s, [&]() {
-                                if (ch == 0) load_weights();
-                              });
+    const auto hook = [&]() {
+      if (ch == 0) load_weights();
+    };
+    if constexpr (KV32)
+      attn_f32_item<HD, NT, NW>(a.q + (size_t)h * SL, (const float *)a.kv_pool, prow + j0 / 16,
+                                min(CH, ctx - j0), a.layer, (size_t)a.num_layers, Hkv * HD, h, G,
+                                s, qs, hook);
+    else
+      attn_f16_item<HD, NT, NW>(a.q + (size_t)h * SL, (const __half *)a.kv_pool, prow + j0 / 16,
+                                min(CH, ctx - j0), a.layer, (size_t)a.num_layers, Hkv * HD, h, G,
+                                s, hook);
 #pragma unroll
     for (int k = 0; k < KO; ++k) {
       const int oi = t + NTH * k;
@@ -1563,12 +1720,15 @@ __global__ __launch_bounds__(64 * NW) void attn_o_kernel(AttnOArgs a) {
   }
   __syncthreads();
   if (nb < NB) {
-    // lane (c, n): group 4 i + c of the slice, row n of the block
+    // lane (c, n): group 4 (q_first + i) + c of the input, row n of the
+    // block; a group outside the slice adds exactly 0
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < KQM; ++i) {
       if (i >= KQS) break;
-      const int g = 4 * i + c;
+      const int gl = 4 * (q_first + i) + c - g_first;  // group within the slice
+      const bool in = gl >= 0 && gl < SG;
+      const int g = in ? gl : 0;
       const uint32_t wj[4] = {wq[i].x, wq[i].y, wq[i].z, wq[i].w};
       const int4 q0 = *(const int4 *)(aq + g * 32);
       const int4 q1 = *(const int4 *)(aq + g * 32 + 16);
@@ -1583,7 +1743,7 @@ __global__ __launch_bounds__(64 * NW) void attn_o_kernel(AttnOArgs a) {
       const float v = (float)(T - mm.corr);
       float tt = v * h2f(wsc[i]);
       tt = tt * mm.scale;
-      acc += tt;
+      acc += in ? tt : 0.0f;
     }
     acc = xor32_add(xor16_add(acc));
     // agent-scope store: written through to the level all XCDs read (see
@@ -1787,7 +1947,12 @@ bool attn_o_ok(const AttnOArgs &a) {
     return false;
   const int G = a.num_heads / a.num_kv_heads;
   if (a.y && (!a.resid || !a.ss_out || !a.counters)) return false;
-  return G <= kMaxGroup && (G * hd) % 128 == 0 && a.K == a.num_heads * hd && a.N > 0 &&
+  // every slice is whole 32-column groups on at most the quads a workgroup
+  // holds (kMaxGroup * hd / 128)
+  const int SG = G * hd / 32;
+  for (int h = 0; h < a.num_kv_heads; ++h)
+    if ((h * SG + SG + 3) / 4 - (h * SG) / 4 > kMaxGroup * hd / 128) return false;
+  return G <= kMaxGroup && (G * hd) % 32 == 0 && a.K == a.num_heads * hd && a.N > 0 &&
          a.N % 16 == 0 && a.max_ctx >= 1 && a.max_pages >= 1 && a.codes && a.scales && a.parts &&
          a.q && a.kv_pool && a.page_table && a.lane_of_row && a.ctx_len;
 }
@@ -1795,12 +1960,15 @@ bool attn_o_ok(const AttnOArgs &a) {
 hipError_t launch_attn_o(const AttnOArgs &a, hipStream_t st) {
   if (!attn_o_ok(a)) return hipErrorInvalidValue;
   const unsigned grid = (unsigned)(attn_o_groups(a.N) * a.num_kv_heads);
-  if (a.head_dim == 64)
-    hipLaunchKernelGGL((attn_o_kernel<64, kAttnONT, kAttnONW>), dim3(grid), dim3(64 * kAttnONW), 0,
-                       st, a);
-  else
-    hipLaunchKernelGGL((attn_o_kernel<128, kAttnONT, kAttnONW>), dim3(grid),
-                       dim3(64 * kAttnONW), 0, st, a);
+#define GK_ATTN_O(HD, KV32) \
+  hipLaunchKernelGGL((attn_o_kernel<HD, kAttnONT, kAttnONW, KV32>), dim3(grid), \
+                     dim3(64 * kAttnONW), 0, st, a)
+  if (a.head_dim == 64) {
+    if (a.kv_f32) GK_ATTN_O(64, true); else GK_ATTN_O(64, false);
+  } else {
+    if (a.kv_f32) GK_ATTN_O(128, true); else GK_ATTN_O(128, false);
+  }
+#undef GK_ATTN_O
   return hipGetLastError();
 }
 

@@ -975,6 +975,7 @@ gk::AttnOArgs attn_o_args(glacier_hip_session *s, const RowPtrs &rp, uint32_t l,
   a.y = s->h;
   a.ss_out = ss;
   a.counters = s->o_counters;
+  a.kv_f32 = s->opt.kv_dtype == GLACIER_HIP_F32 ? 1 : 0;
   return a;
 }
 
@@ -984,13 +985,14 @@ gk::AttnOArgs attn_o_args(glacier_hip_session *s, const RowPtrs &rp, uint32_t l,
 constexpr uint32_t kFusedMaxCtx = 256;
 
 // Whether one-lane decode steps can run attention and the O projection as
-// one launch: fp16 KV, Q8 inputs for O, shapes the fused kernel takes, and
-// its row groups within the partial sums gate/up reads; not when the
-// session options ask for two launches.
+// one launch: fp16 or f32 KV, Q8 inputs for O, shapes the fused kernel
+// takes, and its row groups within the partial sums gate/up reads; not when
+// the session options ask for two launches.
 bool attn_o_usable(glacier_hip_session *s) {
   if (s->attn_o >= 0) return s->attn_o == 1;
   const auto &c = s->model->cfg;
-  bool ok = !s->opt.split_attention_o && s->opt.kv_dtype == GLACIER_HIP_F16 &&
+  bool ok = !s->opt.split_attention_o &&
+            (s->opt.kv_dtype == GLACIER_HIP_F16 || s->opt.kv_dtype == GLACIER_HIP_F32) &&
             s->planes2_rows >= 1 && s->o_parts && s->o_counters && s->ss_parts;
   const RowPtrs rp{s->step_dev->tokens, s->step_dev->lane_of_row, s->step_dev->pos_of_row,
                    s->step_dev->ctx_len};

@@ -378,7 +378,8 @@ int glacier_hip_paged_attention_prefill(glacier_hip_context *ctx, const float *q
  * parts_dev[h][n] = sum over the slice of W_o[n][k] * a[k] (Q8 group
  * arithmetic of glacier_hip_int4_gemv). The sum over h is the O projection
  * of the attention output. num_kv_heads <= 8, head_dim 64 or 128, a slice
- * of whole 128-column tiles; o_weight is [out_f][num_heads * head_dim].
+ * of whole 32-column groups (with head_dim 64 a slice may share a 128-column
+ * tile with its neighbour); o_weight is [out_f][num_heads * head_dim].
  * Asynchronous on `stream`; launches only. */
 int glacier_hip_paged_attention_o(glacier_hip_context *ctx, const float *q_dev,
                                   const void *kv_pool_dev, const int32_t *page_table_dev,

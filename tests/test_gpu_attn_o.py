@@ -1,6 +1,6 @@
 """The one-lane decode launch that fuses attention with the O projection
 (glacier_hip_paged_attention_o; sessions use it for one-lane steps at
-contexts up to 256 positions with fp16 KV).
+contexts up to 256 positions with fp16 or f32 KV).
 
 Kernel parity: every KV head's partial vector parts[h] = W_o[:, slice h] .
 Q8(attention[slice h]) against the oracle's Q8 matvec (linear_int4_q8,
@@ -16,7 +16,9 @@ Q8 code can round the other way, and the bar against the oracle's own
 attention is 5e-3. Session parity: fused and two-launch sessions give the
 same greedy tokens and logits within 5e-2 of each other (the bar of the
 fp16-KV tiny-model test, whose 2-layer model amplifies single Q8 code flips),
-and the oracle's tokens."""
+and the oracle's tokens. With head_dim 64 and 7 query heads per KV head (the
+0.5B model's 14 / 2) a slice is 448 columns, 3.5 tiles: the two KV heads
+share the middle tile, each adding only its own groups."""
 import numpy as np
 import pytest
 
@@ -64,7 +66,7 @@ def _run(gh, gctx, pool, pt, q, w, ctx, Hq, Hkv, hd, out_f, L=3, layer=1):
 
 
 @pytest.mark.parametrize("geom,out_f", [((28, 4, 128), 512), ((4, 2, 64), 256),
-                                        ((8, 2, 64), 384)])
+                                        ((8, 2, 64), 384), ((14, 2, 64), 896)])
 @pytest.mark.parametrize("ctx", [1, 15, 16, 17, 100, 255, 256, 257, 300, 700, 1030])
 def test_parts_match_oracle(gh, gctx, ora, geom, out_f, ctx):
     Hq, Hkv, hd = geom
@@ -100,10 +102,16 @@ def test_rejects_unsupported_shapes(gh, gctx):
     s16 = gh.synth_scales_f16(3, 2, 512 * 14 * 64 // 32)
     w = gctx.weight(packed, s16, 14 * 64, 512)
     try:
-        # 14 q / 2 kv heads of 64: a KV head's slice is 448 columns, not whole tiles
-        rc = gh.lib().glacier_hip_paged_attention_o(gctx.h, p, p, p, 4, p, 0, 1, 14, 2, 64, 64,
-                                                    w, p, None)
-        assert rc == gh.SHAPE_MISMATCH
+        # 9 query heads per KV head: more than the 8 a workgroup takes
+        packed9 = gh.synth_int4(3, 1, 512 * 18 * 64 // 2)
+        s9 = gh.synth_scales_f16(3, 2, 512 * 18 * 64 // 32)
+        w9 = gctx.weight(packed9, s9, 18 * 64, 512)
+        try:
+            rc = gh.lib().glacier_hip_paged_attention_o(gctx.h, p, p, p, 4, p, 0, 1, 18, 2, 64,
+                                                        64, w9, p, None)
+            assert rc == gh.SHAPE_MISMATCH
+        finally:
+            gh.lib().glacier_hip_int4_weight_destroy(w9)
         # weight width must be num_heads * head_dim
         rc = gh.lib().glacier_hip_paged_attention_o(gctx.h, p, p, p, 4, p, 0, 1, 16, 2, 64, 64,
                                                     w, p, None)
@@ -144,16 +152,19 @@ def _decode(sess, prompt, n):
     return toks, logits
 
 
+@pytest.mark.parametrize("kv", ["f16", "f32"])
 @pytest.mark.parametrize("prompt_len,steps", [(20, 30), (230, 50)])
-def test_fused_session_matches_two_launches_and_oracle(gh, tiny, ora, prompt_len, steps):
+def test_fused_session_matches_two_launches_and_oracle(gh, tiny, ora, prompt_len, steps, kv):
     """(230, 50) crosses 256 positions: the session switches from the fused
-    launch to the two launches mid-run (another cached graph)."""
+    launch to the two launches mid-run (another cached graph). f32 KV pages
+    (the reference's storage) run the fused launch's f32 work item
+    (v_mfma_f32_16x16x4f32) against the two-launch path's f32 attention."""
     host, m = tiny
     prompt = gh.synth_tokens(SEED, prompt_len, TINY["vocab_size"], prompt_len)
     runs = {}
     for split in (False, True):
-        sess = gh.Session(m, max_lanes=1, max_positions=320, kv_dtype=gh.F16,
-                          split_attention_o=split)
+        sess = gh.Session(m, max_lanes=1, max_positions=320,
+                          kv_dtype=gh.F16 if kv == "f16" else gh.F32, split_attention_o=split)
         try:
             runs[split] = _decode(sess, prompt, steps)
         finally:
@@ -165,6 +176,6 @@ def test_fused_session_matches_two_launches_and_oracle(gh, tiny, ora, prompt_len
     assert tf == ts
     assert rel < 5e-2
     if prompt_len <= 32:
-        om = ora.OracleModel(TINY, host, kv_fp16=True)
+        om = ora.OracleModel(TINY, host, kv_fp16=kv == "f16")
         want, _, _, _ = om.generate(prompt, steps + 1, logits_steps=[])
         assert tf == want.tolist()
