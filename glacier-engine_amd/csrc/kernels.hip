@@ -1367,20 +1367,25 @@ static __device__ __forceinline__ void attn_f16_item(const float *qrow, const __
 
 // The same work item over f32 KV pages (the reference's KV storage), with
 // the same lane layout, softmax and merge as attn_f16_item, on
-// v_mfma_f32_16x16x4f32: every product is an f32 product, as in the
-// reference's f32 attention (forward.zig:478-533), only the summation order
-// differs.
-//   scores  S^T[pos][head] = K . Q^T, one MFMA per 4 dims: lane (c, j) gives
-//           K[pos j] and q[head j] at dim c * HD / 4 + st in step st (a
-//           dot product may take its dims in any order, so each lane reads
-//           a contiguous quarter of the K row and of q, as float4s); the
-//           result tile is laid out as attn_f16_item's (lane (c, j): head
-//           j's scores of positions 4c + r);
-//   P.V     four MFMAs per page and output block e, one per r = 0..3, over
-//           positions 4c + r: the A operand is P[head j][pos 4c + r], the
-//           lane's own register, the B operand V[4c + r][DPL * j + e] from
-//           the DPL consecutive dims the lane read of each of its four V
-//           rows; lane (c, j) ends with O[head 4c + r][dim DPL * j + e].
+// v_mfma_f32_16x16x16f16 with every f32 operand split into fp16 hi + lo
+// (x = hi + lo to ~2^-22 relative): a product is hi*hi + hi*lo + lo*hi, each
+// term exact in the f32 accumulator (the lo*lo term, ~2^-22 of the product,
+// is dropped), so scores and outputs carry f32 accuracy as in the
+// reference's f32 attention (forward.zig:478-533) up to summation order.
+// (Against v_mfma_f32_16x16x4f32 on the f32 values: three MFMAs of a
+// quarter of the cost each instead of four, 620 against 615 tok/s in the 7B
+// batch-1 token and 1261 against 1245 for the 0.5B model.)
+//   scores  S^T[pos][head] = K . Q^T, 4 dims per lane and step: lane (c, j)
+//           gives K[pos j] and q[head j] at dims c * HD / 4 + 4 st + 0..3 in
+//           step st (a dot product may take its dims in any order, so each
+//           lane reads a contiguous quarter of the K row and of q, as
+//           float4s); the result tile is laid out as attn_f16_item's (lane
+//           (c, j): head j's scores of positions 4c + r);
+//   P.V     one MFMA triple per page and output block e over positions
+//           4c .. 4c + 3: the A operand is P[head j][pos 4c + r], the lane's
+//           own registers, the B operand V[4c + r][DPL * j + e] from the DPL
+//           consecutive dims the lane read of each of its four V rows; lane
+//           (c, j) ends with O[head 4c + r][dim DPL * j + e].
 // Every load is unconditional from an in-range address (as there). q is
 // staged in LDS (qs, kMaxGroup * HD floats) by the whole workgroup and read
 // a float4 per step: f32 K and V rows take twice the registers of fp16 ones.
@@ -1391,7 +1396,17 @@ static __device__ __forceinline__ void attn_f32_item(const float *qrow, const fl
                                                      AttnF16Lds<HD, NW> &s, float *qs,
                                                      const Hook &after_issue = Hook()) {
   typedef attn_f4 f4;
-  constexpr int QD = HD / 4;    // dims per lane of q and of a K row (one MFMA step each)
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  // x = hi + lo to ~2^-22 relative, each part fp16
+  auto split_f16 = [](const float (&x)[4], h4 &hi, h4 &lo) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const _Float16 hv = (_Float16)x[e];
+      hi[e] = hv;
+      lo[e] = (_Float16)(x[e] - (float)hv);
+    }
+  };
+  constexpr int QD = HD / 4;    // dims per lane of q and of a K row (4 per MFMA step)
   constexpr int DPL = HD / 16;  // dims per lane and V row = output blocks of P.V
   constexpr int WP = 16 * NT;   // positions per wave
   const int t = threadIdx.x, l = t & 63;
@@ -1450,13 +1465,16 @@ static __device__ __forceinline__ void attn_f32_item(const float *qrow, const fl
       f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int i = 0; i < QD / 4; ++i) {
-        const float ka[4] = {kr[T][i].x, kr[T][i].y, kr[T][i].z, kr[T][i].w};
         const float4 qv = *(const float4 *)(qr + 4 * i);
         const float qa[4] = {qon ? qv.x : 0.0f, qon ? qv.y : 0.0f, qon ? qv.z : 0.0f,
                              qon ? qv.w : 0.0f};
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[e], qa[e], acc, 0, 0, 0);
+        const float ka[4] = {kr[T][i].x, kr[T][i].y, kr[T][i].z, kr[T][i].w};
+        h4 kh, kl, qh, ql;
+        split_f16(ka, kh, kl);
+        split_f16(qa, qh, ql);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, qh, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kh, ql, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kl, qh, acc, 0, 0, 0);
       }
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
@@ -1484,12 +1502,19 @@ static __device__ __forceinline__ void attn_f32_item(const float *qrow, const fl
         if (16 * T + 4 * c + rr >= wn)
 #pragma unroll
           for (int i = 0; i < DPL / 4; ++i) vr[T][rr][i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      const float pa[4] = {sc[T][0], sc[T][1], sc[T][2], sc[T][3]};
+      h4 ph, pl;
+      split_f16(pa, ph, pl);
+      const float *v0 = (const float *)&vr[T][0][0], *v1 = (const float *)&vr[T][1][0];
+      const float *v2 = (const float *)&vr[T][2][0], *v3 = (const float *)&vr[T][3][0];
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const float *vf = (const float *)&vr[T][rr][0];
-#pragma unroll
-        for (int e = 0; e < DPL; ++e)
-          o[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(sc[T][rr], vf[e], o[e], 0, 0, 0);
+      for (int e = 0; e < DPL; ++e) {
+        const float va[4] = {v0[e], v1[e], v2[e], v3[e]};
+        h4 vh, vl;
+        split_f16(va, vh, vl);
+        o[e] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vh, o[e], 0, 0, 0);
+        o[e] = __builtin_amdgcn_mfma_f32_16x16x16f16(ph, vl, o[e], 0, 0, 0);
+        o[e] = __builtin_amdgcn_mfma_f32_16x16x16f16(pl, vh, o[e], 0, 0, 0);
       }
     }
   }

@@ -157,8 +157,8 @@ def _decode(sess, prompt, n):
 def test_fused_session_matches_two_launches_and_oracle(gh, tiny, ora, prompt_len, steps, kv):
     """(230, 50) crosses 256 positions: the session switches from the fused
     launch to the two launches mid-run (another cached graph). f32 KV pages
-    (the reference's storage) run the fused launch's f32 work item
-    (v_mfma_f32_16x16x4f32) against the two-launch path's f32 attention."""
+    (the reference's storage) run the fused launch's f32 work item (fp16
+    hi + lo MFMA products) against the two-launch path's f32 attention."""
     host, m = tiny
     prompt = gh.synth_tokens(SEED, prompt_len, TINY["vocab_size"], prompt_len)
     runs = {}
