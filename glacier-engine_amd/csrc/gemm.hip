@@ -59,11 +59,29 @@ struct ActStage {
   static constexpr int kUnits = (kUnitCount + 255) / 256;      // per thread
 };
 
-// One thread's share of a quad's activation staging.
+// One thread's share of a quad's activation staging: up to six 16-byte
+// units (3-digit planes, 64 rows) as named members, read and written through
+// at() with indices that are constants once the loops are unrolled. (An
+// array member of six units was kept in scratch memory, whose stores waited
+// for the loads as soon as they were issued.)
 template <int D, int BM>
 struct ActRegs {
-  uint4 v[ActStage<D, BM>::kUnits];
+  static_assert(ActStage<D, BM>::kUnits <= 6, "six units per thread at most");
+  uint4 v0, v1, v2, v3, v4, v5;
   float sc;
+  __device__ __forceinline__ uint4 &at(int i) {
+    switch (i) {
+      case 0: return v0;
+      case 1: return v1;
+      case 2: return v2;
+      case 3: return v3;
+      case 4: return v4;
+      default: return v5;
+    }
+  }
+  __device__ __forceinline__ const uint4 &at(int i) const {
+    return const_cast<ActRegs *>(this)->at(i);
+  }
 };
 
 // Loads quad kq's activation planes (rows m0 .. m0 + BM - 1, clamped to
@@ -80,7 +98,7 @@ __device__ __forceinline__ ActRegs<D, BM> act_load(const GemvArgs &p, int kq, in
     const int half = u & 1, row = (u >> 1) % BM, jd = (u >> 1) / BM;
     const int m = min(m0 + row, M - 1);
     const size_t src = ((size_t)(4 * kq) * D + jd) * M + m;  // group 4kq + j, digit d
-    r.v[i] = *(const uint4 *)(p.act_q + src * 32 + 16 * half);
+    r.at(i) = *(const uint4 *)(p.act_q + src * 32 + 16 * half);
   }
   const int ts = t % (4 * BM);  // threads past 4 BM repeat another's scale
   const int j = ts / BM, row = ts % BM;
@@ -93,7 +111,7 @@ __device__ __forceinline__ void act_store(unsigned char *buf, const ActRegs<D, B
   const int t = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < ActStage<D, BM>::kUnits; ++i)
-    ((uint4 *)buf)[min(t + 256 * i, ActStage<D, BM>::kUnitCount - 1)] = r.v[i];
+    ((uint4 *)buf)[min(t + 256 * i, ActStage<D, BM>::kUnitCount - 1)] = r.at(i);
   // (duplicates store the same value to the same slot: no branch)
   ((float *)(buf + ActStage<D, BM>::kActBytes))[t % (4 * BM)] = r.sc;
 }
