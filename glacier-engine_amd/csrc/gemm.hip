@@ -273,10 +273,11 @@ __global__ __launch_bounds__(256, kRB == 4 ? 2 : kRB == 2 ? 4 : 5) void gemm_ker
   }
 
   // Lane (c, n) holds rows m0 + 16 mt + 4c + r of column 16 nb + n.
-  // (the fold is compiled into tiles of up to 32 rows only: in the 64-row
-  // prompt-chunk tiles its registers would spill the whole kernel)
-  if (BM <= 32 && fold) {
-    if (ks_count > 1) {
+  // (the fold's publication is compiled into tiles of up to 32 rows only: in
+  // the 64-row prompt-chunk tiles its registers would spill the whole
+  // kernel; those fold only without a K split, where the sums are complete)
+  if (fold) {
+    if (BM <= 32 && ks_count > 1) {
       // Publish this split's partial sums; the tile's last split to arrive
       // adds every split's in split order (the finishing kernel's order, so
       // the sums are the same) and runs the epilogue. The publication is the
@@ -658,10 +659,35 @@ static bool gemm_plan(const GemvArgs &a, GemmShape &s) {
   return true;
 }
 
+// Whether a tile of this shape stages its SwiGLU outputs for the plane
+// emission in the kernel's LDS (BM rows x 32 kRB outputs in the two
+// activation buffers).
+static bool swiglu_stage_fits(int D, const GemmShape &s) {
+  const int bm = 16 * s.mt, rb = s.nt / 4;
+  const int buf = 4 * D * bm * 32 + 4 * bm * 4;  // ActStage<D, BM>::kBufBytes
+  return bm * 32 * rb * 4 <= 2 * buf;
+}
+
+// A SwiGLU GEMM without a K split emits down's planes from its own tiles
+// (their sums are complete), with no partial sums, when the staging fits.
+static bool gemm_direct_emit(const GemvArgs &a, const GemmShape &s) {
+  return a.out_q && a.epi == EPI_SWIGLU && s.ks == 1 && swiglu_stage_fits(a.D, s);
+}
+
+// Whether the planes a launch emits overlap the planes it reads.
+static bool emit_overlaps_input(const GemvArgs &a) {
+  const size_t in_bytes = (size_t)(a.K / 32) * a.D * a.M * 32;
+  const size_t out_bytes = a.out_q ? (size_t)(a.N / 64) * a.out_D * a.M * 32 : 0;
+  return a.out_q && (const int8_t *)a.out_q < a.act_q + in_bytes &&
+         a.act_q < (const int8_t *)a.out_q + out_bytes;
+}
+
 bool gemm_emit_ok(const GemvArgs &a) {
   GemmShape s;
   if (!a.out_q || !a.out_meta || (a.out_D != 1 && a.out_D != 3) || !gemm_plan(a, s)) return false;
   if (s.ks != 1 && s.ks != 2 && s.ks != 4 && s.ks != 8 && s.ks != 16) return false;
+  if (a.epi == EPI_SWIGLU && gemm_direct_emit(a, s) && !emit_overlaps_input(a))
+    return (a.N / 2) % 32 == 0;
   if (!a.splitk_ws || (size_t)s.ks * a.M * a.N > a.splitk_ws_floats) return false;
   if (a.epi == EPI_SWIGLU) return (a.N / 2) % 32 == 0;
   if (a.epi == EPI_RESID)
@@ -678,17 +704,21 @@ hipError_t launch_gemm(const GemvArgs &a, hipStream_t st) {
   // the last-arriving split finishes its tile (no finishing kernel) when the
   // counters cover the grid, the tile has at most 32 rows and kFoldSplits
   // splits (their partial sums are read at once), and the epilogue is the
-  // tile's own: any but the residual plane emission (whole-row RMSNorm)
-  // (never when the emitted planes overlap the input planes: a finished
-  // tile would overwrite what the others still read)
-  const size_t in_bytes = (size_t)(a.K / 32) * a.D * a.M * 32;
-  const size_t out_bytes = emit ? (size_t)(a.N / 64) * a.out_D * a.M * 32 : 0;
-  const bool overlap = emit && (const int8_t *)a.out_q < a.act_q + in_bytes &&
-                       a.act_q < (const int8_t *)a.out_q + out_bytes;
-  const bool fold = a.splitk_counters && s.grid <= a.splitk_counter_count && s.mt <= 2 &&
-                    (!emit || (a.epi == EPI_SWIGLU && !overlap)) && (s.ks > 1 || emit) &&
-                    s.ks <= kFoldSplits;
+  // tile's own: any but the residual plane emission (whole-row RMSNorm);
+  // without a K split any tile emits SwiGLU's planes itself (never when the
+  // emitted planes overlap the input planes: a finished tile would
+  // overwrite what the others still read)
+  const bool overlap = emit_overlaps_input(a);
+  const bool fold = (a.splitk_counters && s.grid <= a.splitk_counter_count && s.mt <= 2 &&
+                     (!emit || (a.epi == EPI_SWIGLU && !overlap)) && (s.ks > 1 || emit) &&
+                     s.ks <= kFoldSplits) ||
+                    (emit && !overlap && gemm_direct_emit(a, s));
   float *part = s.ks > 1 || (emit && !fold) ? a.splitk_ws : nullptr;
+  // (an emission that cannot fold, e.g. into its own input planes, needs
+  // the partial sums in the workspace)
+  if ((s.ks > 1 || (emit && !fold)) &&
+      (!a.splitk_ws || (size_t)s.ks * a.M * a.N > a.splitk_ws_floats))
+    return hipErrorInvalidValue;
 #define GK_GEMM(DD, RB, BM)                                                                      \
   hipLaunchKernelGGL((gemm_kernel<DD, RB, BM>), grid, block, 0, st, a, s.m_tiles, s.ks, part, \
                      fold ? 1 : 0)

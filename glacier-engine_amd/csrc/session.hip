@@ -922,12 +922,12 @@ hipError_t run_proj(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, i
 // projection's planes (its inputs come from planes or the conversion kernel,
 // both into act_q, so that is what the check assumes).
 bool gemm_emit_ok(glacier_hip_session *s, glacier_hip_int4_weight *w, int D, int rows, int epi,
-                  const ProjOut &out) {
+                  const ProjIn &in, const ProjOut &out) {
   if (rows <= gk::kGemvMaxRows) return false;
-  ProjIn in;
-  in.planes_q = s->act_q;
-  in.planes_m = s->act_meta;
-  const gk::GemvArgs a = proj_args(s, w, D, rows, epi, in, out);
+  ProjIn pin;  // the planes the launch reads: in's, or the conversion kernel's
+  pin.planes_q = in.x ? s->act_q : in.planes_q;
+  pin.planes_m = in.x ? s->act_meta : in.planes_m;
+  const gk::GemvArgs a = proj_args(s, w, D, rows, epi, pin, out);
   return gk::gemm_emit_ok(a);
 }
 
@@ -1129,9 +1129,9 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
         if (ss_count <= 0) return hipErrorInvalidValue;
       }
       if (!chain) {  // GEMM: gate/up's planes from O's finishing pass
-        oout.emit = gk::PlanesDst{s->act_q, s->act_meta, Dg};
+        oout.emit = gk::PlanesDst{s->act_q2, s->act_meta2, Dg};
         oout.emit_norm_w = L.post_norm;
-        if (!gemm_emit_ok(s, L.o, Do, rows, gk::EPI_RESID, oout)) {
+        if (!gemm_emit_ok(s, L.o, Do, rows, gk::EPI_RESID, oin, oout)) {
           oout.emit = gk::PlanesDst{nullptr, nullptr, 1};
           oout.emit_norm_w = nullptr;
         }
@@ -1143,8 +1143,8 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
       // gate/up + SwiGLU (decode sizes: emitted straight into down's planes)
       ProjIn gin;
       if (oout.emit.q) {
-        gin.planes_q = s->act_q;
-        gin.planes_m = s->act_meta;
+        gin.planes_q = s->act_q2;
+        gin.planes_m = s->act_meta2;
       } else {
         gin.x = s->h;
         gin.norm_w = L.post_norm;
@@ -1154,14 +1154,18 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
       if (chain) {
         gout.emit = gk::PlanesDst{s->act_q2, s->act_meta2, Dd};
       } else {
-        // GEMM: down's planes from gate/up's finishing pass, else the SwiGLU
-        // rows; into act_q2 (free once O has read attention's planes) up to
-        // the rows it holds, so the last K split of each tile can emit its
-        // tile while the others still read act_q, else into act_q (which
-        // gate/up has finished reading by the finishing pass)
-        gout.emit = (uint32_t)rows <= s->planes2_rows ? gk::PlanesDst{s->act_q2, s->act_meta2, Dd}
-                                                      : gk::PlanesDst{s->act_q, s->act_meta, Dd};
-        if (!gemm_emit_ok(s, L.gu, Dg, rows, gk::EPI_SWIGLU, gout)) {
+        // GEMM: down's planes from gate/up's own tiles (the last K split of
+        // each, or every tile without a split) or its finishing pass, else
+        // the SwiGLU rows; into act_q when gate/up reads O's planes from
+        // act_q2 (so no finished tile overwrites planes another still
+        // reads), else into act_q2 up to the rows it holds (gate/up then
+        // reads act_q: the conversion kernel's planes), else into act_q by
+        // the finishing pass
+        gout.emit = gin.planes_q == s->act_q2 ? gk::PlanesDst{s->act_q, s->act_meta, Dd}
+                    : (uint32_t)rows <= s->planes2_rows
+                        ? gk::PlanesDst{s->act_q2, s->act_meta2, Dd}
+                        : gk::PlanesDst{s->act_q, s->act_meta, Dd};
+        if (!gout.emit.q || !gemm_emit_ok(s, L.gu, Dg, rows, gk::EPI_SWIGLU, gin, gout)) {
           gout.emit = gk::PlanesDst{nullptr, nullptr, 1};
           gout.y = s->act;
         }
@@ -1193,7 +1197,7 @@ hipError_t enqueue_layers(glacier_hip_session *s, int rows, const RowPtrs &rp, h
       const LayerDev &N = m->layers[l + 1];
       dout.emit = gk::PlanesDst{s->act_q, s->act_meta, layer_D(s, N.qkv->out_f, N.qkv->in_f)};
       dout.emit_norm_w = N.in_norm;
-      x_planes = gemm_emit_ok(s, L.down, Dd, rows, gk::EPI_RESID, dout);
+      x_planes = gemm_emit_ok(s, L.down, Dd, rows, gk::EPI_RESID, din, dout);
       if (!x_planes) {
         dout.emit = gk::PlanesDst{nullptr, nullptr, 1};
         dout.emit_norm_w = nullptr;
@@ -1857,13 +1861,16 @@ static glacier_hip_session *session_create_impl(glacier_hip_model *m,
   A((void **)&s->act_meta, Gmax * M * sizeof(gk::ActMeta));
   // the gate/up epilogue emits planes for every GEMV launch (up to
   // kGemvMaxRows rows) and attention the O projection's for every step of
-  // up to 32 rows (decode lanes, or a prompt chunk that short); GEMM steps
-  // emit into act_q
+  // up to 32 rows (decode lanes, or a prompt chunk that short); in GEMM
+  // steps of any row count O's finishing pass emits gate/up's planes
+  // (model width) here, so that gate/up can emit down's into act_q, which
+  // none of its tiles read
   s->planes2_rows = std::min<uint32_t>(M, 32);
   // act_q2 also holds the O projection's planes, emitted by attention
   const size_t G2 = std::max<size_t>(c.hidden_dim, (size_t)c.num_heads * c.head_dim) / 32;
-  A((void **)&s->act_q2, G2 * 3 * s->planes2_rows * 32);
-  A((void **)&s->act_meta2, G2 * s->planes2_rows * sizeof(gk::ActMeta));
+  const size_t q2_groups_rows = std::max(G2 * s->planes2_rows, (size_t)(c.dim / 32) * M);
+  A((void **)&s->act_q2, q2_groups_rows * 3 * 32);
+  A((void **)&s->act_meta2, q2_groups_rows * sizeof(gk::ActMeta));
   A((void **)&s->att_scratch, std::max<size_t>(att, 1) * 4);
   A((void **)&s->ss_parts, (size_t)32 * 1024 * sizeof(float));
   A((void **)&s->o_parts, (size_t)c.num_kv_heads * c.dim * sizeof(float));
