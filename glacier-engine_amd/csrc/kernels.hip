@@ -2103,14 +2103,24 @@ __global__ __launch_bounds__(64 * kMaxGroup) void attn_prefill_kernel(
   for (int kp = 0; kp < npages; ++kp) {
     const int b = kp & 1;
     if (kp + 1 < npages) fetch(kp + 1);  // next page in flight
-    // scores S^T[key 4c + r][row j]
+    // scores S^T[key 4c + r][row j]; every K fragment is read from LDS
+    // before the first MFMA (one LDS round trip a page, not one a step)
+    h4 kf[S];
+#pragma unroll
+    for (int st = 0; st < S; ++st) kf[st] = *(const h4 *)&ks[b][j * KP + 16 * st + 4 * c];
+    __builtin_amdgcn_sched_barrier(0);  // (the scheduler would sink them again)
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int st = 0; st < S; ++st) {
-      const h4 a = *(const h4 *)&ks[b][j * KP + 16 * st + 4 * c];
-      acc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qhi[st], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, qlo[st], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kf[st], qhi[st], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x16f16(kf[st], qlo[st], acc, 0, 0, 0);
     }
+    // the V fragments do not depend on the softmax: requested before it
+    __builtin_amdgcn_sched_barrier(0);
+    h4 vf[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) vf[nt] = *(const h4 *)&vt[b][(16 * nt + j) * VP + 4 * c];
+    __builtin_amdgcn_sched_barrier(0);
     float sv[4], pm = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -2142,9 +2152,8 @@ __global__ __launch_bounds__(64 * kMaxGroup) void attn_prefill_kernel(
     for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) o[nt][r] *= ar[r];
-      const h4 bv = *(const h4 *)&vt[b][(16 * nt + j) * VP + 4 * c];
-      o[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi, bv, o[nt], 0, 0, 0);
-      o[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo, bv, o[nt], 0, 0, 0);
+      o[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(phi, vf[nt], o[nt], 0, 0, 0);
+      o[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(plo, vf[nt], o[nt], 0, 0, 0);
     }
     // publish the next page (the other buffer was last read before the
     // previous barrier)
